@@ -1,0 +1,199 @@
+#!/usr/bin/env python3
+"""Benchmark of the KATA-SPD hot path on one MI355X.
+
+Workload: causal concat-SPD attention forward+backward,
+B=8, H=12, T=2048, dk=dv=64, M=4 groups, bf16 inputs / fp32 accumulation,
+q,k,v ~ N(0,1)/8, dO ~ N(0,1) (seed 1), synthetic data already resident in
+HBM.  One step = forward (o, den) + backward (dq, dk, dv) through the C ABI
+(linatt_kata_fwd, linatt_kata_bwd_dq, linatt_kata_bwd_dkdv) on the current
+HIP stream, with preallocated outputs.
+
+Prints ONE JSON line: tokens/s (B*T per step), per-kernel average durations
+measured with HIP events recorded on the launch stream, the roofline of the
+dominant kernel (algorithmic FLOPs per launch / its average duration), and
+the CPU baseline: the float32 restatement of the reference math in
+``oracle/kata.py`` timed on the host cores over a bounded sample of heads.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--groups M]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+METRIC = "KATA/delta fwd+bwd tokens/s & TFLOP/s (% MFMA peak) at B8 H12 T2048 D64"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def kata_flops(B, H, T, dk, dv, M, variant="concat"):
+    """Algorithmic FLOPs (FlashAttention convention, causal half, no
+    recompute): one 'unit' per product over the causal triangle."""
+    qk = B * H * T * T * dk * (M if variant == "sum" else 1)
+    pv = B * H * T * T * dv
+    fwd = qk + pv
+    # backward products: S recompute (qk), dP (pv), dV (pv), dQ (qk), dK (qk)
+    dkdv = qk + pv + pv + qk      # the dk/dv kernel needs S, dP, dV, dK
+    dq = qk                       # the dq kernel's own product (S, dP are recompute)
+    return {"fwd": fwd, "bwd_dq": dq, "bwd_dkdv": dkdv, "total": fwd + dq + dkdv}
+
+
+def cpu_baseline(q, k, v, do, M, seconds):
+    """Time the float32 restatement of the reference path (dense forward +
+    explicit backward, kata/parallel_kata_attn.py:49-146) head by head on the
+    host until `seconds` elapse; return tokens/s scaled to the full step."""
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import kata as K
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    B, T, H, D = q.shape
+    heads = [(b, h) for b in range(B) for h in range(H)]
+    done = 0
+    t0 = time.perf_counter()
+    for b, h in heads:
+        sl = lambda x: x[b:b + 1, :, h:h + 1]  # noqa: E731
+        o, den = K.kata_fwd(sl(q), sl(k), sl(v), M, work_dtype=torch.float32)
+        K.kata_bwd(sl(q), sl(k), sl(v), o, den, sl(do), M, work_dtype=torch.float32)
+        done += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    el = time.perf_counter() - t0
+    tokens = done / len(heads) * B * T
+    return {"value": tokens / el, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{done} of {len(heads)} (batch, head) slices of config 2 "
+                      f"(T={T}, M={M}), float32 dense fwd + explicit bwd, {el:.1f} s",
+            "cpu_model": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--groups", type=int, default=4)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only; multi-GPU runs are not part of "
+              "it (see DESIGN.md for how the path shards). Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from linatt_amd import _lib
+    L = _lib.load()
+
+    B, H, T, D, M = 8, 12, 2048, 64, args.groups
+    scale = 1.0 / math.sqrt(D // M)
+    g = torch.Generator().manual_seed(1)
+    q, k, v = ((torch.randn(B, T, H, D, generator=g) / 8).to(torch.bfloat16) for _ in range(3))
+    do = torch.randn(B, T, H, D, generator=g).to(torch.bfloat16)
+    dev = torch.device("cuda", 0)
+    qd, kd, vd, dod = (x.to(dev) for x in (q, k, v, do))
+    o = torch.empty_like(vd)
+    den = torch.empty(B, T, H, device=dev, dtype=torch.float32)
+    dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+    ws = torch.empty(L.linatt_kata_bwd_workspace_bytes(B, T, H) // 4, device=dev,
+                     dtype=torch.float32)
+    P = _lib.ptr
+    dt = _lib.LINATT_BFLOAT16
+    stream = torch.cuda.current_stream(dev)
+    sp = _lib.stream_of(qd)
+    bargs = (P(qd), P(kd), P(vd), P(o), P(den), P(dod), P(dq), P(dk), P(dv), P(ws),
+             B, T, H, H, D, D, M, scale, 0, dt, sp)
+
+    def fwd():
+        _lib.check("linatt_kata_fwd", L.linatt_kata_fwd(
+            P(qd), P(kd), P(vd), None, P(o), P(den), B, T, H, H, D, D, M, scale, 0, dt, sp))
+
+    def bwd_dq():
+        _lib.check("linatt_kata_bwd_dq", L.linatt_kata_bwd_dq(*bargs))
+
+    def bwd_dkdv():
+        _lib.check("linatt_kata_bwd_dkdv", L.linatt_kata_bwd_dkdv(*bargs))
+
+    parts = [("fwd", fwd), ("bwd_dq", bwd_dq), ("bwd_dkdv", bwd_dkdv)]
+    for _ in range(args.warmup):
+        for _, f in parts:
+            f()
+    torch.cuda.synchronize()
+
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(parts) + 1)]
+          for _ in range(args.steps)]
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for s in range(args.steps):
+        ev[s][0].record(stream)
+        for i, (_, f) in enumerate(parts):
+            f()
+            ev[s][i + 1].record(stream)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    ms_total = start.elapsed_time(stop)
+    ms_step = ms_total / args.steps
+    kern_ms = {name: sum(ev[s][i].elapsed_time(ev[s][i + 1]) for s in range(args.steps)) / args.steps
+               for i, (name, _) in enumerate(parts)}
+
+    fl = kata_flops(B, H, T, D, D, M)
+    kern = {n: {"avg_ms": round(kern_ms[n], 4), "alg_gflop": fl[n] / 1e9,
+                "tflops": fl[n] / (kern_ms[n] * 1e-3) / 1e12} for n in kern_ms}
+    for n in kern:
+        kern[n]["tflops"] = round(kern[n]["tflops"], 1)
+        kern[n]["frac_mfma_peak"] = round(kern[n]["tflops"] / PEAK_BF16_TFLOPS, 4)
+    dom = max(kern_ms, key=kern_ms.get)
+    ach = fl[dom] / (kern_ms[dom] * 1e-3) / 1e12
+    step_tflops = fl["total"] / (ms_step * 1e-3) / 1e12
+    tokens_per_s = B * T / (ms_step * 1e-3)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(q, k, v, do, M, args.cpu_seconds)
+
+    out = {
+        "metric": METRIC,
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "kata_concat_fwd_bwd (BASELINE config 2)", "B": B, "H": H,
+                   "T": T, "dk": D, "dv": D, "num_groups": M, "chunk": 64, "causal": True,
+                   "seed": 1},
+        "tflops": round(step_tflops, 1),
+        "frac_mfma_peak": round(step_tflops / PEAK_BF16_TFLOPS, 4),
+        "alg_gflop_per_step": round(fl["total"] / 1e9, 2),
+        "kernels": kern,
+        "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(ach, 1),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,93 @@
+/* linatt_hip: C ABI of the MI355X (gfx950) KATA-SPD / delta-rule kernels.
+ *
+ * All tensors are device pointers to contiguous, time-major arrays
+ * (batch, time, head, feature).  The caller owns every buffer, including
+ * workspaces sized by the *_workspace_bytes functions; the library never
+ * allocates or frees device memory.  Every call is asynchronous on the
+ * given HIP stream (`stream` is a hipStream_t; NULL means the null stream)
+ * and never synchronises the device.  Functions return LINATT_OK (0) or a
+ * negative status; linatt_last_error() then holds a message for the calling
+ * thread.  No C++ exception crosses this boundary.
+ *
+ * dtype: LINATT_FLOAT32, LINATT_BFLOAT16 or LINATT_FLOAT16, shared by every
+ * floating-point tensor of a call except den / delta / c (always float32).
+ */
+#ifndef LINATT_HIP_H
+#define LINATT_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LINATT_ABI_VERSION 1
+
+enum linatt_dtype { LINATT_FLOAT32 = 0, LINATT_BFLOAT16 = 1, LINATT_FLOAT16 = 2 };
+enum linatt_kata_variant { LINATT_KATA_CONCAT = 0, LINATT_KATA_SUM = 1 };
+enum linatt_status {
+  LINATT_OK = 0,
+  LINATT_EINVAL = -1,       /* null pointer, bad shape or misalignment */
+  LINATT_EUNSUPPORTED = -2, /* valid, but no kernel is compiled for it */
+  LINATT_ELAUNCH = -3       /* the HIP runtime rejected a launch */
+};
+
+/* ABI version of the loaded library (LINATT_ABI_VERSION at build time). */
+int linatt_abi_version(void);
+
+/* Message describing the last failed call on this thread ("" if none). */
+const char* linatt_last_error(void);
+
+/* 1 if a kernel is compiled for this combination, else 0.  No device work. */
+int linatt_kata_supported(int dtype, int dk, int dv, int num_groups, int variant, int decay);
+
+/* KATA-SPD causal attention forward.
+ * Replaces the launch in parallel_kata_attn_fwd_impl
+ * (kata/parallel_kata_attn.py:211-288; kernel kata/kernels/parallel_kata.py:8-197)
+ * and parallel_kata_attn_sum_fwd_impl (kata/parallel_kata_attn.py:539-576;
+ * kernel kata/kernels/parallel_kata.py:200-345).
+ *   q (B,T,HQ,dk), k (B,T,H,dk), v (B,T,H,dv)  [dtype]; HQ % H == 0 (GQA)
+ *   c (B,T,HQ) float32 cumulative log-decay, or NULL (concat variant only)
+ *   o (B,T,HQ,dv) [dtype], den (B,T,HQ) float32 = sum_{s<=t} A[t,s]
+ *   scale multiplies each group dot before squaring (> 0).
+ */
+int linatt_kata_fwd(const void* q, const void* k, const void* v, const float* c, void* o,
+                    float* den, int B, int T, int HQ, int H, int dk, int dv, int num_groups,
+                    float scale, int variant, int dtype, void* stream);
+
+/* Bytes of float32 workspace linatt_kata_bwd needs (the per-row <o, dO>). */
+size_t linatt_kata_bwd_workspace_bytes(int B, int T, int HQ);
+
+/* KATA-SPD causal attention backward: dq, dk, dv from q, k, v, o, den, dO.
+ * Replaces parallel_kata_attn_bwd_triton (kata/parallel_kata_attn.py:364-529;
+ * kernels kata/kernels/parallel_kata.py:348-1342) and
+ * parallel_kata_attn_sum_bwd_triton_M{2,4} (kata/parallel_kata_attn.py:755-901;
+ * kernels kata/kernels/parallel_kata_sum.py:7-825).  Unlike the reference it
+ * also covers GQA (HQ = G*H) and every compiled M without a host fallback.
+ *   dq (B,T,HQ,dk), dk (B,T,H,dk), dv (B,T,H,dv) [dtype], fully overwritten.
+ *   workspace: linatt_kata_bwd_workspace_bytes(B,T,HQ) bytes, 16-byte aligned.
+ */
+int linatt_kata_bwd(const void* q, const void* k, const void* v, const void* o,
+                    const float* den, const void* dout, void* dq, void* dk, void* dv,
+                    void* workspace, int B, int T, int HQ, int H, int dk_dim, int dv_dim,
+                    int num_groups, float scale, int variant, int dtype, void* stream);
+
+/* The two halves of linatt_kata_bwd, with its argument list, mirroring the
+ * reference's separate dq and dk/dv launches (kata/parallel_kata_attn.py:488-528):
+ * linatt_kata_bwd_dq writes dq and the per-row <o, dO> into workspace
+ * (dk, dv may be NULL); linatt_kata_bwd_dkdv then reads workspace and writes
+ * dk, dv (o, dq may be NULL).  Enqueue dq before dkdv on the same stream. */
+int linatt_kata_bwd_dq(const void* q, const void* k, const void* v, const void* o,
+                       const float* den, const void* dout, void* dq, void* dk, void* dv,
+                       void* workspace, int B, int T, int HQ, int H, int dk_dim, int dv_dim,
+                       int num_groups, float scale, int variant, int dtype, void* stream);
+int linatt_kata_bwd_dkdv(const void* q, const void* k, const void* v, const void* o,
+                         const float* den, const void* dout, void* dq, void* dk, void* dv,
+                         void* workspace, int B, int T, int HQ, int H, int dk_dim, int dv_dim,
+                         int num_groups, float scale, int variant, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LINATT_HIP_H */

@@ -1,0 +1,104 @@
+"""ctypes binding of ``liblinatt_hip.so`` (declared in ``include/linatt_hip.h``).
+
+The library is required: importing an op module without it raises
+``ImportError`` naming the build command.  There is no CPU or PyTorch
+fallback on the product path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.environ.get(
+    "LINATT_LIB",
+    os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "liblinatt_hip.so"),
+)
+
+ABI_VERSION = 1
+
+LINATT_FLOAT32, LINATT_BFLOAT16, LINATT_FLOAT16 = 0, 1, 2
+LINATT_KATA_CONCAT, LINATT_KATA_SUM = 0, 1
+STATUS = {0: "LINATT_OK", -1: "LINATT_EINVAL", -2: "LINATT_EUNSUPPORTED", -3: "LINATT_ELAUNCH"}
+
+_DTYPES = {torch.float32: LINATT_FLOAT32, torch.bfloat16: LINATT_BFLOAT16, torch.float16: LINATT_FLOAT16}
+
+_lock = threading.Lock()
+_lib = None
+
+_vp, _i, _f, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/linatt_hip.h
+SIGNATURES = {
+    "linatt_abi_version": (_i, []),
+    "linatt_last_error": (ctypes.c_char_p, []),
+    "linatt_kata_supported": (_i, [_i, _i, _i, _i, _i, _i]),
+    "linatt_kata_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _i, _i, _vp]),
+    "linatt_kata_bwd_workspace_bytes": (_sz, [_i, _i, _i]),
+    "linatt_kata_bwd": (_i, [_vp] * 10 + [_i] * 7 + [_f, _i, _i, _vp]),
+    "linatt_kata_bwd_dq": (_i, [_vp] * 10 + [_i] * 7 + [_f, _i, _i, _vp]),
+    "linatt_kata_bwd_dkdv": (_i, [_vp] * 10 + [_i] * 7 + [_f, _i, _i, _vp]),
+}
+
+
+class LinattError(RuntimeError):
+    """A C-ABI call returned a negative status."""
+
+    def __init__(self, fn: str, status: int, msg: str):
+        super().__init__(f"{fn} -> {STATUS.get(status, status)}: {msg}")
+        self.status = status
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raise ImportError if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"linatt_amd: HIP library not found at {LIB_PATH}; "
+                "build it with `python -m linatt_amd.build` (hipcc, gfx950)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if lib.linatt_abi_version() != ABI_VERSION:
+            raise ImportError(f"linatt_amd: ABI {lib.linatt_abi_version()} != {ABI_VERSION}")
+        _lib = lib
+    return _lib
+
+
+def check(fn: str, status: int) -> None:
+    if status != 0:
+        raise LinattError(fn, status, load().linatt_last_error().decode())
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPES[dt]
+    except KeyError:
+        raise TypeError(f"linatt_amd: unsupported dtype {dt}") from None
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    """Current HIP stream of the tensor's device, as a void pointer."""
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def require_device(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError(
+                "linatt_amd runs only on a ROCm GPU device; got a tensor on "
+                f"{t.device} (there is no CPU path)")

@@ -1,0 +1,172 @@
+// Shared device helpers for the linatt HIP kernels (gfx950 / CDNA4, wave64).
+//
+// Matrix-core conventions used by every kernel in this library
+// (v_mfma_f32_32x32x16_{bf16,f16}; fp32 operands use eight
+// v_mfma_f32_32x32x2f32 steps that consume the same per-lane k-slots):
+//
+//   lane l, half h = l >> 5, column c = l & 31
+//   A operand (32 x 16, row-major m x k): lane holds A[c][8h + j], j = 0..7
+//   B operand (16 x 32, k x n):           lane holds B[8h + j][c]
+//   C/D (32 x 32 fp32, 16 per lane):      acc[4i + r] = D[8i + 4h + r][c]
+//
+// A reduction (k) index may be permuted freely as long as A and B use the
+// same permutation.  The kernels use this to feed a C-layout result
+// straight back as a B operand: for a 32-row C block, k-step j (0 or 1)
+// takes acc elements i in {2j, 2j+1}, so slot p of lane half h maps to row
+//   8 * (2j + (p >> 2)) + 4h + (p & 3)      (see c_to_b below),
+// and the matching A operand reads two runs of four consecutive rows
+// (16j + 4h .. +3 and 16j + 8 + 4h .. +3) from a transposed LDS tile.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace linatt {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+template <typename T> struct vt;
+template <> struct vt<__bf16> { using v8 = bf16x8; using v4 = bf16x4; };
+template <> struct vt<_Float16> { using v8 = f16x8; using v4 = f16x4; };
+template <> struct vt<float> { using v8 = f32x8; using v4 = f32x4; };
+template <typename T> using v8_t = typename vt<T>::v8;
+template <typename T> using v4_t = typename vt<T>::v4;
+
+__device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mma(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mma(f32x8 a, f32x8 b, f32x16 c) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[j], b[j], c, 0, 0, 0);
+  return c;
+}
+
+// 8 contiguous elements (16 B for 16-bit types, 32 B for fp32); p must be
+// 16-byte aligned.
+template <typename T>
+__device__ __forceinline__ v8_t<T> ld8(const T* p) {
+  if constexpr (sizeof(T) == 2) {
+    return __builtin_bit_cast(v8_t<T>, *reinterpret_cast<const uint4*>(p));
+  } else {
+    const float4 a = reinterpret_cast<const float4*>(p)[0];
+    const float4 b = reinterpret_cast<const float4*>(p)[1];
+    return f32x8{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  }
+}
+
+// 4 contiguous elements (8 B for 16-bit types, 16 B for fp32).
+template <typename T>
+__device__ __forceinline__ v4_t<T> ld4(const T* p) {
+  if constexpr (sizeof(T) == 2) {
+    return __builtin_bit_cast(v4_t<T>, *reinterpret_cast<const uint2*>(p));
+  } else {
+    return __builtin_bit_cast(f32x4, *reinterpret_cast<const float4*>(p));
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void st4(T* p, v4_t<T> v) {
+  if constexpr (sizeof(T) == 2) {
+    *reinterpret_cast<uint2*>(p) = __builtin_bit_cast(uint2, v);
+  } else {
+    *reinterpret_cast<float4*>(p) = __builtin_bit_cast(float4, v);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ v8_t<T> cat44(v4_t<T> a, v4_t<T> b) {
+  return v8_t<T>{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Two runs of four consecutive elements: rows 16j + 4h .. +3 and +8.
+template <typename T>
+__device__ __forceinline__ v8_t<T> ld_tr_op(const T* row, int j, int h) {
+  return cat44<T>(ld4<T>(row + 16 * j + 4 * h), ld4<T>(row + 16 * j + 8 + 4 * h));
+}
+
+// C-layout fp32 block -> B operand (k-step j of its 32 rows), converted to T.
+template <typename T>
+__device__ __forceinline__ v8_t<T> c_to_b(const f32x16& a, int j) {
+  f32x8 f{a[8 * j + 0], a[8 * j + 1], a[8 * j + 2], a[8 * j + 3],
+          a[8 * j + 4], a[8 * j + 5], a[8 * j + 6], a[8 * j + 7]};
+  if constexpr (sizeof(T) == 2) {
+    return __builtin_convertvector(f, v8_t<T>);
+  } else {
+    return f;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ v4_t<T> to4(float a, float b, float c, float d) {
+  f32x4 f{a, b, c, d};
+  if constexpr (sizeof(T) == 2) return __builtin_convertvector(f, v4_t<T>);
+  else return f;
+}
+
+template <typename T>
+__device__ __forceinline__ v8_t<T> zero8() {
+  return v8_t<T>{};
+}
+
+// Cooperative copy of a (64 x C) row-major tile of global rows
+// [row0, row0 + 64) into LDS, natural (pitch NP) and/or transposed (pitch
+// TP, element [c][r]).  Rows at or beyond nrows are written as zero.
+// 4x4 element blocks per thread; 16 consecutive threads read one 64-element
+// row segment, so global reads are coalesced.
+template <typename T, int C, int NP, int TP, bool NAT, bool TRANS, int NT = 256>
+__device__ __forceinline__ void load_tile64(const T* __restrict__ g, int row0, int nrows,
+                                            int64_t row_stride, T* nat, T* trans, int tid) {
+  constexpr int CB = C / 4;
+  constexpr int NB = 16 * CB;
+#pragma unroll
+  for (int blk = tid; blk < NB; blk += NT) {
+    const int cb = blk % CB, rb = blk / CB;
+    v4_t<T> vals[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = row0 + 4 * rb + r;
+      if (row < nrows) vals[r] = ld4<T>(g + (int64_t)row * row_stride + 4 * cb);
+      else vals[r] = v4_t<T>{};
+    }
+    if constexpr (NAT) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st4<T>(nat + (4 * rb + r) * NP + 4 * cb, vals[r]);
+    }
+    if constexpr (TRANS) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        st4<T>(trans + (4 * cb + c) * TP + 4 * rb,
+               v4_t<T>{vals[0][c], vals[1][c], vals[2][c], vals[3][c]});
+    }
+  }
+}
+
+// Block id -> (tile, head) with every head's tiles on one XCD (the hardware
+// deals consecutive workgroups round-robin over the 8 XCDs, each with its
+// own L2) and heavy (late, causal-long) tiles dispatched first.
+__device__ __forceinline__ void map_block(int L, int ntiles, int nheads, int& tile, int& head,
+                                          bool heavy_last_index) {
+  int j;
+  if ((nheads & 7) == 0) {
+    const int x = L & 7;
+    const int jj = L >> 3;
+    const int hpx = nheads >> 3;
+    j = jj / hpx;
+    head = x + 8 * (jj % hpx);
+  } else {
+    j = L / nheads;
+    head = L % nheads;
+  }
+  tile = heavy_last_index ? (ntiles - 1 - j) : j;
+}
+
+}  // namespace linatt

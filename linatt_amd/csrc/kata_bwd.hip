@@ -1,0 +1,380 @@
+// KATA-SPD causal attention backward for gfx950.
+//
+// Replaces parallel_kata_attn_bwd_preprocess, ..._bwd_kernel_dq_M{1,2,4},
+// ..._bwd_kernel_dkdv_M{1,2,4} (kata/kernels/parallel_kata.py:348-1342) and
+// the sum-score kernels (kata/kernels/parallel_kata_sum.py:7-825), launched
+// from parallel_kata_attn_bwd_triton / ..._sum_bwd_triton_M{2,4}
+// (kata/parallel_kata_attn.py:364-529, 755-901).  Math as in the reference's
+// explicit backward (kata/parallel_kata_attn.py:97-146):
+//
+//   P = A / D, delta_t = <o_t, dO_t>, dV = P^T dO,
+//   dA = (dO V^T - delta) / D (causal), da_g = 2 scale^2 r_g dA  (r_g = q_g.k_g)
+//   dQ_g = sum_s da_g k_g,  dK_g = sum_t da_g^T q_g
+//
+// with D replaced by 1 where it is not positive (the kernels' safe divide).
+// GQA (HQ = G*H) is handled natively: dK/dV of a kv head accumulate over its
+// G query heads inside one workgroup.
+//
+// Kernel 1 (dq): a workgroup owns 128 queries (4 waves x 32); key tiles of
+// 64 stream through LDS as K (natural), K^T and V (natural).  It also
+// computes delta for its rows and writes it for kernel 2.
+// Kernel 2 (dk/dv): a workgroup owns 128 keys (4 waves x 32); query tiles
+// of 64 stream through LDS as Q, Q^T, dO, dO^T plus delta and 1/D.
+#include "common.h"
+#include "kata_kernels.h"
+
+namespace linatt {
+
+template <typename T, int DK, int DV, int M, bool SUM>
+__global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dq_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const T* __restrict__ o, const float* __restrict__ den, const T* __restrict__ dout,
+    T* __restrict__ dq, float* __restrict__ delta_out, int Tn, int HQ, int H, float scale2,
+    int nqt, int nbh) {
+  constexpr int E = DK / M;
+  constexpr int KE = E / 16;
+  constexpr int PAD = (sizeof(T) == 2 ? 8 : 4);
+  constexpr int KP = DK + PAD, VP = DV + PAD, TP = 64 + 4;
+  __shared__ __attribute__((aligned(16))) T Ks[64 * KP];
+  __shared__ __attribute__((aligned(16))) T Kt[DK * TP];
+  __shared__ __attribute__((aligned(16))) T Vs[64 * VP];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int cl = lane & 31, hh = lane >> 5;
+  int qt, bh;
+  map_block(blockIdx.x, nqt, nbh, qt, bh, true);
+  const int b = bh / HQ, hq = bh % HQ;
+  const int G = HQ / H, h = hq / G;
+  const int t0 = qt * 128;
+  const int tw = t0 + 32 * w;
+  const int tl = tw + cl;
+  const bool tvalid = tl < Tn;
+
+  const int64_t qs = (int64_t)HQ * DK, ks = (int64_t)H * DK, vs = (int64_t)H * DV,
+                os = (int64_t)HQ * DV;
+  const T* kb = k + ((int64_t)b * Tn) * ks + (int64_t)h * DK;
+  const T* vb = v + ((int64_t)b * Tn) * vs + (int64_t)h * DV;
+  const int64_t qrow = ((int64_t)b * Tn + tl) * HQ + hq;
+
+  v8_t<T> qop[DK / 16], doop[DV / 16];
+#pragma unroll
+  for (int kk = 0; kk < DK / 16; ++kk)
+    qop[kk] = tvalid ? ld8<T>(q + qrow * DK + 16 * kk + 8 * hh) : zero8<T>();
+  float dpart = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < DV / 16; ++kk) {
+    doop[kk] = tvalid ? ld8<T>(dout + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
+    const v8_t<T> ov = tvalid ? ld8<T>(o + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dpart += (float)ov[j] * (float)doop[kk][j];
+  }
+  const float delta = dpart + __shfl_xor(dpart, 32);
+  float pdl = 0.f;
+  if (tvalid) {
+    const float d = den[qrow];
+    pdl = scale2 / (d > 0.f ? d : 1.f);
+    if (hh == 0) delta_out[qrow] = delta;
+  }
+
+  f32x16 acc[DK / 32];
+#pragma unroll
+  for (int rb = 0; rb < DK / 32; ++rb) acc[rb] = f32x16{};
+
+  const int s_end = min(t0 + 128, Tn);
+  const int nst = (s_end + 63) / 64;
+  for (int st = 0; st < nst; ++st) {
+    const int s0 = st * 64;
+    __syncthreads();
+    load_tile64<T, DK, KP, TP, true, true>(kb, s0, Tn, ks, Ks, Kt, tid);
+    load_tile64<T, DV, VP, 1, true, false>(vb, s0, Tn, vs, Vs, nullptr, tid);
+    __syncthreads();
+    if (s0 > tw + 31 || tw >= Tn) continue;
+    const bool need_mask = (s0 + 63 > tw) || (s0 + 64 > Tn);
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      // x^T[s][t] = dP^T - delta = V dO^T - delta  (rows s, column t)
+      f32x16 x;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) x[e] = -delta;
+      const T* vrow = Vs + (32 * sb + cl) * VP + 8 * hh;
+#pragma unroll
+      for (int kk = 0; kk < DV / 16; ++kk) x = mma(ld8<T>(vrow + 16 * kk), doop[kk], x);
+      if (need_mask) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int s = s0 + 32 * sb + 8 * i + 4 * hh + r;
+            if (s > tl || s >= Tn) x[4 * i + r] = 0.f;
+          }
+      }
+      const T* krow = Ks + (32 * sb + cl) * KP + 8 * hh;
+#pragma unroll
+      for (int gi = 0; gi < M; ++gi) {
+#pragma unroll
+        for (int gj = 0; gj < (SUM ? M : 1); ++gj) {
+          const int gk = SUM ? gj : gi;  // key group paired with query group gi
+          f32x16 r{};
+#pragma unroll
+          for (int kk = 0; kk < KE; ++kk) r = mma(ld8<T>(krow + gk * E + 16 * kk), qop[gi * KE + kk], r);
+          const f32x16 da = r * x;
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const v8_t<T> bop = c_to_b<T>(da, j);
+            // dQ^T rows R = 32rb + cl belonging to query group gi take K^T rows of key group gk
+#pragma unroll
+            for (int rb = (gi * E) / 32; rb <= ((gi + 1) * E - 1) / 32; ++rb) {
+              const int R = 32 * rb + cl;
+              v8_t<T> aop;
+              if constexpr (E >= 32) {
+                aop = ld_tr_op<T>(Kt + (gk * E + (R - gi * E)) * TP + 32 * sb, j, hh);
+              } else {
+                aop = (R / E == gi) ? ld_tr_op<T>(Kt + (gk * E + (R % E)) * TP + 32 * sb, j, hh)
+                                    : zero8<T>();
+              }
+              acc[rb] = mma(aop, bop, acc[rb]);
+            }
+          }
+        }
+      }
+    }
+  }
+
+  if (tvalid) {
+    const float f = 2.f * pdl;
+    T* drow = dq + qrow * DK;
+#pragma unroll
+    for (int rb = 0; rb < DK / 32; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        st4<T>(drow + 32 * rb + 8 * i + 4 * hh,
+               to4<T>(acc[rb][4 * i] * f, acc[rb][4 * i + 1] * f, acc[rb][4 * i + 2] * f,
+                      acc[rb][4 * i + 3] * f));
+  }
+}
+
+template <typename T, int DK, int DV, int M, bool SUM>
+__global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const float* __restrict__ den, const float* __restrict__ delta, const T* __restrict__ dout,
+    T* __restrict__ dk, T* __restrict__ dv, int Tn, int HQ, int H, float scale2, int nst,
+    int nbh) {
+  constexpr int E = DK / M;
+  constexpr int KE = E / 16;
+  constexpr int PAD = (sizeof(T) == 2 ? 8 : 4);
+  constexpr int QP = DK + PAD, OP = DV + PAD, TP = 64 + 4;
+  __shared__ __attribute__((aligned(16))) T Qs[64 * QP];
+  __shared__ __attribute__((aligned(16))) T Qt[DK * TP];
+  __shared__ __attribute__((aligned(16))) T Os[64 * OP];
+  __shared__ __attribute__((aligned(16))) T Ot[DV * TP];
+  __shared__ __attribute__((aligned(16))) float Dl[64];
+  __shared__ __attribute__((aligned(16))) float Pd[64];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int cl = lane & 31, hh = lane >> 5;
+  int stile, bh;
+  map_block(blockIdx.x, nst, nbh, stile, bh, false);
+  const int b = bh / H, h = bh % H;
+  const int G = HQ / H;
+  const int s0 = stile * 128;
+  const int sw = s0 + 32 * w;
+  const int sl = sw + cl;
+  const bool svalid = sl < Tn;
+
+  const int64_t qs = (int64_t)HQ * DK, os = (int64_t)HQ * DV;
+  const int64_t krow = ((int64_t)b * Tn + sl) * H + h;
+
+  v8_t<T> kop[DK / 16], vop[DV / 16];
+#pragma unroll
+  for (int kk = 0; kk < DK / 16; ++kk)
+    kop[kk] = svalid ? ld8<T>(k + krow * DK + 16 * kk + 8 * hh) : zero8<T>();
+#pragma unroll
+  for (int kk = 0; kk < DV / 16; ++kk)
+    vop[kk] = svalid ? ld8<T>(v + krow * DV + 16 * kk + 8 * hh) : zero8<T>();
+
+  f32x16 dka[DK / 32], dva[DV / 32];
+#pragma unroll
+  for (int rb = 0; rb < DK / 32; ++rb) dka[rb] = f32x16{};
+#pragma unroll
+  for (int db = 0; db < DV / 32; ++db) dva[db] = f32x16{};
+
+  const int ntt = (Tn + 63) / 64;
+  for (int hq = h * G; hq < (h + 1) * G; ++hq) {
+    const T* qb = q + ((int64_t)b * Tn) * qs + (int64_t)hq * DK;
+    const T* ob = dout + ((int64_t)b * Tn) * os + (int64_t)hq * DV;
+    for (int tt = s0 / 64; tt < ntt; ++tt) {
+      const int t0 = tt * 64;
+      __syncthreads();
+      load_tile64<T, DK, QP, TP, true, true>(qb, t0, Tn, qs, Qs, Qt, tid);
+      load_tile64<T, DV, OP, TP, true, true>(ob, t0, Tn, os, Os, Ot, tid);
+      if (tid < 64) {
+        const int t = t0 + tid;
+        float dl = 0.f, pd = 0.f;
+        if (t < Tn) {
+          const int64_t r = ((int64_t)b * Tn + t) * HQ + hq;
+          dl = delta[r];
+          const float d = den[r];
+          pd = scale2 / (d > 0.f ? d : 1.f);
+        }
+        Dl[tid] = dl;
+        Pd[tid] = pd;
+      }
+      __syncthreads();
+      if (t0 + 63 < sw || sw >= Tn) continue;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const int tb = t0 + 32 * mb;
+        if (tb + 31 < sw) continue;
+        const bool need_mask = (tb < sw + 31) || (tb + 32 > Tn);
+        // x[t][s] = dO V^T - delta  (rows t, column s)
+        f32x16 x;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(Dl + 32 * mb + 8 * i + 4 * hh);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) x[4 * i + r] = -d4[r];
+        }
+        const T* orow = Os + (32 * mb + cl) * OP + 8 * hh;
+#pragma unroll
+        for (int kk = 0; kk < DV / 16; ++kk) x = mma(ld8<T>(orow + 16 * kk), vop[kk], x);
+        f32x16 pdv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f32x4 p4 = *reinterpret_cast<const f32x4*>(Pd + 32 * mb + 8 * i + 4 * hh);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) pdv[4 * i + r] = p4[r];
+        }
+        const T* qrow = Qs + (32 * mb + cl) * QP + 8 * hh;
+        // scores r = Q K^T per group (rows t, column s)
+        constexpr int NR = SUM ? 1 : M;
+        f32x16 rg[NR];
+        f32x16 A{};
+        if constexpr (!SUM) {
+#pragma unroll
+          for (int g = 0; g < M; ++g) {
+            f32x16 r{};
+#pragma unroll
+            for (int kk = 0; kk < KE; ++kk) r = mma(ld8<T>(qrow + g * E + 16 * kk), kop[g * KE + kk], r);
+            rg[g] = r;
+            A += r * r;
+          }
+        } else {
+#pragma unroll
+          for (int gi = 0; gi < M; ++gi)
+#pragma unroll
+            for (int gj = 0; gj < M; ++gj) {
+              f32x16 r{};
+#pragma unroll
+              for (int kk = 0; kk < KE; ++kk)
+                r = mma(ld8<T>(qrow + gi * E + 16 * kk), kop[gj * KE + kk], r);
+              A += r * r;
+            }
+        }
+        if (need_mask) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int t = tb + 8 * i + 4 * hh + r;
+              if (t < sl || t >= Tn) {
+                A[4 * i + r] = 0.f;
+                x[4 * i + r] = 0.f;
+              }
+            }
+        }
+        const f32x16 P = A * pdv;
+        const f32x16 xs = x * pdv;
+        // dV^T[dv][s] += sum_t dO^T[dv][t] P[t][s]
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const v8_t<T> pb = c_to_b<T>(P, j);
+#pragma unroll
+          for (int db = 0; db < DV / 32; ++db)
+            dva[db] = mma(ld_tr_op<T>(Ot + (32 * db + cl) * TP + 32 * mb, j, hh), pb, dva[db]);
+        }
+        // dK^T[(g,e)][s] += sum_t Q^T[(g',e)][t] da[t][s]
+#pragma unroll
+        for (int gi = 0; gi < M; ++gi) {
+#pragma unroll
+          for (int gj = 0; gj < (SUM ? M : 1); ++gj) {
+            const int gk = SUM ? gj : gi;  // key group receiving the gradient
+            f32x16 r;
+            if constexpr (!SUM) {
+              r = rg[gi];
+            } else {
+              r = f32x16{};
+#pragma unroll
+              for (int kk = 0; kk < KE; ++kk)
+                r = mma(ld8<T>(qrow + gi * E + 16 * kk), kop[gj * KE + kk], r);
+            }
+            const f32x16 da = r * xs;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const v8_t<T> bop = c_to_b<T>(da, j);
+#pragma unroll
+              for (int rb = (gk * E) / 32; rb <= ((gk + 1) * E - 1) / 32; ++rb) {
+                const int R = 32 * rb + cl;
+                v8_t<T> aop;
+                if constexpr (E >= 32) {
+                  aop = ld_tr_op<T>(Qt + (gi * E + (R - gk * E)) * TP + 32 * mb, j, hh);
+                } else {
+                  aop = (R / E == gk) ? ld_tr_op<T>(Qt + (gi * E + (R % E)) * TP + 32 * mb, j, hh)
+                                      : zero8<T>();
+                }
+                dka[rb] = mma(aop, bop, dka[rb]);
+              }
+            }
+          }
+        }
+      }
+    }
+  }
+
+  if (svalid) {
+    T* dkrow = dk + krow * DK;
+    T* dvrow = dv + krow * DV;
+#pragma unroll
+    for (int rb = 0; rb < DK / 32; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        st4<T>(dkrow + 32 * rb + 8 * i + 4 * hh,
+               to4<T>(2.f * dka[rb][4 * i], 2.f * dka[rb][4 * i + 1], 2.f * dka[rb][4 * i + 2],
+                      2.f * dka[rb][4 * i + 3]));
+#pragma unroll
+    for (int db = 0; db < DV / 32; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        st4<T>(dvrow + 32 * db + 8 * i + 4 * hh,
+               to4<T>(dva[db][4 * i], dva[db][4 * i + 1], dva[db][4 * i + 2], dva[db][4 * i + 3]));
+  }
+}
+
+template <typename T, int DK, int DV, int M, bool SUM>
+hipError_t launch_kata_bwd(const KataArgs& a, int parts, hipStream_t stream) {
+  const float scale2 = a.scale * a.scale;
+  const int nqt = (a.T + 127) / 128;
+  if (parts & KATA_BWD_DQ) {
+    const int nbh = a.B * a.HQ;
+    kata_bwd_dq_kernel<T, DK, DV, M, SUM><<<dim3(nqt * nbh), dim3(256), 0, stream>>>(
+        (const T*)a.q, (const T*)a.k, (const T*)a.v, (const T*)a.o, a.den, (const T*)a.dout,
+        (T*)a.dq, a.delta, a.T, a.HQ, a.H, scale2, nqt, nbh);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (parts & KATA_BWD_DKDV) {
+    const int nbk = a.B * a.H;
+    kata_bwd_dkdv_kernel<T, DK, DV, M, SUM><<<dim3(nqt * nbk), dim3(256), 0, stream>>>(
+        (const T*)a.q, (const T*)a.k, (const T*)a.v, a.den, a.delta, (const T*)a.dout,
+        (T*)a.dk, (T*)a.dv, a.T, a.HQ, a.H, scale2, nqt, nbk);
+    return hipGetLastError();
+  }
+  return hipSuccess;
+}
+
+#define LINATT_BWD_INST(T, DK, DV, M)                                                          \
+  template hipError_t launch_kata_bwd<T, DK, DV, M, false>(const KataArgs&, int, hipStream_t); \
+  template hipError_t launch_kata_bwd<T, DK, DV, M, true>(const KataArgs&, int, hipStream_t);
+
+LINATT_KATA_SHAPES(LINATT_BWD_INST)
+
+}  // namespace linatt

@@ -1,0 +1,178 @@
+// KATA-SPD causal attention forward for gfx950.
+//
+// Replaces the reference's parallel_kata_attn_fwd_kernel and
+// parallel_kata_attn_sum_fwd_kernel (kata/kernels/parallel_kata.py:8-197,
+// 200-345), launched from parallel_kata_attn_fwd_impl /
+// parallel_kata_attn_sum_fwd_impl (kata/parallel_kata_attn.py:211-288,
+// 539-576).
+//
+//   A[t,s] = sum_g (q_g[t].k_g[s])^2          (concat)
+//          = sum_{i,j} (q_i[t].k_j[s])^2      (sum)
+//            [* exp(min(c_t - c_s, 0))]        (decay)
+//   o[t]   = sum_{s<=t} A[t,s] v[s] / den[t],  den[t] = scale^2 * sum_{s<=t} A[t,s]
+//
+// scale^2 is folded into den only: o is scale-invariant.  Where den is not
+// positive the output row is left unnormalised (the reference's safe divide).
+//
+// Work split: a workgroup owns 128 queries of one (batch, query head); each
+// of its four waves owns 32 queries.  Key tiles of 64 rows stream through
+// LDS: K in natural layout (A operand of S^T = K Q^T), V transposed (A
+// operand of O^T = V^T P^T).  Q^T stays in registers as the B operand, so
+// the score block comes out in C layout with one query per lane column and
+// goes back into the P.V product without leaving registers.
+#include "common.h"
+#include "kata_kernels.h"
+
+namespace linatt {
+
+template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
+__global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_fwd_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const float* __restrict__ c, T* __restrict__ o, float* __restrict__ den,
+    int Tn, int HQ, int H, float scale2, int nqt, int nbh) {
+  constexpr int E = DK / M;
+  constexpr int KE = E / 16;           // 16-wide k-steps per group
+  constexpr int KP = DK + (sizeof(T) == 2 ? 8 : 4);   // K tile pitch
+  constexpr int VP = 64 + (sizeof(T) == 2 ? 4 : 4);   // V^T tile pitch
+  static_assert(E % 16 == 0 && DV % 32 == 0, "unsupported head shape");
+  __shared__ __attribute__((aligned(16))) T Ks[64 * KP];
+  __shared__ __attribute__((aligned(16))) T Vt[DV * VP];
+  __shared__ __attribute__((aligned(16))) float Cs[64];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int cl = lane & 31, hh = lane >> 5;
+  int qt, bh;
+  map_block(blockIdx.x, nqt, nbh, qt, bh, true);
+  const int b = bh / HQ, hq = bh % HQ;
+  const int G = HQ / H, h = hq / G;
+  const int t0 = qt * 128;
+  const int tw = t0 + 32 * w;
+  const int tl = tw + cl;
+
+  const int64_t qs = (int64_t)HQ * DK, ks = (int64_t)H * DK, vs = (int64_t)H * DV;
+  const T* qb = q + ((int64_t)b * Tn) * qs + (int64_t)hq * DK;
+  const T* kb = k + ((int64_t)b * Tn) * ks + (int64_t)h * DK;
+  const T* vb = v + ((int64_t)b * Tn) * vs + (int64_t)h * DV;
+
+  // Q^T as B operands: lane (column tl) holds q[tl][16kk + 8hh .. +7].
+  v8_t<T> qop[DK / 16];
+#pragma unroll
+  for (int kk = 0; kk < DK / 16; ++kk)
+    qop[kk] = (tl < Tn) ? ld8<T>(qb + (int64_t)tl * qs + 16 * kk + 8 * hh) : zero8<T>();
+  float ct = 0.f;
+  if constexpr (DECAY) ct = (tl < Tn) ? c[((int64_t)b * Tn + tl) * HQ + hq] : 0.f;
+
+  f32x16 oacc[DV / 32];
+#pragma unroll
+  for (int db = 0; db < DV / 32; ++db) oacc[db] = f32x16{};
+  float dpart = 0.f;
+
+  const int s_end = min(t0 + 128, Tn);
+  const int nst = (s_end + 63) / 64;
+  for (int st = 0; st < nst; ++st) {
+    const int s0 = st * 64;
+    __syncthreads();
+    load_tile64<T, DK, KP, 1, true, false>(kb, s0, Tn, ks, Ks, nullptr, tid);
+    load_tile64<T, DV, 1, VP, false, true>(vb, s0, Tn, vs, nullptr, Vt, tid);
+    if constexpr (DECAY) {
+      if (tid < 64) Cs[tid] = (s0 + tid < Tn) ? c[((int64_t)b * Tn + s0 + tid) * HQ + hq] : 0.f;
+    }
+    __syncthreads();
+    if (s0 > tw + 31 || tw >= Tn) continue;  // whole tile after this wave's queries
+    const bool need_mask = (s0 + 63 > tw) || (s0 + 64 > Tn);
+
+    f32x16 a[2];
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      a[sb] = f32x16{};
+      const T* krow = Ks + (32 * sb + cl) * KP + 8 * hh;
+      if constexpr (!SUM) {
+#pragma unroll
+        for (int g = 0; g < M; ++g) {
+          f32x16 r{};
+#pragma unroll
+          for (int kk = 0; kk < KE; ++kk)
+            r = mma(ld8<T>(krow + g * E + 16 * kk), qop[g * KE + kk], r);
+          a[sb] += r * r;
+        }
+      } else {
+#pragma unroll
+        for (int gi = 0; gi < M; ++gi) {
+#pragma unroll
+          for (int gj = 0; gj < M; ++gj) {
+            f32x16 r{};
+#pragma unroll
+            for (int kk = 0; kk < KE; ++kk)
+              r = mma(ld8<T>(krow + gj * E + 16 * kk), qop[gi * KE + kk], r);
+            a[sb] += r * r;
+          }
+        }
+      }
+      // element 4i+r of block sb is key s0 + 32sb + 8i + 4hh + r, query tl
+      if constexpr (DECAY) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f32x4 cs = *reinterpret_cast<const f32x4*>(Cs + 32 * sb + 8 * i + 4 * hh);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) a[sb][4 * i + r] *= __expf(fminf(ct - cs[r], 0.f));
+        }
+      }
+      if (need_mask) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int s = s0 + 32 * sb + 8 * i + 4 * hh + r;
+            if (s > tl || s >= Tn) a[sb][4 * i + r] = 0.f;
+          }
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) dpart += a[sb][e];
+    }
+
+    // O^T[dv][t] += sum_s V^T[dv][s] P^T[s][t]
+#pragma unroll
+    for (int ks4 = 0; ks4 < 4; ++ks4) {
+      const v8_t<T> pb = c_to_b<T>(a[ks4 >> 1], ks4 & 1);
+#pragma unroll
+      for (int db = 0; db < DV / 32; ++db) {
+        const T* vrow = Vt + (32 * db + cl) * VP + 32 * (ks4 >> 1);
+        oacc[db] = mma(ld_tr_op<T>(vrow, ks4 & 1, hh), pb, oacc[db]);
+      }
+    }
+  }
+
+  const float dsum = dpart + __shfl_xor(dpart, 32);
+  if (tl < Tn) {
+    const float inv = dsum > 0.f ? 1.f / dsum : 1.f;
+    T* orow = o + (((int64_t)b * Tn + tl) * HQ + hq) * DV;
+#pragma unroll
+    for (int db = 0; db < DV / 32; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        st4<T>(orow + 32 * db + 8 * i + 4 * hh,
+               to4<T>(oacc[db][4 * i] * inv, oacc[db][4 * i + 1] * inv,
+                      oacc[db][4 * i + 2] * inv, oacc[db][4 * i + 3] * inv));
+    if (hh == 0) den[((int64_t)b * Tn + tl) * HQ + hq] = dsum * scale2;
+  }
+}
+
+template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
+hipError_t launch_kata_fwd(const KataArgs& a, hipStream_t stream) {
+  const int nqt = (a.T + 127) / 128;
+  const int nbh = a.B * a.HQ;
+  dim3 grid(nqt * nbh), block(256);
+  kata_fwd_kernel<T, DK, DV, M, SUM, DECAY><<<grid, block, 0, stream>>>(
+      (const T*)a.q, (const T*)a.k, (const T*)a.v, a.c, (T*)a.o, a.den, a.T, a.HQ, a.H,
+      a.scale * a.scale, nqt, nbh);
+  return hipGetLastError();
+}
+
+#define LINATT_FWD_INST(T, DK, DV, M)                                                  \
+  template hipError_t launch_kata_fwd<T, DK, DV, M, false, false>(const KataArgs&, hipStream_t); \
+  template hipError_t launch_kata_fwd<T, DK, DV, M, true, false>(const KataArgs&, hipStream_t);  \
+  template hipError_t launch_kata_fwd<T, DK, DV, M, false, true>(const KataArgs&, hipStream_t);
+
+LINATT_KATA_SHAPES(LINATT_FWD_INST)
+
+}  // namespace linatt

@@ -53,7 +53,7 @@ def delta_rule_recurrent(q, k, v, beta, g=None, scale=None, initial_state=None,
     if use_qk_l2norm:
         q, k = l2norm(q), l2norm(k)
     S = (initial_state if initial_state is not None
-         else torch.zeros(B, H, K, V, dtype=q.dtype))
+         else torch.zeros(B, H, K, V, dtype=q.dtype, device=q.device))
     outs = []
     for t in range(T):
         qt, kt, vt, bt = q[:, t], k[:, t], v[:, t], beta[:, t]
@@ -87,8 +87,9 @@ def delta_rule_chunked(q, k, v, beta, g=None, scale=None, initial_state=None,
     if use_qk_l2norm:
         q, k = l2norm(q), l2norm(k)
     dt = q.dtype
+    dev = q.device
     S = (initial_state if initial_state is not None
-         else torch.zeros(B, H, K, V, dtype=dt))
+         else torch.zeros(B, H, K, V, dtype=dt, device=dev))
     qh, kh, vh = (x.transpose(1, 2) for x in (q, k, v))  # (B,H,T,D)
     bh = beta.transpose(1, 2)  # (B,H,T)
     gh = g.transpose(1, 2) if g is not None else None
@@ -100,12 +101,12 @@ def delta_rule_chunked(q, k, v, beta, g=None, scale=None, initial_state=None,
         if gh is not None:
             Gc = torch.cumsum(gh[:, :, c0:c0 + chunk], -1)
         else:
-            Gc = torch.zeros(B, H, C, dtype=dt)
+            Gc = torch.zeros(B, H, C, dtype=dt, device=dev)
         Dg = torch.exp(Gc[..., :, None] - Gc[..., None, :])  # (B,H,C,C)
-        strict = torch.tril(torch.ones(C, C, dtype=torch.bool), -1)
-        lower = torch.tril(torch.ones(C, C, dtype=torch.bool))
+        strict = torch.tril(torch.ones(C, C, dtype=torch.bool, device=dev), -1)
+        lower = torch.tril(torch.ones(C, C, dtype=torch.bool, device=dev))
         A = (bc[..., :, None] * (Kc @ Kc.transpose(-1, -2)) * Dg).masked_fill(~strict, 0.0)
-        eye = torch.eye(C, dtype=dt).expand(B, H, C, C)
+        eye = torch.eye(C, dtype=dt, device=dev).expand(B, H, C, C)
         Tm = torch.linalg.solve_triangular(eye + A, eye, upper=False, unitriangular=True)
         W = Tm @ (Kc * (bc * torch.exp(Gc))[..., None])
         U = Tm @ (Vc * bc[..., None])

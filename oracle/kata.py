@@ -16,7 +16,9 @@ Conventions (reference ``kata/parallel_kata_attn.py``):
   kernel's safe divide (``den > 0`` else 1), ``kernels/parallel_kata.py:193-197``.
 * backward clamps ``den`` at ``1e-12`` (``parallel_kata_attn.py:79``).
 
-Every function upcasts its inputs to float64 and returns float64 tensors.
+Every function upcasts its inputs to float64 and returns float64 tensors
+(``kata_scores``/``kata_fwd``/``kata_bwd`` take ``work_dtype`` so the bench's
+CPU baseline can time the same restatement in float32).
 """
 
 from __future__ import annotations
@@ -59,7 +61,7 @@ def _group_dots(q, k, M, variant):
     raise ValueError(f"unknown variant {variant!r}")
 
 
-def kata_scores(q, k, num_groups, scale=None, variant="concat", c=None):
+def kata_scores(q, k, num_groups, scale=None, variant="concat", c=None, work_dtype=F64):
     """Causal score matrix ``A`` ``(B,HQ,T,T)`` in float64.
 
     Follows ``kernels/parallel_kata.py:115-191`` (scale applied to the dot
@@ -67,8 +69,8 @@ def kata_scores(q, k, num_groups, scale=None, variant="concat", c=None):
     ``c`` ``(B,T,HQ)``, the extra factor ``exp(min(c_t - c_s, 0))``
     (``kernels/parallel_kata.py:128-133, 169-179``).
     """
-    q = q.to(F64)
-    k = _expand_kv(k.to(F64), q.shape[2])
+    q = q.to(work_dtype)
+    k = _expand_kv(k.to(work_dtype), q.shape[2])
     dk = q.shape[-1]
     if scale is None:
         scale = default_scale(dk, num_groups)
@@ -78,15 +80,15 @@ def kata_scores(q, k, num_groups, scale=None, variant="concat", c=None):
     else:
         A = (qk * qk).sum(dim=(-2, -1))
     T = q.shape[1]
-    causal = torch.tril(torch.ones(T, T, dtype=torch.bool))
+    causal = torch.tril(torch.ones(T, T, dtype=torch.bool, device=q.device))
     A = A * causal
     if c is not None:
-        cH = c.to(F64).transpose(1, 2)  # (B,HQ,T)
+        cH = c.to(work_dtype).transpose(1, 2)  # (B,HQ,T)
         A = A * torch.exp(torch.clamp(cH[..., :, None] - cH[..., None, :], max=0.0))
     return A
 
 
-def kata_fwd(q, k, v, num_groups=4, scale=None, variant="concat", c=None):
+def kata_fwd(q, k, v, num_groups=4, scale=None, variant="concat", c=None, work_dtype=F64):
     """Forward ``(o, den)`` in float64: the kernel contract of
     ``parallel_kata_attn_fwd_impl`` (``parallel_kata_attn.py:211-288``) and
     ``parallel_kata_attn_sum_fwd_impl`` (``:539-576``).
@@ -96,8 +98,8 @@ def kata_fwd(q, k, v, num_groups=4, scale=None, variant="concat", c=None):
     (``kernels/parallel_kata.py:193-197``).
     """
     HQ = q.shape[2]
-    A = kata_scores(q, k, num_groups, scale, variant, c)  # (B,HQ,T,T)
-    vf = _expand_kv(v.to(F64), HQ).permute(0, 2, 1, 3)  # (B,HQ,T,dv)
+    A = kata_scores(q, k, num_groups, scale, variant, c, work_dtype)  # (B,HQ,T,T)
+    vf = _expand_kv(v.to(work_dtype), HQ).permute(0, 2, 1, 3)  # (B,HQ,T,dv)
     num = A @ vf
     den = A.sum(-1)  # (B,HQ,T)
     den_safe = torch.where(den > 0, den, torch.ones_like(den))
@@ -105,7 +107,7 @@ def kata_fwd(q, k, v, num_groups=4, scale=None, variant="concat", c=None):
     return o.permute(0, 2, 1, 3).contiguous(), den.permute(0, 2, 1).contiguous()
 
 
-def kata_bwd(q, k, v, o, den, do, num_groups=4, scale=None, variant="concat"):
+def kata_bwd(q, k, v, o, den, do, num_groups=4, scale=None, variant="concat", work_dtype=F64):
     """Explicit backward ``(dq, dk, dv)`` in float64.
 
     Restates ``parallel_kata_attn_bwd`` (``parallel_kata_attn.py:49-146``) for
@@ -123,21 +125,21 @@ def kata_bwd(q, k, v, o, den, do, num_groups=4, scale=None, variant="concat"):
     G = HQ // H
     if scale is None:
         scale = default_scale(dk, M)
-    qf = q.to(F64)
-    kf = _expand_kv(k.to(F64), HQ)
-    vf = _expand_kv(v.to(F64), HQ)
-    dof = do.to(F64)
-    Df = den.to(F64).clamp_min(1e-12)
+    qf = q.to(work_dtype)
+    kf = _expand_kv(k.to(work_dtype), HQ)
+    vf = _expand_kv(v.to(work_dtype), HQ)
+    dof = do.to(work_dtype)
+    Df = den.to(work_dtype).clamp_min(1e-12)
     qk = _group_dots(qf, kf, M, variant) * scale
     if variant == "concat":
         A = (qk * qk).sum(-1)
     else:
         A = (qk * qk).sum(dim=(-2, -1))
-    causal = torch.tril(torch.ones(T, T, dtype=torch.bool))
+    causal = torch.tril(torch.ones(T, T, dtype=torch.bool, device=q.device))
     A = A * causal
     Dh = Df.permute(0, 2, 1)  # (B,HQ,T)
     P = A / Dh[..., None]
-    delta = (o.to(F64) * dof).sum(-1).permute(0, 2, 1)  # (B,HQ,T)
+    delta = (o.to(work_dtype) * dof).sum(-1).permute(0, 2, 1)  # (B,HQ,T)
     do_p = dof.permute(0, 2, 1, 3)
     v_p = vf.permute(0, 2, 1, 3)
     dV = P.transpose(-1, -2) @ do_p  # (B,HQ,T,dv)
@@ -178,7 +180,7 @@ def kata_decay_ref(q, k, v, c, num_groups, scale):
     A = ((scale * qk) ** 2).sum(-1)
     cH = c.transpose(1, 2)
     dec = torch.exp(torch.clamp(cH[:, :, :, None] - cH[:, :, None, :], max=0.0))
-    tri = torch.tril(torch.ones(T, T, dtype=A.dtype))
+    tri = torch.tril(torch.ones(T, T, dtype=A.dtype, device=A.device))
     A = A * dec * tri
     return torch.einsum("bhts,bshd->bthd", A, v) / (
         A.sum(-1).transpose(1, 2)[..., None] + 1e-20
@@ -216,7 +218,7 @@ def spd_concat(x: torch.Tensor, k_splits: int) -> torch.Tensor:
     if e == 1:
         return diag.reshape(*prefix, k_splits)
     outer = g.unsqueeze(-1) * g.unsqueeze(-2)
-    ii, jj = torch.tril_indices(e, e, offset=-1)
+    ii, jj = torch.tril_indices(e, e, offset=-1, device=x.device)
     off = outer[..., ii, jj] * math.sqrt(2.0)
     return torch.cat([diag, off], dim=-1).reshape(*prefix, k_splits * (e * (e + 1) // 2))
 
@@ -321,15 +323,16 @@ def kata_prefill_fwd_state_form(q, k, v, num_groups=4, scale=None, chunk=64, eps
     s = math.sqrt(scale)
     q, k, v = (x.to(F64) for x in (q, k, v))
     P = num_groups * (D // num_groups) ** 2
-    S = torch.zeros(B, H, P, v.shape[-1], dtype=F64)
-    z = torch.zeros(B, H, P, dtype=F64)
+    S = torch.zeros(B, H, P, v.shape[-1], dtype=F64, device=q.device)
+    z = torch.zeros(B, H, P, dtype=F64, device=q.device)
     outs, dens = [], []
     for c0 in range(0, T, chunk):
         qc, kc, vc = q[:, c0:c0 + chunk], k[:, c0:c0 + chunk], v[:, c0:c0 + chunk]
         pq = spd_full(qc * s, num_groups)  # (B,C,H,P)
         pk = spd_full(kc * s, num_groups)
         Cn = qc.shape[1]
-        A = torch.einsum("bthp,bshp->bhts", pq, pk) * torch.tril(torch.ones(Cn, Cn, dtype=F64))
+        A = torch.einsum("bthp,bshp->bhts", pq, pk) * torch.tril(
+            torch.ones(Cn, Cn, dtype=F64, device=q.device))
         num = torch.einsum("bthp,bhpv->bthv", pq, S) + torch.einsum("bhts,bshv->bthv", A, vc)
         den = torch.einsum("bthp,bhp->bth", pq, z) + A.sum(-1).transpose(1, 2)
         den = torch.clamp(den, min=eps)

@@ -1,0 +1,101 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+``include/linatt_hip.h`` declares, and rejects bad arguments with the
+documented status codes before touching the device."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "linatt_hip.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from linatt_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        from linatt_amd import build
+        build.build()
+    return _lib.load()
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(linatt_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 6
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in linatt_hip.h but not exported"
+
+
+def test_python_signatures_cover_header():
+    from linatt_amd import _lib
+    assert set(declared_functions()) == set(_lib.SIGNATURES)
+
+
+def test_version_and_support(lib):
+    assert lib.linatt_abi_version() == 1
+    BF16, F32, F16 = 1, 0, 2
+    for dt in (BF16, F32, F16):
+        for M in (1, 2, 4):
+            assert lib.linatt_kata_supported(dt, 64, 64, M, 0, 0) == 1
+            assert lib.linatt_kata_supported(dt, 64, 64, M, 1, 0) == 1
+            assert lib.linatt_kata_supported(dt, 64, 64, M, 0, 1) == 1
+            assert lib.linatt_kata_supported(dt, 64, 64, M, 1, 1) == 0  # decay is concat-only
+    assert lib.linatt_kata_supported(BF16, 48, 64, 3, 0, 0) == 0
+    assert lib.linatt_kata_bwd_workspace_bytes(2, 10, 3) == 2 * 10 * 3 * 4
+    assert lib.linatt_kata_bwd_workspace_bytes(0, 10, 3) == 0
+
+
+FAKE = ctypes.c_void_p(1 << 20)  # aligned, never dereferenced on the host
+
+
+def _fwd(lib, **kw):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, c=None, o=FAKE, den=FAKE, B=1, T=8, HQ=2, H=2, dk=64,
+             dv=64, M=4, scale=0.25, variant=0, dtype=1, stream=None)
+    a.update(kw)
+    return lib.linatt_kata_fwd(a["q"], a["k"], a["v"], a["c"], a["o"], a["den"], a["B"], a["T"],
+                               a["HQ"], a["H"], a["dk"], a["dv"], a["M"], a["scale"],
+                               a["variant"], a["dtype"], a["stream"])
+
+
+def test_fwd_argument_errors(lib):
+    EINVAL, EUNSUP = -1, -2
+    assert _fwd(lib, T=0) == EINVAL
+    assert b"non-positive" in lib.linatt_last_error()
+    assert _fwd(lib, HQ=3, H=2) == EINVAL
+    assert b"GQA" in lib.linatt_last_error()
+    assert _fwd(lib, dk=64, M=3) == EINVAL
+    assert _fwd(lib, scale=0.0) == EINVAL
+    assert _fwd(lib, variant=7) == EINVAL
+    assert _fwd(lib, dtype=9) == EINVAL
+    assert _fwd(lib, q=None) == EINVAL
+    assert _fwd(lib, k=ctypes.c_void_p((1 << 20) + 2)) == EINVAL
+    assert b"aligned" in lib.linatt_last_error()
+    assert _fwd(lib, c=FAKE, variant=1) == EUNSUP
+    assert _fwd(lib, dk=48, M=3) == EUNSUP
+    assert b"no kernel compiled" in lib.linatt_last_error()
+
+
+def test_bwd_argument_errors(lib):
+    EINVAL, EUNSUP = -1, -2
+    f = lambda **kw: lib.linatt_kata_bwd(  # noqa: E731
+        FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, kw.get("ws", FAKE),
+        1, 8, 2, 2, kw.get("dk", 64), 64, kw.get("M", 4), 0.25, 0, 1, None)
+    assert f(ws=None) == EINVAL
+    assert f(dk=48, M=3) == EUNSUP
+    assert f(dk=64, M=5) == EINVAL
+
+
+def test_python_layer_rejects_cpu_tensors(lib):
+    import torch
+    from linatt_amd import parallel_kata_attn as P
+    q = torch.randn(1, 4, 1, 64)
+    with pytest.raises(RuntimeError, match="only on a ROCm GPU"):
+        P.parallel_kata_attn_fwd(q, q, q)
