@@ -105,6 +105,30 @@ __device__ __forceinline__ v8_t<T> c_to_b(const f32x16& a, int j) {
   }
 }
 
+// acc + sum of the 8 elements of an operand, in fp32.  For 16-bit types one
+// v_dot2 against (1, 1) adds two elements, so a row sum over the rounded
+// operand costs half an instruction per element.
+template <typename T>
+__device__ __forceinline__ float sum8(const v8_t<T>& p, float acc) {
+  if constexpr (__is_same(T, __bf16)) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{p[2 * j], p[2 * j + 1]}, one, acc, false);
+  } else if constexpr (__is_same(T, _Float16)) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc = __builtin_amdgcn_fdot2(f16x2{p[2 * j], p[2 * j + 1]}, one, acc, false);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc += p[j];
+  }
+  return acc;
+}
+
 template <typename T>
 __device__ __forceinline__ v4_t<T> to4(float a, float b, float c, float d) {
   f32x4 f{a, b, c, d};

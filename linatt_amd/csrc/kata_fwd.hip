@@ -13,6 +13,9 @@
 //
 // scale^2 is folded into den only: o is scale-invariant.  Where den is not
 // positive the output row is left unnormalised (the reference's safe divide).
+// den is accumulated from the weights as rounded for the P.V product
+// (v.dtype, as the reference's b_scores.to(b_v.dtype)); it differs from the
+// fp32 sum by at most one rounding unit of that type.
 //
 // Work split: a workgroup owns 128 queries of one (batch, query head); each
 // of its four waves owns 32 queries.  Key tiles of 64 rows stream through
@@ -126,14 +129,15 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_fwd_kernel(
             if (s > tl || s >= Tn) a[sb][4 * i + r] = 0.f;
           }
       }
-#pragma unroll
-      for (int e = 0; e < 16; ++e) dpart += a[sb][e];
     }
 
-    // O^T[dv][t] += sum_s V^T[dv][s] P^T[s][t]
+    // O^T[dv][t] += sum_s V^T[dv][s] P^T[s][t].  den sums the same rounded
+    // weights the product uses, so every output row is an exact convex
+    // combination of v rows (a lone key gives o = v exactly).
 #pragma unroll
     for (int ks4 = 0; ks4 < 4; ++ks4) {
       const v8_t<T> pb = c_to_b<T>(a[ks4 >> 1], ks4 & 1);
+      dpart = sum8<T>(pb, dpart);
 #pragma unroll
       for (int db = 0; db < DV / 32; ++db) {
         const T* vrow = Vt + (32 * db + cl) * VP + 32 * (ks4 >> 1);
