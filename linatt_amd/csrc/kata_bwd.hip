@@ -163,6 +163,8 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
   constexpr int KE = E / 16;
   constexpr int PAD = (sizeof(T) == 2 ? 8 : 4);
   constexpr int QP = DK + PAD, OP = DV + PAD, TP = 64 + 4;
+  constexpr float kPScale = __is_same(T, _Float16) ? 4096.f : 1.f;
+  constexpr float kPInv = 1.f / kPScale;
   __shared__ __attribute__((aligned(16))) T Qs[64 * QP];
   __shared__ __attribute__((aligned(16))) T Qt[DK * TP];
   __shared__ __attribute__((aligned(16))) T Os[64 * OP];
@@ -282,7 +284,9 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
               }
             }
         }
-        const f32x16 P = A * pdv;
+        // fp16 keeps P in [0, 2^12] so small weights stay out of its subnormal
+        // range (bf16 and fp32 have the fp32 exponent range); undone at the store
+        const f32x16 P = A * (pdv * kPScale);
         const f32x16 xs = x * pdv;
         // dV^T[dv][s] += sum_t dO^T[dv][t] P[t][s]
 #pragma unroll
@@ -345,7 +349,8 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         st4<T>(dvrow + 32 * db + 8 * i + 4 * hh,
-               to4<T>(dva[db][4 * i], dva[db][4 * i + 1], dva[db][4 * i + 2], dva[db][4 * i + 3]));
+               to4<T>(dva[db][4 * i] * kPInv, dva[db][4 * i + 1] * kPInv,
+                      dva[db][4 * i + 2] * kPInv, dva[db][4 * i + 3] * kPInv));
   }
 }
 
