@@ -69,6 +69,12 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_fwd_kernel(
 #pragma unroll
   for (int db = 0; db < DV / 32; ++db) oacc[db] = f32x16{};
   float dpart = 0.f;
+  // fp16 only: the weights of query tl are multiplied by the power of two pe
+  // that puts the running row maximum in [2^11, 2^12) before rounding, so
+  // small weights stay out of fp16's subnormal range; oacc and dpart are
+  // rescaled (exactly) whenever pe changes, and pe cancels in o.
+  constexpr bool kRescale = __is_same(T, _Float16);
+  float pe = 1.f, mrun = 0.f;
 
   const int s_end = min(t0 + 128, Tn);
   const int nst = (s_end + 63) / 64;
@@ -131,6 +137,28 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_fwd_kernel(
       }
     }
 
+    if constexpr (kRescale) {
+      float mx = 0.f;
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, a[sb][e]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      if (mx > mrun) {
+        int ex;
+        frexpf(mx, &ex);
+        const float pnew = ldexpf(1.f, 12 - max(ex, -100));
+        const float ratio = pnew / pe;
+#pragma unroll
+        for (int db = 0; db < DV / 32; ++db) oacc[db] *= ratio;
+        dpart *= ratio;
+        pe = pnew;
+        mrun = mx;
+      }
+      a[0] *= pe;
+      a[1] *= pe;
+    }
+
     // O^T[dv][t] += sum_s V^T[dv][s] P^T[s][t].  den sums the same rounded
     // weights the product uses, so every output row is an exact convex
     // combination of v rows (a lone key gives o = v exactly).
@@ -157,7 +185,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_fwd_kernel(
         st4<T>(orow + 32 * db + 8 * i + 4 * hh,
                to4<T>(oacc[db][4 * i] * inv, oacc[db][4 * i + 1] * inv,
                       oacc[db][4 * i + 2] * inv, oacc[db][4 * i + 3] * inv));
-    if (hh == 0) den[((int64_t)b * Tn + tl) * HQ + hq] = dsum * scale2;
+    if (hh == 0) den[((int64_t)b * Tn + tl) * HQ + hq] = dsum * (scale2 / pe);
   }
 }
 

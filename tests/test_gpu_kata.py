@@ -31,10 +31,10 @@ def mar(x, ref, floor=0.0):
 
 
 def grad_floors(q, k, v, do):
-    """1% of the natural gradient scales: o is invariant to the scale of q
+    """10% of the natural gradient scales: o is invariant to the scale of q
     (and of k), so |dq| ~ |dO||v|/|q| and |dk| ~ |dO||v|/|k|."""
     m = lambda t: t.detach().abs().max().item()  # noqa: E731
-    return {"dq": 1e-2 * m(do) * m(v) / m(q), "dk": 1e-2 * m(do) * m(v) / m(k), "dv": 0.0}
+    return {"dq": 0.1 * m(do) * m(v) / m(q), "dk": 0.1 * m(do) * m(v) / m(k), "dv": 0.0}
 
 
 def gen(shape, seed, std=1.0):
