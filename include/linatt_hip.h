@@ -86,6 +86,53 @@ int linatt_kata_bwd_dkdv(const void* q, const void* k, const void* v, const void
                          void* workspace, int B, int T, int HQ, int H, int dk_dim, int dv_dim,
                          int num_groups, float scale, int variant, int dtype, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Chunked (gated) delta rule (DeltaNet / GatedDeltaNet), chunks of 64 tokens.
+ * Replaces fla.ops.delta_rule.chunk_delta_rule and
+ * fla.ops.gated_delta_rule.chunk_gated_delta_rule of the third-party package
+ * flash-linear-attention==0.5.0 (pinned at scripts/setup.sh:27 of the
+ * reference; reached through configs/model/200m/delta_net_200m.yaml:3 and
+ * gated_deltanet_200m.yaml:4).
+ *   q, k (B,T,H,dk), v (B,T,H,dv) [dtype]; beta, g (B,T,H) float32 (g is the
+ *   per-token log decay, NULL for the ungated rule); h0, ht (B,H,dk,dv)
+ *   float32, each optional (NULL: zero initial state / not returned).
+ *   o (B,T,H,dv) [dtype].  scale multiplies q (> 0).
+ * The forward fills `ctx` (linatt_delta_ctx_bytes) with what the backward
+ * reads; keep it unchanged between the two calls.
+ * ------------------------------------------------------------------------- */
+
+/* 1 if a kernel is compiled for (dtype, dk, dv), else 0.  No device work. */
+int linatt_delta_supported(int dtype, int dk, int dv);
+
+/* Bytes of the forward context and of the backward scratch (0 on bad shape). */
+size_t linatt_delta_ctx_bytes(int B, int T, int H, int dk, int dv, int dtype);
+size_t linatt_delta_bwd_workspace_bytes(int B, int T, int H, int dk, int dv, int dtype);
+
+/* Forward: o and (optionally) the final state ht. */
+int linatt_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
+                     const float* g, const float* h0, void* o, float* ht, void* ctx, int B,
+                     int T, int H, int dk, int dv, float scale, int dtype, void* stream);
+
+/* Backward for the loss <o, dout> + <ht, dht> (dht may be NULL): dq, dk, dv
+ * [dtype], dbeta (B,T,H) float32, dg (B,T,H) float32 (required when g is
+ * given), dh0 (B,H,dk,dv) float32 (optional).  Same inputs as the forward
+ * plus its ctx; workspace: linatt_delta_bwd_workspace_bytes. */
+int linatt_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
+                     const float* g, const float* h0, const void* dout, const float* dht,
+                     const void* ctx, void* workspace, void* dq, void* dk, void* dv,
+                     float* dbeta, float* dg, float* dh0, int B, int T, int H, int dk_dim,
+                     int dv_dim, float scale, int dtype, void* stream);
+
+/* Row L2 normalisation over the last dim of a contiguous (n, d) array:
+ * y = x / sqrt(sum x^2 + eps), rstd (n) float32 = 1 / sqrt(sum x^2 + eps);
+ * backward dx = rstd (dy - y <y, dy>).  The normalisation fla applies to q
+ * and k under use_qk_l2norm_in_kernel=True (DeltaNet configs set
+ * qk_norm: l2, configs/model/200m/delta_net_200m.yaml:13). */
+int linatt_l2norm_fwd(const void* x, void* y, float* rstd, int n, int d, float eps, int dtype,
+                      void* stream);
+int linatt_l2norm_bwd(const void* y, const float* rstd, const void* dy, void* dx, int n, int d,
+                      int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

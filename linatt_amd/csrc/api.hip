@@ -5,7 +5,9 @@
 #include <string>
 
 #include "../../include/linatt_hip.h"
+#include "delta_kernels.h"
 #include "kata_kernels.h"
+#include "misc_kernels.h"
 
 namespace {
 
@@ -85,6 +87,45 @@ bool compiled(int dtype, int dk, int dv, int M) {
   LINATT_KATA_SHAPES(LINATT_HAS)
 #undef LINATT_HAS
   return false;
+}
+
+bool delta_compiled(int dtype, int dk, int dv) {
+#define LINATT_HAS_D(T, DK_, DV_) \
+  if (dtype == dtype_of<T>() && dk == DK_ && dv == DV_) return true;
+  LINATT_DELTA_SHAPES(LINATT_HAS_D)
+#undef LINATT_HAS_D
+  return false;
+}
+
+hipError_t dispatch_delta(const DeltaArgs& a, int dtype, int dk, int dv, bool gated, bool bwd,
+                          hipStream_t s) {
+#define LINATT_TRY_D(T, DK_, DV_)                                                         \
+  if (dtype == dtype_of<T>() && dk == DK_ && dv == DV_) {                                 \
+    if (bwd) return gated ? launch_delta_bwd<T, DK_, DV_, true>(a, s)                    \
+                          : launch_delta_bwd<T, DK_, DV_, false>(a, s);                  \
+    return gated ? launch_delta_fwd<T, DK_, DV_, true>(a, s) : launch_delta_fwd<T, DK_, DV_, false>(a, s); \
+  }
+  LINATT_DELTA_SHAPES(LINATT_TRY_D)
+#undef LINATT_TRY_D
+  return hipErrorInvalidValue;
+}
+
+int elt_bytes(int dtype) { return dtype == LINATT_FLOAT32 ? 4 : 2; }
+
+int check_delta(const char* fn, int B, int T, int H, int dk, int dv, float scale, int dtype) {
+  char buf[160];
+  snprintf(buf, sizeof buf, "B=%d T=%d H=%d dk=%d dv=%d", B, T, H, dk, dv);
+  if (B <= 0 || T <= 0 || H <= 0 || dk <= 0 || dv <= 0)
+    return fail(LINATT_EINVAL, std::string(fn) + ": non-positive dimension (" + buf + ")");
+  if (!(scale > 0.f)) return fail(LINATT_EINVAL, std::string(fn) + ": scale must be positive");
+  if (dtype != LINATT_FLOAT32 && dtype != LINATT_BFLOAT16 && dtype != LINATT_FLOAT16)
+    return fail(LINATT_EINVAL, std::string(fn) + ": unknown dtype");
+  if ((int64_t)B * H * (T + 63) > (int64_t)INT32_MAX / 2)
+    return fail(LINATT_EINVAL, std::string(fn) + ": B*H*T too large");
+  if (!delta_compiled(dtype, dk, dv))
+    return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": no kernel compiled for dtype " +
+                                         std::to_string(dtype) + " (" + buf + ")");
+  return LINATT_OK;
 }
 
 }  // namespace
@@ -189,6 +230,100 @@ int linatt_kata_bwd_dkdv(const void* q, const void* k, const void* v, const void
   return kata_bwd_entry("linatt_kata_bwd_dkdv", KATA_BWD_DKDV, q, k, v, o, den, dout, dq, dk,
                         dv, workspace, B, T, HQ, H, dk_dim, dv_dim, num_groups, scale, variant,
                         dtype, stream);
+}
+
+int linatt_delta_supported(int dtype, int dk, int dv) { return delta_compiled(dtype, dk, dv) ? 1 : 0; }
+
+size_t linatt_delta_ctx_bytes(int B, int T, int H, int dk, int dv, int dtype) {
+  if (B <= 0 || T <= 0 || H <= 0 || dk <= 0 || dv <= 0) return 0;
+  return delta_layout(B, T, H, dk, dv, elt_bytes(dtype)).ctx_bytes;
+}
+
+size_t linatt_delta_bwd_workspace_bytes(int B, int T, int H, int dk, int dv, int dtype) {
+  if (B <= 0 || T <= 0 || H <= 0 || dk <= 0 || dv <= 0) return 0;
+  return delta_layout(B, T, H, dk, dv, elt_bytes(dtype)).bwd_bytes;
+}
+
+int linatt_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
+                     const float* g, const float* h0, void* o, float* ht, void* ctx, int B,
+                     int T, int H, int dk, int dv, float scale, int dtype, void* stream) {
+  g_last_error.clear();
+  int st = check_delta("linatt_delta_fwd", B, T, H, dk, dv, scale, dtype);
+  if (st) return st;
+  if (!q || !k || !v || !beta || !o || !ctx)
+    return fail(LINATT_EINVAL, "linatt_delta_fwd: null tensor pointer");
+  const void* ps[] = {q, k, v, o, ctx, h0, ht};
+  for (const void* p : ps)
+    if (p && !aligned16(p))
+      return fail(LINATT_EINVAL, "linatt_delta_fwd: tensors must be 16-byte aligned");
+  DeltaArgs a{};
+  a.q = q; a.k = k; a.v = v; a.beta = beta; a.g = g; a.h0 = h0; a.o = o; a.ht = ht;
+  a.ctx = (char*)ctx;
+  a.B = B; a.T = T; a.H = H; a.NT = (T + kChunk - 1) / kChunk; a.scale = scale;
+  hipError_t e = dispatch_delta(a, dtype, dk, dv, g != nullptr, false, (hipStream_t)stream);
+  if (e != hipSuccess)
+    return fail(LINATT_ELAUNCH, std::string("linatt_delta_fwd: launch failed: ") + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
+int linatt_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
+                     const float* g, const float* h0, const void* dout, const float* dht,
+                     const void* ctx, void* workspace, void* dq, void* dk, void* dv,
+                     float* dbeta, float* dg, float* dh0, int B, int T, int H, int dk_dim,
+                     int dv_dim, float scale, int dtype, void* stream) {
+  g_last_error.clear();
+  int st = check_delta("linatt_delta_bwd", B, T, H, dk_dim, dv_dim, scale, dtype);
+  if (st) return st;
+  if (!q || !k || !v || !beta || !dout || !ctx || !workspace || !dq || !dk || !dv || !dbeta ||
+      (g && !dg))
+    return fail(LINATT_EINVAL, "linatt_delta_bwd: null tensor pointer");
+  const void* ps[] = {q, k, v, dout, ctx, workspace, dq, dk, dv, dht, dh0, h0};
+  for (const void* p : ps)
+    if (p && !aligned16(p))
+      return fail(LINATT_EINVAL, "linatt_delta_bwd: tensors must be 16-byte aligned");
+  DeltaArgs a{};
+  a.q = q; a.k = k; a.v = v; a.beta = beta; a.g = g; a.h0 = h0; a.dout = dout; a.dht = dht;
+  a.dq = dq; a.dk = dk; a.dv = dv; a.dbeta = dbeta; a.dg = dg; a.dh0 = dh0;
+  a.ctx = (char*)const_cast<void*>(ctx);
+  a.ws = (char*)workspace;
+  a.B = B; a.T = T; a.H = H; a.NT = (T + kChunk - 1) / kChunk; a.scale = scale;
+  hipError_t e = dispatch_delta(a, dtype, dk_dim, dv_dim, g != nullptr, true, (hipStream_t)stream);
+  if (e != hipSuccess)
+    return fail(LINATT_ELAUNCH, std::string("linatt_delta_bwd: launch failed: ") + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
+int linatt_l2norm_fwd(const void* x, void* y, float* rstd, int n, int d, float eps, int dtype,
+                      void* stream) {
+  g_last_error.clear();
+  if (n <= 0 || d <= 0) return fail(LINATT_EINVAL, "linatt_l2norm_fwd: non-positive size");
+  if (!x || !y || !rstd) return fail(LINATT_EINVAL, "linatt_l2norm_fwd: null tensor pointer");
+  if (!(eps >= 0.f)) return fail(LINATT_EINVAL, "linatt_l2norm_fwd: eps must be >= 0");
+  hipError_t e;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == LINATT_BFLOAT16) e = launch_l2norm_fwd<__bf16>(x, y, rstd, n, d, eps, s);
+  else if (dtype == LINATT_FLOAT16) e = launch_l2norm_fwd<_Float16>(x, y, rstd, n, d, eps, s);
+  else if (dtype == LINATT_FLOAT32) e = launch_l2norm_fwd<float>(x, y, rstd, n, d, eps, s);
+  else return fail(LINATT_EINVAL, "linatt_l2norm_fwd: unknown dtype");
+  if (e != hipSuccess)
+    return fail(LINATT_ELAUNCH, std::string("linatt_l2norm_fwd: launch failed: ") + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
+int linatt_l2norm_bwd(const void* y, const float* rstd, const void* dy, void* dx, int n, int d,
+                      int dtype, void* stream) {
+  g_last_error.clear();
+  if (n <= 0 || d <= 0) return fail(LINATT_EINVAL, "linatt_l2norm_bwd: non-positive size");
+  if (!y || !rstd || !dy || !dx) return fail(LINATT_EINVAL, "linatt_l2norm_bwd: null tensor pointer");
+  hipError_t e;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == LINATT_BFLOAT16) e = launch_l2norm_bwd<__bf16>(y, rstd, dy, dx, n, d, s);
+  else if (dtype == LINATT_FLOAT16) e = launch_l2norm_bwd<_Float16>(y, rstd, dy, dx, n, d, s);
+  else if (dtype == LINATT_FLOAT32) e = launch_l2norm_bwd<float>(y, rstd, dy, dx, n, d, s);
+  else return fail(LINATT_EINVAL, "linatt_l2norm_bwd: unknown dtype");
+  if (e != hipSuccess)
+    return fail(LINATT_ELAUNCH, std::string("linatt_l2norm_bwd: launch failed: ") + hipGetErrorString(e));
+  return LINATT_OK;
 }
 
 }  // extern "C"

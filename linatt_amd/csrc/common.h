@@ -194,3 +194,66 @@ __device__ __forceinline__ void map_block(int L, int ntiles, int nheads, int& ti
 }
 
 }  // namespace linatt
+
+namespace linatt {
+
+// Cooperative copy of a (64 x C) tile with type conversion and an optional
+// per-row scale: rows [row0, row0 + 64) of g (element type S, row stride
+// rs elements) go to LDS as T, natural (pitch NP, element [r][c]) and/or
+// transposed (pitch TP, element [c][r]).  Rows at or beyond nrows are zero;
+// rowscale (LDS, 64 floats, indexed by tile row) multiplies in fp32 before
+// the conversion.  4x4 element blocks per thread, coalesced global reads.
+template <typename S, typename T, int C, int NP, int TP, bool NAT, bool TRANS, int NT = 256>
+__device__ __forceinline__ void load_tile64x(const S* __restrict__ g, int row0, int nrows,
+                                             int64_t rs, T* nat, T* trans, int tid,
+                                             const float* rowscale) {
+  constexpr int CB = C / 4;
+  constexpr int NB = 16 * CB;
+#pragma unroll
+  for (int blk = tid; blk < NB; blk += NT) {
+    const int cb = blk % CB, rb = blk / CB;
+    float vals[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = row0 + 4 * rb + r;
+      const float sc = rowscale ? rowscale[4 * rb + r] : 1.f;
+      if (row < nrows) {
+        const S* p = g + (int64_t)row * rs + 4 * cb;
+        if constexpr (sizeof(S) == 4) {
+          const float4 x = *reinterpret_cast<const float4*>(p);
+          vals[r][0] = x.x * sc; vals[r][1] = x.y * sc; vals[r][2] = x.z * sc; vals[r][3] = x.w * sc;
+        } else {
+          const v4_t<S> x = ld4<S>(p);
+#pragma unroll
+          for (int cc = 0; cc < 4; ++cc) vals[r][cc] = (float)x[cc] * sc;
+        }
+      } else {
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) vals[r][cc] = 0.f;
+      }
+    }
+    if constexpr (NAT) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        st4<T>(nat + (4 * rb + r) * NP + 4 * cb, to4<T>(vals[r][0], vals[r][1], vals[r][2], vals[r][3]));
+    }
+    if constexpr (TRANS) {
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc)
+        st4<T>(trans + (4 * cb + cc) * TP + 4 * rb,
+               to4<T>(vals[0][cc], vals[1][cc], vals[2][cc], vals[3][cc]));
+    }
+  }
+}
+
+// 8 consecutive fp32 values converted to an MFMA operand of type T.
+template <typename T>
+__device__ __forceinline__ v8_t<T> ld8_f32(const float* p) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0];
+  const float4 b = reinterpret_cast<const float4*>(p)[1];
+  const f32x8 f{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  if constexpr (sizeof(T) == 2) return __builtin_convertvector(f, v8_t<T>);
+  else return f;
+}
+
+}  // namespace linatt

@@ -1,0 +1,437 @@
+// Chunked (gated) delta rule, forward, for gfx950.
+//
+// Replaces the forward of fla.ops.delta_rule.chunk_delta_rule and
+// fla.ops.gated_delta_rule.chunk_gated_delta_rule (third-party
+// flash-linear-attention==0.5.0, pinned at scripts/setup.sh:27 of the
+// reference; reached through model_type delta_net / gated_deltanet,
+// configs/model/200m/delta_net_200m.yaml:3, gated_deltanet_200m.yaml:4).
+// Algorithm: the WY/UT chunk form of Yang et al. (NeurIPS 2024) with the
+// gate of Yang, Kautz, Hatamizadeh (ICLR 2025).  Per chunk of 64 tokens
+// with G the chunk-local inclusive cumsum of g and gamma = G at the last
+// row:
+//
+//   A   = strict_lower(diag(beta) K K^T o e^(G_i - G_j))
+//   Tm  = (I + A)^-1                       (fp32, in LDS)
+//   W   = Tm diag(beta e^G) K,   U = Tm diag(beta) V
+//   Vn  = U - W S                          (S: state entering the chunk)
+//   o   = scale e^G o (Q S) + Aqk Vn,      Aqk = scale (Q K^T) o e^(G_i-G_j), j <= i
+//   S  <- e^gamma S + (diag(e^(gamma - G)) K)^T Vn
+//
+// Kernel 1 (delta_prep) is parallel over (batch, head, chunk): G, the Gram
+// matrix, the triangular solve, W, U and the transposed / pre-scaled
+// operand copies the state passes read.  Kernel 2 (delta_state_fwd) walks
+// the chunks in order: one wave per (batch, head, 32 value columns) keeps
+// its slice of S in MFMA accumulators and produces Vn, o and the per-chunk
+// states h with every operand read straight into registers.
+#include "common.h"
+#include "delta_kernels.h"
+
+namespace linatt {
+
+namespace {
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+}  // namespace
+
+DeltaLayout delta_layout(int B, int T, int H, int DK, int DV, int eb) {
+  DeltaLayout L{};
+  const size_t NT = (size_t)(T + kChunk - 1) / kChunk, Tp = NT * kChunk, BH = (size_t)B * H;
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
+  L.Gc = take(BH * Tp * 4);
+  L.Tm = take(BH * NT * 4096 * eb);
+  L.W = take(BH * Tp * DK * eb);
+  L.U = take(BH * Tp * DV * eb);
+  L.WT = take(BH * Tp * DK * eb);
+  L.KdT = take(BH * Tp * DK * eb);
+  L.QgT = take(BH * Tp * DK * eb);
+  L.Aqk = take(BH * NT * 4096 * eb);
+  L.AqkT = take(BH * NT * 4096 * eb);
+  L.h = take(BH * NT * DK * DV * eb);
+  L.Vn = take(BH * Tp * DV * eb);
+  L.ctx_bytes = off;
+  off = 0;
+  L.dVn = take(BH * Tp * DV * eb);
+  L.dh = take(BH * NT * DK * DV * eb);
+  L.dW = take(BH * Tp * DK * 4);
+  L.dKp = take(BH * Tp * DK * 4);
+  L.dGp = take(BH * Tp * 4);
+  L.bwd_bytes = off;
+  return L;
+}
+
+// ---------------------------------------------------------------------------
+// Kernel 1: per-chunk preparation.
+// ---------------------------------------------------------------------------
+template <typename T, int DK, int DV, bool GATED>
+__global__ __launch_bounds__(256) void delta_prep_kernel(DeltaArgs a, DeltaLayout L) {
+  constexpr int PK = DK + 8;   // natural K tile pitch
+  constexpr int PX = 64 + 8;   // transposed tile pitch
+  constexpr int PA = 68;       // fp32 A / Tm pitch
+  constexpr int XR = DK > DV ? DK : DV;
+  constexpr int U0 = (64 * PK > XR * PX ? 64 * PK : XR * PX);
+  __shared__ __attribute__((aligned(16))) T Un[U0];          // K natural, then X^T tiles
+  __shared__ __attribute__((aligned(16))) float As[64 * PA];  // A, then Tm as T (pitch PX)
+  __shared__ __attribute__((aligned(16))) float Ts[64 * PA];  // Tm fp32
+  __shared__ __attribute__((aligned(16))) float Gs[64], Bs[64], Sc[64];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int cl = lane & 31, hh = lane >> 5;
+  const int Tn = a.T, H = a.H, NT = a.NT;
+  const int c = blockIdx.x % NT, bh = blockIdx.x / NT;
+  const int b = bh / H, h = bh % H;
+  const int t0 = c * kChunk;
+  const size_t Tp = (size_t)NT * kChunk;
+  const size_t ci = (size_t)bh * NT + c;
+
+  T* Kn = Un;
+  T* Xt = Un;
+  T* Tt = reinterpret_cast<T*>(As);
+  float* Gc = reinterpret_cast<float*>(a.ctx + L.Gc);
+
+  const T* qb = (const T*)a.q + ((size_t)b * Tn * H + h) * DK;
+  const T* kb = (const T*)a.k + ((size_t)b * Tn * H + h) * DK;
+  const T* vb = (const T*)a.v + ((size_t)b * Tn * H + h) * DV;
+  const int64_t qks = (int64_t)H * DK, vs = (int64_t)H * DV;
+
+  // beta and G (inclusive cumsum of g; rows past T add 0, so G[63] = gamma).
+  if (tid < 64) {
+    const int t = t0 + tid;
+    float bt = 0.f, gt = 0.f;
+    if (t < Tn) {
+      bt = a.beta[((size_t)b * Tn + t) * H + h];
+      if constexpr (GATED) gt = a.g[((size_t)b * Tn + t) * H + h];
+    }
+    Bs[tid] = bt;
+    float x = gt;
+    if constexpr (GATED) {
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float y = __shfl_up(x, off);
+        if (tid >= off) x += y;
+      }
+      Gc[(size_t)bh * Tp + t0 + tid] = x;
+    }
+    Gs[tid] = x;
+  }
+  for (int idx = tid; idx < 64 * PA; idx += 256) Ts[idx] = 0.f;
+  load_tile64x<T, T, DK, PK, 1, true, false>(kb, t0, Tn, qks, Kn, nullptr, tid, nullptr);
+  __syncthreads();
+
+  // Gram (wave w: tile (w >> 1, w & 1)) -> A in LDS; Q K^T -> Aqk, Aqk^T.
+  {
+    const int ai = w >> 1, bj = w & 1;
+    f32x16 kk{};
+#pragma unroll
+    for (int s = 0; s < DK / 16; ++s)
+      kk = mma(ld8<T>(Kn + (32 * ai + cl) * PK + 16 * s + 8 * hh),
+               ld8<T>(Kn + (32 * bj + cl) * PK + 16 * s + 8 * hh), kk);
+    const int j = 32 * bj + cl;
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 32 * ai + 8 * I + 4 * hh + r;
+        float val = 0.f;
+        if (i > j) {
+          val = Bs[i] * kk[4 * I + r];
+          if constexpr (GATED) val *= __expf(Gs[i] - Gs[j]);
+        }
+        As[i * PA + j] = val;
+      }
+    // D[j][i] = k_j . q_i   (j-tile ai, i-tile bj; lane column i)
+    const int i = 32 * bj + cl;
+    const bool qv = t0 + i < Tn;
+    f32x16 qk{};
+#pragma unroll
+    for (int s = 0; s < DK / 16; ++s)
+      qk = mma(ld8<T>(Kn + (32 * ai + cl) * PK + 16 * s + 8 * hh),
+               qv ? ld8<T>(qb + (int64_t)(t0 + i) * qks + 16 * s + 8 * hh) : zero8<T>(), qk);
+    T* aq = (T*)(a.ctx + L.Aqk) + ci * 4096;
+    T* aqt = (T*)(a.ctx + L.AqkT) + ci * 4096;
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      float vals[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int jj = 32 * ai + 8 * I + 4 * hh + r;
+        float val = 0.f;
+        if (jj <= i) {
+          val = a.scale * qk[4 * I + r];
+          if constexpr (GATED) val *= __expf(Gs[i] - Gs[jj]);
+        }
+        vals[r] = val;
+        aqt[jj * 64 + i] = (T)val;
+      }
+      st4<T>(aq + i * 64 + 32 * ai + 8 * I + 4 * hh, to4<T>(vals[0], vals[1], vals[2], vals[3]));
+    }
+  }
+  __syncthreads();
+
+  // Tm = (I + A)^-1 by 16-row blocks: off-block rows from the finished
+  // rows (all threads), then forward substitution inside the diagonal block
+  // with one column per lane (wave 0).
+#pragma unroll 1
+  for (int R = 0; R < 4; ++R) {
+    if (R > 0) {
+      const int i = 16 * R + (tid >> 4);
+      const int cg = tid & 15;
+      for (int m = 0; m < R; ++m) {
+        const int cc = cg + 16 * m;
+        float y = 0.f;
+        for (int j = cc; j < 16 * R; ++j) y -= As[i * PA + j] * Ts[j * PA + cc];
+        Ts[i * PA + cc] = y;
+      }
+    }
+    __syncthreads();
+    if (tid < 64) {
+      const int cc = tid;
+      float x[16];
+#pragma unroll
+      for (int ii = 0; ii < 16; ++ii) {
+        const int i = 16 * R + ii;
+        float acc = (cc == i ? 1.f : 0.f) + (cc < 16 * R ? Ts[i * PA + cc] : 0.f);
+#pragma unroll
+        for (int jj = 0; jj < ii; ++jj) acc -= As[i * PA + 16 * R + jj] * x[jj];
+        x[ii] = (cc <= i) ? acc : 0.f;
+        Ts[i * PA + cc] = x[ii];
+      }
+    }
+    __syncthreads();
+  }
+
+  // Tm -> T (natural [i][j], pitch PX) over A, and to the context.
+  {
+    T* tmg = (T*)(a.ctx + L.Tm) + ci * 4096;
+    for (int idx = tid; idx < 4096; idx += 256) {
+      const int i = idx >> 6, j = idx & 63;
+      const T val = (T)Ts[i * PA + j];
+      Tt[i * PX + j] = val;
+      tmg[idx] = val;
+    }
+  }
+  if (tid < 64) Sc[tid] = a.scale * (GATED ? __expf(Gs[tid]) : 1.f);
+  __syncthreads();
+
+  // (scale e^G q)^T and (e^(gamma - G) k)^T per chunk, through LDS.
+  {
+    load_tile64x<T, T, DK, 1, PX, false, true>(qb, t0, Tn, qks, nullptr, Xt, tid, Sc);
+    __syncthreads();
+    T* dst = (T*)(a.ctx + L.QgT) + ci * DK * 64;
+    for (int idx = tid; idx < DK * 64; idx += 256) dst[idx] = Xt[(idx >> 6) * PX + (idx & 63)];
+    __syncthreads();
+    if (tid < 64) Sc[tid] = GATED ? __expf(Gs[63] - Gs[tid]) : 1.f;
+    __syncthreads();
+    load_tile64x<T, T, DK, 1, PX, false, true>(kb, t0, Tn, qks, nullptr, Xt, tid, Sc);
+    __syncthreads();
+    dst = (T*)(a.ctx + L.KdT) + ci * DK * 64;
+    for (int idx = tid; idx < DK * 64; idx += 256) dst[idx] = Xt[(idx >> 6) * PX + (idx & 63)];
+    __syncthreads();
+    if (tid < 64) Sc[tid] = Bs[tid] * (GATED ? __expf(Gs[tid]) : 1.f);
+    __syncthreads();
+  }
+
+  // W = Tm (diag(beta e^G) K): D[d][i] = sum_j Xt[d][j] Tt[i][j]; lane column i.
+  {
+    load_tile64x<T, T, DK, 1, PX, false, true>(kb, t0, Tn, qks, nullptr, Xt, tid, Sc);
+    __syncthreads();
+    const int it = w & 1;
+    const int i = 32 * it + cl;
+    T* wrow = (T*)(a.ctx + L.W) + ((size_t)bh * Tp + t0 + i) * DK;
+    T* wt = (T*)(a.ctx + L.WT) + ci * DK * 64;
+#pragma unroll
+    for (int m = 0; m < DK / 64; ++m) {
+      const int dt = (w >> 1) + 2 * m;
+      f32x16 acc{};
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        acc = mma(ld8<T>(Xt + (32 * dt + cl) * PX + 16 * s + 8 * hh),
+                  ld8<T>(Tt + i * PX + 16 * s + 8 * hh), acc);
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        const int d = 32 * dt + 8 * I + 4 * hh;
+        st4<T>(wrow + d, to4<T>(acc[4 * I], acc[4 * I + 1], acc[4 * I + 2], acc[4 * I + 3]));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wt[(d + r) * 64 + i] = (T)acc[4 * I + r];
+      }
+    }
+    __syncthreads();
+    if (tid < 64) Sc[tid] = Bs[tid];
+    __syncthreads();
+  }
+
+  // U = Tm (diag(beta) V).
+  {
+    load_tile64x<T, T, DV, 1, PX, false, true>(vb, t0, Tn, vs, nullptr, Xt, tid, Sc);
+    __syncthreads();
+    const int it = w & 1;
+    const int i = 32 * it + cl;
+    T* urow = (T*)(a.ctx + L.U) + ((size_t)bh * Tp + t0 + i) * DV;
+#pragma unroll
+    for (int m = 0; m < DV / 64; ++m) {
+      const int vt = (w >> 1) + 2 * m;
+      f32x16 acc{};
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        acc = mma(ld8<T>(Xt + (32 * vt + cl) * PX + 16 * s + 8 * hh),
+                  ld8<T>(Tt + i * PX + 16 * s + 8 * hh), acc);
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+        st4<T>(urow + 32 * vt + 8 * I + 4 * hh,
+               to4<T>(acc[4 * I], acc[4 * I + 1], acc[4 * I + 2], acc[4 * I + 3]));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel 2: sequential state pass + output.  One wave per (b, h, 32 value
+// columns); S[d][v] lives in DK/32 accumulator tiles with lane column v.
+// ---------------------------------------------------------------------------
+template <typename T, int DK, int DV, bool GATED>
+__global__ __launch_bounds__(64) void delta_state_fwd_kernel(DeltaArgs a, DeltaLayout L) {
+  constexpr int NDT = DK / 32;
+  constexpr int NVB = DV / 32;
+  const int lane = threadIdx.x, cl = lane & 31, hh = lane >> 5;
+  const int Tn = a.T, H = a.H, NT = a.NT;
+  const int vb = blockIdx.x % NVB, bh = blockIdx.x / NVB;
+  const int b = bh / H, h = bh % H;
+  const int v = 32 * vb + cl;
+  const size_t Tp = (size_t)NT * kChunk;
+
+  const T* qb = (const T*)a.q + ((size_t)b * Tn * H + h) * DK;
+  const int64_t qks = (int64_t)H * DK;
+  T* ob = (T*)a.o + ((size_t)b * Tn * H + h) * DV;
+  const int64_t os = (int64_t)H * DV;
+  const float* Gc = reinterpret_cast<const float*>(a.ctx + L.Gc) + (size_t)bh * Tp;
+  const T* Wg = (const T*)(a.ctx + L.W) + (size_t)bh * Tp * DK;
+  const T* Ug = (const T*)(a.ctx + L.U) + (size_t)bh * Tp * DV;
+  T* Vng = (T*)(a.ctx + L.Vn) + (size_t)bh * Tp * DV;
+
+  f32x16 S[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = 32 * dt + 8 * I + 4 * hh + r;
+        S[dt][4 * I + r] = a.h0 ? a.h0[((size_t)bh * DK + d) * DV + v] : 0.f;
+      }
+  }
+
+#pragma unroll 1
+  for (int c = 0; c < NT; ++c) {
+    const int t0 = c * kChunk;
+    const size_t ci = (size_t)bh * NT + c;
+    // state entering the chunk
+    T* hg = (T*)(a.ctx + L.h) + ci * DK * DV;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int d = 32 * dt + 8 * (e >> 2) + 4 * hh + (e & 3);
+        hg[d * DV + v] = (T)S[dt][e];
+      }
+
+    // P = W S and O = Q S; rows of this chunk in two 32-row tiles.
+    f32x16 P[2], O[2];
+    P[0] = P[1] = O[0] = O[1] = f32x16{};
+#pragma unroll
+    for (int db = 0; db < NDT; ++db)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const v8_t<T> ys = c_to_b<T>(S[db], j);
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+          const int ti = t0 + 32 * it + cl;
+          P[it] = mma(ld_tr_op<T>(Wg + (size_t)(t0 + 32 * it + cl) * DK + 32 * db, j, hh), ys, P[it]);
+          O[it] = mma(ti < Tn ? ld_tr_op<T>(qb + (int64_t)ti * qks + 32 * db, j, hh) : zero8<T>(),
+                      ys, O[it]);
+        }
+      }
+
+    // Vn = U - P (rows padded past T are zero in U and W)
+    f32x16 Vn[2];
+#pragma unroll
+    for (int it = 0; it < 2; ++it)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int i = 32 * it + 8 * (e >> 2) + 4 * hh + (e & 3);
+        const size_t off = (size_t)(t0 + i) * DV + v;
+        const float val = (float)Ug[off] - P[it][e];
+        Vn[it][e] = val;
+        Vng[off] = (T)val;
+      }
+
+    // o = scale e^G (Q S) + Aqk Vn
+    const T* aq = (const T*)(a.ctx + L.Aqk) + ci * 4096;
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        const int i = 32 * it + 8 * I + 4 * hh;
+        float f[4] = {a.scale, a.scale, a.scale, a.scale};
+        if constexpr (GATED) {
+          const f32x4 g4 = *reinterpret_cast<const f32x4*>(Gc + t0 + i);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) f[r] = a.scale * __expf(g4[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) O[it][4 * I + r] *= f[r];
+      }
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+          O[it] = mma(ld_tr_op<T>(aq + (32 * it + cl) * 64 + 32 * jt, jj, hh),
+                      c_to_b<T>(Vn[jt], jj), O[it]);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int t = t0 + 32 * it + 8 * (e >> 2) + 4 * hh + (e & 3);
+        if (t < Tn) ob[(int64_t)t * os + v] = (T)O[it][e];
+      }
+    }
+
+    // S <- e^gamma S + Kd^T Vn
+    const T* kd = (const T*)(a.ctx + L.KdT) + ci * DK * 64;
+    const float eg = GATED ? __expf(Gc[t0 + 63]) : 1.f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      if constexpr (GATED) S[dt] *= eg;
+#pragma unroll
+      for (int it = 0; it < 2; ++it)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+          S[dt] = mma(ld_tr_op<T>(kd + (32 * dt + cl) * 64 + 32 * it, jj, hh),
+                      c_to_b<T>(Vn[it], jj), S[dt]);
+    }
+  }
+
+  if (a.ht) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int d = 32 * dt + 8 * (e >> 2) + 4 * hh + (e & 3);
+        a.ht[((size_t)bh * DK + d) * DV + v] = S[dt][e];
+      }
+  }
+}
+
+template <typename T, int DK, int DV, bool GATED>
+hipError_t launch_delta_fwd(const DeltaArgs& a, hipStream_t stream) {
+  const DeltaLayout L = delta_layout(a.B, a.T, a.H, DK, DV, sizeof(T));
+  const int BH = a.B * a.H;
+  delta_prep_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  delta_state_fwd_kernel<T, DK, DV, GATED><<<dim3(BH * (DV / 32)), dim3(64), 0, stream>>>(a, L);
+  return hipGetLastError();
+}
+
+#define LINATT_DELTA_FWD_INST(T, DK, DV)                                              \
+  template hipError_t launch_delta_fwd<T, DK, DV, false>(const DeltaArgs&, hipStream_t); \
+  template hipError_t launch_delta_fwd<T, DK, DV, true>(const DeltaArgs&, hipStream_t);
+
+LINATT_DELTA_SHAPES(LINATT_DELTA_FWD_INST)
+
+}  // namespace linatt

@@ -1,0 +1,85 @@
+// Internal launch interface between the C-ABI layer (api.hip) and the
+// chunked (gated) delta-rule kernels.  Not part of the public header.
+//
+// Shapes: B batch, T tokens, H heads, DK key dim, DV value dim, chunks of
+// 64 tokens, NT = ceil(T / 64), Tp = 64 * NT.  q, k, v, o and their
+// gradients are time-major (B, T, H, D); beta, g, dbeta, dg are (B, T, H)
+// float32; states (B, H, DK, DV) float32.  Everything else lives in the
+// context / workspace buffers carved by delta_layout().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace linatt {
+
+constexpr int kChunk = 64;
+
+// Byte offsets of the forward context (kept from forward to backward) and of
+// the backward scratch.  Sub-buffers are 256-byte aligned.
+struct DeltaLayout {
+  // context (written by the forward, read by the backward)
+  size_t Gc;    // (B,H,Tp) f32  chunk-local inclusive cumsum of g (gated only)
+  size_t Tm;    // (B,H,NT,64,64) T  (I + A)^-1, natural [i][j]
+  size_t W;     // (B,H,Tp,DK) T  W = Tm diag(beta e^G) K
+  size_t U;     // (B,H,Tp,DV) T  U = Tm diag(beta) V
+  size_t WT;    // (B,H,NT,DK,64) T  W^T per chunk
+  size_t KdT;   // (B,H,NT,DK,64) T  (e^(gamma - G_i) k_i)^T per chunk
+  size_t QgT;   // (B,H,NT,DK,64) T  (scale e^G_i q_i)^T per chunk
+  size_t Aqk;   // (B,H,NT,64,64) T  scale (q_i.k_j) e^(G_i-G_j) [j <= i]
+  size_t AqkT;  // (B,H,NT,64,64) T  its transpose
+  size_t h;     // (B,H,NT,DK,DV) T  state entering each chunk
+  size_t Vn;    // (B,H,Tp,DV) T  v_new = U - W h
+  size_t ctx_bytes;
+  // backward scratch
+  size_t dVn;   // (B,H,Tp,DV) T  gradient of v_new
+  size_t dh;    // (B,H,NT,DK,DV) T  gradient of the state leaving each chunk
+  size_t dW;    // (B,H,Tp,DK) f32
+  size_t dKp;   // (B,H,Tp,DK) f32  dk from the output / state terms
+  size_t dGp;   // (B,H,Tp) f32   dG from the output / state terms (+ d gamma at row 63)
+  size_t bwd_bytes;
+};
+
+DeltaLayout delta_layout(int B, int T, int H, int DK, int DV, int elt_bytes);
+
+struct DeltaArgs {
+  // inputs
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* beta;
+  const float* g;     // null: ungated (DeltaNet)
+  const float* h0;    // null: zero initial state
+  const void* dout;   // backward
+  const float* dht;   // backward, null: no gradient on the final state
+  // outputs
+  void* o;
+  float* ht;          // null: final state not requested
+  void* dq;
+  void* dk;
+  void* dv;
+  float* dbeta;
+  float* dg;
+  float* dh0;         // null: no initial-state gradient
+  // context / scratch base pointers (offsets from DeltaLayout)
+  char* ctx;
+  char* ws;
+  int B, T, H, NT;
+  float scale;
+};
+
+template <typename T, int DK, int DV, bool GATED>
+hipError_t launch_delta_fwd(const DeltaArgs& a, hipStream_t stream);
+
+template <typename T, int DK, int DV, bool GATED>
+hipError_t launch_delta_bwd(const DeltaArgs& a, hipStream_t stream);
+
+// Compiled (dtype, DK, DV) combinations; each for the plain and gated rule.
+#define LINATT_DELTA_SHAPES(X) \
+  X(__bf16, 128, 128)          \
+  X(__bf16, 64, 64)            \
+  X(_Float16, 128, 128)        \
+  X(_Float16, 64, 64)
+
+}  // namespace linatt

@@ -1,0 +1,15 @@
+// Internal launch interface of the small helper kernels (row L2 norm).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace linatt {
+
+template <typename T>
+hipError_t launch_l2norm_fwd(const void* x, void* y, float* rstd, int n, int d, float eps,
+                             hipStream_t s);
+template <typename T>
+hipError_t launch_l2norm_bwd(const void* y, const float* rstd, const void* dy, void* dx, int n,
+                             int d, hipStream_t s);
+
+}  // namespace linatt

@@ -1,0 +1,176 @@
+"""GPU parity of the HIP chunked (gated) delta rule against the float64 CPU
+oracle (``oracle/delta.py``: chunked WY form, itself pinned to the naive
+recurrence by ``tests/test_oracle_delta.py``).
+
+Inputs are drawn on the CPU from seeded generators in float32, rounded once
+to the test dtype, and the same rounded tensors (upcast) feed the oracle.
+Error metric: max-abs-relative ``max|x - ref| / max|ref|`` per tensor; bar
+2e-2 for bf16 and 1e-2 for fp16.  Every case
+calls the C ABI through ``linatt_amd.delta_rule``.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import delta as D
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.bfloat16: 2e-2, torch.float16: 1e-2}
+
+
+def mar(x, ref):
+    x = x.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    den = ref.abs().max().item()
+    return (x - ref).abs().max().item() / (den if den > 0 else 1.0)
+
+
+def gen(shape, seed, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g, dtype=torch.float32) * std
+
+
+@pytest.fixture(scope="module")
+def R():
+    from linatt_amd import delta_rule as R
+    return R
+
+
+def make(B, T, H, K, V, dtype, seed, gated, h0, dht):
+    q = gen((B, T, H, K), seed).to(dtype)
+    k = D.l2norm(gen((B, T, H, K), seed + 1)).to(dtype)
+    v = gen((B, T, H, V), seed + 2).to(dtype)
+    beta = torch.sigmoid(gen((B, T, H), seed + 3))
+    g = torch.nn.functional.logsigmoid(gen((B, T, H), seed + 4) + 4) / 16 if gated else None
+    S0 = gen((B, H, K, V), seed + 5, 0.02) if h0 else None
+    do = gen((B, T, H, V), seed + 6).to(dtype)
+    dS = gen((B, H, K, V), seed + 7) if dht else None
+    return q, k, v, beta, g, S0, do, dS
+
+
+def run_gpu(R, q, k, v, beta, g, S0, do, dS, scale=None, l2=False):
+    dev = torch.device("cuda")
+    leaves = {"q": q, "k": k, "v": v, "beta": beta}
+    if g is not None:
+        leaves["g"] = g
+    if S0 is not None:
+        leaves["h0"] = S0
+    L = {n: t.to(dev).requires_grad_(True) for n, t in leaves.items()}
+    kw = dict(scale=scale, initial_state=L.get("h0"), output_final_state=True,
+              use_qk_l2norm_in_kernel=l2)
+    if g is None:
+        o, ht = R.chunk_delta_rule(L["q"], L["k"], L["v"], L["beta"], **kw)
+    else:
+        o, ht = R.chunk_gated_delta_rule(L["q"], L["k"], L["v"], L["g"], L["beta"], **kw)
+    loss = (o.float() * do.to(dev).float()).sum()
+    if dS is not None:
+        loss = loss + (ht * dS.to(dev)).sum()
+    loss.backward()
+    out = {"o": o, "ht": ht}
+    for n, t in L.items():
+        out["d" + n] = t.grad
+    return out
+
+
+def check(out, ref, tol, names=None):
+    for n in names or ref:
+        if n not in out:
+            continue
+        assert out[n].shape == ref[n].shape, (n, out[n].shape, ref[n].shape)
+        e = mar(out[n], ref[n])
+        assert e < tol, (n, e)
+
+
+SHAPES = [  # B, T, H, K, V
+    (1, 1, 1, 64, 64),
+    (1, 64, 1, 64, 64),
+    (2, 100, 2, 64, 64),
+    (1, 129, 1, 128, 128),
+    (2, 256, 3, 128, 128),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("gated", [False, True], ids=["delta", "gated"])
+@pytest.mark.parametrize("state", [False, True], ids=["nostate", "state"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_delta_parity(R, shape, gated, state, dtype):
+    B, T, H, K, V = shape
+    print(f"case {shape} gated={gated} state={state} {dtype}", flush=True)
+    q, k, v, beta, g, S0, do, dS = make(B, T, H, K, V, dtype, 10 + T, gated, state, state)
+    ref = D.delta_rule_fwd_bwd(q, k, v, beta, g, None, S0, do, dS)
+    out = run_gpu(R, q, k, v, beta, g, S0, do, dS)
+    assert out["o"].dtype == dtype and out["ht"].dtype == torch.float32
+    check(out, ref, TOL[dtype])
+
+
+def test_l2norm_in_kernel(R):
+    B, T, H, K = 2, 96, 2, 64
+    dtype = torch.bfloat16
+    q = gen((B, T, H, K), 1).to(dtype)
+    k = gen((B, T, H, K), 2).to(dtype)
+    v = gen((B, T, H, K), 3).to(dtype)
+    beta = torch.sigmoid(gen((B, T, H), 4))
+    g = torch.nn.functional.logsigmoid(gen((B, T, H), 5) + 4) / 16
+    do = gen((B, T, H, K), 6).to(dtype)
+    ref = D.delta_rule_fwd_bwd(q, k, v, beta, g, None, None, do, None, use_qk_l2norm=True)
+    out = run_gpu(R, q, k, v, beta, g, None, do, None, l2=True)
+    check(out, ref, 2e-2)
+
+
+def test_steep_decay(R):
+    """g far below zero: exp(G) underflows within a chunk; no inf/nan."""
+    B, T, H, K = 1, 200, 2, 64
+    q, k, v, beta, _, S0, do, dS = make(B, T, H, K, K, torch.bfloat16, 3, False, True, True)
+    g = -torch.rand(B, T, H, generator=torch.Generator().manual_seed(9)) * 8.0
+    ref = D.delta_rule_fwd_bwd(q, k, v, beta, g, None, S0, do, dS)
+    out = run_gpu(R, q, k, v, beta, g, S0, do, dS)
+    for n in out:
+        assert torch.isfinite(out[n]).all(), n
+    check(out, ref, 2e-2)
+
+
+@pytest.mark.parametrize("gated", [False, True], ids=["config3_deltanet", "config4_gdn"])
+def test_full_size(R, gated):
+    """BASELINE configs 3/4: B8 H6 T2048 K=V=128 bf16, chunk 64.  q ~ N(0,1),
+    k ~ N(0,1) L2-normalised, v ~ N(0,1), beta = sigmoid(N(0,1)); config 4
+    adds g = logsigmoid(N(0,1)+4)/16 and h0 ~ N(0, 0.02).  Three (b, h) heads
+    are compared with the float64 oracle (the heads are independent)."""
+    B, T, H, K = 8, 2048, 6, 128
+    seed = 3 if gated else 2
+    gg = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, H, K, generator=gg).to(torch.bfloat16)
+    k = D.l2norm(torch.randn(B, T, H, K, generator=gg)).to(torch.bfloat16)
+    v = torch.randn(B, T, H, K, generator=gg).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=gg))
+    g = torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=gg) + 4) / 16 if gated else None
+    S0 = torch.randn(B, H, K, K, generator=gg) * 0.02 if gated else None
+    do = torch.randn(B, T, H, K, generator=gg).to(torch.bfloat16)
+    dS = torch.randn(B, H, K, K, generator=gg)
+    out = run_gpu(R, q, k, v, beta, g, S0, do, dS)
+    for n in out:
+        assert torch.isfinite(out[n]).all(), n
+    for b, h in ((0, 0), (7, 5), (3, 2)):
+        sl = lambda x: x[b:b + 1, :, h:h + 1]  # noqa: E731
+        sh = lambda x: x[b:b + 1, h:h + 1]  # noqa: E731
+        ref = D.delta_rule_fwd_bwd(sl(q), sl(k), sl(v), sl(beta), sl(g) if gated else None, None,
+                                   sh(S0) if gated else None, sl(do), sh(dS))
+        for n in ref:
+            x = out[n]
+            x = sh(x) if n in ("ht", "dh0") else sl(x)
+            e = mar(x, ref[n])
+            assert e < 2e-2, (n, b, h, e)
+
+
+def test_rejects_unsupported(R):
+    dev = torch.device("cuda")
+    q = torch.randn(1, 8, 1, 64, device=dev)
+    beta = torch.rand(1, 8, 1, device=dev)
+    with pytest.raises(TypeError, match="no kernel"):
+        R.chunk_delta_rule(q, q, q, beta)
+    qb = q.bfloat16()
+    with pytest.raises(NotImplementedError, match="cu_seqlens"):
+        R.chunk_delta_rule(qb, qb, qb, beta, cu_seqlens=torch.tensor([0, 8], device=dev))
