@@ -43,6 +43,89 @@ def kata_flops(B, H, T, dk, dv, M, variant="concat"):
     return {"fwd": fwd, "bwd_dq": dq, "bwd_dkdv": dkdv, "total": fwd + dq + dkdv}
 
 
+def delta_flops(B, H, T, K, V, C=64):
+    """Algorithmic FLOPs of the chunked delta rule (count once, no recompute):
+    per token-head C(6K+4V) + 6KV + (2/3)C^2 (Gram, QK^T, W = 3x2C^2K; U and
+    the intra A.v = 2x2C^2V; W.h, Q.h, K^T v_new = 3x2CKV; the 64x64 UT
+    inverse (2/3)C^3 per chunk); backward = 2x forward."""
+    per = C * (6 * K + 4 * V) + 6 * K * V + (2.0 / 3.0) * C * C
+    fwd = per * B * H * T
+    return {"fwd": fwd, "bwd": 2 * fwd, "total": 3 * fwd}
+
+
+def bench_delta(gated, steps, warmup):
+    """BASELINE config 3 (DeltaNet) / 4 (GatedDeltaNet): B8 H6 T2048 K=V=128
+    bf16, chunk 64, fwd + bwd through linatt_delta_fwd / linatt_delta_bwd with
+    preallocated outputs, context and workspace."""
+    import torch
+    from linatt_amd import _lib
+    L = _lib.load()
+    B, H, T, K, V = 8, 6, 2048, 128, 128
+    seed = 3 if gated else 2
+    g_ = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, H, K, generator=g_).to(torch.bfloat16)
+    k = torch.randn(B, T, H, K, generator=g_)
+    k = (k * torch.rsqrt((k * k).sum(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+    v = torch.randn(B, T, H, V, generator=g_).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g_))
+    g = torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=g_) + 4) / 16 if gated else None
+    h0 = torch.randn(B, H, K, V, generator=g_) * 0.02 if gated else None
+    do = torch.randn(B, T, H, V, generator=g_).to(torch.bfloat16)
+    dev = torch.device("cuda", 0)
+    qd, kd, vd, bd, dod = (x.to(dev) for x in (q, k, v, beta, do))
+    gd = g.to(dev) if gated else None
+    h0d = h0.to(dev) if gated else None
+    o = torch.empty_like(vd)
+    ht = torch.empty(B, H, K, V, device=dev)
+    dt = _lib.LINATT_BFLOAT16
+    ctx = torch.empty(L.linatt_delta_ctx_bytes(B, T, H, K, V, dt), device=dev, dtype=torch.uint8)
+    ws = torch.empty(L.linatt_delta_bwd_workspace_bytes(B, T, H, K, V, dt), device=dev,
+                     dtype=torch.uint8)
+    dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+    dbeta = torch.empty(B, T, H, device=dev)
+    dg = torch.empty_like(dbeta) if gated else None
+    dh0 = torch.empty_like(h0d) if gated else None
+    dht = torch.zeros(B, H, K, V, device=dev)
+    P = _lib.ptr
+    sp = _lib.stream_of(qd)
+    scale = K ** -0.5
+    stream = torch.cuda.current_stream(dev)
+
+    def fwd():
+        _lib.check("linatt_delta_fwd", L.linatt_delta_fwd(
+            P(qd), P(kd), P(vd), P(bd), P(gd), P(h0d), P(o), P(ht), P(ctx), B, T, H, K, V,
+            scale, dt, sp))
+
+    def bwd():
+        _lib.check("linatt_delta_bwd", L.linatt_delta_bwd(
+            P(qd), P(kd), P(vd), P(bd), P(gd), P(h0d), P(dod), P(dht), P(ctx), P(ws), P(dq),
+            P(dk), P(dv), P(dbeta), P(dg), P(dh0), B, T, H, K, V, scale, dt, sp))
+
+    for _ in range(warmup):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    for s in range(steps):
+        ev[s][0].record(stream)
+        fwd()
+        ev[s][1].record(stream)
+        bwd()
+        ev[s][2].record(stream)
+    torch.cuda.synchronize()
+    f_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
+    b_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / steps
+    fl = delta_flops(B, H, T, K, V)
+    tot = f_ms + b_ms
+    tf = fl["total"] / (tot * 1e-3) / 1e12
+    return {"config": {"B": B, "H": H, "T": T, "K": K, "V": V, "chunk": 64, "gated": gated,
+                       "seed": seed, "h0": gated},
+            "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4), "ms": round(tot, 4),
+            "tokens_per_s": round(B * T / (tot * 1e-3), 1),
+            "alg_gflop": round(fl["total"] / 1e9, 2), "tflops": round(tf, 1),
+            "frac_mfma_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+
+
 def cpu_baseline(q, k, v, do, M, seconds):
     """Time the float32 restatement of the reference path (dense forward +
     explicit backward, kata/parallel_kata_attn.py:49-146) head by head on the
@@ -82,6 +165,21 @@ def _cpu_model():
     return "unknown"
 
 
+def copy_calibration():
+    """A plain device copy of known size (512 MiB bf16, 3 launches), the
+    reference against which the rocprofv3 FETCH_SIZE / WRITE_SIZE counters are
+    scaled into bytes."""
+    import torch
+    n = 256 * 1024 * 1024
+    src = torch.empty(n, device="cuda", dtype=torch.bfloat16).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_launch": n * 2, "launches": 3}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -90,11 +188,18 @@ def main():
     ap.add_argument("--groups", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-delta", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a 512 MiB device copy (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only; multi-GPU runs are not part of "
               "it (see DESIGN.md for how the path shards). Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_calibration:
+        copy_calibration()
+        return
 
     import torch
     from linatt_amd import _lib
@@ -163,6 +268,11 @@ def main():
     step_tflops = fl["total"] / (ms_step * 1e-3) / 1e12
     tokens_per_s = B * T / (ms_step * 1e-3)
 
+    delta = None
+    if not args.no_delta:
+        delta = {"deltanet_config3": bench_delta(False, max(3, args.steps // 2), 2),
+                 "gated_deltanet_config4": bench_delta(True, max(3, args.steps // 2), 2)}
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(q, k, v, do, M, args.cpu_seconds)
@@ -191,6 +301,7 @@ def main():
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None},
         "cpu_baseline": cpu,
+        "delta_rule": delta,
     }
     print(json.dumps(out), flush=True)
 
