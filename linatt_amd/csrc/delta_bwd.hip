@@ -6,8 +6,8 @@
 // Reverse-mode of the chunk form computed by delta_fwd.hip, per chunk with
 // S the state entering it, dS' the gradient of the state leaving it:
 //
-//   dVn = Aqk^T dO + diag(e^(gamma-G)) K dS'                     (kernel 1)
-//   dS  = e^gamma dS' + (scale e^G Q)^T dO - W^T dVn              (kernel 1)
+//   dVn = Aqk^T dO + diag(e^(gamma-G)) K dS'                     (kernels 0, 1)
+//   dS  = e^gamma dS' + (scale e^G Q)^T dO - W^T dVn              (kernels 0, 1)
 //   dQ  = scale e^G dO S^T + Mq K,  Mq = scale (dO Vn^T) o e^(G_i-G_j) [j<=i]
 //   dK  = diag(e^(gamma-G)) Vn dS'^T + Mq^T Q + ...               (kernel 2)
 //   dW  = -dVn S^T                                                (kernel 2)
@@ -15,16 +15,66 @@
 //   dV  = diag(beta) Tm^T dVn,  dK += diag(beta e^G) Tm^T dW + At K + At^T K
 //   dbeta, dG from the same terms; dg = reverse cumsum of dG in the chunk  (kernel 3)
 //
-// Kernel 1 (delta_state_bwd) walks the chunks backwards, one wave per
-// (b, h, 32 value columns), with dS in MFMA accumulators.  Kernels 2 and 3
-// are parallel over (b, h, chunk).
+// Kernel 0 (delta_bwd_pre) forms the state-independent terms of kernel 1 in
+// parallel; kernel 1 (delta_state_bwd) walks the chunks backwards, one wave
+// per (b, h, 32 value columns), with dS in MFMA accumulators.  Kernels 2 and
+// 3 are parallel over (b, h, chunk).
 #include "common.h"
 #include "delta_kernels.h"
 
 namespace linatt {
 
 // ---------------------------------------------------------------------------
-// Kernel 1: reverse state pass.
+// Kernel 0: the parts of the reverse state pass that do not depend on the
+// state gradient, parallel over (b, h, chunk):
+//   dVnl = Aqk^T dO          (64 x DV)  -> dVnlT [v][j]  f32
+//   Z    = (scale e^G Q)^T dO (DK x DV) -> ZT    [v][d]  f32
+// ---------------------------------------------------------------------------
+template <typename T, int DK, int DV, bool GATED>
+__global__ __launch_bounds__(256) void delta_bwd_pre_kernel(DeltaArgs a, DeltaLayout L) {
+  constexpr int PX = 64 + 8;
+  __shared__ __attribute__((aligned(16))) T dOT[DV * PX];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int cl = lane & 31, hh = lane >> 5;
+  const int Tn = a.T, H = a.H, NT = a.NT;
+  const int c = blockIdx.x % NT, bh = blockIdx.x / NT;
+  const int b = bh / H, h = bh % H;
+  const int t0 = c * kChunk;
+  const size_t ci = (size_t)bh * NT + c;
+  const T* dob = (const T*)a.dout + ((size_t)b * Tn * H + h) * DV;
+  load_tile64x<T, T, DV, 1, PX, false, true>(dob, t0, Tn, (int64_t)H * DV, nullptr, dOT, tid, nullptr);
+  __syncthreads();
+
+  const T* aqt = (const T*)(a.ctx + L.AqkT) + ci * 4096;
+  const T* qgt = (const T*)(a.ctx + L.QgT) + ci * DK * 64;
+  float* dvl = reinterpret_cast<float*>(a.ws + L.dVnlT) + ci * DV * 64;
+  float* zt = reinterpret_cast<float*>(a.ws + L.ZT) + ci * DV * DK;
+  constexpr int NVT = DV / 32;
+  // tiles: 2 * NVT of dVnl (j-tile, v-tile), then (DK/32) * NVT of Z
+  constexpr int NTILE = 2 * NVT + (DK / 32) * NVT;
+  for (int tile = w; tile < NTILE; tile += 4) {
+    const bool isz = tile >= 2 * NVT;
+    const int tt = isz ? tile - 2 * NVT : tile;
+    const int rt = tt / NVT, vt = tt % NVT;
+    const T* xrow = isz ? qgt + (32 * rt + cl) * 64 : aqt + (32 * rt + cl) * 64;
+    f32x16 acc{};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      acc = mma(ld8<T>(xrow + 16 * s + 8 * hh), ld8<T>(dOT + (32 * vt + cl) * PX + 16 * s + 8 * hh), acc);
+    const int v = 32 * vt + cl;
+    float* dst = isz ? zt + (size_t)v * DK : dvl + (size_t)v * 64;
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+      *reinterpret_cast<float4*>(dst + 32 * rt + 8 * I + 4 * hh) =
+          make_float4(acc[4 * I], acc[4 * I + 1], acc[4 * I + 2], acc[4 * I + 3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel 1: reverse state pass, one wave per (b, h, 32 value columns), dS in
+// DK/32 accumulator tiles (lane column v).  Per chunk:
+//   dVn = dVnl + e^(gamma-G) K dS'  ->  dS = e^gamma dS' + Z - W^T dVn
+// with the next (earlier) chunk's K operands loaded during the current one.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
 __global__ __launch_bounds__(64) void delta_state_bwd_kernel(DeltaArgs a, DeltaLayout L) {
@@ -39,10 +89,7 @@ __global__ __launch_bounds__(64) void delta_state_bwd_kernel(DeltaArgs a, DeltaL
 
   const T* kb = (const T*)a.k + ((size_t)b * Tn * H + h) * DK;
   const int64_t ks = (int64_t)H * DK;
-  const T* dob = (const T*)a.dout + ((size_t)b * Tn * H + h) * DV;
-  const int64_t os = (int64_t)H * DV;
   const float* Gc = reinterpret_cast<const float*>(a.ctx + L.Gc) + (size_t)bh * Tp;
-  T* dVng = (T*)(a.ws + L.dVn) + (size_t)bh * Tp * DV;
 
   f32x16 dS[NDT];
 #pragma unroll
@@ -53,88 +100,114 @@ __global__ __launch_bounds__(64) void delta_state_bwd_kernel(DeltaArgs a, DeltaL
       dS[dt][e] = a.dht ? a.dht[((size_t)bh * DK + d) * DV + v] : 0.f;
     }
 
+  // K operands [jt][db][j]: rows 32 jt + cl of a chunk (zero past T)
+  v8_t<T> kc[2][NDT][2];
+  auto load_k = [&](v8_t<T> (&dst)[2][NDT][2], int c) {
+#pragma unroll
+    for (int jt = 0; jt < 2; ++jt) {
+      const int tj = c * kChunk + 32 * jt + cl;
+#pragma unroll
+      for (int db = 0; db < NDT; ++db)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          dst[jt][db][j] = tj < Tn ? ld_tr_op<T>(kb + (int64_t)tj * ks + 32 * db, j, hh) : zero8<T>();
+    }
+  };
+  load_k(kc, NT - 1);
+
 #pragma unroll 1
   for (int c = NT - 1; c >= 0; --c) {
     const int t0 = c * kChunk;
     const size_t ci = (size_t)bh * NT + c;
-    T* dhg = (T*)(a.ws + L.dh) + ci * DK * DV;
+    // this chunk's W^T operands, dVnl, Z and gates, issued early
+    const T* wt = (const T*)(a.ctx + L.WT) + ci * DK * 64;
+    v8_t<T> wop[NDT][2][2];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int d = 32 * dt + 8 * (e >> 2) + 4 * hh + (e & 3);
-        dhg[d * DV + v] = (T)dS[dt][e];
-      }
-
-    // dO as B operands: lane column v, k-slot 16 s + 8 hh + j is row t0 + that.
-    v8_t<T> ydo[4];
+      for (int it = 0; it < 2; ++it)
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+        for (int j = 0; j < 2; ++j) wop[dt][it][j] = ld_tr_op<T>(wt + (32 * dt + cl) * 64 + 32 * it, j, hh);
+    const float* dvl = reinterpret_cast<const float*>(a.ws + L.dVnlT) + (ci * DV + v) * 64;
+    const float* zt = reinterpret_cast<const float*>(a.ws + L.ZT) + (ci * DV + v) * DK;
+    f32x4 dl4[2][4], z4[NDT][4];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int t = t0 + 16 * s + 8 * hh + j;
-        ydo[s][j] = t < Tn ? dob[(int64_t)t * os + v] : (T)0.f;
-      }
-
-    // dVn = Aqk^T dO + e^(gamma - G) K dS'
-    const T* aqt = (const T*)(a.ctx + L.AqkT) + ci * 4096;
-    f32x16 dVn[2], Pk[2];
+    for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
-    for (int jt = 0; jt < 2; ++jt) {
-      dVn[jt] = f32x16{};
-      Pk[jt] = f32x16{};
+      for (int I = 0; I < 4; ++I) dl4[jt][I] = *reinterpret_cast<const f32x4*>(dvl + 32 * jt + 8 * I + 4 * hh);
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        dVn[jt] = mma(ld8<T>(aqt + (32 * jt + cl) * 64 + 16 * s + 8 * hh), ydo[s], dVn[jt]);
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int I = 0; I < 4; ++I) z4[dt][I] = *reinterpret_cast<const f32x4*>(zt + 32 * dt + 8 * I + 4 * hh);
+    float gam = 0.f;
+    f32x4 gj[2][4];
+    if constexpr (GATED) {
+      gam = Gc[t0 + 63];
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+        for (int I = 0; I < 4; ++I) gj[jt][I] = *reinterpret_cast<const f32x4*>(Gc + t0 + 32 * jt + 8 * I + 4 * hh);
     }
+    v8_t<T> kn[2][NDT][2];
+    if (c > 0) load_k(kn, c - 1);
+
+    // gradient of the state leaving this chunk, transposed [v][d]
+    T* dhg = (T*)(a.ws + L.dhT) + (ci * DV + v) * DK;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+        st4<T>(dhg + 32 * dt + 8 * I + 4 * hh,
+               to4<T>(dS[dt][4 * I], dS[dt][4 * I + 1], dS[dt][4 * I + 2], dS[dt][4 * I + 3]));
+
+    // dVn = dVnl + e^(gamma - G_j) (K dS')_j
+    f32x16 Pk[2];
+    Pk[0] = Pk[1] = f32x16{};
 #pragma unroll
     for (int db = 0; db < NDT; ++db)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const v8_t<T> ys = c_to_b<T>(dS[db], j);
 #pragma unroll
-        for (int jt = 0; jt < 2; ++jt) {
-          const int tj = t0 + 32 * jt + cl;
-          Pk[jt] = mma(tj < Tn ? ld_tr_op<T>(kb + (int64_t)tj * ks + 32 * db, j, hh) : zero8<T>(),
-                       ys, Pk[jt]);
-        }
+        for (int jt = 0; jt < 2; ++jt) Pk[jt] = mma(kc[jt][db][j], ys, Pk[jt]);
       }
-    const float gam = GATED ? Gc[t0 + 63] : 0.f;
+    f32x16 dVn[2];
+    T* dvg = (T*)(a.ws + L.dVnT) + (ci * DV + v) * 64;
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
-        const int j = 32 * jt + 8 * I + 4 * hh;
-        float f[4] = {1.f, 1.f, 1.f, 1.f};
-        if constexpr (GATED) {
-          const f32x4 g4 = *reinterpret_cast<const f32x4*>(Gc + t0 + j);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) f[r] = __expf(gam - g4[r]);
-        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float val = dVn[jt][4 * I + r] + f[r] * Pk[jt][4 * I + r];
-          dVn[jt][4 * I + r] = val;
-          dVng[(size_t)(t0 + j + r) * DV + v] = (T)val;
+          const float f = GATED ? __expf(gam - gj[jt][I][r]) : 1.f;
+          dVn[jt][4 * I + r] = dl4[jt][I][r] + f * Pk[jt][4 * I + r];
         }
+        st4<T>(dvg + 32 * jt + 8 * I + 4 * hh,
+               to4<T>(dVn[jt][4 * I], dVn[jt][4 * I + 1], dVn[jt][4 * I + 2], dVn[jt][4 * I + 3]));
       }
 
-    // dS <- e^gamma dS + Qg^T dO - W^T dVn
-    const T* qgt = (const T*)(a.ctx + L.QgT) + ci * DK * 64;
-    const T* wt = (const T*)(a.ctx + L.WT) + ci * DK * 64;
+    // dS <- e^gamma dS + Z - W^T dVn
     const float eg = GATED ? __expf(gam) : 1.f;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
-      f32x16 t1{}, t2{};
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        t1 = mma(ld8<T>(qgt + (32 * dt + cl) * 64 + 16 * s + 8 * hh), ydo[s], t1);
+      f32x16 t2{};
 #pragma unroll
       for (int it = 0; it < 2; ++it)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          t2 = mma(ld_tr_op<T>(wt + (32 * dt + cl) * 64 + 32 * it, j, hh), c_to_b<T>(dVn[it], j), t2);
-      dS[dt] = dS[dt] * eg + t1 - t2;
+        for (int j = 0; j < 2; ++j) t2 = mma(wop[dt][it][j], c_to_b<T>(dVn[it], j), t2);
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          dS[dt][4 * I + r] = dS[dt][4 * I + r] * eg + z4[dt][I][r] - t2[4 * I + r];
+    }
+    if (c > 0) {
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+        for (int db = 0; db < NDT; ++db)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) kc[jt][db][j] = kn[jt][db][j];
     }
   }
 
@@ -152,17 +225,26 @@ __global__ __launch_bounds__(64) void delta_state_bwd_kernel(DeltaArgs a, DeltaL
 // ---------------------------------------------------------------------------
 // Kernel 2: dq, dW, the output/state part of dk and of dG.
 // Wave w: row block ib = w & 1 (lane column = chunk row 32 ib + cl), key
-// dims half dhalf = w >> 1.
+// dims half dhalf = w >> 1.  The transposed per-chunk tiles (h^T, dh^T,
+// v_new^T, dv_new^T) are turned back into value-contiguous rows through LDS
+// in three phases: (A) S and dVn, (B) dS' and Vn, (C) K^T and Q^T.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
 __global__ __launch_bounds__(256) void delta_bwd_chunk_kernel(DeltaArgs a, DeltaLayout L) {
-  constexpr int PX = 64 + 8;
+  constexpr int PX = 64 + 8;   // [d][row] tiles
+  constexpr int PV = DV + 8;   // [row][v] tiles
   constexpr int NDW = DK / 64;  // key-dim tiles per wave
-  __shared__ __attribute__((aligned(16))) T KT[DK * PX];
-  __shared__ __attribute__((aligned(16))) T QT[DK * PX];
+  constexpr int NS = DV / 16;
+  constexpr int RA = DK * PV, RB = 64 * PV, RC = 2 * DK * PX;
+  constexpr int RTOT = (RA + RB > RC) ? RA + RB : RC;
+  __shared__ __attribute__((aligned(16))) T sm[RTOT];
   __shared__ float Gs[64];
   __shared__ float red_gi[2][64], red_kd[2][64], red_rc[64];
   __shared__ float red_s[4];
+  T* Sx = sm;             // phase A: S [d][v];  phase B: dS' [d][v]
+  T* Rx = sm + RA;        // phase A: dVn [i][v]; phase B: Vn [j][v]
+  T* KT = sm;             // phase C: K^T [d][j]
+  T* QT = sm + DK * PX;   // phase C: Q^T [d][i]
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int cl = lane & 31, hh = lane >> 5;
@@ -180,18 +262,22 @@ __global__ __launch_bounds__(256) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
   const T* dob = (const T*)a.dout + ((size_t)b * Tn * H + h) * DV;
   const int64_t os = (int64_t)H * DV;
   const float* Gc = reinterpret_cast<const float*>(a.ctx + L.Gc) + (size_t)bh * Tp;
-  const T* hg = (const T*)(a.ctx + L.h) + ci * DK * DV;
-  const T* dhg = (const T*)(a.ws + L.dh) + ci * DK * DV;
-  const T* Vng = (const T*)(a.ctx + L.Vn) + ((size_t)bh * Tp + t0) * DV;
-  const T* dVng = (const T*)(a.ws + L.dVn) + ((size_t)bh * Tp + t0) * DV;
+  const T* hg = (const T*)(a.ctx + L.hT) + ci * DV * DK;
+  const T* dhg = (const T*)(a.ws + L.dhT) + ci * DV * DK;
+  const T* vng = (const T*)(a.ctx + L.VnT) + ci * DV * 64;
+  const T* dvng = (const T*)(a.ws + L.dVnT) + ci * DV * 64;
   const T* aq = (const T*)(a.ctx + L.Aqk) + ci * 4096;
   const T* aqt = (const T*)(a.ctx + L.AqkT) + ci * 4096;
 
-  load_tile64x<T, T, DK, 1, PX, false, true>(kb, t0, Tn, qks, nullptr, KT, tid, nullptr);
-  load_tile64x<T, T, DK, 1, PX, false, true>(qb, t0, Tn, qks, nullptr, QT, tid, nullptr);
+  // phase A tiles
+#pragma unroll
+  for (int r0 = 0; r0 < DV; r0 += 64) {
+    load_tile64x<T, T, DK, 1, PV, false, true>(hg + (size_t)r0 * DK, 0, 64, DK, nullptr, Sx + r0, tid, nullptr);
+    load_tile64x<T, T, 64, 1, PV, false, true>(dvng + (size_t)r0 * 64, 0, 64, 64, nullptr, Rx + r0, tid, nullptr);
+  }
   if (tid < 64) Gs[tid] = GATED ? Gc[t0 + tid] : 0.f;
 
-  // <S, dS'> over the chunk's state pair (for d gamma), all 256 threads.
+  // <S, dS'> over the chunk's state pair (for d gamma); both stored [v][d].
   float sdot = 0.f;
   for (int idx = 8 * tid; idx < DK * DV; idx += 8 * 256) {
     const v8_t<T> x = ld8<T>(hg + idx), y = ld8<T>(dhg + idx);
@@ -207,13 +293,67 @@ __global__ __launch_bounds__(256) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
   const int ti = t0 + i;
   const bool valid = ti < Tn;
   const float Gi = Gs[i];
-  constexpr int NS = DV / 16;
-  v8_t<T> ydo[NS], ydv[NS], yvn[NS];
+  v8_t<T> ydo[NS];
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    ydo[s] = valid ? ld8<T>(dob + (int64_t)ti * os + 16 * s + 8 * hh) : zero8<T>();
-    ydv[s] = ld8<T>(dVng + (size_t)i * DV + 16 * s + 8 * hh);
-    yvn[s] = ld8<T>(Vng + (size_t)i * DV + 16 * s + 8 * hh);
+  for (int s = 0; s < NS; ++s) ydo[s] = valid ? ld8<T>(dob + (int64_t)ti * os + 16 * s + 8 * hh) : zero8<T>();
+
+  // (A) dQ_inter = scale e^G dO S^T, dW = -dVn S^T   (lane column i)
+  float gi_part = 0.f, kd_part = 0.f;
+  const float eG = GATED ? __expf(Gi) : 1.f;
+  const float eGam = GATED ? __expf(Gs[63] - Gi) : 1.f;
+  float* dWg = reinterpret_cast<float*>(a.ws + L.dW) + ((size_t)bh * Tp + t0 + i) * DK;
+  float* dKg = reinterpret_cast<float*>(a.ws + L.dKp) + ((size_t)bh * Tp + t0 + i) * DK;
+  T* dqg = (T*)a.dq + (((size_t)b * Tn + ti) * H + h) * DK;
+  f32x16 dq[NDW], dks[NDW];
+#pragma unroll
+  for (int m = 0; m < NDW; ++m) {
+    const int dt = dhalf * NDW + m;
+    f32x16 acc{}, dw{};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const v8_t<T> xs = ld8<T>(Sx + (32 * dt + cl) * PV + 16 * s + 8 * hh);
+      acc = mma(xs, ydo[s], acc);
+      dw = mma(xs, ld8<T>(Rx + i * PV + 16 * s + 8 * hh), dw);
+    }
+    acc *= a.scale * eG;
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      const int d = 32 * dt + 8 * I + 4 * hh;
+      const v4_t<T> q4 = valid ? ld4<T>(qb + (int64_t)ti * qks + d) : v4_t<T>{};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) gi_part += (float)q4[r] * acc[4 * I + r];
+      *reinterpret_cast<float4*>(dWg + d) =
+          make_float4(-dw[4 * I], -dw[4 * I + 1], -dw[4 * I + 2], -dw[4 * I + 3]);
+    }
+    dq[m] = acc;
+  }
+  __syncthreads();
+
+  // phase B tiles
+#pragma unroll
+  for (int r0 = 0; r0 < DV; r0 += 64) {
+    load_tile64x<T, T, DK, 1, PV, false, true>(dhg + (size_t)r0 * DK, 0, 64, DK, nullptr, Sx + r0, tid, nullptr);
+    load_tile64x<T, T, 64, 1, PV, false, true>(vng + (size_t)r0 * 64, 0, 64, 64, nullptr, Rx + r0, tid, nullptr);
+  }
+  __syncthreads();
+
+  // (B) dK_state = e^(gamma-G_j) Vn dS'^T   (lane column j = i)
+#pragma unroll
+  for (int m = 0; m < NDW; ++m) {
+    const int dt = dhalf * NDW + m;
+    f32x16 acc{};
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      acc = mma(ld8<T>(Sx + (32 * dt + cl) * PV + 16 * s + 8 * hh), ld8<T>(Rx + i * PV + 16 * s + 8 * hh), acc);
+    acc *= eGam;
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      const int d = 32 * dt + 8 * I + 4 * hh;
+      const v4_t<T> k4 = valid ? ld4<T>(kb + (int64_t)ti * qks + d) : v4_t<T>{};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) kd_part += (float)k4[r] * acc[4 * I + r];
+    }
+    dks[m] = acc;
   }
 
   // Mq (lane column i, rows j) and its transpose MqT (lane column j, rows i).
@@ -222,12 +362,12 @@ __global__ __launch_bounds__(256) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
 #pragma unroll
   for (int jt = 0; jt < 2; ++jt) {
     f32x16 dm{}, dmt{};
+    const int rr0 = 32 * jt + cl;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      const int rr = 32 * jt + cl;
-      dm = mma(ld8<T>(Vng + (size_t)rr * DV + 16 * s + 8 * hh), ydo[s], dm);
-      dmt = mma(t0 + rr < Tn ? ld8<T>(dob + (int64_t)(t0 + rr) * os + 16 * s + 8 * hh) : zero8<T>(),
-                yvn[s], dmt);
+      dm = mma(ld8<T>(Rx + rr0 * PV + 16 * s + 8 * hh), ydo[s], dm);
+      dmt = mma(t0 + rr0 < Tn ? ld8<T>(dob + (int64_t)(t0 + rr0) * os + 16 * s + 8 * hh) : zero8<T>(),
+                ld8<T>(Rx + i * PV + 16 * s + 8 * hh), dmt);
     }
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
@@ -237,7 +377,6 @@ __global__ __launch_bounds__(256) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int rr = r0 + r;
-        // Mq[i][rr] (rr = key j <= i) and Mq[rr][i] (rr = query >= key i)
         const float x = dm[4 * I + r], y = dmt[4 * I + r];
         rowsum += x * (float)aq4[r];
         colsum += y * (float)aqt4[r];
@@ -253,55 +392,31 @@ __global__ __launch_bounds__(256) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
   }
   rowsum += __shfl_xor(rowsum, 32);
   colsum += __shfl_xor(colsum, 32);
+  __syncthreads();
 
-  // dQ, dW (lane column i) and dK (lane column j = i) over this wave's key dims.
-  float gi_part = 0.f, kd_part = 0.f;
-  const float eG = GATED ? __expf(Gi) : 1.f;
-  const float eGam = GATED ? __expf(Gs[63] - Gi) : 1.f;
-  float* dWg = reinterpret_cast<float*>(a.ws + L.dW) + ((size_t)bh * Tp + t0 + i) * DK;
-  float* dKg = reinterpret_cast<float*>(a.ws + L.dKp) + ((size_t)bh * Tp + t0 + i) * DK;
-  T* dqg = (T*)a.dq + (((size_t)b * Tn + ti) * H + h) * DK;
+  // phase C tiles: K^T, Q^T
+  load_tile64x<T, T, DK, 1, PX, false, true>(kb, t0, Tn, qks, nullptr, KT, tid, nullptr);
+  load_tile64x<T, T, DK, 1, PX, false, true>(qb, t0, Tn, qks, nullptr, QT, tid, nullptr);
+  __syncthreads();
+
+  // (C) intra terms: dQ += Mq K, dK += Mq^T Q
 #pragma unroll
   for (int m = 0; m < NDW; ++m) {
     const int dt = dhalf * NDW + m;
-    f32x16 dq{}, dw{}, dks{};
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const v8_t<T> xs = ld8<T>(hg + (32 * dt + cl) * DV + 16 * s + 8 * hh);
-      const v8_t<T> xd = ld8<T>(dhg + (32 * dt + cl) * DV + 16 * s + 8 * hh);
-      dq = mma(xs, ydo[s], dq);
-      dw = mma(xs, ydv[s], dw);
-      dks = mma(xd, yvn[s], dks);
-    }
-    dq *= a.scale * eG;
-    dks *= eGam;
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      const int d = 32 * dt + 8 * I + 4 * hh;
-      const v4_t<T> q4 = valid ? ld4<T>(qb + (int64_t)ti * qks + d) : v4_t<T>{};
-      const v4_t<T> k4 = valid ? ld4<T>(kb + (int64_t)ti * qks + d) : v4_t<T>{};
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        gi_part += (float)q4[r] * dq[4 * I + r];
-        kd_part += (float)k4[r] * dks[4 * I + r];
-      }
-      *reinterpret_cast<float4*>(dWg + d) =
-          make_float4(-dw[4 * I], -dw[4 * I + 1], -dw[4 * I + 2], -dw[4 * I + 3]);
-    }
-    // intra terms
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        dq = mma(ld_tr_op<T>(KT + (32 * dt + cl) * PX + 32 * jt, j, hh), c_to_b<T>(Mq[jt], j), dq);
-        dks = mma(ld_tr_op<T>(QT + (32 * dt + cl) * PX + 32 * jt, j, hh), c_to_b<T>(MqT[jt], j), dks);
+        dq[m] = mma(ld_tr_op<T>(KT + (32 * dt + cl) * PX + 32 * jt, j, hh), c_to_b<T>(Mq[jt], j), dq[m]);
+        dks[m] = mma(ld_tr_op<T>(QT + (32 * dt + cl) * PX + 32 * jt, j, hh), c_to_b<T>(MqT[jt], j), dks[m]);
       }
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       const int d = 32 * dt + 8 * I + 4 * hh;
-      if (valid) st4<T>(dqg + d, to4<T>(dq[4 * I], dq[4 * I + 1], dq[4 * I + 2], dq[4 * I + 3]));
+      if (valid)
+        st4<T>(dqg + d, to4<T>(dq[m][4 * I], dq[m][4 * I + 1], dq[m][4 * I + 2], dq[m][4 * I + 3]));
       *reinterpret_cast<float4*>(dKg + d) =
-          make_float4(dks[4 * I], dks[4 * I + 1], dks[4 * I + 2], dks[4 * I + 3]);
+          make_float4(dks[m][4 * I], dks[m][4 * I + 1], dks[m][4 * I + 2], dks[m][4 * I + 3]);
     }
   }
   gi_part += __shfl_xor(gi_part, 32);
@@ -338,7 +453,8 @@ __global__ __launch_bounds__(256) void delta_wy_bwd_kernel(DeltaArgs a, DeltaLay
   constexpr int NKW = DK / 64, NVW = DV / 64;
   __shared__ __attribute__((aligned(16))) T TmT[64 * PX];
   __shared__ __attribute__((aligned(16))) T X1T[64 * PX];
-  __shared__ __attribute__((aligned(16))) T buf[(DK + DV) * PX];
+  constexpr int PV = DV + 8;
+  __shared__ __attribute__((aligned(16))) T buf[64 * PV + DK * PX];
   __shared__ float Gs[64], Bs[64];
   __shared__ float red_b[2][64], red_g[2][64], red_rb[64];
 
@@ -356,16 +472,18 @@ __global__ __launch_bounds__(256) void delta_wy_bwd_kernel(DeltaArgs a, DeltaLay
   const T* vb = (const T*)a.v + ((size_t)b * Tn * H + h) * DV;
   const int64_t ks = (int64_t)H * DK, vs = (int64_t)H * DV;
   const T* tmg = (const T*)(a.ctx + L.Tm) + ci * 4096;
-  const T* dUg = (const T*)(a.ws + L.dVn) + ((size_t)bh * Tp + t0) * DV;
+  const T* dUt = (const T*)(a.ws + L.dVnT) + ci * DV * 64;  // dU^T [v][i]
   const float* dWg = reinterpret_cast<const float*>(a.ws + L.dW) + ((size_t)bh * Tp + t0) * DK;
   const float* Gc = reinterpret_cast<const float*>(a.ctx + L.Gc) + (size_t)bh * Tp;
 
-  T* dUT = buf;
-  T* dWT = buf + DV * PX;
+  T* dUn = buf;             // dU natural [i][v]
+  T* dWT = buf + 64 * PV;   // dW^T [d][i]
   T* KT = buf;
 
   load_tile64x<T, T, 64, 1, PX, false, true>(tmg, 0, 64, 64, nullptr, TmT, tid, nullptr);
-  load_tile64x<T, T, DV, 1, PX, false, true>(dUg, 0, 64, DV, nullptr, dUT, tid, nullptr);
+#pragma unroll
+  for (int r0 = 0; r0 < DV; r0 += 64)
+    load_tile64x<T, T, 64, 1, PV, false, true>(dUt + (size_t)r0 * 64, 0, 64, 64, nullptr, dUn + r0, tid, nullptr);
   load_tile64x<float, T, DK, 1, PX, false, true>(dWg, 0, 64, DK, nullptr, dWT, tid, nullptr);
   if (tid < 64) {
     const int t = t0 + tid;
@@ -389,7 +507,7 @@ __global__ __launch_bounds__(256) void delta_wy_bwd_kernel(DeltaArgs a, DeltaLay
     f32x16 acc{};
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      acc = mma(ld8<T>(dUT + (32 * vt + cl) * PX + 16 * s + 8 * hh),
+      acc = mma(ld8<T>(dUt + (32 * vt + cl) * 64 + 16 * s + 8 * hh),
                 ld8<T>(TmT + i * PX + 16 * s + 8 * hh), acc);
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
@@ -434,7 +552,7 @@ __global__ __launch_bounds__(256) void delta_wy_bwd_kernel(DeltaArgs a, DeltaLay
 #pragma unroll
     for (int s = 0; s < DV / 16; ++s)
       av = mma(jv ? ld8<T>(vb + (int64_t)(t0 + jr) * vs + 16 * s + 8 * hh) : zero8<T>(),
-               ld8<T>(dUg + (size_t)i * DV + 16 * s + 8 * hh), av);
+               ld8<T>(dUn + i * PV + 16 * s + 8 * hh), av);
 #pragma unroll
     for (int s = 0; s < DK / 16; ++s)
       ak = mma(jv ? ld8<T>(kb + (int64_t)(t0 + jr) * ks + 16 * s + 8 * hh) : zero8<T>(),
@@ -461,7 +579,7 @@ __global__ __launch_bounds__(256) void delta_wy_bwd_kernel(DeltaArgs a, DeltaLay
       X1T[l * PX + i] = (T)x1[e];
     }
   }
-  __syncthreads();  // X1T complete; dUT / dWT no longer needed
+  __syncthreads();  // X1T complete; dUn / dWT no longer needed
   load_tile64x<T, T, DK, 1, PX, false, true>(kb, t0, Tn, ks, nullptr, KT, tid, nullptr);
   __syncthreads();
 
@@ -588,8 +706,11 @@ template <typename T, int DK, int DV, bool GATED>
 hipError_t launch_delta_bwd(const DeltaArgs& a, hipStream_t stream) {
   const DeltaLayout L = delta_layout(a.B, a.T, a.H, DK, DV, sizeof(T));
   const int BH = a.B * a.H;
-  delta_state_bwd_kernel<T, DK, DV, GATED><<<dim3(BH * (DV / 32)), dim3(64), 0, stream>>>(a, L);
+  delta_bwd_pre_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);
   hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  delta_state_bwd_kernel<T, DK, DV, GATED><<<dim3(BH * (DV / 32)), dim3(64), 0, stream>>>(a, L);
+  e = hipGetLastError();
   if (e != hipSuccess) return e;
   delta_bwd_chunk_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);
   e = hipGetLastError();

@@ -19,10 +19,11 @@
 //
 // Kernel 1 (delta_prep) is parallel over (batch, head, chunk): G, the Gram
 // matrix, the triangular solve, W, U and the transposed / pre-scaled
-// operand copies the state passes read.  Kernel 2 (delta_state_fwd) walks
+// operand copies the state pass reads.  Kernel 2 (delta_state_fwd) walks
 // the chunks in order: one wave per (batch, head, 32 value columns) keeps
-// its slice of S in MFMA accumulators and produces Vn, o and the per-chunk
-// states h with every operand read straight into registers.
+// its slice of S in MFMA accumulators and writes v_new and the per-chunk
+// states, with every operand read straight into registers.  Kernel 3
+// (delta_out) forms o in parallel over chunks from those.
 #include "common.h"
 #include "delta_kernels.h"
 
@@ -40,18 +41,20 @@ DeltaLayout delta_layout(int B, int T, int H, int DK, int DV, int eb) {
   L.Gc = take(BH * Tp * 4);
   L.Tm = take(BH * NT * 4096 * eb);
   L.W = take(BH * Tp * DK * eb);
-  L.U = take(BH * Tp * DV * eb);
+  L.UT = take(BH * Tp * DV * eb);
   L.WT = take(BH * Tp * DK * eb);
   L.KdT = take(BH * Tp * DK * eb);
   L.QgT = take(BH * Tp * DK * eb);
   L.Aqk = take(BH * NT * 4096 * eb);
   L.AqkT = take(BH * NT * 4096 * eb);
-  L.h = take(BH * NT * DK * DV * eb);
-  L.Vn = take(BH * Tp * DV * eb);
+  L.hT = take(BH * NT * DK * DV * eb);
+  L.VnT = take(BH * Tp * DV * eb);
   L.ctx_bytes = off;
   off = 0;
-  L.dVn = take(BH * Tp * DV * eb);
-  L.dh = take(BH * NT * DK * DV * eb);
+  L.dVnlT = take(BH * Tp * DV * 4);
+  L.ZT = take(BH * NT * DK * DV * 4);
+  L.dVnT = take(BH * Tp * DV * eb);
+  L.dhT = take(BH * NT * DK * DV * eb);
   L.dW = take(BH * Tp * DK * 4);
   L.dKp = take(BH * Tp * DK * 4);
   L.dGp = take(BH * Tp * 4);
@@ -265,7 +268,7 @@ __global__ __launch_bounds__(256) void delta_prep_kernel(DeltaArgs a, DeltaLayou
     __syncthreads();
     const int it = w & 1;
     const int i = 32 * it + cl;
-    T* urow = (T*)(a.ctx + L.U) + ((size_t)bh * Tp + t0 + i) * DV;
+    T* ut = (T*)(a.ctx + L.UT) + ci * DV * 64;
 #pragma unroll
     for (int m = 0; m < DV / 64; ++m) {
       const int vt = (w >> 1) + 2 * m;
@@ -275,134 +278,126 @@ __global__ __launch_bounds__(256) void delta_prep_kernel(DeltaArgs a, DeltaLayou
         acc = mma(ld8<T>(Xt + (32 * vt + cl) * PX + 16 * s + 8 * hh),
                   ld8<T>(Tt + i * PX + 16 * s + 8 * hh), acc);
 #pragma unroll
-      for (int I = 0; I < 4; ++I)
-        st4<T>(urow + 32 * vt + 8 * I + 4 * hh,
-               to4<T>(acc[4 * I], acc[4 * I + 1], acc[4 * I + 2], acc[4 * I + 3]));
+      for (int e = 0; e < 16; ++e)
+        ut[(32 * vt + 8 * (e >> 2) + 4 * hh + (e & 3)) * 64 + i] = (T)acc[e];
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 2: sequential state pass + output.  One wave per (b, h, 32 value
-// columns); S[d][v] lives in DK/32 accumulator tiles with lane column v.
+// Kernel 2: sequential state pass.  One wave per (b, h, 32 value columns);
+// S[d][v] lives in DK/32 accumulator tiles with lane column v.  Per chunk
+// the chain is  v_new = U - W S  ->  S <- e^gamma S + Kd^T v_new; the W
+// operands of the next chunk are loaded while the current one computes.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
 __global__ __launch_bounds__(64) void delta_state_fwd_kernel(DeltaArgs a, DeltaLayout L) {
   constexpr int NDT = DK / 32;
   constexpr int NVB = DV / 32;
   const int lane = threadIdx.x, cl = lane & 31, hh = lane >> 5;
-  const int Tn = a.T, H = a.H, NT = a.NT;
+  const int NT = a.NT;
   const int vb = blockIdx.x % NVB, bh = blockIdx.x / NVB;
-  const int b = bh / H, h = bh % H;
   const int v = 32 * vb + cl;
   const size_t Tp = (size_t)NT * kChunk;
 
-  const T* qb = (const T*)a.q + ((size_t)b * Tn * H + h) * DK;
-  const int64_t qks = (int64_t)H * DK;
-  T* ob = (T*)a.o + ((size_t)b * Tn * H + h) * DV;
-  const int64_t os = (int64_t)H * DV;
   const float* Gc = reinterpret_cast<const float*>(a.ctx + L.Gc) + (size_t)bh * Tp;
   const T* Wg = (const T*)(a.ctx + L.W) + (size_t)bh * Tp * DK;
-  const T* Ug = (const T*)(a.ctx + L.U) + (size_t)bh * Tp * DV;
-  T* Vng = (T*)(a.ctx + L.Vn) + (size_t)bh * Tp * DV;
 
   f32x16 S[NDT];
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) {
+  for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-    for (int I = 0; I < 4; ++I)
+    for (int e = 0; e < 16; ++e) {
+      const int d = 32 * dt + 8 * (e >> 2) + 4 * hh + (e & 3);
+      S[dt][e] = a.h0 ? a.h0[((size_t)bh * DK + d) * DV + v] : 0.f;
+    }
+
+  // W operands: [it][db][j] for rows 32 it + cl of a chunk
+  v8_t<T> wc[2][NDT][2];
+  auto load_w = [&](v8_t<T> (&dst)[2][NDT][2], int c) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d = 32 * dt + 8 * I + 4 * hh + r;
-        S[dt][4 * I + r] = a.h0 ? a.h0[((size_t)bh * DK + d) * DV + v] : 0.f;
-      }
-  }
+    for (int it = 0; it < 2; ++it)
+#pragma unroll
+      for (int db = 0; db < NDT; ++db)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          dst[it][db][j] = ld_tr_op<T>(Wg + (size_t)(c * kChunk + 32 * it + cl) * DK + 32 * db, j, hh);
+  };
+  load_w(wc, 0);
 
 #pragma unroll 1
   for (int c = 0; c < NT; ++c) {
-    const int t0 = c * kChunk;
     const size_t ci = (size_t)bh * NT + c;
-    // state entering the chunk
-    T* hg = (T*)(a.ctx + L.h) + ci * DK * DV;
+    // this chunk's Kd^T operands and U, issued early
+    const T* kd = (const T*)(a.ctx + L.KdT) + ci * DK * 64;
+    v8_t<T> kop[NDT][2][2];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int d = 32 * dt + 8 * (e >> 2) + 4 * hh + (e & 3);
-        hg[d * DV + v] = (T)S[dt][e];
-      }
+      for (int it = 0; it < 2; ++it)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+          kop[dt][it][jj] = ld_tr_op<T>(kd + (32 * dt + cl) * 64 + 32 * it, jj, hh);
+    const T* ut = (const T*)(a.ctx + L.UT) + (ci * DV + v) * 64;
+    v4_t<T> u4[2][4];
+#pragma unroll
+    for (int it = 0; it < 2; ++it)
+#pragma unroll
+      for (int I = 0; I < 4; ++I) u4[it][I] = ld4<T>(ut + 32 * it + 8 * I + 4 * hh);
+    const float eg = GATED ? __expf(Gc[c * kChunk + 63]) : 1.f;
+    v8_t<T> wn[2][NDT][2];
+    if (c + 1 < NT) load_w(wn, c + 1);
 
-    // P = W S and O = Q S; rows of this chunk in two 32-row tiles.
-    f32x16 P[2], O[2];
-    P[0] = P[1] = O[0] = O[1] = f32x16{};
+    // state entering the chunk, transposed [v][d]
+    T* hg = (T*)(a.ctx + L.hT) + (ci * DV + v) * DK;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+        st4<T>(hg + 32 * dt + 8 * I + 4 * hh,
+               to4<T>(S[dt][4 * I], S[dt][4 * I + 1], S[dt][4 * I + 2], S[dt][4 * I + 3]));
+
+    // P = W S
+    f32x16 P[2];
+    P[0] = P[1] = f32x16{};
 #pragma unroll
     for (int db = 0; db < NDT; ++db)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const v8_t<T> ys = c_to_b<T>(S[db], j);
 #pragma unroll
-        for (int it = 0; it < 2; ++it) {
-          const int ti = t0 + 32 * it + cl;
-          P[it] = mma(ld_tr_op<T>(Wg + (size_t)(t0 + 32 * it + cl) * DK + 32 * db, j, hh), ys, P[it]);
-          O[it] = mma(ti < Tn ? ld_tr_op<T>(qb + (int64_t)ti * qks + 32 * db, j, hh) : zero8<T>(),
-                      ys, O[it]);
-        }
+        for (int it = 0; it < 2; ++it) P[it] = mma(wc[it][db][j], ys, P[it]);
       }
 
-    // Vn = U - P (rows padded past T are zero in U and W)
+    // v_new = U - P (rows past T are zero in U and W), stored transposed
+    T* vg = (T*)(a.ctx + L.VnT) + (ci * DV + v) * 64;
     f32x16 Vn[2];
 #pragma unroll
     for (int it = 0; it < 2; ++it)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int i = 32 * it + 8 * (e >> 2) + 4 * hh + (e & 3);
-        const size_t off = (size_t)(t0 + i) * DV + v;
-        const float val = (float)Ug[off] - P[it][e];
-        Vn[it][e] = val;
-        Vng[off] = (T)val;
-      }
-
-    // o = scale e^G (Q S) + Aqk Vn
-    const T* aq = (const T*)(a.ctx + L.Aqk) + ci * 4096;
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-#pragma unroll
       for (int I = 0; I < 4; ++I) {
-        const int i = 32 * it + 8 * I + 4 * hh;
-        float f[4] = {a.scale, a.scale, a.scale, a.scale};
-        if constexpr (GATED) {
-          const f32x4 g4 = *reinterpret_cast<const f32x4*>(Gc + t0 + i);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) f[r] = a.scale * __expf(g4[r]);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) O[it][4 * I + r] *= f[r];
+        for (int r = 0; r < 4; ++r) Vn[it][4 * I + r] = (float)u4[it][I][r] - P[it][4 * I + r];
+        st4<T>(vg + 32 * it + 8 * I + 4 * hh,
+               to4<T>(Vn[it][4 * I], Vn[it][4 * I + 1], Vn[it][4 * I + 2], Vn[it][4 * I + 3]));
       }
-#pragma unroll
-      for (int jt = 0; jt < 2; ++jt)
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-          O[it] = mma(ld_tr_op<T>(aq + (32 * it + cl) * 64 + 32 * jt, jj, hh),
-                      c_to_b<T>(Vn[jt], jj), O[it]);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int t = t0 + 32 * it + 8 * (e >> 2) + 4 * hh + (e & 3);
-        if (t < Tn) ob[(int64_t)t * os + v] = (T)O[it][e];
-      }
-    }
 
-    // S <- e^gamma S + Kd^T Vn
-    const T* kd = (const T*)(a.ctx + L.KdT) + ci * DK * 64;
-    const float eg = GATED ? __expf(Gc[t0 + 63]) : 1.f;
+    // S <- e^gamma S + Kd^T v_new
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       if constexpr (GATED) S[dt] *= eg;
 #pragma unroll
       for (int it = 0; it < 2; ++it)
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-          S[dt] = mma(ld_tr_op<T>(kd + (32 * dt + cl) * 64 + 32 * it, jj, hh),
-                      c_to_b<T>(Vn[it], jj), S[dt]);
+        for (int jj = 0; jj < 2; ++jj) S[dt] = mma(kop[dt][it][jj], c_to_b<T>(Vn[it], jj), S[dt]);
+    }
+    if (c + 1 < NT) {
+#pragma unroll
+      for (int it = 0; it < 2; ++it)
+#pragma unroll
+        for (int db = 0; db < NDT; ++db)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) wc[it][db][j] = wn[it][db][j];
     }
   }
 
@@ -417,6 +412,55 @@ __global__ __launch_bounds__(64) void delta_state_fwd_kernel(DeltaArgs a, DeltaL
   }
 }
 
+// ---------------------------------------------------------------------------
+// Kernel 3: output, parallel over (b, h, chunk):
+//   o = scale e^G (Q h_c) + Aqk v_new.
+// Wave w: rows 32 (w & 1) + lane (lane column i), value half w >> 1.
+// ---------------------------------------------------------------------------
+template <typename T, int DK, int DV, bool GATED>
+__global__ __launch_bounds__(256) void delta_out_kernel(DeltaArgs a, DeltaLayout L) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int cl = lane & 31, hh = lane >> 5;
+  const int Tn = a.T, H = a.H, NT = a.NT;
+  const int c = blockIdx.x % NT, bh = blockIdx.x / NT;
+  const int b = bh / H, h = bh % H;
+  const int t0 = c * kChunk;
+  const size_t Tp = (size_t)NT * kChunk;
+  const size_t ci = (size_t)bh * NT + c;
+  const int i = 32 * (w & 1) + cl, ti = t0 + i;
+  const bool valid = ti < Tn;
+
+  const T* qrow = (const T*)a.q + (((size_t)b * Tn + ti) * H + h) * DK;
+  const T* arow = (const T*)(a.ctx + L.Aqk) + ci * 4096 + i * 64;
+  const T* hg = (const T*)(a.ctx + L.hT) + ci * DV * DK;
+  const T* vg = (const T*)(a.ctx + L.VnT) + ci * DV * 64;
+  v8_t<T> yq[DK / 16], ya[4];
+#pragma unroll
+  for (int s = 0; s < DK / 16; ++s) yq[s] = valid ? ld8<T>(qrow + 16 * s + 8 * hh) : zero8<T>();
+#pragma unroll
+  for (int s = 0; s < 4; ++s) ya[s] = ld8<T>(arow + 16 * s + 8 * hh);
+  float f = a.scale;
+  if constexpr (GATED) f *= __expf(reinterpret_cast<const float*>(a.ctx + L.Gc)[(size_t)bh * Tp + t0 + i]);
+  T* orow = (T*)a.o + (((size_t)b * Tn + ti) * H + h) * DV;
+#pragma unroll
+  for (int m = 0; m < DV / 64; ++m) {
+    const int vt = (w >> 1) * (DV / 64) + m;
+    f32x16 acc{};
+#pragma unroll
+    for (int s = 0; s < DK / 16; ++s)
+      acc = mma(ld8<T>(hg + (32 * vt + cl) * DK + 16 * s + 8 * hh), yq[s], acc);
+    acc *= f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc = mma(ld8<T>(vg + (32 * vt + cl) * 64 + 16 * s + 8 * hh), ya[s], acc);
+    if (valid) {
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+        st4<T>(orow + 32 * vt + 8 * I + 4 * hh,
+               to4<T>(acc[4 * I], acc[4 * I + 1], acc[4 * I + 2], acc[4 * I + 3]));
+    }
+  }
+}
+
 template <typename T, int DK, int DV, bool GATED>
 hipError_t launch_delta_fwd(const DeltaArgs& a, hipStream_t stream) {
   const DeltaLayout L = delta_layout(a.B, a.T, a.H, DK, DV, sizeof(T));
@@ -425,6 +469,9 @@ hipError_t launch_delta_fwd(const DeltaArgs& a, hipStream_t stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   delta_state_fwd_kernel<T, DK, DV, GATED><<<dim3(BH * (DV / 32)), dim3(64), 0, stream>>>(a, L);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  delta_out_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);
   return hipGetLastError();
 }
 

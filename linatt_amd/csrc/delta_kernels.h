@@ -23,18 +23,20 @@ struct DeltaLayout {
   size_t Gc;    // (B,H,Tp) f32  chunk-local inclusive cumsum of g (gated only)
   size_t Tm;    // (B,H,NT,64,64) T  (I + A)^-1, natural [i][j]
   size_t W;     // (B,H,Tp,DK) T  W = Tm diag(beta e^G) K
-  size_t U;     // (B,H,Tp,DV) T  U = Tm diag(beta) V
+  size_t UT;    // (B,H,NT,DV,64) T  (Tm diag(beta) V)^T per chunk
   size_t WT;    // (B,H,NT,DK,64) T  W^T per chunk
   size_t KdT;   // (B,H,NT,DK,64) T  (e^(gamma - G_i) k_i)^T per chunk
   size_t QgT;   // (B,H,NT,DK,64) T  (scale e^G_i q_i)^T per chunk
   size_t Aqk;   // (B,H,NT,64,64) T  scale (q_i.k_j) e^(G_i-G_j) [j <= i]
   size_t AqkT;  // (B,H,NT,64,64) T  its transpose
-  size_t h;     // (B,H,NT,DK,DV) T  state entering each chunk
-  size_t Vn;    // (B,H,Tp,DV) T  v_new = U - W h
+  size_t hT;    // (B,H,NT,DV,DK) T  state entering each chunk, transposed [v][d]
+  size_t VnT;   // (B,H,NT,DV,64) T  v_new^T per chunk, v_new = U - W h
   size_t ctx_bytes;
   // backward scratch
-  size_t dVn;   // (B,H,Tp,DV) T  gradient of v_new
-  size_t dh;    // (B,H,NT,DK,DV) T  gradient of the state leaving each chunk
+  size_t dVnlT; // (B,H,NT,DV,64) f32  Aqk^T dO per chunk, transposed
+  size_t ZT;    // (B,H,NT,DV,DK) f32  (scale e^G Q)^T dO per chunk, transposed
+  size_t dVnT;  // (B,H,NT,DV,64) T  gradient of v_new, transposed
+  size_t dhT;   // (B,H,NT,DV,DK) T  gradient of the state leaving each chunk, transposed
   size_t dW;    // (B,H,Tp,DK) f32
   size_t dKp;   // (B,H,Tp,DK) f32  dk from the output / state terms
   size_t dGp;   // (B,H,Tp) f32   dG from the output / state terms (+ d gamma at row 63)
