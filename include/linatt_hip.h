@@ -123,6 +123,42 @@ int linatt_delta_bwd(const void* q, const void* k, const void* v, const float* b
                      float* dbeta, float* dg, float* dh0, int B, int T, int H, int dk_dim,
                      int dv_dim, float scale, int dtype, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * KATA-SPD psi-state form: long-context prefill and recurrent decode.
+ * psi(x) = vec(x_g x_g^T) per group (full E^2 rows, p = g E^2 + a E + b),
+ * state S = sum_s psi(sqrt(scale) k_s) v_s^T (B,H,M*E^2,dv) float32 and
+ * z = sum_s psi(sqrt(scale) k_s) (B,H,M*E^2) float32.
+ * ------------------------------------------------------------------------- */
+
+/* 1 if the state-form kernels are compiled for the combination, else 0. */
+int linatt_kata_state_supported(int dtype, int dk, int dv, int num_groups);
+
+/* Bytes of scratch linatt_kata_prefill needs. */
+size_t linatt_kata_prefill_workspace_bytes(int B, int T, int H, int dk, int dv, int num_groups,
+                                           int seg_len, int dtype);
+
+/* Causal KATA forward in O(T) state form, plus the state after the last token.
+ * Replaces spd_chunk_scan_cat (kata/spd/chunk_scan_cat.py:219-345): same output
+ * o = num / max(den, eps) with den = sum_{s<=t} scale^2 sum_g (q_g.k_g)^2.
+ * T is split into segments of seg_len tokens (a multiple of 128): psi states
+ * across segments, the quadratic score inside a segment.
+ *   head_major = 1: q, k (B,H,T,dk), v, o (B,H,T,dv), den (B,H,T)  (reference layout)
+ *   head_major = 0: q, k (B,T,H,dk), v, o (B,T,H,dv), den (B,T,H)
+ *   S_out, z_out may be NULL. */
+int linatt_kata_prefill(const void* q, const void* k, const void* v, void* o, float* den,
+                        float* S_out, float* z_out, void* workspace, int B, int T, int H, int dk,
+                        int dv, int num_groups, float scale, float eps, int seg_len,
+                        int head_major, int dtype, void* stream);
+
+/* One recurrent decode token per (b, h): S += psi(sqrt(scale) k) v^T,
+ * z += psi(sqrt(scale) k), o = psi(sqrt(scale) q)^T S / max(psi(sqrt(scale) q).z, eps).
+ * q, k (B,H,dk), v, o (B,H,dv); S, z updated in place.  No reference
+ * counterpart: the reference's flash path keeps no decode state
+ * (kata/layer.py:492; eval_recall.py:133-144). */
+int linatt_kata_decode_step(const void* q, const void* k, const void* v, float* S, float* z,
+                            void* o, int B, int H, int dk, int dv, int num_groups, float scale,
+                            float eps, int dtype, void* stream);
+
 /* Row L2 normalisation over the last dim of a contiguous (n, d) array:
  * y = x / sqrt(sum x^2 + eps), rstd (n) float32 = 1 / sqrt(sum x^2 + eps);
  * backward dx = rstd (dy - y <y, dy>).  The normalisation fla applies to q

@@ -48,6 +48,10 @@ SIGNATURES = {
     "linatt_delta_bwd": (_i, [_vp] * 16 + [_i] * 5 + [_f, _i, _vp]),
     "linatt_l2norm_fwd": (_i, [_vp, _vp, _vp, _i, _i, _f, _i, _vp]),
     "linatt_l2norm_bwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "linatt_kata_state_supported": (_i, [_i, _i, _i, _i]),
+    "linatt_kata_prefill_workspace_bytes": (_sz, [_i] * 8),
+    "linatt_kata_prefill": (_i, [_vp] * 8 + [_i] * 6 + [_f, _f, _i, _i, _i, _vp]),
+    "linatt_kata_decode_step": (_i, [_vp] * 6 + [_i] * 5 + [_f, _f, _i, _vp]),
 }
 
 

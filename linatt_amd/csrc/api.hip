@@ -112,6 +112,53 @@ hipError_t dispatch_delta(const DeltaArgs& a, int dtype, int dk, int dv, bool ga
 
 int elt_bytes(int dtype) { return dtype == LINATT_FLOAT32 ? 4 : 2; }
 
+bool state_compiled(int dtype, int dk, int dv, int M) {
+#define LINATT_HAS_S(T, DK_, DV_, M_) \
+  if (dtype == dtype_of<T>() && dk == DK_ && dv == DV_ && M == M_) return true;
+  LINATT_KATA_STATE_SHAPES(LINATT_HAS_S)
+#undef LINATT_HAS_S
+  return false;
+}
+
+struct StateWs {
+  size_t seg_S, seg_z, HT, Hz, bytes;
+};
+
+StateWs state_ws(int B, int T, int H, int dk, int dv, int M, int L, int dtype) {
+  StateWs w{};
+  const size_t E = dk / M, P = M * E * E, BH = (size_t)B * H, nseg = (T + L - 1) / L;
+  auto al = [](size_t x) { return (x + 255) & ~size_t(255); };
+  size_t off = 0;
+  w.seg_S = off; off = al(off + BH * nseg * dv * P * 4);
+  w.seg_z = off; off = al(off + BH * nseg * P * 4);
+  w.HT = off; off = al(off + BH * nseg * dv * P * elt_bytes(dtype));
+  w.Hz = off; off = al(off + BH * nseg * P * 4);
+  w.bytes = off;
+  return w;
+}
+
+int check_state(const char* fn, int B, int T, int H, int dk, int dv, int M, float scale, float eps,
+                int L, int dtype) {
+  char buf[160];
+  snprintf(buf, sizeof buf, "B=%d T=%d H=%d dk=%d dv=%d num_groups=%d seg_len=%d", B, T, H, dk,
+           dv, M, L);
+  if (B <= 0 || T <= 0 || H <= 0 || dk <= 0 || dv <= 0 || M <= 0)
+    return fail(LINATT_EINVAL, std::string(fn) + ": non-positive dimension (" + buf + ")");
+  if (dk % M) return fail(LINATT_EINVAL, std::string(fn) + ": dk not divisible by num_groups");
+  if (!(scale > 0.f) || !(eps > 0.f))
+    return fail(LINATT_EINVAL, std::string(fn) + ": scale and eps must be positive");
+  if (L <= 0 || L % 128)
+    return fail(LINATT_EINVAL, std::string(fn) + ": seg_len must be a positive multiple of 128");
+  if (dtype != LINATT_FLOAT32 && dtype != LINATT_BFLOAT16 && dtype != LINATT_FLOAT16)
+    return fail(LINATT_EINVAL, std::string(fn) + ": unknown dtype");
+  if ((int64_t)B * T * H > (int64_t)INT32_MAX / 2)
+    return fail(LINATT_EINVAL, std::string(fn) + ": B*T*H too large");
+  if (!state_compiled(dtype, dk, dv, M))
+    return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": no kernel compiled for dtype " +
+                                         std::to_string(dtype) + " (" + buf + ")");
+  return LINATT_OK;
+}
+
 int check_delta(const char* fn, int B, int T, int H, int dk, int dv, float scale, int dtype) {
   char buf[160];
   snprintf(buf, sizeof buf, "B=%d T=%d H=%d dk=%d dv=%d", B, T, H, dk, dv);
@@ -323,6 +370,88 @@ int linatt_l2norm_bwd(const void* y, const float* rstd, const void* dy, void* dx
   else return fail(LINATT_EINVAL, "linatt_l2norm_bwd: unknown dtype");
   if (e != hipSuccess)
     return fail(LINATT_ELAUNCH, std::string("linatt_l2norm_bwd: launch failed: ") + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
+int linatt_kata_state_supported(int dtype, int dk, int dv, int num_groups) {
+  return state_compiled(dtype, dk, dv, num_groups) ? 1 : 0;
+}
+
+size_t linatt_kata_prefill_workspace_bytes(int B, int T, int H, int dk, int dv, int num_groups,
+                                           int seg_len, int dtype) {
+  if (B <= 0 || T <= 0 || H <= 0 || dk <= 0 || dv <= 0 || num_groups <= 0 || dk % num_groups ||
+      seg_len <= 0)
+    return 0;
+  return state_ws(B, T, H, dk, dv, num_groups, seg_len, dtype).bytes;
+}
+
+int linatt_kata_prefill(const void* q, const void* k, const void* v, void* o, float* den,
+                        float* S_out, float* z_out, void* workspace, int B, int T, int H, int dk,
+                        int dv, int num_groups, float scale, float eps, int seg_len,
+                        int head_major, int dtype, void* stream) {
+  g_last_error.clear();
+  int st = check_state("linatt_kata_prefill", B, T, H, dk, dv, num_groups, scale, eps, seg_len, dtype);
+  if (st) return st;
+  if (!q || !k || !v || !o || !den || !workspace)
+    return fail(LINATT_EINVAL, "linatt_kata_prefill: null tensor pointer");
+  const void* ps[] = {q, k, v, o, workspace, S_out, z_out};
+  for (const void* p : ps)
+    if (p && !aligned16(p))
+      return fail(LINATT_EINVAL, "linatt_kata_prefill: tensors must be 16-byte aligned");
+  const StateWs w = state_ws(B, T, H, dk, dv, num_groups, seg_len, dtype);
+  char* ws = (char*)workspace;
+  KataStateArgs a{};
+  a.q = q; a.k = k; a.v = v; a.o = o; a.den = den;
+  if (head_major) {  // (B, H, T, D)
+    a.sb = (int64_t)H * T * dk; a.sh = (int64_t)T * dk; a.st = dk;
+    a.vsb = (int64_t)H * T * dv; a.vsh = (int64_t)T * dv; a.vst = dv;
+    a.osb = a.vsb; a.osh = a.vsh; a.ost = a.vst;
+    a.dsb = (int64_t)H * T; a.dsh = T; a.dst = 1;
+  } else {           // (B, T, H, D)
+    a.sb = (int64_t)T * H * dk; a.st = (int64_t)H * dk; a.sh = dk;
+    a.vsb = (int64_t)T * H * dv; a.vst = (int64_t)H * dv; a.vsh = dv;
+    a.osb = a.vsb; a.ost = a.vst; a.osh = a.vsh;
+    a.dsb = (int64_t)T * H; a.dst = H; a.dsh = 1;
+  }
+  a.seg_S = (float*)(ws + w.seg_S); a.seg_z = (float*)(ws + w.seg_z);
+  a.HT = ws + w.HT; a.Hz = (float*)(ws + w.Hz);
+  a.S_out = S_out; a.z_out = z_out;
+  a.B = B; a.T = T; a.H = H; a.L = seg_len; a.nseg = (T + seg_len - 1) / seg_len;
+  a.scale = scale; a.scale2 = scale * scale; a.eps = eps;
+  hipError_t e = hipErrorInvalidValue;
+  hipStream_t sm = (hipStream_t)stream;
+#define LINATT_TRY_S(T_, DK_, DV_, M_) \
+  if (dtype == dtype_of<T_>() && dk == DK_ && dv == DV_ && num_groups == M_) e = launch_kata_prefill<T_, DK_, DV_, M_>(a, sm);
+  LINATT_KATA_STATE_SHAPES(LINATT_TRY_S)
+#undef LINATT_TRY_S
+  if (e != hipSuccess)
+    return fail(LINATT_ELAUNCH, std::string("linatt_kata_prefill: launch failed: ") + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
+int linatt_kata_decode_step(const void* q, const void* k, const void* v, float* S, float* z,
+                            void* o, int B, int H, int dk, int dv, int num_groups, float scale,
+                            float eps, int dtype, void* stream) {
+  g_last_error.clear();
+  int st = check_state("linatt_kata_decode_step", B, 1, H, dk, dv, num_groups, scale, eps, 128, dtype);
+  if (st) return st;
+  if (!q || !k || !v || !S || !z || !o)
+    return fail(LINATT_EINVAL, "linatt_kata_decode_step: null tensor pointer");
+  const void* ps[] = {S, z, o};
+  for (const void* p : ps)
+    if (!aligned16(p))
+      return fail(LINATT_EINVAL, "linatt_kata_decode_step: S, z, o must be 16-byte aligned");
+  KataDecodeArgs a{};
+  a.q = q; a.k = k; a.v = v; a.o = o; a.S = S; a.z = z; a.B = B; a.H = H;
+  a.scale = scale; a.eps = eps;
+  hipError_t e = hipErrorInvalidValue;
+  hipStream_t sm = (hipStream_t)stream;
+#define LINATT_TRY_DEC(T_, DK_, DV_, M_) \
+  if (dtype == dtype_of<T_>() && dk == DK_ && dv == DV_ && num_groups == M_) e = launch_kata_decode<T_, DK_, DV_, M_>(a, sm);
+  LINATT_KATA_STATE_SHAPES(LINATT_TRY_DEC)
+#undef LINATT_TRY_DEC
+  if (e != hipSuccess)
+    return fail(LINATT_ELAUNCH, std::string("linatt_kata_decode_step: launch failed: ") + hipGetErrorString(e));
   return LINATT_OK;
 }
 

@@ -45,3 +45,49 @@ hipError_t launch_kata_bwd(const KataArgs& a, int parts, hipStream_t stream);
   X(float, 64, 64, 4)
 
 }  // namespace linatt
+
+namespace linatt {
+
+// Long-context prefill in psi-state form and the recurrent decode step.
+// Element strides (in elements) describe q/k (sb, st, sh), v (vsb, vst, vsh)
+// and o (osb, ost, osh), so time-major and head-major inputs both work.
+struct KataStateArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* den;          // (B, T, H) or strided like o without the feature dim
+  int64_t sb, st, sh, vsb, vst, vsh, osb, ost, osh, dsb, dst, dsh;
+  float* seg_S;        // (B*H, nseg, DV, P) f32 scratch, per-segment Psi(K)^T V transposed
+  float* seg_z;        // (B*H, nseg, P) f32 scratch
+  void* HT;            // (B*H, nseg, DV, P) T scratch, exclusive prefix (unscaled)
+  float* Hz;           // (B*H, nseg, P) f32 scratch
+  float* S_out;        // (B, H, P, DV) f32 final state psi(sqrt(scale) k) v^T, or null
+  float* z_out;        // (B, H, P) f32, or null
+  int B, T, H, L, nseg;
+  float scale, scale2, eps;
+};
+
+template <typename T, int DK, int DV, int M>
+hipError_t launch_kata_prefill(const KataStateArgs& a, hipStream_t stream);
+
+struct KataDecodeArgs {
+  const void* q;   // (B, H, DK)
+  const void* k;
+  const void* v;   // (B, H, DV)
+  void* o;         // (B, H, DV)
+  float* S;        // (B, H, P, DV) f32, updated in place
+  float* z;        // (B, H, P) f32, updated in place
+  int B, H;
+  float scale, eps;
+};
+
+template <typename T, int DK, int DV, int M>
+hipError_t launch_kata_decode(const KataDecodeArgs& a, hipStream_t stream);
+
+// Compiled (dtype, DK, DV, M) combinations of the state form.
+#define LINATT_KATA_STATE_SHAPES(X) \
+  X(__bf16, 64, 64, 4)              \
+  X(__bf16, 64, 64, 2)
+
+}  // namespace linatt

@@ -1,0 +1,115 @@
+"""KATA-SPD in psi-state form on MI355X: O(T) long-context prefill and the
+recurrent decode step.
+
+* ``spd_chunk_scan_cat(q, k, v, M, scale=None, C=32, eps=1e-6, ...)`` keeps
+  the signature of the reference's concat tree-scan
+  (``kata/spd/chunk_scan_cat.py:219-345``): head-major ``(B, H, T, D)``
+  inputs, returns ``(o, den)`` with ``o = num / max(den, eps)``.  ``C``,
+  ``warps`` and ``stages`` are accepted and ignored; ``feature`` must be
+  ``"quad"``.
+* ``kata_prefill(q, k, v, num_groups=4, scale=None, eps=1e-6, seg_len=1024)``
+  takes the time-major ``(B, T, H, D)`` layout of the flash path and also
+  returns the state after the last token: ``S = sum_s psi(sqrt(scale) k_s)
+  v_s^T`` ``(B, H, M*E*E, dv)`` and ``z = sum_s psi(sqrt(scale) k_s)``
+  ``(B, H, M*E*E)``, float32, ``psi(x) = vec(x_g x_g^T)`` per group.
+* ``kata_decode_step(S, z, q, k, v, num_groups=4, scale=None, eps=1e-6)``
+  appends one token per ``(b, h)`` (``q, k, v`` of shape ``(B, H, D)``),
+  updating ``S`` and ``z`` in place, and returns ``o (B, H, dv)``.  The
+  reference's flash path keeps no decode state (``kata/layer.py:492``); this
+  is the state the ``past_key_values`` cache would hold.
+
+All three run in ``liblinatt_hip.so`` (``linatt_kata_prefill``,
+``linatt_kata_decode_step``); unsupported shapes raise.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+_lib.load()
+
+__all__ = ["spd_chunk_scan_cat", "kata_prefill", "kata_decode_step"]
+
+
+def _scale(dk, num_groups, scale):
+    return 1.0 / math.sqrt(dk // num_groups) if scale is None else float(scale)
+
+
+def _check(dtype, dk, dv, M):
+    L = _lib.load()
+    if not L.linatt_kata_state_supported(_lib.dtype_code(dtype), dk, dv, M):
+        raise NotImplementedError(
+            f"linatt_amd state form: no kernel for {dtype}, dk={dk}, dv={dv}, num_groups={M}")
+    return L
+
+
+def _prefill(q, k, v, M, scale, eps, seg_len, head_major, want_state):
+    _lib.require_device(q, k, v)
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("q, k, v must share a dtype")
+    if head_major:
+        B, H, T, dk = q.shape
+    else:
+        B, T, H, dk = q.shape
+    dv = v.shape[-1]
+    if k.shape != q.shape or v.shape[:-1] != q.shape[:-1]:
+        raise ValueError("q, k, v shapes do not match")
+    if dk % M:
+        raise ValueError(f"d_k={dk} not divisible by M={M}")
+    L = _check(q.dtype, dk, dv, M)
+    sc = _scale(dk, M, scale)
+    dt = _lib.dtype_code(q.dtype)
+    P = M * (dk // M) ** 2
+    o = torch.empty_like(v)
+    den = torch.empty(q.shape[:-1], device=q.device, dtype=torch.float32)
+    S = z = None
+    if want_state:
+        S = torch.empty(B, H, P, dv, device=q.device, dtype=torch.float32)
+        z = torch.empty(B, H, P, device=q.device, dtype=torch.float32)
+    ws = torch.empty(L.linatt_kata_prefill_workspace_bytes(B, T, H, dk, dv, M, seg_len, dt),
+                     device=q.device, dtype=torch.uint8)
+    _lib.check("linatt_kata_prefill", L.linatt_kata_prefill(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(den), _lib.ptr(S),
+        _lib.ptr(z), _lib.ptr(ws), B, T, H, dk, dv, M, sc, float(eps), seg_len,
+        1 if head_major else 0, dt, _lib.stream_of(q)))
+    return o, den, S, z
+
+
+def spd_chunk_scan_cat(q, k, v, M, scale=None, C=32, eps=1e-6, warps=4, stages=None,
+                       feature="quad"):
+    """Concat-SPD causal forward in state form, head-major ``(B, H, T, D)``
+    (reference ``kata/spd/chunk_scan_cat.py:219-345``).  Returns ``(o, den)``."""
+    if feature != "quad":
+        raise NotImplementedError("linatt_amd: only feature='quad' (psi = vec(x x^T))")
+    o, den, _, _ = _prefill(q, k, v, M, scale, eps, 1024, True, False)
+    return o, den
+
+
+def kata_prefill(q, k, v, num_groups=4, scale=None, eps=1e-6, seg_len=1024):
+    """Time-major ``(B, T, H, D)`` prefill: ``(o, den, S, z)``."""
+    return _prefill(q, k, v, num_groups, scale, eps, seg_len, False, True)
+
+
+def kata_decode_step(S, z, q, k, v, num_groups=4, scale=None, eps=1e-6):
+    """One token per ``(b, h)``: updates ``S``, ``z`` in place and returns ``o``."""
+    _lib.require_device(S, z, q, k, v)
+    B, H, dk = q.shape
+    dv = v.shape[-1]
+    M = num_groups
+    P = M * (dk // M) ** 2
+    if S.shape != (B, H, P, dv) or z.shape != (B, H, P):
+        raise ValueError(f"state must be S {(B, H, P, dv)}, z {(B, H, P)}")
+    if S.dtype != torch.float32 or z.dtype != torch.float32 or not (S.is_contiguous() and z.is_contiguous()):
+        raise ValueError("S and z must be contiguous float32 (updated in place)")
+    L = _check(q.dtype, dk, dv, M)
+    q, k, v = q.contiguous(), k.to(q.dtype).contiguous(), v.to(q.dtype).contiguous()
+    o = torch.empty(B, H, dv, device=q.device, dtype=q.dtype)
+    _lib.check("linatt_kata_decode_step", L.linatt_kata_decode_step(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(S), _lib.ptr(z), _lib.ptr(o), B, H, dk,
+        dv, M, _scale(dk, M, scale), float(eps), _lib.dtype_code(q.dtype), _lib.stream_of(q)))
+    return o

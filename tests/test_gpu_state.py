@@ -1,0 +1,162 @@
+"""GPU parity of the psi-state KATA prefill and decode step
+against the float64 CPU oracle (``oracle/kata.py``: ``kata_prefill_fwd_state_form``,
+``kata_state_prefill``, ``kata_decode_step``, ``kata_fwd``, themselves pinned by
+``tests/test_oracle_kata.py::test_state_form``).
+
+Inputs are seeded on the CPU, rounded once to bf16, and the same rounded
+tensors (upcast) feed the oracle.  Metric: max-abs-relative error per
+tensor, bar 2e-2 (bf16).  Every case calls the C ABI through
+``linatt_amd.spd_state``.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import kata as K
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+TOL = 2e-2
+
+
+def mar(x, ref):
+    x = x.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    den = ref.abs().max().item()
+    return (x - ref).abs().max().item() / (den if den > 0 else 1.0)
+
+
+def gen(shape, seed, std=0.125):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * std).to(BF)
+
+
+@pytest.fixture(scope="module")
+def S_():
+    from linatt_amd import spd_state as S_
+    return S_
+
+
+@pytest.mark.parametrize("M", [4, 2])
+@pytest.mark.parametrize("case", [(1, 1, 1, 128), (2, 300, 2, 128), (1, 1000, 3, 256),
+                                  (1, 640, 2, 128), (2, 257, 1, 1024)],
+                         ids=lambda c: "B{}T{}H{}L{}".format(*c))
+def test_prefill_parity(S_, M, case):
+    B, T, H, Lseg = case
+    print(f"case {case} M={M}", flush=True)
+    q, k, v = gen((B, T, H, 64), 1 + T), gen((B, T, H, 64), 2 + T), gen((B, T, H, 64), 3 + T)
+    o_ref, den_ref, S_ref, z_ref = K.kata_prefill_fwd_state_form(q, k, v, M, eps=1e-6)
+    dev = torch.device("cuda")
+    o, den, S, z = S_.kata_prefill(q.to(dev), k.to(dev), v.to(dev), num_groups=M, seg_len=Lseg)
+    assert o.dtype == BF and den.dtype == torch.float32
+    for name, x, ref in (("o", o, o_ref), ("den", den, den_ref), ("S", S, S_ref), ("z", z, z_ref)):
+        e = mar(x, ref)
+        assert e < TOL, (name, e)
+
+
+def test_head_major_scan_cat(S_):
+    """Reference layout (B, H, T, D) through spd_chunk_scan_cat."""
+    B, T, H = 1, 700, 2
+    q, k, v = gen((B, T, H, 64), 11), gen((B, T, H, 64), 12), gen((B, T, H, 64), 13)
+    o_ref, den_ref, _, _ = K.kata_prefill_fwd_state_form(q, k, v, 4, eps=1e-6)
+    dev = torch.device("cuda")
+    hm = lambda x: x.transpose(1, 2).contiguous().to(dev)  # noqa: E731
+    o, den = S_.spd_chunk_scan_cat(hm(q), hm(k), hm(v), 4)
+    assert o.shape == (B, H, T, 64) and den.shape == (B, H, T)
+    assert mar(o.transpose(1, 2), o_ref) < TOL
+    assert mar(den.transpose(1, 2), den_ref) < TOL
+
+
+@pytest.mark.parametrize("M", [4, 2])
+def test_decode_equals_parallel_row(S_, M):
+    """Decode after an n-token prefill == row n of the dense parallel form."""
+    B, n, H = 2, 333, 3
+    q, k, v = gen((B, n + 1, H, 64), 21), gen((B, n + 1, H, 64), 22), gen((B, n + 1, H, 64), 23)
+    dev = torch.device("cuda")
+    _, _, S, z = S_.kata_prefill(q[:, :n].to(dev), k[:, :n].to(dev), v[:, :n].to(dev),
+                                 num_groups=M, seg_len=128)
+    S0, z0 = S.cpu().double(), z.cpu().double()
+    o = S_.kata_decode_step(S, z, q[:, n].to(dev), k[:, n].to(dev), v[:, n].to(dev), num_groups=M)
+    o_par, _ = K.kata_fwd(q, k, v, M)
+    assert mar(o, o_par[:, n]) < TOL
+    o_ref, S_ref, z_ref = K.kata_decode_step(S0, z0, q[:, n], k[:, n], v[:, n], M)
+    assert mar(o, o_ref) < TOL
+    assert mar(S, S_ref) < TOL
+    assert mar(z, z_ref) < TOL
+
+
+def test_decode_multi_step(S_):
+    """Eight decode steps at batch 4 from a zero state match the oracle step by step."""
+    B, H, M = 4, 2, 4
+    P = M * 16 * 16
+    dev = torch.device("cuda")
+    S = torch.zeros(B, H, P, 64, device=dev)
+    z = torch.zeros(B, H, P, device=dev)
+    Sr = torch.zeros(B, H, P, 64, dtype=torch.float64)
+    zr = torch.zeros(B, H, P, dtype=torch.float64)
+    for i in range(8):
+        q, k, v = gen((B, H, 64), 100 + i), gen((B, H, 64), 200 + i), gen((B, H, 64), 300 + i)
+        o = S_.kata_decode_step(S, z, q.to(dev), k.to(dev), v.to(dev), num_groups=M)
+        o_ref, Sr, zr = K.kata_decode_step(Sr, zr, q, k, v, M)
+        assert mar(o, o_ref) < TOL, i
+    assert mar(S, Sr) < TOL and mar(z, zr) < TOL
+
+
+def _row_ref(q, k, v, b, h, t, M, eps=1e-6):
+    """Row t of the causal output in float64 (O(t) work)."""
+    E = 64 // M
+    scale = 1.0 / math.sqrt(E)
+    qt = q[b, t, h].double().reshape(M, E)
+    ks = k[b, :t + 1, h].double().reshape(t + 1, M, E)
+    A = ((ks * qt).sum(-1) * scale).pow(2).sum(-1)  # (t+1,)
+    den = max(A.sum().item(), eps)
+    return (A[:, None] * v[b, :t + 1, h].double()).sum(0) / den, den
+
+
+def test_config5_full_size(S_):
+    """B=1 H=12 D=64 M=4 bf16, T=32768 prefill (seed 4)
+    -> fp32 state, then decode steps at batch 64 (prefill state broadcast,
+    fresh q, k, v ~ N(0,1)/8 from seed 4000+i).  Sampled output rows and
+    state rows are checked against float64 sums over the whole prefix; the
+    decode steps against the float64 decode step on two (b, h) slices."""
+    B, T, H, M = 1, 32768, 12, 4
+    g = torch.Generator().manual_seed(4)
+    q, k, v = ((torch.randn(B, T, H, 64, generator=g) / 8).to(BF) for _ in range(3))
+    dev = torch.device("cuda")
+    o, den, S, z = S_.kata_prefill(q.to(dev), k.to(dev), v.to(dev), num_groups=M)
+    assert torch.isfinite(o.float()).all() and torch.isfinite(S).all()
+    oc, denc = o.cpu(), den.cpu()
+    for (h, t) in ((0, 0), (3, 1023), (5, 1024), (11, 5000), (7, 20000), (2, 32767)):
+        ro, rd = _row_ref(q, k, v, 0, h, t, M)
+        e = (oc[0, t, h].double() - ro).abs().max().item() / ro.abs().max().item()
+        assert e < TOL, ("o row", h, t, e)
+        assert abs(denc[0, t, h].item() - rd) / rd < TOL, ("den row", h, t)
+    # state rows p = g E^2 + a E + b for a few p, all value columns, two heads
+    Sc = S.cpu()
+    kd, vd = k.double(), v.double()
+    for h in (0, 9):
+        for p in (0, 17, 255, 256 + 3 * 16 + 5, 1023):
+            gg, a_, b_ = p // 256, (p // 16) % 16, p % 16
+            w = kd[0, :, h, 16 * gg + a_] * kd[0, :, h, 16 * gg + b_] * 0.25
+            ref = (w[:, None] * vd[0, :, h]).sum(0)
+            e = (Sc[0, h, p].double() - ref).abs().max().item() / ref.abs().max().item()
+            assert e < TOL, ("S row", h, p, e)
+    # decode at batch 64 from the broadcast prefill state
+    Bd = 64
+    Sd = S.expand(Bd, H, -1, -1).contiguous()
+    zd = z.expand(Bd, H, -1).contiguous()
+    S_ref = {bh: (S[0, bh[1]].cpu().double().clone(), z[0, bh[1]].cpu().double().clone())
+             for bh in ((0, 0), (63, 11))}
+    for i in range(3):
+        gi = torch.Generator().manual_seed(4000 + i)
+        qd, kd_, vd_ = ((torch.randn(Bd, H, 64, generator=gi) / 8).to(BF) for _ in range(3))
+        od = S_.kata_decode_step(Sd, zd, qd.to(dev), kd_.to(dev), vd_.to(dev), num_groups=M)
+        for (bb, hh) in S_ref:
+            Sr, zr = S_ref[(bb, hh)]
+            sl = lambda x: x[bb:bb + 1, hh:hh + 1]  # noqa: E731
+            o_r, Sr, zr = K.kata_decode_step(Sr[None, None], zr[None, None], sl(qd), sl(kd_),
+                                             sl(vd_), M)
+            S_ref[(bb, hh)] = (Sr[0, 0], zr[0, 0])
+            assert mar(od[bb, hh], o_r[0, 0]) < TOL, (i, bb, hh)
