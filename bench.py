@@ -126,6 +126,91 @@ def bench_delta(gated, steps, warmup):
             "frac_mfma_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
 
 
+def bench_state(prefill_reps, decode_steps):
+    """KATA-SPD M=4, B=1 H=12 D=64 bf16.  A T=32768 prefill
+    (linatt_kata_prefill: o, den and the fp32 psi-state), then decode steps at
+    batch 64 from the broadcast prefill state with fresh q, k, v ~ N(0,1)/8
+    per step (seed 4000+i, all resident on the device before timing).
+    Algorithmic prefill work in the O(T) form: states 2 T P dv + readout
+    2 T P dv + chunk-local scores (SURVEY's 106 GFLOP); decode bytes per step:
+    the fp32 state read + written, 2 B H (P dv + P) 4 + inputs/outputs."""
+    import torch
+    from linatt_amd import _lib
+    L = _lib.load()
+    B, H, T, D, M = 1, 12, 32768, 64, 4
+    P = M * (D // M) ** 2
+    scale = 1.0 / math.sqrt(D // M)
+    g = torch.Generator().manual_seed(4)
+    q, k, v = ((torch.randn(B, T, H, D, generator=g) / 8).to(torch.bfloat16) for _ in range(3))
+    dev = torch.device("cuda", 0)
+    qd, kd, vd = (x.to(dev) for x in (q, k, v))
+    o = torch.empty_like(vd)
+    den = torch.empty(B, T, H, device=dev)
+    S = torch.empty(B, H, P, D, device=dev)
+    z = torch.empty(B, H, P, device=dev)
+    dt = _lib.LINATT_BFLOAT16
+    seg = 1024
+    ws = torch.empty(L.linatt_kata_prefill_workspace_bytes(B, T, H, D, D, M, seg, dt), device=dev,
+                     dtype=torch.uint8)
+    Pp = _lib.ptr
+    sp = _lib.stream_of(qd)
+    stream = torch.cuda.current_stream(dev)
+
+    def prefill():
+        _lib.check("linatt_kata_prefill", L.linatt_kata_prefill(
+            Pp(qd), Pp(kd), Pp(vd), Pp(o), Pp(den), Pp(S), Pp(z), Pp(ws), B, T, H, D, D, M, scale,
+            1e-6, seg, 0, dt, sp))
+
+    prefill()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(prefill_reps):
+        prefill()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    pre_ms = e0.elapsed_time(e1) / prefill_reps
+
+    Bd = 64
+    Sd = S.expand(Bd, H, -1, -1).contiguous()
+    zd = z.expand(Bd, H, -1).contiguous()
+    steps = []
+    for i in range(decode_steps):
+        gi = torch.Generator().manual_seed(4000 + i)
+        steps.append(tuple((torch.randn(Bd, H, D, generator=gi) / 8).to(torch.bfloat16).to(dev)
+                           for _ in range(3)))
+    od = torch.empty(Bd, H, D, device=dev, dtype=torch.bfloat16)
+
+    def decode(x):
+        _lib.check("linatt_kata_decode_step", L.linatt_kata_decode_step(
+            Pp(x[0]), Pp(x[1]), Pp(x[2]), Pp(Sd), Pp(zd), Pp(od), Bd, H, D, D, M, scale, 1e-6, dt,
+            sp))
+
+    decode(steps[0])
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for x in steps:
+        decode(x)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    dec_ms = e0.elapsed_time(e1) / decode_steps
+    pre_flops = 2 * (2 * T * P * D) * B * H + B * H * T * 32 * 2 * D  # states, readout, chunk scores
+    pre_bytes = B * H * T * D * 2 * 4 + B * H * T * 4 + B * H * (P * D + P) * 4
+    dec_bytes = 2 * Bd * H * (P * D + P) * 4 + Bd * H * 4 * D * 2
+    return {"config": {"B": B, "H": H, "T": T, "D": D, "num_groups": M, "seg_len": seg,
+                       "decode_batch": Bd, "decode_steps": decode_steps, "seed": 4},
+            "prefill_ms": round(pre_ms, 4),
+            "prefill_tokens_per_s": round(B * T / (pre_ms * 1e-3), 1),
+            "prefill_alg_gflop": round(pre_flops / 1e9, 2),
+            "prefill_tflops": round(pre_flops / (pre_ms * 1e-3) / 1e12, 1),
+            "prefill_hbm_frac": round(pre_bytes / (pre_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "decode_ms_per_step": round(dec_ms, 4),
+            "decode_steps_per_s": round(1e3 / dec_ms, 1),
+            "decode_bytes_per_step": dec_bytes,
+            "decode_gbs": round(dec_bytes / (dec_ms * 1e-3) / 1e9, 1),
+            "decode_hbm_frac": round(dec_bytes / (dec_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+
+
 def cpu_baseline(q, k, v, do, M, seconds):
     """Time the float32 restatement of the reference path (dense forward +
     explicit backward, kata/parallel_kata_attn.py:49-146) head by head on the
@@ -189,6 +274,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-delta", action="store_true")
+    ap.add_argument("--no-state", action="store_true")
+    ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 512 MiB device copy (counter calibration)")
     args = ap.parse_args()
@@ -273,6 +360,10 @@ def main():
         delta = {"deltanet_config3": bench_delta(False, max(3, args.steps // 2), 2),
                  "gated_deltanet_config4": bench_delta(True, max(3, args.steps // 2), 2)}
 
+    state = None
+    if not args.no_state:
+        state = bench_state(3, args.decode_steps)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(q, k, v, do, M, args.cpu_seconds)
@@ -302,6 +393,7 @@ def main():
                      "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None},
         "cpu_baseline": cpu,
         "delta_rule": delta,
+        "kata_state_config5": state,
     }
     print(json.dumps(out), flush=True)
 

@@ -72,6 +72,18 @@ int linatt_kata_bwd(const void* q, const void* k, const void* v, const void* o,
                     void* workspace, int B, int T, int HQ, int H, int dk_dim, int dv_dim,
                     int num_groups, float scale, int variant, int dtype, void* stream);
 
+/* Backward of the decayed concat score A[t,s] * exp(min(c_t - c_s, 0)):
+ * dq, dk, dv as linatt_kata_bwd plus dc (B,T,HQ) float32, the gradient of the
+ * cumulative log-decay c.  Replaces the O(T^2)-memory autograd recompute of
+ * _KataDecayFunction.backward (kata/parallel_kata_attn.py:313-347, through
+ * _kata_decay_ref :291-310).  o, den come from linatt_kata_fwd with the same c.
+ * Same workspace as linatt_kata_bwd. */
+int linatt_kata_bwd_decay(const void* q, const void* k, const void* v, const float* c,
+                          const void* o, const float* den, const void* dout, void* dq, void* dk,
+                          void* dv, float* dc, void* workspace, int B, int T, int HQ, int H,
+                          int dk_dim, int dv_dim, int num_groups, float scale, int dtype,
+                          void* stream);
+
 /* The two halves of linatt_kata_bwd, with its argument list, mirroring the
  * reference's separate dq and dk/dv launches (kata/parallel_kata_attn.py:488-528):
  * linatt_kata_bwd_dq writes dq and the per-row <o, dO> into workspace

@@ -40,6 +40,7 @@ SIGNATURES = {
     "linatt_kata_bwd_workspace_bytes": (_sz, [_i, _i, _i]),
     "linatt_kata_bwd": (_i, [_vp] * 10 + [_i] * 7 + [_f, _i, _i, _vp]),
     "linatt_kata_bwd_dq": (_i, [_vp] * 10 + [_i] * 7 + [_f, _i, _i, _vp]),
+    "linatt_kata_bwd_decay": (_i, [_vp] * 12 + [_i] * 7 + [_f, _i, _vp]),
     "linatt_kata_bwd_dkdv": (_i, [_vp] * 10 + [_i] * 7 + [_f, _i, _i, _vp]),
     "linatt_delta_supported": (_i, [_i, _i, _i]),
     "linatt_delta_ctx_bytes": (_sz, [_i] * 6),

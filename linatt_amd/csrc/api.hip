@@ -67,14 +67,15 @@ hipError_t dispatch_fwd(const KataArgs& a, int dtype, int variant, bool decay, h
   return hipSuccess;
 }
 
-hipError_t dispatch_bwd(const KataArgs& a, int parts, int dtype, int variant, hipStream_t s,
-                        bool* found) {
+hipError_t dispatch_bwd(const KataArgs& a, int parts, int dtype, int variant, bool decay,
+                        hipStream_t s, bool* found) {
   *found = false;
 #define LINATT_TRY_BWD(T, DK_, DV_, M_)                                             \
   if (dtype == dtype_of<T>() && a.DK == DK_ && a.DV == DV_ && a.M == M_) {          \
     *found = true;                                                                  \
-    if (variant == LINATT_KATA_SUM) return launch_kata_bwd<T, DK_, DV_, M_, true>(a, parts, s); \
-    return launch_kata_bwd<T, DK_, DV_, M_, false>(a, parts, s);                    \
+    if (decay) return launch_kata_bwd<T, DK_, DV_, M_, false, true>(a, parts, s);    \
+    if (variant == LINATT_KATA_SUM) return launch_kata_bwd<T, DK_, DV_, M_, true, false>(a, parts, s); \
+    return launch_kata_bwd<T, DK_, DV_, M_, false, false>(a, parts, s);             \
   }
   LINATT_KATA_SHAPES(LINATT_TRY_BWD)
 #undef LINATT_TRY_BWD
@@ -225,7 +226,7 @@ static int kata_bwd_entry(const char* fn, int parts, const void* q, const void* 
                           const void* o, const float* den, const void* dout, void* dq, void* dk,
                           void* dv, void* workspace, int B, int T, int HQ, int H, int dk_dim,
                           int dv_dim, int num_groups, float scale, int variant, int dtype,
-                          void* stream) {
+                          void* stream, const float* c = nullptr, float* dc = nullptr) {
   g_last_error.clear();
   int st = check_common(B, T, HQ, H, dk_dim, dv_dim, num_groups, scale, variant, dtype);
   if (st) return st;
@@ -242,8 +243,10 @@ static int kata_bwd_entry(const char* fn, int parts, const void* q, const void* 
   a.dout = dout; a.dq = dq; a.dk = dk; a.dv = dv; a.delta = (float*)workspace;
   a.B = B; a.T = T; a.HQ = HQ; a.H = H; a.DK = dk_dim; a.DV = dv_dim; a.M = num_groups;
   a.scale = scale;
+  a.c = c;
+  a.dc = dc;
   bool found = false;
-  hipError_t e = dispatch_bwd(a, parts, dtype, variant, (hipStream_t)stream, &found);
+  hipError_t e = dispatch_bwd(a, parts, dtype, variant, c != nullptr, (hipStream_t)stream, &found);
   if (!found)
     return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": no kernel compiled for " +
                                          shape_str(B, T, HQ, H, dk_dim, dv_dim, num_groups));
@@ -259,6 +262,20 @@ int linatt_kata_bwd(const void* q, const void* k, const void* v, const void* o,
   return kata_bwd_entry("linatt_kata_bwd", KATA_BWD_DQ | KATA_BWD_DKDV, q, k, v, o, den, dout,
                         dq, dk, dv, workspace, B, T, HQ, H, dk_dim, dv_dim, num_groups, scale,
                         variant, dtype, stream);
+}
+
+int linatt_kata_bwd_decay(const void* q, const void* k, const void* v, const float* c,
+                          const void* o, const float* den, const void* dout, void* dq, void* dk,
+                          void* dv, float* dc, void* workspace, int B, int T, int HQ, int H,
+                          int dk_dim, int dv_dim, int num_groups, float scale, int dtype,
+                          void* stream) {
+  if (!c || !dc) {
+    g_last_error = "linatt_kata_bwd_decay: null c or dc";
+    return LINATT_EINVAL;
+  }
+  return kata_bwd_entry("linatt_kata_bwd_decay", KATA_BWD_DQ | KATA_BWD_DKDV, q, k, v, o, den,
+                        dout, dq, dk, dv, workspace, B, T, HQ, H, dk_dim, dv_dim, num_groups,
+                        scale, LINATT_KATA_CONCAT, dtype, stream, c, dc);
 }
 
 int linatt_kata_bwd_dq(const void* q, const void* k, const void* v, const void* o,

@@ -25,12 +25,12 @@
 
 namespace linatt {
 
-template <typename T, int DK, int DV, int M, bool SUM>
+template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
 __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dq_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ o, const float* __restrict__ den, const T* __restrict__ dout,
-    T* __restrict__ dq, float* __restrict__ delta_out, int Tn, int HQ, int H, float scale2,
-    int nqt, int nbh) {
+    T* __restrict__ dq, float* __restrict__ delta_out, const float* __restrict__ c,
+    float* __restrict__ dc, int Tn, int HQ, int H, float scale2, int nqt, int nbh) {
   constexpr int E = DK / M;
   constexpr int KE = E / 16;
   constexpr int PAD = (sizeof(T) == 2 ? 8 : 4);
@@ -38,6 +38,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dq_kerne
   __shared__ __attribute__((aligned(16))) T Ks[64 * KP];
   __shared__ __attribute__((aligned(16))) T Kt[DK * TP];
   __shared__ __attribute__((aligned(16))) T Vs[64 * VP];
+  __shared__ __attribute__((aligned(16))) float Cs[64];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int cl = lane & 31, hh = lane >> 5;
@@ -79,6 +80,10 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dq_kerne
   f32x16 acc[DK / 32];
 #pragma unroll
   for (int rb = 0; rb < DK / 32; ++rb) acc[rb] = f32x16{};
+  // decay: D[t,s] = exp(min(c_t - c_s, 0)) scales dA; dc_t gets
+  // sum_s dA A [c_t - c_s <= 0] (the row part; the dk/dv kernel adds the column part)
+  const float ct = (DECAY && tvalid) ? c[qrow] : 0.f;
+  float dcr = 0.f;
 
   const int s_end = min(t0 + 128, Tn);
   const int nst = (s_end + 63) / 64;
@@ -87,6 +92,9 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dq_kerne
     __syncthreads();
     load_tile64<T, DK, KP, TP, true, true>(kb, s0, Tn, ks, Ks, Kt, tid);
     load_tile64<T, DV, VP, 1, true, false>(vb, s0, Tn, vs, Vs, nullptr, tid);
+    if constexpr (DECAY) {
+      if (tid < 64) Cs[tid] = (s0 + tid < Tn) ? c[((int64_t)b * Tn + s0 + tid) * HQ + hq] : 0.f;
+    }
     __syncthreads();
     if (s0 > tw + 31 || tw >= Tn) continue;
     const bool need_mask = (s0 + 63 > tw) || (s0 + 64 > Tn);
@@ -108,6 +116,20 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dq_kerne
             if (s > tl || s >= Tn) x[4 * i + r] = 0.f;
           }
       }
+      f32x16 msk;  // [c_t - c_s <= 0] (decay only)
+      if constexpr (DECAY) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f32x4 cs4 = *reinterpret_cast<const f32x4*>(Cs + 32 * sb + 8 * i + 4 * hh);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float dd = ct - cs4[r];
+            x[4 * i + r] *= __expf(fminf(dd, 0.f));
+            msk[4 * i + r] = dd <= 0.f ? 1.f : 0.f;
+          }
+        }
+      }
+      f32x16 au{};
       const T* krow = Ks + (32 * sb + cl) * KP + 8 * hh;
 #pragma unroll
       for (int gi = 0; gi < M; ++gi) {
@@ -117,6 +139,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dq_kerne
           f32x16 r{};
 #pragma unroll
           for (int kk = 0; kk < KE; ++kk) r = mma(ld8<T>(krow + gk * E + 16 * kk), qop[gi * KE + kk], r);
+          if constexpr (DECAY) au += r * r;
           const f32x16 da = r * x;
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
@@ -137,9 +160,17 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dq_kerne
           }
         }
       }
+      if constexpr (DECAY) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) dcr += x[e] * au[e] * msk[e];
+      }
     }
   }
 
+  if constexpr (DECAY) {
+    dcr += __shfl_xor(dcr, 32);
+    if (tvalid && hh == 0) dc[qrow] = dcr * pdl;
+  }
   if (tvalid) {
     const float f = 2.f * pdl;
     T* drow = dq + qrow * DK;
@@ -153,12 +184,12 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dq_kerne
   }
 }
 
-template <typename T, int DK, int DV, int M, bool SUM>
+template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
 __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const float* __restrict__ den, const float* __restrict__ delta, const T* __restrict__ dout,
-    T* __restrict__ dk, T* __restrict__ dv, int Tn, int HQ, int H, float scale2, int nst,
-    int nbh) {
+    T* __restrict__ dk, T* __restrict__ dv, const float* __restrict__ c, float* __restrict__ dc,
+    int Tn, int HQ, int H, float scale2, int nst, int nbh) {
   constexpr int E = DK / M;
   constexpr int KE = E / 16;
   constexpr int PAD = (sizeof(T) == 2 ? 8 : 4);
@@ -171,6 +202,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
   __shared__ __attribute__((aligned(16))) T Ot[DV * TP];
   __shared__ __attribute__((aligned(16))) float Dl[64];
   __shared__ __attribute__((aligned(16))) float Pd[64];
+  __shared__ __attribute__((aligned(16))) float Ct[64];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int cl = lane & 31, hh = lane >> 5;
@@ -204,6 +236,8 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
   for (int hq = h * G; hq < (h + 1) * G; ++hq) {
     const T* qb = q + ((int64_t)b * Tn) * qs + (int64_t)hq * DK;
     const T* ob = dout + ((int64_t)b * Tn) * os + (int64_t)hq * DV;
+    const float csl = (DECAY && svalid) ? c[((int64_t)b * Tn + sl) * HQ + hq] : 0.f;
+    float dcc = 0.f;
     for (int tt = s0 / 64; tt < ntt; ++tt) {
       const int t0 = tt * 64;
       __syncthreads();
@@ -220,6 +254,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
         }
         Dl[tid] = dl;
         Pd[tid] = pd;
+        if constexpr (DECAY) Ct[tid] = (t < Tn) ? c[((int64_t)b * Tn + t) * HQ + hq] : 0.f;
       }
       __syncthreads();
       if (t0 + 63 < sw || sw >= Tn) continue;
@@ -284,6 +319,21 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
               }
             }
         }
+        if constexpr (DECAY) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f32x4 ct4 = *reinterpret_cast<const f32x4*>(Ct + 32 * mb + 8 * i + 4 * hh);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float dd = ct4[r] - csl;
+              const float dec = __expf(fminf(dd, 0.f));
+              // column part of dc_s: -sum_t dA A [c_t - c_s <= 0]
+              dcc -= dd <= 0.f ? x[4 * i + r] * pdv[4 * i + r] * A[4 * i + r] * dec : 0.f;
+              A[4 * i + r] *= dec;
+              x[4 * i + r] *= dec;
+            }
+          }
+        }
         // fp16 keeps P in [0, 2^12] so small weights stay out of its subnormal
         // range (bf16 and fp32 have the fp32 exponent range); undone at the store
         const f32x16 P = A * (pdv * kPScale);
@@ -332,6 +382,10 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
         }
       }
     }
+    if constexpr (DECAY) {
+      dcc += __shfl_xor(dcc, 32);
+      if (svalid && hh == 0) dc[((int64_t)b * Tn + sl) * HQ + hq] += dcc;
+    }
   }
 
   if (svalid) {
@@ -354,31 +408,32 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
   }
 }
 
-template <typename T, int DK, int DV, int M, bool SUM>
+template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
 hipError_t launch_kata_bwd(const KataArgs& a, int parts, hipStream_t stream) {
   const float scale2 = a.scale * a.scale;
   const int nqt = (a.T + 127) / 128;
   if (parts & KATA_BWD_DQ) {
     const int nbh = a.B * a.HQ;
-    kata_bwd_dq_kernel<T, DK, DV, M, SUM><<<dim3(nqt * nbh), dim3(256), 0, stream>>>(
+    kata_bwd_dq_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbh), dim3(256), 0, stream>>>(
         (const T*)a.q, (const T*)a.k, (const T*)a.v, (const T*)a.o, a.den, (const T*)a.dout,
-        (T*)a.dq, a.delta, a.T, a.HQ, a.H, scale2, nqt, nbh);
+        (T*)a.dq, a.delta, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt, nbh);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (parts & KATA_BWD_DKDV) {
     const int nbk = a.B * a.H;
-    kata_bwd_dkdv_kernel<T, DK, DV, M, SUM><<<dim3(nqt * nbk), dim3(256), 0, stream>>>(
+    kata_bwd_dkdv_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbk), dim3(256), 0, stream>>>(
         (const T*)a.q, (const T*)a.k, (const T*)a.v, a.den, a.delta, (const T*)a.dout,
-        (T*)a.dk, (T*)a.dv, a.T, a.HQ, a.H, scale2, nqt, nbk);
+        (T*)a.dk, (T*)a.dv, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt, nbk);
     return hipGetLastError();
   }
   return hipSuccess;
 }
 
-#define LINATT_BWD_INST(T, DK, DV, M)                                                          \
-  template hipError_t launch_kata_bwd<T, DK, DV, M, false>(const KataArgs&, int, hipStream_t); \
-  template hipError_t launch_kata_bwd<T, DK, DV, M, true>(const KataArgs&, int, hipStream_t);
+#define LINATT_BWD_INST(T, DK, DV, M)                                                                 \
+  template hipError_t launch_kata_bwd<T, DK, DV, M, false, false>(const KataArgs&, int, hipStream_t); \
+  template hipError_t launch_kata_bwd<T, DK, DV, M, true, false>(const KataArgs&, int, hipStream_t);  \
+  template hipError_t launch_kata_bwd<T, DK, DV, M, false, true>(const KataArgs&, int, hipStream_t);
 
 LINATT_KATA_SHAPES(LINATT_BWD_INST)
 

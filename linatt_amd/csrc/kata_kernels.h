@@ -18,6 +18,7 @@ struct KataArgs {
   void* dk;          // (B, T, H, DK)
   void* dv;          // (B, T, H, DV)
   float* delta;      // (B, T, HQ) workspace: <o, dO> per row
+  float* dc;         // (B, T, HQ) gradient of the cumulative log-decay c (decay backward)
   int B, T, HQ, H, DK, DV, M;
   float scale;
 };
@@ -28,7 +29,7 @@ hipError_t launch_kata_fwd(const KataArgs& a, hipStream_t stream);
 // parts: bit 0 = dq kernel (also writes delta), bit 1 = dk/dv kernel (reads delta)
 enum { KATA_BWD_DQ = 1, KATA_BWD_DKDV = 2 };
 
-template <typename T, int DK, int DV, int M, bool SUM>
+template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
 hipError_t launch_kata_bwd(const KataArgs& a, int parts, hipStream_t stream);
 
 // Compiled (dtype, DK, DV, M) combinations.  Each is built for the concat

@@ -217,8 +217,10 @@ def parallel_kata_attn_sum(q, k, v, num_groups=4, scale=None, bT=64, bK=64, use_
 
 
 class _KataDecayFunction(torch.autograd.Function):
-    """Reference ``kata/parallel_kata_attn.py:313-347``: HIP forward; the
-    backward (incl. dc) is not yet implemented in HIP and raises."""
+    """Reference ``kata/parallel_kata_attn.py:313-347``: forward and backward
+    (dq, dk, dv and dc) on the HIP kernels (``linatt_kata_fwd`` with ``c``,
+    ``linatt_kata_bwd_decay``), without the reference's O(T^2)-memory
+    autograd recompute."""
 
     @staticmethod
     def forward(ctx, q, k, v, c, num_groups, scale):
@@ -227,12 +229,29 @@ class _KataDecayFunction(torch.autograd.Function):
         o, den = parallel_kata_attn_fwd_impl(q, k, v, num_groups, scale, 64, 64, c=c)
         ctx.save_for_backward(q, k, v, c, o, den)
         ctx.num_groups, ctx.scale = num_groups, scale
+        ctx.dtypes = (q.dtype, k.dtype, v.dtype, c.dtype)
         return o
 
     @staticmethod
     def backward(ctx, do):
-        raise NotImplementedError(
-            "linatt_amd: the decayed KATA backward has no HIP kernel yet")
+        q, k, v, c, o, den = ctx.saved_tensors
+        qc, kc, vc = _prep(q, k, v)
+        cf = c.float().contiguous()
+        do = do.to(vc.dtype).contiguous()
+        B, T, HQ, dk = qc.shape
+        H, dv = kc.shape[2], vc.shape[-1]
+        dq, dk_, dv_ = torch.empty_like(qc), torch.empty_like(kc), torch.empty_like(vc)
+        dc = torch.empty_like(cf)
+        L = _lib.load()
+        ws = torch.empty(L.linatt_kata_bwd_workspace_bytes(B, T, HQ) // 4, device=q.device,
+                         dtype=torch.float32)
+        _lib.check("linatt_kata_bwd_decay", L.linatt_kata_bwd_decay(
+            _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(cf), _lib.ptr(o.contiguous()),
+            _lib.ptr(den.float().contiguous()), _lib.ptr(do), _lib.ptr(dq), _lib.ptr(dk_),
+            _lib.ptr(dv_), _lib.ptr(dc), _lib.ptr(ws), B, T, HQ, H, dk, dv, ctx.num_groups,
+            float(ctx.scale), _lib.dtype_code(vc.dtype), _lib.stream_of(qc)))
+        qd, kd, vd, cd = ctx.dtypes
+        return dq.to(qd), dk_.to(kd), dv_.to(vd), dc.to(cd), None, None
 
 
 def parallel_kata_attn_decay(q, k, v, c, num_groups=2, scale=None):

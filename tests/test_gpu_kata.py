@@ -187,3 +187,36 @@ def test_deterministic(P):
         outs.append((o, den) + grads)
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1), (2, 37, 2), (1, 190, 3), (2, 300, 2)],
+                         ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("cmode", ["cumulative", "arbitrary"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+def test_decay_fwd_bwd(P, shape, M, cmode, dtype):
+    """Decayed concat score (reference _KataDecayFunction, parallel_kata_attn.py:313-354):
+    o, dq, dk, dv and dc against float64 autograd through the restated
+    _kata_decay_ref.  'cumulative' c is a running sum of log decays (the
+    layer's use, kata/layer.py:440-447); 'arbitrary' c exercises the
+    min(c_t - c_s, 0) clamp and its gradient mask."""
+    B, T, H = shape
+    q, k, v, do = make(B, T, H, H, 64, 64, dtype, seed=40 + T + M)
+    g = torch.Generator().manual_seed(41 + T)
+    if cmode == "cumulative":
+        c = -torch.cumsum(torch.rand(B, T, H, generator=g) * 0.1, dim=1)
+    else:
+        c = torch.randn(B, T, H, generator=g) * 0.5
+    o_ref, dq_ref, dk_ref, dv_ref, dc_ref = K.kata_decay_fwd_bwd(q, k, v, c, do, M)
+    dev = torch.device("cuda")
+    leaves = [x.to(dev).requires_grad_(True) for x in (q, k, v, c)]
+    o = P.parallel_kata_attn_decay(*leaves, num_groups=M)
+    o.backward(do.to(dev))
+    tol = TOL[dtype]
+    assert mar(o, o_ref) < tol
+    fl = grad_floors(q, k, v, do)
+    fl["dc"] = 0.1 * do.abs().max().item() * v.abs().max().item()
+    for name, leaf, ref in zip(("dq", "dk", "dv", "dc"), leaves, (dq_ref, dk_ref, dv_ref, dc_ref)):
+        assert leaf.grad.dtype == leaf.dtype
+        e = mar(leaf.grad, ref, fl[name])
+        assert e < tol, (name, e)
