@@ -275,6 +275,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-delta", action="store_true")
     ap.add_argument("--no-state", action="store_true")
+    ap.add_argument("--no-kata", action="store_true",
+                    help="skip the KATA config-2 timing (profiling the other workloads)")
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 512 MiB device copy (counter calibration)")
@@ -322,6 +324,8 @@ def main():
         _lib.check("linatt_kata_bwd_dkdv", L.linatt_kata_bwd_dkdv(*bargs))
 
     parts = [("fwd", fwd), ("bwd_dq", bwd_dq), ("bwd_dkdv", bwd_dkdv)]
+    if args.no_kata:
+        args.steps, args.warmup = 1, 0
     for _ in range(args.warmup):
         for _, f in parts:
             f()
