@@ -93,6 +93,21 @@ __device__ __forceinline__ v8_t<T> ld_tr_op(const T* row, int j, int h) {
   return cat44<T>(ld4<T>(row + 16 * j + 4 * h), ld4<T>(row + 16 * j + 8 + 4 * h));
 }
 
+// Index of the calling wave in its workgroup, read from the first lane so the
+// compiler treats it (and what derives from it) as wave-uniform: branches on
+// it become scalar branches instead of exec-masked regions.
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
+
+// Position of logical element e (0..31) of a 32-block in the "operand
+// order" layout: the eight elements ld_tr_op gathers for (j, h), rows
+// 16j + 4h + 0..3 and 16j + 8 + 4h + 0..3, become the 8 contiguous elements
+// at 16j + 8h, so a single 16-byte load (ld8 at 16j + 8h) replaces two.
+__host__ __device__ constexpr int opord32(int e) {
+  return (e & 16) | ((e & 4) << 1) | ((e & 8) >> 1) | (e & 3);
+}
+
 // C-layout fp32 block -> B operand (k-step j of its 32 rows), converted to T.
 template <typename T>
 __device__ __forceinline__ v8_t<T> c_to_b(const f32x16& a, int j) {

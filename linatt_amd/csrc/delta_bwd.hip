@@ -34,7 +34,7 @@ template <typename T, int DK, int DV, bool GATED>
 __global__ __launch_bounds__(256) void delta_bwd_pre_kernel(DeltaArgs a, DeltaLayout L) {
   constexpr int PX = 64 + 8;
   __shared__ __attribute__((aligned(16))) T dOT[DV * PX];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
   const int Tn = a.T, H = a.H, NT = a.NT;
   const int c = blockIdx.x % NT, bh = blockIdx.x / NT;
@@ -127,7 +127,7 @@ __global__ __launch_bounds__(64) void delta_state_bwd_kernel(DeltaArgs a, DeltaL
 #pragma unroll
       for (int it = 0; it < 2; ++it)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) wop[dt][it][j] = ld_tr_op<T>(wt + (32 * dt + cl) * 64 + 32 * it, j, hh);
+        for (int j = 0; j < 2; ++j) wop[dt][it][j] = ld8<T>(wt + (32 * dt + cl) * 64 + 32 * it + 16 * j + 8 * hh);
     const float* dvl = reinterpret_cast<const float*>(a.ws + L.dVnlT) + (ci * DV + v) * 64;
     const float* zt = reinterpret_cast<const float*>(a.ws + L.ZT) + (ci * DV + v) * DK;
     f32x4 dl4[2][4], z4[NDT][4];
@@ -246,7 +246,7 @@ __global__ __launch_bounds__(256) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
   T* KT = sm;             // phase C: K^T [d][j]
   T* QT = sm + DK * PX;   // phase C: Q^T [d][i]
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
   const int ib = w & 1, dhalf = w >> 1;
   const int Tn = a.T, H = a.H, NT = a.NT;
@@ -458,7 +458,7 @@ __global__ __launch_bounds__(256) void delta_wy_bwd_kernel(DeltaArgs a, DeltaLay
   __shared__ float Gs[64], Bs[64];
   __shared__ float red_b[2][64], red_g[2][64], red_rb[64];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
   const int ib = w & 1, chf = w >> 1;
   const int Tn = a.T, H = a.H, NT = a.NT;

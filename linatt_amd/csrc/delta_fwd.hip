@@ -77,7 +77,7 @@ __global__ __launch_bounds__(256) void delta_prep_kernel(DeltaArgs a, DeltaLayou
   __shared__ __attribute__((aligned(16))) float Ts[64 * PA];  // Tm fp32
   __shared__ __attribute__((aligned(16))) float Gs[64], Bs[64], Sc[64];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
   const int Tn = a.T, H = a.H, NT = a.NT;
   const int c = blockIdx.x % NT, bh = blockIdx.x / NT;
@@ -227,7 +227,10 @@ __global__ __launch_bounds__(256) void delta_prep_kernel(DeltaArgs a, DeltaLayou
     load_tile64x<T, T, DK, 1, PX, false, true>(kb, t0, Tn, qks, nullptr, Xt, tid, Sc);
     __syncthreads();
     dst = (T*)(a.ctx + L.KdT) + ci * DK * 64;
-    for (int idx = tid; idx < DK * 64; idx += 256) dst[idx] = Xt[(idx >> 6) * PX + (idx & 63)];
+    for (int idx = tid; idx < DK * 64; idx += 256) {
+      const int i = idx & 63;
+      dst[(idx & ~63) + (i & 32) + opord32(i & 31)] = Xt[(idx >> 6) * PX + i];
+    }
     __syncthreads();
     if (tid < 64) Sc[tid] = Bs[tid] * (GATED ? __expf(Gs[tid]) : 1.f);
     __syncthreads();
@@ -249,12 +252,14 @@ __global__ __launch_bounds__(256) void delta_prep_kernel(DeltaArgs a, DeltaLayou
       for (int s = 0; s < 4; ++s)
         acc = mma(ld8<T>(Xt + (32 * dt + cl) * PX + 16 * s + 8 * hh),
                   ld8<T>(Tt + i * PX + 16 * s + 8 * hh), acc);
+      const int ip = (i & 32) + opord32(i & 31);
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
         const int d = 32 * dt + 8 * I + 4 * hh;
-        st4<T>(wrow + d, to4<T>(acc[4 * I], acc[4 * I + 1], acc[4 * I + 2], acc[4 * I + 3]));
+        st4<T>(wrow + 32 * dt + opord32(8 * I + 4 * hh),
+               to4<T>(acc[4 * I], acc[4 * I + 1], acc[4 * I + 2], acc[4 * I + 3]));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) wt[(d + r) * 64 + i] = (T)acc[4 * I + r];
+        for (int r = 0; r < 4; ++r) wt[(d + r) * 64 + ip] = (T)acc[4 * I + r];
       }
     }
     __syncthreads();
@@ -321,7 +326,7 @@ __global__ __launch_bounds__(64) void delta_state_fwd_kernel(DeltaArgs a, DeltaL
       for (int db = 0; db < NDT; ++db)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          dst[it][db][j] = ld_tr_op<T>(Wg + (size_t)(c * kChunk + 32 * it + cl) * DK + 32 * db, j, hh);
+          dst[it][db][j] = ld8<T>(Wg + (size_t)(c * kChunk + 32 * it + cl) * DK + 32 * db + 16 * j + 8 * hh);
   };
   load_w(wc, 0);
 
@@ -337,7 +342,7 @@ __global__ __launch_bounds__(64) void delta_state_fwd_kernel(DeltaArgs a, DeltaL
       for (int it = 0; it < 2; ++it)
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj)
-          kop[dt][it][jj] = ld_tr_op<T>(kd + (32 * dt + cl) * 64 + 32 * it, jj, hh);
+          kop[dt][it][jj] = ld8<T>(kd + (32 * dt + cl) * 64 + 32 * it + 16 * jj + 8 * hh);
     const T* ut = (const T*)(a.ctx + L.UT) + (ci * DV + v) * 64;
     v4_t<T> u4[2][4];
 #pragma unroll
@@ -419,7 +424,7 @@ __global__ __launch_bounds__(64) void delta_state_fwd_kernel(DeltaArgs a, DeltaL
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
 __global__ __launch_bounds__(256) void delta_out_kernel(DeltaArgs a, DeltaLayout L) {
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
   const int Tn = a.T, H = a.H, NT = a.NT;
   const int c = blockIdx.x % NT, bh = blockIdx.x / NT;

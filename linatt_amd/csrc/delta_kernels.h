@@ -5,7 +5,9 @@
 // 64 tokens, NT = ceil(T / 64), Tp = 64 * NT.  q, k, v, o and their
 // gradients are time-major (B, T, H, D); beta, g, dbeta, dg are (B, T, H)
 // float32; states (B, H, DK, DV) float32.  Everything else lives in the
-// context / workspace buffers carved by delta_layout().
+// context / workspace buffers carved by delta_layout().  "Operand order"
+// (opord32 in common.h) permutes each 32-element block so that the MFMA
+// operand a lane needs is one contiguous 16-byte load.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -22,10 +24,10 @@ struct DeltaLayout {
   // context (written by the forward, read by the backward)
   size_t Gc;    // (B,H,Tp) f32  chunk-local inclusive cumsum of g (gated only)
   size_t Tm;    // (B,H,NT,64,64) T  (I + A)^-1, natural [i][j]
-  size_t W;     // (B,H,Tp,DK) T  W = Tm diag(beta e^G) K
+  size_t W;     // (B,H,Tp,DK) T  W = Tm diag(beta e^G) K, key dims in operand order
   size_t UT;    // (B,H,NT,DV,64) T  (Tm diag(beta) V)^T per chunk
-  size_t WT;    // (B,H,NT,DK,64) T  W^T per chunk
-  size_t KdT;   // (B,H,NT,DK,64) T  (e^(gamma - G_i) k_i)^T per chunk
+  size_t WT;    // (B,H,NT,DK,64) T  W^T per chunk, rows i in operand order
+  size_t KdT;   // (B,H,NT,DK,64) T  (e^(gamma - G_i) k_i)^T per chunk, rows i in operand order
   size_t QgT;   // (B,H,NT,DK,64) T  (scale e^G_i q_i)^T per chunk
   size_t Aqk;   // (B,H,NT,64,64) T  scale (q_i.k_j) e^(G_i-G_j) [j <= i]
   size_t AqkT;  // (B,H,NT,64,64) T  its transpose

@@ -39,9 +39,18 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dq_kerne
   __shared__ __attribute__((aligned(16))) T Kt[DK * TP];
   __shared__ __attribute__((aligned(16))) T Vs[64 * VP];
   __shared__ __attribute__((aligned(16))) float Cs[64];
+  __shared__ __attribute__((aligned(16))) T Zr[64];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
+  if (tid < 64) Zr[tid] = T(0);
+  // K^T row feeding dQ^T row 32 rb + cl of query group gi from key group gk;
+  // for E = 16 a 32-row block holds two groups and the lanes of the other
+  // group read the zero row instead
+  auto kt_row = [&](int gi, int gk, int rb) -> const T* {
+    if constexpr (E >= 32) return Kt + (gk * E + (32 * rb + cl - gi * E)) * TP;
+    else return ((cl >> 4) == (gi & 1)) ? Kt + (gk * E + (cl & 15)) * TP : Zr;
+  };
   int qt, bh;
   map_block(blockIdx.x, nqt, nbh, qt, bh, true);
   const int b = bh / HQ, hq = bh % HQ;
@@ -146,17 +155,8 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dq_kerne
             const v8_t<T> bop = c_to_b<T>(da, j);
             // dQ^T rows R = 32rb + cl belonging to query group gi take K^T rows of key group gk
 #pragma unroll
-            for (int rb = (gi * E) / 32; rb <= ((gi + 1) * E - 1) / 32; ++rb) {
-              const int R = 32 * rb + cl;
-              v8_t<T> aop;
-              if constexpr (E >= 32) {
-                aop = ld_tr_op<T>(Kt + (gk * E + (R - gi * E)) * TP + 32 * sb, j, hh);
-              } else {
-                aop = (R / E == gi) ? ld_tr_op<T>(Kt + (gk * E + (R % E)) * TP + 32 * sb, j, hh)
-                                    : zero8<T>();
-              }
-              acc[rb] = mma(aop, bop, acc[rb]);
-            }
+            for (int rb = (gi * E) / 32; rb <= ((gi + 1) * E - 1) / 32; ++rb)
+              acc[rb] = mma(ld_tr_op<T>(kt_row(gi, gk, rb) + 32 * sb, j, hh), bop, acc[rb]);
           }
         }
       }
@@ -203,9 +203,18 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
   __shared__ __attribute__((aligned(16))) float Dl[64];
   __shared__ __attribute__((aligned(16))) float Pd[64];
   __shared__ __attribute__((aligned(16))) float Ct[64];
+  __shared__ __attribute__((aligned(16))) T Zr[64];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
+  if (tid < 64) Zr[tid] = T(0);
+  // Q^T row feeding dK^T row 32 rb + cl of key group gk from query group gi;
+  // for E = 16 a 32-row block holds two groups and the lanes of the other
+  // group read the zero row instead
+  auto qt_row = [&](int gi, int gk, int rb) -> const T* {
+    if constexpr (E >= 32) return Qt + (gi * E + (32 * rb + cl - gk * E)) * TP;
+    else return ((cl >> 4) == (gk & 1)) ? Qt + (gi * E + (cl & 15)) * TP : Zr;
+  };
   int stile, bh;
   map_block(blockIdx.x, nst, nbh, stile, bh, false);
   const int b = bh / H, h = bh % H;
@@ -252,7 +261,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
           const float d = den[r];
           pd = scale2 / (d > 0.f ? d : 1.f);
         }
-        Dl[tid] = dl;
+        Dl[tid] = -dl;
         Pd[tid] = pd;
         if constexpr (DECAY) Ct[tid] = (t < Tn) ? c[((int64_t)b * Tn + t) * HQ + hq] : 0.f;
       }
@@ -263,81 +272,119 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
         const int tb = t0 + 32 * mb;
         if (tb + 31 < sw) continue;
         const bool need_mask = (tb < sw + 31) || (tb + 32 > Tn);
-        // x[t][s] = dO V^T - delta  (rows t, column s)
-        f32x16 x;
+        auto masked = [&](int e) {
+          const int t = tb + 8 * (e >> 2) + 4 * hh + (e & 3);
+          return t < sl || t >= Tn;
+        };
+        // x[t][s] = dO V^T - delta  (rows t, column s); Dl holds -delta
+        f32x16 x, pdv;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const f32x4 d4 = *reinterpret_cast<const f32x4*>(Dl + 32 * mb + 8 * i + 4 * hh);
+          const f32x4 p4 = *reinterpret_cast<const f32x4*>(Pd + 32 * mb + 8 * i + 4 * hh);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) x[4 * i + r] = -d4[r];
+          for (int r = 0; r < 4; ++r) {
+            x[4 * i + r] = d4[r];
+            pdv[4 * i + r] = p4[r];
+          }
         }
         const T* orow = Os + (32 * mb + cl) * OP + 8 * hh;
 #pragma unroll
         for (int kk = 0; kk < DV / 16; ++kk) x = mma(ld8<T>(orow + 16 * kk), vop[kk], x);
-        f32x16 pdv;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const f32x4 p4 = *reinterpret_cast<const f32x4*>(Pd + 32 * mb + 8 * i + 4 * hh);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) pdv[4 * i + r] = p4[r];
-        }
         const T* qrow = Qs + (32 * mb + cl) * QP + 8 * hh;
-        // scores r = Q K^T per group (rows t, column s)
-        constexpr int NR = SUM ? 1 : M;
-        f32x16 rg[NR];
-        f32x16 A{};
-        if constexpr (!SUM) {
+        // r = Q_gi K_gk^T for query group gi, key group gk (rows t, column s)
+        auto score = [&](int gi, int gk) {
+          f32x16 r{};
 #pragma unroll
-          for (int g = 0; g < M; ++g) {
-            f32x16 r{};
+          for (int kk = 0; kk < KE; ++kk) r = mma(ld8<T>(qrow + gi * E + 16 * kk), kop[gk * KE + kk], r);
+          return r;
+        };
+        // dK^T[(gk,e)][s] += sum_t Q^T[(gi,e)][t] r[t][s] xs[t][s]
+        auto dk_product = [&](const f32x16& r, const f32x16& xs, int gi, int gk) {
+          const f32x16 da = r * xs;
 #pragma unroll
-            for (int kk = 0; kk < KE; ++kk) r = mma(ld8<T>(qrow + g * E + 16 * kk), kop[g * KE + kk], r);
-            rg[g] = r;
-            A += r * r;
+          for (int j = 0; j < 2; ++j) {
+            const v8_t<T> bop = c_to_b<T>(da, j);
+#pragma unroll
+            for (int rb = (gk * E) / 32; rb <= ((gk + 1) * E - 1) / 32; ++rb)
+              dka[rb] = mma(ld_tr_op<T>(qt_row(gi, gk, rb) + 32 * mb, j, hh), bop, dka[rb]);
           }
-        } else {
+        };
+        // decay factors exp(min(c_t - c_s, 0)) and the mask [c_t - c_s <= 0]
+        auto decay_of = [&](int e, bool& nonpos) {
+          const float dd = Ct[32 * mb + 8 * (e >> 2) + 4 * hh + (e & 3)] - csl;
+          nonpos = dd <= 0.f;
+          return __expf(fminf(dd, 0.f));
+        };
+        f32x16 A{}, xs;
+        if constexpr (sizeof(T) == 2) {
+          // one pass per group: the score feeds A and its dK product at once
+          if (need_mask) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) x[e] = masked(e) ? 0.f : x[e];
+          }
+          if constexpr (DECAY) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              bool np;
+              x[e] *= decay_of(e, np);
+            }
+          }
+          xs = x * pdv;
 #pragma unroll
           for (int gi = 0; gi < M; ++gi)
 #pragma unroll
-            for (int gj = 0; gj < M; ++gj) {
-              f32x16 r{};
-#pragma unroll
-              for (int kk = 0; kk < KE; ++kk)
-                r = mma(ld8<T>(qrow + gi * E + 16 * kk), kop[gj * KE + kk], r);
+            for (int gj = 0; gj < (SUM ? M : 1); ++gj) {
+              const f32x16 r = score(gi, SUM ? gj : gi);
               A += r * r;
+              dk_product(r, xs, gi, SUM ? gj : gi);
             }
-        }
-        if (need_mask) {
+          if (need_mask) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
+            for (int e = 0; e < 16; ++e) A[e] = masked(e) ? 0.f : A[e];
+          }
+          if constexpr (DECAY) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int t = tb + 8 * i + 4 * hh + r;
-              if (t < sl || t >= Tn) {
-                A[4 * i + r] = 0.f;
-                x[4 * i + r] = 0.f;
-              }
-            }
-        }
-        if constexpr (DECAY) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const f32x4 ct4 = *reinterpret_cast<const f32x4*>(Ct + 32 * mb + 8 * i + 4 * hh);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float dd = ct4[r] - csl;
-              const float dec = __expf(fminf(dd, 0.f));
-              // column part of dc_s: -sum_t dA A [c_t - c_s <= 0]
-              dcc -= dd <= 0.f ? x[4 * i + r] * pdv[4 * i + r] * A[4 * i + r] * dec : 0.f;
-              A[4 * i + r] *= dec;
-              x[4 * i + r] *= dec;
+            for (int e = 0; e < 16; ++e) {
+              bool np;
+              const float dec = decay_of(e, np);
+              // column part of dc_s: -sum_t dA A [c_t - c_s <= 0] (xs carries the decay)
+              dcc -= np ? xs[e] * A[e] : 0.f;
+              A[e] *= dec;
             }
           }
+        } else {
+          // fp32 keeps the two-pass order (A from all scores, dV, then the
+          // dK products from recomputed scores): the one-pass order above
+          // gave wrong dV in fp32 builds with this compiler, while 16-bit
+          // builds of both orders agree bit for bit
+#pragma unroll
+          for (int gi = 0; gi < M; ++gi)
+#pragma unroll
+            for (int gj = 0; gj < (SUM ? M : 1); ++gj) {
+              const f32x16 r = score(gi, SUM ? gj : gi);
+              A += r * r;
+            }
+          if (need_mask) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              if (masked(e)) A[e] = x[e] = 0.f;
+          }
+          if constexpr (DECAY) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              bool np;
+              const float dec = decay_of(e, np);
+              dcc -= np ? x[e] * pdv[e] * A[e] * dec : 0.f;
+              A[e] *= dec;
+              x[e] *= dec;
+            }
+          }
+          xs = x * pdv;
         }
         // fp16 keeps P in [0, 2^12] so small weights stay out of its subnormal
         // range (bf16 and fp32 have the fp32 exponent range); undone at the store
         const f32x16 P = A * (pdv * kPScale);
-        const f32x16 xs = x * pdv;
         // dV^T[dv][s] += sum_t dO^T[dv][t] P[t][s]
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -346,39 +393,12 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
           for (int db = 0; db < DV / 32; ++db)
             dva[db] = mma(ld_tr_op<T>(Ot + (32 * db + cl) * TP + 32 * mb, j, hh), pb, dva[db]);
         }
-        // dK^T[(g,e)][s] += sum_t Q^T[(g',e)][t] da[t][s]
+        if constexpr (sizeof(T) == 4) {
 #pragma unroll
-        for (int gi = 0; gi < M; ++gi) {
+          for (int gi = 0; gi < M; ++gi)
 #pragma unroll
-          for (int gj = 0; gj < (SUM ? M : 1); ++gj) {
-            const int gk = SUM ? gj : gi;  // key group receiving the gradient
-            f32x16 r;
-            if constexpr (!SUM) {
-              r = rg[gi];
-            } else {
-              r = f32x16{};
-#pragma unroll
-              for (int kk = 0; kk < KE; ++kk)
-                r = mma(ld8<T>(qrow + gi * E + 16 * kk), kop[gj * KE + kk], r);
-            }
-            const f32x16 da = r * xs;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              const v8_t<T> bop = c_to_b<T>(da, j);
-#pragma unroll
-              for (int rb = (gk * E) / 32; rb <= ((gk + 1) * E - 1) / 32; ++rb) {
-                const int R = 32 * rb + cl;
-                v8_t<T> aop;
-                if constexpr (E >= 32) {
-                  aop = ld_tr_op<T>(Qt + (gi * E + (R - gk * E)) * TP + 32 * mb, j, hh);
-                } else {
-                  aop = (R / E == gk) ? ld_tr_op<T>(Qt + (gi * E + (R % E)) * TP + 32 * mb, j, hh)
-                                      : zero8<T>();
-                }
-                dka[rb] = mma(aop, bop, dka[rb]);
-              }
-            }
-          }
+            for (int gj = 0; gj < (SUM ? M : 1); ++gj)
+              dk_product(score(gi, SUM ? gj : gi), xs, gi, SUM ? gj : gi);
         }
       }
     }

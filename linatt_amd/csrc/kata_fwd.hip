@@ -42,7 +42,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_fwd_kernel(
   __shared__ __attribute__((aligned(16))) T Vt[DV * VP];
   __shared__ __attribute__((aligned(16))) float Cs[64];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
   int qt, bh;
   map_block(blockIdx.x, nqt, nbh, qt, bh, true);

@@ -38,7 +38,7 @@ __global__ __launch_bounds__(256) void kata_seg_state_kernel(KataStateArgs a) {
   constexpr int PX = 64 + 8;
   __shared__ __attribute__((aligned(16))) T Kt[DK * PX];
   __shared__ __attribute__((aligned(16))) T Vt[DV * PX];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
   constexpr int NPB = P / 128;
   int blk = blockIdx.x;
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(256, 2) void kata_prefill_out_kernel(KataStateArgs 
   __shared__ __attribute__((aligned(16))) T Vt[DV * VP];
   __shared__ __attribute__((aligned(16))) T Qa[128 * QP];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
   int qt, bh;
   map_block(blockIdx.x, nqt, nbh, qt, bh, true);
