@@ -30,6 +30,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T> struct vt;
 template <> struct vt<__bf16> { using v8 = bf16x8; using v4 = bf16x4; };
@@ -98,6 +99,26 @@ __device__ __forceinline__ v8_t<T> ld_tr_op(const T* row, int j, int h) {
 // it become scalar branches instead of exec-masked regions.
 __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
+
+// Direct global -> LDS copy (global_load_lds_dwordx4): lane l's 16 bytes at
+// p land at lds_base + 16 l.  lds_base must be the same for the whole wave.
+// The copy counts as an outstanding vector-memory load of the issuing wave
+// until it lands; the compiler does not track it, so readers wait with
+// vm_wait_barrier.
+__device__ __forceinline__ void dma16(const void* p, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(p, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) then s_barrier, as one compiler-opaque step (memory
+// clobber: no memory access moves across it).  Vector-memory loads of a
+// wave complete in issue order, so with N = the number of loads issued after
+// some load X, X has landed once vmcnt <= N, whatever stores are also in
+// flight (they only add to the count).
+template <int N>
+__device__ __forceinline__ void vm_wait_barrier() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"i"(N) : "memory");
 }
 
 // Position of logical element e (0..31) of a 32-block in the "operand

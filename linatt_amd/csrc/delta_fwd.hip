@@ -282,31 +282,110 @@ __global__ __launch_bounds__(256) void delta_prep_kernel(DeltaArgs a, DeltaLayou
       for (int s = 0; s < 4; ++s)
         acc = mma(ld8<T>(Xt + (32 * vt + cl) * PX + 16 * s + 8 * hh),
                   ld8<T>(Tt + i * PX + 16 * s + 8 * hh), acc);
+      const int ip = (i & 32) + opord32(i & 31);
 #pragma unroll
       for (int e = 0; e < 16; ++e)
-        ut[(32 * vt + 8 * (e >> 2) + 4 * hh + (e & 3)) * 64 + i] = (T)acc[e];
+        ut[(32 * vt + 8 * (e >> 2) + 4 * hh + (e & 3)) * 64 + ip] = (T)acc[e];
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 2: sequential state pass.  One wave per (b, h, 32 value columns);
-// S[d][v] lives in DK/32 accumulator tiles with lane column v.  Per chunk
-// the chain is  v_new = U - W S  ->  S <- e^gamma S + Kd^T v_new; the W
-// operands of the next chunk are loaded while the current one computes.
+// Kernel 2: sequential state pass.  One workgroup per (b, h) with one wave
+// per 32 value columns; S[d][v] lives in DK/32 accumulator tiles with lane
+// column v.  Per chunk the chain is
+//   v_new = U - W S  ->  S <- e^gamma S + Kd^T v_new.
+// W and Kd^T are the same for every wave of the head and U^T is split by
+// wave: all three reach LDS by direct global->LDS copies into a ring of three
+// slots, issued two chunks ahead (each wave copies 1/NW of W and of Kd^T and
+// its own U^T rows).  Tiles are stored XOR-swizzled by 16-byte chunk so the
+// operand reads of 16 consecutive rows hit distinct banks.
 // ---------------------------------------------------------------------------
+
+// Swizzled 16-byte slot of (row, chunk) in a row-major LDS tile with CPR
+// 16-byte chunks per row (XOR keeps it an involution within a row).
+template <int CPR>
+__device__ __forceinline__ int swz_slot(int row, int ch) {
+  if constexpr (CPR >= 16) return row * CPR + (ch ^ (row & 15));
+  else return row * CPR + (ch ^ ((row >> 1) & 7));
+}
+
+// Wave-level copy of 1 KiB (64 x 16 bytes) of a row-major tile with CPR
+// 16-byte chunks per row into its swizzled LDS image: op covers tile chunks
+// [64 op, 64 op + 64).
+template <int CPR>
+__device__ __forceinline__ void dma_tile_1k(const u32x4* g, u32x4* lds, int op, int lane) {
+  const int row = (64 * op + lane) / CPR, slot = lane % CPR;
+  const int ch = swz_slot<CPR>(row, slot) - row * CPR;  // global chunk held by this slot
+  dma16(g + row * CPR + ch, lds + 64 * op);
+}
+
+// A wave's 32 x 64 block of 16-bit values held in C layout (lane column =
+// tile row cl; cols 32 b + 8 I + 4 hh + r of fp32 blocks X[b], b = 0, 1)
+// written to global rows g + row * ld through a private 4 KiB LDS staging
+// area: 8-byte LDS writes, then 16-byte reads that give each global store
+// instruction 1 KiB of whole rows.
+template <typename T>
+__device__ __forceinline__ void store_rows_staged(const f32x16& x0, const f32x16& x1, u32x4* stage,
+                                                  T* g, int ld, int lane) {
+  const int cl = lane & 31, hh = lane >> 5;
+  char* st = reinterpret_cast<char*>(stage);
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const f32x16& x = b ? x1 : x0;
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+      *reinterpret_cast<v4_t<T>*>(st + 16 * swz_slot<8>(cl, 4 * b + I) + 8 * hh) =
+          to4<T>(x[4 * I], x[4 * I + 1], x[4 * I + 2], x[4 * I + 3]);
+  }
+#pragma unroll
+  for (int op = 0; op < 4; ++op) {
+    const int gi = 64 * op + lane, row = gi >> 3, ch = gi & 7;
+    const u32x4 val = stage[swz_slot<8>(row, ch)];
+    *reinterpret_cast<u32x4*>(g + (size_t)row * ld + 8 * ch) = val;
+  }
+}
+
 template <typename T, int DK, int DV, bool GATED>
-__global__ __launch_bounds__(64) void delta_state_fwd_kernel(DeltaArgs a, DeltaLayout L) {
-  constexpr int NDT = DK / 32;
-  constexpr int NVB = DV / 32;
-  const int lane = threadIdx.x, cl = lane & 31, hh = lane >> 5;
+__global__ __launch_bounds__(64 * (DV / 32)) void delta_state_fwd_kernel(DeltaArgs a, DeltaLayout L,
+                                                                       const float* __restrict__ gcum) {
+  constexpr int NDT = DK / 32, NW = DV / 32;
+  constexpr int WT16 = 64 * DK * (int)sizeof(T) / 16;   // 16-byte chunks per W (= Kd^T) tile
+  constexpr int UT16 = 32 * 64 * (int)sizeof(T) / 16;   // per wave's U^T rows
+  constexpr int WCPR = DK * (int)sizeof(T) / 16;         // chunks per W row
+  constexpr int KCPR = 64 * (int)sizeof(T) / 16;         // chunks per Kd^T / U^T row
+  constexpr int SLOT = 2 * WT16 + NW * UT16;             // W | Kd^T | U^T per chunk
+  constexpr int WOPS = WT16 / 64 / NW, UOPS = UT16 / 64;  // 1 KiB copies per wave
+  constexpr int DMA_PER_CHUNK = 2 * WOPS + UOPS;
+  static_assert(WOPS * 64 * NW == WT16 && UOPS * 64 == UT16, "tile split");
+  __shared__ __attribute__((aligned(16))) u32x4 Sh[3 * SLOT];
+
+  const int lane = threadIdx.x & 63, w = wave_id();
+  const int cl = lane & 31, hh = lane >> 5;
   const int NT = a.NT;
-  const int vb = blockIdx.x % NVB, bh = blockIdx.x / NVB;
-  const int v = 32 * vb + cl;
+  const int bh = blockIdx.x;
+  const int v = 32 * w + cl;
   const size_t Tp = (size_t)NT * kChunk;
 
-  const float* Gc = reinterpret_cast<const float*>(a.ctx + L.Gc) + (size_t)bh * Tp;
-  const T* Wg = (const T*)(a.ctx + L.W) + (size_t)bh * Tp * DK;
+  // gcum = the Gc context buffer, passed on its own as __restrict__ so the
+  // per-chunk gate is a scalar load (no vector-memory wait in the chain)
+  const float* Gc = gcum + (size_t)bh * Tp;
+  const u32x4* Wg = reinterpret_cast<const u32x4*>(a.ctx + L.W) + (size_t)bh * NT * WT16;
+  const u32x4* Kg = reinterpret_cast<const u32x4*>(a.ctx + L.KdT) + (size_t)bh * NT * WT16;
+  const u32x4* Ug = reinterpret_cast<const u32x4*>(a.ctx + L.UT) + (size_t)bh * NT * NW * UT16;
+
+  // this wave's share of chunk c into ring slot c % 3
+  auto issue = [&](int c) __attribute__((always_inline)) {
+    u32x4* sl = Sh + (c % 3) * SLOT;
+#pragma unroll
+    for (int i = 0; i < WOPS; ++i) {
+      dma_tile_1k<WCPR>(Wg + (size_t)c * WT16, sl, WOPS * w + i, lane);
+      dma_tile_1k<KCPR>(Kg + (size_t)c * WT16, sl + WT16, WOPS * w + i, lane);
+    }
+#pragma unroll
+    for (int i = 0; i < UOPS; ++i)
+      dma_tile_1k<KCPR>(Ug + ((size_t)c * NW + w) * UT16, sl + 2 * WT16 + w * UT16, i, lane);
+  };
 
   f32x16 S[NDT];
 #pragma unroll
@@ -317,52 +396,21 @@ __global__ __launch_bounds__(64) void delta_state_fwd_kernel(DeltaArgs a, DeltaL
       S[dt][e] = a.h0 ? a.h0[((size_t)bh * DK + d) * DV + v] : 0.f;
     }
 
-  // W operands: [it][db][j] for rows 32 it + cl of a chunk
-  v8_t<T> wc[2][NDT][2];
-  auto load_w = [&](v8_t<T> (&dst)[2][NDT][2], int c) {
-#pragma unroll
-    for (int it = 0; it < 2; ++it)
-#pragma unroll
-      for (int db = 0; db < NDT; ++db)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          dst[it][db][j] = ld8<T>(Wg + (size_t)(c * kChunk + 32 * it + cl) * DK + 32 * db + 16 * j + 8 * hh);
-  };
-  load_w(wc, 0);
-
+  issue(0);
+  if (NT > 1) issue(1);
 #pragma unroll 1
   for (int c = 0; c < NT; ++c) {
+    // chunk c landed for every wave (only chunk c + 1's copies may remain in
+    // flight), and every wave is done with chunk c - 1, whose slot is refilled
+    if (c + 1 < NT) vm_wait_barrier<DMA_PER_CHUNK>();
+    else vm_wait_barrier<0>();
+    if (c + 2 < NT) issue(c + 2);
     const size_t ci = (size_t)bh * NT + c;
-    // this chunk's Kd^T operands and U, issued early
-    const T* kd = (const T*)(a.ctx + L.KdT) + ci * DK * 64;
-    v8_t<T> kop[NDT][2][2];
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int it = 0; it < 2; ++it)
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-          kop[dt][it][jj] = ld8<T>(kd + (32 * dt + cl) * 64 + 32 * it + 16 * jj + 8 * hh);
-    const T* ut = (const T*)(a.ctx + L.UT) + (ci * DV + v) * 64;
-    v4_t<T> u4[2][4];
-#pragma unroll
-    for (int it = 0; it < 2; ++it)
-#pragma unroll
-      for (int I = 0; I < 4; ++I) u4[it][I] = ld4<T>(ut + 32 * it + 8 * I + 4 * hh);
-    const float eg = GATED ? __expf(Gc[c * kChunk + 63]) : 1.f;
-    v8_t<T> wn[2][NDT][2];
-    if (c + 1 < NT) load_w(wn, c + 1);
+    const u32x4* Ws = Sh + (c % 3) * SLOT;
+    const u32x4* Ks = Ws + WT16;
+    const u32x4* Us = Ws + 2 * WT16 + w * UT16;
 
-    // state entering the chunk, transposed [v][d]
-    T* hg = (T*)(a.ctx + L.hT) + (ci * DV + v) * DK;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int I = 0; I < 4; ++I)
-        st4<T>(hg + 32 * dt + 8 * I + 4 * hh,
-               to4<T>(S[dt][4 * I], S[dt][4 * I + 1], S[dt][4 * I + 2], S[dt][4 * I + 3]));
-
-    // P = W S
+    // P = W S  (W rows 32 it + cl, key dims in operand order)
     f32x16 P[2];
     P[0] = P[1] = f32x16{};
 #pragma unroll
@@ -371,38 +419,47 @@ __global__ __launch_bounds__(64) void delta_state_fwd_kernel(DeltaArgs a, DeltaL
       for (int j = 0; j < 2; ++j) {
         const v8_t<T> ys = c_to_b<T>(S[db], j);
 #pragma unroll
-        for (int it = 0; it < 2; ++it) P[it] = mma(wc[it][db][j], ys, P[it]);
+        for (int it = 0; it < 2; ++it)
+          P[it] = mma(__builtin_bit_cast(v8_t<T>, Ws[swz_slot<WCPR>(32 * it + cl, 4 * db + 2 * j + hh)]), ys, P[it]);
       }
 
-    // v_new = U - P (rows past T are zero in U and W), stored transposed
-    T* vg = (T*)(a.ctx + L.VnT) + (ci * DV + v) * 64;
+    // v_new = U - P (rows past T are zero in U and W); U^T rows of this
+    // wave, chunk rows in operand order
     f32x16 Vn[2];
 #pragma unroll
     for (int it = 0; it < 2; ++it)
 #pragma unroll
-      for (int I = 0; I < 4; ++I) {
+      for (int jq = 0; jq < 2; ++jq) {
+        const v8_t<T> u8 = __builtin_bit_cast(v8_t<T>, Us[swz_slot<KCPR>(cl, 4 * it + 2 * jq + hh)]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Vn[it][4 * I + r] = (float)u4[it][I][r] - P[it][4 * I + r];
-        st4<T>(vg + 32 * it + 8 * I + 4 * hh,
-               to4<T>(Vn[it][4 * I], Vn[it][4 * I + 1], Vn[it][4 * I + 2], Vn[it][4 * I + 3]));
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const int I = 2 * jq + s2;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) Vn[it][4 * I + r] = (float)u8[4 * s2 + r] - P[it][4 * I + r];
+        }
       }
+    // v_new^T and the state entering the chunk (h^T, [v][d]) go out through
+    // this wave's U^T area of the slot, which the wave alone reads and has
+    // finished with
+    u32x4* stage = const_cast<u32x4*>(Us);
+    T* rows = (T*)(a.ctx + L.VnT) + (ci * DV + 32 * w) * 64;
+    store_rows_staged<T>(Vn[0], Vn[1], stage, rows, 64, lane);
+    T* hrows = (T*)(a.ctx + L.hT) + (ci * DV + 32 * w) * DK;
+#pragma unroll
+    for (int blk = 0; blk < NDT / 2; ++blk)
+      store_rows_staged<T>(S[2 * blk], S[2 * blk + 1], stage, hrows + 64 * blk, DK, lane);
 
-    // S <- e^gamma S + Kd^T v_new
+    // S <- e^gamma S + Kd^T v_new  (Kd^T rows 32 dt + cl, chunk rows in operand order)
+    const float eg = GATED ? __expf(Gc[c * kChunk + 63]) : 1.f;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       if constexpr (GATED) S[dt] *= eg;
 #pragma unroll
       for (int it = 0; it < 2; ++it)
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) S[dt] = mma(kop[dt][it][jj], c_to_b<T>(Vn[it], jj), S[dt]);
-    }
-    if (c + 1 < NT) {
-#pragma unroll
-      for (int it = 0; it < 2; ++it)
-#pragma unroll
-        for (int db = 0; db < NDT; ++db)
-#pragma unroll
-          for (int j = 0; j < 2; ++j) wc[it][db][j] = wn[it][db][j];
+        for (int jj = 0; jj < 2; ++jj)
+          S[dt] = mma(__builtin_bit_cast(v8_t<T>, Ks[swz_slot<KCPR>(32 * dt + cl, 4 * it + 2 * jj + hh)]),
+                      c_to_b<T>(Vn[it], jj), S[dt]);
     }
   }
 
@@ -473,7 +530,8 @@ hipError_t launch_delta_fwd(const DeltaArgs& a, hipStream_t stream) {
   delta_prep_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  delta_state_fwd_kernel<T, DK, DV, GATED><<<dim3(BH * (DV / 32)), dim3(64), 0, stream>>>(a, L);
+  delta_state_fwd_kernel<T, DK, DV, GATED><<<dim3(BH), dim3(64 * (DV / 32)), 0, stream>>>(
+      a, L, reinterpret_cast<const float*>(a.ctx + L.Gc));
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   delta_out_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);

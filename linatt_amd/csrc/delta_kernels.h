@@ -25,7 +25,7 @@ struct DeltaLayout {
   size_t Gc;    // (B,H,Tp) f32  chunk-local inclusive cumsum of g (gated only)
   size_t Tm;    // (B,H,NT,64,64) T  (I + A)^-1, natural [i][j]
   size_t W;     // (B,H,Tp,DK) T  W = Tm diag(beta e^G) K, key dims in operand order
-  size_t UT;    // (B,H,NT,DV,64) T  (Tm diag(beta) V)^T per chunk
+  size_t UT;    // (B,H,NT,DV,64) T  (Tm diag(beta) V)^T per chunk, rows i in operand order
   size_t WT;    // (B,H,NT,DK,64) T  W^T per chunk, rows i in operand order
   size_t KdT;   // (B,H,NT,DK,64) T  (e^(gamma - G_i) k_i)^T per chunk, rows i in operand order
   size_t QgT;   // (B,H,NT,DK,64) T  (scale e^G_i q_i)^T per chunk
