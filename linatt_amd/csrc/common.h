@@ -121,6 +121,67 @@ __device__ __forceinline__ void vm_wait_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"i"(N) : "memory");
 }
 
+// ---------------------------------------------------------------------------
+// 64 x 64 tiles of 16-bit elements in LDS: 128-byte rows, unpadded, with the
+// 16-byte chunk c of row r stored in slot c ^ f(r),
+//   f(r) = ((r >> 1) & 1) << 2 | ((r >> 2) & 3),
+// which keeps both access patterns free of bank conflicts: 16-byte operand
+// reads of 16 consecutive rows at one chunk, and the transposing 8-byte
+// reads (4 rows x 4 chunks per 32 lanes) of ld_tr8.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int tile_slot(int row, int ch) {
+  return ch ^ ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
+}
+__device__ __forceinline__ int tile_off(int row, int col) {  // byte offset, col % 4 == 0
+  return row * 128 + (tile_slot(row, col >> 3) << 4) + ((col & 7) << 1);
+}
+
+// Wave-level copy of tile rows [8 op, 8 op + 8) from global rows row0 + r
+// (clamped to nrows - 1: rows past the end repeat the last valid row, which
+// every consumer masks) into the swizzled LDS tile.
+template <typename T>
+__device__ __forceinline__ void dma_tile64(const T* g, int64_t rs, int row0, int nrows, T* tile,
+                                           int op, int lane) {
+  const int row = 8 * op + (lane >> 3), slot = lane & 7;
+  const int grow = min(row0 + row, nrows - 1);
+  dma16(g + (int64_t)grow * rs + 8 * tile_slot(row, slot), reinterpret_cast<char*>(tile) + 1024 * op);
+}
+
+// 8 consecutive elements of row `row` from column col (col % 8 == 0).
+template <typename T>
+__device__ __forceinline__ v8_t<T> tile_ld8(const T* tile, int row, int col) {
+  return *reinterpret_cast<const v8_t<T>*>(reinterpret_cast<const char*>(tile) + tile_off(row, col));
+}
+
+// Transposing 8-byte LDS read (ds_read_tr16_b64): within each 16-lane group,
+// lane i receives element i % 4 of the 4 values read by lanes 4c + i / 4,
+// c = 0..3.
+template <typename T>
+__device__ __forceinline__ v4_t<T> ds_tr4(const T* p) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(v4_t<T>, x);
+}
+
+// MFMA operand with k running down the rows of a natural tile: lane
+// (column c0 + (lane & 31)) receives rows r0 + 16 j + 4 hh + 0..3 and
+// r0 + 16 j + 8 + 4 hh + 0..3, the same k order as ld_tr_op on the
+// transposed tile.  zero (when non-null) is read instead by the 16-lane
+// groups whose (lane >> 4) & 1 differs from keep (half-zero operands).
+template <typename T>
+__device__ __forceinline__ v8_t<T> tile_tr8(const T* tile, int r0, int c0, int j, int lane,
+                                            const T* zero = nullptr, int keep = 0) {
+  const int g = lane >> 4, i = lane & 15;
+  const int row = r0 + 16 * j + 4 * (g >> 1) + (i >> 2);
+  const int col = c0 + 16 * (g & 1) + 4 * (i & 3);
+  const char* base = reinterpret_cast<const char*>(tile);
+  const bool z = zero != nullptr && ((g & 1) != keep);
+  const T* p0 = z ? zero : reinterpret_cast<const T*>(base + tile_off(row, col));
+  const T* p1 = z ? zero : reinterpret_cast<const T*>(base + tile_off(row + 8, col));
+  return cat44<T>(ds_tr4<T>(p0), ds_tr4<T>(p1));
+}
+
 // Position of logical element e (0..31) of a 32-block in the "operand
 // order" layout: the eight elements ld_tr_op gathers for (j, h), rows
 // 16j + 4h + 0..3 and 16j + 8 + 4h + 0..3, become the 8 contiguous elements

@@ -428,12 +428,415 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
   }
 }
 
+// ---------------------------------------------------------------------------
+// 16-bit inputs: the two kernels above with their tiles brought in by direct
+// global->LDS copies into double buffers (the next tile's copies in flight
+// while the current one computes, one barrier per tile), stored swizzled in
+// natural layout only.  Operands with k along the tile rows (K^T for dQ,
+// Q^T for dK, dO^T for dV) come from transposing LDS reads.  Rows past T
+// repeat the last valid row; every use of them is masked.
+// ---------------------------------------------------------------------------
+template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
+__global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const T* __restrict__ o, const float* __restrict__ den, const T* __restrict__ dout,
+    T* __restrict__ dq, float* __restrict__ delta_out, const float* __restrict__ c,
+    float* __restrict__ dc, int Tn, int HQ, int H, float scale2, int nqt, int nbh) {
+  constexpr int E = DK / M;
+  constexpr int KE = E / 16;
+  static_assert(sizeof(T) == 2 && DK == 64 && DV == 64, "64 x 64 16-bit tiles");
+  __shared__ __attribute__((aligned(16))) T Kb[2][64 * 64];
+  __shared__ __attribute__((aligned(16))) T Vb[2][64 * 64];
+  __shared__ __attribute__((aligned(16))) float Cs[2][64];
+  __shared__ __attribute__((aligned(16))) T Zr[8];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+  const int cl = lane & 31, hh = lane >> 5;
+  if (tid < 8) Zr[tid] = T(0);
+  int qt, bh;
+  map_block(blockIdx.x, nqt, nbh, qt, bh, true);
+  const int b = bh / HQ, hq = bh % HQ;
+  const int G = HQ / H, h = hq / G;
+  const int t0 = qt * 128;
+  const int tw = t0 + 32 * w;
+  const int tl = tw + cl;
+  const bool tvalid = tl < Tn;
+
+  const int64_t ks = (int64_t)H * DK, vs = (int64_t)H * DV;
+  const T* kb = k + ((int64_t)b * Tn) * ks + (int64_t)h * DK;
+  const T* vb = v + ((int64_t)b * Tn) * vs + (int64_t)h * DV;
+  const int64_t qrow = ((int64_t)b * Tn + tl) * HQ + hq;
+
+  v8_t<T> qop[DK / 16], doop[DV / 16];
+#pragma unroll
+  for (int kk = 0; kk < DK / 16; ++kk)
+    qop[kk] = tvalid ? ld8<T>(q + qrow * DK + 16 * kk + 8 * hh) : zero8<T>();
+  float dpart = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < DV / 16; ++kk) {
+    doop[kk] = tvalid ? ld8<T>(dout + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
+    const v8_t<T> ov = tvalid ? ld8<T>(o + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dpart += (float)ov[j] * (float)doop[kk][j];
+  }
+  const float delta = dpart + __shfl_xor(dpart, 32);
+  float pdl = 0.f;
+  if (tvalid) {
+    const float d = den[qrow];
+    pdl = scale2 / (d > 0.f ? d : 1.f);
+    if (hh == 0) delta_out[qrow] = delta;
+  }
+
+  f32x16 acc[DK / 32];
+#pragma unroll
+  for (int rb = 0; rb < DK / 32; ++rb) acc[rb] = f32x16{};
+  const float ct = (DECAY && tvalid) ? c[qrow] : 0.f;
+  float dcr = 0.f;
+
+  // K^T operand feeding dQ^T rows 32 rb + cl of query group gi from key group gk
+  auto kt_op = [&](const T* Ks, int sb, int gi, int gk, int rb, int j) __attribute__((always_inline)) {
+    if constexpr (E >= 32) return tile_tr8<T>(Ks, 32 * sb, gk * E + 32 * rb - gi * E, j, lane);
+    else return tile_tr8<T>(Ks, 32 * sb, 16 * gk - 16 * (gi & 1), j, lane, Zr, gi & 1);
+  };
+
+  const int s_end = min(t0 + 128, Tn);
+  const int nst = (s_end + 63) / 64;
+  auto issue = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      dma_tile64<T>(kb, ks, 64 * st, Tn, Kb[st & 1], 2 * w + i, lane);
+      dma_tile64<T>(vb, vs, 64 * st, Tn, Vb[st & 1], 2 * w + i, lane);
+    }
+  };
+  float cnext = 0.f;
+  auto load_c = [&](int st) __attribute__((always_inline)) {
+    if constexpr (DECAY) {
+      const int s = 64 * st + tid;
+      cnext = (tid < 64 && s < Tn) ? c[((int64_t)b * Tn + s) * HQ + hq] : 0.f;
+    }
+  };
+  issue(0);
+  load_c(0);
+  if constexpr (DECAY) {
+    if (tid < 64) Cs[0][tid] = cnext;
+  }
+  for (int st = 0; st < nst; ++st) {
+    const int s0 = st * 64, buf = st & 1;
+    vm_wait_barrier<0>();
+    if (st + 1 < nst) {
+      issue(st + 1);
+      load_c(st + 1);
+    }
+    const T* Ks = Kb[buf];
+    const T* Vs = Vb[buf];
+    if (!(s0 > tw + 31 || tw >= Tn)) {
+      const bool need_mask = (s0 + 63 > tw) || (s0 + 64 > Tn);
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        // x^T[s][t] = V dO^T - delta  (rows s, column t)
+        f32x16 x;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) x[e] = -delta;
+#pragma unroll
+        for (int kk = 0; kk < DV / 16; ++kk)
+          x = mma(tile_ld8<T>(Vs, 32 * sb + cl, 16 * kk + 8 * hh), doop[kk], x);
+        if (need_mask) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int s = s0 + 32 * sb + 8 * (e >> 2) + 4 * hh + (e & 3);
+            if (s > tl || s >= Tn) x[e] = 0.f;
+          }
+        }
+        f32x16 msk;
+        if constexpr (DECAY) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f32x4 cs4 = *reinterpret_cast<const f32x4*>(&Cs[buf][32 * sb + 8 * i + 4 * hh]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float dd = ct - cs4[r];
+              x[4 * i + r] *= __expf(fminf(dd, 0.f));
+              msk[4 * i + r] = dd <= 0.f ? 1.f : 0.f;
+            }
+          }
+        }
+        f32x16 au{};
+#pragma unroll
+        for (int gi = 0; gi < M; ++gi) {
+#pragma unroll
+          for (int gj = 0; gj < (SUM ? M : 1); ++gj) {
+            const int gk = SUM ? gj : gi;
+            f32x16 r{};
+#pragma unroll
+            for (int kk = 0; kk < KE; ++kk)
+              r = mma(tile_ld8<T>(Ks, 32 * sb + cl, gk * E + 16 * kk + 8 * hh), qop[gi * KE + kk], r);
+            if constexpr (DECAY) au += r * r;
+            const f32x16 da = r * x;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const v8_t<T> bop = c_to_b<T>(da, j);
+#pragma unroll
+              for (int rb = (gi * E) / 32; rb <= ((gi + 1) * E - 1) / 32; ++rb)
+                acc[rb] = mma(kt_op(Ks, sb, gi, gk, rb, j), bop, acc[rb]);
+            }
+          }
+        }
+        if constexpr (DECAY) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) dcr += x[e] * au[e] * msk[e];
+        }
+      }
+    }
+    if constexpr (DECAY) {
+      if (st + 1 < nst && tid < 64) Cs[buf ^ 1][tid] = cnext;
+    }
+  }
+
+  if constexpr (DECAY) {
+    dcr += __shfl_xor(dcr, 32);
+    if (tvalid && hh == 0) dc[qrow] = dcr * pdl;
+  }
+  if (tvalid) {
+    const float f = 2.f * pdl;
+    T* drow = dq + qrow * DK;
+#pragma unroll
+    for (int rb = 0; rb < DK / 32; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        st4<T>(drow + 32 * rb + 8 * i + 4 * hh,
+               to4<T>(acc[rb][4 * i] * f, acc[rb][4 * i + 1] * f, acc[rb][4 * i + 2] * f,
+                      acc[rb][4 * i + 3] * f));
+  }
+}
+
+template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
+__global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const float* __restrict__ den, const float* __restrict__ delta, const T* __restrict__ dout,
+    T* __restrict__ dk, T* __restrict__ dv, const float* __restrict__ c, float* __restrict__ dc,
+    int Tn, int HQ, int H, float scale2, int nst, int nbh) {
+  constexpr int E = DK / M;
+  constexpr int KE = E / 16;
+  constexpr float kPScale = __is_same(T, _Float16) ? 4096.f : 1.f;
+  constexpr float kPInv = 1.f / kPScale;
+  static_assert(sizeof(T) == 2 && DK == 64 && DV == 64, "64 x 64 16-bit tiles");
+  __shared__ __attribute__((aligned(16))) T Qb[2][64 * 64];
+  __shared__ __attribute__((aligned(16))) T Ob[2][64 * 64];
+  __shared__ __attribute__((aligned(16))) float Dl[2][64];  // -delta
+  __shared__ __attribute__((aligned(16))) float Pd[2][64];  // scale^2 / den
+  __shared__ __attribute__((aligned(16))) float Ct[2][64];
+  __shared__ __attribute__((aligned(16))) T Zr[8];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+  const int cl = lane & 31, hh = lane >> 5;
+  if (tid < 8) Zr[tid] = T(0);
+  int stile, bh;
+  map_block(blockIdx.x, nst, nbh, stile, bh, false);
+  const int b = bh / H, h = bh % H;
+  const int G = HQ / H;
+  const int s0 = stile * 128;
+  const int sw = s0 + 32 * w;
+  const int sl = sw + cl;
+  const bool svalid = sl < Tn;
+
+  const int64_t qs = (int64_t)HQ * DK, os = (int64_t)HQ * DV;
+  const int64_t krow = ((int64_t)b * Tn + sl) * H + h;
+
+  v8_t<T> kop[DK / 16], vop[DV / 16];
+#pragma unroll
+  for (int kk = 0; kk < DK / 16; ++kk)
+    kop[kk] = svalid ? ld8<T>(k + krow * DK + 16 * kk + 8 * hh) : zero8<T>();
+#pragma unroll
+  for (int kk = 0; kk < DV / 16; ++kk)
+    vop[kk] = svalid ? ld8<T>(v + krow * DV + 16 * kk + 8 * hh) : zero8<T>();
+
+  f32x16 dka[DK / 32], dva[DV / 32];
+#pragma unroll
+  for (int rb = 0; rb < DK / 32; ++rb) dka[rb] = f32x16{};
+#pragma unroll
+  for (int db = 0; db < DV / 32; ++db) dva[db] = f32x16{};
+
+  // Q^T operand feeding dK^T rows 32 rb + cl of key group gk from query group gi
+  auto qt_op = [&](const T* Qs, int mb, int gi, int gk, int rb, int j) __attribute__((always_inline)) {
+    if constexpr (E >= 32) return tile_tr8<T>(Qs, 32 * mb, gi * E + 32 * rb - gk * E, j, lane);
+    else return tile_tr8<T>(Qs, 32 * mb, 16 * gi - 16 * (gk & 1), j, lane, Zr, gk & 1);
+  };
+
+  // query tiles (hq, tt) of this key tile, flattened over the G query heads
+  const int ntt = (Tn + 63) / 64, tt0 = s0 / 64, nq = ntt - tt0;
+  const int ntiles = G * nq;
+  auto issue = [&](int n) __attribute__((always_inline)) {
+    const int hq = h * G + n / nq, t0 = 64 * (tt0 + n % nq);
+    const T* qb = q + ((int64_t)b * Tn) * qs + (int64_t)hq * DK;
+    const T* ob = dout + ((int64_t)b * Tn) * os + (int64_t)hq * DV;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      dma_tile64<T>(qb, qs, t0, Tn, Qb[n & 1], 2 * w + i, lane);
+      dma_tile64<T>(ob, os, t0, Tn, Ob[n & 1], 2 * w + i, lane);
+    }
+  };
+  float nd = 0.f, np = 0.f, nc = 0.f;  // row data of the next tile (tid < 64)
+  auto load_rows = [&](int n) __attribute__((always_inline)) {
+    const int hq = h * G + n / nq, t = 64 * (tt0 + n % nq) + tid;
+    nd = 0.f;
+    np = 0.f;
+    nc = 0.f;
+    if (tid < 64 && t < Tn) {
+      const int64_t r = ((int64_t)b * Tn + t) * HQ + hq;
+      nd = -delta[r];
+      const float d = den[r];
+      np = scale2 / (d > 0.f ? d : 1.f);
+      if constexpr (DECAY) nc = c[r];
+    }
+  };
+  auto store_rows = [&](int buf) __attribute__((always_inline)) {
+    if (tid < 64) {
+      Dl[buf][tid] = nd;
+      Pd[buf][tid] = np;
+      if constexpr (DECAY) Ct[buf][tid] = nc;
+    }
+  };
+
+  issue(0);
+  load_rows(0);
+  store_rows(0);
+  float csl = (DECAY && svalid) ? c[((int64_t)b * Tn + sl) * HQ + h * G] : 0.f;
+  float dcc = 0.f;
+  for (int n = 0; n < ntiles; ++n) {
+    const int buf = n & 1;
+    const int hq = h * G + n / nq, t0 = 64 * (tt0 + n % nq);
+    vm_wait_barrier<0>();
+    if (n + 1 < ntiles) {
+      issue(n + 1);
+      load_rows(n + 1);
+    }
+    const T* Qs = Qb[buf];
+    const T* Os = Ob[buf];
+    if (!(t0 + 63 < sw || sw >= Tn)) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const int tb = t0 + 32 * mb;
+        if (tb + 31 < sw) continue;
+        const bool need_mask = (tb < sw + 31) || (tb + 32 > Tn);
+        auto masked = [&](int e) {
+          const int t = tb + 8 * (e >> 2) + 4 * hh + (e & 3);
+          return t < sl || t >= Tn;
+        };
+        f32x16 x, pdv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&Dl[buf][32 * mb + 8 * i + 4 * hh]);
+          const f32x4 p4 = *reinterpret_cast<const f32x4*>(&Pd[buf][32 * mb + 8 * i + 4 * hh]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            x[4 * i + r] = d4[r];
+            pdv[4 * i + r] = p4[r];
+          }
+        }
+        // x[t][s] = dO V^T - delta  (rows t, column s)
+#pragma unroll
+        for (int kk = 0; kk < DV / 16; ++kk)
+          x = mma(tile_ld8<T>(Os, 32 * mb + cl, 16 * kk + 8 * hh), vop[kk], x);
+        if (need_mask) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) x[e] = masked(e) ? 0.f : x[e];
+        }
+        if constexpr (DECAY) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            x[e] *= __expf(fminf(Ct[buf][32 * mb + 8 * (e >> 2) + 4 * hh + (e & 3)] - csl, 0.f));
+        }
+        const f32x16 xs = x * pdv;
+        // per (query group gi, key group gk): r = Q_gi K_gk^T, A += r^2 and
+        // dK^T[(gk,e)][s] += sum_t Q^T[(gi,e)][t] r[t][s] xs[t][s]
+        f32x16 A{};
+#pragma unroll
+        for (int gi = 0; gi < M; ++gi)
+#pragma unroll
+          for (int gj = 0; gj < (SUM ? M : 1); ++gj) {
+            const int gk = SUM ? gj : gi;
+            f32x16 r{};
+#pragma unroll
+            for (int kk = 0; kk < KE; ++kk)
+              r = mma(tile_ld8<T>(Qs, 32 * mb + cl, gi * E + 16 * kk + 8 * hh), kop[gk * KE + kk], r);
+            A += r * r;
+            const f32x16 da = r * xs;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const v8_t<T> bop = c_to_b<T>(da, j);
+#pragma unroll
+              for (int rb = (gk * E) / 32; rb <= ((gk + 1) * E - 1) / 32; ++rb)
+                dka[rb] = mma(qt_op(Qs, mb, gi, gk, rb, j), bop, dka[rb]);
+            }
+          }
+        if (need_mask) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) A[e] = masked(e) ? 0.f : A[e];
+        }
+        if constexpr (DECAY) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const float dd = Ct[buf][32 * mb + 8 * (e >> 2) + 4 * hh + (e & 3)] - csl;
+            // column part of dc_s: -sum_t dA A [c_t - c_s <= 0] (xs carries the decay)
+            dcc -= dd <= 0.f ? xs[e] * A[e] : 0.f;
+            A[e] *= __expf(fminf(dd, 0.f));
+          }
+        }
+        // fp16 keeps P in [0, 2^12] (subnormal range); undone at the store
+        const f32x16 P = A * (pdv * kPScale);
+        // dV^T[dv][s] += sum_t dO^T[dv][t] P[t][s], dO^T read transposed from dO
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const v8_t<T> pb = c_to_b<T>(P, j);
+#pragma unroll
+          for (int db = 0; db < DV / 32; ++db)
+            dva[db] = mma(tile_tr8<T>(Os, 32 * mb, 32 * db, j, lane), pb, dva[db]);
+        }
+      }
+    }
+    store_rows(buf ^ 1);
+    if constexpr (DECAY) {
+      if (n % nq == nq - 1) {  // last query tile of head hq
+        dcc += __shfl_xor(dcc, 32);
+        if (svalid && hh == 0) dc[((int64_t)b * Tn + sl) * HQ + hq] += dcc;
+        dcc = 0.f;
+        if (hq + 1 < (h + 1) * G) csl = svalid ? c[((int64_t)b * Tn + sl) * HQ + hq + 1] : 0.f;
+      }
+    }
+  }
+
+  if (svalid) {
+    T* dkrow = dk + krow * DK;
+    T* dvrow = dv + krow * DV;
+#pragma unroll
+    for (int rb = 0; rb < DK / 32; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        st4<T>(dkrow + 32 * rb + 8 * i + 4 * hh,
+               to4<T>(2.f * dka[rb][4 * i], 2.f * dka[rb][4 * i + 1], 2.f * dka[rb][4 * i + 2],
+                      2.f * dka[rb][4 * i + 3]));
+#pragma unroll
+    for (int db = 0; db < DV / 32; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        st4<T>(dvrow + 32 * db + 8 * i + 4 * hh,
+               to4<T>(dva[db][4 * i] * kPInv, dva[db][4 * i + 1] * kPInv,
+                      dva[db][4 * i + 2] * kPInv, dva[db][4 * i + 3] * kPInv));
+  }
+}
+
 template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
 hipError_t launch_kata_bwd(const KataArgs& a, int parts, hipStream_t stream) {
   const float scale2 = a.scale * a.scale;
   const int nqt = (a.T + 127) / 128;
+  constexpr bool kTiles = sizeof(T) == 2 && DK == 64 && DV == 64;
   if (parts & KATA_BWD_DQ) {
     const int nbh = a.B * a.HQ;
+    if constexpr (kTiles)
+      kata_bwd_dq_tile_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbh), dim3(256), 0, stream>>>(
+          (const T*)a.q, (const T*)a.k, (const T*)a.v, (const T*)a.o, a.den, (const T*)a.dout,
+          (T*)a.dq, a.delta, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt, nbh);
+    else
     kata_bwd_dq_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbh), dim3(256), 0, stream>>>(
         (const T*)a.q, (const T*)a.k, (const T*)a.v, (const T*)a.o, a.den, (const T*)a.dout,
         (T*)a.dq, a.delta, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt, nbh);
@@ -442,6 +845,11 @@ hipError_t launch_kata_bwd(const KataArgs& a, int parts, hipStream_t stream) {
   }
   if (parts & KATA_BWD_DKDV) {
     const int nbk = a.B * a.H;
+    if constexpr (kTiles)
+      kata_bwd_dkdv_tile_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbk), dim3(256), 0, stream>>>(
+          (const T*)a.q, (const T*)a.k, (const T*)a.v, a.den, a.delta, (const T*)a.dout,
+          (T*)a.dk, (T*)a.dv, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt, nbk);
+    else
     kata_bwd_dkdv_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbk), dim3(256), 0, stream>>>(
         (const T*)a.q, (const T*)a.k, (const T*)a.v, a.den, a.delta, (const T*)a.dout,
         (T*)a.dk, (T*)a.dv, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt, nbk);

@@ -189,11 +189,195 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_fwd_kernel(
   }
 }
 
+// 16-bit inputs: the same computation with the key tiles brought in by
+// direct global->LDS copies (double-buffered, the next tile's copies in
+// flight while the current one computes, one barrier per tile) and stored
+// swizzled in natural layout: K feeds the score MFMAs with 16-byte reads and
+// V^T comes from V through transposing LDS reads, so no transposed copy is
+// built.  Rows past T repeat the last valid row and are masked.
+template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
+__global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const float* __restrict__ c, T* __restrict__ o, float* __restrict__ den,
+    int Tn, int HQ, int H, float scale2, int nqt, int nbh) {
+  constexpr int E = DK / M;
+  constexpr int KE = E / 16;
+  static_assert(sizeof(T) == 2 && DK == 64 && DV == 64, "64 x 64 16-bit tiles");
+  __shared__ __attribute__((aligned(16))) T Kb[2][64 * 64];
+  __shared__ __attribute__((aligned(16))) T Vb[2][64 * 64];
+  __shared__ __attribute__((aligned(16))) float Cs[2][64];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+  const int cl = lane & 31, hh = lane >> 5;
+  int qt, bh;
+  map_block(blockIdx.x, nqt, nbh, qt, bh, true);
+  const int b = bh / HQ, hq = bh % HQ;
+  const int G = HQ / H, h = hq / G;
+  const int t0 = qt * 128;
+  const int tw = t0 + 32 * w;
+  const int tl = tw + cl;
+
+  const int64_t qs = (int64_t)HQ * DK, ks = (int64_t)H * DK, vs = (int64_t)H * DV;
+  const T* qb = q + ((int64_t)b * Tn) * qs + (int64_t)hq * DK;
+  const T* kb = k + ((int64_t)b * Tn) * ks + (int64_t)h * DK;
+  const T* vb = v + ((int64_t)b * Tn) * vs + (int64_t)h * DV;
+
+  v8_t<T> qop[DK / 16];
+#pragma unroll
+  for (int kk = 0; kk < DK / 16; ++kk)
+    qop[kk] = (tl < Tn) ? ld8<T>(qb + (int64_t)tl * qs + 16 * kk + 8 * hh) : zero8<T>();
+  float ct = 0.f;
+  if constexpr (DECAY) ct = (tl < Tn) ? c[((int64_t)b * Tn + tl) * HQ + hq] : 0.f;
+
+  f32x16 oacc[DV / 32];
+#pragma unroll
+  for (int db = 0; db < DV / 32; ++db) oacc[db] = f32x16{};
+  float dpart = 0.f;
+  constexpr bool kRescale = __is_same(T, _Float16);
+  float pe = 1.f, mrun = 0.f;
+
+  const int s_end = min(t0 + 128, Tn);
+  const int nst = (s_end + 63) / 64;
+  // tile st: 8 KiB of K and 8 KiB of V, two 1 KiB copies of each per wave
+  auto issue = [&](int st) __attribute__((always_inline)) {
+    const int buf = st & 1;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      dma_tile64<T>(kb, ks, 64 * st, Tn, Kb[buf], 2 * w + i, lane);
+      dma_tile64<T>(vb, vs, 64 * st, Tn, Vb[buf], 2 * w + i, lane);
+    }
+  };
+  float cnext = 0.f;
+  auto load_c = [&](int st) __attribute__((always_inline)) {
+    if constexpr (DECAY) {
+      const int s = 64 * st + tid;
+      cnext = (tid < 64 && s < Tn) ? c[((int64_t)b * Tn + s) * HQ + hq] : 0.f;
+    }
+  };
+  issue(0);
+  load_c(0);
+  if constexpr (DECAY) {
+    if (tid < 64) Cs[0][tid] = cnext;
+  }
+  for (int st = 0; st < nst; ++st) {
+    const int s0 = st * 64, buf = st & 1;
+    // tile st landed (own copies) and every wave passed tile st - 1
+    vm_wait_barrier<0>();
+    if (st + 1 < nst) {
+      issue(st + 1);
+      load_c(st + 1);
+    }
+    const T* Ks = Kb[buf];
+    const T* Vs = Vb[buf];
+    if (!(s0 > tw + 31 || tw >= Tn)) {
+      const bool need_mask = (s0 + 63 > tw) || (s0 + 64 > Tn);
+      f32x16 a[2];
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        a[sb] = f32x16{};
+        const int krow = 32 * sb + cl;
+        if constexpr (!SUM) {
+#pragma unroll
+          for (int g = 0; g < M; ++g) {
+            f32x16 r{};
+#pragma unroll
+            for (int kk = 0; kk < KE; ++kk)
+              r = mma(tile_ld8<T>(Ks, krow, g * E + 16 * kk + 8 * hh), qop[g * KE + kk], r);
+            a[sb] += r * r;
+          }
+        } else {
+#pragma unroll
+          for (int gi = 0; gi < M; ++gi) {
+#pragma unroll
+            for (int gj = 0; gj < M; ++gj) {
+              f32x16 r{};
+#pragma unroll
+              for (int kk = 0; kk < KE; ++kk)
+                r = mma(tile_ld8<T>(Ks, krow, gj * E + 16 * kk + 8 * hh), qop[gi * KE + kk], r);
+              a[sb] += r * r;
+            }
+          }
+        }
+        if constexpr (DECAY) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f32x4 cs = *reinterpret_cast<const f32x4*>(&Cs[buf][32 * sb + 8 * i + 4 * hh]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) a[sb][4 * i + r] *= __expf(fminf(ct - cs[r], 0.f));
+          }
+        }
+        if (need_mask) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int s = s0 + 32 * sb + 8 * i + 4 * hh + r;
+              if (s > tl || s >= Tn) a[sb][4 * i + r] = 0.f;
+            }
+        }
+      }
+      if constexpr (kRescale) {
+        float mx = 0.f;
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) mx = fmaxf(mx, a[sb][e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        if (mx > mrun) {
+          int ex;
+          frexpf(mx, &ex);
+          const float pnew = ldexpf(1.f, 12 - max(ex, -100));
+          const float ratio = pnew / pe;
+#pragma unroll
+          for (int db = 0; db < DV / 32; ++db) oacc[db] *= ratio;
+          dpart *= ratio;
+          pe = pnew;
+          mrun = mx;
+        }
+        a[0] *= pe;
+        a[1] *= pe;
+      }
+      // O^T[dv][t] += sum_s V^T[dv][s] P^T[s][t], V^T read transposed from V
+#pragma unroll
+      for (int ks4 = 0; ks4 < 4; ++ks4) {
+        const v8_t<T> pb = c_to_b<T>(a[ks4 >> 1], ks4 & 1);
+        dpart = sum8<T>(pb, dpart);
+#pragma unroll
+        for (int db = 0; db < DV / 32; ++db)
+          oacc[db] = mma(tile_tr8<T>(Vs, 32 * (ks4 >> 1), 32 * db, ks4 & 1, lane), pb, oacc[db]);
+      }
+    }
+    if constexpr (DECAY) {
+      if (st + 1 < nst && tid < 64) Cs[buf ^ 1][tid] = cnext;
+    }
+  }
+
+  const float dsum = dpart + __shfl_xor(dpart, 32);
+  if (tl < Tn) {
+    const float inv = dsum > 0.f ? 1.f / dsum : 1.f;
+    T* orow = o + (((int64_t)b * Tn + tl) * HQ + hq) * DV;
+#pragma unroll
+    for (int db = 0; db < DV / 32; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        st4<T>(orow + 32 * db + 8 * i + 4 * hh,
+               to4<T>(oacc[db][4 * i] * inv, oacc[db][4 * i + 1] * inv,
+                      oacc[db][4 * i + 2] * inv, oacc[db][4 * i + 3] * inv));
+    if (hh == 0) den[((int64_t)b * Tn + tl) * HQ + hq] = dsum * (scale2 / pe);
+  }
+}
+
 template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
 hipError_t launch_kata_fwd(const KataArgs& a, hipStream_t stream) {
   const int nqt = (a.T + 127) / 128;
   const int nbh = a.B * a.HQ;
   dim3 grid(nqt * nbh), block(256);
+  if constexpr (sizeof(T) == 2 && DK == 64 && DV == 64) {
+    kata_fwd_tile_kernel<T, DK, DV, M, SUM, DECAY><<<grid, block, 0, stream>>>(
+        (const T*)a.q, (const T*)a.k, (const T*)a.v, a.c, (T*)a.o, a.den, a.T, a.HQ, a.H,
+        a.scale * a.scale, nqt, nbh);
+    return hipGetLastError();
+  }
   kata_fwd_kernel<T, DK, DV, M, SUM, DECAY><<<grid, block, 0, stream>>>(
       (const T*)a.q, (const T*)a.k, (const T*)a.v, a.c, (T*)a.o, a.den, a.T, a.HQ, a.H,
       a.scale * a.scale, nqt, nbh);
