@@ -182,6 +182,17 @@ __device__ __forceinline__ v8_t<T> tile_tr8(const T* tile, int r0, int c0, int j
   return cat44<T>(ds_tr4<T>(p0), ds_tr4<T>(p1));
 }
 
+// Compile-time bool for generic lambdas: body(BoolC<true>{}) instantiates
+// the masked variant of a loop body, so the unmasked one carries no selects.
+template <bool B>
+struct BoolC {
+  static constexpr bool value = B;
+};
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+
 // Position of logical element e (0..31) of a 32-block in the "operand
 // order" layout: the eight elements ld_tr_op gathers for (j, h), rows
 // 16j + 4h + 0..3 and 16j + 8 + 4h + 0..3, become the 8 contiguous elements

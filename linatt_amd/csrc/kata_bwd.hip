@@ -768,6 +768,10 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
               for (int rb = (gk * E) / 32; rb <= ((gk + 1) * E - 1) / 32; ++rb)
                 dka[rb] = mma(qt_op(Qs, mb, gi, gk, rb, j), bop, dka[rb]);
             }
+            // sum and decay variants: keep the next group's score MFMAs from
+            // being hoisted above this group's products (bounds the live
+            // score registers; unbounded, they spill)
+            if constexpr (SUM || DECAY) __builtin_amdgcn_sched_barrier(0);
           }
         if (need_mask) {
 #pragma unroll
