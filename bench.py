@@ -250,6 +250,19 @@ def _cpu_model():
     return "unknown"
 
 
+# HBM bytes per launch of the config-2 kernels (FETCH_SIZE x 1024 x 2.0 +
+# WRITE_SIZE x 1024 x 1.0, the factors a 512 MiB device copy gives the two
+# counters), from the rocprofv3 --pmc runs summarised in
+# profiles/hbm_traffic_bench_all_workloads.md.  Counters cannot be read from
+# inside the timed run, so the figure is carried here and refreshed with the
+# profile.
+MEASURED_TRAFFIC_BYTES = {
+    "fwd": int((105.3 + 30.5) * 1e6),
+    "bwd_dq": int((161.9 + 30.6) * 1e6),
+    "bwd_dkdv": int((174.6 + 53.5) * 1e6),
+}
+
+
 def copy_calibration():
     """A plain device copy of known size (512 MiB bf16, 3 launches), the
     reference against which the rocprofv3 FETCH_SIZE / WRITE_SIZE counters are
@@ -394,7 +407,8 @@ def main():
         "kernels": kern,
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(ach, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None},
+                     "frac": round(ach / PEAK_BF16_TFLOPS, 4),
+                     "traffic": MEASURED_TRAFFIC_BYTES.get(dom)},
         "cpu_baseline": cpu,
         "delta_rule": delta,
         "kata_state_config5": state,
