@@ -29,18 +29,22 @@
 namespace linatt {
 
 // ---------------------------------------------------------------------------
-// Segment states.  Wave w of block (bh, seg, pb) owns state rows
-// p = 128 pb + 32 w + [0, 32) (its X-operand rows) for every value column.
+// Segment states.  One workgroup of 8 waves covers 1024 state rows of one
+// (b, h, segment), so each key/value tile is read once per 1024 rows; wave w
+// owns rows p = 1024 pb + 128 w + 32 i4 + [0, 32), i4 = 0..3 (its X-operand
+// rows).  K^T sits in LDS as fp32 so the psi products need no unpacking.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, int M>
-__global__ __launch_bounds__(256) void kata_seg_state_kernel(KataStateArgs a) {
+__global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
   constexpr int E = DK / M, P = M * E * E;
-  constexpr int PX = 64 + 8;
-  __shared__ __attribute__((aligned(16))) T Kt[DK * PX];
-  __shared__ __attribute__((aligned(16))) T Vt[DV * PX];
+  constexpr int PK = 64 + 4;  // fp32 K^T pitch
+  constexpr int PV = 64 + 8;  // V^T pitch
+  constexpr int NPB = P / 1024;
+  static_assert(P % 1024 == 0, "1024 state rows per workgroup");
+  __shared__ __attribute__((aligned(16))) float Kt[DK * PK];
+  __shared__ __attribute__((aligned(16))) T Vt[DV * PV];
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
-  constexpr int NPB = P / 128;
   int blk = blockIdx.x;
   const int pb = blk % NPB;
   blk /= NPB;
@@ -50,46 +54,91 @@ __global__ __launch_bounds__(256) void kata_seg_state_kernel(KataStateArgs a) {
   const T* kb = (const T*)a.k + (int64_t)b * a.sb + (int64_t)h * a.sh;
   const T* vb = (const T*)a.v + (int64_t)b * a.vsb + (int64_t)h * a.vsh;
 
-  const int p = 128 * pb + 32 * w + cl;  // this lane's X row
-  const int g = p / (E * E), ra = g * E + (p / E) % E, rb = g * E + p % E;
-
-  f32x16 acc[DV / 32];
+  const int p0 = 1024 * pb + 128 * w;
+  int ra[4], rb[4];
 #pragma unroll
-  for (int vt = 0; vt < DV / 32; ++vt) acc[vt] = f32x16{};
-  float zp = 0.f;
+  for (int i4 = 0; i4 < 4; ++i4) {
+    const int p = p0 + 32 * i4 + cl;
+    const int g = p / (E * E);
+    ra[i4] = g * E + (p / E) % E;
+    rb[i4] = g * E + p % E;
+  }
+
+  f32x16 acc[4][DV / 32];
+#pragma unroll
+  for (int i4 = 0; i4 < 4; ++i4)
+#pragma unroll
+    for (int vt = 0; vt < DV / 32; ++vt) acc[i4][vt] = f32x16{};
+  float zp[4] = {0.f, 0.f, 0.f, 0.f};
   const int s_begin = seg * a.L, s_end = min(s_begin + a.L, a.T);
+  // next tile prefetched into registers during the current one's compute:
+  // waves 0-3 carry K, waves 4-7 V, one 4 x 4 block per thread
+  const bool isK = w < 4;
+  const int lt = tid & 255, cb = lt % 16, rq = lt / 16;
+  const T* src = isK ? kb : vb;
+  const int64_t rs = isK ? a.st : a.vst;
+  v4_t<T> pre[4];
+  auto gload = [&](int s0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = s0 + 4 * rq + r;
+      pre[r] = row < a.T ? ld4<T>(src + (int64_t)row * rs + 4 * cb) : v4_t<T>{};
+    }
+  };
+  auto lstore = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      if (isK)
+        *reinterpret_cast<f32x4*>(Kt + (4 * cb + cc) * PK + 4 * rq) =
+            f32x4{(float)pre[0][cc], (float)pre[1][cc], (float)pre[2][cc], (float)pre[3][cc]};
+      else
+        st4<T>(Vt + (4 * cb + cc) * PV + 4 * rq, v4_t<T>{pre[0][cc], pre[1][cc], pre[2][cc], pre[3][cc]});
+    }
+  };
+  static_assert(DK == 64 && DV == 64, "64 x 64 tiles");
+  gload(s_begin);
   for (int s0 = s_begin; s0 < s_end; s0 += 64) {
     __syncthreads();
-    load_tile64x<T, T, DK, 1, PX, false, true>(kb, s0, a.T, a.st, nullptr, Kt, tid, nullptr);
-    load_tile64x<T, T, DV, 1, PX, false, true>(vb, s0, a.T, a.vst, nullptr, Vt, tid, nullptr);
+    lstore();
     __syncthreads();
+    if (s0 + 64 < s_end) gload(s0 + 64);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const v8_t<T> ka = ld8<T>(Kt + ra * PX + 16 * s + 8 * hh);
-      const v8_t<T> kc = ld8<T>(Kt + rb * PX + 16 * s + 8 * hh);
-      f32x8 pf;
+      v8_t<T> vop[DV / 32];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        pf[j] = (float)ka[j] * (float)kc[j];
-        zp += pf[j];
+      for (int vt = 0; vt < DV / 32; ++vt) vop[vt] = ld8<T>(Vt + (32 * vt + cl) * PV + 16 * s + 8 * hh);
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const f32x4* ka = reinterpret_cast<const f32x4*>(Kt + ra[i4] * PK + 16 * s + 8 * hh);
+        const f32x4* kc = reinterpret_cast<const f32x4*>(Kt + rb[i4] * PK + 16 * s + 8 * hh);
+        const f32x4 a0 = ka[0], a1 = ka[1], c0 = kc[0], c1 = kc[1];
+        const f32x8 pf{a0[0] * c0[0], a0[1] * c0[1], a0[2] * c0[2], a0[3] * c0[3],
+                       a1[0] * c1[0], a1[1] * c1[1], a1[2] * c1[2], a1[3] * c1[3]};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) zp[i4] += pf[j];
+        const v8_t<T> x = __builtin_convertvector(pf, v8_t<T>);
+#pragma unroll
+        for (int vt = 0; vt < DV / 32; ++vt) acc[i4][vt] = mma(x, vop[vt], acc[i4][vt]);
       }
-      const v8_t<T> x = __builtin_convertvector(pf, v8_t<T>);
-#pragma unroll
-      for (int vt = 0; vt < DV / 32; ++vt)
-        acc[vt] = mma(x, ld8<T>(Vt + (32 * vt + cl) * PX + 16 * s + 8 * hh), acc[vt]);
     }
   }
-  // acc[vt] = D[p'][v]: rows p' = 128 pb + 32 w + 8 I + 4 hh + r, lane column
+  // acc[i4][vt] = D[p'][v]: rows p' = p0 + 32 i4 + 8 I + 4 hh + r, lane column
   // v = 32 vt + cl  ->  S_seg^T [v][p'] with 16-byte stores.
   float* st = a.seg_S + ((size_t)bh * a.nseg + seg) * DV * P;
 #pragma unroll
-  for (int vt = 0; vt < DV / 32; ++vt)
+  for (int i4 = 0; i4 < 4; ++i4)
 #pragma unroll
-    for (int I = 0; I < 4; ++I)
-      *reinterpret_cast<float4*>(st + (size_t)(32 * vt + cl) * P + 128 * pb + 32 * w + 8 * I + 4 * hh) =
-          make_float4(acc[vt][4 * I], acc[vt][4 * I + 1], acc[vt][4 * I + 2], acc[vt][4 * I + 3]);
-  zp += __shfl_xor(zp, 32);
-  if (hh == 0) a.seg_z[((size_t)bh * a.nseg + seg) * P + p] = zp;
+    for (int vt = 0; vt < DV / 32; ++vt)
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+        *reinterpret_cast<float4*>(st + (size_t)(32 * vt + cl) * P + p0 + 32 * i4 + 8 * I + 4 * hh) =
+            make_float4(acc[i4][vt][4 * I], acc[i4][vt][4 * I + 1], acc[i4][vt][4 * I + 2],
+                        acc[i4][vt][4 * I + 3]);
+#pragma unroll
+  for (int i4 = 0; i4 < 4; ++i4) {
+    const float z = zp[i4] + __shfl_xor(zp[i4], 32);
+    if (hh == 0) a.seg_z[((size_t)bh * a.nseg + seg) * P + p0 + 32 * i4 + cl] = z;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -144,12 +193,20 @@ __global__ __launch_bounds__(256) void kata_seg_scan_kernel(KataStateArgs a) {
 template <typename T, int DK, int DV, int M>
 __global__ __launch_bounds__(256, 2) void kata_prefill_out_kernel(KataStateArgs a, int nqt, int nbh) {
   constexpr int E = DK / M, P = M * E * E, KE = E / 16;
-  constexpr int KP = DK + 8, VP = 64 + 4;
   static_assert(E % 16 == 0, "group width must be a multiple of 16");
   constexpr int QP = DK + 8;
-  __shared__ __attribute__((aligned(16))) T Ks[64 * KP];
-  __shared__ __attribute__((aligned(16))) T Vt[DV * VP];
   __shared__ __attribute__((aligned(16))) T Qa[128 * QP];
+  // One 32 KiB LDS area, used first for the prefix state H^T [v][p] in
+  // chunks of 128 state rows p, double-buffered (64 rows of 256 bytes,
+  // 16-byte chunks swizzled by row), then for the intra-segment key and value
+  // tiles, double-buffered (swizzled 64 x 64 tiles, see tile_slot).
+  constexpr int HCH = 128, HCPR = HCH * (int)sizeof(T) / 16;
+  static_assert(DK == 64 && DV == 64 && HCPR == 16 && P % HCH == 0, "64 x 128 16-bit state chunks");
+  __shared__ __attribute__((aligned(16))) u32x4 Hs[2][DV * HCPR];
+  T* const Kb0 = reinterpret_cast<T*>(Hs[0]);
+  T* const Vb0 = Kb0 + 64 * 64;
+  T* const Kb1 = reinterpret_cast<T*>(Hs[1]);
+  T* const Vb1 = Kb1 + 64 * 64;
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -187,54 +244,93 @@ __global__ __launch_bounds__(256, 2) void kata_prefill_out_kernel(KataStateArgs 
     st4<T>(qa_row + 16 * kk + 8 * hh + 4, v4_t<T>{x[4], x[5], x[6], x[7]});
   }
   __syncthreads();
-  if (seg > 0 && tw < Tn) {
+  if (seg > 0) {  // uniform: a 128-query tile never straddles a segment
     const size_t base = (size_t)bh * a.nseg + seg;
-    const T* hT = (const T*)a.HT + base * DV * P;
+    const u32x4* hT = reinterpret_cast<const u32x4*>((const T*)a.HT + base * DV * P);
     const float* hz = a.Hz + base * P;
+    constexpr int NC = P / HCH;
+    // chunk c: rows v of H^T, columns [128 c, 128 c + 128); 16 KiB = 4 x 1 KiB per wave
+    auto issue = [&](int c) __attribute__((always_inline)) {
 #pragma unroll
-    for (int g = 0; g < M; ++g) {
-#pragma unroll 2
-      for (int ai = 0; ai < E; ++ai) {
-        const float qa = (float)qa_row[g * E + ai];
+      for (int i = 0; i < 4; ++i) {
+        const int op = 4 * w + i;
+        const int row = (64 * op + lane) / HCPR, slot = lane % HCPR;
+        const int ch = slot ^ (row & 15);
+        dma16(hT + (size_t)row * (P / 8) + c * HCPR + ch, Hs[c & 1] + 64 * op);
+      }
+    };
+    constexpr int NCG = E * E / HCH;  // chunks per group
+    static_assert(NCG * HCH == E * E, "chunks do not straddle groups");
+    issue(0);
 #pragma unroll
-        for (int b0 = 0; b0 < E; b0 += 16) {
-          const int p0 = g * E * E + ai * E + b0;
+    for (int g = 0; g < M; ++g)
+#pragma unroll 1
+    for (int cc = 0; cc < NCG; ++cc) {
+      const int c = g * NCG + cc;
+      vm_wait_barrier<0>();
+      if (c + 1 < NC) issue(c + 1);
+      if (tw < Tn) {
+        const u32x4* Hb = Hs[c & 1];
+#pragma unroll
+        for (int j = 0; j < HCH / 16; ++j) {
+          const int p0 = HCH * c + 16 * j;
+          const int ai = (HCH * cc + 16 * j) / E;
+          const int b0 = (16 * j) % E;  // HCH * cc is a multiple of E
           const int kk = (g * E + b0) / 16;
+          const float qa = (float)qa_row[g * E + ai];
           const f32x4 z0 = *reinterpret_cast<const f32x4*>(hz + p0 + 8 * hh);
           const f32x4 z1 = *reinterpret_cast<const f32x4*>(hz + p0 + 8 * hh + 4);
           f32x8 pf;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) pf[j] = qa * (float)qop[kk][j];
+          for (int jj = 0; jj < 8; ++jj) pf[jj] = qa * (float)qop[kk][jj];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) dpart += pf[j] * z0[j] + pf[4 + j] * z1[j];
+          for (int jj = 0; jj < 4; ++jj) dpart += pf[jj] * z0[jj] + pf[4 + jj] * z1[jj];
           const v8_t<T> y = __builtin_convertvector(pf, v8_t<T>);
 #pragma unroll
-          for (int db = 0; db < DV / 32; ++db)
-            oacc[db] = mma(ld8<T>(hT + (size_t)(32 * db + cl) * P + p0 + 8 * hh), y, oacc[db]);
+          for (int db = 0; db < DV / 32; ++db) {
+            const int row = 32 * db + cl;
+            const u32x4 hv = Hb[row * HCPR + ((2 * j + hh) ^ (row & 15))];
+            oacc[db] = mma(__builtin_bit_cast(v8_t<T>, hv), y, oacc[db]);
+          }
         }
       }
     }
   }
 
-  // intra-segment flash term, keys in [seg_start, min(t0 + 128, T))
+  // intra-segment flash term, keys in [seg_start, min(t0 + 128, T)): key and
+  // value tiles by direct global->LDS copies, double-buffered, V^T through
+  // transposing reads (as kata_fwd_tile_kernel)
   const int s_end = min(t0 + 128, Tn);
-  for (int s0 = seg_start; s0 < s_end; s0 += 64) {
-    __syncthreads();
-    load_tile64x<T, T, DK, KP, 1, true, false>(kb, s0, Tn, a.st, Ks, nullptr, tid, nullptr);
-    load_tile64x<T, T, DV, 1, VP, false, true>(vb, s0, Tn, a.vst, nullptr, Vt, tid, nullptr);
-    __syncthreads();
+  const int nst = (s_end - seg_start + 63) / 64;
+  auto issue = [&](int st) __attribute__((always_inline)) {
+    T* kt = (st & 1) ? Kb1 : Kb0;
+    T* vt = (st & 1) ? Vb1 : Vb0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      dma_tile64<T>(kb, a.st, seg_start + 64 * st, Tn, kt, 2 * w + i, lane);
+      dma_tile64<T>(vb, a.vst, seg_start + 64 * st, Tn, vt, 2 * w + i, lane);
+    }
+  };
+  __syncthreads();  // every wave is done with the prefix-state chunks
+  issue(0);
+  for (int st = 0; st < nst; ++st) {
+    const int s0 = seg_start + 64 * st;
+    vm_wait_barrier<0>();
+    if (st + 1 < nst) issue(st + 1);
+    const T* Kt = (st & 1) ? Kb1 : Kb0;
+    const T* Vs = (st & 1) ? Vb1 : Vb0;
     if (s0 > tw + 31 || tw >= Tn) continue;
     const bool need_mask = (s0 + 63 > tw) || (s0 + 64 > Tn);
     f32x16 sc[2];
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
       sc[sb] = f32x16{};
-      const T* krow = Ks + (32 * sb + cl) * KP + 8 * hh;
 #pragma unroll
       for (int g = 0; g < M; ++g) {
         f32x16 r{};
 #pragma unroll
-        for (int kk = 0; kk < KE; ++kk) r = mma(ld8<T>(krow + g * E + 16 * kk), qop[g * KE + kk], r);
+        for (int kk = 0; kk < KE; ++kk)
+          r = mma(tile_ld8<T>(Kt, 32 * sb + cl, g * E + 16 * kk + 8 * hh), qop[g * KE + kk], r);
         sc[sb] += r * r;
       }
       if (need_mask) {
@@ -253,7 +349,7 @@ __global__ __launch_bounds__(256, 2) void kata_prefill_out_kernel(KataStateArgs 
       dpart = sum8<T>(pb, dpart);
 #pragma unroll
       for (int db = 0; db < DV / 32; ++db)
-        oacc[db] = mma(ld_tr_op<T>(Vt + (32 * db + cl) * VP + 32 * (ks4 >> 1), ks4 & 1, hh), pb, oacc[db]);
+        oacc[db] = mma(tile_tr8<T>(Vs, 32 * (ks4 >> 1), 32 * db, ks4 & 1, lane), pb, oacc[db]);
     }
   }
 
@@ -277,7 +373,7 @@ template <typename T, int DK, int DV, int M>
 hipError_t launch_kata_prefill(const KataStateArgs& a, hipStream_t stream) {
   constexpr int E = DK / M, P = M * E * E;
   const int BH = a.B * a.H;
-  kata_seg_state_kernel<T, DK, DV, M><<<dim3(BH * a.nseg * (P / 128)), dim3(256), 0, stream>>>(a);
+  kata_seg_state_kernel<T, DK, DV, M><<<dim3(BH * a.nseg * (P / 1024)), dim3(512), 0, stream>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t items = (int64_t)BH * (DV + 1) * (P / 4);
