@@ -230,7 +230,7 @@ __global__ __launch_bounds__(64) void delta_state_bwd_kernel(DeltaArgs a, DeltaL
 // in three phases: (A) S and dVn, (B) dS' and Vn, (C) K^T and Q^T.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
-__global__ __launch_bounds__(256) void delta_bwd_chunk_kernel(DeltaArgs a, DeltaLayout L) {
+__global__ __launch_bounds__(256, 2) void delta_bwd_chunk_kernel(DeltaArgs a, DeltaLayout L) {
   constexpr int PX = 64 + 8;   // [d][row] tiles
   constexpr int PV = DV + 8;   // [row][v] tiles
   constexpr int NDW = DK / 64;  // key-dim tiles per wave
@@ -448,7 +448,7 @@ __global__ __launch_bounds__(256) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
 // Wave w: row block ib = w & 1, column half chf = w >> 1.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
-__global__ __launch_bounds__(256) void delta_wy_bwd_kernel(DeltaArgs a, DeltaLayout L) {
+__global__ __launch_bounds__(256, 2) void delta_wy_bwd_kernel(DeltaArgs a, DeltaLayout L) {
   constexpr int PX = 64 + 8;
   constexpr int NKW = DK / 64, NVW = DV / 64;
   __shared__ __attribute__((aligned(16))) T TmT[64 * PX];
