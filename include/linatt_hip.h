@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define LINATT_ABI_VERSION 1
+#define LINATT_ABI_VERSION 2
 
 enum linatt_dtype { LINATT_FLOAT32 = 0, LINATT_BFLOAT16 = 1, LINATT_FLOAT16 = 2 };
 enum linatt_kata_variant { LINATT_KATA_CONCAT = 0, LINATT_KATA_SUM = 1 };
@@ -55,7 +55,8 @@ int linatt_kata_fwd(const void* q, const void* k, const void* v, const float* c,
                     float* den, int B, int T, int HQ, int H, int dk, int dv, int num_groups,
                     float scale, int variant, int dtype, void* stream);
 
-/* Bytes of float32 workspace linatt_kata_bwd needs (the per-row <o, dO>). */
+/* Bytes of float32 workspace linatt_kata_bwd needs: two (B, T, HQ) arrays,
+ * -<o, dO> and scale^2 / den per row. */
 size_t linatt_kata_bwd_workspace_bytes(int B, int T, int HQ);
 
 /* KATA-SPD causal attention backward: dq, dk, dv from q, k, v, o, den, dO.
@@ -86,7 +87,7 @@ int linatt_kata_bwd_decay(const void* q, const void* k, const void* v, const flo
 
 /* The two halves of linatt_kata_bwd, with its argument list, mirroring the
  * reference's separate dq and dk/dv launches (kata/parallel_kata_attn.py:488-528):
- * linatt_kata_bwd_dq writes dq and the per-row <o, dO> into workspace
+ * linatt_kata_bwd_dq writes dq and the per-row terms into workspace
  * (dk, dv may be NULL); linatt_kata_bwd_dkdv then reads workspace and writes
  * dk, dv (o, dq may be NULL).  Enqueue dq before dkdv on the same stream. */
 int linatt_kata_bwd_dq(const void* q, const void* k, const void* v, const void* o,

@@ -18,7 +18,7 @@ LIB_PATH = os.environ.get(
     os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "liblinatt_hip.so"),
 )
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 LINATT_FLOAT32, LINATT_BFLOAT16, LINATT_FLOAT16 = 0, 1, 2
 LINATT_KATA_CONCAT, LINATT_KATA_SUM = 0, 1

@@ -216,7 +216,7 @@ int linatt_kata_fwd(const void* q, const void* k, const void* v, const float* c,
 
 size_t linatt_kata_bwd_workspace_bytes(int B, int T, int HQ) {
   if (B <= 0 || T <= 0 || HQ <= 0) return 0;
-  return (size_t)B * T * HQ * sizeof(float);
+  return 2 * (size_t)B * T * HQ * sizeof(float);
 }
 
 // Shared body of the three backward entry points; `parts` selects the

@@ -102,12 +102,42 @@ __device__ __forceinline__ int wave_id() {
 }
 
 // Direct global -> LDS copy (global_load_lds_dwordx4): lane l's 16 bytes at
-// p land at lds_base + 16 l.  lds_base must be the same for the whole wave.
+// p land at lds_base + 16 l; lds_base must be the same for the whole wave.
 // The copy counts as an outstanding vector-memory load of the issuing wave
-// until it lands; the compiler does not track it, so readers wait with
-// vm_wait_barrier.
+// until it lands, and readers wait for it with vm_wait_barrier.  It is
+// issued from inline assembly so that the compiler, which would otherwise
+// stall every later LDS read until all copies in flight have landed (it
+// cannot tell the slots apart), leaves the scheduling of the waits to that
+// explicit barrier; the compiler's own vmcnt waits stay correct because
+// vector-memory loads of a wave complete in issue order.
 __device__ __forceinline__ void dma16(const void* p, void* lds_base) {
-  __builtin_amdgcn_global_load_lds(p, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)lds_base);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(p), "s"(m0)
+               : "memory", "m0");
+}
+
+// 4-byte variant: lane l's float at p lands at lds_base + 4 l.
+__device__ __forceinline__ void dma4(const void* p, void* lds_base) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)lds_base);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :
+               : "v"(p), "s"(m0)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(0) that the compiler's wait tracking sees: every earlier
+// global load of the wave has landed.  Used once before a loop that keeps
+// copies in flight, so no load issued before it is waited for inside the loop
+// (a compiler-inserted vmcnt(0) there would also wait for the copies).
+__device__ __forceinline__ void vm_drain() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Copy of n4 x 16 bytes (n4 <= 64) from src to lds_base by the calling wave.
+__device__ __forceinline__ void dma_small(const void* src, void* lds_base, int n4, int lane) {
+  if (lane < n4) dma16(reinterpret_cast<const char*>(src) + 16 * lane, lds_base);
 }
 
 // s_waitcnt vmcnt(N) then s_barrier, as one compiler-opaque step (memory
@@ -151,6 +181,15 @@ __device__ __forceinline__ void dma_tile64(const T* g, int64_t rs, int row0, int
 template <typename T>
 __device__ __forceinline__ v8_t<T> tile_ld8(const T* tile, int row, int col) {
   return *reinterpret_cast<const v8_t<T>*>(reinterpret_cast<const char*>(tile) + tile_off(row, col));
+}
+
+// Eight elements of row `row` in the k order of ld_tr_op: columns
+// c0 + 16 j + 4 hh + 0..3 and c0 + 16 j + 8 + 4 hh + 0..3 (two 8-byte reads).
+template <typename T>
+__device__ __forceinline__ v8_t<T> tile_ldp8(const T* tile, int row, int c0, int j, int hh) {
+  const char* base = reinterpret_cast<const char*>(tile);
+  return cat44<T>(*reinterpret_cast<const v4_t<T>*>(base + tile_off(row, c0 + 16 * j + 4 * hh)),
+                  *reinterpret_cast<const v4_t<T>*>(base + tile_off(row, c0 + 16 * j + 8 + 4 * hh)));
 }
 
 // Transposing 8-byte LDS read (ds_read_tr16_b64): within each 16-lane group,
@@ -362,6 +401,48 @@ __device__ __forceinline__ v8_t<T> ld8_f32(const float* p) {
   const f32x8 f{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
   if constexpr (sizeof(T) == 2) return __builtin_convertvector(f, v8_t<T>);
   else return f;
+}
+
+// Swizzled 16-byte slot of (row, chunk) in a row-major LDS tile with CPR
+// 16-byte chunks per row (XOR keeps it an involution within a row).
+template <int CPR>
+__device__ __forceinline__ int swz_slot(int row, int ch) {
+  if constexpr (CPR >= 16) return row * CPR + (ch ^ (row & 15));
+  else return row * CPR + (ch ^ ((row >> 1) & 7));
+}
+
+// A wave's 32 x 64 block of 16-bit values held in C layout (lane column =
+// block row cl; columns 32 b + 8 I + 4 hh + r of the fp32 blocks X[b],
+// b = 0, 1) written to global rows g + row * ld through 4 KiB of LDS: 8-byte
+// LDS writes, then 16-byte reads that give each global store instruction
+// 1 KiB of whole rows.  slot(s), s = 0..255, maps the 16-byte staging slots
+// (row-major 32 x 8, XOR-swizzled by row) to LDS addresses owned by the
+// calling wave.
+template <typename T, typename SlotFn>
+__device__ __forceinline__ void store_rows_via(const f32x16& x0, const f32x16& x1, SlotFn slot,
+                                               T* g, int ld, int lane) {
+  const int cl = lane & 31, hh = lane >> 5;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const f32x16& x = b ? x1 : x0;
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+      *reinterpret_cast<v4_t<T>*>(reinterpret_cast<char*>(slot(swz_slot<8>(cl, 4 * b + I))) + 8 * hh) =
+          to4<T>(x[4 * I], x[4 * I + 1], x[4 * I + 2], x[4 * I + 3]);
+  }
+#pragma unroll
+  for (int op = 0; op < 4; ++op) {
+    const int gi = 64 * op + lane, row = gi >> 3, ch = gi & 7;
+    const u32x4 val = *slot(swz_slot<8>(row, ch));
+    *reinterpret_cast<u32x4*>(g + (size_t)row * ld + 8 * ch) = val;
+  }
+}
+
+// The same through a contiguous 4 KiB staging area.
+template <typename T>
+__device__ __forceinline__ void store_rows_staged(const f32x16& x0, const f32x16& x1, u32x4* stage,
+                                                  T* g, int ld, int lane) {
+  store_rows_via<T>(x0, x1, [&](int s) { return stage + s; }, g, ld, lane);
 }
 
 }  // namespace linatt

@@ -6,8 +6,8 @@
 // Reverse-mode of the chunk form computed by delta_fwd.hip, per chunk with
 // S the state entering it, dS' the gradient of the state leaving it:
 //
-//   dVn = Aqk^T dO + diag(e^(gamma-G)) K dS'                     (kernels 0, 1)
-//   dS  = e^gamma dS' + (scale e^G Q)^T dO - W^T dVn              (kernels 0, 1)
+//   dVn = Aqk^T dO + diag(e^(gamma-G)) K dS'                     (kernel 1)
+//   dS  = e^gamma dS' + (scale e^G Q)^T dO - W^T dVn              (kernel 1)
 //   dQ  = scale e^G dO S^T + Mq K,  Mq = scale (dO Vn^T) o e^(G_i-G_j) [j<=i]
 //   dK  = diag(e^(gamma-G)) Vn dS'^T + Mq^T Q + ...               (kernel 2)
 //   dW  = -dVn S^T                                                (kernel 2)
@@ -15,81 +15,78 @@
 //   dV  = diag(beta) Tm^T dVn,  dK += diag(beta e^G) Tm^T dW + At K + At^T K
 //   dbeta, dG from the same terms; dg = reverse cumsum of dG in the chunk  (kernel 3)
 //
-// Kernel 0 (delta_bwd_pre) forms the state-independent terms of kernel 1 in
-// parallel; kernel 1 (delta_state_bwd) walks the chunks backwards, one wave
-// per (b, h, 32 value columns), with dS in MFMA accumulators.  Kernels 2 and
-// 3 are parallel over (b, h, chunk).
+// Kernel 1 (delta_state_bwd) walks the chunks backwards, one workgroup per
+// (b, h) with dS in MFMA accumulators.  Kernels 2 and 3 are parallel over
+// (b, h, chunk).
 #include "common.h"
 #include "delta_kernels.h"
 
 namespace linatt {
 
 // ---------------------------------------------------------------------------
-// Kernel 0: the parts of the reverse state pass that do not depend on the
-// state gradient, parallel over (b, h, chunk):
-//   dVnl = Aqk^T dO          (64 x DV)  -> dVnlT [v][j]  f32
-//   Z    = (scale e^G Q)^T dO (DK x DV) -> ZT    [v][d]  f32
+// Kernel 1: reverse state pass.  One workgroup per (b, h), one wave per 32
+// value columns, dS in DK/32 accumulator tiles (lane column v).  Per chunk,
+// with dS' the gradient of the state leaving it:
+//   dVn = Aqk^T dO + diag(e^(gamma-G)) K dS'
+//   dS  = e^gamma dS' + (scale e^G Q)^T dO - W^T dVn
+// K, W^T, (scale e^G Q)^T, Aqk^T, dO and G of a chunk are shared by the
+// waves of the head: they reach LDS by direct global->LDS copies (swizzled
+// 64 x 64 tiles, see tile_slot) into two slots, the earlier chunk's copies
+// in flight while the current one computes.  dh^T and dv_new^T leave
+// through LDS staging in the wave's own columns of the dO tiles.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
-__global__ __launch_bounds__(256) void delta_bwd_pre_kernel(DeltaArgs a, DeltaLayout L) {
-  constexpr int PX = 64 + 8;
-  __shared__ __attribute__((aligned(16))) T dOT[DV * PX];
-  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+__global__ __launch_bounds__(64 * (DV / 32)) void delta_state_bwd_kernel(DeltaArgs a, DeltaLayout L) {
+  constexpr int NDT = DK / 32, NW = DV / 32;
+  constexpr int KT = DK / 64, VT = DV / 64;      // 64 x 64 tiles per row block
+  constexpr int TE = 64 * 64;                     // elements per tile
+  constexpr int OPW = 8 / NW;                     // 1 KiB copies per wave per tile
+  constexpr int NTILE = 3 * KT + 1 + VT;          // K, W^T, Qg^T, Aqk^T, dO
+  constexpr int SLOT = NTILE * TE + 64 * 4 / (int)sizeof(T);  // + G of the chunk (f32)
+  static_assert(OPW * NW == 8, "tile split");
+  __shared__ __attribute__((aligned(16))) T Sh[2 * SLOT];
+
+  const int lane = threadIdx.x & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
   const int Tn = a.T, H = a.H, NT = a.NT;
-  const int c = blockIdx.x % NT, bh = blockIdx.x / NT;
+  const int bh = blockIdx.x;
   const int b = bh / H, h = bh % H;
-  const int t0 = c * kChunk;
-  const size_t ci = (size_t)bh * NT + c;
-  const T* dob = (const T*)a.dout + ((size_t)b * Tn * H + h) * DV;
-  load_tile64x<T, T, DV, 1, PX, false, true>(dob, t0, Tn, (int64_t)H * DV, nullptr, dOT, tid, nullptr);
-  __syncthreads();
-
-  const T* aqt = (const T*)(a.ctx + L.AqkT) + ci * 4096;
-  const T* qgt = (const T*)(a.ctx + L.QgT) + ci * DK * 64;
-  float* dvl = reinterpret_cast<float*>(a.ws + L.dVnlT) + ci * DV * 64;
-  float* zt = reinterpret_cast<float*>(a.ws + L.ZT) + ci * DV * DK;
-  constexpr int NVT = DV / 32;
-  // tiles: 2 * NVT of dVnl (j-tile, v-tile), then (DK/32) * NVT of Z
-  constexpr int NTILE = 2 * NVT + (DK / 32) * NVT;
-  for (int tile = w; tile < NTILE; tile += 4) {
-    const bool isz = tile >= 2 * NVT;
-    const int tt = isz ? tile - 2 * NVT : tile;
-    const int rt = tt / NVT, vt = tt % NVT;
-    const T* xrow = isz ? qgt + (32 * rt + cl) * 64 : aqt + (32 * rt + cl) * 64;
-    f32x16 acc{};
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-      acc = mma(ld8<T>(xrow + 16 * s + 8 * hh), ld8<T>(dOT + (32 * vt + cl) * PX + 16 * s + 8 * hh), acc);
-    const int v = 32 * vt + cl;
-    float* dst = isz ? zt + (size_t)v * DK : dvl + (size_t)v * 64;
-#pragma unroll
-    for (int I = 0; I < 4; ++I)
-      *reinterpret_cast<float4*>(dst + 32 * rt + 8 * I + 4 * hh) =
-          make_float4(acc[4 * I], acc[4 * I + 1], acc[4 * I + 2], acc[4 * I + 3]);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Kernel 1: reverse state pass, one wave per (b, h, 32 value columns), dS in
-// DK/32 accumulator tiles (lane column v).  Per chunk:
-//   dVn = dVnl + e^(gamma-G) K dS'  ->  dS = e^gamma dS' + Z - W^T dVn
-// with the next (earlier) chunk's K operands loaded during the current one.
-// ---------------------------------------------------------------------------
-template <typename T, int DK, int DV, bool GATED>
-__global__ __launch_bounds__(64) void delta_state_bwd_kernel(DeltaArgs a, DeltaLayout L) {
-  constexpr int NDT = DK / 32;
-  constexpr int NVB = DV / 32;
-  const int lane = threadIdx.x, cl = lane & 31, hh = lane >> 5;
-  const int Tn = a.T, H = a.H, NT = a.NT;
-  const int vb = blockIdx.x % NVB, bh = blockIdx.x / NVB;
-  const int b = bh / H, h = bh % H;
-  const int v = 32 * vb + cl;
+  const int v = 32 * w + cl;
   const size_t Tp = (size_t)NT * kChunk;
 
   const T* kb = (const T*)a.k + ((size_t)b * Tn * H + h) * DK;
-  const int64_t ks = (int64_t)H * DK;
+  const T* dob = (const T*)a.dout + ((size_t)b * Tn * H + h) * DV;
   const float* Gc = reinterpret_cast<const float*>(a.ctx + L.Gc) + (size_t)bh * Tp;
+
+  auto kt = [&](T* sl, int i) { return sl + i * TE; };                 // K tile i (key dims 64 i..)
+  auto wt = [&](T* sl, int i) { return sl + (KT + i) * TE; };          // W^T rows 64 i..
+  auto qt = [&](T* sl, int i) { return sl + (2 * KT + i) * TE; };      // Qg^T rows 64 i..
+  auto at = [&](T* sl) { return sl + 3 * KT * TE; };                   // Aqk^T
+  auto ot = [&](T* sl, int i) { return sl + (3 * KT + 1 + i) * TE; };  // dO columns 64 i..
+  auto gs = [&](T* sl) { return reinterpret_cast<float*>(sl + NTILE * TE); };
+
+  auto issue = [&](int c) __attribute__((always_inline)) {
+    T* sl = Sh + (c & 1) * SLOT;
+    const int t0 = c * kChunk;
+    const size_t ci = (size_t)bh * NT + c;
+    const T* wtg = (const T*)(a.ctx + L.WT) + ci * DK * 64;
+    const T* qtg = (const T*)(a.ctx + L.QgT) + ci * DK * 64;
+    const T* atg = (const T*)(a.ctx + L.AqkT) + ci * 4096;
+#pragma unroll
+    for (int o = 0; o < OPW; ++o) {
+      const int op = OPW * w + o;
+#pragma unroll
+      for (int i = 0; i < KT; ++i) {
+        dma_tile64<T>(kb + 64 * i, (int64_t)H * DK, t0, Tn, kt(sl, i), op, lane);
+        dma_tile64<T>(wtg + (size_t)64 * i * 64, 64, 0, 64, wt(sl, i), op, lane);
+        dma_tile64<T>(qtg + (size_t)64 * i * 64, 64, 0, 64, qt(sl, i), op, lane);
+      }
+      dma_tile64<T>(atg, 64, 0, 64, at(sl), op, lane);
+#pragma unroll
+      for (int i = 0; i < VT; ++i) dma_tile64<T>(dob + 64 * i, (int64_t)H * DV, t0, Tn, ot(sl, i), op, lane);
+    }
+    if (GATED && w == 0 && lane < 16) dma16(Gc + t0 + 4 * lane, gs(sl));
+  };
 
   f32x16 dS[NDT];
 #pragma unroll
@@ -100,114 +97,114 @@ __global__ __launch_bounds__(64) void delta_state_bwd_kernel(DeltaArgs a, DeltaL
       dS[dt][e] = a.dht ? a.dht[((size_t)bh * DK + d) * DV + v] : 0.f;
     }
 
-  // K operands [jt][db][j]: rows 32 jt + cl of a chunk (zero past T)
-  v8_t<T> kc[2][NDT][2];
-  auto load_k = [&](v8_t<T> (&dst)[2][NDT][2], int c) {
-#pragma unroll
-    for (int jt = 0; jt < 2; ++jt) {
-      const int tj = c * kChunk + 32 * jt + cl;
-#pragma unroll
-      for (int db = 0; db < NDT; ++db)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          dst[jt][db][j] = tj < Tn ? ld_tr_op<T>(kb + (int64_t)tj * ks + 32 * db, j, hh) : zero8<T>();
-    }
-  };
-  load_k(kc, NT - 1);
-
+  vm_drain();  // dh_T is in registers
+  issue(NT - 1);
 #pragma unroll 1
   for (int c = NT - 1; c >= 0; --c) {
     const int t0 = c * kChunk;
     const size_t ci = (size_t)bh * NT + c;
-    // this chunk's W^T operands, dVnl, Z and gates, issued early
-    const T* wt = (const T*)(a.ctx + L.WT) + ci * DK * 64;
-    v8_t<T> wop[NDT][2][2];
+    // chunk c landed for every wave; every wave is done with chunk c + 1
+    vm_wait_barrier<0>();
+    if (c > 0) issue(c - 1);
+    T* sl = Sh + (c & 1) * SLOT;
+    const T* Os = ot(sl, w / 2);  // this wave's 64-column dO tile
+    const int oc0 = 32 * (w & 1);
+
+    // dVn = Aqk^T dO (rows j = 32 jt + ..., lane column v); Z = Qg^T dO
+    f32x16 dVn[2], Z[NDT];
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+    for (int jt = 0; jt < 2; ++jt) {
+      dVn[jt] = f32x16{};
 #pragma unroll
-      for (int it = 0; it < 2; ++it)
+      for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) wop[dt][it][j] = ld8<T>(wt + (32 * dt + cl) * 64 + 32 * it + 16 * j + 8 * hh);
-    const float* dvl = reinterpret_cast<const float*>(a.ws + L.dVnlT) + (ci * DV + v) * 64;
-    const float* zt = reinterpret_cast<const float*>(a.ws + L.ZT) + (ci * DV + v) * DK;
-    f32x4 dl4[2][4], z4[NDT][4];
-#pragma unroll
-    for (int jt = 0; jt < 2; ++jt)
-#pragma unroll
-      for (int I = 0; I < 4; ++I) dl4[jt][I] = *reinterpret_cast<const f32x4*>(dvl + 32 * jt + 8 * I + 4 * hh);
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int I = 0; I < 4; ++I) z4[dt][I] = *reinterpret_cast<const f32x4*>(zt + 32 * dt + 8 * I + 4 * hh);
-    float gam = 0.f;
-    f32x4 gj[2][4];
-    if constexpr (GATED) {
-      gam = Gc[t0 + 63];
-#pragma unroll
-      for (int jt = 0; jt < 2; ++jt)
-#pragma unroll
-        for (int I = 0; I < 4; ++I) gj[jt][I] = *reinterpret_cast<const f32x4*>(Gc + t0 + 32 * jt + 8 * I + 4 * hh);
+        for (int j = 0; j < 2; ++j)
+          dVn[jt] = mma(tile_ldp8<T>(at(sl), 32 * jt + cl, 32 * s2, j, hh),
+                        tile_tr8<T>(Os, 32 * s2, oc0, j, lane), dVn[jt]);
     }
-    v8_t<T> kn[2][NDT][2];
-    if (c > 0) load_k(kn, c - 1);
-
-    // gradient of the state leaving this chunk, transposed [v][d]
-    T* dhg = (T*)(a.ws + L.dhT) + (ci * DV + v) * DK;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int I = 0; I < 4; ++I)
-        st4<T>(dhg + 32 * dt + 8 * I + 4 * hh,
-               to4<T>(dS[dt][4 * I], dS[dt][4 * I + 1], dS[dt][4 * I + 2], dS[dt][4 * I + 3]));
-
-    // dVn = dVnl + e^(gamma - G_j) (K dS')_j
-    f32x16 Pk[2];
-    Pk[0] = Pk[1] = f32x16{};
-#pragma unroll
-    for (int db = 0; db < NDT; ++db)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const v8_t<T> ys = c_to_b<T>(dS[db], j);
-#pragma unroll
-        for (int jt = 0; jt < 2; ++jt) Pk[jt] = mma(kc[jt][db][j], ys, Pk[jt]);
-      }
-    f32x16 dVn[2];
-    T* dvg = (T*)(a.ws + L.dVnT) + (ci * DV + v) * 64;
-#pragma unroll
-    for (int jt = 0; jt < 2; ++jt)
-#pragma unroll
-      for (int I = 0; I < 4; ++I) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float f = GATED ? __expf(gam - gj[jt][I][r]) : 1.f;
-          dVn[jt][4 * I + r] = dl4[jt][I][r] + f * Pk[jt][4 * I + r];
-        }
-        st4<T>(dvg + 32 * jt + 8 * I + 4 * hh,
-               to4<T>(dVn[jt][4 * I], dVn[jt][4 * I + 1], dVn[jt][4 * I + 2], dVn[jt][4 * I + 3]));
-      }
-
-    // dS <- e^gamma dS + Z - W^T dVn
-    const float eg = GATED ? __expf(gam) : 1.f;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
-      f32x16 t2{};
+      Z[dt] = f32x16{};
 #pragma unroll
-      for (int it = 0; it < 2; ++it)
+      for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) t2 = mma(wop[dt][it][j], c_to_b<T>(dVn[it], j), t2);
-#pragma unroll
-      for (int I = 0; I < 4; ++I)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          dS[dt][4 * I + r] = dS[dt][4 * I + r] * eg + z4[dt][I][r] - t2[4 * I + r];
+        for (int j = 0; j < 2; ++j)
+          Z[dt] = mma(tile_ldp8<T>(qt(sl, dt / 2), 32 * (dt & 1) + cl, 32 * s2, j, hh),
+                      tile_tr8<T>(Os, 32 * s2, oc0, j, lane), Z[dt]);
     }
-    if (c > 0) {
+
+    // + diag(e^(gamma - G)) K dS'  (K rows 32 jt + cl of the chunk)
+    const float gam = GATED ? gs(sl)[63] : 0.f;
+    if constexpr (!GATED) {
+#pragma unroll
+      for (int db = 0; db < NDT; ++db)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const v8_t<T> ys = c_to_b<T>(dS[db], j);
+#pragma unroll
+          for (int jt = 0; jt < 2; ++jt)
+            dVn[jt] = mma(tile_ldp8<T>(kt(sl, db / 2), 32 * jt + cl, 32 * (db & 1), j, hh), ys, dVn[jt]);
+        }
+    } else {
+      f32x16 Pk[2];
+      Pk[0] = Pk[1] = f32x16{};
+#pragma unroll
+      for (int db = 0; db < NDT; ++db)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const v8_t<T> ys = c_to_b<T>(dS[db], j);
+#pragma unroll
+          for (int jt = 0; jt < 2; ++jt)
+            Pk[jt] = mma(tile_ldp8<T>(kt(sl, db / 2), 32 * jt + cl, 32 * (db & 1), j, hh), ys, Pk[jt]);
+        }
 #pragma unroll
       for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
-        for (int db = 0; db < NDT; ++db)
+        for (int I = 0; I < 4; ++I) {
+          const f32x4 g4 = *reinterpret_cast<const f32x4*>(gs(sl) + 32 * jt + 8 * I + 4 * hh);
 #pragma unroll
-          for (int j = 0; j < 2; ++j) kc[jt][db][j] = kn[jt][db][j];
+          for (int r = 0; r < 4; ++r) dVn[jt][4 * I + r] += __expf(gam - g4[r]) * Pk[jt][4 * I + r];
+        }
+    }
+    if (t0 + 63 >= Tn) {  // rows past T: K repeats its last row there
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (t0 + 32 * jt + 8 * (e >> 2) + 4 * hh + (e & 3) >= Tn) dVn[jt][e] = 0.f;
+    }
+
+    // dh^T (gradient of the state leaving the chunk, [v][d]) and dv_new^T out
+    // through this wave's dO columns, which it alone reads and has consumed
+    {
+      char* ob = reinterpret_cast<char*>(const_cast<T*>(Os));
+      auto slot = [&](int s) {
+        const int tr = s >> 2, q = s & 3;
+        return reinterpret_cast<u32x4*>(ob + tr * 128 + (tile_slot(tr, 4 * (w & 1) + q) << 4));
+      };
+      T* drows = (T*)(a.ws + L.dhT) + (ci * DV + 32 * w) * DK;
+#pragma unroll
+      for (int blk = 0; blk < NDT / 2; ++blk)
+        store_rows_via<T>(dS[2 * blk], dS[2 * blk + 1], slot, drows + 64 * blk, DK, lane);
+      store_rows_via<T>(dVn[0], dVn[1], slot, (T*)(a.ws + L.dVnT) + (ci * DV + 32 * w) * 64, 64, lane);
+    }
+
+    // dS <- e^gamma dS' + Z - W^T dVn
+    const float eg = GATED ? __expf(gam) : 1.f;
+    v8_t<T> nb[2][2];
+#pragma unroll
+    for (int it = 0; it < 2; ++it)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) nb[it][j] = c_to_b<T>(-dVn[it], j);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      f32x16 acc = GATED ? dS[dt] * eg + Z[dt] : dS[dt] + Z[dt];
+#pragma unroll
+      for (int it = 0; it < 2; ++it)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc = mma(tile_ld8<T>(wt(sl, dt / 2), 32 * (dt & 1) + cl, 32 * it + 16 * j + 8 * hh), nb[it][j], acc);
+      dS[dt] = acc;
     }
   }
 
@@ -706,11 +703,8 @@ template <typename T, int DK, int DV, bool GATED>
 hipError_t launch_delta_bwd(const DeltaArgs& a, hipStream_t stream) {
   const DeltaLayout L = delta_layout(a.B, a.T, a.H, DK, DV, sizeof(T));
   const int BH = a.B * a.H;
-  delta_bwd_pre_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);
+  delta_state_bwd_kernel<T, DK, DV, GATED><<<dim3(BH), dim3(64 * (DV / 32)), 0, stream>>>(a, L);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  delta_state_bwd_kernel<T, DK, DV, GATED><<<dim3(BH * (DV / 32)), dim3(64), 0, stream>>>(a, L);
-  e = hipGetLastError();
   if (e != hipSuccess) return e;
   delta_bwd_chunk_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);
   e = hipGetLastError();

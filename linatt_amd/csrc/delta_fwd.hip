@@ -51,8 +51,6 @@ DeltaLayout delta_layout(int B, int T, int H, int DK, int DV, int eb) {
   L.VnT = take(BH * Tp * DV * eb);
   L.ctx_bytes = off;
   off = 0;
-  L.dVnlT = take(BH * Tp * DV * 4);
-  L.ZT = take(BH * NT * DK * DV * 4);
   L.dVnT = take(BH * Tp * DV * eb);
   L.dhT = take(BH * NT * DK * DV * eb);
   L.dW = take(BH * Tp * DK * 4);
@@ -302,14 +300,6 @@ __global__ __launch_bounds__(256) void delta_prep_kernel(DeltaArgs a, DeltaLayou
 // operand reads of 16 consecutive rows hit distinct banks.
 // ---------------------------------------------------------------------------
 
-// Swizzled 16-byte slot of (row, chunk) in a row-major LDS tile with CPR
-// 16-byte chunks per row (XOR keeps it an involution within a row).
-template <int CPR>
-__device__ __forceinline__ int swz_slot(int row, int ch) {
-  if constexpr (CPR >= 16) return row * CPR + (ch ^ (row & 15));
-  else return row * CPR + (ch ^ ((row >> 1) & 7));
-}
-
 // Wave-level copy of 1 KiB (64 x 16 bytes) of a row-major tile with CPR
 // 16-byte chunks per row into its swizzled LDS image: op covers tile chunks
 // [64 op, 64 op + 64).
@@ -318,32 +308,6 @@ __device__ __forceinline__ void dma_tile_1k(const u32x4* g, u32x4* lds, int op, 
   const int row = (64 * op + lane) / CPR, slot = lane % CPR;
   const int ch = swz_slot<CPR>(row, slot) - row * CPR;  // global chunk held by this slot
   dma16(g + row * CPR + ch, lds + 64 * op);
-}
-
-// A wave's 32 x 64 block of 16-bit values held in C layout (lane column =
-// tile row cl; cols 32 b + 8 I + 4 hh + r of fp32 blocks X[b], b = 0, 1)
-// written to global rows g + row * ld through a private 4 KiB LDS staging
-// area: 8-byte LDS writes, then 16-byte reads that give each global store
-// instruction 1 KiB of whole rows.
-template <typename T>
-__device__ __forceinline__ void store_rows_staged(const f32x16& x0, const f32x16& x1, u32x4* stage,
-                                                  T* g, int ld, int lane) {
-  const int cl = lane & 31, hh = lane >> 5;
-  char* st = reinterpret_cast<char*>(stage);
-#pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    const f32x16& x = b ? x1 : x0;
-#pragma unroll
-    for (int I = 0; I < 4; ++I)
-      *reinterpret_cast<v4_t<T>*>(st + 16 * swz_slot<8>(cl, 4 * b + I) + 8 * hh) =
-          to4<T>(x[4 * I], x[4 * I + 1], x[4 * I + 2], x[4 * I + 3]);
-  }
-#pragma unroll
-  for (int op = 0; op < 4; ++op) {
-    const int gi = 64 * op + lane, row = gi >> 3, ch = gi & 7;
-    const u32x4 val = stage[swz_slot<8>(row, ch)];
-    *reinterpret_cast<u32x4*>(g + (size_t)row * ld + 8 * ch) = val;
-  }
 }
 
 template <typename T, int DK, int DV, bool GATED>
@@ -396,6 +360,7 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_fwd_kernel(DeltaAr
       S[dt][e] = a.h0 ? a.h0[((size_t)bh * DK + d) * DV + v] : 0.f;
     }
 
+  vm_drain();  // h0 is in registers
   issue(0);
   if (NT > 1) issue(1);
 #pragma unroll 1

@@ -35,8 +35,6 @@ struct DeltaLayout {
   size_t VnT;   // (B,H,NT,DV,64) T  v_new^T per chunk, v_new = U - W h
   size_t ctx_bytes;
   // backward scratch
-  size_t dVnlT; // (B,H,NT,DV,64) f32  Aqk^T dO per chunk, transposed
-  size_t ZT;    // (B,H,NT,DV,DK) f32  (scale e^G Q)^T dO per chunk, transposed
   size_t dVnT;  // (B,H,NT,DV,64) T  gradient of v_new, transposed
   size_t dhT;   // (B,H,NT,DV,DK) T  gradient of the state leaving each chunk, transposed
   size_t dW;    // (B,H,Tp,DK) f32

@@ -83,7 +83,10 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dq_kerne
   if (tvalid) {
     const float d = den[qrow];
     pdl = scale2 / (d > 0.f ? d : 1.f);
-    if (hh == 0) delta_out[qrow] = delta;
+    if (hh == 0) {
+      delta_out[qrow] = -delta;
+      delta_out[(int64_t)nbh * Tn + qrow] = pdl;
+    }
   }
 
   f32x16 acc[DK / 32];
@@ -257,7 +260,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
         float dl = 0.f, pd = 0.f;
         if (t < Tn) {
           const int64_t r = ((int64_t)b * Tn + t) * HQ + hq;
-          dl = delta[r];
+          dl = -delta[r];
           const float d = den[r];
           pd = scale2 / (d > 0.f ? d : 1.f);
         }
@@ -484,7 +487,10 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
   if (tvalid) {
     const float d = den[qrow];
     pdl = scale2 / (d > 0.f ? d : 1.f);
-    if (hh == 0) delta_out[qrow] = delta;
+    if (hh == 0) {
+      delta_out[qrow] = -delta;
+      delta_out[(int64_t)nbh * Tn + qrow] = pdl;
+    }
   }
 
   f32x16 acc[DK / 32];
@@ -508,18 +514,14 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
       dma_tile64<T>(vb, vs, 64 * st, Tn, Vb[st & 1], 2 * w + i, lane);
     }
   };
-  float cnext = 0.f;
   auto load_c = [&](int st) __attribute__((always_inline)) {
     if constexpr (DECAY) {
-      const int s = 64 * st + tid;
-      cnext = (tid < 64 && s < Tn) ? c[((int64_t)b * Tn + s) * HQ + hq] : 0.f;
+      if (w == 0) dma4(c + ((int64_t)b * Tn + min(64 * st + lane, Tn - 1)) * HQ + hq, Cs[st & 1]);
     }
   };
+  vm_drain();  // q, dO (and c) of this wave's queries are in registers
   issue(0);
   load_c(0);
-  if constexpr (DECAY) {
-    if (tid < 64) Cs[0][tid] = cnext;
-  }
   for (int st = 0; st < nst; ++st) {
     const int s0 = st * 64, buf = st & 1;
     vm_wait_barrier<0>();
@@ -586,9 +588,6 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
           for (int e = 0; e < 16; ++e) dcr += x[e] * au[e] * msk[e];
         }
       }
-    }
-    if constexpr (DECAY) {
-      if (st + 1 < nst && tid < 64) Cs[buf ^ 1][tid] = cnext;
     }
   }
 
@@ -675,32 +674,22 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
       dma_tile64<T>(ob, os, t0, Tn, Ob[n & 1], 2 * w + i, lane);
     }
   };
-  float nd = 0.f, np = 0.f, nc = 0.f;  // row data of the next tile (tid < 64)
+  // per-row data of a query tile: -delta and scale^2/den as the dq kernel
+  // wrote them (rows [0, B T HQ) and [B T HQ, 2 B T HQ) of `delta`), and c;
+  // rows past T repeat the last one and are masked
+  const int64_t nrows = (int64_t)(nbh / H) * Tn * HQ;
   auto load_rows = [&](int n) __attribute__((always_inline)) {
-    const int hq = h * G + n / nq, t = 64 * (tt0 + n % nq) + tid;
-    nd = 0.f;
-    np = 0.f;
-    nc = 0.f;
-    if (tid < 64 && t < Tn) {
-      const int64_t r = ((int64_t)b * Tn + t) * HQ + hq;
-      nd = -delta[r];
-      const float d = den[r];
-      np = scale2 / (d > 0.f ? d : 1.f);
-      if constexpr (DECAY) nc = c[r];
-    }
-  };
-  auto store_rows = [&](int buf) __attribute__((always_inline)) {
-    if (tid < 64) {
-      Dl[buf][tid] = nd;
-      Pd[buf][tid] = np;
-      if constexpr (DECAY) Ct[buf][tid] = nc;
-    }
+    const int hq = h * G + n / nq, t = min(64 * (tt0 + n % nq) + lane, Tn - 1);
+    const int64_t r = ((int64_t)b * Tn + t) * HQ + hq;
+    if (w == 0) dma4(delta + r, Dl[n & 1]);
+    if (w == 1) dma4(delta + nrows + r, Pd[n & 1]);
+    if (DECAY && w == 2) dma4(c + r, Ct[n & 1]);
   };
 
+  float csl = (DECAY && svalid) ? c[((int64_t)b * Tn + sl) * HQ + h * G] : 0.f;
+  vm_drain();  // k, v (and c) of this wave's keys are in registers
   issue(0);
   load_rows(0);
-  store_rows(0);
-  float csl = (DECAY && svalid) ? c[((int64_t)b * Tn + sl) * HQ + h * G] : 0.f;
   float dcc = 0.f;
   for (int n = 0; n < ntiles; ++n) {
     const int buf = n & 1;
@@ -798,7 +787,6 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
         }
       }
     }
-    store_rows(buf ^ 1);
     if constexpr (DECAY) {
       if (n % nq == nq - 1) {  // last query tile of head hq
         dcc += __shfl_xor(dcc, 32);

@@ -247,18 +247,15 @@ __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
       dma_tile64<T>(vb, vs, 64 * st, Tn, Vb[buf], 2 * w + i, lane);
     }
   };
-  float cnext = 0.f;
+  // decay: c of the tile's keys (rows past T repeat the last one; masked)
   auto load_c = [&](int st) __attribute__((always_inline)) {
     if constexpr (DECAY) {
-      const int s = 64 * st + tid;
-      cnext = (tid < 64 && s < Tn) ? c[((int64_t)b * Tn + s) * HQ + hq] : 0.f;
+      if (w == 0) dma4(c + ((int64_t)b * Tn + min(64 * st + lane, Tn - 1)) * HQ + hq, Cs[st & 1]);
     }
   };
+  vm_drain();  // q (and c) of this wave's queries are in registers
   issue(0);
   load_c(0);
-  if constexpr (DECAY) {
-    if (tid < 64) Cs[0][tid] = cnext;
-  }
   for (int st = 0; st < nst; ++st) {
     const int s0 = st * 64, buf = st & 1;
     // tile st landed (own copies) and every wave passed tile st - 1
@@ -346,9 +343,6 @@ __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
         for (int db = 0; db < DV / 32; ++db)
           oacc[db] = mma(tile_tr8<T>(Vs, 32 * (ks4 >> 1), 32 * db, ks4 & 1, lane), pb, oacc[db]);
       }
-    }
-    if constexpr (DECAY) {
-      if (st + 1 < nst && tid < 64) Cs[buf ^ 1][tid] = cnext;
     }
   }
 

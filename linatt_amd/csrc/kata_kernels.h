@@ -17,7 +17,7 @@ struct KataArgs {
   void* dq;          // (B, T, HQ, DK)
   void* dk;          // (B, T, H, DK)
   void* dv;          // (B, T, H, DV)
-  float* delta;      // (B, T, HQ) workspace: <o, dO> per row
+  float* delta;      // (2, B, T, HQ) workspace: -<o, dO> and scale^2 / den per row
   float* dc;         // (B, T, HQ) gradient of the cumulative log-decay c (decay backward)
   int B, T, HQ, H, DK, DV, M;
   float scale;
@@ -26,7 +26,7 @@ struct KataArgs {
 template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
 hipError_t launch_kata_fwd(const KataArgs& a, hipStream_t stream);
 
-// parts: bit 0 = dq kernel (also writes delta), bit 1 = dk/dv kernel (reads delta)
+// parts: bit 0 = dq kernel (also writes the per-row workspace), bit 1 = dk/dv kernel (reads it)
 enum { KATA_BWD_DQ = 1, KATA_BWD_DKDV = 2 };
 
 template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>

@@ -203,6 +203,7 @@ __global__ __launch_bounds__(256, 2) void kata_prefill_out_kernel(KataStateArgs 
   constexpr int HCH = 128, HCPR = HCH * (int)sizeof(T) / 16;
   static_assert(DK == 64 && DV == 64 && HCPR == 16 && P % HCH == 0, "64 x 128 16-bit state chunks");
   __shared__ __attribute__((aligned(16))) u32x4 Hs[2][DV * HCPR];
+  __shared__ __attribute__((aligned(16))) float Hzs[2][HCH];  // z prefix of the chunk
   T* const Kb0 = reinterpret_cast<T*>(Hs[0]);
   T* const Vb0 = Kb0 + 64 * 64;
   T* const Kb1 = reinterpret_cast<T*>(Hs[1]);
@@ -258,9 +259,11 @@ __global__ __launch_bounds__(256, 2) void kata_prefill_out_kernel(KataStateArgs 
         const int ch = slot ^ (row & 15);
         dma16(hT + (size_t)row * (P / 8) + c * HCPR + ch, Hs[c & 1] + 64 * op);
       }
+      if (w == 0) dma_small(hz + HCH * c, Hzs[c & 1], HCH / 4, lane);
     };
     constexpr int NCG = E * E / HCH;  // chunks per group
     static_assert(NCG * HCH == E * E, "chunks do not straddle groups");
+    vm_drain();  // q of this wave's queries is in registers
     issue(0);
 #pragma unroll
     for (int g = 0; g < M; ++g)
@@ -278,8 +281,8 @@ __global__ __launch_bounds__(256, 2) void kata_prefill_out_kernel(KataStateArgs 
           const int b0 = (16 * j) % E;  // HCH * cc is a multiple of E
           const int kk = (g * E + b0) / 16;
           const float qa = (float)qa_row[g * E + ai];
-          const f32x4 z0 = *reinterpret_cast<const f32x4*>(hz + p0 + 8 * hh);
-          const f32x4 z1 = *reinterpret_cast<const f32x4*>(hz + p0 + 8 * hh + 4);
+          const f32x4 z0 = *reinterpret_cast<const f32x4*>(&Hzs[c & 1][16 * j + 8 * hh]);
+          const f32x4 z1 = *reinterpret_cast<const f32x4*>(&Hzs[c & 1][16 * j + 8 * hh + 4]);
           f32x8 pf;
 #pragma unroll
           for (int jj = 0; jj < 8; ++jj) pf[jj] = qa * (float)qop[kk][jj];
@@ -312,6 +315,7 @@ __global__ __launch_bounds__(256, 2) void kata_prefill_out_kernel(KataStateArgs 
     }
   };
   __syncthreads();  // every wave is done with the prefix-state chunks
+  vm_drain();
   issue(0);
   for (int st = 0; st < nst; ++st) {
     const int s0 = seg_start + 64 * st;
