@@ -119,6 +119,23 @@ __device__ __forceinline__ void dma16(const void* p, void* lds_base) {
                : "memory", "m0");
 }
 
+// The same copy addressed as a wave-uniform 64-bit base (SGPRs) plus a
+// per-lane 32-bit byte offset: a loop that walks a tensor then only moves
+// the scalar base, with no per-lane 64-bit address arithmetic.
+__device__ __forceinline__ void dma16s(const void* sbase, unsigned voff, void* lds_base) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)lds_base);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(m0)
+               : "memory", "m0");
+}
+
+// Raw buffer resource over [p, p + bytes): stores past the end are dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
 // 4-byte variant: lane l's float at p lands at lds_base + 4 l.
 __device__ __forceinline__ void dma4(const void* p, void* lds_base) {
   const unsigned m0 = __builtin_amdgcn_readfirstlane(
@@ -417,8 +434,9 @@ __device__ __forceinline__ int swz_slot(int row, int ch) {
 // LDS writes, then 16-byte reads that give each global store instruction
 // 1 KiB of whole rows.  slot(s), s = 0..255, maps the 16-byte staging slots
 // (row-major 32 x 8, XOR-swizzled by row) to LDS addresses owned by the
-// calling wave.
-template <typename T, typename SlotFn>
+// calling wave.  OPORD stores each 32-column block in operand order
+// (column e at 32 b + opord32(e)).
+template <typename T, bool OPORD = false, typename SlotFn>
 __device__ __forceinline__ void store_rows_via(const f32x16& x0, const f32x16& x1, SlotFn slot,
                                                T* g, int ld, int lane) {
   const int cl = lane & 31, hh = lane >> 5;
@@ -426,9 +444,13 @@ __device__ __forceinline__ void store_rows_via(const f32x16& x0, const f32x16& x
   for (int b = 0; b < 2; ++b) {
     const f32x16& x = b ? x1 : x0;
 #pragma unroll
-    for (int I = 0; I < 4; ++I)
-      *reinterpret_cast<v4_t<T>*>(reinterpret_cast<char*>(slot(swz_slot<8>(cl, 4 * b + I))) + 8 * hh) =
+    for (int I = 0; I < 4; ++I) {
+      // natural: columns 8 I + 4 hh + 0..3; operand order: 16 (I >> 1) + 8 hh + 4 (I & 1) + 0..3
+      const int ch = OPORD ? 4 * b + 2 * (I >> 1) + hh : 4 * b + I;
+      const int bo = OPORD ? 8 * (I & 1) : 8 * hh;
+      *reinterpret_cast<v4_t<T>*>(reinterpret_cast<char*>(slot(swz_slot<8>(cl, ch))) + bo) =
           to4<T>(x[4 * I], x[4 * I + 1], x[4 * I + 2], x[4 * I + 3]);
+    }
   }
 #pragma unroll
   for (int op = 0; op < 4; ++op) {
@@ -439,10 +461,34 @@ __device__ __forceinline__ void store_rows_via(const f32x16& x0, const f32x16& x
 }
 
 // The same through a contiguous 4 KiB staging area.
-template <typename T>
+template <typename T, bool OPORD = false>
 __device__ __forceinline__ void store_rows_staged(const f32x16& x0, const f32x16& x1, u32x4* stage,
                                                   T* g, int ld, int lane) {
-  store_rows_via<T>(x0, x1, [&](int s) { return stage + s; }, g, ld, lane);
+  store_rows_via<T, OPORD>(x0, x1, [&](int s) { return stage + s; }, g, ld, lane);
+}
+
+// store_rows_staged with buffer stores: rows at byte offset soff (wave-
+// uniform) + row * ld_bytes of the buffer rs; the per-lane part of every
+// address is chunk-invariant.
+template <typename T>
+__device__ __forceinline__ void store_rows_buf(const f32x16& x0, const f32x16& x1, u32x4* stage,
+                                               __amdgpu_buffer_rsrc_t rs, int soff, int ld_bytes,
+                                               int lane) {
+  const int cl = lane & 31, hh = lane >> 5;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const f32x16& x = b ? x1 : x0;
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+      *reinterpret_cast<v4_t<T>*>(reinterpret_cast<char*>(stage + swz_slot<8>(cl, 4 * b + I)) + 8 * hh) =
+          to4<T>(x[4 * I], x[4 * I + 1], x[4 * I + 2], x[4 * I + 3]);
+  }
+  const int voff = (lane >> 3) * ld_bytes + 16 * (lane & 7);
+#pragma unroll
+  for (int op = 0; op < 4; ++op) {
+    const u32x4 val = stage[swz_slot<8>(8 * op + (lane >> 3), lane & 7)];
+    __builtin_amdgcn_raw_buffer_store_b128(val, rs, voff + 8 * op * ld_bytes, soff, 0);
+  }
 }
 
 }  // namespace linatt

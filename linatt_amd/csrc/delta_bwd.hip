@@ -29,10 +29,11 @@ namespace linatt {
 // with dS' the gradient of the state leaving it:
 //   dVn = Aqk^T dO + diag(e^(gamma-G)) K dS'
 //   dS  = e^gamma dS' + (scale e^G Q)^T dO - W^T dVn
-// K, W^T, (scale e^G Q)^T, Aqk^T, dO and G of a chunk are shared by the
+// K, W^T, Qg = scale e^G Q, Aqk, dO and G of a chunk are shared by the
 // waves of the head: they reach LDS by direct global->LDS copies (swizzled
 // 64 x 64 tiles, see tile_slot) into two slots, the earlier chunk's copies
-// in flight while the current one computes.  dh^T and dv_new^T leave
+// in flight while the current one computes; Qg^T and Aqk^T operands come
+// from transposing reads.  dh^T and dv_new^T leave
 // through LDS staging in the wave's own columns of the dO tiles.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
@@ -41,7 +42,7 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_bwd_kernel(DeltaAr
   constexpr int KT = DK / 64, VT = DV / 64;      // 64 x 64 tiles per row block
   constexpr int TE = 64 * 64;                     // elements per tile
   constexpr int OPW = 8 / NW;                     // 1 KiB copies per wave per tile
-  constexpr int NTILE = 3 * KT + 1 + VT;          // K, W^T, Qg^T, Aqk^T, dO
+  constexpr int NTILE = 3 * KT + 1 + VT;          // K, W^T, Qg, Aqk, dO
   constexpr int SLOT = NTILE * TE + 64 * 4 / (int)sizeof(T);  // + G of the chunk (f32)
   static_assert(OPW * NW == 8, "tile split");
   __shared__ __attribute__((aligned(16))) T Sh[2 * SLOT];
@@ -60,8 +61,8 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_bwd_kernel(DeltaAr
 
   auto kt = [&](T* sl, int i) { return sl + i * TE; };                 // K tile i (key dims 64 i..)
   auto wt = [&](T* sl, int i) { return sl + (KT + i) * TE; };          // W^T rows 64 i..
-  auto qt = [&](T* sl, int i) { return sl + (2 * KT + i) * TE; };      // Qg^T rows 64 i..
-  auto at = [&](T* sl) { return sl + 3 * KT * TE; };                   // Aqk^T
+  auto qt = [&](T* sl, int i) { return sl + (2 * KT + i) * TE; };      // Qg key dims 64 i..
+  auto at = [&](T* sl) { return sl + 3 * KT * TE; };                   // Aqk
   auto ot = [&](T* sl, int i) { return sl + (3 * KT + 1 + i) * TE; };  // dO columns 64 i..
   auto gs = [&](T* sl) { return reinterpret_cast<float*>(sl + NTILE * TE); };
 
@@ -70,8 +71,8 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_bwd_kernel(DeltaAr
     const int t0 = c * kChunk;
     const size_t ci = (size_t)bh * NT + c;
     const T* wtg = (const T*)(a.ctx + L.WT) + ci * DK * 64;
-    const T* qtg = (const T*)(a.ctx + L.QgT) + ci * DK * 64;
-    const T* atg = (const T*)(a.ctx + L.AqkT) + ci * 4096;
+    const T* qgg = (const T*)(a.ctx + L.Qg) + ci * 64 * DK;
+    const T* atg = (const T*)(a.ctx + L.Aqk) + ci * 4096;
 #pragma unroll
     for (int o = 0; o < OPW; ++o) {
       const int op = OPW * w + o;
@@ -79,7 +80,7 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_bwd_kernel(DeltaAr
       for (int i = 0; i < KT; ++i) {
         dma_tile64<T>(kb + 64 * i, (int64_t)H * DK, t0, Tn, kt(sl, i), op, lane);
         dma_tile64<T>(wtg + (size_t)64 * i * 64, 64, 0, 64, wt(sl, i), op, lane);
-        dma_tile64<T>(qtg + (size_t)64 * i * 64, 64, 0, 64, qt(sl, i), op, lane);
+        dma_tile64<T>(qgg + 64 * i, DK, 0, 64, qt(sl, i), op, lane);
       }
       dma_tile64<T>(atg, 64, 0, 64, at(sl), op, lane);
 #pragma unroll
@@ -110,6 +111,28 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_bwd_kernel(DeltaAr
     const T* Os = ot(sl, w / 2);  // this wave's 64-column dO tile
     const int oc0 = 32 * (w & 1);
 
+    // the LDS operands of dVn, Z and K dS' into registers first: the one
+    // wave per SIMD then never waits on a read inside the MFMA chains
+    v8_t<T> oop[2][2], aop[2][2][2], qop[NDT][2][2], kop[NDT][2][2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        oop[s2][j] = tile_tr8<T>(Os, 32 * s2, oc0, j, lane);
+#pragma unroll
+        for (int jt = 0; jt < 2; ++jt) aop[jt][s2][j] = tile_tr8<T>(at(sl), 32 * s2, 32 * jt, j, lane);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) qop[dt][s2][j] = tile_tr8<T>(qt(sl, dt / 2), 32 * s2, 32 * (dt & 1), j, lane);
+      }
+#pragma unroll
+    for (int db = 0; db < NDT; ++db)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int jt = 0; jt < 2; ++jt)
+          kop[db][j][jt] = tile_ldp8<T>(kt(sl, db / 2), 32 * jt + cl, 32 * (db & 1), j, hh);
+    __builtin_amdgcn_sched_barrier(0);
+
     // dVn = Aqk^T dO (rows j = 32 jt + ..., lane column v); Z = Qg^T dO
     f32x16 dVn[2], Z[NDT];
 #pragma unroll
@@ -118,9 +141,7 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_bwd_kernel(DeltaAr
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          dVn[jt] = mma(tile_ldp8<T>(at(sl), 32 * jt + cl, 32 * s2, j, hh),
-                        tile_tr8<T>(Os, 32 * s2, oc0, j, lane), dVn[jt]);
+        for (int j = 0; j < 2; ++j) dVn[jt] = mma(aop[jt][s2][j], oop[s2][j], dVn[jt]);
     }
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
@@ -128,9 +149,7 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_bwd_kernel(DeltaAr
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          Z[dt] = mma(tile_ldp8<T>(qt(sl, dt / 2), 32 * (dt & 1) + cl, 32 * s2, j, hh),
-                      tile_tr8<T>(Os, 32 * s2, oc0, j, lane), Z[dt]);
+        for (int j = 0; j < 2; ++j) Z[dt] = mma(qop[dt][s2][j], oop[s2][j], Z[dt]);
     }
 
     // + diag(e^(gamma - G)) K dS'  (K rows 32 jt + cl of the chunk)
@@ -142,8 +161,7 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_bwd_kernel(DeltaAr
         for (int j = 0; j < 2; ++j) {
           const v8_t<T> ys = c_to_b<T>(dS[db], j);
 #pragma unroll
-          for (int jt = 0; jt < 2; ++jt)
-            dVn[jt] = mma(tile_ldp8<T>(kt(sl, db / 2), 32 * jt + cl, 32 * (db & 1), j, hh), ys, dVn[jt]);
+          for (int jt = 0; jt < 2; ++jt) dVn[jt] = mma(kop[db][j][jt], ys, dVn[jt]);
         }
     } else {
       f32x16 Pk[2];
@@ -154,8 +172,7 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_bwd_kernel(DeltaAr
         for (int j = 0; j < 2; ++j) {
           const v8_t<T> ys = c_to_b<T>(dS[db], j);
 #pragma unroll
-          for (int jt = 0; jt < 2; ++jt)
-            Pk[jt] = mma(tile_ldp8<T>(kt(sl, db / 2), 32 * jt + cl, 32 * (db & 1), j, hh), ys, Pk[jt]);
+          for (int jt = 0; jt < 2; ++jt) Pk[jt] = mma(kop[db][j][jt], ys, Pk[jt]);
         }
 #pragma unroll
       for (int jt = 0; jt < 2; ++jt)
@@ -166,6 +183,15 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_bwd_kernel(DeltaAr
           for (int r = 0; r < 4; ++r) dVn[jt][4 * I + r] += __expf(gam - g4[r]) * Pk[jt][4 * I + r];
         }
     }
+    // W^T operands of the dS update, read while the MFMAs above run
+    v8_t<T> wop[NDT][2][2];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int it = 0; it < 2; ++it)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          wop[dt][it][j] = tile_ld8<T>(wt(sl, dt / 2), 32 * (dt & 1) + cl, 32 * it + 16 * j + 8 * hh);
     if (t0 + 63 >= Tn) {  // rows past T: K repeats its last row there
 #pragma unroll
       for (int jt = 0; jt < 2; ++jt)
@@ -203,7 +229,7 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_bwd_kernel(DeltaAr
       for (int it = 0; it < 2; ++it)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          acc = mma(tile_ld8<T>(wt(sl, dt / 2), 32 * (dt & 1) + cl, 32 * it + 16 * j + 8 * hh), nb[it][j], acc);
+          acc = mma(wop[dt][it][j], nb[it][j], acc);
       dS[dt] = acc;
     }
   }
@@ -264,7 +290,6 @@ __global__ __launch_bounds__(256, 2) void delta_bwd_chunk_kernel(DeltaArgs a, De
   const T* vng = (const T*)(a.ctx + L.VnT) + ci * DV * 64;
   const T* dvng = (const T*)(a.ws + L.dVnT) + ci * DV * 64;
   const T* aq = (const T*)(a.ctx + L.Aqk) + ci * 4096;
-  const T* aqt = (const T*)(a.ctx + L.AqkT) + ci * 4096;
 
   // phase A tiles
 #pragma unroll
@@ -369,8 +394,10 @@ __global__ __launch_bounds__(256, 2) void delta_bwd_chunk_kernel(DeltaArgs a, De
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       const int r0 = 32 * jt + 8 * I + 4 * hh;
-      const v4_t<T> aq4 = ld4<T>(aq + i * 64 + r0);    // Aqk[i][r0 + r]
-      const v4_t<T> aqt4 = ld4<T>(aqt + i * 64 + r0);  // Aqk[r0 + r][i]
+      const v4_t<T> aq4 = ld4<T>(aq + i * 64 + r0);  // Aqk[i][r0 + r]
+      v4_t<T> aqt4;                                  // Aqk[r0 + r][i]
+#pragma unroll
+      for (int r = 0; r < 4; ++r) aqt4[r] = aq[(r0 + r) * 64 + i];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int rr = r0 + r;

@@ -44,9 +44,8 @@ DeltaLayout delta_layout(int B, int T, int H, int DK, int DV, int eb) {
   L.UT = take(BH * Tp * DV * eb);
   L.WT = take(BH * Tp * DK * eb);
   L.KdT = take(BH * Tp * DK * eb);
-  L.QgT = take(BH * Tp * DK * eb);
+  L.Qg = take(BH * Tp * DK * eb);
   L.Aqk = take(BH * NT * 4096 * eb);
-  L.AqkT = take(BH * NT * 4096 * eb);
   L.hT = take(BH * NT * DK * DV * eb);
   L.VnT = take(BH * Tp * DV * eb);
   L.ctx_bytes = off;
@@ -61,19 +60,29 @@ DeltaLayout delta_layout(int B, int T, int H, int DK, int DV, int eb) {
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 1: per-chunk preparation.
+// Kernel 1: per-chunk preparation, one workgroup of four waves per chunk.
+// The chunk's K and V rows reach LDS by direct copies at the start (rows
+// past T repeat the last valid row; beta = 0 there zeroes every use); q rows
+// go straight to registers.  Phases (barrier between each):
+//   1. Gram A (fp32, LDS) by waves 1-3; Aqk rows 0-31 by wave 0
+//   2. diagonal 16 x 16 inverses of I + A in place (wave 0); Aqk rows
+//      32-63 (wave 1); Qg = scale e^G q (waves 2, 3)
+//   3. block rows 1..3 of Tm = (I + A)^-1 in place (all threads)
+//   4. Tm -> context, Tw = Tm diag(beta e^G) and Tu = Tm diag(beta) as
+//      bf16 tiles; the fp32 area becomes the waves' store staging
+//   5. W, W^T, U^T, Kd^T by MFMA / transposing reads, and the Aqk rows,
+//      out as whole 16-byte rows
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
-__global__ __launch_bounds__(256) void delta_prep_kernel(DeltaArgs a, DeltaLayout L) {
-  constexpr int PK = DK + 8;   // natural K tile pitch
-  constexpr int PX = 64 + 8;   // transposed tile pitch
-  constexpr int PA = 68;       // fp32 A / Tm pitch
-  constexpr int XR = DK > DV ? DK : DV;
-  constexpr int U0 = (64 * PK > XR * PX ? 64 * PK : XR * PX);
-  __shared__ __attribute__((aligned(16))) T Un[U0];          // K natural, then X^T tiles
-  __shared__ __attribute__((aligned(16))) float As[64 * PA];  // A, then Tm as T (pitch PX)
-  __shared__ __attribute__((aligned(16))) float Ts[64 * PA];  // Tm fp32
-  __shared__ __attribute__((aligned(16))) float Gs[64], Bs[64], Sc[64];
+__global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLayout L) {
+  constexpr int KT = DK / 64, VT = DV / 64;
+  static_assert(DK % 64 == 0 && DV % 64 == 0 && DK <= 128 && DV <= 128, "64 or 128 wide");
+  __shared__ __attribute__((aligned(16))) T Kt[KT][64 * 64];  // K rows (swizzled tiles)
+  __shared__ __attribute__((aligned(16))) T Vt[VT][64 * 64];  // V rows
+  __shared__ __attribute__((aligned(16))) float AT[64 * 64];  // A, then Tm in place; then staging
+  __shared__ __attribute__((aligned(16))) T Tw[64 * 64];      // Tm diag(beta e^G)
+  __shared__ __attribute__((aligned(16))) T Tu[64 * 64];      // Tm diag(beta)
+  __shared__ float Bs[64], Gs[64];
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -84,208 +93,253 @@ __global__ __launch_bounds__(256) void delta_prep_kernel(DeltaArgs a, DeltaLayou
   const size_t Tp = (size_t)NT * kChunk;
   const size_t ci = (size_t)bh * NT + c;
 
-  T* Kn = Un;
-  T* Xt = Un;
-  T* Tt = reinterpret_cast<T*>(As);
-  float* Gc = reinterpret_cast<float*>(a.ctx + L.Gc);
-
   const T* qb = (const T*)a.q + ((size_t)b * Tn * H + h) * DK;
   const T* kb = (const T*)a.k + ((size_t)b * Tn * H + h) * DK;
   const T* vb = (const T*)a.v + ((size_t)b * Tn * H + h) * DV;
   const int64_t qks = (int64_t)H * DK, vs = (int64_t)H * DV;
 
-  // beta and G (inclusive cumsum of g; rows past T add 0, so G[63] = gamma).
-  if (tid < 64) {
-    const int t = t0 + tid;
+  // 0. copies, q rows (waves 0, 1: rows 32 w + cl), beta and G (wave 3)
+#pragma unroll
+  for (int o = 0; o < 2; ++o) {
+#pragma unroll
+    for (int i = 0; i < KT; ++i) dma_tile64<T>(kb + 64 * i, qks, t0, Tn, Kt[i], 2 * w + o, lane);
+#pragma unroll
+    for (int i = 0; i < VT; ++i) dma_tile64<T>(vb + 64 * i, vs, t0, Tn, Vt[i], 2 * w + o, lane);
+  }
+  v8_t<T> qop[DK / 16];
+  if (w < 2) {
+    const int ti = t0 + 32 * w + cl;
+#pragma unroll
+    for (int kk = 0; kk < DK / 16; ++kk)
+      qop[kk] = ti < Tn ? ld8<T>(qb + (int64_t)ti * qks + 16 * kk + 8 * hh) : zero8<T>();
+  }
+  if (w == 3) {
+    const int t = t0 + lane;
     float bt = 0.f, gt = 0.f;
     if (t < Tn) {
       bt = a.beta[((size_t)b * Tn + t) * H + h];
       if constexpr (GATED) gt = a.g[((size_t)b * Tn + t) * H + h];
     }
-    Bs[tid] = bt;
     float x = gt;
     if constexpr (GATED) {
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
         const float y = __shfl_up(x, off);
-        if (tid >= off) x += y;
+        if (lane >= off) x += y;
       }
-      Gc[(size_t)bh * Tp + t0 + tid] = x;
+      reinterpret_cast<float*>(a.ctx + L.Gc)[(size_t)bh * Tp + t0 + lane] = x;
     }
-    Gs[tid] = x;
+    Bs[lane] = bt;
+    Gs[lane] = x;
   }
-  for (int idx = tid; idx < 64 * PA; idx += 256) Ts[idx] = 0.f;
-  load_tile64x<T, T, DK, PK, 1, true, false>(kb, t0, Tn, qks, Kn, nullptr, tid, nullptr);
+  vm_wait_barrier<0>();
+
+  // Aqk block (rows i of block ib, columns j of block jb) as D[j][i]: lane
+  // column i, scale (q_i . k_j) e^(G_i - G_j) for j <= i
+  auto aqk_block = [&](int ib, int jb) __attribute__((always_inline)) {
+    f32x16 acc{};
+#pragma unroll
+    for (int kk = 0; kk < DK / 16; ++kk)
+      acc = mma(tile_ld8<T>(Kt[kk / 4], 32 * jb + cl, 16 * (kk % 4) + 8 * hh), qop[kk], acc);
+    const int i = 32 * ib + cl;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int j = 32 * jb + 8 * (e >> 2) + 4 * hh + (e & 3);
+      float val = 0.f;
+      if (j <= i) {
+        val = a.scale * acc[e];
+        if constexpr (GATED) val *= __expf(Gs[i] - Gs[j]);
+      }
+      acc[e] = val;
+    }
+    return acc;
+  };
+  f32x16 aq0{}, aq1{};
+
+  // 1. Gram A[i][j] = beta_i (k_i . k_j) e^(G_i - G_j), i > j (zero above)
+  if (w == 0) {
+    aq0 = aqk_block(0, 0);
+    // the all-zero upper block of A / Tm
+#pragma unroll
+    for (int e = 0; e < 16; ++e) AT[(8 * (e >> 2) + 4 * hh + (e & 3)) * 64 + 32 + cl] = 0.f;
+  } else {
+    const int ib = w >= 2, jb = w == 3;
+    f32x16 acc{};
+#pragma unroll
+    for (int kk = 0; kk < DK / 16; ++kk)
+      acc = mma(tile_ld8<T>(Kt[kk / 4], 32 * ib + cl, 16 * (kk % 4) + 8 * hh),
+                tile_ld8<T>(Kt[kk / 4], 32 * jb + cl, 16 * (kk % 4) + 8 * hh), acc);
+    const int j = 32 * jb + cl;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int i = 32 * ib + 8 * (e >> 2) + 4 * hh + (e & 3);
+      float val = 0.f;
+      if (i > j) {
+        val = Bs[i] * acc[e];
+        if constexpr (GATED) val *= __expf(Gs[i] - Gs[j]);
+      }
+      AT[i * 64 + j] = val;
+    }
+  }
   __syncthreads();
 
-  // Gram (wave w: tile (w >> 1, w & 1)) -> A in LDS; Q K^T -> Aqk, Aqk^T.
+  // 2. wave 0: D_R = (I + A_RR)^-1 for the four diagonal 16 x 16 blocks, one
+  //    column per lane (lane = 16 R + column), written over A_RR
+  if (w == 0) {
+    const int R = lane >> 4, cc = lane & 15;
+    float* blk = AT + 16 * R * 64 + 16 * R;
+    float x[16];
+#pragma unroll
+    for (int ii = 0; ii < 16; ++ii) {
+      float acc = ii == cc ? 1.f : 0.f;
+#pragma unroll
+      for (int q4 = 0; q4 < ii / 4 + 1; ++q4) {
+        const f32x4 a4 = *reinterpret_cast<const f32x4*>(blk + ii * 64 + 4 * q4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (4 * q4 + r < ii) acc -= a4[r] * x[4 * q4 + r];
+      }
+      x[ii] = acc;
+    }
+#pragma unroll
+    for (int ii = 0; ii < 16; ++ii) blk[ii * 64 + cc] = x[ii];
+  } else if (w == 1) {
+    aq0 = aqk_block(1, 0);
+    aq1 = aqk_block(1, 1);
+  } else {
+    // Qg[i][d] = scale e^G_i q_i[d] (zero past T), rows 32 (w - 2) + cl
+    const int i = 32 * (w - 2) + cl, ti = t0 + i;
+    const float sc = ti < Tn ? a.scale * (GATED ? __expf(Gs[i]) : 1.f) : 0.f;
+    T* qg = (T*)(a.ctx + L.Qg) + ((size_t)bh * Tp + t0 + i) * DK;
+#pragma unroll
+    for (int kk = 0; kk < DK / 16; ++kk) {
+      const v8_t<T> x = ti < Tn ? ld8<T>(qb + (int64_t)ti * qks + 16 * kk + 8 * hh) : zero8<T>();
+      v8_t<T> y;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = (T)((float)x[e] * sc);
+      *reinterpret_cast<v8_t<T>*>(qg + 16 * kk + 8 * hh) = y;
+    }
+  }
+  __syncthreads();
+
+  // 3. block rows R = 1..3: Tm_R,<R = -D_R (A_R,<R Tm_<R,<R), in place
   {
-    const int ai = w >> 1, bj = w & 1;
-    f32x16 kk{};
-#pragma unroll
-    for (int s = 0; s < DK / 16; ++s)
-      kk = mma(ld8<T>(Kn + (32 * ai + cl) * PK + 16 * s + 8 * hh),
-               ld8<T>(Kn + (32 * bj + cl) * PK + 16 * s + 8 * hh), kk);
-    const int j = 32 * bj + cl;
-#pragma unroll
-    for (int I = 0; I < 4; ++I)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 32 * ai + 8 * I + 4 * hh + r;
-        float val = 0.f;
-        if (i > j) {
-          val = Bs[i] * kk[4 * I + r];
-          if constexpr (GATED) val *= __expf(Gs[i] - Gs[j]);
-        }
-        As[i * PA + j] = val;
-      }
-    // D[j][i] = k_j . q_i   (j-tile ai, i-tile bj; lane column i)
-    const int i = 32 * bj + cl;
-    const bool qv = t0 + i < Tn;
-    f32x16 qk{};
-#pragma unroll
-    for (int s = 0; s < DK / 16; ++s)
-      qk = mma(ld8<T>(Kn + (32 * ai + cl) * PK + 16 * s + 8 * hh),
-               qv ? ld8<T>(qb + (int64_t)(t0 + i) * qks + 16 * s + 8 * hh) : zero8<T>(), qk);
-    T* aq = (T*)(a.ctx + L.Aqk) + ci * 4096;
-    T* aqt = (T*)(a.ctx + L.AqkT) + ci * 4096;
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      float vals[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int jj = 32 * ai + 8 * I + 4 * hh + r;
-        float val = 0.f;
-        if (jj <= i) {
-          val = a.scale * qk[4 * I + r];
-          if constexpr (GATED) val *= __expf(Gs[i] - Gs[jj]);
-        }
-        vals[r] = val;
-        aqt[jj * 64 + i] = (T)val;
-      }
-      st4<T>(aq + i * 64 + 32 * ai + 8 * I + 4 * hh, to4<T>(vals[0], vals[1], vals[2], vals[3]));
-    }
-  }
-  __syncthreads();
-
-  // Tm = (I + A)^-1 by 16-row blocks: off-block rows from the finished
-  // rows (all threads), then forward substitution inside the diagonal block
-  // with one column per lane (wave 0).
+    const int ii = tid >> 4, cg = tid & 15;
 #pragma unroll 1
-  for (int R = 0; R < 4; ++R) {
-    if (R > 0) {
-      const int i = 16 * R + (tid >> 4);
-      const int cg = tid & 15;
-      for (int m = 0; m < R; ++m) {
-        const int cc = cg + 16 * m;
-        float y = 0.f;
-        for (int j = cc; j < 16 * R; ++j) y -= As[i * PA + j] * Ts[j * PA + cc];
-        Ts[i * PA + cc] = y;
-      }
-    }
-    __syncthreads();
-    if (tid < 64) {
-      const int cc = tid;
-      float x[16];
+    for (int R = 1; R < 4; ++R) {
+      const int i = 16 * R + ii;
+      float y[3];
 #pragma unroll
-      for (int ii = 0; ii < 16; ++ii) {
-        const int i = 16 * R + ii;
-        float acc = (cc == i ? 1.f : 0.f) + (cc < 16 * R ? Ts[i * PA + cc] : 0.f);
-#pragma unroll
-        for (int jj = 0; jj < ii; ++jj) acc -= As[i * PA + 16 * R + jj] * x[jj];
-        x[ii] = (cc <= i) ? acc : 0.f;
-        Ts[i * PA + cc] = x[ii];
+      for (int m = 0; m < 3; ++m) {
+        y[m] = 0.f;
+        if (m < R) {
+          const int cc = cg + 16 * m;
+          for (int j = cc; j < 16 * R; ++j) y[m] -= AT[i * 64 + j] * AT[j * 64 + cc];
+        }
       }
+      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < 3; ++m)
+        if (m < R) AT[i * 64 + cg + 16 * m] = y[m];
+      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < 3; ++m) {
+        if (m < R) {
+          const int cc = cg + 16 * m;
+          float t = 0.f;
+          for (int k = 0; k <= ii; ++k) t += AT[i * 64 + 16 * R + k] * AT[(16 * R + k) * 64 + cc];
+          y[m] = t;
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < 3; ++m)
+        if (m < R) AT[i * 64 + cg + 16 * m] = y[m];
+      __syncthreads();
     }
-    __syncthreads();
   }
 
-  // Tm -> T (natural [i][j], pitch PX) over A, and to the context.
+  // 4. Tm (natural [i][j]) to the context; Tw, Tu tiles.  Thread: row
+  //    tid >> 2, columns 16 (tid & 3) .. +15
   {
-    T* tmg = (T*)(a.ctx + L.Tm) + ci * 4096;
-    for (int idx = tid; idx < 4096; idx += 256) {
-      const int i = idx >> 6, j = idx & 63;
-      const T val = (T)Ts[i * PA + j];
-      Tt[i * PX + j] = val;
-      tmg[idx] = val;
+    const int r = tid >> 2, c0 = 16 * (tid & 3);
+    T* tmg = (T*)(a.ctx + L.Tm) + ci * 4096 + r * 64 + c0;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      v8_t<T> tm, tw, tu;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int j = c0 + 8 * hf + e;
+        const float t = AT[r * 64 + j];
+        const float bj = Bs[j];
+        tm[e] = (T)t;
+        tu[e] = (T)(t * bj);
+        tw[e] = (T)(t * bj * (GATED ? __expf(Gs[j]) : 1.f));
+      }
+      *reinterpret_cast<v8_t<T>*>(tmg + 8 * hf) = tm;
+      *reinterpret_cast<v8_t<T>*>(reinterpret_cast<char*>(Tw) + tile_off(r, c0 + 8 * hf)) = tw;
+      *reinterpret_cast<v8_t<T>*>(reinterpret_cast<char*>(Tu) + tile_off(r, c0 + 8 * hf)) = tu;
     }
   }
-  if (tid < 64) Sc[tid] = a.scale * (GATED ? __expf(Gs[tid]) : 1.f);
   __syncthreads();
 
-  // (scale e^G q)^T and (e^(gamma - G) k)^T per chunk, through LDS.
-  {
-    load_tile64x<T, T, DK, 1, PX, false, true>(qb, t0, Tn, qks, nullptr, Xt, tid, Sc);
-    __syncthreads();
-    T* dst = (T*)(a.ctx + L.QgT) + ci * DK * 64;
-    for (int idx = tid; idx < DK * 64; idx += 256) dst[idx] = Xt[(idx >> 6) * PX + (idx & 63)];
-    __syncthreads();
-    if (tid < 64) Sc[tid] = GATED ? __expf(Gs[63] - Gs[tid]) : 1.f;
-    __syncthreads();
-    load_tile64x<T, T, DK, 1, PX, false, true>(kb, t0, Tn, qks, nullptr, Xt, tid, Sc);
-    __syncthreads();
-    dst = (T*)(a.ctx + L.KdT) + ci * DK * 64;
-    for (int idx = tid; idx < DK * 64; idx += 256) {
-      const int i = idx & 63;
-      dst[(idx & ~63) + (i & 32) + opord32(i & 31)] = Xt[(idx >> 6) * PX + i];
+  // 5. outputs through this wave's 4 KiB of the fp32 area
+  u32x4* stage = reinterpret_cast<u32x4*>(AT) + 256 * w;
+  // W[i][d] (key dims in operand order): D[d][i] = sum_j K[j][d] Tw[i][j]
+  if (w >> 1 < KT) {
+    const int ib = w & 1, kt = w >> 1;
+    f32x16 x[2];
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+      x[db] = f32x16{};
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          x[db] = mma(tile_tr8<T>(Kt[kt], 32 * s2, 32 * db, j, lane),
+                      tile_ldp8<T>(Tw, 32 * ib + cl, 32 * s2, j, hh), x[db]);
     }
-    __syncthreads();
-    if (tid < 64) Sc[tid] = Bs[tid] * (GATED ? __expf(Gs[tid]) : 1.f);
-    __syncthreads();
+    store_rows_staged<T, true>(x[0], x[1], stage, (T*)(a.ctx + L.W) + ((size_t)bh * Tp + t0 + 32 * ib) * DK + 64 * kt,
+                               DK, lane);
   }
-
-  // W = Tm (diag(beta e^G) K): D[d][i] = sum_j Xt[d][j] Tt[i][j]; lane column i.
-  {
-    load_tile64x<T, T, DK, 1, PX, false, true>(kb, t0, Tn, qks, nullptr, Xt, tid, Sc);
-    __syncthreads();
-    const int it = w & 1;
-    const int i = 32 * it + cl;
-    T* wrow = (T*)(a.ctx + L.W) + ((size_t)bh * Tp + t0 + i) * DK;
-    T* wt = (T*)(a.ctx + L.WT) + ci * DK * 64;
+  // W^T[d][i], U^T[v][i] (rows i in operand order): D[i][d] = sum_j Tw[i][j] K[j][d]
+  auto trans_out = [&](const T* tile, const T* Tx, T* dst) __attribute__((always_inline)) {
+    f32x16 x[2];
 #pragma unroll
-    for (int m = 0; m < DK / 64; ++m) {
-      const int dt = (w >> 1) + 2 * m;
-      f32x16 acc{};
+    for (int ib = 0; ib < 2; ++ib) {
+      x[ib] = f32x16{};
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        acc = mma(ld8<T>(Xt + (32 * dt + cl) * PX + 16 * s + 8 * hh),
-                  ld8<T>(Tt + i * PX + 16 * s + 8 * hh), acc);
-      const int ip = (i & 32) + opord32(i & 31);
+      for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-      for (int I = 0; I < 4; ++I) {
-        const int d = 32 * dt + 8 * I + 4 * hh;
-        st4<T>(wrow + 32 * dt + opord32(8 * I + 4 * hh),
-               to4<T>(acc[4 * I], acc[4 * I + 1], acc[4 * I + 2], acc[4 * I + 3]));
+        for (int j = 0; j < 2; ++j)
+          x[ib] = mma(tile_ldp8<T>(Tx, 32 * ib + cl, 32 * s2, j, hh),
+                      tile_tr8<T>(tile, 32 * s2, 32 * (w & 1), j, lane), x[ib]);
+    }
+    store_rows_staged<T, true>(x[0], x[1], stage, dst, 64, lane);
+  };
+  if (w < DK / 32) trans_out(Kt[w >> 1], Tw, (T*)(a.ctx + L.WT) + (ci * DK + 32 * w) * 64);
+  if (w < DV / 32) trans_out(Vt[w >> 1], Tu, (T*)(a.ctx + L.UT) + (ci * DV + 32 * w) * 64);
+  // Kd^T[d][i] = e^(gamma - G_i) k_i[d] (zero past T), rows i in operand order
+  if (w < DK / 32) {
+    f32x16 x[2];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) wt[(d + r) * 64 + ip] = (T)acc[4 * I + r];
+    for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const v8_t<T> k8 = tile_tr8<T>(Kt[w >> 1], 32 * ib, 32 * (w & 1), j, lane);
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+          const int e = 8 * j + p;  // C-layout slot: row 8 (e >> 2) + 4 hh + (e & 3)
+          const int i = 32 * ib + 8 * (e >> 2) + 4 * hh + (e & 3);
+          const float sc = t0 + i < Tn ? (GATED ? __expf(Gs[63] - Gs[i]) : 1.f) : 0.f;
+          x[ib][e] = (float)k8[p] * sc;
+        }
       }
-    }
-    __syncthreads();
-    if (tid < 64) Sc[tid] = Bs[tid];
-    __syncthreads();
+    store_rows_staged<T, true>(x[0], x[1], stage, (T*)(a.ctx + L.KdT) + (ci * DK + 32 * w) * 64, 64, lane);
   }
-
-  // U = Tm (diag(beta) V).
-  {
-    load_tile64x<T, T, DV, 1, PX, false, true>(vb, t0, Tn, vs, nullptr, Xt, tid, Sc);
-    __syncthreads();
-    const int it = w & 1;
-    const int i = 32 * it + cl;
-    T* ut = (T*)(a.ctx + L.UT) + ci * DV * 64;
-#pragma unroll
-    for (int m = 0; m < DV / 64; ++m) {
-      const int vt = (w >> 1) + 2 * m;
-      f32x16 acc{};
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        acc = mma(ld8<T>(Xt + (32 * vt + cl) * PX + 16 * s + 8 * hh),
-                  ld8<T>(Tt + i * PX + 16 * s + 8 * hh), acc);
-      const int ip = (i & 32) + opord32(i & 31);
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        ut[(32 * vt + 8 * (e >> 2) + 4 * hh + (e & 3)) * 64 + ip] = (T)acc[e];
-    }
-  }
+  // Aqk rows (natural [i][j]): wave 0 rows 0-31 (upper block zero), wave 1 rows 32-63
+  if (w < 2)
+    store_rows_staged<T>(aq0, aq1, stage, (T*)(a.ctx + L.Aqk) + ci * 4096 + 32 * w * 64, 64, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -334,22 +388,42 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_fwd_kernel(DeltaAr
   // gcum = the Gc context buffer, passed on its own as __restrict__ so the
   // per-chunk gate is a scalar load (no vector-memory wait in the chain)
   const float* Gc = gcum + (size_t)bh * Tp;
-  const u32x4* Wg = reinterpret_cast<const u32x4*>(a.ctx + L.W) + (size_t)bh * NT * WT16;
-  const u32x4* Kg = reinterpret_cast<const u32x4*>(a.ctx + L.KdT) + (size_t)bh * NT * WT16;
-  const u32x4* Ug = reinterpret_cast<const u32x4*>(a.ctx + L.UT) + (size_t)bh * NT * NW * UT16;
+  // wave-uniform byte bases of this head's W, Kd^T and (this wave's) U^T;
+  // chunk c sits at + c * (bytes per chunk)
+  const char* Wg = a.ctx + L.W + (size_t)bh * NT * WT16 * 16;
+  const char* Kg = a.ctx + L.KdT + (size_t)bh * NT * WT16 * 16;
+  const char* Ug = a.ctx + L.UT + ((size_t)bh * NT * NW + w) * UT16 * 16;
+  // per-lane byte offsets of the copies: 1 KiB copy op covers tile chunks
+  // [64 op, 64 op + 64); slot lane of row r holds global chunk swz(r, lane)
+  unsigned wo[WOPS], ko[WOPS], uo[UOPS];
+#pragma unroll
+  for (int i = 0; i < WOPS; ++i) {
+    const int op = WOPS * w + i;
+    const int rw = (64 * op + lane) / WCPR, rk = (64 * op + lane) / KCPR;
+    wo[i] = 16u * swz_slot<WCPR>(rw, lane % WCPR);
+    ko[i] = 16u * swz_slot<KCPR>(rk, lane % KCPR);
+  }
+#pragma unroll
+  for (int i = 0; i < UOPS; ++i) uo[i] = 16u * swz_slot<KCPR>((64 * i + lane) / KCPR, lane % KCPR);
 
-  // this wave's share of chunk c into ring slot c % 3
-  auto issue = [&](int c) __attribute__((always_inline)) {
-    u32x4* sl = Sh + (c % 3) * SLOT;
+  // this wave's share of chunk c into ring slot SL (= c % 3)
+  auto issue = [&](auto SL, int c) __attribute__((always_inline)) {
+    u32x4* sl = Sh + decltype(SL)::value * SLOT;
 #pragma unroll
     for (int i = 0; i < WOPS; ++i) {
-      dma_tile_1k<WCPR>(Wg + (size_t)c * WT16, sl, WOPS * w + i, lane);
-      dma_tile_1k<KCPR>(Kg + (size_t)c * WT16, sl + WT16, WOPS * w + i, lane);
+      dma16s(Wg + (size_t)c * WT16 * 16, wo[i], sl + 64 * (WOPS * w + i));
+      dma16s(Kg + (size_t)c * WT16 * 16, ko[i], sl + WT16 + 64 * (WOPS * w + i));
     }
 #pragma unroll
     for (int i = 0; i < UOPS; ++i)
-      dma_tile_1k<KCPR>(Ug + ((size_t)c * NW + w) * UT16, sl + 2 * WT16 + w * UT16, i, lane);
+      dma16s(Ug + (size_t)c * NW * UT16 * 16, uo[i], sl + 2 * WT16 + w * UT16 + 64 * i);
   };
+
+  // v_new^T and h^T rows of this head (rows [v][.] per chunk, this wave's 32)
+  const __amdgpu_buffer_rsrc_t vn_rs =
+      buf_rsrc(a.ctx + L.VnT + (size_t)bh * NT * DV * 64 * sizeof(T), (unsigned)(NT * DV * 64 * sizeof(T)));
+  const __amdgpu_buffer_rsrc_t h_rs =
+      buf_rsrc(a.ctx + L.hT + (size_t)bh * NT * DV * DK * sizeof(T), (unsigned)(NT * DV * DK * sizeof(T)));
 
   f32x16 S[NDT];
 #pragma unroll
@@ -360,20 +434,30 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_fwd_kernel(DeltaAr
       S[dt][e] = a.h0 ? a.h0[((size_t)bh * DK + d) * DV + v] : 0.f;
     }
 
-  vm_drain();  // h0 is in registers
-  issue(0);
-  if (NT > 1) issue(1);
-#pragma unroll 1
-  for (int c = 0; c < NT; ++c) {
+  // one chunk in ring slot SL; the loop below is unrolled by the ring depth
+  // so every LDS address is a chunk-invariant register plus a constant
+  auto step = [&](auto SL, int c) __attribute__((always_inline)) {
+    constexpr int sl = decltype(SL)::value;
     // chunk c landed for every wave (only chunk c + 1's copies may remain in
     // flight), and every wave is done with chunk c - 1, whose slot is refilled
     if (c + 1 < NT) vm_wait_barrier<DMA_PER_CHUNK>();
     else vm_wait_barrier<0>();
-    if (c + 2 < NT) issue(c + 2);
-    const size_t ci = (size_t)bh * NT + c;
-    const u32x4* Ws = Sh + (c % 3) * SLOT;
+    if (c + 2 < NT) issue(IntC<(sl + 2) % 3>{}, c + 2);
+    const u32x4* Ws = Sh + sl * SLOT;
     const u32x4* Ks = Ws + WT16;
     const u32x4* Us = Ws + 2 * WT16 + w * UT16;
+
+    // the chunk's LDS operands into registers ahead of their MFMA chains (W
+    // first, U^T and Kd^T behind the W S products): the one wave per SIMD
+    // then never waits on a read inside a chain
+    u32x4 wv[2][NDT][2], kv[NDT][2][2], uv[2][2];
+#pragma unroll
+    for (int db = 0; db < NDT; ++db)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int it = 0; it < 2; ++it) wv[it][db][j] = Ws[swz_slot<WCPR>(32 * it + cl, 4 * db + 2 * j + hh)];
+    __builtin_amdgcn_sched_barrier(0);
 
     // P = W S  (W rows 32 it + cl, key dims in operand order)
     f32x16 P[2];
@@ -384,9 +468,21 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_fwd_kernel(DeltaAr
       for (int j = 0; j < 2; ++j) {
         const v8_t<T> ys = c_to_b<T>(S[db], j);
 #pragma unroll
-        for (int it = 0; it < 2; ++it)
-          P[it] = mma(__builtin_bit_cast(v8_t<T>, Ws[swz_slot<WCPR>(32 * it + cl, 4 * db + 2 * j + hh)]), ys, P[it]);
+        for (int it = 0; it < 2; ++it) P[it] = mma(__builtin_bit_cast(v8_t<T>, wv[it][db][j]), ys, P[it]);
       }
+    // U^T and the Kd^T operands of the state update, read while the MFMAs
+    // above run
+#pragma unroll
+    for (int it = 0; it < 2; ++it)
+#pragma unroll
+      for (int jq = 0; jq < 2; ++jq) uv[it][jq] = Us[swz_slot<KCPR>(cl, 4 * it + 2 * jq + hh)];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int it = 0; it < 2; ++it)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) kv[dt][it][jj] = Ks[swz_slot<KCPR>(32 * dt + cl, 4 * it + 2 * jj + hh)];
+    __builtin_amdgcn_sched_barrier(0);
 
     // v_new = U - P (rows past T are zero in U and W); U^T rows of this
     // wave, chunk rows in operand order
@@ -395,7 +491,7 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_fwd_kernel(DeltaAr
     for (int it = 0; it < 2; ++it)
 #pragma unroll
       for (int jq = 0; jq < 2; ++jq) {
-        const v8_t<T> u8 = __builtin_bit_cast(v8_t<T>, Us[swz_slot<KCPR>(cl, 4 * it + 2 * jq + hh)]);
+        const v8_t<T> u8 = __builtin_bit_cast(v8_t<T>, uv[it][jq]);
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
           const int I = 2 * jq + s2;
@@ -407,12 +503,13 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_fwd_kernel(DeltaAr
     // this wave's U^T area of the slot, which the wave alone reads and has
     // finished with
     u32x4* stage = const_cast<u32x4*>(Us);
-    T* rows = (T*)(a.ctx + L.VnT) + (ci * DV + 32 * w) * 64;
-    store_rows_staged<T>(Vn[0], Vn[1], stage, rows, 64, lane);
-    T* hrows = (T*)(a.ctx + L.hT) + (ci * DV + 32 * w) * DK;
+    store_rows_buf<T>(Vn[0], Vn[1], stage, vn_rs, (int)(((size_t)c * DV + 32 * w) * 64 * sizeof(T)),
+                      64 * (int)sizeof(T), lane);
 #pragma unroll
     for (int blk = 0; blk < NDT / 2; ++blk)
-      store_rows_staged<T>(S[2 * blk], S[2 * blk + 1], stage, hrows + 64 * blk, DK, lane);
+      store_rows_buf<T>(S[2 * blk], S[2 * blk + 1], stage, h_rs,
+                        (int)((((size_t)c * DV + 32 * w) * DK + 64 * blk) * sizeof(T)), DK * (int)sizeof(T),
+                        lane);
 
     // S <- e^gamma S + Kd^T v_new  (Kd^T rows 32 dt + cl, chunk rows in operand order)
     const float eg = GATED ? __expf(Gc[c * kChunk + 63]) : 1.f;
@@ -423,9 +520,18 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_fwd_kernel(DeltaAr
       for (int it = 0; it < 2; ++it)
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj)
-          S[dt] = mma(__builtin_bit_cast(v8_t<T>, Ks[swz_slot<KCPR>(32 * dt + cl, 4 * it + 2 * jj + hh)]),
-                      c_to_b<T>(Vn[it], jj), S[dt]);
+          S[dt] = mma(__builtin_bit_cast(v8_t<T>, kv[dt][it][jj]), c_to_b<T>(Vn[it], jj), S[dt]);
     }
+  };
+
+  vm_drain();  // h0 is in registers
+  issue(IntC<0>{}, 0);
+  if (NT > 1) issue(IntC<1>{}, 1);
+#pragma unroll 1
+  for (int c = 0; c < NT; c += 3) {
+    step(IntC<0>{}, c);
+    if (c + 1 < NT) step(IntC<1>{}, c + 1);
+    if (c + 2 < NT) step(IntC<2>{}, c + 2);
   }
 
   if (a.ht) {

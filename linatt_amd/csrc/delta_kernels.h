@@ -28,9 +28,8 @@ struct DeltaLayout {
   size_t UT;    // (B,H,NT,DV,64) T  (Tm diag(beta) V)^T per chunk, rows i in operand order
   size_t WT;    // (B,H,NT,DK,64) T  W^T per chunk, rows i in operand order
   size_t KdT;   // (B,H,NT,DK,64) T  (e^(gamma - G_i) k_i)^T per chunk, rows i in operand order
-  size_t QgT;   // (B,H,NT,DK,64) T  (scale e^G_i q_i)^T per chunk
+  size_t Qg;    // (B,H,Tp,DK) T  scale e^G_i q_i (zero past T)
   size_t Aqk;   // (B,H,NT,64,64) T  scale (q_i.k_j) e^(G_i-G_j) [j <= i]
-  size_t AqkT;  // (B,H,NT,64,64) T  its transpose
   size_t hT;    // (B,H,NT,DV,DK) T  state entering each chunk, transposed [v][d]
   size_t VnT;   // (B,H,NT,DV,64) T  v_new^T per chunk, v_new = U - W h
   size_t ctx_bytes;
