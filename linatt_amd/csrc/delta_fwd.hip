@@ -67,7 +67,7 @@ DeltaLayout delta_layout(int B, int T, int H, int DK, int DV, int eb) {
 //   1. Gram A (fp32, LDS) by waves 1-3; Aqk rows 0-31 by wave 0
 //   2. diagonal 16 x 16 inverses of I + A in place (wave 0); Aqk rows
 //      32-63 (wave 1); Qg = scale e^G q (waves 2, 3)
-//   3. block rows 1..3 of Tm = (I + A)^-1 in place (all threads)
+//   3. block rows 1..3 of Tm = (I + A)^-1 (all threads)
 //   4. Tm -> context, Tw = Tm diag(beta e^G) and Tu = Tm diag(beta) as
 //      bf16 tiles; the fp32 area becomes the waves' store staging
 //   5. W, W^T, U^T, Kd^T by MFMA / transposing reads, and the Aqk rows,
@@ -82,6 +82,7 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
   __shared__ __attribute__((aligned(16))) float AT[64 * 64];  // A, then Tm in place; then staging
   __shared__ __attribute__((aligned(16))) T Tw[64 * 64];      // Tm diag(beta e^G)
   __shared__ __attribute__((aligned(16))) T Tu[64 * 64];      // Tm diag(beta)
+  __shared__ __attribute__((aligned(16))) float Ys[16 * 48];  // A_R,<R Tm_<R,<R of a block row
   __shared__ float Bs[64], Gs[64];
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
@@ -98,7 +99,7 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
   const T* vb = (const T*)a.v + ((size_t)b * Tn * H + h) * DV;
   const int64_t qks = (int64_t)H * DK, vs = (int64_t)H * DV;
 
-  // 0. copies, q rows (waves 0, 1: rows 32 w + cl), beta and G (wave 3)
+  // 0. copies, q rows, beta and G (wave 3)
 #pragma unroll
   for (int o = 0; o < 2; ++o) {
 #pragma unroll
@@ -106,9 +107,9 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
 #pragma unroll
     for (int i = 0; i < VT; ++i) dma_tile64<T>(vb + 64 * i, vs, t0, Tn, Vt[i], 2 * w + o, lane);
   }
-  v8_t<T> qop[DK / 16];
-  if (w < 2) {
-    const int ti = t0 + 32 * w + cl;
+  v8_t<T> qop[DK / 16];  // q row 32 (w & 1) + cl: Aqk operand (waves 0, 1), Qg source (waves 2, 3)
+  {
+    const int ti = t0 + 32 * (w & 1) + cl;
 #pragma unroll
     for (int kk = 0; kk < DK / 16; ++kk)
       qop[kk] = ti < Tn ? ld8<T>(qb + (int64_t)ti * qks + 16 * kk + 8 * hh) : zero8<T>();
@@ -184,25 +185,37 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
   __syncthreads();
 
   // 2. wave 0: D_R = (I + A_RR)^-1 for the four diagonal 16 x 16 blocks, one
-  //    column per lane (lane = 16 R + column), written over A_RR
+  //    column per lane (lane = 16 R + column), by right-looking substitution
+  //    (each finished x_k updates every later row: one FMA deep per step),
+  //    written over A_RR
   if (w == 0) {
     const int R = lane >> 4, cc = lane & 15;
     float* blk = AT + 16 * R * 64 + 16 * R;
-    float x[16];
+    float acc[16];
 #pragma unroll
-    for (int ii = 0; ii < 16; ++ii) {
-      float acc = ii == cc ? 1.f : 0.f;
+    for (int ii = 0; ii < 16; ++ii) acc[ii] = ii == cc ? 1.f : 0.f;
 #pragma unroll
-      for (int q4 = 0; q4 < ii / 4 + 1; ++q4) {
-        const f32x4 a4 = *reinterpret_cast<const f32x4*>(blk + ii * 64 + 4 * q4);
+    for (int g = 0; g < 4; ++g) {
+      // A_RR columns 4 g .. 4 g + 3 of the rows below, then four steps
+      float ag[16][4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (4 * q4 + r < ii) acc -= a4[r] * x[4 * q4 + r];
+      for (int ii = 0; ii < 16; ++ii) {
+        if (ii > 4 * g) {
+          const f32x4 a4 = *reinterpret_cast<const f32x4*>(blk + ii * 64 + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) ag[ii][r] = a4[r];
+        }
       }
-      x[ii] = acc;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const float xk = acc[4 * g + kk];
+#pragma unroll
+        for (int ii = 0; ii < 16; ++ii)
+          if (ii > 4 * g + kk) acc[ii] -= ag[ii][kk] * xk;
+      }
     }
 #pragma unroll
-    for (int ii = 0; ii < 16; ++ii) blk[ii * 64 + cc] = x[ii];
+    for (int ii = 0; ii < 16; ++ii) blk[ii * 64 + cc] = acc[ii];
   } else if (w == 1) {
     aq0 = aqk_block(1, 0);
     aq1 = aqk_block(1, 1);
@@ -213,50 +226,53 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
     T* qg = (T*)(a.ctx + L.Qg) + ((size_t)bh * Tp + t0 + i) * DK;
 #pragma unroll
     for (int kk = 0; kk < DK / 16; ++kk) {
-      const v8_t<T> x = ti < Tn ? ld8<T>(qb + (int64_t)ti * qks + 16 * kk + 8 * hh) : zero8<T>();
       v8_t<T> y;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) y[e] = (T)((float)x[e] * sc);
+      for (int e = 0; e < 8; ++e) y[e] = (T)((float)qop[kk][e] * sc);
       *reinterpret_cast<v8_t<T>*>(qg + 16 * kk + 8 * hh) = y;
     }
   }
   __syncthreads();
 
-  // 3. block rows R = 1..3: Tm_R,<R = -D_R (A_R,<R Tm_<R,<R), in place
+  // 3. block rows R = 1..3: Y = A_R,<R Tm_<R,<R (to Ys), then
+  //    Tm_R,<R = -D_R Y over A_R,<R.  Thread: row 16 R + (tid >> 4), columns
+  //    (tid & 15) + 16 m, m < R; Tm_<R,<R is stored with its zeros, so every
+  //    sum runs over whole 16-blocks
   {
     const int ii = tid >> 4, cg = tid & 15;
-#pragma unroll 1
-    for (int R = 1; R < 4; ++R) {
+    auto block_row = [&](auto RC) __attribute__((always_inline)) {
+      constexpr int R = decltype(RC)::value;
       const int i = 16 * R + ii;
-      float y[3];
 #pragma unroll
-      for (int m = 0; m < 3; ++m) {
-        y[m] = 0.f;
-        if (m < R) {
-          const int cc = cg + 16 * m;
-          for (int j = cc; j < 16 * R; ++j) y[m] -= AT[i * 64 + j] * AT[j * 64 + cc];
+      for (int m = 0; m < R; ++m) {
+        const int cc = cg + 16 * m;
+        float y4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 16 * m; j < 16 * R; j += 4) {
+          const f32x4 a4 = *reinterpret_cast<const f32x4*>(AT + i * 64 + j);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y4[r] += a4[r] * AT[(j + r) * 64 + cc];
         }
+        Ys[ii * 48 + cc] = (y4[0] + y4[1]) + (y4[2] + y4[3]);
       }
       __syncthreads();
 #pragma unroll
-      for (int m = 0; m < 3; ++m)
-        if (m < R) AT[i * 64 + cg + 16 * m] = y[m];
-      __syncthreads();
+      for (int m = 0; m < R; ++m) {
+        const int cc = cg + 16 * m;
+        float t4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int m = 0; m < 3; ++m) {
-        if (m < R) {
-          const int cc = cg + 16 * m;
-          float t = 0.f;
-          for (int k = 0; k <= ii; ++k) t += AT[i * 64 + 16 * R + k] * AT[(16 * R + k) * 64 + cc];
-          y[m] = t;
+        for (int k = 0; k < 16; k += 4) {
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(AT + i * 64 + 16 * R + k);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) t4[r] += d4[r] * Ys[(k + r) * 48 + cc];
         }
+        AT[i * 64 + cc] = -((t4[0] + t4[1]) + (t4[2] + t4[3]));
       }
       __syncthreads();
-#pragma unroll
-      for (int m = 0; m < 3; ++m)
-        if (m < R) AT[i * 64 + cg + 16 * m] = y[m];
-      __syncthreads();
-    }
+    };
+    block_row(IntC<1>{});
+    block_row(IntC<2>{});
+    block_row(IntC<3>{});
   }
 
   // 4. Tm (natural [i][j]) to the context; Tw, Tu tiles.  Thread: row
