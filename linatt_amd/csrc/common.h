@@ -438,7 +438,7 @@ __device__ __forceinline__ int swz_slot(int row, int ch) {
 // (column e at 32 b + opord32(e)).
 template <typename T, bool OPORD = false, typename SlotFn>
 __device__ __forceinline__ void store_rows_via(const f32x16& x0, const f32x16& x1, SlotFn slot,
-                                               T* g, int ld, int lane) {
+                                               T* g, int64_t ld, int lane, int nvalid = 32) {
   const int cl = lane & 31, hh = lane >> 5;
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
@@ -456,15 +456,16 @@ __device__ __forceinline__ void store_rows_via(const f32x16& x0, const f32x16& x
   for (int op = 0; op < 4; ++op) {
     const int gi = 64 * op + lane, row = gi >> 3, ch = gi & 7;
     const u32x4 val = *slot(swz_slot<8>(row, ch));
-    *reinterpret_cast<u32x4*>(g + (size_t)row * ld + 8 * ch) = val;
+    if (row < nvalid) *reinterpret_cast<u32x4*>(g + row * ld + 8 * ch) = val;
   }
 }
 
-// The same through a contiguous 4 KiB staging area.
+// The same through a contiguous 4 KiB staging area (rows >= nvalid are
+// not stored).
 template <typename T, bool OPORD = false>
 __device__ __forceinline__ void store_rows_staged(const f32x16& x0, const f32x16& x1, u32x4* stage,
-                                                  T* g, int ld, int lane) {
-  store_rows_via<T, OPORD>(x0, x1, [&](int s) { return stage + s; }, g, ld, lane);
+                                                  T* g, int64_t ld, int lane, int nvalid = 32) {
+  store_rows_via<T, OPORD>(x0, x1, [&](int s) { return stage + s; }, g, ld, lane, nvalid);
 }
 
 // store_rows_staged with buffer stores: rows at byte offset soff (wave-

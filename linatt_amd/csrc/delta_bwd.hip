@@ -323,7 +323,7 @@ __global__ __launch_bounds__(256, 2) void delta_bwd_chunk_kernel(DeltaArgs a, De
   float gi_part = 0.f, kd_part = 0.f;
   const float eG = GATED ? __expf(Gi) : 1.f;
   const float eGam = GATED ? __expf(Gs[63] - Gi) : 1.f;
-  float* dWg = reinterpret_cast<float*>(a.ws + L.dW) + ((size_t)bh * Tp + t0 + i) * DK;
+  T* dWg = (T*)(a.ws + L.dW) + ((size_t)bh * Tp + t0 + i) * DK;
   float* dKg = reinterpret_cast<float*>(a.ws + L.dKp) + ((size_t)bh * Tp + t0 + i) * DK;
   T* dqg = (T*)a.dq + (((size_t)b * Tn + ti) * H + h) * DK;
   f32x16 dq[NDW], dks[NDW];
@@ -344,8 +344,7 @@ __global__ __launch_bounds__(256, 2) void delta_bwd_chunk_kernel(DeltaArgs a, De
       const v4_t<T> q4 = valid ? ld4<T>(qb + (int64_t)ti * qks + d) : v4_t<T>{};
 #pragma unroll
       for (int r = 0; r < 4; ++r) gi_part += (float)q4[r] * acc[4 * I + r];
-      *reinterpret_cast<float4*>(dWg + d) =
-          make_float4(-dw[4 * I], -dw[4 * I + 1], -dw[4 * I + 2], -dw[4 * I + 3]);
+      st4<T>(dWg + d, to4<T>(-dw[4 * I], -dw[4 * I + 1], -dw[4 * I + 2], -dw[4 * I + 3]));
     }
     dq[m] = acc;
   }
@@ -468,251 +467,287 @@ __global__ __launch_bounds__(256, 2) void delta_bwd_chunk_kernel(DeltaArgs a, De
 
 // ---------------------------------------------------------------------------
 // Kernel 3: backward through W = Tm diag(beta e^G) K, U = Tm diag(beta) V,
-// Tm = (I + A)^-1; final dk, dv, dbeta, dg.
-// Wave w: row block ib = w & 1, column half chf = w >> 1.
+// Tm = (I + A)^-1; final dk, dv, dbeta, dg.  One workgroup of four waves
+// per chunk; Tm, dU^T, V, K and dW reach LDS by one up-front copy.
+//   dv  = diag(beta) Tm^T dU                       (wave: rows j, 64 v)
+//   dkW = diag(beta e^G) Tm^T dW                   (wave: rows j, 64 d)
+//   dTm = dU (diag(beta) V)^T + dW (diag(beta e^G) K)^T   (one 32 x 32 block per wave)
+//   M^T = dTm^T Tm,  dA^T = -Tm M^T                (bf16 tiles through LDS)
+//   P[a][l] = dA[a][l] beta_a e^(G_a - G_l) (l < a),  dk = dKp + dkW + (P + P^T) K
+// dbeta and dG gather the row / column sums of the same terms; dg is the
+// reverse cumulative sum of dG within the chunk.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
 __global__ __launch_bounds__(256, 2) void delta_wy_bwd_kernel(DeltaArgs a, DeltaLayout L) {
-  constexpr int PX = 64 + 8;
-  constexpr int NKW = DK / 64, NVW = DV / 64;
-  __shared__ __attribute__((aligned(16))) T TmT[64 * PX];
-  __shared__ __attribute__((aligned(16))) T X1T[64 * PX];
-  constexpr int PV = DV + 8;
-  __shared__ __attribute__((aligned(16))) T buf[64 * PV + DK * PX];
-  __shared__ float Gs[64], Bs[64];
-  __shared__ float red_b[2][64], red_g[2][64], red_rb[64];
+  constexpr int KT = DK / 64, VT = DV / 64;
+  constexpr int TE = 64 * 64;
+  constexpr int SE = 8192 / (int)sizeof(T) * 2;            // 16 KiB of T
+  constexpr int WE = KT * TE > SE ? KT * TE : SE;          // dW tiles, then store staging
+  constexpr int XE = 2 * VT * TE > SE * 2 ? 2 * VT * TE : SE * 2;
+  static_assert(DK % 64 == 0 && DV % 64 == 0 && DK <= 128 && DV <= 128, "64 or 128 wide");
+  __shared__ __attribute__((aligned(16))) T Tmt[TE];      // Tm [i][j]
+  __shared__ __attribute__((aligned(16))) T Kt[KT * TE];  // K [j][d], tile kt: d in 64 kt..
+  __shared__ __attribute__((aligned(16))) T dWt[WE];      // dW [i][d]; phase 5: store staging
+  // dU^T [v][i] (tile vt: v in 64 vt..) and V [j][v]; after phase 1:
+  // dTm^T then P [a][l] (0 .. TE), M^T as [a][j] (TE .. 2 TE), Q^T fp32 [l][a] (2 TE ..)
+  __shared__ __attribute__((aligned(16))) T Xr[XE];
+  __shared__ float Bs[64], Gs[64];
+  __shared__ float red_b[4][64], red_g[4][64];
+  T* dUt = Xr;
+  T* Vt = Xr + VT * TE;
+  T* dTT = Xr;
+  T* Pn = Xr;
+  T* MTt = Xr + TE;
+  float* Qb = reinterpret_cast<float*>(Xr + 2 * TE);
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
-  const int ib = w & 1, chf = w >> 1;
   const int Tn = a.T, H = a.H, NT = a.NT;
   const int c = blockIdx.x % NT, bh = blockIdx.x / NT;
   const int b = bh / H, h = bh % H;
   const int t0 = c * kChunk;
   const size_t Tp = (size_t)NT * kChunk;
   const size_t ci = (size_t)bh * NT + c;
+  const int lb = w & 1, hf = w >> 1;  // lane block (output rows j / a), column half
+  const int ja = 32 * lb + cl;        // this lane's output row within the chunk
+  const int nvalid = Tn - (t0 + 32 * lb);
 
   const T* kb = (const T*)a.k + ((size_t)b * Tn * H + h) * DK;
   const T* vb = (const T*)a.v + ((size_t)b * Tn * H + h) * DV;
   const int64_t ks = (int64_t)H * DK, vs = (int64_t)H * DV;
-  const T* tmg = (const T*)(a.ctx + L.Tm) + ci * 4096;
-  const T* dUt = (const T*)(a.ws + L.dVnT) + ci * DV * 64;  // dU^T [v][i]
-  const float* dWg = reinterpret_cast<const float*>(a.ws + L.dW) + ((size_t)bh * Tp + t0) * DK;
-  const float* Gc = reinterpret_cast<const float*>(a.ctx + L.Gc) + (size_t)bh * Tp;
 
-  T* dUn = buf;             // dU natural [i][v]
-  T* dWT = buf + 64 * PV;   // dW^T [d][i]
-  T* KT = buf;
-
-  load_tile64x<T, T, 64, 1, PX, false, true>(tmg, 0, 64, 64, nullptr, TmT, tid, nullptr);
+  // 0. copies; beta and G (wave 3); dKp of this wave's dk blocks
 #pragma unroll
-  for (int r0 = 0; r0 < DV; r0 += 64)
-    load_tile64x<T, T, 64, 1, PV, false, true>(dUt + (size_t)r0 * 64, 0, 64, 64, nullptr, dUn + r0, tid, nullptr);
-  load_tile64x<float, T, DK, 1, PX, false, true>(dWg, 0, 64, DK, nullptr, dWT, tid, nullptr);
-  if (tid < 64) {
-    const int t = t0 + tid;
-    Gs[tid] = GATED ? Gc[t0 + tid] : 0.f;
-    Bs[tid] = t < Tn ? a.beta[((size_t)b * Tn + t) * H + h] : 0.f;
-  }
-  __syncthreads();
-
-  const int i = 32 * ib + cl;  // lane's chunk row
-  const int ti = t0 + i;
-  const bool valid = ti < Tn;
-  const float Gi = Gs[i], Bi = Bs[i];
-  const float eGi = GATED ? __expf(Gi) : 1.f;
-
-  // (a) Tm^T dU -> dv; (b) Tm^T dW -> dk (W part).  Lane column i.
-  float db_part = 0.f, dg_part = 0.f;
-  T* dvg = (T*)a.dv + (((size_t)b * Tn + ti) * H + h) * DV;
+  for (int o = 0; o < 2; ++o) {
+    const int op = 2 * w + o;
+    dma_tile64<T>((const T*)(a.ctx + L.Tm) + ci * 4096, 64, 0, 64, Tmt, op, lane);
 #pragma unroll
-  for (int m = 0; m < NVW; ++m) {
-    const int vt = chf * NVW + m;
-    f32x16 acc{};
+    for (int vt = 0; vt < VT; ++vt) {
+      dma_tile64<T>((const T*)(a.ws + L.dVnT) + (ci * DV + 64 * vt) * 64, 64, 0, 64, dUt + vt * TE, op, lane);
+      dma_tile64<T>(vb + 64 * vt, vs, t0, Tn, Vt + vt * TE, op, lane);
+    }
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      acc = mma(ld8<T>(dUt + (32 * vt + cl) * 64 + 16 * s + 8 * hh),
-                ld8<T>(TmT + i * PX + 16 * s + 8 * hh), acc);
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      const int d = 32 * vt + 8 * I + 4 * hh;
-      const v4_t<T> v4 = valid ? ld4<T>(vb + (int64_t)ti * vs + d) : v4_t<T>{};
-#pragma unroll
-      for (int r = 0; r < 4; ++r) db_part += (float)v4[r] * acc[4 * I + r];
-      if (valid)
-        st4<T>(dvg + d, to4<T>(Bi * acc[4 * I], Bi * acc[4 * I + 1], Bi * acc[4 * I + 2],
-                               Bi * acc[4 * I + 3]));
+    for (int kt = 0; kt < KT; ++kt) {
+      dma_tile64<T>(kb + 64 * kt, ks, t0, Tn, Kt + kt * TE, op, lane);
+      dma_tile64<T>((const T*)(a.ws + L.dW) + ((size_t)bh * Tp + t0) * DK + 64 * kt, DK, 0, 64, dWt + kt * TE, op,
+                    lane);
     }
   }
-  f32x16 dkacc[NKW];
+  if (w == 3) {
+    const int t = t0 + lane;
+    Bs[lane] = t < Tn ? a.beta[((size_t)b * Tn + t) * H + h] : 0.f;
+    Gs[lane] = GATED ? reinterpret_cast<const float*>(a.ctx + L.Gc)[(size_t)bh * Tp + t0 + lane] : 0.f;
+  }
+  const bool has_dk = 2 * hf < DK / 32, has_dv = 2 * hf < DV / 32;
+  f32x16 dk[2];
+  if (has_dk) {
+    const float* p = reinterpret_cast<const float*>(a.ws + L.dKp) + ((size_t)bh * Tp + t0 + ja) * DK + 64 * hf;
 #pragma unroll
-  for (int m = 0; m < NKW; ++m) {
-    const int dt = chf * NKW + m;
-    f32x16 acc{};
+    for (int m = 0; m < 2; ++m)
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      acc = mma(ld8<T>(dWT + (32 * dt + cl) * PX + 16 * s + 8 * hh),
-                ld8<T>(TmT + i * PX + 16 * s + 8 * hh), acc);
+      for (int I = 0; I < 4; ++I) {
+        const f32x4 v4 = *reinterpret_cast<const f32x4*>(p + 32 * m + 8 * I + 4 * hh);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dk[m][4 * I + r] = v4[r];
+      }
+  }
+  vm_wait_barrier<0>();
+
+  const float Bj = Bs[ja], Gj = Gs[ja];
+  const float eGj = GATED ? __expf(Gj) : 1.f;
+  float db_part = 0.f, dg_part = 0.f, rq_part = 0.f;
+
+  // 1a. dv[j][v] = beta_j (Tm^T dU)[j][v] as D[v][j] = sum_i dU^T[v][i] Tm[i][j]
+  f32x16 dv[2];
+  if (has_dv) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int vb2 = 2 * hf + m;
+      const T* du = dUt + (vb2 / 2) * TE;
+      dv[m] = f32x16{};
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+          dv[m] = mma(tile_ldp8<T>(du, 32 * (vb2 & 1) + cl, 32 * ib, jj, hh),
+                      tile_tr8<T>(Tmt, 32 * ib, 32 * lb, jj, lane), dv[m]);
+      // dbeta_j += v_j . (Tm^T dU)_j
+      const char* vt = reinterpret_cast<const char*>(Vt + (vb2 / 2) * TE);
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        const v4_t<T> v4 = *reinterpret_cast<const v4_t<T>*>(vt + tile_off(ja, 32 * (vb2 & 1) + 8 * I + 4 * hh));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) db_part += (float)v4[r] * dv[m][4 * I + r];
+      }
+      dv[m] *= Bj;
+    }
+  }
+  // 1b. dkW[j][d] = beta_j e^G_j (Tm^T dW)[j][d] as D[d][j] = sum_i dW^T[d][i] Tm[i][j]
+  if (has_dk) {
     float kdot = 0.f;
 #pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      const int d = 32 * dt + 8 * I + 4 * hh;
-      const v4_t<T> k4 = valid ? ld4<T>(kb + (int64_t)ti * ks + d) : v4_t<T>{};
+    for (int m = 0; m < 2; ++m) {
+      const int db2 = 2 * hf + m;
+      const T* dwt = dWt + (db2 / 2) * TE;
+      f32x16 x{};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) kdot += (float)k4[r] * acc[4 * I + r];
+      for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+          x = mma(tile_tr8<T>(dwt, 32 * ib, 32 * (db2 & 1), jj, lane), tile_tr8<T>(Tmt, 32 * ib, 32 * lb, jj, lane), x);
+      const char* kt = reinterpret_cast<const char*>(Kt + (db2 / 2) * TE);
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        const v4_t<T> k4 = *reinterpret_cast<const v4_t<T>*>(kt + tile_off(ja, 32 * (db2 & 1) + 8 * I + 4 * hh));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) kdot += (float)k4[r] * x[4 * I + r];
+      }
+      dk[m] += x * (Bj * eGj);
     }
-    db_part += eGi * kdot;
-    dg_part += Bi * eGi * kdot;
-    dkacc[m] = acc * (Bi * eGi);
+    db_part += eGj * kdot;
+    dg_part += Bj * eGj * kdot;
   }
-
-  // (c) dTm^T (lane column i, rows j): beta_j (V_j . dU_i) + beta_j e^G_j (K_j . dW_i)
-  f32x16 dTmT[2];
-#pragma unroll
-  for (int jt = 0; jt < 2; ++jt) {
-    const int jr = 32 * jt + cl;
-    const bool jv = t0 + jr < Tn;
-    f32x16 av{}, ak{};
-#pragma unroll
-    for (int s = 0; s < DV / 16; ++s)
-      av = mma(jv ? ld8<T>(vb + (int64_t)(t0 + jr) * vs + 16 * s + 8 * hh) : zero8<T>(),
-               ld8<T>(dUn + i * PV + 16 * s + 8 * hh), av);
-#pragma unroll
-    for (int s = 0; s < DK / 16; ++s)
-      ak = mma(jv ? ld8<T>(kb + (int64_t)(t0 + jr) * ks + 16 * s + 8 * hh) : zero8<T>(),
-               ld8_f32<T>(dWg + (size_t)i * DK + 16 * s + 8 * hh), ak);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int j = 32 * jt + 8 * (e >> 2) + 4 * hh + (e & 3);
-      const float bj = Bs[j];
-      dTmT[jt][e] = bj * (av[e] + (GATED ? __expf(Gs[j]) : 1.f) * ak[e]);
-    }
-  }
-  // (c2) X1[i][l] = sum_j dTm[i][j] Tm[l][j]: tile l in half chf, lane column i -> X1T[l][i]
+  // 1c. dTm block (rows i = 32 hf + .., lane column j = 32 lb + cl):
+  //     beta_j (dU_i . v_j) + beta_j e^G_j (dW_i . k_j)
+  f32x16 dtm{};
   {
-    const int lt = chf;
-    f32x16 x1{};
+    f32x16 d2{};
 #pragma unroll
-    for (int jt = 0; jt < 2; ++jt)
+    for (int vt = 0; vt < VT; ++vt)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        x1 = mma(ld_tr_op<T>(tmg + (32 * lt + cl) * 64 + 32 * jt, j, hh), c_to_b<T>(dTmT[jt], j), x1);
+      for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int l = 32 * lt + 8 * (e >> 2) + 4 * hh + (e & 3);
-      X1T[l * PX + i] = (T)x1[e];
-    }
+        for (int jj = 0; jj < 2; ++jj)
+          dtm = mma(tile_tr8<T>(dUt + vt * TE, 32 * s2, 32 * hf, jj, lane),
+                    tile_ldp8<T>(Vt + vt * TE, ja, 32 * s2, jj, hh), dtm);
+#pragma unroll
+    for (int kk = 0; kk < DK / 16; ++kk)
+      d2 = mma(tile_ld8<T>(dWt + (kk / 4) * TE, 32 * hf + cl, 16 * (kk % 4) + 8 * hh),
+               tile_ld8<T>(Kt + (kk / 4) * TE, ja, 16 * (kk % 4) + 8 * hh), d2);
+    dtm = (dtm + d2 * eGj) * Bj;
   }
-  __syncthreads();  // X1T complete; dUn / dWT no longer needed
-  load_tile64x<T, T, DK, 1, PX, false, true>(kb, t0, Tn, ks, nullptr, KT, tid, nullptr);
+  // KK block (rows l = 32 hf + .., lane column a = ja) of the Gram matrix;
+  // the block above the diagonal (hf > lb) is not needed
+  const bool lower = hf <= lb;
+  f32x16 kk{};
+  if (lower) {
+#pragma unroll
+    for (int q = 0; q < DK / 16; ++q)
+      kk = mma(tile_ld8<T>(Kt + (q / 4) * TE, 32 * hf + cl, 16 * (q % 4) + 8 * hh),
+               tile_ld8<T>(Kt + (q / 4) * TE, ja, 16 * (q % 4) + 8 * hh), kk);
+  }
+  __syncthreads();  // dU^T and V no longer read
+
+  // 2. dTm^T as a [j][i] tile (row j = this lane, columns i of block hf)
+  {
+    char* t = reinterpret_cast<char*>(dTT);
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+      *reinterpret_cast<v4_t<T>*>(t + tile_off(ja, 32 * hf + 8 * I + 4 * hh)) =
+          to4<T>(dtm[4 * I], dtm[4 * I + 1], dtm[4 * I + 2], dtm[4 * I + 3]);
+  }
   __syncthreads();
 
-  // KK tiles: regs index in tile x, lane index i:  KK[x-row][i]
-  f32x16 KK[2];
+  // 3. M^T[j][a] = sum_i dTm^T[j][i] Tm[i][a]: block (rows j = 32 hf + .., lane
+  //    column a = ja), stored as a [a][j] tile
+  {
+    f32x16 x{};
 #pragma unroll
-  for (int x = 0; x < 2; ++x) {
-    const int xr = 32 * x + cl;
-    const bool xv = t0 + xr < Tn;
-    f32x16 acc{};
+    for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
-    for (int s = 0; s < DK / 16; ++s)
-      acc = mma(xv ? ld8<T>(kb + (int64_t)(t0 + xr) * ks + 16 * s + 8 * hh) : zero8<T>(),
-                valid ? ld8<T>(kb + (int64_t)ti * ks + 16 * s + 8 * hh) : zero8<T>(), acc);
-    KK[x] = acc;
+      for (int jj = 0; jj < 2; ++jj)
+        x = mma(tile_ldp8<T>(dTT, 32 * hf + cl, 32 * ib, jj, hh), tile_tr8<T>(Tmt, 32 * ib, 32 * lb, jj, lane), x);
+    char* t = reinterpret_cast<char*>(MTt);
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+      *reinterpret_cast<v4_t<T>*>(t + tile_off(ja, 32 * hf + 8 * I + 4 * hh)) =
+          to4<T>(x[4 * I], x[4 * I + 1], x[4 * I + 2], x[4 * I + 3]);
   }
+  __syncthreads();
 
-  // (d) orientation 1: lane column a = i, regs l.  dA[a][l] = -sum_i' X1[i'][l] Tm[i'][a]
-  float rb_sum = 0.f, rg_sum = 0.f, cg_sum = 0.f;
-  f32x16 At1[2], At2[2];
+  // 4. dA^T[l][a] = -sum_j Tm[l][j] M^T[j][a] (rows l = 32 hf + .., lane a = ja);
+  //    P[a][l] = dA[a][l] beta_a e^(G_a - G_l) and Q = P o KK for l < a.
+  //    P goes to a [a][l] tile over dTm^T, Q^T to fp32 [l][a].
+  {
+    f32x16 x{};
+    if (lower) {
 #pragma unroll
-  for (int x = 0; x < 2; ++x) {
-    f32x16 acc{};
+      for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      acc = mma(ld8<T>(X1T + (32 * x + cl) * PX + 16 * s + 8 * hh),
-                ld8<T>(TmT + i * PX + 16 * s + 8 * hh), acc);
+        for (int jj = 0; jj < 2; ++jj)
+          x = mma(tile_ldp8<T>(Tmt, 32 * hf + cl, 32 * jb, jj, hh), tile_ldp8<T>(MTt, ja, 32 * jb, jj, hh), x);
+    }
+    f32x16 pq, qq;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int l = 32 * x + 8 * (e >> 2) + 4 * hh + (e & 3);
-      float at = 0.f;
-      if (l < i) {
-        const float dA = -acc[e];
-        const float gam = GATED ? __expf(Gi - Gs[l]) : 1.f;
-        const float e1 = dA * KK[x][e] * gam;
-        rb_sum += e1;
-        rg_sum += Bi * e1;
-        at = dA * Bi * gam;
+      const int l = 32 * hf + 8 * (e >> 2) + 4 * hh + (e & 3);
+      float p = 0.f, q = 0.f;
+      if (lower && l < ja) {
+        const float dA = -x[e];
+        const float g = GATED ? __expf(Gj - Gs[l]) : 1.f;
+        p = dA * Bj * g;
+        q = p * kk[e];
+        db_part += dA * kk[e] * g;
+        rq_part += q;
       }
-      At1[x][e] = at;
+      pq[e] = p;
+      qq[e] = q;
     }
+    char* t = reinterpret_cast<char*>(Pn);
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+      *reinterpret_cast<v4_t<T>*>(t + tile_off(ja, 32 * hf + 8 * I + 4 * hh)) =
+          to4<T>(pq[4 * I], pq[4 * I + 1], pq[4 * I + 2], pq[4 * I + 3]);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) Qb[(32 * hf + 8 * (e >> 2) + 4 * hh + (e & 3)) * 64 + ja] = qq[e];
   }
-  // (e) orientation 2: lane column l = i, regs a.  dA[a][l] = -sum_i' Tm[i'][a] X1[i'][l]
-#pragma unroll
-  for (int x = 0; x < 2; ++x) {
-    f32x16 acc{};
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-      acc = mma(ld8<T>(TmT + (32 * x + cl) * PX + 16 * s + 8 * hh),
-                ld8<T>(X1T + i * PX + 16 * s + 8 * hh), acc);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int aa = 32 * x + 8 * (e >> 2) + 4 * hh + (e & 3);
-      float at = 0.f;
-      if (aa > i) {
-        const float dA = -acc[e];
-        const float gam = GATED ? __expf(Gs[aa] - Gi) : 1.f;
-        const float ba = Bs[aa];
-        cg_sum += dA * ba * KK[x][e] * gam;
-        at = dA * ba * gam;
-      }
-      At2[x][e] = at;
-    }
-  }
-  rb_sum += __shfl_xor(rb_sum, 32);
-  rg_sum += __shfl_xor(rg_sum, 32);
-  cg_sum += __shfl_xor(cg_sum, 32);
+  __syncthreads();
 
-  // dk = dKp + dKW + At K + At^T K   (lane column i, this wave's key-dim half)
-  const float* dKp = reinterpret_cast<const float*>(a.ws + L.dKp) + ((size_t)bh * Tp + t0 + i) * DK;
-  T* dkg = (T*)a.dk + (((size_t)b * Tn + ti) * H + h) * DK;
+  // 5. dk[a][d] += sum_l K[l][d] (P[a][l] + P[l][a]); dk and dv out through
+  //    this wave's 4 KiB of the dW area
+  u32x4* stage = reinterpret_cast<u32x4*>(dWt) + 256 * w;
+  if (has_dk) {
 #pragma unroll
-  for (int m = 0; m < NKW; ++m) {
-    const int dt = chf * NKW + m;
-    f32x16 acc = dkacc[m];
+    for (int m = 0; m < 2; ++m) {
+      const int db2 = 2 * hf + m;
+      const T* ktile = Kt + (db2 / 2) * TE;
 #pragma unroll
-    for (int x = 0; x < 2; ++x)
+      for (int lbk = 0; lbk < 2; ++lbk)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const v8_t<T> xo = ld_tr_op<T>(KT + (32 * dt + cl) * PX + 32 * x, j, hh);
-        acc = mma(xo, c_to_b<T>(At1[x], j), acc);
-        acc = mma(xo, c_to_b<T>(At2[x], j), acc);
-      }
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      const int d = 32 * dt + 8 * I + 4 * hh;
-      const float4 p = *reinterpret_cast<const float4*>(dKp + d);
-      if (valid)
-        st4<T>(dkg + d, to4<T>(acc[4 * I] + p.x, acc[4 * I + 1] + p.y, acc[4 * I + 2] + p.z,
-                               acc[4 * I + 3] + p.w));
+        for (int jj = 0; jj < 2; ++jj) {
+          const v8_t<T> kop = tile_tr8<T>(ktile, 32 * lbk, 32 * (db2 & 1), jj, lane);
+          dk[m] = mma(kop, tile_ldp8<T>(Pn, ja, 32 * lbk, jj, hh), dk[m]);
+          dk[m] = mma(kop, tile_tr8<T>(Pn, 32 * lbk, 32 * lb, jj, lane), dk[m]);
+        }
     }
+    store_rows_staged<T>(dk[0], dk[1], stage, (T*)a.dk + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DK + 64 * hf,
+                         (int64_t)H * DK, lane, nvalid);
   }
+  if (has_dv)
+    store_rows_staged<T>(dv[0], dv[1], stage, (T*)a.dv + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DV + 64 * hf,
+                         (int64_t)H * DV, lane, nvalid);
 
   db_part += __shfl_xor(db_part, 32);
   dg_part += __shfl_xor(dg_part, 32);
+  rq_part += __shfl_xor(rq_part, 32);
   if (hh == 0) {
-    red_b[chf][i] = db_part;
-    red_g[chf][i] = dg_part;
-    if (chf == 0) {
-      red_rb[i] = rb_sum;
-      red_g[0][i] += rg_sum - cg_sum;
-    }
+    red_b[w][ja] = db_part;
+    red_g[w][ja] = dg_part + rq_part;
   }
   __syncthreads();
   if (tid < 64) {
+    // column part of dG: sum_a Q[a][l] = row l of Q^T
+    float cq = 0.f;
+#pragma unroll
+    for (int q4 = 0; q4 < 16; ++q4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(Qb + tid * 64 + 4 * q4);
+      cq += (v[0] + v[1]) + (v[2] + v[3]);
+    }
     const int t = t0 + tid;
-    const float dbeta = red_b[0][tid] + red_b[1][tid] + red_rb[tid];
-    float x = reinterpret_cast<const float*>(a.ws + L.dGp)[(size_t)bh * Tp + t0 + tid] +
-              red_g[0][tid] + red_g[1][tid];
+    const int l2 = tid >> 5;  // lane block of this row
+    const float dbeta = red_b[l2][tid] + red_b[l2 + 2][tid];
+    float x = reinterpret_cast<const float*>(a.ws + L.dGp)[(size_t)bh * Tp + t0 + tid] + red_g[l2][tid] +
+              red_g[l2 + 2][tid] - cq;
     // reverse inclusive cumsum over the chunk: dg_l = sum_{i >= l} dG_i
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
