@@ -246,32 +246,37 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_bwd_kernel(DeltaAr
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 2: dq, dW, the output/state part of dk and of dG.
-// Wave w: row block ib = w & 1 (lane column = chunk row 32 ib + cl), key
-// dims half dhalf = w >> 1.  The transposed per-chunk tiles (h^T, dh^T,
-// v_new^T, dv_new^T) are turned back into value-contiguous rows through LDS
-// in three phases: (A) S and dVn, (B) dS' and Vn, (C) K^T and Q^T.
+// Kernel 2: dq, dW, the output/state part of dk and of dG.  One workgroup of
+// eight waves per chunk; every input tile by one up-front copy (rows past T
+// repeat the last valid row and are masked where they could reach a result).
+//   waves 0-3: dq = scale e^G dO S^T and dW = -dVn S^T (rows i, 64 key dims)
+//   waves 4-7: dKs = e^(gamma - G) Vn dS'^T          (rows j, 64 key dims)
+//   waves 4-6: the nonzero blocks of X = dO Vn^T -> Mq = scale X o e^(G_i-G_j)
+//              [j <= i], and Z = X o Aqk for the dG row / column terms
+//   then dq += Mq K (waves 0-3), dKs += Mq^T Q (waves 4-7)
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
-__global__ __launch_bounds__(256, 2) void delta_bwd_chunk_kernel(DeltaArgs a, DeltaLayout L) {
-  constexpr int PX = 64 + 8;   // [d][row] tiles
-  constexpr int PV = DV + 8;   // [row][v] tiles
-  constexpr int NDW = DK / 64;  // key-dim tiles per wave
-  constexpr int NS = DV / 16;
-  constexpr int RA = DK * PV, RB = 64 * PV, RC = 2 * DK * PX;
-  constexpr int RTOT = (RA + RB > RC) ? RA + RB : RC;
-  __shared__ __attribute__((aligned(16))) T sm[RTOT];
-  __shared__ float Gs[64];
-  __shared__ float red_gi[2][64], red_kd[2][64], red_rc[64];
-  __shared__ float red_s[4];
-  T* Sx = sm;             // phase A: S [d][v];  phase B: dS' [d][v]
-  T* Rx = sm + RA;        // phase A: dVn [i][v]; phase B: Vn [j][v]
-  T* KT = sm;             // phase C: K^T [d][j]
-  T* QT = sm + DK * PX;   // phase C: Q^T [d][i]
+__global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, DeltaLayout L) {
+  constexpr int KT = DK / 64, VT = DV / 64, TE = 64 * 64;
+  constexpr int SE0 = 2 * VT * KT * TE, SE1 = 3 * TE + 8 * 2048;
+  constexpr int SE = SE0 > SE1 ? SE0 : SE1;
+  static_assert(DK % 64 == 0 && DV % 64 == 0 && DK <= 128 && DV <= 128, "64 or 128 wide");
+  // S^T and dS'^T as [v][d] tiles (tile vt * KT + kt); after phase 1: Mq [i][j]
+  // (0 .. TE), Z^T fp32 [j][i] (TE .. 3 TE), store staging (3 TE + 2048 w)
+  __shared__ __attribute__((aligned(16))) T St[SE];
+  __shared__ __attribute__((aligned(16))) T dVt[VT * TE];  // dVn^T [v][i]
+  __shared__ __attribute__((aligned(16))) T Vnt[VT * TE];  // Vn^T [v][j]
+  __shared__ __attribute__((aligned(16))) T Ot[VT * TE];   // dO [i][v]
+  __shared__ __attribute__((aligned(16))) T Qt[KT * TE];   // q [i][d]
+  __shared__ __attribute__((aligned(16))) T Kt[KT * TE];   // k [j][d]
+  __shared__ __attribute__((aligned(16))) T At[TE];        // Aqk [i][j]
+  __shared__ __attribute__((aligned(16))) float Gs[64];
+  __shared__ float red_gi[2][64], red_kd[2][64], red_rs[2][64], red_s[8];
+  T* Mqt = St;
+  float* Zt = reinterpret_cast<float*>(St + TE);
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
-  const int ib = w & 1, dhalf = w >> 1;
   const int Tn = a.T, H = a.H, NT = a.NT;
   const int c = blockIdx.x % NT, bh = blockIdx.x / NT;
   const int b = bh / H, h = bh % H;
@@ -281,185 +286,233 @@ __global__ __launch_bounds__(256, 2) void delta_bwd_chunk_kernel(DeltaArgs a, De
 
   const T* qb = (const T*)a.q + ((size_t)b * Tn * H + h) * DK;
   const T* kb = (const T*)a.k + ((size_t)b * Tn * H + h) * DK;
-  const int64_t qks = (int64_t)H * DK;
   const T* dob = (const T*)a.dout + ((size_t)b * Tn * H + h) * DV;
-  const int64_t os = (int64_t)H * DV;
-  const float* Gc = reinterpret_cast<const float*>(a.ctx + L.Gc) + (size_t)bh * Tp;
-  const T* hg = (const T*)(a.ctx + L.hT) + ci * DV * DK;
-  const T* dhg = (const T*)(a.ws + L.dhT) + ci * DV * DK;
-  const T* vng = (const T*)(a.ctx + L.VnT) + ci * DV * 64;
-  const T* dvng = (const T*)(a.ws + L.dVnT) + ci * DV * 64;
-  const T* aq = (const T*)(a.ctx + L.Aqk) + ci * 4096;
+  const int64_t qks = (int64_t)H * DK, os = (int64_t)H * DV;
 
-  // phase A tiles
+  // 0. copies (op w of every tile; Aqk last), G by wave 0
+  {
+    const T* hg = (const T*)(a.ctx + L.hT) + ci * DV * DK;
+    const T* dhg = (const T*)(a.ws + L.dhT) + ci * DV * DK;
 #pragma unroll
-  for (int r0 = 0; r0 < DV; r0 += 64) {
-    load_tile64x<T, T, DK, 1, PV, false, true>(hg + (size_t)r0 * DK, 0, 64, DK, nullptr, Sx + r0, tid, nullptr);
-    load_tile64x<T, T, 64, 1, PV, false, true>(dvng + (size_t)r0 * 64, 0, 64, 64, nullptr, Rx + r0, tid, nullptr);
+    for (int vt = 0; vt < VT; ++vt)
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        dma_tile64<T>(hg + (size_t)64 * vt * DK + 64 * kt, DK, 0, 64, St + (vt * KT + kt) * TE, w, lane);
+        dma_tile64<T>(dhg + (size_t)64 * vt * DK + 64 * kt, DK, 0, 64, St + (VT * KT + vt * KT + kt) * TE, w, lane);
+      }
+#pragma unroll
+    for (int vt = 0; vt < VT; ++vt) {
+      dma_tile64<T>((const T*)(a.ws + L.dVnT) + (ci * DV + 64 * vt) * 64, 64, 0, 64, dVt + vt * TE, w, lane);
+      dma_tile64<T>((const T*)(a.ctx + L.VnT) + (ci * DV + 64 * vt) * 64, 64, 0, 64, Vnt + vt * TE, w, lane);
+      dma_tile64<T>(dob + 64 * vt, os, t0, Tn, Ot + vt * TE, w, lane);
+    }
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      dma_tile64<T>(qb + 64 * kt, qks, t0, Tn, Qt + kt * TE, w, lane);
+      dma_tile64<T>(kb + 64 * kt, qks, t0, Tn, Kt + kt * TE, w, lane);
+    }
+    if (GATED && w == 0 && lane < 16)
+      dma16(reinterpret_cast<const float*>(a.ctx + L.Gc) + (size_t)bh * Tp + t0 + 4 * lane, Gs);
+    dma_tile64<T>((const T*)(a.ctx + L.Aqk) + ci * 4096, 64, 0, 64, At, w, lane);
   }
-  if (tid < 64) Gs[tid] = GATED ? Gc[t0 + tid] : 0.f;
+  if (!GATED && tid < 64) Gs[tid] = 0.f;
+  if (tid < 128) {
+    red_gi[tid >> 6][tid & 63] = 0.f;
+    red_kd[tid >> 6][tid & 63] = 0.f;
+    red_rs[tid >> 6][tid & 63] = 0.f;
+  }
+  vm_wait_barrier<1>();  // everything but Aqk
 
-  // <S, dS'> over the chunk's state pair (for d gamma); both stored [v][d].
+  const float gam = Gs[63];
+  const int wl = w & 3, lb = wl & 1, dp = wl >> 1;  // lane block, key-dim pair (tile dp)
+  const int r = 32 * lb + cl;                      // this lane's row (i or j) in the chunk
+  const bool rvalid = t0 + r < Tn;
+  const bool active = dp < KT;
+  f32x16 acc[2], dwk[2];
+  float part = 0.f;
+
+  // 1. waves 0-3: dq (scaled) and dW; waves 4-7: dKs
+  if (active) {
+    if (w < 4) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        acc[m] = f32x16{};
+        dwk[m] = f32x16{};
+#pragma unroll
+        for (int vt = 0; vt < VT; ++vt)
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+              const v8_t<T> hop = tile_tr8<T>(St + (vt * KT + dp) * TE, 32 * s2, 32 * m, jj, lane);
+              acc[m] = mma(hop, tile_ldp8<T>(Ot + vt * TE, r, 32 * s2, jj, hh), acc[m]);
+              dwk[m] = mma(hop, tile_tr8<T>(dVt + vt * TE, 32 * s2, 32 * lb, jj, lane), dwk[m]);
+            }
+      }
+      const float f = a.scale * (GATED ? __expf(Gs[r]) : 1.f);
+      const char* qrow = reinterpret_cast<const char*>(Qt + dp * TE);
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        acc[m] *= f;
+        dwk[m] = -dwk[m];
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+          const v4_t<T> q4 = *reinterpret_cast<const v4_t<T>*>(qrow + tile_off(r, 32 * m + 8 * I + 4 * hh));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) part += (float)q4[e] * acc[m][4 * I + e];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        acc[m] = f32x16{};
+#pragma unroll
+        for (int vt = 0; vt < VT; ++vt)
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+              acc[m] = mma(tile_tr8<T>(St + (VT * KT + vt * KT + dp) * TE, 32 * s2, 32 * m, jj, lane),
+                           tile_tr8<T>(Vnt + vt * TE, 32 * s2, 32 * lb, jj, lane), acc[m]);
+      }
+      const float f = GATED ? __expf(gam - Gs[r]) : 1.f;
+      const char* krow = reinterpret_cast<const char*>(Kt + dp * TE);
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        acc[m] *= f;
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+          const v4_t<T> k4 = *reinterpret_cast<const v4_t<T>*>(krow + tile_off(r, 32 * m + 8 * I + 4 * hh));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) part += (float)k4[e] * acc[m][4 * I + e];
+        }
+      }
+    }
+    if (!rvalid) part = 0.f;
+  }
+  // <S, dS'> over the chunk's state pair (same tile layout: order-free sum)
   float sdot = 0.f;
-  for (int idx = 8 * tid; idx < DK * DV; idx += 8 * 256) {
-    const v8_t<T> x = ld8<T>(hg + idx), y = ld8<T>(dhg + idx);
+  {
+    constexpr int N16 = VT * KT * TE / 8;  // 16-byte chunks per state
+    const u32x4* s0 = reinterpret_cast<const u32x4*>(St);
+    const u32x4* s1 = s0 + N16;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) sdot += (float)x[j] * (float)y[j];
+    for (int k = 0; k < N16 / 512; ++k) {
+      const v8_t<T> x = __builtin_bit_cast(v8_t<T>, s0[tid + 512 * k]);
+      const v8_t<T> y = __builtin_bit_cast(v8_t<T>, s1[tid + 512 * k]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sdot += (float)x[e] * (float)y[e];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sdot += __shfl_xor(sdot, off);
   }
+  // waves 4-6: X block (ib, jb) = (0,0), (1,0), (1,1) as D[j][i] (lane column i)
+  const int mb = w - 4;  // 0..2: blocks (0,0), (1,0), (1,1); 3: the zero block (0,1)
+  const int xib = mb == 1 || mb == 2, xjb = mb >= 2;
+  f32x16 xs{};
+  if (mb >= 0 && mb < 3) {
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) sdot += __shfl_xor(sdot, off);
+    for (int vt = 0; vt < VT; ++vt)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+          xs = mma(tile_tr8<T>(Vnt + vt * TE, 32 * s2, 32 * xjb, jj, lane),
+                   tile_ldp8<T>(Ot + vt * TE, 32 * xib + cl, 32 * s2, jj, hh), xs);
+  }
+  vm_wait_barrier<0>();  // Aqk landed; the state tiles are no longer read
+
+  // 2. Mq [i][j] tile and Z^T; wave 7 the zero block (i < 32 <= j); waves 0-3 dW out
+  if (mb >= 0) {
+    const int xi = 32 * xib + cl;  // this lane's i
+    const float Gi = Gs[xi];
+    const bool iv = t0 + xi < Tn;
+    f32x16 mq;
+    float rs = 0.f;
+    const char* arow = reinterpret_cast<const char*>(At);
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      const int j0 = 32 * xjb + 8 * I + 4 * hh;
+      const v4_t<T> a4 = mb < 3 ? *reinterpret_cast<const v4_t<T>*>(arow + tile_off(xi, j0)) : v4_t<T>{};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int j = j0 + e;
+        const float x = mb < 3 ? xs[4 * I + e] : 0.f;
+        const float z = x * (float)a4[e];
+        rs += z;
+        Zt[j * 64 + xi] = z;
+        float mv = 0.f;
+        if (mb < 3 && iv && j <= xi) mv = a.scale * x * (GATED ? __expf(Gi - Gs[j]) : 1.f);
+        mq[4 * I + e] = mv;
+      }
+      *reinterpret_cast<v4_t<T>*>(reinterpret_cast<char*>(Mqt) + tile_off(xi, j0)) =
+          to4<T>(mq[4 * I], mq[4 * I + 1], mq[4 * I + 2], mq[4 * I + 3]);
+    }
+    rs += __shfl_xor(rs, 32);
+    if (hh == 0 && mb < 3) red_rs[xjb][xi] = rs;
+  }
+  u32x4* stage = reinterpret_cast<u32x4*>(St + 3 * TE) + 256 * w;
+  if (w < 4 && active)
+    store_rows_staged<T>(dwk[0], dwk[1], stage, (T*)(a.ws + L.dW) + ((size_t)bh * Tp + t0 + 32 * lb) * DK + 64 * dp,
+                         DK, lane);
+  __syncthreads();
+
+  // 3. dq += Mq K (rows i), dKs += Mq^T Q (rows j)
+  if (active) {
+    if (w < 4) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj)
+            acc[m] = mma(tile_tr8<T>(Kt + dp * TE, 32 * jb, 32 * m, jj, lane), tile_ldp8<T>(Mqt, r, 32 * jb, jj, hh),
+                         acc[m]);
+      store_rows_staged<T>(acc[0], acc[1], stage, (T*)a.dq + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DK + 64 * dp,
+                           qks, lane, Tn - (t0 + 32 * lb));
+    } else {
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj)
+            acc[m] = mma(tile_tr8<T>(Qt + dp * TE, 32 * ib, 32 * m, jj, lane),
+                         tile_tr8<T>(Mqt, 32 * ib, 32 * lb, jj, lane), acc[m]);
+      float* dkp = reinterpret_cast<float*>(a.ws + L.dKp) + ((size_t)bh * Tp + t0 + r) * DK + 64 * dp;
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int I = 0; I < 4; ++I)
+          *reinterpret_cast<f32x4*>(dkp + 32 * m + 8 * I + 4 * hh) =
+              f32x4{acc[m][4 * I], acc[m][4 * I + 1], acc[m][4 * I + 2], acc[m][4 * I + 3]};
+    }
+  }
+  part += __shfl_xor(part, 32);
+  if (active && hh == 0) {
+    if (w < 4) red_gi[dp][r] = part;
+    else red_kd[dp][r] = part;
+  }
   if (lane == 0) red_s[w] = sdot;
   __syncthreads();
-
-  const int i = 32 * ib + cl;  // this lane's chunk row (as query i and as key j)
-  const int ti = t0 + i;
-  const bool valid = ti < Tn;
-  const float Gi = Gs[i];
-  v8_t<T> ydo[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) ydo[s] = valid ? ld8<T>(dob + (int64_t)ti * os + 16 * s + 8 * hh) : zero8<T>();
-
-  // (A) dQ_inter = scale e^G dO S^T, dW = -dVn S^T   (lane column i)
-  float gi_part = 0.f, kd_part = 0.f;
-  const float eG = GATED ? __expf(Gi) : 1.f;
-  const float eGam = GATED ? __expf(Gs[63] - Gi) : 1.f;
-  T* dWg = (T*)(a.ws + L.dW) + ((size_t)bh * Tp + t0 + i) * DK;
-  float* dKg = reinterpret_cast<float*>(a.ws + L.dKp) + ((size_t)bh * Tp + t0 + i) * DK;
-  T* dqg = (T*)a.dq + (((size_t)b * Tn + ti) * H + h) * DK;
-  f32x16 dq[NDW], dks[NDW];
-#pragma unroll
-  for (int m = 0; m < NDW; ++m) {
-    const int dt = dhalf * NDW + m;
-    f32x16 acc{}, dw{};
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const v8_t<T> xs = ld8<T>(Sx + (32 * dt + cl) * PV + 16 * s + 8 * hh);
-      acc = mma(xs, ydo[s], acc);
-      dw = mma(xs, ld8<T>(Rx + i * PV + 16 * s + 8 * hh), dw);
-    }
-    acc *= a.scale * eG;
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      const int d = 32 * dt + 8 * I + 4 * hh;
-      const v4_t<T> q4 = valid ? ld4<T>(qb + (int64_t)ti * qks + d) : v4_t<T>{};
-#pragma unroll
-      for (int r = 0; r < 4; ++r) gi_part += (float)q4[r] * acc[4 * I + r];
-      st4<T>(dWg + d, to4<T>(-dw[4 * I], -dw[4 * I + 1], -dw[4 * I + 2], -dw[4 * I + 3]));
-    }
-    dq[m] = acc;
-  }
-  __syncthreads();
-
-  // phase B tiles
-#pragma unroll
-  for (int r0 = 0; r0 < DV; r0 += 64) {
-    load_tile64x<T, T, DK, 1, PV, false, true>(dhg + (size_t)r0 * DK, 0, 64, DK, nullptr, Sx + r0, tid, nullptr);
-    load_tile64x<T, T, 64, 1, PV, false, true>(vng + (size_t)r0 * 64, 0, 64, 64, nullptr, Rx + r0, tid, nullptr);
-  }
-  __syncthreads();
-
-  // (B) dK_state = e^(gamma-G_j) Vn dS'^T   (lane column j = i)
-#pragma unroll
-  for (int m = 0; m < NDW; ++m) {
-    const int dt = dhalf * NDW + m;
-    f32x16 acc{};
-#pragma unroll
-    for (int s = 0; s < NS; ++s)
-      acc = mma(ld8<T>(Sx + (32 * dt + cl) * PV + 16 * s + 8 * hh), ld8<T>(Rx + i * PV + 16 * s + 8 * hh), acc);
-    acc *= eGam;
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      const int d = 32 * dt + 8 * I + 4 * hh;
-      const v4_t<T> k4 = valid ? ld4<T>(kb + (int64_t)ti * qks + d) : v4_t<T>{};
-#pragma unroll
-      for (int r = 0; r < 4; ++r) kd_part += (float)k4[r] * acc[4 * I + r];
-    }
-    dks[m] = acc;
-  }
-
-  // Mq (lane column i, rows j) and its transpose MqT (lane column j, rows i).
-  f32x16 Mq[2], MqT[2];
-  float rowsum = 0.f, colsum = 0.f;
-#pragma unroll
-  for (int jt = 0; jt < 2; ++jt) {
-    f32x16 dm{}, dmt{};
-    const int rr0 = 32 * jt + cl;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      dm = mma(ld8<T>(Rx + rr0 * PV + 16 * s + 8 * hh), ydo[s], dm);
-      dmt = mma(t0 + rr0 < Tn ? ld8<T>(dob + (int64_t)(t0 + rr0) * os + 16 * s + 8 * hh) : zero8<T>(),
-                ld8<T>(Rx + i * PV + 16 * s + 8 * hh), dmt);
-    }
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      const int r0 = 32 * jt + 8 * I + 4 * hh;
-      const v4_t<T> aq4 = ld4<T>(aq + i * 64 + r0);  // Aqk[i][r0 + r]
-      v4_t<T> aqt4;                                  // Aqk[r0 + r][i]
-#pragma unroll
-      for (int r = 0; r < 4; ++r) aqt4[r] = aq[(r0 + r) * 64 + i];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int rr = r0 + r;
-        const float x = dm[4 * I + r], y = dmt[4 * I + r];
-        rowsum += x * (float)aq4[r];
-        colsum += y * (float)aqt4[r];
-        float fm = a.scale, ft = a.scale;
-        if constexpr (GATED) {
-          fm *= __expf(Gi - Gs[rr]);
-          ft *= __expf(Gs[rr] - Gi);
-        }
-        Mq[jt][4 * I + r] = rr <= i ? x * fm : 0.f;
-        MqT[jt][4 * I + r] = rr >= i ? y * ft : 0.f;
-      }
-    }
-  }
-  rowsum += __shfl_xor(rowsum, 32);
-  colsum += __shfl_xor(colsum, 32);
-  __syncthreads();
-
-  // phase C tiles: K^T, Q^T
-  load_tile64x<T, T, DK, 1, PX, false, true>(kb, t0, Tn, qks, nullptr, KT, tid, nullptr);
-  load_tile64x<T, T, DK, 1, PX, false, true>(qb, t0, Tn, qks, nullptr, QT, tid, nullptr);
-  __syncthreads();
-
-  // (C) intra terms: dQ += Mq K, dK += Mq^T Q
-#pragma unroll
-  for (int m = 0; m < NDW; ++m) {
-    const int dt = dhalf * NDW + m;
-#pragma unroll
-    for (int jt = 0; jt < 2; ++jt)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        dq[m] = mma(ld_tr_op<T>(KT + (32 * dt + cl) * PX + 32 * jt, j, hh), c_to_b<T>(Mq[jt], j), dq[m]);
-        dks[m] = mma(ld_tr_op<T>(QT + (32 * dt + cl) * PX + 32 * jt, j, hh), c_to_b<T>(MqT[jt], j), dks[m]);
-      }
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      const int d = 32 * dt + 8 * I + 4 * hh;
-      if (valid)
-        st4<T>(dqg + d, to4<T>(dq[m][4 * I], dq[m][4 * I + 1], dq[m][4 * I + 2], dq[m][4 * I + 3]));
-      *reinterpret_cast<float4*>(dKg + d) =
-          make_float4(dks[m][4 * I], dks[m][4 * I + 1], dks[m][4 * I + 2], dks[m][4 * I + 3]);
-    }
-  }
-  gi_part += __shfl_xor(gi_part, 32);
-  kd_part += __shfl_xor(kd_part, 32);
-  if (hh == 0) {
-    red_gi[dhalf][i] = gi_part;
-    red_kd[dhalf][i] = kd_part;
-    if (dhalf == 0) red_rc[i] = rowsum - colsum;
-  }
-  __syncthreads();
   if (tid < 64) {
+    float cs = 0.f;  // column term: sum_j Z[j][i]
+#pragma unroll
+    for (int q4 = 0; q4 < 16; ++q4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(Zt + tid * 64 + 4 * q4);
+      cs += (v[0] + v[1]) + (v[2] + v[3]);
+    }
     const float kd = red_kd[0][tid] + red_kd[1][tid];
-    float dG = red_gi[0][tid] + red_gi[1][tid] - kd + red_rc[tid];
+    float dG = red_gi[0][tid] + red_gi[1][tid] - kd + (red_rs[0][tid] + red_rs[1][tid]) - cs;
     // d gamma = sum_j k_j . dKs_j + e^gamma <S, dS'>, added at row 63
     float kds = kd;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) kds += __shfl_xor(kds, off);
     if (tid == 63) {
-      const float st = red_s[0] + red_s[1] + red_s[2] + red_s[3];
-      dG += kds + (GATED ? __expf(Gs[63]) : 1.f) * st;
+      float st = 0.f;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) st += red_s[q];
+      dG += kds + (GATED ? __expf(gam) : 1.f) * st;
     }
     reinterpret_cast<float*>(a.ws + L.dGp)[(size_t)bh * Tp + t0 + tid] = dG;
   }
@@ -768,7 +821,7 @@ hipError_t launch_delta_bwd(const DeltaArgs& a, hipStream_t stream) {
   delta_state_bwd_kernel<T, DK, DV, GATED><<<dim3(BH), dim3(64 * (DV / 32)), 0, stream>>>(a, L);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  delta_bwd_chunk_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);
+  delta_bwd_chunk_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(512), 0, stream>>>(a, L);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   delta_wy_bwd_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);
