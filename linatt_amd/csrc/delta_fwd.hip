@@ -564,10 +564,16 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_fwd_kernel(DeltaAr
 // ---------------------------------------------------------------------------
 // Kernel 3: output, parallel over (b, h, chunk):
 //   o = scale e^G (Q h_c) + Aqk v_new.
-// Wave w: rows 32 (w & 1) + lane (lane column i), value half w >> 1.
+// h_c^T and v_new^T tiles by one up-front copy; q and Aqk rows straight to
+// registers.  Wave w: rows 32 (w & 1) + lane (lane column i), value columns
+// 64 (w >> 1) ..; o leaves as whole 16-byte rows.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
-__global__ __launch_bounds__(256) void delta_out_kernel(DeltaArgs a, DeltaLayout L) {
+__global__ __launch_bounds__(256, 2) void delta_out_kernel(DeltaArgs a, DeltaLayout L) {
+  constexpr int KT = DK / 64, VT = DV / 64, TE = 64 * 64;
+  __shared__ __attribute__((aligned(16))) T Ht[VT * KT * TE];  // h^T [v][d], tile vt * KT + kt
+  __shared__ __attribute__((aligned(16))) T Vt[VT * TE];       // v_new^T [v][j]
+  __shared__ __attribute__((aligned(16))) u32x4 Stg[4 * 256];  // store staging, 4 KiB per wave
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
   const int Tn = a.T, H = a.H, NT = a.NT;
@@ -576,13 +582,25 @@ __global__ __launch_bounds__(256) void delta_out_kernel(DeltaArgs a, DeltaLayout
   const int t0 = c * kChunk;
   const size_t Tp = (size_t)NT * kChunk;
   const size_t ci = (size_t)bh * NT + c;
-  const int i = 32 * (w & 1) + cl, ti = t0 + i;
+  const int lb = w & 1, vh = w >> 1;
+  const int i = 32 * lb + cl, ti = t0 + i;
   const bool valid = ti < Tn;
 
-  const T* qrow = (const T*)a.q + (((size_t)b * Tn + ti) * H + h) * DK;
-  const T* arow = (const T*)(a.ctx + L.Aqk) + ci * 4096 + i * 64;
   const T* hg = (const T*)(a.ctx + L.hT) + ci * DV * DK;
   const T* vg = (const T*)(a.ctx + L.VnT) + ci * DV * 64;
+#pragma unroll
+  for (int o = 0; o < 2; ++o) {
+    const int op = 2 * w + o;
+#pragma unroll
+    for (int vt = 0; vt < VT; ++vt) {
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt)
+        dma_tile64<T>(hg + (size_t)64 * vt * DK + 64 * kt, DK, 0, 64, Ht + (vt * KT + kt) * TE, op, lane);
+      dma_tile64<T>(vg + (size_t)64 * vt * 64, 64, 0, 64, Vt + vt * TE, op, lane);
+    }
+  }
+  const T* qrow = (const T*)a.q + (((size_t)b * Tn + ti) * H + h) * DK;
+  const T* arow = (const T*)(a.ctx + L.Aqk) + ci * 4096 + i * 64;
   v8_t<T> yq[DK / 16], ya[4];
 #pragma unroll
   for (int s = 0; s < DK / 16; ++s) yq[s] = valid ? ld8<T>(qrow + 16 * s + 8 * hh) : zero8<T>();
@@ -590,23 +608,25 @@ __global__ __launch_bounds__(256) void delta_out_kernel(DeltaArgs a, DeltaLayout
   for (int s = 0; s < 4; ++s) ya[s] = ld8<T>(arow + 16 * s + 8 * hh);
   float f = a.scale;
   if constexpr (GATED) f *= __expf(reinterpret_cast<const float*>(a.ctx + L.Gc)[(size_t)bh * Tp + t0 + i]);
-  T* orow = (T*)a.o + (((size_t)b * Tn + ti) * H + h) * DV;
+  vm_wait_barrier<0>();
+
+  if (vh < VT) {
+    f32x16 x[2];
 #pragma unroll
-  for (int m = 0; m < DV / 64; ++m) {
-    const int vt = (w >> 1) * (DV / 64) + m;
-    f32x16 acc{};
+    for (int m = 0; m < 2; ++m) {
+      // D[v][i], v = 64 vh + 32 m + ..: h^T rows v (k = d) against q row i
+      const int vr = 32 * m + cl;
+      f32x16 acc{};
 #pragma unroll
-    for (int s = 0; s < DK / 16; ++s)
-      acc = mma(ld8<T>(hg + (32 * vt + cl) * DK + 16 * s + 8 * hh), yq[s], acc);
-    acc *= f;
+      for (int s = 0; s < DK / 16; ++s)
+        acc = mma(tile_ld8<T>(Ht + (vh * KT + s / 4) * TE, vr, 16 * (s % 4) + 8 * hh), yq[s], acc);
+      acc *= f;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) acc = mma(ld8<T>(vg + (32 * vt + cl) * 64 + 16 * s + 8 * hh), ya[s], acc);
-    if (valid) {
-#pragma unroll
-      for (int I = 0; I < 4; ++I)
-        st4<T>(orow + 32 * vt + 8 * I + 4 * hh,
-               to4<T>(acc[4 * I], acc[4 * I + 1], acc[4 * I + 2], acc[4 * I + 3]));
+      for (int s = 0; s < 4; ++s) acc = mma(tile_ld8<T>(Vt + vh * TE, vr, 16 * s + 8 * hh), ya[s], acc);
+      x[m] = acc;
     }
+    store_rows_staged<T>(x[0], x[1], Stg + 256 * w, (T*)a.o + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DV + 64 * vh,
+                         (int64_t)H * DV, lane, Tn - (t0 + 32 * lb));
   }
 }
 
