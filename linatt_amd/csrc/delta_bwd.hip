@@ -66,6 +66,17 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_bwd_kernel(DeltaAr
   auto ot = [&](T* sl, int i) { return sl + (3 * KT + 1 + i) * TE; };  // dO columns 64 i..
   auto gs = [&](T* sl) { return reinterpret_cast<float*>(sl + NTILE * TE); };
 
+  // per-lane byte offsets of this wave's copy ops (full chunks); the last
+  // chunk (rows past T clamped) takes the general path
+  unsigned ok[OPW], ow[OPW], oq[OPW], oo[OPW];
+#pragma unroll
+  for (int o = 0; o < OPW; ++o) {
+    const int op = OPW * w + o;
+    ok[o] = tile_lane_off(op, lane, H * DK * (int)sizeof(T));
+    ow[o] = tile_lane_off(op, lane, 64 * (int)sizeof(T));
+    oq[o] = tile_lane_off(op, lane, DK * (int)sizeof(T));
+    oo[o] = tile_lane_off(op, lane, H * DV * (int)sizeof(T));
+  }
   auto issue = [&](int c) __attribute__((always_inline)) {
     T* sl = Sh + (c & 1) * SLOT;
     const int t0 = c * kChunk;
@@ -73,18 +84,36 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_bwd_kernel(DeltaAr
     const T* wtg = (const T*)(a.ctx + L.WT) + ci * DK * 64;
     const T* qgg = (const T*)(a.ctx + L.Qg) + ci * 64 * DK;
     const T* atg = (const T*)(a.ctx + L.Aqk) + ci * 4096;
+    if (t0 + 64 > Tn) {
 #pragma unroll
-    for (int o = 0; o < OPW; ++o) {
-      const int op = OPW * w + o;
+      for (int o = 0; o < OPW; ++o) {
+        const int op = OPW * w + o;
 #pragma unroll
-      for (int i = 0; i < KT; ++i) {
-        dma_tile64<T>(kb + 64 * i, (int64_t)H * DK, t0, Tn, kt(sl, i), op, lane);
-        dma_tile64<T>(wtg + (size_t)64 * i * 64, 64, 0, 64, wt(sl, i), op, lane);
-        dma_tile64<T>(qgg + 64 * i, DK, 0, 64, qt(sl, i), op, lane);
+        for (int i = 0; i < KT; ++i) {
+          dma_tile64<T>(kb + 64 * i, (int64_t)H * DK, t0, Tn, kt(sl, i), op, lane);
+          dma_tile64<T>(wtg + (size_t)64 * i * 64, 64, 0, 64, wt(sl, i), op, lane);
+          dma_tile64<T>(qgg + 64 * i, DK, 0, 64, qt(sl, i), op, lane);
+        }
+        dma_tile64<T>(atg, 64, 0, 64, at(sl), op, lane);
+#pragma unroll
+        for (int i = 0; i < VT; ++i) dma_tile64<T>(dob + 64 * i, (int64_t)H * DV, t0, Tn, ot(sl, i), op, lane);
       }
-      dma_tile64<T>(atg, 64, 0, 64, at(sl), op, lane);
+    } else {
+      const T* kr = kb + (size_t)t0 * H * DK;
+      const T* dr = dob + (size_t)t0 * H * DV;
 #pragma unroll
-      for (int i = 0; i < VT; ++i) dma_tile64<T>(dob + 64 * i, (int64_t)H * DV, t0, Tn, ot(sl, i), op, lane);
+      for (int o = 0; o < OPW; ++o) {
+        const int op = OPW * w + o;
+#pragma unroll
+        for (int i = 0; i < KT; ++i) {
+          dma16s(kr + 64 * i, ok[o], reinterpret_cast<char*>(kt(sl, i)) + 1024 * op);
+          dma16s(wtg + (size_t)64 * i * 64, ow[o], reinterpret_cast<char*>(wt(sl, i)) + 1024 * op);
+          dma16s(qgg + 64 * i, oq[o], reinterpret_cast<char*>(qt(sl, i)) + 1024 * op);
+        }
+        dma16s(atg, ow[o], reinterpret_cast<char*>(at(sl)) + 1024 * op);
+#pragma unroll
+        for (int i = 0; i < VT; ++i) dma16s(dr + 64 * i, oo[o], reinterpret_cast<char*>(ot(sl, i)) + 1024 * op);
+      }
     }
     if (GATED && w == 0 && lane < 16) dma16(Gc + t0 + 4 * lane, gs(sl));
   };
