@@ -37,26 +37,30 @@ namespace linatt {
 // through LDS staging in the wave's own columns of the dO tiles.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
-__global__ __launch_bounds__(64 * (DV / 32)) void delta_state_bwd_kernel(DeltaArgs a, DeltaLayout L) {
-  constexpr int NDT = DK / 32, NW = DV / 32;
-  constexpr int KT = DK / 64, VT = DV / 64;      // 64 x 64 tiles per row block
+__global__ __launch_bounds__(64 * (DV / 32) / state_split<DV>()) void delta_state_bwd_kernel(DeltaArgs a,
+                                                                                             DeltaLayout L) {
+  constexpr int SPLIT = state_split<DV>();
+  constexpr int NDT = DK / 32, NW = DV / 32 / SPLIT;  // waves of this workgroup
+  constexpr int KT = DK / 64, VT = NW / 2;        // 64 x 64 tiles per row block (dO: this workgroup's)
   constexpr int TE = 64 * 64;                     // elements per tile
   constexpr int OPW = 8 / NW;                     // 1 KiB copies per wave per tile
   constexpr int NTILE = 3 * KT + 1 + VT;          // K, W^T, Qg, Aqk, dO
   constexpr int SLOT = NTILE * TE + 64 * 4 / (int)sizeof(T);  // + G of the chunk (f32)
-  static_assert(OPW * NW == 8, "tile split");
+  static_assert(OPW * NW == 8 && VT >= 1, "tile split");
   __shared__ __attribute__((aligned(16))) T Sh[2 * SLOT];
 
   const int lane = threadIdx.x & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
   const int Tn = a.T, H = a.H, NT = a.NT;
-  const int bh = blockIdx.x;
+  const int BH = a.B * H;
+  const int bh = blockIdx.x % BH, part = blockIdx.x / BH;
   const int b = bh / H, h = bh % H;
-  const int v = 32 * w + cl;
+  const int gw = part * NW + w;  // this wave's 32-column block of the head
+  const int v = 32 * gw + cl;
   const size_t Tp = (size_t)NT * kChunk;
 
   const T* kb = (const T*)a.k + ((size_t)b * Tn * H + h) * DK;
-  const T* dob = (const T*)a.dout + ((size_t)b * Tn * H + h) * DV;
+  const T* dob = (const T*)a.dout + ((size_t)b * Tn * H + h) * DV + 64 * VT * part;  // this workgroup's columns
   const float* Gc = reinterpret_cast<const float*>(a.ctx + L.Gc) + (size_t)bh * Tp;
 
   auto kt = [&](T* sl, int i) { return sl + i * TE; };                 // K tile i (key dims 64 i..)
@@ -237,11 +241,11 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_bwd_kernel(DeltaAr
         const int tr = s >> 2, q = s & 3;
         return reinterpret_cast<u32x4*>(ob + tr * 128 + (tile_slot(tr, 4 * (w & 1) + q) << 4));
       };
-      T* drows = (T*)(a.ws + L.dhT) + (ci * DV + 32 * w) * DK;
+      T* drows = (T*)(a.ws + L.dhT) + (ci * DV + 32 * gw) * DK;
 #pragma unroll
       for (int blk = 0; blk < NDT / 2; ++blk)
         store_rows_via<T>(dS[2 * blk], dS[2 * blk + 1], slot, drows + 64 * blk, DK, lane);
-      store_rows_via<T>(dVn[0], dVn[1], slot, (T*)(a.ws + L.dVnT) + (ci * DV + 32 * w) * 64, 64, lane);
+      store_rows_via<T>(dVn[0], dVn[1], slot, (T*)(a.ws + L.dVnT) + (ci * DV + 32 * gw) * 64, 64, lane);
     }
 
     // dS <- e^gamma dS' + Z - W^T dVn
@@ -847,7 +851,8 @@ template <typename T, int DK, int DV, bool GATED>
 hipError_t launch_delta_bwd(const DeltaArgs& a, hipStream_t stream) {
   const DeltaLayout L = delta_layout(a.B, a.T, a.H, DK, DV, sizeof(T));
   const int BH = a.B * a.H;
-  delta_state_bwd_kernel<T, DK, DV, GATED><<<dim3(BH), dim3(64 * (DV / 32)), 0, stream>>>(a, L);
+  delta_state_bwd_kernel<T, DK, DV, GATED><<<dim3(BH * state_split<DV>()), dim3(64 * (DV / 32) / state_split<DV>()), 0,
+                                             stream>>>(a, L);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   delta_bwd_chunk_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(512), 0, stream>>>(a, L);

@@ -381,9 +381,10 @@ __device__ __forceinline__ void dma_tile_1k(const u32x4* g, u32x4* lds, int op, 
 }
 
 template <typename T, int DK, int DV, bool GATED>
-__global__ __launch_bounds__(64 * (DV / 32)) void delta_state_fwd_kernel(DeltaArgs a, DeltaLayout L,
-                                                                       const float* __restrict__ gcum) {
-  constexpr int NDT = DK / 32, NW = DV / 32;
+__global__ __launch_bounds__(64 * (DV / 32) / state_split<DV>()) void delta_state_fwd_kernel(
+    DeltaArgs a, DeltaLayout L, const float* __restrict__ gcum) {
+  constexpr int SPLIT = state_split<DV>();
+  constexpr int NDT = DK / 32, NW = DV / 32 / SPLIT;      // waves of this workgroup
   constexpr int WT16 = 64 * DK * (int)sizeof(T) / 16;   // 16-byte chunks per W (= Kd^T) tile
   constexpr int UT16 = 32 * 64 * (int)sizeof(T) / 16;   // per wave's U^T rows
   constexpr int WCPR = DK * (int)sizeof(T) / 16;         // chunks per W row
@@ -397,8 +398,10 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_fwd_kernel(DeltaAr
   const int lane = threadIdx.x & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
   const int NT = a.NT;
-  const int bh = blockIdx.x;
-  const int v = 32 * w + cl;
+  const int BH = a.B * a.H;
+  const int bh = blockIdx.x % BH;
+  const int gw = (blockIdx.x / BH) * NW + w;  // this wave's 32-column block of the head
+  const int v = 32 * gw + cl;
   const size_t Tp = (size_t)NT * kChunk;
 
   // gcum = the Gc context buffer, passed on its own as __restrict__ so the
@@ -408,7 +411,7 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_fwd_kernel(DeltaAr
   // chunk c sits at + c * (bytes per chunk)
   const char* Wg = a.ctx + L.W + (size_t)bh * NT * WT16 * 16;
   const char* Kg = a.ctx + L.KdT + (size_t)bh * NT * WT16 * 16;
-  const char* Ug = a.ctx + L.UT + ((size_t)bh * NT * NW + w) * UT16 * 16;
+  const char* Ug = a.ctx + L.UT + ((size_t)bh * NT * NW * SPLIT + gw) * UT16 * 16;
   // per-lane byte offsets of the copies: 1 KiB copy op covers tile chunks
   // [64 op, 64 op + 64); slot lane of row r holds global chunk swz(r, lane)
   unsigned wo[WOPS], ko[WOPS], uo[UOPS];
@@ -432,7 +435,7 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_fwd_kernel(DeltaAr
     }
 #pragma unroll
     for (int i = 0; i < UOPS; ++i)
-      dma16s(Ug + (size_t)c * NW * UT16 * 16, uo[i], sl + 2 * WT16 + w * UT16 + 64 * i);
+      dma16s(Ug + (size_t)c * NW * SPLIT * UT16 * 16, uo[i], sl + 2 * WT16 + w * UT16 + 64 * i);
   };
 
   // v_new^T and h^T rows of this head (rows [v][.] per chunk, this wave's 32)
@@ -519,12 +522,12 @@ __global__ __launch_bounds__(64 * (DV / 32)) void delta_state_fwd_kernel(DeltaAr
     // this wave's U^T area of the slot, which the wave alone reads and has
     // finished with
     u32x4* stage = const_cast<u32x4*>(Us);
-    store_rows_buf<T>(Vn[0], Vn[1], stage, vn_rs, (int)(((size_t)c * DV + 32 * w) * 64 * sizeof(T)),
+    store_rows_buf<T>(Vn[0], Vn[1], stage, vn_rs, (int)(((size_t)c * DV + 32 * gw) * 64 * sizeof(T)),
                       64 * (int)sizeof(T), lane);
 #pragma unroll
     for (int blk = 0; blk < NDT / 2; ++blk)
       store_rows_buf<T>(S[2 * blk], S[2 * blk + 1], stage, h_rs,
-                        (int)((((size_t)c * DV + 32 * w) * DK + 64 * blk) * sizeof(T)), DK * (int)sizeof(T),
+                        (int)((((size_t)c * DV + 32 * gw) * DK + 64 * blk) * sizeof(T)), DK * (int)sizeof(T),
                         lane);
 
     // S <- e^gamma S + Kd^T v_new  (Kd^T rows 32 dt + cl, chunk rows in operand order)
@@ -637,7 +640,8 @@ hipError_t launch_delta_fwd(const DeltaArgs& a, hipStream_t stream) {
   delta_prep_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  delta_state_fwd_kernel<T, DK, DV, GATED><<<dim3(BH), dim3(64 * (DV / 32)), 0, stream>>>(
+  delta_state_fwd_kernel<T, DK, DV, GATED><<<dim3(BH * state_split<DV>()), dim3(64 * (DV / 32) / state_split<DV>()), 0,
+                                             stream>>>(
       a, L, reinterpret_cast<const float*>(a.ctx + L.Gc));
   e = hipGetLastError();
   if (e != hipSuccess) return e;

@@ -44,6 +44,13 @@ struct DeltaLayout {
 
 DeltaLayout delta_layout(int B, int T, int H, int DK, int DV, int elt_bytes);
 
+// Workgroups per head of the two state passes: the value columns of a head
+// are split over this many workgroups (each on its own CU), so the copy and
+// store traffic of the serial chain spreads over that many CUs.  Measured at
+// K = V = 128: two (two waves each) beat one (four waves) and four (one).
+template <int DV>
+constexpr int state_split() { return DV / 32 >= 4 ? 2 : 1; }
+
 struct DeltaArgs {
   // inputs
   const void* q;
