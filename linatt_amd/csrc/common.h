@@ -168,6 +168,9 @@ __device__ __forceinline__ void dma_small(const void* src, void* lds_base, int n
 // wave complete in issue order, so with N = the number of loads issued after
 // some load X, X has landed once vmcnt <= N, whatever stores are also in
 // flight (they only add to the count).
+// s_barrier as a compiler-opaque step (memory clobber), without a wait.
+__device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 template <int N>
 __device__ __forceinline__ void vm_wait_barrier() {
   static_assert(N >= 0 && N <= 63, "vmcnt range");

@@ -37,16 +37,16 @@ namespace linatt {
 // through LDS staging in the wave's own columns of the dO tiles.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
-__global__ __launch_bounds__(64 * (DV / 32) / state_split<DV>()) void delta_state_bwd_kernel(DeltaArgs a,
-                                                                                             DeltaLayout L) {
+__global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_state_bwd_kernel(DeltaArgs a,
+                                                                                                DeltaLayout L) {
   constexpr int SPLIT = state_split<DV>();
-  constexpr int NDT = DK / 32, NW = DV / 32 / SPLIT;  // waves of this workgroup
+  constexpr int NDT = DK / 32, NW = DV / 32 / SPLIT;  // compute waves of this workgroup (+ one copy wave)
   constexpr int KT = DK / 64, VT = NW / 2;        // 64 x 64 tiles per row block (dO: this workgroup's)
   constexpr int TE = 64 * 64;                     // elements per tile
-  constexpr int OPW = 8 / NW;                     // 1 KiB copies per wave per tile
+  constexpr int OPW = 8;                          // 1 KiB copies per tile, all by the copy wave
   constexpr int NTILE = 3 * KT + 1 + VT;          // K, W^T, Qg, Aqk, dO
   constexpr int SLOT = NTILE * TE + 64 * 4 / (int)sizeof(T);  // + G of the chunk (f32)
-  static_assert(OPW * NW == 8 && VT >= 1, "tile split");
+  static_assert(VT >= 1, "tile split");
   __shared__ __attribute__((aligned(16))) T Sh[2 * SLOT];
 
   const int lane = threadIdx.x & 63, w = wave_id();
@@ -70,17 +70,10 @@ __global__ __launch_bounds__(64 * (DV / 32) / state_split<DV>()) void delta_stat
   auto ot = [&](T* sl, int i) { return sl + (3 * KT + 1 + i) * TE; };  // dO columns 64 i..
   auto gs = [&](T* sl) { return reinterpret_cast<float*>(sl + NTILE * TE); };
 
-  // per-lane byte offsets of this wave's copy ops (full chunks); the last
-  // chunk (rows past T clamped) takes the general path
-  unsigned ok[OPW], ow[OPW], oq[OPW], oo[OPW];
-#pragma unroll
-  for (int o = 0; o < OPW; ++o) {
-    const int op = OPW * w + o;
-    ok[o] = tile_lane_off(op, lane, H * DK * (int)sizeof(T));
-    ow[o] = tile_lane_off(op, lane, 64 * (int)sizeof(T));
-    oq[o] = tile_lane_off(op, lane, DK * (int)sizeof(T));
-    oo[o] = tile_lane_off(op, lane, H * DV * (int)sizeof(T));
-  }
+  // The copy wave (w == NW) issues every copy of the next chunk while the
+  // compute waves work on this one, so no compute wave stalls on copy
+  // issue.  Per-lane byte offsets of its copy ops (full chunks); the last
+  // chunk (rows past T clamped) takes the general path.
   auto issue = [&](int c) __attribute__((always_inline)) {
     T* sl = Sh + (c & 1) * SLOT;
     const int t0 = c * kChunk;
@@ -90,8 +83,7 @@ __global__ __launch_bounds__(64 * (DV / 32) / state_split<DV>()) void delta_stat
     const T* atg = (const T*)(a.ctx + L.Aqk) + ci * 4096;
     if (t0 + 64 > Tn) {
 #pragma unroll
-      for (int o = 0; o < OPW; ++o) {
-        const int op = OPW * w + o;
+      for (int op = 0; op < OPW; ++op) {
 #pragma unroll
         for (int i = 0; i < KT; ++i) {
           dma_tile64<T>(kb + 64 * i, (int64_t)H * DK, t0, Tn, kt(sl, i), op, lane);
@@ -106,21 +98,37 @@ __global__ __launch_bounds__(64 * (DV / 32) / state_split<DV>()) void delta_stat
       const T* kr = kb + (size_t)t0 * H * DK;
       const T* dr = dob + (size_t)t0 * H * DV;
 #pragma unroll
-      for (int o = 0; o < OPW; ++o) {
-        const int op = OPW * w + o;
+      for (int op = 0; op < 8; ++op) {
+        const unsigned ok = tile_lane_off(op, lane, H * DK * (int)sizeof(T));
+        const unsigned ow = tile_lane_off(op, lane, 64 * (int)sizeof(T));
+        const unsigned oq = tile_lane_off(op, lane, DK * (int)sizeof(T));
+        const unsigned oo = tile_lane_off(op, lane, H * DV * (int)sizeof(T));
 #pragma unroll
         for (int i = 0; i < KT; ++i) {
-          dma16s(kr + 64 * i, ok[o], reinterpret_cast<char*>(kt(sl, i)) + 1024 * op);
-          dma16s(wtg + (size_t)64 * i * 64, ow[o], reinterpret_cast<char*>(wt(sl, i)) + 1024 * op);
-          dma16s(qgg + 64 * i, oq[o], reinterpret_cast<char*>(qt(sl, i)) + 1024 * op);
+          dma16s(kr + 64 * i, ok, reinterpret_cast<char*>(kt(sl, i)) + 1024 * op);
+          dma16s(wtg + (size_t)64 * i * 64, ow, reinterpret_cast<char*>(wt(sl, i)) + 1024 * op);
+          dma16s(qgg + 64 * i, oq, reinterpret_cast<char*>(qt(sl, i)) + 1024 * op);
         }
-        dma16s(atg, ow[o], reinterpret_cast<char*>(at(sl)) + 1024 * op);
+        dma16s(atg, ow, reinterpret_cast<char*>(at(sl)) + 1024 * op);
 #pragma unroll
-        for (int i = 0; i < VT; ++i) dma16s(dr + 64 * i, oo[o], reinterpret_cast<char*>(ot(sl, i)) + 1024 * op);
+        for (int i = 0; i < VT; ++i) dma16s(dr + 64 * i, oo, reinterpret_cast<char*>(ot(sl, i)) + 1024 * op);
       }
     }
-    if (GATED && w == 0 && lane < 16) dma16(Gc + t0 + 4 * lane, gs(sl));
+    if (GATED && lane < 16) dma16(Gc + t0 + 4 * lane, gs(sl));
   };
+
+  if (w == NW) {
+    // copy wave: chunk c is complete (vmcnt 0) before it reaches the
+    // barrier that opens chunk c for the compute waves; the barrier also
+    // closes chunk c + 1, whose slot then takes chunk c - 1
+    issue(NT - 1);
+#pragma unroll 1
+    for (int c = NT - 1; c >= 0; --c) {
+      vm_wait_barrier<0>();
+      if (c > 0) issue(c - 1);
+    }
+    return;
+  }
 
   f32x16 dS[NDT];
 #pragma unroll
@@ -132,14 +140,12 @@ __global__ __launch_bounds__(64 * (DV / 32) / state_split<DV>()) void delta_stat
     }
 
   vm_drain();  // dh_T is in registers
-  issue(NT - 1);
 #pragma unroll 1
   for (int c = NT - 1; c >= 0; --c) {
     const int t0 = c * kChunk;
     const size_t ci = (size_t)bh * NT + c;
-    // chunk c landed for every wave; every wave is done with chunk c + 1
-    vm_wait_barrier<0>();
-    if (c > 0) issue(c - 1);
+    // chunk c landed (the copy wave waited for it); every wave is done with chunk c + 1
+    block_barrier();
     T* sl = Sh + (c & 1) * SLOT;
     const T* Os = ot(sl, w / 2);  // this wave's 64-column dO tile
     const int oc0 = 32 * (w & 1);
@@ -851,8 +857,8 @@ template <typename T, int DK, int DV, bool GATED>
 hipError_t launch_delta_bwd(const DeltaArgs& a, hipStream_t stream) {
   const DeltaLayout L = delta_layout(a.B, a.T, a.H, DK, DV, sizeof(T));
   const int BH = a.B * a.H;
-  delta_state_bwd_kernel<T, DK, DV, GATED><<<dim3(BH * state_split<DV>()), dim3(64 * (DV / 32) / state_split<DV>()), 0,
-                                             stream>>>(a, L);
+  delta_state_bwd_kernel<T, DK, DV, GATED><<<dim3(BH * state_split<DV>()), dim3(64 * (DV / 32 / state_split<DV>() + 1)),
+                                             0, stream>>>(a, L);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   delta_bwd_chunk_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(512), 0, stream>>>(a, L);
