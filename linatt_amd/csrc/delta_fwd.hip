@@ -381,18 +381,18 @@ __device__ __forceinline__ void dma_tile_1k(const u32x4* g, u32x4* lds, int op, 
 }
 
 template <typename T, int DK, int DV, bool GATED>
-__global__ __launch_bounds__(64 * (DV / 32) / state_split<DV>()) void delta_state_fwd_kernel(
+__global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_state_fwd_kernel(
     DeltaArgs a, DeltaLayout L, const float* __restrict__ gcum) {
   constexpr int SPLIT = state_split<DV>();
-  constexpr int NDT = DK / 32, NW = DV / 32 / SPLIT;      // waves of this workgroup
+  constexpr int NDT = DK / 32, NW = DV / 32 / SPLIT;      // compute waves of this workgroup (+ one copy wave)
   constexpr int WT16 = 64 * DK * (int)sizeof(T) / 16;   // 16-byte chunks per W (= Kd^T) tile
   constexpr int UT16 = 32 * 64 * (int)sizeof(T) / 16;   // per wave's U^T rows
   constexpr int WCPR = DK * (int)sizeof(T) / 16;         // chunks per W row
   constexpr int KCPR = 64 * (int)sizeof(T) / 16;         // chunks per Kd^T / U^T row
   constexpr int SLOT = 2 * WT16 + NW * UT16;             // W | Kd^T | U^T per chunk
-  constexpr int WOPS = WT16 / 64 / NW, UOPS = UT16 / 64;  // 1 KiB copies per wave
+  constexpr int WOPS = WT16 / 64, UOPS = NW * UT16 / 64;  // 1 KiB copies per chunk (copy wave)
   constexpr int DMA_PER_CHUNK = 2 * WOPS + UOPS;
-  static_assert(WOPS * 64 * NW == WT16 && UOPS * 64 == UT16, "tile split");
+  static_assert(WOPS * 64 == WT16 && UOPS * 64 == NW * UT16 && DMA_PER_CHUNK <= 63, "tile split");
   __shared__ __attribute__((aligned(16))) u32x4 Sh[3 * SLOT];
 
   const int lane = threadIdx.x & 63, w = wave_id();
@@ -407,36 +407,42 @@ __global__ __launch_bounds__(64 * (DV / 32) / state_split<DV>()) void delta_stat
   // gcum = the Gc context buffer, passed on its own as __restrict__ so the
   // per-chunk gate is a scalar load (no vector-memory wait in the chain)
   const float* Gc = gcum + (size_t)bh * Tp;
-  // wave-uniform byte bases of this head's W, Kd^T and (this wave's) U^T;
-  // chunk c sits at + c * (bytes per chunk)
-  const char* Wg = a.ctx + L.W + (size_t)bh * NT * WT16 * 16;
-  const char* Kg = a.ctx + L.KdT + (size_t)bh * NT * WT16 * 16;
-  const char* Ug = a.ctx + L.UT + ((size_t)bh * NT * NW * SPLIT + gw) * UT16 * 16;
-  // per-lane byte offsets of the copies: 1 KiB copy op covers tile chunks
-  // [64 op, 64 op + 64); slot lane of row r holds global chunk swz(r, lane)
-  unsigned wo[WOPS], ko[WOPS], uo[UOPS];
+  // The copy wave (w == NW) issues every copy, two chunks ahead, into a ring
+  // of three slots; the compute waves never stall on copy issue.
+  if (w == NW) {
+    // wave-uniform byte bases of this head's W, Kd^T and this workgroup's
+    // U^T rows; chunk c sits at + c * (bytes per chunk).  A 1 KiB copy op
+    // covers tile chunks [64 op, 64 op + 64); slot lane of row r holds
+    // global chunk swz(r, lane).
+    const char* Wg = a.ctx + L.W + (size_t)bh * NT * WT16 * 16;
+    const char* Kg = a.ctx + L.KdT + (size_t)bh * NT * WT16 * 16;
+    const char* Ug = a.ctx + L.UT + ((size_t)bh * NT * NW * SPLIT + (gw - w)) * UT16 * 16;
+    auto issue = [&](int c) __attribute__((always_inline)) {
+      u32x4* sl = Sh + (c % 3) * SLOT;
 #pragma unroll
-  for (int i = 0; i < WOPS; ++i) {
-    const int op = WOPS * w + i;
-    const int rw = (64 * op + lane) / WCPR, rk = (64 * op + lane) / KCPR;
-    wo[i] = 16u * swz_slot<WCPR>(rw, lane % WCPR);
-    ko[i] = 16u * swz_slot<KCPR>(rk, lane % KCPR);
-  }
+      for (int op = 0; op < WOPS; ++op) {
+        const int rw = (64 * op + lane) / WCPR, rk = (64 * op + lane) / KCPR;
+        dma16s(Wg + (size_t)c * WT16 * 16, 16u * swz_slot<WCPR>(rw, lane % WCPR), sl + 64 * op);
+        dma16s(Kg + (size_t)c * WT16 * 16, 16u * swz_slot<KCPR>(rk, lane % KCPR), sl + WT16 + 64 * op);
+      }
 #pragma unroll
-  for (int i = 0; i < UOPS; ++i) uo[i] = 16u * swz_slot<KCPR>((64 * i + lane) / KCPR, lane % KCPR);
-
-  // this wave's share of chunk c into ring slot SL (= c % 3)
-  auto issue = [&](auto SL, int c) __attribute__((always_inline)) {
-    u32x4* sl = Sh + decltype(SL)::value * SLOT;
-#pragma unroll
-    for (int i = 0; i < WOPS; ++i) {
-      dma16s(Wg + (size_t)c * WT16 * 16, wo[i], sl + 64 * (WOPS * w + i));
-      dma16s(Kg + (size_t)c * WT16 * 16, ko[i], sl + WT16 + 64 * (WOPS * w + i));
+      for (int op = 0; op < UOPS; ++op)
+        dma16s(Ug + (size_t)c * NW * SPLIT * UT16 * 16, 16u * swz_slot<KCPR>((64 * op + lane) / KCPR, lane % KCPR),
+               sl + 2 * WT16 + 64 * op);
+    };
+    issue(0);
+    if (NT > 1) issue(1);
+#pragma unroll 1
+    for (int c = 0; c < NT; ++c) {
+      // chunk c landed (only chunk c + 1's copies may remain in flight)
+      // before the barrier that opens it; the barrier also closes chunk
+      // c - 1, whose slot then takes chunk c + 2
+      if (c + 1 < NT) vm_wait_barrier<DMA_PER_CHUNK>();
+      else vm_wait_barrier<0>();
+      if (c + 2 < NT) issue(c + 2);
     }
-#pragma unroll
-    for (int i = 0; i < UOPS; ++i)
-      dma16s(Ug + (size_t)c * NW * SPLIT * UT16 * 16, uo[i], sl + 2 * WT16 + w * UT16 + 64 * i);
-  };
+    return;
+  }
 
   // v_new^T and h^T rows of this head (rows [v][.] per chunk, this wave's 32)
   const __amdgpu_buffer_rsrc_t vn_rs =
@@ -457,11 +463,9 @@ __global__ __launch_bounds__(64 * (DV / 32) / state_split<DV>()) void delta_stat
   // so every LDS address is a chunk-invariant register plus a constant
   auto step = [&](auto SL, int c) __attribute__((always_inline)) {
     constexpr int sl = decltype(SL)::value;
-    // chunk c landed for every wave (only chunk c + 1's copies may remain in
-    // flight), and every wave is done with chunk c - 1, whose slot is refilled
-    if (c + 1 < NT) vm_wait_barrier<DMA_PER_CHUNK>();
-    else vm_wait_barrier<0>();
-    if (c + 2 < NT) issue(IntC<(sl + 2) % 3>{}, c + 2);
+    // chunk c landed (the copy wave waited for it); every wave is done
+    // with chunk c - 1, whose slot the copy wave refills
+    block_barrier();
     const u32x4* Ws = Sh + sl * SLOT;
     const u32x4* Ks = Ws + WT16;
     const u32x4* Us = Ws + 2 * WT16 + w * UT16;
@@ -544,8 +548,6 @@ __global__ __launch_bounds__(64 * (DV / 32) / state_split<DV>()) void delta_stat
   };
 
   vm_drain();  // h0 is in registers
-  issue(IntC<0>{}, 0);
-  if (NT > 1) issue(IntC<1>{}, 1);
 #pragma unroll 1
   for (int c = 0; c < NT; c += 3) {
     step(IntC<0>{}, c);
@@ -640,8 +642,8 @@ hipError_t launch_delta_fwd(const DeltaArgs& a, hipStream_t stream) {
   delta_prep_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  delta_state_fwd_kernel<T, DK, DV, GATED><<<dim3(BH * state_split<DV>()), dim3(64 * (DV / 32) / state_split<DV>()), 0,
-                                             stream>>>(
+  delta_state_fwd_kernel<T, DK, DV, GATED><<<dim3(BH * state_split<DV>()), dim3(64 * (DV / 32 / state_split<DV>() + 1)),
+                                             0, stream>>>(
       a, L, reinterpret_cast<const float*>(a.ctx + L.Gc));
   e = hipGetLastError();
   if (e != hipSuccess) return e;
