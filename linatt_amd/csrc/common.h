@@ -455,6 +455,37 @@ __device__ __forceinline__ int swz_slot(int row, int ch) {
 // (row-major 32 x 8, XOR-swizzled by row) to LDS addresses owned by the
 // calling wave.  OPORD stores each 32-column block in operand order
 // (column e at 32 b + opord32(e)).
+// The LDS half of store_rows_via alone: the block into 256 staging slots.
+template <typename T, bool OPORD = false>
+__device__ __forceinline__ void stage_rows(const f32x16& x0, const f32x16& x1, u32x4* stage, int lane) {
+  const int cl = lane & 31, hh = lane >> 5;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const f32x16& x = b ? x1 : x0;
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      const int ch = OPORD ? 4 * b + 2 * (I >> 1) + hh : 4 * b + I;
+      const int bo = OPORD ? 8 * (I & 1) : 8 * hh;
+      *reinterpret_cast<v4_t<T>*>(reinterpret_cast<char*>(stage + swz_slot<8>(cl, ch)) + bo) =
+          to4<T>(x[4 * I], x[4 * I + 1], x[4 * I + 2], x[4 * I + 3]);
+    }
+  }
+}
+
+// The global half: a staged block's 32 rows to g + row * ld (g wave-uniform,
+// rows >= nvalid dropped), by any wave of the workgroup.
+template <typename T>
+__device__ __forceinline__ void flush_rows(const u32x4* stage, T* g, int64_t ld, int lane, int nvalid = 32) {
+  const int nv = nvalid < 0 ? 0 : (nvalid > 32 ? 32 : nvalid);
+  const unsigned ldb = (unsigned)(ld * (int64_t)sizeof(T));
+  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(g, nv == 0 ? 0u : (unsigned)(nv - 1) * ldb + 128u);
+#pragma unroll
+  for (int op = 0; op < 4; ++op) {
+    const int gi = 64 * op + lane, row = gi >> 3, ch = gi & 7;
+    __builtin_amdgcn_raw_buffer_store_b128(stage[swz_slot<8>(row, ch)], rs, (int)(row * ldb + 16 * ch), 0, 0);
+  }
+}
+
 template <typename T, bool OPORD = false, typename SlotFn>
 __device__ __forceinline__ void store_rows_via(const f32x16& x0, const f32x16& x1, SlotFn slot,
                                                T* g, int64_t ld, int lane, int nvalid = 32) {

@@ -41,13 +41,17 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
                                                                                                 DeltaLayout L) {
   constexpr int SPLIT = state_split<DV>();
   constexpr int NDT = DK / 32, NW = DV / 32 / SPLIT;  // compute waves of this workgroup (+ one copy wave)
-  constexpr int KT = DK / 64, VT = NW / 2;        // 64 x 64 tiles per row block (dO: this workgroup's)
+  constexpr int KT = DK / 64, VT = NW > 1 ? NW / 2 : 1;  // 64 x 64 tiles per row block (dO: this workgroup's)
   constexpr int TE = 64 * 64;                     // elements per tile
   constexpr int OPW = 8;                          // 1 KiB copies per tile, all by the copy wave
   constexpr int NTILE = 3 * KT + 1 + VT;          // K, W^T, Qg, Aqk, dO
   constexpr int SLOT = NTILE * TE + 64 * 4 / (int)sizeof(T);  // + G of the chunk (f32)
   static_assert(VT >= 1, "tile split");
   __shared__ __attribute__((aligned(16))) T Sh[2 * SLOT];
+  // per chunk (two buffers): this workgroup's compute waves' dh^T blocks
+  // (NDT / 2 each) and dv_new^T block, staged for the copy wave's stores
+  constexpr int NSTG = NW * (NDT / 2 + 1);
+  __shared__ __attribute__((aligned(16))) u32x4 Stg[2][NSTG][256];
 
   const int lane = threadIdx.x & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -60,7 +64,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
   const size_t Tp = (size_t)NT * kChunk;
 
   const T* kb = (const T*)a.k + ((size_t)b * Tn * H + h) * DK;
-  const T* dob = (const T*)a.dout + ((size_t)b * Tn * H + h) * DV + 64 * VT * part;  // this workgroup's columns
+  const T* dob = (const T*)a.dout + ((size_t)b * Tn * H + h) * DV + 64 * ((part * NW) / 2);  // this workgroup's columns
   const float* Gc = reinterpret_cast<const float*>(a.ctx + L.Gc) + (size_t)bh * Tp;
 
   auto kt = [&](T* sl, int i) { return sl + i * TE; };                 // K tile i (key dims 64 i..)
@@ -117,16 +121,35 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
     if (GATED && lane < 16) dma16(Gc + t0 + 4 * lane, gs(sl));
   };
 
+  // staged outputs of chunk c: dh^T rows (ci DV + 32 gw) and dv_new^T rows
+  auto flush = [&](int c) __attribute__((always_inline)) {
+    const size_t ci = (size_t)bh * NT + c;
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {
+      const int g2 = part * NW + q;
+      T* drows = (T*)(a.ws + L.dhT) + (ci * DV + 32 * g2) * DK;
+#pragma unroll
+      for (int blk = 0; blk < NDT / 2; ++blk)
+        flush_rows<T>(Stg[c & 1][q * (NDT / 2 + 1) + blk], drows + 64 * blk, DK, lane);
+      flush_rows<T>(Stg[c & 1][q * (NDT / 2 + 1) + NDT / 2], (T*)(a.ws + L.dVnT) + (ci * DV + 32 * g2) * 64, 64,
+                    lane);
+    }
+  };
   if (w == NW) {
     // copy wave: chunk c is complete (vmcnt 0) before it reaches the
     // barrier that opens chunk c for the compute waves; the barrier also
-    // closes chunk c + 1, whose slot then takes chunk c - 1
+    // closes chunk c + 1, whose slot then takes chunk c - 1 and whose
+    // staged outputs this wave then stores (stores first, so waiting for
+    // the copies covers them too)
     issue(NT - 1);
 #pragma unroll 1
     for (int c = NT - 1; c >= 0; --c) {
       vm_wait_barrier<0>();
+      if (c < NT - 1) flush(c + 1);
       if (c > 0) issue(c - 1);
     }
+    block_barrier();  // chunk 0 staged
+    flush(0);
     return;
   }
 
@@ -148,7 +171,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
     block_barrier();
     T* sl = Sh + (c & 1) * SLOT;
     const T* Os = ot(sl, w / 2);  // this wave's 64-column dO tile
-    const int oc0 = 32 * (w & 1);
+    const int oc0 = 32 * (gw & 1);
 
     // the LDS operands of dVn, Z and K dS' into registers first: the one
     // wave per SIMD then never waits on a read inside the MFMA chains
@@ -239,20 +262,12 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
           if (t0 + 32 * jt + 8 * (e >> 2) + 4 * hh + (e & 3) >= Tn) dVn[jt][e] = 0.f;
     }
 
-    // dh^T (gradient of the state leaving the chunk, [v][d]) and dv_new^T out
-    // through this wave's dO columns, which it alone reads and has consumed
-    {
-      char* ob = reinterpret_cast<char*>(const_cast<T*>(Os));
-      auto slot = [&](int s) {
-        const int tr = s >> 2, q = s & 3;
-        return reinterpret_cast<u32x4*>(ob + tr * 128 + (tile_slot(tr, 4 * (w & 1) + q) << 4));
-      };
-      T* drows = (T*)(a.ws + L.dhT) + (ci * DV + 32 * gw) * DK;
+    // dh^T (gradient of the state leaving the chunk, [v][d]) and dv_new^T:
+    // staged here, stored by the copy wave during the next chunk
 #pragma unroll
-      for (int blk = 0; blk < NDT / 2; ++blk)
-        store_rows_via<T>(dS[2 * blk], dS[2 * blk + 1], slot, drows + 64 * blk, DK, lane);
-      store_rows_via<T>(dVn[0], dVn[1], slot, (T*)(a.ws + L.dVnT) + (ci * DV + 32 * gw) * 64, 64, lane);
-    }
+    for (int blk = 0; blk < NDT / 2; ++blk)
+      stage_rows<T>(dS[2 * blk], dS[2 * blk + 1], Stg[c & 1][w * (NDT / 2 + 1) + blk], lane);
+    stage_rows<T>(dVn[0], dVn[1], Stg[c & 1][w * (NDT / 2 + 1) + NDT / 2], lane);
 
     // dS <- e^gamma dS' + Z - W^T dVn
     const float eg = GATED ? __expf(gam) : 1.f;
@@ -273,6 +288,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
     }
   }
 
+  block_barrier();  // chunk 0's staged outputs are complete for the copy wave
   if (a.dh0) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)

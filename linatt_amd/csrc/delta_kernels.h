@@ -45,11 +45,12 @@ struct DeltaLayout {
 DeltaLayout delta_layout(int B, int T, int H, int DK, int DV, int elt_bytes);
 
 // Workgroups per head of the two state passes: the value columns of a head
-// are split over this many workgroups (each on its own CU), so the copy and
-// store traffic of the serial chain spreads over that many CUs.  Measured at
-// K = V = 128: two (two waves each) beat one (four waves) and four (one).
+// are split over this many workgroups (each on its own CU: one compute wave
+// per 32 columns plus a copy wave), so the copy and store traffic of the
+// serial chain spreads over that many CUs.  Measured at K = V = 128: one
+// compute wave per workgroup beats two and four.
 template <int DV>
-constexpr int state_split() { return DV / 32 >= 4 ? 2 : 1; }
+constexpr int state_split() { return DV / 32; }
 
 struct DeltaArgs {
   // inputs
