@@ -394,6 +394,10 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
   constexpr int DMA_PER_CHUNK = 2 * WOPS + UOPS;
   static_assert(WOPS * 64 == WT16 && UOPS * 64 == NW * UT16 && DMA_PER_CHUNK <= 63, "tile split");
   __shared__ __attribute__((aligned(16))) u32x4 Sh[3 * SLOT];
+  // per chunk (two buffers): the compute waves' v_new^T block and h^T blocks
+  // (NDT / 2 each), staged for the copy wave's stores
+  constexpr int NSTG = NW * (NDT / 2 + 1);
+  __shared__ __attribute__((aligned(16))) u32x4 Stg[2][NSTG][256];
 
   const int lane = threadIdx.x & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -430,25 +434,37 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
         dma16s(Ug + (size_t)c * NW * SPLIT * UT16 * 16, 16u * swz_slot<KCPR>((64 * op + lane) / KCPR, lane % KCPR),
                sl + 2 * WT16 + 64 * op);
     };
+    // staged outputs of chunk c: v_new^T and h^T rows (ci DV + 32 g2)
+    auto flush = [&](int c) __attribute__((always_inline)) {
+      const size_t ci = (size_t)bh * NT + c;
+#pragma unroll
+      for (int q = 0; q < NW; ++q) {
+        const int g2 = gw - w + q;
+        flush_rows<T>(Stg[c & 1][q * (NDT / 2 + 1)], (T*)(a.ctx + L.VnT) + (ci * DV + 32 * g2) * 64, 64, lane);
+#pragma unroll
+        for (int blk = 0; blk < NDT / 2; ++blk)
+          flush_rows<T>(Stg[c & 1][q * (NDT / 2 + 1) + 1 + blk],
+                        (T*)(a.ctx + L.hT) + (ci * DV + 32 * g2) * DK + 64 * blk, DK, lane);
+      }
+    };
     issue(0);
     if (NT > 1) issue(1);
 #pragma unroll 1
     for (int c = 0; c < NT; ++c) {
-      // chunk c landed (only chunk c + 1's copies may remain in flight)
-      // before the barrier that opens it; the barrier also closes chunk
-      // c - 1, whose slot then takes chunk c + 2
+      // chunk c landed (only chunk c + 1's copies may remain in flight;
+      // stores only add to the count) before the barrier that opens it;
+      // the barrier also closes chunk c - 1, whose staged outputs this wave
+      // stores and whose slot then takes chunk c + 2
       if (c + 1 < NT) vm_wait_barrier<DMA_PER_CHUNK>();
       else vm_wait_barrier<0>();
+      if (c > 0) flush(c - 1);
       if (c + 2 < NT) issue(c + 2);
     }
+    block_barrier();  // the last chunk staged
+    flush(NT - 1);
     return;
   }
 
-  // v_new^T and h^T rows of this head (rows [v][.] per chunk, this wave's 32)
-  const __amdgpu_buffer_rsrc_t vn_rs =
-      buf_rsrc(a.ctx + L.VnT + (size_t)bh * NT * DV * 64 * sizeof(T), (unsigned)(NT * DV * 64 * sizeof(T)));
-  const __amdgpu_buffer_rsrc_t h_rs =
-      buf_rsrc(a.ctx + L.hT + (size_t)bh * NT * DV * DK * sizeof(T), (unsigned)(NT * DV * DK * sizeof(T)));
 
   f32x16 S[NDT];
 #pragma unroll
@@ -522,17 +538,12 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
           for (int r = 0; r < 4; ++r) Vn[it][4 * I + r] = (float)u8[4 * s2 + r] - P[it][4 * I + r];
         }
       }
-    // v_new^T and the state entering the chunk (h^T, [v][d]) go out through
-    // this wave's U^T area of the slot, which the wave alone reads and has
-    // finished with
-    u32x4* stage = const_cast<u32x4*>(Us);
-    store_rows_buf<T>(Vn[0], Vn[1], stage, vn_rs, (int)(((size_t)c * DV + 32 * gw) * 64 * sizeof(T)),
-                      64 * (int)sizeof(T), lane);
+    // v_new^T and the state entering the chunk (h^T, [v][d]): staged here,
+    // stored by the copy wave during the next chunk
+    stage_rows<T>(Vn[0], Vn[1], Stg[c & 1][w * (NDT / 2 + 1)], lane);
 #pragma unroll
     for (int blk = 0; blk < NDT / 2; ++blk)
-      store_rows_buf<T>(S[2 * blk], S[2 * blk + 1], stage, h_rs,
-                        (int)((((size_t)c * DV + 32 * gw) * DK + 64 * blk) * sizeof(T)), DK * (int)sizeof(T),
-                        lane);
+      stage_rows<T>(S[2 * blk], S[2 * blk + 1], Stg[c & 1][w * (NDT / 2 + 1) + 1 + blk], lane);
 
     // S <- e^gamma S + Kd^T v_new  (Kd^T rows 32 dt + cl, chunk rows in operand order)
     const float eg = GATED ? __expf(Gc[c * kChunk + 63]) : 1.f;
@@ -554,6 +565,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
     if (c + 1 < NT) step(IntC<1>{}, c + 1);
     if (c + 2 < NT) step(IntC<2>{}, c + 2);
   }
+  block_barrier();  // the last chunk's staged outputs are complete for the copy wave
 
   if (a.ht) {
 #pragma unroll
