@@ -722,14 +722,17 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
             pdv[4 * i + r] = p4[r];
           }
         }
+        // the causal / past-T mask rides on the row scale scale^2/den, which
+        // multiplies both x (into xs) and A (into P): zero where masked.  Its
+        // branch closes before the products, which stay one basic block.
+        if (need_mask) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) pdv[e] = masked(e) ? 0.f : pdv[e];
+        }
         // x[t][s] = dO V^T - delta  (rows t, column s)
 #pragma unroll
         for (int kk = 0; kk < DV / 16; ++kk)
           x = mma(tile_ld8<T>(Os, 32 * mb + cl, 16 * kk + 8 * hh), vop[kk], x);
-        if (need_mask) {
-#pragma unroll
-          for (int e = 0; e < 16; ++e) x[e] = masked(e) ? 0.f : x[e];
-        }
         if constexpr (DECAY) {
 #pragma unroll
           for (int e = 0; e < 16; ++e)
@@ -762,10 +765,6 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
             // score registers; unbounded, they spill)
             if constexpr (SUM || DECAY) __builtin_amdgcn_sched_barrier(0);
           }
-        if (need_mask) {
-#pragma unroll
-          for (int e = 0; e < 16; ++e) A[e] = masked(e) ? 0.f : A[e];
-        }
         if constexpr (DECAY) {
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
