@@ -472,6 +472,30 @@ __device__ __forceinline__ void stage_rows(const f32x16& x0, const f32x16& x1, u
   }
 }
 
+// A wave's 32 x 32 block of 16-bit values in C layout (lane column = block
+// row cl; columns 8 I + 4 hh + r) through 2 KiB of LDS (128 16-byte slots,
+// row-major 32 x 4, XOR-swizzled by row) to rows g + row * ld: 8-byte LDS
+// writes, then two buffer-store instructions of 16 whole 64-byte rows each
+// (g wave-uniform, rows >= nvalid dropped).
+__device__ __forceinline__ int swz4(int row, int ch) { return row * 4 + (ch ^ ((row >> 1) & 3)); }
+template <typename T>
+__device__ __forceinline__ void store_rows32(const f32x16& x, u32x4* stage, T* g, int64_t ld, int lane,
+                                             int nvalid = 32) {
+  const int cl = lane & 31, hh = lane >> 5;
+#pragma unroll
+  for (int I = 0; I < 4; ++I)
+    *reinterpret_cast<v4_t<T>*>(reinterpret_cast<char*>(stage + swz4(cl, I)) + 8 * hh) =
+        to4<T>(x[4 * I], x[4 * I + 1], x[4 * I + 2], x[4 * I + 3]);
+  const int nv = nvalid < 0 ? 0 : (nvalid > 32 ? 32 : nvalid);
+  const unsigned ldb = (unsigned)(ld * (int64_t)sizeof(T));
+  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(g, nv == 0 ? 0u : (unsigned)(nv - 1) * ldb + 64u);
+#pragma unroll
+  for (int op = 0; op < 2; ++op) {
+    const int gi = 64 * op + lane, row = gi >> 2, ch = gi & 3;
+    __builtin_amdgcn_raw_buffer_store_b128(stage[swz4(row, ch)], rs, (int)(row * ldb + 16 * ch), 0, 0);
+  }
+}
+
 // The global half: a staged block's 32 rows to g + row * ld (g wave-uniform,
 // rows >= nvalid dropped), by any wave of the workgroup.
 template <typename T>

@@ -302,22 +302,25 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
 
 // ---------------------------------------------------------------------------
 // Kernel 2: dq, dW, the output/state part of dk and of dG.  One workgroup of
-// eight waves per chunk; every input tile by one up-front copy (rows past T
-// repeat the last valid row and are masked where they could reach a result).
-//   waves 0-3: dq = scale e^G dO S^T and dW = -dVn S^T (rows i, 64 key dims)
-//   waves 4-7: dKs = e^(gamma - G) Vn dS'^T          (rows j, 64 key dims)
-//   waves 4-6: the nonzero blocks of X = dO Vn^T -> Mq = scale X o e^(G_i-G_j)
-//              [j <= i], and Z = X o Aqk for the dG row / column terms
-//   then dq += Mq K (waves 0-3), dKs += Mq^T Q (waves 4-7)
+// eight waves per chunk.  Input tiles arrive by direct copies issued at the
+// start in the order of use, so the dq / dW products run while the tiles of
+// the later phases are still landing (rows past T repeat the last valid row
+// and are masked where they could reach a result).  Wave w owns the 32 x 32
+// output blocks (rows 32 (w & 1) .., key dims 32 (w >> 1) ..):
+//   1a. dq = scale e^G dO S^T and dW = -dVn S^T            (S, dVn, dO, q)
+//   1b. dKs = e^(gamma - G) Vn dS'^T                        (dS', Vn, k);
+//       waves 0-2: the nonzero blocks of X = dO Vn^T
+//   2.  Mq = scale X o e^(G_i-G_j) [j <= i] to an LDS tile, Z = X o Aqk
+//   3.  dq += Mq K, dKs += Mq^T Q
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
 __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, DeltaLayout L) {
   constexpr int KT = DK / 64, VT = DV / 64, TE = 64 * 64;
-  constexpr int SE0 = 2 * VT * KT * TE, SE1 = 3 * TE + 8 * 2048;
+  constexpr int SE0 = 2 * VT * KT * TE, SE1 = 3 * TE + 8 * 1024;
   constexpr int SE = SE0 > SE1 ? SE0 : SE1;
   static_assert(DK % 64 == 0 && DV % 64 == 0 && DK <= 128 && DV <= 128, "64 or 128 wide");
-  // S^T and dS'^T as [v][d] tiles (tile vt * KT + kt); after phase 1: Mq [i][j]
-  // (0 .. TE), Z^T fp32 [j][i] (TE .. 3 TE), store staging (3 TE + 2048 w)
+  // S^T then dS'^T as [v][d] tiles (tile vt * KT + kt); after phase 1: Mq
+  // [i][j] (0 .. TE), Z^T fp32 [j][i] (TE .. 3 TE), store staging (3 TE + 1024 w)
   __shared__ __attribute__((aligned(16))) T St[SE];
   __shared__ __attribute__((aligned(16))) T dVt[VT * TE];  // dVn^T [v][i]
   __shared__ __attribute__((aligned(16))) T Vnt[VT * TE];  // Vn^T [v][j]
@@ -326,7 +329,7 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
   __shared__ __attribute__((aligned(16))) T Kt[KT * TE];   // k [j][d]
   __shared__ __attribute__((aligned(16))) T At[TE];        // Aqk [i][j]
   __shared__ __attribute__((aligned(16))) float Gs[64];
-  __shared__ float red_gi[2][64], red_kd[2][64], red_rs[2][64], red_s[8];
+  __shared__ float red_gi[4][64], red_kd[4][64], red_rs[2][64], red_s[8];
   T* Mqt = St;
   float* Zt = reinterpret_cast<float*>(St + TE);
 
@@ -344,108 +347,98 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
   const T* dob = (const T*)a.dout + ((size_t)b * Tn * H + h) * DV;
   const int64_t qks = (int64_t)H * DK, os = (int64_t)H * DV;
 
-  // 0. copies (op w of every tile; Aqk last), G by wave 0
+  // 0. copies, op w of every tile: phase 1a's (S, dVn, dO, q, G), then 1b's
+  //    (dS', Vn, k: 2 KT VT... ops), then Aqk
+  constexpr int N1B = VT * KT + VT + KT;  // copies per wave after phase 1a's
   {
     const T* hg = (const T*)(a.ctx + L.hT) + ci * DV * DK;
     const T* dhg = (const T*)(a.ws + L.dhT) + ci * DV * DK;
 #pragma unroll
-    for (int vt = 0; vt < VT; ++vt)
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
-        dma_tile64<T>(hg + (size_t)64 * vt * DK + 64 * kt, DK, 0, 64, St + (vt * KT + kt) * TE, w, lane);
-        dma_tile64<T>(dhg + (size_t)64 * vt * DK + 64 * kt, DK, 0, 64, St + (VT * KT + vt * KT + kt) * TE, w, lane);
-      }
-#pragma unroll
     for (int vt = 0; vt < VT; ++vt) {
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt)
+        dma_tile64<T>(hg + (size_t)64 * vt * DK + 64 * kt, DK, 0, 64, St + (vt * KT + kt) * TE, w, lane);
       dma_tile64<T>((const T*)(a.ws + L.dVnT) + (ci * DV + 64 * vt) * 64, 64, 0, 64, dVt + vt * TE, w, lane);
-      dma_tile64<T>((const T*)(a.ctx + L.VnT) + (ci * DV + 64 * vt) * 64, 64, 0, 64, Vnt + vt * TE, w, lane);
       dma_tile64<T>(dob + 64 * vt, os, t0, Tn, Ot + vt * TE, w, lane);
     }
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-      dma_tile64<T>(qb + 64 * kt, qks, t0, Tn, Qt + kt * TE, w, lane);
-      dma_tile64<T>(kb + 64 * kt, qks, t0, Tn, Kt + kt * TE, w, lane);
-    }
+    for (int kt = 0; kt < KT; ++kt) dma_tile64<T>(qb + 64 * kt, qks, t0, Tn, Qt + kt * TE, w, lane);
     if (GATED && w == 0 && lane < 16)
       dma16(reinterpret_cast<const float*>(a.ctx + L.Gc) + (size_t)bh * Tp + t0 + 4 * lane, Gs);
+    // phase 1b
+#pragma unroll
+    for (int vt = 0; vt < VT; ++vt) {
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt)
+        dma_tile64<T>(dhg + (size_t)64 * vt * DK + 64 * kt, DK, 0, 64, St + (VT * KT + vt * KT + kt) * TE, w, lane);
+      dma_tile64<T>((const T*)(a.ctx + L.VnT) + (ci * DV + 64 * vt) * 64, 64, 0, 64, Vnt + vt * TE, w, lane);
+    }
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) dma_tile64<T>(kb + 64 * kt, qks, t0, Tn, Kt + kt * TE, w, lane);
     dma_tile64<T>((const T*)(a.ctx + L.Aqk) + ci * 4096, 64, 0, 64, At, w, lane);
   }
   if (!GATED && tid < 64) Gs[tid] = 0.f;
-  if (tid < 128) {
+  if (tid < 256) {
     red_gi[tid >> 6][tid & 63] = 0.f;
     red_kd[tid >> 6][tid & 63] = 0.f;
-    red_rs[tid >> 6][tid & 63] = 0.f;
   }
-  vm_wait_barrier<1>();  // everything but Aqk
+  if (tid < 128) red_rs[tid >> 6][tid & 63] = 0.f;
+  vm_wait_barrier<N1B + 1>();  // phase 1a's tiles
 
-  const float gam = Gs[63];
-  const int wl = w & 3, lb = wl & 1, dp = wl >> 1;  // lane block, key-dim pair (tile dp)
-  const int r = 32 * lb + cl;                      // this lane's row (i or j) in the chunk
+  const int lb = w & 1, db = w >> 1;  // row block, 32 key dims (tile db / 2, columns 32 (db & 1))
+  const int r = 32 * lb + cl;         // this lane's row (i or j) in the chunk
   const bool rvalid = t0 + r < Tn;
-  const bool active = dp < KT;
-  f32x16 acc[2], dwk[2];
-  float part = 0.f;
+  const bool active = db < DK / 32;
+  const T* stile = St + (db / 2) * TE;  // + vt * KT * TE
+  f32x16 dqa{}, dwa{}, dka{};
+  float gi = 0.f, kd = 0.f;
 
-  // 1. waves 0-3: dq (scaled) and dW; waves 4-7: dKs
+  // 1a. dq (scaled) and dW, rows i = r, key dims 32 db ..
   if (active) {
-    if (w < 4) {
 #pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        acc[m] = f32x16{};
-        dwk[m] = f32x16{};
+    for (int vt = 0; vt < VT; ++vt)
 #pragma unroll
-        for (int vt = 0; vt < VT; ++vt)
+      for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-          for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj) {
-              const v8_t<T> hop = tile_tr8<T>(St + (vt * KT + dp) * TE, 32 * s2, 32 * m, jj, lane);
-              acc[m] = mma(hop, tile_ldp8<T>(Ot + vt * TE, r, 32 * s2, jj, hh), acc[m]);
-              dwk[m] = mma(hop, tile_tr8<T>(dVt + vt * TE, 32 * s2, 32 * lb, jj, lane), dwk[m]);
-            }
-      }
-      const float f = a.scale * (GATED ? __expf(Gs[r]) : 1.f);
-      const char* qrow = reinterpret_cast<const char*>(Qt + dp * TE);
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        acc[m] *= f;
-        dwk[m] = -dwk[m];
-#pragma unroll
-        for (int I = 0; I < 4; ++I) {
-          const v4_t<T> q4 = *reinterpret_cast<const v4_t<T>*>(qrow + tile_off(r, 32 * m + 8 * I + 4 * hh));
-#pragma unroll
-          for (int e = 0; e < 4; ++e) part += (float)q4[e] * acc[m][4 * I + e];
+        for (int jj = 0; jj < 2; ++jj) {
+          const v8_t<T> hop = tile_tr8<T>(stile + vt * KT * TE, 32 * s2, 32 * (db & 1), jj, lane);
+          dqa = mma(hop, tile_ldp8<T>(Ot + vt * TE, r, 32 * s2, jj, hh), dqa);
+          dwa = mma(hop, tile_tr8<T>(dVt + vt * TE, 32 * s2, 32 * lb, jj, lane), dwa);
         }
-      }
-    } else {
+    dqa *= a.scale * (GATED ? __expf(Gs[r]) : 1.f);
+    dwa = -dwa;
+    const char* qrow = reinterpret_cast<const char*>(Qt + (db / 2) * TE);
 #pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        acc[m] = f32x16{};
+    for (int I = 0; I < 4; ++I) {
+      const v4_t<T> q4 = *reinterpret_cast<const v4_t<T>*>(qrow + tile_off(r, 32 * (db & 1) + 8 * I + 4 * hh));
 #pragma unroll
-        for (int vt = 0; vt < VT; ++vt)
-#pragma unroll
-          for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj)
-              acc[m] = mma(tile_tr8<T>(St + (VT * KT + vt * KT + dp) * TE, 32 * s2, 32 * m, jj, lane),
-                           tile_tr8<T>(Vnt + vt * TE, 32 * s2, 32 * lb, jj, lane), acc[m]);
-      }
-      const float f = GATED ? __expf(gam - Gs[r]) : 1.f;
-      const char* krow = reinterpret_cast<const char*>(Kt + dp * TE);
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        acc[m] *= f;
-#pragma unroll
-        for (int I = 0; I < 4; ++I) {
-          const v4_t<T> k4 = *reinterpret_cast<const v4_t<T>*>(krow + tile_off(r, 32 * m + 8 * I + 4 * hh));
-#pragma unroll
-          for (int e = 0; e < 4; ++e) part += (float)k4[e] * acc[m][4 * I + e];
-        }
-      }
+      for (int e = 0; e < 4; ++e) gi += (float)q4[e] * dqa[4 * I + e];
     }
-    if (!rvalid) part = 0.f;
+    if (!rvalid) gi = 0.f;
   }
-  // <S, dS'> over the chunk's state pair (same tile layout: order-free sum)
+  vm_wait_barrier<1>();  // phase 1b's tiles
+
+  // 1b. dKs rows j = r, key dims 32 db ..; the state-pair dot; X blocks
+  const float gam = Gs[63];
+  if (active) {
+#pragma unroll
+    for (int vt = 0; vt < VT; ++vt)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+          dka = mma(tile_tr8<T>(stile + (VT * KT + vt * KT) * TE, 32 * s2, 32 * (db & 1), jj, lane),
+                    tile_tr8<T>(Vnt + vt * TE, 32 * s2, 32 * lb, jj, lane), dka);
+    dka *= GATED ? __expf(gam - Gs[r]) : 1.f;
+    const char* krow = reinterpret_cast<const char*>(Kt + (db / 2) * TE);
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      const v4_t<T> k4 = *reinterpret_cast<const v4_t<T>*>(krow + tile_off(r, 32 * (db & 1) + 8 * I + 4 * hh));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) kd += (float)k4[e] * dka[4 * I + e];
+    }
+    if (!rvalid) kd = 0.f;
+  }
   float sdot = 0.f;
   {
     constexpr int N16 = VT * KT * TE / 8;  // 16-byte chunks per state
@@ -461,11 +454,11 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) sdot += __shfl_xor(sdot, off);
   }
-  // waves 4-6: X block (ib, jb) = (0,0), (1,0), (1,1) as D[j][i] (lane column i)
-  const int mb = w - 4;  // 0..2: blocks (0,0), (1,0), (1,1); 3: the zero block (0,1)
-  const int xib = mb == 1 || mb == 2, xjb = mb >= 2;
+  // waves 0..2: X block (ib, jb) = (0,0), (1,0), (1,1) as D[j][i] (lane column i);
+  // wave 3: the zero block (0, 1)
+  const int xib = w == 1 || w == 2, xjb = w >= 2;
   f32x16 xs{};
-  if (mb >= 0 && mb < 3) {
+  if (w < 3) {
 #pragma unroll
     for (int vt = 0; vt < VT; ++vt)
 #pragma unroll
@@ -477,8 +470,8 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
   }
   vm_wait_barrier<0>();  // Aqk landed; the state tiles are no longer read
 
-  // 2. Mq [i][j] tile and Z^T; wave 7 the zero block (i < 32 <= j); waves 0-3 dW out
-  if (mb >= 0) {
+  // 2. Mq [i][j] tile and Z^T (waves 0-3); dW out
+  if (w < 4) {
     const int xi = 32 * xib + cl;  // this lane's i
     const float Gi = Gs[xi];
     const bool iv = t0 + xi < Tn;
@@ -488,65 +481,52 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       const int j0 = 32 * xjb + 8 * I + 4 * hh;
-      const v4_t<T> a4 = mb < 3 ? *reinterpret_cast<const v4_t<T>*>(arow + tile_off(xi, j0)) : v4_t<T>{};
+      const v4_t<T> a4 = w < 3 ? *reinterpret_cast<const v4_t<T>*>(arow + tile_off(xi, j0)) : v4_t<T>{};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int j = j0 + e;
-        const float x = mb < 3 ? xs[4 * I + e] : 0.f;
+        const float x = w < 3 ? xs[4 * I + e] : 0.f;
         const float z = x * (float)a4[e];
         rs += z;
         Zt[j * 64 + xi] = z;
         float mv = 0.f;
-        if (mb < 3 && iv && j <= xi) mv = a.scale * x * (GATED ? __expf(Gi - Gs[j]) : 1.f);
+        if (w < 3 && iv && j <= xi) mv = a.scale * x * (GATED ? __expf(Gi - Gs[j]) : 1.f);
         mq[4 * I + e] = mv;
       }
       *reinterpret_cast<v4_t<T>*>(reinterpret_cast<char*>(Mqt) + tile_off(xi, j0)) =
           to4<T>(mq[4 * I], mq[4 * I + 1], mq[4 * I + 2], mq[4 * I + 3]);
     }
     rs += __shfl_xor(rs, 32);
-    if (hh == 0 && mb < 3) red_rs[xjb][xi] = rs;
+    if (hh == 0 && w < 3) red_rs[xjb][xi] = rs;
   }
-  u32x4* stage = reinterpret_cast<u32x4*>(St + 3 * TE) + 256 * w;
-  if (w < 4 && active)
-    store_rows_staged<T>(dwk[0], dwk[1], stage, (T*)(a.ws + L.dW) + ((size_t)bh * Tp + t0 + 32 * lb) * DK + 64 * dp,
-                         DK, lane);
+  u32x4* stage = reinterpret_cast<u32x4*>(St + 3 * TE) + 128 * w;
+  if (active)
+    store_rows32<T>(dwa, stage, (T*)(a.ws + L.dW) + ((size_t)bh * Tp + t0 + 32 * lb) * DK + 32 * db, DK, lane);
   __syncthreads();
 
   // 3. dq += Mq K (rows i), dKs += Mq^T Q (rows j)
   if (active) {
-    if (w < 4) {
 #pragma unroll
-      for (int m = 0; m < 2; ++m)
+    for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb)
+      for (int jj = 0; jj < 2; ++jj) {
+        dqa = mma(tile_tr8<T>(Kt + (db / 2) * TE, 32 * jb, 32 * (db & 1), jj, lane),
+                  tile_ldp8<T>(Mqt, r, 32 * jb, jj, hh), dqa);
+        dka = mma(tile_tr8<T>(Qt + (db / 2) * TE, 32 * jb, 32 * (db & 1), jj, lane),
+                  tile_tr8<T>(Mqt, 32 * jb, 32 * lb, jj, lane), dka);
+      }
+    store_rows32<T>(dqa, stage, (T*)a.dq + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DK + 32 * db, qks, lane,
+                    Tn - (t0 + 32 * lb));
+    float* dkp = reinterpret_cast<float*>(a.ws + L.dKp) + ((size_t)bh * Tp + t0 + r) * DK + 32 * db;
 #pragma unroll
-          for (int jj = 0; jj < 2; ++jj)
-            acc[m] = mma(tile_tr8<T>(Kt + dp * TE, 32 * jb, 32 * m, jj, lane), tile_ldp8<T>(Mqt, r, 32 * jb, jj, hh),
-                         acc[m]);
-      store_rows_staged<T>(acc[0], acc[1], stage, (T*)a.dq + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DK + 64 * dp,
-                           qks, lane, Tn - (t0 + 32 * lb));
-    } else {
-#pragma unroll
-      for (int m = 0; m < 2; ++m)
-#pragma unroll
-        for (int ib = 0; ib < 2; ++ib)
-#pragma unroll
-          for (int jj = 0; jj < 2; ++jj)
-            acc[m] = mma(tile_tr8<T>(Qt + dp * TE, 32 * ib, 32 * m, jj, lane),
-                         tile_tr8<T>(Mqt, 32 * ib, 32 * lb, jj, lane), acc[m]);
-      float* dkp = reinterpret_cast<float*>(a.ws + L.dKp) + ((size_t)bh * Tp + t0 + r) * DK + 64 * dp;
-#pragma unroll
-      for (int m = 0; m < 2; ++m)
-#pragma unroll
-        for (int I = 0; I < 4; ++I)
-          *reinterpret_cast<f32x4*>(dkp + 32 * m + 8 * I + 4 * hh) =
-              f32x4{acc[m][4 * I], acc[m][4 * I + 1], acc[m][4 * I + 2], acc[m][4 * I + 3]};
-    }
+    for (int I = 0; I < 4; ++I)
+      *reinterpret_cast<f32x4*>(dkp + 8 * I + 4 * hh) = f32x4{dka[4 * I], dka[4 * I + 1], dka[4 * I + 2], dka[4 * I + 3]};
   }
-  part += __shfl_xor(part, 32);
+  gi += __shfl_xor(gi, 32);
+  kd += __shfl_xor(kd, 32);
   if (active && hh == 0) {
-    if (w < 4) red_gi[dp][r] = part;
-    else red_kd[dp][r] = part;
+    red_gi[db][r] = gi;
+    red_kd[db][r] = kd;
   }
   if (lane == 0) red_s[w] = sdot;
   __syncthreads();
@@ -557,10 +537,15 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
       const f32x4 v = *reinterpret_cast<const f32x4*>(Zt + tid * 64 + 4 * q4);
       cs += (v[0] + v[1]) + (v[2] + v[3]);
     }
-    const float kd = red_kd[0][tid] + red_kd[1][tid];
-    float dG = red_gi[0][tid] + red_gi[1][tid] - kd + (red_rs[0][tid] + red_rs[1][tid]) - cs;
+    float kdt = 0.f, git = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      kdt += red_kd[q][tid];
+      git += red_gi[q][tid];
+    }
+    float dG = git - kdt + (red_rs[0][tid] + red_rs[1][tid]) - cs;
     // d gamma = sum_j k_j . dKs_j + e^gamma <S, dS'>, added at row 63
-    float kds = kd;
+    float kds = kdt;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) kds += __shfl_xor(kds, off);
     if (tid == 63) {
