@@ -177,6 +177,26 @@ __device__ __forceinline__ void vm_wait_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"i"(N) : "memory");
 }
 
+// Compile-time integer as a value, for lambdas unrolled over ring slots.
+template <int N>
+struct IC {
+  static constexpr int value = N;
+};
+
+// vm_wait_barrier for a wave-uniform count n in [0, 6] (the counter field is
+// an immediate); larger n waits for everything.
+__device__ __forceinline__ void vm_wait_barrier_n(int n) {
+  switch (n) {
+    case 6: vm_wait_barrier<6>(); break;
+    case 5: vm_wait_barrier<5>(); break;
+    case 4: vm_wait_barrier<4>(); break;
+    case 3: vm_wait_barrier<3>(); break;
+    case 2: vm_wait_barrier<2>(); break;
+    case 1: vm_wait_barrier<1>(); break;
+    default: vm_wait_barrier<0>(); break;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // 64 x 64 tiles of 16-bit elements in LDS: 128-byte rows, unpadded, with the
 // 16-byte chunk c of row r stored in slot c ^ f(r),

@@ -448,9 +448,10 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
   constexpr int E = DK / M;
   constexpr int KE = E / 16;
   static_assert(sizeof(T) == 2 && DK == 64 && DV == 64, "64 x 64 16-bit tiles");
-  __shared__ __attribute__((aligned(16))) T Kb[2][64 * 64];
-  __shared__ __attribute__((aligned(16))) T Vb[2][64 * 64];
-  __shared__ __attribute__((aligned(16))) float Cs[2][64];
+  constexpr int NB = 3;  // ring depth: tiles st + 1 and st + 2 in flight during tile st
+  __shared__ __attribute__((aligned(16))) T Kb[NB][64 * 64];
+  __shared__ __attribute__((aligned(16))) T Vb[NB][64 * 64];
+  __shared__ __attribute__((aligned(16))) float Cs[NB][64];
   __shared__ __attribute__((aligned(16))) T Zr[8];
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
@@ -510,24 +511,30 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
   auto issue = [&](int st) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      dma_tile64<T>(kb, ks, 64 * st, Tn, Kb[st & 1], 2 * w + i, lane);
-      dma_tile64<T>(vb, vs, 64 * st, Tn, Vb[st & 1], 2 * w + i, lane);
+      dma_tile64<T>(kb, ks, 64 * st, Tn, Kb[st % NB], 2 * w + i, lane);
+      dma_tile64<T>(vb, vs, 64 * st, Tn, Vb[st % NB], 2 * w + i, lane);
     }
   };
   auto load_c = [&](int st) __attribute__((always_inline)) {
     if constexpr (DECAY) {
-      if (w == 0) dma4(c + ((int64_t)b * Tn + min(64 * st + lane, Tn - 1)) * HQ + hq, Cs[st & 1]);
+      if (w == 0) dma4(c + ((int64_t)b * Tn + min(64 * st + lane, Tn - 1)) * HQ + hq, Cs[st % NB]);
     }
   };
+  const int ops = 4 + (DECAY && w == 0 ? 1 : 0);  // copies per tile and wave
   vm_drain();  // q, dO (and c) of this wave's queries are in registers
-  issue(0);
-  load_c(0);
+#pragma unroll
+  for (int st = 0; st < NB - 1; ++st)
+    if (st < nst) {
+      issue(st);
+      load_c(st);
+    }
   for (int st = 0; st < nst; ++st) {
-    const int s0 = st * 64, buf = st & 1;
-    vm_wait_barrier<0>();
-    if (st + 1 < nst) {
-      issue(st + 1);
-      load_c(st + 1);
+    const int s0 = st * 64, buf = st % NB;
+    // tile st landed; tile st - 1's slot is free for tile st + 2
+    vm_wait_barrier_n(st + 1 < nst ? ops : 0);
+    if (st + NB - 1 < nst) {
+      issue(st + NB - 1);
+      load_c(st + NB - 1);
     }
     const T* Ks = Kb[buf];
     const T* Vs = Vb[buf];
@@ -619,11 +626,14 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
   constexpr float kPScale = __is_same(T, _Float16) ? 4096.f : 1.f;
   constexpr float kPInv = 1.f / kPScale;
   static_assert(sizeof(T) == 2 && DK == 64 && DV == 64, "64 x 64 16-bit tiles");
-  __shared__ __attribute__((aligned(16))) T Qb[2][64 * 64];
-  __shared__ __attribute__((aligned(16))) T Ob[2][64 * 64];
-  __shared__ __attribute__((aligned(16))) float Dl[2][64];  // -delta
-  __shared__ __attribute__((aligned(16))) float Pd[2][64];  // scale^2 / den
-  __shared__ __attribute__((aligned(16))) float Ct[2][64];
+  // ring depth 2: tile n + 1 in flight during tile n (a third slot costs
+  // registers in this kernel and spills)
+  constexpr int NB = 2;
+  __shared__ __attribute__((aligned(16))) T Qb[NB][64 * 64];
+  __shared__ __attribute__((aligned(16))) T Ob[NB][64 * 64];
+  __shared__ __attribute__((aligned(16))) float Dl[NB][64];  // -delta
+  __shared__ __attribute__((aligned(16))) float Pd[NB][64];  // scale^2 / den
+  __shared__ __attribute__((aligned(16))) float Ct[NB][64];
   __shared__ __attribute__((aligned(16))) T Zr[8];
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
@@ -670,8 +680,8 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
     const T* ob = dout + ((int64_t)b * Tn) * os + (int64_t)hq * DV;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      dma_tile64<T>(qb, qs, t0, Tn, Qb[n & 1], 2 * w + i, lane);
-      dma_tile64<T>(ob, os, t0, Tn, Ob[n & 1], 2 * w + i, lane);
+      dma_tile64<T>(qb, qs, t0, Tn, Qb[n % NB], 2 * w + i, lane);
+      dma_tile64<T>(ob, os, t0, Tn, Ob[n % NB], 2 * w + i, lane);
     }
   };
   // per-row data of a query tile: -delta and scale^2/den as the dq kernel
@@ -681,23 +691,30 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
   auto load_rows = [&](int n) __attribute__((always_inline)) {
     const int hq = h * G + n / nq, t = min(64 * (tt0 + n % nq) + lane, Tn - 1);
     const int64_t r = ((int64_t)b * Tn + t) * HQ + hq;
-    if (w == 0) dma4(delta + r, Dl[n & 1]);
-    if (w == 1) dma4(delta + nrows + r, Pd[n & 1]);
-    if (DECAY && w == 2) dma4(c + r, Ct[n & 1]);
+    if (w == 0) dma4(delta + r, Dl[n % NB]);
+    if (w == 1) dma4(delta + nrows + r, Pd[n % NB]);
+    if (DECAY && w == 2) dma4(c + r, Ct[n % NB]);
   };
 
   float csl = (DECAY && svalid) ? c[((int64_t)b * Tn + sl) * HQ + h * G] : 0.f;
+  // copies per tile and wave: two of q, two of dO, a row vector by waves 0-2
+  const int ops = 4 + (w < 2 || (DECAY && w == 2) ? 1 : 0);
   vm_drain();  // k, v (and c) of this wave's keys are in registers
-  issue(0);
-  load_rows(0);
+#pragma unroll
+  for (int n = 0; n < NB - 1; ++n)
+    if (n < ntiles) {
+      issue(n);
+      load_rows(n);
+    }
   float dcc = 0.f;
   for (int n = 0; n < ntiles; ++n) {
-    const int buf = n & 1;
+    const int buf = n % NB;
     const int hq = h * G + n / nq, t0 = 64 * (tt0 + n % nq);
-    vm_wait_barrier<0>();
-    if (n + 1 < ntiles) {
-      issue(n + 1);
-      load_rows(n + 1);
+    // tile n landed; tile n - 1's slot is free for tile n + NB - 1
+    vm_wait_barrier_n(NB > 2 && n + 1 < ntiles ? ops : 0);
+    if (n + NB - 1 < ntiles) {
+      issue(n + NB - 1);
+      load_rows(n + NB - 1);
     }
     const T* Qs = Qb[buf];
     const T* Os = Ob[buf];

@@ -190,11 +190,14 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_fwd_kernel(
 }
 
 // 16-bit inputs: the same computation with the key tiles brought in by
-// direct global->LDS copies (double-buffered, the next tile's copies in
-// flight while the current one computes, one barrier per tile) and stored
+// direct global->LDS copies through a three-slot ring (tiles st + 1 and
+// st + 2 in flight while tile st computes, one barrier per tile) and stored
 // swizzled in natural layout: K feeds the score MFMAs with 16-byte reads and
 // V^T comes from V through transposing LDS reads, so no transposed copy is
-// built.  Rows past T repeat the last valid row and are masked.
+// built.  Rows past T repeat the last valid row and are masked.  The loop is
+// unrolled over the ring so every LDS operand address is a per-lane offset
+// fixed for the kernel plus an immediate, and full tiles are copied from a
+// scalar base: the VALU, which bounds this kernel, only does the math.
 template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
 __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
@@ -203,9 +206,10 @@ __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
   constexpr int E = DK / M;
   constexpr int KE = E / 16;
   static_assert(sizeof(T) == 2 && DK == 64 && DV == 64, "64 x 64 16-bit tiles");
-  __shared__ __attribute__((aligned(16))) T Kb[2][64 * 64];
-  __shared__ __attribute__((aligned(16))) T Vb[2][64 * 64];
-  __shared__ __attribute__((aligned(16))) float Cs[2][64];
+  constexpr int NB = 3;
+  __shared__ __attribute__((aligned(16))) T Kb[NB][64 * 64];
+  __shared__ __attribute__((aligned(16))) T Vb[NB][64 * 64];
+  __shared__ __attribute__((aligned(16))) float Cs[NB][64];
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -238,112 +242,134 @@ __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
 
   const int s_end = min(t0 + 128, Tn);
   const int nst = (s_end + 63) / 64;
-  // tile st: 8 KiB of K and 8 KiB of V, two 1 KiB copies of each per wave
-  auto issue = [&](int st) __attribute__((always_inline)) {
-    const int buf = st & 1;
+  // tile st: 8 KiB of K and 8 KiB of V, copies 2w and 2w + 1 of each by wave w
+  // (full tiles: scalar base + these per-lane offsets)
+  unsigned ko[2], vo[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      dma_tile64<T>(kb, ks, 64 * st, Tn, Kb[buf], 2 * w + i, lane);
-      dma_tile64<T>(vb, vs, 64 * st, Tn, Vb[buf], 2 * w + i, lane);
+  for (int i = 0; i < 2; ++i) {
+    ko[i] = tile_lane_off(2 * w + i, lane, (int)(ks * sizeof(T)));
+    vo[i] = tile_lane_off(2 * w + i, lane, (int)(vs * sizeof(T)));
+  }
+  auto issue = [&](int st, auto slot) __attribute__((always_inline)) {
+    constexpr int sl = decltype(slot)::value;
+    if (64 * st + 64 <= Tn) {
+      const T* kt = kb + (int64_t)64 * st * ks;
+      const T* vt = vb + (int64_t)64 * st * vs;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        dma16s(kt, ko[i], reinterpret_cast<char*>(Kb[sl]) + 1024 * (2 * w + i));
+        dma16s(vt, vo[i], reinterpret_cast<char*>(Vb[sl]) + 1024 * (2 * w + i));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        dma_tile64<T>(kb, ks, 64 * st, Tn, Kb[sl], 2 * w + i, lane);
+        dma_tile64<T>(vb, vs, 64 * st, Tn, Vb[sl], 2 * w + i, lane);
+      }
     }
-  };
-  // decay: c of the tile's keys (rows past T repeat the last one; masked)
-  auto load_c = [&](int st) __attribute__((always_inline)) {
+    // decay: c of the tile's keys (rows past T repeat the last one; masked)
     if constexpr (DECAY) {
-      if (w == 0) dma4(c + ((int64_t)b * Tn + min(64 * st + lane, Tn - 1)) * HQ + hq, Cs[st & 1]);
+      if (w == 0) dma4(c + ((int64_t)b * Tn + min(64 * st + lane, Tn - 1)) * HQ + hq, Cs[sl]);
     }
   };
-  vm_drain();  // q (and c) of this wave's queries are in registers
-  issue(0);
-  load_c(0);
-  for (int st = 0; st < nst; ++st) {
-    const int s0 = st * 64, buf = st & 1;
-    // tile st landed (own copies) and every wave passed tile st - 1
-    vm_wait_barrier<0>();
-    if (st + 1 < nst) {
-      issue(st + 1);
-      load_c(st + 1);
-    }
+  // copies per tile and wave: two of K, two of V, c by wave 0
+  const int ops = 4 + (DECAY && w == 0 ? 1 : 0);
+
+  auto step = [&](int st, auto slot) __attribute__((always_inline)) {
+    constexpr int buf = decltype(slot)::value;
+    const int s0 = st * 64;
+    // tile st landed (only tile st + 1's copies may be in flight) and every
+    // wave passed tile st - 1, whose slot tile st + 2 takes
+    vm_wait_barrier_n(st + 1 < nst ? ops : 0);
+    if (st + 2 < nst) issue(st + 2, IC<(buf + 2) % NB>{});
     const T* Ks = Kb[buf];
     const T* Vs = Vb[buf];
-    if (!(s0 > tw + 31 || tw >= Tn)) {
-      const bool need_mask = (s0 + 63 > tw) || (s0 + 64 > Tn);
-      f32x16 a[2];
+    if (s0 > tw + 31 || tw >= Tn) return;
+    const bool need_mask = (s0 + 63 > tw) || (s0 + 64 > Tn);
+    f32x16 a[2];
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-        a[sb] = f32x16{};
-        const int krow = 32 * sb + cl;
-        if constexpr (!SUM) {
+    for (int sb = 0; sb < 2; ++sb) {
+      a[sb] = f32x16{};
+      const int krow = 32 * sb + cl;
+      if constexpr (!SUM) {
 #pragma unroll
-          for (int g = 0; g < M; ++g) {
+        for (int g = 0; g < M; ++g) {
+          f32x16 r{};
+#pragma unroll
+          for (int kk = 0; kk < KE; ++kk)
+            r = mma(tile_ld8<T>(Ks, krow, g * E + 16 * kk + 8 * hh), qop[g * KE + kk], r);
+          a[sb] += r * r;
+        }
+      } else {
+#pragma unroll
+        for (int gi = 0; gi < M; ++gi) {
+#pragma unroll
+          for (int gj = 0; gj < M; ++gj) {
             f32x16 r{};
 #pragma unroll
             for (int kk = 0; kk < KE; ++kk)
-              r = mma(tile_ld8<T>(Ks, krow, g * E + 16 * kk + 8 * hh), qop[g * KE + kk], r);
+              r = mma(tile_ld8<T>(Ks, krow, gj * E + 16 * kk + 8 * hh), qop[gi * KE + kk], r);
             a[sb] += r * r;
           }
-        } else {
-#pragma unroll
-          for (int gi = 0; gi < M; ++gi) {
-#pragma unroll
-            for (int gj = 0; gj < M; ++gj) {
-              f32x16 r{};
-#pragma unroll
-              for (int kk = 0; kk < KE; ++kk)
-                r = mma(tile_ld8<T>(Ks, krow, gj * E + 16 * kk + 8 * hh), qop[gi * KE + kk], r);
-              a[sb] += r * r;
-            }
-          }
-        }
-        if constexpr (DECAY) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const f32x4 cs = *reinterpret_cast<const f32x4*>(&Cs[buf][32 * sb + 8 * i + 4 * hh]);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) a[sb][4 * i + r] *= __expf(fminf(ct - cs[r], 0.f));
-          }
-        }
-        if (need_mask) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int s = s0 + 32 * sb + 8 * i + 4 * hh + r;
-              if (s > tl || s >= Tn) a[sb][4 * i + r] = 0.f;
-            }
         }
       }
-      if constexpr (kRescale) {
-        float mx = 0.f;
+      if constexpr (DECAY) {
 #pragma unroll
-        for (int sb = 0; sb < 2; ++sb)
+        for (int i = 0; i < 4; ++i) {
+          const f32x4 cs = *reinterpret_cast<const f32x4*>(&Cs[buf][32 * sb + 8 * i + 4 * hh]);
 #pragma unroll
-          for (int e = 0; e < 16; ++e) mx = fmaxf(mx, a[sb][e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        if (mx > mrun) {
-          int ex;
-          frexpf(mx, &ex);
-          const float pnew = ldexpf(1.f, 12 - max(ex, -100));
-          const float ratio = pnew / pe;
-#pragma unroll
-          for (int db = 0; db < DV / 32; ++db) oacc[db] *= ratio;
-          dpart *= ratio;
-          pe = pnew;
-          mrun = mx;
+          for (int r = 0; r < 4; ++r) a[sb][4 * i + r] *= __expf(fminf(ct - cs[r], 0.f));
         }
-        a[0] *= pe;
-        a[1] *= pe;
       }
-      // O^T[dv][t] += sum_s V^T[dv][s] P^T[s][t], V^T read transposed from V
+      if (need_mask) {
 #pragma unroll
-      for (int ks4 = 0; ks4 < 4; ++ks4) {
-        const v8_t<T> pb = c_to_b<T>(a[ks4 >> 1], ks4 & 1);
-        dpart = sum8<T>(pb, dpart);
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int db = 0; db < DV / 32; ++db)
-          oacc[db] = mma(tile_tr8<T>(Vs, 32 * (ks4 >> 1), 32 * db, ks4 & 1, lane), pb, oacc[db]);
+          for (int r = 0; r < 4; ++r) {
+            const int s = s0 + 32 * sb + 8 * i + 4 * hh + r;
+            if (s > tl || s >= Tn) a[sb][4 * i + r] = 0.f;
+          }
       }
     }
+    if constexpr (kRescale) {
+      float mx = 0.f;
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, a[sb][e]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      if (mx > mrun) {
+        int ex;
+        frexpf(mx, &ex);
+        const float pnew = ldexpf(1.f, 12 - max(ex, -100));
+        const float ratio = pnew / pe;
+#pragma unroll
+        for (int db = 0; db < DV / 32; ++db) oacc[db] *= ratio;
+        dpart *= ratio;
+        pe = pnew;
+        mrun = mx;
+      }
+      a[0] *= pe;
+      a[1] *= pe;
+    }
+    // O^T[dv][t] += sum_s V^T[dv][s] P^T[s][t], V^T read transposed from V
+#pragma unroll
+    for (int ks4 = 0; ks4 < 4; ++ks4) {
+      const v8_t<T> pb = c_to_b<T>(a[ks4 >> 1], ks4 & 1);
+      dpart = sum8<T>(pb, dpart);
+#pragma unroll
+      for (int db = 0; db < DV / 32; ++db)
+        oacc[db] = mma(tile_tr8<T>(Vs, 32 * (ks4 >> 1), 32 * db, ks4 & 1, lane), pb, oacc[db]);
+    }
+  };
+
+  vm_drain();  // q (and c) of this wave's queries are in registers
+  issue(0, IC<0>{});
+  if (nst > 1) issue(1, IC<1>{});
+  for (int st = 0; st < nst; st += NB) {
+    step(st, IC<0>{});
+    if (st + 1 < nst) step(st + 1, IC<1>{});
+    if (st + 2 < nst) step(st + 2, IC<2>{});
   }
 
   const float dsum = dpart + __shfl_xor(dpart, 32);
