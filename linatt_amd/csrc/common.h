@@ -125,9 +125,14 @@ __device__ __forceinline__ void dma16(const void* p, void* lds_base) {
 __device__ __forceinline__ void dma16s(const void* sbase, unsigned voff, void* lds_base) {
   const unsigned m0 = __builtin_amdgcn_readfirstlane(
       (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)lds_base);
+  // the base is wave-uniform by contract; readfirstlane lets the compiler
+  // keep it in SGPRs where it cannot prove that itself
+  const uint64_t a = (uint64_t)(uintptr_t)sbase;
+  const uint64_t u = ((uint64_t)__builtin_amdgcn_readfirstlane((unsigned)(a >> 32)) << 32) |
+                     (unsigned)__builtin_amdgcn_readfirstlane((unsigned)a);
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :
-               : "v"(voff), "s"(sbase), "s"(m0)
+               : "v"(voff), "s"(u), "s"(m0)
                : "memory", "m0");
 }
 
@@ -176,12 +181,6 @@ __device__ __forceinline__ void vm_wait_barrier() {
   static_assert(N >= 0 && N <= 63, "vmcnt range");
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"i"(N) : "memory");
 }
-
-// Compile-time integer as a value, for lambdas unrolled over ring slots.
-template <int N>
-struct IC {
-  static constexpr int value = N;
-};
 
 // vm_wait_barrier for a wave-uniform count n in [0, 6] (the counter field is
 // an immediate); larger n waits for everything.

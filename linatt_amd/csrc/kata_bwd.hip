@@ -508,11 +508,31 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
 
   const int s_end = min(t0 + 128, Tn);
   const int nst = (s_end + 63) / 64;
-  auto issue = [&](int st) __attribute__((always_inline)) {
+  // tile st: copies 2w and 2w + 1 of K and of V by wave w (full tiles from a
+  // scalar base plus these per-lane offsets; the last tile clamps its rows)
+  unsigned ko[2], vo[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      dma_tile64<T>(kb, ks, 64 * st, Tn, Kb[st % NB], 2 * w + i, lane);
-      dma_tile64<T>(vb, vs, 64 * st, Tn, Vb[st % NB], 2 * w + i, lane);
+  for (int i = 0; i < 2; ++i) {
+    ko[i] = tile_lane_off(2 * w + i, lane, (int)(ks * sizeof(T)));
+    vo[i] = tile_lane_off(2 * w + i, lane, (int)(vs * sizeof(T)));
+  }
+  auto issue = [&](int st) __attribute__((always_inline)) {
+    char* kd = reinterpret_cast<char*>(Kb[st % NB]);
+    char* vd = reinterpret_cast<char*>(Vb[st % NB]);
+    if (64 * st + 64 <= Tn) {
+      const T* kt = kb + (int64_t)64 * st * ks;
+      const T* vt = vb + (int64_t)64 * st * vs;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        dma16s(kt, ko[i], kd + 1024 * (2 * w + i));
+        dma16s(vt, vo[i], vd + 1024 * (2 * w + i));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        dma_tile64<T>(kb, ks, 64 * st, Tn, reinterpret_cast<T*>(kd), 2 * w + i, lane);
+        dma_tile64<T>(vb, vs, 64 * st, Tn, reinterpret_cast<T*>(vd), 2 * w + i, lane);
+      }
     }
   };
   auto load_c = [&](int st) __attribute__((always_inline)) {
@@ -674,14 +694,34 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
   // query tiles (hq, tt) of this key tile, flattened over the G query heads
   const int ntt = (Tn + 63) / 64, tt0 = s0 / 64, nq = ntt - tt0;
   const int ntiles = G * nq;
+  // tile n: copies 2w and 2w + 1 of q and of dO by wave w (full tiles from a
+  // scalar base plus these per-lane offsets; a head's last tile clamps rows)
+  unsigned qo[2], oo[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    qo[i] = tile_lane_off(2 * w + i, lane, (int)(qs * sizeof(T)));
+    oo[i] = tile_lane_off(2 * w + i, lane, (int)(os * sizeof(T)));
+  }
   auto issue = [&](int n) __attribute__((always_inline)) {
     const int hq = h * G + n / nq, t0 = 64 * (tt0 + n % nq);
     const T* qb = q + ((int64_t)b * Tn) * qs + (int64_t)hq * DK;
     const T* ob = dout + ((int64_t)b * Tn) * os + (int64_t)hq * DV;
+    char* qd = reinterpret_cast<char*>(Qb[n % NB]);
+    char* od = reinterpret_cast<char*>(Ob[n % NB]);
+    if (t0 + 64 <= Tn) {
+      const T* qt = qb + (int64_t)t0 * qs;
+      const T* ot = ob + (int64_t)t0 * os;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      dma_tile64<T>(qb, qs, t0, Tn, Qb[n % NB], 2 * w + i, lane);
-      dma_tile64<T>(ob, os, t0, Tn, Ob[n % NB], 2 * w + i, lane);
+      for (int i = 0; i < 2; ++i) {
+        dma16s(qt, qo[i], qd + 1024 * (2 * w + i));
+        dma16s(ot, oo[i], od + 1024 * (2 * w + i));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        dma_tile64<T>(qb, qs, t0, Tn, reinterpret_cast<T*>(qd), 2 * w + i, lane);
+        dma_tile64<T>(ob, os, t0, Tn, reinterpret_cast<T*>(od), 2 * w + i, lane);
+      }
     }
   };
   // per-row data of a query tile: -delta and scale^2/den as the dq kernel

@@ -281,7 +281,7 @@ __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
     // tile st landed (only tile st + 1's copies may be in flight) and every
     // wave passed tile st - 1, whose slot tile st + 2 takes
     vm_wait_barrier_n(st + 1 < nst ? ops : 0);
-    if (st + 2 < nst) issue(st + 2, IC<(buf + 2) % NB>{});
+    if (st + 2 < nst) issue(st + 2, IntC<(buf + 2) % NB>{});
     const T* Ks = Kb[buf];
     const T* Vs = Vb[buf];
     if (s0 > tw + 31 || tw >= Tn) return;
@@ -364,12 +364,12 @@ __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
   };
 
   vm_drain();  // q (and c) of this wave's queries are in registers
-  issue(0, IC<0>{});
-  if (nst > 1) issue(1, IC<1>{});
+  issue(0, IntC<0>{});
+  if (nst > 1) issue(1, IntC<1>{});
   for (int st = 0; st < nst; st += NB) {
-    step(st, IC<0>{});
-    if (st + 1 < nst) step(st + 1, IC<1>{});
-    if (st + 2 < nst) step(st + 2, IC<2>{});
+    step(st, IntC<0>{});
+    if (st + 1 < nst) step(st + 1, IntC<1>{});
+    if (st + 2 < nst) step(st + 2, IntC<2>{});
   }
 
   const float dsum = dpart + __shfl_xor(dpart, 32);
