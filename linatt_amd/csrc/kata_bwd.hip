@@ -761,8 +761,10 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
     if (!(t0 + 63 < sw || sw >= Tn)) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
+        // a block wholly before this wave's keys (diagonal tiles only) is all
+        // masked below and adds zeros: no early exit, whose join costs
+        // accumulator copies on every block
         const int tb = t0 + 32 * mb;
-        if (tb + 31 < sw) continue;
         const bool need_mask = (tb < sw + 31) || (tb + 32 > Tn);
         auto masked = [&](int e) {
           const int t = tb + 8 * (e >> 2) + 4 * hh + (e & 3);
