@@ -317,7 +317,7 @@ def main():
     o = torch.empty_like(vd)
     den = torch.empty(B, T, H, device=dev, dtype=torch.float32)
     dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
-    ws = torch.empty(L.linatt_kata_bwd_workspace_bytes(B, T, H) // 4, device=dev,
+    ws = torch.empty(L.linatt_kata_bwd_workspace_bytes(B, T, H, D, _lib.LINATT_BFLOAT16) // 4, device=dev,
                      dtype=torch.float32)
     P = _lib.ptr
     dt = _lib.LINATT_BFLOAT16

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define LINATT_ABI_VERSION 2
+#define LINATT_ABI_VERSION 3
 
 enum linatt_dtype { LINATT_FLOAT32 = 0, LINATT_BFLOAT16 = 1, LINATT_FLOAT16 = 2 };
 enum linatt_kata_variant { LINATT_KATA_CONCAT = 0, LINATT_KATA_SUM = 1 };
@@ -55,9 +55,11 @@ int linatt_kata_fwd(const void* q, const void* k, const void* v, const float* c,
                     float* den, int B, int T, int HQ, int H, int dk, int dv, int num_groups,
                     float scale, int variant, int dtype, void* stream);
 
-/* Bytes of float32 workspace linatt_kata_bwd needs: two (B, T, HQ) arrays,
- * -<o, dO> and scale^2 / den per row. */
-size_t linatt_kata_bwd_workspace_bytes(int B, int T, int HQ);
+/* Bytes of workspace linatt_kata_bwd needs: two (B, T, HQ) float32 arrays
+ * (-<o, dO> and scale^2 / den per row) and, for LINATT_BFLOAT16, dO scaled by
+ * scale^2 / den (B, T, HQ, dv_dim), which the dk/dv pass reads instead of dO.
+ * ABI 3 added dv_dim and dtype. */
+size_t linatt_kata_bwd_workspace_bytes(int B, int T, int HQ, int dv_dim, int dtype);
 
 /* KATA-SPD causal attention backward: dq, dk, dv from q, k, v, o, den, dO.
  * Replaces parallel_kata_attn_bwd_triton (kata/parallel_kata_attn.py:364-529;
@@ -66,7 +68,8 @@ size_t linatt_kata_bwd_workspace_bytes(int B, int T, int HQ);
  * kernels kata/kernels/parallel_kata_sum.py:7-825).  Unlike the reference it
  * also covers GQA (HQ = G*H) and every compiled M without a host fallback.
  *   dq (B,T,HQ,dk), dk (B,T,H,dk), dv (B,T,H,dv) [dtype], fully overwritten.
- *   workspace: linatt_kata_bwd_workspace_bytes(B,T,HQ) bytes, 16-byte aligned.
+ *   workspace: linatt_kata_bwd_workspace_bytes(B,T,HQ,dv,dtype) bytes, 256-byte
+ *   aligned.
  */
 int linatt_kata_bwd(const void* q, const void* k, const void* v, const void* o,
                     const float* den, const void* dout, void* dq, void* dk, void* dv,

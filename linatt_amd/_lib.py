@@ -18,7 +18,7 @@ LIB_PATH = os.environ.get(
     os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "liblinatt_hip.so"),
 )
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 LINATT_FLOAT32, LINATT_BFLOAT16, LINATT_FLOAT16 = 0, 1, 2
 LINATT_KATA_CONCAT, LINATT_KATA_SUM = 0, 1
@@ -37,7 +37,7 @@ SIGNATURES = {
     "linatt_last_error": (ctypes.c_char_p, []),
     "linatt_kata_supported": (_i, [_i, _i, _i, _i, _i, _i]),
     "linatt_kata_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _i, _i, _vp]),
-    "linatt_kata_bwd_workspace_bytes": (_sz, [_i, _i, _i]),
+    "linatt_kata_bwd_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "linatt_kata_bwd": (_i, [_vp] * 10 + [_i] * 7 + [_f, _i, _i, _vp]),
     "linatt_kata_bwd_dq": (_i, [_vp] * 10 + [_i] * 7 + [_f, _i, _i, _vp]),
     "linatt_kata_bwd_decay": (_i, [_vp] * 12 + [_i] * 7 + [_f, _i, _vp]),

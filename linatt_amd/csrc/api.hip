@@ -214,9 +214,12 @@ int linatt_kata_fwd(const void* q, const void* k, const void* v, const float* c,
   return LINATT_OK;
 }
 
-size_t linatt_kata_bwd_workspace_bytes(int B, int T, int HQ) {
-  if (B <= 0 || T <= 0 || HQ <= 0) return 0;
-  return 2 * (size_t)B * T * HQ * sizeof(float);
+size_t linatt_kata_bwd_workspace_bytes(int B, int T, int HQ, int dv_dim, int dtype) {
+  if (B <= 0 || T <= 0 || HQ <= 0 || dv_dim <= 0) return 0;
+  const int64_t rows = (int64_t)B * T * HQ;
+  // bf16: the dk/dv pass reads dO prescaled by scale^2/den (written by dq)
+  const size_t dop = dtype == LINATT_BFLOAT16 ? (size_t)rows * dv_dim * 2 : 0;
+  return linatt::kata_dop_offset(rows) + dop;
 }
 
 // Shared body of the three backward entry points; `parts` selects the

@@ -475,24 +475,54 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
 #pragma unroll
   for (int kk = 0; kk < DK / 16; ++kk)
     qop[kk] = tvalid ? ld8<T>(q + qrow * DK + 16 * kk + 8 * hh) : zero8<T>();
-  float dpart = 0.f;
+  // bf16: the dk/dv kernel takes dO scaled by scale^2/den (the row scale of P
+  // and of dA), which saves it two products per score, and the matching
+  // delta' = <o, dO'> from the same rounded dO', so x' = dO' v - delta' keeps
+  // the cancellation of x = dO v - delta (zero for a lone key)
+  constexpr bool kPre = __is_same(T, __bf16);
+  float pdl = 0.f;
+  if (tvalid) {
+    const float d = den[qrow];
+    pdl = scale2 / (d > 0.f ? d : 1.f);
+  }
+  float dpart = 0.f, dppart = 0.f;
 #pragma unroll
   for (int kk = 0; kk < DV / 16; ++kk) {
     doop[kk] = tvalid ? ld8<T>(dout + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
     const v8_t<T> ov = tvalid ? ld8<T>(o + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
 #pragma unroll
-    for (int j = 0; j < 8; ++j) dpart += (float)ov[j] * (float)doop[kk][j];
-  }
-  const float delta = dpart + __shfl_xor(dpart, 32);
-  float pdl = 0.f;
-  if (tvalid) {
-    const float d = den[qrow];
-    pdl = scale2 / (d > 0.f ? d : 1.f);
-    if (hh == 0) {
-      delta_out[qrow] = -delta;
-      delta_out[(int64_t)nbh * Tn + qrow] = pdl;
+    for (int j = 0; j < 8; ++j) {
+      dpart += (float)ov[j] * (float)doop[kk][j];
+      if constexpr (kPre) dppart += (float)ov[j] * (float)(T)((float)doop[kk][j] * pdl);
     }
   }
+  const float delta = dpart + __shfl_xor(dpart, 32);
+  const float deltap = dppart + __shfl_xor(dppart, 32);
+  // the per-row terms for the dk/dv kernel, stored once q and dO have landed
+  // (right after the drain below, so no wait covers these stores; the key
+  // loop's copy waits stay exact because loads complete in order among
+  // themselves)
+  auto write_rows = [&]() __attribute__((always_inline)) {
+    if constexpr (kPre) {
+      // recomputed here, not kept from the delta' sum above: an opaque copy of
+      // the scale stops the compiler from carrying dO' through the loop
+      float ps = pdl;
+      asm volatile("" : "+v"(ps));
+      T* dop = reinterpret_cast<T*>(reinterpret_cast<char*>(delta_out) + kata_dop_offset((int64_t)nbh * Tn)) +
+               qrow * DV;
+#pragma unroll
+      for (int kk = 0; kk < DV / 16; ++kk) {
+        v8_t<T> y;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = (T)((float)doop[kk][j] * ps);
+        if (tvalid) *reinterpret_cast<v8_t<T>*>(dop + 16 * kk + 8 * hh) = y;
+      }
+    }
+    if (tvalid && hh == 0) {
+      delta_out[qrow] = kPre ? -deltap : -delta;
+      delta_out[(int64_t)nbh * Tn + qrow] = pdl;
+    }
+  };
 
   f32x16 acc[DK / 32];
 #pragma unroll
@@ -542,6 +572,7 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
   };
   const int ops = 4 + (DECAY && w == 0 ? 1 : 0);  // copies per tile and wave
   vm_drain();  // q, dO (and c) of this wave's queries are in registers
+  write_rows();
 #pragma unroll
   for (int st = 0; st < NB - 1; ++st)
     if (st < nst) {
@@ -655,6 +686,8 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
   __shared__ __attribute__((aligned(16))) float Pd[NB][64];  // scale^2 / den
   __shared__ __attribute__((aligned(16))) float Ct[NB][64];
   __shared__ __attribute__((aligned(16))) T Zr[8];
+  // this wave's k and v rows as MFMA B operands (lane l: 16 bytes per k-step)
+  __shared__ __attribute__((aligned(16))) u32x4 KVop[4][(DK + DV) / 16][64];
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -671,17 +704,26 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
   const int64_t qs = (int64_t)HQ * DK, os = (int64_t)HQ * DV;
   const int64_t krow = ((int64_t)b * Tn + sl) * H + h;
 
-  v8_t<T> kop[DK / 16], vop[DV / 16];
 #pragma unroll
   for (int kk = 0; kk < DK / 16; ++kk)
-    kop[kk] = svalid ? ld8<T>(k + krow * DK + 16 * kk + 8 * hh) : zero8<T>();
+    KVop[w][kk][lane] = __builtin_bit_cast(u32x4, svalid ? ld8<T>(k + krow * DK + 16 * kk + 8 * hh) : zero8<T>());
 #pragma unroll
   for (int kk = 0; kk < DV / 16; ++kk)
-    vop[kk] = svalid ? ld8<T>(v + krow * DV + 16 * kk + 8 * hh) : zero8<T>();
+    KVop[w][DK / 16 + kk][lane] = __builtin_bit_cast(u32x4, svalid ? ld8<T>(v + krow * DV + 16 * kk + 8 * hh) : zero8<T>());
+  auto kop = [&](int kk) __attribute__((always_inline)) { return __builtin_bit_cast(v8_t<T>, KVop[w][kk][lane]); };
+  auto vop = [&](int kk) __attribute__((always_inline)) { return __builtin_bit_cast(v8_t<T>, KVop[w][DK / 16 + kk][lane]); };
 
-  f32x16 dka[DK / 32], dva[DV / 32];
+  // concat groups narrower than 32 (E = 16): dK^T rows of two groups share a
+  // 32-row MFMA block, and group gk's product fills the other group's rows
+  // with values that are never used; they go to an accumulator of their own
+  // per group parity instead of zeroing half the operand
+  constexpr bool kPar = !SUM && E < 32;
+  constexpr int NP = kPar ? 2 : 1;
+  f32x16 dka[NP][DK / 32], dva[DV / 32];
 #pragma unroll
-  for (int rb = 0; rb < DK / 32; ++rb) dka[rb] = f32x16{};
+  for (int p = 0; p < NP; ++p)
+#pragma unroll
+    for (int rb = 0; rb < DK / 32; ++rb) dka[p][rb] = f32x16{};
 #pragma unroll
   for (int db = 0; db < DV / 32; ++db) dva[db] = f32x16{};
 
@@ -702,10 +744,15 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
     qo[i] = tile_lane_off(2 * w + i, lane, (int)(qs * sizeof(T)));
     oo[i] = tile_lane_off(2 * w + i, lane, (int)(os * sizeof(T)));
   }
+  // bf16: dO and delta come prescaled by scale^2/den from the dq kernel
+  constexpr bool kPre = __is_same(T, __bf16);
+  const int64_t nrows = (int64_t)(nbh / H) * Tn * HQ;
+  const T* dsrc = kPre ? reinterpret_cast<const T*>(reinterpret_cast<const char*>(delta) + kata_dop_offset(nrows))
+                       : dout;
   auto issue = [&](int n) __attribute__((always_inline)) {
     const int hq = h * G + n / nq, t0 = 64 * (tt0 + n % nq);
     const T* qb = q + ((int64_t)b * Tn) * qs + (int64_t)hq * DK;
-    const T* ob = dout + ((int64_t)b * Tn) * os + (int64_t)hq * DV;
+    const T* ob = dsrc + ((int64_t)b * Tn) * os + (int64_t)hq * DV;
     char* qd = reinterpret_cast<char*>(Qb[n % NB]);
     char* od = reinterpret_cast<char*>(Ob[n % NB]);
     if (t0 + 64 <= Tn) {
@@ -724,10 +771,9 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
       }
     }
   };
-  // per-row data of a query tile: -delta and scale^2/den as the dq kernel
-  // wrote them (rows [0, B T HQ) and [B T HQ, 2 B T HQ) of `delta`), and c;
-  // rows past T repeat the last one and are masked
-  const int64_t nrows = (int64_t)(nbh / H) * Tn * HQ;
+  // per-row data of a query tile: -delta (bf16: prescaled) and scale^2/den
+  // as the dq kernel wrote them (rows [0, B T HQ) and [B T HQ, 2 B T HQ) of
+  // `delta`), and c; rows past T repeat the last one and are masked
   auto load_rows = [&](int n) __attribute__((always_inline)) {
     const int hq = h * G + n / nq, t = min(64 * (tt0 + n % nq) + lane, Tn - 1);
     const int64_t r = ((int64_t)b * Tn + t) * HQ + hq;
@@ -774,30 +820,39 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const f32x4 d4 = *reinterpret_cast<const f32x4*>(&Dl[buf][32 * mb + 8 * i + 4 * hh]);
-          const f32x4 p4 = *reinterpret_cast<const f32x4*>(&Pd[buf][32 * mb + 8 * i + 4 * hh]);
+          const f32x4 p4 = kPre ? f32x4{} : *reinterpret_cast<const f32x4*>(&Pd[buf][32 * mb + 8 * i + 4 * hh]);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             x[4 * i + r] = d4[r];
             pdv[4 * i + r] = p4[r];
           }
         }
-        // the causal / past-T mask rides on the row scale scale^2/den, which
-        // multiplies both x (into xs) and A (into P): zero where masked.  Its
-        // branch closes before the products, which stay one basic block.
-        if (need_mask) {
+        // fp16: the causal / past-T mask rides on the row scale scale^2/den,
+        // which multiplies both x (into xs) and A (into P): zero where masked.
+        // Its branch closes before the products, which stay one basic block.
+        if (!kPre && need_mask) {
 #pragma unroll
           for (int e = 0; e < 16; ++e) pdv[e] = masked(e) ? 0.f : pdv[e];
         }
-        // x[t][s] = dO V^T - delta  (rows t, column s)
+        // x[t][s] = dO V^T - delta  (rows t, column s; bf16: both prescaled)
 #pragma unroll
         for (int kk = 0; kk < DV / 16; ++kk)
-          x = mma(tile_ld8<T>(Os, 32 * mb + cl, 16 * kk + 8 * hh), vop[kk], x);
+          x = mma(tile_ld8<T>(Os, 32 * mb + cl, 16 * kk + 8 * hh), vop(kk), x);
         if constexpr (DECAY) {
 #pragma unroll
           for (int e = 0; e < 16; ++e)
             x[e] *= __expf(fminf(Ct[buf][32 * mb + 8 * (e >> 2) + 4 * hh + (e & 3)] - csl, 0.f));
         }
-        const f32x16 xs = x * pdv;
+        f32x16 xs;
+        if constexpr (kPre) {
+          xs = x;
+          if (need_mask) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) xs[e] = masked(e) ? 0.f : xs[e];
+          }
+        } else {
+          xs = x * pdv;
+        }
         // per (query group gi, key group gk): r = Q_gi K_gk^T, A += r^2 and
         // dK^T[(gk,e)][s] += sum_t Q^T[(gi,e)][t] r[t][s] xs[t][s]
         f32x16 A{};
@@ -809,7 +864,7 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
             f32x16 r{};
 #pragma unroll
             for (int kk = 0; kk < KE; ++kk)
-              r = mma(tile_ld8<T>(Qs, 32 * mb + cl, gi * E + 16 * kk + 8 * hh), kop[gk * KE + kk], r);
+              r = mma(tile_ld8<T>(Qs, 32 * mb + cl, gi * E + 16 * kk + 8 * hh), kop(gk * KE + kk), r);
             A += r * r;
             const f32x16 da = r * xs;
 #pragma unroll
@@ -817,7 +872,10 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
               const v8_t<T> bop = c_to_b<T>(da, j);
 #pragma unroll
               for (int rb = (gk * E) / 32; rb <= ((gk + 1) * E - 1) / 32; ++rb)
-                dka[rb] = mma(qt_op(Qs, mb, gi, gk, rb, j), bop, dka[rb]);
+                if constexpr (kPar)
+                  dka[gk & 1][rb] = mma(tile_tr8<T>(Qs, 32 * mb, 32 * rb, j, lane), bop, dka[gk & 1][rb]);
+                else
+                  dka[0][rb] = mma(qt_op(Qs, mb, gi, gk, rb, j), bop, dka[0][rb]);
             }
             // sum and decay variants: keep the next group's score MFMAs from
             // being hoisted above this group's products (bounds the live
@@ -833,8 +891,18 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
             A[e] *= __expf(fminf(dd, 0.f));
           }
         }
-        // fp16 keeps P in [0, 2^12] (subnormal range); undone at the store
-        const f32x16 P = A * (pdv * kPScale);
+        // bf16: P = A against the prescaled dO; fp16 keeps P in [0, 2^12]
+        // (subnormal range), undone at the store
+        f32x16 P;
+        if constexpr (kPre) {
+          P = A;
+          if (need_mask) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) P[e] = masked(e) ? 0.f : P[e];
+          }
+        } else {
+          P = A * (pdv * kPScale);
+        }
         // dV^T[dv][s] += sum_t dO^T[dv][t] P[t][s], dO^T read transposed from dO
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -862,9 +930,12 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
     for (int rb = 0; rb < DK / 32; ++rb)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
+      {
+        // rows 8i + 4hh + 0..3 of the block: i < 2 the even group, else the odd
+        const f32x16& d = dka[kPar && i >= 2 ? 1 : 0][rb];
         st4<T>(dkrow + 32 * rb + 8 * i + 4 * hh,
-               to4<T>(2.f * dka[rb][4 * i], 2.f * dka[rb][4 * i + 1], 2.f * dka[rb][4 * i + 2],
-                      2.f * dka[rb][4 * i + 3]));
+               to4<T>(2.f * d[4 * i], 2.f * d[4 * i + 1], 2.f * d[4 * i + 2], 2.f * d[4 * i + 3]));
+      }
 #pragma unroll
     for (int db = 0; db < DV / 32; ++db)
 #pragma unroll

@@ -6,6 +6,12 @@
 
 namespace linatt {
 
+// Byte offset of the prescaled dO (bf16) in the backward workspace, after the
+// two per-row float arrays of nrows = B T HQ rows each.
+__host__ __device__ inline size_t kata_dop_offset(int64_t nrows) {
+  return ((size_t)nrows * 2 * sizeof(float) + 255) & ~(size_t)255;
+}
+
 struct KataArgs {
   const void* q;     // (B, T, HQ, DK) time-major, contiguous
   const void* k;     // (B, T, H, DK)
@@ -17,7 +23,8 @@ struct KataArgs {
   void* dq;          // (B, T, HQ, DK)
   void* dk;          // (B, T, H, DK)
   void* dv;          // (B, T, H, DV)
-  float* delta;      // (2, B, T, HQ) workspace: -<o, dO> and scale^2 / den per row
+  float* delta;      // workspace: (2, B, T, HQ) per-row -<o, dO> (bf16: times scale^2 / den)
+                     // and scale^2 / den; bf16: then dO scale^2 / den (B, T, HQ, DV)
   float* dc;         // (B, T, HQ) gradient of the cumulative log-decay c (decay backward)
   int B, T, HQ, H, DK, DV, M;
   float scale;

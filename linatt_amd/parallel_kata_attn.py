@@ -100,8 +100,8 @@ def _bwd(q, k, v, o, den, do, num_groups, scale, variant):
     dk_ = torch.empty_like(k)
     dv_ = torch.empty_like(v)
     L = _lib.load()
-    ws = torch.empty(L.linatt_kata_bwd_workspace_bytes(B, T, HQ) // 4, device=q.device,
-                     dtype=torch.float32)
+    ws = torch.empty(L.linatt_kata_bwd_workspace_bytes(B, T, HQ, dv, _lib.dtype_code(v.dtype)) // 4,
+                     device=q.device, dtype=torch.float32)
     _lib.check("linatt_kata_bwd", L.linatt_kata_bwd(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(den), _lib.ptr(do),
         _lib.ptr(dq), _lib.ptr(dk_), _lib.ptr(dv_), _lib.ptr(ws),
@@ -243,8 +243,8 @@ class _KataDecayFunction(torch.autograd.Function):
         dq, dk_, dv_ = torch.empty_like(qc), torch.empty_like(kc), torch.empty_like(vc)
         dc = torch.empty_like(cf)
         L = _lib.load()
-        ws = torch.empty(L.linatt_kata_bwd_workspace_bytes(B, T, HQ) // 4, device=q.device,
-                         dtype=torch.float32)
+        ws = torch.empty(L.linatt_kata_bwd_workspace_bytes(B, T, HQ, dv, _lib.dtype_code(vc.dtype)) // 4,
+                         device=q.device, dtype=torch.float32)
         _lib.check("linatt_kata_bwd_decay", L.linatt_kata_bwd_decay(
             _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(cf), _lib.ptr(o.contiguous()),
             _lib.ptr(den.float().contiguous()), _lib.ptr(do), _lib.ptr(dq), _lib.ptr(dk_),

@@ -40,7 +40,7 @@ def test_python_signatures_cover_header():
 
 
 def test_version_and_support(lib):
-    assert lib.linatt_abi_version() == 2
+    assert lib.linatt_abi_version() == 3
     BF16, F32, F16 = 1, 0, 2
     for dt in (BF16, F32, F16):
         for M in (1, 2, 4):
@@ -49,8 +49,11 @@ def test_version_and_support(lib):
             assert lib.linatt_kata_supported(dt, 64, 64, M, 0, 1) == 1
             assert lib.linatt_kata_supported(dt, 64, 64, M, 1, 1) == 0  # decay is concat-only
     assert lib.linatt_kata_supported(BF16, 48, 64, 3, 0, 0) == 0
-    assert lib.linatt_kata_bwd_workspace_bytes(2, 10, 3) == 2 * (2 * 10 * 3 * 4)  # -<o,dO> and scale^2/den rows
-    assert lib.linatt_kata_bwd_workspace_bytes(0, 10, 3) == 0
+    # -<o,dO> and scale^2/den rows (256-byte rounded); bf16 adds the prescaled dO
+    assert lib.linatt_kata_bwd_workspace_bytes(2, 10, 3, 64, F32) == 512  # 480 rounded up
+    assert lib.linatt_kata_bwd_workspace_bytes(2, 10, 3, 64, F16) == 512
+    assert lib.linatt_kata_bwd_workspace_bytes(2, 10, 3, 64, BF16) == 512 + 2 * 10 * 3 * 64 * 2
+    assert lib.linatt_kata_bwd_workspace_bytes(0, 10, 3, 64, BF16) == 0
 
 
 FAKE = ctypes.c_void_p(1 << 20)  # aligned, never dereferenced on the host
