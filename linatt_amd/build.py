@@ -34,6 +34,9 @@ CFLAGS = [
     "-fPIC",
     "-ffp-contract=fast",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the kernels touch them with VALU ops, and
+    # AGPR-held accumulators cost a v_accvgpr_read per element each time
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-command-line-argument",
     "-I", os.path.join(ROOT, "include"),
 ]
