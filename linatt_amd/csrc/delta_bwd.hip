@@ -301,33 +301,45 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 2: dq, dW, the output/state part of dk and of dG.  One workgroup of
-// eight waves per chunk.  Input tiles arrive by direct copies issued at the
-// start in the order of use, so the dq / dW products run while the tiles of
-// the later phases are still landing (rows past T repeat the last valid row
-// and are masked where they could reach a result).  Wave w owns the 32 x 32
-// output blocks (rows 32 (w & 1) .., key dims 32 (w >> 1) ..):
+// Kernel 2: everything of the backward that is local to a chunk: dq, then
+// dk, dv, dbeta and dg through W = Tm diag(beta e^G) K and
+// U = Tm diag(beta) V, Tm = (I + A)^-1.  One workgroup of eight waves per
+// chunk.  Input tiles arrive by direct copies issued at the start in the
+// order of use, so the dq / dW products run while the tiles of the later
+// phases are still landing (rows past T repeat the last valid row and are
+// masked where they could reach a result); Tm and V follow once the state
+// tiles are consumed.  Wave w owns the 32 x 32 output blocks with rows
+// 32 (w & 1) .. and key / value columns 32 (w >> 1) ..:
 //   1a. dq = scale e^G dO S^T and dW = -dVn S^T            (S, dVn, dO, q)
 //   1b. dKs = e^(gamma - G) Vn dS'^T                        (dS', Vn, k);
 //       waves 0-2: the nonzero blocks of X = dO Vn^T
 //   2.  Mq = scale X o e^(G_i-G_j) [j <= i] to an LDS tile, Z = X o Aqk
-//   3.  dq += Mq K, dKs += Mq^T Q
+//   3.  dq += Mq K, dKs += Mq^T Q; dq out, dW to LDS, dG of these terms
+//   4.  dv = diag(beta) Tm^T dU,  dk = dKs + diag(beta e^G) Tm^T dW
+//       dTm = dU (diag(beta) V)^T + dW (diag(beta e^G) K)^T   (waves 0-3)
+//       KK = K K^T, lower blocks                               (waves 4-7)
+//   5.  M^T = dTm^T Tm (waves 0-3), dA^T = -Tm M^T and
+//       P[a][l] = dA[a][l] beta_a e^(G_a - G_l) (l < a) (waves 4-7)
+//   6.  dk += (P + P^T) K; dk, dv out; dbeta and dg (reverse cumulative
+//       sum of dG within the chunk)
+// dW, dKs and the dG of phase 3 stay in LDS / registers.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
 __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, DeltaLayout L) {
   constexpr int KT = DK / 64, VT = DV / 64, TE = 64 * 64;
-  constexpr int SE0 = 2 * VT * KT * TE, SE1 = 3 * TE + 8 * 1024;
+  // St after phase 1: Mq then dTm^T / P (0 .. TE), Z^T then Q^T fp32 (TE ..
+  // 3 TE), store staging (3 TE .. 5 TE), Tm (5 TE ..), V (6 TE ..)
+  constexpr int SE0 = 2 * VT * KT * TE, SE1 = 6 * TE + VT * TE;
   constexpr int SE = SE0 > SE1 ? SE0 : SE1;
   static_assert(DK % 64 == 0 && DV % 64 == 0 && DK <= 128 && DV <= 128, "64 or 128 wide");
-  // S^T then dS'^T as [v][d] tiles (tile vt * KT + kt); after phase 1: Mq
-  // [i][j] (0 .. TE), Z^T fp32 [j][i] (TE .. 3 TE), store staging (3 TE + 1024 w)
+  // S^T then dS'^T as [v][d] tiles (tile vt * KT + kt) in phase 1
   __shared__ __attribute__((aligned(16))) T St[SE];
   __shared__ __attribute__((aligned(16))) T dVt[VT * TE];  // dVn^T [v][i]
-  __shared__ __attribute__((aligned(16))) T Vnt[VT * TE];  // Vn^T [v][j]
-  __shared__ __attribute__((aligned(16))) T Ot[VT * TE];   // dO [i][v]
-  __shared__ __attribute__((aligned(16))) T Qt[KT * TE];   // q [i][d]
+  __shared__ __attribute__((aligned(16))) T Vnt[VT * TE];  // Vn^T [v][j]; phases 4-6: reductions
+  __shared__ __attribute__((aligned(16))) T Ot[VT * TE];   // dO [i][v]; from phase 2: beta
+  __shared__ __attribute__((aligned(16))) T Qt[KT * TE];   // q [i][d]; from phase 3: dW [i][d]
   __shared__ __attribute__((aligned(16))) T Kt[KT * TE];   // k [j][d]
-  __shared__ __attribute__((aligned(16))) T At[TE];        // Aqk [i][j]
+  __shared__ __attribute__((aligned(16))) T At[TE];        // Aqk [i][j]; phase 5: M^T as [a][j]
   __shared__ __attribute__((aligned(16))) float Gs[64];
   __shared__ float red_gi[4][64], red_kd[4][64], red_rs[2][64], red_s[8];
   T* Mqt = St;
@@ -469,8 +481,17 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
                    tile_ldp8<T>(Ot + vt * TE, 32 * xib + cl, 32 * s2, jj, hh), xs);
   }
   vm_wait_barrier<0>();  // Aqk landed; the state tiles are no longer read
+  // copies for phases 4-6, landing during phases 2-3: Tm, V (rows past T
+  // repeat the last valid row; beta is zeroed there), beta
+  float* Bs = reinterpret_cast<float*>(Ot);
+  dma_tile64<T>((const T*)(a.ctx + L.Tm) + ci * 4096, 64, 0, 64, St + 5 * TE, w, lane);
+#pragma unroll
+  for (int vt = 0; vt < VT; ++vt)
+    dma_tile64<T>((const T*)a.v + ((size_t)b * Tn * H + h) * DV + 64 * vt, os, t0, Tn, St + 6 * TE + vt * TE, w,
+                  lane);
+  if (w == 0) dma4(a.beta + ((size_t)b * Tn + min(t0 + lane, Tn - 1)) * H + h, Bs);
 
-  // 2. Mq [i][j] tile and Z^T (waves 0-3); dW out
+  // 2. Mq [i][j] tile and Z^T (waves 0-3)
   if (w < 4) {
     const int xi = 32 * xib + cl;  // this lane's i
     const float Gi = Gs[xi];
@@ -500,8 +521,6 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
     if (hh == 0 && w < 3) red_rs[xjb][xi] = rs;
   }
   u32x4* stage = reinterpret_cast<u32x4*>(St + 3 * TE) + 128 * w;
-  if (active)
-    store_rows32<T>(dwa, stage, (T*)(a.ws + L.dW) + ((size_t)bh * Tp + t0 + 32 * lb) * DK + 32 * db, DK, lane);
   __syncthreads();
 
   // 3. dq += Mq K (rows i), dKs += Mq^T Q (rows j)
@@ -517,10 +536,6 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
       }
     store_rows32<T>(dqa, stage, (T*)a.dq + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DK + 32 * db, qks, lane,
                     Tn - (t0 + 32 * lb));
-    float* dkp = reinterpret_cast<float*>(a.ws + L.dKp) + ((size_t)bh * Tp + t0 + r) * DK + 32 * db;
-#pragma unroll
-    for (int I = 0; I < 4; ++I)
-      *reinterpret_cast<f32x4*>(dkp + 8 * I + 4 * hh) = f32x4{dka[4 * I], dka[4 * I + 1], dka[4 * I + 2], dka[4 * I + 3]};
   }
   gi += __shfl_xor(gi, 32);
   kd += __shfl_xor(kd, 32);
@@ -529,7 +544,19 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
     red_kd[db][r] = kd;
   }
   if (lane == 0) red_s[w] = sdot;
-  __syncthreads();
+  __syncthreads();  // phase 3 done: q, Mq and the staging of dq are free
+
+  // dW [i][d] into the q tiles
+  T* dWt = Qt;
+  if (active) {
+    char* t = reinterpret_cast<char*>(dWt + (db / 2) * TE);
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+      *reinterpret_cast<v4_t<T>*>(t + tile_off(r, 32 * (db & 1) + 8 * I + 4 * hh)) =
+          to4<T>(dwa[4 * I], dwa[4 * I + 1], dwa[4 * I + 2], dwa[4 * I + 3]);
+  }
+  // dG of the output / state terms, row tid (threads 0..63), kept for phase 6
+  float dGo = 0.f;
   if (tid < 64) {
     float cs = 0.f;  // column term: sum_j Z[j][i]
 #pragma unroll
@@ -543,7 +570,7 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
       kdt += red_kd[q][tid];
       git += red_gi[q][tid];
     }
-    float dG = git - kdt + (red_rs[0][tid] + red_rs[1][tid]) - cs;
+    dGo = git - kdt + (red_rs[0][tid] + red_rs[1][tid]) - cs;
     // d gamma = sum_j k_j . dKs_j + e^gamma <S, dS'>, added at row 63
     float kds = kdt;
 #pragma unroll
@@ -552,158 +579,73 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
       float st = 0.f;
 #pragma unroll
       for (int q = 0; q < 8; ++q) st += red_s[q];
-      dG += kds + (GATED ? __expf(gam) : 1.f) * st;
-    }
-    reinterpret_cast<float*>(a.ws + L.dGp)[(size_t)bh * Tp + t0 + tid] = dG;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Kernel 3: backward through W = Tm diag(beta e^G) K, U = Tm diag(beta) V,
-// Tm = (I + A)^-1; final dk, dv, dbeta, dg.  One workgroup of four waves
-// per chunk; Tm, dU^T, V, K and dW reach LDS by one up-front copy.
-//   dv  = diag(beta) Tm^T dU                       (wave: rows j, 64 v)
-//   dkW = diag(beta e^G) Tm^T dW                   (wave: rows j, 64 d)
-//   dTm = dU (diag(beta) V)^T + dW (diag(beta e^G) K)^T   (one 32 x 32 block per wave)
-//   M^T = dTm^T Tm,  dA^T = -Tm M^T                (bf16 tiles through LDS)
-//   P[a][l] = dA[a][l] beta_a e^(G_a - G_l) (l < a),  dk = dKp + dkW + (P + P^T) K
-// dbeta and dG gather the row / column sums of the same terms; dg is the
-// reverse cumulative sum of dG within the chunk.
-// ---------------------------------------------------------------------------
-template <typename T, int DK, int DV, bool GATED>
-__global__ __launch_bounds__(256, 2) void delta_wy_bwd_kernel(DeltaArgs a, DeltaLayout L) {
-  constexpr int KT = DK / 64, VT = DV / 64;
-  constexpr int TE = 64 * 64;
-  constexpr int SE = 8192 / (int)sizeof(T) * 2;            // 16 KiB of T
-  constexpr int WE = KT * TE > SE ? KT * TE : SE;          // dW tiles, then store staging
-  constexpr int XE = 2 * VT * TE > SE * 2 ? 2 * VT * TE : SE * 2;
-  static_assert(DK % 64 == 0 && DV % 64 == 0 && DK <= 128 && DV <= 128, "64 or 128 wide");
-  __shared__ __attribute__((aligned(16))) T Tmt[TE];      // Tm [i][j]
-  __shared__ __attribute__((aligned(16))) T Kt[KT * TE];  // K [j][d], tile kt: d in 64 kt..
-  __shared__ __attribute__((aligned(16))) T dWt[WE];      // dW [i][d]; phase 5: store staging
-  // dU^T [v][i] (tile vt: v in 64 vt..) and V [j][v]; after phase 1:
-  // dTm^T then P [a][l] (0 .. TE), M^T as [a][j] (TE .. 2 TE), Q^T fp32 [l][a] (2 TE ..)
-  __shared__ __attribute__((aligned(16))) T Xr[XE];
-  __shared__ float Bs[64], Gs[64];
-  __shared__ float red_b[4][64], red_g[4][64];
-  T* dUt = Xr;
-  T* Vt = Xr + VT * TE;
-  T* dTT = Xr;
-  T* Pn = Xr;
-  T* MTt = Xr + TE;
-  float* Qb = reinterpret_cast<float*>(Xr + 2 * TE);
-
-  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
-  const int cl = lane & 31, hh = lane >> 5;
-  const int Tn = a.T, H = a.H, NT = a.NT;
-  const int c = blockIdx.x % NT, bh = blockIdx.x / NT;
-  const int b = bh / H, h = bh % H;
-  const int t0 = c * kChunk;
-  const size_t Tp = (size_t)NT * kChunk;
-  const size_t ci = (size_t)bh * NT + c;
-  const int lb = w & 1, hf = w >> 1;  // lane block (output rows j / a), column half
-  const int ja = 32 * lb + cl;        // this lane's output row within the chunk
-  const int nvalid = Tn - (t0 + 32 * lb);
-
-  const T* kb = (const T*)a.k + ((size_t)b * Tn * H + h) * DK;
-  const T* vb = (const T*)a.v + ((size_t)b * Tn * H + h) * DV;
-  const int64_t ks = (int64_t)H * DK, vs = (int64_t)H * DV;
-
-  // 0. copies; beta and G (wave 3); dKp of this wave's dk blocks
-#pragma unroll
-  for (int o = 0; o < 2; ++o) {
-    const int op = 2 * w + o;
-    dma_tile64<T>((const T*)(a.ctx + L.Tm) + ci * 4096, 64, 0, 64, Tmt, op, lane);
-#pragma unroll
-    for (int vt = 0; vt < VT; ++vt) {
-      dma_tile64<T>((const T*)(a.ws + L.dVnT) + (ci * DV + 64 * vt) * 64, 64, 0, 64, dUt + vt * TE, op, lane);
-      dma_tile64<T>(vb + 64 * vt, vs, t0, Tn, Vt + vt * TE, op, lane);
-    }
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-      dma_tile64<T>(kb + 64 * kt, ks, t0, Tn, Kt + kt * TE, op, lane);
-      dma_tile64<T>((const T*)(a.ws + L.dW) + ((size_t)bh * Tp + t0) * DK + 64 * kt, DK, 0, 64, dWt + kt * TE, op,
-                    lane);
+      dGo += kds + (GATED ? __expf(gam) : 1.f) * st;
     }
   }
-  if (w == 3) {
-    const int t = t0 + lane;
-    Bs[lane] = t < Tn ? a.beta[((size_t)b * Tn + t) * H + h] : 0.f;
-    Gs[lane] = GATED ? reinterpret_cast<const float*>(a.ctx + L.Gc)[(size_t)bh * Tp + t0 + lane] : 0.f;
-  }
-  const bool has_dk = 2 * hf < DK / 32, has_dv = 2 * hf < DV / 32;
-  f32x16 dk[2];
-  if (has_dk) {
-    const float* p = reinterpret_cast<const float*>(a.ws + L.dKp) + ((size_t)bh * Tp + t0 + ja) * DK + 64 * hf;
-#pragma unroll
-    for (int m = 0; m < 2; ++m)
-#pragma unroll
-      for (int I = 0; I < 4; ++I) {
-        const f32x4 v4 = *reinterpret_cast<const f32x4*>(p + 32 * m + 8 * I + 4 * hh);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dk[m][4 * I + r] = v4[r];
-      }
-  }
-  vm_wait_barrier<0>();
+  vm_wait_barrier<0>();  // Tm, V and beta landed; dW written; Z^T no longer read
 
-  const float Bj = Bs[ja], Gj = Gs[ja];
+  // 4.-6. backward through W and U.  dU = dVn (dU^T tiles in dVt); rows j,
+  // a and l index the chunk; this lane's row is r; column block cb = w >> 1, hf = cb & 1.
+  const T* Tmt = St + 5 * TE;        // Tm [i][j]
+  const T* Vt = St + 6 * TE;         // V [j][v]
+  T* const PT = St;                  // dTm^T [j][i], then P [a][l]
+  T* const MTt = At;                 // M^T as [a][j]
+  float* const Qb = Zt;              // Q^T fp32 [l][a]
+  float* const red_b = reinterpret_cast<float*>(Vnt);  // [8][64]
+  float* const red_g = red_b + 8 * 64;                 // [8][64]
+  const int cb = w >> 1, hf = cb & 1;
+  const bool has_dv = cb < DV / 32;
+  const bool lower = hf <= lb;
+  const float Bj = t0 + r < Tn ? Bs[r] : 0.f, Gj = Gs[r];
   const float eGj = GATED ? __expf(Gj) : 1.f;
   float db_part = 0.f, dg_part = 0.f, rq_part = 0.f;
 
-  // 1a. dv[j][v] = beta_j (Tm^T dU)[j][v] as D[v][j] = sum_i dU^T[v][i] Tm[i][j]
-  f32x16 dv[2];
+  // 4a. dv[j][v] = beta_j (Tm^T dU)[j][v], values 32 cb .., as D[v][j]
+  f32x16 dvx{};
   if (has_dv) {
+    const T* du = dVt + (cb / 2) * TE;
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int vb2 = 2 * hf + m;
-      const T* du = dUt + (vb2 / 2) * TE;
-      dv[m] = f32x16{};
+    for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
-      for (int ib = 0; ib < 2; ++ib)
+      for (int jj = 0; jj < 2; ++jj)
+        dvx = mma(tile_ldp8<T>(du, 32 * (cb & 1) + cl, 32 * ib, jj, hh), tile_tr8<T>(Tmt, 32 * ib, 32 * lb, jj, lane),
+                  dvx);
+    // dbeta_j += v_j . (Tm^T dU)_j
+    const char* vt = reinterpret_cast<const char*>(Vt + (cb / 2) * TE);
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-          dv[m] = mma(tile_ldp8<T>(du, 32 * (vb2 & 1) + cl, 32 * ib, jj, hh),
-                      tile_tr8<T>(Tmt, 32 * ib, 32 * lb, jj, lane), dv[m]);
-      // dbeta_j += v_j . (Tm^T dU)_j
-      const char* vt = reinterpret_cast<const char*>(Vt + (vb2 / 2) * TE);
+    for (int I = 0; I < 4; ++I) {
+      const v4_t<T> v4 = *reinterpret_cast<const v4_t<T>*>(vt + tile_off(r, 32 * (cb & 1) + 8 * I + 4 * hh));
 #pragma unroll
-      for (int I = 0; I < 4; ++I) {
-        const v4_t<T> v4 = *reinterpret_cast<const v4_t<T>*>(vt + tile_off(ja, 32 * (vb2 & 1) + 8 * I + 4 * hh));
-#pragma unroll
-        for (int r = 0; r < 4; ++r) db_part += (float)v4[r] * dv[m][4 * I + r];
-      }
-      dv[m] *= Bj;
+      for (int e = 0; e < 4; ++e) db_part += (float)v4[e] * dvx[4 * I + e];
     }
+    dvx *= Bj;
   }
-  // 1b. dkW[j][d] = beta_j e^G_j (Tm^T dW)[j][d] as D[d][j] = sum_i dW^T[d][i] Tm[i][j]
-  if (has_dk) {
+  // 4b. dk += beta_j e^G_j (Tm^T dW)[j][d], key dims 32 db .., as D[d][j]
+  if (active) {
+    f32x16 x{};
+    const T* dwt = dWt + (db / 2) * TE;
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+        x = mma(tile_tr8<T>(dwt, 32 * ib, 32 * (db & 1), jj, lane), tile_tr8<T>(Tmt, 32 * ib, 32 * lb, jj, lane), x);
+    const char* krow = reinterpret_cast<const char*>(Kt + (db / 2) * TE);
     float kdot = 0.f;
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int db2 = 2 * hf + m;
-      const T* dwt = dWt + (db2 / 2) * TE;
-      f32x16 x{};
+    for (int I = 0; I < 4; ++I) {
+      const v4_t<T> k4 = *reinterpret_cast<const v4_t<T>*>(krow + tile_off(r, 32 * (db & 1) + 8 * I + 4 * hh));
 #pragma unroll
-      for (int ib = 0; ib < 2; ++ib)
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-          x = mma(tile_tr8<T>(dwt, 32 * ib, 32 * (db2 & 1), jj, lane), tile_tr8<T>(Tmt, 32 * ib, 32 * lb, jj, lane), x);
-      const char* kt = reinterpret_cast<const char*>(Kt + (db2 / 2) * TE);
-#pragma unroll
-      for (int I = 0; I < 4; ++I) {
-        const v4_t<T> k4 = *reinterpret_cast<const v4_t<T>*>(kt + tile_off(ja, 32 * (db2 & 1) + 8 * I + 4 * hh));
-#pragma unroll
-        for (int r = 0; r < 4; ++r) kdot += (float)k4[r] * x[4 * I + r];
-      }
-      dk[m] += x * (Bj * eGj);
+      for (int e = 0; e < 4; ++e) kdot += (float)k4[e] * x[4 * I + e];
     }
+    dka += x * (Bj * eGj);
     db_part += eGj * kdot;
     dg_part += Bj * eGj * kdot;
   }
-  // 1c. dTm block (rows i = 32 hf + .., lane column j = 32 lb + cl):
-  //     beta_j (dU_i . v_j) + beta_j e^G_j (dW_i . k_j)
-  f32x16 dtm{};
-  {
+  // 4c. waves 0-3: dTm block (rows i = 32 hf .., lane column j = r):
+  //     beta_j (dU_i . v_j) + beta_j e^G_j (dW_i . k_j);
+  //     waves 4-7: KK block (rows l = 32 hf .., lane column a = r), lower only
+  f32x16 dtm{}, kk{};
+  if (w < 4) {
     f32x16 d2{};
 #pragma unroll
     for (int vt = 0; vt < VT; ++vt)
@@ -711,71 +653,61 @@ __global__ __launch_bounds__(256, 2) void delta_wy_bwd_kernel(DeltaArgs a, Delta
       for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj)
-          dtm = mma(tile_tr8<T>(dUt + vt * TE, 32 * s2, 32 * hf, jj, lane),
-                    tile_ldp8<T>(Vt + vt * TE, ja, 32 * s2, jj, hh), dtm);
+          dtm = mma(tile_tr8<T>(dVt + vt * TE, 32 * s2, 32 * hf, jj, lane),
+                    tile_ldp8<T>(Vt + vt * TE, r, 32 * s2, jj, hh), dtm);
 #pragma unroll
-    for (int kk = 0; kk < DK / 16; ++kk)
-      d2 = mma(tile_ld8<T>(dWt + (kk / 4) * TE, 32 * hf + cl, 16 * (kk % 4) + 8 * hh),
-               tile_ld8<T>(Kt + (kk / 4) * TE, ja, 16 * (kk % 4) + 8 * hh), d2);
+    for (int kq = 0; kq < DK / 16; ++kq)
+      d2 = mma(tile_ld8<T>(dWt + (kq / 4) * TE, 32 * hf + cl, 16 * (kq % 4) + 8 * hh),
+               tile_ld8<T>(Kt + (kq / 4) * TE, r, 16 * (kq % 4) + 8 * hh), d2);
     dtm = (dtm + d2 * eGj) * Bj;
-  }
-  // KK block (rows l = 32 hf + .., lane column a = ja) of the Gram matrix;
-  // the block above the diagonal (hf > lb) is not needed
-  const bool lower = hf <= lb;
-  f32x16 kk{};
-  if (lower) {
-#pragma unroll
-    for (int q = 0; q < DK / 16; ++q)
-      kk = mma(tile_ld8<T>(Kt + (q / 4) * TE, 32 * hf + cl, 16 * (q % 4) + 8 * hh),
-               tile_ld8<T>(Kt + (q / 4) * TE, ja, 16 * (q % 4) + 8 * hh), kk);
-  }
-  __syncthreads();  // dU^T and V no longer read
-
-  // 2. dTm^T as a [j][i] tile (row j = this lane, columns i of block hf)
-  {
-    char* t = reinterpret_cast<char*>(dTT);
+    char* t = reinterpret_cast<char*>(PT);
 #pragma unroll
     for (int I = 0; I < 4; ++I)
-      *reinterpret_cast<v4_t<T>*>(t + tile_off(ja, 32 * hf + 8 * I + 4 * hh)) =
+      *reinterpret_cast<v4_t<T>*>(t + tile_off(r, 32 * hf + 8 * I + 4 * hh)) =
           to4<T>(dtm[4 * I], dtm[4 * I + 1], dtm[4 * I + 2], dtm[4 * I + 3]);
+  } else if (lower) {
+#pragma unroll
+    for (int kq = 0; kq < DK / 16; ++kq)
+      kk = mma(tile_ld8<T>(Kt + (kq / 4) * TE, 32 * hf + cl, 16 * (kq % 4) + 8 * hh),
+               tile_ld8<T>(Kt + (kq / 4) * TE, r, 16 * (kq % 4) + 8 * hh), kk);
   }
   __syncthreads();
 
-  // 3. M^T[j][a] = sum_i dTm^T[j][i] Tm[i][a]: block (rows j = 32 hf + .., lane
-  //    column a = ja), stored as a [a][j] tile
-  {
+  // 5a. waves 0-3: M^T[j][a] = sum_i dTm^T[j][i] Tm[i][a], block (rows j =
+  //     32 hf .., lane column a = r), stored as a [a][j] tile
+  if (w < 4) {
     f32x16 x{};
 #pragma unroll
     for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj)
-        x = mma(tile_ldp8<T>(dTT, 32 * hf + cl, 32 * ib, jj, hh), tile_tr8<T>(Tmt, 32 * ib, 32 * lb, jj, lane), x);
+        x = mma(tile_ldp8<T>(PT, 32 * hf + cl, 32 * ib, jj, hh), tile_tr8<T>(Tmt, 32 * ib, 32 * lb, jj, lane), x);
     char* t = reinterpret_cast<char*>(MTt);
 #pragma unroll
     for (int I = 0; I < 4; ++I)
-      *reinterpret_cast<v4_t<T>*>(t + tile_off(ja, 32 * hf + 8 * I + 4 * hh)) =
+      *reinterpret_cast<v4_t<T>*>(t + tile_off(r, 32 * hf + 8 * I + 4 * hh)) =
           to4<T>(x[4 * I], x[4 * I + 1], x[4 * I + 2], x[4 * I + 3]);
   }
   __syncthreads();
 
-  // 4. dA^T[l][a] = -sum_j Tm[l][j] M^T[j][a] (rows l = 32 hf + .., lane a = ja);
-  //    P[a][l] = dA[a][l] beta_a e^(G_a - G_l) and Q = P o KK for l < a.
-  //    P goes to a [a][l] tile over dTm^T, Q^T to fp32 [l][a].
-  {
+  // 5b. waves 4-7: dA^T[l][a] = -sum_j Tm[l][j] M^T[j][a] (rows l = 32 hf ..,
+  //     lane a = r); P[a][l] = dA[a][l] beta_a e^(G_a - G_l) and Q = P o KK
+  //     for l < a.  P goes to a [a][l] tile over dTm^T, Q^T to fp32 [l][a].
+  if (w >= 4) {
     f32x16 x{};
     if (lower) {
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj)
-          x = mma(tile_ldp8<T>(Tmt, 32 * hf + cl, 32 * jb, jj, hh), tile_ldp8<T>(MTt, ja, 32 * jb, jj, hh), x);
+          x = mma(tile_ldp8<T>(Tmt, 32 * hf + cl, 32 * jb, jj, hh), tile_ldp8<T>(MTt, r, 32 * jb, jj, hh), x);
     }
     f32x16 pq, qq;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int l = 32 * hf + 8 * (e >> 2) + 4 * hh + (e & 3);
       float p = 0.f, q = 0.f;
-      if (lower && l < ja) {
+      if (lower && l < r) {
         const float dA = -x[e];
         const float g = GATED ? __expf(Gj - Gs[l]) : 1.f;
         p = dA * Bj * g;
@@ -786,46 +718,40 @@ __global__ __launch_bounds__(256, 2) void delta_wy_bwd_kernel(DeltaArgs a, Delta
       pq[e] = p;
       qq[e] = q;
     }
-    char* t = reinterpret_cast<char*>(Pn);
+    char* t = reinterpret_cast<char*>(PT);
 #pragma unroll
     for (int I = 0; I < 4; ++I)
-      *reinterpret_cast<v4_t<T>*>(t + tile_off(ja, 32 * hf + 8 * I + 4 * hh)) =
+      *reinterpret_cast<v4_t<T>*>(t + tile_off(r, 32 * hf + 8 * I + 4 * hh)) =
           to4<T>(pq[4 * I], pq[4 * I + 1], pq[4 * I + 2], pq[4 * I + 3]);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) Qb[(32 * hf + 8 * (e >> 2) + 4 * hh + (e & 3)) * 64 + ja] = qq[e];
+    for (int e = 0; e < 16; ++e) Qb[(32 * hf + 8 * (e >> 2) + 4 * hh + (e & 3)) * 64 + r] = qq[e];
   }
   __syncthreads();
 
-  // 5. dk[a][d] += sum_l K[l][d] (P[a][l] + P[l][a]); dk and dv out through
-  //    this wave's 4 KiB of the dW area
-  u32x4* stage = reinterpret_cast<u32x4*>(dWt) + 256 * w;
-  if (has_dk) {
+  // 6. dk[a][d] += sum_l K[l][d] (P[a][l] + P[l][a]); dk and dv out
+  if (active) {
+    const T* ktile = Kt + (db / 2) * TE;
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int db2 = 2 * hf + m;
-      const T* ktile = Kt + (db2 / 2) * TE;
+    for (int lbk = 0; lbk < 2; ++lbk)
 #pragma unroll
-      for (int lbk = 0; lbk < 2; ++lbk)
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          const v8_t<T> kop = tile_tr8<T>(ktile, 32 * lbk, 32 * (db2 & 1), jj, lane);
-          dk[m] = mma(kop, tile_ldp8<T>(Pn, ja, 32 * lbk, jj, hh), dk[m]);
-          dk[m] = mma(kop, tile_tr8<T>(Pn, 32 * lbk, 32 * lb, jj, lane), dk[m]);
-        }
-    }
-    store_rows_staged<T>(dk[0], dk[1], stage, (T*)a.dk + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DK + 64 * hf,
-                         (int64_t)H * DK, lane, nvalid);
+      for (int jj = 0; jj < 2; ++jj) {
+        const v8_t<T> kop = tile_tr8<T>(ktile, 32 * lbk, 32 * (db & 1), jj, lane);
+        dka = mma(kop, tile_ldp8<T>(PT, r, 32 * lbk, jj, hh), dka);
+        dka = mma(kop, tile_tr8<T>(PT, 32 * lbk, 32 * lb, jj, lane), dka);
+      }
+    store_rows32<T>(dka, stage, (T*)a.dk + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DK + 32 * db, qks, lane,
+                    Tn - (t0 + 32 * lb));
   }
   if (has_dv)
-    store_rows_staged<T>(dv[0], dv[1], stage, (T*)a.dv + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DV + 64 * hf,
-                         (int64_t)H * DV, lane, nvalid);
+    store_rows32<T>(dvx, stage, (T*)a.dv + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DV + 32 * cb, os, lane,
+                    Tn - (t0 + 32 * lb));
 
   db_part += __shfl_xor(db_part, 32);
   dg_part += __shfl_xor(dg_part, 32);
   rq_part += __shfl_xor(rq_part, 32);
   if (hh == 0) {
-    red_b[w][ja] = db_part;
-    red_g[w][ja] = dg_part + rq_part;
+    red_b[w * 64 + r] = db_part;
+    red_g[w * 64 + r] = dg_part + rq_part;
   }
   __syncthreads();
   if (tid < 64) {
@@ -837,10 +763,14 @@ __global__ __launch_bounds__(256, 2) void delta_wy_bwd_kernel(DeltaArgs a, Delta
       cq += (v[0] + v[1]) + (v[2] + v[3]);
     }
     const int t = t0 + tid;
-    const int l2 = tid >> 5;  // lane block of this row
-    const float dbeta = red_b[l2][tid] + red_b[l2 + 2][tid];
-    float x = reinterpret_cast<const float*>(a.ws + L.dGp)[(size_t)bh * Tp + t0 + tid] + red_g[l2][tid] +
-              red_g[l2 + 2][tid] - cq;
+    const int l2 = tid >> 5;  // row block of this row; waves l2 + 2 q hold it
+    float dbeta = 0.f, gsum = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      dbeta += red_b[(l2 + 2 * q) * 64 + tid];
+      gsum += red_g[(l2 + 2 * q) * 64 + tid];
+    }
+    float x = dGo + gsum - cq;
     // reverse inclusive cumsum over the chunk: dg_l = sum_{i >= l} dG_i
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -863,9 +793,6 @@ hipError_t launch_delta_bwd(const DeltaArgs& a, hipStream_t stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   delta_bwd_chunk_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(512), 0, stream>>>(a, L);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  delta_wy_bwd_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);
   return hipGetLastError();
 }
 

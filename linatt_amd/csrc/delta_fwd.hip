@@ -52,9 +52,6 @@ DeltaLayout delta_layout(int B, int T, int H, int DK, int DV, int eb) {
   off = 0;
   L.dVnT = take(BH * Tp * DV * eb);
   L.dhT = take(BH * NT * DK * DV * eb);
-  L.dW = take(BH * Tp * DK * eb);
-  L.dKp = take(BH * Tp * DK * 4);
-  L.dGp = take(BH * Tp * 4);
   L.bwd_bytes = off;
   return L;
 }

@@ -36,9 +36,6 @@ struct DeltaLayout {
   // backward scratch
   size_t dVnT;  // (B,H,NT,DV,64) T  gradient of v_new, transposed
   size_t dhT;   // (B,H,NT,DV,DK) T  gradient of the state leaving each chunk, transposed
-  size_t dW;    // (B,H,Tp,DK) T  gradient of W (an MFMA operand only)
-  size_t dKp;   // (B,H,Tp,DK) f32  dk from the output / state terms
-  size_t dGp;   // (B,H,Tp) f32   dG from the output / state terms (+ d gamma at row 63)
   size_t bwd_bytes;
 };
 
