@@ -503,6 +503,7 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
     for (int I = 0; I < 4; ++I) {
       const int j0 = 32 * xjb + 8 * I + 4 * hh;
       const v4_t<T> a4 = w < 3 ? *reinterpret_cast<const v4_t<T>*>(arow + tile_off(xi, j0)) : v4_t<T>{};
+      const f32x4 g4 = *reinterpret_cast<const f32x4*>(Gs + j0);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int j = j0 + e;
@@ -510,9 +511,10 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
         const float z = x * (float)a4[e];
         rs += z;
         Zt[j * 64 + xi] = z;
-        float mv = 0.f;
-        if (w < 3 && iv && j <= xi) mv = a.scale * x * (GATED ? __expf(Gi - Gs[j]) : 1.f);
-        mq[4 * I + e] = mv;
+        // branch-free: the exponent is zeroed where the entry is masked
+        const bool m = w < 3 && iv && j <= xi;
+        const float g = GATED ? __expf(m ? Gi - g4[e] : 0.f) : 1.f;
+        mq[4 * I + e] = m ? a.scale * x * g : 0.f;
       }
       *reinterpret_cast<v4_t<T>*>(reinterpret_cast<char*>(Mqt) + tile_off(xi, j0)) =
           to4<T>(mq[4 * I], mq[4 * I + 1], mq[4 * I + 2], mq[4 * I + 3]);
@@ -706,15 +708,15 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int l = 32 * hf + 8 * (e >> 2) + 4 * hh + (e & 3);
-      float p = 0.f, q = 0.f;
-      if (lower && l < r) {
-        const float dA = -x[e];
-        const float g = GATED ? __expf(Gj - Gs[l]) : 1.f;
-        p = dA * Bj * g;
-        q = p * kk[e];
-        db_part += dA * kk[e] * g;
-        rq_part += q;
-      }
+      // branch-free: the exponent is zeroed where the entry is masked
+      const bool m = lower && l < r;
+      const float dA = -x[e];
+      const float Gl = reinterpret_cast<const f32x4*>(Gs + 32 * hf + 8 * (e >> 2) + 4 * hh)[0][e & 3];
+      const float g = GATED ? __expf(m ? Gj - Gl : 0.f) : 1.f;
+      const float p = m ? dA * Bj * g : 0.f;
+      const float q = p * kk[e];
+      db_part += m ? dA * kk[e] * g : 0.f;
+      rq_part += q;
       pq[e] = p;
       qq[e] = q;
     }

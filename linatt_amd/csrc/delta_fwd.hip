@@ -143,12 +143,11 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int j = 32 * jb + 8 * (e >> 2) + 4 * hh + (e & 3);
-      float val = 0.f;
-      if (j <= i) {
-        val = a.scale * acc[e];
-        if constexpr (GATED) val *= __expf(Gs[i] - Gs[j]);
-      }
-      acc[e] = val;
+      // branch-free: the exponent is zeroed where the entry is masked
+      const bool m = j <= i;
+      float val = a.scale * acc[e];
+      if constexpr (GATED) val *= __expf(m ? Gs[i] - Gs[j] : 0.f);
+      acc[e] = m ? val : 0.f;
     }
     return acc;
   };
@@ -171,12 +170,10 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int i = 32 * ib + 8 * (e >> 2) + 4 * hh + (e & 3);
-      float val = 0.f;
-      if (i > j) {
-        val = Bs[i] * acc[e];
-        if constexpr (GATED) val *= __expf(Gs[i] - Gs[j]);
-      }
-      AT[i * 64 + j] = val;
+      const bool m = i > j;
+      float val = Bs[i] * acc[e];
+      if constexpr (GATED) val *= __expf(m ? Gs[i] - Gs[j] : 0.f);
+      AT[i * 64 + j] = m ? val : 0.f;
     }
   }
   __syncthreads();
