@@ -80,7 +80,8 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
   __shared__ __attribute__((aligned(16))) T Tw[64 * 64];      // Tm diag(beta e^G)
   __shared__ __attribute__((aligned(16))) T Tu[64 * 64];      // Tm diag(beta)
   __shared__ __attribute__((aligned(16))) float Ys[16 * 48];  // A_R,<R Tm_<R,<R of a block row
-  __shared__ float Bs[64], Gs[64];
+  __shared__ __attribute__((aligned(16))) float Bs[64];
+  __shared__ __attribute__((aligned(16))) float Gs[64];
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -140,13 +141,15 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
     for (int kk = 0; kk < DK / 16; ++kk)
       acc = mma(tile_ld8<T>(Kt[kk / 4], 32 * jb + cl, 16 * (kk % 4) + 8 * hh), qop[kk], acc);
     const int i = 32 * ib + cl;
+    const float Giv = Gs[i];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int j = 32 * jb + 8 * (e >> 2) + 4 * hh + (e & 3);
       // branch-free: the exponent is zeroed where the entry is masked
       const bool m = j <= i;
+      const float Gjv = reinterpret_cast<const f32x4*>(Gs + 32 * jb + 8 * (e >> 2) + 4 * hh)[0][e & 3];
       float val = a.scale * acc[e];
-      if constexpr (GATED) val *= __expf(m ? Gs[i] - Gs[j] : 0.f);
+      if constexpr (GATED) val *= __expf(m ? Giv - Gjv : 0.f);
       acc[e] = m ? val : 0.f;
     }
     return acc;
@@ -167,12 +170,16 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
       acc = mma(tile_ld8<T>(Kt[kk / 4], 32 * ib + cl, 16 * (kk % 4) + 8 * hh),
                 tile_ld8<T>(Kt[kk / 4], 32 * jb + cl, 16 * (kk % 4) + 8 * hh), acc);
     const int j = 32 * jb + cl;
+    const float Gjv = Gs[j];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int i = 32 * ib + 8 * (e >> 2) + 4 * hh + (e & 3);
       const bool m = i > j;
-      float val = Bs[i] * acc[e];
-      if constexpr (GATED) val *= __expf(m ? Gs[i] - Gs[j] : 0.f);
+      const int i4 = 32 * ib + 8 * (e >> 2) + 4 * hh;
+      const float Biv = reinterpret_cast<const f32x4*>(Bs + i4)[0][e & 3];
+      const float Giv = reinterpret_cast<const f32x4*>(Gs + i4)[0][e & 3];
+      float val = Biv * acc[e];
+      if constexpr (GATED) val *= __expf(m ? Giv - Gjv : 0.f);
       AT[i * 64 + j] = m ? val : 0.f;
     }
   }
@@ -216,7 +223,8 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
   } else {
     // Qg[i][d] = scale e^G_i q_i[d] (zero past T), rows 32 (w - 2) + cl
     const int i = 32 * (w - 2) + cl, ti = t0 + i;
-    const float sc = ti < Tn ? a.scale * (GATED ? __expf(Gs[i]) : 1.f) : 0.f;
+    const float eg = GATED ? __expf(Gs[i]) : 1.f;
+    const float sc = ti < Tn ? a.scale * eg : 0.f;
     T* qg = (T*)(a.ctx + L.Qg) + ((size_t)bh * Tp + t0 + i) * DK;
 #pragma unroll
     for (int kk = 0; kk < DK / 16; ++kk) {
@@ -341,7 +349,8 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
         for (int p = 0; p < 8; ++p) {
           const int e = 8 * j + p;  // C-layout slot: row 8 (e >> 2) + 4 hh + (e & 3)
           const int i = 32 * ib + 8 * (e >> 2) + 4 * hh + (e & 3);
-          const float sc = t0 + i < Tn ? (GATED ? __expf(Gs[63] - Gs[i]) : 1.f) : 0.f;
+          const float eg = GATED ? __expf(Gs[63] - Gs[i]) : 1.f;
+          const float sc = t0 + i < Tn ? eg : 0.f;
           x[ib][e] = (float)k8[p] * sc;
         }
       }
