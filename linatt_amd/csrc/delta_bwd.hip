@@ -84,6 +84,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
     const size_t ci = (size_t)bh * NT + c;
     const T* wtg = (const T*)(a.ctx + L.WT) + ci * DK * 64;
     const T* qgg = (const T*)(a.ctx + L.Qg) + ci * 64 * DK;
+    const T* qb = (const T*)a.q + ((size_t)b * Tn * H + h) * DK;  // ungated: q tiles
     const T* atg = (const T*)(a.ctx + L.Aqk) + ci * 4096;
     if (t0 + 64 > Tn) {
 #pragma unroll
@@ -92,7 +93,8 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
         for (int i = 0; i < KT; ++i) {
           dma_tile64<T>(kb + 64 * i, (int64_t)H * DK, t0, Tn, kt(sl, i), op, lane);
           dma_tile64<T>(wtg + (size_t)64 * i * 64, 64, 0, 64, wt(sl, i), op, lane);
-          dma_tile64<T>(qgg + 64 * i, DK, 0, 64, qt(sl, i), op, lane);
+          if constexpr (GATED) dma_tile64<T>(qgg + 64 * i, DK, 0, 64, qt(sl, i), op, lane);
+          else dma_tile64<T>(qb + 64 * i, (int64_t)H * DK, t0, Tn, qt(sl, i), op, lane);
         }
         dma_tile64<T>(atg, 64, 0, 64, at(sl), op, lane);
 #pragma unroll
@@ -100,6 +102,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
       }
     } else {
       const T* kr = kb + (size_t)t0 * H * DK;
+      const T* qr = qb + (size_t)t0 * H * DK;
       const T* dr = dob + (size_t)t0 * H * DV;
 #pragma unroll
       for (int op = 0; op < 8; ++op) {
@@ -111,7 +114,8 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
         for (int i = 0; i < KT; ++i) {
           dma16s(kr + 64 * i, ok, reinterpret_cast<char*>(kt(sl, i)) + 1024 * op);
           dma16s(wtg + (size_t)64 * i * 64, ow, reinterpret_cast<char*>(wt(sl, i)) + 1024 * op);
-          dma16s(qgg + 64 * i, oq, reinterpret_cast<char*>(qt(sl, i)) + 1024 * op);
+          if constexpr (GATED) dma16s(qgg + 64 * i, oq, reinterpret_cast<char*>(qt(sl, i)) + 1024 * op);
+          else dma16s(qr + 64 * i, ok, reinterpret_cast<char*>(qt(sl, i)) + 1024 * op);
         }
         dma16s(atg, ow, reinterpret_cast<char*>(at(sl)) + 1024 * op);
 #pragma unroll
@@ -170,8 +174,15 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
     // chunk c landed (the copy wave waited for it); every wave is done with chunk c + 1
     block_barrier();
     T* sl = Sh + (c & 1) * SLOT;
-    const T* Os = ot(sl, w / 2);  // this wave's 64-column dO tile
+    T* Os = ot(sl, w / 2);  // this wave's 64-column dO tile
     const int oc0 = 32 * (gw & 1);
+    static_assert(GATED || NW == 1, "ungated Z zeroes the rows of a dO tile of its own");
+    if (!GATED && t0 + kChunk > Tn) {
+      // ungated Z = scale q^T dO with raw q tiles: dO rows past T (copies of
+      // the last row) are zeroed (Aqk is zero there already)
+      for (int idx = lane; idx < (kChunk - (Tn - t0)) * 8; idx += 64)
+        reinterpret_cast<u32x4*>(Os + (Tn - t0 + idx / 8) * 64)[idx % 8] = u32x4{0u, 0u, 0u, 0u};
+    }
 
     // the LDS operands of dVn, Z and K dS' into registers first: the one
     // wave per SIMD then never waits on a read inside the MFMA chains
@@ -278,7 +289,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
       for (int j = 0; j < 2; ++j) nb[it][j] = c_to_b<T>(-dVn[it], j);
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
-      f32x16 acc = GATED ? dS[dt] * eg + Z[dt] : dS[dt] + Z[dt];
+      f32x16 acc = GATED ? dS[dt] * eg + Z[dt] : dS[dt] + Z[dt] * a.scale;
 #pragma unroll
       for (int it = 0; it < 2; ++it)
 #pragma unroll

@@ -231,7 +231,7 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
       v8_t<T> y;
 #pragma unroll
       for (int e = 0; e < 8; ++e) y[e] = (T)((float)qop[kk][e] * sc);
-      *reinterpret_cast<v8_t<T>*>(qg + 16 * kk + 8 * hh) = y;
+      if constexpr (GATED) *reinterpret_cast<v8_t<T>*>(qg + 16 * kk + 8 * hh) = y;
     }
   }
   __syncthreads();
@@ -337,8 +337,9 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
   };
   if (w < DK / 32) trans_out(Kt[w >> 1], Tw, (T*)(a.ctx + L.WT) + (ci * DK + 32 * w) * 64);
   if (w < DV / 32) trans_out(Vt[w >> 1], Tu, (T*)(a.ctx + L.UT) + (ci * DV + 32 * w) * 64);
-  // Kd^T[d][i] = e^(gamma - G_i) k_i[d] (zero past T), rows i in operand order
-  if (w < DK / 32) {
+  // Kd^T[d][i] = e^(gamma - G_i) k_i[d] (zero past T), rows i in operand
+  // order; gated only (ungated, the forward state pass reads k itself)
+  if (GATED && w < DK / 32) {
     f32x16 x[2];
 #pragma unroll
     for (int ib = 0; ib < 2; ++ib)
@@ -423,14 +424,39 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
     // global chunk swz(r, lane).
     const char* Wg = a.ctx + L.W + (size_t)bh * NT * WT16 * 16;
     const char* Kg = a.ctx + L.KdT + (size_t)bh * NT * WT16 * 16;
+    const int b = bh / a.H, h = bh % a.H, Tn = a.T;
+    const T* kb = (const T*)a.k + ((size_t)b * Tn * a.H + h) * DK;
+    const int kbytes = a.H * DK * (int)sizeof(T);  // k row stride
     const char* Ug = a.ctx + L.UT + ((size_t)bh * NT * NW * SPLIT + (gw - w)) * UT16 * 16;
     auto issue = [&](int c) __attribute__((always_inline)) {
       u32x4* sl = Sh + (c % 3) * SLOT;
 #pragma unroll
-      for (int op = 0; op < WOPS; ++op) {
-        const int rw = (64 * op + lane) / WCPR, rk = (64 * op + lane) / KCPR;
-        dma16s(Wg + (size_t)c * WT16 * 16, 16u * swz_slot<WCPR>(rw, lane % WCPR), sl + 64 * op);
-        dma16s(Kg + (size_t)c * WT16 * 16, 16u * swz_slot<KCPR>(rk, lane % KCPR), sl + WT16 + 64 * op);
+      for (int op = 0; op < WOPS; ++op)
+        dma16s(Wg + (size_t)c * WT16 * 16, 16u * swz_slot<WCPR>((64 * op + lane) / WCPR, lane % WCPR), sl + 64 * op);
+      if constexpr (GATED) {
+#pragma unroll
+        for (int op = 0; op < WOPS; ++op)
+          dma16s(Kg + (size_t)c * WT16 * 16, 16u * swz_slot<KCPR>((64 * op + lane) / KCPR, lane % KCPR),
+                 sl + WT16 + 64 * op);
+      } else {
+        // the chunk's k rows as DK/64 natural 64 x 64 tiles (rows past T
+        // repeat the last one; v_new is zero there)
+        T* kt = reinterpret_cast<T*>(sl + WT16);
+        const int t0 = c * kChunk;
+        if (t0 + kChunk <= Tn) {
+#pragma unroll
+          for (int op = 0; op < 8; ++op)
+#pragma unroll
+            for (int i = 0; i < DK / 64; ++i)
+              dma16s(kb + (size_t)t0 * a.H * DK + 64 * i, tile_lane_off(op, lane, kbytes),
+                     reinterpret_cast<char*>(kt + i * 4096) + 1024 * op);
+        } else {
+#pragma unroll
+          for (int op = 0; op < 8; ++op)
+#pragma unroll
+            for (int i = 0; i < DK / 64; ++i)
+              dma_tile64<T>(kb + 64 * i, (int64_t)a.H * DK, t0, Tn, kt + i * 4096, op, lane);
+        }
       }
 #pragma unroll
       for (int op = 0; op < UOPS; ++op)
@@ -492,7 +518,8 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
     // the chunk's LDS operands into registers ahead of their MFMA chains (W
     // first, U^T and Kd^T behind the W S products): the one wave per SIMD
     // then never waits on a read inside a chain
-    u32x4 wv[2][NDT][2], kv[NDT][2][2], uv[2][2];
+    u32x4 wv[2][NDT][2], kv[GATED ? NDT : 1][2][2], uv[2][2];
+    v8_t<T> kt8[GATED ? 1 : NDT][2][2];
 #pragma unroll
     for (int db = 0; db < NDT; ++db)
 #pragma unroll
@@ -523,7 +550,12 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
 #pragma unroll
       for (int it = 0; it < 2; ++it)
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) kv[dt][it][jj] = Ks[swz_slot<KCPR>(32 * dt + cl, 4 * it + 2 * jj + hh)];
+        for (int jj = 0; jj < 2; ++jj) {
+          if constexpr (GATED)
+            kv[dt][it][jj] = Ks[swz_slot<KCPR>(32 * dt + cl, 4 * it + 2 * jj + hh)];
+          else  // k^T by transposing reads of the natural k tiles
+            kt8[dt][it][jj] = tile_tr8<T>(reinterpret_cast<const T*>(Ks) + (dt / 2) * 4096, 32 * it, 32 * (dt & 1), jj, lane);
+        }
     __builtin_amdgcn_sched_barrier(0);
 
     // v_new = U - P (rows past T are zero in U and W); U^T rows of this
@@ -557,7 +589,8 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
       for (int it = 0; it < 2; ++it)
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj)
-          S[dt] = mma(__builtin_bit_cast(v8_t<T>, kv[dt][it][jj]), c_to_b<T>(Vn[it], jj), S[dt]);
+          S[dt] = mma(GATED ? __builtin_bit_cast(v8_t<T>, kv[GATED ? dt : 0][it][jj]) : kt8[GATED ? 0 : dt][it][jj],
+                      c_to_b<T>(Vn[it], jj), S[dt]);
     }
   };
 
