@@ -68,7 +68,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
   const float* Gc = reinterpret_cast<const float*>(a.ctx + L.Gc) + (size_t)bh * Tp;
 
   auto kt = [&](T* sl, int i) { return sl + i * TE; };                 // K tile i (key dims 64 i..)
-  auto wt = [&](T* sl, int i) { return sl + (KT + i) * TE; };          // W^T rows 64 i..
+  auto wt = [&](T* sl, int i) { return sl + (KT + i) * TE; };          // W [i][d], key dims 64 i..
   auto qt = [&](T* sl, int i) { return sl + (2 * KT + i) * TE; };      // Qg key dims 64 i..
   auto at = [&](T* sl) { return sl + 3 * KT * TE; };                   // Aqk
   auto ot = [&](T* sl, int i) { return sl + (3 * KT + 1 + i) * TE; };  // dO columns 64 i..
@@ -82,7 +82,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
     T* sl = Sh + (c & 1) * SLOT;
     const int t0 = c * kChunk;
     const size_t ci = (size_t)bh * NT + c;
-    const T* wtg = (const T*)(a.ctx + L.WT) + ci * DK * 64;
+    const T* wtg = (const T*)(a.ctx + L.W) + ci * 64 * DK;  // W [i][d], natural
     const T* qgg = (const T*)(a.ctx + L.Qg) + ci * 64 * DK;
     const T* qb = (const T*)a.q + ((size_t)b * Tn * H + h) * DK;  // ungated: q tiles
     const T* atg = (const T*)(a.ctx + L.Aqk) + ci * 4096;
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
 #pragma unroll
         for (int i = 0; i < KT; ++i) {
           dma_tile64<T>(kb + 64 * i, (int64_t)H * DK, t0, Tn, kt(sl, i), op, lane);
-          dma_tile64<T>(wtg + (size_t)64 * i * 64, 64, 0, 64, wt(sl, i), op, lane);
+          dma_tile64<T>(wtg + 64 * i, DK, 0, 64, wt(sl, i), op, lane);
           if constexpr (GATED) dma_tile64<T>(qgg + 64 * i, DK, 0, 64, qt(sl, i), op, lane);
           else dma_tile64<T>(qb + 64 * i, (int64_t)H * DK, t0, Tn, qt(sl, i), op, lane);
         }
@@ -113,7 +113,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
 #pragma unroll
         for (int i = 0; i < KT; ++i) {
           dma16s(kr + 64 * i, ok, reinterpret_cast<char*>(kt(sl, i)) + 1024 * op);
-          dma16s(wtg + (size_t)64 * i * 64, ow, reinterpret_cast<char*>(wt(sl, i)) + 1024 * op);
+          dma16s(wtg + 64 * i, oq, reinterpret_cast<char*>(wt(sl, i)) + 1024 * op);
           if constexpr (GATED) dma16s(qgg + 64 * i, oq, reinterpret_cast<char*>(qt(sl, i)) + 1024 * op);
           else dma16s(qr + 64 * i, ok, reinterpret_cast<char*>(qt(sl, i)) + 1024 * op);
         }
@@ -256,7 +256,8 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
           for (int r = 0; r < 4; ++r) dVn[jt][4 * I + r] += __expf(gam - g4[r]) * Pk[jt][4 * I + r];
         }
     }
-    // W^T operands of the dS update, read while the MFMAs above run
+    // W^T operands of the dS update (transposing reads of W), read while
+    // the MFMAs above run
     v8_t<T> wop[NDT][2][2];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
@@ -264,7 +265,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
       for (int it = 0; it < 2; ++it)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          wop[dt][it][j] = tile_ld8<T>(wt(sl, dt / 2), 32 * (dt & 1) + cl, 32 * it + 16 * j + 8 * hh);
+          wop[dt][it][j] = tile_tr8<T>(wt(sl, dt / 2), 32 * it, 32 * (dt & 1), j, lane);
     if (t0 + 63 >= Tn) {  // rows past T: K repeats its last row there
 #pragma unroll
       for (int jt = 0; jt < 2; ++jt)

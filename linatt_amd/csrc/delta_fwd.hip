@@ -42,7 +42,6 @@ DeltaLayout delta_layout(int B, int T, int H, int DK, int DV, int eb) {
   L.Tm = take(BH * NT * 4096 * eb);
   L.W = take(BH * Tp * DK * eb);
   L.UT = take(BH * Tp * DV * eb);
-  L.WT = take(BH * Tp * DK * eb);
   L.KdT = take(BH * Tp * DK * eb);
   L.Qg = take(BH * Tp * DK * eb);
   L.Aqk = take(BH * NT * 4096 * eb);
@@ -303,7 +302,8 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
 
   // 5. outputs through this wave's 4 KiB of the fp32 area
   u32x4* stage = reinterpret_cast<u32x4*>(AT) + 256 * w;
-  // W[i][d] (key dims in operand order): D[d][i] = sum_j K[j][d] Tw[i][j]
+  // W[i][d] (natural): D[d][i] = sum_j K[j][d] Tw[i][j]; both state passes
+  // read it, the reverse pass through transposing reads
   if (w >> 1 < KT) {
     const int ib = w & 1, kt = w >> 1;
     f32x16 x[2];
@@ -317,10 +317,10 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
           x[db] = mma(tile_tr8<T>(Kt[kt], 32 * s2, 32 * db, j, lane),
                       tile_ldp8<T>(Tw, 32 * ib + cl, 32 * s2, j, hh), x[db]);
     }
-    store_rows_staged<T, true>(x[0], x[1], stage, (T*)(a.ctx + L.W) + ((size_t)bh * Tp + t0 + 32 * ib) * DK + 64 * kt,
-                               DK, lane);
+    store_rows_staged<T>(x[0], x[1], stage, (T*)(a.ctx + L.W) + ((size_t)bh * Tp + t0 + 32 * ib) * DK + 64 * kt,
+                         DK, lane);
   }
-  // W^T[d][i], U^T[v][i] (rows i in operand order): D[i][d] = sum_j Tw[i][j] K[j][d]
+  // U^T[v][i] (rows i in operand order): D[i][v] = sum_j Tu[i][j] V[j][v]
   auto trans_out = [&](const T* tile, const T* Tx, T* dst) __attribute__((always_inline)) {
     f32x16 x[2];
 #pragma unroll
@@ -335,7 +335,6 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
     }
     store_rows_staged<T, true>(x[0], x[1], stage, dst, 64, lane);
   };
-  if (w < DK / 32) trans_out(Kt[w >> 1], Tw, (T*)(a.ctx + L.WT) + (ci * DK + 32 * w) * 64);
   if (w < DV / 32) trans_out(Vt[w >> 1], Tu, (T*)(a.ctx + L.UT) + (ci * DV + 32 * w) * 64);
   // Kd^T[d][i] = e^(gamma - G_i) k_i[d] (zero past T), rows i in operand
   // order; gated only (ungated, the forward state pass reads k itself)
@@ -525,7 +524,16 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int it = 0; it < 2; ++it) wv[it][db][j] = Ws[swz_slot<WCPR>(32 * it + cl, 4 * db + 2 * j + hh)];
+        for (int it = 0; it < 2; ++it) {
+          // k-step (db, j) of row 32 it + cl in ld_tr_op order: the 8-byte
+          // halves hh of its two 16-byte chunks 4 db + 2 j and 4 db + 2 j + 1
+          const char* row = reinterpret_cast<const char*>(Ws);
+          const v4_t<T> lo = *reinterpret_cast<const v4_t<T>*>(
+              row + 16 * swz_slot<WCPR>(32 * it + cl, 4 * db + 2 * j) + 8 * hh);
+          const v4_t<T> hi = *reinterpret_cast<const v4_t<T>*>(
+              row + 16 * swz_slot<WCPR>(32 * it + cl, 4 * db + 2 * j + 1) + 8 * hh);
+          wv[it][db][j] = __builtin_bit_cast(u32x4, cat44<T>(lo, hi));
+        }
     __builtin_amdgcn_sched_barrier(0);
 
     // P = W S  (W rows 32 it + cl, key dims in operand order)

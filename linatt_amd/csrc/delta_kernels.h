@@ -24,11 +24,10 @@ struct DeltaLayout {
   // context (written by the forward, read by the backward)
   size_t Gc;    // (B,H,Tp) f32  chunk-local inclusive cumsum of g (gated only)
   size_t Tm;    // (B,H,NT,64,64) T  (I + A)^-1, natural [i][j]
-  size_t W;     // (B,H,Tp,DK) T  W = Tm diag(beta e^G) K, key dims in operand order
+  size_t W;     // (B,H,Tp,DK) T  W = Tm diag(beta e^G) K
   size_t UT;    // (B,H,NT,DV,64) T  (Tm diag(beta) V)^T per chunk, rows i in operand order
-  size_t WT;    // (B,H,NT,DK,64) T  W^T per chunk, rows i in operand order
-  size_t KdT;   // (B,H,NT,DK,64) T  (e^(gamma - G_i) k_i)^T per chunk, rows i in operand order
-  size_t Qg;    // (B,H,Tp,DK) T  scale e^G_i q_i (zero past T)
+  size_t KdT;   // (B,H,NT,DK,64) T  (e^(gamma - G_i) k_i)^T per chunk, rows i in operand order (gated only)
+  size_t Qg;    // (B,H,Tp,DK) T  scale e^G_i q_i (zero past T; gated only)
   size_t Aqk;   // (B,H,NT,64,64) T  scale (q_i.k_j) e^(G_i-G_j) [j <= i]
   size_t hT;    // (B,H,NT,DV,DK) T  state entering each chunk, transposed [v][d]
   size_t VnT;   // (B,H,NT,DV,64) T  v_new^T per chunk, v_new = U - W h
