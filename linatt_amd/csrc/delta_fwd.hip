@@ -362,26 +362,17 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 2: sequential state pass.  One workgroup per (b, h) with one wave
-// per 32 value columns; S[d][v] lives in DK/32 accumulator tiles with lane
-// column v.  Per chunk the chain is
+// Kernel 2: sequential state pass.  The value columns of a head are split
+// over DV/32 workgroups; each holds its 32 columns of S[d][v] in DK/32
+// accumulator tiles (lane column v) on one compute wave.  Per chunk the
+// chain is
 //   v_new = U - W S  ->  S <- e^gamma S + Kd^T v_new.
-// W and Kd^T are the same for every wave of the head and U^T is split by
-// wave: all three reach LDS by direct global->LDS copies into a ring of three
-// slots, issued two chunks ahead (each wave copies 1/NW of W and of Kd^T and
-// its own U^T rows).  Tiles are stored XOR-swizzled by 16-byte chunk so the
-// operand reads of 16 consecutive rows hit distinct banks.
+// A copy wave issues W, Kd^T (ungated: the chunk's k rows, read transposed)
+// and this workgroup's U^T rows two chunks ahead into a ring of three slots,
+// and stores the v_new^T / h^T blocks the compute wave staged one chunk
+// earlier.  W, Kd^T and U^T rows are stored XOR-swizzled by 16-byte chunk so
+// the operand reads of 16 consecutive rows hit distinct banks.
 // ---------------------------------------------------------------------------
-
-// Wave-level copy of 1 KiB (64 x 16 bytes) of a row-major tile with CPR
-// 16-byte chunks per row into its swizzled LDS image: op covers tile chunks
-// [64 op, 64 op + 64).
-template <int CPR>
-__device__ __forceinline__ void dma_tile_1k(const u32x4* g, u32x4* lds, int op, int lane) {
-  const int row = (64 * op + lane) / CPR, slot = lane % CPR;
-  const int ch = swz_slot<CPR>(row, slot) - row * CPR;  // global chunk held by this slot
-  dma16(g + row * CPR + ch, lds + 64 * op);
-}
 
 template <typename T, int DK, int DV, bool GATED>
 __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_state_fwd_kernel(
@@ -536,7 +527,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
         }
     __builtin_amdgcn_sched_barrier(0);
 
-    // P = W S  (W rows 32 it + cl, key dims in operand order)
+    // P = W S  (W rows 32 it + cl)
     f32x16 P[2];
     P[0] = P[1] = f32x16{};
 #pragma unroll
@@ -588,7 +579,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
     for (int blk = 0; blk < NDT / 2; ++blk)
       stage_rows<T>(S[2 * blk], S[2 * blk + 1], Stg[c & 1][w * (NDT / 2 + 1) + 1 + blk], lane);
 
-    // S <- e^gamma S + Kd^T v_new  (Kd^T rows 32 dt + cl, chunk rows in operand order)
+    // S <- e^gamma S + Kd^T v_new  (Kd^T rows 32 dt + cl)
     const float eg = GATED ? __expf(Gc[c * kChunk + 63]) : 1.f;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
