@@ -496,8 +496,14 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
 
   // one chunk in ring slot SL; the loop below is unrolled by the ring depth
   // so every LDS address is a chunk-invariant register plus a constant
+  // gated: G at the last row of chunks 64 m + lane, reloaded every 64 chunks
+  float gl = 0.f;
+  auto load_gl = [&](int c0) __attribute__((always_inline)) {
+    if constexpr (GATED) gl = c0 + lane < NT ? Gc[(size_t)(c0 + lane) * kChunk + 63] : 0.f;
+  };
   auto step = [&](auto SL, int c) __attribute__((always_inline)) {
     constexpr int sl = decltype(SL)::value;
+    if (GATED && c > 0 && (c & 63) == 0) load_gl(c);
     // chunk c landed (the copy wave waited for it); every wave is done
     // with chunk c - 1, whose slot the copy wave refills
     block_barrier();
@@ -538,6 +544,19 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
 #pragma unroll
         for (int it = 0; it < 2; ++it) P[it] = mma(__builtin_bit_cast(v8_t<T>, wv[it][db][j]), ys, P[it]);
       }
+    // the state entering the chunk (h^T, [v][d]) is staged here, before the
+    // decay, and stored by the copy wave during the next chunk
+#pragma unroll
+    for (int blk = 0; blk < NDT / 2; ++blk)
+      stage_rows<T>(S[2 * blk], S[2 * blk + 1], Stg[c & 1][w * (NDT / 2 + 1) + 1 + blk], lane);
+    // gated: S's decay for the update, applied while the products above run
+    // (they read S through the bf16 operands already formed); e^gamma of
+    // chunk c from lane c % 64 of gl
+    if constexpr (GATED) {
+      const float eg = __expf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gl), c & 63)));
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) S[dt] *= eg;
+    }
     // U^T and the Kd^T operands of the state update, read while the MFMAs
     // above run
 #pragma unroll
@@ -572,18 +591,12 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
           for (int r = 0; r < 4; ++r) Vn[it][4 * I + r] = (float)u8[4 * s2 + r] - P[it][4 * I + r];
         }
       }
-    // v_new^T and the state entering the chunk (h^T, [v][d]): staged here,
-    // stored by the copy wave during the next chunk
+    // v_new^T: staged here, stored by the copy wave during the next chunk
     stage_rows<T>(Vn[0], Vn[1], Stg[c & 1][w * (NDT / 2 + 1)], lane);
-#pragma unroll
-    for (int blk = 0; blk < NDT / 2; ++blk)
-      stage_rows<T>(S[2 * blk], S[2 * blk + 1], Stg[c & 1][w * (NDT / 2 + 1) + 1 + blk], lane);
 
     // S <- e^gamma S + Kd^T v_new  (Kd^T rows 32 dt + cl)
-    const float eg = GATED ? __expf(Gc[c * kChunk + 63]) : 1.f;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
-      if constexpr (GATED) S[dt] *= eg;
 #pragma unroll
       for (int it = 0; it < 2; ++it)
 #pragma unroll
@@ -593,7 +606,8 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
     }
   };
 
-  vm_drain();  // h0 is in registers
+  load_gl(0);
+  vm_drain();  // h0 (and gl) are in registers
 #pragma unroll 1
   for (int c = 0; c < NT; c += 3) {
     step(IntC<0>{}, c);
