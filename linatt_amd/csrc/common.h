@@ -168,18 +168,22 @@ __device__ __forceinline__ void dma_small(const void* src, void* lds_base, int n
   if (lane < n4) dma16(reinterpret_cast<const char*>(src) + 16 * lane, lds_base);
 }
 
-// s_waitcnt vmcnt(N) then s_barrier, as one compiler-opaque step (memory
-// clobber: no memory access moves across it).  Vector-memory loads of a
-// wave complete in issue order, so with N = the number of loads issued after
-// some load X, X has landed once vmcnt <= N, whatever stores are also in
-// flight (they only add to the count).
-// s_barrier as a compiler-opaque step (memory clobber), without a wait.
-__device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
+// s_barrier as a compiler-opaque step (memory clobber).  The wave's LDS
+// operations drain first (lgkmcnt(0)): s_barrier itself does not wait for
+// them, and LDS accesses of different waves are not ordered, so an LDS write
+// still queued at the barrier could be read stale by another wave after it.
+__device__ __forceinline__ void block_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// s_waitcnt vmcnt(N) lgkmcnt(0) then s_barrier, as one compiler-opaque step
+// (memory clobber: no memory access moves across it).  Vector-memory loads
+// of a wave complete in issue order, so with N = the number of loads issued
+// after some load X, X has landed once vmcnt <= N, whatever stores are also
+// in flight (they only add to the count); LDS operations drain as in
+// block_barrier.
 template <int N>
 __device__ __forceinline__ void vm_wait_barrier() {
   static_assert(N >= 0 && N <= 63, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"i"(N) : "memory");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"i"(N) : "memory");
 }
 
 // vm_wait_barrier for a wave-uniform count n in [0, 6] (the counter field is
