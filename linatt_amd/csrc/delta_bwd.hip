@@ -45,7 +45,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
   constexpr int TE = 64 * 64;                     // elements per tile
   constexpr int OPW = 8;                          // 1 KiB copies per tile, all by the copy wave
   constexpr int NTILE = 3 * KT + 1 + VT;          // K, W^T, Qg, Aqk, dO
-  constexpr int SLOT = NTILE * TE + 64 * 4 / (int)sizeof(T);  // + G of the chunk (f32)
+  constexpr int SLOT = NTILE * TE + 2 * 64 * 4 / (int)sizeof(T);  // + G and e^(gamma - G) of the chunk (f32)
   static_assert(VT >= 1, "tile split");
   __shared__ __attribute__((aligned(16))) T Sh[2 * SLOT];
   // per chunk (two buffers): this workgroup's compute waves' dh^T blocks
@@ -66,6 +66,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
   const T* kb = (const T*)a.k + ((size_t)b * Tn * H + h) * DK;
   const T* dob = (const T*)a.dout + ((size_t)b * Tn * H + h) * DV + 64 * ((part * NW) / 2);  // this workgroup's columns
   const float* Gc = reinterpret_cast<const float*>(a.ctx + L.Gc) + (size_t)bh * Tp;
+  const float* Fk = reinterpret_cast<const float*>(a.ctx + L.Fk) + (size_t)bh * Tp;
 
   auto kt = [&](T* sl, int i) { return sl + i * TE; };                 // K tile i (key dims 64 i..)
   auto wt = [&](T* sl, int i) { return sl + (KT + i) * TE; };          // W [i][d], key dims 64 i..
@@ -122,7 +123,8 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
         for (int i = 0; i < VT; ++i) dma16s(dr + 64 * i, oo, reinterpret_cast<char*>(ot(sl, i)) + 1024 * op);
       }
     }
-    if (GATED && lane < 16) dma16(Gc + t0 + 4 * lane, gs(sl));
+    if (GATED && lane < 32)  // G (lanes 0-15), then e^(gamma - G) (lanes 16-31)
+      dma16((lane < 16 ? Gc : Fk) + t0 + 4 * (lane & 15), gs(sl));
   };
 
   // staged outputs of chunk c: dh^T rows (ci DV + 32 gw) and dv_new^T rows
@@ -251,9 +253,9 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
       for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
         for (int I = 0; I < 4; ++I) {
-          const f32x4 g4 = *reinterpret_cast<const f32x4*>(gs(sl) + 32 * jt + 8 * I + 4 * hh);
+          const f32x4 f4 = *reinterpret_cast<const f32x4*>(gs(sl) + 64 + 32 * jt + 8 * I + 4 * hh);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) dVn[jt][4 * I + r] += __expf(gam - g4[r]) * Pk[jt][4 * I + r];
+          for (int r = 0; r < 4; ++r) dVn[jt][4 * I + r] += f4[r] * Pk[jt][4 * I + r];
         }
     }
     // W^T operands of the dS update (transposing reads of W), read while

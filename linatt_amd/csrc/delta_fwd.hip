@@ -39,6 +39,7 @@ DeltaLayout delta_layout(int B, int T, int H, int DK, int DV, int eb) {
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
   L.Gc = take(BH * Tp * 4);
+  L.Fk = take(BH * Tp * 4);
   L.Tm = take(BH * NT * 4096 * eb);
   L.W = take(BH * Tp * DK * eb);
   L.UT = take(BH * Tp * DV * eb);
@@ -126,6 +127,7 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
         if (lane >= off) x += y;
       }
       reinterpret_cast<float*>(a.ctx + L.Gc)[(size_t)bh * Tp + t0 + lane] = x;
+      reinterpret_cast<float*>(a.ctx + L.Fk)[(size_t)bh * Tp + t0 + lane] = __expf(__shfl(x, 63) - x);
     }
     Bs[lane] = bt;
     Gs[lane] = x;

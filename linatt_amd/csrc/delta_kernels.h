@@ -23,6 +23,7 @@ constexpr int kChunk = 64;
 struct DeltaLayout {
   // context (written by the forward, read by the backward)
   size_t Gc;    // (B,H,Tp) f32  chunk-local inclusive cumsum of g (gated only)
+  size_t Fk;    // (B,H,Tp) f32  e^(gamma - G_i), gamma = G at the chunk's last row (gated only)
   size_t Tm;    // (B,H,NT,64,64) T  (I + A)^-1, natural [i][j]
   size_t W;     // (B,H,Tp,DK) T  W = Tm diag(beta e^G) K
   size_t UT;    // (B,H,NT,DV,64) T  (Tm diag(beta) V)^T per chunk, rows i in operand order
