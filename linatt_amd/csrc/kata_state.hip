@@ -43,6 +43,8 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
   static_assert(P % 1024 == 0, "1024 state rows per workgroup");
   __shared__ __attribute__((aligned(16))) float Kt[DK * PK];
   __shared__ __attribute__((aligned(16))) T Vt[DV * PV];
+  // per-wave partial 32 x 32 tiles of the Gram matrix K^T K (z, below)
+  __shared__ __attribute__((aligned(16))) float Gp[8][32 * 32];
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
   int blk = blockIdx.x;
@@ -69,7 +71,16 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
   for (int i4 = 0; i4 < 4; ++i4)
 #pragma unroll
     for (int vt = 0; vt < DV / 32; ++vt) acc[i4][vt] = f32x16{};
-  float zp[4] = {0.f, 0.f, 0.f, 0.f};
+  // z_p = sum_s k_s[ra] k_s[rb] = (K^T K)[ra][rb]: the workgroup's rows need
+  // two 32 x 32 tiles of the Gram matrix (M = 1: the two column halves of
+  // row half pb / 2; M = 2: the diagonal tile of group pb, twice; M = 4: both
+  // diagonal tiles).  Waves 4 u .. 4 u + 3 accumulate tile u, each over its
+  // own 16-key step w % 4 of every key tile, so z costs one MFMA per wave
+  // and key tile instead of a sum per psi feature.
+  auto gt_i = [&](int u) { return M == 1 ? pb >> 1 : (M == 2 ? pb : u); };
+  auto gt_j = [&](int u) { return M == 1 ? u : gt_i(u); };
+  const int gti = gt_i(w >> 2), gtj = gt_j(w >> 2);
+  f32x16 gz{};
   const int s_begin = seg * a.L, s_end = min(s_begin + a.L, a.T);
   // next tile prefetched into registers during the current one's compute:
   // waves 0-3 carry K, waves 4-7 V, one 4 x 4 block per thread
@@ -114,12 +125,21 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
         const f32x4 a0 = ka[0], a1 = ka[1], c0 = kc[0], c1 = kc[1];
         const f32x8 pf{a0[0] * c0[0], a0[1] * c0[1], a0[2] * c0[2], a0[3] * c0[3],
                        a1[0] * c1[0], a1[1] * c1[1], a1[2] * c1[2], a1[3] * c1[3]};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) zp[i4] += pf[j];
         const v8_t<T> x = __builtin_convertvector(pf, v8_t<T>);
 #pragma unroll
         for (int vt = 0; vt < DV / 32; ++vt) acc[i4][vt] = mma(x, vop[vt], acc[i4][vt]);
       }
+    }
+    {
+      // Gram step: rows 32 gti + cl and columns 32 gtj + cl of K^T, keys
+      // 16 (w % 4) + 8 hh + [0, 8) (the same k-order on both operands)
+      const int ks = 16 * (w & 3) + 8 * hh;
+      const f32x4* ga = reinterpret_cast<const f32x4*>(Kt + (32 * gti + cl) * PK + ks);
+      const f32x4* gb = reinterpret_cast<const f32x4*>(Kt + (32 * gtj + cl) * PK + ks);
+      const f32x4 a0 = ga[0], a1 = ga[1], b0 = gb[0], b1 = gb[1];
+      const v8_t<T> xa = __builtin_convertvector(f32x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]}, v8_t<T>);
+      const v8_t<T> xb = __builtin_convertvector(f32x8{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]}, v8_t<T>);
+      gz = mma(xa, xb, gz);
     }
   }
   // acc[i4][vt] = D[p'][v]: rows p' = p0 + 32 i4 + 8 I + 4 hh + r, lane column
@@ -134,9 +154,16 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
         *reinterpret_cast<float4*>(st + (size_t)(32 * vt + cl) * P + p0 + 32 * i4 + 8 * I + 4 * hh) =
             make_float4(acc[i4][vt][4 * I], acc[i4][vt][4 * I + 1], acc[i4][vt][4 * I + 2],
                         acc[i4][vt][4 * I + 3]);
+  // partial Gram tiles -> LDS (C layout: row 8 I + 4 hh + r, lane column),
+  // summed over the four waves of each tile in a fixed order
+#pragma unroll
+  for (int e = 0; e < 16; ++e) Gp[w][(8 * (e >> 2) + 4 * hh + (e & 3)) * 32 + cl] = gz[e];
+  __syncthreads();
 #pragma unroll
   for (int i4 = 0; i4 < 4; ++i4) {
-    const float z = zp[i4] + __shfl_xor(zp[i4], 32);
+    const int u = (ra[i4] >> 5) == gt_i(0) && (rb[i4] >> 5) == gt_j(0) ? 0 : 1;
+    const int o = (ra[i4] & 31) * 32 + (rb[i4] & 31);
+    const float z = (Gp[4 * u][o] + Gp[4 * u + 1][o]) + (Gp[4 * u + 2][o] + Gp[4 * u + 3][o]);
     if (hh == 0) a.seg_z[((size_t)bh * a.nseg + seg) * P + p0 + 32 * i4 + cl] = z;
   }
 }
