@@ -230,7 +230,6 @@ __global__ __launch_bounds__(256, 2) void kata_prefill_out_kernel(KataStateArgs 
   constexpr int HCH = 128, HCPR = HCH * (int)sizeof(T) / 16;
   static_assert(DK == 64 && DV == 64 && HCPR == 16 && P % HCH == 0, "64 x 128 16-bit state chunks");
   __shared__ __attribute__((aligned(16))) u32x4 Hs[2][DV * HCPR];
-  __shared__ __attribute__((aligned(16))) float Hzs[2][HCH];  // z prefix of the chunk
   T* const Kb0 = reinterpret_cast<T*>(Hs[0]);
   T* const Vb0 = Kb0 + 64 * 64;
   T* const Kb1 = reinterpret_cast<T*>(Hs[1]);
@@ -286,12 +285,36 @@ __global__ __launch_bounds__(256, 2) void kata_prefill_out_kernel(KataStateArgs 
         const int ch = slot ^ (row & 15);
         dma16(hT + (size_t)row * (P / 8) + c * HCPR + ch, Hs[c & 1] + 64 * op);
       }
-      if (w == 0) dma_small(hz + HCH * c, Hzs[c & 1], HCH / 4, lane);
     };
     constexpr int NCG = E * E / HCH;  // chunks per group
     static_assert(NCG * HCH == E * E, "chunks do not straddle groups");
     vm_drain();  // q of this wave's queries is in registers
     issue(0);
+    // den's prefix part psi(q).z = sum_g q_g^T Z_g q_g with Z_g[a][b] =
+    // z[g E^2 + a E + b]: Y = blockdiag(Z_g) Q^T by MFMA (A rows (g, a) of
+    // row tile rt, k = features (g', b) of k-steps 2 rt, 2 rt + 1, zero where
+    // g != g'), then q^T Y per query from the LDS copy of its q row
+    static_assert(E <= 32, "a group lies within one 32-row tile");
+#pragma unroll
+    for (int rt = 0; rt < DK / 32; ++rt) {
+      f32x16 y{};
+      const int ar = 32 * rt + cl, ga = ar / E;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int ks = 2 * rt + u, f = 16 * ks + 8 * hh, gf = f / E;
+        const float* zr = hz + ga * E * E + (ar % E) * E + f % E;
+        const f32x4 z0 = ga == gf ? *reinterpret_cast<const f32x4*>(zr) : f32x4{};
+        const f32x4 z1 = ga == gf ? *reinterpret_cast<const f32x4*>(zr + 4) : f32x4{};
+        const v8_t<T> za = __builtin_convertvector(f32x8{z0[0], z0[1], z0[2], z0[3], z1[0], z1[1], z1[2], z1[3]}, v8_t<T>);
+        y = mma(za, qop[ks], y);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const v4_t<T> q4 = *reinterpret_cast<const v4_t<T>*>(qa_row + 32 * rt + 8 * i + 4 * hh);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dpart += (float)q4[r] * y[4 * i + r];
+      }
+    }
 #pragma unroll
     for (int g = 0; g < M; ++g)
 #pragma unroll 1
@@ -303,18 +326,13 @@ __global__ __launch_bounds__(256, 2) void kata_prefill_out_kernel(KataStateArgs 
         const u32x4* Hb = Hs[c & 1];
 #pragma unroll
         for (int j = 0; j < HCH / 16; ++j) {
-          const int p0 = HCH * c + 16 * j;
           const int ai = (HCH * cc + 16 * j) / E;
           const int b0 = (16 * j) % E;  // HCH * cc is a multiple of E
           const int kk = (g * E + b0) / 16;
           const float qa = (float)qa_row[g * E + ai];
-          const f32x4 z0 = *reinterpret_cast<const f32x4*>(&Hzs[c & 1][16 * j + 8 * hh]);
-          const f32x4 z1 = *reinterpret_cast<const f32x4*>(&Hzs[c & 1][16 * j + 8 * hh + 4]);
           f32x8 pf;
 #pragma unroll
           for (int jj = 0; jj < 8; ++jj) pf[jj] = qa * (float)qop[kk][jj];
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) dpart += pf[jj] * z0[jj] + pf[4 + jj] * z1[jj];
           const v8_t<T> y = __builtin_convertvector(pf, v8_t<T>);
 #pragma unroll
           for (int db = 0; db < DV / 32; ++db) {
