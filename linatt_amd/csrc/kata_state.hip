@@ -65,6 +65,18 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
     ra[i4] = g * E + (p / E) % E;
     rb[i4] = g * E + p % E;
   }
+  // K^T row d holds keys in groups of four, group q at 4 (q ^ ((d >> 4) & 3)):
+  // the conversion's 16-lane f32x4 writes (rows 4 cb + cc, groups rq) then
+  // fall in 16 distinct bank quads, and the reads of 16 distinct rows stay so
+  auto kt_off = [](int d, int q) { return d * PK + 4 * (q ^ ((d >> 4) & 3)); };
+  int ko[4][4];  // per i4: rows ra (key groups 2 hh, 2 hh + 1) and rb, before + 16 s
+#pragma unroll
+  for (int i4 = 0; i4 < 4; ++i4) {
+    ko[0][i4] = kt_off(ra[i4], 2 * hh);
+    ko[1][i4] = kt_off(ra[i4], 2 * hh + 1);
+    ko[2][i4] = kt_off(rb[i4], 2 * hh);
+    ko[3][i4] = kt_off(rb[i4], 2 * hh + 1);
+  }
 
   f32x16 acc[4][DV / 32];
 #pragma unroll
@@ -100,7 +112,7 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) {
       if (isK)
-        *reinterpret_cast<f32x4*>(Kt + (4 * cb + cc) * PK + 4 * rq) =
+        *reinterpret_cast<f32x4*>(Kt + (4 * cb + cc) * PK + 4 * (rq ^ (cb >> 2))) =
             f32x4{(float)pre[0][cc], (float)pre[1][cc], (float)pre[2][cc], (float)pre[3][cc]};
       else
         st4<T>(Vt + (4 * cb + cc) * PV + 4 * rq, v4_t<T>{pre[0][cc], pre[1][cc], pre[2][cc], pre[3][cc]});
@@ -120,9 +132,10 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
       for (int vt = 0; vt < DV / 32; ++vt) vop[vt] = ld8<T>(Vt + (32 * vt + cl) * PV + 16 * s + 8 * hh);
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
-        const f32x4* ka = reinterpret_cast<const f32x4*>(Kt + ra[i4] * PK + 16 * s + 8 * hh);
-        const f32x4* kc = reinterpret_cast<const f32x4*>(Kt + rb[i4] * PK + 16 * s + 8 * hh);
-        const f32x4 a0 = ka[0], a1 = ka[1], c0 = kc[0], c1 = kc[1];
+        const f32x4 a0 = *reinterpret_cast<const f32x4*>(Kt + ko[0][i4] + 16 * s);
+        const f32x4 a1 = *reinterpret_cast<const f32x4*>(Kt + ko[1][i4] + 16 * s);
+        const f32x4 c0 = *reinterpret_cast<const f32x4*>(Kt + ko[2][i4] + 16 * s);
+        const f32x4 c1 = *reinterpret_cast<const f32x4*>(Kt + ko[3][i4] + 16 * s);
         const f32x8 pf{a0[0] * c0[0], a0[1] * c0[1], a0[2] * c0[2], a0[3] * c0[3],
                        a1[0] * c1[0], a1[1] * c1[1], a1[2] * c1[2], a1[3] * c1[3]};
         const v8_t<T> x = __builtin_convertvector(pf, v8_t<T>);
@@ -133,10 +146,10 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
     {
       // Gram step: rows 32 gti + cl and columns 32 gtj + cl of K^T, keys
       // 16 (w % 4) + 8 hh + [0, 8) (the same k-order on both operands)
-      const int ks = 16 * (w & 3) + 8 * hh;
-      const f32x4* ga = reinterpret_cast<const f32x4*>(Kt + (32 * gti + cl) * PK + ks);
-      const f32x4* gb = reinterpret_cast<const f32x4*>(Kt + (32 * gtj + cl) * PK + ks);
-      const f32x4 a0 = ga[0], a1 = ga[1], b0 = gb[0], b1 = gb[1];
+      const f32x4 a0 = *reinterpret_cast<const f32x4*>(Kt + kt_off(32 * gti + cl, 4 * (w & 3) + 2 * hh));
+      const f32x4 a1 = *reinterpret_cast<const f32x4*>(Kt + kt_off(32 * gti + cl, 4 * (w & 3) + 2 * hh + 1));
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(Kt + kt_off(32 * gtj + cl, 4 * (w & 3) + 2 * hh));
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(Kt + kt_off(32 * gtj + cl, 4 * (w & 3) + 2 * hh + 1));
       const v8_t<T> xa = __builtin_convertvector(f32x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]}, v8_t<T>);
       const v8_t<T> xb = __builtin_convertvector(f32x8{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]}, v8_t<T>);
       gz = mma(xa, xb, gz);
