@@ -69,6 +69,17 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
   // the conversion's 16-lane f32x4 writes (rows 4 cb + cc, groups rq) then
   // fall in 16 distinct bank quads, and the reads of 16 distinct rows stay so
   auto kt_off = [](int d, int q) { return d * PK + 4 * (q ^ ((d >> 4) & 3)); };
+  // V^T row d the same way in groups of eight keys (16 bytes), group q at
+  // 8 (q ^ ((d >> 4) & 3)); the read of group 2 s + hh splits into a lane
+  // base for even and for odd s plus 16 s
+  int vo[DV / 32][2];
+#pragma unroll
+  for (int vt = 0; vt < DV / 32; ++vt) {
+    const int d = 32 * vt + cl, f = (d >> 4) & 3;
+    const int b0 = d * PV + 8 * (hh ^ (f & 1)), fs = 16 * (f >> 1);
+    vo[vt][0] = b0 + fs;  // even s: s ^ (f >> 1) = s + (f >> 1)
+    vo[vt][1] = b0 - fs;  // odd s: s ^ (f >> 1) = s - (f >> 1)
+  }
   int ko[4][4];  // per i4: rows ra (key groups 2 hh, 2 hh + 1) and rb, before + 16 s
 #pragma unroll
   for (int i4 = 0; i4 < 4; ++i4) {
@@ -115,7 +126,8 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
         *reinterpret_cast<f32x4*>(Kt + (4 * cb + cc) * PK + 4 * (rq ^ (cb >> 2))) =
             f32x4{(float)pre[0][cc], (float)pre[1][cc], (float)pre[2][cc], (float)pre[3][cc]};
       else
-        st4<T>(Vt + (4 * cb + cc) * PV + 4 * rq, v4_t<T>{pre[0][cc], pre[1][cc], pre[2][cc], pre[3][cc]});
+        st4<T>(Vt + (4 * cb + cc) * PV + 8 * ((rq >> 1) ^ (cb >> 2)) + 4 * (rq & 1),
+               v4_t<T>{pre[0][cc], pre[1][cc], pre[2][cc], pre[3][cc]});
     }
   };
   static_assert(DK == 64 && DV == 64, "64 x 64 tiles");
@@ -129,7 +141,7 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
     for (int s = 0; s < 4; ++s) {
       v8_t<T> vop[DV / 32];
 #pragma unroll
-      for (int vt = 0; vt < DV / 32; ++vt) vop[vt] = ld8<T>(Vt + (32 * vt + cl) * PV + 16 * s + 8 * hh);
+      for (int vt = 0; vt < DV / 32; ++vt) vop[vt] = ld8<T>(Vt + vo[vt][s & 1] + 16 * s);
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
         const f32x4 a0 = *reinterpret_cast<const f32x4*>(Kt + ko[0][i4] + 16 * s);
