@@ -132,7 +132,7 @@ def bench_state(prefill_reps, decode_steps):
     batch 64 from the broadcast prefill state with fresh q, k, v ~ N(0,1)/8
     per step (seed 4000+i, all resident on the device before timing).
     Algorithmic prefill work in the O(T) form: states 2 T P dv + readout
-    2 T P dv + chunk-local scores (SURVEY's 106 GFLOP); decode bytes per step:
+    2 T P dv + chunk-local scores (about 105 GFLOP at this shape); decode bytes per step:
     the fp32 state read + written, 2 B H (P dv + P) 4 + inputs/outputs."""
     import torch
     from linatt_amd import _lib
@@ -296,7 +296,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only; multi-GPU runs are not part of "
-              "it (see DESIGN.md for how the path shards). Use --gpus 1.", file=sys.stderr)
+              "it. Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     if args.copy_calibration:
