@@ -41,10 +41,16 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
   constexpr int PV = 64 + 8;  // V^T pitch
   constexpr int NPB = P / 1024;
   static_assert(P % 1024 == 0, "1024 state rows per workgroup");
-  __shared__ __attribute__((aligned(16))) float Kt[DK * PK];
-  __shared__ __attribute__((aligned(16))) T Vt[DV * PV];
-  // per-wave partial 32 x 32 tiles of the Gram matrix K^T K (z, below)
-  __shared__ __attribute__((aligned(16))) float Gp[8][32 * 32];
+  // one LDS area: K^T (fp32) | V^T | per-wave partial 32 x 32 tiles of the
+  // Gram matrix K^T K (z, below) during the key loop, then the stage of
+  // S_seg^T: VC value rows of 1024 state rows (pitch SP) per pass
+  constexpr int VC = 16, SP = 1024 + 4;
+  constexpr int LOOPF = DK * PK + DV * PV * (int)sizeof(T) / 4 + 8 * 1024;
+  constexpr int LDSF = LOOPF > VC * SP ? LOOPF : VC * SP;
+  __shared__ __attribute__((aligned(16))) float Lds[LDSF];
+  float* const Kt = Lds;
+  T* const Vt = reinterpret_cast<T*>(Lds + DK * PK);
+  float (*const Gp)[32 * 32] = reinterpret_cast<float (*)[32 * 32]>(Lds + DK * PK + DV * PV * (int)sizeof(T) / 4);
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
   int blk = blockIdx.x;
@@ -167,18 +173,6 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
       gz = mma(xa, xb, gz);
     }
   }
-  // acc[i4][vt] = D[p'][v]: rows p' = p0 + 32 i4 + 8 I + 4 hh + r, lane column
-  // v = 32 vt + cl  ->  S_seg^T [v][p'] with 16-byte stores.
-  float* st = a.seg_S + ((size_t)bh * a.nseg + seg) * DV * P;
-#pragma unroll
-  for (int i4 = 0; i4 < 4; ++i4)
-#pragma unroll
-    for (int vt = 0; vt < DV / 32; ++vt)
-#pragma unroll
-      for (int I = 0; I < 4; ++I)
-        *reinterpret_cast<float4*>(st + (size_t)(32 * vt + cl) * P + p0 + 32 * i4 + 8 * I + 4 * hh) =
-            make_float4(acc[i4][vt][4 * I], acc[i4][vt][4 * I + 1], acc[i4][vt][4 * I + 2],
-                        acc[i4][vt][4 * I + 3]);
   // partial Gram tiles -> LDS (C layout: row 8 I + 4 hh + r, lane column),
   // summed over the four waves of each tile in a fixed order
 #pragma unroll
@@ -190,6 +184,30 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
     const int o = (ra[i4] & 31) * 32 + (rb[i4] & 31);
     const float z = (Gp[4 * u][o] + Gp[4 * u + 1][o]) + (Gp[4 * u + 2][o] + Gp[4 * u + 3][o]);
     if (hh == 0) a.seg_z[((size_t)bh * a.nseg + seg) * P + p0 + 32 * i4 + cl] = z;
+  }
+  // acc[i4][vt] = D[p'][v]: rows p' = 128 w + 32 i4 + 8 I + 4 hh + r of the
+  // workgroup's 1024, lane column v = 32 vt + cl  ->  stage [v - vc0][p'],
+  // then S_seg^T [v][1024 pb + p'] rows by whole 16-byte runs
+  float* st = a.seg_S + ((size_t)bh * a.nseg + seg) * DV * P + 1024 * pb;
+#pragma unroll
+  for (int pass = 0; pass < DV / VC; ++pass) {
+    const int vc0 = VC * pass, vt = vc0 / 32, vl = 32 * vt + cl - vc0;
+    __syncthreads();  // the Gram partials (or the previous pass) are read
+    if (vl >= 0 && vl < VC) {
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4)
+#pragma unroll
+        for (int I = 0; I < 4; ++I)
+          *reinterpret_cast<f32x4*>(Lds + vl * SP + 128 * w + 32 * i4 + 8 * I + 4 * hh) =
+              f32x4{acc[i4][vt][4 * I], acc[i4][vt][4 * I + 1], acc[i4][vt][4 * I + 2], acc[i4][vt][4 * I + 3]};
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < VC * 1024 / 4 / 512; ++it) {
+      const int idx = 512 * it + tid, row = idx / 256, c4 = idx % 256;
+      *reinterpret_cast<f32x4*>(st + (size_t)(vc0 + row) * P + 4 * c4) =
+          *reinterpret_cast<const f32x4*>(Lds + row * SP + 4 * c4);
+    }
   }
 }
 
