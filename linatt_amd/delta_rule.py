@@ -19,7 +19,8 @@ both returning ``(o, final_state)``.  Layout is fla's default time-major
 back in each input's dtype.  Every computation runs in ``liblinatt_hip.so``
 (``linatt_delta_fwd`` / ``linatt_delta_bwd``, plus ``linatt_l2norm_*`` for
 ``use_qk_l2norm_in_kernel``); variable-length batches (``cu_seqlens``) and
-float32 inputs raise.
+float32 inputs raise, and so do ``head_first=True`` and any other keyword
+fla would accept but this build does not implement.
 """
 
 from __future__ import annotations
@@ -148,6 +149,18 @@ class ChunkDeltaRuleFunction(torch.autograd.Function):
                 dh0.to(hdt) if dh0 is not None else None, None)
 
 
+def _check_kwargs(fn, kwargs):
+    """fla's ops take ``**kwargs`` for deprecated arguments; the only one with
+    a meaning here is ``head_first`` (a ``(B, H, T, D)`` layout), which is
+    refused, as is anything unknown, so that no argument is silently lost."""
+    kwargs = dict(kwargs)
+    if kwargs.pop("head_first", False):
+        raise NotImplementedError(
+            f"{fn}: head_first=True is not supported; pass time-major (B, T, H, D) tensors")
+    if kwargs:
+        raise TypeError(f"{fn}: unexpected keyword arguments {sorted(kwargs)}")
+
+
 def _run(q, k, v, beta, g, scale, initial_state, output_final_state, cu_seqlens,
          use_qk_l2norm_in_kernel):
     if cu_seqlens is not None:
@@ -165,6 +178,7 @@ def chunk_delta_rule(q, k, v, beta, scale=None, initial_state=None, output_final
                      cu_seqlens=None, use_qk_l2norm_in_kernel=False, **kwargs):
     """DeltaNet: ``S_t = S_{t-1} + beta_t k_t (v_t - S_{t-1}^T k_t)^T``,
     ``o_t = scale S_t^T q_t``.  Returns ``(o, final_state or None)``."""
+    _check_kwargs("chunk_delta_rule", kwargs)
     return _run(q, k, v, beta, None, scale, initial_state, output_final_state, cu_seqlens,
                 use_qk_l2norm_in_kernel)
 
@@ -175,5 +189,6 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
     """GatedDeltaNet: ``S_t = e^{g_t} S_{t-1} + beta_t k_t (v_t - e^{g_t}
     S_{t-1}^T k_t)^T``, ``o_t = scale S_t^T q_t``.  Returns ``(o, final_state
     or None)``."""
+    _check_kwargs("chunk_gated_delta_rule", kwargs)
     return _run(q, k, v, beta, g, scale, initial_state, output_final_state, cu_seqlens,
                 use_qk_l2norm_in_kernel)

@@ -242,12 +242,16 @@ class _KataDecayFunction(torch.autograd.Function):
         H, dv = kc.shape[2], vc.shape[-1]
         dq, dk_, dv_ = torch.empty_like(qc), torch.empty_like(kc), torch.empty_like(vc)
         dc = torch.empty_like(cf)
+        # bound to locals: a temporary made inside the argument list would be
+        # freed (and its memory reusable) before the kernels read it
+        oc = o.contiguous()
+        denc = den.float().contiguous()
         L = _lib.load()
         ws = torch.empty(L.linatt_kata_bwd_workspace_bytes(B, T, HQ, dv, _lib.dtype_code(vc.dtype)) // 4,
                          device=q.device, dtype=torch.float32)
         _lib.check("linatt_kata_bwd_decay", L.linatt_kata_bwd_decay(
-            _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(cf), _lib.ptr(o.contiguous()),
-            _lib.ptr(den.float().contiguous()), _lib.ptr(do), _lib.ptr(dq), _lib.ptr(dk_),
+            _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(cf), _lib.ptr(oc),
+            _lib.ptr(denc), _lib.ptr(do), _lib.ptr(dq), _lib.ptr(dk_),
             _lib.ptr(dv_), _lib.ptr(dc), _lib.ptr(ws), B, T, HQ, H, dk, dv, ctx.num_groups,
             float(ctx.scale), _lib.dtype_code(vc.dtype), _lib.stream_of(qc)))
         qd, kd, vd, cd = ctx.dtypes

@@ -97,10 +97,21 @@ def kata_prefill(q, k, v, num_groups=4, scale=None, eps=1e-6, seg_len=1024):
 
 def kata_decode_step(S, z, q, k, v, num_groups=4, scale=None, eps=1e-6):
     """One token per ``(b, h)``: updates ``S``, ``z`` in place and returns ``o``."""
-    _lib.require_device(S, z, q, k, v)
+    if q.dim() != 3 or v.dim() != 3:
+        raise ValueError(f"q, k must be (B, H, dk) and v (B, H, dv); got q {tuple(q.shape)}, "
+                         f"v {tuple(v.shape)}")
     B, H, dk = q.shape
     dv = v.shape[-1]
+    if k.shape != q.shape or v.shape[:2] != (B, H):
+        raise ValueError(f"k must be {tuple(q.shape)} and v (B, H, dv) = {(B, H)} + (dv,); "
+                         f"got k {tuple(k.shape)}, v {tuple(v.shape)}")
+    _lib.require_device(S, z, q, k, v)
+    devs = {t.device for t in (S, z, q, k, v)}
+    if len(devs) != 1:
+        raise ValueError(f"S, z, q, k, v must be on one device, got {sorted(map(str, devs))}")
     M = num_groups
+    if dk % M:
+        raise ValueError(f"d_k={dk} not divisible by M={M}")
     P = M * (dk // M) ** 2
     if S.shape != (B, H, P, dv) or z.shape != (B, H, P):
         raise ValueError(f"state must be S {(B, H, P, dv)}, z {(B, H, P)}")

@@ -1,0 +1,129 @@
+"""Host-side boundary checks that need no GPU: the run-time rebinding hook
+(``linatt_amd.patch``, after the reference's ``fla_patches.py:19-31, 195-200``)
+and argument validation that must raise before any device work."""
+
+import sys
+import types
+
+import pytest
+import torch
+
+from linatt_amd import delta_rule, parallel_kata_attn, patch, spd_state
+
+
+def _stub(name, **attrs):
+    m = types.ModuleType(name)
+    for k, v in attrs.items():
+        setattr(m, k, v)
+    return m
+
+
+def _orig(tag):
+    def f(*a, **k):
+        return tag
+    f.__name__ = tag
+    return f
+
+
+KATA_NAMES = ("parallel_kata_attn", "parallel_kata_attn_fwd", "parallel_kata_attn_sum",
+              "parallel_kata_attn_sum_fwd_impl", "parallel_kata_attn_decay",
+              "parallel_kata_attn_bwd", "parallel_kata_attn_bwd_triton")
+
+
+@pytest.fixture
+def stub_reference(monkeypatch):
+    """The reference's modules as stubs in sys.modules: kata.layer imports the
+    KATA ops by name (kata/layer.py:29-37), fla's layers import the delta ops
+    by name."""
+    mods = {
+        "kata": _stub("kata"),
+        "kata.parallel_kata_attn": _stub("kata.parallel_kata_attn", **{n: _orig("ref_" + n) for n in KATA_NAMES}),
+        # the mixer binds a subset of the names (no backward entry points)
+        "kata.layer": _stub("kata.layer", **{n: _orig("layer_" + n) for n in KATA_NAMES[:5]}),
+        "kata.spd": _stub("kata.spd"),
+        "kata.spd.chunk_scan_cat": _stub("kata.spd.chunk_scan_cat", spd_chunk_scan_cat=_orig("ref_scan")),
+        "fla": _stub("fla"),
+        "fla.layers": _stub("fla.layers"),
+        "fla.layers.delta_net": _stub("fla.layers.delta_net", chunk_delta_rule=_orig("fla_dn")),
+        "fla.layers.gated_deltanet": _stub("fla.layers.gated_deltanet",
+                                           chunk_gated_delta_rule=_orig("fla_gdn")),
+        "fla.ops": _stub("fla.ops"),
+        "fla.ops.delta_rule": _stub("fla.ops.delta_rule", chunk_delta_rule=_orig("fla_op_dn")),
+        "fla.ops.gated_delta_rule": _stub("fla.ops.gated_delta_rule",
+                                          chunk_gated_delta_rule=_orig("fla_op_gdn")),
+    }
+    for name, m in mods.items():
+        monkeypatch.setitem(sys.modules, name, m)
+    yield mods
+    patch.restore()
+
+
+def test_patch_rebinds_every_name(stub_reference):
+    m = stub_reference
+    done = patch.apply()
+    for n in KATA_NAMES:
+        assert getattr(m["kata.parallel_kata_attn"], n) is getattr(parallel_kata_attn, n)
+    for n in KATA_NAMES[:5]:
+        assert getattr(m["kata.layer"], n) is getattr(parallel_kata_attn, n)
+    # a name the mixer never imported is not added to it
+    assert not hasattr(m["kata.layer"], "parallel_kata_attn_bwd")
+    assert m["kata.spd.chunk_scan_cat"].spd_chunk_scan_cat is spd_state.spd_chunk_scan_cat
+    assert m["fla.layers.delta_net"].chunk_delta_rule is delta_rule.chunk_delta_rule
+    assert m["fla.ops.delta_rule"].chunk_delta_rule is delta_rule.chunk_delta_rule
+    assert m["fla.layers.gated_deltanet"].chunk_gated_delta_rule is delta_rule.chunk_gated_delta_rule
+    assert m["fla.ops.gated_delta_rule"].chunk_gated_delta_rule is delta_rule.chunk_gated_delta_rule
+    assert len(done) == len(KATA_NAMES) + 5 + 5
+
+
+def test_patch_is_idempotent_and_restorable(stub_reference):
+    m = stub_reference
+    first = patch.apply()
+    second = patch.apply()
+    assert first == second
+    assert m["kata.layer"].parallel_kata_attn is parallel_kata_attn.parallel_kata_attn
+    patch.restore()
+    assert m["kata.layer"].parallel_kata_attn() == "layer_parallel_kata_attn"
+    assert m["fla.layers.delta_net"].chunk_delta_rule() == "fla_dn"
+    assert m["kata.parallel_kata_attn"].parallel_kata_attn_bwd() == "ref_parallel_kata_attn_bwd"
+
+
+def test_patch_skips_absent_modules(monkeypatch):
+    # no reference packages at all: nothing to rebind, and no error
+    for name in [n for n in sys.modules if n == "kata" or n.startswith(("kata.", "fla"))]:
+        monkeypatch.delitem(sys.modules, name)
+    monkeypatch.setattr(sys, "path", [p for p in sys.path if "reference" not in p])
+    assert patch.apply() == []
+
+
+def _cpu(*shape, dtype=torch.bfloat16):
+    return torch.zeros(*shape, dtype=dtype)
+
+
+@pytest.mark.parametrize("fn", ["chunk_delta_rule", "chunk_gated_delta_rule"])
+def test_delta_rule_refuses_head_first_and_unknown_kwargs(fn):
+    q = _cpu(1, 8, 2, 64)
+    beta = _cpu(1, 8, 2, dtype=torch.float32)
+    args = (q, q, q, beta) if fn == "chunk_delta_rule" else (q, q, q, beta, beta)
+    op = getattr(delta_rule, fn)
+    with pytest.raises(NotImplementedError, match="head_first"):
+        op(*args, head_first=True)
+    with pytest.raises(TypeError, match="unexpected keyword"):
+        op(*args, chunk_size=32)
+    with pytest.raises(NotImplementedError, match="cu_seqlens"):
+        op(*args, cu_seqlens=torch.tensor([0, 8]))
+
+
+def test_decode_step_validates_shapes_before_launch():
+    B, H, D = 2, 3, 64
+    S = torch.zeros(B, H, 4 * 16 * 16, D)
+    z = torch.zeros(B, H, 4 * 16 * 16)
+    q = _cpu(B, H, D)
+    with pytest.raises(ValueError, match="k must be"):
+        spd_state.kata_decode_step(S, z, q, _cpu(B, 1, D), _cpu(B, H, D))
+    with pytest.raises(ValueError, match="k must be"):
+        spd_state.kata_decode_step(S, z, q, q, _cpu(B + 1, H, D))
+    with pytest.raises(ValueError, match=r"\(B, H, dk\)"):
+        spd_state.kata_decode_step(S, z, _cpu(B, 1, H, D), q, q)
+    # well-formed CPU tensors still raise: there is no CPU path
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        spd_state.kata_decode_step(S, z, q, q, _cpu(B, H, D))

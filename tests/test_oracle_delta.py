@@ -10,7 +10,10 @@ third-party ``fla`` package), so the oracle is pinned by mathematics:
 * with orthonormal keys and beta == 1 each write overwrites exactly:
   S^T k_i == v_i afterwards;
 * a single step from S=0 gives o = scale * beta (q.k) v (closed form);
-* finite differences (``gradcheck``) on the recurrence, incl. dg and dh0.
+* finite differences (``gradcheck``) on the recurrence, incl. dg and dh0;
+* gated with beta == 0: S_T = e^{sum g} h0 and o_t = scale e^{G_t} h0^T q_t;
+* l2norm by closed forms: unit rows, direction and scale invariance, and the
+  eps placement inside the square root (x / sqrt(x^2 + eps) for one element).
 """
 
 import math
@@ -111,3 +114,62 @@ def test_l2norm_in_kernel():
     torch.testing.assert_close(a[0], b[0])
     c = D.delta_rule_chunked(q * 3, k * 2, v, beta, g, initial_state=h0, chunk=4, use_qk_l2norm=True)
     torch.testing.assert_close(a[0], c[0])
+
+
+# ---------------------------------------------------------------------------
+# l2norm: fla.modules.l2norm.l2norm (third-party, absent; called at
+# kata/layer.py:347-348 and by use_qk_l2norm_in_kernel) is x / sqrt(sum x^2 + eps)
+# with eps = 1e-6 inside the square root.  Pinned by closed forms.
+# ---------------------------------------------------------------------------
+
+
+def test_l2norm_closed_forms():
+    x = torch.randn(7, 33, generator=torch.Generator().manual_seed(60), dtype=F64) * 5
+    y = D.l2norm(x)
+    # unit rows when |x|^2 >> eps
+    torch.testing.assert_close(y.norm(dim=-1), torch.ones(7, dtype=F64), rtol=1e-6, atol=0)
+    # direction kept: y is a positive multiple of x
+    ratio = y / x
+    torch.testing.assert_close(ratio, ratio[:, :1].expand_as(ratio))
+    assert (ratio > 0).all()
+    # scale invariance for large rows
+    torch.testing.assert_close(D.l2norm(x * 1e3), y, rtol=1e-9, atol=1e-12)
+    # eps inside the sqrt: a one-element row gives x / sqrt(x^2 + eps) exactly
+    for xv in (1e-4, 3e-3, 0.5, -2.0):
+        got = D.l2norm(torch.tensor([[xv]], dtype=F64)).item()
+        assert got == pytest.approx(xv / math.sqrt(xv * xv + 1e-6), rel=1e-14)
+    # eps placement distinguishes the plausible mistake x / (|x| + eps):
+    # for |x| = 1e-4, inside -> ~0.0995, outside -> ~0.99
+    small = torch.full((1, 4), 5e-5, dtype=F64)  # |x| = 1e-4
+    assert D.l2norm(small).norm().item() == pytest.approx(1e-4 / math.sqrt(1e-8 + 1e-6), rel=1e-12)
+    # a zero row stays zero (no division by zero)
+    assert torch.equal(D.l2norm(torch.zeros(2, 5, dtype=F64)), torch.zeros(2, 5, dtype=F64))
+    # explicit eps argument
+    assert D.l2norm(torch.tensor([[0.1]], dtype=F64), eps=0.03).item() == pytest.approx(0.1 / math.sqrt(0.04), rel=1e-14)
+
+
+# ---------------------------------------------------------------------------
+# Gated rule with beta == 0: only the gate acts, S_t = e^{G_t} h0 with
+# G_t = sum_{i<=t} g_i, so o_t = scale e^{G_t} h0^T q_t and S_T = e^{G_T} h0.
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("chunk", [None, 4, 8])
+def test_gated_beta_zero_closed_form(chunk):
+    q, k, v, beta, g, h0 = _inputs(2, 11, 3, 5, 4, 61, gated=True)
+    beta0 = torch.zeros_like(beta)
+    scale = 0.37
+    if chunk is None:
+        o, s = D.delta_rule_recurrent(q, k, v, beta0, g, scale=scale, initial_state=h0)
+    else:
+        o, s = D.delta_rule_chunked(q, k, v, beta0, g, scale=scale, initial_state=h0, chunk=chunk)
+    G = torch.cumsum(g, 1)  # (B, T, H)
+    want_o = scale * torch.exp(G)[..., None] * torch.einsum("bthk,bhkv->bthv", q, h0)
+    want_s = torch.exp(G[:, -1])[..., None, None] * h0
+    torch.testing.assert_close(o, want_o, rtol=1e-11, atol=1e-12)
+    torch.testing.assert_close(s, want_s, rtol=1e-11, atol=1e-12)
+    # a plausible mistake (decaying after the write instead of before, i.e.
+    # G shifted by one step) is visible
+    Gs = torch.cumsum(torch.cat([torch.zeros_like(g[:, :1]), g[:, :-1]], 1), 1)
+    wrong = scale * torch.exp(Gs)[..., None] * torch.einsum("bthk,bhkv->bthv", q, h0)
+    assert (wrong - o).abs().max() > 1e-3

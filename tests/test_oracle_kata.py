@@ -11,8 +11,10 @@ edge, a missing GQA reduction, a sign slip in the backward) fails at least one:
   consistent group permutation leaves A unchanged, A >= 0;
 * backward: the explicit formulas vs. float64 autograd through the dense form,
   and finite differences (``torch.autograd.gradcheck``);
-* decay: c == 0 reduces to concat; dense-with-decay forward vs. the restated
-  ``_kata_decay_ref``;
+* decay: c == 0 reduces to concat; for c_t = -lam t the output equals an
+  independent decayed psi-state recurrence (S <- e^{-lam} S + psi(k) v^T);
+  c -> c + const changes nothing; a pure-Python brute force with a
+  non-monotone c pins the clamp min(c_t - c_s, 0), its sign and its scale;
 * state form: prefill state equals the psi sums, decode after n tokens equals
   row n of the parallel form, chunked state-form prefill equals the dense form.
 """
@@ -223,3 +225,98 @@ def test_feature_map_inner_products():
         want_sum = sum((x[:, i * E:(i + 1) * E] * y[:, j * E:(j + 1) * E]).sum(-1) ** 2
                        for i in range(M) for j in range(M))
         torch.testing.assert_close((K.spd_sum(x, M) * K.spd_sum(y, M)).sum(-1), want_sum)
+
+
+# ---------------------------------------------------------------------------
+# Decay factor exp(min(c_t - c_s, 0)) (reference kata/parallel_kata_attn.py:291-310,
+# c from kata/layer.py:440-447), pinned without the oracle's own formula.
+# ---------------------------------------------------------------------------
+
+
+def _decayed_psi_recurrence(q, k, v, lam, M, scale):
+    """Independent form for c_t = -lam * t: the psi-state recurrence with a
+    per-step forgetting factor, S <- e^{-lam} S + psi(k) v^T and
+    z <- e^{-lam} z + psi(k), o_t = psi(q_t)^T S / psi(q_t).z, den_t =
+    scale^2 psi(q_t).z (psi from feature_maps.py:29-58 via spd_concat)."""
+    B, T, H, dk = q.shape
+    pq, pk = K.spd_concat(q, M), K.spd_concat(k, M)
+    P, dv = pq.shape[-1], v.shape[-1]
+    S = torch.zeros(B, H, P, dv, dtype=F64)
+    z = torch.zeros(B, H, P, dtype=F64)
+    a = math.exp(-lam)
+    os_, dens = [], []
+    for t in range(T):
+        S = a * S + pk[:, t, :, :, None] * v[:, t, :, None, :]
+        z = a * z + pk[:, t]
+        num = torch.einsum("bhp,bhpd->bhd", pq[:, t], S)
+        dn = (pq[:, t] * z).sum(-1)
+        os_.append(num / dn[..., None])
+        dens.append(scale * scale * dn)
+    return torch.stack(os_, 1), torch.stack(dens, 1)
+
+
+@pytest.mark.parametrize("lam", [0.0, 0.05, 0.7])
+def test_decay_linear_c_equals_decayed_recurrence(lam):
+    B, T, H, dk, dv, M = 2, 19, 2, 8, 5, 2
+    q, k, v = _rand((B, T, H, dk), 40), _rand((B, T, H, dk), 41), _rand((B, T, H, dv), 42)
+    t = torch.arange(T, dtype=F64)
+    c = (-lam * t)[None, :, None].expand(B, T, H).contiguous()
+    scale = K.default_scale(dk, M)
+    want_o, want_den = _decayed_psi_recurrence(q, k, v, lam, M, scale)
+    o, den = K.kata_fwd(q, k, v, M, None, "concat", c=c)
+    torch.testing.assert_close(o, want_o, rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(den, want_den, rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(K.kata_decay_ref(q, k, v, c, M, scale), want_o, rtol=1e-10, atol=1e-12)
+
+
+def test_decay_shift_invariance():
+    # only differences c_t - c_s enter: c -> c + const leaves o and den unchanged
+    B, T, H, dk, dv, M = 1, 17, 3, 8, 4, 4
+    q, k, v = _rand((B, T, H, dk), 43), _rand((B, T, H, dk), 44), _rand((B, T, H, dv), 45)
+    c = -torch.cumsum(torch.rand(B, T, H, generator=torch.Generator().manual_seed(46), dtype=F64), 1)
+    o1, d1 = K.kata_fwd(q, k, v, M, None, "concat", c=c)
+    o2, d2 = K.kata_fwd(q, k, v, M, None, "concat", c=c + 3.25)
+    torch.testing.assert_close(o1, o2, rtol=1e-12, atol=1e-13)
+    torch.testing.assert_close(d1, d2, rtol=1e-12, atol=1e-13)
+
+
+def _brute_decay(q, k, v, c, M, scale, clamp=True):
+    """Pure-Python loops: A[t,s] = sum_g (scale q_g.k_g)^2 * exp(min(c_t - c_s, 0)),
+    s <= t; o = sum A v / (sum A + 1e-20) (parallel_kata_attn.py:291-310)."""
+    B, T, H, dk = q.shape
+    E, dv = dk // M, v.shape[-1]
+    o = torch.zeros(B, T, H, dv, dtype=F64)
+    for b in range(B):
+        for h in range(H):
+            for t in range(T):
+                num = [0.0] * dv
+                den = 0.0
+                for s in range(t + 1):
+                    a = 0.0
+                    for g in range(M):
+                        d = sum(float(q[b, t, h, g * E + e]) * float(k[b, s, h, g * E + e]) for e in range(E))
+                        a += (scale * d) ** 2
+                    dc = float(c[b, t, h]) - float(c[b, s, h])
+                    a *= math.exp(min(dc, 0.0) if clamp else dc)
+                    den += a
+                    for j in range(dv):
+                        num[j] += a * float(v[b, s, h, j])
+                for j in range(dv):
+                    o[b, t, h, j] = num[j] / (den + 1e-20)
+    return o
+
+
+def test_decay_brute_force_non_monotone_c():
+    # c is NOT cumulative here: c_t - c_s takes both signs, so the clamp at 0,
+    # the sign of the difference and the exponent scale are all exercised
+    B, T, H, dk, dv, M = 1, 6, 2, 4, 3, 2
+    q, k, v = _rand((B, T, H, dk), 47), _rand((B, T, H, dk), 48), _rand((B, T, H, dv), 49)
+    c = _rand((B, T, H), 50, 1.5)
+    scale = 0.7
+    want = _brute_decay(q, k, v, c, M, scale)
+    got, _ = K.kata_fwd(q, k, v, M, scale, "concat", c=c)
+    torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-13)
+    torch.testing.assert_close(K.kata_decay_ref(q, k, v, c, M, scale), want, rtol=1e-12, atol=1e-13)
+    # plausible mistakes are visible at this size: no clamp, or no decay at all
+    assert (_brute_decay(q, k, v, c, M, scale, clamp=False) - want).abs().max() > 1e-3
+    assert (K.kata_fwd(q, k, v, M, scale, "concat")[0] - want).abs().max() > 1e-3
