@@ -102,6 +102,28 @@ int linatt_kata_bwd_dkdv(const void* q, const void* k, const void* v, const void
                          void* workspace, int B, int T, int HQ, int H, int dk_dim, int dv_dim,
                          int num_groups, float scale, int variant, int dtype, void* stream);
 
+/* Size of the fixed device scratch behind linatt_kata_bwd_noalloc (32 MiB). */
+#define LINATT_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* linatt_kata_bwd without a workspace argument and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments and results as linatt_kata_bwd; the
+ * workspace comes from a fixed per-device array of
+ * LINATT_NOALLOC_SCRATCH_BYTES inside the library (held from the first call
+ * on a device until the process ends).  A call whose
+ * linatt_kata_bwd_workspace_bytes(B, T, HQ, dv_dim, dtype) exceeds it returns
+ * LINATT_EINVAL before any device work (bf16 config B8 T2048 HQ12 dv64 needs
+ * 25.5 MiB).  Calls that overlap on one device share the array and race:
+ * serialise them.  Calls no hipMalloc/hipFree. */
+int linatt_kata_bwd_noalloc(const void* q, const void* k, const void* v, const void* o,
+                            const float* den, const void* dout, void* dq, void* dk, void* dv,
+                            int B, int T, int HQ, int H, int dk_dim, int dv_dim, int num_groups,
+                            float scale, int variant, int dtype, void* stream);
+
+/* LINATT_NOALLOC_SCRATCH_BYTES as compiled into the library. */
+size_t linatt_noalloc_scratch_bytes(void);
+
 /* ---------------------------------------------------------------------------
  * Chunked (gated) delta rule (DeltaNet / GatedDeltaNet), chunks of 64 tokens.
  * Replaces fla.ops.delta_rule.chunk_delta_rule and

@@ -49,6 +49,12 @@ int check_common(int B, int T, int HQ, int H, int dk, int dv, int M, float scale
   return LINATT_OK;
 }
 
+}  // namespace
+
+int linatt::set_last_error(int code, const char* msg) { return fail(code, msg); }
+
+namespace {
+
 using namespace linatt;
 
 // Returns 1 and sets *err when a kernel exists for the combination.

@@ -12,4 +12,8 @@ template <typename T>
 hipError_t launch_l2norm_bwd(const void* y, const float* rstd, const void* dy, void* dx, int n,
                              int d, hipStream_t s);
 
+// Sets the calling thread's linatt_last_error() message and returns code
+// (defined with the C-ABI entry points in api.hip).
+int set_last_error(int code, const char* msg);
+
 }  // namespace linatt

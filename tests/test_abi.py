@@ -102,3 +102,17 @@ def test_python_layer_rejects_cpu_tensors(lib):
     q = torch.randn(1, 4, 1, 64)
     with pytest.raises(RuntimeError, match="only on a ROCm GPU"):
         P.parallel_kata_attn_fwd(q, q, q)
+
+
+def test_noalloc_rejects_oversized_before_device_work(lib):
+    EINVAL = -1
+    assert lib.linatt_noalloc_scratch_bytes() == 32 << 20
+    # bf16 B8 T4096 HQ12 dv64 needs ~51 MiB of workspace: refused with a clear
+    # message before any HIP call (null pointers would also be refused later)
+    st = lib.linatt_kata_bwd_noalloc(None, None, None, None, None, None, None, None, None,
+                                     8, 4096, 12, 12, 64, 64, 4, 0.25, 0, 1, None)
+    assert st == EINVAL
+    assert b"exceeds the fixed scratch" in lib.linatt_last_error()
+    st = lib.linatt_kata_bwd_noalloc(None, None, None, None, None, None, None, None, None,
+                                     0, 8, 2, 2, 64, 64, 4, 0.25, 0, 1, None)
+    assert st == EINVAL
