@@ -4,7 +4,7 @@
 #include <cstdio>
 #include <string>
 
-#include "../../include/linatt_hip.h"
+#include "linatt_hip.h"
 #include "delta_kernels.h"
 #include "kata_kernels.h"
 #include "misc_kernels.h"

@@ -265,19 +265,15 @@ __device__ __forceinline__ v4_t<T> ds_tr4(const T* p) {
 // MFMA operand with k running down the rows of a natural tile: lane
 // (column c0 + (lane & 31)) receives rows r0 + 16 j + 4 hh + 0..3 and
 // r0 + 16 j + 8 + 4 hh + 0..3, the same k order as ld_tr_op on the
-// transposed tile.  zero (when non-null) is read instead by the 16-lane
-// groups whose (lane >> 4) & 1 differs from keep (half-zero operands).
+// transposed tile.
 template <typename T>
-__device__ __forceinline__ v8_t<T> tile_tr8(const T* tile, int r0, int c0, int j, int lane,
-                                            const T* zero = nullptr, int keep = 0) {
+__device__ __forceinline__ v8_t<T> tile_tr8(const T* tile, int r0, int c0, int j, int lane) {
   const int g = lane >> 4, i = lane & 15;
   const int row = r0 + 16 * j + 4 * (g >> 1) + (i >> 2);
   const int col = c0 + 16 * (g & 1) + 4 * (i & 3);
   const char* base = reinterpret_cast<const char*>(tile);
-  const bool z = zero != nullptr && ((g & 1) != keep);
-  const T* p0 = z ? zero : reinterpret_cast<const T*>(base + tile_off(row, col));
-  const T* p1 = z ? zero : reinterpret_cast<const T*>(base + tile_off(row + 8, col));
-  return cat44<T>(ds_tr4<T>(p0), ds_tr4<T>(p1));
+  return cat44<T>(ds_tr4<T>(reinterpret_cast<const T*>(base + tile_off(row, col))),
+                  ds_tr4<T>(reinterpret_cast<const T*>(base + tile_off(row + 8, col))));
 }
 
 // Compile-time bool for generic lambdas: body(BoolC<true>{}) instantiates
@@ -309,6 +305,56 @@ __device__ __forceinline__ v8_t<T> c_to_b(const f32x16& a, int j) {
   } else {
     return f;
   }
+}
+
+// ---------------------------------------------------------------------------
+// 16 x 16 x 32 products for 16-wide outputs (a 16-dim SPD group).  Layout of
+// v_mfma_f32_16x16x32_{bf16,f16}, lane l, row rho = l >> 4, i = l & 15:
+//   A (16 x 32): lane holds A[i][8 rho + j],  B (32 x 16): B[8 rho + j][i],
+//   C/D (16 x 16, 4 per lane): acc[r] = D[4 rho + r][i].
+// A 32 x 32 fp32 block X in the 32x32 C layout (rows k, lane column n) feeds
+// the two 16-column halves of such a product after one v_permlane16_swap per
+// packed register pair: lane rows 1 and 3 trade their k-rows {0-11}+4h with
+// rows 0 and 2's {16-27}+4h, after which 16-lane row rho holds, for column
+// n = (half) 16 + i, the eight k-rows
+//   t0(rho) + {0, 1, 2, 3, 8, 9, 10, 11},  t0(rho) = 16 (rho & 1) + 4 (rho >> 1),
+// in that order.  The matching A operand reads the same k-rows (tile_tr8_16).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f32x4 mma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// X (32x32 C layout, converted to T) -> B operands for columns 0-15 (b0) and 16-31 (b1).
+template <typename T>
+__device__ __forceinline__ void c_to_b16x2(const f32x16& x, v8_t<T>& b0, v8_t<T>& b1) {
+  static_assert(sizeof(T) == 2, "16-bit operands");
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  u32x4 lo = __builtin_bit_cast(u32x4, c_to_b<T>(x, 0));
+  u32x4 hi = __builtin_bit_cast(u32x4, c_to_b<T>(x, 1));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u32x2 sw = __builtin_amdgcn_permlane16_swap(lo[i], hi[i], false, false);
+    lo[i] = sw[0];
+    hi[i] = sw[1];
+  }
+  b0 = __builtin_bit_cast(v8_t<T>, lo);
+  b1 = __builtin_bit_cast(v8_t<T>, hi);
+}
+
+// The A operand matching c_to_b16x2 from a natural 64 x 64 tile (tile_off
+// layout): lane (rho, i) receives column c0 + i of rows r0 + t0(rho) + 0..3
+// and r0 + t0(rho) + 8..11 (two transposing 8-byte reads).
+template <typename T>
+__device__ __forceinline__ v8_t<T> tile_tr8_16(const T* tile, int r0, int c0, int lane) {
+  const int rho = lane >> 4, i = lane & 15;
+  const int row = r0 + 16 * (rho & 1) + 4 * (rho >> 1) + (i >> 2);
+  const int col = c0 + 4 * (i & 3);
+  const char* base = reinterpret_cast<const char*>(tile);
+  return cat44<T>(ds_tr4<T>(reinterpret_cast<const T*>(base + tile_off(row, col))),
+                  ds_tr4<T>(reinterpret_cast<const T*>(base + tile_off(row + 8, col))));
 }
 
 // acc + sum of the 8 elements of an operand, in fp32.  For 16-bit types one

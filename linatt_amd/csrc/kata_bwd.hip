@@ -452,11 +452,9 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
   __shared__ __attribute__((aligned(16))) T Kb[NB][64 * 64];
   __shared__ __attribute__((aligned(16))) T Vb[NB][64 * 64];
   __shared__ __attribute__((aligned(16))) float Cs[NB][64];
-  __shared__ __attribute__((aligned(16))) T Zr[8];
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
-  if (tid < 8) Zr[tid] = T(0);
   int qt, bh;
   map_block(blockIdx.x, nqt, nbh, qt, bh, true);
   const int b = bh / HQ, hq = bh % HQ;
@@ -524,16 +522,27 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
     }
   };
 
-  f32x16 acc[DK / 32];
+  // 16-wide groups (E = 16): dQ_g^T (16 x 32 queries) by two 16x16x32
+  // products per group and key block, whose B operands come from da by one
+  // lane swap per register pair (c_to_b16x2); wider groups fill whole 32-row
+  // blocks of 32x32x16 products
+  constexpr bool k16 = E == 16;
+  f32x16 acc[k16 ? 1 : DK / 32];
+  f32x4 acc16[k16 ? M : 1][2];
+  if constexpr (k16) {
 #pragma unroll
-  for (int rb = 0; rb < DK / 32; ++rb) acc[rb] = f32x16{};
+    for (int g = 0; g < M; ++g) acc16[g][0] = acc16[g][1] = f32x4{};
+  } else {
+#pragma unroll
+    for (int rb = 0; rb < DK / 32; ++rb) acc[rb] = f32x16{};
+  }
   const float ct = (DECAY && tvalid) ? c[qrow] : 0.f;
   float dcr = 0.f;
 
-  // K^T operand feeding dQ^T rows 32 rb + cl of query group gi from key group gk
+  // K^T operand feeding dQ^T rows 32 rb + cl of query group gi from key group
+  // gk (E >= 32: whole 32-row blocks of the group)
   auto kt_op = [&](const T* Ks, int sb, int gi, int gk, int rb, int j) __attribute__((always_inline)) {
-    if constexpr (E >= 32) return tile_tr8<T>(Ks, 32 * sb, gk * E + 32 * rb - gi * E, j, lane);
-    else return tile_tr8<T>(Ks, 32 * sb, 16 * gk - 16 * (gi & 1), j, lane, Zr, gi & 1);
+    return tile_tr8<T>(Ks, 32 * sb, gk * E + 32 * rb - gi * E, j, lane);
   };
 
   const int s_end = min(t0 + 128, Tn);
@@ -632,12 +641,20 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
               r = mma(tile_ld8<T>(Ks, 32 * sb + cl, gk * E + 16 * kk + 8 * hh), qop[gi * KE + kk], r);
             if constexpr (DECAY) au += r * r;
             const f32x16 da = r * x;
+            if constexpr (k16) {
+              v8_t<T> b0, b1;
+              c_to_b16x2<T>(da, b0, b1);
+              const v8_t<T> ka = tile_tr8_16<T>(Ks, 32 * sb, 16 * gk, lane);
+              acc16[gi][0] = mma16(ka, b0, acc16[gi][0]);
+              acc16[gi][1] = mma16(ka, b1, acc16[gi][1]);
+            } else {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              const v8_t<T> bop = c_to_b<T>(da, j);
+              for (int j = 0; j < 2; ++j) {
+                const v8_t<T> bop = c_to_b<T>(da, j);
 #pragma unroll
-              for (int rb = (gi * E) / 32; rb <= ((gi + 1) * E - 1) / 32; ++rb)
-                acc[rb] = mma(kt_op(Ks, sb, gi, gk, rb, j), bop, acc[rb]);
+                for (int rb = (gi * E) / 32; rb <= ((gi + 1) * E - 1) / 32; ++rb)
+                  acc[rb] = mma(kt_op(Ks, sb, gi, gk, rb, j), bop, acc[rb]);
+              }
             }
           }
         }
@@ -653,7 +670,23 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
     dcr += __shfl_xor(dcr, 32);
     if (tvalid && hh == 0) dc[qrow] = dcr * pdl;
   }
-  if (tvalid) {
+  if constexpr (k16) {
+    // lane (rho, i) holds dQ_g[t][4 rho + 0..3] for t = tw + 16 th + i; the
+    // row scale of query t lives in lane t - tw
+    const int rho = lane >> 4, i16 = lane & 15;
+#pragma unroll
+    for (int th = 0; th < 2; ++th) {
+      const float f = 2.f * __shfl(pdl, 16 * th + i16);
+      const int t = tw + 16 * th + i16;
+      if (t < Tn) {
+        T* drow = dq + (((int64_t)b * Tn + t) * HQ + hq) * DK;
+#pragma unroll
+        for (int g = 0; g < M; ++g)
+          st4<T>(drow + 16 * g + 4 * rho, to4<T>(acc16[g][th][0] * f, acc16[g][th][1] * f,
+                                                   acc16[g][th][2] * f, acc16[g][th][3] * f));
+      }
+    }
+  } else if (tvalid) {
     const float f = 2.f * pdl;
     T* drow = dq + qrow * DK;
 #pragma unroll
@@ -685,13 +718,11 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
   __shared__ __attribute__((aligned(16))) float Dl[NB][64];  // -delta
   __shared__ __attribute__((aligned(16))) float Pd[NB][64];  // scale^2 / den
   __shared__ __attribute__((aligned(16))) float Ct[NB][64];
-  __shared__ __attribute__((aligned(16))) T Zr[8];
   // this wave's k and v rows as MFMA B operands (lane l: 16 bytes per k-step)
   __shared__ __attribute__((aligned(16))) u32x4 KVop[4][(DK + DV) / 16][64];
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
-  if (tid < 8) Zr[tid] = T(0);
   int stile, bh;
   map_block(blockIdx.x, nst, nbh, stile, bh, false);
   const int b = bh / H, h = bh % H;
@@ -713,24 +744,26 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
   auto kop = [&](int kk) __attribute__((always_inline)) { return __builtin_bit_cast(v8_t<T>, KVop[w][kk][lane]); };
   auto vop = [&](int kk) __attribute__((always_inline)) { return __builtin_bit_cast(v8_t<T>, KVop[w][DK / 16 + kk][lane]); };
 
-  // concat groups narrower than 32 (E = 16): dK^T rows of two groups share a
-  // 32-row MFMA block, and group gk's product fills the other group's rows
-  // with values that are never used; they go to an accumulator of their own
-  // per group parity instead of zeroing half the operand
-  constexpr bool kPar = !SUM && E < 32;
-  constexpr int NP = kPar ? 2 : 1;
-  f32x16 dka[NP][DK / 32], dva[DV / 32];
+  // 16-wide groups (E = 16): dK_g^T (16 x 32 keys) by two 16x16x32 products
+  // per group and query block, B operands from da by one lane swap per
+  // register pair (c_to_b16x2); wider groups fill whole 32-row blocks
+  constexpr bool k16 = E == 16;
+  f32x16 dka[k16 ? 1 : DK / 32], dva[DV / 32];
+  f32x4 dk16[k16 ? M : 1][2];
+  if constexpr (k16) {
 #pragma unroll
-  for (int p = 0; p < NP; ++p)
+    for (int g = 0; g < M; ++g) dk16[g][0] = dk16[g][1] = f32x4{};
+  } else {
 #pragma unroll
-    for (int rb = 0; rb < DK / 32; ++rb) dka[p][rb] = f32x16{};
+    for (int rb = 0; rb < DK / 32; ++rb) dka[rb] = f32x16{};
+  }
 #pragma unroll
   for (int db = 0; db < DV / 32; ++db) dva[db] = f32x16{};
 
-  // Q^T operand feeding dK^T rows 32 rb + cl of key group gk from query group gi
+  // Q^T operand feeding dK^T rows 32 rb + cl of key group gk from query group
+  // gi (E >= 32: whole 32-row blocks of the group)
   auto qt_op = [&](const T* Qs, int mb, int gi, int gk, int rb, int j) __attribute__((always_inline)) {
-    if constexpr (E >= 32) return tile_tr8<T>(Qs, 32 * mb, gi * E + 32 * rb - gk * E, j, lane);
-    else return tile_tr8<T>(Qs, 32 * mb, 16 * gi - 16 * (gk & 1), j, lane, Zr, gk & 1);
+    return tile_tr8<T>(Qs, 32 * mb, gi * E + 32 * rb - gk * E, j, lane);
   };
 
   // query tiles (hq, tt) of this key tile, flattened over the G query heads
@@ -793,7 +826,12 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
       load_rows(n);
     }
   float dcc = 0.f;
-  for (int n = 0; n < ntiles; ++n) {
+  // query tile n (global index over the G heads) with or without the causal /
+  // past-T masks: only the two tiles on this workgroup's diagonal and a
+  // ragged last tile take MASKED, so the other tiles' block bodies are each
+  // one basic block
+  auto tile = [&](int n, auto masked_c) __attribute__((always_inline)) {
+    constexpr bool kMaskTile = decltype(masked_c)::value;
     const int buf = n % NB;
     const int hq = h * G + n / nq, t0 = 64 * (tt0 + n % nq);
     // tile n landed; tile n - 1's slot is free for tile n + NB - 1
@@ -804,14 +842,10 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
     }
     const T* Qs = Qb[buf];
     const T* Os = Ob[buf];
-    if (!(t0 + 63 < sw || sw >= Tn)) {
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        // a block wholly before this wave's keys (diagonal tiles only) is all
-        // masked below and adds zeros: no early exit, whose join costs
-        // accumulator copies on every block
+    // one 32-query block against this wave's 32 keys; NEED_MASK only for the
+    // block on the diagonal (tb == sw) and one that crosses T
+    auto block = [&](int mb, bool need_mask) __attribute__((always_inline)) {
         const int tb = t0 + 32 * mb;
-        const bool need_mask = (tb < sw + 31) || (tb + 32 > Tn);
         auto masked = [&](int e) {
           const int t = tb + 8 * (e >> 2) + 4 * hh + (e & 3);
           return t < sl || t >= Tn;
@@ -867,15 +901,20 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
               r = mma(tile_ld8<T>(Qs, 32 * mb + cl, gi * E + 16 * kk + 8 * hh), kop(gk * KE + kk), r);
             A += r * r;
             const f32x16 da = r * xs;
+            if constexpr (k16) {
+              v8_t<T> b0, b1;
+              c_to_b16x2<T>(da, b0, b1);
+              const v8_t<T> qa = tile_tr8_16<T>(Qs, 32 * mb, 16 * gi, lane);
+              dk16[gk][0] = mma16(qa, b0, dk16[gk][0]);
+              dk16[gk][1] = mma16(qa, b1, dk16[gk][1]);
+            } else {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              const v8_t<T> bop = c_to_b<T>(da, j);
+              for (int j = 0; j < 2; ++j) {
+                const v8_t<T> bop = c_to_b<T>(da, j);
 #pragma unroll
-              for (int rb = (gk * E) / 32; rb <= ((gk + 1) * E - 1) / 32; ++rb)
-                if constexpr (kPar)
-                  dka[gk & 1][rb] = mma(tile_tr8<T>(Qs, 32 * mb, 32 * rb, j, lane), bop, dka[gk & 1][rb]);
-                else
-                  dka[0][rb] = mma(qt_op(Qs, mb, gi, gk, rb, j), bop, dka[0][rb]);
+                for (int rb = (gk * E) / 32; rb <= ((gk + 1) * E - 1) / 32; ++rb)
+                  dka[rb] = mma(qt_op(Qs, mb, gi, gk, rb, j), bop, dka[rb]);
+              }
             }
             // sum and decay variants: keep the next group's score MFMAs from
             // being hoisted above this group's products (bounds the live
@@ -911,6 +950,20 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
           for (int db = 0; db < DV / 32; ++db)
             dva[db] = mma(tile_tr8<T>(Os, 32 * mb, 32 * db, j, lane), pb, dva[db]);
         }
+    };
+    if (!(t0 + 63 < sw || sw >= Tn)) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        // blocks whose queries all precede this wave's keys are skipped (the
+        // diagonal tiles only); the block on the diagonal, and one crossing
+        // T, is masked; every other block runs unmasked
+        const int tb = t0 + 32 * mb;
+        if constexpr (kMaskTile) {
+          if (tb + 31 < sw) continue;
+          block(mb, tb < sw + 31 || tb + 32 > Tn);
+        } else {
+          block(mb, false);
+        }
       }
     }
     if constexpr (DECAY) {
@@ -921,21 +974,44 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
         if (hq + 1 < (h + 1) * G) csl = svalid ? c[((int64_t)b * Tn + sl) * HQ + hq + 1] : 0.f;
       }
     }
+  };
+  // per query head: the two diagonal tiles, the tiles wholly inside T, the ragged rest
+  const int nfull = Tn / 64 - tt0;
+  for (int hi = 0; hi < G; ++hi) {
+    const int nb = hi * nq;
+    int i = 0;
+    for (; i < nq && i < 2; ++i) tile(nb + i, BoolC<true>{});
+    for (; i < nfull; ++i) tile(nb + i, BoolC<false>{});
+    for (; i < nq; ++i) tile(nb + i, BoolC<true>{});
   }
 
+  if constexpr (k16) {
+    // lane (rho, i) holds dK_g[s][4 rho + 0..3] for s = sw + 16 sh + i
+    const int rho = lane >> 4, i16 = lane & 15;
+#pragma unroll
+    for (int sh = 0; sh < 2; ++sh) {
+      const int s = sw + 16 * sh + i16;
+      if (s < Tn) {
+        T* dkrow = dk + (((int64_t)b * Tn + s) * H + h) * DK;
+#pragma unroll
+        for (int g = 0; g < M; ++g)
+          st4<T>(dkrow + 16 * g + 4 * rho, to4<T>(2.f * dk16[g][sh][0], 2.f * dk16[g][sh][1],
+                                                    2.f * dk16[g][sh][2], 2.f * dk16[g][sh][3]));
+      }
+    }
+  }
   if (svalid) {
     T* dkrow = dk + krow * DK;
     T* dvrow = dv + krow * DV;
+    if constexpr (!k16) {
 #pragma unroll
-    for (int rb = 0; rb < DK / 32; ++rb)
+      for (int rb = 0; rb < DK / 32; ++rb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-      {
-        // rows 8i + 4hh + 0..3 of the block: i < 2 the even group, else the odd
-        const f32x16& d = dka[kPar && i >= 2 ? 1 : 0][rb];
-        st4<T>(dkrow + 32 * rb + 8 * i + 4 * hh,
-               to4<T>(2.f * d[4 * i], 2.f * d[4 * i + 1], 2.f * d[4 * i + 2], 2.f * d[4 * i + 3]));
-      }
+        for (int i = 0; i < 4; ++i)
+          st4<T>(dkrow + 32 * rb + 8 * i + 4 * hh,
+                 to4<T>(2.f * dka[rb][4 * i], 2.f * dka[rb][4 * i + 1], 2.f * dka[rb][4 * i + 2],
+                        2.f * dka[rb][4 * i + 3]));
+    }
 #pragma unroll
     for (int db = 0; db < DV / 32; ++db)
 #pragma unroll

@@ -14,7 +14,7 @@
 #include <mutex>
 #include <string>
 
-#include "../../include/linatt_hip.h"
+#include "linatt_hip.h"
 #include "misc_kernels.h"
 
 namespace {
