@@ -588,7 +588,10 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
       issue(st);
       load_c(st);
     }
-  for (int st = 0; st < nst; ++st) {
+  // key tile st; MASKED applies the causal / past-T masks where the tile
+  // reaches the workgroup's diagonal
+  auto tile = [&](int st, auto masked_c) __attribute__((always_inline)) {
+    constexpr bool kMaskTile = decltype(masked_c)::value;
     const int s0 = st * 64, buf = st % NB;
     // tile st landed; tile st - 1's slot is free for tile st + 2
     vm_wait_barrier_n(st + 1 < nst ? ops : 0);
@@ -599,9 +602,11 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
     const T* Ks = Kb[buf];
     const T* Vs = Vb[buf];
     if (!(s0 > tw + 31 || tw >= Tn)) {
-      const bool need_mask = (s0 + 63 > tw) || (s0 + 64 > Tn);
+      const bool need_mask = kMaskTile && ((s0 + 63 > tw) || (s0 + 64 > Tn));
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
+        // a block of keys all after this wave's queries adds nothing
+        if (kMaskTile && s0 + 32 * sb > tw + 31) continue;
         // x^T[s][t] = V dO^T - delta  (rows s, column t)
         f32x16 x;
 #pragma unroll
@@ -664,7 +669,10 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
         }
       }
     }
-  }
+  };
+  // one body for every tile: a second, unmasked copy of it for the tiles
+  // before the diagonal raises this kernel's register count past occupancy 3
+  for (int st = 0; st < nst; ++st) tile(st, BoolC<true>{});
 
   if constexpr (DECAY) {
     dcr += __shfl_xor(dcr, 32);
@@ -782,12 +790,12 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
   const int64_t nrows = (int64_t)(nbh / H) * Tn * HQ;
   const T* dsrc = kPre ? reinterpret_cast<const T*>(reinterpret_cast<const char*>(delta) + kata_dop_offset(nrows))
                        : dout;
-  auto issue = [&](int n) __attribute__((always_inline)) {
+  auto issue = [&](int n, int slot) __attribute__((always_inline)) {
     const int hq = h * G + n / nq, t0 = 64 * (tt0 + n % nq);
     const T* qb = q + ((int64_t)b * Tn) * qs + (int64_t)hq * DK;
     const T* ob = dsrc + ((int64_t)b * Tn) * os + (int64_t)hq * DV;
-    char* qd = reinterpret_cast<char*>(Qb[n % NB]);
-    char* od = reinterpret_cast<char*>(Ob[n % NB]);
+    char* qd = reinterpret_cast<char*>(Qb[slot]);
+    char* od = reinterpret_cast<char*>(Ob[slot]);
     if (t0 + 64 <= Tn) {
       const T* qt = qb + (int64_t)t0 * qs;
       const T* ot = ob + (int64_t)t0 * os;
@@ -807,24 +815,18 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
   // per-row data of a query tile: -delta (bf16: prescaled) and scale^2/den
   // as the dq kernel wrote them (rows [0, B T HQ) and [B T HQ, 2 B T HQ) of
   // `delta`), and c; rows past T repeat the last one and are masked
-  auto load_rows = [&](int n) __attribute__((always_inline)) {
+  auto load_rows = [&](int n, int slot) __attribute__((always_inline)) {
     const int hq = h * G + n / nq, t = min(64 * (tt0 + n % nq) + lane, Tn - 1);
     const int64_t r = ((int64_t)b * Tn + t) * HQ + hq;
-    if (w == 0) dma4(delta + r, Dl[n % NB]);
-    if (w == 1) dma4(delta + nrows + r, Pd[n % NB]);
-    if (DECAY && w == 2) dma4(c + r, Ct[n % NB]);
+    if (w == 0) dma4(delta + r, Dl[slot]);
+    if (w == 1) dma4(delta + nrows + r, Pd[slot]);
+    if (DECAY && w == 2) dma4(c + r, Ct[slot]);
   };
 
   float csl = (DECAY && svalid) ? c[((int64_t)b * Tn + sl) * HQ + h * G] : 0.f;
-  // copies per tile and wave: two of q, two of dO, a row vector by waves 0-2
-  const int ops = 4 + (w < 2 || (DECAY && w == 2) ? 1 : 0);
   vm_drain();  // k, v (and c) of this wave's keys are in registers
-#pragma unroll
-  for (int n = 0; n < NB - 1; ++n)
-    if (n < ntiles) {
-      issue(n);
-      load_rows(n);
-    }
+  issue(0, 0);
+  load_rows(0, 0);
   float dcc = 0.f;
   // query tile n (global index over the G heads) with or without the causal /
   // past-T masks: only the two tiles on this workgroup's diagonal and a
@@ -834,11 +836,11 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
     constexpr bool kMaskTile = decltype(masked_c)::value;
     const int buf = n % NB;
     const int hq = h * G + n / nq, t0 = 64 * (tt0 + n % nq);
-    // tile n landed; tile n - 1's slot is free for tile n + NB - 1
-    vm_wait_barrier_n(NB > 2 && n + 1 < ntiles ? ops : 0);
-    if (n + NB - 1 < ntiles) {
-      issue(n + NB - 1);
-      load_rows(n + NB - 1);
+    // tile n landed and every wave is done with the other slot
+    vm_wait_barrier_n(0);
+    if (n + 1 < ntiles) {
+      issue(n + 1, 1 - buf);
+      load_rows(n + 1, 1 - buf);
     }
     const T* Qs = Qb[buf];
     const T* Os = Ob[buf];

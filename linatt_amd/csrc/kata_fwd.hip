@@ -290,6 +290,8 @@ __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
       a[sb] = f32x16{};
+      // a block of keys all after this wave's queries adds nothing
+      if (s0 + 32 * sb > tw + 31) continue;
       const int krow = 32 * sb + cl;
       if constexpr (!SUM) {
 #pragma unroll
@@ -363,13 +365,85 @@ __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
     }
   };
 
+  // concat, no decay, 16-bit without rescaling: key tiles wholly before the
+  // workgroup's queries need no mask, and there the group score MFMAs run one
+  // (block, group) unit ahead of the squares that consume them, with block
+  // 0's P.V products issued under block 1's squares; the body is one basic
+  // block
+  auto step_plain = [&](int st, auto slot) __attribute__((always_inline)) {
+    constexpr int buf = decltype(slot)::value;
+    vm_wait_barrier_n(st + 1 < nst ? ops : 0);
+    if (st + 2 < nst) issue(st + 2, IntC<(buf + 2) % NB>{});
+    const T* Ks = Kb[buf];
+    const T* Vs = Vb[buf];
+    if (tw >= Tn) return;
+    auto score = [&](int sb, int g) __attribute__((always_inline)) {
+      f32x16 r{};
+#pragma unroll
+      for (int kk = 0; kk < KE; ++kk)
+        r = mma(tile_ld8<T>(Ks, 32 * sb + cl, g * E + 16 * kk + 8 * hh), qop[g * KE + kk], r);
+      return r;
+    };
+    auto finish = [&](int sb, const f32x16& ab) __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const v8_t<T> pb = c_to_b<T>(ab, j);
+        dpart = sum8<T>(pb, dpart);
+#pragma unroll
+        for (int db = 0; db < DV / 32; ++db)
+          oacc[db] = mma(tile_tr8<T>(Vs, 32 * sb, 32 * db, j, lane), pb, oacc[db]);
+      }
+    };
+    if constexpr (M == 1) {
+      // one group: its score is a chain of four MFMAs; running a second
+      // block's chain ahead costs the registers of occupancy 3
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        const f32x16 r = score(sb, 0);
+        finish(sb, r * r);
+      }
+    } else {
+      f32x16 a0, a1;
+      f32x16 rc = score(0, 0);
+#pragma unroll
+      for (int u = 1; u < 2 * M; ++u) {
+        const f32x16 rn = score(u / M, u % M);
+        const int pg = (u - 1) % M;
+        if ((u - 1) / M == 0) {
+          if (pg == 0) a0 = rc * rc; else a0 += rc * rc;
+          if (pg == M - 1) finish(0, a0);
+        } else {
+          if (pg == 0) a1 = rc * rc; else a1 += rc * rc;
+        }
+        rc = rn;
+      }
+      a1 += rc * rc;
+      finish(1, a1);
+    }
+  };
+
   vm_drain();  // q (and c) of this wave's queries are in registers
   issue(0, IntC<0>{});
   if (nst > 1) issue(1, IntC<1>{});
-  for (int st = 0; st < nst; st += NB) {
-    step(st, IntC<0>{});
-    if (st + 1 < nst) step(st + 1, IntC<1>{});
-    if (st + 2 < nst) step(st + 2, IntC<2>{});
+  constexpr bool kPlain = !SUM && !DECAY && !kRescale;
+  int st = 0;
+  if constexpr (kPlain) {
+    // tiles wholly before this workgroup's first query, then the rest
+    const int nplain = min(t0 / 64, nst);
+    for (; st + NB <= nplain; st += NB) {
+      step_plain(st, IntC<0>{});
+      step_plain(st + 1, IntC<1>{});
+      step_plain(st + 2, IntC<2>{});
+    }
+    if (st < nplain) step_plain(st++, IntC<0>{});
+    if (st < nplain) step_plain(st++, IntC<1>{});
+  }
+  for (; st < nst; ++st) {
+    switch (st % NB) {
+      case 0: step(st, IntC<0>{}); break;
+      case 1: step(st, IntC<1>{}); break;
+      default: step(st, IntC<2>{}); break;
+    }
   }
 
   const float dsum = dpart + __shfl_xor(dpart, 32);
