@@ -40,17 +40,24 @@ template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
 hipError_t launch_kata_bwd(const KataArgs& a, int parts, hipStream_t stream);
 
 // Compiled (dtype, DK, DV, M) combinations.  Each is built for the concat
-// and sum scores; the forward also for the decayed concat score.
+// and sum scores and, forward and backward, for the decayed concat score.
+// (128, 64, 2) is the shape of the offset-gated mixer (kata/layer.py:237-281:
+// each group of E = 32 padded to 64, so dk = 128 for dv = 64 at M = 2), which
+// is also the one decayed configuration (configs/model/
+// kataconv_cat_l2_gdn_340m.yaml:12,18-19).
 #define LINATT_KATA_SHAPES(X) \
   X(__bf16, 64, 64, 1)        \
   X(__bf16, 64, 64, 2)        \
   X(__bf16, 64, 64, 4)        \
+  X(__bf16, 128, 64, 2)       \
   X(_Float16, 64, 64, 1)      \
   X(_Float16, 64, 64, 2)      \
   X(_Float16, 64, 64, 4)      \
+  X(_Float16, 128, 64, 2)     \
   X(float, 64, 64, 1)         \
   X(float, 64, 64, 2)         \
-  X(float, 64, 64, 4)
+  X(float, 64, 64, 4)         \
+  X(float, 128, 64, 2)
 
 }  // namespace linatt
 

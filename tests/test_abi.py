@@ -49,6 +49,10 @@ def test_version_and_support(lib):
             assert lib.linatt_kata_supported(dt, 64, 64, M, 0, 1) == 1
             assert lib.linatt_kata_supported(dt, 64, 64, M, 1, 1) == 0  # decay is concat-only
     assert lib.linatt_kata_supported(BF16, 48, 64, 3, 0, 0) == 0
+    # the offset-gated mixer's shape (groups of 32 padded to 64): concat, sum, decay
+    for dt in (BF16, F32, F16):
+        assert lib.linatt_kata_supported(dt, 128, 64, 2, 0, 1) == 1
+        assert lib.linatt_kata_supported(dt, 128, 64, 2, 1, 0) == 1
     # -<o,dO> and scale^2/den rows (256-byte rounded); bf16 adds the prescaled dO
     assert lib.linatt_kata_bwd_workspace_bytes(2, 10, 3, 64, F32) == 512  # 480 rounded up
     assert lib.linatt_kata_bwd_workspace_bytes(2, 10, 3, 64, F16) == 512

@@ -220,3 +220,62 @@ def test_decay_fwd_bwd(P, shape, M, cmode, dtype):
         assert leaf.grad.dtype == leaf.dtype
         e = mar(leaf.grad, ref, fl[name])
         assert e < tol, (name, e)
+
+
+def _augment_offset(q, k, off, M, E, Ep):
+    """The offset-gated mixer's packing (kata/layer.py:265-281): per group, q
+    gets [q_g, off_t, 0...] and k gets [k_g, 1, 0...], each padded to Ep, so
+    the concat score becomes sum_g (scale (q_g . k_g + off_t))^2."""
+    B, T, H, _ = q.shape
+
+    def pack(x, col):
+        xg = x.reshape(B, T, H, M, E)
+        cc = col[..., None, None].expand(B, T, H, M, 1).to(x.dtype)
+        z = x.new_zeros(B, T, H, M, Ep - E - 1)
+        return torch.cat([xg, cc, z], dim=-1).reshape(B, T, H, M * Ep)
+
+    return pack(q, off), pack(k, torch.ones_like(off))
+
+
+@pytest.mark.parametrize("decay", [False, True], ids=["plain", "decay"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+@pytest.mark.parametrize("T", [200, 333])
+def test_offset_gate_shape_dk128(P, decay, dtype, T):
+    """dk = 128, dv = 64, M = 2: the shape kataconv_cat_l2_gdn_340m.yaml:12,18-19
+    runs (M = 2 groups of E = 32 padded to 64 by the offset gate; scale =
+    1/sqrt(32) passed explicitly, kata/layer.py:237-244, 440-455)."""
+    B, H, M, E, Ep, dv = 2, 2, 2, 32, 64, 64
+    q0 = gen((B, T, H, M * E), 60 + T, 0.125)
+    k0 = gen((B, T, H, M * E), 61 + T, 0.125)
+    off = torch.sigmoid(gen((B, T, H), 62 + T))
+    q, k = _augment_offset(q0, k0, off, M, E, Ep)
+    q, k = q.to(dtype), k.to(dtype)
+    v = gen((B, T, H, dv), 63 + T, 0.125).to(dtype)
+    do = gen((B, T, H, dv), 64 + T).to(dtype)
+    scale = 1.0 / math.sqrt(E)
+    dev = torch.device("cuda")
+    tol = TOL[dtype]
+    if decay:
+        c = -torch.cumsum(torch.rand(B, T, H, generator=torch.Generator().manual_seed(65)) * 0.1, 1)
+        o_ref, *grads_ref = K.kata_decay_fwd_bwd(q, k, v, c, do, M, scale)
+        leaves = [x.to(dev).requires_grad_(True) for x in (q, k, v, c)]
+        o = P.parallel_kata_attn_decay(*leaves, num_groups=M, scale=scale)
+        names = ("dq", "dk", "dv", "dc")
+    else:
+        o_ref, den_ref = K.kata_fwd(q, k, v, M, scale)
+        grads_ref = K.kata_bwd(q, k, v, o_ref, den_ref, do, M, scale)
+        leaves = [x.to(dev).requires_grad_(True) for x in (q, k, v)]
+        o = P.parallel_kata_attn(*leaves, num_groups=M, scale=scale)
+        names = ("dq", "dk", "dv")
+    o.backward(do.to(dev))
+    assert mar(o, o_ref) < tol
+    fl = grad_floors(q, k, v, do)
+    fl["dc"] = 0.1 * do.abs().max().item() * v.abs().max().item()
+    for name, leaf, ref in zip(names, leaves, grads_ref):
+        e = mar(leaf.grad, ref, fl[name])
+        assert e < tol, (name, e)
+    # the zero padding of every group receives gradient only through the
+    # offset coordinate: the padded columns of dq, dk stay (numerically) zero
+    if not decay:
+        pad = leaves[0].grad.reshape(B, T, H, M, Ep)[..., E + 1:]
+        assert pad.abs().max().item() <= 1e-6 * max(1.0, leaves[0].grad.abs().max().item())
