@@ -188,6 +188,18 @@ int linatt_kata_prefill(const void* q, const void* k, const void* v, void* o, fl
                         int dv, int num_groups, float scale, float eps, int seg_len,
                         int head_major, int dtype, void* stream);
 
+/* linatt_kata_prefill continued from a state: S_in (B,H,M*E^2,dv) and z_in
+ * (B,H,M*E^2) float32 (both NULL: zero state) hold the state after the
+ * tokens before q's first one; every output, and S_out / z_out, then covers
+ * those tokens too.  S_out / z_out may alias S_in / z_in (in-place update).
+ * The prefill a past_key_values cache needs to append a chunk of tokens to a
+ * state (the reference keeps none for its flash path, kata/layer.py:492). */
+int linatt_kata_prefill_state(const void* q, const void* k, const void* v, void* o, float* den,
+                              const float* S_in, const float* z_in, float* S_out, float* z_out,
+                              void* workspace, int B, int T, int H, int dk, int dv, int num_groups,
+                              float scale, float eps, int seg_len, int head_major, int dtype,
+                              void* stream);
+
 /* One recurrent decode token per (b, h): S += psi(sqrt(scale) k) v^T,
  * z += psi(sqrt(scale) k), o = psi(sqrt(scale) q)^T S / max(psi(sqrt(scale) q).z, eps).
  * q, k (B,H,dk), v, o (B,H,dv); S, z updated in place.  No reference

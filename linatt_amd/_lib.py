@@ -54,6 +54,7 @@ SIGNATURES = {
     "linatt_kata_state_supported": (_i, [_i, _i, _i, _i]),
     "linatt_kata_prefill_workspace_bytes": (_sz, [_i] * 8),
     "linatt_kata_prefill": (_i, [_vp] * 8 + [_i] * 6 + [_f, _f, _i, _i, _i, _vp]),
+    "linatt_kata_prefill_state": (_i, [_vp] * 10 + [_i] * 6 + [_f, _f, _i, _i, _i, _vp]),
     "linatt_kata_decode_step": (_i, [_vp] * 6 + [_i] * 5 + [_f, _f, _i, _vp]),
 }
 

@@ -411,19 +411,23 @@ size_t linatt_kata_prefill_workspace_bytes(int B, int T, int H, int dk, int dv, 
   return state_ws(B, T, H, dk, dv, num_groups, seg_len, dtype).bytes;
 }
 
-int linatt_kata_prefill(const void* q, const void* k, const void* v, void* o, float* den,
-                        float* S_out, float* z_out, void* workspace, int B, int T, int H, int dk,
-                        int dv, int num_groups, float scale, float eps, int seg_len,
-                        int head_major, int dtype, void* stream) {
+int linatt_kata_prefill_state(const void* q, const void* k, const void* v, void* o, float* den,
+                              const float* S_in, const float* z_in, float* S_out, float* z_out,
+                              void* workspace, int B, int T, int H, int dk, int dv, int num_groups,
+                              float scale, float eps, int seg_len, int head_major, int dtype,
+                              void* stream) {
   g_last_error.clear();
-  int st = check_state("linatt_kata_prefill", B, T, H, dk, dv, num_groups, scale, eps, seg_len, dtype);
+  const char* fn = "linatt_kata_prefill_state";
+  int st = check_state(fn, B, T, H, dk, dv, num_groups, scale, eps, seg_len, dtype);
   if (st) return st;
   if (!q || !k || !v || !o || !den || !workspace)
-    return fail(LINATT_EINVAL, "linatt_kata_prefill: null tensor pointer");
-  const void* ps[] = {q, k, v, o, workspace, S_out, z_out};
+    return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  if ((S_in == nullptr) != (z_in == nullptr))
+    return fail(LINATT_EINVAL, std::string(fn) + ": S_in and z_in must be given together");
+  const void* ps[] = {q, k, v, o, workspace, S_out, z_out, S_in, z_in};
   for (const void* p : ps)
     if (p && !aligned16(p))
-      return fail(LINATT_EINVAL, "linatt_kata_prefill: tensors must be 16-byte aligned");
+      return fail(LINATT_EINVAL, std::string(fn) + ": tensors must be 16-byte aligned");
   const StateWs w = state_ws(B, T, H, dk, dv, num_groups, seg_len, dtype);
   char* ws = (char*)workspace;
   KataStateArgs a{};
@@ -441,7 +445,7 @@ int linatt_kata_prefill(const void* q, const void* k, const void* v, void* o, fl
   }
   a.seg_S = (float*)(ws + w.seg_S); a.seg_z = (float*)(ws + w.seg_z);
   a.HT = ws + w.HT; a.Hz = (float*)(ws + w.Hz);
-  a.S_out = S_out; a.z_out = z_out;
+  a.S_out = S_out; a.z_out = z_out; a.S_in = S_in; a.z_in = z_in;
   a.B = B; a.T = T; a.H = H; a.L = seg_len; a.nseg = (T + seg_len - 1) / seg_len;
   a.scale = scale; a.scale2 = scale * scale; a.eps = eps;
   hipError_t e = hipErrorInvalidValue;
@@ -451,8 +455,17 @@ int linatt_kata_prefill(const void* q, const void* k, const void* v, void* o, fl
   LINATT_KATA_STATE_SHAPES(LINATT_TRY_S)
 #undef LINATT_TRY_S
   if (e != hipSuccess)
-    return fail(LINATT_ELAUNCH, std::string("linatt_kata_prefill: launch failed: ") + hipGetErrorString(e));
+    return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
   return LINATT_OK;
+}
+
+int linatt_kata_prefill(const void* q, const void* k, const void* v, void* o, float* den,
+                        float* S_out, float* z_out, void* workspace, int B, int T, int H, int dk,
+                        int dv, int num_groups, float scale, float eps, int seg_len,
+                        int head_major, int dtype, void* stream) {
+  return linatt_kata_prefill_state(q, k, v, o, den, nullptr, nullptr, S_out, z_out, workspace, B,
+                                   T, H, dk, dv, num_groups, scale, eps, seg_len, head_major,
+                                   dtype, stream);
 }
 
 int linatt_kata_decode_step(const void* q, const void* k, const void* v, float* S, float* z,

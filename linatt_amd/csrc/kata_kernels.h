@@ -79,6 +79,8 @@ struct KataStateArgs {
   float* Hz;           // (B*H, nseg, P) f32 scratch
   float* S_out;        // (B, H, P, DV) f32 final state psi(sqrt(scale) k) v^T, or null
   float* z_out;        // (B, H, P) f32, or null
+  const float* S_in;   // (B, H, P, DV) f32 state before the first token (may alias S_out), or null
+  const float* z_in;   // (B, H, P) f32 (may alias z_out), or null; set together with S_in
   int B, T, H, L, nseg;
   float scale, scale2, eps;
 };

@@ -225,7 +225,20 @@ __global__ __launch_bounds__(256) void kata_seg_scan_kernel(KataStateArgs a) {
   const int64_t rem = idx % per_bh;
   const int v = (int)(rem / (P / 4));
   const int p = 4 * (int)(rem % (P / 4));
+  // the running sum starts from the initial state (stored scaled by
+  // `scale`; the scan runs unscaled); each thread reads, then writes, only
+  // its own state elements, so S_in may alias S_out
   float4 run = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (a.S_in) {
+    const float is = 1.f / a.scale;
+    if (v < DV) {
+      const float* si = a.S_in + ((size_t)bh * P + p) * DV + v;
+      run = make_float4(si[0] * is, si[DV] * is, si[2 * DV] * is, si[3 * DV] * is);
+    } else {
+      const float4 zi = *reinterpret_cast<const float4*>(a.z_in + (size_t)bh * P + p);
+      run = make_float4(zi.x * is, zi.y * is, zi.z * is, zi.w * is);
+    }
+  }
   for (int seg = 0; seg < a.nseg; ++seg) {
     const size_t base = (size_t)bh * a.nseg + seg;
     float4 x;
@@ -314,7 +327,9 @@ __global__ __launch_bounds__(256, 2) void kata_prefill_out_kernel(KataStateArgs 
     st4<T>(qa_row + 16 * kk + 8 * hh + 4, v4_t<T>{x[4], x[5], x[6], x[7]});
   }
   __syncthreads();
-  if (seg > 0) {  // uniform: a 128-query tile never straddles a segment
+  // uniform: a 128-query tile never straddles a segment; the first segment's
+  // prefix is the initial state, or zero
+  if (seg > 0 || a.S_in) {
     const size_t base = (size_t)bh * a.nseg + seg;
     const u32x4* hT = reinterpret_cast<const u32x4*>((const T*)a.HT + base * DV * P);
     const float* hz = a.Hz + base * P;

@@ -7,8 +7,9 @@ recurrent decode step.
   inputs, returns ``(o, den)`` with ``o = num / max(den, eps)``.  ``C``,
   ``warps`` and ``stages`` are accepted and ignored; ``feature`` must be
   ``"quad"``.
-* ``kata_prefill(q, k, v, num_groups=4, scale=None, eps=1e-6, seg_len=1024)``
-  takes the time-major ``(B, T, H, D)`` layout of the flash path and also
+* ``kata_prefill(q, k, v, num_groups=4, scale=None, eps=1e-6, seg_len=1024,
+  initial_state=None)`` takes the time-major ``(B, T, H, D)`` layout of the
+  flash path, optionally continues from a state ``(S0, z0)``, and also
   returns the state after the last token: ``S = sum_s psi(sqrt(scale) k_s)
   v_s^T`` ``(B, H, M*E*E, dv)`` and ``z = sum_s psi(sqrt(scale) k_s)``
   ``(B, H, M*E*E)``, float32, ``psi(x) = vec(x_g x_g^T)`` per group.
@@ -18,7 +19,7 @@ recurrent decode step.
   reference's flash path keeps no decode state (``kata/layer.py:492``); this
   is the state the ``past_key_values`` cache would hold.
 
-All three run in ``liblinatt_hip.so`` (``linatt_kata_prefill``,
+All three run in ``liblinatt_hip.so`` (``linatt_kata_prefill_state``,
 ``linatt_kata_decode_step``); unsupported shapes raise.
 """
 
@@ -47,7 +48,8 @@ def _check(dtype, dk, dv, M):
     return L
 
 
-def _prefill(q, k, v, M, scale, eps, seg_len, head_major, want_state):
+def _prefill(q, k, v, M, scale, eps, seg_len, head_major, want_state, initial_state=None,
+             in_place=False):
     _lib.require_device(q, k, v)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     if not (q.dtype == k.dtype == v.dtype):
@@ -67,16 +69,29 @@ def _prefill(q, k, v, M, scale, eps, seg_len, head_major, want_state):
     P = M * (dk // M) ** 2
     o = torch.empty_like(v)
     den = torch.empty(q.shape[:-1], device=q.device, dtype=torch.float32)
+    S0 = z0 = None
+    if initial_state is not None:
+        S0, z0 = initial_state
+        _lib.require_device(S0, z0)
+        if (S0.shape != (B, H, P, dv) or z0.shape != (B, H, P) or S0.dtype != torch.float32
+                or z0.dtype != torch.float32 or S0.device != q.device or z0.device != q.device):
+            raise ValueError(f"initial_state must be float32 S {(B, H, P, dv)}, z {(B, H, P)} "
+                             f"on {q.device}")
+        S0, z0 = S0.contiguous(), z0.contiguous()
     S = z = None
-    if want_state:
+    if in_place and S0 is not None:
+        if not (initial_state[0].is_contiguous() and initial_state[1].is_contiguous()):
+            raise ValueError("an in-place state must be contiguous")
+        S, z = S0, z0  # the scan reads each state element before it writes it
+    elif want_state:
         S = torch.empty(B, H, P, dv, device=q.device, dtype=torch.float32)
         z = torch.empty(B, H, P, device=q.device, dtype=torch.float32)
     ws = torch.empty(L.linatt_kata_prefill_workspace_bytes(B, T, H, dk, dv, M, seg_len, dt),
                      device=q.device, dtype=torch.uint8)
-    _lib.check("linatt_kata_prefill", L.linatt_kata_prefill(
-        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(den), _lib.ptr(S),
-        _lib.ptr(z), _lib.ptr(ws), B, T, H, dk, dv, M, sc, float(eps), seg_len,
-        1 if head_major else 0, dt, _lib.stream_of(q)))
+    _lib.check("linatt_kata_prefill_state", L.linatt_kata_prefill_state(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(den), _lib.ptr(S0),
+        _lib.ptr(z0), _lib.ptr(S), _lib.ptr(z), _lib.ptr(ws), B, T, H, dk, dv, M, sc, float(eps),
+        seg_len, 1 if head_major else 0, dt, _lib.stream_of(q)))
     return o, den, S, z
 
 
@@ -90,9 +105,14 @@ def spd_chunk_scan_cat(q, k, v, M, scale=None, C=32, eps=1e-6, warps=4, stages=N
     return o, den
 
 
-def kata_prefill(q, k, v, num_groups=4, scale=None, eps=1e-6, seg_len=1024):
-    """Time-major ``(B, T, H, D)`` prefill: ``(o, den, S, z)``."""
-    return _prefill(q, k, v, num_groups, scale, eps, seg_len, False, True)
+def kata_prefill(q, k, v, num_groups=4, scale=None, eps=1e-6, seg_len=1024, initial_state=None,
+                 in_place=False):
+    """Time-major ``(B, T, H, D)`` prefill: ``(o, den, S, z)``.  With
+    ``initial_state=(S0, z0)`` (the state after earlier tokens) the outputs and
+    the returned state also cover those tokens; ``in_place=True`` writes that
+    state back into ``S0, z0`` (returned as ``S, z``)."""
+    return _prefill(q, k, v, num_groups, scale, eps, seg_len, False, True, initial_state,
+                    in_place)
 
 
 def kata_decode_step(S, z, q, k, v, num_groups=4, scale=None, eps=1e-6):

@@ -127,3 +127,43 @@ def test_decode_step_validates_shapes_before_launch():
     # well-formed CPU tensors still raise: there is no CPU path
     with pytest.raises(RuntimeError, match="no CPU path"):
         spd_state.kata_decode_step(S, z, q, q, _cpu(B, H, D))
+
+
+# ---------------------------------------------------------------------------
+# the decode cache's host logic (linatt_amd.kata_cache)
+# ---------------------------------------------------------------------------
+
+
+def test_layer_state_cache_contract():
+    from linatt_amd.kata_cache import LayerStateCache, get_layer_cache, update_layer_cache
+
+    class Layer:
+        def __init__(self, i):
+            self.layer_idx = i
+
+    l0, l1 = Layer(0), Layer(1)
+    assert get_layer_cache(l0, None) is None
+    assert update_layer_cache(l0, None, recurrent_state=1) is None
+    cache = LayerStateCache()
+    assert get_layer_cache(l0, cache) is None and cache.get_seq_length() == 0
+    update_layer_cache(l0, cache, recurrent_state="s0", conv_state="c0", offset=7)
+    update_layer_cache(l1, cache, recurrent_state="s1", offset=7)
+    assert len(cache) == 2 and cache.get_seq_length() == 7
+    assert get_layer_cache(l0, cache)["recurrent_state"] == "s0"
+    # a later update replaces only the entries it names
+    update_layer_cache(l0, cache, recurrent_state="s0b", offset=1)
+    assert cache[0] == {"recurrent_state": "s0b", "attn_state": None, "conv_state": "c0",
+                        "ffn_state": None}
+    assert cache.get_seq_length() == 8
+    with pytest.raises(IndexError):
+        cache.update(recurrent_state="x", layer_idx=5)
+
+
+def test_cached_attention_validates_shapes():
+    from linatt_amd.kata_cache import KataState, parallel_kata_attn_cached
+    q = _cpu(2, 3, 4, 64)
+    with pytest.raises(ValueError, match="q, k must be"):
+        parallel_kata_attn_cached(q, _cpu(2, 3, 4, 32), q)
+    st = KataState(torch.zeros(1, 4, 1024, 64), torch.zeros(1, 4, 1024), 10)
+    with pytest.raises(ValueError, match="state is for"):
+        parallel_kata_attn_cached(q, q, q, st)

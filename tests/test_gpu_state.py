@@ -160,3 +160,88 @@ def test_config5_full_size(S_):
                                              sl(vd_), M)
             S_ref[(bb, hh)] = (Sr[0, 0], zr[0, 0])
             assert mar(od[bb, hh], o_r[0, 0]) < TOL, (i, bb, hh)
+
+
+# ---------------------------------------------------------------------------
+# decode cache (linatt_amd.kata_cache): prefill, continued prefill, decode
+# steps, all against the flash forward over every token so far
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("M", [4, 2])
+def test_cache_prefill_then_decode_equals_parallel(M):
+    from linatt_amd import parallel_kata_attn as P
+    from linatt_amd.kata_cache import parallel_kata_attn_cached
+    B, H, n, steps = 2, 3, 300, 5
+    T = n + steps
+    q, k, v = gen((B, T, H, 64), 70), gen((B, T, H, 64), 71), gen((B, T, H, 64), 72)
+    dev = torch.device("cuda")
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    o_par, _ = P.parallel_kata_attn_fwd(qd, kd, vd, num_groups=M)
+    o_ref, _ = K.kata_fwd(q, k, v, M)
+    o_pre, st = parallel_kata_attn_cached(qd[:, :n], kd[:, :n], vd[:, :n], None, M)
+    assert st.offset == n
+    assert mar(o_pre, o_ref[:, :n]) < TOL
+    for i in range(steps):
+        t = n + i
+        o_t, st = parallel_kata_attn_cached(qd[:, t:t + 1], kd[:, t:t + 1], vd[:, t:t + 1], st, M)
+        assert o_t.shape == (B, 1, H, 64) and st.offset == t + 1
+        assert mar(o_t[:, 0], o_ref[:, t]) < TOL, i
+        assert mar(o_t[:, 0], o_par[:, t].float()) < TOL, i
+    # the state after all tokens equals the psi sums of every key
+    S_ref, z_ref = K.kata_state_prefill(k, v, M)
+    assert mar(st.S, S_ref) < TOL and mar(st.z, z_ref) < TOL
+
+
+@pytest.mark.parametrize("split", [(200, 333), (128, 1), (1, 256), (1100, 500)])
+def test_cache_continued_prefill(split):
+    """Prefill of n1 tokens continued by a prefill of n2 (the scan starts from
+    the cached state) equals one prefill of n1 + n2, outputs and state."""
+    from linatt_amd.kata_cache import parallel_kata_attn_cached
+    n1, n2 = split
+    B, H, M = 1, 2, 4
+    T = n1 + n2
+    q, k, v = gen((B, T, H, 64), 73 + T), gen((B, T, H, 64), 74 + T), gen((B, T, H, 64), 75 + T)
+    dev = torch.device("cuda")
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    o_all, st_all = parallel_kata_attn_cached(qd, kd, vd, None, M)
+    o1, st = parallel_kata_attn_cached(qd[:, :n1], kd[:, :n1], vd[:, :n1], None, M)
+    o2, st = parallel_kata_attn_cached(qd[:, n1:], kd[:, n1:], vd[:, n1:], st, M)
+    assert st.offset == T
+    o_ref, _ = K.kata_fwd(q, k, v, M)
+    assert mar(torch.cat([o1, o2], 1), o_ref) < TOL
+    assert mar(o2, o_all[:, n1:].float()) < TOL
+    # the prefill forms segment states by MFMA from bf16-rounded psi features,
+    # a one-token continuation (the decode step) adds fp32 products: the two
+    # states agree to bf16 rounding, not bit for bit
+    assert mar(st.S, st_all.S) < 2e-3 and mar(st.z, st_all.z) < 2e-3
+
+
+def test_layer_cache_decode_loop():
+    """Two mixer layers keeping their state through the fla-style helpers:
+    a prompt, then three generated tokens, as an incremental generate() does."""
+    from linatt_amd.kata_cache import (LayerStateCache, get_layer_cache, parallel_kata_attn_cached,
+                                       update_layer_cache)
+
+    class Layer:
+        def __init__(self, i):
+            self.layer_idx = i
+
+    layers = [Layer(0), Layer(1)]
+    B, H, n, M = 2, 2, 129, 4
+    T = n + 3
+    dev = torch.device("cuda")
+    xs = [[gen((B, T, H, 64), 80 + 10 * li + j).to(dev) for j in range(3)] for li in range(2)]
+    cache = LayerStateCache()
+    outs = [[], []]
+    for lo, hi in [(0, n), (n, n + 1), (n + 1, n + 2), (n + 2, n + 3)]:
+        for layer, (q, k, v) in zip(layers, xs):
+            last = get_layer_cache(layer, cache)
+            rec = last["recurrent_state"] if last is not None else None
+            o, fin = parallel_kata_attn_cached(q[:, lo:hi], k[:, lo:hi], v[:, lo:hi], rec, M)
+            update_layer_cache(layer, cache, recurrent_state=fin, offset=hi - lo)
+            outs[layer.layer_idx].append(o)
+    assert cache.get_seq_length() == T
+    for li, (q, k, v) in enumerate(xs):
+        o_ref, _ = K.kata_fwd(q.cpu(), k.cpu(), v.cpu(), M)
+        assert mar(torch.cat(outs[li], 1), o_ref) < TOL
