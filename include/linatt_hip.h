@@ -209,6 +209,26 @@ int linatt_kata_decode_step(const void* q, const void* k, const void* v, float* 
                             void* o, int B, int H, int dk, int dv, int num_groups, float scale,
                             float eps, int dtype, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * SPD delta rule (DeltaKata), forward.  Replaces the forward of flash_delta
+ * (kata/spd/flash_delta.py:1060-1116: _flash_U_kernel :25-183,
+ * _readout_kernel :898-972, _den_kernel :986-1046), called by the mixer's
+ * delta branch (kata/layer.py:377-420).  With the sum-SPD kernel
+ * kappa(a, b) = sum_{g,h} (scale a_g . b_h)^2 (the reference's sqrt(scale)
+ * on q and on k):
+ *   U = (I + diag(beta) strict_lower(kappa(k, k)))^-1 diag(beta) V,
+ *   den_t = sum_{s<=t} kappa(q_t, k_s),  num = lower(kappa(q, k)) U,
+ *   o = normalize ? num / (den + eps) : num.
+ *   q, k (B,T,H,d), v (B,T,H,dv) [dtype]; beta (B,T,H) float32;
+ *   U (B,T,H,dv) float32 (may be NULL), o (B,T,H,dv) float32, den (B,T,H) float32.
+ * workspace: linatt_dkata_workspace_bytes. */
+int linatt_dkata_supported(int dtype, int d, int dv, int num_groups);
+size_t linatt_dkata_workspace_bytes(int B, int T, int H, int d, int dv, int dtype);
+int linatt_dkata_fwd(const void* q, const void* k, const void* v, const float* beta, float* U,
+                     float* o, float* den, void* workspace, int B, int T, int H, int d, int dv,
+                     int num_groups, float scale, int normalize, float eps, int dtype,
+                     void* stream);
+
 /* Row L2 normalisation over the last dim of a contiguous (n, d) array:
  * y = x / sqrt(sum x^2 + eps), rstd (n) float32 = 1 / sqrt(sum x^2 + eps);
  * backward dx = rstd (dy - y <y, dy>).  The normalisation fla applies to q

@@ -56,6 +56,9 @@ SIGNATURES = {
     "linatt_kata_prefill": (_i, [_vp] * 8 + [_i] * 6 + [_f, _f, _i, _i, _i, _vp]),
     "linatt_kata_prefill_state": (_i, [_vp] * 10 + [_i] * 6 + [_f, _f, _i, _i, _i, _vp]),
     "linatt_kata_decode_step": (_i, [_vp] * 6 + [_i] * 5 + [_f, _f, _i, _vp]),
+    "linatt_dkata_supported": (_i, [_i, _i, _i, _i]),
+    "linatt_dkata_workspace_bytes": (_sz, [_i] * 6),
+    "linatt_dkata_fwd": (_i, [_vp] * 8 + [_i] * 6 + [_f, _i, _f, _i, _vp]),
 }
 
 

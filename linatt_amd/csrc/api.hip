@@ -399,6 +399,59 @@ int linatt_l2norm_bwd(const void* y, const float* rstd, const void* dy, void* dx
   return LINATT_OK;
 }
 
+int linatt_dkata_supported(int dtype, int d, int dv, int num_groups) {
+#define LINATT_HAS_DK(T_, D_, DV_, M_) \
+  if (dtype == dtype_of<T_>() && d == D_ && dv == DV_ && num_groups == M_) return 1;
+  LINATT_DKATA_SHAPES(LINATT_HAS_DK)
+#undef LINATT_HAS_DK
+  return 0;
+}
+
+size_t linatt_dkata_workspace_bytes(int B, int T, int H, int d, int dv, int dtype) {
+  if (B <= 0 || T <= 0 || H <= 0 || d <= 0 || dv <= 0) return 0;
+  return dkata_layout(B, T, H, d, dv, elt_bytes(dtype)).bytes;
+}
+
+int linatt_dkata_fwd(const void* q, const void* k, const void* v, const float* beta, float* U,
+                     float* o, float* den, void* workspace, int B, int T, int H, int d, int dv,
+                     int num_groups, float scale, int normalize, float eps, int dtype,
+                     void* stream) {
+  g_last_error.clear();
+  const char* fn = "linatt_dkata_fwd";
+  char buf[160];
+  snprintf(buf, sizeof buf, "B=%d T=%d H=%d d=%d dv=%d num_groups=%d", B, T, H, d, dv, num_groups);
+  if (B <= 0 || T <= 0 || H <= 0 || d <= 0 || dv <= 0 || num_groups <= 0)
+    return fail(LINATT_EINVAL, std::string(fn) + ": non-positive dimension (" + buf + ")");
+  if (!(scale > 0.f) || (normalize && !(eps >= 0.f)))
+    return fail(LINATT_EINVAL, std::string(fn) + ": scale must be positive and eps non-negative");
+  if ((int64_t)B * H * (T + 63) > (int64_t)INT32_MAX / 2)
+    return fail(LINATT_EINVAL, std::string(fn) + ": B*H*T too large");
+  if (!linatt_dkata_supported(dtype, d, dv, num_groups))
+    return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": no kernel compiled for dtype " +
+                                         std::to_string(dtype) + " (" + buf + ")");
+  if (!q || !k || !v || !beta || !o || !den || !workspace)
+    return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  const void* ps[] = {q, k, v, o, U, workspace};
+  for (const void* p : ps)
+    if (p && !aligned16(p))
+      return fail(LINATT_EINVAL, std::string(fn) + ": tensors must be 16-byte aligned");
+  DKataArgs a{};
+  a.q = q; a.k = k; a.v = v; a.beta = beta; a.U = U; a.o = o; a.den = den;
+  a.ws = (char*)workspace;
+  a.L = dkata_layout(B, T, H, d, dv, elt_bytes(dtype));
+  a.B = B; a.T = T; a.H = H;
+  a.scale = scale; a.scale2 = scale * scale; a.eps = eps; a.normalize = normalize ? 1 : 0;
+  hipError_t e = hipErrorInvalidValue;
+#define LINATT_TRY_DK(T_, D_, DV_, M_) \
+  if (dtype == dtype_of<T_>() && d == D_ && dv == DV_ && num_groups == M_) \
+    e = launch_dkata_fwd<T_, D_, DV_, M_>(a, (hipStream_t)stream);
+  LINATT_DKATA_SHAPES(LINATT_TRY_DK)
+#undef LINATT_TRY_DK
+  if (e != hipSuccess)
+    return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
 int linatt_kata_state_supported(int dtype, int dk, int dv, int num_groups) {
   return state_compiled(dtype, dk, dv, num_groups) ? 1 : 0;
 }

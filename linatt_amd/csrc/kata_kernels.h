@@ -108,3 +108,45 @@ hipError_t launch_kata_decode(const KataDecodeArgs& a, hipStream_t stream);
   X(__bf16, 64, 64, 2)
 
 }  // namespace linatt
+
+namespace linatt {
+
+// SPD delta rule (DeltaKata) forward: workspace layout (byte offsets) and
+// launch arguments.
+struct DKataLayout {
+  size_t TmHi, TmLo;  // (B*H, NC, 64, 64) T: Tm = (I + N)^-1 per chunk, hi + lo
+  size_t UT;          // (B*H, DV, 64 NC) T: U^T
+  size_t Ub;          // (B, T, H, DV) T: U for the readout
+  size_t Ob;          // (B, T, H, DV) T: readout num / den
+  size_t bytes;
+};
+DKataLayout dkata_layout(int B, int T, int H, int D, int DV, int eb);
+
+struct DKataArgs {
+  const void* q;      // (B, T, H, D) time-major
+  const void* k;
+  const void* v;      // (B, T, H, DV)
+  const float* beta;  // (B, T, H)
+  float* U;           // (B, T, H, DV) f32 pseudo-values, or null
+  float* o;           // (B, T, H, DV) f32
+  float* den;         // (B, T, H) f32
+  char* ws;
+  DKataLayout L;
+  int B, T, H;
+  float scale, scale2, eps;
+  int normalize;
+};
+
+template <typename T, int D, int DV, int M>
+hipError_t launch_dkata_fwd(const DKataArgs& a, hipStream_t stream);
+
+// Compiled (dtype, D, DV, M) combinations of the SPD delta rule.
+#define LINATT_DKATA_SHAPES(X) \
+  X(__bf16, 64, 64, 1)         \
+  X(__bf16, 64, 64, 2)         \
+  X(__bf16, 64, 64, 4)         \
+  X(_Float16, 64, 64, 1)       \
+  X(_Float16, 64, 64, 2)       \
+  X(_Float16, 64, 64, 4)
+
+}  // namespace linatt

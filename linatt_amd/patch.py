@@ -18,6 +18,10 @@ Names rebound (only in modules that are importable; the rest are skipped):
   (``kata/layer.py:29-37``), so rebinding the defining module alone would not
   reach the mixer;
 * ``kata.spd.chunk_scan_cat.spd_chunk_scan_cat``;
+* the SPD delta rule's forward pieces ``flash_delta_U``,
+  ``flash_delta_readout`` and ``flash_delta_den`` in ``kata.spd.flash_delta``
+  (``flash_delta`` itself stays the reference's while its backward has no
+  HIP kernel here, so training through the mixer keeps working);
 * fla's delta-rule ops where fla's layers bind them
   (``fla.layers.delta_net.chunk_delta_rule``,
   ``fla.layers.gated_deltanet.chunk_gated_delta_rule``) and where fla defines
@@ -42,6 +46,8 @@ TARGETS = (
                    "parallel_kata_attn_sum_fwd_impl", "parallel_kata_attn_decay",
                    "parallel_kata_attn_bwd", "parallel_kata_attn_bwd_triton")),
     ("kata.spd.chunk_scan_cat", "spd_chunk_scan_cat", "spd_state", "spd_chunk_scan_cat"),
+    *(("kata.spd.flash_delta", name, "flash_delta", name)
+      for name in ("flash_delta_U", "flash_delta_readout", "flash_delta_den")),
     ("fla.layers.delta_net", "chunk_delta_rule", "delta_rule", "chunk_delta_rule"),
     ("fla.ops.delta_rule", "chunk_delta_rule", "delta_rule", "chunk_delta_rule"),
     ("fla.layers.gated_deltanet", "chunk_gated_delta_rule", "delta_rule", "chunk_gated_delta_rule"),

@@ -25,6 +25,7 @@ def _orig(tag):
     return f
 
 
+DELTA_KATA_NAMES = ("flash_delta", "flash_delta_U", "flash_delta_readout", "flash_delta_den")
 KATA_NAMES = ("parallel_kata_attn", "parallel_kata_attn_fwd", "parallel_kata_attn_sum",
               "parallel_kata_attn_sum_fwd_impl", "parallel_kata_attn_decay",
               "parallel_kata_attn_bwd", "parallel_kata_attn_bwd_triton")
@@ -42,6 +43,8 @@ def stub_reference(monkeypatch):
         "kata.layer": _stub("kata.layer", **{n: _orig("layer_" + n) for n in KATA_NAMES[:5]}),
         "kata.spd": _stub("kata.spd"),
         "kata.spd.chunk_scan_cat": _stub("kata.spd.chunk_scan_cat", spd_chunk_scan_cat=_orig("ref_scan")),
+        "kata.spd.flash_delta": _stub("kata.spd.flash_delta",
+                                      **{n: _orig("ref_" + n) for n in DELTA_KATA_NAMES}),
         "fla": _stub("fla"),
         "fla.layers": _stub("fla.layers"),
         "fla.layers.delta_net": _stub("fla.layers.delta_net", chunk_delta_rule=_orig("fla_dn")),
@@ -68,11 +71,16 @@ def test_patch_rebinds_every_name(stub_reference):
     # a name the mixer never imported is not added to it
     assert not hasattr(m["kata.layer"], "parallel_kata_attn_bwd")
     assert m["kata.spd.chunk_scan_cat"].spd_chunk_scan_cat is spd_state.spd_chunk_scan_cat
+    from linatt_amd import flash_delta as fd
+    for n in DELTA_KATA_NAMES[1:]:
+        assert getattr(m["kata.spd.flash_delta"], n) is getattr(fd, n)
+    # no HIP backward yet: the trainable op stays the reference's
+    assert m["kata.spd.flash_delta"].flash_delta() == "ref_flash_delta"
     assert m["fla.layers.delta_net"].chunk_delta_rule is delta_rule.chunk_delta_rule
     assert m["fla.ops.delta_rule"].chunk_delta_rule is delta_rule.chunk_delta_rule
     assert m["fla.layers.gated_deltanet"].chunk_gated_delta_rule is delta_rule.chunk_gated_delta_rule
     assert m["fla.ops.gated_delta_rule"].chunk_gated_delta_rule is delta_rule.chunk_gated_delta_rule
-    assert len(done) == len(KATA_NAMES) + 5 + 5
+    assert len(done) == len(KATA_NAMES) + 5 + 5 + 3
 
 
 def test_patch_is_idempotent_and_restorable(stub_reference):
@@ -167,3 +175,11 @@ def test_cached_attention_validates_shapes():
     st = KataState(torch.zeros(1, 4, 1024, 64), torch.zeros(1, 4, 1024), 10)
     with pytest.raises(ValueError, match="state is for"):
         parallel_kata_attn_cached(q, q, q, st)
+
+
+def test_flash_delta_validates_before_launch():
+    from linatt_amd import flash_delta as fd
+    q = _cpu(1, 8, 2, 64)
+    beta = _cpu(1, 8, 2, dtype=torch.float32)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        fd.flash_delta(q, q, q, beta, 1)

@@ -1,0 +1,170 @@
+"""GPU parity of the SPD delta rule (``linatt_amd.flash_delta``, C ABI
+``linatt_dkata_fwd``) against the float64 CPU oracle ``oracle.delta_kata``.
+
+Inputs are drawn on the CPU from seeded generators, rounded once to the test
+dtype, and the same rounded tensors feed both sides.  q and k are
+l2-normalised per head, as the delta mixer does (``norm_q: l2``, ``norm_k:
+l2`` in ``configs/model/kata_delta_m1_340m.yaml``), so that
+``beta kappa(k, k) <= 1`` and the delta recursion stays bounded; beta is a
+sigmoid of a normal draw.  Error metric: ``max|x - ref| / max|ref|`` per
+tensor; bars: bfloat16 2e-2, float16 1e-2.
+"""
+
+import pytest
+import torch
+
+from oracle import delta_kata as DK
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.bfloat16: 2e-2, torch.float16: 1e-2}
+
+
+def mar(x, ref):
+    x = x.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    den = ref.abs().max().item()
+    return (x - ref).abs().max().item() / (den if den > 0 else 1.0)
+
+
+def make(B, T, H, D, DV, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.nn.functional.normalize(torch.randn(B, T, H, D, generator=g), dim=-1).to(dtype)
+    k = torch.nn.functional.normalize(torch.randn(B, T, H, D, generator=g), dim=-1).to(dtype)
+    v = torch.randn(B, T, H, DV, generator=g).to(dtype)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g))
+    return q, k, v, beta
+
+
+@pytest.fixture(scope="module")
+def F():
+    from linatt_amd import flash_delta as F
+    return F
+
+
+def dev(*ts):
+    return [t.cuda() for t in ts]
+
+
+SHAPES = [  # B, T, H
+    (1, 1, 1),
+    (2, 37, 2),
+    (1, 64, 1),
+    (1, 129, 3),
+    (2, 300, 2),
+    (1, 700, 2),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("scale", [None, 0.5, 1.0])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_forward_parity(F, shape, M, scale, dtype):
+    B, T, H = shape
+    q, k, v, beta = make(B, T, H, 64, 64, dtype, 7 + T + M)
+    print(f"\nflash_delta B={B} T={T} H={H} M={M} scale={scale} {dtype}", flush=True)
+    o_ref, U_ref, num_ref, den_ref = DK.flash_delta_fwd(q, k, v, beta, M, scale)
+    qd, kd, vd, bd = dev(q, k, v, beta)
+    tol = TOL[dtype]
+    U = F.flash_delta_U(qd, kd, vd, bd, M, scale=scale)
+    assert U.dtype == torch.float32 and U.shape == (B, T, H, 64)
+    assert mar(U, U_ref) < tol, ("U", mar(U, U_ref))
+    o = F.flash_delta(qd, kd, vd, bd, M, scale=scale)
+    assert o.dtype == torch.float32
+    assert mar(o, num_ref) < tol, ("num", mar(o, num_ref))
+    on = F.flash_delta(qd, kd, vd, bd, M, scale=scale, normalize=True, eps=1e-5)
+    on_ref = num_ref / (den_ref[..., None] + 1e-5)
+    assert mar(on, on_ref) < tol, ("o normalised", mar(on, on_ref))
+    den = F.flash_delta_den(qd, kd, M, scale=scale)
+    assert mar(den, den_ref) < tol, ("den", mar(den, den_ref))
+    num = F.flash_delta_readout(qd, kd, U, M, scale=scale)
+    assert mar(num, num_ref) < tol, ("readout", mar(num, num_ref))
+
+
+def test_config_full_size(F):
+    """``kata_delta_m1_340m``: M = 1, H = 16 heads of 64, T = 2048,
+    delta_scale 0.5, bf16 inputs (``kata/layer.py:409-418``)."""
+    B, T, H, M = 1, 2048, 16, 1
+    q, k, v, beta = make(B, T, H, 64, 64, torch.bfloat16, 11)
+    beta = beta.bfloat16().float()  # the mixer hands beta over in bf16
+    print(f"\nflash_delta config B={B} T={T} H={H} M={M}", flush=True)
+    o_ref, U_ref, num_ref, den_ref = DK.flash_delta_fwd(q, k, v, beta, M, 0.5)
+    qd, kd, vd, bd = dev(q, k, v, beta)
+    o = F.flash_delta(qd, kd, vd, bd, M, scale=0.5)
+    assert mar(o, num_ref) < 2e-2, mar(o, num_ref)
+    U = F.flash_delta_U(qd, kd, vd, bd, M, scale=0.5)
+    assert mar(U, U_ref) < 2e-2, mar(U, U_ref)
+
+
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_orthonormal_keys_overwrite(F, M):
+    """Closed form, no oracle: with keys from the first E standard basis
+    vectors (all in group 0), scale 1 and beta = 1, ``kappa(e_a, e_b) =
+    [a == b]``, the rule overwrites, and a query ``e_a`` at time t reads the
+    value last written under key a at or before t (zero if none).  (Basis
+    vectors at the same position of different groups would collide: the
+    sum-SPD score pairs every group of q with every group of k.)"""
+    B, T, H, D = 1, 517, 2, 64
+    nkeys = D // M
+    g = torch.Generator().manual_seed(M)
+    ki = torch.randint(0, nkeys, (B, T, H), generator=g)
+    qi = torch.randint(0, nkeys, (B, T, H), generator=g)
+    eye = torch.eye(D)
+    k = eye[ki].bfloat16()
+    q = eye[qi].bfloat16()
+    v = torch.randn(B, T, H, D, generator=g).bfloat16()
+    beta = torch.ones(B, T, H)
+    want = torch.zeros(B, T, H, D)
+    for b in range(B):
+        for h in range(H):
+            last = {}
+            for t in range(T):
+                last[int(ki[b, t, h])] = v[b, t, h].float()
+                if int(qi[b, t, h]) in last:
+                    want[b, t, h] = last[int(qi[b, t, h])]
+    o = F.flash_delta(*dev(q, k, v, beta), M, scale=1.0)
+    assert mar(o, want) < 1e-2, mar(o, want)
+
+
+def test_causal_prefix_and_padding(F):
+    """Rows t < T1 depend on tokens <= t only: a prefix run equals the prefix
+    of a longer run, and zero padding (the mixer pads T up to a power of two,
+    ``kata/layer.py:383-394``) changes nothing before it."""
+    B, T, H, M = 2, 1500, 4, 2
+    q, k, v, beta = dev(*make(B, T, H, 64, 64, torch.bfloat16, 3))
+    full = F.flash_delta(q, k, v, beta, M, scale=0.5, normalize=True)
+    T1 = 701
+    pre = F.flash_delta(q[:, :T1], k[:, :T1], v[:, :T1], beta[:, :T1], M, scale=0.5,
+                        normalize=True)
+    # the two runs chunk the prefix identically, so only the readout's
+    # key-tile schedule may differ: agreement to fp32 accumulation order
+    assert mar(pre, full[:, :T1]) < 1e-5
+    pad = 2048 - T
+    zp = lambda x: torch.nn.functional.pad(x, (0, 0) * (x.dim() - 2) + (0, pad))  # noqa: E731
+    padded = F.flash_delta(zp(q), zp(k), zp(v), zp(beta), M, scale=0.5, normalize=True)
+    assert mar(padded[:, :T], full) < 1e-5
+
+
+def test_deterministic(F):
+    q, k, v, beta = dev(*make(2, 777, 3, 64, 64, torch.bfloat16, 5))
+    a = F.flash_delta(q, k, v, beta, 4, scale=0.5)
+    b = F.flash_delta(q, k, v, beta, 4, scale=0.5)
+    assert torch.equal(a, b)
+
+
+def test_backward_raises(F):
+    q, k, v, beta = dev(*make(1, 64, 1, 64, 64, torch.bfloat16, 1))
+    q.requires_grad_(True)
+    o = F.flash_delta(q, k, v, beta, 1, scale=0.5)
+    with pytest.raises(NotImplementedError, match="backward"):
+        o.sum().backward()
+
+
+def test_unsupported_shape_raises(F):
+    q, k, v, beta = dev(*make(1, 8, 1, 64, 32, torch.bfloat16, 1))
+    with pytest.raises(NotImplementedError, match="no kernel"):
+        F.flash_delta(q, k, v, beta, 1)
+    q32, k32, v32 = (x.float() for x in dev(*make(1, 8, 1, 64, 64, torch.bfloat16, 1)[:3]))
+    with pytest.raises((NotImplementedError, TypeError)):
+        F.flash_delta(q32, k32, v32, beta, 1)
