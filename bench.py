@@ -47,30 +47,52 @@ def delta_flops(B, H, T, K, V, C=64):
     """Algorithmic FLOPs of the chunked delta rule (count once, no recompute):
     per token-head C(6K+4V) + 6KV + (2/3)C^2 (Gram, QK^T, W = 3x2C^2K; U and
     the intra A.v = 2x2C^2V; W.h, Q.h, K^T v_new = 3x2CKV; the 64x64 UT
-    inverse (2/3)C^3 per chunk); backward = 2x forward."""
-    per = C * (6 * K + 4 * V) + 6 * K * V + (2.0 / 3.0) * C * C
-    fwd = per * B * H * T
-    return {"fwd": fwd, "bwd": 2 * fwd, "total": 3 * fwd}
+    inverse (2/3)C^3 per chunk); backward = 2x forward.  Split by kernel:
+    prep = Gram, QK^T, W, U, inverse; state pass = W.h, K^T v_new; output =
+    Q.h, intra A.v; reverse state pass = Aqk^T dO, K dS, Q^T dO, W^T dVn
+    (2CV + 8KV); the backward chunk kernel the rest of 2x forward."""
+    n = B * H * T
+    prep = n * (6 * C * K + 2 * C * V + (2.0 / 3.0) * C * C)
+    state = n * 4 * K * V
+    out = n * (2 * K * V + 2 * C * V)
+    fwd = prep + state + out
+    state_bwd = n * (2 * C * V + 8 * K * V)
+    return {"prep": prep, "state_fwd": state, "out": out, "fwd": fwd,
+            "state_bwd": state_bwd, "bwd_chunk": 2 * fwd - state_bwd, "bwd": 2 * fwd,
+            "total": 3 * fwd}
+
+
+def delta_state_bytes(B, H, T, K, V, gated, h0, C=64):
+    """Compulsory HBM bytes of the two state passes (bf16 tensors, fp32 g and
+    states).  Forward: k, w, u read, v_new written, g, the per-chunk states
+    h (bf16), h0 read and ht written.  Backward: q, k, w, dO read, dv_new
+    written, g, the per-chunk dh (bf16), dh0 written."""
+    n, NT = B * T * H, (T + C - 1) // C
+    gb = 4 if gated else 0
+    st = B * H * K * V * 4
+    fwd = n * (2 * K + 2 * K + 2 * V + 2 * V + gb) + B * H * NT * K * V * 2 + st * (2 if h0 else 1)
+    bwd = n * (2 * K + 2 * K + 2 * K + 2 * V + 2 * V + gb) + B * H * NT * K * V * 2 + \
+        (st if h0 else 0)
+    return {"state_fwd": fwd, "state_bwd": bwd}
+
+
+DELTA_FWD_STAGES = (("prep", 1), ("state_fwd", 2), ("out", 4))
+DELTA_BWD_STAGES = (("state_bwd", 1), ("bwd_chunk", 2))
 
 
 def bench_delta(gated, steps, warmup):
     """BASELINE config 3 (DeltaNet) / 4 (GatedDeltaNet): B8 H6 T2048 K=V=128
-    bf16, chunk 64, fwd + bwd through linatt_delta_fwd / linatt_delta_bwd with
-    preallocated outputs, context and workspace."""
+    bf16, chunk 64, fwd + bwd through the C ABI with preallocated outputs,
+    context and workspace.  Each kernel is launched on its own
+    (linatt_delta_fwd_stages / linatt_delta_bwd_stages, which together make
+    exactly the launches of linatt_delta_fwd + linatt_delta_bwd) between HIP
+    events on the launch stream, so every kernel has a measured duration."""
     import torch
     from linatt_amd import _lib
     L = _lib.load()
     B, H, T, K, V = 8, 6, 2048, 128, 128
     seed = 3 if gated else 2
-    g_ = torch.Generator().manual_seed(seed)
-    q = torch.randn(B, T, H, K, generator=g_).to(torch.bfloat16)
-    k = torch.randn(B, T, H, K, generator=g_)
-    k = (k * torch.rsqrt((k * k).sum(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
-    v = torch.randn(B, T, H, V, generator=g_).to(torch.bfloat16)
-    beta = torch.sigmoid(torch.randn(B, T, H, generator=g_))
-    g = torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=g_) + 4) / 16 if gated else None
-    h0 = torch.randn(B, H, K, V, generator=g_) * 0.02 if gated else None
-    do = torch.randn(B, T, H, V, generator=g_).to(torch.bfloat16)
+    q, k, v, beta, g, h0, do = delta_inputs(B, H, T, K, V, gated, seed)
     dev = torch.device("cuda", 0)
     qd, kd, vd, bd, dod = (x.to(dev) for x in (q, k, v, beta, do))
     gd = g.to(dev) if gated else None
@@ -91,31 +113,49 @@ def bench_delta(gated, steps, warmup):
     scale = K ** -0.5
     stream = torch.cuda.current_stream(dev)
 
-    def fwd():
-        _lib.check("linatt_delta_fwd", L.linatt_delta_fwd(
+    def fwd(stages):
+        _lib.check("linatt_delta_fwd_stages", L.linatt_delta_fwd_stages(
             P(qd), P(kd), P(vd), P(bd), P(gd), P(h0d), P(o), P(ht), P(ctx), B, T, H, K, V,
-            scale, dt, sp))
+            scale, stages, dt, sp))
 
-    def bwd():
-        _lib.check("linatt_delta_bwd", L.linatt_delta_bwd(
+    def bwd(stages):
+        _lib.check("linatt_delta_bwd_stages", L.linatt_delta_bwd_stages(
             P(qd), P(kd), P(vd), P(bd), P(gd), P(h0d), P(dod), P(dht), P(ctx), P(ws), P(dq),
-            P(dk), P(dv), P(dbeta), P(dg), P(dh0), B, T, H, K, V, scale, dt, sp))
+            P(dk), P(dv), P(dbeta), P(dg), P(dh0), B, T, H, K, V, scale, stages, dt, sp))
 
+    parts = [(n, (lambda m=m: fwd(m))) for n, m in DELTA_FWD_STAGES] + \
+            [(n, (lambda m=m: bwd(m))) for n, m in DELTA_BWD_STAGES]
     for _ in range(warmup):
-        fwd()
-        bwd()
+        for _, f in parts:
+            f()
     torch.cuda.synchronize()
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(parts) + 1)]
+          for _ in range(steps)]
     for s in range(steps):
         ev[s][0].record(stream)
-        fwd()
-        ev[s][1].record(stream)
-        bwd()
-        ev[s][2].record(stream)
+        for i, (_, f) in enumerate(parts):
+            f()
+            ev[s][i + 1].record(stream)
     torch.cuda.synchronize()
-    f_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
-    b_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / steps
+    kms = {n: sum(ev[s][i].elapsed_time(ev[s][i + 1]) for s in range(steps)) / steps
+           for i, (n, _) in enumerate(parts)}
+    f_ms = sum(kms[n] for n, _ in DELTA_FWD_STAGES)
+    b_ms = sum(kms[n] for n, _ in DELTA_BWD_STAGES)
     fl = delta_flops(B, H, T, K, V)
+    by = delta_state_bytes(B, H, T, K, V, gated, gated)
+    kern = {}
+    for n in kms:
+        e = {"avg_ms": round(kms[n], 4)}
+        if n in by:
+            gbs = by[n] / (kms[n] * 1e-3) / 1e9
+            e.update({"bound": "hbm", "alg_mb": round(by[n] / 1e6, 1), "gbs": round(gbs, 1),
+                      "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)})
+        tf = fl[n] / (kms[n] * 1e-3) / 1e12
+        e.update({"alg_gflop": round(fl[n] / 1e9, 2), "tflops": round(tf, 1),
+                  "frac_mfma_peak": round(tf / PEAK_BF16_TFLOPS, 4)})
+        if n not in by:
+            e["bound"] = "mfma"
+        kern[n] = e
     tot = f_ms + b_ms
     tf = fl["total"] / (tot * 1e-3) / 1e12
     return {"config": {"B": B, "H": H, "T": T, "K": K, "V": V, "chunk": 64, "gated": gated,
@@ -123,7 +163,24 @@ def bench_delta(gated, steps, warmup):
             "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4), "ms": round(tot, 4),
             "tokens_per_s": round(B * T / (tot * 1e-3), 1),
             "alg_gflop": round(fl["total"] / 1e9, 2), "tflops": round(tf, 1),
-            "frac_mfma_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+            "frac_mfma_peak": round(tf / PEAK_BF16_TFLOPS, 4), "kernels": kern}
+
+
+def delta_inputs(B, H, T, K, V, gated, seed):
+    """Config 3 / 4 inputs, drawn on the CPU in float32 (q, v ~ N(0,1); k
+    ~ N(0,1) l2-normalised; beta = sigmoid(N(0,1)); g = logsigmoid(N(0,1)+4)/16;
+    h0 ~ N(0, 0.02^2)), rounded once to bf16 where the op takes bf16."""
+    import torch
+    g_ = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, H, K, generator=g_).to(torch.bfloat16)
+    k = torch.randn(B, T, H, K, generator=g_)
+    k = (k * torch.rsqrt((k * k).sum(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+    v = torch.randn(B, T, H, V, generator=g_).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g_))
+    g = torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=g_) + 4) / 16 if gated else None
+    h0 = torch.randn(B, H, K, V, generator=g_) * 0.02 if gated else None
+    do = torch.randn(B, T, H, V, generator=g_).to(torch.bfloat16)
+    return q, k, v, beta, g, h0, do
 
 
 def bench_state(prefill_reps, decode_steps):
@@ -211,15 +268,28 @@ def bench_state(prefill_reps, decode_steps):
             "decode_hbm_frac": round(dec_bytes / (dec_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
 
 
+def _cpu_threads():
+    """Threads for the CPU baselines: every core the host reports, capped at
+    the 16 CPUs the GPU box allots to one GPU."""
+    import torch
+    n = os.cpu_count() or 1
+    torch.set_num_threads(min(n, 16))
+    return {"cores": torch.get_num_threads(), "os_cpu_count": n, "cpu_model": _cpu_model()}
+
+
+def _oracle():
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import delta as D, kata as K
+    return K, D
+
+
 def cpu_baseline(q, k, v, do, M, seconds):
     """Time the float32 restatement of the reference path (dense forward +
     explicit backward, kata/parallel_kata_attn.py:49-146) head by head on the
     host until `seconds` elapse; return tokens/s scaled to the full step."""
     import torch
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle import kata as K
-    threads = min(os.cpu_count() or 1, 16)
-    torch.set_num_threads(threads)
+    K, _ = _oracle()
+    th = _cpu_threads()
     B, T, H, D = q.shape
     heads = [(b, h) for b in range(B) for h in range(H)]
     done = 0
@@ -233,11 +303,95 @@ def cpu_baseline(q, k, v, do, M, seconds):
             break
     el = time.perf_counter() - t0
     tokens = done / len(heads) * B * T
-    return {"value": tokens / el, "unit": "tokens/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+    return {"value": tokens / el, "unit": "tokens/s", **th, "kind": "port",
             "sample": f"{done} of {len(heads)} (batch, head) slices of config 2 "
-                      f"(T={T}, M={M}), float32 dense fwd + explicit bwd, {el:.1f} s",
-            "cpu_model": _cpu_model()}
+                      f"(T={T}, M={M}), float32 dense fwd + explicit bwd, {el:.1f} s"}
+
+
+def cpu_baseline_config1(q, M, seconds):
+    """Config 1 (forward only, (1, 4, 512, 64) fp32, M groups): the float32
+    dense forward of the reference (kata/parallel_kata_attn.py:49-75) on the
+    whole input, repeated until `seconds` elapse."""
+    import torch
+    K, _ = _oracle()
+    th = _cpu_threads()
+    B, T, H, D = q.shape
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        K.kata_fwd(q, q, q, M, work_dtype=torch.float32)
+        reps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    el = time.perf_counter() - t0
+    return {"value": reps * B * T / el, "unit": "tokens/s", **th, "kind": "port",
+            "sample": f"{reps} full config-1 forwards (B={B} T={T} H={H} M={M}), float32, "
+                      f"{el:.1f} s"}
+
+
+def cpu_baseline_delta(gated, seconds):
+    """Config 3 / 4: the chunked WY/UT restatement (oracle/delta.py) in float32
+    with autograd for the backward, (batch, head) slice by slice until
+    `seconds` elapse; tokens/s scaled to the full config."""
+    import torch
+    _, Dm = _oracle()
+    th = _cpu_threads()
+    B, H, T, Kd, Vd = 8, 6, 2048, 128, 128
+    q, k, v, beta, g, h0, do = delta_inputs(B, H, T, Kd, Vd, gated, 3 if gated else 2)
+    heads = [(b, h) for b in range(B) for h in range(H)]
+    done = 0
+    t0 = time.perf_counter()
+    for b, h in heads:
+        sl = lambda x: x[b:b + 1, :, h:h + 1].float().requires_grad_(True)  # noqa: E731
+        leaves = [sl(q), sl(k), sl(v), beta[b:b + 1, :, h:h + 1].clone().requires_grad_(True)]
+        gg = g[b:b + 1, :, h:h + 1].clone().requires_grad_(True) if gated else None
+        hh = h0[b:b + 1, h:h + 1].clone().requires_grad_(True) if gated else None
+        o, ht = Dm.delta_rule_chunked(*leaves, g=gg, scale=Kd ** -0.5, initial_state=hh)
+        (o * do[b:b + 1, :, h:h + 1].float()).sum().backward()
+        done += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    el = time.perf_counter() - t0
+    return {"value": done / len(heads) * B * T / el, "unit": "tokens/s", **th, "kind": "port",
+            "sample": f"{done} of {len(heads)} (batch, head) slices of config "
+                      f"{4 if gated else 3}, float32 chunked fwd + autograd bwd, {el:.1f} s"}
+
+
+def bench_config1(steps):
+    """Config 1 on the GPU: the fp32 KATA forward at (1, 512, 4, 64), M=4,
+    q,k,v ~ N(0,1) (seed 0), through linatt_kata_fwd."""
+    import torch
+    from linatt_amd import _lib
+    L = _lib.load()
+    B, T, H, D, M = 1, 512, 4, 64, 4
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(B, T, H, D, generator=g)
+    dev = torch.device("cuda", 0)
+    qd = q.to(dev)
+    o = torch.empty_like(qd)
+    den = torch.empty(B, T, H, device=dev)
+    sp = _lib.stream_of(qd)
+    P = _lib.ptr
+
+    def fwd():
+        _lib.check("linatt_kata_fwd", L.linatt_kata_fwd(
+            P(qd), P(qd), P(qd), None, P(o), P(den), B, T, H, H, D, D, M, 1.0 / math.sqrt(D // M),
+            0, _lib.LINATT_FLOAT32, sp))
+
+    for _ in range(3):
+        fwd()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        fwd()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return q, {"config": {"B": B, "T": T, "H": H, "D": D, "num_groups": M, "dtype": "f32",
+                          "seed": 0},
+               "fwd_ms": round(ms, 4), "tokens_per_s": round(B * T / (ms * 1e-3), 1)}
 
 
 def _cpu_model():
@@ -257,9 +411,9 @@ def _cpu_model():
 # inside the timed run, so the figure is carried here and refreshed with the
 # profile.
 MEASURED_TRAFFIC_BYTES = {
-    "fwd": int((109.2 + 30.5) * 1e6),
-    "bwd_dq": int((172.0 + 61.1) * 1e6),
-    "bwd_dkdv": int((171.7 + 50.3) * 1e6),
+    "fwd": int((122.9 + 30.5) * 1e6),
+    "bwd_dq": int((187.5 + 61.1) * 1e6),
+    "bwd_dkdv": int((170.6 + 50.3) * 1e6),
 }
 
 
@@ -381,9 +535,16 @@ def main():
     if not args.no_state:
         state = bench_state(3, args.decode_steps)
 
+    q1, config1 = bench_config1(max(10, args.steps))
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(q, k, v, do, M, args.cpu_seconds)
+        config1["cpu_baseline"] = cpu_baseline_config1(q1, 4, args.cpu_seconds / 3)
+        if delta is not None:
+            delta["deltanet_config3"]["cpu_baseline"] = cpu_baseline_delta(False, args.cpu_seconds / 3)
+            delta["gated_deltanet_config4"]["cpu_baseline"] = cpu_baseline_delta(
+                True, args.cpu_seconds / 3)
 
     out = {
         "metric": METRIC,
@@ -412,6 +573,7 @@ def main():
         "cpu_baseline": cpu,
         "delta_rule": delta,
         "kata_state_config5": state,
+        "kata_config1": config1,
     }
     print(json.dumps(out), flush=True)
 

@@ -49,6 +49,8 @@ SIGNATURES = {
     "linatt_delta_bwd_workspace_bytes": (_sz, [_i] * 6),
     "linatt_delta_fwd": (_i, [_vp] * 9 + [_i] * 5 + [_f, _i, _vp]),
     "linatt_delta_bwd": (_i, [_vp] * 16 + [_i] * 5 + [_f, _i, _vp]),
+    "linatt_delta_fwd_stages": (_i, [_vp] * 9 + [_i] * 5 + [_f, _i, _i, _vp]),
+    "linatt_delta_bwd_stages": (_i, [_vp] * 16 + [_i] * 5 + [_f, _i, _i, _vp]),
     "linatt_l2norm_fwd": (_i, [_vp, _vp, _vp, _i, _i, _f, _i, _vp]),
     "linatt_l2norm_bwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "linatt_kata_state_supported": (_i, [_i, _i, _i, _i]),

@@ -320,7 +320,17 @@ size_t linatt_delta_bwd_workspace_bytes(int B, int T, int H, int dk, int dv, int
 int linatt_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
                      const float* g, const float* h0, void* o, float* ht, void* ctx, int B,
                      int T, int H, int dk, int dv, float scale, int dtype, void* stream) {
+  return linatt_delta_fwd_stages(q, k, v, beta, g, h0, o, ht, ctx, B, T, H, dk, dv, scale, 7,
+                                 dtype, stream);
+}
+
+int linatt_delta_fwd_stages(const void* q, const void* k, const void* v, const float* beta,
+                            const float* g, const float* h0, void* o, float* ht, void* ctx, int B,
+                            int T, int H, int dk, int dv, float scale, int stages, int dtype,
+                            void* stream) {
   g_last_error.clear();
+  if (stages < 0 || stages > 7)
+    return fail(LINATT_EINVAL, "linatt_delta_fwd: stages must be a mask of bits 0-2");
   int st = check_delta("linatt_delta_fwd", B, T, H, dk, dv, scale, dtype);
   if (st) return st;
   if (!q || !k || !v || !beta || !o || !ctx)
@@ -333,6 +343,7 @@ int linatt_delta_fwd(const void* q, const void* k, const void* v, const float* b
   a.q = q; a.k = k; a.v = v; a.beta = beta; a.g = g; a.h0 = h0; a.o = o; a.ht = ht;
   a.ctx = (char*)ctx;
   a.B = B; a.T = T; a.H = H; a.NT = (T + kChunk - 1) / kChunk; a.scale = scale;
+  a.stages = stages;
   hipError_t e = dispatch_delta(a, dtype, dk, dv, g != nullptr, false, (hipStream_t)stream);
   if (e != hipSuccess)
     return fail(LINATT_ELAUNCH, std::string("linatt_delta_fwd: launch failed: ") + hipGetErrorString(e));
@@ -344,7 +355,18 @@ int linatt_delta_bwd(const void* q, const void* k, const void* v, const float* b
                      const void* ctx, void* workspace, void* dq, void* dk, void* dv,
                      float* dbeta, float* dg, float* dh0, int B, int T, int H, int dk_dim,
                      int dv_dim, float scale, int dtype, void* stream) {
+  return linatt_delta_bwd_stages(q, k, v, beta, g, h0, dout, dht, ctx, workspace, dq, dk, dv,
+                                 dbeta, dg, dh0, B, T, H, dk_dim, dv_dim, scale, 3, dtype, stream);
+}
+
+int linatt_delta_bwd_stages(const void* q, const void* k, const void* v, const float* beta,
+                            const float* g, const float* h0, const void* dout, const float* dht,
+                            const void* ctx, void* workspace, void* dq, void* dk, void* dv,
+                            float* dbeta, float* dg, float* dh0, int B, int T, int H, int dk_dim,
+                            int dv_dim, float scale, int stages, int dtype, void* stream) {
   g_last_error.clear();
+  if (stages < 0 || stages > 3)
+    return fail(LINATT_EINVAL, "linatt_delta_bwd: stages must be a mask of bits 0-1");
   int st = check_delta("linatt_delta_bwd", B, T, H, dk_dim, dv_dim, scale, dtype);
   if (st) return st;
   if (!q || !k || !v || !beta || !dout || !ctx || !workspace || !dq || !dk || !dv || !dbeta ||
@@ -360,6 +382,7 @@ int linatt_delta_bwd(const void* q, const void* k, const void* v, const float* b
   a.ctx = (char*)const_cast<void*>(ctx);
   a.ws = (char*)workspace;
   a.B = B; a.T = T; a.H = H; a.NT = (T + kChunk - 1) / kChunk; a.scale = scale;
+  a.stages = stages;
   hipError_t e = dispatch_delta(a, dtype, dk_dim, dv_dim, g != nullptr, true, (hipStream_t)stream);
   if (e != hipSuccess)
     return fail(LINATT_ELAUNCH, std::string("linatt_delta_bwd: launch failed: ") + hipGetErrorString(e));

@@ -804,12 +804,17 @@ template <typename T, int DK, int DV, bool GATED>
 hipError_t launch_delta_bwd(const DeltaArgs& a, hipStream_t stream) {
   const DeltaLayout L = delta_layout(a.B, a.T, a.H, DK, DV, sizeof(T));
   const int BH = a.B * a.H;
-  delta_state_bwd_kernel<T, DK, DV, GATED><<<dim3(BH * state_split<DV>()), dim3(64 * (DV / 32 / state_split<DV>() + 1)),
-                                             0, stream>>>(a, L);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  delta_bwd_chunk_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(512), 0, stream>>>(a, L);
-  return hipGetLastError();
+  hipError_t e = hipSuccess;
+  if (a.stages & 1) {
+    delta_state_bwd_kernel<T, DK, DV, GATED><<<dim3(BH * state_split<DV>()),
+                                               dim3(64 * (DV / 32 / state_split<DV>() + 1)), 0, stream>>>(a, L);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (a.stages & 2) {
+    delta_bwd_chunk_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(512), 0, stream>>>(a, L);
+    e = hipGetLastError();
+  }
+  return e;
 }
 
 #define LINATT_DELTA_BWD_INST(T, DK, DV)                                              \

@@ -702,16 +702,22 @@ template <typename T, int DK, int DV, bool GATED>
 hipError_t launch_delta_fwd(const DeltaArgs& a, hipStream_t stream) {
   const DeltaLayout L = delta_layout(a.B, a.T, a.H, DK, DV, sizeof(T));
   const int BH = a.B * a.H;
-  delta_prep_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  delta_state_fwd_kernel<T, DK, DV, GATED><<<dim3(BH * state_split<DV>()), dim3(64 * (DV / 32 / state_split<DV>() + 1)),
-                                             0, stream>>>(
-      a, L, reinterpret_cast<const float*>(a.ctx + L.Gc));
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  delta_out_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);
-  return hipGetLastError();
+  hipError_t e = hipSuccess;
+  if (a.stages & 1) {
+    delta_prep_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (a.stages & 2) {
+    delta_state_fwd_kernel<T, DK, DV, GATED><<<dim3(BH * state_split<DV>()),
+                                               dim3(64 * (DV / 32 / state_split<DV>() + 1)), 0, stream>>>(
+        a, L, reinterpret_cast<const float*>(a.ctx + L.Gc));
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (a.stages & 4) {
+    delta_out_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);
+    e = hipGetLastError();
+  }
+  return e;
 }
 
 #define LINATT_DELTA_FWD_INST(T, DK, DV)                                              \

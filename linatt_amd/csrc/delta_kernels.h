@@ -73,6 +73,9 @@ struct DeltaArgs {
   char* ws;
   int B, T, H, NT;
   float scale;
+  // kernels to launch, in order: forward bit 0 prep, 1 state pass, 2 output;
+  // backward bit 0 state pass, 1 chunk kernel
+  int stages;
 };
 
 template <typename T, int DK, int DV, bool GATED>
