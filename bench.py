@@ -8,6 +8,10 @@ HBM.  One step = forward (o, den) + backward (dq, dk, dv) through the C ABI
 (linatt_kata_fwd, linatt_kata_bwd_dq, linatt_kata_bwd_dkdv) on the current
 HIP stream, with preallocated outputs.
 
+Before each workload's warmup steps the launches run untimed for about a
+second (``--settle-seconds``) so that the GPU has left its idle clock; the
+timed steps then measure sustained throughput, as a training loop sees it.
+
 Prints ONE JSON line: tokens/s (B*T per step), per-kernel average durations
 measured with HIP events recorded on the launch stream, the roofline of the
 dominant kernel (algorithmic FLOPs per launch / its average duration), and
@@ -76,11 +80,26 @@ def delta_state_bytes(B, H, T, K, V, gated, h0, C=64):
     return {"state_fwd": fwd, "state_bwd": bwd}
 
 
+def settle(parts, seconds):
+    """Run the step's launches untimed for `seconds` of wall time.  An idle
+    MI355X starts a burst at a low shader clock and needs about a second of
+    sustained load to reach its working clock; without this, a short warmup
+    times the clock ramp (KATA config 2: 0.40 ms/step after 5 warmup steps
+    from idle, 0.33 ms/step once the clock has settled)."""
+    import torch
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            for _, f in parts:
+                f()
+        torch.cuda.synchronize()
+
+
 DELTA_FWD_STAGES = (("prep", 1), ("state_fwd", 2), ("out", 4))
 DELTA_BWD_STAGES = (("state_bwd", 1), ("bwd_chunk", 2))
 
 
-def bench_delta(gated, steps, warmup):
+def bench_delta(gated, steps, warmup, settle_s):
     """BASELINE config 3 (DeltaNet) / 4 (GatedDeltaNet): B8 H6 T2048 K=V=128
     bf16, chunk 64, fwd + bwd through the C ABI with preallocated outputs,
     context and workspace.  Each kernel is launched on its own
@@ -125,6 +144,7 @@ def bench_delta(gated, steps, warmup):
 
     parts = [(n, (lambda m=m: fwd(m))) for n, m in DELTA_FWD_STAGES] + \
             [(n, (lambda m=m: bwd(m))) for n, m in DELTA_BWD_STAGES]
+    settle(parts, settle_s)
     for _ in range(warmup):
         for _, f in parts:
             f()
@@ -183,7 +203,7 @@ def delta_inputs(B, H, T, K, V, gated, seed):
     return q, k, v, beta, g, h0, do
 
 
-def bench_state(prefill_reps, decode_steps):
+def bench_state(prefill_reps, decode_steps, settle_s):
     """KATA-SPD M=4, B=1 H=12 D=64 bf16.  A T=32768 prefill
     (linatt_kata_prefill: o, den and the fp32 psi-state), then decode steps at
     batch 64 from the broadcast prefill state with fresh q, k, v ~ N(0,1)/8
@@ -218,6 +238,7 @@ def bench_state(prefill_reps, decode_steps):
             Pp(qd), Pp(kd), Pp(vd), Pp(o), Pp(den), Pp(S), Pp(z), Pp(ws), B, T, H, D, D, M, scale,
             1e-6, seg, 0, dt, sp))
 
+    settle([("prefill", prefill)], settle_s)
     prefill()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -411,9 +432,9 @@ def _cpu_model():
 # inside the timed run, so the figure is carried here and refreshed with the
 # profile.
 MEASURED_TRAFFIC_BYTES = {
-    "fwd": int((122.9 + 30.5) * 1e6),
-    "bwd_dq": int((187.5 + 61.1) * 1e6),
-    "bwd_dkdv": int((170.6 + 50.3) * 1e6),
+    "fwd": int((122.8 + 30.5) * 1e6),
+    "bwd_dq": int((188.7 + 61.1) * 1e6),
+    "bwd_dkdv": int((170.8 + 50.3) * 1e6),
 }
 
 
@@ -445,6 +466,8 @@ def main():
     ap.add_argument("--no-kata", action="store_true",
                     help="skip the KATA config-2 timing (profiling the other workloads)")
     ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--settle-seconds", type=float, default=1.5,
+                    help="untimed sustained load before each workload's warmup steps")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 512 MiB device copy (counter calibration)")
     args = ap.parse_args()
@@ -493,6 +516,8 @@ def main():
     parts = [("fwd", fwd), ("bwd_dq", bwd_dq), ("bwd_dkdv", bwd_dkdv)]
     if args.no_kata:
         args.steps, args.warmup = 1, 0
+    else:
+        settle(parts, args.settle_seconds)
     for _ in range(args.warmup):
         for _, f in parts:
             f()
@@ -528,12 +553,13 @@ def main():
 
     delta = None
     if not args.no_delta:
-        delta = {"deltanet_config3": bench_delta(False, max(3, args.steps // 2), 2),
-                 "gated_deltanet_config4": bench_delta(True, max(3, args.steps // 2), 2)}
+        st = args.settle_seconds / 2
+        delta = {"deltanet_config3": bench_delta(False, max(3, args.steps // 2), 2, st),
+                 "gated_deltanet_config4": bench_delta(True, max(3, args.steps // 2), 2, st)}
 
     state = None
     if not args.no_state:
-        state = bench_state(3, args.decode_steps)
+        state = bench_state(3, args.decode_steps, args.settle_seconds / 3)
 
     q1, config1 = bench_config1(max(10, args.steps))
 

@@ -197,3 +197,56 @@ def test_rejects_unsupported(R):
     qb = q.bfloat16()
     with pytest.raises(NotImplementedError, match="cu_seqlens"):
         R.chunk_delta_rule(qb, qb, qb, beta, cu_seqlens=torch.tensor([0, 8], device=dev))
+
+
+@pytest.mark.parametrize("gated", [False, True], ids=["deltanet", "gdn"])
+def test_stage_calls_equal_full_calls(gated):
+    """linatt_delta_fwd_stages / linatt_delta_bwd_stages with every stage bit
+    once, in order, launch exactly the kernels of linatt_delta_fwd /
+    linatt_delta_bwd: the outputs agree bit for bit (called through the C ABI)."""
+    from linatt_amd import _lib
+    L = _lib.load()
+    B, T, H, K = 2, 300, 3, 128
+    gg = torch.Generator().manual_seed(9)
+    dev = torch.device("cuda")
+    q = torch.randn(B, T, H, K, generator=gg).bfloat16().to(dev)
+    k = D.l2norm(torch.randn(B, T, H, K, generator=gg)).bfloat16().to(dev)
+    v = torch.randn(B, T, H, K, generator=gg).bfloat16().to(dev)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=gg)).to(dev)
+    g = (torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=gg) + 4) / 16).to(dev) \
+        if gated else None
+    h0 = (torch.randn(B, H, K, K, generator=gg) * 0.02).to(dev) if gated else None
+    do = torch.randn(B, T, H, K, generator=gg).bfloat16().to(dev)
+    dht = torch.randn(B, H, K, K, generator=gg).to(dev)
+    dt = _lib.LINATT_BFLOAT16
+    P, sp = _lib.ptr, _lib.stream_of(q)
+
+    def run(staged):
+        o = torch.empty_like(v)
+        ht = torch.empty(B, H, K, K, device=dev)
+        ctx = torch.zeros(L.linatt_delta_ctx_bytes(B, T, H, K, K, dt), device=dev, dtype=torch.uint8)
+        ws = torch.zeros(L.linatt_delta_bwd_workspace_bytes(B, T, H, K, K, dt), device=dev,
+                         dtype=torch.uint8)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        db = torch.empty(B, T, H, device=dev)
+        dg = torch.empty_like(db) if gated else None
+        dh0 = torch.empty_like(h0) if gated else None
+        fa = (P(q), P(k), P(v), P(beta), P(g), P(h0), P(o), P(ht), P(ctx), B, T, H, K, K, K ** -0.5)
+        ba = (P(q), P(k), P(v), P(beta), P(g), P(h0), P(do), P(dht), P(ctx), P(ws), P(dq), P(dk),
+              P(dv), P(db), P(dg), P(dh0), B, T, H, K, K, K ** -0.5)
+        if staged:
+            for s in (1, 2, 4):
+                _lib.check("linatt_delta_fwd_stages", L.linatt_delta_fwd_stages(*fa, s, dt, sp))
+            for s in (1, 2):
+                _lib.check("linatt_delta_bwd_stages", L.linatt_delta_bwd_stages(*ba, s, dt, sp))
+        else:
+            _lib.check("linatt_delta_fwd", L.linatt_delta_fwd(*fa, dt, sp))
+            _lib.check("linatt_delta_bwd", L.linatt_delta_bwd(*ba, dt, sp))
+        torch.cuda.synchronize()
+        return [x for x in (o, ht, dq, dk, dv, db, dg, dh0) if x is not None]
+
+    for a, b in zip(run(False), run(True)):
+        assert torch.equal(a, b)
+    with pytest.raises(_lib.LinattError, match="stages"):
+        _lib.check("linatt_delta_fwd_stages", L.linatt_delta_fwd_stages(
+            P(q), P(k), P(v), P(beta), None, None, P(q), None, P(q), B, T, H, K, K, 1.0, 8, dt, sp))
