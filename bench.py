@@ -186,6 +186,59 @@ def bench_delta(gated, steps, warmup, settle_s):
             "frac_mfma_peak": round(tf / PEAK_BF16_TFLOPS, 4), "kernels": kern}
 
 
+def bench_delta_kata(steps, settle_s):
+    """The SPD delta rule (DeltaKata, kata/spd/flash_delta.py:1060-1116)
+    forward at the KATA bench shape with the mixer's settings
+    (configs/model/kata_delta_m1_340m.yaml: M=1, delta_scale 0.5, l2-normalised
+    q, k, beta = sigmoid): B8 H12 T2048 D64 bf16 through linatt_dkata_fwd.
+    Algorithmic FLOPs, causal pairs T^2/2 per head: the Gram kappa(k, k)
+    (2 M D) and the Ec product (2 dv) of the solve, the readout kappa(q, k)
+    (2 M D) and its product (2 dv)."""
+    import torch
+    from linatt_amd import _lib
+    L = _lib.load()
+    B, H, T, D, M, scale = 8, 12, 2048, 64, 1, 0.5
+    g = torch.Generator().manual_seed(6)
+    nrm = lambda x: x * torch.rsqrt((x * x).sum(-1, keepdim=True))  # noqa: E731
+    q = nrm(torch.randn(B, T, H, D, generator=g)).to(torch.bfloat16)
+    k = nrm(torch.randn(B, T, H, D, generator=g)).to(torch.bfloat16)
+    v = torch.randn(B, T, H, D, generator=g).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g))
+    dev = torch.device("cuda", 0)
+    qd, kd, vd, bd = (x.to(dev) for x in (q, k, v, beta))
+    o = torch.empty(B, T, H, D, device=dev)
+    den = torch.empty(B, T, H, device=dev)
+    dt = _lib.LINATT_BFLOAT16
+    ws = torch.empty(L.linatt_dkata_workspace_bytes(B, T, H, D, D, dt), device=dev,
+                     dtype=torch.uint8)
+    P, sp = _lib.ptr, _lib.stream_of(qd)
+
+    def fwd():
+        _lib.check("linatt_dkata_fwd", L.linatt_dkata_fwd(
+            P(qd), P(kd), P(vd), P(bd), None, P(o), P(den), P(ws), B, T, H, D, D, M, scale, 0,
+            1e-5, dt, sp))
+
+    settle([("fwd", fwd)], settle_s)
+    for _ in range(2):
+        fwd()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        fwd()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = B * H * T * T / 2 * (4 * M * D + 4 * D)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"config": {"B": B, "H": H, "T": T, "D": D, "num_groups": M, "scale": scale,
+                       "normalize": False, "seed": 6},
+            "fwd_ms": round(ms, 4), "tokens_per_s": round(B * T / (ms * 1e-3), 1),
+            "alg_gflop": round(flops / 1e9, 2), "tflops": round(tf, 1),
+            "frac_mfma_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+
+
 def delta_inputs(B, H, T, K, V, gated, seed):
     """Config 3 / 4 inputs, drawn on the CPU in float32 (q, v ~ N(0,1); k
     ~ N(0,1) l2-normalised; beta = sigmoid(N(0,1)); g = logsigmoid(N(0,1)+4)/16;
@@ -562,6 +615,8 @@ def main():
         state = bench_state(3, args.decode_steps, args.settle_seconds / 3)
 
     q1, config1 = bench_config1(max(10, args.steps))
+    delta_kata = None if args.no_delta else bench_delta_kata(max(3, args.steps // 2),
+                                                             args.settle_seconds / 3)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -600,6 +655,7 @@ def main():
         "delta_rule": delta,
         "kata_state_config5": state,
         "kata_config1": config1,
+        "delta_kata_fwd": delta_kata,
     }
     print(json.dumps(out), flush=True)
 

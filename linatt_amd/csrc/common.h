@@ -186,10 +186,16 @@ __device__ __forceinline__ void vm_wait_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"i"(N) : "memory");
 }
 
-// vm_wait_barrier for a wave-uniform count n in [0, 6] (the counter field is
+// vm_wait_barrier for a wave-uniform count n in [0, 12] (the counter field is
 // an immediate); larger n waits for everything.
 __device__ __forceinline__ void vm_wait_barrier_n(int n) {
   switch (n) {
+    case 12: vm_wait_barrier<12>(); break;
+    case 11: vm_wait_barrier<11>(); break;
+    case 10: vm_wait_barrier<10>(); break;
+    case 9: vm_wait_barrier<9>(); break;
+    case 8: vm_wait_barrier<8>(); break;
+    case 7: vm_wait_barrier<7>(); break;
     case 6: vm_wait_barrier<6>(); break;
     case 5: vm_wait_barrier<5>(); break;
     case 4: vm_wait_barrier<4>(); break;

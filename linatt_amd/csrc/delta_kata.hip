@@ -186,15 +186,27 @@ __global__ __launch_bounds__(256) void dkata_prep_kernel(DKataArgs a) {
 // Kernel 2: the pseudo-values U, chunk after chunk, one workgroup per (b, h).
 // Wave w = (tb, ub): tb = w & 1 is its 32-row block of the current chunk's
 // tokens t, ub = w >> 1 its 32-row block of each earlier chunk's tokens u
-// (for Ec) and, afterwards, its 32-column block of U (jb = ub).
+// (for Ec) and, afterwards, its 32-column block of U.
+//
+// Every operand of the Ec products comes from LDS.  The K and U^T tiles of
+// the earlier chunks c' <= c - 2 stream through a ring of kRing slots by
+// direct global->LDS copies issued kRing - 1 steps ahead (the first ones
+// during the previous chunk's epilogue); chunk c - 1's K and U^T, which the
+// previous epilogue has just produced, stay in LDS (Klast, Ulast).  Tm of
+// the chunk is copied in while its Ec loop runs, and the next chunk's key
+// rows, values and betas are loaded into registers during the epilogue.
 // ---------------------------------------------------------------------------
 template <typename T, int D, int DV, int M>
 __global__ __launch_bounds__(256) void dkata_U_kernel(DKataArgs a) {
-  constexpr int E = D / M, KE = E / 16;
+  constexpr int E = D / M, KE = E / 16, kRing = 5, TE = 64 * 64;
   static_assert(D == 64 && DV == 64 && E % 16 == 0, "64-wide heads");
+  __shared__ __attribute__((aligned(16))) T ring[kRing][2][TE];  // K, U^T tiles of chunk c'
+  __shared__ __attribute__((aligned(16))) T Klast[TE];           // K of chunk c - 1, [u][d]
+  __shared__ __attribute__((aligned(16))) T Ulast[TE];           // U^T of chunk c - 1, [j][u]
+  __shared__ __attribute__((aligned(16))) T TmS[2][TE];          // Tm hi / lo of the chunk
+  __shared__ __attribute__((aligned(16))) T Vh[TE];              // (beta (V - Ec))^T hi, [j][u]
+  __shared__ __attribute__((aligned(16))) T Vl[TE];              // ... lo
   __shared__ __attribute__((aligned(16))) float Xc[4][16][64];   // Ec^T partials
-  __shared__ __attribute__((aligned(16))) T Vh[64 * 64];          // (beta (V - Ec))^T hi, [j][u]
-  __shared__ __attribute__((aligned(16))) T Vl[64 * 64];          // ... lo
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -205,103 +217,152 @@ __global__ __launch_bounds__(256) void dkata_U_kernel(DKataArgs a) {
   const T* kb = (const T*)a.k + ((int64_t)b * Tn * a.H + h) * D;
   const T* vb = (const T*)a.v + ((int64_t)b * Tn * a.H + h) * DV;
   T* UT = (T*)(a.ws + a.L.UT) + (size_t)bh * DV * Tp;          // [j][t]
-  const T* TmH = (const T*)(a.ws + a.L.TmHi) + (size_t)bh * NC * 4096;
-  const T* TmL = (const T*)(a.ws + a.L.TmLo) + (size_t)bh * NC * 4096;
+  const T* TmH = (const T*)(a.ws + a.L.TmHi) + (size_t)bh * NC * TE;
+  const T* TmL = (const T*)(a.ws + a.L.TmLo) + (size_t)bh * NC * TE;
 
-  auto krow = [&](int t, int kk) -> v8_t<T> {  // 8 dims of key row t (zero past T)
-    return t < Tn ? ld8<T>(kb + (int64_t)t * rs + 16 * kk + 8 * hh) : zero8<T>();
+  // copies: each wave moves ops 2w, 2w + 1 of each 8-op tile (4 per wave)
+  auto issue_step = [&](int cp, int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      dma_tile64<T>(kb, rs, 64 * cp, Tn, ring[slot][0], 2 * w + i, lane);
+      dma_tile64<T>(UT + 64 * cp, Tp, 0, DV, ring[slot][1], 2 * w + i, lane);
+    }
   };
+  auto issue_tm = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      dma_tile64<T>(TmH + (size_t)c * TE, 64, 0, 64, TmS[0], 2 * w + i, lane);
+      dma_tile64<T>(TmL + (size_t)c * TE, 64, 0, 64, TmS[1], 2 * w + i, lane);
+    }
+  };
+  // this lane's token of chunk c: 8 dims of K per k-step, its 16 V columns, beta
+  auto load_chunk = [&](int c, v8_t<T>* kx, v4_t<T>* vx, float& bx) __attribute__((always_inline)) {
+    const int t = 64 * c + 32 * tb + cl;
+    const bool in = t < Tn;
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk)
+      kx[kk] = in ? ld8<T>(kb + (int64_t)t * rs + 16 * kk + 8 * hh) : zero8<T>();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      vx[i] = in ? ld4<T>(vb + (int64_t)t * vrs + 32 * ub + 8 * i + 4 * hh) : v4_t<T>{};
+    bx = in ? a.beta[((int64_t)b * Tn + t) * a.H + h] : 0.f;
+  };
+  // A^T[u][t] / scale^2 = sum_{g,g2} (k_u,g2 . k_t,g)^2 for the 32 keys u of
+  // block ub of one earlier chunk (K tile Kt) and this wave's 32 tokens t,
+  // as the two B operands of the Ec product
+  auto gram = [&](const T* Kt, const v8_t<T>* kc, v8_t<T>* bop) __attribute__((always_inline)) {
+    v8_t<T> ka[D / 16];
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) ka[kk] = tile_ld8<T>(Kt, 32 * ub + cl, 16 * kk + 8 * hh);
+    f32x16 At{};
+#pragma unroll
+    for (int g = 0; g < M; ++g)
+#pragma unroll
+      for (int g2 = 0; g2 < M; ++g2) {
+        f32x16 r{};
+#pragma unroll
+        for (int kk = 0; kk < KE; ++kk) r = mma(ka[g2 * KE + kk], kc[g * KE + kk], r);
+        At += r * r;
+      }
+    bop[0] = c_to_b<T>(At, 0);
+    bop[1] = c_to_b<T>(At, 1);
+  };
+  // Ec^T[j][t] (/ scale^2) += U^T[j][u] A^T[u][t] over those 32 keys
+  auto ec_update = [&](const T* Ut, const v8_t<T>* bop, f32x16 (&ec)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+        ec[jb] = mma(tile_ldp8<T>(Ut, 32 * jb + cl, 32 * ub, ks, hh), bop[ks], ec[jb]);
+  };
+
+  v8_t<T> kc[D / 16];
+  v4_t<T> vc[4];
+  float bc;
+  load_chunk(0, kc, vc, bc);
+  issue_tm(0);
 
   for (int c = 0; c < NC; ++c) {
     const int t0 = 64 * c;
     const int tl = t0 + 32 * tb + cl;  // this lane's token of the current chunk
-    v8_t<T> kc[D / 16];
-#pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) kc[kk] = krow(tl, kk);
+    const int nring = c - 1;           // ring steps: earlier chunks 0 .. c - 2
 
-    // Ec^T[j][t] over the earlier chunks, u-block ub, both j-blocks
+    // Steps 0 .. nring: step s reads the K and U^T tiles of chunk s (ring slot
+    // s % kRing; the last one from Klast / Ulast).  Software-pipelined: the
+    // Gram block of step s + 1 is formed while the Ec product of step s runs.
     f32x16 ec[2] = {f32x16{}, f32x16{}};
-    v8_t<T> ka[D / 16], uo[2][2][2];  // operands of chunk cp (prefetched one ahead)
-    auto fetch = [&](int cp, v8_t<T>* kx, v8_t<T> (*ux)[2][2]) __attribute__((always_inline)) {
-      const int u0 = 64 * cp + 32 * ub;
-#pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk) kx[kk] = ld8<T>(kb + (int64_t)(u0 + cl) * rs + 16 * kk + 8 * hh);
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const T* row = UT + (size_t)(32 * jb + cl) * Tp + u0;
-          ux[jb][ks][0] = ld_tr_op<T>(row, ks, hh);
+    if (c > 0) {
+      v8_t<T> bop[2];
+      if (nring > 0) vm_wait_barrier_n(4 * (min(kRing - 1, nring) - 1));
+      gram(nring > 0 ? ring[0][0] : Klast, kc, bop);
+      for (int s = 0; s < nring; ++s) {
+        if (s + 1 < nring) {
+          // ring copies issued after slot s + 1's: steps s + 2 .. min(s + 3, nring - 1)
+          // (Tm's copies, issued after the first ones, only make the wait stricter)
+          vm_wait_barrier_n(4 * min(2, nring - 2 - s));
+          if (s + kRing - 1 < nring) issue_step(s + kRing - 1, (s + kRing - 1) % kRing);
         }
-    };
-    if (c > 0) fetch(0, ka, uo);
-    for (int cp = 0; cp < c; ++cp) {
-      v8_t<T> kn[D / 16], un[2][2][2];
-      if (cp + 1 < c) fetch(cp + 1, kn, un);
-      // A^T[u][t] = scale^2 sum_{g,g2} (k_u,g2 . k_t,g)^2  (u: chunk cp, block ub; t: block tb)
-      f32x16 At{};
-#pragma unroll
-      for (int g = 0; g < M; ++g)
-#pragma unroll
-        for (int g2 = 0; g2 < M; ++g2) {
-          f32x16 r{};
-#pragma unroll
-          for (int kk = 0; kk < KE; ++kk) r = mma(ka[g2 * KE + kk], kc[g * KE + kk], r);
-          At += r * r;
-        }
-      At *= a.scale2;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const v8_t<T> bop = c_to_b<T>(At, ks);
-#pragma unroll
-        for (int jb = 0; jb < 2; ++jb) ec[jb] = mma(uo[jb][ks][0], bop, ec[jb]);
+        v8_t<T> bnext[2];
+        gram(s + 1 < nring ? ring[(s + 1) % kRing][0] : Klast, kc, bnext);
+        ec_update(ring[s % kRing][1], bop, ec);
+        bop[0] = bnext[0];
+        bop[1] = bnext[1];
       }
-      if (cp + 1 < c) {
-#pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk) ka[kk] = kn[kk];
-#pragma unroll
-        for (int jb = 0; jb < 2; ++jb)
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks) uo[jb][ks][0] = un[jb][ks][0];
-      }
+      ec_update(Ulast, bop, ec);
     }
+
+    // every copy in flight has landed (Tm of this chunk included) and every
+    // wave is done reading the ring, Klast and Ulast
+    vm_wait_barrier<0>();
+    v8_t<T> kn[D / 16];
+    v4_t<T> vn[4];
+    float bn = 0.f;
+    if (c + 1 < NC) {
+      load_chunk(c + 1, kn, vn, bn);
+      // chunk c + 1's ring steps are earlier chunks 0 .. c - 1, all stored
+      for (int s = 0; s < min(kRing - 1, c); ++s) issue_step(s, s);
+    }
+
     // the partner wave (same tb, other ub) holds the other u-block's partial:
     // trade the j-block each does not keep (keep jb = ub)
 #pragma unroll
     for (int e = 0; e < 16; ++e) Xc[w][e][lane] = ec[1 - ub][e];
-    __syncthreads();
+    // K of this chunk for the next one's last step (rows 32 tb + cl)
+    if (ub == 0) {
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk)
+        *reinterpret_cast<v8_t<T>*>(reinterpret_cast<char*>(Klast) + tile_off(32 * tb + cl, 16 * kk + 8 * hh)) = kc[kk];
+    }
+    block_barrier();
     const int partner = tb | ((1 - ub) << 1);
     f32x16 ecs = ec[ub];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) ecs[e] += Xc[partner][e][lane];
+    for (int e = 0; e < 16; ++e) ecs[e] = a.scale2 * (ecs[e] + Xc[partner][e][lane]);
 
     // beta_t (V[t][j] - Ec[t][j]) for j in block ub, as 16-bit hi + lo in [j][t]
-    const float bt = tl < Tn ? a.beta[((int64_t)b * Tn + tl) * a.H + h] : 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const v4_t<T> vv = tl < Tn ? ld4<T>(vb + (int64_t)tl * vrs + 32 * ub + 8 * i + 4 * hh) : v4_t<T>{};
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int e = 4 * i + r, j = 32 * ub + 8 * i + 4 * hh + r;
-        const float x = bt * ((float)vv[r] - ecs[e]);
+        const float x = bc * ((float)vc[i][r] - ecs[e]);
         const T xh = (T)x;
-        T* ph = reinterpret_cast<T*>(reinterpret_cast<char*>(Vh) + tile_off(j, (32 * tb + cl) & ~3)) + (cl & 3);
-        T* pl = reinterpret_cast<T*>(reinterpret_cast<char*>(Vl) + tile_off(j, (32 * tb + cl) & ~3)) + (cl & 3);
-        *ph = xh;
-        *pl = (T)(x - (float)xh);
+        const int off = tile_off(j, (32 * tb + cl) & ~3);
+        reinterpret_cast<T*>(reinterpret_cast<char*>(Vh) + off)[cl & 3] = xh;
+        reinterpret_cast<T*>(reinterpret_cast<char*>(Vl) + off)[cl & 3] = (T)(x - (float)xh);
       }
     }
-    __syncthreads();
+    block_barrier();
 
     // U^T[j][t] = sum_{u <= t} Vp^T[j][u] Tm[t][u]  (j block ub, t block tb)
     f32x16 uacc{};
-    const T* tmh = TmH + (size_t)c * 4096 + (size_t)(32 * tb + cl) * 64;
-    const T* tml = TmL + (size_t)c * 4096 + (size_t)(32 * tb + cl) * 64;
+    const T* th = TmS[0];
+    const T* tlo = TmS[1];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       if (ks >= 2 * (tb + 1)) break;  // Tm[t][u] = 0 for u > t
-      const v8_t<T> bh8 = ld8<T>(tmh + 16 * ks + 8 * hh);
-      const v8_t<T> bl8 = ld8<T>(tml + 16 * ks + 8 * hh);
+      const v8_t<T> bh8 = tile_ld8<T>(th, 32 * tb + cl, 16 * ks + 8 * hh);
+      const v8_t<T> bl8 = tile_ld8<T>(tlo, 32 * tb + cl, 16 * ks + 8 * hh);
       const v8_t<T> ah = tile_ld8<T>(Vh, 32 * ub + cl, 16 * ks + 8 * hh);
       const v8_t<T> alo = tile_ld8<T>(Vl, 32 * ub + cl, 16 * ks + 8 * hh);
       uacc = mma(ah, bh8, uacc);
@@ -309,11 +370,14 @@ __global__ __launch_bounds__(256) void dkata_U_kernel(DKataArgs a) {
       uacc = mma(alo, bh8, uacc);
     }
 
-    // U (float32 and 16-bit, time-major) and U^T for the later chunks
+    // U^T for the later chunks (global and, for the next chunk, Ulast) and
+    // U (float32 and 16-bit, time-major)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int j = 32 * ub + 8 * (e >> 2) + 4 * hh + (e & 3);
-      UT[(size_t)j * Tp + tl] = (T)uacc[e];
+      const T u16 = (T)uacc[e];
+      UT[(size_t)j * Tp + tl] = u16;
+      reinterpret_cast<T*>(reinterpret_cast<char*>(Ulast) + tile_off(j, (32 * tb + cl) & ~3))[cl & 3] = u16;
     }
     if (tl < Tn) {
       const int64_t row = ((int64_t)b * Tn + tl) * a.H + h;
@@ -326,9 +390,18 @@ __global__ __launch_bounds__(256) void dkata_U_kernel(DKataArgs a) {
             make_float4(uacc[4 * i], uacc[4 * i + 1], uacc[4 * i + 2], uacc[4 * i + 3]);
       }
     }
-    // U^T of this chunk is read by every wave from the next chunk on
-    __threadfence_block();
-    __syncthreads();
+    // Ulast and the Vh / Vl, Xc, TmS reuse; the global U^T is drained by the
+    // next chunk's vm_wait_barrier<0> before any copy reads it
+    block_barrier();
+    // Tm of the next chunk, behind its first ring copies (the ring waits
+    // count only ring copies after a slot's, so they also wait for these:
+    // stricter, never short)
+    if (c + 1 < NC) issue_tm(c + 1);
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) kc[kk] = kn[kk];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vc[i] = vn[i];
+    bc = bn;
   }
 }
 
