@@ -26,6 +26,7 @@
 // (delta_out) forms o in parallel over chunks from those.
 #include "common.h"
 #include "delta_kernels.h"
+#include "tri_inv.h"
 
 namespace linatt {
 
@@ -64,7 +65,8 @@ DeltaLayout delta_layout(int B, int T, int H, int DK, int DV, int eb) {
 //   1. Gram A (fp32, LDS) by waves 1-3; Aqk rows 0-31 by wave 0
 //   2. diagonal 16 x 16 inverses of I + A in place (wave 0); Aqk rows
 //      32-63 (wave 1); Qg = scale e^G q (waves 2, 3)
-//   3. block rows 1..3 of Tm = (I + A)^-1 (all threads)
+//   3. the off-diagonal blocks of Tm = (I + A)^-1 by two merges (16 -> 32
+//      in fp32 by all threads, 32 -> 64 by MFMA in wave 0)
 //   4. Tm -> context, Tw = Tm diag(beta e^G) and Tu = Tm diag(beta) as
 //      bf16 tiles; the fp32 area becomes the waves' store staging
 //   5. W, W^T, U^T, Kd^T by MFMA / transposing reads, and the Aqk rows,
@@ -79,7 +81,7 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
   __shared__ __attribute__((aligned(16))) float AT[64 * 64];  // A, then Tm in place; then staging
   __shared__ __attribute__((aligned(16))) T Tw[64 * 64];      // Tm diag(beta e^G)
   __shared__ __attribute__((aligned(16))) T Tu[64 * 64];      // Tm diag(beta)
-  __shared__ __attribute__((aligned(16))) float Ys[16 * 48];  // A_R,<R Tm_<R,<R of a block row
+  __shared__ __attribute__((aligned(16))) float Ys[16 * 48];  // scratch of the inverse merges
   __shared__ __attribute__((aligned(16))) float Bs[64];
   __shared__ __attribute__((aligned(16))) float Gs[64];
 
@@ -237,46 +239,9 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
   }
   __syncthreads();
 
-  // 3. block rows R = 1..3: Y = A_R,<R Tm_<R,<R (to Ys), then
-  //    Tm_R,<R = -D_R Y over A_R,<R.  Thread: row 16 R + (tid >> 4), columns
-  //    (tid & 15) + 16 m, m < R; Tm_<R,<R is stored with its zeros, so every
-  //    sum runs over whole 16-blocks
-  {
-    const int ii = tid >> 4, cg = tid & 15;
-    auto block_row = [&](auto RC) __attribute__((always_inline)) {
-      constexpr int R = decltype(RC)::value;
-      const int i = 16 * R + ii;
-#pragma unroll
-      for (int m = 0; m < R; ++m) {
-        const int cc = cg + 16 * m;
-        float y4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 16 * m; j < 16 * R; j += 4) {
-          const f32x4 a4 = *reinterpret_cast<const f32x4*>(AT + i * 64 + j);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) y4[r] += a4[r] * AT[(j + r) * 64 + cc];
-        }
-        Ys[ii * 48 + cc] = (y4[0] + y4[1]) + (y4[2] + y4[3]);
-      }
-      __syncthreads();
-#pragma unroll
-      for (int m = 0; m < R; ++m) {
-        const int cc = cg + 16 * m;
-        float t4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < 16; k += 4) {
-          const f32x4 d4 = *reinterpret_cast<const f32x4*>(AT + i * 64 + 16 * R + k);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) t4[r] += d4[r] * Ys[(k + r) * 48 + cc];
-        }
-        AT[i * 64 + cc] = -((t4[0] + t4[1]) + (t4[2] + t4[3]));
-      }
-      __syncthreads();
-    };
-    block_row(IntC<1>{});
-    block_row(IntC<2>{});
-    block_row(IntC<3>{});
-  }
+  // 3. the off-diagonal blocks of Tm = (I + A)^-1: 16 -> 32 merges in fp32,
+  //    32 -> 64 by MFMA on split bf16 operands (tri_inv.h)
+  tri_inv64_merge(AT, Ys, tid);
 
   // 4. Tm (natural [i][j]) to the context; Tw, Tu tiles.  Thread: row
   //    tid >> 2, columns 16 (tid & 3) .. +15

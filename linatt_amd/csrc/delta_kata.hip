@@ -27,6 +27,7 @@
 // num / den and den give num = o den; kernel 3 applies the normalisation.
 #include "common.h"
 #include "kata_kernels.h"
+#include "tri_inv.h"
 
 namespace linatt {
 
@@ -58,7 +59,7 @@ __global__ __launch_bounds__(256) void dkata_prep_kernel(DKataArgs a) {
   __shared__ __attribute__((aligned(16))) T Ks[64 * 64];
   __shared__ __attribute__((aligned(16))) float NT[64 * 64];  // N, then Tm (natural [i][j])
   __shared__ __attribute__((aligned(16))) float Bs[64];
-  __shared__ __attribute__((aligned(16))) float Ys[16 * 48];
+  __shared__ __attribute__((aligned(16))) float Ys[512];
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -129,35 +130,8 @@ __global__ __launch_bounds__(256) void dkata_prep_kernel(DKataArgs a) {
   }
   __syncthreads();
 
-  // block rows R = 1..3: Y = N_R,<R Tm_<R,<R, then Tm_R,<R = -D_R Y
-  {
-    const int ii = tid >> 4, cg = tid & 15;
-    auto block_row = [&](auto RC) __attribute__((always_inline)) {
-      constexpr int R = decltype(RC)::value;
-      const int i = 16 * R + ii;
-#pragma unroll
-      for (int m = 0; m < R; ++m) {
-        const int cc = cg + 16 * m;
-        float y = 0.f;
-#pragma unroll
-        for (int j = 16 * m; j < 16 * R; ++j) y += NT[i * 64 + j] * NT[j * 64 + cc];
-        Ys[ii * 48 + cc] = y;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int m = 0; m < R; ++m) {
-        const int cc = cg + 16 * m;
-        float t = 0.f;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) t += NT[i * 64 + 16 * R + k] * Ys[k * 48 + cc];
-        NT[i * 64 + cc] = -t;
-      }
-      __syncthreads();
-    };
-    block_row(IntC<1>{});
-    block_row(IntC<2>{});
-    block_row(IntC<3>{});
-  }
+  // the off-diagonal blocks: 16 -> 32 merges in fp32, 32 -> 64 by MFMA
+  tri_inv64_merge(NT, Ys, tid);
 
   // Tm (unit lower triangular, zero above) as 16-bit hi + lo, natural [i][j]
   {
