@@ -363,8 +363,13 @@ __global__ __launch_bounds__(256, 2) void kata_prefill_out_kernel(KataStateArgs 
         const float* zr = hz + ga * E * E + (ar % E) * E + f % E;
         const f32x4 z0 = ga == gf ? *reinterpret_cast<const f32x4*>(zr) : f32x4{};
         const f32x4 z1 = ga == gf ? *reinterpret_cast<const f32x4*>(zr + 4) : f32x4{};
-        const v8_t<T> za = __builtin_convertvector(f32x8{z0[0], z0[1], z0[2], z0[3], z1[0], z1[1], z1[2], z1[3]}, v8_t<T>);
+        // z as 16-bit hi + lo parts: the sums grow with the prefix length,
+        // and one rounding of them would cost den its fp32 accuracy
+        const f32x8 zf{z0[0], z0[1], z0[2], z0[3], z1[0], z1[1], z1[2], z1[3]};
+        const v8_t<T> za = __builtin_convertvector(zf, v8_t<T>);
+        const v8_t<T> zl = __builtin_convertvector(zf - __builtin_convertvector(za, f32x8), v8_t<T>);
         y = mma(za, qop[ks], y);
+        y = mma(zl, qop[ks], y);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {

@@ -56,6 +56,27 @@ def test_prefill_parity(S_, M, case):
         assert e < TOL, (name, e)
 
 
+@pytest.mark.parametrize("M", [4, 2])
+def test_prefill_den_nonzero_mean_keys(S_, M):
+    """Keys and queries with a non-zero mean and unequal per-dimension
+    scales: every psi-feature sum z grows with the prefix, the case where a
+    single 16-bit rounding of z would cost den its accuracy (about 4e-4
+    relative here, computed on the CPU; hi + lo parts give about 2e-5), so
+    den is checked to 1e-4."""
+    B, T, H = 1, 3000, 2
+    g = torch.Generator().manual_seed(77)
+    scale_d = torch.linspace(0.05, 0.3, 64)
+    mk = lambda: (torch.randn(B, T, H, 64, generator=g) * scale_d + 0.2).to(BF)  # noqa: E731
+    q, k, v = mk(), mk(), gen((B, T, H, 64), 78)
+    o_ref, den_ref, S_ref, z_ref = K.kata_prefill_fwd_state_form(q, k, v, M, eps=1e-6)
+    dev = torch.device("cuda")
+    o, den, S, z = S_.kata_prefill(q.to(dev), k.to(dev), v.to(dev), num_groups=M, seg_len=256)
+    errs = {n: mar(x, r) for n, x, r in (("o", o, o_ref), ("den", den, den_ref), ("z", z, z_ref))}
+    print(errs, flush=True)
+    assert errs["o"] < TOL and errs["z"] < 1e-5
+    assert errs["den"] < 1e-4, errs
+
+
 def test_head_major_scan_cat(S_):
     """Reference layout (B, H, T, D) through spd_chunk_scan_cat."""
     B, T, H = 1, 700, 2
