@@ -239,6 +239,64 @@ def bench_delta_kata(steps, settle_s):
             "frac_mfma_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
 
 
+def bench_mixer(steps, settle_s):
+    """The mixer's non-GEMM ops at the 200M KATA shape (B8 T2048, hidden 768,
+    12 heads of 64; configs/model/200m/kata_quadratic_200m.yaml: short conv 4
+    with SiLU on q, k, v, output RMSNorm): linatt_short_conv_fwd/bwd on one
+    (B, T, 768) bf16 tensor and linatt_rmsnorm_fwd/bwd on (B*T*12, 64) bf16,
+    each against HBM with its compulsory bytes (inputs read once, outputs
+    written once)."""
+    import torch
+    from linatt_amd import _lib
+    L = _lib.load()
+    B, T, C, W, H, D = 8, 2048, 768, 4, 12, 64
+    g = torch.Generator().manual_seed(7)
+    dev = torch.device("cuda", 0)
+    x = torch.randn(B, T, C, generator=g).bfloat16().to(dev)
+    dy = torch.randn(B, T, C, generator=g).bfloat16().to(dev)
+    w = (torch.randn(C, W, generator=g) / W).to(dev)
+    y, dx = torch.empty_like(x), torch.empty_like(x)
+    dw = torch.empty(C, W, device=dev)
+    cws = torch.empty(L.linatt_short_conv_bwd_workspace_bytes(B, T, C, W), device=dev,
+                      dtype=torch.uint8)
+    n = B * T * H
+    rw = torch.ones(D, device=dev)
+    rstd = torch.empty(n, device=dev)
+    rdw = torch.empty(D, device=dev)
+    rws = torch.empty(L.linatt_rmsnorm_bwd_workspace_bytes(n, D), device=dev, dtype=torch.uint8)
+    P, sp, bf = _lib.ptr, _lib.stream_of(x), _lib.LINATT_BFLOAT16
+    parts = [
+        ("short_conv_fwd", lambda: _lib.check("linatt_short_conv_fwd", L.linatt_short_conv_fwd(
+            P(x), P(w), None, None, P(y), None, B, T, C, W, 1, bf, sp))),
+        ("short_conv_bwd", lambda: _lib.check("linatt_short_conv_bwd", L.linatt_short_conv_bwd(
+            P(x), P(w), None, None, P(dy), P(dx), P(dw), None, P(cws), B, T, C, W, 1, bf, sp))),
+        ("rmsnorm_fwd", lambda: _lib.check("linatt_rmsnorm_fwd", L.linatt_rmsnorm_fwd(
+            P(x), P(rw), P(y), P(rstd), n, D, 1e-5, bf, sp))),
+        ("rmsnorm_bwd", lambda: _lib.check("linatt_rmsnorm_bwd", L.linatt_rmsnorm_bwd(
+            P(x), P(rw), P(rstd), P(dy), P(dx), P(rdw), P(rws), n, D, bf, sp))),
+    ]
+    settle(parts, settle_s)
+    stream = torch.cuda.current_stream(dev)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(parts) + 1)] for _ in range(steps)]
+    for s_ in range(steps):
+        ev[s_][0].record(stream)
+        for i, (_, f) in enumerate(parts):
+            f()
+            ev[s_][i + 1].record(stream)
+    torch.cuda.synchronize()
+    nb = B * T * C * 2
+    alg = {"short_conv_fwd": 2 * nb, "short_conv_bwd": 3 * nb, "rmsnorm_fwd": 2 * nb + n * 4,
+           "rmsnorm_bwd": 3 * nb + n * 4}
+    out = {"config": {"B": B, "T": T, "hidden": C, "kernel_size": W, "heads": H, "head_dim": D,
+                      "dtype": "bf16", "seed": 7}}
+    for i, (name, _) in enumerate(parts):
+        ms = sum(ev[s_][i].elapsed_time(ev[s_][i + 1]) for s_ in range(steps)) / steps
+        gbs = alg[name] / (ms * 1e-3) / 1e9
+        out[name] = {"avg_ms": round(ms, 4), "alg_mb": round(alg[name] / 1e6, 1),
+                     "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+    return out
+
+
 def delta_inputs(B, H, T, K, V, gated, seed):
     """Config 3 / 4 inputs, drawn on the CPU in float32 (q, v ~ N(0,1); k
     ~ N(0,1) l2-normalised; beta = sigmoid(N(0,1)); g = logsigmoid(N(0,1)+4)/16;
@@ -617,6 +675,7 @@ def main():
     q1, config1 = bench_config1(max(10, args.steps))
     delta_kata = None if args.no_delta else bench_delta_kata(max(3, args.steps // 2),
                                                              args.settle_seconds / 3)
+    mixer = bench_mixer(max(5, args.steps), args.settle_seconds / 3)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -656,6 +715,7 @@ def main():
         "kata_state_config5": state,
         "kata_config1": config1,
         "delta_kata_fwd": delta_kata,
+        "mixer_ops": mixer,
     }
     print(json.dumps(out), flush=True)
 

@@ -245,6 +245,44 @@ int linatt_dkata_fwd(const void* q, const void* k, const void* v, const float* b
                      int num_groups, float scale, int normalize, float eps, int dtype,
                      void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Token-mixer prologue / epilogue (the non-GEMM ops around the attention op
+ * in kata/layer.py KataAttention.forward).
+ *
+ * Causal depthwise short convolution with optional SiLU, replacing
+ * fla.modules.ShortConvolution as the mixer uses it (kata/layer.py:178-197,
+ * 299-318; third-party flash-linear-attention==0.5.0, absent here):
+ *   z[b,t,c] = bias[c] + sum_{w<W} weight[c,w] x[b, t-(W-1)+w, c],
+ *   y = activation ? silu(z) : z.
+ * x, y (B,T,C) [dtype], C a multiple of 8, W in {2,3,4}; weight (C,W) and
+ * bias (C) float32 (bias may be NULL).  cache_in (B,C,W) [dtype]: the W inputs
+ * before position 0, newest last (NULL: zeros); cache_out (B,C,W): the W
+ * inputs before position T, for the next call (may be NULL).  The backward
+ * gives dx and float32 dweight (C,W) / dbias (C, may be NULL); no gradient
+ * flows to cache_in.  Workspace: linatt_short_conv_bwd_workspace_bytes. */
+int linatt_short_conv_fwd(const void* x, const float* weight, const float* bias,
+                          const void* cache_in, void* y, void* cache_out, int B, int T, int C,
+                          int W, int activation, int dtype, void* stream);
+size_t linatt_short_conv_bwd_workspace_bytes(int B, int T, int C, int W);
+int linatt_short_conv_bwd(const void* x, const float* weight, const float* bias,
+                          const void* cache_in, const void* dy, void* dx, float* dweight,
+                          float* dbias, void* workspace, int B, int T, int C, int W,
+                          int activation, int dtype, void* stream);
+
+/* RMSNorm over the last dim of a contiguous (n, d) array, fp32 arithmetic,
+ * replacing fla.modules.RMSNorm as the mixer uses it (output norm
+ * kata/layer.py:199-205, 539; q/k norm :126-128, 347):
+ *   y = x r weight, r = (mean(x^2) + eps)^-1/2 (rstd (n) float32 saved);
+ * weight (d) float32 or NULL (no affine).  d = 8 times a power of two, at
+ * most 512.  Backward: dx and, with weight, dweight (d) float32.
+ * Workspace: linatt_rmsnorm_bwd_workspace_bytes. */
+int linatt_rmsnorm_fwd(const void* x, const float* weight, void* y, float* rstd, int n, int d,
+                       float eps, int dtype, void* stream);
+size_t linatt_rmsnorm_bwd_workspace_bytes(int n, int d);
+int linatt_rmsnorm_bwd(const void* x, const float* weight, const float* rstd, const void* dy,
+                       void* dx, float* dweight, void* workspace, int n, int d, int dtype,
+                       void* stream);
+
 /* Row L2 normalisation over the last dim of a contiguous (n, d) array:
  * y = x / sqrt(sum x^2 + eps), rstd (n) float32 = 1 / sqrt(sum x^2 + eps);
  * backward dx = rstd (dy - y <y, dy>).  The normalisation fla applies to q

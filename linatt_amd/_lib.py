@@ -58,6 +58,12 @@ SIGNATURES = {
     "linatt_kata_prefill": (_i, [_vp] * 8 + [_i] * 6 + [_f, _f, _i, _i, _i, _vp]),
     "linatt_kata_prefill_state": (_i, [_vp] * 10 + [_i] * 6 + [_f, _f, _i, _i, _i, _vp]),
     "linatt_kata_decode_step": (_i, [_vp] * 6 + [_i] * 5 + [_f, _f, _i, _vp]),
+    "linatt_short_conv_fwd": (_i, [_vp] * 6 + [_i] * 6 + [_vp]),
+    "linatt_short_conv_bwd_workspace_bytes": (_sz, [_i] * 4),
+    "linatt_short_conv_bwd": (_i, [_vp] * 9 + [_i] * 6 + [_vp]),
+    "linatt_rmsnorm_fwd": (_i, [_vp] * 4 + [_i, _i, _f, _i, _vp]),
+    "linatt_rmsnorm_bwd_workspace_bytes": (_sz, [_i, _i]),
+    "linatt_rmsnorm_bwd": (_i, [_vp] * 7 + [_i] * 3 + [_vp]),
     "linatt_dkata_supported": (_i, [_i, _i, _i, _i]),
     "linatt_dkata_workspace_bytes": (_sz, [_i] * 6),
     "linatt_dkata_fwd": (_i, [_vp] * 8 + [_i] * 6 + [_f, _i, _f, _i, _vp]),

@@ -389,6 +389,118 @@ int linatt_delta_bwd_stages(const void* q, const void* k, const void* v, const f
   return LINATT_OK;
 }
 
+extern "C++" {
+namespace {
+template <typename F>
+hipError_t by_dtype(int dtype, F&& f) {
+  if (dtype == LINATT_BFLOAT16) return f(__bf16{});
+  if (dtype == LINATT_FLOAT16) return f(_Float16{});
+  if (dtype == LINATT_FLOAT32) return f(float{});
+  return hipErrorInvalidValue;
+}
+bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+bool known_dtype(int d) { return d == LINATT_BFLOAT16 || d == LINATT_FLOAT16 || d == LINATT_FLOAT32; }
+}  // namespace
+}  // extern "C++"
+
+int linatt_short_conv_fwd(const void* x, const float* weight, const float* bias,
+                          const void* cache_in, void* y, void* cache_out, int B, int T, int C,
+                          int W, int activation, int dtype, void* stream) {
+  g_last_error.clear();
+  const char* fn = "linatt_short_conv_fwd";
+  if (B <= 0 || T <= 0 || C <= 0) return fail(LINATT_EINVAL, std::string(fn) + ": non-positive size");
+  if (C % 8) return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": channels must be a multiple of 8");
+  if (W < 2 || W > 4) return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": kernel size must be 2, 3 or 4");
+  if (activation != 0 && activation != 1) return fail(LINATT_EINVAL, std::string(fn) + ": activation must be 0 (none) or 1 (silu)");
+  if (!known_dtype(dtype)) return fail(LINATT_EINVAL, std::string(fn) + ": unknown dtype");
+  if (!x || !weight || !y) return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  if (!aligned16(x) || !aligned16(y)) return fail(LINATT_EINVAL, std::string(fn) + ": x and y must be 16-byte aligned");
+  ConvArgs a{};
+  a.x = x; a.w = weight; a.bias = bias; a.cache_in = cache_in; a.y = y; a.cache_out = cache_out;
+  a.B = B; a.T = T; a.C = C; a.act = activation;
+  hipError_t e = by_dtype(dtype, [&](auto t) { return launch_short_conv<decltype(t)>(a, W, false, (hipStream_t)stream); });
+  if (e != hipSuccess) return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
+size_t linatt_short_conv_bwd_workspace_bytes(int B, int T, int C, int W) {
+  if (B <= 0 || T <= 0 || C <= 0 || W < 2 || W > 4) return 0;
+  return short_conv_bwd_workspace(B, T, C, W);
+}
+
+int linatt_short_conv_bwd(const void* x, const float* weight, const float* bias,
+                          const void* cache_in, const void* dy, void* dx, float* dweight,
+                          float* dbias, void* workspace, int B, int T, int C, int W,
+                          int activation, int dtype, void* stream) {
+  g_last_error.clear();
+  const char* fn = "linatt_short_conv_bwd";
+  if (B <= 0 || T <= 0 || C <= 0) return fail(LINATT_EINVAL, std::string(fn) + ": non-positive size");
+  if (C % 8) return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": channels must be a multiple of 8");
+  if (W < 2 || W > 4) return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": kernel size must be 2, 3 or 4");
+  if (activation != 0 && activation != 1) return fail(LINATT_EINVAL, std::string(fn) + ": activation must be 0 (none) or 1 (silu)");
+  if (!known_dtype(dtype)) return fail(LINATT_EINVAL, std::string(fn) + ": unknown dtype");
+  if (!x || !weight || !dy || !dx || !dweight || !workspace)
+    return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  if (!aligned16(x) || !aligned16(dy) || !aligned16(dx))
+    return fail(LINATT_EINVAL, std::string(fn) + ": x, dy and dx must be 16-byte aligned");
+  ConvArgs a{};
+  a.x = x; a.w = weight; a.bias = bias; a.cache_in = cache_in; a.dy = dy; a.dx = dx;
+  a.part = (float*)workspace; a.dw = dweight; a.db = dbias;
+  a.B = B; a.T = T; a.C = C; a.act = activation;
+  hipError_t e = by_dtype(dtype, [&](auto t) { return launch_short_conv<decltype(t)>(a, W, true, (hipStream_t)stream); });
+  if (e != hipSuccess) return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
+static int check_rms(const char* fn, int n, int d, int dtype) {
+  if (n <= 0 || d <= 0) return fail(LINATT_EINVAL, std::string(fn) + ": non-positive size");
+  if (d % 8 || !pow2(d / 8) || d > 512)
+    return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": row length must be 8 times a power of two, at most 512");
+  if (!known_dtype(dtype)) return fail(LINATT_EINVAL, std::string(fn) + ": unknown dtype");
+  return LINATT_OK;
+}
+
+int linatt_rmsnorm_fwd(const void* x, const float* weight, void* y, float* rstd, int n, int d,
+                       float eps, int dtype, void* stream) {
+  g_last_error.clear();
+  const char* fn = "linatt_rmsnorm_fwd";
+  int st = check_rms(fn, n, d, dtype);
+  if (st) return st;
+  if (!(eps >= 0.f)) return fail(LINATT_EINVAL, std::string(fn) + ": eps must be >= 0");
+  if (!x || !y || !rstd) return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  if (!aligned16(x) || !aligned16(y)) return fail(LINATT_EINVAL, std::string(fn) + ": x and y must be 16-byte aligned");
+  hipError_t e = by_dtype(dtype, [&](auto t) {
+    return launch_rmsnorm<decltype(t)>(x, weight, nullptr, nullptr, y, rstd, nullptr, nullptr, n, d,
+                                       eps, false, (hipStream_t)stream);
+  });
+  if (e != hipSuccess) return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
+size_t linatt_rmsnorm_bwd_workspace_bytes(int n, int d) {
+  if (n <= 0 || d <= 0 || d % 8 || !pow2(d / 8) || d > 512) return 0;
+  return (size_t)rmsnorm_bwd_blocks(n, d) * d * sizeof(float);
+}
+
+int linatt_rmsnorm_bwd(const void* x, const float* weight, const float* rstd, const void* dy,
+                       void* dx, float* dweight, void* workspace, int n, int d, int dtype,
+                       void* stream) {
+  g_last_error.clear();
+  const char* fn = "linatt_rmsnorm_bwd";
+  int st = check_rms(fn, n, d, dtype);
+  if (st) return st;
+  if (!x || !rstd || !dy || !dx || !workspace || (dweight && !weight))
+    return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  if (!aligned16(x) || !aligned16(dy) || !aligned16(dx))
+    return fail(LINATT_EINVAL, std::string(fn) + ": x, dy and dx must be 16-byte aligned");
+  hipError_t e = by_dtype(dtype, [&](auto t) {
+    return launch_rmsnorm<decltype(t)>(x, weight, rstd, dy, dx, nullptr, dweight, (float*)workspace,
+                                       n, d, 0.f, true, (hipStream_t)stream);
+  });
+  if (e != hipSuccess) return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
 int linatt_l2norm_fwd(const void* x, void* y, float* rstd, int n, int d, float eps, int dtype,
                       void* stream) {
   g_last_error.clear();

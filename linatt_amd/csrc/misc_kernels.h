@@ -1,4 +1,5 @@
-// Internal launch interface of the small helper kernels (row L2 norm).
+// Internal launch interface of the small helper kernels: row L2 norm, the
+// mixer's short convolution and RMSNorm.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -11,6 +12,34 @@ hipError_t launch_l2norm_fwd(const void* x, void* y, float* rstd, int n, int d, 
 template <typename T>
 hipError_t launch_l2norm_bwd(const void* y, const float* rstd, const void* dy, void* dx, int n,
                              int d, hipStream_t s);
+
+// Causal depthwise short convolution (mixer.hip).  part / dw / db: backward
+// only (partials workspace, weight and bias gradients).
+struct ConvArgs {
+  const void* x;         // (B, T, C)
+  const float* w;        // (C, W)
+  const float* bias;     // (C) or null
+  const void* cache_in;  // (B, C, W) inputs before position 0 (newest last), or null
+  void* y;               // (B, T, C)
+  void* cache_out;       // (B, C, W) the W inputs before position T, or null
+  const void* dy;
+  void* dx;
+  float* part;
+  float* dw;
+  float* db;
+  int B, T, C, act;
+};
+template <typename T>
+hipError_t launch_short_conv(const ConvArgs& a, int W, bool bwd, hipStream_t stream);
+size_t short_conv_bwd_workspace(int B, int T, int C, int W);
+
+// RMSNorm over rows of d (mixer.hip): forward (out = y, rstd_out) or
+// backward (out = dx, dw with the partials workspace).
+template <typename T>
+hipError_t launch_rmsnorm(const void* x, const float* w, const float* rstd_in, const void* dy,
+                          void* out, float* rstd_out, float* dw, float* part, int n, int d,
+                          float eps, bool bwd, hipStream_t stream);
+int rmsnorm_bwd_blocks(int n, int d);
 
 // Sets the calling thread's linatt_last_error() message and returns code
 // (defined with the C-ABI entry points in api.hip).

@@ -1,0 +1,435 @@
+// Elementwise prologue / epilogue of the KATA token mixer, for gfx950.
+//
+// Replaces the two non-GEMM pieces of kata/layer.py's KataAttention.forward
+// around the attention op: the causal short convolutions with SiLU on the
+// projected q, k, v (:299-318, fla.modules.ShortConvolution, constructed at
+// :178-197) and the fp32 output RMSNorm over each head (:539, fla.modules.
+// RMSNorm constructed at :199-205; also the q/k RMSNorm at :126-128, :347).
+// The projections and o_proj stay plain library GEMMs.
+//
+// Short convolution (depthwise, causal, kernel W):
+//   z[t, c] = bias[c] + sum_{w < W} weight[c, w] x[t - (W - 1) + w, c]
+//   y = silu(z) = z / (1 + e^-z)  (or y = z)
+// with x[t < 0] taken from a cache of the W inputs before the chunk (the
+// newest last), or zero.  One lane owns 8 adjacent channels (one 16-byte
+// load per token) and a run of kConvTB tokens, sliding the window in
+// registers; each input row is read once plus a W - 1 row halo.  The
+// backward recomputes z, forms dz = dy silu'(z), dx[s] = sum_w weight[c, w]
+// dz[s + W - 1 - w], and per-lane partial sums of dweight and dbias that a
+// second kernel adds up in a fixed order.
+//
+// RMSNorm over rows of d (fp32 arithmetic): y = x r w, r = (mean x^2 + eps)^-1/2;
+// backward dx = r (g - xh mean(g xh)), g = dy w, xh = x r; dw = sum_rows dy xh.
+// d / 8 lanes own a row (16 bytes each).
+#include "common.h"
+#include "misc_kernels.h"
+
+namespace linatt {
+
+namespace {
+
+constexpr int kConvTB = 16;  // tokens per lane
+
+template <typename T>
+__device__ __forceinline__ void load8f(const T* p, float* out) {
+  const v8_t<T> v = *reinterpret_cast<const v8_t<T>*>(p);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) out[e] = (float)v[e];
+}
+template <>
+__device__ __forceinline__ void load8f<float>(const float* p, float* out) {
+  const f32x4 a = reinterpret_cast<const f32x4*>(p)[0], b = reinterpret_cast<const f32x4*>(p)[1];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    out[e] = a[e];
+    out[4 + e] = b[e];
+  }
+}
+template <typename T>
+__device__ __forceinline__ void store8f(T* p, const float* v) {
+  v8_t<T> o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (T)v[e];
+  *reinterpret_cast<v8_t<T>*>(p) = o;
+}
+template <>
+__device__ __forceinline__ void store8f<float>(float* p, const float* v) {
+  reinterpret_cast<f32x4*>(p)[0] = f32x4{v[0], v[1], v[2], v[3]};
+  reinterpret_cast<f32x4*>(p)[1] = f32x4{v[4], v[5], v[6], v[7]};
+}
+
+// 8 channels of input position pos of batch row b (pos < 0: the cache, or 0)
+template <typename T, int W>
+__device__ __forceinline__ void conv_input(const ConvArgs& a, int b, int c0, int pos, float* out) {
+  if (pos >= 0) {
+    load8f<T>((const T*)a.x + ((int64_t)b * a.T + pos) * a.C + c0, out);
+  } else if (a.cache_in) {
+    const T* cb = (const T*)a.cache_in + ((int64_t)b * a.C + c0) * W + (W + pos);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = (float)cb[e * W];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = 0.f;
+  }
+}
+
+}  // namespace
+
+template <typename T, int W>
+__global__ __launch_bounds__(64) void short_conv_fwd_kernel(ConvArgs a) {
+  const int cg = blockIdx.x * 64 + threadIdx.x, tb = blockIdx.y, b = blockIdx.z;
+  if (8 * cg >= a.C) return;
+  const int c0 = 8 * cg, t0 = tb * kConvTB;
+  float wv[8][W], bv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+#pragma unroll
+    for (int w = 0; w < W; ++w) wv[e][w] = a.w[(c0 + e) * W + w];
+    bv[e] = a.bias ? a.bias[c0 + e] : 0.f;
+  }
+  float win[W][8];  // win[j] = input t - (W - 1) + j for the current t
+#pragma unroll
+  for (int j = 0; j < W - 1; ++j) conv_input<T, W>(a, b, c0, t0 - (W - 1) + j, win[j + 1]);
+  const T* __restrict__ xb = (const T*)a.x + (int64_t)b * a.T * a.C + c0;
+  T* __restrict__ yb = (T*)a.y + (int64_t)b * a.T * a.C + c0;
+  // the run's rows up front (independent loads in flight), rows past T as zero
+  v8_t<T> xr[kConvTB];
+#pragma unroll
+  for (int i = 0; i < kConvTB; ++i)
+    xr[i] = t0 + i < a.T ? *reinterpret_cast<const v8_t<T>*>(xb + (int64_t)(t0 + i) * a.C) : v8_t<T>{};
+#pragma unroll
+  for (int i = 0; i < kConvTB; ++i) {
+    const int t = t0 + i;
+#pragma unroll
+    for (int j = 0; j < W - 1; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) win[j][e] = win[j + 1][e];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) win[W - 1][e] = (float)xr[i][e];
+    if (t >= a.T) break;
+    float yv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float z = bv[e];
+#pragma unroll
+      for (int w = 0; w < W; ++w) z += wv[e][w] * win[w][e];
+      yv[e] = a.act ? z / (1.f + __expf(-z)) : z;
+    }
+    store8f<T>(yb + (int64_t)t * a.C, yv);
+  }
+  // the W inputs before position T, for a later call (decode)
+  if (a.cache_out && t0 <= a.T - 1 && a.T - 1 < t0 + kConvTB) {
+    T* co = (T*)a.cache_out + ((int64_t)b * a.C + c0) * W;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      float v[8];
+      conv_input<T, W>(a, b, c0, a.T - W + w, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) co[e * W + w] = (T)v[e];
+    }
+  }
+}
+
+template <typename T, int W>
+__global__ __launch_bounds__(64) void short_conv_bwd_kernel(ConvArgs a) {
+  const int cg = blockIdx.x * 64 + threadIdx.x, tb = blockIdx.y, b = blockIdx.z;
+  if (8 * cg >= a.C) return;
+  const int c0 = 8 * cg, t0 = tb * kConvTB, t1 = min(t0 + kConvTB, a.T);
+  float wv[8][W], bv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+#pragma unroll
+    for (int w = 0; w < W; ++w) wv[e][w] = a.w[(c0 + e) * W + w];
+    bv[e] = a.bias ? a.bias[c0 + e] : 0.f;
+  }
+  float win[W][8], dz[W][8];  // inputs u - (W - 1) .. u; dz[u - (W - 1)] .. dz[u]
+  float dwp[8][W], dbp[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      dwp[e][w] = 0.f;
+      dz[w][e] = 0.f;
+    }
+    dbp[e] = 0.f;
+  }
+#pragma unroll
+  for (int j = 0; j < W - 1; ++j) conv_input<T, W>(a, b, c0, t0 - (W - 1) + j, win[j + 1]);
+  const int64_t rowb = (int64_t)b * a.T;
+  const T* __restrict__ xb = (const T*)a.x + rowb * a.C + c0;
+  const T* __restrict__ gb = (const T*)a.dy + rowb * a.C + c0;
+  T* __restrict__ dxb = (T*)a.dx + rowb * a.C + c0;
+  constexpr int NU = kConvTB + W - 1;  // positions u whose dz reaches dx[t0 .. t0 + kConvTB - 1]
+  v8_t<T> xr[NU], gr[NU];
+#pragma unroll
+  for (int i = 0; i < NU; ++i) {
+    const bool in = t0 + i < a.T;
+    xr[i] = in ? *reinterpret_cast<const v8_t<T>*>(xb + (int64_t)(t0 + i) * a.C) : v8_t<T>{};
+    gr[i] = in ? *reinterpret_cast<const v8_t<T>*>(gb + (int64_t)(t0 + i) * a.C) : v8_t<T>{};
+  }
+#pragma unroll
+  for (int i = 0; i < NU; ++i) {
+    const int u = t0 + i;
+    if (u >= t1 + W - 1) break;
+#pragma unroll
+    for (int j = 0; j < W - 1; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        win[j][e] = win[j + 1][e];
+        dz[j][e] = dz[j + 1][e];
+      }
+    if (u < a.T) {
+      float g[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        win[W - 1][e] = (float)xr[i][e];
+        g[e] = (float)gr[i][e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float z = bv[e];
+#pragma unroll
+        for (int w = 0; w < W; ++w) z += wv[e][w] * win[w][e];
+        float d = g[e];
+        if (a.act) {
+          const float s = 1.f / (1.f + __expf(-z));
+          d *= s * (1.f + z * (1.f - s));
+        }
+        dz[W - 1][e] = d;
+      }
+      if (u < t1) {  // this lane's own positions: weight and bias gradients
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+#pragma unroll
+          for (int w = 0; w < W; ++w) dwp[e][w] += dz[W - 1][e] * win[w][e];
+          dbp[e] += dz[W - 1][e];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dz[W - 1][e] = 0.f;
+    }
+    const int s = u - (W - 1);  // dx[s] = sum_w weight[w] dz[s + W - 1 - w]
+    if (s >= t0) {
+      float dxv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) acc += wv[e][w] * dz[W - 1 - w][e];
+        dxv[e] = acc;
+      }
+      store8f<T>(dxb + (int64_t)s * a.C, dxv);
+    }
+  }
+  // partials: part[(b * ntb + tb)][c][0 .. W - 1 weight, W bias]
+  float* pp = a.part + ((int64_t)(b * gridDim.y + tb) * a.C + c0) * (W + 1);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+#pragma unroll
+    for (int w = 0; w < W; ++w) pp[e * (W + 1) + w] = dwp[e][w];
+    pp[e * (W + 1) + W] = dbp[e];
+  }
+}
+
+// out[i] = sum_p part[p][i] for i < n, in a fixed order: 1024 threads per
+// block, 32 columns by 32 row phases (phase k sums rows k, k + 32, ...), then
+// one thread per column adds the 32 phase sums.
+__global__ __launch_bounds__(1024) void colsum_kernel(const float* __restrict__ part,
+                                                      float* __restrict__ out, int np, int n) {
+  __shared__ float red[32][33];
+  const int c = blockIdx.x * 32 + (threadIdx.x & 31), k = threadIdx.x >> 5;
+  float s = 0.f;
+  if (c < n)
+    for (int p = k; p < np; p += 32) s += part[(int64_t)p * n + c];
+  red[k][threadIdx.x & 31] = s;
+  __syncthreads();
+  if (threadIdx.x < 32 && c < n) {
+    float t = 0.f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) t += red[j][threadIdx.x];
+    out[c] = t;
+  }
+}
+
+// dweight[c][w] and dbias[c] from the summed partials [c][0 .. W - 1, W]
+__global__ __launch_bounds__(256) void short_conv_split_kernel(const float* __restrict__ sum,
+                                                               float* __restrict__ dw,
+                                                               float* __restrict__ db, int C,
+                                                               int W) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= C * (W + 1)) return;
+  const int c = i / (W + 1), w = i % (W + 1);
+  if (w < W) dw[c * W + w] = sum[i];
+  else if (db) db[c] = sum[i];
+}
+
+template <typename T>
+hipError_t launch_short_conv(const ConvArgs& a, int W, bool bwd, hipStream_t stream) {
+  const int ntb = (a.T + kConvTB - 1) / kConvTB;
+  const dim3 grid((a.C / 8 + 63) / 64, ntb, a.B);
+#define LINATT_CONV_W(WW)                                                              \
+  case WW:                                                                             \
+    if (bwd) short_conv_bwd_kernel<T, WW><<<grid, dim3(64), 0, stream>>>(a);           \
+    else short_conv_fwd_kernel<T, WW><<<grid, dim3(64), 0, stream>>>(a);               \
+    break;
+  switch (W) {
+    LINATT_CONV_W(2)
+    LINATT_CONV_W(3)
+    LINATT_CONV_W(4)
+    default: return hipErrorInvalidValue;
+  }
+#undef LINATT_CONV_W
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !bwd) return e;
+  const int n = a.C * (W + 1), np = a.B * ntb;
+  float* sum = a.part + (size_t)np * n;
+  colsum_kernel<<<dim3((n + 31) / 32), dim3(1024), 0, stream>>>(a.part, sum, np, n);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  short_conv_split_kernel<<<dim3((n + 255) / 256), dim3(256), 0, stream>>>(sum, a.dw, a.db, a.C, W);
+  return hipGetLastError();
+}
+
+size_t short_conv_bwd_workspace(int B, int T, int C, int W) {
+  const size_t ntb = (size_t)(T + kConvTB - 1) / kConvTB;
+  return ((size_t)B * ntb + 1) * C * (W + 1) * sizeof(float);  // partials + their sums
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm
+// ---------------------------------------------------------------------------
+constexpr int kRmsRows = 4;  // rows per lane group in the forward
+
+template <typename T, int L>  // L = d / 8 lanes per row
+__global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ x,
+                                                          const float* __restrict__ wt,
+                                                          T* __restrict__ y,
+                                                          float* __restrict__ rstd, int n,
+                                                          float eps) {
+  constexpr int d = 8 * L, RPB = 256 / L;
+  const int li = threadIdx.x % L;
+  const int row0 = blockIdx.x * RPB * kRmsRows + threadIdx.x / L;
+  float wv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) wv[e] = wt ? wt[8 * li + e] : 1.f;
+  float v[kRmsRows][8];
+#pragma unroll
+  for (int r = 0; r < kRmsRows; ++r) {
+    const int row = row0 + r * RPB;
+    if (row < n) load8f<T>(x + (int64_t)row * d + 8 * li, v[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < kRmsRows; ++r) {
+    const int row = row0 + r * RPB;
+    if (row >= n) break;  // uniform over the row's L lanes
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += v[r][e] * v[r][e];
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    const float rr = rsqrtf(ss / d + eps);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[r][e] *= rr * wv[e];
+    store8f<T>(y + (int64_t)row * d + 8 * li, v[r]);
+    if (li == 0) rstd[row] = rr;
+  }
+}
+
+template <typename T, int L>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const T* __restrict__ x,
+                                                          const float* __restrict__ wt,
+                                                          const float* __restrict__ rstd,
+                                                          const T* __restrict__ dy,
+                                                          T* __restrict__ dx,
+                                                          float* __restrict__ part, int n) {
+  constexpr int d = 8 * L, RPB = 256 / L;
+  __shared__ float red[RPB][d + 1];
+  const int li = threadIdx.x % L, rg = threadIdx.x / L;
+  float dwp[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) dwp[e] = 0.f;
+  for (int row = blockIdx.x * RPB + rg; row < n; row += gridDim.x * RPB) {
+    float xv[8], g[8], wv[8];
+    load8f<T>(x + (int64_t)row * d + 8 * li, xv);
+    load8f<T>(dy + (int64_t)row * d + 8 * li, g);
+    const float r = rstd[row];
+    float dot = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      wv[e] = wt ? wt[8 * li + e] : 1.f;
+      xv[e] *= r;  // xh
+      dwp[e] += g[e] * xv[e];
+      g[e] *= wv[e];
+      dot += g[e] * xv[e];
+    }
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) dot += __shfl_xor(dot, off);
+    dot /= d;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) g[e] = r * (g[e] - xv[e] * dot);
+    store8f<T>(dx + (int64_t)row * d + 8 * li, g);
+  }
+  // per-block weight-gradient partial: sum over the block's row groups
+#pragma unroll
+  for (int e = 0; e < 8; ++e) red[rg][8 * li + e] = dwp[e];
+  __syncthreads();
+  for (int c = threadIdx.x; c < d; c += 256) {
+    float s = 0.f;
+    for (int k = 0; k < RPB; ++k) s += red[k][c];
+    part[(int64_t)blockIdx.x * d + c] = s;
+  }
+}
+
+int rmsnorm_bwd_blocks(int n, int d) {
+  const int rpb = 256 / (d / 8);
+  const int need = (n + rpb - 1) / rpb;
+  return need < 1024 ? need : 1024;
+}
+
+template <typename T>
+hipError_t launch_rmsnorm(const void* x, const float* w, const float* rstd_in, const void* dy,
+                          void* out, float* rstd_out, float* dw, float* part, int n, int d,
+                          float eps, bool bwd, hipStream_t stream) {
+  const int L = d / 8;
+  const int rpb = 256 / L;
+  const int nbf = (n + rpb * kRmsRows - 1) / (rpb * kRmsRows), nbb = rmsnorm_bwd_blocks(n, d);
+#define LINATT_RMS_L(LL)                                                                          \
+  case LL:                                                                                        \
+    if (bwd)                                                                                      \
+      rmsnorm_bwd_kernel<T, LL><<<dim3(nbb), dim3(256), 0, stream>>>(                             \
+          (const T*)x, w, rstd_in, (const T*)dy, (T*)out, part, n);                               \
+    else                                                                                          \
+      rmsnorm_fwd_kernel<T, LL><<<dim3(nbf), dim3(256), 0, stream>>>((const T*)x, w, (T*)out,     \
+                                                                     rstd_out, n, eps);           \
+    break;
+  switch (L) {
+    LINATT_RMS_L(1)
+    LINATT_RMS_L(2)
+    LINATT_RMS_L(4)
+    LINATT_RMS_L(8)
+    LINATT_RMS_L(16)
+    LINATT_RMS_L(32)
+    LINATT_RMS_L(64)
+    default: return hipErrorInvalidValue;
+  }
+#undef LINATT_RMS_L
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !bwd || !dw) return e;
+  colsum_kernel<<<dim3((d + 31) / 32), dim3(1024), 0, stream>>>(part, dw, nbb, d);
+  return hipGetLastError();
+}
+
+template hipError_t launch_short_conv<__bf16>(const ConvArgs&, int, bool, hipStream_t);
+template hipError_t launch_short_conv<_Float16>(const ConvArgs&, int, bool, hipStream_t);
+template hipError_t launch_short_conv<float>(const ConvArgs&, int, bool, hipStream_t);
+template hipError_t launch_rmsnorm<__bf16>(const void*, const float*, const float*, const void*,
+                                           void*, float*, float*, float*, int, int, float, bool,
+                                           hipStream_t);
+template hipError_t launch_rmsnorm<_Float16>(const void*, const float*, const float*, const void*,
+                                             void*, float*, float*, float*, int, int, float, bool,
+                                             hipStream_t);
+template hipError_t launch_rmsnorm<float>(const void*, const float*, const float*, const void*,
+                                          void*, float*, float*, float*, int, int, float, bool,
+                                          hipStream_t);
+
+}  // namespace linatt

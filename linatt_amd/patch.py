@@ -18,6 +18,9 @@ Names rebound (only in modules that are importable; the rest are skipped):
   (``kata/layer.py:29-37``), so rebinding the defining module alone would not
   reach the mixer;
 * ``kata.spd.chunk_scan_cat.spd_chunk_scan_cat``;
+* the mixer's ``ShortConvolution`` and ``RMSNorm`` classes, which
+  ``kata.layer`` imports from ``fla.modules`` (``kata/layer.py:20``); the
+  rebinding must happen before the model is built;
 * the SPD delta rule's forward pieces ``flash_delta_U``,
   ``flash_delta_readout`` and ``flash_delta_den`` in ``kata.spd.flash_delta``
   (``flash_delta`` itself stays the reference's while its backward has no
@@ -46,6 +49,8 @@ TARGETS = (
                    "parallel_kata_attn_sum_fwd_impl", "parallel_kata_attn_decay",
                    "parallel_kata_attn_bwd", "parallel_kata_attn_bwd_triton")),
     ("kata.spd.chunk_scan_cat", "spd_chunk_scan_cat", "spd_state", "spd_chunk_scan_cat"),
+    ("kata.layer", "ShortConvolution", "mixer", "ShortConvolution"),
+    ("kata.layer", "RMSNorm", "mixer", "RMSNorm"),
     *(("kata.spd.flash_delta", name, "flash_delta", name)
       for name in ("flash_delta_U", "flash_delta_readout", "flash_delta_den")),
     ("fla.layers.delta_net", "chunk_delta_rule", "delta_rule", "chunk_delta_rule"),

@@ -39,6 +39,36 @@ def test_python_signatures_cover_header():
     assert set(declared_functions()) == set(_lib.SIGNATURES)
 
 
+def declared_prototypes():
+    """{name: [parameter declarations]} from the header's prototypes."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(linatt_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        params = [p.strip() for p in m.group(2).split(",") if p.strip()]
+        out[m.group(1)] = [] if params == ["void"] else params
+    return out
+
+
+def test_python_signatures_match_prototypes():
+    """Each ctypes signature has the header prototype's arity, and pointer,
+    float, int and size_t parameters line up."""
+    from linatt_amd import _lib
+    protos = declared_prototypes()
+    assert set(protos) == set(_lib.SIGNATURES)
+    for name, params in protos.items():
+        res, args = _lib.SIGNATURES[name]
+        assert len(args) == len(params), (name, len(args), len(params))
+        for decl, ct in zip(params, args):
+            if "*" in decl:
+                assert ct is ctypes.c_void_p, (name, decl)
+            elif decl.startswith("float"):
+                assert ct is ctypes.c_float, (name, decl)
+            elif decl.startswith("size_t"):
+                assert ct is ctypes.c_size_t, (name, decl)
+            else:
+                assert ct is ctypes.c_int, (name, decl)
+
+
 def test_version_and_support(lib):
     assert lib.linatt_abi_version() == 3
     BF16, F32, F16 = 1, 0, 2

@@ -25,6 +25,7 @@ def _orig(tag):
     return f
 
 
+MIXER_NAMES = ("ShortConvolution", "RMSNorm")
 DELTA_KATA_NAMES = ("flash_delta", "flash_delta_U", "flash_delta_readout", "flash_delta_den")
 KATA_NAMES = ("parallel_kata_attn", "parallel_kata_attn_fwd", "parallel_kata_attn_sum",
               "parallel_kata_attn_sum_fwd_impl", "parallel_kata_attn_decay",
@@ -40,7 +41,8 @@ def stub_reference(monkeypatch):
         "kata": _stub("kata"),
         "kata.parallel_kata_attn": _stub("kata.parallel_kata_attn", **{n: _orig("ref_" + n) for n in KATA_NAMES}),
         # the mixer binds a subset of the names (no backward entry points)
-        "kata.layer": _stub("kata.layer", **{n: _orig("layer_" + n) for n in KATA_NAMES[:5]}),
+        "kata.layer": _stub("kata.layer", **{n: _orig("layer_" + n)
+                                              for n in KATA_NAMES[:5] + MIXER_NAMES}),
         "kata.spd": _stub("kata.spd"),
         "kata.spd.chunk_scan_cat": _stub("kata.spd.chunk_scan_cat", spd_chunk_scan_cat=_orig("ref_scan")),
         "kata.spd.flash_delta": _stub("kata.spd.flash_delta",
@@ -71,7 +73,9 @@ def test_patch_rebinds_every_name(stub_reference):
     # a name the mixer never imported is not added to it
     assert not hasattr(m["kata.layer"], "parallel_kata_attn_bwd")
     assert m["kata.spd.chunk_scan_cat"].spd_chunk_scan_cat is spd_state.spd_chunk_scan_cat
-    from linatt_amd import flash_delta as fd
+    from linatt_amd import flash_delta as fd, mixer
+    for n in MIXER_NAMES:
+        assert getattr(m["kata.layer"], n) is getattr(mixer, n)
     for n in DELTA_KATA_NAMES[1:]:
         assert getattr(m["kata.spd.flash_delta"], n) is getattr(fd, n)
     # no HIP backward yet: the trainable op stays the reference's
@@ -80,7 +84,7 @@ def test_patch_rebinds_every_name(stub_reference):
     assert m["fla.ops.delta_rule"].chunk_delta_rule is delta_rule.chunk_delta_rule
     assert m["fla.layers.gated_deltanet"].chunk_gated_delta_rule is delta_rule.chunk_gated_delta_rule
     assert m["fla.ops.gated_delta_rule"].chunk_gated_delta_rule is delta_rule.chunk_gated_delta_rule
-    assert len(done) == len(KATA_NAMES) + 5 + 5 + 3
+    assert len(done) == len(KATA_NAMES) + 5 + 5 + 3 + len(MIXER_NAMES)
 
 
 def test_patch_is_idempotent_and_restorable(stub_reference):

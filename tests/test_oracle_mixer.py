@@ -1,0 +1,77 @@
+"""Pins for ``oracle/mixer.py`` (the mixer's short convolution and RMSNorm):
+explicit loops, the library convolution, cache continuation and closed forms.
+CPU only."""
+
+import pytest
+import torch
+
+from oracle import mixer as X
+
+
+def _data(B, T, C, W, seed, bias=True, cache=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, T, C, generator=g, dtype=torch.float64)
+    w = torch.randn(C, W, generator=g, dtype=torch.float64) / W
+    b = torch.randn(C, generator=g, dtype=torch.float64) if bias else None
+    c = torch.randn(B, C, W, generator=g, dtype=torch.float64) if cache else None
+    return x, w, b, c
+
+
+@pytest.mark.parametrize("W", [2, 3, 4])
+@pytest.mark.parametrize("act", ["silu", None])
+@pytest.mark.parametrize("bias,cache", [(True, True), (False, False), (False, True)])
+def test_conv_matches_loops(W, act, bias, cache):
+    x, w, b, c = _data(2, 7, 5, W, W, bias, cache)
+    y, _ = X.short_conv(x, w, b, act, c)
+    assert torch.allclose(y, X.short_conv_loop(x, w, b, act, c), atol=1e-12)
+
+
+@pytest.mark.parametrize("W", [2, 4])
+def test_conv_matches_library_conv1d(W):
+    """Without a cache: a depthwise nn.functional.conv1d with W - 1 left
+    padding, truncated to T (the nn.Conv1d fla's module derives from)."""
+    x, w, b, _ = _data(3, 20, 6, W, 11)
+    ref = torch.nn.functional.conv1d(x.transpose(1, 2), w[:, None, :], b, padding=W - 1,
+                                     groups=6)[..., :20].transpose(1, 2)
+    y, _ = X.short_conv(x, w, b, None)
+    assert torch.allclose(y, ref, atol=1e-12)
+    ys, _ = X.short_conv(x, w[:, None, :], b, "silu")  # (C, 1, W) weights accepted
+    assert torch.allclose(ys, ref * torch.sigmoid(ref), atol=1e-12)
+
+
+@pytest.mark.parametrize("split", [1, 2, 3, 9])
+def test_conv_cache_continuation(split):
+    """A sequence cut anywhere, the second part continued from the first
+    part's final cache, gives the same outputs and the same final cache."""
+    x, w, b, c = _data(2, 12, 4, 4, 5)
+    y, fin = X.short_conv(x, w, b, "silu", c)
+    y1, f1 = X.short_conv(x[:, :split], w, b, "silu", c)
+    y2, f2 = X.short_conv(x[:, split:], w, b, "silu", f1)
+    assert torch.allclose(torch.cat([y1, y2], 1), y, atol=1e-12)
+    assert torch.allclose(f2, fin, atol=0)
+    # the final cache is the last W inputs, newest last
+    assert torch.equal(fin, x[:, -4:].transpose(1, 2))
+
+
+def test_conv_cache_shorter_sequence():
+    """T < W: the final cache keeps the older cache entries before x."""
+    x, w, b, c = _data(1, 2, 3, 4, 6)
+    _, fin = X.short_conv(x, w, b, "silu", c)
+    assert torch.equal(fin[:, :, :2], c[:, :, 2:])
+    assert torch.equal(fin[:, :, 2:], x.transpose(1, 2))
+
+
+def test_rmsnorm_closed_forms():
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(5, 64, generator=g, dtype=torch.float64) * 3
+    eps = 1e-5
+    y = X.rmsnorm(x, None, eps)
+    ms = (x * x).mean(-1)
+    assert torch.allclose((y * y).mean(-1), ms / (ms + eps), atol=1e-12)
+    # scale invariance at eps = 0, weight scales each column
+    assert torch.allclose(X.rmsnorm(7.5 * x, None, 0.0), X.rmsnorm(x, None, 0.0), atol=1e-12)
+    w = torch.linspace(0.5, 2.0, 64, dtype=torch.float64)
+    assert torch.allclose(X.rmsnorm(x, w, eps), y * w, atol=1e-12)
+    # a constant row maps to sign * sqrt(c^2 / (c^2 + eps))
+    c = torch.full((1, 64), -0.01, dtype=torch.float64)
+    assert torch.allclose(X.rmsnorm(c, None, eps), -torch.full_like(c, (1e-4 / (1e-4 + eps)) ** 0.5))
