@@ -188,7 +188,8 @@ def bench_delta(gated, steps, warmup, settle_s):
 
 def bench_delta_kata(steps, settle_s):
     """The SPD delta rule (DeltaKata, kata/spd/flash_delta.py:1060-1116)
-    forward at the KATA bench shape with the mixer's settings
+    forward (the training variant, which keeps what the backward reads) and
+    backward at the KATA bench shape with the mixer's settings
     (configs/model/kata_delta_m1_340m.yaml: M=1, delta_scale 0.5, l2-normalised
     q, k, beta = sigmoid): B8 H12 T2048 D64 bf16 through linatt_dkata_fwd.
     Algorithmic FLOPs, causal pairs T^2/2 per head: the Gram kappa(k, k)
@@ -213,30 +214,45 @@ def bench_delta_kata(steps, settle_s):
                      dtype=torch.uint8)
     P, sp = _lib.ptr, _lib.stream_of(qd)
 
+    U = torch.empty(B, T, H, D, device=dev)
+    do = torch.randn(B, T, H, D, generator=g).to(dev)
+    dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+    dbeta = torch.empty(B, T, H, device=dev)
+    bws = torch.empty(L.linatt_dkata_bwd_workspace_bytes(B, T, H, D, D, dt), device=dev,
+                      dtype=torch.uint8)
+
     def fwd():
-        _lib.check("linatt_dkata_fwd", L.linatt_dkata_fwd(
-            P(qd), P(kd), P(vd), P(bd), None, P(o), P(den), P(ws), B, T, H, D, D, M, scale, 0,
+        _lib.check("linatt_dkata_fwd_train", L.linatt_dkata_fwd_train(
+            P(qd), P(kd), P(vd), P(bd), P(U), P(o), P(den), P(ws), B, T, H, D, D, M, scale, 0,
             1e-5, dt, sp))
 
-    settle([("fwd", fwd)], settle_s)
-    for _ in range(2):
-        fwd()
+    def bwd():
+        _lib.check("linatt_dkata_bwd", L.linatt_dkata_bwd(
+            P(qd), P(kd), P(vd), P(bd), P(U), None, P(den), P(do), P(dq), P(dk), P(dv),
+            P(dbeta), P(ws), P(bws), B, T, H, D, D, M, scale, 0, 1e-5, dt, sp))
+
+    parts = [("fwd", fwd), ("bwd", bwd)]
+    settle(parts, settle_s)
     stream = torch.cuda.current_stream(dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(steps):
+    for s_ in range(steps):
+        ev[s_][0].record(stream)
         fwd()
-    e1.record(stream)
+        ev[s_][1].record(stream)
+        bwd()
+        ev[s_][2].record(stream)
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+    f_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
+    b_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / steps
     flops = B * H * T * T / 2 * (4 * M * D + 4 * D)
-    tf = flops / (ms * 1e-3) / 1e12
+    tf = flops / (f_ms * 1e-3) / 1e12
     return {"config": {"B": B, "H": H, "T": T, "D": D, "num_groups": M, "scale": scale,
                        "normalize": False, "seed": 6},
-            "fwd_ms": round(ms, 4), "tokens_per_s": round(B * T / (ms * 1e-3), 1),
-            "alg_gflop": round(flops / 1e9, 2), "tflops": round(tf, 1),
-            "frac_mfma_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+            "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4),
+            "tokens_per_s_fwd_bwd": round(B * T / ((f_ms + b_ms) * 1e-3), 1),
+            "fwd_alg_gflop": round(flops / 1e9, 2), "fwd_tflops": round(tf, 1),
+            "fwd_frac_mfma_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
 
 
 def bench_mixer(steps, settle_s):

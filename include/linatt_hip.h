@@ -226,7 +226,7 @@ int linatt_kata_decode_step(const void* q, const void* k, const void* v, float* 
                             float eps, int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------
- * SPD delta rule (DeltaKata), forward.  Replaces the forward of flash_delta
+ * SPD delta rule (DeltaKata).  Replaces the forward of flash_delta
  * (kata/spd/flash_delta.py:1060-1116: _flash_U_kernel :25-183,
  * _readout_kernel :898-972, _den_kernel :986-1046), called by the mixer's
  * delta branch (kata/layer.py:377-420).  With the sum-SPD kernel
@@ -244,6 +244,27 @@ int linatt_dkata_fwd(const void* q, const void* k, const void* v, const float* b
                      float* o, float* den, void* workspace, int B, int T, int H, int d, int dv,
                      int num_groups, float scale, int normalize, float eps, int dtype,
                      void* stream);
+
+/* The forward for training: as linatt_dkata_fwd, U required; the workspace
+ * then also holds what linatt_dkata_bwd reads and must reach it unchanged. */
+int linatt_dkata_fwd_train(const void* q, const void* k, const void* v, const float* beta,
+                           float* U, float* o, float* den, void* workspace, int B, int T, int H,
+                           int d, int dv, int num_groups, float scale, int normalize, float eps,
+                           int dtype, void* stream);
+
+/* Backward, replacing flash_delta_bwd (kata/spd/flash_delta.py:830-895) and
+ * _FlashDelta.backward (:1084-1108): dq, dk (B,T,H,d), dv (B,T,H,dv) [dtype]
+ * and dbeta (B,T,H) float32 for the loss <o, dout> (dout float32, the
+ * forward's output dtype).  U, o (normalize only), den: the training
+ * forward's outputs; fwd_workspace: its workspace; workspace:
+ * linatt_dkata_bwd_workspace_bytes.  bfloat16 only (fp16 cannot carry the
+ * intermediate dU at small scales); other dtypes return LINATT_EUNSUPPORTED. */
+size_t linatt_dkata_bwd_workspace_bytes(int B, int T, int H, int d, int dv, int dtype);
+int linatt_dkata_bwd(const void* q, const void* k, const void* v, const float* beta,
+                     const float* U, const float* o, const float* den, const float* dout,
+                     void* dq, void* dk, void* dv, float* dbeta, void* fwd_workspace,
+                     void* workspace, int B, int T, int H, int d, int dv_dim, int num_groups,
+                     float scale, int normalize, float eps, int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Token-mixer prologue / epilogue (the non-GEMM ops around the attention op

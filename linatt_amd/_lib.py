@@ -67,6 +67,9 @@ SIGNATURES = {
     "linatt_dkata_supported": (_i, [_i, _i, _i, _i]),
     "linatt_dkata_workspace_bytes": (_sz, [_i] * 6),
     "linatt_dkata_fwd": (_i, [_vp] * 8 + [_i] * 6 + [_f, _i, _f, _i, _vp]),
+    "linatt_dkata_fwd_train": (_i, [_vp] * 8 + [_i] * 6 + [_f, _i, _f, _i, _vp]),
+    "linatt_dkata_bwd_workspace_bytes": (_sz, [_i] * 6),
+    "linatt_dkata_bwd": (_i, [_vp] * 14 + [_i] * 6 + [_f, _i, _f, _i, _vp]),
 }
 
 

@@ -547,12 +547,91 @@ size_t linatt_dkata_workspace_bytes(int B, int T, int H, int d, int dv, int dtyp
   return dkata_layout(B, T, H, d, dv, elt_bytes(dtype)).bytes;
 }
 
+static int dkata_fwd_entry(const char* fn, int keep_e, const void* q, const void* k,
+                           const void* v, const float* beta, float* U, float* o, float* den,
+                           void* workspace, int B, int T, int H, int d, int dv, int num_groups,
+                           float scale, int normalize, float eps, int dtype, void* stream);
+
 int linatt_dkata_fwd(const void* q, const void* k, const void* v, const float* beta, float* U,
                      float* o, float* den, void* workspace, int B, int T, int H, int d, int dv,
                      int num_groups, float scale, int normalize, float eps, int dtype,
                      void* stream) {
+  return dkata_fwd_entry("linatt_dkata_fwd", 0, q, k, v, beta, U, o, den, workspace, B, T, H, d,
+                         dv, num_groups, scale, normalize, eps, dtype, stream);
+}
+
+int linatt_dkata_fwd_train(const void* q, const void* k, const void* v, const float* beta,
+                           float* U, float* o, float* den, void* workspace, int B, int T, int H,
+                           int d, int dv, int num_groups, float scale, int normalize, float eps,
+                           int dtype, void* stream) {
+  if (!U) {
+    g_last_error = "linatt_dkata_fwd_train: U is required (the backward reads it)";
+    return LINATT_EINVAL;
+  }
+  return dkata_fwd_entry("linatt_dkata_fwd_train", 1, q, k, v, beta, U, o, den, workspace, B, T,
+                         H, d, dv, num_groups, scale, normalize, eps, dtype, stream);
+}
+
+size_t linatt_dkata_bwd_workspace_bytes(int B, int T, int H, int d, int dv, int dtype) {
+  if (B <= 0 || T <= 0 || H <= 0 || d <= 0 || dv <= 0) return 0;
+  return dkata_bwd_layout(B, T, H, d, dv, elt_bytes(dtype)).bytes;
+}
+
+int linatt_dkata_bwd(const void* q, const void* k, const void* v, const float* beta,
+                     const float* U, const float* o, const float* den, const float* dout,
+                     void* dq, void* dk, void* dv, float* dbeta, void* fwd_workspace,
+                     void* workspace, int B, int T, int H, int d, int dv_dim, int num_groups,
+                     float scale, int normalize, float eps, int dtype, void* stream) {
   g_last_error.clear();
-  const char* fn = "linatt_dkata_fwd";
+  const char* fn = "linatt_dkata_bwd";
+  char buf[160];
+  snprintf(buf, sizeof buf, "B=%d T=%d H=%d d=%d dv=%d num_groups=%d", B, T, H, d, dv_dim, num_groups);
+  if (B <= 0 || T <= 0 || H <= 0 || d <= 0 || dv_dim <= 0 || num_groups <= 0)
+    return fail(LINATT_EINVAL, std::string(fn) + ": non-positive dimension (" + buf + ")");
+  if (!(scale > 0.f) || (normalize && !(eps >= 0.f)))
+    return fail(LINATT_EINVAL, std::string(fn) + ": scale must be positive and eps non-negative");
+  if ((int64_t)B * H * (T + 63) > (int64_t)INT32_MAX / 2)
+    return fail(LINATT_EINVAL, std::string(fn) + ": B*H*T too large");
+  if (!linatt_dkata_supported(dtype, d, dv_dim, num_groups))
+    return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": no kernel compiled for dtype " +
+                                         std::to_string(dtype) + " (" + buf + ")");
+  // dU = lower(A_qk)^T do' is carried in the input dtype; fp16's range loses
+  // it for small scales (kappa ~ scale^2), so the backward is bf16 only, the
+  // dtype the mixer calls flash_delta with (kata/layer.py:409-412)
+  if (dtype != LINATT_BFLOAT16)
+    return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": the backward is compiled for bfloat16 only");
+  if (!q || !k || !v || !beta || !U || !den || !dout || !dq || !dk || !dv || !dbeta ||
+      !fwd_workspace || !workspace || (normalize && !o))
+    return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  const void* ps[] = {q, k, v, U, o, dout, dq, dk, dv, fwd_workspace, workspace};
+  for (const void* p : ps)
+    if (p && !aligned16(p))
+      return fail(LINATT_EINVAL, std::string(fn) + ": tensors must be 16-byte aligned");
+  DKataBwdArgs a{};
+  a.q = q; a.k = k; a.v = v; a.beta = beta; a.U = U; a.o = o; a.den = den; a.dout = dout;
+  a.dq = dq; a.dk = dk; a.dv = dv; a.dbeta = dbeta;
+  a.ws = (char*)fwd_workspace;
+  a.L = dkata_layout(B, T, H, d, dv_dim, elt_bytes(dtype));
+  a.bws = (char*)workspace;
+  a.BL = dkata_bwd_layout(B, T, H, d, dv_dim, elt_bytes(dtype));
+  a.B = B; a.T = T; a.H = H;
+  a.scale = scale; a.scale2 = scale * scale; a.eps = eps; a.normalize = normalize ? 1 : 0;
+  hipError_t e = hipErrorInvalidValue;
+#define LINATT_TRY_DKB(T_, D_, DV_, M_) \
+  if (dtype == dtype_of<T_>() && d == D_ && dv_dim == DV_ && num_groups == M_) \
+    e = launch_dkata_bwd<T_, D_, DV_, M_>(a, (hipStream_t)stream);
+  LINATT_DKATA_SHAPES(LINATT_TRY_DKB)
+#undef LINATT_TRY_DKB
+  if (e != hipSuccess)
+    return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
+static int dkata_fwd_entry(const char* fn, int keep_e, const void* q, const void* k,
+                           const void* v, const float* beta, float* U, float* o, float* den,
+                           void* workspace, int B, int T, int H, int d, int dv, int num_groups,
+                           float scale, int normalize, float eps, int dtype, void* stream) {
+  g_last_error.clear();
   char buf[160];
   snprintf(buf, sizeof buf, "B=%d T=%d H=%d d=%d dv=%d num_groups=%d", B, T, H, d, dv, num_groups);
   if (B <= 0 || T <= 0 || H <= 0 || d <= 0 || dv <= 0 || num_groups <= 0)
@@ -576,6 +655,7 @@ int linatt_dkata_fwd(const void* q, const void* k, const void* v, const float* b
   a.L = dkata_layout(B, T, H, d, dv, elt_bytes(dtype));
   a.B = B; a.T = T; a.H = H;
   a.scale = scale; a.scale2 = scale * scale; a.eps = eps; a.normalize = normalize ? 1 : 0;
+  a.keep_e = keep_e;
   hipError_t e = hipErrorInvalidValue;
 #define LINATT_TRY_DK(T_, D_, DV_, M_) \
   if (dtype == dtype_of<T_>() && d == D_ && dv == DV_ && num_groups == M_) \

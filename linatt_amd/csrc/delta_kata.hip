@@ -45,6 +45,30 @@ DKataLayout dkata_layout(int B, int T, int H, int D, int DV, int eb) {
   L.UT = take(BH * DV * Tp * eb);
   L.Ub = take((size_t)B * T * H * DV * eb);
   L.Ob = take((size_t)B * T * H * DV * eb);
+  L.Ein = take((size_t)B * T * H * DV * 4);
+  L.bytes = off;
+  return L;
+}
+
+DKataBwdLayout dkata_bwd_layout(int B, int T, int H, int D, int DV, int eb) {
+  DKataBwdLayout L{};
+  const size_t NC = (size_t)(T + 63) / 64, Tp = NC * 64, rows = (size_t)B * T * H;
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off = al256(off + bytes); return o; };
+  L.dOp = take(rows * DV * eb);
+  L.O16 = take(rows * DV * eb);
+  L.Zo = take(rows * DV * eb);
+  L.ones = take(rows * 4);
+  L.kws = take(kata_dop_offset((int64_t)rows) + (eb == 2 ? rows * DV * 2 : 0));
+  L.dU = take(rows * DV * eb);
+  L.dkr = take(rows * D * eb);
+  L.Ksh = take(rows * D * eb);
+  L.Xn = take(rows * DV * eb);
+  L.XT = take((size_t)B * H * DV * Tp * eb);
+  L.dbV = take(rows * DV * 4);
+  L.dqe = take(rows * D * eb);
+  L.dke = take(rows * D * eb);
+  L.dve = take(rows * DV * eb);
   L.bytes = off;
   return L;
 }
@@ -312,6 +336,13 @@ __global__ __launch_bounds__(256) void dkata_U_kernel(DKataArgs a) {
     f32x16 ecs = ec[ub];
 #pragma unroll
     for (int e = 0; e < 16; ++e) ecs[e] = a.scale2 * (ecs[e] + Xc[partner][e][lane]);
+    if (a.keep_e && tl < Tn) {  // the inter-chunk part of E_t, for the backward's dbeta
+      float* er = (float*)(a.ws + a.L.Ein) + (((int64_t)b * Tn + tl) * a.H + h) * DV;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<float4*>(er + 32 * ub + 8 * i + 4 * hh) =
+            make_float4(ecs[4 * i], ecs[4 * i + 1], ecs[4 * i + 2], ecs[4 * i + 3]);
+    }
 
     // beta_t (V[t][j] - Ec[t][j]) for j in block ub, as 16-bit hi + lo in [j][t]
 #pragma unroll
@@ -421,8 +452,418 @@ hipError_t launch_dkata_fwd(const DKataArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-#define LINATT_DKATA_INST(T, D, DV, M) \
-  template hipError_t launch_dkata_fwd<T, D, DV, M>(const DKataArgs&, hipStream_t);
+// ===========================================================================
+// Backward (kata/spd/flash_delta.py:1084-1108, flash_delta_bwd :830-895).
+// With do' = do / (den + eps), z_t = <do'_t, o_t> (normalize) or do' = do,
+// z = 0, and X = diag(beta) dbV:
+//
+//   readout:  dA_qk[t,s] = <do'_t, U_s> - z_t (s <= t),  dU = lower(A_qk)^T do'
+//   solve:    dbV = (I + diag(beta) strict_lower(A_kk))^-T dU
+//   erase:    dA_kk[t,s] = -beta_t <dbV_t, U_s> (s < t)
+//   dv = beta dbV,  dbeta_t = <v_t - E_t, dbV_t>,  E_t = sum_{s<t} A_kk[t,s] U_s
+//
+// and dq, dk through kappa.  The readout part is the KATA sum-score backward
+// of (q, k, v := U) with den := 1 and o := the normalised output (or 0):
+// it then forms exactly scale^2 dA_qk and returns dq, the readout part of dk
+// and dU as its dv.  The erase part is the same backward run on queries
+// shifted by one token, q'_t = k_{t+1}, keys k, values U, dO'_t = -X_{t+1},
+// o := 0: its causal pairs s <= t are exactly the strict pairs s < t + 1 of
+// A_kk, its dq' is the query side (dk_{t+1} += dq'_t) and its dk the key
+// side.  The reverse solve walks the chunks backwards like dkata_U_kernel
+// walks them forwards.
+// ===========================================================================
+
+template <typename T>
+__global__ __launch_bounds__(256) void dkata_bwd_prep_kernel(DKataBwdArgs a, int D, int DV) {
+  const int64_t rows = (int64_t)a.B * a.T * a.H, n4 = rows * DV / 4;
+  const int64_t hrow = (int64_t)a.T * a.H;  // rows per batch entry
+  // k one token later (rows t < T - 1 of each batch entry), zero at T - 1;
+  // the last row of the shifted -X is zeroed here, the rest written by the
+  // reverse solve
+  T* ksh = (T*)(a.bws + a.BL.Ksh);
+  T* xn = (T*)(a.bws + a.BL.Xn);
+  const int64_t k4 = rows * D / 4;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < k4; i += (int64_t)gridDim.x * 256) {
+    const int64_t row = 4 * i / D, bt = row % hrow;  // (t, h) within the batch entry
+    if (bt < hrow - a.H) {
+      st4<T>(ksh + 4 * i, ld4<T>((const T*)a.k + 4 * i + (int64_t)a.H * D));
+    } else {
+      st4<T>(ksh + 4 * i, to4<T>(0.f, 0.f, 0.f, 0.f));
+      const int64_t col = 4 * i - row * D;  // zero the same row of xn, D and DV apart
+      for (int64_t c = col; c < DV; c += D) st4<T>(xn + row * DV + c, to4<T>(0.f, 0.f, 0.f, 0.f));
+    }
+  }
+  T* dop = (T*)(a.bws + a.BL.dOp);
+  T* o16 = (T*)(a.bws + a.BL.O16);
+  T* zo = (T*)(a.bws + a.BL.Zo);
+  float* ones = (float*)(a.bws + a.BL.ones);
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+    const int64_t row = 4 * i / DV;
+    const float f = a.normalize ? 1.f / (a.den[row] + a.eps) : 1.f;
+    const float4 g = reinterpret_cast<const float4*>(a.dout)[i];
+    st4<T>(dop + 4 * i, to4<T>(g.x * f, g.y * f, g.z * f, g.w * f));
+    if (a.normalize) {
+      const float4 o = reinterpret_cast<const float4*>(a.o)[i];
+      st4<T>(o16 + 4 * i, to4<T>(o.x, o.y, o.z, o.w));
+    } else {
+      st4<T>(o16 + 4 * i, to4<T>(0.f, 0.f, 0.f, 0.f));
+    }
+    st4<T>(zo + 4 * i, to4<T>(0.f, 0.f, 0.f, 0.f));
+    if ((4 * i) % DV == 0) ones[row] = 1.f;
+  }
+}
+
+// dbV = (I + diag(beta) strict_lower(A_kk))^-T dU, chunk after chunk from the
+// last: R_c = sum_{c' > c} A_kk[c, c'] X_c' (A_kk is symmetric), dbV_c =
+// Tm_c^T (dU_c - R_c), X_c = beta_c dbV_c.  Layout and schedule as
+// dkata_U_kernel with the chunk order reversed: wave w = (tb, ub), ring of
+// later chunks' K and X^T tiles, chunk c + 1's in Klast / Xlast.
+template <typename T, int D, int DV, int M>
+__global__ __launch_bounds__(256) void dkata_dbV_kernel(DKataBwdArgs a) {
+  constexpr int E = D / M, KE = E / 16, kRing = 5, TE = 64 * 64;
+  static_assert(D == 64 && DV == 64 && E % 16 == 0, "64-wide heads");
+  __shared__ __attribute__((aligned(16))) T ring[kRing][2][TE];  // K, X^T tiles of chunk c'
+  __shared__ __attribute__((aligned(16))) T Klast[TE];
+  __shared__ __attribute__((aligned(16))) T Xlast[TE];
+  __shared__ __attribute__((aligned(16))) T TmS[2][TE];
+  __shared__ __attribute__((aligned(16))) T Vh[TE];  // (dU - R)^T hi, [j][t]
+  __shared__ __attribute__((aligned(16))) T Vl[TE];
+  __shared__ __attribute__((aligned(16))) float Xc[4][16][64];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+  const int cl = lane & 31, hh = lane >> 5;
+  const int tb = w & 1, ub = w >> 1;
+  const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H;
+  const int Tn = a.T, NC = (Tn + 63) / 64, Tp = 64 * NC;
+  const int64_t rs = (int64_t)a.H * D, vrs = (int64_t)a.H * DV;
+  const T* kb = (const T*)a.k + ((int64_t)b * Tn * a.H + h) * D;
+  const T* dub = (const T*)(a.bws + a.BL.dU) + ((int64_t)b * Tn * a.H + h) * DV;
+  T* XT = (T*)(a.bws + a.BL.XT) + (size_t)bh * DV * Tp;  // [j][t]
+  const T* TmH = (const T*)(a.ws + a.L.TmHi) + (size_t)bh * NC * TE;
+  const T* TmL = (const T*)(a.ws + a.L.TmLo) + (size_t)bh * NC * TE;
+
+  auto issue_step = [&](int cp, int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      dma_tile64<T>(kb, rs, 64 * cp, Tn, ring[slot][0], 2 * w + i, lane);
+      dma_tile64<T>(XT + 64 * cp, Tp, 0, DV, ring[slot][1], 2 * w + i, lane);
+    }
+  };
+  auto issue_tm = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      dma_tile64<T>(TmH + (size_t)c * TE, 64, 0, 64, TmS[0], 2 * w + i, lane);
+      dma_tile64<T>(TmL + (size_t)c * TE, 64, 0, 64, TmS[1], 2 * w + i, lane);
+    }
+  };
+  auto load_chunk = [&](int c, v8_t<T>* kx, v4_t<T>* dx, float& bx) __attribute__((always_inline)) {
+    const int t = 64 * c + 32 * tb + cl;
+    const bool in = t < Tn;
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk)
+      kx[kk] = in ? ld8<T>(kb + (int64_t)t * rs + 16 * kk + 8 * hh) : zero8<T>();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dx[i] = in ? ld4<T>(dub + (int64_t)t * vrs + 32 * ub + 8 * i + 4 * hh) : v4_t<T>{};
+    bx = in ? a.beta[((int64_t)b * Tn + t) * a.H + h] : 0.f;
+  };
+  auto gram = [&](const T* Kt, const v8_t<T>* kc, v8_t<T>* bop) __attribute__((always_inline)) {
+    v8_t<T> ka[D / 16];
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) ka[kk] = tile_ld8<T>(Kt, 32 * ub + cl, 16 * kk + 8 * hh);
+    f32x16 At{};
+#pragma unroll
+    for (int g = 0; g < M; ++g)
+#pragma unroll
+      for (int g2 = 0; g2 < M; ++g2) {
+        f32x16 r{};
+#pragma unroll
+        for (int kk = 0; kk < KE; ++kk) r = mma(ka[g2 * KE + kk], kc[g * KE + kk], r);
+        At += r * r;
+      }
+    bop[0] = c_to_b<T>(At, 0);
+    bop[1] = c_to_b<T>(At, 1);
+  };
+  auto r_update = [&](const T* Xt, const v8_t<T>* bop, f32x16 (&ec)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+        ec[jb] = mma(tile_ldp8<T>(Xt, 32 * jb + cl, 32 * ub, ks, hh), bop[ks], ec[jb]);
+  };
+
+  v8_t<T> kc[D / 16];
+  v4_t<T> duc[4];
+  float bc;
+  load_chunk(NC - 1, kc, duc, bc);
+  issue_tm(NC - 1);
+
+  for (int c = NC - 1; c >= 0; --c) {
+    const int tl = 64 * c + 32 * tb + cl;
+    const int nring = NC - c - 2;  // ring steps: later chunks c + 2 .. NC - 1 (step s: c + 2 + s)
+    f32x16 ec[2] = {f32x16{}, f32x16{}};
+    if (c + 1 < NC) {
+      v8_t<T> bop[2];
+      if (nring > 0) vm_wait_barrier_n(4 * (min(kRing - 1, nring) - 1));
+      gram(nring > 0 ? ring[0][0] : Klast, kc, bop);
+      for (int s = 0; s < nring; ++s) {
+        if (s + 1 < nring) {
+          vm_wait_barrier_n(4 * min(2, nring - 2 - s));
+          if (s + kRing - 1 < nring) issue_step(c + 2 + s + kRing - 1, (s + kRing - 1) % kRing);
+        }
+        v8_t<T> bnext[2];
+        gram(s + 1 < nring ? ring[(s + 1) % kRing][0] : Klast, kc, bnext);
+        r_update(ring[s % kRing][1], bop, ec);
+        bop[0] = bnext[0];
+        bop[1] = bnext[1];
+      }
+      r_update(Xlast, bop, ec);
+    }
+
+    vm_wait_barrier<0>();
+    v8_t<T> kn[D / 16];
+    v4_t<T> dun[4];
+    float bn = 0.f;
+    if (c > 0) {
+      load_chunk(c - 1, kn, dun, bn);
+      // chunk c - 1's ring steps are later chunks c + 1 .. NC - 1, all stored
+      for (int s = 0; s < min(kRing - 1, NC - c - 1); ++s) issue_step(c + 1 + s, s);
+    }
+
+#pragma unroll
+    for (int e = 0; e < 16; ++e) Xc[w][e][lane] = ec[1 - ub][e];
+    if (ub == 0) {
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk)
+        *reinterpret_cast<v8_t<T>*>(reinterpret_cast<char*>(Klast) + tile_off(32 * tb + cl, 16 * kk + 8 * hh)) = kc[kk];
+    }
+    block_barrier();
+    const int partner = tb | ((1 - ub) << 1);
+    f32x16 ecs = ec[ub];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) ecs[e] = a.scale2 * (ecs[e] + Xc[partner][e][lane]);
+
+    // (dU - R)^T[j][t] for j in block ub, as 16-bit hi + lo
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int e = 4 * i + r, j = 32 * ub + 8 * i + 4 * hh + r;
+        const float x = (float)duc[i][r] - ecs[e];
+        const T xh = (T)x;
+        const int off = tile_off(j, (32 * tb + cl) & ~3);
+        reinterpret_cast<T*>(reinterpret_cast<char*>(Vh) + off)[cl & 3] = xh;
+        reinterpret_cast<T*>(reinterpret_cast<char*>(Vl) + off)[cl & 3] = (T)(x - (float)xh);
+      }
+    }
+    block_barrier();
+
+    // dbV^T[j][i] = sum_{t >= i} (dU - R)^T[j][t] Tm[t][i]  (j block ub, i block tb)
+    f32x16 uacc{};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (ks < 2 * tb) continue;  // Tm[t][i] = 0 for t < i
+      const v8_t<T> bh8 = tile_tr8<T>(TmS[0], 0, 32 * tb, ks, lane);
+      const v8_t<T> bl8 = tile_tr8<T>(TmS[1], 0, 32 * tb, ks, lane);
+      const v8_t<T> ah = tile_ldp8<T>(Vh, 32 * ub + cl, 0, ks, hh);
+      const v8_t<T> alo = tile_ldp8<T>(Vl, 32 * ub + cl, 0, ks, hh);
+      uacc = mma(ah, bh8, uacc);
+      uacc = mma(ah, bl8, uacc);
+      uacc = mma(alo, bh8, uacc);
+    }
+
+    // X = beta dbV: X^T for the earlier chunks (global, and Xlast for chunk
+    // c - 1); dbV (float32) and -X (the erase pass's dO), time-major
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int j = 32 * ub + 8 * (e >> 2) + 4 * hh + (e & 3);
+      const T x16 = (T)(bc * uacc[e]);
+      XT[(size_t)j * Tp + tl] = x16;
+      reinterpret_cast<T*>(reinterpret_cast<char*>(Xlast) + tile_off(j, (32 * tb + cl) & ~3))[cl & 3] = x16;
+    }
+    if (tl < Tn) {
+      const int64_t row = ((int64_t)b * Tn + tl) * a.H + h;
+      float* dbv = (float*)(a.bws + a.BL.dbV) + row * DV;
+      // -X_t goes to row t - 1 of the shifted erase dO
+      T* xn = tl > 0 ? (T*)(a.bws + a.BL.Xn) + (row - a.H) * DV : nullptr;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j0 = 32 * ub + 8 * i + 4 * hh;
+        *reinterpret_cast<float4*>(dbv + j0) =
+            make_float4(uacc[4 * i], uacc[4 * i + 1], uacc[4 * i + 2], uacc[4 * i + 3]);
+        if (xn)
+          st4<T>(xn + j0, to4<T>(-(float)(T)(bc * uacc[4 * i]), -(float)(T)(bc * uacc[4 * i + 1]),
+                                 -(float)(T)(bc * uacc[4 * i + 2]), -(float)(T)(bc * uacc[4 * i + 3])));
+      }
+    }
+    block_barrier();
+    if (c > 0) issue_tm(c - 1);
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) kc[kk] = kn[kk];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) duc[i] = dun[i];
+    bc = bn;
+  }
+}
+
+// Per (b, h, chunk), four waves (tb, ub) as in dkata_U_kernel:
+//   E_t = Ein_t + sum_{s<t in the chunk} kappa(k_t, k_s) U_s  (MFMA, the
+//         chunk's own Gram block masked strictly lower, U^T from the forward),
+//   dbeta_t = <v_t - E_t, dbV_t>,  dv_t = beta_t dbV_t,
+//   dk_t = readout part + key side of the erase pass + its query side one row
+//          earlier.
+template <typename T, int D, int DV, int M>
+__global__ __launch_bounds__(256) void dkata_bwd_fix_kernel(DKataBwdArgs a) {
+  constexpr int E = D / M, KE = E / 16, TE = 64 * 64;
+  static_assert(D == 64 && DV == 64 && E % 16 == 0, "64-wide heads");
+  __shared__ __attribute__((aligned(16))) T Ks[TE];   // K rows of the chunk
+  __shared__ __attribute__((aligned(16))) T UTs[TE];  // U^T [j][s] of the chunk
+  __shared__ __attribute__((aligned(16))) float Xc[4][16][64];
+  __shared__ float Db[2][64];                          // dbeta partials per j block
+
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+  const int cl = lane & 31, hh = lane >> 5;
+  const int tb = w & 1, ub = w >> 1;
+  const int Tn = a.T, NC = (Tn + 63) / 64, Tp = 64 * NC;
+  const int ci = blockIdx.x % NC, bh = blockIdx.x / NC, b = bh / a.H, h = bh % a.H;
+  const int t0 = 64 * ci;
+  const int64_t rs = (int64_t)a.H * D;
+  const T* kb = (const T*)a.k + ((int64_t)b * Tn * a.H + h) * D;
+  const T* UT = (const T*)(a.ws + a.L.UT) + (size_t)bh * DV * Tp;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    dma_tile64<T>(kb, rs, t0, Tn, Ks, 2 * w + i, lane);
+    dma_tile64<T>(UT + t0, Tp, 0, DV, UTs, 2 * w + i, lane);
+  }
+  const int tl = t0 + 32 * tb + cl;
+  v8_t<T> kc[D / 16];
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk)
+    kc[kk] = tl < Tn ? ld8<T>(kb + (int64_t)tl * rs + 16 * kk + 8 * hh) : zero8<T>();
+  // this lane's rows of everything else, loaded while the tiles land
+  const bool in = tl < Tn;
+  const int64_t row = ((int64_t)b * Tn + (in ? tl : t0)) * a.H + h;
+  float4 g4[4], e4[4];
+  v4_t<T> v4[4], x4[4], y4[4], z4[4];
+  const float bt = in ? a.beta[((int64_t)b * Tn + tl) * a.H + h] : 0.f;
+  {
+    const float* dbv = (const float*)(a.bws + a.BL.dbV) + row * DV;
+    const float* ein = (const float*)(a.ws + a.L.Ein) + row * DV;
+    const T* vr = (const T*)a.v + row * DV;
+    const T* dkr = (const T*)(a.bws + a.BL.dkr) + row * D;
+    const T* dke = (const T*)(a.bws + a.BL.dke) + row * D;
+    const T* dqe = (const T*)(a.bws + a.BL.dqe) + (row - a.H) * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j0 = 32 * ub + 8 * i + 4 * hh, d0 = 32 * ub + 16 * hh + 4 * i;
+      g4[i] = in ? *reinterpret_cast<const float4*>(dbv + j0) : make_float4(0.f, 0.f, 0.f, 0.f);
+      e4[i] = in ? *reinterpret_cast<const float4*>(ein + j0) : make_float4(0.f, 0.f, 0.f, 0.f);
+      v4[i] = in ? ld4<T>(vr + j0) : v4_t<T>{};
+      x4[i] = in ? ld4<T>(dkr + d0) : v4_t<T>{};
+      y4[i] = in ? ld4<T>(dke + d0) : v4_t<T>{};
+      z4[i] = in && tl > 0 ? ld4<T>(dqe + d0) : v4_t<T>{};
+    }
+  }
+  vm_wait_barrier<0>();
+
+  // A^T[s][t] / scale^2 for s in block ub, t in block tb, zero unless s < t
+  f32x16 At{};
+#pragma unroll
+  for (int g = 0; g < M; ++g)
+#pragma unroll
+    for (int g2 = 0; g2 < M; ++g2) {
+      f32x16 r{};
+#pragma unroll
+      for (int kk = 0; kk < KE; ++kk)
+        r = mma(tile_ld8<T>(Ks, 32 * ub + cl, g2 * E + 16 * kk + 8 * hh), kc[g * KE + kk], r);
+      At += r * r;
+    }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int s_ = 32 * ub + 8 * (e >> 2) + 4 * hh + (e & 3), t_ = 32 * tb + cl;
+    if (s_ >= t_) At[e] = 0.f;
+  }
+  f32x16 ec[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const v8_t<T> bop = c_to_b<T>(At, ks);
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+      ec[jb] = mma(tile_ldp8<T>(UTs, 32 * jb + cl, 32 * ub, ks, hh), bop, ec[jb]);
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) Xc[w][e][lane] = ec[1 - ub][e];
+  block_barrier();
+  const int partner = tb | ((1 - ub) << 1);
+  // dbeta partial over this wave's 32 value columns j (block ub); dv
+  float part = 0.f;
+  T* dvr = (T*)a.dv + row * DV;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int j0 = 32 * ub + 8 * i + 4 * hh;
+    const float gv[4] = {g4[i].x, g4[i].y, g4[i].z, g4[i].w};
+    const float ev[4] = {e4[i].x, e4[i].y, e4[i].z, e4[i].w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int e = 4 * i + r;
+      const float Et = ev[r] + a.scale2 * (ec[ub][e] + Xc[partner][e][lane]);
+      part += ((float)v4[i][r] - Et) * gv[r];
+    }
+    if (in) st4<T>(dvr + j0, to4<T>(bt * gv[0], bt * gv[1], bt * gv[2], bt * gv[3]));
+  }
+  part += __shfl_xor(part, 32);
+  if (hh == 0) Db[ub][32 * tb + cl] = part;
+  // dk: the wave's 32 tokens (tb) x half of the key dims (ub), 16 per lane
+  if (in) {
+    T* dko = (T*)a.dk + row * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d0 = 32 * ub + 16 * hh + 4 * i;
+      st4<T>(dko + d0, to4<T>((float)x4[i][0] + (float)y4[i][0] + (float)z4[i][0],
+                              (float)x4[i][1] + (float)y4[i][1] + (float)z4[i][1],
+                              (float)x4[i][2] + (float)y4[i][2] + (float)z4[i][2],
+                              (float)x4[i][3] + (float)y4[i][3] + (float)z4[i][3]));
+    }
+  }
+  block_barrier();
+  if (ub == 0 && hh == 0 && in) a.dbeta[((int64_t)b * Tn + tl) * a.H + h] = Db[0][32 * tb + cl] + Db[1][32 * tb + cl];
+}
+
+template <typename T, int D, int DV, int M>
+hipError_t launch_dkata_bwd(const DKataBwdArgs& a, hipStream_t stream) {
+  const int NC = (a.T + 63) / 64, BH = a.B * a.H;
+  const int64_t n4 = (int64_t)a.B * a.T * a.H * DV / 4;
+  const int blocks = (int)((n4 + 255) / 256 < 4096 ? (n4 + 255) / 256 : 4096);
+  dkata_bwd_prep_kernel<T><<<dim3(blocks), dim3(256), 0, stream>>>(a, D, DV);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const float* ones = (const float*)(a.bws + a.BL.ones);
+  // readout: KATA sum backward of (q, k, U), den := 1
+  KataArgs r{};
+  r.q = a.q; r.k = a.k; r.v = a.ws + a.L.Ub; r.o = a.bws + a.BL.O16; r.den = const_cast<float*>(ones);
+  r.dout = a.bws + a.BL.dOp; r.dq = a.dq; r.dk = a.bws + a.BL.dkr; r.dv = a.bws + a.BL.dU;
+  r.delta = (float*)(a.bws + a.BL.kws);
+  r.B = a.B; r.T = a.T; r.HQ = a.H; r.H = a.H; r.DK = D; r.DV = DV; r.M = M; r.scale = a.scale;
+  e = launch_kata_bwd<T, D, DV, M, true, false>(r, KATA_BWD_DQ | KATA_BWD_DKDV, stream);
+  if (e != hipSuccess) return e;
+  dkata_dbV_kernel<T, D, DV, M><<<dim3(BH), dim3(256), 0, stream>>>(a);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  // erase: KATA sum backward of (k shifted one token, k, U) with the shifted
+  // dO := -X, o := 0, den := 1
+  KataArgs x{};
+  x.q = a.bws + a.BL.Ksh; x.k = a.k; x.v = a.ws + a.L.Ub; x.o = a.bws + a.BL.Zo; x.den = const_cast<float*>(ones);
+  x.dout = a.bws + a.BL.Xn; x.dq = a.bws + a.BL.dqe; x.dk = a.bws + a.BL.dke; x.dv = a.bws + a.BL.dve;
+  x.delta = (float*)(a.bws + a.BL.kws);
+  x.B = a.B; x.T = a.T; x.HQ = a.H; x.H = a.H; x.DK = D; x.DV = DV; x.M = M; x.scale = a.scale;
+  e = launch_kata_bwd<T, D, DV, M, true, false>(x, KATA_BWD_DQ | KATA_BWD_DKDV, stream);
+  if (e != hipSuccess) return e;
+  dkata_bwd_fix_kernel<T, D, DV, M><<<dim3(BH * NC), dim3(256), 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+#define LINATT_DKATA_INST(T, D, DV, M)                                              \
+  template hipError_t launch_dkata_fwd<T, D, DV, M>(const DKataArgs&, hipStream_t); \
+  template hipError_t launch_dkata_bwd<T, D, DV, M>(const DKataBwdArgs&, hipStream_t);
 LINATT_DKATA_SHAPES(LINATT_DKATA_INST)
 
 }  // namespace linatt

@@ -118,9 +118,28 @@ struct DKataLayout {
   size_t UT;          // (B*H, DV, 64 NC) T: U^T
   size_t Ub;          // (B, T, H, DV) T: U for the readout
   size_t Ob;          // (B, T, H, DV) T: readout num / den
+  size_t Ein;         // (B, T, H, DV) f32: sum over earlier chunks of kappa(k_t, k_j) U_j
   size_t bytes;
 };
 DKataLayout dkata_layout(int B, int T, int H, int D, int DV, int eb);
+
+// Backward scratch of the SPD delta rule, after the forward's workspace.
+struct DKataBwdLayout {
+  size_t dOp;   // (B, T, H, DV) T: do' = do / (den + eps) (or do)
+  size_t O16;   // (B, T, H, DV) T: the normalised output (or zeros)
+  size_t Zo;    // (B, T, H, DV) T: zeros, the erase pass's o
+  size_t ones;  // (B, T, H) f32: 1, the KATA backward's den
+  size_t kws;   // KATA backward workspace
+  size_t dU;    // (B, T, H, DV) T: readout VJP, KATA backward's dv
+  size_t dkr;   // (B, T, H, D) T: readout part of dk
+  size_t Ksh;   // (B, T, H, D) T: k one token later (zero at T - 1), the erase pass's q
+  size_t Xn;    // (B, T, H, DV) T: -beta dbV one token later (zero at T - 1), its dO
+  size_t XT;    // (B*H, DV, 64 NC) T: (beta dbV)^T for the reverse solve
+  size_t dbV;   // (B, T, H, DV) f32
+  size_t dqe, dke, dve;  // erase pass outputs (T)
+  size_t bytes;
+};
+DKataBwdLayout dkata_bwd_layout(int B, int T, int H, int D, int DV, int eb);
 
 struct DKataArgs {
   const void* q;      // (B, T, H, D) time-major
@@ -135,7 +154,33 @@ struct DKataArgs {
   int B, T, H;
   float scale, scale2, eps;
   int normalize;
+  int keep_e;  // forward: also store Ein (for the backward)
 };
+
+struct DKataBwdArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* beta;
+  const float* U;     // (B, T, H, DV) f32 from the forward
+  const float* o;     // (B, T, H, DV) f32 forward output (normalize), else null
+  const float* den;   // (B, T, H) f32 from the forward
+  const float* dout;  // (B, T, H, DV) f32
+  void* dq;           // (B, T, H, D) T
+  void* dk;
+  void* dv;           // (B, T, H, DV) T
+  float* dbeta;       // (B, T, H) f32
+  char* ws;           // the forward's workspace (kept) ...
+  DKataLayout L;
+  char* bws;          // ... and the backward's
+  DKataBwdLayout BL;
+  int B, T, H;
+  float scale, scale2, eps;
+  int normalize;
+};
+
+template <typename T, int D, int DV, int M>
+hipError_t launch_dkata_bwd(const DKataBwdArgs& a, hipStream_t stream);
 
 template <typename T, int D, int DV, int M>
 hipError_t launch_dkata_fwd(const DKataArgs& a, hipStream_t stream);

@@ -14,8 +14,9 @@ With ``s = sqrt(scale)`` on q and k (``scale`` defaults to ``1 / E``,
   ``(B, T, H, DV)`` output.  The forward runs in ``liblinatt_hip.so``
   (``linatt_dkata_fwd``): a chunk-parallel solve of the 64-token diagonal
   blocks, a chunk-sequential MFMA pass for ``U`` and the KATA sum-score
-  forward for the readout.  Its backward is not implemented: calling it
-  raises.
+  forward for the readout.  The backward (``linatt_dkata_bwd``) runs the
+  KATA sum-score backward for the readout and for the erase terms around a
+  reverse chunk solve.
 * ``flash_delta_U`` (``:186-212``), ``flash_delta_readout`` (``:975-985``) and
   ``flash_delta_den`` (``:1049-1057``) return the forward's intermediates
   with the reference's signatures.
@@ -40,7 +41,7 @@ def _scale(D, M, scale):
     return 1.0 / (D // M) if scale is None else float(scale)
 
 
-def _run(q, k, v, beta, M, scale, normalize, eps, want_U):
+def _run(q, k, v, beta, M, scale, normalize, eps, want_U, train=False):
     _lib.require_device(q, k, v, beta)
     if not (q.dtype == k.dtype == v.dtype):
         raise TypeError("q, k, v must share a dtype")
@@ -60,31 +61,65 @@ def _run(q, k, v, beta, M, scale, normalize, eps, want_U):
             f"linatt_amd flash_delta: no kernel for {q.dtype}, D={D}, DV={DV}, M={M}")
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     beta = beta.float().contiguous()
-    U = torch.empty(B, T, H, DV, device=q.device, dtype=torch.float32) if want_U else None
+    U = (torch.empty(B, T, H, DV, device=q.device, dtype=torch.float32)
+         if want_U or train else None)
     o = torch.empty(B, T, H, DV, device=q.device, dtype=torch.float32)
     den = torch.empty(B, T, H, device=q.device, dtype=torch.float32)
     ws = torch.empty(L.linatt_dkata_workspace_bytes(B, T, H, D, DV, dt), device=q.device,
                      dtype=torch.uint8)
-    _lib.check("linatt_dkata_fwd", L.linatt_dkata_fwd(
+    fn = "linatt_dkata_fwd_train" if train else "linatt_dkata_fwd"
+    _lib.check(fn, getattr(L, fn)(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(beta), _lib.ptr(U), _lib.ptr(o),
         _lib.ptr(den), _lib.ptr(ws), B, T, H, D, DV, M, _scale(D, M, scale),
         1 if normalize else 0, float(eps), dt, _lib.stream_of(q)))
+    if train:
+        return o, U, den, ws, (q, k, v, beta)
     return o, U, den
 
 
 class _FlashDelta(torch.autograd.Function):
-    """Forward of ``_FlashDelta`` (``kata/spd/flash_delta.py:1060-1082``)."""
+    """``_FlashDelta`` (``kata/spd/flash_delta.py:1060-1108``): the forward keeps
+    U, the output, den and its workspace for the backward
+    (``linatt_dkata_fwd_train`` / ``linatt_dkata_bwd``)."""
 
     @staticmethod
     def forward(ctx, q, k, v, beta, M, scale, normalize, eps):
-        o, _, _ = _run(q, k, v, beta, M, scale, normalize, eps, False)
+        train = any(ctx.needs_input_grad[:4])
+        if train and q.dtype != torch.bfloat16:
+            raise NotImplementedError(
+                "linatt_amd flash_delta: the backward runs in bfloat16 only (the mixer calls "
+                "flash_delta with bf16 inputs, kata/layer.py:409-412)")
+        if not train:
+            o, _, _ = _run(q, k, v, beta, M, scale, normalize, eps, False)
+            return o
+        o, U, den, ws, (qc, kc, vc, bc) = _run(q, k, v, beta, M, scale, normalize, eps, False,
+                                                train=True)
+        ctx.save_for_backward(qc, kc, vc, bc, U, o, den, ws)
+        ctx.M, ctx.scale, ctx.normalize, ctx.eps = M, scale, normalize, eps
+        ctx.dtypes = (q.dtype, k.dtype, v.dtype, beta.dtype)
         return o
 
     @staticmethod
     def backward(ctx, do):
-        raise NotImplementedError(
-            "linatt_amd flash_delta: the backward (kata/spd/flash_delta.py:830-897) is not "
-            "implemented on the HIP path")
+        q, k, v, beta, U, o, den, ws = ctx.saved_tensors
+        B, T, H, D = q.shape
+        DV = v.shape[-1]
+        M = ctx.M
+        L = _lib.load()
+        dt = _lib.dtype_code(q.dtype)
+        do = do.float().contiguous()
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        dbeta = torch.empty(B, T, H, device=q.device, dtype=torch.float32)
+        bws = torch.empty(L.linatt_dkata_bwd_workspace_bytes(B, T, H, D, DV, dt),
+                          device=q.device, dtype=torch.uint8)
+        _lib.check("linatt_dkata_bwd", L.linatt_dkata_bwd(
+            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(beta), _lib.ptr(U),
+            _lib.ptr(o if ctx.normalize else None), _lib.ptr(den), _lib.ptr(do), _lib.ptr(dq),
+            _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dbeta), _lib.ptr(ws), _lib.ptr(bws),
+            B, T, H, D, DV, M, _scale(D, M, ctx.scale), 1 if ctx.normalize else 0,
+            float(ctx.eps), dt, _lib.stream_of(q)))
+        tq, tk, tv, tb = ctx.dtypes
+        return dq.to(tq), dk.to(tk), dv.to(tv), dbeta.to(tb), None, None, None, None
 
 
 def flash_delta(q, k, v, beta, M, scale=None, C=64, normalize=False, eps=1e-5):

@@ -21,10 +21,10 @@ Names rebound (only in modules that are importable; the rest are skipped):
 * the mixer's ``ShortConvolution`` and ``RMSNorm`` classes, which
   ``kata.layer`` imports from ``fla.modules`` (``kata/layer.py:20``); the
   rebinding must happen before the model is built;
-* the SPD delta rule's forward pieces ``flash_delta_U``,
-  ``flash_delta_readout`` and ``flash_delta_den`` in ``kata.spd.flash_delta``
-  (``flash_delta`` itself stays the reference's while its backward has no
-  HIP kernel here, so training through the mixer keeps working);
+* the SPD delta rule ``flash_delta`` (trainable, bf16 backward) and its
+  forward pieces ``flash_delta_U``, ``flash_delta_readout``,
+  ``flash_delta_den`` in ``kata.spd.flash_delta``, and ``flash_delta`` where
+  the mixer imports it (``kata/layer.py:36``);
 * fla's delta-rule ops where fla's layers bind them
   (``fla.layers.delta_net.chunk_delta_rule``,
   ``fla.layers.gated_deltanet.chunk_gated_delta_rule``) and where fla defines
@@ -52,7 +52,8 @@ TARGETS = (
     ("kata.layer", "ShortConvolution", "mixer", "ShortConvolution"),
     ("kata.layer", "RMSNorm", "mixer", "RMSNorm"),
     *(("kata.spd.flash_delta", name, "flash_delta", name)
-      for name in ("flash_delta_U", "flash_delta_readout", "flash_delta_den")),
+      for name in ("flash_delta", "flash_delta_U", "flash_delta_readout", "flash_delta_den")),
+    ("kata.layer", "flash_delta", "flash_delta", "flash_delta"),
     ("fla.layers.delta_net", "chunk_delta_rule", "delta_rule", "chunk_delta_rule"),
     ("fla.ops.delta_rule", "chunk_delta_rule", "delta_rule", "chunk_delta_rule"),
     ("fla.layers.gated_deltanet", "chunk_gated_delta_rule", "delta_rule", "chunk_gated_delta_rule"),

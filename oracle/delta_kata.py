@@ -97,3 +97,15 @@ def flash_delta_recurrent(q, k, v, beta, M, scale=None):
         S = S + kt[..., :, None] * u[..., None, :]
         outs.append(torch.einsum("bhp,bhpd->bhd", pq[:, t], S))
     return torch.stack(outs, 1), S
+
+
+def flash_delta_fwd_bwd(q, k, v, beta, M, do, scale=None, normalize=False, eps=1e-5):
+    """float64 ``o`` and the gradients ``dq, dk, dv, dbeta`` of ``<o, do>``
+    by autograd through :func:`flash_delta_fwd` (the reference's
+    ``_FlashDelta.backward``, ``flash_delta.py:1084-1108``, differentiates
+    the same function)."""
+    leaves = [t.detach().to(F64).requires_grad_(True) for t in (q, k, v, beta)]
+    with torch.enable_grad():
+        o = flash_delta_fwd(*leaves, M, scale, normalize, eps)[0]
+        grads = torch.autograd.grad((o * do.to(F64)).sum(), leaves)
+    return (o.detach(), *[g.detach() for g in grads])

@@ -42,7 +42,7 @@ def stub_reference(monkeypatch):
         "kata.parallel_kata_attn": _stub("kata.parallel_kata_attn", **{n: _orig("ref_" + n) for n in KATA_NAMES}),
         # the mixer binds a subset of the names (no backward entry points)
         "kata.layer": _stub("kata.layer", **{n: _orig("layer_" + n)
-                                              for n in KATA_NAMES[:5] + MIXER_NAMES}),
+                                              for n in KATA_NAMES[:5] + MIXER_NAMES + ("flash_delta",)}),
         "kata.spd": _stub("kata.spd"),
         "kata.spd.chunk_scan_cat": _stub("kata.spd.chunk_scan_cat", spd_chunk_scan_cat=_orig("ref_scan")),
         "kata.spd.flash_delta": _stub("kata.spd.flash_delta",
@@ -76,15 +76,14 @@ def test_patch_rebinds_every_name(stub_reference):
     from linatt_amd import flash_delta as fd, mixer
     for n in MIXER_NAMES:
         assert getattr(m["kata.layer"], n) is getattr(mixer, n)
-    for n in DELTA_KATA_NAMES[1:]:
+    for n in DELTA_KATA_NAMES:
         assert getattr(m["kata.spd.flash_delta"], n) is getattr(fd, n)
-    # no HIP backward yet: the trainable op stays the reference's
-    assert m["kata.spd.flash_delta"].flash_delta() == "ref_flash_delta"
+    assert m["kata.layer"].flash_delta is fd.flash_delta
     assert m["fla.layers.delta_net"].chunk_delta_rule is delta_rule.chunk_delta_rule
     assert m["fla.ops.delta_rule"].chunk_delta_rule is delta_rule.chunk_delta_rule
     assert m["fla.layers.gated_deltanet"].chunk_gated_delta_rule is delta_rule.chunk_gated_delta_rule
     assert m["fla.ops.gated_delta_rule"].chunk_gated_delta_rule is delta_rule.chunk_gated_delta_rule
-    assert len(done) == len(KATA_NAMES) + 5 + 5 + 3 + len(MIXER_NAMES)
+    assert len(done) == len(KATA_NAMES) + 5 + 5 + 4 + 1 + len(MIXER_NAMES)
 
 
 def test_patch_is_idempotent_and_restorable(stub_reference):

@@ -20,10 +20,14 @@ pytestmark = pytest.mark.gpu
 TOL = {torch.bfloat16: 2e-2, torch.float16: 1e-2}
 
 
-def mar(x, ref):
+def mar(x, ref, floor=0.0):
+    """max|x - ref| / max(max|ref|, floor).  The floor matters only where the
+    exact gradient nearly vanishes: a normalised output at T = 1 is
+    U_0 kappa / (kappa + eps), invariant to q and k up to eps, so dq and dk
+    are ~eps-sized there and would be measured against their own rounding."""
     x = x.detach().double().cpu()
     ref = ref.detach().double().cpu()
-    den = ref.abs().max().item()
+    den = max(ref.abs().max().item(), floor)
     return (x - ref).abs().max().item() / (den if den > 0 else 1.0)
 
 
@@ -153,12 +157,81 @@ def test_deterministic(F):
     assert torch.equal(a, b)
 
 
-def test_backward_raises(F):
-    q, k, v, beta = dev(*make(1, 64, 1, 64, 64, torch.bfloat16, 1))
-    q.requires_grad_(True)
-    o = F.flash_delta(q, k, v, beta, 1, scale=0.5)
-    with pytest.raises(NotImplementedError, match="backward"):
-        o.sum().backward()
+BWD_SHAPES = [(1, 1, 1), (2, 37, 2), (1, 129, 3), (2, 300, 2), (1, 700, 1)]
+
+
+@pytest.mark.parametrize("shape", BWD_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("normalize", [False, True], ids=["raw", "norm"])
+@pytest.mark.parametrize("scale,dtype", [(0.5, torch.bfloat16), (1.0, torch.bfloat16),
+                                         (None, torch.bfloat16)], ids=["s0.5", "s1", "sE"])
+def test_backward_parity(F, shape, M, normalize, scale, dtype):
+    """dq, dk, dv, dbeta of <o, do> against float64 autograd through the
+    oracle (the reference's _FlashDelta.backward differentiates the same
+    function, kata/spd/flash_delta.py:1084-1108)."""
+    B, T, H = shape
+    q, k, v, beta = make(B, T, H, 64, 64, dtype, 31 + T + M)
+    g = torch.Generator().manual_seed(5 + T)
+    do = torch.randn(B, T, H, 64, generator=g)
+    print(f"\nflash_delta bwd B={B} T={T} H={H} M={M} norm={normalize} scale={scale} {dtype}",
+          flush=True)
+    o_ref, dq_ref, dk_ref, dv_ref, db_ref = DK.flash_delta_fwd_bwd(q, k, v, beta, M, do, scale,
+                                                                  normalize)
+    qd, kd, vd, bd = (t.cuda().requires_grad_(True) for t in (q, k, v, beta))
+    o = F.flash_delta(qd, kd, vd, bd, M, scale=scale, normalize=normalize)
+    o.backward(do.cuda())
+    tol = TOL[dtype]
+    assert mar(o, o_ref) < tol, ("o", mar(o, o_ref))
+    # 10% of the natural scale of dq, dk for a normalised output,
+    # |do / (den + eps)| |v| / |q| (the output is a den-weighted average)
+    m = lambda t: t.abs().max().item()  # noqa: E731
+    if normalize:
+        den = DK.flash_delta_fwd(q, k, v, beta, M, scale)[3]
+        fl = 0.1 * m(do.double() / (den[..., None] + 1e-5)) * m(v.float()) / m(q.float())
+    else:
+        fl = 0.0
+    for name, got, ref in (("dq", qd.grad, dq_ref), ("dk", kd.grad, dk_ref),
+                           ("dv", vd.grad, dv_ref), ("dbeta", bd.grad, db_ref)):
+        assert got.dtype == (torch.float32 if name == "dbeta" else dtype)
+        e = mar(got, ref, fl if name in ("dq", "dk") else 0.0)
+        assert e < tol, (name, e)
+
+
+def test_backward_fp16_raises(F):
+    q, k, v, beta = make(1, 64, 1, 64, 64, torch.float16, 1)
+    qd = q.cuda().requires_grad_(True)
+    with pytest.raises(NotImplementedError, match="bfloat16"):
+        F.flash_delta(qd, k.cuda(), v.cuda(), beta.cuda(), 1)
+
+
+def test_backward_config_full_size(F):
+    """The kata_delta_m1_340m shape (H=16, T=2048, M=1, scale 0.5), three heads
+    against the oracle."""
+    B, T, H, M = 1, 2048, 16, 1
+    q, k, v, beta = make(B, T, H, 64, 64, torch.bfloat16, 13)
+    do = torch.randn(B, T, H, 64, generator=torch.Generator().manual_seed(14))
+    qd, kd, vd, bd = (t.cuda().requires_grad_(True) for t in (q, k, v, beta))
+    F.flash_delta(qd, kd, vd, bd, M, scale=0.5).backward(do.cuda())
+    for h in (0, 7, 15):
+        sl = lambda x: x[:, :, h:h + 1]  # noqa: E731
+        _, dq_ref, dk_ref, dv_ref, db_ref = DK.flash_delta_fwd_bwd(
+            sl(q), sl(k), sl(v), sl(beta), M, sl(do), 0.5)
+        for name, got, ref in (("dq", qd.grad, dq_ref), ("dk", kd.grad, dk_ref),
+                               ("dv", vd.grad, dv_ref), ("dbeta", bd.grad, db_ref)):
+            e = mar(sl(got), ref)
+            assert e < 2e-2, (name, h, e)
+
+
+def test_backward_deterministic(F):
+    q, k, v, beta = make(2, 500, 3, 64, 64, torch.bfloat16, 8)
+    do = torch.randn(2, 500, 3, 64, generator=torch.Generator().manual_seed(9)).cuda()
+    res = []
+    for _ in range(2):
+        qd, kd, vd, bd = (t.cuda().requires_grad_(True) for t in (q, k, v, beta))
+        F.flash_delta(qd, kd, vd, bd, 2, scale=0.5, normalize=True).backward(do)
+        res.append([t.grad.clone() for t in (qd, kd, vd, bd)])
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
 
 
 def test_unsupported_shape_raises(F):

@@ -91,3 +91,37 @@ def test_normalize_and_den():
     A = torch.tril(DK.kappa_gram(q, k, M))
     torch.testing.assert_close(den, A.sum(-1).permute(0, 2, 1))
     torch.testing.assert_close(o, num / (den[..., None] + 1e-3))
+
+
+def test_gradients_gradcheck():
+    """The oracle's autograd gradients (what the GPU backward is checked
+    against) agree with finite differences on a tiny case, normalised too."""
+    g = torch.Generator().manual_seed(4)
+    B, T, H, D, M = 1, 5, 1, 8, 2
+    q = torch.randn(B, T, H, D, generator=g, dtype=torch.float64) * 0.5
+    k = torch.randn(B, T, H, D, generator=g, dtype=torch.float64) * 0.5
+    v = torch.randn(B, T, H, 3, generator=g, dtype=torch.float64)
+    beta = torch.rand(B, T, H, generator=g, dtype=torch.float64)
+    for normalize in (False, True):
+        f = lambda *a: DK.flash_delta_fwd(*a, M, 0.7, normalize)[0]  # noqa: E731
+        ins = [t.clone().requires_grad_(True) for t in (q, k, v, beta)]
+        assert torch.autograd.gradcheck(f, ins, eps=1e-6, atol=1e-6)
+
+
+def test_dbeta_closed_form_at_beta_zero():
+    """beta = 0: U = 0 and o = 0, so dq = dk = dv = 0 and, with dbV = dU =
+    lower(A_qk)^T do, dbeta_t = <v_t, sum_{s >= t} A_qk[s, t] do_s>."""
+    g = torch.Generator().manual_seed(6)
+    B, T, H, D, M = 2, 9, 2, 8, 2
+    q, k = (torch.randn(B, T, H, D, generator=g, dtype=torch.float64) for _ in range(2))
+    v, do = (torch.randn(B, T, H, 4, generator=g, dtype=torch.float64) for _ in range(2))
+    beta = torch.zeros(B, T, H, dtype=torch.float64)
+    o, dq, dk, dv, db = DK.flash_delta_fwd_bwd(q, k, v, beta, M, do, 0.5)
+    assert o.abs().max() == 0 and dq.abs().max() == 0 and dk.abs().max() == 0
+    Aqk = torch.tril(DK.kappa_gram(q, k, M, 0.5))                  # (B, H, T, T)
+    dU = torch.einsum("bhts,bthd->bshd", Aqk, do)
+    assert torch.allclose(dv, beta[..., None] * dU)
+    assert torch.allclose(db, (v * dU).sum(-1), atol=1e-12)
+    # and the mistake of dropping the transpose fails
+    wrong = torch.einsum("bhst,bthd->bshd", Aqk, do)
+    assert not torch.allclose(db, (v * wrong).sum(-1), atol=1e-6)
