@@ -290,6 +290,15 @@ int linatt_short_conv_bwd(const void* x, const float* weight, const float* bias,
                           float* dbias, void* workspace, int B, int T, int C, int W,
                           int activation, int dtype, void* stream);
 
+/* Rotary position embedding, replacing fla.modules.RotaryEmbedding as the
+ * mixer uses it (kata/layer.py:130-148, 352-372): x, y (B,T,H,D) [dtype]
+ * (y may equal x); pair p of the first rot_dim dims -- (2p, 2p+1) if
+ * interleaved, else (p, p + rot_dim/2) -- is rotated by the angle
+ * (t + offset) * base^(-2p/rot_dim) computed in fp32; inverse != 0 rotates
+ * the other way (the backward).  Dims past rot_dim are copied. */
+int linatt_rope(const void* x, void* y, int B, int T, int H, int D, int rot_dim, float base,
+                int offset, int interleaved, int inverse, int dtype, void* stream);
+
 /* RMSNorm over the last dim of a contiguous (n, d) array, fp32 arithmetic,
  * replacing fla.modules.RMSNorm as the mixer uses it (output norm
  * kata/layer.py:199-205, 539; q/k norm :126-128, 347):

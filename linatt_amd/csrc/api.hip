@@ -452,6 +452,25 @@ int linatt_short_conv_bwd(const void* x, const float* weight, const float* bias,
   return LINATT_OK;
 }
 
+int linatt_rope(const void* x, void* y, int B, int T, int H, int D, int rot_dim, float base,
+                int offset, int interleaved, int inverse, int dtype, void* stream) {
+  g_last_error.clear();
+  const char* fn = "linatt_rope";
+  if (B <= 0 || T <= 0 || H <= 0 || D <= 0) return fail(LINATT_EINVAL, std::string(fn) + ": non-positive size");
+  if (rot_dim <= 0 || rot_dim > D || rot_dim % 2 || (D - rot_dim) % 2)
+    return fail(LINATT_EINVAL, std::string(fn) + ": rot_dim must be even, positive and at most D (D - rot_dim even)");
+  if (!(base > 1.f)) return fail(LINATT_EINVAL, std::string(fn) + ": base must be > 1");
+  if (offset < 0) return fail(LINATT_EINVAL, std::string(fn) + ": offset must be >= 0");
+  if (!known_dtype(dtype)) return fail(LINATT_EINVAL, std::string(fn) + ": unknown dtype");
+  if (!x || !y) return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  hipError_t e = by_dtype(dtype, [&](auto t) {
+    return launch_rope<decltype(t)>(x, y, B, T, H, D, rot_dim, base, offset, interleaved ? 1 : 0,
+                                    inverse ? 1 : 0, (hipStream_t)stream);
+  });
+  if (e != hipSuccess) return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
 static int check_rms(const char* fn, int n, int d, int dtype) {
   if (n <= 0 || d <= 0) return fail(LINATT_EINVAL, std::string(fn) + ": non-positive size");
   if (d % 8 || !pow2(d / 8) || d > 512)

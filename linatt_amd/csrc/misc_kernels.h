@@ -41,6 +41,11 @@ hipError_t launch_rmsnorm(const void* x, const float* w, const float* rstd_in, c
                           float eps, bool bwd, hipStream_t stream);
 int rmsnorm_bwd_blocks(int n, int d);
 
+// Rotary position embedding over (B, T, H, D) rows (mixer.hip).
+template <typename T>
+hipError_t launch_rope(const void* x, void* y, int B, int T_, int H, int D, int rot_dim, float base,
+                       int offset, int interleaved, int inverse, hipStream_t stream);
+
 // Sets the calling thread's linatt_last_error() message and returns code
 // (defined with the C-ABI entry points in api.hip).
 int set_last_error(int code, const char* msg);

@@ -18,6 +18,8 @@
 // dz[s + W - 1 - w], and per-lane partial sums of dweight and dbias that a
 // second kernel adds up in a fixed order.
 //
+// Rotary position embedding: see rope_kernel.
+//
 // RMSNorm over rows of d (fp32 arithmetic): y = x r w, r = (mean x^2 + eps)^-1/2;
 // backward dx = r (g - xh mean(g xh)), g = dy w, xh = x r; dw = sum_rows dy xh.
 // d / 8 lanes own a row (16 bytes each).
@@ -418,6 +420,62 @@ hipError_t launch_rmsnorm(const void* x, const float* w, const float* rstd_in, c
   colsum_kernel<<<dim3((d + 31) / 32), dim3(1024), 0, stream>>>(part, dw, nbb, d);
   return hipGetLastError();
 }
+
+// ---------------------------------------------------------------------------
+// Rotary position embedding (fla.modules.RotaryEmbedding as the mixer uses
+// it, kata/layer.py:130-148, 352-372): pair p of the first rot_dim dims of
+// each (B, T, H, D) row -- (2p, 2p + 1) interleaved, (p, p + rot_dim / 2)
+// otherwise -- is rotated by the angle (t + offset) base^(-2p / rot_dim),
+// in fp32; inverse = 1 rotates by minus that angle (the backward).  Dims past
+// rot_dim pass through.  One thread per pair.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void rope_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                   int64_t rows, int T_, int H, int D,
+                                                   int rot_dim, float log2_base, int offset,
+                                                   int interleaved, float sign) {
+  const int half = rot_dim / 2, npass = (D - rot_dim) / 2;
+  const int per_row = half + npass;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * per_row) return;
+  const int64_t row = i / per_row;
+  const int p = (int)(i % per_row);
+  const T* xr = x + row * D;
+  T* yr = y + row * D;
+  if (p >= half) {  // two pass-through dims past rot_dim
+    const int d = rot_dim + 2 * (p - half);
+    yr[d] = xr[d];
+    yr[d + 1] = xr[d + 1];
+    return;
+  }
+  const int t = (int)((row / H) % T_) + offset;
+  const float inv_freq = exp2f(-(2.f * p / rot_dim) * log2_base);
+  float sn, cs;
+  sincosf((float)t * inv_freq, &sn, &cs);
+  sn *= sign;
+  const int d0 = interleaved ? 2 * p : p, d1 = interleaved ? 2 * p + 1 : p + half;
+  const float a = (float)xr[d0], b = (float)xr[d1];
+  yr[d0] = (T)(a * cs - b * sn);
+  yr[d1] = (T)(a * sn + b * cs);
+}
+
+template <typename T>
+hipError_t launch_rope(const void* x, void* y, int B, int T_, int H, int D, int rot_dim,
+                       float base, int offset, int interleaved, int inverse, hipStream_t stream) {
+  const int64_t rows = (int64_t)B * T_ * H;
+  const int64_t n = rows * (rot_dim / 2 + (D - rot_dim) / 2);
+  rope_kernel<T><<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream>>>(
+      (const T*)x, (T*)y, rows, T_, H, D, rot_dim, log2f(base), offset, interleaved,
+      inverse ? -1.f : 1.f);
+  return hipGetLastError();
+}
+
+template hipError_t launch_rope<__bf16>(const void*, void*, int, int, int, int, int, float, int, int,
+                                        int, hipStream_t);
+template hipError_t launch_rope<_Float16>(const void*, void*, int, int, int, int, int, float, int,
+                                          int, int, hipStream_t);
+template hipError_t launch_rope<float>(const void*, void*, int, int, int, int, int, float, int, int,
+                                       int, hipStream_t);
 
 template hipError_t launch_short_conv<__bf16>(const ConvArgs&, int, bool, hipStream_t);
 template hipError_t launch_short_conv<_Float16>(const ConvArgs&, int, bool, hipStream_t);

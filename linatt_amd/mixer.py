@@ -16,7 +16,10 @@ and shapes (so checkpoints load) and call contract, running on
   W inputs, newest last (``linatt_short_conv_fwd`` / ``_bwd``);
 * ``RMSNorm(hidden_size, elementwise_affine=True, eps=1e-5)`` over the last
   dim, fp32 arithmetic, output in the input's dtype (``linatt_rmsnorm_fwd`` /
-  ``_bwd``).
+  ``_bwd``);
+* ``RotaryEmbedding(dim, base=10000.0, interleaved=False)``:
+  ``forward(q, k, seqlen_offset=0)`` returns the rotated ``(q, k)``
+  (``linatt_rope``; the backward is the inverse rotation).
 
 Both have autograd backwards.  The q/k/v projections and ``o_proj`` stay
 library GEMMs.  Unsupported arguments (fla's ``residual``, ``mask``,
@@ -34,7 +37,7 @@ from . import _lib
 
 _lib.load()
 
-__all__ = ["short_conv", "rms_norm", "ShortConvolution", "RMSNorm"]
+__all__ = ["short_conv", "rms_norm", "rotary", "ShortConvolution", "RMSNorm", "RotaryEmbedding"]
 
 _ACT = {None: 0, "identity": 0, "silu": 1, "swish": 1}
 
@@ -199,3 +202,59 @@ class RMSNorm(nn.Module):
         if x.shape[-1] != self.hidden_size:
             raise ValueError(f"last dim {x.shape[-1]} != hidden_size {self.hidden_size}")
         return rms_norm(x, self.weight, self.eps)
+
+
+class _RopeFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, rot_dim, base, offset, interleaved):
+        _lib.require_device(x)
+        if x.dim() != 4:
+            raise ValueError(f"x must be (B, T, H, D), got {tuple(x.shape)}")
+        x = x.contiguous()
+        y = torch.empty_like(x)
+        ctx.args = (rot_dim, base, offset, interleaved)
+        _rope(x, y, rot_dim, base, offset, interleaved, False)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        dy = dy.contiguous()
+        dx = torch.empty_like(dy)
+        _rope(dy, dx, *ctx.args, True)
+        return dx, None, None, None, None
+
+
+def _rope(x, y, rot_dim, base, offset, interleaved, inverse):
+    B, T, H, D = x.shape
+    L = _lib.load()
+    _lib.check("linatt_rope", L.linatt_rope(
+        _lib.ptr(x), _lib.ptr(y), B, T, H, D, rot_dim, float(base), int(offset),
+        1 if interleaved else 0, 1 if inverse else 0, _lib.dtype_code(x.dtype),
+        _lib.stream_of(x)))
+
+
+def rotary(x, rot_dim=None, base=10000.0, offset=0, interleaved=False):
+    """Rotary position embedding of ``x (B, T, H, D)`` over its first
+    ``rot_dim`` dims (default all), positions ``offset .. offset + T - 1``."""
+    return _RopeFn.apply(x, x.shape[-1] if rot_dim is None else int(rot_dim), base, offset,
+                         interleaved)
+
+
+class RotaryEmbedding(nn.Module):
+    """Drop-in for ``fla.modules.RotaryEmbedding`` as ``kata/layer.py:130-148``
+    builds it and ``:352-372`` calls it: ``forward(q, k, seqlen_offset=0,
+    max_seqlen=None)`` on ``(B, T, H, D)`` tensors."""
+
+    def __init__(self, dim, base=10000.0, scale_base=None, interleaved=False,
+                 pos_idx_in_fp32=True, device=None):
+        super().__init__()
+        if scale_base is not None:
+            raise NotImplementedError("linatt_amd RotaryEmbedding: scale_base (xPos) is not supported")
+        self.dim, self.base, self.interleaved = int(dim), float(base), bool(interleaved)
+
+    def forward(self, q, k, seqlen_offset=0, max_seqlen=None, cu_seqlens=None, **kwargs):
+        if cu_seqlens is not None or kwargs or isinstance(seqlen_offset, torch.Tensor):
+            raise NotImplementedError("linatt_amd RotaryEmbedding: cu_seqlens, per-sequence "
+                                      "offsets and other options are not supported")
+        return (rotary(q, self.dim, self.base, seqlen_offset, self.interleaved),
+                rotary(k, self.dim, self.base, seqlen_offset, self.interleaved))

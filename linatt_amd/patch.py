@@ -18,7 +18,7 @@ Names rebound (only in modules that are importable; the rest are skipped):
   (``kata/layer.py:29-37``), so rebinding the defining module alone would not
   reach the mixer;
 * ``kata.spd.chunk_scan_cat.spd_chunk_scan_cat``;
-* the mixer's ``ShortConvolution`` and ``RMSNorm`` classes, which
+* the mixer's ``ShortConvolution``, ``RMSNorm`` and ``RotaryEmbedding`` classes, which
   ``kata.layer`` imports from ``fla.modules`` (``kata/layer.py:20``); the
   rebinding must happen before the model is built;
 * the SPD delta rule ``flash_delta`` (trainable, bf16 backward) and its
@@ -51,6 +51,7 @@ TARGETS = (
     ("kata.spd.chunk_scan_cat", "spd_chunk_scan_cat", "spd_state", "spd_chunk_scan_cat"),
     ("kata.layer", "ShortConvolution", "mixer", "ShortConvolution"),
     ("kata.layer", "RMSNorm", "mixer", "RMSNorm"),
+    ("kata.layer", "RotaryEmbedding", "mixer", "RotaryEmbedding"),
     *(("kata.spd.flash_delta", name, "flash_delta", name)
       for name in ("flash_delta", "flash_delta_U", "flash_delta_readout", "flash_delta_den")),
     ("kata.layer", "flash_delta", "flash_delta", "flash_delta"),

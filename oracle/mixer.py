@@ -15,6 +15,9 @@ here; they are restated from their published definitions:
   followed by SiLU; its decode cache holds the last W inputs, newest last.
 * RMSNorm(hidden_size, elementwise_affine, eps) is
   ``x / sqrt(mean(x^2) + eps) * weight`` in fp32.
+* RotaryEmbedding(dim, base, interleaved) rotates pair p of the first
+  ``dim`` dims of every head -- (2p, 2p + 1) interleaved (GPT-J), (p,
+  p + dim / 2) otherwise (GPT-NeoX) -- by ``(t + offset) * base^(-2p / dim)``.
 
 Parity against fla itself is unpinned (fla is absent and the reference holds
 no outputs of these modules); the tests pin this restatement against a
@@ -92,3 +95,23 @@ def fwd_bwd(fn, inputs, dy, **kw):
         grads = torch.autograd.grad((y * dy.to(F64)).sum(), [t for t in leaves if t is not None])
     it = iter(grads)
     return y.detach(), [next(it) if t is not None else None for t in leaves]
+
+
+def rope(x, rot_dim, base=10000.0, offset=0, interleaved=False, inverse=False):
+    """``x (B, T, H, D)`` rotated as fla's RotaryEmbedding does, float64."""
+    x = x.to(F64)
+    B, T, H, D = x.shape
+    half = rot_dim // 2
+    p = torch.arange(half, dtype=F64)
+    inv_freq = base ** (-2.0 * p / rot_dim)
+    ang = (torch.arange(T, dtype=F64) + offset)[:, None] * inv_freq[None, :]   # (T, half)
+    cs, sn = torch.cos(ang)[None, :, None, :], torch.sin(ang)[None, :, None, :]
+    if inverse:
+        sn = -sn
+    y = x.clone()
+    i0 = 2 * p.long() if interleaved else p.long()
+    i1 = i0 + 1 if interleaved else p.long() + half
+    a, b = x[..., i0], x[..., i1]
+    y[..., i0] = a * cs - b * sn
+    y[..., i1] = a * sn + b * cs
+    return y

@@ -25,7 +25,7 @@ def _orig(tag):
     return f
 
 
-MIXER_NAMES = ("ShortConvolution", "RMSNorm")
+MIXER_NAMES = ("ShortConvolution", "RMSNorm", "RotaryEmbedding")
 DELTA_KATA_NAMES = ("flash_delta", "flash_delta_U", "flash_delta_readout", "flash_delta_den")
 KATA_NAMES = ("parallel_kata_attn", "parallel_kata_attn_fwd", "parallel_kata_attn_sum",
               "parallel_kata_attn_sum_fwd_impl", "parallel_kata_attn_decay",

@@ -1,5 +1,6 @@
-"""GPU parity of the mixer's short convolution and RMSNorm
-(``linatt_amd.mixer``, C ABI ``linatt_short_conv_*`` / ``linatt_rmsnorm_*``)
+"""GPU parity of the mixer's short convolution, RMSNorm and rotary embedding
+(``linatt_amd.mixer``, C ABI ``linatt_short_conv_*`` / ``linatt_rmsnorm_*`` /
+``linatt_rope``)
 against the float64 oracle ``oracle/mixer.py`` (forward and float64 autograd
 gradients).  Inputs are drawn on the CPU, rounded once to the test dtype and
 shared by both sides.  Metric ``max|x - ref| / max|ref|``; bars: float32
@@ -156,3 +157,36 @@ def test_repeat_runs_identical(MX):
     for r in res[1:]:
         for a, b in zip(r, res[0]):
             assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("interleaved", [True, False], ids=["gptj", "neox"])
+@pytest.mark.parametrize("dtype", DT, ids=["bf16", "f16", "f32"])
+@pytest.mark.parametrize("shape,rot,offset", [((2, 300, 12, 64), 64, 0), ((1, 17, 3, 64), 48, 5),
+                                              ((2, 50, 8, 16), 16, 2040)],
+                         ids=["full", "partial", "group-late"])
+def test_rope_parity(MX, interleaved, dtype, shape, rot, offset):
+    """fwd against the float64 oracle; bwd = the inverse rotation of dy (the
+    rotation is orthogonal), checked against float64 autograd."""
+    g = torch.Generator().manual_seed(rot + offset)
+    x = torch.randn(*shape, generator=g).to(dtype)
+    dy = torch.randn(*shape, generator=g).to(dtype)
+    y_ref, grads = X.fwd_bwd(lambda xx: X.rope(xx, rot, 10000.0, offset, interleaved), [x], dy)
+    xd = x.cuda().requires_grad_(True)
+    y = MX.rotary(xd, rot, 10000.0, offset, interleaved)
+    y.backward(dy.cuda())
+    # fp32: the angle (t + offset) * inv_freq is formed in fp32, as fla forms it
+    # (pos_idx_in_fp32), so positions near 2048 carry ~1e-4 rad: the 1e-4 bar
+    tol = 1e-4 if dtype == torch.float32 else TOL[dtype]
+    assert mar(y, y_ref) < tol and mar(xd.grad, grads[0]) < tol
+
+
+def test_rope_module_decode_offset(MX):
+    """Decode through the module: token t with seqlen_offset t equals row t of
+    the full-sequence rotation."""
+    m = MX.RotaryEmbedding(64, base=10000.0, interleaved=True)
+    q = torch.randn(1, 40, 4, 64, device="cuda").bfloat16()
+    k = torch.randn(1, 40, 4, 64, device="cuda").bfloat16()
+    qf, kf = m(q, k)
+    for t in (0, 17, 39):
+        qt, kt = m(q[:, t:t + 1], k[:, t:t + 1], seqlen_offset=t)
+        assert torch.equal(qt, qf[:, t:t + 1]) and torch.equal(kt, kf[:, t:t + 1])

@@ -75,3 +75,34 @@ def test_rmsnorm_closed_forms():
     # a constant row maps to sign * sqrt(c^2 / (c^2 + eps))
     c = torch.full((1, 64), -0.01, dtype=torch.float64)
     assert torch.allclose(X.rmsnorm(c, None, eps), -torch.full_like(c, (1e-4 / (1e-4 + eps)) ** 0.5))
+
+
+@pytest.mark.parametrize("interleaved", [True, False])
+def test_rope_relative_position(interleaved):
+    """<R_t q, R_s k> depends on t - s only (per rotated pair), rotation keeps
+    norms, the inverse undoes it, and dims past rot_dim pass through."""
+    g = torch.Generator().manual_seed(2)
+    D, rot = 16, 12
+    q = torch.randn(1, 1, 1, D, generator=g, dtype=torch.float64).expand(1, 9, 1, D).contiguous()
+    k = torch.randn(1, 1, 1, D, generator=g, dtype=torch.float64).expand(1, 9, 1, D).contiguous()
+    rq, rk = X.rope(q, rot, 500.0, 0, interleaved), X.rope(k, rot, 500.0, 0, interleaved)
+    dots = torch.einsum("btd,bsd->bts", rq[:, :, 0], rk[:, :, 0])
+    for dlt in range(-3, 4):
+        diag = torch.diagonal(dots, offset=dlt, dim1=1, dim2=2)
+        assert torch.allclose(diag, diag[:, :1].expand_as(diag), atol=1e-12)
+    assert torch.allclose(rq.norm(dim=-1), q.norm(dim=-1), atol=1e-12)
+    assert torch.equal(rq[..., rot:], q[..., rot:])
+    assert torch.allclose(X.rope(rq, rot, 500.0, 0, interleaved, inverse=True), q, atol=1e-12)
+    # an offset is a shift in time
+    assert torch.allclose(X.rope(q[:, 3:], rot, 500.0, 3, interleaved), rq[:, 3:], atol=1e-12)
+
+
+def test_rope_layouts_are_a_permutation():
+    """Interleaved pairs (2p, 2p+1) are the half-split pairs (p, p + D/2)
+    after the matching permutation of the dims."""
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 5, 3, 8, generator=g, dtype=torch.float64)
+    perm = torch.tensor([0, 4, 1, 5, 2, 6, 3, 7])  # interleaved dim -> half-split dim
+    a = X.rope(x, 8, 100.0, 2, interleaved=True)
+    b = X.rope(x[..., perm.argsort()], 8, 100.0, 2, interleaved=False)[..., perm]
+    assert torch.allclose(a, b, atol=1e-12)
