@@ -99,9 +99,10 @@ DELTA_FWD_STAGES = (("prep", 1), ("state_fwd", 2), ("out", 4))
 DELTA_BWD_STAGES = (("state_bwd", 1), ("bwd_chunk", 2))
 
 
-def bench_delta(gated, steps, warmup, settle_s):
+def bench_delta(gated, steps, warmup, settle_s, H=6, K=128):
     """BASELINE config 3 (DeltaNet) / 4 (GatedDeltaNet): B8 H6 T2048 K=V=128
-    bf16, chunk 64, fwd + bwd through the C ABI with preallocated outputs,
+    (or the given H, K = V) bf16, chunk 64, fwd + bwd through the C ABI with
+    preallocated outputs,
     context and workspace.  Each kernel is launched on its own
     (linatt_delta_fwd_stages / linatt_delta_bwd_stages, which together make
     exactly the launches of linatt_delta_fwd + linatt_delta_bwd) between HIP
@@ -109,7 +110,7 @@ def bench_delta(gated, steps, warmup, settle_s):
     import torch
     from linatt_amd import _lib
     L = _lib.load()
-    B, H, T, K, V = 8, 6, 2048, 128, 128
+    B, T, V = 8, 2048, K
     seed = 3 if gated else 2
     q, k, v, beta, g, h0, do = delta_inputs(B, H, T, K, V, gated, seed)
     dev = torch.device("cuda", 0)
@@ -681,8 +682,13 @@ def main():
     delta = None
     if not args.no_delta:
         st = args.settle_seconds / 2
-        delta = {"deltanet_config3": bench_delta(False, max(3, args.steps // 2), 2, st),
-                 "gated_deltanet_config4": bench_delta(True, max(3, args.steps // 2), 2, st)}
+        ds = max(3, args.steps // 2)
+        delta = {"deltanet_config3": bench_delta(False, ds, 2, st),
+                 "gated_deltanet_config4": bench_delta(True, ds, 2, st),
+                 # the 200M models' own shape (configs/model/200m/gated_deltanet_200m.yaml:
+                 # 12 heads of 64) and the north star's B8 H12 T2048 D64
+                 "deltanet_h12_d64": bench_delta(False, ds, 2, st / 2, H=12, K=64),
+                 "gated_deltanet_h12_d64": bench_delta(True, ds, 2, st / 2, H=12, K=64)}
 
     state = None
     if not args.no_state:
