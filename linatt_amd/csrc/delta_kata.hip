@@ -33,6 +33,7 @@ namespace linatt {
 
 namespace {
 inline size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
+constexpr int kDkataSB = 8;  // chunks per super-chunk of the sequential passes
 }  // namespace
 
 DKataLayout dkata_layout(int B, int T, int H, int D, int DV, int eb) {
@@ -181,30 +182,29 @@ __global__ __launch_bounds__(256) void dkata_prep_kernel(DKataArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 2: the pseudo-values U, chunk after chunk, one workgroup per (b, h).
-// Wave w = (tb, ub): tb = w & 1 is its 32-row block of the current chunk's
-// tokens t, ub = w >> 1 its 32-row block of each earlier chunk's tokens u
-// (for Ec) and, afterwards, its 32-column block of U.
+// Kernel 2: the pseudo-values U, chunk after chunk over one super-chunk of
+// at most kDkataSB chunks [cb, ce), one workgroup per (b, h).  The chunks
+// before cb enter through Ein (dkata_ext_kernel).  Wave w = (tb, ub): tb =
+// w & 1 is its 32-row block of the current chunk's tokens t, ub = w >> 1 its
+// 32-row block of each earlier chunk's tokens u (for Ec) and, afterwards,
+// its 32-column block of U.
 //
-// Every operand of the Ec products comes from LDS.  The K and U^T tiles of
-// the earlier chunks c' <= c - 2 stream through a ring of kRing slots by
-// direct global->LDS copies issued kRing - 1 steps ahead (the first ones
-// during the previous chunk's epilogue); chunk c - 1's K and U^T, which the
-// previous epilogue has just produced, stay in LDS (Klast, Ulast).  Tm of
-// the chunk is copied in while its Ec loop runs, and the next chunk's key
-// rows, values and betas are loaded into registers during the epilogue.
+// The super-chunk's K and U^T tiles stay in LDS once their chunk is done
+// (Ks, Us: 2 x 8 x 8 KB), so the Ec steps read only LDS and wait on no copy.
+// The next chunk's key rows, values, beta and Tm operands are loaded into
+// registers while the current chunk runs.
 // ---------------------------------------------------------------------------
 template <typename T, int D, int DV, int M>
-__global__ __launch_bounds__(256) void dkata_U_kernel(DKataArgs a) {
-  constexpr int E = D / M, KE = E / 16, kRing = 5, TE = 64 * 64;
+__global__ __launch_bounds__(256) void dkata_U_kernel(DKataArgs a, int cb, int ce) {
+  constexpr int E = D / M, KE = E / 16, TE = 64 * 64;
   static_assert(D == 64 && DV == 64 && E % 16 == 0, "64-wide heads");
-  __shared__ __attribute__((aligned(16))) T ring[kRing][2][TE];  // K, U^T tiles of chunk c'
-  __shared__ __attribute__((aligned(16))) T Klast[TE];           // K of chunk c - 1, [u][d]
-  __shared__ __attribute__((aligned(16))) T Ulast[TE];           // U^T of chunk c - 1, [j][u]
-  __shared__ __attribute__((aligned(16))) T TmS[2][TE];          // Tm hi / lo of the chunk
-  __shared__ __attribute__((aligned(16))) T Vh[TE];              // (beta (V - Ec))^T hi, [j][u]
-  __shared__ __attribute__((aligned(16))) T Vl[TE];              // ... lo
-  __shared__ __attribute__((aligned(16))) float Xc[4][16][64];   // Ec^T partials
+  __shared__ __attribute__((aligned(16))) T Ks[kDkataSB][TE];  // K of chunk cb + i, [u][d]
+  __shared__ __attribute__((aligned(16))) T Us[kDkataSB][TE];  // U^T of chunk cb + i, [j][u]
+  // the Ec^T partials' exchange, then (beta (V - Ec))^T hi / lo, [j][u]
+  __shared__ __attribute__((aligned(16))) float Xv[4 * 16 * 64];
+  float(*Xc)[16][64] = reinterpret_cast<float(*)[16][64]>(Xv);
+  T* Vh = reinterpret_cast<T*>(Xv);
+  T* Vl = Vh + TE;
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -218,25 +218,19 @@ __global__ __launch_bounds__(256) void dkata_U_kernel(DKataArgs a) {
   const T* TmH = (const T*)(a.ws + a.L.TmHi) + (size_t)bh * NC * TE;
   const T* TmL = (const T*)(a.ws + a.L.TmLo) + (size_t)bh * NC * TE;
 
-  // copies: each wave moves ops 2w, 2w + 1 of each 8-op tile (4 per wave)
-  auto issue_step = [&](int cp, int slot) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      dma_tile64<T>(kb, rs, 64 * cp, Tn, ring[slot][0], 2 * w + i, lane);
-      dma_tile64<T>(UT + 64 * cp, Tp, 0, DV, ring[slot][1], 2 * w + i, lane);
-    }
-  };
-  auto issue_tm = [&](int c) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      dma_tile64<T>(TmH + (size_t)c * TE, 64, 0, 64, TmS[0], 2 * w + i, lane);
-      dma_tile64<T>(TmL + (size_t)c * TE, 64, 0, 64, TmS[1], 2 * w + i, lane);
-    }
-  };
-  // this lane's token of chunk c: 8 dims of K per k-step, its 16 V columns, beta
-  auto load_chunk = [&](int c, v8_t<T>* kx, v4_t<T>* vx, float& bx) __attribute__((always_inline)) {
+  // this lane's token of chunk c: 8 dims of K per k-step, its 16 V columns,
+  // beta, its row of Tm (hi, lo) as the B operands of the U product, and
+  // (after the first super-chunk) its Ein columns
+  auto load_chunk = [&](int c, v8_t<T>* kx, v4_t<T>* vx, float& bx, v8_t<T>* th, v8_t<T>* tlo,
+                        float4* ex) __attribute__((always_inline)) {
     const int t = 64 * c + 32 * tb + cl;
     const bool in = t < Tn;
+    if (cb > 0) {
+      const float* er = (const float*)(a.ws + a.L.Ein) + (((int64_t)b * Tn + t) * a.H + h) * DV;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        ex[q] = in ? *reinterpret_cast<const float4*>(er + 32 * ub + 8 * q + 4 * hh) : float4{};
+    }
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk)
       kx[kk] = in ? ld8<T>(kb + (int64_t)t * rs + 16 * kk + 8 * hh) : zero8<T>();
@@ -244,6 +238,12 @@ __global__ __launch_bounds__(256) void dkata_U_kernel(DKataArgs a) {
     for (int i = 0; i < 4; ++i)
       vx[i] = in ? ld4<T>(vb + (int64_t)t * vrs + 32 * ub + 8 * i + 4 * hh) : v4_t<T>{};
     bx = in ? a.beta[((int64_t)b * Tn + t) * a.H + h] : 0.f;
+    const size_t tr = (size_t)c * TE + (size_t)(32 * tb + cl) * 64 + 8 * hh;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      th[ks] = ld8<T>(TmH + tr + 16 * ks);
+      tlo[ks] = ld8<T>(TmL + tr + 16 * ks);
+    }
   };
   // A^T[u][t] / scale^2 = sum_{g,g2} (k_u,g2 . k_t,g)^2 for the 32 keys u of
   // block ub of one earlier chunk (K tile Kt) and this wave's 32 tokens t,
@@ -274,83 +274,80 @@ __global__ __launch_bounds__(256) void dkata_U_kernel(DKataArgs a) {
         ec[jb] = mma(tile_ldp8<T>(Ut, 32 * jb + cl, 32 * ub, ks, hh), bop[ks], ec[jb]);
   };
 
-  v8_t<T> kc[D / 16];
+  v8_t<T> kc[D / 16], tmh[4], tml[4];
   v4_t<T> vc[4];
   float bc;
-  load_chunk(0, kc, vc, bc);
-  issue_tm(0);
+  float4 einc[4] = {};
+  load_chunk(cb, kc, vc, bc, tmh, tml, einc);
+  vm_drain();  // the loop sees these operands as loaded, like the ones it prefetches
 
-  for (int c = 0; c < NC; ++c) {
-    const int t0 = 64 * c;
-    const int tl = t0 + 32 * tb + cl;  // this lane's token of the current chunk
-    const int nring = c - 1;           // ring steps: earlier chunks 0 .. c - 2
+  for (int c = cb; c < ce; ++c) {
+    const int i = c - cb;
+    const int tl = 64 * c + 32 * tb + cl;  // this lane's token of the current chunk
+    // the next chunk's operands, in flight while this one runs
+    v8_t<T> kn[D / 16], tnh[4], tnl[4];
+    v4_t<T> vn[4];
+    float bn = 0.f;
+    float4 einn[4] = {};
+    if (c + 1 < ce) load_chunk(c + 1, kn, vn, bn, tnh, tnl, einn);
 
-    // Steps 0 .. nring: step s reads the K and U^T tiles of chunk s (ring slot
-    // s % kRing; the last one from Klast / Ulast).  Software-pipelined: the
-    // Gram block of step s + 1 is formed while the Ec product of step s runs.
+    // Ec over the super-chunk's earlier chunks cb .. c - 1, all in LDS; the
+    // Gram block of step s + 1 is formed while the Ec product of step s runs
     f32x16 ec[2] = {f32x16{}, f32x16{}};
-    if (c > 0) {
+    if (i > 0) {
       v8_t<T> bop[2];
-      if (nring > 0) vm_wait_barrier_n(4 * (min(kRing - 1, nring) - 1));
-      gram(nring > 0 ? ring[0][0] : Klast, kc, bop);
-      for (int s = 0; s < nring; ++s) {
-        if (s + 1 < nring) {
-          // ring copies issued after slot s + 1's: steps s + 2 .. min(s + 3, nring - 1)
-          // (Tm's copies, issued after the first ones, only make the wait stricter)
-          vm_wait_barrier_n(4 * min(2, nring - 2 - s));
-          if (s + kRing - 1 < nring) issue_step(s + kRing - 1, (s + kRing - 1) % kRing);
-        }
+      gram(Ks[0], kc, bop);
+      for (int s = 0; s < i; ++s) {
         v8_t<T> bnext[2];
-        gram(s + 1 < nring ? ring[(s + 1) % kRing][0] : Klast, kc, bnext);
-        ec_update(ring[s % kRing][1], bop, ec);
+        if (s + 1 < i) gram(Ks[s + 1], kc, bnext);
+        ec_update(Us[s], bop, ec);
         bop[0] = bnext[0];
         bop[1] = bnext[1];
       }
-      ec_update(Ulast, bop, ec);
-    }
-
-    // every copy in flight has landed (Tm of this chunk included) and every
-    // wave is done reading the ring, Klast and Ulast
-    vm_wait_barrier<0>();
-    v8_t<T> kn[D / 16];
-    v4_t<T> vn[4];
-    float bn = 0.f;
-    if (c + 1 < NC) {
-      load_chunk(c + 1, kn, vn, bn);
-      // chunk c + 1's ring steps are earlier chunks 0 .. c - 1, all stored
-      for (int s = 0; s < min(kRing - 1, c); ++s) issue_step(s, s);
     }
 
     // the partner wave (same tb, other ub) holds the other u-block's partial:
     // trade the j-block each does not keep (keep jb = ub)
 #pragma unroll
     for (int e = 0; e < 16; ++e) Xc[w][e][lane] = ec[1 - ub][e];
-    // K of this chunk for the next one's last step (rows 32 tb + cl)
+    // K of this chunk for the later ones (rows 32 tb + cl)
     if (ub == 0) {
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk)
-        *reinterpret_cast<v8_t<T>*>(reinterpret_cast<char*>(Klast) + tile_off(32 * tb + cl, 16 * kk + 8 * hh)) = kc[kk];
+        *reinterpret_cast<v8_t<T>*>(reinterpret_cast<char*>(Ks[i]) + tile_off(32 * tb + cl, 16 * kk + 8 * hh)) = kc[kk];
     }
     block_barrier();
     const int partner = tb | ((1 - ub) << 1);
     f32x16 ecs = ec[ub];
 #pragma unroll
     for (int e = 0; e < 16; ++e) ecs[e] = a.scale2 * (ecs[e] + Xc[partner][e][lane]);
-    if (a.keep_e && tl < Tn) {  // the inter-chunk part of E_t, for the backward's dbeta
+    // Ein held the sum over the chunks before cb (dkata_ext_kernel)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ecs[4 * q] += einc[q].x;
+      ecs[4 * q + 1] += einc[q].y;
+      ecs[4 * q + 2] += einc[q].z;
+      ecs[4 * q + 3] += einc[q].w;
+    }
+    // the next chunk's operands have landed during the steps: from here on
+    // no load is waited for behind this chunk's stores
+    vm_drain();
+    if (a.keep_e && tl < Tn) {  // the whole inter-chunk part of E_t, for dbeta
       float* er = (float*)(a.ws + a.L.Ein) + (((int64_t)b * Tn + tl) * a.H + h) * DV;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<float4*>(er + 32 * ub + 8 * i + 4 * hh) =
-            make_float4(ecs[4 * i], ecs[4 * i + 1], ecs[4 * i + 2], ecs[4 * i + 3]);
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<float4*>(er + 32 * ub + 8 * q + 4 * hh) =
+            make_float4(ecs[4 * q], ecs[4 * q + 1], ecs[4 * q + 2], ecs[4 * q + 3]);
     }
+    block_barrier();  // Vh / Vl overwrite the exchange
 
     // beta_t (V[t][j] - Ec[t][j]) for j in block ub, as 16-bit hi + lo in [j][t]
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int q = 0; q < 4; ++q) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int e = 4 * i + r, j = 32 * ub + 8 * i + 4 * hh + r;
-        const float x = bc * ((float)vc[i][r] - ecs[e]);
+        const int e = 4 * q + r, j = 32 * ub + 8 * q + 4 * hh + r;
+        const float x = bc * ((float)vc[q][r] - ecs[e]);
         const T xh = (T)x;
         const int off = tile_off(j, (32 * tb + cl) & ~3);
         reinterpret_cast<T*>(reinterpret_cast<char*>(Vh) + off)[cl & 3] = xh;
@@ -361,52 +358,153 @@ __global__ __launch_bounds__(256) void dkata_U_kernel(DKataArgs a) {
 
     // U^T[j][t] = sum_{u <= t} Vp^T[j][u] Tm[t][u]  (j block ub, t block tb)
     f32x16 uacc{};
-    const T* th = TmS[0];
-    const T* tlo = TmS[1];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       if (ks >= 2 * (tb + 1)) break;  // Tm[t][u] = 0 for u > t
-      const v8_t<T> bh8 = tile_ld8<T>(th, 32 * tb + cl, 16 * ks + 8 * hh);
-      const v8_t<T> bl8 = tile_ld8<T>(tlo, 32 * tb + cl, 16 * ks + 8 * hh);
       const v8_t<T> ah = tile_ld8<T>(Vh, 32 * ub + cl, 16 * ks + 8 * hh);
       const v8_t<T> alo = tile_ld8<T>(Vl, 32 * ub + cl, 16 * ks + 8 * hh);
-      uacc = mma(ah, bh8, uacc);
-      uacc = mma(ah, bl8, uacc);
-      uacc = mma(alo, bh8, uacc);
+      uacc = mma(ah, tmh[ks], uacc);
+      uacc = mma(ah, tml[ks], uacc);
+      uacc = mma(alo, tmh[ks], uacc);
     }
 
-    // U^T for the later chunks (global and, for the next chunk, Ulast) and
-    // U (float32 and 16-bit, time-major)
+    // U^T for the later chunks (global and Us) and U (float32 and 16-bit,
+    // time-major)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int j = 32 * ub + 8 * (e >> 2) + 4 * hh + (e & 3);
       const T u16 = (T)uacc[e];
       UT[(size_t)j * Tp + tl] = u16;
-      reinterpret_cast<T*>(reinterpret_cast<char*>(Ulast) + tile_off(j, (32 * tb + cl) & ~3))[cl & 3] = u16;
+      reinterpret_cast<T*>(reinterpret_cast<char*>(Us[i]) + tile_off(j, (32 * tb + cl) & ~3))[cl & 3] = u16;
     }
     if (tl < Tn) {
       const int64_t row = ((int64_t)b * Tn + tl) * a.H + h;
       T* ub16 = (T*)(a.ws + a.L.Ub) + row * DV;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int j0 = 32 * ub + 8 * i + 4 * hh;
-        st4<T>(ub16 + j0, to4<T>(uacc[4 * i], uacc[4 * i + 1], uacc[4 * i + 2], uacc[4 * i + 3]));
+      for (int q = 0; q < 4; ++q) {
+        const int j0 = 32 * ub + 8 * q + 4 * hh;
+        st4<T>(ub16 + j0, to4<T>(uacc[4 * q], uacc[4 * q + 1], uacc[4 * q + 2], uacc[4 * q + 3]));
         if (a.U) *reinterpret_cast<float4*>(a.U + row * DV + j0) =
-            make_float4(uacc[4 * i], uacc[4 * i + 1], uacc[4 * i + 2], uacc[4 * i + 3]);
+            make_float4(uacc[4 * q], uacc[4 * q + 1], uacc[4 * q + 2], uacc[4 * q + 3]);
       }
     }
-    // Ulast and the Vh / Vl, Xc, TmS reuse; the global U^T is drained by the
-    // next chunk's vm_wait_barrier<0> before any copy reads it
+    // Us / Ks for the next chunk's steps, and the Vh / Vl reuse
     block_barrier();
-    // Tm of the next chunk, behind its first ring copies (the ring waits
-    // count only ring copies after a slot's, so they also wait for these:
-    // stricter, never short)
-    if (c + 1 < NC) issue_tm(c + 1);
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) kc[kk] = kn[kk];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) vc[i] = vn[i];
+    for (int q = 0; q < 4; ++q) {
+      vc[q] = vn[q];
+      tmh[q] = tnh[q];
+      tml[q] = tnl[q];
+      einc[q] = einn[q];
+    }
     bc = bn;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel 2a: the part of a chunk-sequential pass that comes from chunks
+// outside the current super-chunk, in parallel over (b, h, target chunk):
+//   dst_t = scale^2 sum_{c' in [s0, s0 + ns)} A[c, c'] Y_c'
+// for the tokens t of the nsb chunks c0 .. c0 + nsb - 1, with A[t][u] /
+// scale^2 = sum_{g,g2} (k_t,g . k_u,g2)^2 and Y^T = srcT ([j][t] per (b, h),
+// rows padded to whole chunks).  The forward takes Y = U over the earlier
+// chunks (into Ein), the backward Y = X = beta dbV over the later ones (into
+// dbV's rows, which the dbV pass reads and then overwrites).  Waves and
+// products as in dkata_U_kernel; the source chunks' K and Y^T tiles stream
+// through a 4-slot ring; a head's target chunks run on one XCD, where they
+// share those tiles in L2.
+// ---------------------------------------------------------------------------
+template <typename T, int D, int DV, int M>
+__global__ __launch_bounds__(256) void dkata_ext_kernel(const T* __restrict__ k, const T* __restrict__ srcT,
+                                                        float* __restrict__ dst, int H, int Tn, float scale2,
+                                                        int c0, int nsb, int s0, int n, int BH) {
+  constexpr int E = D / M, KE = E / 16, kRing = 4, TE = 64 * 64;
+  static_assert(D == 64 && DV == 64 && E % 16 == 0, "64-wide heads");
+  __shared__ __attribute__((aligned(16))) T ring[kRing][2][TE];
+  __shared__ __attribute__((aligned(16))) float Xc[4][16][64];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+  const int cl = lane & 31, hh = lane >> 5;
+  const int tb = w & 1, ub = w >> 1;
+  int bh, jc;
+  map_block(blockIdx.x, nsb, BH, jc, bh, false);
+  const int c = c0 + jc;
+  const int b = bh / H, h = bh % H;
+  const int NC = (Tn + 63) / 64, Tp = 64 * NC;
+  const int64_t rs = (int64_t)H * D;
+  const T* kb = k + ((int64_t)b * Tn * H + h) * D;
+  const T* YT = srcT + (size_t)bh * DV * Tp;
+  const int tl = 64 * c + 32 * tb + cl;
+
+  v8_t<T> kc[D / 16];
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk)
+    kc[kk] = tl < Tn ? ld8<T>(kb + (int64_t)tl * rs + 16 * kk + 8 * hh) : zero8<T>();
+  auto issue_step = [&](int s, int slot) __attribute__((always_inline)) {
+    const int cp = s0 + s;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      dma_tile64<T>(kb, rs, 64 * cp, Tn, ring[slot][0], 2 * w + i, lane);
+      dma_tile64<T>(YT + 64 * cp, Tp, 0, DV, ring[slot][1], 2 * w + i, lane);
+    }
+  };
+  auto gram = [&](const T* Kt, v8_t<T>* bop) __attribute__((always_inline)) {
+    v8_t<T> ka[D / 16];
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) ka[kk] = tile_ld8<T>(Kt, 32 * ub + cl, 16 * kk + 8 * hh);
+    f32x16 At{};
+#pragma unroll(M > 2 ? 1 : M)  // M = 4 fully unrolled keeps 16 Gram blocks live and spills
+    for (int g = 0; g < M; ++g)
+#pragma unroll
+      for (int g2 = 0; g2 < M; ++g2) {
+        f32x16 r{};
+#pragma unroll
+        for (int kk = 0; kk < KE; ++kk) r = mma(ka[g2 * KE + kk], kc[g * KE + kk], r);
+        At += r * r;
+      }
+    bop[0] = c_to_b<T>(At, 0);
+    bop[1] = c_to_b<T>(At, 1);
+  };
+  auto y_update = [&](const T* Yt, const v8_t<T>* bop, f32x16 (&ec)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+        ec[jb] = mma(tile_ldp8<T>(Yt, 32 * jb + cl, 32 * ub, ks, hh), bop[ks], ec[jb]);
+  };
+
+  for (int s = 0; s < min(kRing - 1, n); ++s) issue_step(s, s);
+  f32x16 ec[2] = {f32x16{}, f32x16{}};
+  v8_t<T> bop[2];
+  vm_wait_barrier_n(4 * (min(kRing - 1, n) - 1));
+  gram(ring[0][0], bop);
+  for (int s = 0; s < n; ++s) {
+    v8_t<T> bnext[2];
+    if (s + 1 < n) {
+      // copies issued after slot s + 1's: step s + 2 when it exists
+      vm_wait_barrier_n(4 * min(kRing - 3, n - 2 - s));
+      if (s + kRing - 1 < n) issue_step(s + kRing - 1, (s + kRing - 1) % kRing);
+      gram(ring[(s + 1) % kRing][0], bnext);
+    }
+    y_update(ring[s % kRing][1], bop, ec);
+    bop[0] = bnext[0];
+    bop[1] = bnext[1];
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) Xc[w][e][lane] = ec[1 - ub][e];
+  block_barrier();
+  if (tl < Tn) {
+    const int partner = tb | ((1 - ub) << 1);
+    float* er = dst + (((int64_t)b * Tn + tl) * H + h) * DV;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v4[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v4[r] = scale2 * (ec[ub][4 * i + r] + Xc[partner][4 * i + r][lane]);
+      *reinterpret_cast<float4*>(er + 32 * ub + 8 * i + 4 * hh) = make_float4(v4[0], v4[1], v4[2], v4[3]);
+    }
   }
 }
 
@@ -435,9 +533,19 @@ hipError_t launch_dkata_fwd(const DKataArgs& a, hipStream_t stream) {
   dkata_prep_kernel<T, D, M><<<dim3(BH * NC), dim3(256), 0, stream>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  dkata_U_kernel<T, D, DV, M><<<dim3(BH), dim3(256), 0, stream>>>(a);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  // chunk-sequential only inside super-chunks of kDkataSB chunks; between
+  // them, the earlier super-chunks' contribution in parallel
+  for (int cb = 0; cb < NC; cb += kDkataSB) {
+    const int ce = cb + kDkataSB < NC ? cb + kDkataSB : NC;
+    if (cb > 0) {
+      dkata_ext_kernel<T, D, DV, M><<<dim3(BH * (ce - cb)), dim3(256), 0, stream>>>(
+          (const T*)a.k, (const T*)(a.ws + a.L.UT), (float*)(a.ws + a.L.Ein), a.H, a.T, a.scale2, cb,
+          ce - cb, 0, cb, BH);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    dkata_U_kernel<T, D, DV, M><<<dim3(BH), dim3(256), 0, stream>>>(a, cb, ce);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
   // readout: the KATA sum-score forward of (q, k, U) with the same scale
   KataArgs r{};
   r.q = a.q; r.k = a.k; r.v = a.ws + a.L.Ub; r.c = nullptr;
@@ -514,21 +622,26 @@ __global__ __launch_bounds__(256) void dkata_bwd_prep_kernel(DKataBwdArgs a, int
 }
 
 // dbV = (I + diag(beta) strict_lower(A_kk))^-T dU, chunk after chunk from the
-// last: R_c = sum_{c' > c} A_kk[c, c'] X_c' (A_kk is symmetric), dbV_c =
-// Tm_c^T (dU_c - R_c), X_c = beta_c dbV_c.  Layout and schedule as
-// dkata_U_kernel with the chunk order reversed: wave w = (tb, ub), ring of
-// later chunks' K and X^T tiles, chunk c + 1's in Klast / Xlast.
+// last of one super-chunk [cb, ce) to its first: R_c = sum_{c' > c} A_kk[c,
+// c'] X_c' (A_kk is symmetric), dbV_c = Tm_c^T (dU_c - R_c), X_c = beta_c
+// dbV_c.  The chunks at or after ce enter through dbV's rows
+// (dkata_ext_kernel).  Layout and schedule as dkata_U_kernel with the chunk
+// order reversed: wave w = (tb, ub), the super-chunk's K and X^T tiles
+// resident in LDS; the next chunk's Tm is copied into LDS (read back
+// transposed) and its other operands loaded into registers while the
+// current chunk runs.  LDS: 160 KB.
 template <typename T, int D, int DV, int M>
-__global__ __launch_bounds__(256) void dkata_dbV_kernel(DKataBwdArgs a) {
-  constexpr int E = D / M, KE = E / 16, kRing = 5, TE = 64 * 64;
+__global__ __launch_bounds__(256) void dkata_dbV_kernel(DKataBwdArgs a, int cb, int ce) {
+  constexpr int E = D / M, KE = E / 16, TE = 64 * 64;
   static_assert(D == 64 && DV == 64 && E % 16 == 0, "64-wide heads");
-  __shared__ __attribute__((aligned(16))) T ring[kRing][2][TE];  // K, X^T tiles of chunk c'
-  __shared__ __attribute__((aligned(16))) T Klast[TE];
-  __shared__ __attribute__((aligned(16))) T Xlast[TE];
-  __shared__ __attribute__((aligned(16))) T TmS[2][TE];
-  __shared__ __attribute__((aligned(16))) T Vh[TE];  // (dU - R)^T hi, [j][t]
-  __shared__ __attribute__((aligned(16))) T Vl[TE];
-  __shared__ __attribute__((aligned(16))) float Xc[4][16][64];
+  __shared__ __attribute__((aligned(16))) T Ks[kDkataSB][TE];  // K of chunk cb + i, [u][d]
+  __shared__ __attribute__((aligned(16))) T Xs[kDkataSB][TE];  // X^T of chunk cb + i, [j][u]
+  // the R^T partials' exchange, then (dU - R)^T hi / lo, [j][t]
+  __shared__ __attribute__((aligned(16))) float Xv[4 * 16 * 64];
+  __shared__ __attribute__((aligned(16))) T TmS[2][TE];  // Tm hi / lo of the chunk, [t][i]
+  float(*Xc)[16][64] = reinterpret_cast<float(*)[16][64]>(Xv);
+  T* Vh = reinterpret_cast<T*>(Xv);
+  T* Vl = Vh + TE;
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -542,13 +655,6 @@ __global__ __launch_bounds__(256) void dkata_dbV_kernel(DKataBwdArgs a) {
   const T* TmH = (const T*)(a.ws + a.L.TmHi) + (size_t)bh * NC * TE;
   const T* TmL = (const T*)(a.ws + a.L.TmLo) + (size_t)bh * NC * TE;
 
-  auto issue_step = [&](int cp, int slot) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      dma_tile64<T>(kb, rs, 64 * cp, Tn, ring[slot][0], 2 * w + i, lane);
-      dma_tile64<T>(XT + 64 * cp, Tp, 0, DV, ring[slot][1], 2 * w + i, lane);
-    }
-  };
   auto issue_tm = [&](int c) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -556,9 +662,18 @@ __global__ __launch_bounds__(256) void dkata_dbV_kernel(DKataBwdArgs a) {
       dma_tile64<T>(TmL + (size_t)c * TE, 64, 0, 64, TmS[1], 2 * w + i, lane);
     }
   };
-  auto load_chunk = [&](int c, v8_t<T>* kx, v4_t<T>* dx, float& bx) __attribute__((always_inline)) {
+  // this lane's token of chunk c: K row, dU columns, beta and (before the
+  // last super-chunk) the part of R from the later super-chunks
+  auto load_chunk = [&](int c, v8_t<T>* kx, v4_t<T>* dx, float& bx, float4* rx)
+      __attribute__((always_inline)) {
     const int t = 64 * c + 32 * tb + cl;
     const bool in = t < Tn;
+    if (ce < NC) {  // dbV's row holds the part of R_t from the chunks at or after ce
+      const float* rr = (const float*)(a.bws + a.BL.dbV) + (((int64_t)b * Tn + t) * a.H + h) * DV;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        rx[q] = in ? *reinterpret_cast<const float4*>(rr + 32 * ub + 8 * q + 4 * hh) : float4{};
+    }
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk)
       kx[kk] = in ? ld8<T>(kb + (int64_t)t * rs + 16 * kk + 8 * hh) : zero8<T>();
@@ -595,39 +710,33 @@ __global__ __launch_bounds__(256) void dkata_dbV_kernel(DKataBwdArgs a) {
   v8_t<T> kc[D / 16];
   v4_t<T> duc[4];
   float bc;
-  load_chunk(NC - 1, kc, duc, bc);
-  issue_tm(NC - 1);
+  float4 rxc[4] = {};
+  load_chunk(ce - 1, kc, duc, bc, rxc);
+  issue_tm(ce - 1);
+  vm_drain();  // the loop sees these operands as loaded, like the ones it prefetches
 
-  for (int c = NC - 1; c >= 0; --c) {
+  for (int c = ce - 1; c >= cb; --c) {
+    const int i = c - cb;
     const int tl = 64 * c + 32 * tb + cl;
-    const int nring = NC - c - 2;  // ring steps: later chunks c + 2 .. NC - 1 (step s: c + 2 + s)
-    f32x16 ec[2] = {f32x16{}, f32x16{}};
-    if (c + 1 < NC) {
-      v8_t<T> bop[2];
-      if (nring > 0) vm_wait_barrier_n(4 * (min(kRing - 1, nring) - 1));
-      gram(nring > 0 ? ring[0][0] : Klast, kc, bop);
-      for (int s = 0; s < nring; ++s) {
-        if (s + 1 < nring) {
-          vm_wait_barrier_n(4 * min(2, nring - 2 - s));
-          if (s + kRing - 1 < nring) issue_step(c + 2 + s + kRing - 1, (s + kRing - 1) % kRing);
-        }
-        v8_t<T> bnext[2];
-        gram(s + 1 < nring ? ring[(s + 1) % kRing][0] : Klast, kc, bnext);
-        r_update(ring[s % kRing][1], bop, ec);
-        bop[0] = bnext[0];
-        bop[1] = bnext[1];
-      }
-      r_update(Xlast, bop, ec);
-    }
-
-    vm_wait_barrier<0>();
     v8_t<T> kn[D / 16];
     v4_t<T> dun[4];
     float bn = 0.f;
-    if (c > 0) {
-      load_chunk(c - 1, kn, dun, bn);
-      // chunk c - 1's ring steps are later chunks c + 1 .. NC - 1, all stored
-      for (int s = 0; s < min(kRing - 1, NC - c - 1); ++s) issue_step(c + 1 + s, s);
+    float4 rxn[4] = {};
+    if (c > cb) load_chunk(c - 1, kn, dun, bn, rxn);
+
+    // R over the super-chunk's later chunks c + 1 .. ce - 1, all in LDS
+    f32x16 ec[2] = {f32x16{}, f32x16{}};
+    const int n = ce - 1 - c;  // step s: chunk c + 1 + s
+    if (n > 0) {
+      v8_t<T> bop[2];
+      gram(Ks[i + 1], kc, bop);
+      for (int s = 0; s < n; ++s) {
+        v8_t<T> bnext[2];
+        if (s + 1 < n) gram(Ks[i + 2 + s], kc, bnext);
+        r_update(Xs[i + 1 + s], bop, ec);
+        bop[0] = bnext[0];
+        bop[1] = bnext[1];
+      }
     }
 
 #pragma unroll
@@ -635,21 +744,34 @@ __global__ __launch_bounds__(256) void dkata_dbV_kernel(DKataBwdArgs a) {
     if (ub == 0) {
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk)
-        *reinterpret_cast<v8_t<T>*>(reinterpret_cast<char*>(Klast) + tile_off(32 * tb + cl, 16 * kk + 8 * hh)) = kc[kk];
+        *reinterpret_cast<v8_t<T>*>(reinterpret_cast<char*>(Ks[i]) + tile_off(32 * tb + cl, 16 * kk + 8 * hh)) = kc[kk];
     }
     block_barrier();
     const int partner = tb | ((1 - ub) << 1);
     f32x16 ecs = ec[ub];
 #pragma unroll
     for (int e = 0; e < 16; ++e) ecs[e] = a.scale2 * (ecs[e] + Xc[partner][e][lane]);
+    // the part of R from the chunks at or after ce (dkata_ext_kernel, in
+    // dbV's rows, which this lane overwrites with dbV below)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ecs[4 * q] += rxc[q].x;
+      ecs[4 * q + 1] += rxc[q].y;
+      ecs[4 * q + 2] += rxc[q].z;
+      ecs[4 * q + 3] += rxc[q].w;
+    }
+    // this chunk's Tm and the next chunk's operands have landed during the
+    // steps: from here on no load is waited for behind this chunk's stores
+    vm_drain();
+    block_barrier();  // Vh / Vl overwrite the exchange; every wave's Tm copies are in
 
     // (dU - R)^T[j][t] for j in block ub, as 16-bit hi + lo
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int q = 0; q < 4; ++q) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int e = 4 * i + r, j = 32 * ub + 8 * i + 4 * hh + r;
-        const float x = (float)duc[i][r] - ecs[e];
+        const int e = 4 * q + r, j = 32 * ub + 8 * q + 4 * hh + r;
+        const float x = (float)duc[q][r] - ecs[e];
         const T xh = (T)x;
         const int off = tile_off(j, (32 * tb + cl) & ~3);
         reinterpret_cast<T*>(reinterpret_cast<char*>(Vh) + off)[cl & 3] = xh;
@@ -672,14 +794,14 @@ __global__ __launch_bounds__(256) void dkata_dbV_kernel(DKataBwdArgs a) {
       uacc = mma(alo, bh8, uacc);
     }
 
-    // X = beta dbV: X^T for the earlier chunks (global, and Xlast for chunk
-    // c - 1); dbV (float32) and -X (the erase pass's dO), time-major
+    // X = beta dbV: X^T for the earlier chunks (global, and Xs); dbV
+    // (float32) and -X (the erase pass's dO), time-major
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int j = 32 * ub + 8 * (e >> 2) + 4 * hh + (e & 3);
       const T x16 = (T)(bc * uacc[e]);
       XT[(size_t)j * Tp + tl] = x16;
-      reinterpret_cast<T*>(reinterpret_cast<char*>(Xlast) + tile_off(j, (32 * tb + cl) & ~3))[cl & 3] = x16;
+      reinterpret_cast<T*>(reinterpret_cast<char*>(Xs[i]) + tile_off(j, (32 * tb + cl) & ~3))[cl & 3] = x16;
     }
     if (tl < Tn) {
       const int64_t row = ((int64_t)b * Tn + tl) * a.H + h;
@@ -687,21 +809,24 @@ __global__ __launch_bounds__(256) void dkata_dbV_kernel(DKataBwdArgs a) {
       // -X_t goes to row t - 1 of the shifted erase dO
       T* xn = tl > 0 ? (T*)(a.bws + a.BL.Xn) + (row - a.H) * DV : nullptr;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int j0 = 32 * ub + 8 * i + 4 * hh;
+      for (int q = 0; q < 4; ++q) {
+        const int j0 = 32 * ub + 8 * q + 4 * hh;
         *reinterpret_cast<float4*>(dbv + j0) =
-            make_float4(uacc[4 * i], uacc[4 * i + 1], uacc[4 * i + 2], uacc[4 * i + 3]);
+            make_float4(uacc[4 * q], uacc[4 * q + 1], uacc[4 * q + 2], uacc[4 * q + 3]);
         if (xn)
-          st4<T>(xn + j0, to4<T>(-(float)(T)(bc * uacc[4 * i]), -(float)(T)(bc * uacc[4 * i + 1]),
-                                 -(float)(T)(bc * uacc[4 * i + 2]), -(float)(T)(bc * uacc[4 * i + 3])));
+          st4<T>(xn + j0, to4<T>(-(float)(T)(bc * uacc[4 * q]), -(float)(T)(bc * uacc[4 * q + 1]),
+                                 -(float)(T)(bc * uacc[4 * q + 2]), -(float)(T)(bc * uacc[4 * q + 3])));
       }
     }
     block_barrier();
-    if (c > 0) issue_tm(c - 1);
+    if (c > cb) issue_tm(c - 1);  // every wave is done reading TmS
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) kc[kk] = kn[kk];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) duc[i] = dun[i];
+    for (int q = 0; q < 4; ++q) {
+      duc[q] = dun[q];
+      rxc[q] = rxn[q];
+    }
     bc = bn;
   }
 }
@@ -846,8 +971,19 @@ hipError_t launch_dkata_bwd(const DKataBwdArgs& a, hipStream_t stream) {
   r.B = a.B; r.T = a.T; r.HQ = a.H; r.H = a.H; r.DK = D; r.DV = DV; r.M = M; r.scale = a.scale;
   e = launch_kata_bwd<T, D, DV, M, true, false>(r, KATA_BWD_DQ | KATA_BWD_DKDV, stream);
   if (e != hipSuccess) return e;
-  dkata_dbV_kernel<T, D, DV, M><<<dim3(BH), dim3(256), 0, stream>>>(a);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+  // chunk-sequential only inside super-chunks, last one first; the later
+  // super-chunks' part of R in parallel before each
+  for (int cb = (NC - 1) / kDkataSB * kDkataSB; cb >= 0; cb -= kDkataSB) {
+    const int ce = cb + kDkataSB < NC ? cb + kDkataSB : NC;
+    if (ce < NC) {
+      dkata_ext_kernel<T, D, DV, M><<<dim3(BH * (ce - cb)), dim3(256), 0, stream>>>(
+          (const T*)a.k, (const T*)(a.bws + a.BL.XT), (float*)(a.bws + a.BL.dbV), a.H, a.T, a.scale2,
+          cb, ce - cb, ce, NC - ce, BH);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    dkata_dbV_kernel<T, D, DV, M><<<dim3(BH), dim3(256), 0, stream>>>(a, cb, ce);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
   // erase: KATA sum backward of (k shifted one token, k, U) with the shifted
   // dO := -X, o := 0, den := 1
   KataArgs x{};

@@ -197,6 +197,25 @@ def test_backward_parity(F, shape, M, normalize, scale, dtype):
         assert e < tol, (name, e)
 
 
+@pytest.mark.parametrize("T", [512, 513, 1025, 1600])
+def test_super_chunk_boundaries(F, T):
+    """The chunk-sequential passes run in super-chunks of 8 chunks (512
+    tokens), with the other super-chunks' terms added by a parallel kernel:
+    lengths at and just past those boundaries, forward and backward."""
+    B, H, M = 1, 2, 2
+    q, k, v, beta = make(B, T, H, 64, 64, torch.bfloat16, 40 + T)
+    do = torch.randn(B, T, H, 64, generator=torch.Generator().manual_seed(T))
+    print(f"\nflash_delta super-chunks T={T}", flush=True)
+    o_ref, dq_ref, dk_ref, dv_ref, db_ref = DK.flash_delta_fwd_bwd(q, k, v, beta, M, do, 0.5)
+    qd, kd, vd, bd = (t.cuda().requires_grad_(True) for t in (q, k, v, beta))
+    o = F.flash_delta(qd, kd, vd, bd, M, scale=0.5)
+    o.backward(do.cuda())
+    for name, got, ref in (("o", o, o_ref), ("dq", qd.grad, dq_ref), ("dk", kd.grad, dk_ref),
+                           ("dv", vd.grad, dv_ref), ("dbeta", bd.grad, db_ref)):
+        e = mar(got, ref)
+        assert e < 2e-2, (name, e)
+
+
 def test_backward_fp16_raises(F):
     q, k, v, beta = make(1, 64, 1, 64, 64, torch.float16, 1)
     qd = q.cuda().requires_grad_(True)
