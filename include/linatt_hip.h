@@ -245,7 +245,8 @@ int linatt_dkata_fwd(const void* q, const void* k, const void* v, const float* b
                      int num_groups, float scale, int normalize, float eps, int dtype,
                      void* stream);
 
-/* The forward for training: as linatt_dkata_fwd, U required; the workspace
+/* The forward for training: as linatt_dkata_fwd (U may be NULL: the
+ * backward reads the workspace's 16-bit copy of U, not U); the workspace
  * then also holds what linatt_dkata_bwd reads and must reach it unchanged. */
 int linatt_dkata_fwd_train(const void* q, const void* k, const void* v, const float* beta,
                            float* U, float* o, float* den, void* workspace, int B, int T, int H,
@@ -255,8 +256,9 @@ int linatt_dkata_fwd_train(const void* q, const void* k, const void* v, const fl
 /* Backward, replacing flash_delta_bwd (kata/spd/flash_delta.py:830-895) and
  * _FlashDelta.backward (:1084-1108): dq, dk (B,T,H,d), dv (B,T,H,dv) [dtype]
  * and dbeta (B,T,H) float32 for the loss <o, dout> (dout float32, the
- * forward's output dtype).  U, o (normalize only), den: the training
- * forward's outputs; fwd_workspace: its workspace; workspace:
+ * forward's output dtype).  o (normalize only), den: the training
+ * forward's outputs (U is not read and may be NULL; it stays in the list
+ * the reference's backward saves); fwd_workspace: its workspace; workspace:
  * linatt_dkata_bwd_workspace_bytes.  bfloat16 only (fp16 cannot carry the
  * intermediate dU at small scales); other dtypes return LINATT_EUNSUPPORTED. */
 size_t linatt_dkata_bwd_workspace_bytes(int B, int T, int H, int d, int dv, int dtype);

@@ -583,10 +583,6 @@ int linatt_dkata_fwd_train(const void* q, const void* k, const void* v, const fl
                            float* U, float* o, float* den, void* workspace, int B, int T, int H,
                            int d, int dv, int num_groups, float scale, int normalize, float eps,
                            int dtype, void* stream) {
-  if (!U) {
-    g_last_error = "linatt_dkata_fwd_train: U is required (the backward reads it)";
-    return LINATT_EINVAL;
-  }
   return dkata_fwd_entry("linatt_dkata_fwd_train", 1, q, k, v, beta, U, o, den, workspace, B, T,
                          H, d, dv, num_groups, scale, normalize, eps, dtype, stream);
 }
@@ -619,7 +615,7 @@ int linatt_dkata_bwd(const void* q, const void* k, const void* v, const float* b
   // dtype the mixer calls flash_delta with (kata/layer.py:409-412)
   if (dtype != LINATT_BFLOAT16)
     return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": the backward is compiled for bfloat16 only");
-  if (!q || !k || !v || !beta || !U || !den || !dout || !dq || !dk || !dv || !dbeta ||
+  if (!q || !k || !v || !beta || !den || !dout || !dq || !dk || !dv || !dbeta ||
       !fwd_workspace || !workspace || (normalize && !o))
     return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
   const void* ps[] = {q, k, v, U, o, dout, dq, dk, dv, fwd_workspace, workspace};

@@ -405,16 +405,18 @@ __global__ __launch_bounds__(256) void dkata_U_kernel(DKataArgs a, int cb, int c
 
 // ---------------------------------------------------------------------------
 // Kernel 2a: the part of a chunk-sequential pass that comes from chunks
-// outside the current super-chunk, in parallel over (b, h, target chunk):
-//   dst_t = scale^2 sum_{c' in [s0, s0 + ns)} A[c, c'] Y_c'
+// outside the current super-chunk, in parallel over (b, h, pair of target
+// chunks):
+//   dst_t = scale^2 sum_{c' in [s0, s0 + n)} A[c, c'] Y_c'
 // for the tokens t of the nsb chunks c0 .. c0 + nsb - 1, with A[t][u] /
 // scale^2 = sum_{g,g2} (k_t,g . k_u,g2)^2 and Y^T = srcT ([j][t] per (b, h),
 // rows padded to whole chunks).  The forward takes Y = U over the earlier
 // chunks (into Ein), the backward Y = X = beta dbV over the later ones (into
 // dbV's rows, which the dbV pass reads and then overwrites).  Waves and
-// products as in dkata_U_kernel; the source chunks' K and Y^T tiles stream
-// through a 4-slot ring; a head's target chunks run on one XCD, where they
-// share those tiles in L2.
+// products as in dkata_U_kernel, for two target chunks at once, so each
+// source tile copied into LDS serves twice the products; the source
+// chunks' K and Y^T tiles stream through a 4-slot ring; a head's target
+// chunks run on one XCD, where they share those tiles in L2.
 // ---------------------------------------------------------------------------
 template <typename T, int D, int DV, int M>
 __global__ __launch_bounds__(256) void dkata_ext_kernel(const T* __restrict__ k, const T* __restrict__ srcT,
@@ -428,20 +430,30 @@ __global__ __launch_bounds__(256) void dkata_ext_kernel(const T* __restrict__ k,
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
   const int tb = w & 1, ub = w >> 1;
-  int bh, jc;
-  map_block(blockIdx.x, nsb, BH, jc, bh, false);
-  const int c = c0 + jc;
+  const int npair = (nsb + 1) / 2;
+  int bh, jp;
+  map_block(blockIdx.x, npair, BH, jp, bh, false);
   const int b = bh / H, h = bh % H;
   const int NC = (Tn + 63) / 64, Tp = 64 * NC;
   const int64_t rs = (int64_t)H * D;
   const T* kb = k + ((int64_t)b * Tn * H + h) * D;
   const T* YT = srcT + (size_t)bh * DV * Tp;
-  const int tl = 64 * c + 32 * tb + cl;
-
-  v8_t<T> kc[D / 16];
+  // this lane's token in each target chunk (the second past the range when
+  // nsb is odd: its rows then hold zeros and are not stored)
+  int tl[2];
+  bool st[2];
 #pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk)
-    kc[kk] = tl < Tn ? ld8<T>(kb + (int64_t)tl * rs + 16 * kk + 8 * hh) : zero8<T>();
+  for (int x = 0; x < 2; ++x) {
+    tl[x] = 64 * (c0 + 2 * jp + x) + 32 * tb + cl;
+    st[x] = 2 * jp + x < nsb && tl[x] < Tn;
+  }
+
+  v8_t<T> kc[2][D / 16];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk)
+      kc[x][kk] = st[x] ? ld8<T>(kb + (int64_t)tl[x] * rs + 16 * kk + 8 * hh) : zero8<T>();
   auto issue_step = [&](int s, int slot) __attribute__((always_inline)) {
     const int cp = s0 + s;
 #pragma unroll
@@ -450,38 +462,46 @@ __global__ __launch_bounds__(256) void dkata_ext_kernel(const T* __restrict__ k,
       dma_tile64<T>(YT + 64 * cp, Tp, 0, DV, ring[slot][1], 2 * w + i, lane);
     }
   };
-  auto gram = [&](const T* Kt, v8_t<T>* bop) __attribute__((always_inline)) {
+  // the Gram blocks of source keys (block ub of tile Kt) against both target
+  // chunks' tokens, as the B operands of the Y products
+  auto gram = [&](const T* Kt, v8_t<T> (&bop)[2][2]) __attribute__((always_inline)) {
     v8_t<T> ka[D / 16];
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) ka[kk] = tile_ld8<T>(Kt, 32 * ub + cl, 16 * kk + 8 * hh);
-    f32x16 At{};
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      f32x16 At{};
 #pragma unroll(M > 2 ? 1 : M)  // M = 4 fully unrolled keeps 16 Gram blocks live and spills
-    for (int g = 0; g < M; ++g)
+      for (int g = 0; g < M; ++g)
 #pragma unroll
-      for (int g2 = 0; g2 < M; ++g2) {
-        f32x16 r{};
+        for (int g2 = 0; g2 < M; ++g2) {
+          f32x16 r{};
 #pragma unroll
-        for (int kk = 0; kk < KE; ++kk) r = mma(ka[g2 * KE + kk], kc[g * KE + kk], r);
-        At += r * r;
-      }
-    bop[0] = c_to_b<T>(At, 0);
-    bop[1] = c_to_b<T>(At, 1);
+          for (int kk = 0; kk < KE; ++kk) r = mma(ka[g2 * KE + kk], kc[x][g * KE + kk], r);
+          At += r * r;
+        }
+      bop[x][0] = c_to_b<T>(At, 0);
+      bop[x][1] = c_to_b<T>(At, 1);
+    }
   };
-  auto y_update = [&](const T* Yt, const v8_t<T>* bop, f32x16 (&ec)[2]) __attribute__((always_inline)) {
+  auto y_update = [&](const T* Yt, const v8_t<T> (&bop)[2][2], f32x16 (&ec)[2][2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
-        ec[jb] = mma(tile_ldp8<T>(Yt, 32 * jb + cl, 32 * ub, ks, hh), bop[ks], ec[jb]);
+      for (int jb = 0; jb < 2; ++jb) {
+        const v8_t<T> ya = tile_ldp8<T>(Yt, 32 * jb + cl, 32 * ub, ks, hh);
+#pragma unroll
+        for (int x = 0; x < 2; ++x) ec[x][jb] = mma(ya, bop[x][ks], ec[x][jb]);
+      }
   };
 
   for (int s = 0; s < min(kRing - 1, n); ++s) issue_step(s, s);
-  f32x16 ec[2] = {f32x16{}, f32x16{}};
-  v8_t<T> bop[2];
+  f32x16 ec[2][2] = {{f32x16{}, f32x16{}}, {f32x16{}, f32x16{}}};
+  v8_t<T> bop[2][2];
   vm_wait_barrier_n(4 * (min(kRing - 1, n) - 1));
   gram(ring[0][0], bop);
   for (int s = 0; s < n; ++s) {
-    v8_t<T> bnext[2];
+    v8_t<T> bnext[2][2];
     if (s + 1 < n) {
       // copies issued after slot s + 1's: step s + 2 when it exists
       vm_wait_barrier_n(4 * min(kRing - 3, n - 2 - s));
@@ -489,21 +509,32 @@ __global__ __launch_bounds__(256) void dkata_ext_kernel(const T* __restrict__ k,
       gram(ring[(s + 1) % kRing][0], bnext);
     }
     y_update(ring[s % kRing][1], bop, ec);
-    bop[0] = bnext[0];
-    bop[1] = bnext[1];
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      bop[x][0] = bnext[x][0];
+      bop[x][1] = bnext[x][1];
+    }
   }
+  // the partner wave (same tb, other ub) holds the other u-block's partial:
+  // trade the j-block each does not keep, one target chunk at a time
+  const int partner = tb | ((1 - ub) << 1);
 #pragma unroll
-  for (int e = 0; e < 16; ++e) Xc[w][e][lane] = ec[1 - ub][e];
-  block_barrier();
-  if (tl < Tn) {
-    const int partner = tb | ((1 - ub) << 1);
-    float* er = dst + (((int64_t)b * Tn + tl) * H + h) * DV;
+  for (int x = 0; x < 2; ++x) {
+    const f32x16 keep = ub ? ec[x][1] : ec[x][0];
+    const f32x16 give = ub ? ec[x][0] : ec[x][1];
+    if (x) block_barrier();  // every wave has read the first chunk's partials
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float v4[4];
+    for (int e = 0; e < 16; ++e) Xc[w][e][lane] = give[e];
+    block_barrier();
+    if (st[x]) {
+      float* er = dst + (((int64_t)b * Tn + tl[x]) * H + h) * DV;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v4[r] = scale2 * (ec[ub][4 * i + r] + Xc[partner][4 * i + r][lane]);
-      *reinterpret_cast<float4*>(er + 32 * ub + 8 * i + 4 * hh) = make_float4(v4[0], v4[1], v4[2], v4[3]);
+      for (int i = 0; i < 4; ++i) {
+        float v4[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v4[r] = scale2 * (keep[4 * i + r] + Xc[partner][4 * i + r][lane]);
+        *reinterpret_cast<float4*>(er + 32 * ub + 8 * i + 4 * hh) = make_float4(v4[0], v4[1], v4[2], v4[3]);
+      }
     }
   }
 }
@@ -538,7 +569,7 @@ hipError_t launch_dkata_fwd(const DKataArgs& a, hipStream_t stream) {
   for (int cb = 0; cb < NC; cb += kDkataSB) {
     const int ce = cb + kDkataSB < NC ? cb + kDkataSB : NC;
     if (cb > 0) {
-      dkata_ext_kernel<T, D, DV, M><<<dim3(BH * (ce - cb)), dim3(256), 0, stream>>>(
+      dkata_ext_kernel<T, D, DV, M><<<dim3(BH * ((ce - cb + 1) / 2)), dim3(256), 0, stream>>>(
           (const T*)a.k, (const T*)(a.ws + a.L.UT), (float*)(a.ws + a.L.Ein), a.H, a.T, a.scale2, cb,
           ce - cb, 0, cb, BH);
       if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -976,7 +1007,7 @@ hipError_t launch_dkata_bwd(const DKataBwdArgs& a, hipStream_t stream) {
   for (int cb = (NC - 1) / kDkataSB * kDkataSB; cb >= 0; cb -= kDkataSB) {
     const int ce = cb + kDkataSB < NC ? cb + kDkataSB : NC;
     if (ce < NC) {
-      dkata_ext_kernel<T, D, DV, M><<<dim3(BH * (ce - cb)), dim3(256), 0, stream>>>(
+      dkata_ext_kernel<T, D, DV, M><<<dim3(BH * ((ce - cb + 1) / 2)), dim3(256), 0, stream>>>(
           (const T*)a.k, (const T*)(a.bws + a.BL.XT), (float*)(a.bws + a.BL.dbV), a.H, a.T, a.scale2,
           cb, ce - cb, ce, NC - ce, BH);
       if ((e = hipGetLastError()) != hipSuccess) return e;

@@ -61,8 +61,9 @@ def _run(q, k, v, beta, M, scale, normalize, eps, want_U, train=False):
             f"linatt_amd flash_delta: no kernel for {q.dtype}, D={D}, DV={DV}, M={M}")
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     beta = beta.float().contiguous()
-    U = (torch.empty(B, T, H, DV, device=q.device, dtype=torch.float32)
-         if want_U or train else None)
+    # training keeps no float32 U: the backward reads the workspace's 16-bit
+    # copy of U
+    U = torch.empty(B, T, H, DV, device=q.device, dtype=torch.float32) if want_U else None
     o = torch.empty(B, T, H, DV, device=q.device, dtype=torch.float32)
     den = torch.empty(B, T, H, device=q.device, dtype=torch.float32)
     ws = torch.empty(L.linatt_dkata_workspace_bytes(B, T, H, D, DV, dt), device=q.device,
@@ -79,8 +80,9 @@ def _run(q, k, v, beta, M, scale, normalize, eps, want_U, train=False):
 
 class _FlashDelta(torch.autograd.Function):
     """``_FlashDelta`` (``kata/spd/flash_delta.py:1060-1108``): the forward keeps
-    U, the output, den and its workspace for the backward
-    (``linatt_dkata_fwd_train`` / ``linatt_dkata_bwd``)."""
+    the output, den and its workspace (which holds a 16-bit copy of U, all the
+    backward reads of U) for the backward (``linatt_dkata_fwd_train`` /
+    ``linatt_dkata_bwd``)."""
 
     @staticmethod
     def forward(ctx, q, k, v, beta, M, scale, normalize, eps):

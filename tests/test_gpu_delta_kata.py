@@ -216,6 +216,42 @@ def test_super_chunk_boundaries(F, T):
         assert e < 2e-2, (name, e)
 
 
+def test_train_forward_keeps_no_U(F):
+    """The training forward through the C ABI with U = NULL writes the same
+    output, den and backward-visible workspace as with U given, and the
+    backward (which never reads U) gives identical gradients either way."""
+    from linatt_amd import _lib
+    L = _lib.load()
+    B, T, H, D, M = 1, 300, 2, 64, 2
+    q, k, v, beta = dev(*make(B, T, H, D, D, torch.bfloat16, 77))
+    do = torch.randn(B, T, H, D, device="cuda")
+    dt = _lib.dtype_code(q.dtype)
+    P, sp = _lib.ptr, _lib.stream_of(q)
+    outs = []
+    for with_u in (True, False):
+        U = torch.empty(B, T, H, D, device="cuda") if with_u else None
+        o = torch.empty(B, T, H, D, device="cuda")
+        den = torch.empty(B, T, H, device="cuda")
+        ws = torch.zeros(L.linatt_dkata_workspace_bytes(B, T, H, D, D, dt), device="cuda",
+                         dtype=torch.uint8)
+        _lib.check("linatt_dkata_fwd_train", L.linatt_dkata_fwd_train(
+            P(q), P(k), P(v), P(beta), P(U), P(o), P(den), P(ws), B, T, H, D, D, M, 0.5, 0,
+            1e-5, dt, sp))
+        g = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
+             torch.empty(B, T, H, device="cuda")]
+        bws = torch.empty(L.linatt_dkata_bwd_workspace_bytes(B, T, H, D, D, dt), device="cuda",
+                          dtype=torch.uint8)
+        _lib.check("linatt_dkata_bwd", L.linatt_dkata_bwd(
+            P(q), P(k), P(v), P(beta), P(U), None, P(den), P(do), *(P(t) for t in g), P(ws),
+            P(bws), B, T, H, D, D, M, 0.5, 0, 1e-5, dt, sp))
+        outs.append([o, den] + g)
+        if with_u:
+            ref = F.flash_delta_U(q, k, v, beta, M, scale=0.5)
+            assert torch.equal(U, ref)
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
 def test_backward_fp16_raises(F):
     q, k, v, beta = make(1, 64, 1, 64, 64, torch.float16, 1)
     qd = q.cuda().requires_grad_(True)
