@@ -37,13 +37,14 @@ namespace linatt {
 // through LDS staging in the wave's own columns of the dO tiles.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
-__global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_state_bwd_kernel(DeltaArgs a,
+__global__ __launch_bounds__(state_threads<DV>()) void delta_state_bwd_kernel(DeltaArgs a,
                                                                                                 DeltaLayout L) {
   constexpr int SPLIT = state_split<DV>();
   constexpr int NDT = DK / 32, NW = DV / 32 / SPLIT;  // compute waves of this workgroup (+ one copy wave)
   constexpr int KT = DK / 64, VT = NW > 1 ? NW / 2 : 1;  // 64 x 64 tiles per row block (dO: this workgroup's)
   constexpr int TE = 64 * 64;                     // elements per tile
-  constexpr int OPW = 8;                          // 1 KiB copies per tile, all by the copy wave
+  constexpr int OPW = 8;                          // 1 KiB copies per tile, split over the copy waves
+  constexpr int OPC = OPW / kStateCopyWaves;      // per copy wave
   constexpr int NTILE = 3 * KT + 1 + VT;          // K, W^T, Qg, Aqk, dO
   constexpr int SLOT = NTILE * TE + 2 * 64 * 4 / (int)sizeof(T);  // + G and e^(gamma - G) of the chunk (f32)
   static_assert(VT >= 1, "tile split");
@@ -75,10 +76,12 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
   auto ot = [&](T* sl, int i) { return sl + (3 * KT + 1 + i) * TE; };  // dO columns 64 i..
   auto gs = [&](T* sl) { return reinterpret_cast<float*>(sl + NTILE * TE); };
 
-  // The copy wave (w == NW) issues every copy of the next chunk while the
+  // The copy waves (w >= NW) issue every copy of the next chunk while the
   // compute waves work on this one, so no compute wave stalls on copy
-  // issue.  Per-lane byte offsets of its copy ops (full chunks); the last
-  // chunk (rows past T clamped) takes the general path.
+  // issue; copy wave cw takes ops [OPC cw, OPC cw + OPC) of every tile.
+  // Per-lane byte offsets of its copy ops (full chunks); the last chunk
+  // (rows past T clamped) takes the general path.
+  const int cw = w - NW;
   auto issue = [&](int c) __attribute__((always_inline)) {
     T* sl = Sh + (c & 1) * SLOT;
     const int t0 = c * kChunk;
@@ -89,7 +92,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
     const T* atg = (const T*)(a.ctx + L.Aqk) + ci * 4096;
     if (t0 + 64 > Tn) {
 #pragma unroll
-      for (int op = 0; op < OPW; ++op) {
+      for (int op = OPC * cw; op < OPC * cw + OPC; ++op) {
 #pragma unroll
         for (int i = 0; i < KT; ++i) {
           dma_tile64<T>(kb + 64 * i, (int64_t)H * DK, t0, Tn, kt(sl, i), op, lane);
@@ -106,7 +109,7 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
       const T* qr = qb + (size_t)t0 * H * DK;
       const T* dr = dob + (size_t)t0 * H * DV;
 #pragma unroll
-      for (int op = 0; op < 8; ++op) {
+      for (int op = OPC * cw; op < OPC * cw + OPC; ++op) {
         const unsigned ok = tile_lane_off(op, lane, H * DK * (int)sizeof(T));
         const unsigned ow = tile_lane_off(op, lane, 64 * (int)sizeof(T));
         const unsigned oq = tile_lane_off(op, lane, DK * (int)sizeof(T));
@@ -123,11 +126,12 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
         for (int i = 0; i < VT; ++i) dma16s(dr + 64 * i, oo, reinterpret_cast<char*>(ot(sl, i)) + 1024 * op);
       }
     }
-    if (GATED && lane < 32)  // G (lanes 0-15), then e^(gamma - G) (lanes 16-31)
+    if (GATED && cw == 0 && lane < 32)  // G (lanes 0-15), then e^(gamma - G) (lanes 16-31)
       dma16((lane < 16 ? Gc : Fk) + t0 + 4 * (lane & 15), gs(sl));
   };
 
-  // staged outputs of chunk c: dh^T rows (ci DV + 32 gw) and dv_new^T rows
+  // staged outputs of chunk c: dh^T rows (ci DV + 32 gw) and dv_new^T rows;
+  // copy wave cw stores the blocks with index cw modulo the copy waves
   auto flush = [&](int c) __attribute__((always_inline)) {
     const size_t ci = (size_t)bh * NT + c;
 #pragma unroll
@@ -136,13 +140,15 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
       T* drows = (T*)(a.ws + L.dhT) + (ci * DV + 32 * g2) * DK;
 #pragma unroll
       for (int blk = 0; blk < NDT / 2; ++blk)
-        flush_rows<T>(Stg[c & 1][q * (NDT / 2 + 1) + blk], drows + 64 * blk, DK, lane);
-      flush_rows<T>(Stg[c & 1][q * (NDT / 2 + 1) + NDT / 2], (T*)(a.ws + L.dVnT) + (ci * DV + 32 * g2) * 64, 64,
-                    lane);
+        if ((q * (NDT / 2 + 1) + blk) % kStateCopyWaves == cw)
+          flush_rows<T>(Stg[c & 1][q * (NDT / 2 + 1) + blk], drows + 64 * blk, DK, lane);
+      if ((q * (NDT / 2 + 1) + NDT / 2) % kStateCopyWaves == cw)
+        flush_rows<T>(Stg[c & 1][q * (NDT / 2 + 1) + NDT / 2], (T*)(a.ws + L.dVnT) + (ci * DV + 32 * g2) * 64, 64,
+                      lane);
     }
   };
-  if (w == NW) {
-    // copy wave: chunk c is complete (vmcnt 0) before it reaches the
+  if (w >= NW) {
+    // copy waves: chunk c is complete (vmcnt 0) before they reach the
     // barrier that opens chunk c for the compute waves; the barrier also
     // closes chunk c + 1, whose slot then takes chunk c - 1 and whose
     // staged outputs this wave then stores (stores first, so waiting for
@@ -806,8 +812,8 @@ hipError_t launch_delta_bwd(const DeltaArgs& a, hipStream_t stream) {
   const int BH = a.B * a.H;
   hipError_t e = hipSuccess;
   if (a.stages & 1) {
-    delta_state_bwd_kernel<T, DK, DV, GATED><<<dim3(BH * state_split<DV>()),
-                                               dim3(64 * (DV / 32 / state_split<DV>() + 1)), 0, stream>>>(a, L);
+    delta_state_bwd_kernel<T, DK, DV, GATED><<<dim3(BH * state_split<DV>()), dim3(state_threads<DV>()), 0,
+                                               stream>>>(a, L);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   if (a.stages & 2) {

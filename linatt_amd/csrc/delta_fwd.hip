@@ -342,7 +342,7 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
 // ---------------------------------------------------------------------------
 
 template <typename T, int DK, int DV, bool GATED>
-__global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_state_fwd_kernel(
+__global__ __launch_bounds__(state_threads<DV>()) void delta_state_fwd_kernel(
     DeltaArgs a, DeltaLayout L, const float* __restrict__ gcum) {
   constexpr int SPLIT = state_split<DV>();
   constexpr int NDT = DK / 32, NW = DV / 32 / SPLIT;      // compute waves of this workgroup (+ one copy wave)
@@ -351,9 +351,13 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
   constexpr int WCPR = DK * (int)sizeof(T) / 16;         // chunks per W row
   constexpr int KCPR = 64 * (int)sizeof(T) / 16;         // chunks per Kd^T / U^T row
   constexpr int SLOT = 2 * WT16 + NW * UT16;             // W | Kd^T | U^T per chunk
-  constexpr int WOPS = WT16 / 64, UOPS = NW * UT16 / 64;  // 1 KiB copies per chunk (copy wave)
-  constexpr int DMA_PER_CHUNK = 2 * WOPS + UOPS;
-  static_assert(WOPS * 64 == WT16 && UOPS * 64 == NW * UT16 && DMA_PER_CHUNK <= 63, "tile split");
+  constexpr int WOPS = WT16 / 64, UOPS = NW * UT16 / 64;  // 1 KiB copies per chunk
+  constexpr int NCW = kStateCopyWaves;                     // copy waves, each a 1 / NCW share
+  constexpr int WOPC = WOPS / NCW, UOPC = UOPS / NCW;
+  constexpr int DMA_PER_CHUNK = (2 * WOPS + UOPS) / NCW;   // per copy wave
+  static_assert(WOPS * 64 == WT16 && UOPS * 64 == NW * UT16 && WOPC * NCW == WOPS && UOPC * NCW == UOPS &&
+                    8 % NCW == 0 && DMA_PER_CHUNK <= 63,
+                "tile split");
   __shared__ __attribute__((aligned(16))) u32x4 Sh[3 * SLOT];
   // per chunk (two buffers): the compute waves' v_new^T block and h^T blocks
   // (NDT / 2 each), staged for the copy wave's stores
@@ -372,9 +376,11 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
   // gcum = the Gc context buffer, passed on its own as __restrict__ so the
   // per-chunk gate is a scalar load (no vector-memory wait in the chain)
   const float* Gc = gcum + (size_t)bh * Tp;
-  // The copy wave (w == NW) issues every copy, two chunks ahead, into a ring
-  // of three slots; the compute waves never stall on copy issue.
-  if (w == NW) {
+  // The copy waves (w >= NW) issue every copy, two chunks ahead, into a ring
+  // of three slots; the compute waves never stall on copy issue.  Copy wave
+  // cw issues share cw of each tile's copies.
+  if (w >= NW) {
+    const int cw = w - NW;
     // wave-uniform byte bases of this head's W, Kd^T and this workgroup's
     // U^T rows; chunk c sits at + c * (bytes per chunk).  A 1 KiB copy op
     // covers tile chunks [64 op, 64 op + 64); slot lane of row r holds
@@ -388,11 +394,11 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
     auto issue = [&](int c) __attribute__((always_inline)) {
       u32x4* sl = Sh + (c % 3) * SLOT;
 #pragma unroll
-      for (int op = 0; op < WOPS; ++op)
+      for (int op = WOPC * cw; op < WOPC * cw + WOPC; ++op)
         dma16s(Wg + (size_t)c * WT16 * 16, 16u * swz_slot<WCPR>((64 * op + lane) / WCPR, lane % WCPR), sl + 64 * op);
       if constexpr (GATED) {
 #pragma unroll
-        for (int op = 0; op < WOPS; ++op)
+        for (int op = WOPC * cw; op < WOPC * cw + WOPC; ++op)
           dma16s(Kg + (size_t)c * WT16 * 16, 16u * swz_slot<KCPR>((64 * op + lane) / KCPR, lane % KCPR),
                  sl + WT16 + 64 * op);
       } else {
@@ -402,35 +408,38 @@ __global__ __launch_bounds__(64 * (DV / 32 / state_split<DV>() + 1)) void delta_
         const int t0 = c * kChunk;
         if (t0 + kChunk <= Tn) {
 #pragma unroll
-          for (int op = 0; op < 8; ++op)
+          for (int op = 8 / NCW * cw; op < 8 / NCW * (cw + 1); ++op)
 #pragma unroll
             for (int i = 0; i < DK / 64; ++i)
               dma16s(kb + (size_t)t0 * a.H * DK + 64 * i, tile_lane_off(op, lane, kbytes),
                      reinterpret_cast<char*>(kt + i * 4096) + 1024 * op);
         } else {
 #pragma unroll
-          for (int op = 0; op < 8; ++op)
+          for (int op = 8 / NCW * cw; op < 8 / NCW * (cw + 1); ++op)
 #pragma unroll
             for (int i = 0; i < DK / 64; ++i)
               dma_tile64<T>(kb + 64 * i, (int64_t)a.H * DK, t0, Tn, kt + i * 4096, op, lane);
         }
       }
 #pragma unroll
-      for (int op = 0; op < UOPS; ++op)
+      for (int op = UOPC * cw; op < UOPC * cw + UOPC; ++op)
         dma16s(Ug + (size_t)c * NW * SPLIT * UT16 * 16, 16u * swz_slot<KCPR>((64 * op + lane) / KCPR, lane % KCPR),
                sl + 2 * WT16 + 64 * op);
     };
-    // staged outputs of chunk c: v_new^T and h^T rows (ci DV + 32 g2)
+    // staged outputs of chunk c: v_new^T and h^T rows (ci DV + 32 g2); copy
+    // wave cw stores the blocks with index cw modulo the copy waves
     auto flush = [&](int c) __attribute__((always_inline)) {
       const size_t ci = (size_t)bh * NT + c;
 #pragma unroll
       for (int q = 0; q < NW; ++q) {
         const int g2 = gw - w + q;
-        flush_rows<T>(Stg[c & 1][q * (NDT / 2 + 1)], (T*)(a.ctx + L.VnT) + (ci * DV + 32 * g2) * 64, 64, lane);
+        if ((q * (NDT / 2 + 1)) % NCW == cw)
+          flush_rows<T>(Stg[c & 1][q * (NDT / 2 + 1)], (T*)(a.ctx + L.VnT) + (ci * DV + 32 * g2) * 64, 64, lane);
 #pragma unroll
         for (int blk = 0; blk < NDT / 2; ++blk)
-          flush_rows<T>(Stg[c & 1][q * (NDT / 2 + 1) + 1 + blk],
-                        (T*)(a.ctx + L.hT) + (ci * DV + 32 * g2) * DK + 64 * blk, DK, lane);
+          if ((q * (NDT / 2 + 1) + 1 + blk) % NCW == cw)
+            flush_rows<T>(Stg[c & 1][q * (NDT / 2 + 1) + 1 + blk],
+                          (T*)(a.ctx + L.hT) + (ci * DV + 32 * g2) * DK + 64 * blk, DK, lane);
       }
     };
     issue(0);
@@ -673,8 +682,8 @@ hipError_t launch_delta_fwd(const DeltaArgs& a, hipStream_t stream) {
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   if (a.stages & 2) {
-    delta_state_fwd_kernel<T, DK, DV, GATED><<<dim3(BH * state_split<DV>()),
-                                               dim3(64 * (DV / 32 / state_split<DV>() + 1)), 0, stream>>>(
+    delta_state_fwd_kernel<T, DK, DV, GATED><<<dim3(BH * state_split<DV>()), dim3(state_threads<DV>()), 0,
+                                               stream>>>(
         a, L, reinterpret_cast<const float*>(a.ctx + L.Gc));
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }

@@ -48,6 +48,12 @@ DeltaLayout delta_layout(int B, int T, int H, int DK, int DV, int elt_bytes);
 // compute wave per workgroup beats two and four.
 template <int DV>
 constexpr int state_split() { return DV / 32; }
+// Copy waves per workgroup of the state passes: one wave alone issues L2 ->
+// LDS copies at about a third of what a CU takes in (44 against 125 GB/s
+// per CU in a probe), so the copies of a chunk are split over two.
+constexpr int kStateCopyWaves = 2;
+template <int DV>
+constexpr int state_threads() { return 64 * (DV / 32 / state_split<DV>() + kStateCopyWaves); }
 
 struct DeltaArgs {
   // inputs
