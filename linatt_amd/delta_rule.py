@@ -18,9 +18,17 @@ both returning ``(o, final_state)``.  Layout is fla's default time-major
 ``1/sqrt(K)``; ``g`` is the per-token log decay (``<= 0``).  Gradients come
 back in each input's dtype.  Every computation runs in ``liblinatt_hip.so``
 (``linatt_delta_fwd`` / ``linatt_delta_bwd``, plus ``linatt_l2norm_*`` for
-``use_qk_l2norm_in_kernel``); variable-length batches (``cu_seqlens``) and
-float32 inputs raise, and so do ``head_first=True`` and any other keyword
-fla would accept but this build does not implement.
+``use_qk_l2norm_in_kernel``); float32 inputs raise, and so do
+``head_first=True`` and any other keyword fla would accept but this build
+does not implement.
+
+Variable-length batches follow fla's convention: ``B == 1``, the N sequences
+packed along T with offsets ``cu_seqlens`` ``(N + 1,)``, ``initial_state``
+and the final state ``(N, H, K, V)``.  The sequences are laid out as the N
+rows of a right-padded batch (on the GPU, by one index copy) and run through
+the same kernels: the padding has beta = 0, g = 0 and zero q, k, v, so the
+state passes through it unchanged, the final state of each row is that
+sequence's own, and nothing flows back from it.
 """
 
 from __future__ import annotations
@@ -161,15 +169,52 @@ def _check_kwargs(fn, kwargs):
         raise TypeError(f"{fn}: unexpected keyword arguments {sorted(kwargs)}")
 
 
+def _seq_layout(cu_seqlens, T, device):
+    """Row-major positions in the padded ``(N, Tmax)`` batch of the T packed
+    tokens, from fla-style offsets ``cu_seqlens`` ``(N + 1,)``."""
+    cu = torch.as_tensor(cu_seqlens).to("cpu", torch.int64)
+    if cu.dim() != 1 or cu.numel() < 2:
+        raise ValueError("cu_seqlens must be a 1-D tensor of N + 1 offsets")
+    lens = cu[1:] - cu[:-1]
+    if int(cu[0]) != 0 or int(cu[-1]) != T or bool((lens < 0).any()):
+        raise ValueError(f"cu_seqlens must rise from 0 to T = {T}, got {cu.tolist()}")
+    N, Tmax = lens.numel(), int(lens.max())
+    if Tmax == 0:
+        raise ValueError("cu_seqlens describes only empty sequences")
+    seq = torch.repeat_interleave(torch.arange(N), lens)
+    dst = seq * Tmax + torch.arange(T) - cu[:-1][seq]
+    return dst.to(device), N, Tmax
+
+
+def _run_varlen(q, k, v, beta, g, scale, initial_state, output_final_state, cu_seqlens):
+    B, T, H, K = q.shape
+    if B != 1:
+        raise ValueError(f"cu_seqlens needs the sequences packed into B = 1, got B = {B}")
+    dst, N, Tmax = _seq_layout(cu_seqlens, T, q.device)
+    if initial_state is not None and initial_state.shape[0] != N:
+        raise ValueError(f"initial_state must hold N = {N} states, got {tuple(initial_state.shape)}")
+
+    def pad(x):  # (1, T, ...) -> (N, Tmax, ...), zeros in the padding
+        z = x.new_zeros((N * Tmax,) + tuple(x.shape[2:]))
+        return z.index_copy(0, dst, x[0]).reshape((N, Tmax) + tuple(x.shape[2:]))
+
+    o, ht = ChunkDeltaRuleFunction.apply(pad(q), pad(k), pad(v), pad(beta),
+                                         pad(g) if g is not None else None, scale,
+                                         initial_state, output_final_state)
+    o = o.reshape((N * Tmax,) + tuple(o.shape[2:])).index_select(0, dst).unsqueeze(0)
+    return o, ht
+
+
 def _run(q, k, v, beta, g, scale, initial_state, output_final_state, cu_seqlens,
          use_qk_l2norm_in_kernel):
-    if cu_seqlens is not None:
-        raise NotImplementedError("linatt_amd delta rule: cu_seqlens (varlen) is not supported")
     _check_inputs(q, k, v, beta, g)
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
     if use_qk_l2norm_in_kernel:
         q, k = l2norm(q), l2norm(k)
+    if cu_seqlens is not None:
+        return _run_varlen(q, k, v, beta, g, scale, initial_state, output_final_state,
+                           cu_seqlens)
     return ChunkDeltaRuleFunction.apply(q, k, v, beta, g, scale, initial_state,
                                         output_final_state)
 

@@ -121,6 +121,50 @@ def test_l2norm_in_kernel(R):
     check(out, ref, 2e-2)
 
 
+@pytest.mark.parametrize("gated", [False, True], ids=["delta", "gated"])
+def test_varlen_cu_seqlens(R, gated):
+    """fla's variable-length form: N sequences packed into B = 1 with offsets
+    ``cu_seqlens`` and one initial / final state each.  Every sequence is
+    checked against the oracle run on it alone; an empty sequence keeps its
+    initial state, and its state gradient passes straight through."""
+    lens = [37, 128, 0, 1, 200, 64]
+    N, T, H, K = len(lens), sum(lens), 2, 64
+    dtype = torch.bfloat16
+    q, k, v, beta, g, _, do, _ = make(1, T, H, K, K, dtype, 91, gated, False, False)
+    S0 = gen((N, H, K, K), 95, 0.02)
+    dS = gen((N, H, K, K), 96)
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    dev = torch.device("cuda")
+    leaves = {"q": q, "k": k, "v": v, "beta": beta, "h0": S0}
+    if gated:
+        leaves["g"] = g
+    L = {n: t.to(dev).requires_grad_(True) for n, t in leaves.items()}
+    kw = dict(initial_state=L["h0"], output_final_state=True,
+              cu_seqlens=torch.tensor(cu, device=dev, dtype=torch.int32))
+    if gated:
+        o, ht = R.chunk_gated_delta_rule(L["q"], L["k"], L["v"], L["g"], L["beta"], **kw)
+    else:
+        o, ht = R.chunk_delta_rule(L["q"], L["k"], L["v"], L["beta"], **kw)
+    assert o.shape == (1, T, H, K) and ht.shape == (N, H, K, K)
+    ((o.float() * do.to(dev).float()).sum() + (ht * dS.to(dev)).sum()).backward()
+    for n in range(N):
+        a, b = cu[n], cu[n + 1]
+        print(f"varlen sequence {n}: tokens {a}..{b}", flush=True)
+        if a == b:
+            assert torch.equal(ht[n].detach().cpu(), S0[n])
+            assert torch.equal(L["h0"].grad[n].cpu(), dS[n])
+            continue
+        ref = D.delta_rule_fwd_bwd(q[:, a:b], k[:, a:b], v[:, a:b], beta[:, a:b],
+                                   g[:, a:b] if gated else None, None, S0[n:n + 1],
+                                   do[:, a:b], dS[n:n + 1])
+        got = {"o": o[:, a:b], "ht": ht[n:n + 1], "dh0": L["h0"].grad[n:n + 1]}
+        for nm in ("q", "k", "v", "beta") + (("g",) if gated else ()):
+            got["d" + nm] = L[nm].grad[:, a:b]
+        check(got, ref, TOL[dtype])
+
+
 def test_steep_decay(R):
     """g far below zero: exp(G) underflows within a chunk; no inf/nan."""
     B, T, H, K = 1, 200, 2, 64
@@ -195,8 +239,12 @@ def test_rejects_unsupported(R):
     with pytest.raises(TypeError, match="no kernel"):
         R.chunk_delta_rule(q, q, q, beta)
     qb = q.bfloat16()
-    with pytest.raises(NotImplementedError, match="cu_seqlens"):
-        R.chunk_delta_rule(qb, qb, qb, beta, cu_seqlens=torch.tensor([0, 8], device=dev))
+    with pytest.raises(ValueError, match="cu_seqlens"):  # offsets must end at T
+        R.chunk_delta_rule(qb, qb, qb, beta, cu_seqlens=torch.tensor([0, 7], device=dev))
+    with pytest.raises(ValueError, match="B = 1"):
+        q2 = qb.expand(2, 8, 1, 64).contiguous()
+        R.chunk_delta_rule(q2, q2, q2, beta.expand(2, 8, 1).contiguous(),
+                           cu_seqlens=torch.tensor([0, 8], device=dev))
 
 
 @pytest.mark.parametrize("gated", [False, True], ids=["deltanet", "gdn"])
