@@ -216,6 +216,18 @@ int linatt_kata_prefill_state(const void* q, const void* k, const void* v, void*
                               float scale, float eps, int seg_len, int head_major, int dtype,
                               void* stream);
 
+/* The linear feature of the same tree-scan, spd_chunk_scan_cat(...,
+ * feature="linear") (kata/spd/chunk_scan_cat.py:219-345): psi(x) =
+ * sqrt(scale) x per group, so kappa(q, k) = scale (q . k) whatever the group
+ * split, den_t = max(sum_{s<=t} kappa(q_t, k_s), eps) (it may be negative
+ * before the clamp) and o_t = sum_{s<=t} kappa(q_t, k_s) v_s / den_t.
+ * Head-major q, k (B,H,T,d), v, o (B,H,T,dv) [dtype], den (B,H,T) float32;
+ * d = dv = 64, bf16 or fp16.  A chunked state pass (64-token chunks, state
+ * k^T v in float32, one workgroup per (b, h)). */
+int linatt_linear_scan_fwd(const void* q, const void* k, const void* v, void* o, float* den, int B,
+                           int H, int T, int d, int dv, float scale, float eps, int dtype,
+                           void* stream);
+
 /* One recurrent decode token per (b, h): S += psi(sqrt(scale) k) v^T,
  * z += psi(sqrt(scale) k), o = psi(sqrt(scale) q)^T S / max(psi(sqrt(scale) q).z, eps).
  * q, k (B,H,dk), v, o (B,H,dv); S, z updated in place.  No reference

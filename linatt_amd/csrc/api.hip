@@ -471,6 +471,29 @@ int linatt_rope(const void* x, void* y, int B, int T, int H, int D, int rot_dim,
   return LINATT_OK;
 }
 
+int linatt_linear_scan_fwd(const void* q, const void* k, const void* v, void* o, float* den, int B,
+                           int H, int T, int d, int dv, float scale, float eps, int dtype,
+                           void* stream) {
+  g_last_error.clear();
+  const char* fn = "linatt_linear_scan_fwd";
+  if (B <= 0 || T <= 0 || H <= 0 || d <= 0 || dv <= 0)
+    return fail(LINATT_EINVAL, std::string(fn) + ": non-positive size");
+  if ((int64_t)B * H * (T + 63) > (int64_t)INT32_MAX / 2)
+    return fail(LINATT_EINVAL, std::string(fn) + ": B*H*T too large");
+  if (!(scale > 0.f) || !(eps > 0.f)) return fail(LINATT_EINVAL, std::string(fn) + ": scale and eps must be positive");
+  if (d != 64 || dv != 64 || (dtype != LINATT_BFLOAT16 && dtype != LINATT_FLOAT16))
+    return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": compiled for d = dv = 64, bfloat16 / float16");
+  if (!q || !k || !v || !o || !den) return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+    return fail(LINATT_EINVAL, std::string(fn) + ": tensors must be 16-byte aligned");
+  const hipError_t e =
+      dtype == LINATT_BFLOAT16
+          ? launch_linear_scan<__bf16>(q, k, v, o, den, B, H, T, scale, eps, (hipStream_t)stream)
+          : launch_linear_scan<_Float16>(q, k, v, o, den, B, H, T, scale, eps, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
 static int check_rms(const char* fn, int n, int d, int dtype) {
   if (n <= 0 || d <= 0) return fail(LINATT_EINVAL, std::string(fn) + ": non-positive size");
   if (d % 8 || !pow2(d / 8) || d > 512)

@@ -46,6 +46,12 @@ template <typename T>
 hipError_t launch_rope(const void* x, void* y, int B, int T_, int H, int D, int rot_dim, float base,
                        int offset, int interleaved, int inverse, hipStream_t stream);
 
+// Causal linear attention, chunked state form (linear_scan.hip); head-major,
+// D = DV = 64, 16-bit types.
+template <typename T>
+hipError_t launch_linear_scan(const void* q, const void* k, const void* v, void* o, float* den, int B,
+                              int H, int T_, float scale, float eps, hipStream_t stream);
+
 // Sets the calling thread's linatt_last_error() message and returns code
 // (defined with the C-ABI entry points in api.hip).
 int set_last_error(int code, const char* msg);

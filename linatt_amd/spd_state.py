@@ -5,8 +5,10 @@ recurrent decode step.
   the signature of the reference's concat tree-scan
   (``kata/spd/chunk_scan_cat.py:219-345``): head-major ``(B, H, T, D)``
   inputs, returns ``(o, den)`` with ``o = num / max(den, eps)``.  ``C``,
-  ``warps`` and ``stages`` are accepted and ignored; ``feature`` must be
-  ``"quad"``.
+  ``warps`` and ``stages`` are accepted and ignored.  ``feature="quad"`` (the
+  SPD kernel) runs the state-form prefill below; ``feature="linear"``
+  (psi(x) = x, kappa = scale q.k) runs ``linatt_linear_scan_fwd``, a chunked
+  linear-attention state pass (d = dv = 64).
 * ``kata_prefill(q, k, v, num_groups=4, scale=None, eps=1e-6, seg_len=1024,
   initial_state=None)`` takes the time-major ``(B, T, H, D)`` layout of the
   flash path, optionally continues from a state ``(S0, z0)``, and also
@@ -20,7 +22,8 @@ recurrent decode step.
   is the state the ``past_key_values`` cache would hold.
 
 All three run in ``liblinatt_hip.so`` (``linatt_kata_prefill_state``,
-``linatt_kata_decode_step``); unsupported shapes raise.
+``linatt_linear_scan_fwd``, ``linatt_kata_decode_step``); unsupported shapes
+raise.
 """
 
 from __future__ import annotations
@@ -99,9 +102,34 @@ def spd_chunk_scan_cat(q, k, v, M, scale=None, C=32, eps=1e-6, warps=4, stages=N
                        feature="quad"):
     """Concat-SPD causal forward in state form, head-major ``(B, H, T, D)``
     (reference ``kata/spd/chunk_scan_cat.py:219-345``).  Returns ``(o, den)``."""
+    if feature == "linear":
+        return _linear_scan(q, k, v, M, scale, eps)
     if feature != "quad":
-        raise NotImplementedError("linatt_amd: only feature='quad' (psi = vec(x x^T))")
+        raise ValueError(f"spd_chunk_scan_cat: feature must be 'quad' or 'linear', got {feature!r}")
     o, den, _, _ = _prefill(q, k, v, M, scale, eps, 1024, True, False)
+    return o, den
+
+
+def _linear_scan(q, k, v, M, scale, eps):
+    """``feature="linear"`` of the tree-scan (``kata/spd/chunk_scan_cat.py:
+    90-92, 219-235``): kappa = scale q.k, head-major ``(B, H, T, D)``."""
+    _lib.require_device(q, k, v)
+    B, H, T, D = q.shape
+    dv = v.shape[-1]
+    if k.shape != q.shape or v.shape[:3] != (B, H, T):
+        raise ValueError(f"q, k must be (B, H, T, D) and v (B, H, T, dv); got q {tuple(q.shape)}, "
+                         f"k {tuple(k.shape)}, v {tuple(v.shape)}")
+    if D % M:
+        raise ValueError(f"D={D} not divisible by M={M}")
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.bfloat16, torch.float16):
+        raise NotImplementedError(f"linatt_amd linear scan: bfloat16 / float16 only, got {q.dtype}")
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    o = torch.empty(B, H, T, dv, device=q.device, dtype=q.dtype)
+    den = torch.empty(B, H, T, device=q.device, dtype=torch.float32)
+    L = _lib.load()
+    _lib.check("linatt_linear_scan_fwd", L.linatt_linear_scan_fwd(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(den), B, H, T, D, dv,
+        _scale(D, M, scale), float(eps), _lib.dtype_code(q.dtype), _lib.stream_of(q)))
     return o, den
 
 

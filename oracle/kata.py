@@ -311,25 +311,33 @@ def kata_decode_step(S, z, q, k, v, num_groups=4, scale=None, eps=1e-6):
     return num / den[..., None], S, z
 
 
-def kata_prefill_fwd_state_form(q, k, v, num_groups=4, scale=None, chunk=64, eps=1e-6):
+def psi_features(x, num_groups, feature="quad"):
+    """The tree-scan's feature map (``kata/spd/chunk_scan_cat.py:90-98``):
+    ``"quad"`` is psi(x) = vec(x_g x_g^T) per group, ``"linear"`` psi(x) = x_g,
+    which concatenated over the groups is x itself."""
+    return spd_full(x, num_groups) if feature == "quad" else x
+
+
+def kata_prefill_fwd_state_form(q, k, v, num_groups=4, scale=None, chunk=64, eps=1e-6,
+                                feature="quad"):
     """Chunked O(T) prefill output ``(o, den)`` in the state form (float64):
     per chunk, inter-chunk ``psi(sq) S_prev`` plus the intra-chunk causal
     block, normalised with the EPS floor of ``chunk_scan_cat.py:188-191``.
-    Returns also the final ``(S, z)``.
+    Returns also the final ``(S, z)``.  ``feature`` as ``psi_features``.
     """
     B, T, H, D = q.shape
     if scale is None:
         scale = default_scale(D, num_groups)
     s = math.sqrt(scale)
     q, k, v = (x.to(F64) for x in (q, k, v))
-    P = num_groups * (D // num_groups) ** 2
+    P = num_groups * (D // num_groups) ** 2 if feature == "quad" else D
     S = torch.zeros(B, H, P, v.shape[-1], dtype=F64, device=q.device)
     z = torch.zeros(B, H, P, dtype=F64, device=q.device)
     outs, dens = [], []
     for c0 in range(0, T, chunk):
         qc, kc, vc = q[:, c0:c0 + chunk], k[:, c0:c0 + chunk], v[:, c0:c0 + chunk]
-        pq = spd_full(qc * s, num_groups)  # (B,C,H,P)
-        pk = spd_full(kc * s, num_groups)
+        pq = psi_features(qc * s, num_groups, feature)  # (B,C,H,P)
+        pk = psi_features(kc * s, num_groups, feature)
         Cn = qc.shape[1]
         A = torch.einsum("bthp,bshp->bhts", pq, pk) * torch.tril(
             torch.ones(Cn, Cn, dtype=F64, device=q.device))
@@ -341,3 +349,15 @@ def kata_prefill_fwd_state_form(q, k, v, num_groups=4, scale=None, chunk=64, eps
         S = S + torch.einsum("bshp,bshv->bhpv", pk, vc)
         z = z + pk.sum(1)
     return torch.cat(outs, 1), torch.cat(dens, 1), S, z
+
+
+def linear_attn_dense(q, k, v, scale, eps=1e-6):
+    """Dense causal form of the tree-scan's linear feature (float64,
+    time-major ``(B, T, H, D)``): kappa = scale q.k, den_t = max(sum_{s<=t}
+    kappa, eps) (``kata/spd/chunk_scan_cat.py:188-191``), o = num / den."""
+    q, k, v = (x.to(F64) for x in (q, k, v))
+    T = q.shape[1]
+    A = scale * torch.einsum("bthd,bshd->bhts", q, k) * torch.tril(torch.ones(T, T, dtype=F64))
+    num = torch.einsum("bhts,bshv->bthv", A, v)
+    den = torch.clamp(A.sum(-1).transpose(1, 2), min=eps)
+    return num / den[..., None], den

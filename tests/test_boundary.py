@@ -120,7 +120,8 @@ def test_delta_rule_refuses_head_first_and_unknown_kwargs(fn):
         op(*args, head_first=True)
     with pytest.raises(TypeError, match="unexpected keyword"):
         op(*args, chunk_size=32)
-    with pytest.raises(NotImplementedError, match="cu_seqlens"):
+    # varlen takes the same device check as every call: no CPU path
+    with pytest.raises(RuntimeError, match="no CPU path"):
         op(*args, cu_seqlens=torch.tensor([0, 8]))
 
 

@@ -90,6 +90,47 @@ def test_head_major_scan_cat(S_):
     assert mar(den.transpose(1, 2), den_ref) < TOL
 
 
+@pytest.mark.parametrize("T", [1, 37, 64, 129, 700])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_scan_cat_linear_feature(S_, T, dtype):
+    """spd_chunk_scan_cat(feature="linear") (linatt_linear_scan_fwd) against the
+    float64 dense causal form.  q and k have a positive mean so that every
+    den stays far above the eps clamp: near a zero den the output amplifies
+    rounding without bound, in the reference too."""
+    B, H, M = 2, 3, 4
+    g = torch.Generator().manual_seed(T)
+    q = (torch.randn(B, T, H, 64, generator=g) * 0.125 + 0.1).to(dtype)
+    k = (torch.randn(B, T, H, 64, generator=g) * 0.125 + 0.1).to(dtype)
+    v = torch.randn(B, T, H, 64, generator=g).to(dtype)
+    print(f"\nlinear scan T={T} {dtype}", flush=True)
+    o_ref, den_ref = K.linear_attn_dense(q, k, v, 1 / math.sqrt(64 // M))
+    dev = torch.device("cuda")
+    hm = lambda x: x.transpose(1, 2).contiguous().to(dev)  # noqa: E731
+    o, den = S_.spd_chunk_scan_cat(hm(q), hm(k), hm(v), M, feature="linear")
+    assert o.dtype == dtype and o.shape == (B, H, T, 64) and den.shape == (B, H, T)
+    tol = TOL if dtype == BF else 1e-2
+    assert mar(o.transpose(1, 2), o_ref) < tol, mar(o.transpose(1, 2), o_ref)
+    assert mar(den.transpose(1, 2), den_ref) < 1e-3, mar(den.transpose(1, 2), den_ref)
+
+
+def test_scan_cat_linear_clamp(S_):
+    """Every q.k negative: den is the eps floor and o = num / eps (bf16: the
+    outputs reach ~1e5, past fp16's range)."""
+    B, T, H = 1, 150, 2
+    g = torch.Generator().manual_seed(5)
+    q = (-0.1 * (1 + 0.1 * torch.rand(B, T, H, 64, generator=g))).to(BF)
+    k = (0.1 * (1 + 0.1 * torch.rand(B, T, H, 64, generator=g))).to(BF)
+    v = torch.randn(B, T, H, 64, generator=g).to(BF)
+    eps = 1e-4
+    o_ref, den_ref = K.linear_attn_dense(q, k, v, 0.25, eps)
+    assert (den_ref == eps).all()
+    dev = torch.device("cuda")
+    hm = lambda x: x.transpose(1, 2).contiguous().to(dev)  # noqa: E731
+    o, den = S_.spd_chunk_scan_cat(hm(q), hm(k), hm(v), 4, eps=eps, feature="linear")
+    assert (den == eps).all()
+    assert mar(o.transpose(1, 2), o_ref) < TOL
+
+
 @pytest.mark.parametrize("M", [4, 2])
 def test_decode_equals_parallel_row(S_, M):
     """Decode after an n-token prefill == row n of the dense parallel form."""

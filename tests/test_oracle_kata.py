@@ -320,3 +320,31 @@ def test_decay_brute_force_non_monotone_c():
     # plausible mistakes are visible at this size: no clamp, or no decay at all
     assert (_brute_decay(q, k, v, c, M, scale, clamp=False) - want).abs().max() > 1e-3
     assert (K.kata_fwd(q, k, v, M, scale, "concat")[0] - want).abs().max() > 1e-3
+
+
+def test_linear_feature():
+    """The tree-scan's linear feature (``kata/spd/chunk_scan_cat.py:90-92``):
+    the chunked state form equals the dense causal form and a token-by-token
+    loop, the group split drops out, and den is clamped at eps (where it is
+    negative, o = num / eps)."""
+    B, T, H, D, dv = 1, 50, 2, 8, 4
+    q, k, v = _rand((B, T, H, D), 41), _rand((B, T, H, D), 42), _rand((B, T, H, dv), 43)
+    scale, eps = 0.3, 1e-6
+    o_d, den_d = K.linear_attn_dense(q, k, v, scale, eps)
+    assert (den_d == eps).any() and (den_d > eps).any()  # both sides of the clamp occur
+    for M, C in ((1, 64), (2, 7), (4, 16)):
+        o_s, den_s, S, z = K.kata_prefill_fwd_state_form(q, k, v, M, scale, C, eps, feature="linear")
+        torch.testing.assert_close(o_s, o_d)
+        torch.testing.assert_close(den_s, den_d)
+        assert S.shape == (B, H, D, dv) and z.shape == (B, H, D)
+    # token-by-token: S_t = S_{t-1} + k_t v_t^T, z_t = z_{t-1} + k_t
+    for b in range(B):
+        for h in range(H):
+            St = torch.zeros(D, dv, dtype=F64)
+            zt = torch.zeros(D, dtype=F64)
+            for t in range(T):
+                St = St + torch.outer(k[b, t, h], v[b, t, h])
+                zt = zt + k[b, t, h]
+                dn = max(scale * float(q[b, t, h] @ zt), eps)
+                torch.testing.assert_close(den_d[b, t, h], torch.tensor(dn, dtype=F64))
+                torch.testing.assert_close(o_d[b, t, h], scale * (q[b, t, h] @ St) / dn)
