@@ -547,6 +547,17 @@ __device__ __forceinline__ void stage_rows(const f32x16& x0, const f32x16& x1, u
   }
 }
 
+// One half of stage_rows: the 32 x 32 block x as columns 32 b .. 32 b + 31
+// of the 32 x 64 staged block (the other half is another wave's).
+template <typename T>
+__device__ __forceinline__ void stage_half(const f32x16& x, int b, u32x4* stage, int lane) {
+  const int cl = lane & 31, hh = lane >> 5;
+#pragma unroll
+  for (int I = 0; I < 4; ++I)
+    *reinterpret_cast<v4_t<T>*>(reinterpret_cast<char*>(stage + swz_slot<8>(cl, 4 * b + I)) + 8 * hh) =
+        to4<T>(x[4 * I], x[4 * I + 1], x[4 * I + 2], x[4 * I + 3]);
+}
+
 // A wave's 32 x 32 block of 16-bit values in C layout (lane column = block
 // row cl; columns 8 I + 4 hh + r) through 2 KiB of LDS (128 16-byte slots,
 // row-major 32 x 4, XOR-swizzled by row) to rows g + row * ld: 8-byte LDS

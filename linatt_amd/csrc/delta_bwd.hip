@@ -24,35 +24,52 @@
 namespace linatt {
 
 // ---------------------------------------------------------------------------
-// Kernel 1: reverse state pass.  One workgroup per (b, h), one wave per 32
-// value columns, dS in DK/32 accumulator tiles (lane column v).  Per chunk,
-// with dS' the gradient of the state leaving it:
+// Kernel 1: reverse state pass.  One workgroup per (b, h, 32 value columns):
+// two compute waves and the copy waves.  Per chunk, with dS' the gradient
+// of the state leaving it:
 //   dVn = Aqk^T dO + diag(e^(gamma-G)) K dS'
 //   dS  = e^gamma dS' + (scale e^G Q)^T dO - W^T dVn
-// K, W^T, Qg = scale e^G Q, Aqk, dO and G of a chunk are shared by the
-// waves of the head: they reach LDS by direct global->LDS copies (swizzled
-// 64 x 64 tiles, see tile_slot) into two slots, the earlier chunk's copies
-// in flight while the current one computes; Qg^T and Aqk^T operands come
-// from transposing reads.  dh^T and dv_new^T leave
-// through LDS staging in the wave's own columns of the dO tiles.
+// Compute wave p holds dS key-dim blocks ND2 p .. ND2 p + ND2 - 1 in MFMA
+// accumulators and forms dVn for the chunk rows 32 p .. 32 p + 31.  The
+// two trade 16-bit operand images through LDS: each wave's dS blocks (for
+// the other's K dS' product, written at the end of the previous chunk) and
+// its dVn rows (for the other's W^T dVn product, before the mid-chunk
+// barrier).  K, W, Qg (ungated: q), Aqk, dO and G of a chunk reach LDS by
+// direct global->LDS copies (swizzled 64 x 64 tiles, see tile_slot) into
+// two slots, issued by the copy waves one chunk ahead; dh^T and dv_new^T
+// leave through LDS staging, stored by the copy waves one chunk later.
+//
+// Barriers per chunk c (every wave): TOP (chunk c landed; the dS images of
+// chunk c are written; chunk c + 1's slot and staged outputs are free) and
+// MID (every ring read and dS-image read of chunk c is done, the dVn images
+// are written, and the copy waves have read chunk c + 1's staged outputs).
+// The dS images of chunk c live in the staging buffer of chunk c, which is
+// free from TOP until the outputs of chunk c are staged after MID.
 // ---------------------------------------------------------------------------
+constexpr int kStateBwdComputeWaves = 2;
+constexpr int state_bwd_threads() { return 64 * (kStateBwdComputeWaves + kStateCopyWaves); }
+
 template <typename T, int DK, int DV, bool GATED>
-__global__ __launch_bounds__(state_threads<DV>()) void delta_state_bwd_kernel(DeltaArgs a,
-                                                                                                DeltaLayout L) {
-  constexpr int SPLIT = state_split<DV>();
-  constexpr int NDT = DK / 32, NW = DV / 32 / SPLIT;  // compute waves of this workgroup (+ one copy wave)
-  constexpr int KT = DK / 64, VT = NW > 1 ? NW / 2 : 1;  // 64 x 64 tiles per row block (dO: this workgroup's)
+__global__ __launch_bounds__(state_bwd_threads()) void delta_state_bwd_kernel(DeltaArgs a, DeltaLayout L) {
+  constexpr int SPLIT = DV / 32;                  // workgroups per head, 32 value columns each
+  constexpr int NDT = DK / 32, ND2 = NDT / 2;     // dS key-dim blocks: all, per compute wave
+  constexpr int NCW = kStateBwdComputeWaves;
+  constexpr int KT = DK / 64;                     // 64 x 64 tiles per row block
   constexpr int TE = 64 * 64;                     // elements per tile
   constexpr int OPW = 8;                          // 1 KiB copies per tile, split over the copy waves
   constexpr int OPC = OPW / kStateCopyWaves;      // per copy wave
-  constexpr int NTILE = 3 * KT + 1 + VT;          // K, W^T, Qg, Aqk, dO
+  constexpr int NTILE = 3 * KT + 2;               // K, W, Qg, Aqk, dO (the 64 columns holding ours)
   constexpr int SLOT = NTILE * TE + 2 * 64 * 4 / (int)sizeof(T);  // + G and e^(gamma - G) of the chunk (f32)
-  static_assert(VT >= 1, "tile split");
+  static_assert(NDT % 2 == 0 && NCW == 2, "key dims split over two compute waves");
   __shared__ __attribute__((aligned(16))) T Sh[2 * SLOT];
-  // per chunk (two buffers): this workgroup's compute waves' dh^T blocks
-  // (NDT / 2 each) and dv_new^T block, staged for the copy wave's stores
-  constexpr int NSTG = NW * (NDT / 2 + 1);
+  // per chunk (two buffers): the dh^T blocks (64 key dims each) and the
+  // dv_new^T block of the 32 columns, staged for the copy waves' stores;
+  // also the home of the chunk's dS images (2 ND2 * 128 slots, before MID)
+  constexpr int NSTG = NDT / 2 + 1;
   __shared__ __attribute__((aligned(16))) u32x4 Stg[2][NSTG][256];
+  static_assert(2 * ND2 * 128 <= (NSTG - 1) * 256, "dS images fit below the dv_new^T block");
+  // dVn images: -dVn rows of compute wave p as B operands (k-steps j = 0, 1)
+  __shared__ __attribute__((aligned(16))) u32x4 Xv[NCW][2][64];
 
   const int lane = threadIdx.x & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -60,12 +77,11 @@ __global__ __launch_bounds__(state_threads<DV>()) void delta_state_bwd_kernel(De
   const int BH = a.B * H;
   const int bh = blockIdx.x % BH, part = blockIdx.x / BH;
   const int b = bh / H, h = bh % H;
-  const int gw = part * NW + w;  // this wave's 32-column block of the head
-  const int v = 32 * gw + cl;
+  const int v = 32 * part + cl;
   const size_t Tp = (size_t)NT * kChunk;
 
   const T* kb = (const T*)a.k + ((size_t)b * Tn * H + h) * DK;
-  const T* dob = (const T*)a.dout + ((size_t)b * Tn * H + h) * DV + 64 * ((part * NW) / 2);  // this workgroup's columns
+  const T* dob = (const T*)a.dout + ((size_t)b * Tn * H + h) * DV + 64 * (part / 2);  // the 64 columns holding ours
   const float* Gc = reinterpret_cast<const float*>(a.ctx + L.Gc) + (size_t)bh * Tp;
   const float* Fk = reinterpret_cast<const float*>(a.ctx + L.Fk) + (size_t)bh * Tp;
 
@@ -73,15 +89,13 @@ __global__ __launch_bounds__(state_threads<DV>()) void delta_state_bwd_kernel(De
   auto wt = [&](T* sl, int i) { return sl + (KT + i) * TE; };          // W [i][d], key dims 64 i..
   auto qt = [&](T* sl, int i) { return sl + (2 * KT + i) * TE; };      // Qg key dims 64 i..
   auto at = [&](T* sl) { return sl + 3 * KT * TE; };                   // Aqk
-  auto ot = [&](T* sl, int i) { return sl + (3 * KT + 1 + i) * TE; };  // dO columns 64 i..
+  auto ot = [&](T* sl) { return sl + (3 * KT + 1) * TE; };             // dO
   auto gs = [&](T* sl) { return reinterpret_cast<float*>(sl + NTILE * TE); };
 
-  // The copy waves (w >= NW) issue every copy of the next chunk while the
-  // compute waves work on this one, so no compute wave stalls on copy
-  // issue; copy wave cw takes ops [OPC cw, OPC cw + OPC) of every tile.
-  // Per-lane byte offsets of its copy ops (full chunks); the last chunk
-  // (rows past T clamped) takes the general path.
-  const int cw = w - NW;
+  // copy wave cw takes ops [OPC cw, OPC cw + OPC) of every tile, i.e. tile
+  // rows [8 OPC cw, 8 OPC cw + 8 OPC); per-lane byte offsets for full
+  // chunks, the general path for the last one (rows past T clamped)
+  const int cw = w - NCW;
   auto issue = [&](int c) __attribute__((always_inline)) {
     T* sl = Sh + (c & 1) * SLOT;
     const int t0 = c * kChunk;
@@ -101,8 +115,7 @@ __global__ __launch_bounds__(state_threads<DV>()) void delta_state_bwd_kernel(De
           else dma_tile64<T>(qb + 64 * i, (int64_t)H * DK, t0, Tn, qt(sl, i), op, lane);
         }
         dma_tile64<T>(atg, 64, 0, 64, at(sl), op, lane);
-#pragma unroll
-        for (int i = 0; i < VT; ++i) dma_tile64<T>(dob + 64 * i, (int64_t)H * DV, t0, Tn, ot(sl, i), op, lane);
+        dma_tile64<T>(dob, (int64_t)H * DV, t0, Tn, ot(sl), op, lane);
       }
     } else {
       const T* kr = kb + (size_t)t0 * H * DK;
@@ -122,200 +135,205 @@ __global__ __launch_bounds__(state_threads<DV>()) void delta_state_bwd_kernel(De
           else dma16s(qr + 64 * i, ok, reinterpret_cast<char*>(qt(sl, i)) + 1024 * op);
         }
         dma16s(atg, ow, reinterpret_cast<char*>(at(sl)) + 1024 * op);
-#pragma unroll
-        for (int i = 0; i < VT; ++i) dma16s(dr + 64 * i, oo, reinterpret_cast<char*>(ot(sl, i)) + 1024 * op);
+        dma16s(dr, oo, reinterpret_cast<char*>(ot(sl)) + 1024 * op);
       }
     }
     if (GATED && cw == 0 && lane < 32)  // G (lanes 0-15), then e^(gamma - G) (lanes 16-31)
       dma16((lane < 16 ? Gc : Fk) + t0 + 4 * (lane & 15), gs(sl));
   };
 
-  // staged outputs of chunk c: dh^T rows (ci DV + 32 gw) and dv_new^T rows;
+  // staged outputs of chunk c: dh^T rows (ci DV + 32 part) and dv_new^T rows;
   // copy wave cw stores the blocks with index cw modulo the copy waves
   auto flush = [&](int c) __attribute__((always_inline)) {
     const size_t ci = (size_t)bh * NT + c;
+    T* drows = (T*)(a.ws + L.dhT) + (ci * DV + 32 * part) * DK;
 #pragma unroll
-    for (int q = 0; q < NW; ++q) {
-      const int g2 = part * NW + q;
-      T* drows = (T*)(a.ws + L.dhT) + (ci * DV + 32 * g2) * DK;
-#pragma unroll
-      for (int blk = 0; blk < NDT / 2; ++blk)
-        if ((q * (NDT / 2 + 1) + blk) % kStateCopyWaves == cw)
-          flush_rows<T>(Stg[c & 1][q * (NDT / 2 + 1) + blk], drows + 64 * blk, DK, lane);
-      if ((q * (NDT / 2 + 1) + NDT / 2) % kStateCopyWaves == cw)
-        flush_rows<T>(Stg[c & 1][q * (NDT / 2 + 1) + NDT / 2], (T*)(a.ws + L.dVnT) + (ci * DV + 32 * g2) * 64, 64,
-                      lane);
-    }
+    for (int blk = 0; blk < NDT / 2; ++blk)
+      if (blk % kStateCopyWaves == cw) flush_rows<T>(Stg[c & 1][blk], drows + 64 * blk, DK, lane);
+    if ((NDT / 2) % kStateCopyWaves == cw)
+      flush_rows<T>(Stg[c & 1][NDT / 2], (T*)(a.ws + L.dVnT) + (ci * DV + 32 * part) * 64, 64, lane);
   };
-  if (w >= NW) {
-    // copy waves: chunk c is complete (vmcnt 0) before they reach the
-    // barrier that opens chunk c for the compute waves; the barrier also
-    // closes chunk c + 1, whose slot then takes chunk c - 1 and whose
-    // staged outputs this wave then stores (stores first, so waiting for
-    // the copies covers them too)
+  if (w >= NCW) {
     issue(NT - 1);
 #pragma unroll 1
     for (int c = NT - 1; c >= 0; --c) {
-      vm_wait_barrier<0>();
-      if (c < NT - 1) flush(c + 1);
+      vm_drain();  // this wave's copies of chunk c (and its stores of chunk c + 2) are done
+      const int t0 = c * kChunk;
+      if (!GATED && t0 + kChunk > Tn) {
+        // ungated Z = scale q^T dO with raw q tiles: dO rows past T (copies
+        // of the last row) are zeroed, each copy wave in its own rows
+        const int r0 = max(Tn - t0, 8 * OPC * cw), r1 = 8 * OPC * (cw + 1);
+        for (int idx = lane; idx < (r1 - r0) * 8; idx += 64)
+          reinterpret_cast<u32x4*>(ot(Sh + (c & 1) * SLOT) + (r0 + idx / 8) * 64)[idx % 8] = u32x4{0u, 0u, 0u, 0u};
+      }
+      block_barrier();  // TOP
       if (c > 0) issue(c - 1);
+      if (c < NT - 1) flush(c + 1);
+      block_barrier();  // MID: chunk c + 1's staged outputs are read
     }
     block_barrier();  // chunk 0 staged
     flush(0);
     return;
   }
 
-  f32x16 dS[NDT];
+  const int p = w;  // compute wave: dS blocks ND2 p .., chunk rows 32 p ..
+  f32x16 dS[ND2];
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
+  for (int i = 0; i < ND2; ++i)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int d = 32 * dt + 8 * (e >> 2) + 4 * hh + (e & 3);
-      dS[dt][e] = a.dht ? a.dht[((size_t)bh * DK + d) * DV + v] : 0.f;
+      const int d = 32 * (ND2 * p + i) + 8 * (e >> 2) + 4 * hh + (e & 3);
+      dS[i][e] = a.dht ? a.dht[((size_t)bh * DK + d) * DV + v] : 0.f;
     }
-
+  // this wave's dS images for chunk c (B operands of K dS', k-steps j)
+  auto write_img = [&](int c) __attribute__((always_inline)) {
+    u32x4* img = &Stg[c & 1][0][0] + p * (ND2 * 2 * 64);
+#pragma unroll
+    for (int i = 0; i < ND2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) img[(2 * i + j) * 64 + lane] = __builtin_bit_cast(u32x4, c_to_b<T>(dS[i], j));
+  };
   vm_drain();  // dh_T is in registers
+  write_img(NT - 1);
+
 #pragma unroll 1
   for (int c = NT - 1; c >= 0; --c) {
     const int t0 = c * kChunk;
-    const size_t ci = (size_t)bh * NT + c;
-    // chunk c landed (the copy wave waited for it); every wave is done with chunk c + 1
-    block_barrier();
+    block_barrier();  // TOP
     T* sl = Sh + (c & 1) * SLOT;
-    T* Os = ot(sl, w / 2);  // this wave's 64-column dO tile
-    const int oc0 = 32 * (gw & 1);
-    static_assert(GATED || NW == 1, "ungated Z zeroes the rows of a dO tile of its own");
-    if (!GATED && t0 + kChunk > Tn) {
-      // ungated Z = scale q^T dO with raw q tiles: dO rows past T (copies of
-      // the last row) are zeroed (Aqk is zero there already)
-      for (int idx = lane; idx < (kChunk - (Tn - t0)) * 8; idx += 64)
-        reinterpret_cast<u32x4*>(Os + (Tn - t0 + idx / 8) * 64)[idx % 8] = u32x4{0u, 0u, 0u, 0u};
-    }
+    const T* Os = ot(sl);
+    const int oc0 = 32 * (part & 1);
+    const u32x4* oimg = &Stg[c & 1][0][0] + (1 - p) * (ND2 * 2 * 64);
 
-    // the LDS operands of dVn, Z and K dS' into registers first: the one
-    // wave per SIMD then never waits on a read inside the MFMA chains
-    v8_t<T> oop[2][2], aop[2][2][2], qop[NDT][2][2], kop[NDT][2][2];
+    // the LDS operands of dVn and Z into registers first: the one wave per
+    // SIMD then never waits on a read inside the MFMA chains
+    v8_t<T> oop[2][2], aop[2][2], qop[ND2][2][2], kop[NDT][2], ysx[ND2][2];
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         oop[s2][j] = tile_tr8<T>(Os, 32 * s2, oc0, j, lane);
+        aop[s2][j] = tile_tr8<T>(at(sl), 32 * s2, 32 * p, j, lane);
 #pragma unroll
-        for (int jt = 0; jt < 2; ++jt) aop[jt][s2][j] = tile_tr8<T>(at(sl), 32 * s2, 32 * jt, j, lane);
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) qop[dt][s2][j] = tile_tr8<T>(qt(sl, dt / 2), 32 * s2, 32 * (dt & 1), j, lane);
+        for (int i = 0; i < ND2; ++i) {
+          const int dt = ND2 * p + i;
+          qop[i][s2][j] = tile_tr8<T>(qt(sl, dt / 2), 32 * s2, 32 * (dt & 1), j, lane);
+        }
       }
 #pragma unroll
     for (int db = 0; db < NDT; ++db)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < 2; ++j) kop[db][j] = tile_ldp8<T>(kt(sl, db / 2), 32 * p + cl, 32 * (db & 1), j, hh);
 #pragma unroll
-        for (int jt = 0; jt < 2; ++jt)
-          kop[db][j][jt] = tile_ldp8<T>(kt(sl, db / 2), 32 * jt + cl, 32 * (db & 1), j, hh);
+    for (int i = 0; i < ND2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) ysx[i][j] = __builtin_bit_cast(v8_t<T>, oimg[(2 * i + j) * 64 + lane]);
     __builtin_amdgcn_sched_barrier(0);
 
-    // dVn = Aqk^T dO (rows j = 32 jt + ..., lane column v); Z = Qg^T dO
-    f32x16 dVn[2], Z[NDT];
+    // dVn = Aqk^T dO (rows 32 p + ..., lane column v)
+    f32x16 dVn{};
 #pragma unroll
-    for (int jt = 0; jt < 2; ++jt) {
-      dVn[jt] = f32x16{};
+    for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) dVn[jt] = mma(aop[jt][s2][j], oop[s2][j], dVn[jt]);
-    }
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      Z[dt] = f32x16{};
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) Z[dt] = mma(qop[dt][s2][j], oop[s2][j], Z[dt]);
-    }
-
-    // + diag(e^(gamma - G)) K dS'  (K rows 32 jt + cl of the chunk)
-    const float gam = GATED ? gs(sl)[63] : 0.f;
+      for (int j = 0; j < 2; ++j) dVn = mma(aop[s2][j], oop[s2][j], dVn);
+    // + diag(e^(gamma - G)) K dS', dS' blocks in key-dim order (ours from
+    // registers, the other wave's from its images)
+    auto ys_op = [&](int db, int j) __attribute__((always_inline)) {
+      return db / ND2 == p ? c_to_b<T>(dS[db % ND2], j) : ysx[db % ND2][j];
+    };
     if constexpr (!GATED) {
 #pragma unroll
       for (int db = 0; db < NDT; ++db)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const v8_t<T> ys = c_to_b<T>(dS[db], j);
-#pragma unroll
-          for (int jt = 0; jt < 2; ++jt) dVn[jt] = mma(kop[db][j][jt], ys, dVn[jt]);
-        }
+        for (int j = 0; j < 2; ++j) dVn = mma(kop[db][j], ys_op(db, j), dVn);
     } else {
-      f32x16 Pk[2];
-      Pk[0] = Pk[1] = f32x16{};
+      f32x16 Pk{};
 #pragma unroll
       for (int db = 0; db < NDT; ++db)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const v8_t<T> ys = c_to_b<T>(dS[db], j);
+        for (int j = 0; j < 2; ++j) Pk = mma(kop[db][j], ys_op(db, j), Pk);
 #pragma unroll
-          for (int jt = 0; jt < 2; ++jt) Pk[jt] = mma(kop[db][j][jt], ys, Pk[jt]);
-        }
+      for (int I = 0; I < 4; ++I) {
+        const f32x4 f4 = *reinterpret_cast<const f32x4*>(gs(sl) + 64 + 32 * p + 8 * I + 4 * hh);
 #pragma unroll
-      for (int jt = 0; jt < 2; ++jt)
-#pragma unroll
-        for (int I = 0; I < 4; ++I) {
-          const f32x4 f4 = *reinterpret_cast<const f32x4*>(gs(sl) + 64 + 32 * jt + 8 * I + 4 * hh);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) dVn[jt][4 * I + r] += f4[r] * Pk[jt][4 * I + r];
-        }
+        for (int r = 0; r < 4; ++r) dVn[4 * I + r] += f4[r] * Pk[4 * I + r];
+      }
     }
-    // W^T operands of the dS update (transposing reads of W), read while
-    // the MFMAs above run
-    v8_t<T> wop[NDT][2][2];
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int it = 0; it < 2; ++it)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          wop[dt][it][j] = tile_tr8<T>(wt(sl, dt / 2), 32 * it, 32 * (dt & 1), j, lane);
     if (t0 + 63 >= Tn) {  // rows past T: K repeats its last row there
 #pragma unroll
-      for (int jt = 0; jt < 2; ++jt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e)
-          if (t0 + 32 * jt + 8 * (e >> 2) + 4 * hh + (e & 3) >= Tn) dVn[jt][e] = 0.f;
+      for (int e = 0; e < 16; ++e)
+        if (t0 + 32 * p + 8 * (e >> 2) + 4 * hh + (e & 3) >= Tn) dVn[e] = 0.f;
     }
-
-    // dh^T (gradient of the state leaving the chunk, [v][d]) and dv_new^T:
-    // staged here, stored by the copy wave during the next chunk
+    // Z = Qg^T dO for our key dims (independent of the chain)
+    f32x16 Z[ND2];
 #pragma unroll
-    for (int blk = 0; blk < NDT / 2; ++blk)
-      stage_rows<T>(dS[2 * blk], dS[2 * blk + 1], Stg[c & 1][w * (NDT / 2 + 1) + blk], lane);
-    stage_rows<T>(dVn[0], dVn[1], Stg[c & 1][w * (NDT / 2 + 1) + NDT / 2], lane);
-
-    // dS <- e^gamma dS' + Z - W^T dVn
-    const float eg = GATED ? __expf(gam) : 1.f;
-    v8_t<T> nb[2][2];
+    for (int i = 0; i < ND2; ++i) {
+      Z[i] = f32x16{};
 #pragma unroll
-    for (int it = 0; it < 2; ++it)
+      for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) nb[it][j] = c_to_b<T>(-dVn[it], j);
+        for (int j = 0; j < 2; ++j) Z[i] = mma(qop[i][s2][j], oop[s2][j], Z[i]);
+    }
+    // our -dVn rows as B operands: for us, and as the image for the other wave
+    v8_t<T> nb_own[2];
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      f32x16 acc = GATED ? dS[dt] * eg + Z[dt] : dS[dt] + Z[dt] * a.scale;
+    for (int j = 0; j < 2; ++j) {
+      nb_own[j] = c_to_b<T>(-dVn, j);
+      Xv[p][j][lane] = __builtin_bit_cast(u32x4, nb_own[j]);
+    }
+    // dv_new^T: our 32 of the block's 64 columns, stored by a copy wave
+    // during the next chunk
+    stage_half<T>(dVn, p, Stg[c & 1][NDT / 2], lane);
+    // W^T operands of our key dims (transposing reads of W)
+    v8_t<T> wop[ND2][2][2];
+#pragma unroll
+    for (int i = 0; i < ND2; ++i)
 #pragma unroll
       for (int it = 0; it < 2; ++it)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc = mma(wop[dt][it][j], nb[it][j], acc);
-      dS[dt] = acc;
+        for (int j = 0; j < 2; ++j) {
+          const int dt = ND2 * p + i;
+          wop[i][it][j] = tile_tr8<T>(wt(sl, dt / 2), 32 * it, 32 * (dt & 1), j, lane);
+        }
+    const float eg = GATED ? __expf(gs(sl)[63]) : 1.f;
+    block_barrier();  // MID
+
+    // dh^T (gradient of the state leaving the chunk, [v][d]) of our key
+    // dims, staged over our dS images of this chunk (read before MID)
+    if constexpr (ND2 == 2) {
+      stage_rows<T>(dS[0], dS[1], Stg[c & 1][p], lane);
+    } else {
+      stage_half<T>(dS[0], p, Stg[c & 1][0], lane);
     }
+    // dS <- e^gamma dS' + Z - W^T dVn, the -dVn rows in chunk-row order
+    // (rows 0-31 first) whichever wave holds them
+    v8_t<T> nb[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const v8_t<T> oth = __builtin_bit_cast(v8_t<T>, Xv[1 - p][j][lane]);
+      nb[0][j] = p == 0 ? nb_own[j] : oth;
+      nb[1][j] = p == 0 ? oth : nb_own[j];
+    }
+#pragma unroll
+    for (int i = 0; i < ND2; ++i) {
+      f32x16 acc = GATED ? dS[i] * eg + Z[i] : dS[i] + Z[i] * a.scale;
+#pragma unroll
+      for (int it = 0; it < 2; ++it)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc = mma(wop[i][it][j], nb[it][j], acc);
+      dS[i] = acc;
+    }
+    if (c > 0) write_img(c - 1);
   }
 
-  block_barrier();  // chunk 0's staged outputs are complete for the copy wave
+  block_barrier();  // chunk 0's staged outputs are complete for the copy waves
   if (a.dh0) {
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+    for (int i = 0; i < ND2; ++i)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int d = 32 * dt + 8 * (e >> 2) + 4 * hh + (e & 3);
-        a.dh0[((size_t)bh * DK + d) * DV + v] = dS[dt][e];
+        const int d = 32 * (ND2 * p + i) + 8 * (e >> 2) + 4 * hh + (e & 3);
+        a.dh0[((size_t)bh * DK + d) * DV + v] = dS[i][e];
       }
   }
 }
@@ -812,8 +830,7 @@ hipError_t launch_delta_bwd(const DeltaArgs& a, hipStream_t stream) {
   const int BH = a.B * a.H;
   hipError_t e = hipSuccess;
   if (a.stages & 1) {
-    delta_state_bwd_kernel<T, DK, DV, GATED><<<dim3(BH * state_split<DV>()), dim3(state_threads<DV>()), 0,
-                                               stream>>>(a, L);
+    delta_state_bwd_kernel<T, DK, DV, GATED><<<dim3(BH * (DV / 32)), dim3(state_bwd_threads()), 0, stream>>>(a, L);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   if (a.stages & 2) {
