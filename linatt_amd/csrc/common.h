@@ -291,6 +291,7 @@ struct BoolC {
 template <int V>
 struct IntC {
   static constexpr int value = V;
+  constexpr operator int() const { return V; }
 };
 
 // Position of logical element e (0..31) of a 32-block in the "operand

@@ -590,9 +590,10 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
     }
   // key tile st; MASKED applies the causal / past-T masks where the tile
   // reaches the workgroup's diagonal
-  auto tile = [&](int st, auto masked_c) __attribute__((always_inline)) {
+  auto tile = [&](int st, auto masked_c, auto slot_c) __attribute__((always_inline)) {
     constexpr bool kMaskTile = decltype(masked_c)::value;
-    const int s0 = st * 64, buf = st % NB;
+    const int buf = slot_c;
+    const int s0 = st * 64;
     // tile st landed; tile st - 1's slot is free for tile st + 2
     vm_wait_barrier_n(st + 1 < nst ? ops : 0);
     if (st + NB - 1 < nst) {
@@ -672,7 +673,20 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
   };
   // one body for every tile: a second, unmasked copy of it for the tiles
   // before the diagonal raises this kernel's register count past occupancy 3
-  for (int st = 0; st < nst; ++st) tile(st, BoolC<true>{});
+  // unrolled by the ring depth where registers allow (M > 1): the slot is then
+  // a constant in each body, its LDS base folds into the ds_read offsets, and
+  // the unmasked block issues 116 VALU instructions instead of 128; with one
+  // group the unrolled loop needs 170 VGPRs, past occupancy 3
+  static_assert(NB == 3, "ring of three");
+  if constexpr (M > 1) {
+    for (int st = 0; st < nst; st += 3) {
+      tile(st, BoolC<true>{}, IntC<0>{});
+      if (st + 1 < nst) tile(st + 1, BoolC<true>{}, IntC<1>{});
+      if (st + 2 < nst) tile(st + 2, BoolC<true>{}, IntC<2>{});
+    }
+  } else {
+    for (int st = 0; st < nst; ++st) tile(st, BoolC<true>{}, st % NB);
+  }
 
   if constexpr (DECAY) {
     dcr += __shfl_xor(dcr, 32);
