@@ -16,7 +16,9 @@ With ``s = sqrt(scale)`` on q and k (``scale`` defaults to ``1 / E``,
   blocks, a chunk-sequential MFMA pass for ``U`` and the KATA sum-score
   forward for the readout.  The backward (``linatt_dkata_bwd``) runs the
   KATA sum-score backward for the readout and for the erase terms around a
-  reverse chunk solve.
+  reverse chunk solve, in bfloat16: with a gradient, float16 inputs run
+  forward and backward in bfloat16 (float16's range cannot hold the
+  backward's intermediates at small scales) and get float16 gradients.
 * ``flash_delta_U`` (``:186-212``), ``flash_delta_readout`` (``:975-985``) and
   ``flash_delta_den`` (``:1049-1057``) return the forward's intermediates
   with the reference's signatures.
@@ -87,18 +89,24 @@ class _FlashDelta(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, beta, M, scale, normalize, eps):
         train = any(ctx.needs_input_grad[:4])
-        if train and q.dtype != torch.bfloat16:
-            raise NotImplementedError(
-                "linatt_amd flash_delta: the backward runs in bfloat16 only (the mixer calls "
-                "flash_delta with bf16 inputs, kata/layer.py:409-412)")
         if not train:
             o, _, _ = _run(q, k, v, beta, M, scale, normalize, eps, False)
             return o
+        ctx.dtypes = (q.dtype, k.dtype, v.dtype, beta.dtype)
+        if q.dtype == torch.float16 and k.dtype == v.dtype == torch.float16:
+            # the backward's 16-bit intermediates (dU ~ scale^2) fall below
+            # float16's normal range at small scales: with a gradient, float16
+            # inputs run forward and backward in bfloat16, and the gradients
+            # come back in float16
+            q, k, v = q.bfloat16(), k.bfloat16(), v.bfloat16()
+        elif q.dtype != torch.bfloat16:
+            raise NotImplementedError(
+                "linatt_amd flash_delta: the backward runs in bfloat16 (float16 inputs are "
+                f"converted); got {q.dtype}")
         o, U, den, ws, (qc, kc, vc, bc) = _run(q, k, v, beta, M, scale, normalize, eps, False,
                                                 train=True)
         ctx.save_for_backward(qc, kc, vc, bc, U, o, den, ws)
         ctx.M, ctx.scale, ctx.normalize, ctx.eps = M, scale, normalize, eps
-        ctx.dtypes = (q.dtype, k.dtype, v.dtype, beta.dtype)
         return o
 
     @staticmethod

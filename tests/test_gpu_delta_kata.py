@@ -252,8 +252,35 @@ def test_train_forward_keeps_no_U(F):
         assert torch.equal(a, b)
 
 
-def test_backward_fp16_raises(F):
-    q, k, v, beta = make(1, 64, 1, 64, 64, torch.float16, 1)
+@pytest.mark.parametrize("shape,M", [((2, 37, 2), 1), ((1, 300, 2), 4), ((1, 1, 1), 2)],
+                         ids=["2x37x2_M1", "1x300x2_M4", "1x1x1_M2"])
+def test_backward_fp16_runs_in_bf16(F, shape, M):
+    """float16 inputs with a gradient run forward and backward in bfloat16:
+    the output equals the bfloat16 op's on the converted inputs bit for bit,
+    the gradients come back in float16 and meet the bfloat16 bar against the
+    float64 oracle on the float16 inputs themselves."""
+    B, T, H = shape
+    q, k, v, beta = make(B, T, H, 64, 64, torch.float16, 90 + T)
+    do = torch.randn(B, T, H, 64, generator=torch.Generator().manual_seed(91 + T))
+    o_ref, dq_ref, dk_ref, dv_ref, db_ref = DK.flash_delta_fwd_bwd(q, k, v, beta, M, do, None, False)
+    qd, kd, vd, bd = (t.cuda().requires_grad_(True) for t in (q, k, v, beta))
+    o = F.flash_delta(qd, kd, vd, bd, M)
+    o.backward(do.cuda())
+    with torch.no_grad():
+        o_bf = F.flash_delta(*(t.cuda().bfloat16() for t in (q, k, v)), beta.cuda(), M)
+    assert torch.equal(o, o_bf)
+    bar = TOL[torch.bfloat16]
+    assert mar(o, o_ref) < bar
+    for name, got, ref in (("dq", qd.grad, dq_ref), ("dk", kd.grad, dk_ref),
+                           ("dv", vd.grad, dv_ref), ("dbeta", bd.grad, db_ref)):
+        assert got.dtype == (torch.float32 if name == "dbeta" else torch.float16), name
+        e = mar(got, ref)
+        print(f"  fp16-in {name} {e:.2e}", flush=True)
+        assert e < bar, (name, e)
+
+
+def test_backward_fp32_raises(F):
+    q, k, v, beta = make(1, 64, 1, 64, 64, torch.float32, 1)
     qd = q.cuda().requires_grad_(True)
     with pytest.raises(NotImplementedError, match="bfloat16"):
         F.flash_delta(qd, k.cuda(), v.cuda(), beta.cuda(), 1)
