@@ -23,6 +23,35 @@
 
 namespace linatt {
 
+// Row sums of a 32 x 32 fp32 block held in C layout (lane column l & 31,
+// rows 8 (e >> 2) + 4 (l >> 5) + (e & 3), e = 0..15): dst[row] = the sum
+// over the 32 columns.  Each value is summed over its 16-lane row by DPP
+// moves (quad xor 1, quad xor 2, half-row mirror, row mirror: after each
+// step every lane holds the sum over twice as many lanes), then over the
+// two rows of its 32-lane half by one xor-16 shuffle.
+__device__ __forceinline__ float dpp_add(float v, int ctrl_sel) {
+  int m;
+  switch (ctrl_sel) {
+    case 0: m = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false); break;
+    case 1: m = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false); break;
+    case 2: m = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false); break;
+    default: m = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false); break;
+  }
+  return v + __builtin_bit_cast(float, m);
+}
+__device__ __forceinline__ void row_sums32(f32x16 x, float* dst, int lane) {
+#pragma unroll
+  for (int st = 0; st < 4; ++st)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) x[e] = dpp_add(x[e], st);
+#pragma unroll
+  for (int e = 0; e < 16; ++e) x[e] += __shfl_xor(x[e], 16);
+  if ((lane & 31) == 0) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dst[8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)] = x[e];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Kernel 1: reverse state pass.  One workgroup per (b, h, 32 value columns):
 // two compute waves and the copy waves.  Per chunk, with dS' the gradient
@@ -368,23 +397,31 @@ __global__ __launch_bounds__(state_bwd_threads()) void delta_state_bwd_kernel(De
 template <typename T, int DK, int DV, bool GATED>
 __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, DeltaLayout L) {
   constexpr int KT = DK / 64, VT = DV / 64, TE = 64 * 64;
-  // St after phase 1: Mq then dTm^T / P (0 .. TE), Z^T then Q^T fp32 (TE ..
-  // 3 TE), store staging (3 TE .. 5 TE), Tm (5 TE ..), V (6 TE ..)
-  constexpr int SE0 = 2 * VT * KT * TE, SE1 = 6 * TE + VT * TE;
+  // St after phase 1: Mq then dTm^T / P (0 .. TE), Tm (TE .. 2 TE; phase 6:
+  // the dbeta / dG reductions), V (2 TE ..).  At K = V = 64 the kernel then
+  // needs under 80 KB of LDS, so two workgroups share a CU.
+  constexpr int SE0 = 2 * VT * KT * TE, SE1 = 2 * TE + VT * TE;
   constexpr int SE = SE0 > SE1 ? SE0 : SE1;
   static_assert(DK % 64 == 0 && DV % 64 == 0 && DK <= 128 && DV <= 128, "64 or 128 wide");
   // S^T then dS'^T as [v][d] tiles (tile vt * KT + kt) in phase 1
   __shared__ __attribute__((aligned(16))) T St[SE];
   __shared__ __attribute__((aligned(16))) T dVt[VT * TE];  // dVn^T [v][i]
-  __shared__ __attribute__((aligned(16))) T Vnt[VT * TE];  // Vn^T [v][j]; phases 4-6: reductions
-  __shared__ __attribute__((aligned(16))) T Ot[VT * TE];   // dO [i][v]; from phase 2: beta
+  // dO [i][v] (tiles 0 .. VT), Vn^T [v][j] (tiles VT .. 2 VT); both are read
+  // only in phase 1, then their first 16 KiB are the waves' store staging
+  __shared__ __attribute__((aligned(16))) T OVt[2 * VT * TE];
+  T* const Ot = OVt;
+  T* const Vnt = OVt + VT * TE;
   __shared__ __attribute__((aligned(16))) T Qt[KT * TE];   // q [i][d]; from phase 3: dW [i][d]
   __shared__ __attribute__((aligned(16))) T Kt[KT * TE];   // k [j][d]
   __shared__ __attribute__((aligned(16))) T At[TE];        // Aqk [i][j]; phase 5: M^T as [a][j]
   __shared__ __attribute__((aligned(16))) float Gs[64];
+  __shared__ __attribute__((aligned(16))) float Bs[64];  // beta of the chunk's rows
   __shared__ float red_gi[4][64], red_kd[4][64], red_rs[2][64], red_s[8];
+  // row sums over a 32-column block: Z = X o Aqk (phase 2, by i block) and
+  // Q = P o KK (phase 5b, by a block)
+  __shared__ float zrow[2][64], qrow[2][64];
+  static_assert(2 * VT * TE * (int)sizeof(T) >= 8 * 2048, "store staging fits in the dO / Vn^T tiles");
   T* Mqt = St;
-  float* Zt = reinterpret_cast<float*>(St + TE);
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -524,11 +561,10 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
   vm_wait_barrier<0>();  // Aqk landed; the state tiles are no longer read
   // copies for phases 4-6, landing during phases 2-3: Tm, V (rows past T
   // repeat the last valid row; beta is zeroed there), beta
-  float* Bs = reinterpret_cast<float*>(Ot);
-  dma_tile64<T>((const T*)(a.ctx + L.Tm) + ci * 4096, 64, 0, 64, St + 5 * TE, w, lane);
+  dma_tile64<T>((const T*)(a.ctx + L.Tm) + ci * 4096, 64, 0, 64, St + TE, w, lane);
 #pragma unroll
   for (int vt = 0; vt < VT; ++vt)
-    dma_tile64<T>((const T*)a.v + ((size_t)b * Tn * H + h) * DV + 64 * vt, os, t0, Tn, St + 6 * TE + vt * TE, w,
+    dma_tile64<T>((const T*)a.v + ((size_t)b * Tn * H + h) * DV + 64 * vt, os, t0, Tn, St + 2 * TE + vt * TE, w,
                   lane);
   if (w == 0) dma4(a.beta + ((size_t)b * Tn + min(t0 + lane, Tn - 1)) * H + h, Bs);
 
@@ -537,7 +573,7 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
     const int xi = 32 * xib + cl;  // this lane's i
     const float Gi = Gs[xi];
     const bool iv = t0 + xi < Tn;
-    f32x16 mq;
+    f32x16 mq, zs;
     float rs = 0.f;
     const char* arow = reinterpret_cast<const char*>(At);
 #pragma unroll
@@ -551,7 +587,7 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
         const float x = w < 3 ? xs[4 * I + e] : 0.f;
         const float z = x * (float)a4[e];
         rs += z;
-        Zt[j * 64 + xi] = z;
+        zs[4 * I + e] = z;
         // branch-free: the exponent is zeroed where the entry is masked
         const bool m = w < 3 && iv && j <= xi;
         const float g = GATED ? __expf(m ? Gi - g4[e] : 0.f) : 1.f;
@@ -562,8 +598,10 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
     }
     rs += __shfl_xor(rs, 32);
     if (hh == 0 && w < 3) red_rs[xjb][xi] = rs;
+    // row j's sum over this block's 32 columns i (wave 3: the zero block)
+    row_sums32(zs, &zrow[xib][32 * xjb], lane);
   }
-  u32x4* stage = reinterpret_cast<u32x4*>(St + 3 * TE) + 128 * w;
+  u32x4* stage = reinterpret_cast<u32x4*>(OVt) + 128 * w;
   __syncthreads();
 
   // 3. dq += Mq K (rows i), dKs += Mq^T Q (rows j)
@@ -601,12 +639,7 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
   // dG of the output / state terms, row tid (threads 0..63), kept for phase 6
   float dGo = 0.f;
   if (tid < 64) {
-    float cs = 0.f;  // column term: sum_j Z[j][i]
-#pragma unroll
-    for (int q4 = 0; q4 < 16; ++q4) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(Zt + tid * 64 + 4 * q4);
-      cs += (v[0] + v[1]) + (v[2] + v[3]);
-    }
+    const float cs = zrow[0][tid] + zrow[1][tid];  // sum_i Z[tid][i]
     float kdt = 0.f, git = 0.f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -625,17 +658,17 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
       dGo += kds + (GATED ? __expf(gam) : 1.f) * st;
     }
   }
-  vm_wait_barrier<0>();  // Tm, V and beta landed; dW written; Z^T no longer read
+  vm_wait_barrier<0>();  // Tm, V and beta landed; dW written
 
   // 4.-6. backward through W and U.  dU = dVn (dU^T tiles in dVt); rows j,
   // a and l index the chunk; this lane's row is r; column block cb = w >> 1, hf = cb & 1.
-  const T* Tmt = St + 5 * TE;        // Tm [i][j]
-  const T* Vt = St + 6 * TE;         // V [j][v]
+  const T* Tmt = St + TE;            // Tm [i][j]
+  const T* Vt = St + 2 * TE;         // V [j][v]
   T* const PT = St;                  // dTm^T [j][i], then P [a][l]
   T* const MTt = At;                 // M^T as [a][j]
-  float* const Qb = Zt;              // Q^T fp32 [l][a]
-  float* const red_b = reinterpret_cast<float*>(Vnt);  // [8][64]
-  float* const red_g = red_b + 8 * 64;                 // [8][64]
+  // phase 6, after Tm's last read: [8][64] each
+  float* const red_b = reinterpret_cast<float*>(St + TE);
+  float* const red_g = red_b + 8 * 64;
   const int cb = w >> 1, hf = cb & 1;
   const bool has_dv = cb < DV / 32;
   const bool lower = hf <= lb;
@@ -766,8 +799,8 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
     for (int I = 0; I < 4; ++I)
       *reinterpret_cast<v4_t<T>*>(t + tile_off(r, 32 * hf + 8 * I + 4 * hh)) =
           to4<T>(pq[4 * I], pq[4 * I + 1], pq[4 * I + 2], pq[4 * I + 3]);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) Qb[(32 * hf + 8 * (e >> 2) + 4 * hh + (e & 3)) * 64 + r] = qq[e];
+    // row l's sum over this wave's 32 columns a
+    row_sums32(qq, &qrow[lb][32 * hf], lane);
   }
   __syncthreads();
 
@@ -798,13 +831,8 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
   }
   __syncthreads();
   if (tid < 64) {
-    // column part of dG: sum_a Q[a][l] = row l of Q^T
-    float cq = 0.f;
-#pragma unroll
-    for (int q4 = 0; q4 < 16; ++q4) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(Qb + tid * 64 + 4 * q4);
-      cq += (v[0] + v[1]) + (v[2] + v[3]);
-    }
+    // column part of dG: sum_a Q[a][l], l = tid
+    const float cq = qrow[0][tid] + qrow[1][tid];
     const int t = t0 + tid;
     const int l2 = tid >> 5;  // row block of this row; waves l2 + 2 q hold it
     float dbeta = 0.f, gsum = 0.f;
