@@ -539,17 +539,15 @@ __global__ __launch_bounds__(state_threads<DV>()) void delta_state_fwd_kernel(
     for (int it = 0; it < 2; ++it)
 #pragma unroll
       for (int jq = 0; jq < 2; ++jq) uv[it][jq] = Us[swz_slot<KCPR>(cl, 4 * it + 2 * jq + hh)];
+    if constexpr (!GATED) {
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+      for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-      for (int it = 0; it < 2; ++it)
+        for (int it = 0; it < 2; ++it)
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          if constexpr (GATED)
-            kv[dt][it][jj] = Ks[swz_slot<KCPR>(32 * dt + cl, 4 * it + 2 * jj + hh)];
-          else  // k^T by transposing reads of the natural k tiles
+          for (int jj = 0; jj < 2; ++jj)  // k^T by transposing reads of the natural k tiles
             kt8[dt][it][jj] = tile_tr8<T>(reinterpret_cast<const T*>(Ks) + (dt / 2) * 4096, 32 * it, 32 * (dt & 1), jj, lane);
-        }
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     // v_new = U - P (rows past T are zero in U and W); U^T rows of this
@@ -567,6 +565,17 @@ __global__ __launch_bounds__(state_threads<DV>()) void delta_state_fwd_kernel(
           for (int r = 0; r < 4; ++r) Vn[it][4 * I + r] = (float)u8[4 * s2 + r] - P[it][4 * I + r];
         }
       }
+    // gated: the Kd^T operands only now, once the W operands are dead (read
+    // with the W operands, they pushed the wave past 256 VGPRs and 28 values
+    // per chunk went through AGPRs)
+    if constexpr (GATED) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int it = 0; it < 2; ++it)
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) kv[dt][it][jj] = Ks[swz_slot<KCPR>(32 * dt + cl, 4 * it + 2 * jj + hh)];
+    }
     // v_new^T: staged here, stored by the copy wave during the next chunk
     stage_rows<T>(Vn[0], Vn[1], Stg[c & 1][w * (NDT / 2 + 1)], lane);
 
