@@ -11,9 +11,10 @@
 //   z[t, c] = bias[c] + sum_{w < W} weight[c, w] x[t - (W - 1) + w, c]
 //   y = silu(z) = z / (1 + e^-z)  (or y = z)
 // with x[t < 0] taken from a cache of the W inputs before the chunk (the
-// newest last), or zero.  One lane owns 8 adjacent channels (one 16-byte
-// load per token) and a run of kConvTB tokens, sliding the window in
-// registers; each input row is read once plus a W - 1 row halo.  The
+// newest last), or zero.  One lane owns kConvCh = 4 adjacent channels (one
+// 8-byte load per token in 16-bit types, so C = 768 fills its 64-lane waves
+// exactly) and a run of kConvTB tokens, sliding the window in registers;
+// each input row is read once plus a W - 1 row halo.  The
 // backward recomputes z, forms dz = dy silu'(z), dx[s] = sum_w weight[c, w]
 // dz[s + W - 1 - w], and per-lane partial sums of dweight and dbias that a
 // second kernel adds up in a fixed order.
@@ -31,6 +32,21 @@ namespace linatt {
 namespace {
 
 constexpr int kConvTB = 16;  // tokens per lane
+constexpr int kConvCh = 4;   // channels per lane of the short convolution
+
+template <typename T>
+__device__ __forceinline__ void load4f(const T* p, float* out) {
+  const v4_t<T> v = *reinterpret_cast<const v4_t<T>*>(p);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) out[e] = (float)v[e];
+}
+template <typename T>
+__device__ __forceinline__ void store4f(T* p, const float* v) {
+  v4_t<T> o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = (T)v[e];
+  *reinterpret_cast<v4_t<T>*>(p) = o;
+}
 
 template <typename T>
 __device__ __forceinline__ void load8f(const T* p, float* out) {
@@ -60,18 +76,19 @@ __device__ __forceinline__ void store8f<float>(float* p, const float* v) {
   reinterpret_cast<f32x4*>(p)[1] = f32x4{v[4], v[5], v[6], v[7]};
 }
 
-// 8 channels of input position pos of batch row b (pos < 0: the cache, or 0)
+// kConvCh channels of input position pos of batch row b (pos < 0: the
+// cache, or 0)
 template <typename T, int W>
 __device__ __forceinline__ void conv_input(const ConvArgs& a, int b, int c0, int pos, float* out) {
   if (pos >= 0) {
-    load8f<T>((const T*)a.x + ((int64_t)b * a.T + pos) * a.C + c0, out);
+    load4f<T>((const T*)a.x + ((int64_t)b * a.T + pos) * a.C + c0, out);
   } else if (a.cache_in) {
     const T* cb = (const T*)a.cache_in + ((int64_t)b * a.C + c0) * W + (W + pos);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = (float)cb[e * W];
+    for (int e = 0; e < kConvCh; ++e) out[e] = (float)cb[e * W];
   } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = 0.f;
+    for (int e = 0; e < kConvCh; ++e) out[e] = 0.f;
   }
 }
 
@@ -80,54 +97,54 @@ __device__ __forceinline__ void conv_input(const ConvArgs& a, int b, int c0, int
 template <typename T, int W>
 __global__ __launch_bounds__(64) void short_conv_fwd_kernel(ConvArgs a) {
   const int cg = blockIdx.x * 64 + threadIdx.x, tb = blockIdx.y, b = blockIdx.z;
-  if (8 * cg >= a.C) return;
-  const int c0 = 8 * cg, t0 = tb * kConvTB;
-  float wv[8][W], bv[8];
+  if (kConvCh * cg >= a.C) return;
+  const int c0 = kConvCh * cg, t0 = tb * kConvTB;
+  float wv[kConvCh][W], bv[kConvCh];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
+  for (int e = 0; e < kConvCh; ++e) {
 #pragma unroll
     for (int w = 0; w < W; ++w) wv[e][w] = a.w[(c0 + e) * W + w];
     bv[e] = a.bias ? a.bias[c0 + e] : 0.f;
   }
-  float win[W][8];  // win[j] = input t - (W - 1) + j for the current t
+  float win[W][kConvCh];  // win[j] = input t - (W - 1) + j for the current t
 #pragma unroll
   for (int j = 0; j < W - 1; ++j) conv_input<T, W>(a, b, c0, t0 - (W - 1) + j, win[j + 1]);
   const T* __restrict__ xb = (const T*)a.x + (int64_t)b * a.T * a.C + c0;
   T* __restrict__ yb = (T*)a.y + (int64_t)b * a.T * a.C + c0;
   // the run's rows up front (independent loads in flight), rows past T as zero
-  v8_t<T> xr[kConvTB];
+  v4_t<T> xr[kConvTB];
 #pragma unroll
   for (int i = 0; i < kConvTB; ++i)
-    xr[i] = t0 + i < a.T ? *reinterpret_cast<const v8_t<T>*>(xb + (int64_t)(t0 + i) * a.C) : v8_t<T>{};
+    xr[i] = t0 + i < a.T ? *reinterpret_cast<const v4_t<T>*>(xb + (int64_t)(t0 + i) * a.C) : v4_t<T>{};
 #pragma unroll
   for (int i = 0; i < kConvTB; ++i) {
     const int t = t0 + i;
 #pragma unroll
     for (int j = 0; j < W - 1; ++j)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) win[j][e] = win[j + 1][e];
+      for (int e = 0; e < kConvCh; ++e) win[j][e] = win[j + 1][e];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) win[W - 1][e] = (float)xr[i][e];
+    for (int e = 0; e < kConvCh; ++e) win[W - 1][e] = (float)xr[i][e];
     if (t >= a.T) break;
-    float yv[8];
+    float yv[kConvCh];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+    for (int e = 0; e < kConvCh; ++e) {
       float z = bv[e];
 #pragma unroll
       for (int w = 0; w < W; ++w) z += wv[e][w] * win[w][e];
       yv[e] = a.act ? z / (1.f + __expf(-z)) : z;
     }
-    store8f<T>(yb + (int64_t)t * a.C, yv);
+    store4f<T>(yb + (int64_t)t * a.C, yv);
   }
   // the W inputs before position T, for a later call (decode)
   if (a.cache_out && t0 <= a.T - 1 && a.T - 1 < t0 + kConvTB) {
     T* co = (T*)a.cache_out + ((int64_t)b * a.C + c0) * W;
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-      float v[8];
+      float v[kConvCh];
       conv_input<T, W>(a, b, c0, a.T - W + w, v);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) co[e * W + w] = (T)v[e];
+      for (int e = 0; e < kConvCh; ++e) co[e * W + w] = (T)v[e];
     }
   }
 }
@@ -135,19 +152,19 @@ __global__ __launch_bounds__(64) void short_conv_fwd_kernel(ConvArgs a) {
 template <typename T, int W>
 __global__ __launch_bounds__(64) void short_conv_bwd_kernel(ConvArgs a) {
   const int cg = blockIdx.x * 64 + threadIdx.x, tb = blockIdx.y, b = blockIdx.z;
-  if (8 * cg >= a.C) return;
-  const int c0 = 8 * cg, t0 = tb * kConvTB, t1 = min(t0 + kConvTB, a.T);
-  float wv[8][W], bv[8];
+  if (kConvCh * cg >= a.C) return;
+  const int c0 = kConvCh * cg, t0 = tb * kConvTB, t1 = min(t0 + kConvTB, a.T);
+  float wv[kConvCh][W], bv[kConvCh];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
+  for (int e = 0; e < kConvCh; ++e) {
 #pragma unroll
     for (int w = 0; w < W; ++w) wv[e][w] = a.w[(c0 + e) * W + w];
     bv[e] = a.bias ? a.bias[c0 + e] : 0.f;
   }
-  float win[W][8], dz[W][8];  // inputs u - (W - 1) .. u; dz[u - (W - 1)] .. dz[u]
-  float dwp[8][W], dbp[8];
+  float win[W][kConvCh], dz[W][kConvCh];  // inputs u - (W - 1) .. u; dz[u - (W - 1)] .. dz[u]
+  float dwp[kConvCh][W], dbp[kConvCh];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
+  for (int e = 0; e < kConvCh; ++e) {
 #pragma unroll
     for (int w = 0; w < W; ++w) {
       dwp[e][w] = 0.f;
@@ -162,12 +179,12 @@ __global__ __launch_bounds__(64) void short_conv_bwd_kernel(ConvArgs a) {
   const T* __restrict__ gb = (const T*)a.dy + rowb * a.C + c0;
   T* __restrict__ dxb = (T*)a.dx + rowb * a.C + c0;
   constexpr int NU = kConvTB + W - 1;  // positions u whose dz reaches dx[t0 .. t0 + kConvTB - 1]
-  v8_t<T> xr[NU], gr[NU];
+  v4_t<T> xr[NU], gr[NU];
 #pragma unroll
   for (int i = 0; i < NU; ++i) {
     const bool in = t0 + i < a.T;
-    xr[i] = in ? *reinterpret_cast<const v8_t<T>*>(xb + (int64_t)(t0 + i) * a.C) : v8_t<T>{};
-    gr[i] = in ? *reinterpret_cast<const v8_t<T>*>(gb + (int64_t)(t0 + i) * a.C) : v8_t<T>{};
+    xr[i] = in ? *reinterpret_cast<const v4_t<T>*>(xb + (int64_t)(t0 + i) * a.C) : v4_t<T>{};
+    gr[i] = in ? *reinterpret_cast<const v4_t<T>*>(gb + (int64_t)(t0 + i) * a.C) : v4_t<T>{};
   }
 #pragma unroll
   for (int i = 0; i < NU; ++i) {
@@ -176,19 +193,19 @@ __global__ __launch_bounds__(64) void short_conv_bwd_kernel(ConvArgs a) {
 #pragma unroll
     for (int j = 0; j < W - 1; ++j)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
+      for (int e = 0; e < kConvCh; ++e) {
         win[j][e] = win[j + 1][e];
         dz[j][e] = dz[j + 1][e];
       }
     if (u < a.T) {
-      float g[8];
+      float g[kConvCh];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
+      for (int e = 0; e < kConvCh; ++e) {
         win[W - 1][e] = (float)xr[i][e];
         g[e] = (float)gr[i][e];
       }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
+      for (int e = 0; e < kConvCh; ++e) {
         float z = bv[e];
 #pragma unroll
         for (int w = 0; w < W; ++w) z += wv[e][w] * win[w][e];
@@ -201,7 +218,7 @@ __global__ __launch_bounds__(64) void short_conv_bwd_kernel(ConvArgs a) {
       }
       if (u < t1) {  // this lane's own positions: weight and bias gradients
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
+        for (int e = 0; e < kConvCh; ++e) {
 #pragma unroll
           for (int w = 0; w < W; ++w) dwp[e][w] += dz[W - 1][e] * win[w][e];
           dbp[e] += dz[W - 1][e];
@@ -209,25 +226,25 @@ __global__ __launch_bounds__(64) void short_conv_bwd_kernel(ConvArgs a) {
       }
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dz[W - 1][e] = 0.f;
+      for (int e = 0; e < kConvCh; ++e) dz[W - 1][e] = 0.f;
     }
     const int s = u - (W - 1);  // dx[s] = sum_w weight[w] dz[s + W - 1 - w]
     if (s >= t0) {
-      float dxv[8];
+      float dxv[kConvCh];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
+      for (int e = 0; e < kConvCh; ++e) {
         float acc = 0.f;
 #pragma unroll
         for (int w = 0; w < W; ++w) acc += wv[e][w] * dz[W - 1 - w][e];
         dxv[e] = acc;
       }
-      store8f<T>(dxb + (int64_t)s * a.C, dxv);
+      store4f<T>(dxb + (int64_t)s * a.C, dxv);
     }
   }
   // partials: part[(b * ntb + tb)][c][0 .. W - 1 weight, W bias]
   float* pp = a.part + ((int64_t)(b * gridDim.y + tb) * a.C + c0) * (W + 1);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
+  for (int e = 0; e < kConvCh; ++e) {
 #pragma unroll
     for (int w = 0; w < W; ++w) pp[e * (W + 1) + w] = dwp[e][w];
     pp[e * (W + 1) + W] = dbp[e];
@@ -269,7 +286,7 @@ __global__ __launch_bounds__(256) void short_conv_split_kernel(const float* __re
 template <typename T>
 hipError_t launch_short_conv(const ConvArgs& a, int W, bool bwd, hipStream_t stream) {
   const int ntb = (a.T + kConvTB - 1) / kConvTB;
-  const dim3 grid((a.C / 8 + 63) / 64, ntb, a.B);
+  const dim3 grid((a.C / kConvCh + 63) / 64, ntb, a.B);
 #define LINATT_CONV_W(WW)                                                              \
   case WW:                                                                             \
     if (bwd) short_conv_bwd_kernel<T, WW><<<grid, dim3(64), 0, stream>>>(a);           \
