@@ -317,7 +317,7 @@ size_t short_conv_bwd_workspace(int B, int T, int C, int W) {
 // ---------------------------------------------------------------------------
 // RMSNorm
 // ---------------------------------------------------------------------------
-constexpr int kRmsRows = 4;  // rows per lane group in the forward
+constexpr int kRmsRows = 4;  // rows per lane group and step, forward and backward
 
 template <typename T, int L>  // L = d / 8 lanes per row
 __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ x,
@@ -367,26 +367,41 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const T* __restrict__ 
   float dwp[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) dwp[e] = 0.f;
-  for (int row = blockIdx.x * RPB + rg; row < n; row += gridDim.x * RPB) {
-    float xv[8], g[8], wv[8];
-    load8f<T>(x + (int64_t)row * d + 8 * li, xv);
-    load8f<T>(dy + (int64_t)row * d + 8 * li, g);
-    const float r = rstd[row];
-    float dot = 0.f;
+  float wv[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      wv[e] = wt ? wt[8 * li + e] : 1.f;
-      xv[e] *= r;  // xh
-      dwp[e] += g[e] * xv[e];
-      g[e] *= wv[e];
-      dot += g[e] * xv[e];
+  for (int e = 0; e < 8; ++e) wv[e] = wt ? wt[8 * li + e] : 1.f;
+  // kRmsRows rows per lane group and step: every load of the step is issued
+  // before the first row's arithmetic
+  for (int row0 = blockIdx.x * RPB * kRmsRows + rg; row0 < n; row0 += gridDim.x * RPB * kRmsRows) {
+    float xv[kRmsRows][8], g[kRmsRows][8], r[kRmsRows];
+#pragma unroll
+    for (int k = 0; k < kRmsRows; ++k) {
+      const int row = row0 + k * RPB;
+      if (row < n) {
+        load8f<T>(x + (int64_t)row * d + 8 * li, xv[k]);
+        load8f<T>(dy + (int64_t)row * d + 8 * li, g[k]);
+        r[k] = rstd[row];
+      }
     }
 #pragma unroll
-    for (int off = L / 2; off > 0; off >>= 1) dot += __shfl_xor(dot, off);
-    dot /= d;
+    for (int k = 0; k < kRmsRows; ++k) {
+      const int row = row0 + k * RPB;
+      if (row >= n) break;  // uniform over the row's L lanes
+      float dot = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) g[e] = r * (g[e] - xv[e] * dot);
-    store8f<T>(dx + (int64_t)row * d + 8 * li, g);
+      for (int e = 0; e < 8; ++e) {
+        xv[k][e] *= r[k];  // xh
+        dwp[e] += g[k][e] * xv[k][e];
+        g[k][e] *= wv[e];
+        dot += g[k][e] * xv[k][e];
+      }
+#pragma unroll
+      for (int off = L / 2; off > 0; off >>= 1) dot += __shfl_xor(dot, off);
+      dot /= d;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) g[k][e] = r[k] * (g[k][e] - xv[k][e] * dot);
+      store8f<T>(dx + (int64_t)row * d + 8 * li, g[k]);
+    }
   }
   // per-block weight-gradient partial: sum over the block's row groups
 #pragma unroll
@@ -400,7 +415,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const T* __restrict__ 
 }
 
 int rmsnorm_bwd_blocks(int n, int d) {
-  const int rpb = 256 / (d / 8);
+  const int rpb = 256 / (d / 8) * kRmsRows;
   const int need = (n + rpb - 1) / rpb;
   return need < 1024 ? need : 1024;
 }
