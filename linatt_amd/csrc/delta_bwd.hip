@@ -568,7 +568,7 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
                   lane);
   if (w == 0) dma4(a.beta + ((size_t)b * Tn + min(t0 + lane, Tn - 1)) * H + h, Bs);
 
-  // 2. Mq [i][j] tile and Z^T (waves 0-3)
+  // 2. Mq [i][j] tile and the row sums of Z = X o Aqk (waves 0-3)
   if (w < 4) {
     const int xi = 32 * xib + cl;  // this lane's i
     const float Gi = Gs[xi];
