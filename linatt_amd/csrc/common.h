@@ -206,6 +206,34 @@ __device__ __forceinline__ void vm_wait_barrier_n(int n) {
   }
 }
 
+// s_waitcnt vmcnt(n) alone, for a wave-uniform n in [0, 15] (larger n waits
+// for everything); the same in-order argument as vm_wait_barrier.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory");
+}
+__device__ __forceinline__ void vm_wait_n(int n) {
+  switch (n) {
+    case 15: vm_wait<15>(); break;
+    case 14: vm_wait<14>(); break;
+    case 13: vm_wait<13>(); break;
+    case 12: vm_wait<12>(); break;
+    case 11: vm_wait<11>(); break;
+    case 10: vm_wait<10>(); break;
+    case 9: vm_wait<9>(); break;
+    case 8: vm_wait<8>(); break;
+    case 7: vm_wait<7>(); break;
+    case 6: vm_wait<6>(); break;
+    case 5: vm_wait<5>(); break;
+    case 4: vm_wait<4>(); break;
+    case 3: vm_wait<3>(); break;
+    case 2: vm_wait<2>(); break;
+    case 1: vm_wait<1>(); break;
+    default: vm_wait<0>(); break;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // 64 x 64 tiles of 16-bit elements in LDS: 128-byte rows, unpadded, with the
 // 16-byte chunk c of row r stored in slot c ^ f(r),

@@ -93,15 +93,20 @@ __global__ __launch_bounds__(state_bwd_threads()) void delta_state_bwd_kernel(De
   constexpr int NTILE = 3 * KT + 2;               // K, W, Qg, Aqk, dO (the 64 columns holding ours)
   constexpr int SLOT = NTILE * TE + 2 * 64 * 4 / (int)sizeof(T);  // + G and e^(gamma - G) of the chunk (f32)
   static_assert(NDT % 2 == 0 && NCW == 2 && OPW % kStateBwdCopyWaves == 0, "key dims over two compute waves");
-  __shared__ __attribute__((aligned(16))) T Sh[2 * SLOT];
   // per chunk (two buffers): the dh^T blocks (64 key dims each) and the
   // dv_new^T block of the 32 columns, staged for the copy waves' stores;
   // also the home of the chunk's dS images (2 ND2 * 128 slots, before MID)
   constexpr int NSTG = NDT / 2 + 1;
+  // ring slots: three (copies two chunks ahead) where LDS allows (K = V = 64),
+  // else two
+  constexpr int FIXED = (2 * NSTG * 256 + NCW * 2 * 64) * 16;
+  constexpr int NSLOT = 3 * SLOT * (int)sizeof(T) + FIXED <= 160 * 1024 ? 3 : 2;
+  __shared__ __attribute__((aligned(16))) T Sh[NSLOT * SLOT];
   __shared__ __attribute__((aligned(16))) u32x4 Stg[2][NSTG][256];
   static_assert(2 * ND2 * 128 <= (NSTG - 1) * 256, "dS images fit below the dv_new^T block");
   // dVn images: -dVn rows of compute wave p as B operands (k-steps j = 0, 1)
   __shared__ __attribute__((aligned(16))) u32x4 Xv[NCW][2][64];
+  static_assert(NSLOT * SLOT * (int)sizeof(T) + FIXED <= 160 * 1024, "LDS");
 
   const int lane = threadIdx.x & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -129,7 +134,7 @@ __global__ __launch_bounds__(state_bwd_threads()) void delta_state_bwd_kernel(De
   // chunks, the general path for the last one (rows past T clamped)
   const int cw = w - NCW;
   auto issue = [&](int c) __attribute__((always_inline)) {
-    T* sl = Sh + (c & 1) * SLOT;
+    T* sl = Sh + (c % NSLOT) * SLOT;
     const int t0 = c * kChunk;
     const size_t ci = (size_t)bh * NT + c;
     const T* wtg = (const T*)(a.ctx + L.W) + ci * 64 * DK;  // W [i][d], natural
@@ -186,21 +191,34 @@ __global__ __launch_bounds__(state_bwd_threads()) void delta_state_bwd_kernel(De
       flush_rows<T>(Stg[c & 1][NDT / 2], (T*)(a.ws + L.dVnT) + (ci * DV + 32 * part) * 64, 64, lane);
   };
   if (w >= NCW) {
+    // this wave's vector-memory ops per chunk of copies (G and e^(gamma - G):
+    // one more for copy wave 0)
+    const int nops = OPC * NTILE + (GATED && cw == 0 ? 1 : 0);
     issue(NT - 1);
+    if (NSLOT == 3 && NT > 1) issue(NT - 2);
 #pragma unroll 1
     for (int c = NT - 1; c >= 0; --c) {
-      vm_drain();  // this wave's copies of chunk c (and its stores of chunk c + 2) are done
+      // chunk c's copies are done.  With three slots the previous iteration
+      // ended with chunk c - 2's copies (issued after its stores), which may
+      // stay in flight; the first chunk and chunk 0 wait for everything.
+      if (NSLOT == 3 && c > 0 && c < NT - 1) vm_wait_n(nops);
+      else vm_drain();
       const int t0 = c * kChunk;
       if (!GATED && t0 + kChunk > Tn) {
         // ungated Z = scale q^T dO with raw q tiles: dO rows past T (copies
         // of the last row) are zeroed, each copy wave in its own rows
         const int r0 = max(Tn - t0, 8 * OPC * cw), r1 = 8 * OPC * (cw + 1);
         for (int idx = lane; idx < (r1 - r0) * 8; idx += 64)
-          reinterpret_cast<u32x4*>(ot(Sh + (c & 1) * SLOT) + (r0 + idx / 8) * 64)[idx % 8] = u32x4{0u, 0u, 0u, 0u};
+          reinterpret_cast<u32x4*>(ot(Sh + (c % NSLOT) * SLOT) + (r0 + idx / 8) * 64)[idx % 8] = u32x4{0u, 0u, 0u, 0u};
       }
       block_barrier();  // TOP
-      if (c > 0) issue(c - 1);
-      if (c < NT - 1) flush(c + 1);
+      if (NSLOT == 3) {
+        if (c < NT - 1) flush(c + 1);
+        if (c > 1) issue(c - 2);  // into chunk c + 1's slot
+      } else {
+        if (c > 0) issue(c - 1);
+        if (c < NT - 1) flush(c + 1);
+      }
       block_barrier();  // MID: chunk c + 1's staged outputs are read
     }
     block_barrier();  // chunk 0 staged
@@ -232,7 +250,7 @@ __global__ __launch_bounds__(state_bwd_threads()) void delta_state_bwd_kernel(De
   for (int c = NT - 1; c >= 0; --c) {
     const int t0 = c * kChunk;
     block_barrier();  // TOP
-    T* sl = Sh + (c & 1) * SLOT;
+    T* sl = Sh + (c % NSLOT) * SLOT;
     const T* Os = ot(sl);
     const int oc0 = 32 * (part & 1);
     const u32x4* oimg = &Stg[c & 1][0][0] + (1 - p) * (ND2 * 2 * 64);
