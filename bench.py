@@ -560,9 +560,9 @@ def _cpu_model():
 # inside the timed run, so the figure is carried here and refreshed with the
 # profile.
 MEASURED_TRAFFIC_BYTES = {
-    "fwd": int((122.9 + 30.5) * 1e6),
-    "bwd_dq": int((182.2 + 61.2) * 1e6),
-    "bwd_dkdv": int((170.5 + 50.3) * 1e6),
+    "fwd": int((121.7 + 30.5) * 1e6),
+    "bwd_dq": int((182.1 + 61.1) * 1e6),
+    "bwd_dkdv": int((170.9 + 50.3) * 1e6),
 }
 
 
