@@ -57,10 +57,8 @@ namespace {
 
 using namespace linatt;
 
-// Returns 1 and sets *err when a kernel exists for the combination.  With
-// one group the sum form sum_{g,g'} (q_g . k_g')^2 is the concat form
-// (q . k)^2, so num_groups = 1 runs the concat kernels, whose forward has the
-// pipelined body for unmasked tiles.
+// Returns 1 and sets *err when a kernel exists for the combination (one
+// group of the sum form runs the concat kernels: launch_kata_fwd / _bwd).
 hipError_t dispatch_fwd(const KataArgs& a, int dtype, int variant, bool decay, hipStream_t s,
                         bool* found) {
   *found = false;
@@ -68,7 +66,7 @@ hipError_t dispatch_fwd(const KataArgs& a, int dtype, int variant, bool decay, h
   if (dtype == dtype_of<T>() && a.DK == DK_ && a.DV == DV_ && a.M == M_) {          \
     *found = true;                                                                  \
     if (decay) return launch_kata_fwd<T, DK_, DV_, M_, false, true>(a, s);           \
-    if (variant == LINATT_KATA_SUM && M_ > 1) return launch_kata_fwd<T, DK_, DV_, M_, true, false>(a, s); \
+    if (variant == LINATT_KATA_SUM) return launch_kata_fwd<T, DK_, DV_, M_, true, false>(a, s); \
     return launch_kata_fwd<T, DK_, DV_, M_, false, false>(a, s);                    \
   }
   LINATT_KATA_SHAPES(LINATT_TRY_FWD)
@@ -83,7 +81,7 @@ hipError_t dispatch_bwd(const KataArgs& a, int parts, int dtype, int variant, bo
   if (dtype == dtype_of<T>() && a.DK == DK_ && a.DV == DV_ && a.M == M_) {          \
     *found = true;                                                                  \
     if (decay) return launch_kata_bwd<T, DK_, DV_, M_, false, true>(a, parts, s);    \
-    if (variant == LINATT_KATA_SUM && M_ > 1) return launch_kata_bwd<T, DK_, DV_, M_, true, false>(a, parts, s); \
+    if (variant == LINATT_KATA_SUM) return launch_kata_bwd<T, DK_, DV_, M_, true, false>(a, parts, s); \
     return launch_kata_bwd<T, DK_, DV_, M_, false, false>(a, parts, s);             \
   }
   LINATT_KATA_SHAPES(LINATT_TRY_BWD)

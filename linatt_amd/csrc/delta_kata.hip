@@ -577,14 +577,13 @@ hipError_t launch_dkata_fwd(const DKataArgs& a, hipStream_t stream) {
     dkata_U_kernel<T, D, DV, M><<<dim3(BH), dim3(256), 0, stream>>>(a, cb, ce);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  // readout: the KATA sum-score forward of (q, k, U) with the same scale (one
-  // group: the sum form is the concat form, whose kernels run it faster)
+  // readout: the KATA sum-score forward of (q, k, U) with the same scale
   KataArgs r{};
   r.q = a.q; r.k = a.k; r.v = a.ws + a.L.Ub; r.c = nullptr;
   r.o = a.ws + a.L.Ob; r.den = a.den;
   r.B = a.B; r.T = a.T; r.HQ = a.H; r.H = a.H; r.DK = D; r.DV = DV; r.M = M;
   r.scale = a.scale;
-  e = launch_kata_fwd<T, D, DV, M, (M > 1), false>(r, stream);
+  e = launch_kata_fwd<T, D, DV, M, true, false>(r, stream);
   if (e != hipSuccess) return e;
   const int64_t n4 = (int64_t)a.B * a.T * a.H * DV / 4;
   const int blocks = (int)((n4 + 255) / 256 < 4096 ? (n4 + 255) / 256 : 4096);
@@ -1001,7 +1000,7 @@ hipError_t launch_dkata_bwd(const DKataBwdArgs& a, hipStream_t stream) {
   r.dout = a.bws + a.BL.dOp; r.dq = a.dq; r.dk = a.bws + a.BL.dkr; r.dv = a.bws + a.BL.dU;
   r.delta = (float*)(a.bws + a.BL.kws);
   r.B = a.B; r.T = a.T; r.HQ = a.H; r.H = a.H; r.DK = D; r.DV = DV; r.M = M; r.scale = a.scale;
-  e = launch_kata_bwd<T, D, DV, M, (M > 1), false>(r, KATA_BWD_DQ | KATA_BWD_DKDV, stream);
+  e = launch_kata_bwd<T, D, DV, M, true, false>(r, KATA_BWD_DQ | KATA_BWD_DKDV, stream);
   if (e != hipSuccess) return e;
   // chunk-sequential only inside super-chunks, last one first; the later
   // super-chunks' part of R in parallel before each
@@ -1023,7 +1022,7 @@ hipError_t launch_dkata_bwd(const DKataBwdArgs& a, hipStream_t stream) {
   x.dout = a.bws + a.BL.Xn; x.dq = a.bws + a.BL.dqe; x.dk = a.bws + a.BL.dke; x.dv = a.bws + a.BL.dve;
   x.delta = (float*)(a.bws + a.BL.kws);
   x.B = a.B; x.T = a.T; x.HQ = a.H; x.H = a.H; x.DK = D; x.DV = DV; x.M = M; x.scale = a.scale;
-  e = launch_kata_bwd<T, D, DV, M, (M > 1), false>(x, KATA_BWD_DQ | KATA_BWD_DKDV, stream);
+  e = launch_kata_bwd<T, D, DV, M, true, false>(x, KATA_BWD_DQ | KATA_BWD_DKDV, stream);
   if (e != hipSuccess) return e;
   dkata_bwd_fix_kernel<T, D, DV, M><<<dim3(BH * NC), dim3(256), 0, stream>>>(a);
   return hipGetLastError();

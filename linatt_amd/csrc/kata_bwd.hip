@@ -1040,35 +1040,40 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
 
 template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
 hipError_t launch_kata_bwd(const KataArgs& a, int parts, hipStream_t stream) {
-  const float scale2 = a.scale * a.scale;
-  const int nqt = (a.T + 127) / 128;
-  constexpr bool kTiles = sizeof(T) == 2 && DK == 64 && DV == 64;
-  if (parts & KATA_BWD_DQ) {
-    const int nbh = a.B * a.HQ;
-    if constexpr (kTiles)
-      kata_bwd_dq_tile_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbh), dim3(256), 0, stream>>>(
+  if constexpr (SUM && M == 1) {
+    // one group: the sum form is the concat form
+    return launch_kata_bwd<T, DK, DV, M, false, DECAY>(a, parts, stream);
+  } else {
+    const float scale2 = a.scale * a.scale;
+    const int nqt = (a.T + 127) / 128;
+    constexpr bool kTiles = sizeof(T) == 2 && DK == 64 && DV == 64;
+    if (parts & KATA_BWD_DQ) {
+      const int nbh = a.B * a.HQ;
+      if constexpr (kTiles)
+        kata_bwd_dq_tile_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbh), dim3(256), 0, stream>>>(
+            (const T*)a.q, (const T*)a.k, (const T*)a.v, (const T*)a.o, a.den, (const T*)a.dout,
+            (T*)a.dq, a.delta, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt, nbh);
+      else
+      kata_bwd_dq_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbh), dim3(256), 0, stream>>>(
           (const T*)a.q, (const T*)a.k, (const T*)a.v, (const T*)a.o, a.den, (const T*)a.dout,
           (T*)a.dq, a.delta, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt, nbh);
-    else
-    kata_bwd_dq_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbh), dim3(256), 0, stream>>>(
-        (const T*)a.q, (const T*)a.k, (const T*)a.v, (const T*)a.o, a.den, (const T*)a.dout,
-        (T*)a.dq, a.delta, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt, nbh);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
-  if (parts & KATA_BWD_DKDV) {
-    const int nbk = a.B * a.H;
-    if constexpr (kTiles)
-      kata_bwd_dkdv_tile_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbk), dim3(256), 0, stream>>>(
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
+    if (parts & KATA_BWD_DKDV) {
+      const int nbk = a.B * a.H;
+      if constexpr (kTiles)
+        kata_bwd_dkdv_tile_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbk), dim3(256), 0, stream>>>(
+            (const T*)a.q, (const T*)a.k, (const T*)a.v, a.den, a.delta, (const T*)a.dout,
+            (T*)a.dk, (T*)a.dv, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt, nbk);
+      else
+      kata_bwd_dkdv_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbk), dim3(256), 0, stream>>>(
           (const T*)a.q, (const T*)a.k, (const T*)a.v, a.den, a.delta, (const T*)a.dout,
           (T*)a.dk, (T*)a.dv, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt, nbk);
-    else
-    kata_bwd_dkdv_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbk), dim3(256), 0, stream>>>(
-        (const T*)a.q, (const T*)a.k, (const T*)a.v, a.den, a.delta, (const T*)a.dout,
-        (T*)a.dk, (T*)a.dv, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt, nbk);
-    return hipGetLastError();
+      return hipGetLastError();
+    }
+    return hipSuccess;
   }
-  return hipSuccess;
 }
 
 #define LINATT_BWD_INST(T, DK, DV, M)                                                                 \

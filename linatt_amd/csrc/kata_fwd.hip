@@ -463,19 +463,25 @@ __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
 
 template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
 hipError_t launch_kata_fwd(const KataArgs& a, hipStream_t stream) {
-  const int nqt = (a.T + 127) / 128;
-  const int nbh = a.B * a.HQ;
-  dim3 grid(nqt * nbh), block(256);
-  if constexpr (sizeof(T) == 2 && DK == 64 && DV == 64) {
-    kata_fwd_tile_kernel<T, DK, DV, M, SUM, DECAY><<<grid, block, 0, stream>>>(
-        (const T*)a.q, (const T*)a.k, (const T*)a.v, a.c, (T*)a.o, a.den, a.T, a.HQ, a.H,
-        a.scale * a.scale, nqt, nbh);
+  if constexpr (SUM && M == 1) {
+    // one group: the sum form sum_{g,g'} (q_g . k_g')^2 is the concat form
+    // (q . k)^2, whose tile kernel has the pipelined body for unmasked tiles
+    return launch_kata_fwd<T, DK, DV, M, false, DECAY>(a, stream);
+  } else {
+    const int nqt = (a.T + 127) / 128;
+    const int nbh = a.B * a.HQ;
+    dim3 grid(nqt * nbh), block(256);
+    if constexpr (sizeof(T) == 2 && DK == 64 && DV == 64) {
+      kata_fwd_tile_kernel<T, DK, DV, M, SUM, DECAY><<<grid, block, 0, stream>>>(
+          (const T*)a.q, (const T*)a.k, (const T*)a.v, a.c, (T*)a.o, a.den, a.T, a.HQ, a.H,
+          a.scale * a.scale, nqt, nbh);
+    } else {
+      kata_fwd_kernel<T, DK, DV, M, SUM, DECAY><<<grid, block, 0, stream>>>(
+          (const T*)a.q, (const T*)a.k, (const T*)a.v, a.c, (T*)a.o, a.den, a.T, a.HQ, a.H,
+          a.scale * a.scale, nqt, nbh);
+    }
     return hipGetLastError();
   }
-  kata_fwd_kernel<T, DK, DV, M, SUM, DECAY><<<grid, block, 0, stream>>>(
-      (const T*)a.q, (const T*)a.k, (const T*)a.v, a.c, (T*)a.o, a.den, a.T, a.HQ, a.H,
-      a.scale * a.scale, nqt, nbh);
-  return hipGetLastError();
 }
 
 #define LINATT_FWD_INST(T, DK, DV, M)                                                  \
