@@ -88,6 +88,8 @@ SHAPES = [  # B, T, H, K, V
     (1, 1, 1, 64, 64),
     (1, 64, 1, 64, 64),
     (2, 100, 2, 64, 64),
+    (1, 200, 2, 64, 64),   # NT = 4: every ring slot of the reverse pass in use
+    (1, 321, 1, 64, 64),   # NT = 6, ragged last chunk
     (1, 129, 1, 128, 128),
     (2, 256, 3, 128, 128),
 ]
@@ -209,13 +211,16 @@ def test_full_size(R, gated):
             assert e < 2e-2, (n, b, h, e)
 
 
-@pytest.mark.parametrize("gated", [False, True], ids=["config3_deltanet", "config4_gdn"])
-def test_repeat_runs_identical(R, gated):
+@pytest.mark.parametrize("gated,H,K", [(False, 6, 128), (True, 6, 128), (False, 12, 64), (True, 12, 64)],
+                         ids=["config3_deltanet", "config4_gdn", "h12_k64_deltanet", "h12_k64_gdn"])
+def test_repeat_runs_identical(R, gated, H, K):
     """Every kernel of the path is deterministic (no atomics, fixed reduction
     order), so repeated fwd+bwd runs on the same inputs must agree bit for
     bit on every head.  A cross-wave LDS race shows up here as a few heads
-    that differ between runs, which a per-head oracle check can miss."""
-    B, T, H, K = 8, 2048, 6, 128
+    that differ between runs, which a per-head oracle check can miss.  The
+    K = V = 64 shape runs the three-slot reverse ring and two backward chunk
+    workgroups per CU."""
+    B, T = 8, 2048
     gg = torch.Generator().manual_seed(5)
     q = torch.randn(B, T, H, K, generator=gg).to(torch.bfloat16)
     k = D.l2norm(torch.randn(B, T, H, K, generator=gg)).to(torch.bfloat16)
