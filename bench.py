@@ -260,9 +260,12 @@ def bench_mixer(steps, settle_s):
     """The mixer's non-GEMM ops at the 200M KATA shape (B8 T2048, hidden 768,
     12 heads of 64; configs/model/200m/kata_quadratic_200m.yaml: short conv 4
     with SiLU on q, k, v, output RMSNorm): linatt_short_conv_fwd/bwd on one
-    (B, T, 768) bf16 tensor and linatt_rmsnorm_fwd/bwd on (B*T*12, 64) bf16,
-    each against HBM with its compulsory bytes (inputs read once, outputs
-    written once)."""
+    (B, T, 768) bf16 tensor, linatt_rmsnorm_fwd/bwd on (B*T*12, 64) bf16 and
+    linatt_rope forward / inverse (interleaved, the full head), each against
+    HBM with its compulsory bytes (inputs read once, outputs written once);
+    then the fused q/k prologue linatt_qk_prologue_fwd/bwd (the same three
+    steps with the RMSNorm over each head, one kernel each way) beside the sum
+    of the three unfused kernels."""
     import torch
     from linatt_amd import _lib
     L = _lib.load()
@@ -281,6 +284,8 @@ def bench_mixer(steps, settle_s):
     rstd = torch.empty(n, device=dev)
     rdw = torch.empty(D, device=dev)
     rws = torch.empty(L.linatt_rmsnorm_bwd_workspace_bytes(n, D), device=dev, dtype=torch.uint8)
+    qws = torch.empty(L.linatt_qk_prologue_bwd_workspace_bytes(B, T, H, D, W), device=dev,
+                      dtype=torch.uint8)
     P, sp, bf = _lib.ptr, _lib.stream_of(x), _lib.LINATT_BFLOAT16
     parts = [
         ("short_conv_fwd", lambda: _lib.check("linatt_short_conv_fwd", L.linatt_short_conv_fwd(
@@ -291,6 +296,16 @@ def bench_mixer(steps, settle_s):
             P(x), P(rw), P(y), P(rstd), n, D, 1e-5, bf, sp))),
         ("rmsnorm_bwd", lambda: _lib.check("linatt_rmsnorm_bwd", L.linatt_rmsnorm_bwd(
             P(x), P(rw), P(rstd), P(dy), P(dx), P(rdw), P(rws), n, D, bf, sp))),
+        ("rope_fwd", lambda: _lib.check("linatt_rope", L.linatt_rope(
+            P(x), P(y), B, T, H, D, D, 10000.0, 0, 1, 0, bf, sp))),
+        ("rope_bwd", lambda: _lib.check("linatt_rope", L.linatt_rope(
+            P(dy), P(dx), B, T, H, D, D, 10000.0, 0, 1, 1, bf, sp))),
+        ("qk_prologue_fwd", lambda: _lib.check("linatt_qk_prologue_fwd", L.linatt_qk_prologue_fwd(
+            P(x), P(w), None, None, P(rw), P(y), None, B, T, H, D, W, 1, 1, 1e-5, D, D, 10000.0,
+            0, 1, bf, sp))),
+        ("qk_prologue_bwd", lambda: _lib.check("linatt_qk_prologue_bwd", L.linatt_qk_prologue_bwd(
+            P(x), P(w), None, None, P(rw), P(dy), P(dx), P(dw), None, P(rdw), P(qws), B, T, H, D,
+            W, 1, 1, 1e-5, D, D, 10000.0, 0, 1, bf, sp))),
     ]
     settle(parts, settle_s)
     stream = torch.cuda.current_stream(dev)
@@ -303,7 +318,8 @@ def bench_mixer(steps, settle_s):
     torch.cuda.synchronize()
     nb = B * T * C * 2
     alg = {"short_conv_fwd": 2 * nb, "short_conv_bwd": 3 * nb, "rmsnorm_fwd": 2 * nb + n * 4,
-           "rmsnorm_bwd": 3 * nb + n * 4}
+           "rmsnorm_bwd": 3 * nb + n * 4, "rope_fwd": 2 * nb, "rope_bwd": 2 * nb,
+           "qk_prologue_fwd": 2 * nb, "qk_prologue_bwd": 3 * nb}
     out = {"config": {"B": B, "T": T, "hidden": C, "kernel_size": W, "heads": H, "head_dim": D,
                       "dtype": "bf16", "seed": 7}}
     for i, (name, _) in enumerate(parts):
@@ -311,6 +327,10 @@ def bench_mixer(steps, settle_s):
         gbs = alg[name] / (ms * 1e-3) / 1e9
         out[name] = {"avg_ms": round(ms, 4), "alg_mb": round(alg[name] / 1e6, 1),
                      "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+    for d in ("fwd", "bwd"):
+        chain = sum(out[f"{k}_{d}"]["avg_ms"] for k in ("short_conv", "rmsnorm", "rope"))
+        out[f"qk_chain_unfused_{d}_ms"] = round(chain, 4)
+        out[f"qk_fused_speedup_{d}"] = round(chain / out[f"qk_prologue_{d}"]["avg_ms"], 2)
     return out
 
 

@@ -313,6 +313,41 @@ int linatt_short_conv_bwd(const void* x, const float* weight, const float* bias,
 int linatt_rope(const void* x, void* y, int B, int T, int H, int D, int rot_dim, float base,
                 int offset, int interleaved, int inverse, int dtype, void* stream);
 
+/* Fused q/k prologue: the short convolution + activation, the per-head norm
+ * and the rotary embedding in one pass.  It replaces the chain that
+ * kata/layer.py:305-318, 345-372 runs on q and on k as three modules
+ * (ShortConvolution -> RMSNorm(head_k_dim, fp32 weight) or l2norm ->
+ * RotaryEmbedding), with the intermediates kept in fp32 instead of rounded to
+ * the input dtype between the modules:
+ *   u = act(bias + sum_w conv_weight[c,w] x[b, t-(W-1)+w, c])   (as
+ *       linatt_short_conv_fwd, with cache_in / cache_out),
+ *   norm 1: n = u (mean_d u^2 + eps)^-1/2 norm_weight (norm_weight NULL: 1);
+ *   norm 2: n = u (sum_d u^2 + eps)^-1/2 (fla l2norm; norm_weight must be
+ *           NULL); norm 0: n = u;
+ *   y = n rotated as linatt_rope rotates each row of rope_width dims (the
+ *       head dim D for full-head RoPE, the group width E for rope_group) over
+ *       its first rot_dim dims, positions offset .. offset + T - 1;
+ *       rot_dim 0: no rotation.
+ * x, y (B,T,H*D) [dtype] (y is (B,T,H,D)); conv_weight (H*D,W), conv_bias
+ * (H*D) or NULL, norm_weight (D): float32.  D in {32, 64, 128}, W in
+ * {2,3,4}; rope_width a multiple of 4 dividing D; rot_dim even and at most
+ * rope_width, a multiple of 8 when not interleaved.  The backward gives dx
+ * and float32 dconv_weight (H*D,W), dconv_bias (H*D, may be NULL),
+ * dnorm_weight (D, may be NULL); no gradient flows to cache_in.
+ * Workspace: linatt_qk_prologue_bwd_workspace_bytes. */
+int linatt_qk_prologue_fwd(const void* x, const float* conv_weight, const float* conv_bias,
+                           const void* cache_in, const float* norm_weight, void* y,
+                           void* cache_out, int B, int T, int H, int D, int W, int activation,
+                           int norm, float eps, int rope_width, int rot_dim, float base,
+                           int offset, int interleaved, int dtype, void* stream);
+size_t linatt_qk_prologue_bwd_workspace_bytes(int B, int T, int H, int D, int W);
+int linatt_qk_prologue_bwd(const void* x, const float* conv_weight, const float* conv_bias,
+                           const void* cache_in, const float* norm_weight, const void* dy,
+                           void* dx, float* dconv_weight, float* dconv_bias, float* dnorm_weight,
+                           void* workspace, int B, int T, int H, int D, int W, int activation,
+                           int norm, float eps, int rope_width, int rot_dim, float base,
+                           int offset, int interleaved, int dtype, void* stream);
+
 /* RMSNorm over the last dim of a contiguous (n, d) array, fp32 arithmetic,
  * replacing fla.modules.RMSNorm as the mixer uses it (output norm
  * kata/layer.py:199-205, 539; q/k norm :126-128, 347):

@@ -62,6 +62,9 @@ SIGNATURES = {
     "linatt_short_conv_bwd_workspace_bytes": (_sz, [_i] * 4),
     "linatt_short_conv_bwd": (_i, [_vp] * 9 + [_i] * 6 + [_vp]),
     "linatt_rope": (_i, [_vp] * 2 + [_i] * 5 + [_f] + [_i] * 4 + [_vp]),
+    "linatt_qk_prologue_fwd": (_i, [_vp] * 7 + [_i] * 7 + [_f, _i, _i, _f, _i, _i, _i, _vp]),
+    "linatt_qk_prologue_bwd_workspace_bytes": (_sz, [_i] * 5),
+    "linatt_qk_prologue_bwd": (_i, [_vp] * 11 + [_i] * 7 + [_f, _i, _i, _f, _i, _i, _i, _vp]),
     "linatt_linear_scan_fwd": (_i, [_vp] * 5 + [_i] * 5 + [_f] * 2 + [_i] + [_vp]),
     "linatt_rmsnorm_fwd": (_i, [_vp] * 4 + [_i, _i, _f, _i, _vp]),
     "linatt_rmsnorm_bwd_workspace_bytes": (_sz, [_i, _i]),

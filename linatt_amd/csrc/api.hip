@@ -495,6 +495,95 @@ int linatt_linear_scan_fwd(const void* q, const void* k, const void* v, void* o,
   return LINATT_OK;
 }
 
+static int check_qk(const char* fn, int B, int T, int H, int D, int W, int activation, int norm,
+                    const float* norm_weight, float eps, int rope_width, int rot_dim, float base,
+                    int offset, int interleaved, int dtype) {
+  if (B <= 0 || T <= 0 || H <= 0 || D <= 0) return fail(LINATT_EINVAL, std::string(fn) + ": non-positive size");
+  if (B > 65535 || (T + 15) / 16 > 65535 || (int64_t)H * D > INT32_MAX / 8)
+    return fail(LINATT_EINVAL, std::string(fn) + ": B, T or H*D too large");
+  if (D != 32 && D != 64 && D != 128)
+    return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": head dim must be 32, 64 or 128");
+  if (W < 2 || W > 4) return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": kernel size must be 2, 3 or 4");
+  if (activation != 0 && activation != 1) return fail(LINATT_EINVAL, std::string(fn) + ": activation must be 0 (none) or 1 (silu)");
+  if (norm < 0 || norm > 2) return fail(LINATT_EINVAL, std::string(fn) + ": norm must be 0 (none), 1 (RMSNorm) or 2 (L2)");
+  if (norm == 2 && norm_weight) return fail(LINATT_EINVAL, std::string(fn) + ": the L2 norm takes no weight");
+  if (!(eps >= 0.f)) return fail(LINATT_EINVAL, std::string(fn) + ": eps must be >= 0");
+  if (rot_dim != 0) {
+    if (rope_width <= 0 || rope_width % 4 || D % rope_width)
+      return fail(LINATT_EINVAL, std::string(fn) + ": rope_width must be a multiple of 4 dividing the head dim");
+    if (rot_dim < 0 || rot_dim % 2 || rot_dim > rope_width)
+      return fail(LINATT_EINVAL, std::string(fn) + ": rot_dim must be even, positive and at most rope_width");
+    if (!interleaved && rot_dim % 8)
+      return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": a non-interleaved rotation needs rot_dim a multiple of 8");
+    if (!(base > 1.f)) return fail(LINATT_EINVAL, std::string(fn) + ": base must be > 1");
+    if (offset < 0) return fail(LINATT_EINVAL, std::string(fn) + ": offset must be >= 0");
+  }
+  if (!known_dtype(dtype)) return fail(LINATT_EINVAL, std::string(fn) + ": unknown dtype");
+  return LINATT_OK;
+}
+
+static QKArgs qk_args(const void* x, const float* w, const float* bias, const void* cache_in,
+                      const float* nw, int B, int T, int H, int D, int activation, int norm,
+                      float eps, int rope_width, int rot_dim, float base, int offset,
+                      int interleaved) {
+  QKArgs a{};
+  a.x = x; a.w = w; a.bias = bias; a.cache_in = cache_in; a.nw = norm == 1 ? nw : nullptr;
+  a.B = B; a.T = T; a.C = H * D; a.D = D; a.act = activation; a.norm = norm;
+  a.eps = eps; a.inv_n = norm == 1 ? 1.f / D : 1.f;
+  a.rot = rot_dim; a.rw = rot_dim ? rope_width : 0; a.interleaved = interleaved ? 1 : 0;
+  a.offset = offset; a.log2_base = rot_dim ? log2f(base) : 0.f;
+  return a;
+}
+
+int linatt_qk_prologue_fwd(const void* x, const float* conv_weight, const float* conv_bias,
+                           const void* cache_in, const float* norm_weight, void* y,
+                           void* cache_out, int B, int T, int H, int D, int W, int activation,
+                           int norm, float eps, int rope_width, int rot_dim, float base,
+                           int offset, int interleaved, int dtype, void* stream) {
+  g_last_error.clear();
+  const char* fn = "linatt_qk_prologue_fwd";
+  int st = check_qk(fn, B, T, H, D, W, activation, norm, norm_weight, eps, rope_width, rot_dim,
+                    base, offset, interleaved, dtype);
+  if (st) return st;
+  if (!x || !conv_weight || !y) return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  if (!aligned16(x) || !aligned16(y)) return fail(LINATT_EINVAL, std::string(fn) + ": x and y must be 16-byte aligned");
+  QKArgs a = qk_args(x, conv_weight, conv_bias, cache_in, norm_weight, B, T, H, D, activation,
+                     norm, eps, rope_width, rot_dim, base, offset, interleaved);
+  a.y = y; a.cache_out = cache_out;
+  hipError_t e = by_dtype(dtype, [&](auto t) { return launch_qk_prologue<decltype(t)>(a, W, false, (hipStream_t)stream); });
+  if (e != hipSuccess) return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
+size_t linatt_qk_prologue_bwd_workspace_bytes(int B, int T, int H, int D, int W) {
+  if (B <= 0 || T <= 0 || H <= 0 || D <= 0 || W < 2 || W > 4) return 0;
+  return qk_prologue_bwd_workspace(B, T, H * D, D, W);
+}
+
+int linatt_qk_prologue_bwd(const void* x, const float* conv_weight, const float* conv_bias,
+                           const void* cache_in, const float* norm_weight, const void* dy,
+                           void* dx, float* dconv_weight, float* dconv_bias, float* dnorm_weight,
+                           void* workspace, int B, int T, int H, int D, int W, int activation,
+                           int norm, float eps, int rope_width, int rot_dim, float base,
+                           int offset, int interleaved, int dtype, void* stream) {
+  g_last_error.clear();
+  const char* fn = "linatt_qk_prologue_bwd";
+  int st = check_qk(fn, B, T, H, D, W, activation, norm, norm_weight, eps, rope_width, rot_dim,
+                    base, offset, interleaved, dtype);
+  if (st) return st;
+  if (!x || !conv_weight || !dy || !dx || !dconv_weight || !workspace || (dnorm_weight && !norm_weight))
+    return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  if (!aligned16(x) || !aligned16(dy) || !aligned16(dx) || !aligned16(workspace))
+    return fail(LINATT_EINVAL, std::string(fn) + ": x, dy, dx and the workspace must be 16-byte aligned");
+  QKArgs a = qk_args(x, conv_weight, conv_bias, cache_in, norm_weight, B, T, H, D, activation,
+                     norm, eps, rope_width, rot_dim, base, offset, interleaved);
+  a.dy = dy; a.dx = dx; a.part = (float*)workspace;
+  a.dw = dconv_weight; a.db = dconv_bias; a.dnw = dnorm_weight;
+  hipError_t e = by_dtype(dtype, [&](auto t) { return launch_qk_prologue<decltype(t)>(a, W, true, (hipStream_t)stream); });
+  if (e != hipSuccess) return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
 static int check_rms(const char* fn, int n, int d, int dtype) {
   if (n <= 0 || d <= 0) return fail(LINATT_EINVAL, std::string(fn) + ": non-positive size");
   if (d % 8 || !pow2(d / 8) || d > 512)

@@ -33,6 +33,32 @@ template <typename T>
 hipError_t launch_short_conv(const ConvArgs& a, int W, bool bwd, hipStream_t stream);
 size_t short_conv_bwd_workspace(int B, int T, int C, int W);
 
+// Fused q/k prologue (mixer.hip): short convolution + activation, per-head
+// norm, rotary embedding, over (B, T, C = H D).
+struct QKArgs {
+  const void* x;         // (B, T, C) the projection output
+  const float* w;        // (C, W) convolution weight
+  const float* bias;     // (C) or null
+  const void* cache_in;  // (B, C, W) or null
+  const float* nw;       // (D) RMSNorm weight or null
+  void* y;               // (B, T, H, D)
+  void* cache_out;       // (B, C, W) or null
+  const void* dy;
+  void* dx;
+  float* part;    // convolution weight / bias partials, then their sums
+  float* npart;   // norm weight partials
+  float* dw;
+  float* db;
+  float* dnw;
+  int B, T, C, D, act, norm;  // norm: 0 none, 1 RMSNorm, 2 L2
+  float eps, inv_n;           // r = (inv_n sum u^2 + eps)^-1/2
+  int rw, rot, interleaved, offset;  // rotation rows of rw dims, first rot rotated; rot = 0: none
+  float log2_base;
+};
+template <typename T>
+hipError_t launch_qk_prologue(const QKArgs& a, int W, bool bwd, hipStream_t stream);
+size_t qk_prologue_bwd_workspace(int B, int T, int C, int D, int W);
+
 // RMSNorm over rows of d (mixer.hip): forward (out = y, rstd_out) or
 // backward (out = dx, dw with the partials workspace).
 template <typename T>

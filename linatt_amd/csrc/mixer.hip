@@ -78,8 +78,8 @@ __device__ __forceinline__ void store8f<float>(float* p, const float* v) {
 
 // kConvCh channels of input position pos of batch row b (pos < 0: the
 // cache, or 0)
-template <typename T, int W>
-__device__ __forceinline__ void conv_input(const ConvArgs& a, int b, int c0, int pos, float* out) {
+template <typename T, int W, typename A>
+__device__ __forceinline__ void conv_input(const A& a, int b, int c0, int pos, float* out) {
   if (pos >= 0) {
     load4f<T>((const T*)a.x + ((int64_t)b * a.T + pos) * a.C + c0, out);
   } else if (a.cache_in) {
@@ -251,24 +251,42 @@ __global__ __launch_bounds__(64) void short_conv_bwd_kernel(ConvArgs a) {
   }
 }
 
-// out[i] = sum_p part[p][i] for i < n, in a fixed order: 1024 threads per
-// block, 32 columns by 32 row phases (phase k sums rows k, k + 32, ...), then
-// one thread per column adds the 32 phase sums.
+// out[y][i] = sum_p part[p][i] for i < n over the rows p of block row y
+// (rows y rows_per .. min(np, (y + 1) rows_per) - 1), in a fixed order: 1024
+// threads per block, 32 columns by 32 row phases (phase k sums rows k, k + 32,
+// ... of the range, eight loads in flight), then one thread per column adds
+// the 32 phase sums.
 __global__ __launch_bounds__(1024) void colsum_kernel(const float* __restrict__ part,
-                                                      float* __restrict__ out, int np, int n) {
+                                                      float* __restrict__ out, int np, int n,
+                                                      int rows_per) {
   __shared__ float red[32][33];
   const int c = blockIdx.x * 32 + (threadIdx.x & 31), k = threadIdx.x >> 5;
+  const int p0 = blockIdx.y * rows_per, p1 = min(np, p0 + rows_per);
   float s = 0.f;
-  if (c < n)
-    for (int p = k; p < np; p += 32) s += part[(int64_t)p * n + c];
+  if (c < n) {
+    int p = p0 + k;
+    for (; p + 7 * 32 < p1; p += 8 * 32) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = part[(int64_t)(p + 32 * j) * n + c];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += v[j];
+    }
+    for (; p < p1; p += 32) s += part[(int64_t)p * n + c];
+  }
   red[k][threadIdx.x & 31] = s;
   __syncthreads();
   if (threadIdx.x < 32 && c < n) {
     float t = 0.f;
 #pragma unroll
     for (int j = 0; j < 32; ++j) t += red[j][threadIdx.x];
-    out[c] = t;
+    out[(int64_t)blockIdx.y * n + c] = t;
   }
+}
+
+// column sums of a (np, n) array in one block row
+static void colsum(const float* part, float* out, int np, int n, hipStream_t stream) {
+  colsum_kernel<<<dim3((n + 31) / 32), dim3(1024), 0, stream>>>(part, out, np, n, np);
 }
 
 // dweight[c][w] and dbias[c] from the summed partials [c][0 .. W - 1, W]
@@ -303,7 +321,7 @@ hipError_t launch_short_conv(const ConvArgs& a, int W, bool bwd, hipStream_t str
   if (e != hipSuccess || !bwd) return e;
   const int n = a.C * (W + 1), np = a.B * ntb;
   float* sum = a.part + (size_t)np * n;
-  colsum_kernel<<<dim3((n + 31) / 32), dim3(1024), 0, stream>>>(a.part, sum, np, n);
+  colsum(a.part, sum, np, n, stream);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   short_conv_split_kernel<<<dim3((n + 255) / 256), dim3(256), 0, stream>>>(sum, a.dw, a.db, a.C, W);
   return hipGetLastError();
@@ -449,7 +467,7 @@ hipError_t launch_rmsnorm(const void* x, const float* w, const float* rstd_in, c
 #undef LINATT_RMS_L
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !bwd || !dw) return e;
-  colsum_kernel<<<dim3((d + 31) / 32), dim3(1024), 0, stream>>>(part, dw, nbb, d);
+  colsum(part, dw, nbb, d, stream);
   return hipGetLastError();
 }
 
@@ -501,6 +519,345 @@ hipError_t launch_rope(const void* x, void* y, int B, int T_, int H, int D, int 
       inverse ? -1.f : 1.f);
   return hipGetLastError();
 }
+
+// ---------------------------------------------------------------------------
+// Fused q/k prologue.  kata/layer.py:305-372 runs three modules in a row on q
+// and on k: the short convolution with SiLU (fla ShortConvolution), the
+// per-head norm (fla RMSNorm with an fp32 weight, or fla's l2norm) and the
+// rotary embedding (fla RotaryEmbedding: interleaved over the whole head, or,
+// with rope_group, non-interleaved over each E-dim group).  Here one pass
+// reads the projection output once and writes the rotated rows once; the
+// intermediates stay in fp32 registers (the three-module chain rounds them to
+// the input dtype twice).  Per (token, head):
+//   z = bias + sum_w weight[w] x[t - (W - 1) + w],   u = act(z),
+//   n = u r nw,  r = (inv_n sum_d u^2 + eps)^-1/2    (RMSNorm: inv_n = 1 / D;
+//                                                      L2: inv_n = 1, no nw),
+//   y_j = n_j cos_j + n_partner(j) sin'_j,
+// where, for rotation rows of rw dims whose first rot dims rotate, the pair
+// of dim j is (j, j ^ 1) when interleaved and (j, j +- rot / 2) otherwise,
+// cos_j / sin'_j hold cos and -sin (first of a pair) or +sin (second) of the
+// angle (t + offset) base^(-2p / rot), and dims past rot have (1, 0).
+// A lane owns kConvCh = 4 channels and a run of kQkTB tokens, as in the
+// convolution; a head's D / 4 lanes are adjacent in one wave, so the norm's
+// sums are shuffle reductions over them.  The angles come from an LDS table
+// per block (tokens x rotation dims) filled with the formula of rope_kernel,
+// so each table entry costs one sincos per block rather than one per lane.
+// The backward recomputes z, u, r, rotates dy back (sin' negated) to g, then
+//   du = r (g nw - uh inv_n sum_d g nw uh),  uh = u r,  dnw += g uh,
+//   dz = du act'(z), and dx, dweight, dbias as in short_conv_bwd_kernel.
+// ---------------------------------------------------------------------------
+constexpr int kQkTB = 16;      // tokens per lane and block
+constexpr int kQkMaxRw = 128;  // widest rotation row (D <= 128)
+constexpr int kQkSumRows = 256;  // norm-weight partial rows per block of the first sum
+
+namespace {
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int off = L / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// (cos, sin') of rotation dims j < a.rw for the nrow positions from pos0
+__device__ __forceinline__ void fill_rot_table(const QKArgs& a, int pos0, int nrow,
+                                               float (*tc)[kQkMaxRw], float (*ts)[kQkMaxRw]) {
+  const int half = a.rot / 2;
+  for (int i = threadIdx.x; i < nrow * a.rw; i += blockDim.x) {
+    const int r = i / a.rw, j = i % a.rw;
+    float cs = 1.f, sn = 0.f;
+    if (j < a.rot) {
+      const int p = a.interleaved ? j >> 1 : (j < half ? j : j - half);
+      const bool second = a.interleaved ? (j & 1) : j >= half;
+      const float inv_freq = exp2f(-(2.f * p / a.rot) * a.log2_base);
+      sincosf((float)(pos0 + r + a.offset) * inv_freq, &sn, &cs);
+      if (!second) sn = -sn;
+    }
+    tc[r][j] = cs;
+    ts[r][j] = sn;
+  }
+}
+
+// the partner value of each of a lane's four rotation dims: in the lane when
+// interleaved, else in lane + dl (dl = 0 past rot, where sin' = 0)
+__device__ __forceinline__ void rot_partner(const float* v, float* p, bool inter, int src) {
+  if (inter) {
+#pragma unroll
+    for (int e = 0; e < kConvCh; ++e) p[e] = v[e ^ 1];
+  } else {
+#pragma unroll
+    for (int e = 0; e < kConvCh; ++e) p[e] = __shfl(v[e], src);
+  }
+}
+}  // namespace
+
+template <typename T, int W, int L>  // L = D / 4 lanes per head
+__global__ __launch_bounds__(256) void qk_prologue_fwd_kernel(QKArgs a) {
+  __shared__ __align__(16) float tc[kQkTB][kQkMaxRw], ts[kQkTB][kQkMaxRw];
+  const int cg = blockIdx.x * blockDim.x + threadIdx.x, tb = blockIdx.y, b = blockIdx.z;
+  const int t0 = tb * kQkTB;
+  if (a.rot) fill_rot_table(a, t0, kQkTB, tc, ts);
+  __syncthreads();
+  if (kConvCh * cg >= a.C) return;  // whole heads: C / 4 is a multiple of L
+  const int c0 = kConvCh * cg, d0 = c0 % a.D, j0 = d0 % (a.rw > 0 ? a.rw : 1);
+  const int lane = threadIdx.x & 63;
+  const int src = lane + (j0 < a.rot / 2 ? a.rot / 8 : (j0 < a.rot ? -(a.rot / 8) : 0));
+  float wv[kConvCh][W], bv[kConvCh], nwv[kConvCh];
+#pragma unroll
+  for (int e = 0; e < kConvCh; ++e) {
+#pragma unroll
+    for (int w = 0; w < W; ++w) wv[e][w] = a.w[(c0 + e) * W + w];
+    bv[e] = a.bias ? a.bias[c0 + e] : 0.f;
+    nwv[e] = a.nw ? a.nw[d0 + e] : 1.f;
+  }
+  float win[W][kConvCh];
+#pragma unroll
+  for (int j = 0; j < W - 1; ++j) conv_input<T, W>(a, b, c0, t0 - (W - 1) + j, win[j + 1]);
+  const T* __restrict__ xb = (const T*)a.x + (int64_t)b * a.T * a.C + c0;
+  T* __restrict__ yb = (T*)a.y + (int64_t)b * a.T * a.C + c0;
+  v4_t<T> xr[kQkTB];
+#pragma unroll
+  for (int i = 0; i < kQkTB; ++i)
+    xr[i] = t0 + i < a.T ? *reinterpret_cast<const v4_t<T>*>(xb + (int64_t)(t0 + i) * a.C) : v4_t<T>{};
+#pragma unroll
+  for (int i = 0; i < kQkTB; ++i) {
+    const int t = t0 + i;
+#pragma unroll
+    for (int j = 0; j < W - 1; ++j)
+#pragma unroll
+      for (int e = 0; e < kConvCh; ++e) win[j][e] = win[j + 1][e];
+#pragma unroll
+    for (int e = 0; e < kConvCh; ++e) win[W - 1][e] = (float)xr[i][e];
+    if (t >= a.T) break;  // uniform over the block
+    float u[kConvCh], ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < kConvCh; ++e) {
+      float z = bv[e];
+#pragma unroll
+      for (int w = 0; w < W; ++w) z += wv[e][w] * win[w][e];
+      u[e] = a.act ? z / (1.f + __expf(-z)) : z;
+      ss += u[e] * u[e];
+    }
+    if (a.norm) {
+      const float r = rsqrtf(group_sum<L>(ss) * a.inv_n + a.eps);
+#pragma unroll
+      for (int e = 0; e < kConvCh; ++e) u[e] *= r * nwv[e];
+    }
+    if (a.rot) {
+      const f32x4 c = *reinterpret_cast<const f32x4*>(&tc[i][j0]);
+      const f32x4 s = *reinterpret_cast<const f32x4*>(&ts[i][j0]);
+      float pv[kConvCh];
+      rot_partner(u, pv, a.interleaved, src);
+#pragma unroll
+      for (int e = 0; e < kConvCh; ++e) u[e] = u[e] * c[e] + pv[e] * s[e];
+    }
+    store4f<T>(yb + (int64_t)t * a.C, u);
+  }
+  if (a.cache_out && t0 <= a.T - 1 && a.T - 1 < t0 + kQkTB) {
+    T* co = (T*)a.cache_out + ((int64_t)b * a.C + c0) * W;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      float v[kConvCh];
+      conv_input<T, W>(a, b, c0, a.T - W + w, v);
+#pragma unroll
+      for (int e = 0; e < kConvCh; ++e) co[e * W + w] = (T)v[e];
+    }
+  }
+}
+
+template <typename T, int W, int L>
+__global__ __launch_bounds__(256) void qk_prologue_bwd_kernel(QKArgs a) {
+  constexpr int NU = kQkTB + W - 1;  // positions u whose dz reaches dx[t0 .. t0 + kQkTB - 1]
+  __shared__ __align__(16) float tc[kQkTB + 3][kQkMaxRw], ts[kQkTB + 3][kQkMaxRw];
+  const int cg = blockIdx.x * blockDim.x + threadIdx.x, tb = blockIdx.y, b = blockIdx.z;
+  const int t0 = tb * kQkTB, t1 = min(t0 + kQkTB, a.T);
+  if (a.rot) fill_rot_table(a, t0, NU, tc, ts);
+  __syncthreads();
+  if (kConvCh * cg >= a.C) return;
+  const int c0 = kConvCh * cg, d0 = c0 % a.D, j0 = d0 % (a.rw > 0 ? a.rw : 1);
+  const int lane = threadIdx.x & 63;
+  const int src = lane + (j0 < a.rot / 2 ? a.rot / 8 : (j0 < a.rot ? -(a.rot / 8) : 0));
+  float wv[kConvCh][W], bv[kConvCh], nwv[kConvCh];
+#pragma unroll
+  for (int e = 0; e < kConvCh; ++e) {
+#pragma unroll
+    for (int w = 0; w < W; ++w) wv[e][w] = a.w[(c0 + e) * W + w];
+    bv[e] = a.bias ? a.bias[c0 + e] : 0.f;
+    nwv[e] = a.nw ? a.nw[d0 + e] : 1.f;
+  }
+  float win[W][kConvCh], dz[W][kConvCh];
+  float dwp[kConvCh][W], dbp[kConvCh], dnp[kConvCh];
+#pragma unroll
+  for (int e = 0; e < kConvCh; ++e) {
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      dwp[e][w] = 0.f;
+      dz[w][e] = 0.f;
+    }
+    dbp[e] = 0.f;
+    dnp[e] = 0.f;
+  }
+#pragma unroll
+  for (int j = 0; j < W - 1; ++j) conv_input<T, W>(a, b, c0, t0 - (W - 1) + j, win[j + 1]);
+  const int64_t rowb = (int64_t)b * a.T;
+  const T* __restrict__ xb = (const T*)a.x + rowb * a.C + c0;
+  const T* __restrict__ gb = (const T*)a.dy + rowb * a.C + c0;
+  T* __restrict__ dxb = (T*)a.dx + rowb * a.C + c0;
+  v4_t<T> xr[NU], gr[NU];
+#pragma unroll
+  for (int i = 0; i < NU; ++i) {
+    const bool in = t0 + i < a.T;
+    xr[i] = in ? *reinterpret_cast<const v4_t<T>*>(xb + (int64_t)(t0 + i) * a.C) : v4_t<T>{};
+    gr[i] = in ? *reinterpret_cast<const v4_t<T>*>(gb + (int64_t)(t0 + i) * a.C) : v4_t<T>{};
+  }
+#pragma unroll
+  for (int i = 0; i < NU; ++i) {
+    const int u = t0 + i;
+    if (u >= t1 + W - 1) break;  // uniform over the block
+#pragma unroll
+    for (int j = 0; j < W - 1; ++j)
+#pragma unroll
+      for (int e = 0; e < kConvCh; ++e) {
+        win[j][e] = win[j + 1][e];
+        dz[j][e] = dz[j + 1][e];
+      }
+    if (u < a.T) {
+      float z[kConvCh], uv[kConvCh], g[kConvCh], ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < kConvCh; ++e) {
+        win[W - 1][e] = (float)xr[i][e];
+        g[e] = (float)gr[i][e];
+      }
+#pragma unroll
+      for (int e = 0; e < kConvCh; ++e) {
+        z[e] = bv[e];
+#pragma unroll
+        for (int w = 0; w < W; ++w) z[e] += wv[e][w] * win[w][e];
+        uv[e] = a.act ? z[e] / (1.f + __expf(-z[e])) : z[e];
+        ss += uv[e] * uv[e];
+      }
+      if (a.rot) {  // g = R^T dy
+        const f32x4 c = *reinterpret_cast<const f32x4*>(&tc[i][j0]);
+        const f32x4 s = *reinterpret_cast<const f32x4*>(&ts[i][j0]);
+        float pv[kConvCh];
+        rot_partner(g, pv, a.interleaved, src);
+#pragma unroll
+        for (int e = 0; e < kConvCh; ++e) g[e] = g[e] * c[e] - pv[e] * s[e];
+      }
+      if (a.norm) {
+        const float r = rsqrtf(group_sum<L>(ss) * a.inv_n + a.eps);
+        float dot = 0.f;
+#pragma unroll
+        for (int e = 0; e < kConvCh; ++e) {
+          const float uh = uv[e] * r;
+          if (u < t1) dnp[e] += g[e] * uh;
+          g[e] *= nwv[e];
+          dot += g[e] * uh;
+          uv[e] = uh;
+        }
+        dot = group_sum<L>(dot) * a.inv_n;
+#pragma unroll
+        for (int e = 0; e < kConvCh; ++e) g[e] = r * (g[e] - uv[e] * dot);
+      }
+#pragma unroll
+      for (int e = 0; e < kConvCh; ++e) {
+        float d = g[e];
+        if (a.act) {
+          const float sg = 1.f / (1.f + __expf(-z[e]));
+          d *= sg * (1.f + z[e] * (1.f - sg));
+        }
+        dz[W - 1][e] = d;
+      }
+      if (u < t1) {
+#pragma unroll
+        for (int e = 0; e < kConvCh; ++e) {
+#pragma unroll
+          for (int w = 0; w < W; ++w) dwp[e][w] += dz[W - 1][e] * win[w][e];
+          dbp[e] += dz[W - 1][e];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < kConvCh; ++e) dz[W - 1][e] = 0.f;
+    }
+    const int s = u - (W - 1);
+    if (s >= t0) {
+      float dxv[kConvCh];
+#pragma unroll
+      for (int e = 0; e < kConvCh; ++e) {
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) acc += wv[e][w] * dz[W - 1 - w][e];
+        dxv[e] = acc;
+      }
+      store4f<T>(dxb + (int64_t)s * a.C, dxv);
+    }
+  }
+  const int64_t prow = (int64_t)b * gridDim.y + tb;
+  float* pp = a.part + (prow * a.C + c0) * (W + 1);
+#pragma unroll
+  for (int e = 0; e < kConvCh; ++e) {
+#pragma unroll
+    for (int w = 0; w < W; ++w) pp[e * (W + 1) + w] = dwp[e][w];
+    pp[e * (W + 1) + W] = dbp[e];
+  }
+  if (a.nw) *reinterpret_cast<f32x4*>(a.npart + prow * a.C + c0) = f32x4{dnp[0], dnp[1], dnp[2], dnp[3]};
+}
+
+namespace {
+int qk_threads(int C) {  // lanes of C / 4 channel groups, whole waves, at most 256
+  const int lanes = C / kConvCh;
+  return lanes >= 256 ? 256 : (lanes + 63) / 64 * 64;
+}
+}  // namespace
+
+// backward workspace: the convolution partials [B ntb][C][W + 1], their sums
+// [C][W + 1], the norm-weight partials [B ntb][C], then their chunk sums
+template <typename T>
+hipError_t launch_qk_prologue(const QKArgs& args, int W, bool bwd, hipStream_t stream) {
+  const int ntb = (args.T + kQkTB - 1) / kQkTB, nthr = qk_threads(args.C);
+  const int n = args.C * (W + 1), np = args.B * ntb;
+  QKArgs a = args;
+  if (bwd) a.npart = a.part + (size_t)(np + 1) * n;
+  const dim3 grid((a.C / kConvCh + nthr - 1) / nthr, ntb, a.B), block(nthr);
+#define LINATT_QK(WW, LL)                                                            \
+  if (W == WW && a.D / 4 == LL) {                                                   \
+    if (bwd) qk_prologue_bwd_kernel<T, WW, LL><<<grid, block, 0, stream>>>(a);      \
+    else qk_prologue_fwd_kernel<T, WW, LL><<<grid, block, 0, stream>>>(a);          \
+    launched = true;                                                                \
+  }
+  bool launched = false;
+  LINATT_QK(2, 8) LINATT_QK(2, 16) LINATT_QK(2, 32)
+  LINATT_QK(3, 8) LINATT_QK(3, 16) LINATT_QK(3, 32)
+  LINATT_QK(4, 8) LINATT_QK(4, 16) LINATT_QK(4, 32)
+#undef LINATT_QK
+  if (!launched) return hipErrorInvalidValue;
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !bwd) return e;
+  float* sum = a.part + (size_t)np * n;
+  colsum(a.part, sum, np, n, stream);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  short_conv_split_kernel<<<dim3((n + 255) / 256), dim3(256), 0, stream>>>(sum, a.dw, a.db, a.C, W);
+  if ((e = hipGetLastError()) != hipSuccess || !a.nw || !a.dnw) return e;
+  // norm weight: the partials as (np H) rows of D, summed in chunks of
+  // kQkSumRows rows by many blocks, then the chunk sums
+  const int rows = np * (a.C / a.D), nch = (rows + kQkSumRows - 1) / kQkSumRows;
+  float* chunk = a.npart + (size_t)np * a.C;
+  colsum_kernel<<<dim3((a.D + 31) / 32, nch), dim3(1024), 0, stream>>>(a.npart, chunk, rows, a.D,
+                                                                       kQkSumRows);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  colsum(chunk, a.dnw, nch, a.D, stream);
+  return hipGetLastError();
+}
+
+size_t qk_prologue_bwd_workspace(int B, int T, int C, int D, int W) {
+  const size_t np = (size_t)B * ((T + kQkTB - 1) / kQkTB);
+  const size_t nch = (np * (C / D) + kQkSumRows - 1) / kQkSumRows;
+  return ((np + 1) * C * (W + 1) + np * C + nch * D) * sizeof(float);
+}
+
+template hipError_t launch_qk_prologue<__bf16>(const QKArgs&, int, bool, hipStream_t);
+template hipError_t launch_qk_prologue<_Float16>(const QKArgs&, int, bool, hipStream_t);
+template hipError_t launch_qk_prologue<float>(const QKArgs&, int, bool, hipStream_t);
 
 template hipError_t launch_rope<__bf16>(const void*, void*, int, int, int, int, int, float, int, int,
                                         int, hipStream_t);

@@ -21,9 +21,13 @@ and shapes (so checkpoints load) and call contract, running on
   ``forward(q, k, seqlen_offset=0)`` returns the rotated ``(q, k)``
   (``linatt_rope``; the backward is the inverse rotation).
 
-Both have autograd backwards.  The q/k/v projections and ``o_proj`` stay
-library GEMMs.  Unsupported arguments (fla's ``residual``, ``mask``,
-``cu_seqlens``, a norm bias) raise.
+All have autograd backwards.  ``qk_prologue`` (and ``fused_qk_prologue``,
+which takes the three modules) runs the q or k chain of ``:305-372`` --
+short convolution, per-head RMSNorm or L2 norm, rotary embedding -- as one
+kernel pair (``linatt_qk_prologue_fwd`` / ``_bwd``), keeping the
+intermediates in fp32.  The q/k/v projections and ``o_proj`` stay library
+GEMMs.  Unsupported arguments (fla's ``residual``, ``mask``, ``cu_seqlens``,
+a norm bias) raise.
 """
 
 from __future__ import annotations
@@ -37,7 +41,8 @@ from . import _lib
 
 _lib.load()
 
-__all__ = ["short_conv", "rms_norm", "rotary", "ShortConvolution", "RMSNorm", "RotaryEmbedding"]
+__all__ = ["short_conv", "rms_norm", "rotary", "qk_prologue", "fused_qk_prologue",
+           "ShortConvolution", "RMSNorm", "RotaryEmbedding"]
 
 _ACT = {None: 0, "identity": 0, "silu": 1, "swish": 1}
 
@@ -258,3 +263,134 @@ class RotaryEmbedding(nn.Module):
                                       "offsets and other options are not supported")
         return (rotary(q, self.dim, self.base, seqlen_offset, self.interleaved),
                 rotary(k, self.dim, self.base, seqlen_offset, self.interleaved))
+
+
+_NORM = {None: 0, "none": 0, "rmsnorm": 1, "l2": 2}
+
+
+class _QKPrologueFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, conv_weight, conv_bias, norm_weight, cache, cfg, want_state):
+        _lib.require_device(x, conv_weight)
+        H, D, W, act, norm, eps, rw, rot, base, offset, inter = cfg
+        B, T, C = x.shape
+        L = _lib.load()
+        x = x.contiguous()
+        w2 = conv_weight.detach().reshape(C, W).float().contiguous()
+        b = conv_bias.detach().float().contiguous() if conv_bias is not None else None
+        nw = norm_weight.detach().float().contiguous() if norm_weight is not None else None
+        for t in (b, nw):
+            if t is not None:
+                _lib.require_device(t)
+        if cache is not None:
+            _lib.require_device(cache)
+            if cache.shape != (B, C, W):
+                raise ValueError(f"cache must be (B, C, W) = {(B, C, W)}, got {tuple(cache.shape)}")
+            cache = cache.to(x.dtype).contiguous()
+        y = torch.empty(B, T, H, D, device=x.device, dtype=x.dtype)
+        state = torch.empty(B, C, W, device=x.device, dtype=x.dtype) if want_state else None
+        _lib.check("linatt_qk_prologue_fwd", L.linatt_qk_prologue_fwd(
+            _lib.ptr(x), _lib.ptr(w2), _lib.ptr(b), _lib.ptr(cache), _lib.ptr(nw), _lib.ptr(y),
+            _lib.ptr(state), B, T, H, D, W, act, norm, eps, rw, rot, base, offset, inter,
+            _lib.dtype_code(x.dtype), _lib.stream_of(x)))
+        ctx.save_for_backward(x, w2, b, nw, cache)
+        ctx.cfg = cfg
+        ctx.dtypes = (conv_weight.dtype, conv_bias.dtype if conv_bias is not None else None,
+                      norm_weight.dtype if norm_weight is not None else None)
+        ctx.wshape = conv_weight.shape
+        if state is not None:
+            ctx.mark_non_differentiable(state)
+        return y, state
+
+    @staticmethod
+    def backward(ctx, dy, _dstate):
+        x, w2, b, nw, cache = ctx.saved_tensors
+        H, D, W, act, norm, eps, rw, rot, base, offset, inter = ctx.cfg
+        B, T, C = x.shape
+        L = _lib.load()
+        dy = dy.to(x.dtype).contiguous()
+        dx = torch.empty_like(x)
+        dw = torch.empty(C, W, device=x.device, dtype=torch.float32)
+        db = torch.empty(C, device=x.device, dtype=torch.float32) if b is not None else None
+        dnw = torch.empty(D, device=x.device, dtype=torch.float32) if nw is not None else None
+        ws = torch.empty(L.linatt_qk_prologue_bwd_workspace_bytes(B, T, H, D, W),
+                         device=x.device, dtype=torch.uint8)
+        _lib.check("linatt_qk_prologue_bwd", L.linatt_qk_prologue_bwd(
+            _lib.ptr(x), _lib.ptr(w2), _lib.ptr(b), _lib.ptr(cache), _lib.ptr(nw), _lib.ptr(dy),
+            _lib.ptr(dx), _lib.ptr(dw), _lib.ptr(db), _lib.ptr(dnw), _lib.ptr(ws), B, T, H, D, W,
+            act, norm, eps, rw, rot, base, offset, inter, _lib.dtype_code(x.dtype),
+            _lib.stream_of(x)))
+        wdt, bdt, ndt = ctx.dtypes
+        return (dx, dw.reshape(ctx.wshape).to(wdt), db.to(bdt) if db is not None else None,
+                dnw.to(ndt) if dnw is not None else None, None, None, None)
+
+
+def qk_prologue(x, conv_weight, conv_bias=None, *, head_dim, activation="silu", norm="rmsnorm",
+                norm_weight=None, eps=None, rot_dim=None, rope_width=None, base=10000.0,
+                offset=0, interleaved=True, cache=None, output_final_state=False):
+    """The q or k prologue of ``kata/layer.py:305-372`` in one kernel:
+    ``x (B, T, H * head_dim)`` (the projection output) through the causal
+    short convolution + activation (``conv_weight (C, 1, W)`` or ``(C, W)``,
+    ``cache`` as ``short_conv``), the per-head norm (``norm="rmsnorm"`` with
+    ``norm_weight (head_dim,)`` or None, eps 1e-5 by default; ``"l2"``, fla's
+    ``l2norm``, eps 1e-6 by default; ``None``) and the rotary embedding of
+    rows of ``rope_width`` dims (default ``head_dim``; the group width E for
+    the mixer's ``rope_group``) over their first ``rot_dim`` dims (default
+    ``rope_width``; 0: no rotation) at positions ``offset ..``.  Returns
+    ``(y (B, T, H, head_dim), final_cache)``; the intermediates stay in fp32,
+    so y differs from the three-module chain by that chain's two roundings to
+    x's dtype."""
+    if x.dim() != 3:
+        raise ValueError(f"x must be (B, T, H * head_dim), got {tuple(x.shape)}")
+    C = x.shape[-1]
+    D = int(head_dim)
+    if D <= 0 or C % D:
+        raise ValueError(f"the channel count {C} is not a multiple of head_dim {D}")
+    if conv_weight.shape[0] != C or conv_weight.numel() != C * conv_weight.shape[-1]:
+        raise ValueError(f"conv_weight must be (C, 1, W) with C = {C}, got {tuple(conv_weight.shape)}")
+    if conv_bias is not None and conv_bias.shape != (C,):
+        raise ValueError(f"conv_bias must be ({C},), got {tuple(conv_bias.shape)}")
+    if norm not in _NORM:
+        raise ValueError(f"norm must be 'rmsnorm', 'l2' or None, got {norm!r}")
+    nk = _NORM[norm]
+    if nk != 1 and norm_weight is not None:
+        raise ValueError("norm_weight is only used with norm='rmsnorm'")
+    if norm_weight is not None and norm_weight.shape != (D,):
+        raise ValueError(f"norm_weight must be ({D},), got {tuple(norm_weight.shape)}")
+    if eps is None:
+        eps = 1e-6 if nk == 2 else 1e-5
+    rw = D if rope_width is None else int(rope_width)
+    rot = rw if rot_dim is None else int(rot_dim)
+    if isinstance(offset, torch.Tensor):
+        raise NotImplementedError("qk_prologue: per-sequence offsets are not supported")
+    cfg = (C // D, D, int(conv_weight.shape[-1]), _act(activation), nk, float(eps), rw, rot,
+           float(base), int(offset), 1 if interleaved else 0)
+    return _QKPrologueFn.apply(x, conv_weight, conv_bias, norm_weight, cache, cfg,
+                               bool(output_final_state))
+
+
+def fused_qk_prologue(x, conv, norm, rotary, head_dim, seqlen_offset=0, cache=None,
+                      output_final_state=False):
+    """``qk_prologue`` configured from the mixer's modules: ``conv`` a
+    ``ShortConvolution``; ``norm`` an ``RMSNorm`` (its weight and eps), the
+    string ``"l2"`` or None; ``rotary`` a ``RotaryEmbedding`` (its dim is the
+    rotation row width: the head dim, or E under ``rope_group``) or None.
+    Equals ``rotary(norm(conv(x)[0].view(B, T, H, D)))`` up to the chain's
+    intermediate roundings."""
+    if isinstance(norm, RMSNorm):
+        if norm.hidden_size != head_dim:
+            raise ValueError(f"RMSNorm width {norm.hidden_size} != head_dim {head_dim}")
+        nk, nw, eps = "rmsnorm", norm.weight, norm.eps
+    elif norm == "l2" or norm is None:
+        nk, nw, eps = norm, None, None
+    else:
+        raise TypeError("norm must be a linatt_amd RMSNorm, 'l2' or None")
+    if rotary is None:
+        rw, rot, base, inter = None, 0, 10000.0, True
+    else:
+        rw = rot = rotary.dim
+        base, inter = rotary.base, rotary.interleaved
+    return qk_prologue(x, conv.weight, conv.bias, head_dim=head_dim, activation=conv.activation,
+                       norm=nk, norm_weight=nw, eps=eps, rot_dim=rot, rope_width=rw, base=base,
+                       offset=seqlen_offset, interleaved=inter, cache=cache,
+                       output_final_state=output_final_state)

@@ -150,3 +150,71 @@ def test_noalloc_rejects_oversized_before_device_work(lib):
     st = lib.linatt_kata_bwd_noalloc(None, None, None, None, None, None, None, None, None,
                                      0, 8, 2, 2, 64, 64, 4, 0.25, 0, 1, None)
     assert st == EINVAL
+
+
+def _qk(lib, bwd=False, **kw):
+    a = dict(x=FAKE, w=FAKE, b=None, cache=None, nw=None, y=FAKE, B=1, T=8, H=2, D=64, W=4,
+             act=1, norm=1, eps=1e-5, rw=64, rot=64, base=10000.0, offset=0, inter=1, dtype=1)
+    a.update(kw)
+    if bwd:
+        return lib.linatt_qk_prologue_bwd(
+            a["x"], a["w"], a["b"], a["cache"], a["nw"], FAKE, FAKE, FAKE, None,
+            kw.get("dnw"), kw.get("ws", FAKE), a["B"], a["T"], a["H"], a["D"], a["W"], a["act"],
+            a["norm"], a["eps"], a["rw"], a["rot"], a["base"], a["offset"], a["inter"],
+            a["dtype"], None)
+    return lib.linatt_qk_prologue_fwd(
+        a["x"], a["w"], a["b"], a["cache"], a["nw"], a["y"], None, a["B"], a["T"], a["H"],
+        a["D"], a["W"], a["act"], a["norm"], a["eps"], a["rw"], a["rot"], a["base"],
+        a["offset"], a["inter"], a["dtype"], None)
+
+
+def test_qk_prologue_argument_errors(lib):
+    EINVAL, EUNSUP = -1, -2
+    assert _qk(lib, T=0) == EINVAL
+    assert _qk(lib, D=48, rw=48, rot=48) == EUNSUP
+    assert b"head dim" in lib.linatt_last_error()
+    assert _qk(lib, W=5) == EUNSUP
+    assert _qk(lib, norm=3) == EINVAL
+    assert _qk(lib, norm=2, nw=FAKE) == EINVAL
+    assert b"L2 norm takes no weight" in lib.linatt_last_error()
+    assert _qk(lib, rw=24, rot=24) == EINVAL          # 24 does not divide 64
+    assert _qk(lib, rw=16, rot=18) == EINVAL          # rot_dim > rope_width
+    assert _qk(lib, rw=16, rot=12, inter=0) == EUNSUP  # half-split needs rot_dim % 8 == 0
+    assert _qk(lib, offset=-1) == EINVAL
+    assert _qk(lib, base=1.0) == EINVAL
+    assert _qk(lib, x=ctypes.c_void_p((1 << 20) + 2)) == EINVAL
+    assert _qk(lib, dtype=9) == EINVAL
+    assert _qk(lib, bwd=True, ws=None) == EINVAL
+    assert _qk(lib, bwd=True, dnw=FAKE) == EINVAL     # dnorm_weight without norm_weight
+    # rot_dim 0 switches the rotation off and ignores rope_width
+    assert _qk(lib, rot=0, rw=-3, T=0) == EINVAL
+    assert b"non-positive" in lib.linatt_last_error()
+
+
+def test_qk_prologue_workspace_bytes(lib):
+    # convolution partials [B ntb][C][W + 1] + their sums [C][W + 1] + norm partials
+    # [B ntb][C] + their sums over chunks of 256 of the (B ntb H) rows of D
+    B, T, H, D, W = 2, 33, 3, 64, 4
+    np_, C = B * 3, H * D
+    assert lib.linatt_qk_prologue_bwd_workspace_bytes(B, T, H, D, W) == \
+        ((np_ + 1) * C * (W + 1) + np_ * C + 1 * D) * 4
+    B, T = 8, 2048  # 1024 partial rows x 12 heads -> 48 chunks
+    np_ = B * 128
+    assert lib.linatt_qk_prologue_bwd_workspace_bytes(B, T, 12, 64, W) == \
+        ((np_ + 1) * 768 * (W + 1) + np_ * 768 + 48 * 64) * 4
+    assert lib.linatt_qk_prologue_bwd_workspace_bytes(B, T, H, D, 5) == 0
+
+
+def test_qk_prologue_python_checks():
+    import torch
+    from linatt_amd import mixer
+    x = torch.randn(1, 4, 128)
+    w = torch.randn(128, 1, 4)
+    with pytest.raises(ValueError, match="multiple of head_dim"):
+        mixer.qk_prologue(x, w, head_dim=48)
+    with pytest.raises(ValueError, match="norm_weight is only used"):
+        mixer.qk_prologue(x, w, head_dim=64, norm="l2", norm_weight=torch.ones(64))
+    with pytest.raises(ValueError, match="norm must be"):
+        mixer.qk_prologue(x, w, head_dim=64, norm="layer")
+    with pytest.raises(RuntimeError, match="only on a ROCm GPU"):
+        mixer.qk_prologue(x, w, head_dim=64)

@@ -11,6 +11,10 @@ The harness keeps the reference layer's order of operations:
   (``:377-420``);
 - the output RMSNorm and ``o_proj`` (``:539-541``).
 
+The ``flash_M4_fused`` case runs the q and k chains (convolution, RMSNorm,
+rotation) through ``fused_qk_prologue`` instead of the three modules, against
+the same float64 layer.
+
 It runs under ``torch.autocast(bf16)`` with float32 parameters and input, as
 ``train_llm.py:424`` runs the model.  The output and every gradient (input,
 projections, convolution and norm weights) meet the bf16 bar of 2e-2
@@ -42,10 +46,10 @@ def mar(x, ref):
 class MiniMixer(nn.Module):
     """The flash or delta branch of the reference mixer, through linatt_amd."""
 
-    def __init__(self, hidden, H, D, M, branch, conv=4):
+    def __init__(self, hidden, H, D, M, branch, conv=4, fused=False):
         super().__init__()
         from linatt_amd.mixer import RMSNorm, RotaryEmbedding, ShortConvolution
-        self.H, self.D, self.M, self.branch = H, D, M, branch
+        self.H, self.D, self.M, self.branch, self.fused = H, D, M, branch, fused
         self.q_proj = nn.Linear(hidden, H * D, bias=False)
         self.k_proj = nn.Linear(hidden, H * D, bias=False)
         self.v_proj = nn.Linear(hidden, H * D, bias=False)
@@ -65,13 +69,19 @@ class MiniMixer(nn.Module):
     def forward(self, x):
         from linatt_amd.flash_delta import flash_delta
         from linatt_amd.parallel_kata_attn import parallel_kata_attn, parallel_kata_attn_fwd
+        from linatt_amd.mixer import fused_qk_prologue
         B, T, _ = x.shape
-        q, _ = self.q_conv1d(self.q_proj(x))
-        k, _ = self.k_conv1d(self.k_proj(x))
         v, _ = self.v_conv1d(self.v_proj(x))
-        q, k, v = (t.reshape(B, T, self.H, self.D) for t in (q, k, v))
-        q, k = self.q_norm(q), self.k_norm(k)
-        q, k = self.rotary(q, k)
+        v = v.reshape(B, T, self.H, self.D)
+        if self.fused:
+            q, _ = fused_qk_prologue(self.q_proj(x), self.q_conv1d, self.q_norm, self.rotary, self.D)
+            k, _ = fused_qk_prologue(self.k_proj(x), self.k_conv1d, self.k_norm, self.rotary, self.D)
+        else:
+            q, _ = self.q_conv1d(self.q_proj(x))
+            k, _ = self.k_conv1d(self.k_proj(x))
+            q, k = (t.reshape(B, T, self.H, self.D) for t in (q, k))
+            q, k = self.q_norm(q), self.k_norm(k)
+            q, k = self.rotary(q, k)
         if self.branch == "flash":
             grad_on = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v))
             if grad_on:
@@ -115,12 +125,13 @@ class MiniMixer(nn.Module):
         return o @ P["o_proj.weight"].T, x, P
 
 
-@pytest.mark.parametrize("branch,T,M", [("flash", 200, 4), ("delta", 100, 1)],
-                         ids=["flash_M4", "delta_M1_padded"])
-def test_mixer_layer_under_autocast(branch, T, M):
+@pytest.mark.parametrize("branch,T,M,fused", [("flash", 200, 4, False), ("delta", 100, 1, False),
+                                              ("flash", 200, 4, True)],
+                         ids=["flash_M4", "delta_M1_padded", "flash_M4_fused"])
+def test_mixer_layer_under_autocast(branch, T, M, fused):
     torch.manual_seed(0)
     B, hidden, H, D = 2, 256, 4, 64
-    layer = MiniMixer(hidden, H, D, M, branch).to(DEV)
+    layer = MiniMixer(hidden, H, D, M, branch, fused=fused).to(DEV)
     x = torch.randn(B, T, hidden, generator=torch.Generator().manual_seed(1)).to(DEV)
     dy = torch.randn(B, T, hidden, generator=torch.Generator().manual_seed(2)).to(DEV)
     xg = x.clone().requires_grad_(True)
