@@ -255,10 +255,12 @@ __global__ __launch_bounds__(64) void short_conv_bwd_kernel(ConvArgs a) {
 // (rows y rows_per .. min(np, (y + 1) rows_per) - 1), in a fixed order: 1024
 // threads per block, 32 columns by 32 row phases (phase k sums rows k, k + 32,
 // ... of the range, eight loads in flight), then one thread per column adds
-// the 32 phase sums.
+// the 32 phase sums.  With split_w > 0 the columns are [c][0 .. split_w - 1
+// weight, split_w bias] of a convolution and go to dw[c][w] and db[c] instead.
 __global__ __launch_bounds__(1024) void colsum_kernel(const float* __restrict__ part,
                                                       float* __restrict__ out, int np, int n,
-                                                      int rows_per) {
+                                                      int rows_per, int split_w = 0,
+                                                      float* __restrict__ db = nullptr) {
   __shared__ float red[32][33];
   const int c = blockIdx.x * 32 + (threadIdx.x & 31), k = threadIdx.x >> 5;
   const int p0 = blockIdx.y * rows_per, p1 = min(np, p0 + rows_per);
@@ -280,7 +282,13 @@ __global__ __launch_bounds__(1024) void colsum_kernel(const float* __restrict__ 
     float t = 0.f;
 #pragma unroll
     for (int j = 0; j < 32; ++j) t += red[j][threadIdx.x];
-    out[(int64_t)blockIdx.y * n + c] = t;
+    if (split_w == 0) {
+      out[(int64_t)blockIdx.y * n + c] = t;
+    } else {
+      const int cc = c / (split_w + 1), w = c % (split_w + 1);
+      if (w < split_w) out[cc * split_w + w] = t;
+      else if (db) db[cc] = t;
+    }
   }
 }
 
@@ -289,16 +297,11 @@ static void colsum(const float* part, float* out, int np, int n, hipStream_t str
   colsum_kernel<<<dim3((n + 31) / 32), dim3(1024), 0, stream>>>(part, out, np, n, np);
 }
 
-// dweight[c][w] and dbias[c] from the summed partials [c][0 .. W - 1, W]
-__global__ __launch_bounds__(256) void short_conv_split_kernel(const float* __restrict__ sum,
-                                                               float* __restrict__ dw,
-                                                               float* __restrict__ db, int C,
-                                                               int W) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= C * (W + 1)) return;
-  const int c = i / (W + 1), w = i % (W + 1);
-  if (w < W) dw[c * W + w] = sum[i];
-  else if (db) db[c] = sum[i];
+// dweight (C, W) and dbias (C) from the convolution partials [np][C][W + 1]
+static void conv_grad_sums(const float* part, float* dw, float* db, int np, int C, int W,
+                           hipStream_t stream) {
+  const int n = C * (W + 1);
+  colsum_kernel<<<dim3((n + 31) / 32), dim3(1024), 0, stream>>>(part, dw, np, n, np, W, db);
 }
 
 template <typename T>
@@ -319,17 +322,13 @@ hipError_t launch_short_conv(const ConvArgs& a, int W, bool bwd, hipStream_t str
 #undef LINATT_CONV_W
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !bwd) return e;
-  const int n = a.C * (W + 1), np = a.B * ntb;
-  float* sum = a.part + (size_t)np * n;
-  colsum(a.part, sum, np, n, stream);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  short_conv_split_kernel<<<dim3((n + 255) / 256), dim3(256), 0, stream>>>(sum, a.dw, a.db, a.C, W);
+  conv_grad_sums(a.part, a.dw, a.db, a.B * ntb, a.C, W, stream);
   return hipGetLastError();
 }
 
 size_t short_conv_bwd_workspace(int B, int T, int C, int W) {
   const size_t ntb = (size_t)(T + kConvTB - 1) / kConvTB;
-  return ((size_t)B * ntb + 1) * C * (W + 1) * sizeof(float);  // partials + their sums
+  return (size_t)B * ntb * C * (W + 1) * sizeof(float);  // the partials
 }
 
 // ---------------------------------------------------------------------------
@@ -548,7 +547,6 @@ hipError_t launch_rope(const void* x, void* y, int B, int T_, int H, int D, int 
 // ---------------------------------------------------------------------------
 constexpr int kQkTB = 16;      // tokens per lane and block
 constexpr int kQkMaxRw = 128;  // widest rotation row (D <= 128)
-constexpr int kQkSumRows = 256;  // norm-weight partial rows per block of the first sum
 
 namespace {
 template <int L>
@@ -597,7 +595,7 @@ __global__ __launch_bounds__(256) void qk_prologue_fwd_kernel(QKArgs a) {
   const int t0 = tb * kQkTB;
   if (a.rot) fill_rot_table(a, t0, kQkTB, tc, ts);
   __syncthreads();
-  if (kConvCh * cg >= a.C) return;  // whole heads: C / 4 is a multiple of L
+  // every lane is in range: the block is a whole number of heads dividing H
   const int c0 = kConvCh * cg, d0 = c0 % a.D, j0 = d0 % (a.rw > 0 ? a.rw : 1);
   const int lane = threadIdx.x & 63;
   const int src = lane + (j0 < a.rot / 2 ? a.rot / 8 : (j0 < a.rot ? -(a.rot / 8) : 0));
@@ -672,7 +670,7 @@ __global__ __launch_bounds__(256) void qk_prologue_bwd_kernel(QKArgs a) {
   const int t0 = tb * kQkTB, t1 = min(t0 + kQkTB, a.T);
   if (a.rot) fill_rot_table(a, t0, NU, tc, ts);
   __syncthreads();
-  if (kConvCh * cg >= a.C) return;
+  // every lane is in range: the block is a whole number of heads dividing H
   const int c0 = kConvCh * cg, d0 = c0 % a.D, j0 = d0 % (a.rw > 0 ? a.rw : 1);
   const int lane = threadIdx.x & 63;
   const int src = lane + (j0 < a.rot / 2 ? a.rot / 8 : (j0 < a.rot ? -(a.rot / 8) : 0));
@@ -800,25 +798,42 @@ __global__ __launch_bounds__(256) void qk_prologue_bwd_kernel(QKArgs a) {
     for (int w = 0; w < W; ++w) pp[e * (W + 1) + w] = dwp[e][w];
     pp[e * (W + 1) + W] = dbp[e];
   }
-  if (a.nw) *reinterpret_cast<f32x4*>(a.npart + prow * a.C + c0) = f32x4{dnp[0], dnp[1], dnp[2], dnp[3]};
+  if (a.nw) {  // the block's heads summed in LDS (the table's space): one row of D per block
+    __syncthreads();
+    float* red = &tc[0][0];
+    *reinterpret_cast<f32x4*>(red + kConvCh * threadIdx.x) = f32x4{dnp[0], dnp[1], dnp[2], dnp[3]};
+    __syncthreads();
+    const int nh = blockDim.x / L;
+    for (int d = threadIdx.x; d < a.D; d += blockDim.x) {
+      float sum = 0.f;
+      for (int hh = 0; hh < nh; ++hh) sum += red[hh * a.D + d];
+      a.npart[(prow * gridDim.x + blockIdx.x) * a.D + d] = sum;
+    }
+  }
 }
 
 namespace {
-int qk_threads(int C) {  // lanes of C / 4 channel groups, whole waves, at most 256
-  const int lanes = C / kConvCh;
-  return lanes >= 256 ? 256 : (lanes + 63) / 64 * 64;
+// lanes per block: the D / 4 lanes of each of h heads, h the largest divisor
+// of H with at most 256 lanes, so that blocks hold whole heads and no lane is
+// out of range
+int qk_threads(int C, int D) {
+  const int L = D / kConvCh, H = C / D;
+  int h = 1;
+  for (int c = 1; c <= H && c * L <= 256; ++c)
+    if (H % c == 0) h = c;
+  return h * L;
 }
 }  // namespace
 
-// backward workspace: the convolution partials [B ntb][C][W + 1], their sums
-// [C][W + 1], the norm-weight partials [B ntb][C], then their chunk sums
+// backward workspace: the convolution partials [B ntb][C][W + 1], then the
+// norm-weight partials [B ntb][H / h][D]
 template <typename T>
 hipError_t launch_qk_prologue(const QKArgs& args, int W, bool bwd, hipStream_t stream) {
-  const int ntb = (args.T + kQkTB - 1) / kQkTB, nthr = qk_threads(args.C);
+  const int ntb = (args.T + kQkTB - 1) / kQkTB, nthr = qk_threads(args.C, args.D);
   const int n = args.C * (W + 1), np = args.B * ntb;
   QKArgs a = args;
-  if (bwd) a.npart = a.part + (size_t)(np + 1) * n;
-  const dim3 grid((a.C / kConvCh + nthr - 1) / nthr, ntb, a.B), block(nthr);
+  if (bwd) a.npart = a.part + (size_t)np * n;
+  const dim3 grid(a.C / kConvCh / nthr, ntb, a.B), block(nthr);
 #define LINATT_QK(WW, LL)                                                            \
   if (W == WW && a.D / 4 == LL) {                                                   \
     if (bwd) qk_prologue_bwd_kernel<T, WW, LL><<<grid, block, 0, stream>>>(a);      \
@@ -833,26 +848,16 @@ hipError_t launch_qk_prologue(const QKArgs& args, int W, bool bwd, hipStream_t s
   if (!launched) return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !bwd) return e;
-  float* sum = a.part + (size_t)np * n;
-  colsum(a.part, sum, np, n, stream);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  short_conv_split_kernel<<<dim3((n + 255) / 256), dim3(256), 0, stream>>>(sum, a.dw, a.db, a.C, W);
+  conv_grad_sums(a.part, a.dw, a.db, np, a.C, W, stream);
   if ((e = hipGetLastError()) != hipSuccess || !a.nw || !a.dnw) return e;
-  // norm weight: the partials as (np H) rows of D, summed in chunks of
-  // kQkSumRows rows by many blocks, then the chunk sums
-  const int rows = np * (a.C / a.D), nch = (rows + kQkSumRows - 1) / kQkSumRows;
-  float* chunk = a.npart + (size_t)np * a.C;
-  colsum_kernel<<<dim3((a.D + 31) / 32, nch), dim3(1024), 0, stream>>>(a.npart, chunk, rows, a.D,
-                                                                       kQkSumRows);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  colsum(chunk, a.dnw, nch, a.D, stream);
+  colsum(a.npart, a.dnw, np * (int)grid.x, a.D, stream);
   return hipGetLastError();
 }
 
 size_t qk_prologue_bwd_workspace(int B, int T, int C, int D, int W) {
   const size_t np = (size_t)B * ((T + kQkTB - 1) / kQkTB);
-  const size_t nch = (np * (C / D) + kQkSumRows - 1) / kQkSumRows;
-  return ((np + 1) * C * (W + 1) + np * C + nch * D) * sizeof(float);
+  const size_t nblk = (size_t)C / kConvCh / qk_threads(C, D);
+  return (np * C * (W + 1) + np * nblk * D) * sizeof(float);
 }
 
 template hipError_t launch_qk_prologue<__bf16>(const QKArgs&, int, bool, hipStream_t);

@@ -192,16 +192,19 @@ def test_qk_prologue_argument_errors(lib):
 
 
 def test_qk_prologue_workspace_bytes(lib):
-    # convolution partials [B ntb][C][W + 1] + their sums [C][W + 1] + norm partials
-    # [B ntb][C] + their sums over chunks of 256 of the (B ntb H) rows of D
+    # convolution partials [B ntb][C][W + 1] + norm-weight partials [B ntb][H / h][D], h the
+    # heads per block (the largest divisor of H with h D / 4 <= 256 lanes)
     B, T, H, D, W = 2, 33, 3, 64, 4
     np_, C = B * 3, H * D
     assert lib.linatt_qk_prologue_bwd_workspace_bytes(B, T, H, D, W) == \
-        ((np_ + 1) * C * (W + 1) + np_ * C + 1 * D) * 4
-    B, T = 8, 2048  # 1024 partial rows x 12 heads -> 48 chunks
+        (np_ * C * (W + 1) + np_ * 1 * D) * 4
+    B, T = 8, 2048  # 12 heads of 64 in one block of 192 lanes
     np_ = B * 128
     assert lib.linatt_qk_prologue_bwd_workspace_bytes(B, T, 12, 64, W) == \
-        ((np_ + 1) * 768 * (W + 1) + np_ * 768 + 48 * 64) * 4
+        (np_ * 768 * (W + 1) + np_ * 1 * 64) * 4
+    # 20 heads of 128: 32 lanes each, h = 5 (8 would not divide 20) -> 4 blocks per row
+    assert lib.linatt_qk_prologue_bwd_workspace_bytes(1, 16, 20, 128, W) == \
+        (1 * 2560 * (W + 1) + 1 * 4 * 128) * 4
     assert lib.linatt_qk_prologue_bwd_workspace_bytes(B, T, H, D, 5) == 0
 
 
