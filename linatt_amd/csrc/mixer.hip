@@ -31,6 +31,27 @@ namespace linatt {
 
 namespace {
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_plus(float v) {
+  return v + __builtin_bit_cast(
+                 float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// sum over each aligned group of L lanes (a power of two up to 64), the same
+// bits on every lane: DPP steps inside a 16-lane row (quad xor 1, quad xor 2,
+// half-row mirror, row mirror; each adds the same two partial sums on both
+// sides), then xor-16 and xor-32 shuffles for wider groups
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(L >= 1 && L <= 64 && (L & (L - 1)) == 0, "a power of two up to 64 lanes");
+  if constexpr (L >= 2) v = dpp_plus<0xB1>(v);
+  if constexpr (L >= 4) v = dpp_plus<0x4E>(v);
+  if constexpr (L >= 8) v = dpp_plus<0x141>(v);
+  if constexpr (L >= 16) v = dpp_plus<0x140>(v);
+  if constexpr (L >= 32) v += __shfl_xor(v, 16);
+  if constexpr (L >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+
 constexpr int kConvTB = 16;  // tokens per lane
 constexpr int kConvCh = 4;   // channels per lane of the short convolution
 
@@ -361,8 +382,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ 
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss += v[r][e] * v[r][e];
-#pragma unroll
-    for (int off = L / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    ss = group_sum<L>(ss);
     const float rr = rsqrtf(ss / d + eps);
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[r][e] *= rr * wv[e];
@@ -412,9 +432,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const T* __restrict__ 
         g[k][e] *= wv[e];
         dot += g[k][e] * xv[k][e];
       }
-#pragma unroll
-      for (int off = L / 2; off > 0; off >>= 1) dot += __shfl_xor(dot, off);
-      dot /= d;
+      dot = group_sum<L>(dot) / d;
 #pragma unroll
       for (int e = 0; e < 8; ++e) g[k][e] = r[k] * (g[k][e] - xv[k][e] * dot);
       store8f<T>(dx + (int64_t)row * d + 8 * li, g[k]);
@@ -538,7 +556,7 @@ hipError_t launch_rope(const void* x, void* y, int B, int T_, int H, int D, int 
 // angle (t + offset) base^(-2p / rot), and dims past rot have (1, 0).
 // A lane owns kConvCh = 4 channels and a run of kQkTB tokens, as in the
 // convolution; a head's D / 4 lanes are adjacent in one wave, so the norm's
-// sums are shuffle reductions over them.  The angles come from an LDS table
+// sums are DPP reductions over them.  The angles come from an LDS table
 // per block (tokens x rotation dims) filled with the formula of rope_kernel,
 // so each table entry costs one sincos per block rather than one per lane.
 // The backward recomputes z, u, r, rotates dy back (sin' negated) to g, then
@@ -549,29 +567,27 @@ constexpr int kQkTB = 16;      // tokens per lane and block
 constexpr int kQkMaxRw = 128;  // widest rotation row (D <= 128)
 
 namespace {
-template <int L>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int off = L / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  return v;
-}
-
-// (cos, sin') of rotation dims j < a.rw for the nrow positions from pos0
+// (cos, sin') of rotation dims j < a.rw for the nrow positions from pos0:
+// one sincos per rotated pair, written to both of its dims; (1, 0) past rot
 __device__ __forceinline__ void fill_rot_table(const QKArgs& a, int pos0, int nrow,
                                                float (*tc)[kQkMaxRw], float (*ts)[kQkMaxRw]) {
-  const int half = a.rot / 2;
-  for (int i = threadIdx.x; i < nrow * a.rw; i += blockDim.x) {
-    const int r = i / a.rw, j = i % a.rw;
-    float cs = 1.f, sn = 0.f;
-    if (j < a.rot) {
-      const int p = a.interleaved ? j >> 1 : (j < half ? j : j - half);
-      const bool second = a.interleaved ? (j & 1) : j >= half;
-      const float inv_freq = exp2f(-(2.f * p / a.rot) * a.log2_base);
-      sincosf((float)(pos0 + r + a.offset) * inv_freq, &sn, &cs);
-      if (!second) sn = -sn;
+  const int half = a.rot / 2, npair = half + (a.rw - a.rot);  // pairs, then pass-through dims
+  for (int i = threadIdx.x; i < nrow * npair; i += blockDim.x) {
+    const int r = i / npair, p = i % npair;
+    if (p >= half) {
+      const int j = a.rot + (p - half);
+      tc[r][j] = 1.f;
+      ts[r][j] = 0.f;
+      continue;
     }
-    tc[r][j] = cs;
-    ts[r][j] = sn;
+    float cs, sn;
+    const float inv_freq = exp2f(-(2.f * p / a.rot) * a.log2_base);
+    sincosf((float)(pos0 + r + a.offset) * inv_freq, &sn, &cs);
+    const int j0 = a.interleaved ? 2 * p : p, j1 = a.interleaved ? 2 * p + 1 : p + half;
+    tc[r][j0] = cs;
+    ts[r][j0] = -sn;
+    tc[r][j1] = cs;
+    ts[r][j1] = sn;
   }
 }
 
