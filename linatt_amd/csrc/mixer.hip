@@ -494,7 +494,10 @@ hipError_t launch_rmsnorm(const void* x, const float* w, const float* rstd_in, c
 // each (B, T, H, D) row -- (2p, 2p + 1) interleaved, (p, p + rot_dim / 2)
 // otherwise -- is rotated by the angle (t + offset) base^(-2p / rot_dim),
 // in fp32; inverse = 1 rotates by minus that angle (the backward).  Dims past
-// rot_dim pass through.  One thread per pair.
+// rot_dim pass through.  rope_rows_kernel (after the fused q/k prologue, whose
+// table and lane layout it shares) takes the shapes the mixer uses: 4 dims per
+// lane, 16-token runs, one (cos, sin') table per block.  rope_kernel, one
+// thread per pair, takes the rest.
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void rope_kernel(const T* __restrict__ x, T* __restrict__ y,
@@ -526,16 +529,6 @@ __global__ __launch_bounds__(256) void rope_kernel(const T* __restrict__ x, T* _
   yr[d1] = (T)(a * sn + b * cs);
 }
 
-template <typename T>
-hipError_t launch_rope(const void* x, void* y, int B, int T_, int H, int D, int rot_dim,
-                       float base, int offset, int interleaved, int inverse, hipStream_t stream) {
-  const int64_t rows = (int64_t)B * T_ * H;
-  const int64_t n = rows * (rot_dim / 2 + (D - rot_dim) / 2);
-  rope_kernel<T><<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream>>>(
-      (const T*)x, (T*)y, rows, T_, H, D, rot_dim, log2f(base), offset, interleaved,
-      inverse ? -1.f : 1.f);
-  return hipGetLastError();
-}
 
 // ---------------------------------------------------------------------------
 // Fused q/k prologue.  kata/layer.py:305-372 runs three modules in a row on q
@@ -874,6 +867,63 @@ size_t qk_prologue_bwd_workspace(int B, int T, int C, int D, int W) {
   const size_t np = (size_t)B * ((T + kQkTB - 1) / kQkTB);
   const size_t nblk = (size_t)C / kConvCh / qk_threads(C, D);
   return (np * C * (W + 1) + np * nblk * D) * sizeof(float);
+}
+
+// Rotary embedding on the fused prologue's layout: x, y (B, T, H D) rows; a
+// lane owns 4 dims and a run of kQkTB tokens; a block holds whole heads.
+template <typename T>
+__global__ __launch_bounds__(256) void rope_rows_kernel(QKArgs a, float sign) {
+  __shared__ __align__(16) float tc[kQkTB][kQkMaxRw], ts[kQkTB][kQkMaxRw];
+  const int cg = blockIdx.x * blockDim.x + threadIdx.x, t0 = blockIdx.y * kQkTB, b = blockIdx.z;
+  fill_rot_table(a, t0, kQkTB, tc, ts);
+  __syncthreads();
+  const int c0 = kConvCh * cg, j0 = c0 % a.rw, lane = threadIdx.x & 63;
+  const int src = lane + (j0 < a.rot / 2 ? a.rot / 8 : (j0 < a.rot ? -(a.rot / 8) : 0));
+  const T* xb = (const T*)a.x + (int64_t)b * a.T * a.C + c0;  // y may equal x
+  T* yb = (T*)a.y + (int64_t)b * a.T * a.C + c0;
+  v4_t<T> xr[kQkTB];
+#pragma unroll
+  for (int i = 0; i < kQkTB; ++i)
+    xr[i] = t0 + i < a.T ? *reinterpret_cast<const v4_t<T>*>(xb + (int64_t)(t0 + i) * a.C) : v4_t<T>{};
+#pragma unroll
+  for (int i = 0; i < kQkTB; ++i) {
+    if (t0 + i >= a.T) break;  // uniform over the block
+    float u[kConvCh], pv[kConvCh];
+#pragma unroll
+    for (int e = 0; e < kConvCh; ++e) u[e] = (float)xr[i][e];
+    const f32x4 c = *reinterpret_cast<const f32x4*>(&tc[i][j0]);
+    const f32x4 s = *reinterpret_cast<const f32x4*>(&ts[i][j0]);
+    rot_partner(u, pv, a.interleaved, src);
+#pragma unroll
+    for (int e = 0; e < kConvCh; ++e) u[e] = u[e] * c[e] + pv[e] * (sign * s[e]);
+    store4f<T>(yb + (int64_t)(t0 + i) * a.C, u);
+  }
+}
+
+template <typename T>
+hipError_t launch_rope(const void* x, void* y, int B, int T_, int H, int D, int rot_dim,
+                       float base, int offset, int interleaved, int inverse, hipStream_t stream) {
+  const float sign = inverse ? -1.f : 1.f;
+  const bool rows_form = D % 4 == 0 && D <= kQkMaxRw && (interleaved || rot_dim % 8 == 0) &&
+                         B <= 65535 && (T_ + kQkTB - 1) / kQkTB <= 65535 &&
+                         (int64_t)H * D <= INT32_MAX / 8 &&
+                         (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                         (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+  if (rows_form) {
+    QKArgs a{};
+    a.x = x; a.y = y; a.B = B; a.T = T_; a.C = H * D; a.D = D;
+    a.rw = D; a.rot = rot_dim; a.interleaved = interleaved ? 1 : 0; a.offset = offset;
+    a.log2_base = log2f(base);
+    const int nthr = qk_threads(a.C, D);
+    rope_rows_kernel<T><<<dim3(a.C / kConvCh / nthr, (T_ + kQkTB - 1) / kQkTB, B), dim3(nthr), 0,
+                          stream>>>(a, sign);
+    return hipGetLastError();
+  }
+  const int64_t rows = (int64_t)B * T_ * H;
+  const int64_t n = rows * (rot_dim / 2 + (D - rot_dim) / 2);
+  rope_kernel<T><<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream>>>(
+      (const T*)x, (T*)y, rows, T_, H, D, rot_dim, log2f(base), offset, interleaved, sign);
+  return hipGetLastError();
 }
 
 template hipError_t launch_qk_prologue<__bf16>(const QKArgs&, int, bool, hipStream_t);
