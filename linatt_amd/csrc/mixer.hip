@@ -9,7 +9,7 @@
 //
 // Short convolution (depthwise, causal, kernel W):
 //   z[t, c] = bias[c] + sum_{w < W} weight[c, w] x[t - (W - 1) + w, c]
-//   y = silu(z) = z / (1 + e^-z)  (or y = z)
+//   y = silu(z) = z / (1 + e^-z)  (or y = z), the reciprocal by v_rcp_f32
 // with x[t < 0] taken from a cache of the W inputs before the chunk (the
 // newest last), or zero.  One lane owns kConvCh = 4 adjacent channels (one
 // 8-byte load per token in 16-bit types, so C = 768 fills its 64-lane waves
@@ -51,6 +51,10 @@ __device__ __forceinline__ float group_sum(float v) {
   if constexpr (L >= 64) v += __shfl_xor(v, 32);
   return v;
 }
+
+// 1 / (1 + e^-z) with the hardware reciprocal (1 ulp; an IEEE division is a
+// ten-instruction sequence, and the convolutions take one per element)
+__device__ __forceinline__ float sigmoidf(float z) { return __builtin_amdgcn_rcpf(1.f + __expf(-z)); }
 
 constexpr int kConvTB = 16;  // tokens per lane
 constexpr int kConvCh = 4;   // channels per lane of the short convolution
@@ -153,7 +157,7 @@ __global__ __launch_bounds__(64) void short_conv_fwd_kernel(ConvArgs a) {
       float z = bv[e];
 #pragma unroll
       for (int w = 0; w < W; ++w) z += wv[e][w] * win[w][e];
-      yv[e] = a.act ? z / (1.f + __expf(-z)) : z;
+      yv[e] = a.act ? z * sigmoidf(z) : z;
     }
     store4f<T>(yb + (int64_t)t * a.C, yv);
   }
@@ -232,7 +236,7 @@ __global__ __launch_bounds__(64) void short_conv_bwd_kernel(ConvArgs a) {
         for (int w = 0; w < W; ++w) z += wv[e][w] * win[w][e];
         float d = g[e];
         if (a.act) {
-          const float s = 1.f / (1.f + __expf(-z));
+          const float s = sigmoidf(z);
           d *= s * (1.f + z * (1.f - s));
         }
         dz[W - 1][e] = d;
@@ -641,7 +645,7 @@ __global__ __launch_bounds__(256) void qk_prologue_fwd_kernel(QKArgs a) {
       float z = bv[e];
 #pragma unroll
       for (int w = 0; w < W; ++w) z += wv[e][w] * win[w][e];
-      u[e] = a.act ? z / (1.f + __expf(-z)) : z;
+      u[e] = a.act ? z * sigmoidf(z) : z;
       ss += u[e] * u[e];
     }
     if (a.norm) {
@@ -739,7 +743,7 @@ __global__ __launch_bounds__(256) void qk_prologue_bwd_kernel(QKArgs a) {
         z[e] = bv[e];
 #pragma unroll
         for (int w = 0; w < W; ++w) z[e] += wv[e][w] * win[w][e];
-        uv[e] = a.act ? z[e] / (1.f + __expf(-z[e])) : z[e];
+        uv[e] = a.act ? z[e] * sigmoidf(z[e]) : z[e];
         ss += uv[e] * uv[e];
       }
       if (a.rot) {  // g = R^T dy
@@ -769,7 +773,7 @@ __global__ __launch_bounds__(256) void qk_prologue_bwd_kernel(QKArgs a) {
       for (int e = 0; e < kConvCh; ++e) {
         float d = g[e];
         if (a.act) {
-          const float sg = 1.f / (1.f + __expf(-z[e]));
+          const float sg = sigmoidf(z[e]);
           d *= sg * (1.f + z[e] * (1.f - sg));
         }
         dz[W - 1][e] = d;
