@@ -477,18 +477,19 @@ def cpu_baseline(q, k, v, do, M, seconds):
                       f"(T={T}, M={M}), float32 dense fwd + explicit bwd, {el:.1f} s"}
 
 
-def cpu_baseline_config1(q, M, seconds):
+def cpu_baseline_config1(qkv, M, seconds):
     """Config 1 (forward only, (1, 4, 512, 64) fp32, M groups): the float32
     dense forward of the reference (kata/parallel_kata_attn.py:49-75) on the
     whole input, repeated until `seconds` elapse."""
     import torch
     K, _ = _oracle()
     th = _cpu_threads()
+    q, k, v = qkv
     B, T, H, D = q.shape
     reps = 0
     t0 = time.perf_counter()
     while True:
-        K.kata_fwd(q, q, q, M, work_dtype=torch.float32)
+        K.kata_fwd(q, k, v, M, work_dtype=torch.float32)
         reps += 1
         if time.perf_counter() - t0 >= seconds:
             break
@@ -528,15 +529,15 @@ def cpu_baseline_delta(gated, seconds):
 
 def bench_config1(steps):
     """Config 1 on the GPU: the fp32 KATA forward at (1, 512, 4, 64), M=4,
-    q,k,v ~ N(0,1) (seed 0), through linatt_kata_fwd."""
+    q, k, v i.i.d. N(0,1) (seed 0), through linatt_kata_fwd."""
     import torch
     from linatt_amd import _lib
     L = _lib.load()
     B, T, H, D, M = 1, 512, 4, 64, 4
     g = torch.Generator().manual_seed(0)
-    q = torch.randn(B, T, H, D, generator=g)
+    q, k, v = (torch.randn(B, T, H, D, generator=g) for _ in range(3))
     dev = torch.device("cuda", 0)
-    qd = q.to(dev)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
     o = torch.empty_like(qd)
     den = torch.empty(B, T, H, device=dev)
     sp = _lib.stream_of(qd)
@@ -544,7 +545,7 @@ def bench_config1(steps):
 
     def fwd():
         _lib.check("linatt_kata_fwd", L.linatt_kata_fwd(
-            P(qd), P(qd), P(qd), None, P(o), P(den), B, T, H, H, D, D, M, 1.0 / math.sqrt(D // M),
+            P(qd), P(kd), P(vd), None, P(o), P(den), B, T, H, H, D, D, M, 1.0 / math.sqrt(D // M),
             0, _lib.LINATT_FLOAT32, sp))
 
     for _ in range(3):
@@ -558,7 +559,7 @@ def bench_config1(steps):
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
-    return q, {"config": {"B": B, "T": T, "H": H, "D": D, "num_groups": M, "dtype": "f32",
+    return (q, k, v), {"config": {"B": B, "T": T, "H": H, "D": D, "num_groups": M, "dtype": "f32",
                           "seed": 0},
                "fwd_ms": round(ms, 4), "tokens_per_s": round(B * T / (ms * 1e-3), 1)}
 

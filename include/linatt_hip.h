@@ -292,7 +292,8 @@ int linatt_dkata_bwd(const void* q, const void* k, const void* v, const float* b
  * x, y (B,T,C) [dtype], C a multiple of 8, W in {2,3,4}; weight (C,W) and
  * bias (C) float32 (bias may be NULL).  cache_in (B,C,W) [dtype]: the W inputs
  * before position 0, newest last (NULL: zeros); cache_out (B,C,W): the W
- * inputs before position T, for the next call (may be NULL).  The backward
+ * inputs before position T, for the next call (may be NULL; it may alias
+ * cache_in only when T <= 16, else LINATT_EINVAL).  The backward
  * gives dx and float32 dweight (C,W) / dbias (C, may be NULL); no gradient
  * flows to cache_in.  Workspace: linatt_short_conv_bwd_workspace_bytes. */
 int linatt_short_conv_fwd(const void* x, const float* weight, const float* bias,
@@ -320,7 +321,8 @@ int linatt_rope(const void* x, void* y, int B, int T, int H, int D, int rot_dim,
  * RotaryEmbedding), with the intermediates kept in fp32 instead of rounded to
  * the input dtype between the modules:
  *   u = act(bias + sum_w conv_weight[c,w] x[b, t-(W-1)+w, c])   (as
- *       linatt_short_conv_fwd, with cache_in / cache_out),
+ *       linatt_short_conv_fwd, with cache_in / cache_out, which may alias
+ *       only when T <= 16),
  *   norm 1: n = u (mean_d u^2 + eps)^-1/2 norm_weight (norm_weight NULL: 1);
  *   norm 2: n = u (sum_d u^2 + eps)^-1/2 (fla l2norm; norm_weight must be
  *           NULL); norm 0: n = u;

@@ -25,6 +25,17 @@ template <> constexpr int dtype_of<_Float16>() { return LINATT_FLOAT16; }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// the convolution kernels write cache_out from the block holding token T - 1
+// while the block of tokens 0..15 reads cache_in: with more than one 16-token
+// run the two must not share memory (one run reads its halo before it writes)
+bool cache_races(const void* cache_in, const void* cache_out, int B, int C, int W, int T,
+                 int dtype) {
+  if (!cache_in || !cache_out || T <= 16) return false;
+  const size_t n = (size_t)B * C * W * (dtype == LINATT_FLOAT32 ? 4 : 2);
+  const uintptr_t i0 = reinterpret_cast<uintptr_t>(cache_in), o0 = reinterpret_cast<uintptr_t>(cache_out);
+  return i0 < o0 + n && o0 < i0 + n;
+}
+
 std::string shape_str(int B, int T, int HQ, int H, int dk, int dv, int M) {
   char buf[160];
   snprintf(buf, sizeof buf, "B=%d T=%d HQ=%d H=%d dk=%d dv=%d num_groups=%d", B, T, HQ, H, dk,
@@ -416,6 +427,8 @@ int linatt_short_conv_fwd(const void* x, const float* weight, const float* bias,
   if (!known_dtype(dtype)) return fail(LINATT_EINVAL, std::string(fn) + ": unknown dtype");
   if (!x || !weight || !y) return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
   if (!aligned16(x) || !aligned16(y)) return fail(LINATT_EINVAL, std::string(fn) + ": x and y must be 16-byte aligned");
+  if (cache_races(cache_in, cache_out, B, C, W, T, dtype))
+    return fail(LINATT_EINVAL, std::string(fn) + ": cache_out overlaps cache_in with T > 16");
   ConvArgs a{};
   a.x = x; a.w = weight; a.bias = bias; a.cache_in = cache_in; a.y = y; a.cache_out = cache_out;
   a.B = B; a.T = T; a.C = C; a.act = activation;
@@ -547,6 +560,8 @@ int linatt_qk_prologue_fwd(const void* x, const float* conv_weight, const float*
   if (st) return st;
   if (!x || !conv_weight || !y) return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
   if (!aligned16(x) || !aligned16(y)) return fail(LINATT_EINVAL, std::string(fn) + ": x and y must be 16-byte aligned");
+  if (cache_races(cache_in, cache_out, B, H * D, W, T, dtype))
+    return fail(LINATT_EINVAL, std::string(fn) + ": cache_out overlaps cache_in with T > 16");
   QKArgs a = qk_args(x, conv_weight, conv_bias, cache_in, norm_weight, B, T, H, D, activation,
                      norm, eps, rope_width, rot_dim, base, offset, interleaved);
   a.y = y; a.cache_out = cache_out;

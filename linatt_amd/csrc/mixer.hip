@@ -908,7 +908,10 @@ template <typename T>
 hipError_t launch_rope(const void* x, void* y, int B, int T_, int H, int D, int rot_dim,
                        float base, int offset, int interleaved, int inverse, hipStream_t stream) {
   const float sign = inverse ? -1.f : 1.f;
-  const bool rows_form = D % 4 == 0 && D <= kQkMaxRw && (interleaved || rot_dim % 8 == 0) &&
+  // half-split partners come from lane +- rot / 8 by a wave shuffle, so a
+  // head's D / 4 lanes must not cross a wave boundary: D / 4 must divide 64
+  const bool rows_form = D % 4 == 0 && D <= kQkMaxRw &&
+                         (interleaved || (rot_dim % 8 == 0 && 64 % (D / 4) == 0)) &&
                          B <= 65535 && (T_ + kQkTB - 1) / kQkTB <= 65535 &&
                          (int64_t)H * D <= INT32_MAX / 8 &&
                          (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&

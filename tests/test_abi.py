@@ -163,7 +163,7 @@ def _qk(lib, bwd=False, **kw):
             a["norm"], a["eps"], a["rw"], a["rot"], a["base"], a["offset"], a["inter"],
             a["dtype"], None)
     return lib.linatt_qk_prologue_fwd(
-        a["x"], a["w"], a["b"], a["cache"], a["nw"], a["y"], None, a["B"], a["T"], a["H"],
+        a["x"], a["w"], a["b"], a["cache"], a["nw"], a["y"], kw.get("co"), a["B"], a["T"], a["H"],
         a["D"], a["W"], a["act"], a["norm"], a["eps"], a["rw"], a["rot"], a["base"],
         a["offset"], a["inter"], a["dtype"], None)
 
@@ -189,6 +189,19 @@ def test_qk_prologue_argument_errors(lib):
     # rot_dim 0 switches the rotation off and ignores rope_width
     assert _qk(lib, rot=0, rw=-3, T=0) == EINVAL
     assert b"non-positive" in lib.linatt_last_error()
+    # an in-place cache update races across 16-token runs
+    c0, c1 = ctypes.c_void_p(1 << 24), ctypes.c_void_p((1 << 24) + 64)
+    assert _qk(lib, T=17, cache=c0, co=c1) == EINVAL
+    assert b"cache_out overlaps cache_in" in lib.linatt_last_error()
+
+
+def test_short_conv_cache_alias_rejected(lib):
+    EINVAL = -1
+    c0, c1 = ctypes.c_void_p(1 << 24), ctypes.c_void_p((1 << 24) + 2 * 8 * 4 - 2)
+    st = lib.linatt_short_conv_fwd(FAKE, FAKE, None, c0, FAKE, c1, 1, 40, 8, 4, 1, 1, None)
+    assert st == EINVAL and b"cache_out overlaps cache_in" in lib.linatt_last_error()
+    st = lib.linatt_short_conv_fwd(FAKE, FAKE, None, c0, FAKE, c0, 2, 17, 8, 4, 1, 0, None)
+    assert st == EINVAL
 
 
 def test_qk_prologue_workspace_bytes(lib):

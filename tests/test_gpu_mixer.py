@@ -162,8 +162,9 @@ def test_repeat_runs_identical(MX):
 @pytest.mark.parametrize("interleaved", [True, False], ids=["gptj", "neox"])
 @pytest.mark.parametrize("dtype", DT, ids=["bf16", "f16", "f32"])
 @pytest.mark.parametrize("shape,rot,offset", [((2, 300, 12, 64), 64, 0), ((1, 17, 3, 64), 48, 5),
-                                              ((2, 50, 8, 16), 16, 2040)],
-                         ids=["full", "partial", "group-late"])
+                                              ((2, 50, 8, 16), 16, 2040),
+                                              ((2, 40, 8, 96), 96, 3), ((1, 33, 5, 48), 32, 0)],
+                         ids=["full", "partial", "group-late", "d96", "d48"])
 def test_rope_parity(MX, interleaved, dtype, shape, rot, offset):
     """fwd against the float64 oracle; bwd = the inverse rotation of dy (the
     rotation is orthogonal), checked against float64 autograd."""

@@ -106,3 +106,45 @@ def test_rope_layouts_are_a_permutation():
     a = X.rope(x, 8, 100.0, 2, interleaved=True)
     b = X.rope(x[..., perm.argsort()], 8, 100.0, 2, interleaved=False)[..., perm]
     assert torch.allclose(a, b, atol=1e-12)
+
+
+@pytest.mark.parametrize("interleaved", [True, False])
+@pytest.mark.parametrize("offset", [0, 5])
+def test_rope_closed_form_frequencies_and_sign(interleaved, offset):
+    """RoFormer's rotation (Su et al. 2021, eq. 34) at single positions and
+    pairs: pair p of a rot_dim-wide rotation at position t turns (a, b) into
+    (a cos t th_p - b sin t th_p, a sin t th_p + b cos t th_p) with
+    th_p = base^(-2p / rot_dim).  Checked element by element with scalar
+    math at t = 1 and t = 7 (plus an offset) for the first and last pair, and
+    against hand-computed constants for unit inputs."""
+    import math
+    g = torch.Generator().manual_seed(9)
+    D, rot, base = 12, 8, 10000.0
+    half = rot // 2
+    x = torch.randn(1, 8, 1, D, generator=g, dtype=torch.float64)
+    y = X.rope(x, rot, base, offset, interleaved)
+    for t in (1, 7):
+        pos = t + offset
+        for p in (0, half - 1):
+            i0, i1 = (2 * p, 2 * p + 1) if interleaved else (p, p + half)
+            th = base ** (-2.0 * p / rot)
+            a, b = float(x[0, t, 0, i0]), float(x[0, t, 0, i1])
+            c, s = math.cos(pos * th), math.sin(pos * th)
+            assert abs(float(y[0, t, 0, i0]) - (a * c - b * s)) < 1e-12
+            assert abs(float(y[0, t, 0, i1]) - (a * s + b * c)) < 1e-12
+    # unit vector on the first element of pair 1 at t = 7, rot_dim = 4,
+    # base = 10000: th_1 = 10000^(-1/2) = 0.01, so the angle is 0.07 rad
+    # and the rotated vector is (cos 0.07, sin 0.07) = (0.99755100, 0.06994285)
+    e = torch.zeros(1, 8, 1, 4, dtype=torch.float64)
+    i0, i1 = (2, 3) if interleaved else (1, 3)
+    e[0, 7, 0, i0] = 1.0
+    r = X.rope(e, 4, 10000.0, 0, interleaved)
+    assert abs(float(r[0, 7, 0, i0]) - 0.9975510002532796) < 1e-12
+    assert abs(float(r[0, 7, 0, i1]) - 0.0699428473375328) < 1e-12
+    # pair 0 turns by t radians: at t = 1, (0, 1) -> (-sin 1, cos 1)
+    e = torch.zeros(1, 2, 1, 4, dtype=torch.float64)
+    j0, j1 = (0, 1) if interleaved else (0, 2)
+    e[0, 1, 0, j1] = 1.0
+    r = X.rope(e, 4, 10000.0, 0, interleaved)
+    assert abs(float(r[0, 1, 0, j0]) + 0.8414709848078965) < 1e-12
+    assert abs(float(r[0, 1, 0, j1]) - 0.5403023058681398) < 1e-12
