@@ -102,6 +102,42 @@ int linatt_kata_bwd_dkdv(const void* q, const void* k, const void* v, const void
                          void* workspace, int B, int T, int HQ, int H, int dk_dim, int dv_dim,
                          int num_groups, float scale, int variant, int dtype, void* stream);
 
+/* KATA forward with the mixer's output RMSNorm fused into its epilogue.
+ * Replaces the pair parallel_kata_attn(...) -> self.norm(o) of
+ * KataAttention.forward (kata/layer.py:456-487, 539; the norm is
+ * fla.modules.RMSNorm(head_v_dim, eps=norm_eps, dtype=float32), built at
+ * :199-205).  Writes o and den exactly as linatt_kata_fwd, and also
+ *   rstd (B,T,HQ) float32 = (mean_d o_r[d]^2 + eps)^-1/2,
+ *   y (B,T,HQ,dv) [dtype]  = o_r * rstd * norm_weight   (norm_weight (dv)
+ *   float32, or NULL for weight 1),
+ * where o_r is o as stored (rounded to dtype), as the unfused norm reads it.
+ * dk = dv = 64 in bfloat16 or float16 (else LINATT_EUNSUPPORTED); concat,
+ * sum and decayed (c non-NULL) scores. */
+int linatt_kata_fwd_onorm(const void* q, const void* k, const void* v, const float* c, void* o,
+                          float* den, const float* norm_weight, float eps, void* y, float* rstd,
+                          int B, int T, int HQ, int H, int dk, int dv, int num_groups, float scale,
+                          int variant, int dtype, void* stream);
+
+/* Bytes of workspace linatt_kata_bwd_onorm needs: linatt_kata_bwd's, then
+ * per-workgroup partials of the norm-weight gradient. */
+size_t linatt_kata_bwd_onorm_workspace_bytes(int B, int T, int HQ, int dv_dim, int dtype);
+
+/* Backward of linatt_kata_fwd_onorm from dy, the gradient of y: the norm's
+ * backward dO = rstd (w dy) - (rstd^3 / dv) <o, w dy> o (rounded to dtype, as
+ * the unfused norm's dx) is formed in the dq pass's registers, then the
+ * attention backward runs as linatt_kata_bwd (linatt_kata_bwd_decay when c
+ * and dc are non-NULL).  dnorm_weight (dv) float32 = sum over rows of
+ * dy * o * rstd, in a fixed order (may be NULL; requires norm_weight).  o,
+ * den, rstd from linatt_kata_fwd_onorm with the same inputs.  bfloat16 at
+ * dk = dv = 64 only.  Replaces the norm's backward and
+ * parallel_kata_attn_bwd_triton (kata/parallel_kata_attn.py:364-529). */
+int linatt_kata_bwd_onorm(const void* q, const void* k, const void* v, const float* c,
+                          const void* o, const float* den, const float* rstd,
+                          const float* norm_weight, const void* dy, void* dq, void* dk, void* dv,
+                          float* dc, float* dnorm_weight, void* workspace, int B, int T, int HQ,
+                          int H, int dk_dim, int dv_dim, int num_groups, float scale, int variant,
+                          int dtype, void* stream);
+
 /* Size of the fixed device scratch behind linatt_kata_bwd_noalloc (32 MiB). */
 #define LINATT_NOALLOC_SCRATCH_BYTES (32u << 20)
 

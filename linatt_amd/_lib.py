@@ -44,6 +44,9 @@ SIGNATURES = {
     "linatt_kata_bwd_dkdv": (_i, [_vp] * 10 + [_i] * 7 + [_f, _i, _i, _vp]),
     "linatt_kata_bwd_noalloc": (_i, [_vp] * 9 + [_i] * 7 + [_f, _i, _i, _vp]),
     "linatt_noalloc_scratch_bytes": (_sz, []),
+    "linatt_kata_fwd_onorm": (_i, [_vp] * 7 + [_f, _vp, _vp] + [_i] * 7 + [_f, _i, _i, _vp]),
+    "linatt_kata_bwd_onorm_workspace_bytes": (_sz, [_i] * 5),
+    "linatt_kata_bwd_onorm": (_i, [_vp] * 15 + [_i] * 7 + [_f, _i, _i, _vp]),
     "linatt_delta_supported": (_i, [_i, _i, _i]),
     "linatt_delta_ctx_bytes": (_sz, [_i] * 6),
     "linatt_delta_bwd_workspace_bytes": (_sz, [_i] * 6),

@@ -317,6 +317,99 @@ int linatt_kata_bwd_dkdv(const void* q, const void* k, const void* v, const void
                         dtype, stream);
 }
 
+// The output RMSNorm fused into the KATA tile kernels: 16-bit, dk = dv = 64
+// (the backward: bf16, whose dk/dv pass reads the dO' the dq pass forms)
+static int check_onorm(const char* fn, int dk, int dv, int dtype, float eps, bool bwd) {
+  if (dk != 64 || dv != 64 || dtype == LINATT_FLOAT32 || (bwd && dtype != LINATT_BFLOAT16))
+    return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": the fused output norm runs at dk = dv = 64 in " +
+                                         (bwd ? "bfloat16" : "bfloat16 or float16"));
+  if (!(eps >= 0.f)) return fail(LINATT_EINVAL, std::string(fn) + ": eps must be non-negative");
+  return LINATT_OK;
+}
+
+static size_t onorm_part_offset(int B, int T, int HQ, int dv_dim, int dtype) {
+  return (linatt_kata_bwd_workspace_bytes(B, T, HQ, dv_dim, dtype) + 255) & ~(size_t)255;
+}
+
+int linatt_kata_fwd_onorm(const void* q, const void* k, const void* v, const float* c, void* o,
+                          float* den, const float* norm_weight, float eps, void* y, float* rstd,
+                          int B, int T, int HQ, int H, int dk, int dv, int num_groups, float scale,
+                          int variant, int dtype, void* stream) {
+  g_last_error.clear();
+  const char* fn = "linatt_kata_fwd_onorm";
+  int st = check_common(B, T, HQ, H, dk, dv, num_groups, scale, variant, dtype);
+  if (st) return st;
+  if ((st = check_onorm(fn, dk, dv, dtype, eps, false))) return st;
+  if (!q || !k || !v || !o || !den || !y || !rstd) return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  if (c && variant != LINATT_KATA_CONCAT)
+    return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": decay is only defined for the concat score");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(y) ||
+      (norm_weight && !aligned16(norm_weight)))
+    return fail(LINATT_EINVAL, std::string(fn) + ": q, k, v, o, y, norm_weight must be 16-byte aligned");
+  KataArgs a{};
+  a.q = q; a.k = k; a.v = v; a.c = c; a.o = o; a.den = den;
+  a.B = B; a.T = T; a.HQ = HQ; a.H = H; a.DK = dk; a.DV = dv; a.M = num_groups; a.scale = scale;
+  a.nw = norm_weight; a.y = y; a.rstd = rstd; a.eps = eps;
+  bool found = false;
+  hipError_t e = dispatch_fwd(a, dtype, variant, c != nullptr, (hipStream_t)stream, &found);
+  if (!found)
+    return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": no kernel compiled for " +
+                                         shape_str(B, T, HQ, H, dk, dv, num_groups));
+  if (e != hipSuccess)
+    return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
+size_t linatt_kata_bwd_onorm_workspace_bytes(int B, int T, int HQ, int dv_dim, int dtype) {
+  if (B <= 0 || T <= 0 || HQ <= 0 || dv_dim <= 0) return 0;
+  const size_t nblk = (size_t)B * HQ * ((T + 127) / 128);
+  return onorm_part_offset(B, T, HQ, dv_dim, dtype) + nblk * dv_dim * sizeof(float);
+}
+
+int linatt_kata_bwd_onorm(const void* q, const void* k, const void* v, const float* c,
+                          const void* o, const float* den, const float* rstd,
+                          const float* norm_weight, const void* dy, void* dq, void* dk, void* dv,
+                          float* dc, float* dnorm_weight, void* workspace, int B, int T, int HQ,
+                          int H, int dk_dim, int dv_dim, int num_groups, float scale, int variant,
+                          int dtype, void* stream) {
+  g_last_error.clear();
+  const char* fn = "linatt_kata_bwd_onorm";
+  int st = check_common(B, T, HQ, H, dk_dim, dv_dim, num_groups, scale, variant, dtype);
+  if (st) return st;
+  if ((st = check_onorm(fn, dk_dim, dv_dim, dtype, 0.f, true))) return st;
+  if (!q || !k || !v || !o || !den || !rstd || !dy || !dq || !dk || !dv || !workspace)
+    return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  if ((c == nullptr) != (dc == nullptr)) return fail(LINATT_EINVAL, std::string(fn) + ": c and dc go together");
+  if (c && variant != LINATT_KATA_CONCAT)
+    return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": decay is only defined for the concat score");
+  if (dnorm_weight && !norm_weight)
+    return fail(LINATT_EINVAL, std::string(fn) + ": dnorm_weight without norm_weight");
+  const void* ps[] = {q, k, v, o, dy, dq, dk, dv, workspace, norm_weight};
+  for (const void* p : ps)
+    if (p && !aligned16(p))
+      return fail(LINATT_EINVAL, std::string(fn) + ": tensors and workspace must be 16-byte aligned");
+  KataArgs a{};
+  a.q = q; a.k = k; a.v = v; a.o = const_cast<void*>(o); a.den = const_cast<float*>(den);
+  a.dout = nullptr; a.dq = dq; a.dk = dk; a.dv = dv; a.delta = (float*)workspace;
+  a.B = B; a.T = T; a.HQ = HQ; a.H = H; a.DK = dk_dim; a.DV = dv_dim; a.M = num_groups;
+  a.scale = scale; a.c = c; a.dc = dc;
+  a.nw = norm_weight; a.rstd = const_cast<float*>(rstd); a.dy = dy;
+  float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                         onorm_part_offset(B, T, HQ, dv_dim, dtype));
+  a.nw_part = dnorm_weight ? part : nullptr;
+  bool found = false;
+  hipError_t e = dispatch_bwd(a, KATA_BWD_DQ | KATA_BWD_DKDV, dtype, variant, c != nullptr,
+                              (hipStream_t)stream, &found);
+  if (!found)
+    return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": no kernel compiled for " +
+                                         shape_str(B, T, HQ, H, dk_dim, dv_dim, num_groups));
+  if (e == hipSuccess && dnorm_weight)
+    e = launch_colsum(part, dnorm_weight, B * HQ * ((T + 127) / 128), dv_dim, (hipStream_t)stream);
+  if (e != hipSuccess)
+    return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
 int linatt_delta_supported(int dtype, int dk, int dv) { return delta_compiled(dtype, dk, dv) ? 1 : 0; }
 
 size_t linatt_delta_ctx_bytes(int B, int T, int H, int dk, int dv, int dtype) {

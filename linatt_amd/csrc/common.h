@@ -392,6 +392,27 @@ __device__ __forceinline__ v8_t<T> tile_tr8_16(const T* tile, int r0, int c0, in
                   ds_tr4<T>(reinterpret_cast<const T*>(base + tile_off(row + 8, col))));
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_plus(float v) {
+  return v + __builtin_bit_cast(
+                 float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// sum over each aligned group of L lanes (a power of two up to 64), the same
+// bits on every lane: DPP steps inside a 16-lane row (quad xor 1, quad xor 2,
+// half-row mirror, row mirror; each adds the same two partial sums on both
+// sides), then xor-16 and xor-32 shuffles for wider groups
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(L >= 1 && L <= 64 && (L & (L - 1)) == 0, "a power of two up to 64 lanes");
+  if constexpr (L >= 2) v = dpp_plus<0xB1>(v);
+  if constexpr (L >= 4) v = dpp_plus<0x4E>(v);
+  if constexpr (L >= 8) v = dpp_plus<0x141>(v);
+  if constexpr (L >= 16) v = dpp_plus<0x140>(v);
+  if constexpr (L >= 32) v += __shfl_xor(v, 16);
+  if constexpr (L >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+
 // acc + sum of the 8 elements of an operand, in fp32.  For 16-bit types one
 // v_dot2 against (1, 1) adds two elements, so a row sum over the rounded
 // operand costs half an instruction per element.

@@ -440,11 +440,11 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
 // repeat the last valid row; every use of them is masked.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
-__global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
+__global__ __launch_bounds__(256, (SUM || DECAY) ? 2 : 3) void kata_bwd_dq_tile_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ o, const float* __restrict__ den, const T* __restrict__ dout,
     T* __restrict__ dq, float* __restrict__ delta_out, const float* __restrict__ c,
-    float* __restrict__ dc, int Tn, int HQ, int H, float scale2, int nqt, int nbh) {
+    float* __restrict__ dc, int Tn, int HQ, int H, float scale2, int nqt, int nbh, OutNorm on) {
   constexpr int E = DK / M;
   constexpr int KE = E / 16;
   static_assert(sizeof(T) == 2 && DK == 64 && DV == 64, "64 x 64 16-bit tiles");
@@ -452,6 +452,7 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
   __shared__ __attribute__((aligned(16))) T Kb[NB][64 * 64];
   __shared__ __attribute__((aligned(16))) T Vb[NB][64 * 64];
   __shared__ __attribute__((aligned(16))) float Cs[NB][64];
+  __shared__ __attribute__((aligned(16))) float Wred[4][DV];  // output-norm weight gradient per wave
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -484,14 +485,56 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
     pdl = scale2 / (d > 0.f ? d : 1.f);
   }
   float dpart = 0.f, dppart = 0.f;
+  // this lane's dims 16 kk + 8 hh + 0..7 of dO (or of dy) and of o
+  v8_t<T> ov[DV / 16];
+  const T* dsrc = on.y ? (const T*)on.y : dout;
 #pragma unroll
   for (int kk = 0; kk < DV / 16; ++kk) {
-    doop[kk] = tvalid ? ld8<T>(dout + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
-    const v8_t<T> ov = tvalid ? ld8<T>(o + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
+    doop[kk] = tvalid ? ld8<T>(dsrc + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
+    ov[kk] = tvalid ? ld8<T>(o + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
+  }
+  if (on.y) {
+    // output RMSNorm backward (uniform branch), y = o r w with r = rstd:
+    // dO = r w dy - (r^3 / DV) <o, w dy> o, rounded to T as the unfused
+    // norm's dx is; the weight gradient sum_rows dy o r goes to this
+    // workgroup's partial (summed over the wave's 32 rows by DPP, eight dims
+    // at a time to bound the live registers, then over the four waves at
+    // the end of the kernel)
+    const float rr = tvalid ? on.rstd[qrow] : 0.f;
+    float wv[DV / 16][8];
+    float sdot = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < DV / 16; ++kk) {
+      const int d0 = 16 * kk + 8 * hh;
+      const f32x4 w0 = on.w ? *reinterpret_cast<const f32x4*>(on.w + d0) : f32x4{1.f, 1.f, 1.f, 1.f};
+      const f32x4 w1 = on.w ? *reinterpret_cast<const f32x4*>(on.w + d0 + 4) : f32x4{1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        wv[kk][j] = w0[j];
+        wv[kk][4 + j] = w1[j];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sdot += wv[kk][j] * (float)doop[kk][j] * (float)ov[kk][j];
+    }
+    sdot += __shfl_xor(sdot, 32);
+    const float cf = rr * rr * rr * sdot / DV;
+#pragma unroll
+    for (int kk = 0; kk < DV / 16; ++kk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float g = (float)doop[kk][j], x = (float)ov[kk][j];
+        const float wp = group_sum<32>(g * x * rr);
+        if (cl == 0) Wred[w][16 * kk + 8 * hh + j] = wp;
+        doop[kk][j] = (T)(rr * (wv[kk][j] * g) - cf * x);
+        if (j == 7) __builtin_amdgcn_sched_barrier(0);
+      }
+  }
+#pragma unroll
+  for (int kk = 0; kk < DV / 16; ++kk) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      dpart += (float)ov[j] * (float)doop[kk][j];
-      if constexpr (kPre) dppart += (float)ov[j] * (float)(T)((float)doop[kk][j] * pdl);
+      dpart += (float)ov[kk][j] * (float)doop[kk][j];
+      if constexpr (kPre) dppart += (float)ov[kk][j] * (float)(T)((float)doop[kk][j] * pdl);
     }
   }
   const float delta = dpart + __shfl_xor(dpart, 32);
@@ -718,6 +761,13 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
         st4<T>(drow + 32 * rb + 8 * i + 4 * hh,
                to4<T>(acc[rb][4 * i] * f, acc[rb][4 * i + 1] * f, acc[rb][4 * i + 2] * f,
                       acc[rb][4 * i + 3] * f));
+  }
+  // output-norm weight gradient: this workgroup's partial, the four waves'
+  // row sums added in a fixed order (every wave reaches this barrier)
+  if (on.part) {
+    __syncthreads();
+    if (tid < DV)
+      on.part[((int64_t)bh * nqt + qt) * DV + tid] = (Wred[0][tid] + Wred[1][tid]) + (Wred[2][tid] + Wred[3][tid]);
   }
 }
 
@@ -1052,7 +1102,10 @@ hipError_t launch_kata_bwd(const KataArgs& a, int parts, hipStream_t stream) {
       if constexpr (kTiles)
         kata_bwd_dq_tile_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbh), dim3(256), 0, stream>>>(
             (const T*)a.q, (const T*)a.k, (const T*)a.v, (const T*)a.o, a.den, (const T*)a.dout,
-            (T*)a.dq, a.delta, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt, nbh);
+            (T*)a.dq, a.delta, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt, nbh,
+            OutNorm{a.nw, const_cast<void*>(a.dy), a.rstd, a.nw_part, a.eps});
+      else if (a.dy)
+        return hipErrorInvalidValue;  // the output norm is fused in the tile kernel only
       else
       kata_bwd_dq_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbh), dim3(256), 0, stream>>>(
           (const T*)a.q, (const T*)a.k, (const T*)a.v, (const T*)a.o, a.den, (const T*)a.dout,

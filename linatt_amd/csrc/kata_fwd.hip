@@ -202,7 +202,7 @@ template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
 __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const float* __restrict__ c, T* __restrict__ o, float* __restrict__ den,
-    int Tn, int HQ, int H, float scale2, int nqt, int nbh) {
+    int Tn, int HQ, int H, float scale2, int nqt, int nbh, OutNorm on) {
   constexpr int E = DK / M;
   constexpr int KE = E / 16;
   static_assert(sizeof(T) == 2 && DK == 64 && DV == 64, "64 x 64 16-bit tiles");
@@ -447,17 +447,50 @@ __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
   }
 
   const float dsum = dpart + __shfl_xor(dpart, 32);
+  const float inv = dsum > 0.f ? 1.f / dsum : 1.f;
+  // this lane's 32 elements of its query's output row (dims 32 db + 8 i +
+  // 4 hh + r), rounded to T as stored
+  v4_t<T> ov[DV / 32][4];
+#pragma unroll
+  for (int db = 0; db < DV / 32; ++db)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      ov[db][i] = to4<T>(oacc[db][4 * i] * inv, oacc[db][4 * i + 1] * inv,
+                         oacc[db][4 * i + 2] * inv, oacc[db][4 * i + 3] * inv);
+  const int64_t row = ((int64_t)b * Tn + tl) * HQ + hq;
   if (tl < Tn) {
-    const float inv = dsum > 0.f ? 1.f / dsum : 1.f;
-    T* orow = o + (((int64_t)b * Tn + tl) * HQ + hq) * DV;
+    T* orow = o + row * DV;
+#pragma unroll
+    for (int db = 0; db < DV / 32; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st4<T>(orow + 32 * db + 8 * i + 4 * hh, ov[db][i]);
+    if (hh == 0) den[row] = dsum * (scale2 / pe);
+  }
+  // output RMSNorm (uniform branch): y = o rsqrt(mean(o^2) + eps) w over the
+  // row of the stored (rounded) o, whose two halves are lanes l and l ^ 32
+  if (on.y) {
+    float ss = 0.f;
 #pragma unroll
     for (int db = 0; db < DV / 32; ++db)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        st4<T>(orow + 32 * db + 8 * i + 4 * hh,
-               to4<T>(oacc[db][4 * i] * inv, oacc[db][4 * i + 1] * inv,
-                      oacc[db][4 * i + 2] * inv, oacc[db][4 * i + 3] * inv));
-    if (hh == 0) den[((int64_t)b * Tn + tl) * HQ + hq] = dsum * (scale2 / pe);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ss += (float)ov[db][i][r] * (float)ov[db][i][r];
+    ss += __shfl_xor(ss, 32);
+    const float rr = rsqrtf(ss / DV + on.eps);
+    if (tl < Tn) {
+      T* yrow = (T*)on.y + row * DV;
+#pragma unroll
+      for (int db = 0; db < DV / 32; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d0 = 32 * db + 8 * i + 4 * hh;
+          const f32x4 w4 = on.w ? *reinterpret_cast<const f32x4*>(on.w + d0) : f32x4{1.f, 1.f, 1.f, 1.f};
+          st4<T>(yrow + d0, to4<T>((float)ov[db][i][0] * (rr * w4[0]), (float)ov[db][i][1] * (rr * w4[1]),
+                                   (float)ov[db][i][2] * (rr * w4[2]), (float)ov[db][i][3] * (rr * w4[3])));
+        }
+      if (hh == 0) on.rstd[row] = rr;
+    }
   }
 }
 
@@ -472,10 +505,12 @@ hipError_t launch_kata_fwd(const KataArgs& a, hipStream_t stream) {
     const int nbh = a.B * a.HQ;
     dim3 grid(nqt * nbh), block(256);
     if constexpr (sizeof(T) == 2 && DK == 64 && DV == 64) {
+      const OutNorm on{a.nw, a.y, a.rstd, nullptr, a.eps};
       kata_fwd_tile_kernel<T, DK, DV, M, SUM, DECAY><<<grid, block, 0, stream>>>(
           (const T*)a.q, (const T*)a.k, (const T*)a.v, a.c, (T*)a.o, a.den, a.T, a.HQ, a.H,
-          a.scale * a.scale, nqt, nbh);
+          a.scale * a.scale, nqt, nbh, on);
     } else {
+      if (a.y) return hipErrorInvalidValue;  // the output norm is fused in the tile kernel only
       kata_fwd_kernel<T, DK, DV, M, SUM, DECAY><<<grid, block, 0, stream>>>(
           (const T*)a.q, (const T*)a.k, (const T*)a.v, a.c, (T*)a.o, a.den, a.T, a.HQ, a.H,
           a.scale * a.scale, nqt, nbh);

@@ -28,6 +28,24 @@ struct KataArgs {
   float* dc;         // (B, T, HQ) gradient of the cumulative log-decay c (decay backward)
   int B, T, HQ, H, DK, DV, M;
   float scale;
+  // output RMSNorm over each (b, t, hq) row of o (16-bit 64 x 64 tile
+  // kernels only): the forward writes y and rstd beside o and den when y is
+  // set; the backward takes dy instead of dO when dy is set
+  const float* nw;   // (DV) norm weight, or null (weight 1)
+  void* y;           // (B, T, HQ, DV) normalised output, or null
+  float* rstd;       // (B, T, HQ) (mean(o^2) + eps)^-1/2: forward writes, backward reads
+  float eps;
+  const void* dy;    // (B, T, HQ, DV) gradient of y, or null
+  float* nw_part;    // (nqt B HQ, DV) per-workgroup weight-gradient partials (dq pass)
+};
+
+// The output-norm arguments of the tile kernels (a kernel argument struct).
+struct OutNorm {
+  const float* w;
+  void* y;        // forward: normalised output; backward: dy
+  float* rstd;
+  float* part;    // backward: weight-gradient partials, or null
+  float eps;
 };
 
 template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>

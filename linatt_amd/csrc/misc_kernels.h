@@ -78,6 +78,10 @@ template <typename T>
 hipError_t launch_linear_scan(const void* q, const void* k, const void* v, void* o, float* den, int B,
                               int H, int T_, float scale, float eps, hipStream_t stream);
 
+// Column sums out[i] = sum_p part[p][i] of a (np, n) float32 array in a
+// fixed order (mixer.hip).
+hipError_t launch_colsum(const float* part, float* out, int np, int n, hipStream_t stream);
+
 // Sets the calling thread's linatt_last_error() message and returns code
 // (defined with the C-ABI entry points in api.hip).
 int set_last_error(int code, const char* msg);

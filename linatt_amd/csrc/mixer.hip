@@ -31,27 +31,6 @@ namespace linatt {
 
 namespace {
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_plus(float v) {
-  return v + __builtin_bit_cast(
-                 float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-// sum over each aligned group of L lanes (a power of two up to 64), the same
-// bits on every lane: DPP steps inside a 16-lane row (quad xor 1, quad xor 2,
-// half-row mirror, row mirror; each adds the same two partial sums on both
-// sides), then xor-16 and xor-32 shuffles for wider groups
-template <int L>
-__device__ __forceinline__ float group_sum(float v) {
-  static_assert(L >= 1 && L <= 64 && (L & (L - 1)) == 0, "a power of two up to 64 lanes");
-  if constexpr (L >= 2) v = dpp_plus<0xB1>(v);
-  if constexpr (L >= 4) v = dpp_plus<0x4E>(v);
-  if constexpr (L >= 8) v = dpp_plus<0x141>(v);
-  if constexpr (L >= 16) v = dpp_plus<0x140>(v);
-  if constexpr (L >= 32) v += __shfl_xor(v, 16);
-  if constexpr (L >= 64) v += __shfl_xor(v, 32);
-  return v;
-}
-
 // 1 / (1 + e^-z) with the hardware reciprocal (1 ulp; an IEEE division is a
 // ten-instruction sequence, and the convolutions take one per element)
 __device__ __forceinline__ float sigmoidf(float z) { return __builtin_amdgcn_rcpf(1.f + __expf(-z)); }
@@ -320,6 +299,11 @@ __global__ __launch_bounds__(1024) void colsum_kernel(const float* __restrict__ 
 // column sums of a (np, n) array in one block row
 static void colsum(const float* part, float* out, int np, int n, hipStream_t stream) {
   colsum_kernel<<<dim3((n + 31) / 32), dim3(1024), 0, stream>>>(part, out, np, n, np);
+}
+
+hipError_t launch_colsum(const float* part, float* out, int np, int n, hipStream_t stream) {
+  colsum(part, out, np, n, stream);
+  return hipGetLastError();
 }
 
 // dweight (C, W) and dbias (C) from the convolution partials [np][C][W + 1]

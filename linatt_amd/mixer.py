@@ -377,14 +377,18 @@ def fused_qk_prologue(x, conv, norm, rotary, head_dim, seqlen_offset=0, cache=No
     rotation row width: the head dim, or E under ``rope_group``) or None.
     Equals ``rotary(norm(conv(x)[0].view(B, T, H, D)))`` up to the chain's
     intermediate roundings."""
-    if isinstance(norm, RMSNorm):
-        if norm.hidden_size != head_dim:
-            raise ValueError(f"RMSNorm width {norm.hidden_size} != head_dim {head_dim}")
-        nk, nw, eps = "rmsnorm", norm.weight, norm.eps
-    elif norm == "l2" or norm is None:
+    if norm is None or isinstance(norm, str):
+        if norm not in (None, "l2"):
+            raise ValueError(f"norm must be an RMSNorm module, 'l2' or None, got {norm!r}")
         nk, nw, eps = norm, None, None
+    elif hasattr(norm, "weight") and hasattr(norm, "eps"):
+        # this module's RMSNorm or fla's (weight (head_dim,) or None, eps)
+        width = getattr(norm, "hidden_size", head_dim)
+        if width != head_dim:
+            raise ValueError(f"RMSNorm width {width} != head_dim {head_dim}")
+        nk, nw, eps = "rmsnorm", norm.weight, norm.eps
     else:
-        raise TypeError("norm must be a linatt_amd RMSNorm, 'l2' or None")
+        raise TypeError("norm must be an RMSNorm module (weight, eps), 'l2' or None")
     if rotary is None:
         rw, rot, base, inter = None, 0, 10000.0, True
     else:

@@ -41,6 +41,7 @@ __all__ = [
     "parallel_kata_attn_sum_fwd_impl",
     "parallel_kata_attn_bwd_sum",
     "parallel_kata_attn_decay",
+    "parallel_kata_attn_onorm",
     "ParallelKataAttnFunction",
     "ParallelKataAttnSumFunction",
 ]
@@ -262,3 +263,109 @@ def parallel_kata_attn_decay(q, k, v, c, num_groups=2, scale=None):
     """Decayed SPD attention (reference ``kata/parallel_kata_attn.py:350-354``):
     ``o_t = sum_{s<=t} exp(min(c_t-c_s,0)) A[t,s] v_s / sum(...)``."""
     return _KataDecayFunction.apply(q, k, v, c, num_groups, scale)
+
+
+# ---------------------------------------------------------------------------
+# The mixer's output RMSNorm fused into the attention kernels
+# ---------------------------------------------------------------------------
+
+
+def _onorm_fused(dtype, dk, dv, need_grad):
+    """The fused kernels cover dk = dv = 64 in bf16 (and fp16 without a
+    gradient: the fp16 dk/dv pass reads the unscaled dO, which the fused dq
+    pass never forms)."""
+    if dk != 64 or dv != 64:
+        return False
+    return dtype == torch.bfloat16 or (dtype == torch.float16 and not need_grad)
+
+
+class _KataONormFunction(torch.autograd.Function):
+    """y = RMSNorm(KATA(q, k, v)) per (b, t, head) row: ``linatt_kata_fwd_onorm``
+    writes o, den, y and rstd in one forward; ``linatt_kata_bwd_onorm`` forms
+    the norm's dO from dy inside the dq pass and sums the weight gradient."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, c, weight, eps, num_groups, scale, variant):
+        qc, kc, vc = _prep(q, k, v)
+        B, T, HQ, dk = qc.shape
+        H, dv = kc.shape[2], vc.shape[-1]
+        if scale is None:
+            scale = _default_scale(dk, num_groups)
+        cf = None
+        if c is not None:
+            _lib.require_device(c)
+            cf = c.float().contiguous()
+            assert cf.shape == (B, T, HQ), f"c must be (B,T,HQ) = {(B, T, HQ)}, got {tuple(cf.shape)}"
+        w = None
+        if weight is not None:
+            _lib.require_device(weight)
+            w = weight.detach().float().contiguous()
+        o = torch.empty(B, T, HQ, dv, device=q.device, dtype=vc.dtype)
+        y = torch.empty_like(o)
+        den = torch.empty(B, T, HQ, device=q.device, dtype=torch.float32)
+        rstd = torch.empty_like(den)
+        L = _lib.load()
+        _lib.check("linatt_kata_fwd_onorm", L.linatt_kata_fwd_onorm(
+            _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(cf), _lib.ptr(o), _lib.ptr(den),
+            _lib.ptr(w), float(eps), _lib.ptr(y), _lib.ptr(rstd), B, T, HQ, H, dk, dv, num_groups,
+            float(scale), _VARIANT[variant], _lib.dtype_code(vc.dtype), _lib.stream_of(qc)))
+        ctx.save_for_backward(qc, kc, vc, cf, o, den, rstd, w)
+        ctx.args = (num_groups, float(scale), variant)
+        ctx.dtypes = (q.dtype, k.dtype, v.dtype, c.dtype if c is not None else None,
+                      weight.dtype if weight is not None else None)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        q, k, v, cf, o, den, rstd, w = ctx.saved_tensors
+        num_groups, scale, variant = ctx.args
+        B, T, HQ, dk = q.shape
+        H, dv = k.shape[2], v.shape[-1]
+        dy = dy.to(v.dtype).contiguous()
+        dq, dk_, dv_ = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        dc = torch.empty_like(cf) if cf is not None else None
+        dw = torch.empty(dv, device=q.device, dtype=torch.float32) if w is not None else None
+        L = _lib.load()
+        ws = torch.empty(L.linatt_kata_bwd_onorm_workspace_bytes(B, T, HQ, dv, _lib.dtype_code(v.dtype)),
+                         device=q.device, dtype=torch.uint8)
+        _lib.check("linatt_kata_bwd_onorm", L.linatt_kata_bwd_onorm(
+            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(cf), _lib.ptr(o), _lib.ptr(den),
+            _lib.ptr(rstd), _lib.ptr(w), _lib.ptr(dy), _lib.ptr(dq), _lib.ptr(dk_), _lib.ptr(dv_),
+            _lib.ptr(dc), _lib.ptr(dw), _lib.ptr(ws), B, T, HQ, H, dk, dv, num_groups, scale,
+            _VARIANT[variant], _lib.dtype_code(v.dtype), _lib.stream_of(q)))
+        qd, kd, vd, cd, wd = ctx.dtypes
+        return (dq.to(qd), dk_.to(kd), dv_.to(vd), dc.to(cd) if dc is not None else None,
+                dw.to(wd) if dw is not None else None, None, None, None, None)
+
+
+def parallel_kata_attn_onorm(q, k, v, norm_weight=None, eps=1e-5, num_groups=4, scale=None,
+                             variant="concat", c=None):
+    """KATA attention followed by the mixer's output RMSNorm over each
+    ``(b, t, head)`` row of o (``kata/layer.py:456-487, 539``:
+    ``self.norm(parallel_kata_attn(...))`` with ``fla.modules.RMSNorm(head_v_dim,
+    eps=norm_eps, dtype=float32)``).  Returns ``y (B, T, HQ, dv)`` in v's
+    dtype; gradients flow to q, k, v, ``c`` (the decayed score's cumulative
+    log-decay, concat only) and ``norm_weight``.
+
+    At dk = dv = 64 in bf16 (fp16 without a gradient) the norm runs inside
+    the attention kernels: the forward's epilogue normalises each row it
+    writes, and the backward's dq pass forms the norm's gradient in
+    registers.  Elsewhere it is the attention op followed by
+    ``linatt_amd.mixer.rms_norm`` (both HIP)."""
+    if variant not in _VARIANT:
+        raise ValueError(f"variant must be 'concat' or 'sum', got {variant!r}")
+    if c is not None and variant != "concat":
+        raise NotImplementedError("decay is only defined for the concat score")
+    need_grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (q, k, v, c, norm_weight))
+    if _onorm_fused(v.dtype, q.shape[-1], v.shape[-1], need_grad):
+        return _KataONormFunction.apply(q, k, v, c, norm_weight, float(eps), num_groups, scale,
+                                        variant)
+    from .mixer import rms_norm
+    if c is not None:
+        o = parallel_kata_attn_decay(q, k, v, c, num_groups, scale)
+    elif variant == "sum":
+        o = parallel_kata_attn_sum(q, k, v, num_groups, scale)
+    else:
+        o = parallel_kata_attn(q, k, v, num_groups, scale)
+    return rms_norm(o, norm_weight, eps)

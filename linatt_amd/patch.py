@@ -32,6 +32,14 @@ Names rebound (only in modules that are importable; the rest are skipped):
 
 fla's short-sequence ``fused_recurrent_*`` ops are left alone.  ``restore()``
 puts every original back (used by the tests).
+
+``apply_mixer()`` (opt-in, not applied on import) goes one step further and
+replaces ``kata.layer.KataAttention.forward`` itself with
+``linatt_amd.kata_layer.kata_attention_forward``: the q/k chains as one fused
+kernel each, the output RMSNorm inside the attention kernels, and a real
+decode state when a cache is used (the reference's flash branch keeps none,
+``kata/layer.py:492``).  Configurations it does not cover run the original
+method.  ``restore()`` undoes it too.
 """
 
 from __future__ import annotations
@@ -39,7 +47,7 @@ from __future__ import annotations
 import importlib
 import threading
 
-__all__ = ["apply", "restore", "TARGETS"]
+__all__ = ["apply", "apply_mixer", "restore", "TARGETS"]
 
 # (module, attribute, provider module in linatt_amd, provider attribute)
 TARGETS = (
@@ -93,14 +101,45 @@ def apply() -> list[tuple[str, str]]:
     return done
 
 
+_mixer_originals: dict[type, object] = {}
+
+
+def apply_mixer() -> bool:
+    """Install the fused ``KataAttention.forward`` on ``kata.layer.KataAttention``
+    (its subclasses ``FlashKata``, ``ChunkedKata`` and ``DeltaKata`` inherit
+    it).  Returns False when ``kata.layer`` is not importable.  Idempotent;
+    ``restore()`` puts the original method back."""
+    mod = _try_import("kata.layer")
+    if mod is None or not hasattr(mod, "KataAttention"):
+        return False
+    from . import kata_layer
+    cls = mod.KataAttention
+    with _lock:
+        if cls.forward is not kata_layer.kata_attention_forward:
+            # (the class's own attribute, or None when it inherits forward)
+            _mixer_originals.setdefault(cls, cls.__dict__.get("forward"))
+            kata_layer.ORIGINAL_FORWARD[cls] = cls.forward
+            cls.forward = kata_layer.kata_attention_forward
+    return True
+
+
 def restore() -> None:
-    """Put back every attribute ``apply()`` replaced."""
+    """Put back every attribute ``apply()`` replaced and the method
+    ``apply_mixer()`` replaced."""
     with _lock:
         for (mod_name, attr), orig in list(_originals.items()):
             mod = _try_import(mod_name)
             if mod is not None:
                 setattr(mod, attr, orig)
             del _originals[(mod_name, attr)]
+        from . import kata_layer
+        for cls, orig in list(_mixer_originals.items()):
+            if orig is None:
+                del cls.forward
+            else:
+                cls.forward = orig
+            kata_layer.ORIGINAL_FORWARD.pop(cls, None)
+            del _mixer_originals[cls]
 
 
 apply()

@@ -187,3 +187,119 @@ def test_flash_delta_validates_before_launch():
     beta = _cpu(1, 8, 2, dtype=torch.float32)
     with pytest.raises(RuntimeError, match="no CPU path"):
         fd.flash_delta(q, q, q, beta, 1)
+
+
+# ---------------------------------------------------------------------------
+# the fused mixer forward (linatt_amd.patch.apply_mixer)
+# ---------------------------------------------------------------------------
+
+
+@pytest.fixture
+def mixer_hook(monkeypatch):
+    """kata.layer as a stub module whose KataAttention has the reference's
+    attribute layout, the hook installed on it, and the device ops the hook
+    calls replaced by recorders (no GPU here): each returns tensors of the
+    right shapes and logs its name."""
+    import mixer_layout
+    from linatt_amd import kata_cache, kata_layer
+
+    class KataAttention(mixer_layout.KataAttentionLayout):
+        pass
+
+    mods = {"kata": _stub("kata"), "kata.layer": _stub("kata.layer", KataAttention=KataAttention)}
+    for name, m in mods.items():
+        monkeypatch.setitem(sys.modules, name, m)
+    calls = []
+
+    def prologue(x, conv, norm, rot, head_dim, seqlen_offset=0, cache=None, output_final_state=False):
+        calls.append(("fused_qk_prologue", norm if isinstance(norm, (str, type(None))) else "rmsnorm",
+                      seqlen_offset))
+        B, T, C = x.shape
+        st = torch.zeros(B, C, conv.weight.shape[-1]) if output_final_state else None
+        return x.reshape(B, T, C // head_dim, head_dim), st
+
+    def conv(x, w, b, act, cache, out_state):
+        calls.append(("short_conv",))
+        return x, (torch.zeros(x.shape[0], x.shape[-1], w.shape[-1]) if out_state else None)
+
+    def onorm(q, k, v, w, eps, M, scale, variant, c):
+        calls.append(("parallel_kata_attn_onorm", variant, c is not None, tuple(k.shape)))
+        return torch.zeros(*q.shape[:3], v.shape[-1], dtype=v.dtype)
+
+    def cached(q, k, v, state, M, scale):
+        calls.append(("parallel_kata_attn_cached", state is not None, tuple(k.shape)))
+        off = 0 if state is None else state.offset
+        return (torch.zeros(*q.shape[:3], v.shape[-1], dtype=v.dtype),
+                kata_cache.KataState(None, None, off + q.shape[1]))
+
+    def norm(x, w, eps):
+        calls.append(("rms_norm",))
+        return x
+
+    monkeypatch.setattr(kata_layer, "fused_qk_prologue", prologue)
+    monkeypatch.setattr(kata_layer, "short_conv", conv)
+    monkeypatch.setattr(kata_layer, "parallel_kata_attn_onorm", onorm)
+    monkeypatch.setattr(kata_layer.kata_cache, "parallel_kata_attn_cached", cached)
+    monkeypatch.setattr(kata_layer, "rms_norm", norm)
+    assert patch.apply_mixer()
+    yield KataAttention, calls
+    patch.restore()
+    assert KataAttention.forward is mixer_layout.KataAttentionLayout.forward
+
+
+def test_apply_mixer_reaches_prologue_epilogue_and_cache(mixer_hook):
+    KataAttention, calls = mixer_hook
+    from linatt_amd import kata_cache, kata_layer
+    assert KataAttention.forward is kata_layer.kata_attention_forward
+    assert patch.apply_mixer()  # idempotent
+    layer = KataAttention(64, 4, 64, 4, num_kv_heads=2)
+    x = torch.randn(2, 10, 64)
+    out, _, pkv = layer(x)
+    assert out.shape == (2, 10, 64) and pkv is None and layer.original_calls == 0
+    assert [c[0] for c in calls] == ["short_conv", "fused_qk_prologue", "fused_qk_prologue",
+                                     "parallel_kata_attn_onorm"]
+    # GQA runs natively: k keeps its 2 kv heads
+    assert calls[-1] == ("parallel_kata_attn_onorm", "concat", False, (2, 10, 2, 64))
+
+    # with a cache: the state form, prefill then one decode step, the rotation
+    # offset advancing and the convolution states kept for the next call
+    # (bf16 projections, as under autocast: the state kernels are bf16)
+    calls.clear()
+    layer, x = layer.bfloat16(), x.bfloat16()
+    cache = kata_cache.LayerStateCache()
+    layer(x, past_key_values=cache, use_cache=True)
+    layer(x[:, :1], past_key_values=cache, use_cache=True)
+    names = [c[0] for c in calls]
+    assert names.count("parallel_kata_attn_cached") == 2 and names.count("rms_norm") == 2
+    assert [c for c in calls if c[0] == "parallel_kata_attn_cached"] == [
+        ("parallel_kata_attn_cached", False, (2, 10, 4, 64)),   # k repeated to the 4 heads
+        ("parallel_kata_attn_cached", True, (2, 1, 4, 64))]
+    assert [c[2] for c in calls if c[0] == "fused_qk_prologue"] == [0, 0, 10, 10]
+    assert cache.get_seq_length(0) == 11 and cache[0]["conv_state"] is not None
+    assert cache[0]["recurrent_state"].offset == 11
+
+
+@pytest.mark.parametrize("kw,expect", [
+    (dict(feature_map="kata_quadratic_sum", norm_q="l2", norm_k="l2", rope_group=True),
+     ("parallel_kata_attn_onorm", "sum", False)),
+    (dict(use_decay=True), ("parallel_kata_attn_onorm", "concat", True)),
+])
+def test_apply_mixer_variants(mixer_hook, kw, expect):
+    KataAttention, calls = mixer_hook
+    layer = KataAttention(64, 4, 64, 2, **kw)
+    layer(torch.randn(1, 5, 64))
+    assert calls[-1][:3] == expect
+    assert [c[1] for c in calls if c[0] == "fused_qk_prologue"] == (
+        ["l2", "l2"] if kw.get("norm_q") == "l2" else ["rmsnorm", "rmsnorm"])
+
+
+def test_apply_mixer_falls_back_outside_its_scope(mixer_hook):
+    KataAttention, calls = mixer_hook
+    from linatt_amd import kata_cache
+    # a psi-feature map: the reference's own forward
+    layer = KataAttention(64, 4, 64, 4, feature_map="positive")
+    assert layer(torch.randn(1, 5, 64))[0][0] == "original" and layer.original_calls == 1
+    # a cache for a score with no state form (sum): the reference's forward
+    layer = KataAttention(64, 4, 64, 4, feature_map="kata_quadratic_sum")
+    layer(torch.randn(1, 5, 64), past_key_values=kata_cache.LayerStateCache(), use_cache=True)
+    assert layer.original_calls == 1 and not calls

@@ -160,3 +160,94 @@ def test_mixer_layer_under_autocast(branch, T, M, fused):
         with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
             y_ng = layer(x)
         assert torch.equal(y_ng, y.detach())
+
+
+# ---------------------------------------------------------------------------
+# The fused KataAttention.forward installed by linatt_amd.patch.apply_mixer(),
+# on a module with the reference mixer's attribute layout
+# ---------------------------------------------------------------------------
+
+
+@pytest.fixture
+def hooked(monkeypatch):
+    import sys
+    import types
+    import mixer_layout
+    from linatt_amd import patch
+
+    class KataAttention(mixer_layout.KataAttentionLayout):
+        pass
+
+    layer_mod = types.ModuleType("kata.layer")
+    layer_mod.KataAttention = KataAttention
+    monkeypatch.setitem(sys.modules, "kata", types.ModuleType("kata"))
+    monkeypatch.setitem(sys.modules, "kata.layer", layer_mod)
+    assert patch.apply_mixer()
+    yield KataAttention
+    patch.restore()
+
+
+HOOK_CASES = {
+    "concat_M4": dict(M=4),
+    "concat_M2_gqa": dict(M=2, num_kv_heads=2),
+    "sum_M2_l2_ropegroup": dict(M=2, feature_map="kata_quadratic_sum", norm_q="l2", norm_k="l2",
+                                rope_group=True),
+    "concat_M2_decay": dict(M=2, use_decay=True),
+    "concat_M2_offset_gate": dict(M=2, use_offset_gate=True),
+}
+
+
+@pytest.mark.parametrize("case", list(HOOK_CASES))
+def test_hooked_mixer_under_autocast(hooked, case):
+    """Output and every gradient through the fused forward within 2e-2 of
+    the float64 layer."""
+    import mixer_layout
+    kw = dict(HOOK_CASES[case])
+    M = kw.pop("M")
+    torch.manual_seed(0)
+    B, T, hidden, H, D = 2, 200, 256, 4, 64
+    layer = hooked(hidden, H, D, M, **kw).to(DEV)
+    x = torch.randn(B, T, hidden, generator=torch.Generator().manual_seed(1)).to(DEV)
+    dy = torch.randn(B, T, hidden, generator=torch.Generator().manual_seed(2)).to(DEV)
+    xg = x.clone().requires_grad_(True)
+    print(f"\nhooked mixer {case}", flush=True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y, _, _ = layer(xg)
+    assert layer.original_calls == 0
+    assert y.dtype == torch.bfloat16 and y.shape == (B, T, hidden)
+    y.float().backward(dy)
+    y_ref, x_ref, P_ref = mixer_layout.layout_reference(layer, x)
+    (y_ref * dy.double().cpu()).sum().backward()
+    print(f"  y {mar(y, y_ref):.2e} dx {mar(xg.grad, x_ref.grad):.2e}", flush=True)
+    assert mar(y, y_ref) < BAR
+    assert mar(xg.grad, x_ref.grad) < BAR
+    for name, p in layer.named_parameters():
+        assert p.grad is not None, name
+        e = mar(p.grad, P_ref[name].grad)
+        print(f"  d{name} {e:.2e}", flush=True)
+        assert e < BAR, (name, e)
+
+
+@pytest.mark.parametrize("M", [4, 2])
+def test_hooked_mixer_prefill_then_decode_equals_parallel(hooked, M):
+    """Prefill 150 tokens and decode 10 more one at a time through the hook
+    with a LayerStateCache: the outputs equal the same layer's parallel
+    forward over all 160 tokens (convolution, rotation and attention states
+    carried across calls)."""
+    from linatt_amd.kata_cache import LayerStateCache
+    torch.manual_seed(3)
+    B, T, P0, hidden, H, D = 2, 160, 150, 256, 4, 64
+    layer = hooked(hidden, H, D, M).to(DEV)
+    x = torch.randn(B, T, hidden, generator=torch.Generator().manual_seed(4)).to(DEV)
+    print(f"\nhooked decode M{M}", flush=True)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        y_par, _, _ = layer(x)
+        cache = LayerStateCache()
+        outs = [layer(x[:, :P0], past_key_values=cache, use_cache=True)[0]]
+        for t in range(P0, T):
+            outs.append(layer(x[:, t:t + 1], past_key_values=cache, use_cache=True)[0])
+    y_inc = torch.cat(outs, dim=1)
+    assert layer.original_calls == 0 and cache.get_seq_length(0) == T
+    e_pre, e_dec = mar(y_inc[:, :P0], y_par[:, :P0]), mar(y_inc[:, P0:], y_par[:, P0:])
+    print(f"  prefill {e_pre:.2e} decode {e_dec:.2e}", flush=True)
+    assert e_pre < BAR and e_dec < BAR
