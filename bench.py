@@ -187,6 +187,138 @@ def bench_delta(gated, steps, warmup, settle_s, H=6, K=128):
             "frac_mfma_peak": round(tf / PEAK_BF16_TFLOPS, 4), "kernels": kern}
 
 
+def _time_parts(parts, steps, settle_s, warmup=2):
+    """Average ms per part and per step of `parts` (name, fn) launched in
+    order on the current stream, bracketed by HIP events."""
+    import torch
+    settle(parts, settle_s)
+    for _ in range(warmup):
+        for _, f in parts:
+            f()
+    stream = torch.cuda.current_stream()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(parts) + 1)]
+          for _ in range(steps)]
+    torch.cuda.synchronize()
+    for s in range(steps):
+        ev[s][0].record(stream)
+        for i, (_, f) in enumerate(parts):
+            f()
+            ev[s][i + 1].record(stream)
+    torch.cuda.synchronize()
+    per = {name: sum(ev[s][i].elapsed_time(ev[s][i + 1]) for s in range(steps)) / steps
+           for i, (name, _) in enumerate(parts)}
+    return per, sum(per.values())
+
+
+def bench_kata_variant(steps, settle_s, B, H, T, dk, dv, M, variant, decay, seed):
+    """KATA fwd + bwd through the C ABI at a trained mixer's shape: the sum
+    score (kata_quadratic_sum) or the decayed concat score at the offset-gated
+    width (dk = 128 packs two 32-wide groups padded to 64,
+    kataconv_cat_l2_gdn_340m.yaml).  The decayed backward is one call
+    (linatt_kata_bwd_decay: dq pass, then dk/dv pass)."""
+    import torch
+    from linatt_amd import _lib
+    L = _lib.load()
+    g = torch.Generator().manual_seed(seed)
+    dev = torch.device("cuda", 0)
+    q, k = ((torch.randn(B, T, H, dk, generator=g) / 8).to(torch.bfloat16).to(dev) for _ in range(2))
+    v = (torch.randn(B, T, H, dv, generator=g) / 8).to(torch.bfloat16).to(dev)
+    do = torch.randn(B, T, H, dv, generator=g).to(torch.bfloat16).to(dev)
+    c = None
+    if decay:
+        c = (-(torch.rand(B, T, H, generator=g) * 0.05)).cumsum(1).to(dev)
+    o = torch.empty_like(v)
+    den = torch.empty(B, T, H, device=dev)
+    dq, dk_, dv_ = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dc = torch.empty_like(c) if decay else None
+    ws = torch.empty(L.linatt_kata_bwd_workspace_bytes(B, T, H, dv, _lib.LINATT_BFLOAT16),
+                     device=dev, dtype=torch.uint8)
+    P, bt, sp = _lib.ptr, _lib.LINATT_BFLOAT16, _lib.stream_of(q)
+    scale = 1.0 / math.sqrt(dk // M)
+    var = 1 if variant == "sum" else 0
+
+    def fwd():
+        _lib.check("linatt_kata_fwd", L.linatt_kata_fwd(
+            P(q), P(k), P(v), P(c), P(o), P(den), B, T, H, H, dk, dv, M, scale, var, bt, sp))
+
+    def bwd():
+        if decay:
+            _lib.check("linatt_kata_bwd_decay", L.linatt_kata_bwd_decay(
+                P(q), P(k), P(v), P(c), P(o), P(den), P(do), P(dq), P(dk_), P(dv_), P(dc), P(ws),
+                B, T, H, H, dk, dv, M, scale, bt, sp))
+        else:
+            _lib.check("linatt_kata_bwd", L.linatt_kata_bwd(
+                P(q), P(k), P(v), P(o), P(den), P(do), P(dq), P(dk_), P(dv_), P(ws),
+                B, T, H, H, dk, dv, M, scale, var, bt, sp))
+
+    per, ms = _time_parts([("fwd", fwd), ("bwd", bwd)], steps, settle_s)
+    fl = kata_flops(B, H, T, dk, dv, M, variant)
+    out = {"config": {"B": B, "H": H, "T": T, "dk": dk, "dv": dv, "num_groups": M,
+                      "variant": variant, "decay": decay, "dtype": "bf16", "seed": seed},
+           "fwd_ms": round(per["fwd"], 4), "bwd_ms": round(per["bwd"], 4), "ms": round(ms, 4),
+           "tokens_per_s": round(B * T / (ms * 1e-3), 1), "alg_gflop": round(fl["total"] / 1e9, 2)}
+    out["tflops"] = round(fl["total"] / (ms * 1e-3) / 1e12, 1)
+    out["frac_mfma_peak"] = round(out["tflops"] / PEAK_BF16_TFLOPS, 4)
+    out["fwd_frac_mfma_peak"] = round(fl["fwd"] / (per["fwd"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)
+    out["bwd_frac_mfma_peak"] = round((fl["bwd_dq"] + fl["bwd_dkdv"]) / (per["bwd"] * 1e-3) / 1e12
+                                      / PEAK_BF16_TFLOPS, 4)
+    return out
+
+
+def bench_kata_onorm(steps, settle_s, M=4):
+    """The mixer's output RMSNorm fused into the KATA kernels against the
+    two-step chain (KATA, then the RMSNorm kernels) at config 2 (B8 H12
+    T2048 D64, bf16): forward y and backward dq, dk, dv, dnorm_weight."""
+    import torch
+    from linatt_amd import _lib
+    L = _lib.load()
+    B, H, T, D = 8, 12, 2048, 64
+    g = torch.Generator().manual_seed(8)
+    dev = torch.device("cuda", 0)
+    q, k, v = ((torch.randn(B, T, H, D, generator=g) / 8).to(torch.bfloat16).to(dev) for _ in range(3))
+    dy = torch.randn(B, T, H, D, generator=g).to(torch.bfloat16).to(dev)
+    w = (0.75 + 0.5 * torch.rand(D, generator=g)).to(dev)
+    o, y, dO, dq, dk, dv = (torch.empty_like(q) for _ in range(6))
+    den, rstd = (torch.empty(B, T, H, device=dev) for _ in range(2))
+    dw = torch.empty(D, device=dev)
+    bt = _lib.LINATT_BFLOAT16
+    n = B * T * H
+    ws = torch.empty(L.linatt_kata_bwd_onorm_workspace_bytes(B, T, H, D, bt), device=dev, dtype=torch.uint8)
+    rws = torch.empty(L.linatt_rmsnorm_bwd_workspace_bytes(n, D), device=dev, dtype=torch.uint8)
+    P, sp, scale = _lib.ptr, _lib.stream_of(q), 1.0 / math.sqrt(D // M)
+
+    def f_fwd():
+        _lib.check("linatt_kata_fwd_onorm", L.linatt_kata_fwd_onorm(
+            P(q), P(k), P(v), None, P(o), P(den), P(w), 1e-5, P(y), P(rstd), B, T, H, H, D, D, M,
+            scale, 0, bt, sp))
+
+    def f_bwd():
+        _lib.check("linatt_kata_bwd_onorm", L.linatt_kata_bwd_onorm(
+            P(q), P(k), P(v), None, P(o), P(den), P(rstd), P(w), P(dy), P(dq), P(dk), P(dv), None,
+            P(dw), P(ws), B, T, H, H, D, D, M, scale, 0, bt, sp))
+
+    def u_fwd():
+        _lib.check("linatt_kata_fwd", L.linatt_kata_fwd(
+            P(q), P(k), P(v), None, P(o), P(den), B, T, H, H, D, D, M, scale, 0, bt, sp))
+        _lib.check("linatt_rmsnorm_fwd", L.linatt_rmsnorm_fwd(
+            P(o), P(w), P(y), P(rstd), n, D, 1e-5, bt, sp))
+
+    def u_bwd():
+        _lib.check("linatt_rmsnorm_bwd", L.linatt_rmsnorm_bwd(
+            P(o), P(w), P(rstd), P(dy), P(dO), P(dw), P(rws), n, D, bt, sp))
+        _lib.check("linatt_kata_bwd", L.linatt_kata_bwd(
+            P(q), P(k), P(v), P(o), P(den), P(dO), P(dq), P(dk), P(dv), P(ws),
+            B, T, H, H, D, D, M, scale, 0, bt, sp))
+
+    pf, msf = _time_parts([("fwd", f_fwd), ("bwd", f_bwd)], steps, settle_s)
+    pu, msu = _time_parts([("fwd", u_fwd), ("bwd", u_bwd)], steps, settle_s / 2)
+    return {"config": {"B": B, "H": H, "T": T, "D": D, "num_groups": M, "dtype": "bf16", "seed": 8},
+            "fused_fwd_ms": round(pf["fwd"], 4), "fused_bwd_ms": round(pf["bwd"], 4),
+            "fused_ms": round(msf, 4), "unfused_fwd_ms": round(pu["fwd"], 4),
+            "unfused_bwd_ms": round(pu["bwd"], 4), "unfused_ms": round(msu, 4),
+            "speedup": round(msu / msf, 3)}
+
+
 def bench_delta_kata(steps, settle_s):
     """The SPD delta rule (DeltaKata, kata/spd/flash_delta.py:1060-1116)
     forward (the training variant, which keeps what the backward reads) and
@@ -719,6 +851,17 @@ def main():
     delta_kata = None if args.no_delta else bench_delta_kata(max(3, args.steps // 2),
                                                              args.settle_seconds / 3)
     mixer = bench_mixer(max(5, args.steps), args.settle_seconds / 3)
+    vs = max(5, args.steps // 2)
+    variants = {
+        # kata_quadratic_sum_m4_200m.yaml: 12 heads of 64, four groups
+        "sum_m4_h12_d64": bench_kata_variant(vs, args.settle_seconds / 3, 8, 12, 2048, 64, 64, 4,
+                                             "sum", False, 9),
+        # kataconv_cat_l2_gdn_340m.yaml: 16 heads, decayed concat score over
+        # offset-packed groups (dk = 128, dv = 64, two groups)
+        "decay_m2_h16_dk128": bench_kata_variant(vs, args.settle_seconds / 3, 8, 16, 2048, 128, 64,
+                                                 2, "concat", True, 10),
+    }
+    onorm = bench_kata_onorm(vs, args.settle_seconds / 3, M)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -759,6 +902,8 @@ def main():
         "kata_config1": config1,
         "delta_kata_fwd_bwd": delta_kata,
         "mixer_ops": mixer,
+        "kata_variants": variants,
+        "kata_output_norm_config2": onorm,
     }
     print(json.dumps(out), flush=True)
 

@@ -118,6 +118,16 @@ int linatt_kata_fwd_onorm(const void* q, const void* k, const void* v, const flo
                           int B, int T, int HQ, int H, int dk, int dv, int num_groups, float scale,
                           int variant, int dtype, void* stream);
 
+/* KATA forward's unnormalised numerator in float32:
+ *   num (B,T,HQ,dv) float32 = sum_{s<=t} A[t,s] v_s  (= o * den, unrounded),
+ *   den (B,T,HQ) float32 as linatt_kata_fwd.
+ * Replaces the SPD delta rule's readout, whose kernel keeps its float32
+ * accumulator (_readout_kernel, kata/spd/flash_delta.py:975-985, with the
+ * sum score).  dk = dv = 64 in bfloat16 or float16. */
+int linatt_kata_fwd_num(const void* q, const void* k, const void* v, float* num, float* den,
+                        int B, int T, int HQ, int H, int dk, int dv, int num_groups, float scale,
+                        int variant, int dtype, void* stream);
+
 /* Bytes of workspace linatt_kata_bwd_onorm needs: linatt_kata_bwd's, then
  * per-workgroup partials of the norm-weight gradient. */
 size_t linatt_kata_bwd_onorm_workspace_bytes(int B, int T, int HQ, int dv_dim, int dtype);

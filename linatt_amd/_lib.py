@@ -46,6 +46,7 @@ SIGNATURES = {
     "linatt_noalloc_scratch_bytes": (_sz, []),
     "linatt_kata_fwd_onorm": (_i, [_vp] * 7 + [_f, _vp, _vp] + [_i] * 7 + [_f, _i, _i, _vp]),
     "linatt_kata_bwd_onorm_workspace_bytes": (_sz, [_i] * 5),
+    "linatt_kata_fwd_num": (_i, [_vp] * 5 + [_i] * 7 + [_f, _i, _i, _vp]),
     "linatt_kata_bwd_onorm": (_i, [_vp] * 15 + [_i] * 7 + [_f, _i, _i, _vp]),
     "linatt_delta_supported": (_i, [_i, _i, _i]),
     "linatt_delta_ctx_bytes": (_sz, [_i] * 6),

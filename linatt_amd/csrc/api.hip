@@ -360,6 +360,31 @@ int linatt_kata_fwd_onorm(const void* q, const void* k, const void* v, const flo
   return LINATT_OK;
 }
 
+int linatt_kata_fwd_num(const void* q, const void* k, const void* v, float* num, float* den,
+                        int B, int T, int HQ, int H, int dk, int dv, int num_groups, float scale,
+                        int variant, int dtype, void* stream) {
+  g_last_error.clear();
+  const char* fn = "linatt_kata_fwd_num";
+  int st = check_common(B, T, HQ, H, dk, dv, num_groups, scale, variant, dtype);
+  if (st) return st;
+  if (dk != 64 || dv != 64 || dtype == LINATT_FLOAT32)
+    return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": runs at dk = dv = 64 in bfloat16 or float16");
+  if (!q || !k || !v || !num || !den) return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(num))
+    return fail(LINATT_EINVAL, std::string(fn) + ": q, k, v, num must be 16-byte aligned");
+  KataArgs a{};
+  a.q = q; a.k = k; a.v = v; a.num32 = num; a.den = den;
+  a.B = B; a.T = T; a.HQ = HQ; a.H = H; a.DK = dk; a.DV = dv; a.M = num_groups; a.scale = scale;
+  bool found = false;
+  hipError_t e = dispatch_fwd(a, dtype, variant, false, (hipStream_t)stream, &found);
+  if (!found)
+    return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": no kernel compiled for " +
+                                         shape_str(B, T, HQ, H, dk, dv, num_groups));
+  if (e != hipSuccess)
+    return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
 size_t linatt_kata_bwd_onorm_workspace_bytes(int B, int T, int HQ, int dv_dim, int dtype) {
   if (B <= 0 || T <= 0 || HQ <= 0 || dv_dim <= 0) return 0;
   const size_t nblk = (size_t)B * HQ * ((T + 127) / 128);

@@ -45,7 +45,6 @@ DKataLayout dkata_layout(int B, int T, int H, int D, int DV, int eb) {
   L.TmLo = take(BH * NC * 4096 * eb);
   L.UT = take(BH * DV * Tp * eb);
   L.Ub = take((size_t)B * T * H * DV * eb);
-  L.Ob = take((size_t)B * T * H * DV * eb);
   L.Ein = take((size_t)B * T * H * DV * 4);
   L.bytes = off;
   return L;
@@ -540,21 +539,18 @@ __global__ __launch_bounds__(256) void dkata_ext_kernel(const T* __restrict__ k,
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 3: o = num (/ (den + eps)) from the readout's o_k = num / den_k and
-// den_k (the KATA forward leaves o_k = num where den_k = 0, num = 0 there).
+// Kernel 3 (normalize only): o = num / (den + eps) in place, from the
+// readout's float32 numerator and den.
 // ---------------------------------------------------------------------------
-template <typename T>
 __global__ __launch_bounds__(256) void dkata_finish_kernel(DKataArgs a, int DV) {
   const int64_t rows = (int64_t)a.B * a.T * a.H;
   const int64_t n4 = rows * DV / 4;
-  const T* ob = (const T*)(a.ws + a.L.Ob);
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
     const int64_t row = 4 * i / DV;
-    const float d = a.den[row];
-    const float f = a.normalize ? d / (d + a.eps) : d;
-    const v4_t<T> x = ld4<T>(ob + 4 * i);
-    *reinterpret_cast<float4*>(a.o + 4 * i) =
-        make_float4((float)x[0] * f, (float)x[1] * f, (float)x[2] * f, (float)x[3] * f);
+    const float f = 1.f / (a.den[row] + a.eps);
+    float4 x = *reinterpret_cast<const float4*>(a.o + 4 * i);
+    x.x *= f; x.y *= f; x.z *= f; x.w *= f;
+    *reinterpret_cast<float4*>(a.o + 4 * i) = x;
   }
 }
 
@@ -577,17 +573,18 @@ hipError_t launch_dkata_fwd(const DKataArgs& a, hipStream_t stream) {
     dkata_U_kernel<T, D, DV, M><<<dim3(BH), dim3(256), 0, stream>>>(a, cb, ce);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  // readout: the KATA sum-score forward of (q, k, U) with the same scale
+  // readout: the KATA sum-score forward of (q, k, U) with the same scale,
+  // its float32 numerator straight into o (no 16-bit rounding of o)
   KataArgs r{};
   r.q = a.q; r.k = a.k; r.v = a.ws + a.L.Ub; r.c = nullptr;
-  r.o = a.ws + a.L.Ob; r.den = a.den;
+  r.o = nullptr; r.num32 = a.o; r.den = a.den;
   r.B = a.B; r.T = a.T; r.HQ = a.H; r.H = a.H; r.DK = D; r.DV = DV; r.M = M;
   r.scale = a.scale;
   e = launch_kata_fwd<T, D, DV, M, true, false>(r, stream);
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || !a.normalize) return e;
   const int64_t n4 = (int64_t)a.B * a.T * a.H * DV / 4;
   const int blocks = (int)((n4 + 255) / 256 < 4096 ? (n4 + 255) / 256 : 4096);
-  dkata_finish_kernel<T><<<dim3(blocks), dim3(256), 0, stream>>>(a, DV);
+  dkata_finish_kernel<<<dim3(blocks), dim3(256), 0, stream>>>(a, DV);
   return hipGetLastError();
 }
 

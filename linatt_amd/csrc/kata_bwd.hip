@@ -439,8 +439,10 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
 // Q^T for dK, dO^T for dV) come from transposing LDS reads.  Rows past T
 // repeat the last valid row; every use of them is masked.
 // ---------------------------------------------------------------------------
-template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
-__global__ __launch_bounds__(256, (SUM || DECAY) ? 2 : 3) void kata_bwd_dq_tile_kernel(
+// ONORM: dy replaces dO, and the output RMSNorm's backward runs in the
+// prologue (compile-time, so the plain kernel carries none of it)
+template <typename T, int DK, int DV, int M, bool SUM, bool DECAY, bool ONORM>
+__global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ o, const float* __restrict__ den, const T* __restrict__ dout,
     T* __restrict__ dq, float* __restrict__ delta_out, const float* __restrict__ c,
@@ -487,14 +489,14 @@ __global__ __launch_bounds__(256, (SUM || DECAY) ? 2 : 3) void kata_bwd_dq_tile_
   float dpart = 0.f, dppart = 0.f;
   // this lane's dims 16 kk + 8 hh + 0..7 of dO (or of dy) and of o
   v8_t<T> ov[DV / 16];
-  const T* dsrc = on.y ? (const T*)on.y : dout;
+  const T* dsrc = ONORM ? (const T*)on.y : dout;
 #pragma unroll
   for (int kk = 0; kk < DV / 16; ++kk) {
     doop[kk] = tvalid ? ld8<T>(dsrc + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
     ov[kk] = tvalid ? ld8<T>(o + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
   }
-  if (on.y) {
-    // output RMSNorm backward (uniform branch), y = o r w with r = rstd:
+  if constexpr (ONORM) {
+    // output RMSNorm backward, y = o r w with r = rstd:
     // dO = r w dy - (r^3 / DV) <o, w dy> o, rounded to T as the unfused
     // norm's dx is; the weight gradient sum_rows dy o r goes to this
     // workgroup's partial (summed over the wave's 32 rows by DPP, eight dims
@@ -764,7 +766,7 @@ __global__ __launch_bounds__(256, (SUM || DECAY) ? 2 : 3) void kata_bwd_dq_tile_
   }
   // output-norm weight gradient: this workgroup's partial, the four waves'
   // row sums added in a fixed order (every wave reaches this barrier)
-  if (on.part) {
+  if (ONORM && on.part) {
     __syncthreads();
     if (tid < DV)
       on.part[((int64_t)bh * nqt + qt) * DV + tid] = (Wred[0][tid] + Wred[1][tid]) + (Wred[2][tid] + Wred[3][tid]);
@@ -1100,10 +1102,19 @@ hipError_t launch_kata_bwd(const KataArgs& a, int parts, hipStream_t stream) {
     if (parts & KATA_BWD_DQ) {
       const int nbh = a.B * a.HQ;
       if constexpr (kTiles)
-        kata_bwd_dq_tile_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbh), dim3(256), 0, stream>>>(
-            (const T*)a.q, (const T*)a.k, (const T*)a.v, (const T*)a.o, a.den, (const T*)a.dout,
-            (T*)a.dq, a.delta, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt, nbh,
-            OutNorm{a.nw, const_cast<void*>(a.dy), a.rstd, a.nw_part, a.eps});
+      {
+        const OutNorm on{a.nw, const_cast<void*>(a.dy), a.rstd, a.nw_part, a.eps, nullptr};
+        auto go = [&](auto onorm) {
+          kata_bwd_dq_tile_kernel<T, DK, DV, M, SUM, DECAY, decltype(onorm)::value>
+              <<<dim3(nqt * nbh), dim3(256), 0, stream>>>(
+                  (const T*)a.q, (const T*)a.k, (const T*)a.v, (const T*)a.o, a.den,
+                  (const T*)a.dout, (T*)a.dq, a.delta, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt,
+                  nbh, on);
+        };
+        if (!a.dy) go(BoolC<false>{});
+        else if constexpr (__is_same(T, __bf16)) go(BoolC<true>{});  // (the API admits bf16 only)
+        else return hipErrorInvalidValue;
+      }
       else if (a.dy)
         return hipErrorInvalidValue;  // the output norm is fused in the tile kernel only
       else

@@ -198,7 +198,10 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_fwd_kernel(
 // unrolled over the ring so every LDS operand address is a per-lane offset
 // fixed for the kernel plus an immediate, and full tiles are copied from a
 // scalar base: the VALU, which bounds this kernel, only does the math.
-template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
+// EPI: 0 writes o; 1 also the output RMSNorm's y and rstd; 2 the float32
+// numerator o den instead of o (compile-time, so each variant carries only
+// its own epilogue)
+template <typename T, int DK, int DV, int M, bool SUM, bool DECAY, int EPI>
 __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const float* __restrict__ c, T* __restrict__ o, float* __restrict__ den,
@@ -459,16 +462,29 @@ __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
                          oacc[db][4 * i + 2] * inv, oacc[db][4 * i + 3] * inv);
   const int64_t row = ((int64_t)b * Tn + tl) * HQ + hq;
   if (tl < Tn) {
-    T* orow = o + row * DV;
+    if constexpr (EPI == 2) {
+      // float32 numerator o den = oacc scale^2 / pe, unrounded
+      const float f = scale2 / pe;
+      float* nrow = on.num + row * DV;
 #pragma unroll
-    for (int db = 0; db < DV / 32; ++db)
+      for (int db = 0; db < DV / 32; ++db)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) st4<T>(orow + 32 * db + 8 * i + 4 * hh, ov[db][i]);
+        for (int i = 0; i < 4; ++i)
+          *reinterpret_cast<f32x4*>(nrow + 32 * db + 8 * i + 4 * hh) =
+              f32x4{oacc[db][4 * i] * f, oacc[db][4 * i + 1] * f, oacc[db][4 * i + 2] * f,
+                    oacc[db][4 * i + 3] * f};
+    } else {
+      T* orow = o + row * DV;
+#pragma unroll
+      for (int db = 0; db < DV / 32; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st4<T>(orow + 32 * db + 8 * i + 4 * hh, ov[db][i]);
+    }
     if (hh == 0) den[row] = dsum * (scale2 / pe);
   }
   // output RMSNorm (uniform branch): y = o rsqrt(mean(o^2) + eps) w over the
   // row of the stored (rounded) o, whose two halves are lanes l and l ^ 32
-  if (on.y) {
+  if constexpr (EPI == 1) {
     float ss = 0.f;
 #pragma unroll
     for (int db = 0; db < DV / 32; ++db)
@@ -505,12 +521,19 @@ hipError_t launch_kata_fwd(const KataArgs& a, hipStream_t stream) {
     const int nbh = a.B * a.HQ;
     dim3 grid(nqt * nbh), block(256);
     if constexpr (sizeof(T) == 2 && DK == 64 && DV == 64) {
-      const OutNorm on{a.nw, a.y, a.rstd, nullptr, a.eps};
-      kata_fwd_tile_kernel<T, DK, DV, M, SUM, DECAY><<<grid, block, 0, stream>>>(
-          (const T*)a.q, (const T*)a.k, (const T*)a.v, a.c, (T*)a.o, a.den, a.T, a.HQ, a.H,
-          a.scale * a.scale, nqt, nbh, on);
+      const OutNorm on{a.nw, a.y, a.rstd, nullptr, a.eps, a.num32};
+      auto go = [&](auto epi) {
+        kata_fwd_tile_kernel<T, DK, DV, M, SUM, DECAY, decltype(epi)::value><<<grid, block, 0, stream>>>(
+            (const T*)a.q, (const T*)a.k, (const T*)a.v, a.c, (T*)a.o, a.den, a.T, a.HQ, a.H,
+            a.scale * a.scale, nqt, nbh, on);
+      };
+      if (a.y && a.num32) return hipErrorInvalidValue;
+      if (a.y) go(IntC<1>{});
+      else if (a.num32) go(IntC<2>{});
+      else go(IntC<0>{});
     } else {
-      if (a.y) return hipErrorInvalidValue;  // the output norm is fused in the tile kernel only
+      // the output norm and the float32 numerator are tile-kernel options
+      if (a.y || a.num32) return hipErrorInvalidValue;
       kata_fwd_kernel<T, DK, DV, M, SUM, DECAY><<<grid, block, 0, stream>>>(
           (const T*)a.q, (const T*)a.k, (const T*)a.v, a.c, (T*)a.o, a.den, a.T, a.HQ, a.H,
           a.scale * a.scale, nqt, nbh);

@@ -37,6 +37,10 @@ struct KataArgs {
   float eps;
   const void* dy;    // (B, T, HQ, DV) gradient of y, or null
   float* nw_part;    // (nqt B HQ, DV) per-workgroup weight-gradient partials (dq pass)
+  // forward, 16-bit 64 x 64 tile kernels: when set, the unnormalised
+  // numerator num = o den = sum_s A[t,s] v_s is written here in float32
+  // instead of o (o may then be null)
+  float* num32;
 };
 
 // The output-norm arguments of the tile kernels (a kernel argument struct).
@@ -46,6 +50,7 @@ struct OutNorm {
   float* rstd;
   float* part;    // backward: weight-gradient partials, or null
   float eps;
+  float* num;     // forward: float32 numerator instead of o, or null
 };
 
 template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
@@ -135,7 +140,6 @@ struct DKataLayout {
   size_t TmHi, TmLo;  // (B*H, NC, 64, 64) T: Tm = (I + N)^-1 per chunk, hi + lo
   size_t UT;          // (B*H, DV, 64 NC) T: U^T
   size_t Ub;          // (B, T, H, DV) T: U for the readout
-  size_t Ob;          // (B, T, H, DV) T: readout num / den
   size_t Ein;         // (B, T, H, DV) f32: sum over earlier chunks of kappa(k_t, k_j) U_j
   size_t bytes;
 };

@@ -105,7 +105,8 @@ class _FlashDelta(torch.autograd.Function):
                 f"converted); got {q.dtype}")
         o, U, den, ws, (qc, kc, vc, bc) = _run(q, k, v, beta, M, scale, normalize, eps, False,
                                                 train=True)
-        ctx.save_for_backward(qc, kc, vc, bc, U, o, den, ws)
+        # o is read back only when normalize (its z = <do', o> term)
+        ctx.save_for_backward(qc, kc, vc, bc, U, o if normalize else None, den, ws)
         ctx.M, ctx.scale, ctx.normalize, ctx.eps = M, scale, normalize, eps
         return o
 
@@ -158,8 +159,19 @@ def flash_delta_den(q, k, M, scale=None, C=64, BM=128):
 def flash_delta_readout(q, k, U, M, scale=None, C=64, BM=128):
     """``num = lower(kappa(q, k)) U``, float32 ``(B, T, H, DV)``
     (``kata/spd/flash_delta.py:975-985``): the KATA sum-score forward of
-    ``(q, k, U)`` gives ``num / den`` and ``den``.  ``U`` is rounded to q's
-    dtype for the product."""
-    D = q.shape[-1]
-    o, den = _kata_fwd(q, k, U.to(q.dtype), M, _scale(D, M, scale), "sum")
-    return o.float() * den[..., None]
+    ``(q, k, U)`` with its float32 accumulator written out
+    (``linatt_kata_fwd_num``).  ``U`` is rounded to q's dtype for the
+    product, as the reference's kernel loads it."""
+    _lib.require_device(q, k, U)
+    B, T, H, D = q.shape
+    DV = U.shape[-1]
+    qc, kc = q.contiguous(), k.to(q.dtype).contiguous()
+    Uc = U.to(q.dtype).contiguous()
+    num = torch.empty(B, T, H, DV, device=q.device, dtype=torch.float32)
+    den = torch.empty(B, T, H, device=q.device, dtype=torch.float32)
+    L = _lib.load()
+    _lib.check("linatt_kata_fwd_num", L.linatt_kata_fwd_num(
+        _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(Uc), _lib.ptr(num), _lib.ptr(den), B, T, H, H, D, DV,
+        M, _scale(D, M, scale), _lib.LINATT_KATA_SUM, _lib.dtype_code(q.dtype),
+        _lib.stream_of(q)))
+    return num

@@ -323,3 +323,29 @@ def test_unsupported_shape_raises(F):
     q32, k32, v32 = (x.float() for x in dev(*make(1, 8, 1, 64, 64, torch.bfloat16, 1)[:3]))
     with pytest.raises((NotImplementedError, TypeError)):
         F.flash_delta(q32, k32, v32, beta, 1)
+
+
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_readout_keeps_float32_accumulator(F, M):
+    """The readout as the reference's kernel computes it
+    (``kata/spd/flash_delta.py:915-972``): A_qk and U rounded to bf16, the
+    products summed in float32 and stored unrounded.  Against that
+    computation in float64 (same roundings), the HIP readout is within
+    1e-3 (measured at most 3.5e-4): only the fp32 sum order and an
+    occasional one-ulp difference in a rounded A_qk element remain (no
+    16-bit rounding of the result)."""
+    B, T, H = 2, 300, 2
+    q, k, v, beta = make(B, T, H, 64, 64, torch.bfloat16, 40 + M)
+    qd, kd, vd, bd = dev(q, k, v, beta)
+    U = F.flash_delta_U(qd, kd, vd, bd, M, scale=0.5)
+    num = F.flash_delta_readout(qd, kd, U, M, scale=0.5)
+    A = torch.tril(DK.kappa_gram(q.double(), k.double(), M, 0.5))      # (B, H, T, T)
+    A16 = A.float().bfloat16().double()
+    U16 = U.cpu().bfloat16().double().transpose(1, 2)                  # (B, H, T, DV)
+    ref = (A16 @ U16).transpose(1, 2)
+    e = mar(num, ref)
+    print(f"\nreadout M={M}: {e:.2e} against the reference's roundings", flush=True)
+    assert e < 1e-3
+    # the training forward's output is that readout of its own U: num itself
+    o = F.flash_delta(qd, kd, vd, bd, M, scale=0.5)
+    assert mar(o, num) < 2e-3
