@@ -230,6 +230,45 @@ int linatt_delta_bwd_stages(const void* q, const void* k, const void* v, const f
  * z = sum_s psi(sqrt(scale) k_s) (B,H,M*E^2) float32.
  * ------------------------------------------------------------------------- */
 
+/* State form of every flash score, for decoding (no reference counterpart:
+ * the reference's flash branch keeps no state, kata/layer.py:492).  Features
+ *   concat (variant 0): psi(x)_p = scale x[gE+a] x[gE+b],  p = g E^2 + a E + b,
+ *                       P = num_groups E^2  (kata/parallel_kata_attn.py:49-75)
+ *   sum (variant 1):    psi(x)_p = scale sum_g x[gE+a] x[gE+b],  p = a E + b,
+ *                       P = E^2  (the sum score, :539-576)
+ * with E = dk / num_groups a power of two >= 16, dk <= 128, dv = 64; state
+ * S (B,H,P,64) and z (B,H,P) float32.  c is the cumulative log-decay of the
+ * decayed score (:291-310) within the call (each call's c starts from the
+ * stored state at 0), non-increasing; NULL for no decay.
+ *   S_t = e^(c_t - c_{t-1}) S_{t-1} + psi(k_t) v_t^T,  z likewise,
+ *   o_t = psi(q_t)^T S_t / max(psi(q_t) . z_t, eps). */
+
+/* Rows P of the state for (dk, num_groups, variant); 0 on bad arguments. */
+int linatt_kata_gen_state_rows(int dk, int num_groups, int variant);
+
+/* One decode step per (b, h): q, k (B,H,dk), v, o (B,H,64) [dtype]; c (B,H)
+ * float32 the step's log-decay or NULL; S, z updated in place. */
+int linatt_kata_gen_decode(const void* q, const void* k, const void* v, const float* c, float* S,
+                           float* z, void* o, int B, int H, int dk, int dv, int num_groups,
+                           int variant, float scale, float eps, int dtype, void* stream);
+
+/* A prefill continued from a state: o (B,T,H,64) [dtype] and den (B,T,H)
+ * float32 hold the flash forward (linatt_kata_fwd) over the call's tokens on
+ * entry; on return o = (o den + e^{c_t} psi(q_t)^T S) / max(den', eps) with
+ * den' = den + e^{c_t} psi(q_t) . z, and den = max(den', eps).  q (B,T,H,dk);
+ * c (B,T,H) or NULL; S, z are read only. */
+int linatt_kata_gen_readout(const void* q, const float* c, const float* S, const float* z,
+                            void* o, float* den, int B, int T, int H, int dk, int dv,
+                            int num_groups, int variant, float scale, float eps, int dtype,
+                            void* stream);
+
+/* The state after the call's tokens: S <- (init ? e^{c_T} S : 0) +
+ * sum_s e^{c_T - c_s} psi(k_s) v_s^T, z likewise; k (B,T,H,dk), v (B,T,H,64),
+ * c (B,T,H) or NULL; S, z updated in place. */
+int linatt_kata_gen_update(const void* k, const void* v, const float* c, float* S, float* z,
+                           int init, int B, int T, int H, int dk, int dv, int num_groups,
+                           int variant, float scale, int dtype, void* stream);
+
 /* 1 if the state-form kernels are compiled for the combination, else 0. */
 int linatt_kata_state_supported(int dtype, int dk, int dv, int num_groups);
 

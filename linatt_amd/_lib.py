@@ -58,6 +58,10 @@ SIGNATURES = {
     "linatt_l2norm_fwd": (_i, [_vp, _vp, _vp, _i, _i, _f, _i, _vp]),
     "linatt_l2norm_bwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "linatt_kata_state_supported": (_i, [_i, _i, _i, _i]),
+    "linatt_kata_gen_state_rows": (_i, [_i, _i, _i]),
+    "linatt_kata_gen_decode": (_i, [_vp] * 7 + [_i] * 6 + [_f, _f, _i, _vp]),
+    "linatt_kata_gen_readout": (_i, [_vp] * 6 + [_i] * 7 + [_f, _f, _i, _vp]),
+    "linatt_kata_gen_update": (_i, [_vp] * 5 + [_i] * 8 + [_f, _i, _vp]),
     "linatt_kata_prefill_workspace_bytes": (_sz, [_i] * 8),
     "linatt_kata_prefill": (_i, [_vp] * 8 + [_i] * 6 + [_f, _f, _i, _i, _i, _vp]),
     "linatt_kata_prefill_state": (_i, [_vp] * 10 + [_i] * 6 + [_f, _f, _i, _i, _i, _vp]),

@@ -1023,4 +1023,87 @@ int linatt_kata_decode_step(const void* q, const void* k, const void* v, float* 
   return LINATT_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Generic state form (kata_state_gen.hip)
+// ---------------------------------------------------------------------------
+static int gen_state_args(const char* fn, KataGenStateArgs& a, int B, int T, int H, int dk, int dv,
+                          int M, int variant, float scale, float eps, int dtype) {
+  if (B <= 0 || T <= 0 || H <= 0 || dk <= 0 || dv <= 0 || M <= 0)
+    return fail(LINATT_EINVAL, std::string(fn) + ": non-positive dimension");
+  if (variant != LINATT_KATA_CONCAT && variant != LINATT_KATA_SUM)
+    return fail(LINATT_EINVAL, std::string(fn) + ": unknown KATA variant");
+  if (!known_dtype(dtype)) return fail(LINATT_EINVAL, std::string(fn) + ": unknown dtype");
+  if (!(scale > 0.f) || !(eps > 0.f)) return fail(LINATT_EINVAL, std::string(fn) + ": scale and eps must be positive");
+  if (dk % M) return fail(LINATT_EINVAL, std::string(fn) + ": dk not divisible by num_groups");
+  const int E = dk / M;
+  if (dv != 64 || dk > 128 || E < 16 || !pow2(E))
+    return fail(LINATT_EUNSUPPORTED, std::string(fn) + ": needs dv = 64, dk <= 128 and a group width "
+                                     "E = dk / num_groups that is a power of two >= 16");
+  if ((int64_t)B * T * H > (int64_t)INT32_MAX / 64)
+    return fail(LINATT_EINVAL, std::string(fn) + ": B*T*H too large");
+  int lgE = 0;
+  while ((1 << lgE) < E) ++lgE;
+  a.B = B; a.T = T; a.H = H; a.dk = dk; a.E = E; a.lgE = lgE; a.M = M;
+  a.sum = variant == LINATT_KATA_SUM ? 1 : 0;
+  a.P = a.sum ? E * E : M * E * E;
+  a.scale = scale; a.eps = eps;
+  return LINATT_OK;
+}
+
+static int gen_state_launch(const char* fn, const KataGenStateArgs& a, int which, int dtype, void* stream) {
+  hipError_t e = by_dtype(dtype, [&](auto t) { return launch_kata_gen_state<decltype(t)>(a, which, (hipStream_t)stream); });
+  if (e != hipSuccess) return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
+  return LINATT_OK;
+}
+
+int linatt_kata_gen_state_rows(int dk, int num_groups, int variant) {
+  if (dk <= 0 || num_groups <= 0 || dk % num_groups) return 0;
+  const int E = dk / num_groups;
+  return variant == LINATT_KATA_SUM ? E * E : num_groups * E * E;
+}
+
+int linatt_kata_gen_decode(const void* q, const void* k, const void* v, const float* c, float* S,
+                           float* z, void* o, int B, int H, int dk, int dv, int num_groups,
+                           int variant, float scale, float eps, int dtype, void* stream) {
+  g_last_error.clear();
+  const char* fn = "linatt_kata_gen_decode";
+  KataGenStateArgs a{};
+  int st = gen_state_args(fn, a, B, 1, H, dk, dv, num_groups, variant, scale, eps, dtype);
+  if (st) return st;
+  if (!q || !k || !v || !S || !z || !o) return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  if (!aligned16(S) || !aligned16(o)) return fail(LINATT_EINVAL, std::string(fn) + ": S and o must be 16-byte aligned");
+  a.q = q; a.k = k; a.v = v; a.c = c; a.S = S; a.z = z; a.o = o;
+  return gen_state_launch(fn, a, KATA_GEN_DECODE, dtype, stream);
+}
+
+int linatt_kata_gen_readout(const void* q, const float* c, const float* S, const float* z,
+                            void* o, float* den, int B, int T, int H, int dk, int dv,
+                            int num_groups, int variant, float scale, float eps, int dtype,
+                            void* stream) {
+  g_last_error.clear();
+  const char* fn = "linatt_kata_gen_readout";
+  KataGenStateArgs a{};
+  int st = gen_state_args(fn, a, B, T, H, dk, dv, num_groups, variant, scale, eps, dtype);
+  if (st) return st;
+  if (!q || !S || !z || !o || !den) return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  if (!aligned16(S) || !aligned16(o)) return fail(LINATT_EINVAL, std::string(fn) + ": S and o must be 16-byte aligned");
+  a.q = q; a.c = c; a.S = const_cast<float*>(S); a.z = const_cast<float*>(z); a.o = o; a.den = den;
+  return gen_state_launch(fn, a, KATA_GEN_READOUT, dtype, stream);
+}
+
+int linatt_kata_gen_update(const void* k, const void* v, const float* c, float* S, float* z,
+                           int init, int B, int T, int H, int dk, int dv, int num_groups,
+                           int variant, float scale, int dtype, void* stream) {
+  g_last_error.clear();
+  const char* fn = "linatt_kata_gen_update";
+  KataGenStateArgs a{};
+  int st = gen_state_args(fn, a, B, T, H, dk, dv, num_groups, variant, scale, 1.f, dtype);
+  if (st) return st;
+  if (!k || !v || !S || !z) return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  if (!aligned16(S)) return fail(LINATT_EINVAL, std::string(fn) + ": S must be 16-byte aligned");
+  a.k = k; a.v = v; a.c = c; a.S = S; a.z = z; a.init = init ? 1 : 0;
+  return gen_state_launch(fn, a, KATA_GEN_UPDATE, dtype, stream);
+}
+
+
 }  // extern "C"

@@ -125,6 +125,26 @@ struct KataDecodeArgs {
 template <typename T, int DK, int DV, int M>
 hipError_t launch_kata_decode(const KataDecodeArgs& a, hipStream_t stream);
 
+// The state form of every flash score (kata_state_gen.hip): concat or sum
+// features, optional decay, dk <= 128, dv = 64, fp32 state (B, H, P, 64).
+struct KataGenStateArgs {
+  const void* q;     // decode: (B, H, dk); readout: (B, T, H, dk)
+  const void* k;     // decode: (B, H, dk); update: (B, T, H, dk)
+  const void* v;     // decode: (B, H, 64); update: (B, T, H, 64)
+  const float* c;    // decode: (B, H) the step's log-decay; else (B, T, H) cumulative in the call; or null
+  float* S;          // (B, H, P, 64)
+  float* z;          // (B, H, P)
+  void* o;           // decode: (B, H, 64) out; readout: (B, T, H, 64) in (flash) and out
+  float* den;        // readout: (B, T, H) in (flash) and out
+  int B, T, H, dk, E, lgE, M, P, sum;
+  float scale, eps;
+  int init;          // update: 1 = add to f_T S, 0 = start from zero
+};
+enum { KATA_GEN_DECODE = 0, KATA_GEN_READOUT = 1, KATA_GEN_UPDATE = 2 };
+
+template <typename T>
+hipError_t launch_kata_gen_state(const KataGenStateArgs& a, int which, hipStream_t stream);
+
 // Compiled (dtype, DK, DV, M) combinations of the state form.
 #define LINATT_KATA_STATE_SHAPES(X) \
   X(__bf16, 64, 64, 4)              \

@@ -4,16 +4,25 @@ entry the reference's flash path never fills.
 The reference's flash branch sets ``final_state = None`` (``kata/layer.py:492``)
 and hands it to ``update_layer_cache`` (``:532-537``), so incremental decoding
 makes each new token attend only to itself; its evaluation forces
-``use_cache=False`` for KATA to stay correct (``eval_recall.py:133-144``).  The
-concat-SPD score has an exact O(1)-per-token state form, kept here per layer:
+``use_cache=False`` for KATA to stay correct (``eval_recall.py:133-144``).
+Every flash score has an exact O(1)-per-token state form, kept here per layer:
 
-    S = sum_s psi(sqrt(scale) k_s) v_s^T   (B, H, M*E*E, dv) float32
-    z = sum_s psi(sqrt(scale) k_s)         (B, H, M*E*E)     float32
-    psi(x) = vec(x_g x_g^T) per group,  o_t = psi(sqrt(scale) q_t)^T S / max(psi(.) . z, eps)
+    S = sum_s psi(sqrt(scale) k_s) v_s^T   (B, H, P, dv) float32
+    z = sum_s psi(sqrt(scale) k_s)         (B, H, P)     float32
+    o_t = psi(sqrt(scale) q_t)^T S / max(psi(.) . z, eps)
 
-A chunk of T > 1 tokens goes through the state-form prefill continued from the
-current state (``linatt_kata_prefill_state``); a single token through the
-decode step (``linatt_kata_decode_step``), both in ``liblinatt_hip.so``.
+with psi(x) = vec(x_g x_g^T) per group for the concat score (P = M E^2),
+vec(sum_g x_g x_g^T) for the sum score (P = E^2), and, for the decayed
+score, S and z scaled by exp(c_t - c_{t-1}) before each token's term.
+
+The concat score without decay at the MFMA state-form shapes
+(``linatt_kata_state_supported``) takes a chunk of T > 1 tokens through the
+state-form prefill continued from the current state
+(``linatt_kata_prefill_state``) and a single token through
+``linatt_kata_decode_step``.  Every other flash score (M = 1, the sum
+score, the decayed score, the offset gate's padded width dk = 128) takes a
+chunk through the flash forward plus the stored state's readout and a state
+update, and a single token through ``linatt_kata_gen_decode``.
 
 The cache contract is fla's (``fla.layers.utils.get_layer_cache`` /
 ``update_layer_cache``, imported at ``kata/layer.py:19`` from the third-party
@@ -29,56 +38,135 @@ mixer's flash branch can keep a real state:
     o, final_state = parallel_kata_attn_cached(q_in, k_in, v, rec, self.spd_num_groups, scale_in)
     update_layer_cache(self, past_key_values, recurrent_state=final_state, offset=q.shape[1])
 
-Scope: the concat score without decay or offset gate, at the shapes the
-state-form kernels are compiled for (``linatt_kata_state_supported``); other
-mixers raise.
+Scope: dv = 64, dk <= 128 with a power-of-two group width of at least 16
+(every flash configuration of the reference); other shapes raise.
 """
 
 from __future__ import annotations
 
+import math
 from typing import NamedTuple
 
 import torch
 
-from . import spd_state
+from . import _lib, spd_state
+from .parallel_kata_attn import _fwd as _kata_fwd
 
 __all__ = ["KataState", "parallel_kata_attn_cached", "LayerStateCache", "get_layer_cache",
            "update_layer_cache"]
 
 
 class KataState(NamedTuple):
-    """A layer's recurrent state: ``S (B, H, P, dv)``, ``z (B, H, P)`` float32
-    (``P = M E^2``) and the number of tokens it covers."""
+    """A layer's recurrent state: ``S (B, H, P, dv)``, ``z (B, H, P)`` float32,
+    the number of tokens it covers, and the score it belongs to (``variant``
+    "concat" or "sum", ``num_groups``)."""
 
     S: torch.Tensor
     z: torch.Tensor
     offset: int
+    variant: str = "concat"
+    num_groups: int = 0
 
 
-def parallel_kata_attn_cached(q, k, v, state=None, num_groups=4, scale=None, eps=1e-6):
-    """Concat-SPD causal attention of ``q, k, v`` (time-major ``(B, T, H, D)``)
+def _state_rows(dk, M, variant):
+    E = dk // M
+    return E * E if variant == "sum" else M * E * E
+
+
+def parallel_kata_attn_cached(q, k, v, state=None, num_groups=4, scale=None, eps=1e-6,
+                              variant="concat", c=None):
+    """KATA causal attention of ``q, k, v`` (time-major ``(B, T, H, D)``)
     continued from ``state`` (a :class:`KataState`, or ``None`` for an empty
-    cache).  Returns ``(o, new_state)``: ``o (B, T, H, dv)`` in v's dtype equals
-    rows ``offset .. offset + T - 1`` of the flash forward over every token so
-    far (``kata/parallel_kata_attn.py:357-361``), up to the ``max(den, eps)``
-    guard of the state form.  An existing state's tensors are updated in
-    place (a decode step reads and writes the state once, at HBM speed) and
-    returned in ``new_state``."""
+    cache).  Returns ``(o, new_state)``: ``o (B, T, H, dv)`` in v's dtype
+    equals rows ``offset .. offset + T - 1`` of the flash forward over every
+    token so far (``kata/parallel_kata_attn.py:357-361``, ``:539-576`` for
+    ``variant="sum"``, ``:291-354`` with the decay ``c``), up to the
+    ``max(den, eps)`` guard of the state form.  ``c (B, T, H)`` is the decay's
+    cumulative log-decay over this call's tokens (non-increasing; the mixer's
+    ``cumsum`` over the call).  An existing state's tensors are updated in
+    place and returned in ``new_state``.
+
+    The concat score without decay at the shapes of
+    ``linatt_kata_state_supported`` runs the MFMA state-form prefill
+    (``spd_state.kata_prefill``); every other flash score runs the flash
+    forward over the call's tokens plus the generic state kernels
+    (``linatt_kata_gen_*``: dk <= 128, dv = 64)."""
     if q.dim() != 4 or k.shape != q.shape or v.shape[:3] != q.shape[:3]:
         raise ValueError(f"q, k must be (B, T, H, dk) and v (B, T, H, dv); got {tuple(q.shape)}, "
                          f"{tuple(k.shape)}, {tuple(v.shape)}")
-    B, T, H, _ = q.shape
-    if state is not None and (state.S.shape[:2] != (B, H) or state.z.shape[:2] != (B, H)):
-        raise ValueError(f"state is for (B, H) = {tuple(state.S.shape[:2])}, inputs are {(B, H)}")
+    if variant not in ("concat", "sum"):
+        raise ValueError(f"variant must be 'concat' or 'sum', got {variant!r}")
+    if c is not None and variant != "concat":
+        raise NotImplementedError("decay is only defined for the concat score")
+    B, T, H, dk = q.shape
+    dv = v.shape[-1]
+    M = num_groups
+    if state is not None:
+        if state.S.shape[:2] != (B, H) or state.z.shape[:2] != (B, H):
+            raise ValueError(f"state is for (B, H) = {tuple(state.S.shape[:2])}, inputs are {(B, H)}")
+        if state.variant != variant or (state.num_groups and state.num_groups != M):
+            raise ValueError(f"state is for the {state.variant} score with {state.num_groups} groups, "
+                             f"the call is {variant} with {M}")
     offset = 0 if state is None else state.offset
+    L = _lib.load()
+    dt = v.dtype
+    fast = (variant == "concat" and c is None
+            and L.linatt_kata_state_supported(_lib.dtype_code(dt), dk, dv, M))
+    if fast:
+        if T == 1 and state is not None:
+            o = spd_state.kata_decode_step(state.S, state.z, q[:, 0], k[:, 0], v[:, 0], M,
+                                           scale, eps)
+            return o[:, None], KataState(state.S, state.z, offset + 1, variant, M)
+        init = None if state is None else (state.S, state.z)
+        o, _, S, z = spd_state.kata_prefill(q, k, v, M, scale, eps, initial_state=init,
+                                            in_place=state is not None)
+        return o, KataState(S, z, offset + T, variant, M)
+    return _generic(q, k, v, state, M, scale, eps, variant, c, offset)
+
+
+def _generic(q, k, v, state, M, scale, eps, variant, c, offset):
+    _lib.require_device(q, k, v)
+    B, T, H, dk = q.shape
+    dv = v.shape[-1]
+    if dk % M:
+        raise ValueError(f"d_k={dk} not divisible by M={M}")
+    sc = 1.0 / math.sqrt(dk // M) if scale is None else float(scale)
+    var = _lib.LINATT_KATA_SUM if variant == "sum" else _lib.LINATT_KATA_CONCAT
+    dt = v.dtype
+    q, k, v = q.to(dt).contiguous(), k.to(dt).contiguous(), v.contiguous()
+    P = _state_rows(dk, M, variant)
+    cf = None
+    if c is not None:
+        _lib.require_device(c)
+        cf = c.float().contiguous()
+        if cf.shape != (B, T, H):
+            raise ValueError(f"c must be (B, T, H) = {(B, T, H)}, got {tuple(cf.shape)}")
+    if state is not None:
+        S, z = state.S, state.z
+        if S.shape != (B, H, P, dv) or z.shape != (B, H, P) or S.dtype != torch.float32 \
+                or not (S.is_contiguous() and z.is_contiguous()):
+            raise ValueError(f"state must be contiguous float32 S {(B, H, P, dv)}, z {(B, H, P)}")
+    L = _lib.load()
+    code, sp = _lib.dtype_code(dt), _lib.stream_of(q)
     if T == 1 and state is not None:
-        o = spd_state.kata_decode_step(state.S, state.z, q[:, 0], k[:, 0], v[:, 0], num_groups,
-                                       scale, eps)
-        return o[:, None], KataState(state.S, state.z, offset + 1)
-    init = None if state is None else (state.S, state.z)
-    o, _, S, z = spd_state.kata_prefill(q, k, v, num_groups, scale, eps, initial_state=init,
-                                        in_place=state is not None)
-    return o, KataState(S, z, offset + T)
+        o = torch.empty(B, H, dv, device=q.device, dtype=dt)
+        _lib.check("linatt_kata_gen_decode", L.linatt_kata_gen_decode(
+            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(cf), _lib.ptr(S), _lib.ptr(z),
+            _lib.ptr(o), B, H, dk, dv, M, var, sc, float(eps), code, sp))
+        return o[:, None], KataState(S, z, offset + 1, variant, M)
+    # the call's own tokens by the flash forward, then the stored state's part
+    o, den = _kata_fwd(q, k, v, M, sc, variant, cf)
+    if state is not None:
+        _lib.check("linatt_kata_gen_readout", L.linatt_kata_gen_readout(
+            _lib.ptr(q), _lib.ptr(cf), _lib.ptr(S), _lib.ptr(z), _lib.ptr(o), _lib.ptr(den),
+            B, T, H, dk, dv, M, var, sc, float(eps), code, sp))
+    else:
+        S = torch.empty(B, H, P, dv, device=q.device, dtype=torch.float32)
+        z = torch.empty(B, H, P, device=q.device, dtype=torch.float32)
+    _lib.check("linatt_kata_gen_update", L.linatt_kata_gen_update(
+        _lib.ptr(k), _lib.ptr(v), _lib.ptr(cf), _lib.ptr(S), _lib.ptr(z),
+        1 if state is not None else 0, B, T, H, dk, dv, M, var, sc, code, sp))
+    return o, KataState(S, z, offset + T, variant, M)
 
 
 class LayerStateCache:

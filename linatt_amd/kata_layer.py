@@ -20,15 +20,16 @@ return value ``(o, None, past_key_values)``), installed by
   offset-gated inputs go through the same op); GQA natively (k and v keep
   their ``num_kv_heads`` heads, the reference repeats them);
 * with a cache (``use_cache`` or a non-empty ``past_key_values``), the
-  recurrent state form (``kata_cache.parallel_kata_attn_cached``: a prefill
-  continued from the layer's state, or one decode step), and the
-  convolution states are stored with it, so prefill + decode equals the
-  parallel forward over the whole sequence;
+  recurrent state form of the score (``kata_cache.parallel_kata_attn_cached``:
+  a prefill continued from the layer's state, or one decode step; concat,
+  sum, decayed, offset-gated), and the convolution states are stored with
+  it, so prefill + decode equals the parallel forward over the whole
+  sequence;
 * the SPD delta branch through ``linatt_amd.flash_delta``.
 
 The projections and ``o_proj`` stay library GEMMs.  Anything else (the
-psi-feature maps, ``delta_state``, a cache for a score without a state form,
-module types it does not know) runs the original forward unchanged.
+psi-feature maps, ``delta_state``, a cache for the delta branch or for a
+shape without a state form) runs the original forward unchanged.
 """
 
 from __future__ import annotations
@@ -82,15 +83,21 @@ def _apply_norm(x, spec):
 
 
 def _state_form_ok(self, q_dtype):
-    """The recurrent state kernels cover the concat score without decay or
-    offset gate at the compiled shapes."""
-    if self.use_delta or self.feature_map_name != "kata_quadratic":
+    """A recurrent state exists for every flash score (concat, sum, decayed,
+    offset-gated) at dv = 64 and a key width (the offset gate's padded one)
+    of at most 128 split into power-of-two groups of at least 16, where the
+    flash forward is compiled too."""
+    if self.use_delta or self.feature_map_name not in _FLASH_MAPS:
         return False
-    if self.use_offset_gate or self.use_decay:
+    M = self.spd_num_groups
+    dk = M * self._off_Epad if self.use_offset_gate else self.head_k_dim
+    E = dk // M
+    if self.head_v_dim != 64 or dk > 128 or dk % M or E < 16 or E & (E - 1):
         return False
     L = _lib.load()
-    return bool(L.linatt_kata_state_supported(_lib.dtype_code(q_dtype), self.head_k_dim,
-                                              self.head_v_dim, self.spd_num_groups))
+    variant = _lib.LINATT_KATA_SUM if self.feature_map_name == "kata_quadratic_sum" else 0
+    return bool(L.linatt_kata_supported(_lib.dtype_code(q_dtype), dk, self.head_v_dim, M, variant,
+                                        1 if self.use_decay else 0))
 
 
 def _proj_dtype(x):
@@ -210,17 +217,19 @@ def kata_attention_forward(self, hidden_states, attention_mask=None, past_key_va
             q_in, k_in = self._augment_offset(q, k, off)
             scale = self._off_scale
         variant = "sum" if self.feature_map_name == "kata_quadratic_sum" else "concat"
+        c = None
+        if self.use_decay:
+            # the call's cumulative log-decay (a stored state sits at c = 0)
+            dt_ = F.softplus(self.dt_proj(x) + self.dt_bias)
+            c = (-self.A_log.float().exp() * dt_.float()).cumsum(dim=1).contiguous()
         if cached:
             if self.num_kv_groups > 1:
                 k_in = k_in.repeat_interleave(self.num_kv_groups, dim=2)
                 v = v.repeat_interleave(self.num_kv_groups, dim=2)
             rec = last.get("recurrent_state") if last is not None else None
-            o, final_state = kata_cache.parallel_kata_attn_cached(q_in, k_in, v, rec, M, scale)
+            o, final_state = kata_cache.parallel_kata_attn_cached(q_in, k_in, v, rec, M, scale,
+                                                                  variant=variant, c=c)
         else:
-            c = None
-            if self.use_decay:
-                dt_ = F.softplus(self.dt_proj(x) + self.dt_bias)
-                c = (-self.A_log.float().exp() * dt_.float()).cumsum(dim=1).contiguous()
             if has_norm:
                 y = parallel_kata_attn_onorm(q_in, k_in, v, norm.weight, norm.eps, M, scale,
                                              variant, c)

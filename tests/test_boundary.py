@@ -226,8 +226,9 @@ def mixer_hook(monkeypatch):
         calls.append(("parallel_kata_attn_onorm", variant, c is not None, tuple(k.shape)))
         return torch.zeros(*q.shape[:3], v.shape[-1], dtype=v.dtype)
 
-    def cached(q, k, v, state, M, scale):
+    def cached(q, k, v, state, M, scale, variant="concat", c=None):
         calls.append(("parallel_kata_attn_cached", state is not None, tuple(k.shape)))
+        calls.append(("cached_score", variant, c is not None))
         off = 0 if state is None else state.offset
         return (torch.zeros(*q.shape[:3], v.shape[-1], dtype=v.dtype),
                 kata_cache.KataState(None, None, off + q.shape[1]))
@@ -299,7 +300,24 @@ def test_apply_mixer_falls_back_outside_its_scope(mixer_hook):
     # a psi-feature map: the reference's own forward
     layer = KataAttention(64, 4, 64, 4, feature_map="positive")
     assert layer(torch.randn(1, 5, 64))[0][0] == "original" and layer.original_calls == 1
-    # a cache for a score with no state form (sum): the reference's forward
-    layer = KataAttention(64, 4, 64, 4, feature_map="kata_quadratic_sum")
-    layer(torch.randn(1, 5, 64), past_key_values=kata_cache.LayerStateCache(), use_cache=True)
+    # a cache for a shape with no state form (groups of 8 dims): the
+    # reference's forward
+    layer = KataAttention(64, 4, 64, 8).bfloat16()
+    layer(torch.randn(1, 5, 64).bfloat16(), past_key_values=kata_cache.LayerStateCache(),
+          use_cache=True)
     assert layer.original_calls == 1 and not calls
+
+
+@pytest.mark.parametrize("kw,score", [
+    (dict(feature_map="kata_quadratic_sum"), ("cached_score", "sum", False)),
+    (dict(use_decay=True), ("cached_score", "concat", True)),
+    (dict(use_offset_gate=True), ("cached_score", "concat", False)),
+])
+def test_apply_mixer_cache_for_every_flash_score(mixer_hook, kw, score):
+    """Sum, decayed and offset-gated scores decode from a state too."""
+    KataAttention, calls = mixer_hook
+    from linatt_amd import kata_cache
+    layer = KataAttention(64, 4, 64, 2, **kw).bfloat16()
+    layer(torch.randn(1, 5, 64).bfloat16(), past_key_values=kata_cache.LayerStateCache(),
+          use_cache=True)
+    assert layer.original_calls == 0 and score in calls

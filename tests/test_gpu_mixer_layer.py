@@ -251,3 +251,30 @@ def test_hooked_mixer_prefill_then_decode_equals_parallel(hooked, M):
     e_pre, e_dec = mar(y_inc[:, :P0], y_par[:, :P0]), mar(y_inc[:, P0:], y_par[:, P0:])
     print(f"  prefill {e_pre:.2e} decode {e_dec:.2e}", flush=True)
     assert e_pre < BAR and e_dec < BAR
+
+
+@pytest.mark.parametrize("kw", [dict(M=2, feature_map="kata_quadratic_sum"), dict(M=2, use_decay=True),
+                                dict(M=1), dict(M=2, use_offset_gate=True)],
+                         ids=["sum_M2", "decay_M2", "concat_M1", "offset_gate_M2"])
+def test_hooked_mixer_decode_every_flash_score(hooked, kw):
+    """The sum, decayed, one-group and offset-gated mixers decode from a
+    state too: prefill + decode through the hook equals the parallel
+    forward."""
+    from linatt_amd.kata_cache import LayerStateCache
+    kw = dict(kw)
+    M = kw.pop("M")
+    torch.manual_seed(5)
+    B, T, P0, hidden, H, D = 2, 140, 130, 256, 4, 64
+    layer = hooked(hidden, H, D, M, **kw).to(DEV)
+    x = torch.randn(B, T, hidden, generator=torch.Generator().manual_seed(6)).to(DEV)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        y_par, _, _ = layer(x)
+        cache = LayerStateCache()
+        outs = [layer(x[:, :P0], past_key_values=cache, use_cache=True)[0]]
+        for t in range(P0, T):
+            outs.append(layer(x[:, t:t + 1], past_key_values=cache, use_cache=True)[0])
+    y_inc = torch.cat(outs, dim=1)
+    assert layer.original_calls == 0
+    e = mar(y_inc, y_par)
+    print(f"\nhooked decode {kw}: {e:.2e}", flush=True)
+    assert e < BAR
