@@ -617,14 +617,18 @@ __global__ __launch_bounds__(state_threads<DV>()) void delta_state_fwd_kernel(
 //   o = scale e^G (Q h_c) + Aqk v_new.
 // h_c^T and v_new^T tiles by one up-front copy; q and Aqk rows straight to
 // registers.  Wave w: rows 32 (w & 1) + lane (lane column i), value columns
-// 64 (w >> 1) ..; o leaves as whole 16-byte rows.
+// 64 (w >> 1) ..; o leaves as whole 16-byte rows, staged through the tiles'
+// LDS once every wave has consumed them (48 KiB at K = V = 128, so three
+// workgroups share a CU instead of two).
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, bool GATED>
 __global__ __launch_bounds__(256, 2) void delta_out_kernel(DeltaArgs a, DeltaLayout L) {
   constexpr int KT = DK / 64, VT = DV / 64, TE = 64 * 64;
-  __shared__ __attribute__((aligned(16))) T Ht[VT * KT * TE];  // h^T [v][d], tile vt * KT + kt
-  __shared__ __attribute__((aligned(16))) T Vt[VT * TE];       // v_new^T [v][j]
-  __shared__ __attribute__((aligned(16))) u32x4 Stg[4 * 256];  // store staging, 4 KiB per wave
+  __shared__ __attribute__((aligned(16))) T Lds[VT * KT * TE + VT * TE];
+  T* const Ht = Lds;                 // h^T [v][d], tile vt * KT + kt
+  T* const Vt = Lds + VT * KT * TE;  // v_new^T [v][j]
+  u32x4* const Stg = reinterpret_cast<u32x4*>(Lds);  // store staging, 4 KiB per wave, after the products
+  static_assert(4 * 256 * 16 <= (int)sizeof(Lds), "the staging fits the consumed tiles");
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
   const int Tn = a.T, H = a.H, NT = a.NT;
@@ -661,8 +665,8 @@ __global__ __launch_bounds__(256, 2) void delta_out_kernel(DeltaArgs a, DeltaLay
   if constexpr (GATED) f *= __expf(reinterpret_cast<const float*>(a.ctx + L.Gc)[(size_t)bh * Tp + t0 + i]);
   vm_wait_barrier<0>();
 
+  f32x16 x[2];
   if (vh < VT) {
-    f32x16 x[2];
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       // D[v][i], v = 64 vh + 32 m + ..: h^T rows v (k = d) against q row i
@@ -676,9 +680,11 @@ __global__ __launch_bounds__(256, 2) void delta_out_kernel(DeltaArgs a, DeltaLay
       for (int s = 0; s < 4; ++s) acc = mma(tile_ld8<T>(Vt + vh * TE, vr, 16 * s + 8 * hh), ya[s], acc);
       x[m] = acc;
     }
+  }
+  block_barrier();  // every wave has read its tiles: the staging reuses them
+  if (vh < VT)
     store_rows_staged<T>(x[0], x[1], Stg + 256 * w, (T*)a.o + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DV + 64 * vh,
                          (int64_t)H * DV, lane, Tn - (t0 + 32 * lb));
-  }
 }
 
 template <typename T, int DK, int DV, bool GATED>
