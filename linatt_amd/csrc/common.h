@@ -276,6 +276,16 @@ __device__ __forceinline__ v8_t<T> tile_ld8(const T* tile, int row, int col) {
   return *reinterpret_cast<const v8_t<T>*>(reinterpret_cast<const char*>(tile) + tile_off(row, col));
 }
 
+// A tile of 64 rows and KT * 64 columns kept as KT natural 64 x 64
+// sub-tiles (columns 64 j .. 64 j + 63 in sub-tile j, 4096 elements apart,
+// each swizzled as tile_slot says).  An operand's 8 or 32 columns never
+// straddle two sub-tiles.
+template <typename T>
+__device__ __forceinline__ v8_t<T> wtile_ld8(const T* tile, int row, int col) {
+  return *reinterpret_cast<const v8_t<T>*>(reinterpret_cast<const char*>(tile + (col >> 6) * 4096) +
+                                          tile_off(row, col & 63));
+}
+
 // Eight elements of row `row` in the k order of ld_tr_op: columns
 // c0 + 16 j + 4 hh + 0..3 and c0 + 16 j + 8 + 4 hh + 0..3 (two 8-byte reads).
 template <typename T>
@@ -308,6 +318,11 @@ __device__ __forceinline__ v8_t<T> tile_tr8(const T* tile, int r0, int c0, int j
   const char* base = reinterpret_cast<const char*>(tile);
   return cat44<T>(ds_tr4<T>(reinterpret_cast<const T*>(base + tile_off(row, col))),
                   ds_tr4<T>(reinterpret_cast<const T*>(base + tile_off(row + 8, col))));
+}
+// tile_tr8 on a wide tile (see wtile_ld8); c0 a multiple of 32
+template <typename T>
+__device__ __forceinline__ v8_t<T> wtile_tr8(const T* tile, int r0, int c0, int j, int lane) {
+  return tile_tr8<T>(tile + (c0 >> 6) * 4096, r0, c0 & 63, j, lane);
 }
 
 // Compile-time bool for generic lambdas: body(BoolC<true>{}) instantiates

@@ -449,9 +449,11 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
     float* __restrict__ dc, int Tn, int HQ, int H, float scale2, int nqt, int nbh, OutNorm on) {
   constexpr int E = DK / M;
   constexpr int KE = E / 16;
-  static_assert(sizeof(T) == 2 && DK == 64 && DV == 64, "64 x 64 16-bit tiles");
+  static_assert(sizeof(T) == 2 && (DK == 64 || (DK == 128 && E >= 32)) && DV == 64,
+                "64 x 64 16-bit tiles");
+  constexpr int KT = DK / 64;  // key tiles as KT 64 x 64 sub-tiles (wtile_ld8)
   constexpr int NB = 3;  // ring depth: tiles st + 1 and st + 2 in flight during tile st
-  __shared__ __attribute__((aligned(16))) T Kb[NB][64 * 64];
+  __shared__ __attribute__((aligned(16))) T Kb[NB][KT * 64 * 64];
   __shared__ __attribute__((aligned(16))) T Vb[NB][64 * 64];
   __shared__ __attribute__((aligned(16))) float Cs[NB][64];
   __shared__ __attribute__((aligned(16))) float Wred[4][DV];  // output-norm weight gradient per wave
@@ -480,7 +482,9 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
   // and of dA), which saves it two products per score, and the matching
   // delta' = <o, dO'> from the same rounded dO', so x' = dO' v - delta' keeps
   // the cancellation of x = dO v - delta (zero for a lone key)
-  constexpr bool kPre = __is_same(T, __bf16);
+  // (only the 64 x 64 tile dk/dv kernel reads this form; at dk = 128 the
+  // generic one reads -<o, dO> and dO itself)
+  constexpr bool kPre = __is_same(T, __bf16) && DK == 64;
   float pdl = 0.f;
   if (tvalid) {
     const float d = den[qrow];
@@ -587,7 +591,7 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
   // K^T operand feeding dQ^T rows 32 rb + cl of query group gi from key group
   // gk (E >= 32: whole 32-row blocks of the group)
   auto kt_op = [&](const T* Ks, int sb, int gi, int gk, int rb, int j) __attribute__((always_inline)) {
-    return tile_tr8<T>(Ks, 32 * sb, gk * E + 32 * rb - gi * E, j, lane);
+    return wtile_tr8<T>(Ks, 32 * sb, gk * E + 32 * rb - gi * E, j, lane);
   };
 
   const int s_end = min(t0 + 128, Tn);
@@ -608,13 +612,16 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
       const T* vt = vb + (int64_t)64 * st * vs;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        dma16s(kt, ko[i], kd + 1024 * (2 * w + i));
+#pragma unroll
+        for (int jt = 0; jt < KT; ++jt) dma16s(kt + 64 * jt, ko[i], kd + 8192 * jt + 1024 * (2 * w + i));
         dma16s(vt, vo[i], vd + 1024 * (2 * w + i));
       }
     } else {
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        dma_tile64<T>(kb, ks, 64 * st, Tn, reinterpret_cast<T*>(kd), 2 * w + i, lane);
+#pragma unroll
+        for (int jt = 0; jt < KT; ++jt)
+          dma_tile64<T>(kb + 64 * jt, ks, 64 * st, Tn, reinterpret_cast<T*>(kd) + 4096 * jt, 2 * w + i, lane);
         dma_tile64<T>(vb, vs, 64 * st, Tn, reinterpret_cast<T*>(vd), 2 * w + i, lane);
       }
     }
@@ -624,7 +631,7 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
       if (w == 0) dma4(c + ((int64_t)b * Tn + min(64 * st + lane, Tn - 1)) * HQ + hq, Cs[st % NB]);
     }
   };
-  const int ops = 4 + (DECAY && w == 0 ? 1 : 0);  // copies per tile and wave
+  const int ops = 2 * KT + 2 + (DECAY && w == 0 ? 1 : 0);  // copies per tile and wave
   vm_drain();  // q, dO (and c) of this wave's queries are in registers
   write_rows();
 #pragma unroll
@@ -667,17 +674,12 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
             if (s > tl || s >= Tn) x[e] = 0.f;
           }
         }
-        f32x16 msk;
         if constexpr (DECAY) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const f32x4 cs4 = *reinterpret_cast<const f32x4*>(&Cs[buf][32 * sb + 8 * i + 4 * hh]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float dd = ct - cs4[r];
-              x[4 * i + r] *= __expf(fminf(dd, 0.f));
-              msk[4 * i + r] = dd <= 0.f ? 1.f : 0.f;
-            }
+            for (int r = 0; r < 4; ++r) x[4 * i + r] *= __expf(fminf(ct - cs4[r], 0.f));
           }
         }
         f32x16 au{};
@@ -689,7 +691,7 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
             f32x16 r{};
 #pragma unroll
             for (int kk = 0; kk < KE; ++kk)
-              r = mma(tile_ld8<T>(Ks, 32 * sb + cl, gk * E + 16 * kk + 8 * hh), qop[gi * KE + kk], r);
+              r = mma(wtile_ld8<T>(Ks, 32 * sb + cl, gk * E + 16 * kk + 8 * hh), qop[gi * KE + kk], r);
             if constexpr (DECAY) au += r * r;
             const f32x16 da = r * x;
             if constexpr (k16) {
@@ -711,7 +713,14 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
         }
         if constexpr (DECAY) {
 #pragma unroll
-          for (int e = 0; e < 16; ++e) dcr += x[e] * au[e] * msk[e];
+          for (int i = 0; i < 4; ++i) {
+            // [c_t - c_s <= 0], from c in LDS again rather than kept
+            // through the group loop (16 registers fewer)
+            const f32x4 cs4 = *reinterpret_cast<const f32x4*>(&Cs[buf][32 * sb + 8 * i + 4 * hh]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              dcr += ct - cs4[r] <= 0.f ? x[4 * i + r] * au[4 * i + r] : 0.f;
+          }
         }
       }
     }
@@ -1098,10 +1107,13 @@ hipError_t launch_kata_bwd(const KataArgs& a, int parts, hipStream_t stream) {
   } else {
     const float scale2 = a.scale * a.scale;
     const int nqt = (a.T + 127) / 128;
+    // 16-bit tile kernels: dk/dv at dk = dv = 64; dq (and the forward) also at
+    // dk = 128 with groups of at least 32
     constexpr bool kTiles = sizeof(T) == 2 && DK == 64 && DV == 64;
+    constexpr bool kTilesDq = sizeof(T) == 2 && DV == 64 && (DK == 64 || (DK == 128 && DK / M >= 32));
     if (parts & KATA_BWD_DQ) {
       const int nbh = a.B * a.HQ;
-      if constexpr (kTiles)
+      if constexpr (kTilesDq)
       {
         const OutNorm on{a.nw, const_cast<void*>(a.dy), a.rstd, a.nw_part, a.eps, nullptr};
         auto go = [&](auto onorm) {

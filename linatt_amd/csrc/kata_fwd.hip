@@ -208,9 +208,10 @@ __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
     int Tn, int HQ, int H, float scale2, int nqt, int nbh, OutNorm on) {
   constexpr int E = DK / M;
   constexpr int KE = E / 16;
-  static_assert(sizeof(T) == 2 && DK == 64 && DV == 64, "64 x 64 16-bit tiles");
+  static_assert(sizeof(T) == 2 && (DK == 64 || DK == 128) && DV == 64, "64 x 64 16-bit tiles");
   constexpr int NB = 3;
-  __shared__ __attribute__((aligned(16))) T Kb[NB][64 * 64];
+  constexpr int KT = DK / 64;  // key tiles as KT 64 x 64 sub-tiles (wtile_ld8)
+  __shared__ __attribute__((aligned(16))) T Kb[NB][KT * 64 * 64];
   __shared__ __attribute__((aligned(16))) T Vb[NB][64 * 64];
   __shared__ __attribute__((aligned(16))) float Cs[NB][64];
 
@@ -260,13 +261,17 @@ __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
       const T* vt = vb + (int64_t)64 * st * vs;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        dma16s(kt, ko[i], reinterpret_cast<char*>(Kb[sl]) + 1024 * (2 * w + i));
+#pragma unroll
+        for (int j = 0; j < KT; ++j)
+          dma16s(kt + 64 * j, ko[i], reinterpret_cast<char*>(Kb[sl] + 4096 * j) + 1024 * (2 * w + i));
         dma16s(vt, vo[i], reinterpret_cast<char*>(Vb[sl]) + 1024 * (2 * w + i));
       }
     } else {
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        dma_tile64<T>(kb, ks, 64 * st, Tn, Kb[sl], 2 * w + i, lane);
+#pragma unroll
+        for (int j = 0; j < KT; ++j)
+          dma_tile64<T>(kb + 64 * j, ks, 64 * st, Tn, Kb[sl] + 4096 * j, 2 * w + i, lane);
         dma_tile64<T>(vb, vs, 64 * st, Tn, Vb[sl], 2 * w + i, lane);
       }
     }
@@ -275,8 +280,8 @@ __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
       if (w == 0) dma4(c + ((int64_t)b * Tn + min(64 * st + lane, Tn - 1)) * HQ + hq, Cs[sl]);
     }
   };
-  // copies per tile and wave: two of K, two of V, c by wave 0
-  const int ops = 4 + (DECAY && w == 0 ? 1 : 0);
+  // copies per tile and wave: two of each K sub-tile, two of V, c by wave 0
+  const int ops = 2 * KT + 2 + (DECAY && w == 0 ? 1 : 0);
 
   auto step = [&](int st, auto slot) __attribute__((always_inline)) {
     constexpr int buf = decltype(slot)::value;
@@ -302,7 +307,7 @@ __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
           f32x16 r{};
 #pragma unroll
           for (int kk = 0; kk < KE; ++kk)
-            r = mma(tile_ld8<T>(Ks, krow, g * E + 16 * kk + 8 * hh), qop[g * KE + kk], r);
+            r = mma(wtile_ld8<T>(Ks, krow, g * E + 16 * kk + 8 * hh), qop[g * KE + kk], r);
           a[sb] += r * r;
         }
       } else {
@@ -313,7 +318,7 @@ __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
             f32x16 r{};
 #pragma unroll
             for (int kk = 0; kk < KE; ++kk)
-              r = mma(tile_ld8<T>(Ks, krow, gj * E + 16 * kk + 8 * hh), qop[gi * KE + kk], r);
+              r = mma(wtile_ld8<T>(Ks, krow, gj * E + 16 * kk + 8 * hh), qop[gi * KE + kk], r);
             a[sb] += r * r;
           }
         }
@@ -384,7 +389,7 @@ __global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
       f32x16 r{};
 #pragma unroll
       for (int kk = 0; kk < KE; ++kk)
-        r = mma(tile_ld8<T>(Ks, 32 * sb + cl, g * E + 16 * kk + 8 * hh), qop[g * KE + kk], r);
+        r = mma(wtile_ld8<T>(Ks, 32 * sb + cl, g * E + 16 * kk + 8 * hh), qop[g * KE + kk], r);
       return r;
     };
     auto finish = [&](int sb, const f32x16& ab) __attribute__((always_inline)) {
@@ -520,7 +525,7 @@ hipError_t launch_kata_fwd(const KataArgs& a, hipStream_t stream) {
     const int nqt = (a.T + 127) / 128;
     const int nbh = a.B * a.HQ;
     dim3 grid(nqt * nbh), block(256);
-    if constexpr (sizeof(T) == 2 && DK == 64 && DV == 64) {
+    if constexpr (sizeof(T) == 2 && (DK == 64 || DK == 128) && DV == 64) {
       const OutNorm on{a.nw, a.y, a.rstd, nullptr, a.eps, a.num32};
       auto go = [&](auto epi) {
         kata_fwd_tile_kernel<T, DK, DV, M, SUM, DECAY, decltype(epi)::value><<<grid, block, 0, stream>>>(
