@@ -482,9 +482,7 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
   // and of dA), which saves it two products per score, and the matching
   // delta' = <o, dO'> from the same rounded dO', so x' = dO' v - delta' keeps
   // the cancellation of x = dO v - delta (zero for a lone key)
-  // (only the 64 x 64 tile dk/dv kernel reads this form; at dk = 128 the
-  // generic one reads -<o, dO> and dO itself)
-  constexpr bool kPre = __is_same(T, __bf16) && DK == 64;
+  constexpr bool kPre = __is_same(T, __bf16);
   float pdl = 0.f;
   if (tvalid) {
     const float d = den[qrow];
@@ -783,7 +781,7 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
 }
 
 template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
-__global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
+__global__ __launch_bounds__(256, DK == 64 ? 2 : 1) void kata_bwd_dkdv_tile_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const float* __restrict__ den, const float* __restrict__ delta, const T* __restrict__ dout,
     T* __restrict__ dk, T* __restrict__ dv, const float* __restrict__ c, float* __restrict__ dc,
@@ -792,11 +790,13 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
   constexpr int KE = E / 16;
   constexpr float kPScale = __is_same(T, _Float16) ? 4096.f : 1.f;
   constexpr float kPInv = 1.f / kPScale;
-  static_assert(sizeof(T) == 2 && DK == 64 && DV == 64, "64 x 64 16-bit tiles");
+  static_assert(sizeof(T) == 2 && (DK == 64 || (DK == 128 && E >= 32)) && DV == 64,
+                "64 x 64 16-bit tiles");
+  constexpr int KT = DK / 64;  // query tiles as KT 64 x 64 sub-tiles (wtile_ld8)
   // ring depth 2: tile n + 1 in flight during tile n (a third slot costs
   // registers in this kernel and spills)
   constexpr int NB = 2;
-  __shared__ __attribute__((aligned(16))) T Qb[NB][64 * 64];
+  __shared__ __attribute__((aligned(16))) T Qb[NB][KT * 64 * 64];
   __shared__ __attribute__((aligned(16))) T Ob[NB][64 * 64];
   __shared__ __attribute__((aligned(16))) float Dl[NB][64];  // -delta
   __shared__ __attribute__((aligned(16))) float Pd[NB][64];  // scale^2 / den
@@ -846,7 +846,7 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
   // Q^T operand feeding dK^T rows 32 rb + cl of key group gk from query group
   // gi (E >= 32: whole 32-row blocks of the group)
   auto qt_op = [&](const T* Qs, int mb, int gi, int gk, int rb, int j) __attribute__((always_inline)) {
-    return tile_tr8<T>(Qs, 32 * mb, gi * E + 32 * rb - gk * E, j, lane);
+    return wtile_tr8<T>(Qs, 32 * mb, gi * E + 32 * rb - gk * E, j, lane);
   };
 
   // query tiles (hq, tt) of this key tile, flattened over the G query heads
@@ -876,13 +876,16 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
       const T* ot = ob + (int64_t)t0 * os;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        dma16s(qt, qo[i], qd + 1024 * (2 * w + i));
+#pragma unroll
+        for (int jt = 0; jt < KT; ++jt) dma16s(qt + 64 * jt, qo[i], qd + 8192 * jt + 1024 * (2 * w + i));
         dma16s(ot, oo[i], od + 1024 * (2 * w + i));
       }
     } else {
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        dma_tile64<T>(qb, qs, t0, Tn, reinterpret_cast<T*>(qd), 2 * w + i, lane);
+#pragma unroll
+        for (int jt = 0; jt < KT; ++jt)
+          dma_tile64<T>(qb + 64 * jt, qs, t0, Tn, reinterpret_cast<T*>(qd) + 4096 * jt, 2 * w + i, lane);
         dma_tile64<T>(ob, os, t0, Tn, reinterpret_cast<T*>(od), 2 * w + i, lane);
       }
     }
@@ -975,7 +978,7 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dkdv_tile_kernel(
             f32x16 r{};
 #pragma unroll
             for (int kk = 0; kk < KE; ++kk)
-              r = mma(tile_ld8<T>(Qs, 32 * mb + cl, gi * E + 16 * kk + 8 * hh), kop(gk * KE + kk), r);
+              r = mma(wtile_ld8<T>(Qs, 32 * mb + cl, gi * E + 16 * kk + 8 * hh), kop(gk * KE + kk), r);
             A += r * r;
             const f32x16 da = r * xs;
             if constexpr (k16) {
@@ -1107,13 +1110,12 @@ hipError_t launch_kata_bwd(const KataArgs& a, int parts, hipStream_t stream) {
   } else {
     const float scale2 = a.scale * a.scale;
     const int nqt = (a.T + 127) / 128;
-    // 16-bit tile kernels: dk/dv at dk = dv = 64; dq (and the forward) also at
-    // dk = 128 with groups of at least 32
-    constexpr bool kTiles = sizeof(T) == 2 && DK == 64 && DV == 64;
-    constexpr bool kTilesDq = sizeof(T) == 2 && DV == 64 && (DK == 64 || (DK == 128 && DK / M >= 32));
+    // 16-bit tile kernels (both passes, which share the prescaled bf16 rows):
+    // dv = 64, dk = 64 or dk = 128 with groups of at least 32
+    constexpr bool kTiles = sizeof(T) == 2 && DV == 64 && (DK == 64 || (DK == 128 && DK / M >= 32));
     if (parts & KATA_BWD_DQ) {
       const int nbh = a.B * a.HQ;
-      if constexpr (kTilesDq)
+      if constexpr (kTiles)
       {
         const OutNorm on{a.nw, const_cast<void*>(a.dy), a.rstd, a.nw_part, a.eps, nullptr};
         auto go = [&](auto onorm) {
