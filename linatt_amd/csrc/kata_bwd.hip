@@ -780,8 +780,15 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
   }
 }
 
+// waves (of 32 keys each) per workgroup of the tile dk/dv kernel: eight at
+// dk = 128, where the k and v operands of four waves and a two-slot query
+// ring would take 97 KiB of LDS (one workgroup, four waves, per CU); eight
+// waves share one ring in 145 KiB, two waves per SIMD
+template <int DK>
+constexpr int kata_dkdv_waves() { return DK == 64 ? 4 : 8; }
+
 template <typename T, int DK, int DV, int M, bool SUM, bool DECAY>
-__global__ __launch_bounds__(256, DK == 64 ? 2 : 1) void kata_bwd_dkdv_tile_kernel(
+__global__ __launch_bounds__(64 * kata_dkdv_waves<DK>(), 2) void kata_bwd_dkdv_tile_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const float* __restrict__ den, const float* __restrict__ delta, const T* __restrict__ dout,
     T* __restrict__ dk, T* __restrict__ dv, const float* __restrict__ c, float* __restrict__ dc,
@@ -793,6 +800,8 @@ __global__ __launch_bounds__(256, DK == 64 ? 2 : 1) void kata_bwd_dkdv_tile_kern
   static_assert(sizeof(T) == 2 && (DK == 64 || (DK == 128 && E >= 32)) && DV == 64,
                 "64 x 64 16-bit tiles");
   constexpr int KT = DK / 64;  // query tiles as KT 64 x 64 sub-tiles (wtile_ld8)
+  constexpr int NW = kata_dkdv_waves<DK>();
+  constexpr int CPW = 8 / NW;  // 1 KiB copies per wave and 64 x 64 sub-tile
   // ring depth 2: tile n + 1 in flight during tile n (a third slot costs
   // registers in this kernel and spills)
   constexpr int NB = 2;
@@ -802,7 +811,7 @@ __global__ __launch_bounds__(256, DK == 64 ? 2 : 1) void kata_bwd_dkdv_tile_kern
   __shared__ __attribute__((aligned(16))) float Pd[NB][64];  // scale^2 / den
   __shared__ __attribute__((aligned(16))) float Ct[NB][64];
   // this wave's k and v rows as MFMA B operands (lane l: 16 bytes per k-step)
-  __shared__ __attribute__((aligned(16))) u32x4 KVop[4][(DK + DV) / 16][64];
+  __shared__ __attribute__((aligned(16))) u32x4 KVop[NW][(DK + DV) / 16][64];
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -810,7 +819,7 @@ __global__ __launch_bounds__(256, DK == 64 ? 2 : 1) void kata_bwd_dkdv_tile_kern
   map_block(blockIdx.x, nst, nbh, stile, bh, false);
   const int b = bh / H, h = bh % H;
   const int G = HQ / H;
-  const int s0 = stile * 128;
+  const int s0 = stile * 32 * NW;
   const int sw = s0 + 32 * w;
   const int sl = sw + cl;
   const bool svalid = sl < Tn;
@@ -852,13 +861,14 @@ __global__ __launch_bounds__(256, DK == 64 ? 2 : 1) void kata_bwd_dkdv_tile_kern
   // query tiles (hq, tt) of this key tile, flattened over the G query heads
   const int ntt = (Tn + 63) / 64, tt0 = s0 / 64, nq = ntt - tt0;
   const int ntiles = G * nq;
-  // tile n: copies 2w and 2w + 1 of q and of dO by wave w (full tiles from a
-  // scalar base plus these per-lane offsets; a head's last tile clamps rows)
-  unsigned qo[2], oo[2];
+  // tile n: copies CPW w .. CPW w + CPW - 1 of each sub-tile of q and of dO by
+  // wave w (full tiles from a scalar base plus these per-lane offsets; a
+  // head's last tile clamps rows)
+  unsigned qo[CPW], oo[CPW];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    qo[i] = tile_lane_off(2 * w + i, lane, (int)(qs * sizeof(T)));
-    oo[i] = tile_lane_off(2 * w + i, lane, (int)(os * sizeof(T)));
+  for (int i = 0; i < CPW; ++i) {
+    qo[i] = tile_lane_off(CPW * w + i, lane, (int)(qs * sizeof(T)));
+    oo[i] = tile_lane_off(CPW * w + i, lane, (int)(os * sizeof(T)));
   }
   // bf16: dO and delta come prescaled by scale^2/den from the dq kernel
   constexpr bool kPre = __is_same(T, __bf16);
@@ -875,18 +885,18 @@ __global__ __launch_bounds__(256, DK == 64 ? 2 : 1) void kata_bwd_dkdv_tile_kern
       const T* qt = qb + (int64_t)t0 * qs;
       const T* ot = ob + (int64_t)t0 * os;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < CPW; ++i) {
 #pragma unroll
-        for (int jt = 0; jt < KT; ++jt) dma16s(qt + 64 * jt, qo[i], qd + 8192 * jt + 1024 * (2 * w + i));
-        dma16s(ot, oo[i], od + 1024 * (2 * w + i));
+        for (int jt = 0; jt < KT; ++jt) dma16s(qt + 64 * jt, qo[i], qd + 8192 * jt + 1024 * (CPW * w + i));
+        dma16s(ot, oo[i], od + 1024 * (CPW * w + i));
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < CPW; ++i) {
 #pragma unroll
         for (int jt = 0; jt < KT; ++jt)
-          dma_tile64<T>(qb + 64 * jt, qs, t0, Tn, reinterpret_cast<T*>(qd) + 4096 * jt, 2 * w + i, lane);
-        dma_tile64<T>(ob, os, t0, Tn, reinterpret_cast<T*>(od), 2 * w + i, lane);
+          dma_tile64<T>(qb + 64 * jt, qs, t0, Tn, reinterpret_cast<T*>(qd) + 4096 * jt, CPW * w + i, lane);
+        dma_tile64<T>(ob, os, t0, Tn, reinterpret_cast<T*>(od), CPW * w + i, lane);
       }
     }
   };
@@ -907,7 +917,7 @@ __global__ __launch_bounds__(256, DK == 64 ? 2 : 1) void kata_bwd_dkdv_tile_kern
   load_rows(0, 0);
   float dcc = 0.f;
   // query tile n (global index over the G heads) with or without the causal /
-  // past-T masks: only the two tiles on this workgroup's diagonal and a
+  // past-T masks: only the NW / 2 tiles on this workgroup's diagonal and a
   // ragged last tile take MASKED, so the other tiles' block bodies are each
   // one basic block
   auto tile = [&](int n, auto masked_c) __attribute__((always_inline)) {
@@ -1055,12 +1065,12 @@ __global__ __launch_bounds__(256, DK == 64 ? 2 : 1) void kata_bwd_dkdv_tile_kern
       }
     }
   };
-  // per query head: the two diagonal tiles, the tiles wholly inside T, the ragged rest
+  // per query head: the diagonal tiles, the tiles wholly inside T, the ragged rest
   const int nfull = Tn / 64 - tt0;
   for (int hi = 0; hi < G; ++hi) {
     const int nb = hi * nq;
     int i = 0;
-    for (; i < nq && i < 2; ++i) tile(nb + i, BoolC<true>{});
+    for (; i < nq && i < NW / 2; ++i) tile(nb + i, BoolC<true>{});
     for (; i < nfull; ++i) tile(nb + i, BoolC<false>{});
     for (; i < nq; ++i) tile(nb + i, BoolC<true>{});
   }
@@ -1140,11 +1150,13 @@ hipError_t launch_kata_bwd(const KataArgs& a, int parts, hipStream_t stream) {
     }
     if (parts & KATA_BWD_DKDV) {
       const int nbk = a.B * a.H;
-      if constexpr (kTiles)
-        kata_bwd_dkdv_tile_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbk), dim3(256), 0, stream>>>(
+      if constexpr (kTiles) {
+        constexpr int kw = kata_dkdv_waves<DK>();
+        const int nkt = (a.T + 32 * kw - 1) / (32 * kw);
+        kata_bwd_dkdv_tile_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nkt * nbk), dim3(64 * kw), 0, stream>>>(
             (const T*)a.q, (const T*)a.k, (const T*)a.v, a.den, a.delta, (const T*)a.dout,
-            (T*)a.dk, (T*)a.dv, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt, nbk);
-      else
+            (T*)a.dk, (T*)a.dv, a.c, a.dc, a.T, a.HQ, a.H, scale2, nkt, nbk);
+      } else
       kata_bwd_dkdv_kernel<T, DK, DV, M, SUM, DECAY><<<dim3(nqt * nbk), dim3(256), 0, stream>>>(
           (const T*)a.q, (const T*)a.k, (const T*)a.v, a.den, a.delta, (const T*)a.dout,
           (T*)a.dk, (T*)a.dv, a.c, a.dc, a.T, a.HQ, a.H, scale2, nqt, nbk);

@@ -279,3 +279,42 @@ def test_offset_gate_shape_dk128(P, decay, dtype, T):
     if not decay:
         pad = leaves[0].grad.reshape(B, T, H, M, Ep)[..., E + 1:]
         assert pad.abs().max().item() <= 1e-6 * max(1.0, leaves[0].grad.abs().max().item())
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1, 1), (2, 37, 2, 2), (1, 300, 2, 2), (1, 520, 4, 2)],
+                         ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("variant", ["concat", "sum", "decay"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32],
+                         ids=["bf16", "f16", "f32"])
+def test_dense_dk128(P, shape, variant, dtype):
+    """dk = 128, dv = 64, M = 2 with every key column live (the offset gate's
+    inputs leave half of each group zero): one key block, two and three
+    blocks of 256 keys with a ragged end, and GQA (HQ = 2 H)."""
+    B, T, HQ, H = shape
+    M = 2
+    print(f"case {shape} dk128 {variant} {dtype}", flush=True)
+    q, k, v, do = make(B, T, HQ, H, 128, 64, dtype, seed=300 + T)
+    dev = torch.device("cuda")
+    tol = TOL[dtype]
+    fl = grad_floors(q, k, v, do)
+    if variant == "decay":
+        if HQ != H:
+            pytest.skip("the decayed score takes HQ = H")
+        c = -torch.cumsum(torch.rand(B, T, H, generator=torch.Generator().manual_seed(T)) * 0.1, 1)
+        o_ref, *refs = K.kata_decay_fwd_bwd(q, k, v, c, do, M)
+        leaves = [x.to(dev).requires_grad_(True) for x in (q, k, v, c)]
+        o = P.parallel_kata_attn_decay(*leaves, num_groups=M)
+        names = ("dq", "dk", "dv", "dc")
+        fl["dc"] = 0.1 * do.abs().max().item() * v.abs().max().item()
+    else:
+        o_ref, den_ref = K.kata_fwd(q, k, v, M, None, variant)
+        refs = K.kata_bwd(q, k, v, o_ref, den_ref, do, M, None, variant)
+        leaves = [x.to(dev).requires_grad_(True) for x in (q, k, v)]
+        fn = P.parallel_kata_attn if variant == "concat" else P.parallel_kata_attn_sum
+        o = fn(*leaves, num_groups=M)
+        names = ("dq", "dk", "dv")
+    o.backward(do.to(dev))
+    assert mar(o, o_ref) < tol
+    for name, leaf, ref in zip(names, leaves, refs):
+        e = mar(leaf.grad, ref, fl[name])
+        assert e < tol, (name, e)
