@@ -52,29 +52,31 @@ def delta_flops(B, H, T, K, V, C=64):
     per token-head C(6K+4V) + 6KV + (2/3)C^2 (Gram, QK^T, W = 3x2C^2K; U and
     the intra A.v = 2x2C^2V; W.h, Q.h, K^T v_new = 3x2CKV; the 64x64 UT
     inverse (2/3)C^3 per chunk); backward = 2x forward.  Split by kernel:
-    prep = Gram, QK^T, W, U, inverse; state pass = W.h, K^T v_new; output =
-    Q.h, intra A.v; reverse state pass = Aqk^T dO, K dS, Q^T dO, W^T dVn
-    (2CV + 8KV); the backward chunk kernel the rest of 2x forward."""
+    prep = Gram, QK^T, W, U, inverse; state pass = W.h, K^T v_new and the
+    output's Q.h, intra A.v (one kernel); reverse state pass = Aqk^T dO,
+    K dS, Q^T dO, W^T dVn (2CV + 8KV); the backward chunk kernel the rest of
+    2x forward."""
     n = B * H * T
     prep = n * (6 * C * K + 2 * C * V + (2.0 / 3.0) * C * C)
-    state = n * 4 * K * V
-    out = n * (2 * K * V + 2 * C * V)
-    fwd = prep + state + out
+    state = n * (4 * K * V + 2 * K * V + 2 * C * V)
+    fwd = prep + state
     state_bwd = n * (2 * C * V + 8 * K * V)
-    return {"prep": prep, "state_fwd": state, "out": out, "fwd": fwd,
+    return {"prep": prep, "state_fwd": state, "fwd": fwd,
             "state_bwd": state_bwd, "bwd_chunk": 2 * fwd - state_bwd, "bwd": 2 * fwd,
             "total": 3 * fwd}
 
 
 def delta_state_bytes(B, H, T, K, V, gated, h0, C=64):
     """Compulsory HBM bytes of the two state passes (bf16 tensors, fp32 g and
-    states).  Forward: k, w, u read, v_new written, g, the per-chunk states
-    h (bf16), h0 read and ht written.  Backward: q, k, w, dO read, dv_new
-    written, g, the per-chunk dh (bf16), dh0 written."""
+    states).  Forward, with the output: k, w, u, q and the chunks' Aqk
+    blocks read, v_new and o written, g, the per-chunk states h (bf16), h0
+    read and ht written.  Backward: q, k, w, dO read, dv_new written, g, the
+    per-chunk dh (bf16), dh0 written."""
     n, NT = B * T * H, (T + C - 1) // C
     gb = 4 if gated else 0
     st = B * H * K * V * 4
-    fwd = n * (2 * K + 2 * K + 2 * V + 2 * V + gb) + B * H * NT * K * V * 2 + st * (2 if h0 else 1)
+    fwd = n * (2 * K + 2 * K + 2 * V + 2 * V + 2 * K + 2 * C + 2 * V + gb) + \
+        B * H * NT * K * V * 2 + st * (2 if h0 else 1)
     bwd = n * (2 * K + 2 * K + 2 * K + 2 * V + 2 * V + gb) + B * H * NT * K * V * 2 + \
         (st if h0 else 0)
     return {"state_fwd": fwd, "state_bwd": bwd}
@@ -95,7 +97,7 @@ def settle(parts, seconds):
         torch.cuda.synchronize()
 
 
-DELTA_FWD_STAGES = (("prep", 1), ("state_fwd", 2), ("out", 4))
+DELTA_FWD_STAGES = (("prep", 1), ("state_fwd", 2))
 DELTA_BWD_STAGES = (("state_bwd", 1), ("bwd_chunk", 2))
 
 

@@ -210,9 +210,9 @@ int linatt_delta_bwd(const void* q, const void* k, const void* v, const float* b
 /* The two calls above, one kernel at a time, for timing each kernel apart
  * (no counterpart in the reference, whose fla ops are single calls).
  * `stages` selects the kernels to launch, in this order: forward bit 0 the
- * chunk-local prep, bit 1 the state pass, bit 2 the output; backward bit 0
- * the reverse state pass, bit 1 the chunk kernel.  Running every bit once,
- * in order, on one stream equals the full call. */
+ * chunk-local prep, bit 1 the state pass (which also writes o); backward
+ * bit 0 the reverse state pass, bit 1 the chunk kernel.  Running every bit
+ * once, in order, on one stream equals the full call. */
 int linatt_delta_fwd_stages(const void* q, const void* k, const void* v, const float* beta,
                             const float* g, const float* h0, void* o, float* ht, void* ctx, int B,
                             int T, int H, int dk, int dv, float scale, int stages, int dtype,

@@ -450,7 +450,7 @@ size_t linatt_delta_bwd_workspace_bytes(int B, int T, int H, int dk, int dv, int
 int linatt_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
                      const float* g, const float* h0, void* o, float* ht, void* ctx, int B,
                      int T, int H, int dk, int dv, float scale, int dtype, void* stream) {
-  return linatt_delta_fwd_stages(q, k, v, beta, g, h0, o, ht, ctx, B, T, H, dk, dv, scale, 7,
+  return linatt_delta_fwd_stages(q, k, v, beta, g, h0, o, ht, ctx, B, T, H, dk, dv, scale, 3,
                                  dtype, stream);
 }
 
@@ -459,8 +459,8 @@ int linatt_delta_fwd_stages(const void* q, const void* k, const void* v, const f
                             int T, int H, int dk, int dv, float scale, int stages, int dtype,
                             void* stream) {
   g_last_error.clear();
-  if (stages < 0 || stages > 7)
-    return fail(LINATT_EINVAL, "linatt_delta_fwd: stages must be a mask of bits 0-2");
+  if (stages < 0 || stages > 3)
+    return fail(LINATT_EINVAL, "linatt_delta_fwd: stages must be a mask of bits 0-1");
   int st = check_delta("linatt_delta_fwd", B, T, H, dk, dv, scale, dtype);
   if (st) return st;
   if (!q || !k || !v || !beta || !o || !ctx)

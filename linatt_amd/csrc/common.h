@@ -629,27 +629,42 @@ __device__ __forceinline__ void stage_half(const f32x16& x, int b, u32x4* stage,
 // writes, then two buffer-store instructions of 16 whole 64-byte rows each
 // (g wave-uniform, rows >= nvalid dropped).
 __device__ __forceinline__ int swz4(int row, int ch) { return row * 4 + (ch ^ ((row >> 1) & 3)); }
+// Cache policy of a buffer store: non-temporal (nt), for outputs the storing
+// kernel does not read back.  Their lines then leave L2 first and do not
+// displace the input tiles that a kernel's workgroups share through L2.
+constexpr int kStoreStream = 2;
+// Its LDS half: the block into the 128 staging slots.
 template <typename T>
-__device__ __forceinline__ void store_rows32(const f32x16& x, u32x4* stage, T* g, int64_t ld, int lane,
-                                             int nvalid = 32) {
+__device__ __forceinline__ void stage_rows32(const f32x16& x, u32x4* stage, int lane) {
   const int cl = lane & 31, hh = lane >> 5;
 #pragma unroll
   for (int I = 0; I < 4; ++I)
     *reinterpret_cast<v4_t<T>*>(reinterpret_cast<char*>(stage + swz4(cl, I)) + 8 * hh) =
         to4<T>(x[4 * I], x[4 * I + 1], x[4 * I + 2], x[4 * I + 3]);
+}
+// Its global half, by any wave of the workgroup once the block is staged.
+// CP is the stores' cache policy (kStoreStream: non-temporal).
+template <typename T, int CP = 0>
+__device__ __forceinline__ void flush_rows32(const u32x4* stage, T* g, int64_t ld, int lane, int nvalid = 32) {
   const int nv = nvalid < 0 ? 0 : (nvalid > 32 ? 32 : nvalid);
   const unsigned ldb = (unsigned)(ld * (int64_t)sizeof(T));
   const __amdgpu_buffer_rsrc_t rs = buf_rsrc(g, nv == 0 ? 0u : (unsigned)(nv - 1) * ldb + 64u);
 #pragma unroll
   for (int op = 0; op < 2; ++op) {
     const int gi = 64 * op + lane, row = gi >> 2, ch = gi & 3;
-    __builtin_amdgcn_raw_buffer_store_b128(stage[swz4(row, ch)], rs, (int)(row * ldb + 16 * ch), 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(stage[swz4(row, ch)], rs, (int)(row * ldb + 16 * ch), 0, CP);
   }
+}
+template <typename T, int CP = 0>
+__device__ __forceinline__ void store_rows32(const f32x16& x, u32x4* stage, T* g, int64_t ld, int lane,
+                                             int nvalid = 32) {
+  stage_rows32<T>(x, stage, lane);
+  flush_rows32<T, CP>(stage, g, ld, lane, nvalid);
 }
 
 // The global half: a staged block's 32 rows to g + row * ld (g wave-uniform,
 // rows >= nvalid dropped), by any wave of the workgroup.
-template <typename T>
+template <typename T, int CP = 0>
 __device__ __forceinline__ void flush_rows(const u32x4* stage, T* g, int64_t ld, int lane, int nvalid = 32) {
   const int nv = nvalid < 0 ? 0 : (nvalid > 32 ? 32 : nvalid);
   const unsigned ldb = (unsigned)(ld * (int64_t)sizeof(T));
@@ -657,7 +672,7 @@ __device__ __forceinline__ void flush_rows(const u32x4* stage, T* g, int64_t ld,
 #pragma unroll
   for (int op = 0; op < 4; ++op) {
     const int gi = 64 * op + lane, row = gi >> 3, ch = gi & 7;
-    __builtin_amdgcn_raw_buffer_store_b128(stage[swz_slot<8>(row, ch)], rs, (int)(row * ldb + 16 * ch), 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(stage[swz_slot<8>(row, ch)], rs, (int)(row * ldb + 16 * ch), 0, CP);
   }
 }
 

@@ -186,9 +186,9 @@ __global__ __launch_bounds__(state_bwd_threads()) void delta_state_bwd_kernel(De
     T* drows = (T*)(a.ws + L.dhT) + (ci * DV + 32 * part) * DK;
 #pragma unroll
     for (int blk = 0; blk < NDT / 2; ++blk)
-      if (blk % kStateBwdCopyWaves == cw) flush_rows<T>(Stg[c & 1][blk], drows + 64 * blk, DK, lane);
+      if (blk % kStateBwdCopyWaves == cw) flush_rows<T, kStoreStream>(Stg[c & 1][blk], drows + 64 * blk, DK, lane);
     if ((NDT / 2) % kStateBwdCopyWaves == cw)
-      flush_rows<T>(Stg[c & 1][NDT / 2], (T*)(a.ws + L.dVnT) + (ci * DV + 32 * part) * 64, 64, lane);
+      flush_rows<T, kStoreStream>(Stg[c & 1][NDT / 2], (T*)(a.ws + L.dVnT) + (ci * DV + 32 * part) * 64, 64, lane);
   };
   if (w >= NCW) {
     // this wave's vector-memory ops per chunk of copies (G and e^(gamma - G):
@@ -633,7 +633,7 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
         dka = mma(tile_tr8<T>(Qt + (db / 2) * TE, 32 * jb, 32 * (db & 1), jj, lane),
                   tile_tr8<T>(Mqt, 32 * jb, 32 * lb, jj, lane), dka);
       }
-    store_rows32<T>(dqa, stage, (T*)a.dq + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DK + 32 * db, qks, lane,
+    store_rows32<T, kStoreStream>(dqa, stage, (T*)a.dq + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DK + 32 * db, qks, lane,
                     Tn - (t0 + 32 * lb));
   }
   gi += __shfl_xor(gi, 32);
@@ -833,11 +833,11 @@ __global__ __launch_bounds__(512) void delta_bwd_chunk_kernel(DeltaArgs a, Delta
         dka = mma(kop, tile_ldp8<T>(PT, r, 32 * lbk, jj, hh), dka);
         dka = mma(kop, tile_tr8<T>(PT, 32 * lbk, 32 * lb, jj, lane), dka);
       }
-    store_rows32<T>(dka, stage, (T*)a.dk + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DK + 32 * db, qks, lane,
+    store_rows32<T, kStoreStream>(dka, stage, (T*)a.dk + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DK + 32 * db, qks, lane,
                     Tn - (t0 + 32 * lb));
   }
   if (has_dv)
-    store_rows32<T>(dvx, stage, (T*)a.dv + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DV + 32 * cb, os, lane,
+    store_rows32<T, kStoreStream>(dvx, stage, (T*)a.dv + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DV + 32 * cb, os, lane,
                     Tn - (t0 + 32 * lb));
 
   db_part += __shfl_xor(db_part, 32);

@@ -22,8 +22,8 @@
 // operand copies the state pass reads.  Kernel 2 (delta_state_fwd) walks
 // the chunks in order: one wave per (batch, head, 32 value columns) keeps
 // its slice of S in MFMA accumulators and writes v_new and the per-chunk
-// states, with every operand read straight into registers.  Kernel 3
-// (delta_out) forms o in parallel over chunks from those.
+// states, with every operand read straight into registers, and forms o from
+// the states it stages.
 #include "common.h"
 #include "delta_kernels.h"
 #include "tri_inv.h"
@@ -329,16 +329,24 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 2: sequential state pass.  The value columns of a head are split
-// over DV/32 workgroups; each holds its 32 columns of S[d][v] in DK/32
-// accumulator tiles (lane column v) on one compute wave.  Per chunk the
-// chain is
+// Kernel 2: sequential state pass and output.  The value columns of a head
+// are split over DV/32 workgroups; each holds its 32 columns of S[d][v] in
+// DK/32 accumulator tiles (lane column v) on one compute wave.  Per chunk
+// the chain is
 //   v_new = U - W S  ->  S <- e^gamma S + Kd^T v_new.
-// A copy wave issues W, Kd^T (ungated: the chunk's k rows, read transposed)
-// and this workgroup's U^T rows two chunks ahead into a ring of three slots,
-// and stores the v_new^T / h^T blocks the compute wave staged one chunk
-// earlier.  W, Kd^T and U^T rows are stored XOR-swizzled by 16-byte chunk so
-// the operand reads of 16 consecutive rows hit distinct banks.
+// Two copy waves issue W, Kd^T (ungated: the chunk's k rows, read
+// transposed) and this workgroup's U^T rows two chunks ahead into a ring of
+// three slots, and store the v_new^T / h^T blocks the compute wave staged
+// one chunk earlier.  W, Kd^T and U^T rows are stored XOR-swizzled by
+// 16-byte chunk so the operand reads of 16 consecutive rows hit distinct
+// banks.  The output wave forms the workgroup's 32 columns of
+//   o = scale e^G (Q h) + Aqk v_new
+// for each chunk from the same staged h^T and v_new^T blocks while the
+// compute wave runs the next chunk, with q and Aqk rows loaded one chunk
+// ahead into registers, so no output pass reads h and v_new back.  It
+// stages o for the copy waves' stores and issues none itself: its loads
+// would otherwise wait for its stores (a load is waited for by count only
+// when no store was issued after it), and the chain for the output wave.
 // ---------------------------------------------------------------------------
 
 template <typename T, int DK, int DV, bool GATED>
@@ -363,6 +371,10 @@ __global__ __launch_bounds__(state_threads<DV>()) void delta_state_fwd_kernel(
   // (NDT / 2 each), staged for the copy wave's stores
   constexpr int NSTG = NW * (NDT / 2 + 1);
   __shared__ __attribute__((aligned(16))) u32x4 Stg[2][NSTG][256];
+  // the output wave's chunk c rows of o (two 32 x 32 blocks), staged in
+  // Ostg[c & 1] for the copy waves, which store them two barriers later
+  __shared__ __attribute__((aligned(16))) u32x4 Ostg[2][2][128];
+  static_assert(NW == 1, "one compute wave per workgroup (the output wave reads its staged blocks)");
 
   const int lane = threadIdx.x & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -376,10 +388,76 @@ __global__ __launch_bounds__(state_threads<DV>()) void delta_state_fwd_kernel(
   // gcum = the Gc context buffer, passed on its own as __restrict__ so the
   // per-chunk gate is a scalar load (no vector-memory wait in the chain)
   const float* Gc = gcum + (size_t)bh * Tp;
+  if (w == NW + kStateCopyWaves) {
+    // The output wave: chunk c's rows of o in this workgroup's 32 value
+    // columns, once the barrier that opens chunk c + 1 has closed chunk c
+    // (its h^T and v_new^T blocks are staged in Stg[c & 1] until the compute
+    // wave stages chunk c + 2 there, after the next barrier).  As MFMA
+    // products with the value columns as rows: D[v][i] = sum_d h^T[v][d]
+    // q[i][d] (A operand from the staged h^T rows, B from q row i in
+    // registers), scaled per query row i, plus sum_j v_new^T[v][j] Aqk[i][j].
+    const int b = bh / a.H, h = bh % a.H, Tn = a.T, H = a.H;
+    const T* qh = (const T*)a.q + ((size_t)b * Tn * H + h) * DK;
+    const T* ah = (const T*)(a.ctx + L.Aqk) + (size_t)bh * NT * 4096;
+    v8_t<T> yq[2][DK / 16], ya[2][4];
+    float f[2];
+    // chunk c's q rows, Aqk rows and row factors scale e^G of this lane's
+    // query rows 32 ib + cl (rows past T: zero q; their o is not stored),
+    // issued once chunk c - 1's products have read the registers, a chunk
+    // ahead of their use
+    auto load = [&](int c) __attribute__((always_inline)) {
+      const int t0 = c * kChunk;
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) {
+        const int i = 32 * ib + cl;
+        const bool valid = t0 + i < Tn;
+        const T* qr = qh + (size_t)(t0 + i) * H * DK;
+#pragma unroll
+        for (int s = 0; s < DK / 16; ++s) yq[ib][s] = valid ? ld8<T>(qr + 16 * s + 8 * hh) : zero8<T>();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) ya[ib][s] = ld8<T>(ah + (size_t)c * 4096 + i * 64 + 16 * s + 8 * hh);
+        f[ib] = a.scale;
+        if constexpr (GATED) f[ib] *= __expf(Gc[t0 + i]);
+      }
+    };
+    load(0);
+    block_barrier();  // opens chunk 0
+#pragma unroll 1
+    for (int c = 0; c < NT; ++c) {
+      block_barrier();  // chunk c staged (the compute wave's barrier opening chunk c + 1, or its last)
+      const u32x4* vs = &Stg[c & 1][0][0];  // v_new^T [v][j]
+      const u32x4* hs = vs + 256;          // h^T [v][d], NDT / 2 blocks of 64 columns
+      // every staged operand read first, so the products run back to back
+      u32x4 hop[DK / 16], vop[4];
+#pragma unroll
+      for (int s = 0; s < DK / 16; ++s) hop[s] = hs[(s / 4) * 256 + swz_slot<8>(cl, 2 * (s % 4) + hh)];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) vop[s] = vs[swz_slot<8>(cl, 2 * s + hh)];
+      __builtin_amdgcn_sched_barrier(0);
+      f32x16 x[2];
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) x[ib] = f32x16{};
+#pragma unroll
+      for (int s = 0; s < DK / 16; ++s)
+#pragma unroll
+        for (int ib = 0; ib < 2; ++ib) x[ib] = mma(__builtin_bit_cast(v8_t<T>, hop[s]), yq[ib][s], x[ib]);
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) x[ib] *= f[ib];
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int ib = 0; ib < 2; ++ib) x[ib] = mma(__builtin_bit_cast(v8_t<T>, vop[s]), ya[ib][s], x[ib]);
+      if (c + 1 < NT) load(c + 1);
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) stage_rows32<T>(x[ib], Ostg[c & 1][ib], lane);
+    }
+    block_barrier();  // the last chunk's o staged for the copy waves
+    return;
+  }
   // The copy waves (w >= NW) issue every copy, two chunks ahead, into a ring
   // of three slots; the compute waves never stall on copy issue.  Copy wave
   // cw issues share cw of each tile's copies.
-  if (w >= NW) {
+  if (w >= NW) {  // (the output wave has returned above)
     const int cw = w - NW;
     // wave-uniform byte bases of this head's W, Kd^T and this workgroup's
     // U^T rows; chunk c sits at + c * (bytes per chunk).  A 1 KiB copy op
@@ -428,17 +506,25 @@ __global__ __launch_bounds__(state_threads<DV>()) void delta_state_fwd_kernel(
     };
     // staged outputs of chunk c: v_new^T and h^T rows (ci DV + 32 g2); copy
     // wave cw stores the blocks with index cw modulo the copy waves
+    // o rows of chunk c in the compute wave's columns: copy wave cw stores
+    // block cw (rows 32 cw ..) of Ostg[c & 1]
+    T* oh = (T*)a.o + ((size_t)b * Tn * a.H + h) * DV + 32 * (gw - w);
+    auto flush_o = [&](int c) __attribute__((always_inline)) {
+      const int r0 = c * kChunk + 32 * cw;
+      flush_rows32<T, kStoreStream>(Ostg[c & 1][cw], oh + (size_t)r0 * a.H * DV, (int64_t)a.H * DV, lane, Tn - r0);
+    };
+    static_assert(NCW == 2, "one o block per copy wave");
     auto flush = [&](int c) __attribute__((always_inline)) {
       const size_t ci = (size_t)bh * NT + c;
 #pragma unroll
       for (int q = 0; q < NW; ++q) {
         const int g2 = gw - w + q;
         if ((q * (NDT / 2 + 1)) % NCW == cw)
-          flush_rows<T>(Stg[c & 1][q * (NDT / 2 + 1)], (T*)(a.ctx + L.VnT) + (ci * DV + 32 * g2) * 64, 64, lane);
+          flush_rows<T, kStoreStream>(Stg[c & 1][q * (NDT / 2 + 1)], (T*)(a.ctx + L.VnT) + (ci * DV + 32 * g2) * 64, 64, lane);
 #pragma unroll
         for (int blk = 0; blk < NDT / 2; ++blk)
           if ((q * (NDT / 2 + 1) + 1 + blk) % NCW == cw)
-            flush_rows<T>(Stg[c & 1][q * (NDT / 2 + 1) + 1 + blk],
+            flush_rows<T, kStoreStream>(Stg[c & 1][q * (NDT / 2 + 1) + 1 + blk],
                           (T*)(a.ctx + L.hT) + (ci * DV + 32 * g2) * DK + 64 * blk, DK, lane);
       }
     };
@@ -453,10 +539,14 @@ __global__ __launch_bounds__(state_threads<DV>()) void delta_state_fwd_kernel(
       if (c + 1 < NT) vm_wait_barrier<DMA_PER_CHUNK>();
       else vm_wait_barrier<0>();
       if (c > 0) flush(c - 1);
+      if (c > 1) flush_o(c - 2);
       if (c + 2 < NT) issue(c + 2);
     }
     block_barrier();  // the last chunk staged
     flush(NT - 1);
+    if (NT > 1) flush_o(NT - 2);
+    block_barrier();  // the last chunk's o staged
+    flush_o(NT - 1);
     return;
   }
 
@@ -600,6 +690,7 @@ __global__ __launch_bounds__(state_threads<DV>()) void delta_state_fwd_kernel(
     if (c + 2 < NT) step(IntC<2>{}, c + 2);
   }
   block_barrier();  // the last chunk's staged outputs are complete for the copy wave
+  block_barrier();  // (the output wave's last o)
 
   if (a.ht) {
 #pragma unroll
@@ -610,81 +701,6 @@ __global__ __launch_bounds__(state_threads<DV>()) void delta_state_fwd_kernel(
         a.ht[((size_t)bh * DK + d) * DV + v] = S[dt][e];
       }
   }
-}
-
-// ---------------------------------------------------------------------------
-// Kernel 3: output, parallel over (b, h, chunk):
-//   o = scale e^G (Q h_c) + Aqk v_new.
-// h_c^T and v_new^T tiles by one up-front copy; q and Aqk rows straight to
-// registers.  Wave w: rows 32 (w & 1) + lane (lane column i), value columns
-// 64 (w >> 1) ..; o leaves as whole 16-byte rows, staged through the tiles'
-// LDS once every wave has consumed them (48 KiB at K = V = 128, so three
-// workgroups share a CU instead of two).
-// ---------------------------------------------------------------------------
-template <typename T, int DK, int DV, bool GATED>
-__global__ __launch_bounds__(256, 2) void delta_out_kernel(DeltaArgs a, DeltaLayout L) {
-  constexpr int KT = DK / 64, VT = DV / 64, TE = 64 * 64;
-  __shared__ __attribute__((aligned(16))) T Lds[VT * KT * TE + VT * TE];
-  T* const Ht = Lds;                 // h^T [v][d], tile vt * KT + kt
-  T* const Vt = Lds + VT * KT * TE;  // v_new^T [v][j]
-  u32x4* const Stg = reinterpret_cast<u32x4*>(Lds);  // store staging, 4 KiB per wave, after the products
-  static_assert(4 * 256 * 16 <= (int)sizeof(Lds), "the staging fits the consumed tiles");
-  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
-  const int cl = lane & 31, hh = lane >> 5;
-  const int Tn = a.T, H = a.H, NT = a.NT;
-  const int c = blockIdx.x % NT, bh = blockIdx.x / NT;
-  const int b = bh / H, h = bh % H;
-  const int t0 = c * kChunk;
-  const size_t Tp = (size_t)NT * kChunk;
-  const size_t ci = (size_t)bh * NT + c;
-  const int lb = w & 1, vh = w >> 1;
-  const int i = 32 * lb + cl, ti = t0 + i;
-  const bool valid = ti < Tn;
-
-  const T* hg = (const T*)(a.ctx + L.hT) + ci * DV * DK;
-  const T* vg = (const T*)(a.ctx + L.VnT) + ci * DV * 64;
-#pragma unroll
-  for (int o = 0; o < 2; ++o) {
-    const int op = 2 * w + o;
-#pragma unroll
-    for (int vt = 0; vt < VT; ++vt) {
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt)
-        dma_tile64<T>(hg + (size_t)64 * vt * DK + 64 * kt, DK, 0, 64, Ht + (vt * KT + kt) * TE, op, lane);
-      dma_tile64<T>(vg + (size_t)64 * vt * 64, 64, 0, 64, Vt + vt * TE, op, lane);
-    }
-  }
-  const T* qrow = (const T*)a.q + (((size_t)b * Tn + ti) * H + h) * DK;
-  const T* arow = (const T*)(a.ctx + L.Aqk) + ci * 4096 + i * 64;
-  v8_t<T> yq[DK / 16], ya[4];
-#pragma unroll
-  for (int s = 0; s < DK / 16; ++s) yq[s] = valid ? ld8<T>(qrow + 16 * s + 8 * hh) : zero8<T>();
-#pragma unroll
-  for (int s = 0; s < 4; ++s) ya[s] = ld8<T>(arow + 16 * s + 8 * hh);
-  float f = a.scale;
-  if constexpr (GATED) f *= __expf(reinterpret_cast<const float*>(a.ctx + L.Gc)[(size_t)bh * Tp + t0 + i]);
-  vm_wait_barrier<0>();
-
-  f32x16 x[2];
-  if (vh < VT) {
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      // D[v][i], v = 64 vh + 32 m + ..: h^T rows v (k = d) against q row i
-      const int vr = 32 * m + cl;
-      f32x16 acc{};
-#pragma unroll
-      for (int s = 0; s < DK / 16; ++s)
-        acc = mma(tile_ld8<T>(Ht + (vh * KT + s / 4) * TE, vr, 16 * (s % 4) + 8 * hh), yq[s], acc);
-      acc *= f;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) acc = mma(tile_ld8<T>(Vt + vh * TE, vr, 16 * s + 8 * hh), ya[s], acc);
-      x[m] = acc;
-    }
-  }
-  block_barrier();  // every wave has read its tiles: the staging reuses them
-  if (vh < VT)
-    store_rows_staged<T>(x[0], x[1], Stg + 256 * w, (T*)a.o + (((size_t)b * Tn + t0 + 32 * lb) * H + h) * DV + 64 * vh,
-                         (int64_t)H * DV, lane, Tn - (t0 + 32 * lb));
 }
 
 template <typename T, int DK, int DV, bool GATED>
@@ -700,10 +716,6 @@ hipError_t launch_delta_fwd(const DeltaArgs& a, hipStream_t stream) {
     delta_state_fwd_kernel<T, DK, DV, GATED><<<dim3(BH * state_split<DV>()), dim3(state_threads<DV>()), 0,
                                                stream>>>(
         a, L, reinterpret_cast<const float*>(a.ctx + L.Gc));
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
-  if (a.stages & 4) {
-    delta_out_kernel<T, DK, DV, GATED><<<dim3(BH * a.NT), dim3(256), 0, stream>>>(a, L);
     e = hipGetLastError();
   }
   return e;

@@ -52,8 +52,11 @@ constexpr int state_split() { return DV / 32; }
 // LDS copies at about a third of what a CU takes in (44 against 125 GB/s
 // per CU in a probe), so the copies of a chunk are split over two.
 constexpr int kStateCopyWaves = 2;
+// Threads of a forward state-pass workgroup: the compute wave, the copy
+// waves and one output wave, which forms the output rows of each chunk from
+// the states the compute wave staged for the copy waves' stores.
 template <int DV>
-constexpr int state_threads() { return 64 * (DV / 32 / state_split<DV>() + kStateCopyWaves); }
+constexpr int state_threads() { return 64 * (DV / 32 / state_split<DV>() + kStateCopyWaves + 1); }
 
 struct DeltaArgs {
   // inputs
