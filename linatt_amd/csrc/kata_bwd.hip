@@ -319,71 +319,41 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
           nonpos = dd <= 0.f;
           return __expf(fminf(dd, 0.f));
         };
-        f32x16 A{}, xs;
-        if constexpr (sizeof(T) == 2) {
-          // one pass per group: the score feeds A and its dK product at once
-          if (need_mask) {
+        // one pass per group: the score feeds A and its dK product at once
+        f32x16 A{};
+        if (need_mask) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) x[e] = masked(e) ? 0.f : x[e];
+          for (int e = 0; e < 16; ++e) x[e] = masked(e) ? 0.f : x[e];
+        }
+        if constexpr (DECAY) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            bool np;
+            x[e] *= decay_of(e, np);
           }
-          if constexpr (DECAY) {
+        }
+        const f32x16 xs = x * pdv;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-              bool np;
-              x[e] *= decay_of(e, np);
-            }
+        for (int gi = 0; gi < M; ++gi)
+#pragma unroll
+          for (int gj = 0; gj < (SUM ? M : 1); ++gj) {
+            const f32x16 r = score(gi, SUM ? gj : gi);
+            A += r * r;
+            dk_product(r, xs, gi, SUM ? gj : gi);
           }
-          xs = x * pdv;
+        if (need_mask) {
 #pragma unroll
-          for (int gi = 0; gi < M; ++gi)
+          for (int e = 0; e < 16; ++e) A[e] = masked(e) ? 0.f : A[e];
+        }
+        if constexpr (DECAY) {
 #pragma unroll
-            for (int gj = 0; gj < (SUM ? M : 1); ++gj) {
-              const f32x16 r = score(gi, SUM ? gj : gi);
-              A += r * r;
-              dk_product(r, xs, gi, SUM ? gj : gi);
-            }
-          if (need_mask) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) A[e] = masked(e) ? 0.f : A[e];
+          for (int e = 0; e < 16; ++e) {
+            bool np;
+            const float dec = decay_of(e, np);
+            // column part of dc_s: -sum_t dA A [c_t - c_s <= 0] (xs carries the decay)
+            dcc -= np ? xs[e] * A[e] : 0.f;
+            A[e] *= dec;
           }
-          if constexpr (DECAY) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-              bool np;
-              const float dec = decay_of(e, np);
-              // column part of dc_s: -sum_t dA A [c_t - c_s <= 0] (xs carries the decay)
-              dcc -= np ? xs[e] * A[e] : 0.f;
-              A[e] *= dec;
-            }
-          }
-        } else {
-          // fp32 keeps the two-pass order (A from all scores, dV, then the
-          // dK products from recomputed scores): the one-pass order above
-          // gave wrong dV in fp32 builds with this compiler, while 16-bit
-          // builds of both orders agree bit for bit
-#pragma unroll
-          for (int gi = 0; gi < M; ++gi)
-#pragma unroll
-            for (int gj = 0; gj < (SUM ? M : 1); ++gj) {
-              const f32x16 r = score(gi, SUM ? gj : gi);
-              A += r * r;
-            }
-          if (need_mask) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e)
-              if (masked(e)) A[e] = x[e] = 0.f;
-          }
-          if constexpr (DECAY) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-              bool np;
-              const float dec = decay_of(e, np);
-              dcc -= np ? x[e] * pdv[e] * A[e] * dec : 0.f;
-              A[e] *= dec;
-              x[e] *= dec;
-            }
-          }
-          xs = x * pdv;
         }
         // fp16 keeps P in [0, 2^12] so small weights stay out of its subnormal
         // range (bf16 and fp32 have the fp32 exponent range); undone at the store
@@ -395,13 +365,6 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dkdv_ker
 #pragma unroll
           for (int db = 0; db < DV / 32; ++db)
             dva[db] = mma(ld_tr_op<T>(Ot + (32 * db + cl) * TP + 32 * mb, j, hh), pb, dva[db]);
-        }
-        if constexpr (sizeof(T) == 4) {
-#pragma unroll
-          for (int gi = 0; gi < M; ++gi)
-#pragma unroll
-            for (int gj = 0; gj < (SUM ? M : 1); ++gj)
-              dk_product(score(gi, SUM ? gj : gi), xs, gi, SUM ? gj : gi);
         }
       }
     }
