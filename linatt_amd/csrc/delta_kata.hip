@@ -57,7 +57,6 @@ DKataBwdLayout dkata_bwd_layout(int B, int T, int H, int D, int DV, int eb) {
   auto take = [&](size_t bytes) { size_t o = off; off = al256(off + bytes); return o; };
   L.dOp = take(rows * DV * eb);
   L.O16 = take(rows * DV * eb);
-  L.Zo = take(rows * DV * eb);
   L.ones = take(rows * 4);
   L.kws = take(kata_dop_offset((int64_t)rows) + (eb == 2 ? rows * DV * 2 : 0));
   L.dU = take(rows * DV * eb);
@@ -631,7 +630,6 @@ __global__ __launch_bounds__(256) void dkata_bwd_prep_kernel(DKataBwdArgs a, int
   }
   T* dop = (T*)(a.bws + a.BL.dOp);
   T* o16 = (T*)(a.bws + a.BL.O16);
-  T* zo = (T*)(a.bws + a.BL.Zo);
   float* ones = (float*)(a.bws + a.BL.ones);
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
     const int64_t row = 4 * i / DV;
@@ -641,10 +639,7 @@ __global__ __launch_bounds__(256) void dkata_bwd_prep_kernel(DKataBwdArgs a, int
     if (a.normalize) {
       const float4 o = reinterpret_cast<const float4*>(a.o)[i];
       st4<T>(o16 + 4 * i, to4<T>(o.x, o.y, o.z, o.w));
-    } else {
-      st4<T>(o16 + 4 * i, to4<T>(0.f, 0.f, 0.f, 0.f));
     }
-    st4<T>(zo + 4 * i, to4<T>(0.f, 0.f, 0.f, 0.f));
     if ((4 * i) % DV == 0) ones[row] = 1.f;
   }
 }
@@ -993,7 +988,9 @@ hipError_t launch_dkata_bwd(const DKataBwdArgs& a, hipStream_t stream) {
   const float* ones = (const float*)(a.bws + a.BL.ones);
   // readout: KATA sum backward of (q, k, U), den := 1
   KataArgs r{};
-  r.q = a.q; r.k = a.k; r.v = a.ws + a.L.Ub; r.o = a.bws + a.BL.O16; r.den = const_cast<float*>(ones);
+  // (o: the normalised output when normalising, else none: delta = 0)
+  r.q = a.q; r.k = a.k; r.v = a.ws + a.L.Ub; r.o = a.normalize ? a.bws + a.BL.O16 : nullptr;
+  r.den = const_cast<float*>(ones);
   r.dout = a.bws + a.BL.dOp; r.dq = a.dq; r.dk = a.bws + a.BL.dkr; r.dv = a.bws + a.BL.dU;
   r.delta = (float*)(a.bws + a.BL.kws);
   r.B = a.B; r.T = a.T; r.HQ = a.H; r.H = a.H; r.DK = D; r.DV = DV; r.M = M; r.scale = a.scale;
@@ -1013,9 +1010,9 @@ hipError_t launch_dkata_bwd(const DKataBwdArgs& a, hipStream_t stream) {
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   // erase: KATA sum backward of (k shifted one token, k, U) with the shifted
-  // dO := -X, o := 0, den := 1
+  // dO := -X, o := 0 (none), den := 1
   KataArgs x{};
-  x.q = a.bws + a.BL.Ksh; x.k = a.k; x.v = a.ws + a.L.Ub; x.o = a.bws + a.BL.Zo; x.den = const_cast<float*>(ones);
+  x.q = a.bws + a.BL.Ksh; x.k = a.k; x.v = a.ws + a.L.Ub; x.o = nullptr; x.den = const_cast<float*>(ones);
   x.dout = a.bws + a.BL.Xn; x.dq = a.bws + a.BL.dqe; x.dk = a.bws + a.BL.dke; x.dv = a.bws + a.BL.dve;
   x.delta = (float*)(a.bws + a.BL.kws);
   x.B = a.B; x.T = a.T; x.HQ = a.H; x.H = a.H; x.DK = D; x.DV = DV; x.M = M; x.scale = a.scale;

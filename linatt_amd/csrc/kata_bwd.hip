@@ -74,7 +74,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_bwd_dq_kerne
 #pragma unroll
   for (int kk = 0; kk < DV / 16; ++kk) {
     doop[kk] = tvalid ? ld8<T>(dout + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
-    const v8_t<T> ov = tvalid ? ld8<T>(o + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
+    const v8_t<T> ov = (tvalid && o) ? ld8<T>(o + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
 #pragma unroll
     for (int j = 0; j < 8; ++j) dpart += (float)ov[j] * (float)doop[kk][j];
   }
@@ -458,7 +458,7 @@ __global__ __launch_bounds__(256, 2) void kata_bwd_dq_tile_kernel(
 #pragma unroll
   for (int kk = 0; kk < DV / 16; ++kk) {
     doop[kk] = tvalid ? ld8<T>(dsrc + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
-    ov[kk] = tvalid ? ld8<T>(o + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
+    ov[kk] = (tvalid && o) ? ld8<T>(o + qrow * DV + 16 * kk + 8 * hh) : zero8<T>();
   }
   if constexpr (ONORM) {
     // output RMSNorm backward, y = o r w with r = rstd:

@@ -17,7 +17,7 @@ struct KataArgs {
   const void* k;     // (B, T, H, DK)
   const void* v;     // (B, T, H, DV)
   const float* c;    // (B, T, HQ) cumulative log-decay, or null
-  void* o;           // (B, T, HQ, DV)
+  void* o;           // (B, T, HQ, DV); backward: null reads as zero (delta = 0; internal callers)
   float* den;        // (B, T, HQ)
   const void* dout;  // (B, T, HQ, DV) upstream gradient (backward only)
   void* dq;          // (B, T, HQ, DK)
@@ -168,8 +168,7 @@ DKataLayout dkata_layout(int B, int T, int H, int D, int DV, int eb);
 // Backward scratch of the SPD delta rule, after the forward's workspace.
 struct DKataBwdLayout {
   size_t dOp;   // (B, T, H, DV) T: do' = do / (den + eps) (or do)
-  size_t O16;   // (B, T, H, DV) T: the normalised output (or zeros)
-  size_t Zo;    // (B, T, H, DV) T: zeros, the erase pass's o
+  size_t O16;   // (B, T, H, DV) T: the normalised output (normalize only)
   size_t ones;  // (B, T, H) f32: 1, the KATA backward's den
   size_t kws;   // KATA backward workspace
   size_t dU;    // (B, T, H, DV) T: readout VJP, KATA backward's dv
