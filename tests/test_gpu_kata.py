@@ -298,10 +298,14 @@ def test_dense_dk128(P, shape, variant, dtype):
     tol = TOL[dtype]
     fl = grad_floors(q, k, v, do)
     if variant == "decay":
-        if HQ != H:
-            pytest.skip("the decayed score takes HQ = H")
-        c = -torch.cumsum(torch.rand(B, T, H, generator=torch.Generator().manual_seed(T)) * 0.1, 1)
-        o_ref, *refs = K.kata_decay_fwd_bwd(q, k, v, c, do, M)
+        c = -torch.cumsum(torch.rand(B, T, HQ, generator=torch.Generator().manual_seed(T)) * 0.1, 1)
+        # GQA: the oracle's decayed form over k, v repeated to the query heads
+        # (query head hq reads kv head hq // G); dk, dv of a kv head are the
+        # sums over its G query heads
+        G = HQ // H
+        o_ref, dq_r, dk_r, dv_r, dc_r = K.kata_decay_fwd_bwd(
+            q, k.repeat_interleave(G, dim=2), v.repeat_interleave(G, dim=2), c, do, M)
+        refs = (dq_r, dk_r.reshape(B, T, H, G, -1).sum(3), dv_r.reshape(B, T, H, G, -1).sum(3), dc_r)
         leaves = [x.to(dev).requires_grad_(True) for x in (q, k, v, c)]
         o = P.parallel_kata_attn_decay(*leaves, num_groups=M)
         names = ("dq", "dk", "dv", "dc")
