@@ -337,16 +337,16 @@ __global__ __launch_bounds__(256, 2) void delta_prep_kernel(DeltaArgs a, DeltaLa
 // Two copy waves issue W, Kd^T (ungated: the chunk's k rows, read
 // transposed) and this workgroup's U^T rows two chunks ahead into a ring of
 // three slots, and store the v_new^T / h^T blocks the compute wave staged
-// one chunk earlier.  W, Kd^T and U^T rows are stored XOR-swizzled by
+// one chunk earlier (and the output wave's o blocks).  W, Kd^T and U^T rows are stored XOR-swizzled by
 // 16-byte chunk so the operand reads of 16 consecutive rows hit distinct
 // banks.  The output wave forms the workgroup's 32 columns of
 //   o = scale e^G (Q h) + Aqk v_new
 // for each chunk from the same staged h^T and v_new^T blocks while the
 // compute wave runs the next chunk, with q and Aqk rows loaded one chunk
 // ahead into registers, so no output pass reads h and v_new back.  It
-// stages o for the copy waves' stores and issues none itself: its loads
-// would otherwise wait for its stores (a load is waited for by count only
-// when no store was issued after it), and the chain for the output wave.
+// stages o for the copy waves, which store it two barriers later.  Every
+// store of the pass is non-temporal: the written lines then leave L2 first
+// and do not evict the W / k tiles the head's workgroups share there.
 // ---------------------------------------------------------------------------
 
 template <typename T, int DK, int DV, bool GATED>
@@ -504,8 +504,6 @@ __global__ __launch_bounds__(state_threads<DV>()) void delta_state_fwd_kernel(
         dma16s(Ug + (size_t)c * NW * SPLIT * UT16 * 16, 16u * swz_slot<KCPR>((64 * op + lane) / KCPR, lane % KCPR),
                sl + 2 * WT16 + 64 * op);
     };
-    // staged outputs of chunk c: v_new^T and h^T rows (ci DV + 32 g2); copy
-    // wave cw stores the blocks with index cw modulo the copy waves
     // o rows of chunk c in the compute wave's columns: copy wave cw stores
     // block cw (rows 32 cw ..) of Ostg[c & 1]
     T* oh = (T*)a.o + ((size_t)b * Tn * a.H + h) * DV + 32 * (gw - w);
@@ -514,6 +512,8 @@ __global__ __launch_bounds__(state_threads<DV>()) void delta_state_fwd_kernel(
       flush_rows32<T, kStoreStream>(Ostg[c & 1][cw], oh + (size_t)r0 * a.H * DV, (int64_t)a.H * DV, lane, Tn - r0);
     };
     static_assert(NCW == 2, "one o block per copy wave");
+    // staged outputs of chunk c: v_new^T and h^T rows (ci DV + 32 g2); copy
+    // wave cw stores the blocks with index cw modulo the copy waves
     auto flush = [&](int c) __attribute__((always_inline)) {
       const size_t ci = (size_t)bh * NT + c;
 #pragma unroll
@@ -690,7 +690,7 @@ __global__ __launch_bounds__(state_threads<DV>()) void delta_state_fwd_kernel(
     if (c + 2 < NT) step(IntC<2>{}, c + 2);
   }
   block_barrier();  // the last chunk's staged outputs are complete for the copy wave
-  block_barrier();  // (the output wave's last o)
+  block_barrier();  // the output wave's last o is staged (a barrier every wave takes)
 
   if (a.ht) {
 #pragma unroll
