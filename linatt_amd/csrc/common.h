@@ -309,13 +309,16 @@ __device__ __forceinline__ v4_t<T> ds_tr4(const T* p) {
 // MFMA operand with k running down the rows of a natural tile: lane
 // (column c0 + (lane & 31)) receives rows r0 + 16 j + 4 hh + 0..3 and
 // r0 + 16 j + 8 + 4 hh + 0..3, the same k order as ld_tr_op on the
-// transposed tile.
+// transposed tile.  r0 is a multiple of 16.
 template <typename T>
 __device__ __forceinline__ v8_t<T> tile_tr8(const T* tile, int r0, int c0, int j, int lane) {
   const int g = lane >> 4, i = lane & 15;
-  const int row = r0 + 16 * j + 4 * (g >> 1) + (i >> 2);
+  const int row = 4 * (g >> 1) + (i >> 2);
   const int col = c0 + 16 * (g & 1) + 4 * (i & 3);
-  const char* base = reinterpret_cast<const char*>(tile);
+  // the slot depends on row bits 1-3 only, so rows r0 + 16 j + .. are the
+  // lane's rows moved by a plain byte offset (an immediate of the read where
+  // r0 and j are constants; the lane part is then loop-invariant)
+  const char* base = reinterpret_cast<const char*>(tile) + (r0 + 16 * j) * 128;
   return cat44<T>(ds_tr4<T>(reinterpret_cast<const T*>(base + tile_off(row, col))),
                   ds_tr4<T>(reinterpret_cast<const T*>(base + tile_off(row + 8, col))));
 }
@@ -396,13 +399,14 @@ __device__ __forceinline__ void c_to_b16x2(const f32x16& x, v8_t<T>& b0, v8_t<T>
 
 // The A operand matching c_to_b16x2 from a natural 64 x 64 tile (tile_off
 // layout): lane (rho, i) receives column c0 + i of rows r0 + t0(rho) + 0..3
-// and r0 + t0(rho) + 8..11 (two transposing 8-byte reads).
+// and r0 + t0(rho) + 8..11 (two transposing 8-byte reads).  r0 is a
+// multiple of 16 (a plain byte offset, as in tile_tr8).
 template <typename T>
 __device__ __forceinline__ v8_t<T> tile_tr8_16(const T* tile, int r0, int c0, int lane) {
   const int rho = lane >> 4, i = lane & 15;
-  const int row = r0 + 16 * (rho & 1) + 4 * (rho >> 1) + (i >> 2);
+  const int row = 16 * (rho & 1) + 4 * (rho >> 1) + (i >> 2);
   const int col = c0 + 4 * (i & 3);
-  const char* base = reinterpret_cast<const char*>(tile);
+  const char* base = reinterpret_cast<const char*>(tile) + r0 * 128;
   return cat44<T>(ds_tr4<T>(reinterpret_cast<const T*>(base + tile_off(row, col))),
                   ds_tr4<T>(reinterpret_cast<const T*>(base + tile_off(row + 8, col))));
 }

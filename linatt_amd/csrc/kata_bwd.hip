@@ -924,7 +924,7 @@ __global__ __launch_bounds__(64 * kata_dkdv_waves<DK>(), 2) void kata_bwd_dkdv_t
         // x[t][s] = dO V^T - delta  (rows t, column s; bf16: both prescaled)
 #pragma unroll
         for (int kk = 0; kk < DV / 16; ++kk)
-          x = mma(tile_ld8<T>(Os, 32 * mb + cl, 16 * kk + 8 * hh), vop(kk), x);
+          x = mma(tile_ld8<T>(Os + 2048 * mb, cl, 16 * kk + 8 * hh), vop(kk), x);
         if constexpr (DECAY) {
 #pragma unroll
           for (int e = 0; e < 16; ++e)
@@ -951,7 +951,7 @@ __global__ __launch_bounds__(64 * kata_dkdv_waves<DK>(), 2) void kata_bwd_dkdv_t
             f32x16 r{};
 #pragma unroll
             for (int kk = 0; kk < KE; ++kk)
-              r = mma(wtile_ld8<T>(Qs, 32 * mb + cl, gi * E + 16 * kk + 8 * hh), kop(gk * KE + kk), r);
+              r = mma(wtile_ld8<T>(Qs + 2048 * mb, cl, gi * E + 16 * kk + 8 * hh), kop(gk * KE + kk), r);
             A += r * r;
             const f32x16 da = r * xs;
             if constexpr (k16) {

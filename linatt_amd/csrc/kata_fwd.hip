@@ -200,9 +200,10 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void kata_fwd_kernel(
 // scalar base: the VALU, which bounds this kernel, only does the math.
 // EPI: 0 writes o; 1 also the output RMSNorm's y and rstd; 2 the float32
 // numerator o den instead of o (compile-time, so each variant carries only
-// its own epilogue)
+// its own epilogue).  Three waves per SIMD at dk = 64 (at most 168 VGPRs;
+// the compiler otherwise lets some variants grow just past it)
 template <typename T, int DK, int DV, int M, bool SUM, bool DECAY, int EPI>
-__global__ __launch_bounds__(256, 2) void kata_fwd_tile_kernel(
+__global__ __launch_bounds__(256, DK == 64 ? 3 : 2) void kata_fwd_tile_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const float* __restrict__ c, T* __restrict__ o, float* __restrict__ den,
     int Tn, int HQ, int H, float scale2, int nqt, int nbh, OutNorm on) {
