@@ -925,10 +925,15 @@ __global__ __launch_bounds__(64 * kata_dkdv_waves<DK>(), 2) void kata_bwd_dkdv_t
 #pragma unroll
         for (int kk = 0; kk < DV / 16; ++kk)
           x = mma(tile_ld8<T>(Os + 2048 * mb, cl, 16 * kk + 8 * hh), vop(kk), x);
+        // decayed score: the factors exp(min(c_t - c_s, 0)) once per block,
+        // for x here and for A after the group loop
+        f32x16 dec;
         if constexpr (DECAY) {
 #pragma unroll
-          for (int e = 0; e < 16; ++e)
-            x[e] *= __expf(fminf(Ct[buf][32 * mb + 8 * (e >> 2) + 4 * hh + (e & 3)] - csl, 0.f));
+          for (int e = 0; e < 16; ++e) {
+            dec[e] = __expf(fminf(Ct[buf][32 * mb + 8 * (e >> 2) + 4 * hh + (e & 3)] - csl, 0.f));
+            x[e] *= dec[e];
+          }
         }
         f32x16 xs;
         if constexpr (kPre) {
@@ -980,7 +985,7 @@ __global__ __launch_bounds__(64 * kata_dkdv_waves<DK>(), 2) void kata_bwd_dkdv_t
             const float dd = Ct[buf][32 * mb + 8 * (e >> 2) + 4 * hh + (e & 3)] - csl;
             // column part of dc_s: -sum_t dA A [c_t - c_s <= 0] (xs carries the decay)
             dcc -= dd <= 0.f ? xs[e] * A[e] : 0.f;
-            A[e] *= __expf(fminf(dd, 0.f));
+            A[e] *= dec[e];
           }
         }
         // bf16: P = A against the prescaled dO; fp16 keeps P in [0, 2^12]
