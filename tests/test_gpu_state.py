@@ -41,7 +41,8 @@ def S_():
 
 @pytest.mark.parametrize("M", [4, 2])
 @pytest.mark.parametrize("case", [(1, 1, 1, 128), (2, 300, 2, 128), (1, 1000, 3, 256),
-                                  (1, 640, 2, 128), (2, 257, 1, 1024)],
+                                  (1, 640, 2, 128), (2, 257, 1, 1024), (1, 800, 4, 512),
+                                  (2, 1000, 4, 256)],
                          ids=lambda c: "B{}T{}H{}L{}".format(*c))
 def test_prefill_parity(S_, M, case):
     B, T, H, Lseg = case
