@@ -356,30 +356,37 @@ def bench_delta_kata(steps, settle_s):
     bws = torch.empty(L.linatt_dkata_bwd_workspace_bytes(B, T, H, D, D, dt), device=dev,
                       dtype=torch.uint8)
 
-    def fwd():
-        _lib.check("linatt_dkata_fwd_train", L.linatt_dkata_fwd_train(
-            P(qd), P(kd), P(vd), P(bd), P(U), P(o), P(den), P(ws), B, T, H, D, D, M, scale, 0,
-            1e-5, dt, sp))
+    def timed(norm):
+        """(fwd ms, bwd ms) with normalize = norm: o = num / (den + eps), whose
+        backward also reads o."""
+        def fwd():
+            _lib.check("linatt_dkata_fwd_train", L.linatt_dkata_fwd_train(
+                P(qd), P(kd), P(vd), P(bd), P(U), P(o), P(den), P(ws), B, T, H, D, D, M, scale,
+                norm, 1e-5, dt, sp))
 
-    def bwd():
-        _lib.check("linatt_dkata_bwd", L.linatt_dkata_bwd(
-            P(qd), P(kd), P(vd), P(bd), P(U), None, P(den), P(do), P(dq), P(dk), P(dv),
-            P(dbeta), P(ws), P(bws), B, T, H, D, D, M, scale, 0, 1e-5, dt, sp))
+        def bwd():
+            _lib.check("linatt_dkata_bwd", L.linatt_dkata_bwd(
+                P(qd), P(kd), P(vd), P(bd), P(U), P(o) if norm else None, P(den), P(do), P(dq),
+                P(dk), P(dv), P(dbeta), P(ws), P(bws), B, T, H, D, D, M, scale, norm, 1e-5, dt, sp))
 
-    parts = [("fwd", fwd), ("bwd", bwd)]
-    settle(parts, settle_s)
-    stream = torch.cuda.current_stream(dev)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
-    torch.cuda.synchronize()
-    for s_ in range(steps):
-        ev[s_][0].record(stream)
-        fwd()
-        ev[s_][1].record(stream)
-        bwd()
-        ev[s_][2].record(stream)
-    torch.cuda.synchronize()
-    f_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
-    b_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / steps
+        settle([("fwd", fwd), ("bwd", bwd)], settle_s)
+        stream = torch.cuda.current_stream(dev)
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+        torch.cuda.synchronize()
+        for s_ in range(steps):
+            ev[s_][0].record(stream)
+            fwd()
+            ev[s_][1].record(stream)
+            bwd()
+            ev[s_][2].record(stream)
+        torch.cuda.synchronize()
+        return (sum(e[0].elapsed_time(e[1]) for e in ev) / steps,
+                sum(e[1].elapsed_time(e[2]) for e in ev) / steps)
+
+    # the mixer's setting (delta_normalize defaults to False, kata/layer.py:59)
+    # first, then the normalised form
+    f_ms, b_ms = timed(0)
+    fn_ms, bn_ms = timed(1)
     flops = B * H * T * T / 2 * (4 * M * D + 4 * D)
     tf = flops / (f_ms * 1e-3) / 1e12
     return {"config": {"B": B, "H": H, "T": T, "D": D, "num_groups": M, "scale": scale,
@@ -387,7 +394,8 @@ def bench_delta_kata(steps, settle_s):
             "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4),
             "tokens_per_s_fwd_bwd": round(B * T / ((f_ms + b_ms) * 1e-3), 1),
             "fwd_alg_gflop": round(flops / 1e9, 2), "fwd_tflops": round(tf, 1),
-            "fwd_frac_mfma_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+            "fwd_frac_mfma_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+            "normalize_fwd_ms": round(fn_ms, 4), "normalize_bwd_ms": round(bn_ms, 4)}
 
 
 def bench_mixer(steps, settle_s):
@@ -858,6 +866,9 @@ def main():
         # kata_quadratic_sum_m4_200m.yaml: 12 heads of 64, four groups
         "sum_m4_h12_d64": bench_kata_variant(vs, args.settle_seconds / 3, 8, 12, 2048, 64, 64, 4,
                                              "sum", False, 9),
+        # kata_quadratic_sum_m2_200m.yaml: the same heads, two groups
+        "sum_m2_h12_d64": bench_kata_variant(vs, args.settle_seconds / 3, 8, 12, 2048, 64, 64, 2,
+                                             "sum", False, 11),
         # kataconv_cat_l2_gdn_340m.yaml: 16 heads, decayed concat score over
         # offset-packed groups (dk = 128, dv = 64, two groups)
         "decay_m2_h16_dk128": bench_kata_variant(vs, args.settle_seconds / 3, 8, 16, 2048, 128, 64,
