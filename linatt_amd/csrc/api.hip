@@ -146,11 +146,12 @@ struct StateWs {
 StateWs state_ws(int B, int T, int H, int dk, int dv, int M, int L, int dtype) {
   StateWs w{};
   const size_t E = dk / M, P = M * E * E, BH = (size_t)B * H, nseg = (T + L - 1) / L;
+  const size_t PP = 3 * P / 4;  // packed state rows (symmetric pairs; kata_state.hip)
   auto al = [](size_t x) { return (x + 255) & ~size_t(255); };
   size_t off = 0;
-  w.seg_S = off; off = al(off + BH * nseg * dv * P * 4);
+  w.seg_S = off; off = al(off + BH * nseg * dv * PP * 4);
   w.seg_z = off; off = al(off + BH * nseg * P * 4);
-  w.HT = off; off = al(off + BH * nseg * dv * P * elt_bytes(dtype));
+  w.HT = off; off = al(off + BH * nseg * dv * PP * elt_bytes(dtype));
   w.Hz = off; off = al(off + BH * nseg * P * 4);
   w.bytes = off;
   return w;

@@ -96,9 +96,9 @@ struct KataStateArgs {
   void* o;
   float* den;          // (B, T, H) or strided like o without the feature dim
   int64_t sb, st, sh, vsb, vst, vsh, osb, ost, osh, dsb, dst, dsh;
-  float* seg_S;        // (B*H, nseg, DV, P) f32 scratch, per-segment Psi(K)^T V transposed
+  float* seg_S;        // (B*H, nseg, DV, 3P/4) f32 scratch, per-segment Psi(K)^T V transposed, packed rows
   float* seg_z;        // (B*H, nseg, P) f32 scratch
-  void* HT;            // (B*H, nseg, DV, P) T scratch, exclusive prefix (unscaled)
+  void* HT;            // (B*H, nseg, DV, 3P/4) T scratch, weighted exclusive prefix (unscaled), packed rows
   float* Hz;           // (B*H, nseg, P) f32 scratch
   float* S_out;        // (B, H, P, DV) f32 final state psi(sqrt(scale) k) v^T, or null
   float* z_out;        // (B, H, P) f32, or null

@@ -11,7 +11,7 @@
 // identity "decode after n tokens == row n of the parallel form".
 //
 // Prefill here splits T into segments of L tokens (L a multiple of 128):
-//   kata_seg_state_kernel   per (b, h, segment, 128 state rows):
+//   kata_seg_state_kernel   per (b, h, segment, 768 packed state rows):
 //                           S_seg = Psi(K_seg)^T V_seg, z_seg = Psi(K_seg)^T 1
 //                           (MFMA; the psi features are formed in registers
 //                           from a transposed K tile in LDS)
@@ -23,28 +23,57 @@
 // State rows are p = g E^2 + a E + b.  Inside the prefill psi is unscaled
 // (o is scale-invariant); the returned state is psi(sqrt(scale) x) as in the
 // reference, i.e. the unscaled sums times scale.
+//
+// Packed rows: psi(x)_g = vec(x_g x_g^T) is symmetric in (a, b), so the
+// segment states and the prefix keep 3/4 of each group's rows (pk_ab): the
+// rows a < E/2 with every b, then the rows a >= E/2 with b >= E/2.  Each
+// unordered pair {a, b} is one of them with a <= b, and the scan folds the
+// pair weight c_ab (2 for a < b, 1 for a = b, 0 for the rows below the
+// diagonal, which repeat a pair) into the prefix state, so
+// psi(q)^T H = sum over packed rows of q_a q_b (c_ab H_ab).  z stays in the
+// full layout (the den product reads it as E x E blocks), and the returned
+// state is unpacked to the full layout.
 #include "common.h"
 #include "kata_kernels.h"
 
 namespace linatt {
 
+// packed rows per group, and (a, b) of packed row r of a group
+template <int E>
+constexpr int kPkRows = 3 * E * E / 4;
+template <int E>
+__host__ __device__ __forceinline__ void pk_ab(int r, int& a, int& b) {
+  if (r < E * E / 2) {
+    a = r / E;
+    b = r % E;
+  } else {
+    const int s = r - E * E / 2;
+    a = E / 2 + s / (E / 2);
+    b = E / 2 + s % (E / 2);
+  }
+}
+// weight of packed pair (a, b) in psi(q)^T H
+__host__ __device__ __forceinline__ float pk_weight(int a, int b) { return b < a ? 0.f : (a == b ? 1.f : 2.f); }
+
 // ---------------------------------------------------------------------------
-// Segment states.  One workgroup of 8 waves covers 1024 state rows of one
-// (b, h, segment), so each key/value tile is read once per 1024 rows; wave w
-// owns rows p = 1024 pb + 128 w + 32 i4 + [0, 32), i4 = 0..3 (its X-operand
-// rows).  K^T sits in LDS as fp32 so the psi products need no unpacking.
+// Segment states.  One workgroup of 8 waves covers 768 packed state rows of
+// one (b, h, segment), so each key/value tile is read once per 768 rows; wave
+// w owns packed rows p = 768 pb + 96 w + 32 i4 + [0, 32), i4 = 0..2 (its
+// X-operand rows).  K^T sits in LDS as fp32 so the psi products need no
+// unpacking.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, int M>
 __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
-  constexpr int E = DK / M, P = M * E * E;
+  constexpr int E = DK / M, P = M * E * E, PR = kPkRows<E>, PP = M * PR;
   constexpr int PK = 64 + 4;  // fp32 K^T pitch
   constexpr int PV = 64 + 8;  // V^T pitch
-  constexpr int NPB = P / 1024;
-  static_assert(P % 1024 == 0, "1024 state rows per workgroup");
+  constexpr int WR = 768, NI = WR / 256;  // rows per workgroup, 32-row blocks per wave
+  constexpr int NPB = PP / WR;
+  static_assert(PP % WR == 0 && (M == 2 || M == 4), "768 packed rows per workgroup");
   // one LDS area: K^T (fp32) | V^T | per-wave partial 32 x 32 tiles of the
   // Gram matrix K^T K (z, below) during the key loop, then the stage of
   // S_seg^T: VC value rows of 1024 state rows (pitch SP) per pass
-  constexpr int VC = 16, SP = 1024 + 4;
+  constexpr int VC = 16, SP = WR + 4;
   constexpr int LOOPF = DK * PK + DV * PV * (int)sizeof(T) / 4 + 8 * 1024;
   constexpr int LDSF = LOOPF > VC * SP ? LOOPF : VC * SP;
   __shared__ __attribute__((aligned(16))) float Lds[LDSF];
@@ -62,14 +91,15 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
   const T* kb = (const T*)a.k + (int64_t)b * a.sb + (int64_t)h * a.sh;
   const T* vb = (const T*)a.v + (int64_t)b * a.vsb + (int64_t)h * a.vsh;
 
-  const int p0 = 1024 * pb + 128 * w;
-  int ra[4], rb[4];
+  const int p0 = WR * pb + 96 * w;
+  int ra[NI], rb[NI];
 #pragma unroll
-  for (int i4 = 0; i4 < 4; ++i4) {
-    const int p = p0 + 32 * i4 + cl;
-    const int g = p / (E * E);
-    ra[i4] = g * E + (p / E) % E;
-    rb[i4] = g * E + p % E;
+  for (int i4 = 0; i4 < NI; ++i4) {
+    const int p = p0 + 32 * i4 + cl, g = p / PR;
+    int ga, gb;
+    pk_ab<E>(p % PR, ga, gb);
+    ra[i4] = g * E + ga;
+    rb[i4] = g * E + gb;
   }
   // K^T row d holds keys in groups of four, group q at 4 (q ^ ((d >> 4) & 3)):
   // the conversion's 16-lane f32x4 writes (rows 4 cb + cc, groups rq) then
@@ -86,18 +116,18 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
     vo[vt][0] = b0 + fs;  // even s: s ^ (f >> 1) = s + (f >> 1)
     vo[vt][1] = b0 - fs;  // odd s: s ^ (f >> 1) = s - (f >> 1)
   }
-  int ko[4][4];  // per i4: rows ra (key groups 2 hh, 2 hh + 1) and rb, before + 16 s
+  int ko[4][NI];  // per i4: rows ra (key groups 2 hh, 2 hh + 1) and rb, before + 16 s
 #pragma unroll
-  for (int i4 = 0; i4 < 4; ++i4) {
+  for (int i4 = 0; i4 < NI; ++i4) {
     ko[0][i4] = kt_off(ra[i4], 2 * hh);
     ko[1][i4] = kt_off(ra[i4], 2 * hh + 1);
     ko[2][i4] = kt_off(rb[i4], 2 * hh);
     ko[3][i4] = kt_off(rb[i4], 2 * hh + 1);
   }
 
-  f32x16 acc[4][DV / 32];
+  f32x16 acc[NI][DV / 32];
 #pragma unroll
-  for (int i4 = 0; i4 < 4; ++i4)
+  for (int i4 = 0; i4 < NI; ++i4)
 #pragma unroll
     for (int vt = 0; vt < DV / 32; ++vt) acc[i4][vt] = f32x16{};
   // z_p = sum_s k_s[ra] k_s[rb] = (K^T K)[ra][rb]: the workgroup's rows need
@@ -149,7 +179,7 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
 #pragma unroll
       for (int vt = 0; vt < DV / 32; ++vt) vop[vt] = ld8<T>(Vt + vo[vt][s & 1] + 16 * s);
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
+      for (int i4 = 0; i4 < NI; ++i4) {
         const f32x4 a0 = *reinterpret_cast<const f32x4*>(Kt + ko[0][i4] + 16 * s);
         const f32x4 a1 = *reinterpret_cast<const f32x4*>(Kt + ko[1][i4] + 16 * s);
         const f32x4 c0 = *reinterpret_cast<const f32x4*>(Kt + ko[2][i4] + 16 * s);
@@ -178,61 +208,83 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
 #pragma unroll
   for (int e = 0; e < 16; ++e) Gp[w][(8 * (e >> 2) + 4 * hh + (e & 3)) * 32 + cl] = gz[e];
   __syncthreads();
+  // z in the full layout: each unordered pair is the packed row with
+  // ra <= rb, which writes both of its entries
 #pragma unroll
-  for (int i4 = 0; i4 < 4; ++i4) {
+  for (int i4 = 0; i4 < NI; ++i4) {
     const int u = (ra[i4] >> 5) == gt_i(0) && (rb[i4] >> 5) == gt_j(0) ? 0 : 1;
     const int o = (ra[i4] & 31) * 32 + (rb[i4] & 31);
     const float z = (Gp[4 * u][o] + Gp[4 * u + 1][o]) + (Gp[4 * u + 2][o] + Gp[4 * u + 3][o]);
-    if (hh == 0) a.seg_z[((size_t)bh * a.nseg + seg) * P + p0 + 32 * i4 + cl] = z;
+    if (hh == 0 && ra[i4] <= rb[i4]) {
+      const int g = ra[i4] / E, za = ra[i4] % E, zb = rb[i4] % E;
+      float* zs = a.seg_z + ((size_t)bh * a.nseg + seg) * P + g * E * E;
+      zs[za * E + zb] = z;
+      if (za != zb) zs[zb * E + za] = z;
+    }
   }
-  // acc[i4][vt] = D[p'][v]: rows p' = 128 w + 32 i4 + 8 I + 4 hh + r of the
-  // workgroup's 1024, lane column v = 32 vt + cl  ->  stage [v - vc0][p'],
-  // then S_seg^T [v][1024 pb + p'] rows by whole 16-byte runs
-  float* st = a.seg_S + ((size_t)bh * a.nseg + seg) * DV * P + 1024 * pb;
+  // acc[i4][vt] = D[p'][v]: rows p' = 96 w + 32 i4 + 8 I + 4 hh + r of the
+  // workgroup's 768, lane column v = 32 vt + cl  ->  stage [v - vc0][p'],
+  // then S_seg^T [v][768 pb + p'] rows by whole 16-byte runs
+  float* st = a.seg_S + ((size_t)bh * a.nseg + seg) * DV * PP + WR * pb;
 #pragma unroll
   for (int pass = 0; pass < DV / VC; ++pass) {
     const int vc0 = VC * pass, vt = vc0 / 32, vl = 32 * vt + cl - vc0;
     __syncthreads();  // the Gram partials (or the previous pass) are read
     if (vl >= 0 && vl < VC) {
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4)
+      for (int i4 = 0; i4 < NI; ++i4)
 #pragma unroll
         for (int I = 0; I < 4; ++I)
-          *reinterpret_cast<f32x4*>(Lds + vl * SP + 128 * w + 32 * i4 + 8 * I + 4 * hh) =
+          *reinterpret_cast<f32x4*>(Lds + vl * SP + 96 * w + 32 * i4 + 8 * I + 4 * hh) =
               f32x4{acc[i4][vt][4 * I], acc[i4][vt][4 * I + 1], acc[i4][vt][4 * I + 2], acc[i4][vt][4 * I + 3]};
     }
     __syncthreads();
+    static_assert(VC * WR / 4 % 512 == 0, "whole store rounds");
 #pragma unroll
-    for (int it = 0; it < VC * 1024 / 4 / 512; ++it) {
-      const int idx = 512 * it + tid, row = idx / 256, c4 = idx % 256;
-      *reinterpret_cast<f32x4*>(st + (size_t)(vc0 + row) * P + 4 * c4) =
+    for (int it = 0; it < VC * WR / 4 / 512; ++it) {
+      const int idx = 512 * it + tid, row = idx / (WR / 4), c4 = idx % (WR / 4);
+      *reinterpret_cast<f32x4*>(st + (size_t)(vc0 + row) * PP + 4 * c4) =
           *reinterpret_cast<const f32x4*>(Lds + row * SP + 4 * c4);
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Exclusive prefix over segments.  One thread per (bh, row v in [0, DV]
-// (row DV is z), 4 consecutive state rows p).
+// Exclusive prefix over segments.  One thread per (bh, value row v, 4
+// consecutive packed state rows, which share their a), then one per (bh, 4
+// consecutive full rows of z).  The prefix state is written as c_ab H_ab.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, int M>
 __global__ __launch_bounds__(256) void kata_seg_scan_kernel(KataStateArgs a) {
-  constexpr int E = DK / M, P = M * E * E;
-  const int64_t per_bh = (int64_t)(DV + 1) * (P / 4);
+  constexpr int E = DK / M, P = M * E * E, PR = kPkRows<E>, PP = M * PR;
+  static_assert(PR % 4 == 0 && (E / 2) % 4 == 0, "4 packed rows share their a");
+  constexpr int64_t nS = (int64_t)DV * (PP / 4), per_bh = nS + P / 4;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)a.B * a.H * per_bh) return;
   const int bh = (int)(idx / per_bh);
   const int64_t rem = idx % per_bh;
-  const int v = (int)(rem / (P / 4));
-  const int p = 4 * (int)(rem % (P / 4));
+  const bool isS = rem < nS;
+  const int v = isS ? (int)(rem / (PP / 4)) : DV;
+  // packed row (S) or full row (z), 4 consecutive
+  const int p = isS ? 4 * (int)(rem % (PP / 4)) : 4 * (int)(rem - nS);
+  // S: the rows' pair (a, b0 + j) of group g, their full rows and weights
+  int g = 0, pa = 0, pb0 = 0;
+  if (isS) {
+    g = p / PR;
+    pk_ab<E>(p % PR, pa, pb0);
+  }
+  const int pf0 = g * E * E + pa * E + pb0;  // full row of (a, b0)
+  float cw[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) cw[j] = pk_weight(pa, pb0 + j);
   // the running sum starts from the initial state (stored scaled by
   // `scale`; the scan runs unscaled); each thread reads, then writes, only
   // its own state elements, so S_in may alias S_out
   float4 run = make_float4(0.f, 0.f, 0.f, 0.f);
   if (a.S_in) {
     const float is = 1.f / a.scale;
-    if (v < DV) {
-      const float* si = a.S_in + ((size_t)bh * P + p) * DV + v;
+    if (isS) {
+      const float* si = a.S_in + ((size_t)bh * P + pf0) * DV + v;
       run = make_float4(si[0] * is, si[DV] * is, si[2 * DV] * is, si[3 * DV] * is);
     } else {
       const float4 zi = *reinterpret_cast<const float4*>(a.z_in + (size_t)bh * P + p);
@@ -242,27 +294,33 @@ __global__ __launch_bounds__(256) void kata_seg_scan_kernel(KataStateArgs a) {
   for (int seg = 0; seg < a.nseg; ++seg) {
     const size_t base = (size_t)bh * a.nseg + seg;
     float4 x;
-    if (v < DV) {
-      x = *reinterpret_cast<const float4*>(a.seg_S + (base * DV + v) * P + p);
-      st4<T>((T*)a.HT + (base * DV + v) * P + p, to4<T>(run.x, run.y, run.z, run.w));
+    if (isS) {
+      x = *reinterpret_cast<const float4*>(a.seg_S + (base * DV + v) * PP + p);
+      st4<T>((T*)a.HT + (base * DV + v) * PP + p,
+             to4<T>(run.x * cw[0], run.y * cw[1], run.z * cw[2], run.w * cw[3]));
     } else {
       x = *reinterpret_cast<const float4*>(a.seg_z + base * P + p);
       *reinterpret_cast<float4*>(a.Hz + base * P + p) = run;
     }
     run.x += x.x; run.y += x.y; run.z += x.z; run.w += x.w;
   }
-  const float s = a.scale;
-  if (v < DV) {
+  const float sc = a.scale;
+  if (isS) {
     if (a.S_out) {
-      float* so = a.S_out + ((size_t)bh * P + p) * DV + v;
-      so[0] = run.x * s;
-      so[DV] = run.y * s;
-      so[2 * DV] = run.z * s;
-      so[3 * DV] = run.w * s;
+      // full layout: rows (a, b) with a <= b write both entries of the pair
+      float* so = a.S_out + (size_t)bh * P * DV + v;
+      const float r4[4] = {run.x * sc, run.y * sc, run.z * sc, run.w * sc};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int b = pb0 + j;
+        if (b < pa) continue;
+        so[(size_t)(pf0 + j) * DV] = r4[j];
+        if (b != pa) so[(size_t)(g * E * E + b * E + pa) * DV] = r4[j];
+      }
     }
   } else if (a.z_out) {
     *reinterpret_cast<float4*>(a.z_out + (size_t)bh * P + p) =
-        make_float4(run.x * s, run.y * s, run.z * s, run.w * s);
+        make_float4(run.x * sc, run.y * sc, run.z * sc, run.w * sc);
   }
 }
 
@@ -331,21 +389,22 @@ __global__ __launch_bounds__(256, 2) void kata_prefill_out_kernel(KataStateArgs 
   // prefix is the initial state, or zero
   if (seg > 0 || a.S_in) {
     const size_t base = (size_t)bh * a.nseg + seg;
-    const u32x4* hT = reinterpret_cast<const u32x4*>((const T*)a.HT + base * DV * P);
+    constexpr int PR = kPkRows<E>, PP = M * PR, NC = PP / HCH, KSG = PR / 16;
+    static_assert(PP % HCH == 0 && (E == 16 || E == 32), "whole chunks of packed rows");
+    const u32x4* hT = reinterpret_cast<const u32x4*>((const T*)a.HT + base * DV * PP);
     const float* hz = a.Hz + base * P;
-    constexpr int NC = P / HCH;
-    // chunk c: rows v of H^T, columns [128 c, 128 c + 128); 16 KiB = 4 x 1 KiB per wave
+    // chunk c: rows v of H^T, packed columns [128 c, 128 c + 128); 16 KiB = 4 x 1 KiB per
+    // wave, from a scalar base per chunk plus these chunk-invariant lane offsets
+    unsigned hoff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = (64 * (4 * w + i) + lane) / HCPR, slot = lane % HCPR;
+      hoff[i] = (unsigned)((row * (PP / 8) + (slot ^ (row & 15))) * 16);
+    }
     auto issue = [&](int c) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int op = 4 * w + i;
-        const int row = (64 * op + lane) / HCPR, slot = lane % HCPR;
-        const int ch = slot ^ (row & 15);
-        dma16(hT + (size_t)row * (P / 8) + c * HCPR + ch, Hs[c & 1] + 64 * op);
-      }
+      for (int i = 0; i < 4; ++i) dma16s(hT + c * HCPR, hoff[i], Hs[c & 1] + 64 * (4 * w + i));
     };
-    constexpr int NCG = E * E / HCH;  // chunks per group
-    static_assert(NCG * HCH == E * E, "chunks do not straddle groups");
     vm_drain();  // q of this wave's queries is in registers
     issue(0);
     // den's prefix part psi(q).z = sum_g q_g^T Z_g q_g with Z_g[a][b] =
@@ -378,24 +437,38 @@ __global__ __launch_bounds__(256, 2) void kata_prefill_out_kernel(KataStateArgs 
         for (int r = 0; r < 4; ++r) dpart += (float)q4[r] * y[4 * i + r];
       }
     }
-#pragma unroll
-    for (int g = 0; g < M; ++g)
+    // k-step ks of the packed rows (16 of them): group ks / KSG; rows a < E/2
+    // take one a and 16 b's, as do E = 32's rows a >= 16 (b = 16..31);
+    // E = 16's rows a >= 8 pair up, a = 8 + 2 i + hh per lane half, both on
+    // b = 8..15.  q_a and the lane's eight q_b come from the LDS copy of its
+    // query row, so the k-step may be a runtime index
 #pragma unroll 1
-    for (int cc = 0; cc < NCG; ++cc) {
-      const int c = g * NCG + cc;
+    for (int c = 0; c < NC; ++c) {
       vm_wait_barrier<0>();
       if (c + 1 < NC) issue(c + 1);
       if (tw < Tn) {
         const u32x4* Hb = Hs[c & 1];
 #pragma unroll
         for (int j = 0; j < HCH / 16; ++j) {
-          const int ai = (HCH * cc + 16 * j) / E;
-          const int b0 = (16 * j) % E;  // HCH * cc is a multiple of E
-          const int kk = (g * E + b0) / 16;
-          const float qa = (float)qa_row[g * E + ai];
+          const int ks = c * (HCH / 16) + j, g = ks / KSG, l = ks % KSG;
+          int aU, bU;
+          bool pair = false;
+          if (l < E * E / 32) {
+            aU = 16 * l / E;
+            bU = 16 * l % E;
+          } else if (E == 16) {
+            aU = 8 + 2 * (l - 8);
+            bU = 8;
+            pair = true;
+          } else {
+            aU = E / 2 + (l - E * E / 32);
+            bU = E / 2;
+          }
+          const float qa = (float)qa_row[g * E + aU + (pair ? hh : 0)];
+          const v8_t<T> qb = *reinterpret_cast<const v8_t<T>*>(qa_row + g * E + bU + (pair ? 0 : 8 * hh));
           f32x8 pf;
 #pragma unroll
-          for (int jj = 0; jj < 8; ++jj) pf[jj] = qa * (float)qop[kk][jj];
+          for (int jj = 0; jj < 8; ++jj) pf[jj] = qa * (float)qb[jj];
           const v8_t<T> y = __builtin_convertvector(pf, v8_t<T>);
 #pragma unroll
           for (int db = 0; db < DV / 32; ++db) {
@@ -485,10 +558,10 @@ template <typename T, int DK, int DV, int M>
 hipError_t launch_kata_prefill(const KataStateArgs& a, hipStream_t stream) {
   constexpr int E = DK / M, P = M * E * E;
   const int BH = a.B * a.H;
-  kata_seg_state_kernel<T, DK, DV, M><<<dim3(BH * a.nseg * (P / 1024)), dim3(512), 0, stream>>>(a);
+  kata_seg_state_kernel<T, DK, DV, M><<<dim3(BH * a.nseg * (M * kPkRows<E> / 768)), dim3(512), 0, stream>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int64_t items = (int64_t)BH * (DV + 1) * (P / 4);
+  const int64_t items = (int64_t)BH * (DV * (M * kPkRows<E> / 4) + P / 4);
   kata_seg_scan_kernel<T, DK, DV, M><<<dim3((unsigned)((items + 255) / 256)), dim3(256), 0, stream>>>(a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
