@@ -500,7 +500,9 @@ def bench_state(prefill_reps, decode_steps, settle_s):
     per step (seed 4000+i, all resident on the device before timing).
     Algorithmic prefill work in the O(T) form: states 2 T P dv + readout
     2 T P dv + chunk-local scores (about 105 GFLOP at this shape); decode bytes per step:
-    the fp32 state read + written, 2 B H (P dv + P) 4 + inputs/outputs."""
+    the fp32 state read + written, 2 B H (P dv + P) 4 + inputs/outputs.  The
+    same decode steps also run on the packed state (one row per unordered
+    pair a <= b of each group, P' = M E (E + 1) / 2 rows: decode_packed_*)."""
     import torch
     from linatt_amd import _lib
     L = _lib.load()
@@ -562,9 +564,32 @@ def bench_state(prefill_reps, decode_steps, settle_s):
     e1.record(stream)
     torch.cuda.synchronize()
     dec_ms = e0.elapsed_time(e1) / decode_steps
+
+    # the same steps on the packed state (one row per unordered pair a <= b
+    # of each group: M E (E + 1) / 2 rows instead of M E^2)
+    from linatt_amd import spd_state
+    PT = spd_state.state_rows(D, M, True)
+    Sp1, zp1 = spd_state.pack_state(S, z, M)
+    Sp = Sp1.expand(Bd, H, -1, -1).contiguous()
+    zp = zp1.expand(Bd, H, -1).contiguous()
+
+    def decode_packed(x):
+        _lib.check("linatt_kata_decode_step_packed", L.linatt_kata_decode_step_packed(
+            Pp(x[0]), Pp(x[1]), Pp(x[2]), Pp(Sp), Pp(zp), Pp(od), Bd, H, D, D, M, scale, 1e-6, dt,
+            sp))
+
+    decode_packed(steps[0])
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for x in steps:
+        decode_packed(x)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    decp_ms = e0.elapsed_time(e1) / decode_steps
     pre_flops = 2 * (2 * T * P * D) * B * H + B * H * T * 32 * 2 * D  # states, readout, chunk scores
     pre_bytes = B * H * T * D * 2 * 4 + B * H * T * 4 + B * H * (P * D + P) * 4
     dec_bytes = 2 * Bd * H * (P * D + P) * 4 + Bd * H * 4 * D * 2
+    decp_bytes = 2 * Bd * H * (PT * D + PT) * 4 + Bd * H * 4 * D * 2
     return {"config": {"B": B, "H": H, "T": T, "D": D, "num_groups": M, "seg_len": seg,
                        "decode_batch": Bd, "decode_steps": decode_steps, "seed": 4},
             "prefill_ms": round(pre_ms, 4),
@@ -576,7 +601,11 @@ def bench_state(prefill_reps, decode_steps, settle_s):
             "decode_steps_per_s": round(1e3 / dec_ms, 1),
             "decode_bytes_per_step": dec_bytes,
             "decode_gbs": round(dec_bytes / (dec_ms * 1e-3) / 1e9, 1),
-            "decode_hbm_frac": round(dec_bytes / (dec_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+            "decode_hbm_frac": round(dec_bytes / (dec_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "decode_packed_ms_per_step": round(decp_ms, 4),
+            "decode_packed_bytes_per_step": decp_bytes,
+            "decode_packed_gbs": round(decp_bytes / (decp_ms * 1e-3) / 1e9, 1),
+            "decode_packed_hbm_frac": round(decp_bytes / (decp_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
 
 
 def _cpu_threads():

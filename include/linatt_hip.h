@@ -322,6 +322,25 @@ int linatt_kata_decode_step(const void* q, const void* k, const void* v, float* 
                             void* o, int B, int H, int dk, int dv, int num_groups, float scale,
                             float eps, int dtype, void* stream);
 
+/* The same state in the packed layout.  psi(x)_g = vec(x_g x_g^T) is
+ * symmetric in (a, b), so the packed state keeps one row per unordered pair
+ * a <= b of each group: row g E (E + 1) / 2 + a E - a (a - 1) / 2 + (b - a)
+ * holds what rows g E^2 + a E + b and g E^2 + b E + a of the full layout
+ * both hold (E = dk / num_groups).  S (B,H,M E (E + 1) / 2,dv), z
+ * (B,H,M E (E + 1) / 2) float32: 136 of 256 rows per group at M = 4, so a
+ * decode step moves about half the bytes.  Outputs equal the full-layout
+ * calls', and the states hold the same values (the pair's rows).  No
+ * reference counterpart (the reference keeps no decode state); for
+ * callers that keep a state between calls (decode caches, serving). */
+int linatt_kata_prefill_state_packed(const void* q, const void* k, const void* v, void* o,
+                                     float* den, const float* S_in, const float* z_in, float* S_out,
+                                     float* z_out, void* workspace, int B, int T, int H, int dk,
+                                     int dv, int num_groups, float scale, float eps, int seg_len,
+                                     int head_major, int dtype, void* stream);
+int linatt_kata_decode_step_packed(const void* q, const void* k, const void* v, float* S, float* z,
+                                   void* o, int B, int H, int dk, int dv, int num_groups,
+                                   float scale, float eps, int dtype, void* stream);
+
 /* ---------------------------------------------------------------------------
  * SPD delta rule (DeltaKata).  Replaces the forward of flash_delta
  * (kata/spd/flash_delta.py:1060-1116: _flash_U_kernel :25-183,

@@ -66,6 +66,8 @@ SIGNATURES = {
     "linatt_kata_prefill": (_i, [_vp] * 8 + [_i] * 6 + [_f, _f, _i, _i, _i, _vp]),
     "linatt_kata_prefill_state": (_i, [_vp] * 10 + [_i] * 6 + [_f, _f, _i, _i, _i, _vp]),
     "linatt_kata_decode_step": (_i, [_vp] * 6 + [_i] * 5 + [_f, _f, _i, _vp]),
+    "linatt_kata_prefill_state_packed": (_i, [_vp] * 10 + [_i] * 6 + [_f, _f, _i, _i, _i, _vp]),
+    "linatt_kata_decode_step_packed": (_i, [_vp] * 6 + [_i] * 5 + [_f, _f, _i, _vp]),
     "linatt_short_conv_fwd": (_i, [_vp] * 6 + [_i] * 6 + [_vp]),
     "linatt_short_conv_bwd_workspace_bytes": (_sz, [_i] * 4),
     "linatt_short_conv_bwd": (_i, [_vp] * 9 + [_i] * 6 + [_vp]),

@@ -941,13 +941,13 @@ size_t linatt_kata_prefill_workspace_bytes(int B, int T, int H, int dk, int dv, 
   return state_ws(B, T, H, dk, dv, num_groups, seg_len, dtype).bytes;
 }
 
-int linatt_kata_prefill_state(const void* q, const void* k, const void* v, void* o, float* den,
-                              const float* S_in, const float* z_in, float* S_out, float* z_out,
-                              void* workspace, int B, int T, int H, int dk, int dv, int num_groups,
-                              float scale, float eps, int seg_len, int head_major, int dtype,
-                              void* stream) {
+// the prefill with the state in the full (tri = 0) or packed (tri = 1) layout
+static int kata_prefill_state_impl(const char* fn, int tri, const void* q, const void* k,
+                                   const void* v, void* o, float* den, const float* S_in,
+                                   const float* z_in, float* S_out, float* z_out, void* workspace,
+                                   int B, int T, int H, int dk, int dv, int num_groups, float scale,
+                                   float eps, int seg_len, int head_major, int dtype, void* stream) {
   g_last_error.clear();
-  const char* fn = "linatt_kata_prefill_state";
   int st = check_state(fn, B, T, H, dk, dv, num_groups, scale, eps, seg_len, dtype);
   if (st) return st;
   if (!q || !k || !v || !o || !den || !workspace)
@@ -978,6 +978,7 @@ int linatt_kata_prefill_state(const void* q, const void* k, const void* v, void*
   a.S_out = S_out; a.z_out = z_out; a.S_in = S_in; a.z_in = z_in;
   a.B = B; a.T = T; a.H = H; a.L = seg_len; a.nseg = (T + seg_len - 1) / seg_len;
   a.scale = scale; a.scale2 = scale * scale; a.eps = eps;
+  a.tri = tri;
   hipError_t e = hipErrorInvalidValue;
   hipStream_t sm = (hipStream_t)stream;
 #define LINATT_TRY_S(T_, DK_, DV_, M_) \
@@ -989,6 +990,26 @@ int linatt_kata_prefill_state(const void* q, const void* k, const void* v, void*
   return LINATT_OK;
 }
 
+int linatt_kata_prefill_state(const void* q, const void* k, const void* v, void* o, float* den,
+                              const float* S_in, const float* z_in, float* S_out, float* z_out,
+                              void* workspace, int B, int T, int H, int dk, int dv, int num_groups,
+                              float scale, float eps, int seg_len, int head_major, int dtype,
+                              void* stream) {
+  return kata_prefill_state_impl("linatt_kata_prefill_state", 0, q, k, v, o, den, S_in, z_in, S_out,
+                                 z_out, workspace, B, T, H, dk, dv, num_groups, scale, eps, seg_len,
+                                 head_major, dtype, stream);
+}
+
+int linatt_kata_prefill_state_packed(const void* q, const void* k, const void* v, void* o,
+                                     float* den, const float* S_in, const float* z_in, float* S_out,
+                                     float* z_out, void* workspace, int B, int T, int H, int dk,
+                                     int dv, int num_groups, float scale, float eps, int seg_len,
+                                     int head_major, int dtype, void* stream) {
+  return kata_prefill_state_impl("linatt_kata_prefill_state_packed", 1, q, k, v, o, den, S_in, z_in,
+                                 S_out, z_out, workspace, B, T, H, dk, dv, num_groups, scale, eps,
+                                 seg_len, head_major, dtype, stream);
+}
+
 int linatt_kata_prefill(const void* q, const void* k, const void* v, void* o, float* den,
                         float* S_out, float* z_out, void* workspace, int B, int T, int H, int dk,
                         int dv, int num_groups, float scale, float eps, int seg_len,
@@ -998,21 +1019,23 @@ int linatt_kata_prefill(const void* q, const void* k, const void* v, void* o, fl
                                    dtype, stream);
 }
 
-int linatt_kata_decode_step(const void* q, const void* k, const void* v, float* S, float* z,
-                            void* o, int B, int H, int dk, int dv, int num_groups, float scale,
-                            float eps, int dtype, void* stream) {
+// one decode step on the full (tri = 0) or packed (tri = 1) state
+static int kata_decode_step_impl(const char* fn, int tri, const void* q, const void* k,
+                                 const void* v, float* S, float* z, void* o, int B, int H, int dk,
+                                 int dv, int num_groups, float scale, float eps, int dtype,
+                                 void* stream) {
   g_last_error.clear();
-  int st = check_state("linatt_kata_decode_step", B, 1, H, dk, dv, num_groups, scale, eps, 128, dtype);
+  int st = check_state(fn, B, 1, H, dk, dv, num_groups, scale, eps, 128, dtype);
   if (st) return st;
   if (!q || !k || !v || !S || !z || !o)
-    return fail(LINATT_EINVAL, "linatt_kata_decode_step: null tensor pointer");
+    return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
   const void* ps[] = {S, z, o};
   for (const void* p : ps)
     if (!aligned16(p))
-      return fail(LINATT_EINVAL, "linatt_kata_decode_step: S, z, o must be 16-byte aligned");
+      return fail(LINATT_EINVAL, std::string(fn) + ": S, z, o must be 16-byte aligned");
   KataDecodeArgs a{};
   a.q = q; a.k = k; a.v = v; a.o = o; a.S = S; a.z = z; a.B = B; a.H = H;
-  a.scale = scale; a.eps = eps;
+  a.scale = scale; a.eps = eps; a.tri = tri;
   hipError_t e = hipErrorInvalidValue;
   hipStream_t sm = (hipStream_t)stream;
 #define LINATT_TRY_DEC(T_, DK_, DV_, M_) \
@@ -1020,8 +1043,22 @@ int linatt_kata_decode_step(const void* q, const void* k, const void* v, float* 
   LINATT_KATA_STATE_SHAPES(LINATT_TRY_DEC)
 #undef LINATT_TRY_DEC
   if (e != hipSuccess)
-    return fail(LINATT_ELAUNCH, std::string("linatt_kata_decode_step: launch failed: ") + hipGetErrorString(e));
+    return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
   return LINATT_OK;
+}
+
+int linatt_kata_decode_step(const void* q, const void* k, const void* v, float* S, float* z,
+                            void* o, int B, int H, int dk, int dv, int num_groups, float scale,
+                            float eps, int dtype, void* stream) {
+  return kata_decode_step_impl("linatt_kata_decode_step", 0, q, k, v, S, z, o, B, H, dk, dv,
+                               num_groups, scale, eps, dtype, stream);
+}
+
+int linatt_kata_decode_step_packed(const void* q, const void* k, const void* v, float* S, float* z,
+                                   void* o, int B, int H, int dk, int dv, int num_groups,
+                                   float scale, float eps, int dtype, void* stream) {
+  return kata_decode_step_impl("linatt_kata_decode_step_packed", 1, q, k, v, S, z, o, B, H, dk, dv,
+                               num_groups, scale, eps, dtype, stream);
 }
 
 // ---------------------------------------------------------------------------

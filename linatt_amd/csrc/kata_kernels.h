@@ -106,7 +106,18 @@ struct KataStateArgs {
   const float* z_in;   // (B, H, P) f32 (may alias z_out), or null; set together with S_in
   int B, T, H, L, nseg;
   float scale, scale2, eps;
+  // layout of S_in / z_in / S_out / z_out: 0 full (P rows), 1 packed
+  // (the M E (E + 1) / 2 rows a <= b of each group; kata_state_tri_row)
+  int tri;
 };
+
+// Packed state row of pair (a, b), a <= b, of group g (groups of width E):
+// the upper triangle of each group, row by row.  The state rows p = g E^2 +
+// a E + b and g E^2 + b E + a of the full layout both map here (psi(x) is
+// symmetric in a and b).
+__host__ __device__ inline int kata_state_tri_row(int E, int g, int a, int b) {
+  return g * (E * (E + 1) / 2) + a * E - a * (a - 1) / 2 + (b - a);
+}
 
 template <typename T, int DK, int DV, int M>
 hipError_t launch_kata_prefill(const KataStateArgs& a, hipStream_t stream);
@@ -116,10 +127,11 @@ struct KataDecodeArgs {
   const void* k;
   const void* v;   // (B, H, DV)
   void* o;         // (B, H, DV)
-  float* S;        // (B, H, P, DV) f32, updated in place
-  float* z;        // (B, H, P) f32, updated in place
+  float* S;        // (B, H, P, DV) f32, updated in place (tri: (B, H, M E (E + 1) / 2, DV))
+  float* z;        // (B, H, P) f32, updated in place (tri: (B, H, M E (E + 1) / 2))
   int B, H;
   float scale, eps;
+  int tri;         // packed state layout (kata_state_tri_row)
 };
 
 template <typename T, int DK, int DV, int M>

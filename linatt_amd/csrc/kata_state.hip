@@ -251,76 +251,98 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
 
 // ---------------------------------------------------------------------------
 // Exclusive prefix over segments.  One thread per (bh, value row v, 4
-// consecutive packed state rows, which share their a), then one per (bh, 4
-// consecutive full rows of z).  The prefix state is written as c_ab H_ab.
+// consecutive packed state rows, which share their a), then one per (bh,
+// unordered pair {a, b} of z).  The prefix state is written as c_ab H_ab.
+// S_in / S_out and z_in / z_out are in the full or the packed layout
+// (a.tri).  Each thread reads, then writes, only state elements no other
+// thread writes, so S_in / z_in may alias S_out / z_out; the packed rows
+// below the diagonal, whose prefix is weighted by 0, start from zero.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, int M>
 __global__ __launch_bounds__(256) void kata_seg_scan_kernel(KataStateArgs a) {
   constexpr int E = DK / M, P = M * E * E, PR = kPkRows<E>, PP = M * PR;
+  constexpr int PT = M * E * (E + 1) / 2;  // unordered pairs (packed layout rows)
   static_assert(PR % 4 == 0 && (E / 2) % 4 == 0, "4 packed rows share their a");
-  constexpr int64_t nS = (int64_t)DV * (PP / 4), per_bh = nS + P / 4;
+  constexpr int64_t nS = (int64_t)DV * (PP / 4), per_bh = nS + PT;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)a.B * a.H * per_bh) return;
   const int bh = (int)(idx / per_bh);
   const int64_t rem = idx % per_bh;
-  const bool isS = rem < nS;
-  const int v = isS ? (int)(rem / (PP / 4)) : DV;
-  // packed row (S) or full row (z), 4 consecutive
-  const int p = isS ? 4 * (int)(rem % (PP / 4)) : 4 * (int)(rem - nS);
-  // S: the rows' pair (a, b0 + j) of group g, their full rows and weights
-  int g = 0, pa = 0, pb0 = 0;
-  if (isS) {
-    g = p / PR;
-    pk_ab<E>(p % PR, pa, pb0);
+  const float is = 1.f / a.scale, sc = a.scale;
+  if (rem >= nS) {
+    // z: pair t of the packed layout, (g, za <= zb)
+    const int t = (int)(rem - nS), g = t / (E * (E + 1) / 2);
+    int za = 0, r = t % (E * (E + 1) / 2);
+    while (r >= E - za) {
+      r -= E - za;
+      ++za;
+    }
+    const int zb = za + r, f0 = g * E * E + za * E + zb, f1 = g * E * E + zb * E + za;
+    float run = 0.f;
+    if (a.z_in) run = (a.tri ? a.z_in[(size_t)bh * PT + t] : a.z_in[(size_t)bh * P + f0]) * is;
+    for (int seg = 0; seg < a.nseg; ++seg) {
+      const size_t base = ((size_t)bh * a.nseg + seg) * P;
+      const float x = a.seg_z[base + f0];
+      a.Hz[base + f0] = run;
+      a.Hz[base + f1] = run;
+      run += x;
+    }
+    if (a.z_out) {
+      if (a.tri) {
+        a.z_out[(size_t)bh * PT + t] = run * sc;
+      } else {
+        a.z_out[(size_t)bh * P + f0] = run * sc;
+        a.z_out[(size_t)bh * P + f1] = run * sc;
+      }
+    }
+    return;
   }
+  // S: value row v, packed rows p .. p + 3 = pairs (a, b0 + j) of group g
+  const int v = (int)(rem / (PP / 4));
+  const int p = 4 * (int)(rem % (PP / 4));
+  const int g = p / PR;
+  int pa, pb0;
+  pk_ab<E>(p % PR, pa, pb0);
   const int pf0 = g * E * E + pa * E + pb0;  // full row of (a, b0)
   float cw[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) cw[j] = pk_weight(pa, pb0 + j);
-  // the running sum starts from the initial state (stored scaled by
-  // `scale`; the scan runs unscaled); each thread reads, then writes, only
-  // its own state elements, so S_in may alias S_out
-  float4 run = make_float4(0.f, 0.f, 0.f, 0.f);
+  float r4[4] = {0.f, 0.f, 0.f, 0.f};
   if (a.S_in) {
-    const float is = 1.f / a.scale;
-    if (isS) {
-      const float* si = a.S_in + ((size_t)bh * P + pf0) * DV + v;
-      run = make_float4(si[0] * is, si[DV] * is, si[2 * DV] * is, si[3 * DV] * is);
-    } else {
-      const float4 zi = *reinterpret_cast<const float4*>(a.z_in + (size_t)bh * P + p);
-      run = make_float4(zi.x * is, zi.y * is, zi.z * is, zi.w * is);
+    // the rows b >= a read their pair's element; the initial state is
+    // stored scaled by `scale`, the scan runs unscaled
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int b = pb0 + j;
+      if (b < pa) continue;
+      r4[j] = (a.tri ? a.S_in[((size_t)bh * PT + kata_state_tri_row(E, g, pa, b)) * DV + v]
+                     : a.S_in[((size_t)bh * P + pf0 + j) * DV + v]) * is;
     }
   }
+  float4 run = make_float4(r4[0], r4[1], r4[2], r4[3]);
   for (int seg = 0; seg < a.nseg; ++seg) {
     const size_t base = (size_t)bh * a.nseg + seg;
-    float4 x;
-    if (isS) {
-      x = *reinterpret_cast<const float4*>(a.seg_S + (base * DV + v) * PP + p);
-      st4<T>((T*)a.HT + (base * DV + v) * PP + p,
-             to4<T>(run.x * cw[0], run.y * cw[1], run.z * cw[2], run.w * cw[3]));
-    } else {
-      x = *reinterpret_cast<const float4*>(a.seg_z + base * P + p);
-      *reinterpret_cast<float4*>(a.Hz + base * P + p) = run;
-    }
+    const float4 x = *reinterpret_cast<const float4*>(a.seg_S + (base * DV + v) * PP + p);
+    st4<T>((T*)a.HT + (base * DV + v) * PP + p,
+           to4<T>(run.x * cw[0], run.y * cw[1], run.z * cw[2], run.w * cw[3]));
     run.x += x.x; run.y += x.y; run.z += x.z; run.w += x.w;
   }
-  const float sc = a.scale;
-  if (isS) {
-    if (a.S_out) {
-      // full layout: rows (a, b) with a <= b write both entries of the pair
-      float* so = a.S_out + (size_t)bh * P * DV + v;
-      const float r4[4] = {run.x * sc, run.y * sc, run.z * sc, run.w * sc};
+  if (a.S_out) {
+    // rows (a, b) with a <= b write their pair: once (packed layout) or
+    // both entries (full layout)
+    const float o4[4] = {run.x * sc, run.y * sc, run.z * sc, run.w * sc};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int b = pb0 + j;
-        if (b < pa) continue;
-        so[(size_t)(pf0 + j) * DV] = r4[j];
-        if (b != pa) so[(size_t)(g * E * E + b * E + pa) * DV] = r4[j];
+    for (int j = 0; j < 4; ++j) {
+      const int b = pb0 + j;
+      if (b < pa) continue;
+      if (a.tri) {
+        a.S_out[((size_t)bh * PT + kata_state_tri_row(E, g, pa, b)) * DV + v] = o4[j];
+      } else {
+        float* so = a.S_out + (size_t)bh * P * DV + v;
+        so[(size_t)(pf0 + j) * DV] = o4[j];
+        if (b != pa) so[(size_t)(g * E * E + b * E + pa) * DV] = o4[j];
       }
     }
-  } else if (a.z_out) {
-    *reinterpret_cast<float4*>(a.z_out + (size_t)bh * P + p) =
-        make_float4(run.x * sc, run.y * sc, run.z * sc, run.w * sc);
   }
 }
 
@@ -561,7 +583,7 @@ hipError_t launch_kata_prefill(const KataStateArgs& a, hipStream_t stream) {
   kata_seg_state_kernel<T, DK, DV, M><<<dim3(BH * a.nseg * (M * kPkRows<E> / 768)), dim3(512), 0, stream>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int64_t items = (int64_t)BH * (DV * (M * kPkRows<E> / 4) + P / 4);
+  const int64_t items = (int64_t)BH * (DV * (M * kPkRows<E> / 4) + M * E * (E + 1) / 2);
   kata_seg_scan_kernel<T, DK, DV, M><<<dim3((unsigned)((items + 255) / 256)), dim3(256), 0, stream>>>(a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -574,15 +596,20 @@ hipError_t launch_kata_prefill(const KataStateArgs& a, hipStream_t stream) {
 // Decode step: one workgroup per (b, h) streams its (P x DV) f32 state once:
 //   S += psi(k) v^T, z += psi(k);  o = psi(q)^T S / max(psi(q).z, eps)
 // with psi(x)_p = scale x_a x_b.  16 threads cover one state row (4 value
-// columns each), 16 rows per pass.
+// columns each), 16 rows per pass.  TRI: the packed state, one row per
+// unordered pair (a <= b, kata_state_tri_row), whose readout weight is 2 off
+// the diagonal; it moves M E (E + 1) / 2 rows instead of M E^2.
 // ---------------------------------------------------------------------------
-template <typename T, int DK, int DV, int M>
+template <typename T, int DK, int DV, int M, bool TRI>
 __global__ __launch_bounds__(256) void kata_decode_kernel(KataDecodeArgs a) {
-  constexpr int E = DK / M, P = M * E * E;
+  constexpr int E = DK / M, P = M * E * E, PT = M * E * (E + 1) / 2;
+  constexpr int NR = TRI ? PT : P;  // state rows
   static_assert(DV == 64, "decode maps 16 threads x 4 columns onto a row");
+  static_assert(DK <= 256, "8-bit dims in the pair table");
   __shared__ float qs[DK], ks[DK], vs[DV];
   __shared__ float4 red[16][16];
   __shared__ float dred[16];
+  __shared__ unsigned short pairs[TRI ? PT : 1];  // packed row -> (dim a << 8) | dim b
   const int tid = threadIdx.x;
   const int bh = blockIdx.x;
   if (tid < DK) {
@@ -590,17 +617,39 @@ __global__ __launch_bounds__(256) void kata_decode_kernel(KataDecodeArgs a) {
     ks[tid] = (float)((const T*)a.k)[(size_t)bh * DK + tid];
   }
   if (tid < DV) vs[tid] = (float)((const T*)a.v)[(size_t)bh * DV + tid];
+  if constexpr (TRI) {
+    for (int t = tid; t < PT; t += 256) {
+      const int g = t / (E * (E + 1) / 2);
+      int za = 0, r = t % (E * (E + 1) / 2);
+      while (r >= E - za) {
+        r -= E - za;
+        ++za;
+      }
+      pairs[t] = (unsigned short)(((g * E + za) << 8) | (g * E + za + r));
+    }
+  }
   __syncthreads();
   const int c4 = tid & 15, r = tid >> 4;
   const float4 vv = *reinterpret_cast<const float4*>(vs + 4 * c4);
   float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
   float dacc = 0.f;
-  float* S = a.S + (size_t)bh * P * DV;
-  float* z = a.z + (size_t)bh * P;
-  for (int p = r; p < P; p += 16) {
-    const int g = p / (E * E), ia = g * E + (p / E) % E, ib = g * E + p % E;
+  float* S = a.S + (size_t)bh * NR * DV;
+  float* z = a.z + (size_t)bh * NR;
+  for (int p = r; p < NR; p += 16) {
+    int ia, ib;
+    float wq = a.scale;
+    if constexpr (TRI) {
+      const unsigned pr = pairs[p];
+      ia = (int)(pr >> 8);
+      ib = (int)(pr & 255u);
+      if (ia != ib) wq *= 2.f;
+    } else {
+      const int g = p / (E * E);
+      ia = g * E + (p / E) % E;
+      ib = g * E + p % E;
+    }
     const float pk = a.scale * ks[ia] * ks[ib];
-    const float pq = a.scale * qs[ia] * qs[ib];
+    const float pq = wq * qs[ia] * qs[ib];
     float4* sp = reinterpret_cast<float4*>(S + (size_t)p * DV + 4 * c4);
     float4 x = *sp;
     x.x += pk * vv.x; x.y += pk * vv.y; x.z += pk * vv.z; x.w += pk * vv.w;
@@ -630,7 +679,10 @@ __global__ __launch_bounds__(256) void kata_decode_kernel(KataDecodeArgs a) {
 
 template <typename T, int DK, int DV, int M>
 hipError_t launch_kata_decode(const KataDecodeArgs& a, hipStream_t stream) {
-  kata_decode_kernel<T, DK, DV, M><<<dim3(a.B * a.H), dim3(256), 0, stream>>>(a);
+  if (a.tri)
+    kata_decode_kernel<T, DK, DV, M, true><<<dim3(a.B * a.H), dim3(256), 0, stream>>>(a);
+  else
+    kata_decode_kernel<T, DK, DV, M, false><<<dim3(a.B * a.H), dim3(256), 0, stream>>>(a);
   return hipGetLastError();
 }
 

@@ -59,7 +59,10 @@ __all__ = ["KataState", "parallel_kata_attn_cached", "LayerStateCache", "get_lay
 class KataState(NamedTuple):
     """A layer's recurrent state: ``S (B, H, P, dv)``, ``z (B, H, P)`` float32,
     the number of tokens it covers, and the score it belongs to (``variant``
-    "concat" or "sum", ``num_groups``)."""
+    "concat" or "sum", ``num_groups``).  The concat score's MFMA path keeps
+    the packed layout (``spd_state.state_rows(dk, M, packed=True)`` rows, one
+    per unordered pair of each group; ``spd_state.unpack_state`` gives the
+    full one), and continues a full-layout state it is given as such."""
 
     S: torch.Tensor
     z: torch.Tensor
@@ -117,9 +120,12 @@ def parallel_kata_attn_cached(q, k, v, state=None, num_groups=4, scale=None, eps
             o = spd_state.kata_decode_step(state.S, state.z, q[:, 0], k[:, 0], v[:, 0], M,
                                            scale, eps)
             return o[:, None], KataState(state.S, state.z, offset + 1, variant, M)
+        # a new state is packed (a decode step then streams about half the
+        # bytes); an existing one keeps its layout
+        packed = state is None or state.S.shape[2] == spd_state.state_rows(dk, M, True)
         init = None if state is None else (state.S, state.z)
         o, _, S, z = spd_state.kata_prefill(q, k, v, M, scale, eps, initial_state=init,
-                                            in_place=state is not None)
+                                            in_place=state is not None, packed_state=packed)
         return o, KataState(S, z, offset + T, variant, M)
     return _generic(q, k, v, state, M, scale, eps, variant, c, offset)
 

@@ -20,10 +20,16 @@ recurrent decode step.
   updating ``S`` and ``z`` in place, and returns ``o (B, H, dv)``.  The
   reference's flash path keeps no decode state (``kata/layer.py:492``); this
   is the state the ``past_key_values`` cache would hold.
+* The state also comes in a packed layout (``kata_prefill(...,
+  packed_state=True)``; ``kata_decode_step`` takes either): psi(x) is
+  symmetric in each group's (a, b), so one row per unordered pair a <= b
+  holds all of it, ``M E (E + 1) / 2`` rows instead of ``M E^2`` (136 of 256
+  per group at M = 4), and a decode step streams about half the bytes.
+  ``pack_state`` / ``unpack_state`` convert between the layouts.
 
-All three run in ``liblinatt_hip.so`` (``linatt_kata_prefill_state``,
-``linatt_linear_scan_fwd``, ``linatt_kata_decode_step``); unsupported shapes
-raise.
+All three run in ``liblinatt_hip.so`` (``linatt_kata_prefill_state[_packed]``,
+``linatt_linear_scan_fwd``, ``linatt_kata_decode_step[_packed]``); unsupported
+shapes raise.
 """
 
 from __future__ import annotations
@@ -51,8 +57,45 @@ def _check(dtype, dk, dv, M):
     return L
 
 
+def state_rows(dk, num_groups, packed=False):
+    """State rows per (b, h): M E^2 in the full layout, M E (E + 1) / 2 in the
+    packed one (one row per unordered pair a <= b of each group)."""
+    E = dk // num_groups
+    return num_groups * E * (E + 1) // 2 if packed else num_groups * E * E
+
+
+def _pair_index(dk, num_groups, device):
+    """(full rows of the packed rows, packed row of every full row)."""
+    E, M = dk // num_groups, num_groups
+    full_of, tri_of = [], [0] * (M * E * E)
+    for g in range(M):
+        for a in range(E):
+            for b in range(a, E):
+                t = len(full_of)
+                full_of.append(g * E * E + a * E + b)
+                tri_of[g * E * E + a * E + b] = t
+                tri_of[g * E * E + b * E + a] = t
+    return (torch.tensor(full_of, device=device, dtype=torch.long),
+            torch.tensor(tri_of, device=device, dtype=torch.long))
+
+
+def pack_state(S, z, num_groups):
+    """Full-layout state ``S (B, H, M E^2, dv)``, ``z (B, H, M E^2)`` to the
+    packed layout (the rows a <= b; linatt_kata_decode_step_packed)."""
+    dk = round((S.shape[2] // num_groups) ** 0.5) * num_groups
+    full_of, _ = _pair_index(dk, num_groups, S.device)
+    return S.index_select(2, full_of).contiguous(), z.index_select(2, full_of).contiguous()
+
+
+def unpack_state(S, z, num_groups):
+    """Packed state to the full layout (each pair's row to both of its rows)."""
+    E = next(e for e in range(1, 257) if num_groups * e * (e + 1) // 2 == S.shape[2])
+    _, tri_of = _pair_index(E * num_groups, num_groups, S.device)
+    return S.index_select(2, tri_of).contiguous(), z.index_select(2, tri_of).contiguous()
+
+
 def _prefill(q, k, v, M, scale, eps, seg_len, head_major, want_state, initial_state=None,
-             in_place=False):
+             in_place=False, packed=False):
     _lib.require_device(q, k, v)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     if not (q.dtype == k.dtype == v.dtype):
@@ -69,7 +112,7 @@ def _prefill(q, k, v, M, scale, eps, seg_len, head_major, want_state, initial_st
     L = _check(q.dtype, dk, dv, M)
     sc = _scale(dk, M, scale)
     dt = _lib.dtype_code(q.dtype)
-    P = M * (dk // M) ** 2
+    P = state_rows(dk, M, packed)
     o = torch.empty_like(v)
     den = torch.empty(q.shape[:-1], device=q.device, dtype=torch.float32)
     S0 = z0 = None
@@ -91,7 +134,8 @@ def _prefill(q, k, v, M, scale, eps, seg_len, head_major, want_state, initial_st
         z = torch.empty(B, H, P, device=q.device, dtype=torch.float32)
     ws = torch.empty(L.linatt_kata_prefill_workspace_bytes(B, T, H, dk, dv, M, seg_len, dt),
                      device=q.device, dtype=torch.uint8)
-    _lib.check("linatt_kata_prefill_state", L.linatt_kata_prefill_state(
+    name = "linatt_kata_prefill_state_packed" if packed else "linatt_kata_prefill_state"
+    _lib.check(name, getattr(L, name)(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(den), _lib.ptr(S0),
         _lib.ptr(z0), _lib.ptr(S), _lib.ptr(z), _lib.ptr(ws), B, T, H, dk, dv, M, sc, float(eps),
         seg_len, 1 if head_major else 0, dt, _lib.stream_of(q)))
@@ -134,17 +178,23 @@ def _linear_scan(q, k, v, M, scale, eps):
 
 
 def kata_prefill(q, k, v, num_groups=4, scale=None, eps=1e-6, seg_len=1024, initial_state=None,
-                 in_place=False):
+                 in_place=False, packed_state=False):
     """Time-major ``(B, T, H, D)`` prefill: ``(o, den, S, z)``.  With
     ``initial_state=(S0, z0)`` (the state after earlier tokens) the outputs and
     the returned state also cover those tokens; ``in_place=True`` writes that
-    state back into ``S0, z0`` (returned as ``S, z``)."""
+    state back into ``S0, z0`` (returned as ``S, z``).  ``packed_state``: the
+    state (returned and initial) in the packed layout, one row per unordered
+    pair a <= b of each group (``state_rows``, ``pack_state`` /
+    ``unpack_state``), which ``kata_decode_step`` takes as well and streams in
+    about half the bytes."""
     return _prefill(q, k, v, num_groups, scale, eps, seg_len, False, True, initial_state,
-                    in_place)
+                    in_place, packed_state)
 
 
 def kata_decode_step(S, z, q, k, v, num_groups=4, scale=None, eps=1e-6):
-    """One token per ``(b, h)``: updates ``S``, ``z`` in place and returns ``o``."""
+    """One token per ``(b, h)``: updates ``S``, ``z`` in place and returns ``o``.
+    The state may be in the full or the packed layout (told apart by its row
+    count, ``state_rows``)."""
     if q.dim() != 3 or v.dim() != 3:
         raise ValueError(f"q, k must be (B, H, dk) and v (B, H, dv); got q {tuple(q.shape)}, "
                          f"v {tuple(v.shape)}")
@@ -160,15 +210,19 @@ def kata_decode_step(S, z, q, k, v, num_groups=4, scale=None, eps=1e-6):
     M = num_groups
     if dk % M:
         raise ValueError(f"d_k={dk} not divisible by M={M}")
-    P = M * (dk // M) ** 2
-    if S.shape != (B, H, P, dv) or z.shape != (B, H, P):
-        raise ValueError(f"state must be S {(B, H, P, dv)}, z {(B, H, P)}")
+    P, PT = state_rows(dk, M), state_rows(dk, M, True)
+    packed = S.dim() == 4 and S.shape[2] == PT
+    R = PT if packed else P
+    if S.shape != (B, H, R, dv) or z.shape != (B, H, R):
+        raise ValueError(f"state must be S {(B, H, P, dv)}, z {(B, H, P)} (full layout) or "
+                         f"S {(B, H, PT, dv)}, z {(B, H, PT)} (packed)")
     if S.dtype != torch.float32 or z.dtype != torch.float32 or not (S.is_contiguous() and z.is_contiguous()):
         raise ValueError("S and z must be contiguous float32 (updated in place)")
     L = _check(q.dtype, dk, dv, M)
     q, k, v = q.contiguous(), k.to(q.dtype).contiguous(), v.to(q.dtype).contiguous()
     o = torch.empty(B, H, dv, device=q.device, dtype=q.dtype)
-    _lib.check("linatt_kata_decode_step", L.linatt_kata_decode_step(
+    name = "linatt_kata_decode_step_packed" if packed else "linatt_kata_decode_step"
+    _lib.check(name, getattr(L, name)(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(S), _lib.ptr(z), _lib.ptr(o), B, H, dk,
         dv, M, _scale(dk, M, scale), float(eps), _lib.dtype_code(q.dtype), _lib.stream_of(q)))
     return o

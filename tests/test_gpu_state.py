@@ -226,6 +226,73 @@ def test_config5_full_size(S_):
 
 
 # ---------------------------------------------------------------------------
+# packed state layout: one row per unordered pair a <= b of each group
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("M", [4, 2])
+@pytest.mark.parametrize("case", [(2, 300, 2, 128), (1, 1000, 3, 256)],
+                         ids=lambda c: "B{}T{}H{}L{}".format(*c))
+def test_packed_prefill_equals_full(S_, M, case):
+    """The packed-layout prefill runs the same kernels: o and den are
+    bit-identical to the full-layout call's, and its state holds the full
+    state's pair rows bit for bit (the scan writes one value to both rows of
+    a pair).  Also continued in place from a packed state."""
+    B, T, H, L = case
+    print(f"packed prefill {case} M={M}", flush=True)
+    dev = torch.device("cuda")
+    q, k, v = (gen((B, T, H, 64), 60 + i + T).to(dev) for i in range(3))
+    o, den, S, z = S_.kata_prefill(q, k, v, num_groups=M, seg_len=L)
+    op, denp, Sp, zp = S_.kata_prefill(q, k, v, num_groups=M, seg_len=L, packed_state=True)
+    PT = S_.state_rows(64, M, True)
+    assert Sp.shape == (B, H, PT, 64) and zp.shape == (B, H, PT)
+    assert torch.equal(o, op) and torch.equal(den, denp)
+    Su, zu = S_.unpack_state(Sp, zp, M)
+    assert torch.equal(Su, S) and torch.equal(zu, z)
+    n = T // 3
+    _, _, F1, y1 = S_.kata_prefill(q[:, :n], k[:, :n], v[:, :n], num_groups=M, seg_len=L)
+    of, denf, F2, y2 = S_.kata_prefill(q[:, n:], k[:, n:], v[:, n:], num_groups=M, seg_len=L,
+                                       initial_state=(F1, y1), in_place=True)
+    _, _, P1, x1 = S_.kata_prefill(q[:, :n], k[:, :n], v[:, :n], num_groups=M, seg_len=L,
+                                   packed_state=True)
+    o2, den2, P2, x2 = S_.kata_prefill(q[:, n:], k[:, n:], v[:, n:], num_groups=M, seg_len=L,
+                                       initial_state=(P1, x1), in_place=True, packed_state=True)
+    assert P2.data_ptr() == P1.data_ptr() and x2.data_ptr() == x1.data_ptr()
+    assert torch.equal(o2, of) and torch.equal(den2, denf)
+    Su2, zu2 = S_.unpack_state(P2, x2, M)
+    assert torch.equal(Su2, F2) and torch.equal(zu2, y2)
+
+
+@pytest.mark.parametrize("M", [4, 2])
+def test_packed_decode_equals_full(S_, M):
+    """Decode steps on the packed state.  Its rows stay the full state's pair
+    rows a <= b bit for bit.  The full layout forms a pair's two rows in two
+    rounding orders, so those agree to float32 rounding.  o agrees with the
+    full-layout step to one bf16 rounding (the readout sums each pair once,
+    weighted 2 off the diagonal) and with the float64 oracle."""
+    B, n, H, steps = 3, 200, 2, 4
+    print(f"packed decode M={M}", flush=True)
+    dev = torch.device("cuda")
+    q, k, v = (gen((B, n + steps, H, 64), 91 + i) for i in range(3))
+    _, _, S, z = S_.kata_prefill(q[:, :n].to(dev), k[:, :n].to(dev), v[:, :n].to(dev),
+                                 num_groups=M, seg_len=128)
+    Sp, zp = S_.pack_state(S, z, M)
+    Sr, zr = S.cpu().double(), z.cpu().double()
+    for i in range(steps):
+        t = n + i
+        x = [y[:, t].to(dev) for y in (q, k, v)]
+        o = S_.kata_decode_step(S, z, *x, num_groups=M)
+        op = S_.kata_decode_step(Sp, zp, *x, num_groups=M)
+        o_ref, Sr, zr = K.kata_decode_step(Sr, zr, q[:, t], k[:, t], v[:, t], M)
+        assert mar(op, o_ref) < TOL, (i, mar(op, o_ref))
+        assert mar(op, o) < 8e-3, (i, mar(op, o))
+        Sf, zf = S_.pack_state(S, z, M)
+        assert torch.equal(Sf, Sp) and torch.equal(zf, zp), i
+        Su, zu = S_.unpack_state(Sp, zp, M)
+        assert mar(Su, S) < 1e-6 and mar(zu, z) < 1e-6, i
+
+
+# ---------------------------------------------------------------------------
 # decode cache (linatt_amd.kata_cache): prefill, continued prefill, decode
 # steps, all against the flash forward over every token so far
 # ---------------------------------------------------------------------------
@@ -251,9 +318,13 @@ def test_cache_prefill_then_decode_equals_parallel(M):
         assert o_t.shape == (B, 1, H, 64) and st.offset == t + 1
         assert mar(o_t[:, 0], o_ref[:, t]) < TOL, i
         assert mar(o_t[:, 0], o_par[:, t].float()) < TOL, i
-    # the state after all tokens equals the psi sums of every key
+    # the state after all tokens equals the psi sums of every key (the cache
+    # keeps the packed layout)
+    from linatt_amd import spd_state as S_
+    assert st.S.shape[2] == S_.state_rows(64, M, True)
+    S_full, z_full = S_.unpack_state(st.S, st.z, M)
     S_ref, z_ref = K.kata_state_prefill(k, v, M)
-    assert mar(st.S, S_ref) < TOL and mar(st.z, z_ref) < TOL
+    assert mar(S_full, S_ref) < TOL and mar(z_full, z_ref) < TOL
 
 
 @pytest.mark.parametrize("split", [(200, 333), (128, 1), (1, 256), (1100, 500)])
