@@ -140,7 +140,7 @@ bool state_compiled(int dtype, int dk, int dv, int M) {
 }
 
 struct StateWs {
-  size_t seg_S, seg_z, HT, Hz, bytes;
+  size_t seg_S, seg_z, HT, Hz, zc, bytes;
 };
 
 StateWs state_ws(int B, int T, int H, int dk, int dv, int M, int L, int dtype) {
@@ -153,6 +153,7 @@ StateWs state_ws(int B, int T, int H, int dk, int dv, int M, int L, int dtype) {
   w.seg_z = off; off = al(off + BH * nseg * P * 4);
   w.HT = off; off = al(off + BH * nseg * dv * PP * elt_bytes(dtype));
   w.Hz = off; off = al(off + BH * nseg * P * 4);
+  w.zc = off; off = al(off + BH * (M * E * (E + 1) / 2) * 4);  // packed z_in copy (in place)
   w.bytes = off;
   return w;
 }
@@ -981,6 +982,16 @@ static int kata_prefill_state_impl(const char* fn, int tri, const void* q, const
   a.tri = tri;
   hipError_t e = hipErrorInvalidValue;
   hipStream_t sm = (hipStream_t)stream;
+  if (tri && z_in && z_in == z_out) {
+    // packed layout in place: two scan threads read each off-diagonal pair's
+    // z element and one of them writes it, so the scan reads a copy
+    const int64_t n = (int64_t)B * H * (num_groups * (dk / num_groups) * (dk / num_groups + 1) / 2);
+    e = launch_f32_copy(z_in, (float*)(ws + w.zc), n, sm);
+    if (e != hipSuccess)
+      return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
+    a.z_in = (const float*)(ws + w.zc);
+    e = hipErrorInvalidValue;
+  }
 #define LINATT_TRY_S(T_, DK_, DV_, M_) \
   if (dtype == dtype_of<T_>() && dk == DK_ && dv == DV_ && num_groups == M_) e = launch_kata_prefill<T_, DK_, DV_, M_>(a, sm);
   LINATT_KATA_STATE_SHAPES(LINATT_TRY_S)

@@ -122,6 +122,9 @@ __host__ __device__ inline int kata_state_tri_row(int E, int g, int a, int b) {
 template <typename T, int DK, int DV, int M>
 hipError_t launch_kata_prefill(const KataStateArgs& a, hipStream_t stream);
 
+// n floats from src to dst on the stream (a small copy kernel)
+hipError_t launch_f32_copy(const float* src, float* dst, int64_t n, hipStream_t stream);
+
 struct KataDecodeArgs {
   const void* q;   // (B, H, DK)
   const void* k;

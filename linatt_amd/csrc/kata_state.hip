@@ -251,48 +251,61 @@ __global__ __launch_bounds__(512) void kata_seg_state_kernel(KataStateArgs a) {
 
 // ---------------------------------------------------------------------------
 // Exclusive prefix over segments.  One thread per (bh, value row v, 4
-// consecutive packed state rows, which share their a), then one per (bh,
-// unordered pair {a, b} of z).  The prefix state is written as c_ab H_ab.
+// consecutive packed state rows, which share their a), then one per (bh, 4
+// consecutive full rows of z).  The prefix state is written as c_ab H_ab.
 // S_in / S_out and z_in / z_out are in the full or the packed layout
-// (a.tri).  Each thread reads, then writes, only state elements no other
-// thread writes, so S_in / z_in may alias S_out / z_out; the packed rows
-// below the diagonal, whose prefix is weighted by 0, start from zero.
+// (a.tri).  A thread reads, then writes, only its own state elements, so
+// the full layout's S_in / z_in may alias S_out / z_out; in the packed
+// layout a full row of z below the diagonal reads its pair's element, which
+// another thread writes, so the host hands an aliased z_in over as a copy.
+// The packed state rows below the diagonal, whose prefix is weighted by 0,
+// start from zero.
 // ---------------------------------------------------------------------------
 template <typename T, int DK, int DV, int M>
 __global__ __launch_bounds__(256) void kata_seg_scan_kernel(KataStateArgs a) {
   constexpr int E = DK / M, P = M * E * E, PR = kPkRows<E>, PP = M * PR;
   constexpr int PT = M * E * (E + 1) / 2;  // unordered pairs (packed layout rows)
   static_assert(PR % 4 == 0 && (E / 2) % 4 == 0, "4 packed rows share their a");
-  constexpr int64_t nS = (int64_t)DV * (PP / 4), per_bh = nS + PT;
+  constexpr int64_t nS = (int64_t)DV * (PP / 4), per_bh = nS + P / 4;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)a.B * a.H * per_bh) return;
   const int bh = (int)(idx / per_bh);
   const int64_t rem = idx % per_bh;
   const float is = 1.f / a.scale, sc = a.scale;
   if (rem >= nS) {
-    // z: pair t of the packed layout, (g, za <= zb)
-    const int t = (int)(rem - nS), g = t / (E * (E + 1) / 2);
-    int za = 0, r = t % (E * (E + 1) / 2);
-    while (r >= E - za) {
-      r -= E - za;
-      ++za;
+    // z: full rows p .. p + 3 = pairs (za, zb0 + j) of group zg
+    const int p = 4 * (int)(rem - nS);
+    const int zg = p / (E * E), za = (p / E) % E, zb0 = p % E;
+    auto tri = [&](int j) {
+      const int zb = zb0 + j;
+      return (size_t)bh * PT + kata_state_tri_row(E, zg, za < zb ? za : zb, za < zb ? zb : za);
+    };
+    float4 run = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (a.z_in) {
+      if (a.tri) {
+        run = make_float4(a.z_in[tri(0)] * is, a.z_in[tri(1)] * is, a.z_in[tri(2)] * is,
+                          a.z_in[tri(3)] * is);
+      } else {
+        const float4 zi = *reinterpret_cast<const float4*>(a.z_in + (size_t)bh * P + p);
+        run = make_float4(zi.x * is, zi.y * is, zi.z * is, zi.w * is);
+      }
     }
-    const int zb = za + r, f0 = g * E * E + za * E + zb, f1 = g * E * E + zb * E + za;
-    float run = 0.f;
-    if (a.z_in) run = (a.tri ? a.z_in[(size_t)bh * PT + t] : a.z_in[(size_t)bh * P + f0]) * is;
     for (int seg = 0; seg < a.nseg; ++seg) {
-      const size_t base = ((size_t)bh * a.nseg + seg) * P;
-      const float x = a.seg_z[base + f0];
-      a.Hz[base + f0] = run;
-      a.Hz[base + f1] = run;
-      run += x;
+      const size_t base = ((size_t)bh * a.nseg + seg) * P + p;
+      const float4 x = *reinterpret_cast<const float4*>(a.seg_z + base);
+      *reinterpret_cast<float4*>(a.Hz + base) = run;
+      run.x += x.x; run.y += x.y; run.z += x.z; run.w += x.w;
     }
     if (a.z_out) {
       if (a.tri) {
-        a.z_out[(size_t)bh * PT + t] = run * sc;
+        // the pair's element, from its full row with za <= zb
+        const float r4[4] = {run.x * sc, run.y * sc, run.z * sc, run.w * sc};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (zb0 + j >= za) a.z_out[tri(j)] = r4[j];
       } else {
-        a.z_out[(size_t)bh * P + f0] = run * sc;
-        a.z_out[(size_t)bh * P + f1] = run * sc;
+        *reinterpret_cast<float4*>(a.z_out + (size_t)bh * P + p) =
+            make_float4(run.x * sc, run.y * sc, run.z * sc, run.w * sc);
       }
     }
     return;
@@ -576,6 +589,20 @@ __global__ __launch_bounds__(256, 2) void kata_prefill_out_kernel(KataStateArgs 
   }
 }
 
+// n floats from src to dst (the packed layout's aliased z_in, handed to the
+// scan as a copy)
+__global__ __launch_bounds__(256) void kata_copy_f32_kernel(const float* __restrict__ src,
+                                                            float* __restrict__ dst, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    dst[i] = src[i];
+}
+
+hipError_t launch_f32_copy(const float* src, float* dst, int64_t n, hipStream_t stream) {
+  const int64_t blocks = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
+  if (blocks > 0) kata_copy_f32_kernel<<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(src, dst, n);
+  return hipGetLastError();
+}
+
 template <typename T, int DK, int DV, int M>
 hipError_t launch_kata_prefill(const KataStateArgs& a, hipStream_t stream) {
   constexpr int E = DK / M, P = M * E * E;
@@ -583,7 +610,7 @@ hipError_t launch_kata_prefill(const KataStateArgs& a, hipStream_t stream) {
   kata_seg_state_kernel<T, DK, DV, M><<<dim3(BH * a.nseg * (M * kPkRows<E> / 768)), dim3(512), 0, stream>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int64_t items = (int64_t)BH * (DV * (M * kPkRows<E> / 4) + M * E * (E + 1) / 2);
+  const int64_t items = (int64_t)BH * (DV * (M * kPkRows<E> / 4) + P / 4);
   kata_seg_scan_kernel<T, DK, DV, M><<<dim3((unsigned)((items + 255) / 256)), dim3(256), 0, stream>>>(a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
