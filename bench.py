@@ -608,6 +608,64 @@ def bench_state(prefill_reps, decode_steps, settle_s):
             "decode_packed_hbm_frac": round(decp_bytes / (decp_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
 
 
+def bench_gen_decode(decode_steps):
+    """Decode steps of the generic state kernels (linatt_kata_gen_decode: the
+    flash scores outside the MFMA state form) at batch 64, 12 heads, bf16,
+    from a fixed random fp32 state, in the full layout (P rows) and the
+    packed one (P' rows, one per pair a <= b: variant | LINATT_KATA_PACKED_STATE).
+    Fresh q, k, v ~ N(0,1)/8 per step, resident before timing.  Bytes per step:
+    the state read + written, 2 B H (P dv + P) 4, + inputs/outputs."""
+    import torch
+    from linatt_amd import _lib
+    from linatt_amd.kata_cache import state_rows
+    L = _lib.load()
+    dev = torch.device("cuda", 0)
+    B, H, dv = 64, 12, 64
+    dt = _lib.LINATT_BFLOAT16
+    out = {}
+    for name, dk, M, variant, decay in (("concat_m1_d64", 64, 1, "concat", False),
+                                        ("sum_m4_d64", 64, 4, "sum", False),
+                                        ("decay_m2_dk128", 128, 2, "concat", True)):
+        g = torch.Generator().manual_seed(21)
+        steps = [tuple((torch.randn(B, H, w, generator=g) / 8).to(torch.bfloat16).to(dev)
+                       for w in (dk, dk, dv)) for _ in range(decode_steps)]
+        c = torch.full((B, H), -0.01, device=dev) if decay else None
+        od = torch.empty(B, H, dv, device=dev, dtype=torch.bfloat16)
+        scale = 1.0 / math.sqrt(dk // M)
+        var0 = 1 if variant == "sum" else 0
+        res = {"dk": dk, "num_groups": M, "variant": variant, "decay": decay}
+        for tag, packed in (("full", False), ("packed", True)):
+            P = state_rows(dk, M, variant, packed)
+            S = (torch.randn(B, H, P, dv, generator=g) * 0.01).to(dev)
+            z = (1.0 + torch.rand(B, H, P, generator=g)).to(dev)
+            var = var0 | (_lib.LINATT_KATA_PACKED_STATE if packed else 0)
+
+            def dec(x):
+                _lib.check("linatt_kata_gen_decode", L.linatt_kata_gen_decode(
+                    _lib.ptr(x[0]), _lib.ptr(x[1]), _lib.ptr(x[2]), _lib.ptr(c), _lib.ptr(S),
+                    _lib.ptr(z), _lib.ptr(od), B, H, dk, dv, M, var, scale, 1e-6, dt,
+                    _lib.stream_of(od)))
+
+            dec(steps[0])
+            torch.cuda.synchronize()
+            stream = torch.cuda.current_stream(dev)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for x in steps:
+                dec(x)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / decode_steps
+            nbytes = 2 * B * H * (P * dv + P) * 4 + B * H * (2 * dk + 2 * dv) * 2
+            res[tag] = {"rows": P, "ms_per_step": round(ms, 4), "bytes_per_step": nbytes,
+                        "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                        "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+            del S, z
+        out[name] = res
+    out["config"] = {"B": B, "H": H, "dv": dv, "decode_steps": decode_steps, "seed": 21}
+    return out
+
+
 def _cpu_threads():
     """Threads for the CPU baselines: every core the host reports, capped at
     the 16 CPUs the GPU box allots to one GPU."""
@@ -882,9 +940,10 @@ def main():
                  "deltanet_h12_d64": bench_delta(False, ds, 2, st / 2, H=12, K=64),
                  "gated_deltanet_h12_d64": bench_delta(True, ds, 2, st / 2, H=12, K=64)}
 
-    state = None
+    state = gen_decode = None
     if not args.no_state:
         state = bench_state(3, args.decode_steps, args.settle_seconds / 3)
+        gen_decode = bench_gen_decode(max(16, args.decode_steps // 4))
 
     q1, config1 = bench_config1(max(10, args.steps))
     delta_kata = None if args.no_delta else bench_delta_kata(max(3, args.steps // 2),
@@ -941,6 +1000,7 @@ def main():
         "cpu_baseline": cpu,
         "delta_rule": delta,
         "kata_state_config5": state,
+        "kata_state_decode_generic": gen_decode,
         "kata_config1": config1,
         "delta_kata_fwd_bwd": delta_kata,
         "mixer_ops": mixer,

@@ -25,6 +25,9 @@ extern "C" {
 
 enum linatt_dtype { LINATT_FLOAT32 = 0, LINATT_BFLOAT16 = 1, LINATT_FLOAT16 = 2 };
 enum linatt_kata_variant { LINATT_KATA_CONCAT = 0, LINATT_KATA_SUM = 1 };
+/* OR-ed into the variant of the linatt_kata_gen_* calls: the packed state
+ * layout (one row per unordered pair a <= b). */
+enum { LINATT_KATA_PACKED_STATE = 4 };
 enum linatt_status {
   LINATT_OK = 0,
   LINATT_EINVAL = -1,       /* null pointer, bad shape or misalignment */
@@ -241,7 +244,12 @@ int linatt_delta_bwd_stages(const void* q, const void* k, const void* v, const f
  * decayed score (:291-310) within the call (each call's c starts from the
  * stored state at 0), non-increasing; NULL for no decay.
  *   S_t = e^(c_t - c_{t-1}) S_{t-1} + psi(k_t) v_t^T,  z likewise,
- *   o_t = psi(q_t)^T S_t / max(psi(q_t) . z_t, eps). */
+ *   o_t = psi(q_t)^T S_t / max(psi(q_t) . z_t, eps).
+ * variant | LINATT_KATA_PACKED_STATE keeps the state packed: psi's rows
+ * (a, b) and (b, a) are equal, so one row per pair a <= b of each group,
+ *   p = g TE + a E - a (a - 1) / 2 + (b - a),  TE = E (E + 1) / 2,
+ * P = num_groups TE (concat) or TE (sum); each row equals the full layout's
+ * row (a, b), and the readouts count an off-diagonal row twice. */
 
 /* Rows P of the state for (dk, num_groups, variant); 0 on bad arguments. */
 int linatt_kata_gen_state_rows(int dk, int num_groups, int variant);

@@ -22,6 +22,7 @@ ABI_VERSION = 3
 
 LINATT_FLOAT32, LINATT_BFLOAT16, LINATT_FLOAT16 = 0, 1, 2
 LINATT_KATA_CONCAT, LINATT_KATA_SUM = 0, 1
+LINATT_KATA_PACKED_STATE = 4  # OR-ed into a linatt_kata_gen_* variant
 STATUS = {0: "LINATT_OK", -1: "LINATT_EINVAL", -2: "LINATT_EUNSUPPORTED", -3: "LINATT_ELAUNCH"}
 
 _DTYPES = {torch.float32: LINATT_FLOAT32, torch.bfloat16: LINATT_BFLOAT16, torch.float16: LINATT_FLOAT16}

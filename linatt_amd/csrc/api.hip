@@ -1079,6 +1079,8 @@ static int gen_state_args(const char* fn, KataGenStateArgs& a, int B, int T, int
                           int M, int variant, float scale, float eps, int dtype) {
   if (B <= 0 || T <= 0 || H <= 0 || dk <= 0 || dv <= 0 || M <= 0)
     return fail(LINATT_EINVAL, std::string(fn) + ": non-positive dimension");
+  const int tri = (variant & LINATT_KATA_PACKED_STATE) ? 1 : 0;
+  variant &= ~LINATT_KATA_PACKED_STATE;
   if (variant != LINATT_KATA_CONCAT && variant != LINATT_KATA_SUM)
     return fail(LINATT_EINVAL, std::string(fn) + ": unknown KATA variant");
   if (!known_dtype(dtype)) return fail(LINATT_EINVAL, std::string(fn) + ": unknown dtype");
@@ -1094,7 +1096,9 @@ static int gen_state_args(const char* fn, KataGenStateArgs& a, int B, int T, int
   while ((1 << lgE) < E) ++lgE;
   a.B = B; a.T = T; a.H = H; a.dk = dk; a.E = E; a.lgE = lgE; a.M = M;
   a.sum = variant == LINATT_KATA_SUM ? 1 : 0;
-  a.P = a.sum ? E * E : M * E * E;
+  a.tri = tri;
+  a.TE = E * (E + 1) / 2;
+  a.P = (a.sum ? 1 : M) * (tri ? a.TE : E * E);
   a.scale = scale; a.eps = eps;
   return LINATT_OK;
 }
@@ -1108,7 +1112,10 @@ static int gen_state_launch(const char* fn, const KataGenStateArgs& a, int which
 int linatt_kata_gen_state_rows(int dk, int num_groups, int variant) {
   if (dk <= 0 || num_groups <= 0 || dk % num_groups) return 0;
   const int E = dk / num_groups;
-  return variant == LINATT_KATA_SUM ? E * E : num_groups * E * E;
+  const bool tri = (variant & LINATT_KATA_PACKED_STATE) != 0;
+  variant &= ~LINATT_KATA_PACKED_STATE;
+  if (variant != LINATT_KATA_CONCAT && variant != LINATT_KATA_SUM) return 0;
+  return (variant == LINATT_KATA_SUM ? 1 : num_groups) * (tri ? E * (E + 1) / 2 : E * E);
 }
 
 int linatt_kata_gen_decode(const void* q, const void* k, const void* v, const float* c, float* S,

@@ -152,6 +152,8 @@ struct KataGenStateArgs {
   void* o;           // decode: (B, H, 64) out; readout: (B, T, H, 64) in (flash) and out
   float* den;        // readout: (B, T, H) in (flash) and out
   int B, T, H, dk, E, lgE, M, P, sum;
+  int tri;           // 1: packed rows, one per unordered pair a <= b of each group
+  int TE;            // packed rows per group, E (E + 1) / 2
   float scale, eps;
   int init;          // update: 1 = add to f_T S, 0 = start from zero
 };

@@ -16,6 +16,13 @@
 // c is the cumulative log-decay within one call (the mixer's cumsum over the
 // call's tokens), so a stored state sits at c = 0 of the next call.
 //
+// psi(x)_{(a,b)} = psi(x)_{(b,a)} for both scores, so the state may also be
+// kept packed (tri = 1): one row per unordered pair a <= b of each group,
+//   p = g TE + a E - a (a - 1) / 2 + (b - a),  TE = E (E + 1) / 2,
+// (the concat score's P = M TE, the sum score's P = TE).  A packed row equals
+// the full layout's row (a, b) bit for bit (the same products in the same
+// order); the readouts weigh an off-diagonal row's q-side feature by 2.
+//
 // Three kernels, fp32 throughout (the state is fp32 (B, H, P, 64)):
 //   kata_gen_decode_kernel   one token per (b, h): S, z updated in place, o
 //   kata_gen_readout_kernel  a prefill continued from a state: the flash
@@ -33,16 +40,44 @@ namespace {
 
 constexpr int kGenDV = 64;
 
-// feature p of the row x (fp32), scaled by s
-__device__ __forceinline__ float psi_feat(const float* x, int p, int E, int lgE, int M, bool sum,
-                                          float s) {
-  if (!sum) {
-    const int g = p >> (2 * lgE), a = (p >> lgE) & (E - 1), b = p & (E - 1);
-    return s * x[g * E + a] * x[g * E + b];
+// State row p as (group, a, b) and the weight of its q-side feature in a
+// readout (2 for an off-diagonal packed row, which stands for (a, b) and
+// (b, a)).  The packed row index is inverted by the quadratic formula for
+// the row start a E - a (a - 1) / 2 and an exact integer correction.
+struct RowPair {
+  int g, a, b;
+  float w;
+};
+
+__device__ __forceinline__ RowPair row_pair(const KataGenStateArgs& k, int p) {
+  RowPair r;
+  if (!k.tri) {
+    r.g = k.sum ? 0 : p >> (2 * k.lgE);
+    r.a = (p >> k.lgE) & (k.E - 1);
+    r.b = p & (k.E - 1);
+    r.w = 1.f;
+    return r;
   }
-  const int a = p >> lgE, b = p & (E - 1);
+  r.g = k.sum ? 0 : p / k.TE;
+  const int q = p - r.g * k.TE, n = 2 * k.E + 1;
+  int i = (int)((n - sqrtf((float)(n * n - 8 * q))) * 0.5f);
+  i = min(max(i, 0), k.E - 1);
+  while (i > 0 && i * k.E - i * (i - 1) / 2 > q) --i;
+  while (i + 1 < k.E && (i + 1) * k.E - (i + 1) * i / 2 <= q) ++i;
+  r.a = i;
+  r.b = i + q - (i * k.E - i * (i - 1) / 2);
+  r.w = r.a == r.b ? 1.f : 2.f;
+  return r;
+}
+
+// feature (a, b) of group g of the row x (fp32), scaled by s; the product
+// x_a x_b is rounded before the scale, so (a, b) and (b, a) are equal bit
+// for bit and the full layout's state is exactly symmetric
+__device__ __forceinline__ float psi_feat(const float* x, const RowPair& r, int E, int M, bool sum,
+                                          float s) {
+  if (!sum) return s * (x[r.g * E + r.a] * x[r.g * E + r.b]);
   float acc = 0.f;
-  for (int g = 0; g < M; ++g) acc += x[g * E + a] * x[g * E + b];
+  for (int g = 0; g < M; ++g) acc += x[g * E + r.a] * x[g * E + r.b];
   return s * acc;
 }
 
@@ -75,19 +110,39 @@ __global__ __launch_bounds__(256) void kata_gen_decode_kernel(KataGenStateArgs a
   float dacc = 0.f;
   float* S = a.S + (size_t)bh * a.P * kGenDV;
   float* z = a.z + (size_t)bh * a.P;
-  for (int p = r; p < a.P; p += 16) {
-    const float pk = psi_feat(ks, p, a.E, a.lgE, a.M, a.sum, a.scale);
-    const float pq = psi_feat(qs, p, a.E, a.lgE, a.M, a.sum, a.scale);
-    float4* sp = reinterpret_cast<float4*>(S + (size_t)p * kGenDV + 4 * c4);
-    float4 x = *sp;
-    x.x = f * x.x + pk * vv.x; x.y = f * x.y + pk * vv.y;
-    x.z = f * x.z + pk * vv.z; x.w = f * x.w + pk * vv.w;
-    *sp = x;
-    num.x += pq * x.x; num.y += pq * x.y; num.z += pq * x.z; num.w += pq * x.w;
-    if (c4 == 0) {
-      const float zz = f * z[p] + pk;
-      z[p] = zz;
-      dacc += pq * zz;
+  // rows r, r + 16, ...: each thread loads kDecU rows before updating them,
+  // so that kDecU loads per thread are in flight
+  constexpr int kDecU = 4;
+  for (int p0 = r; p0 < a.P; p0 += 16 * kDecU) {
+    float4 xs[kDecU];
+    float zs[kDecU];
+#pragma unroll
+    for (int u = 0; u < kDecU; ++u) {
+      const int p = p0 + 16 * u;
+      xs[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      zs[u] = 0.f;
+      if (p < a.P) {
+        xs[u] = *reinterpret_cast<const float4*>(S + (size_t)p * kGenDV + 4 * c4);
+        if (c4 == 0) zs[u] = z[p];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kDecU; ++u) {
+      const int p = p0 + 16 * u;
+      if (p >= a.P) break;
+      const RowPair rp = row_pair(a, p);
+      const float pk = psi_feat(ks, rp, a.E, a.M, a.sum, a.scale);
+      const float pq = rp.w * psi_feat(qs, rp, a.E, a.M, a.sum, a.scale);
+      float4 x = xs[u];
+      x.x = f * x.x + pk * vv.x; x.y = f * x.y + pk * vv.y;
+      x.z = f * x.z + pk * vv.z; x.w = f * x.w + pk * vv.w;
+      *reinterpret_cast<float4*>(S + (size_t)p * kGenDV + 4 * c4) = x;
+      num.x += pq * x.x; num.y += pq * x.y; num.z += pq * x.z; num.w += pq * x.w;
+      if (c4 == 0) {
+        const float zz = f * zs[u] + pk;
+        z[p] = zz;
+        dacc += pq * zz;
+      }
     }
   }
   red[r][c4] = num;
@@ -109,8 +164,9 @@ __global__ __launch_bounds__(256) void kata_gen_decode_kernel(KataGenStateArgs a
 // Continued prefill: per (b, h, 64 queries).  Thread (qi, cj) = (tid / 16,
 // tid % 16) owns queries 4 qi .. 4 qi + 3 of the tile and value columns
 // 4 cj .. 4 cj + 3.  Per 32 state rows the workgroup forms psi of its 64
-// queries into LDS and stages the rows of S and z, then each thread adds
-// 16 products per row.  The result is combined with the flash forward's
+// queries into LDS and stages the rows of S and z (zeros past row P, which
+// the packed layout need not fill to a multiple of 32), then each thread
+// adds 16 products per row.  The result is combined with the flash forward's
 // (o, den) of the call's tokens, which o and den hold on entry:
 //   num = o den + f_t psi(q_t)^T S,  den' = den + f_t psi(q_t) . z,
 //   o = num / max(den', eps),  den = max(den', eps).
@@ -140,11 +196,18 @@ __global__ __launch_bounds__(256) void kata_gen_readout_kernel(KataGenStateArgs 
     __syncthreads();  // the previous rows are consumed (and Qs is complete)
     for (int i = tid; i < 32 * 64; i += 256) {
       const int pp = i >> 6, t = i & 63;
-      Ps[pp][t] = psi_feat(Qs[t], p0 + pp, a.E, a.lgE, a.M, a.sum, a.scale);
+      float f = 0.f;
+      if (p0 + pp < a.P) {
+        const RowPair rp = row_pair(a, p0 + pp);
+        f = rp.w * psi_feat(Qs[t], rp, a.E, a.M, a.sum, a.scale);
+      }
+      Ps[pp][t] = f;
     }
     for (int i = tid; i < 32 * 16; i += 256)
-      Sr[i >> 4][i & 15] = *reinterpret_cast<const float4*>(S + (size_t)(p0 + (i >> 4)) * kGenDV + 4 * (i & 15));
-    if (tid < 32) Zs[tid] = z[p0 + tid];
+      Sr[i >> 4][i & 15] = p0 + (i >> 4) < a.P
+                               ? *reinterpret_cast<const float4*>(S + (size_t)(p0 + (i >> 4)) * kGenDV + 4 * (i & 15))
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (tid < 32) Zs[tid] = p0 + tid < a.P ? z[p0 + tid] : 0.f;
     __syncthreads();
 #pragma unroll 4
     for (int pp = 0; pp < 32; ++pp) {
@@ -190,7 +253,9 @@ __global__ __launch_bounds__(256) void kata_gen_readout_kernel(KataGenStateArgs 
 
 // State update: per (b, h, 64 state rows).  Thread (ri, cj) owns rows
 // 4 ri .. 4 ri + 3 of the tile and columns 4 cj .. 4 cj + 3; tokens stream
-// through LDS 32 at a time with their weights f_Ts = exp(c_T - c_s).
+// through LDS 32 at a time with their weights f_Ts = exp(c_T - c_s).  Each
+// thread forms the features of one row (p0 + tid % 64); rows past P (the
+// packed layout's last tile) get zero features and are not stored.
 //   S <- (init ? f_T S : 0) + sum_s f_Ts psi(k_s) v_s^T,  z likewise.
 template <typename T>
 __global__ __launch_bounds__(256) void kata_gen_update_kernel(KataGenStateArgs a) {
@@ -202,6 +267,9 @@ __global__ __launch_bounds__(256) void kata_gen_update_kernel(KataGenStateArgs a
   const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H, p0 = blockIdx.y * 64;
   const int ri = tid >> 4, cj = tid & 15;
   const float cT = a.c ? a.c[((int64_t)b * a.T + a.T - 1) * a.H + h] : 0.f;
+  const int prow = p0 + (tid & 63);
+  const bool live = prow < a.P;
+  const RowPair rp = row_pair(a, live ? prow : 0);
   float4 acc[4];
   float zacc[4];
 #pragma unroll
@@ -230,8 +298,8 @@ __global__ __launch_bounds__(256) void kata_gen_update_kernel(KataGenStateArgs a
     }
     __syncthreads();
     for (int i = tid; i < 32 * 64; i += 256) {
-      const int s = i >> 6, pp = i & 63;
-      Ps[s][pp] = Ws[s] * psi_feat(Ks[s], p0 + pp, a.E, a.lgE, a.M, a.sum, a.scale);
+      const int s = i >> 6, pp = i & 63;  // pp = tid % 64: the row of rp
+      Ps[s][pp] = live ? Ws[s] * psi_feat(Ks[s], rp, a.E, a.M, a.sum, a.scale) : 0.f;
     }
     __syncthreads();
 #pragma unroll 4
@@ -253,6 +321,7 @@ __global__ __launch_bounds__(256) void kata_gen_update_kernel(KataGenStateArgs a
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int p = p0 + 4 * ri + i;
+    if (p >= a.P) break;
     float4* sp = reinterpret_cast<float4*>(S + (size_t)p * kGenDV + 4 * cj);
     float4 x = acc[i];
     if (a.init) {
@@ -272,7 +341,7 @@ hipError_t launch_kata_gen_state(const KataGenStateArgs& a, int which, hipStream
   else if (which == KATA_GEN_READOUT)
     kata_gen_readout_kernel<T><<<dim3(BH, (a.T + 63) / 64), dim3(256), 0, stream>>>(a);
   else
-    kata_gen_update_kernel<T><<<dim3(BH, a.P / 64), dim3(256), 0, stream>>>(a);
+    kata_gen_update_kernel<T><<<dim3(BH, (a.P + 63) / 64), dim3(256), 0, stream>>>(a);
   return hipGetLastError();
 }
 

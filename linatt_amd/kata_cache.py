@@ -14,6 +14,9 @@ Every flash score has an exact O(1)-per-token state form, kept here per layer:
 with psi(x) = vec(x_g x_g^T) per group for the concat score (P = M E^2),
 vec(sum_g x_g x_g^T) for the sum score (P = E^2), and, for the decayed
 score, S and z scaled by exp(c_t - c_{t-1}) before each token's term.
+Since x_g x_g^T is symmetric, a new state keeps only the rows a <= b of each
+group (P = M E (E + 1) / 2, or E (E + 1) / 2 for the sum score), which about
+halves a decode step's bytes and the cache's memory.
 
 The concat score without decay at the MFMA state-form shapes
 (``linatt_kata_state_supported``) takes a chunk of T > 1 tokens through the
@@ -52,17 +55,18 @@ import torch
 from . import _lib, spd_state
 from .parallel_kata_attn import _fwd as _kata_fwd
 
-__all__ = ["KataState", "parallel_kata_attn_cached", "LayerStateCache", "get_layer_cache",
+__all__ = ["KataState", "state_rows", "parallel_kata_attn_cached", "LayerStateCache", "get_layer_cache",
            "update_layer_cache"]
 
 
 class KataState(NamedTuple):
     """A layer's recurrent state: ``S (B, H, P, dv)``, ``z (B, H, P)`` float32,
     the number of tokens it covers, and the score it belongs to (``variant``
-    "concat" or "sum", ``num_groups``).  The concat score's MFMA path keeps
-    the packed layout (``spd_state.state_rows(dk, M, packed=True)`` rows, one
-    per unordered pair of each group; ``spd_state.unpack_state`` gives the
-    full one), and continues a full-layout state it is given as such."""
+    "concat" or "sum", ``num_groups``).  A new state is kept in the packed
+    layout (one row per unordered pair a <= b of each group: ``state_rows(dk,
+    M, variant, packed=True)`` rows; ``spd_state.unpack_state(S, z, G)`` with
+    G = M for the concat score, 1 for the sum score, gives the full one); a
+    full-layout state given to a call is continued as such."""
 
     S: torch.Tensor
     z: torch.Tensor
@@ -71,9 +75,11 @@ class KataState(NamedTuple):
     num_groups: int = 0
 
 
-def _state_rows(dk, M, variant):
+def state_rows(dk, M, variant="concat", packed=False):
+    """State rows per (b, h) of a score: M E^2 (concat) or E^2 (sum) in the
+    full layout, M E (E + 1) / 2 or E (E + 1) / 2 packed."""
     E = dk // M
-    return E * E if variant == "sum" else M * E * E
+    return (1 if variant == "sum" else M) * (E * (E + 1) // 2 if packed else E * E)
 
 
 def parallel_kata_attn_cached(q, k, v, state=None, num_groups=4, scale=None, eps=1e-6,
@@ -140,7 +146,12 @@ def _generic(q, k, v, state, M, scale, eps, variant, c, offset):
     var = _lib.LINATT_KATA_SUM if variant == "sum" else _lib.LINATT_KATA_CONCAT
     dt = v.dtype
     q, k, v = q.to(dt).contiguous(), k.to(dt).contiguous(), v.contiguous()
-    P = _state_rows(dk, M, variant)
+    # a new state is packed (a decode step streams about half the bytes); an
+    # existing one keeps its layout
+    packed = state is None or state.S.shape[2] == state_rows(dk, M, variant, True)
+    if packed:
+        var |= _lib.LINATT_KATA_PACKED_STATE
+    P = state_rows(dk, M, variant, packed)
     cf = None
     if c is not None:
         _lib.require_device(c)
@@ -151,7 +162,9 @@ def _generic(q, k, v, state, M, scale, eps, variant, c, offset):
         S, z = state.S, state.z
         if S.shape != (B, H, P, dv) or z.shape != (B, H, P) or S.dtype != torch.float32 \
                 or not (S.is_contiguous() and z.is_contiguous()):
-            raise ValueError(f"state must be contiguous float32 S {(B, H, P, dv)}, z {(B, H, P)}")
+            Pf, Pp = state_rows(dk, M, variant), state_rows(dk, M, variant, True)
+            raise ValueError(f"state must be contiguous float32 S {(B, H, Pf, dv)}, z {(B, H, Pf)} "
+                             f"or packed S {(B, H, Pp, dv)}, z {(B, H, Pp)}")
     L = _lib.load()
     code, sp = _lib.dtype_code(dt), _lib.stream_of(q)
     if T == 1 and state is not None:

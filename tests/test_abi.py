@@ -90,6 +90,28 @@ def test_version_and_support(lib):
     assert lib.linatt_kata_bwd_workspace_bytes(0, 10, 3, 64, BF16) == 0
 
 
+def test_gen_state_rows_full_and_packed(lib):
+    from linatt_amd.kata_cache import state_rows
+    PK = 4  # LINATT_KATA_PACKED_STATE
+    for dk, M in ((64, 1), (64, 2), (64, 4), (128, 2), (128, 8)):
+        E = dk // M
+        for var, name, G in ((0, "concat", M), (1, "sum", 1)):
+            assert lib.linatt_kata_gen_state_rows(dk, M, var) == G * E * E == state_rows(dk, M, name)
+            assert lib.linatt_kata_gen_state_rows(dk, M, var | PK) == G * E * (E + 1) // 2 \
+                == state_rows(dk, M, name, True)
+    assert lib.linatt_kata_gen_state_rows(64, 3, 0) == 0
+    assert lib.linatt_kata_gen_state_rows(64, 2, 2) == 0  # no variant 2
+    assert lib.linatt_kata_gen_state_rows(64, 2, 2 | PK) == 0
+
+
+def test_gen_state_rejects_unknown_variant_bits(lib):
+    null = None
+    for var in (2, 2 | 4, 8):
+        assert lib.linatt_kata_gen_decode(FAKE, FAKE, FAKE, null, FAKE, FAKE, FAKE, 1, 2, 64, 64, 2,
+                                          var, 0.25, 1e-6, 1, null) == -1
+        assert b"unknown KATA variant" in lib.linatt_last_error()
+
+
 FAKE = ctypes.c_void_p(1 << 20)  # aligned, never dereferenced on the host
 
 

@@ -11,8 +11,13 @@ Covered: the concat score with one group (P = 4096 state rows), the sum
 score (M = 2, 4), the decayed concat score (each call gets its own
 cumulative log-decay, as the mixer computes it), and the offset gate's
 padded width (dk = 128, two groups of 64 with zero padding, decayed, the
-``kataconv_cat_l2_gdn_340m`` mixer).
+``kataconv_cat_l2_gdn_340m`` mixer).  The cache keeps a new state packed
+(rows a <= b of each group); the same calls continued from the unpacked
+state must keep the full layout's rows a <= b equal to the packed rows bit
+for bit, and agree on the outputs within rounding.
 """
+
+import math
 
 import pytest
 import torch
@@ -105,3 +110,67 @@ def test_state_form_rejects_mismatched_state():
     _, st = parallel_kata_attn_cached(q, q, q, None, 2, None, variant="sum")
     with pytest.raises(ValueError, match="state is for the sum score"):
         parallel_kata_attn_cached(q, q, q, st, 2, None, variant="concat")
+
+
+def _inputs(case, B, H, T):
+    dk, M, variant, decay, padded = CASES[case]
+    seed = 7 + dk + M
+    q, k = gen((B, T, H, dk), seed, 0.5), gen((B, T, H, dk), seed + 1, 0.5)
+    v = gen((B, T, H, 64), seed + 3)
+    c = -(gen((B, T, H), seed + 4).abs() * 0.05).cumsum(1) if decay else None
+    scale = (1.0 / 32) ** 0.5 if padded else None
+    return q.bfloat16().cuda(), k.bfloat16().cuda(), v.bfloat16().cuda(), c, scale
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_packed_state_equals_full(case):
+    from linatt_amd import _lib, spd_state
+    from linatt_amd.kata_cache import KataState, parallel_kata_attn_cached, state_rows
+    dk, M, variant, decay, padded = CASES[case]
+    G = 1 if variant == "sum" else M
+    B, H, T = 2, 3, 160
+    splits = [0, 100, 101, 102, 140, 141, 160]
+    print(f"\npacked vs full state {case}: B{B} H{H} T{T}", flush=True)
+    q, k, v, c, scale = _inputs(case, B, H, T)
+    Pf, Pp = state_rows(dk, M, variant), state_rows(dk, M, variant, True)
+    L = _lib.load()
+    var = 1 if variant == "sum" else 0
+    sc = scale if scale is not None else 1.0 / math.sqrt(dk // M)  # the cache's default
+
+    def cc(s, e):
+        if c is None:
+            return None
+        return (c[:, s:e] - (c[:, s - 1:s] if s > 0 else 0.0)).cuda()
+
+    # a state from zero through the C-ABI in both layouts
+    n0 = splits[1]
+    c0 = cc(0, n0)
+    c0 = c0.contiguous() if c0 is not None else None
+    kk, vv = k[:, :n0].contiguous(), v[:, :n0].contiguous()
+    full = (torch.empty(B, H, Pf, 64, device="cuda"), torch.empty(B, H, Pf, device="cuda"))
+    pack = (torch.empty(B, H, Pp, 64, device="cuda"), torch.empty(B, H, Pp, device="cuda"))
+    for (S, z), vr in ((full, var), (pack, var | _lib.LINATT_KATA_PACKED_STATE)):
+        _lib.check("linatt_kata_gen_update", L.linatt_kata_gen_update(
+            _lib.ptr(kk), _lib.ptr(vv), _lib.ptr(c0), _lib.ptr(S), _lib.ptr(z), 0, B, n0, H, dk, 64,
+            M, vr, float(sc), _lib.dtype_code(v.dtype), _lib.stream_of(v)))
+    Sp, zp = spd_state.pack_state(*full, G)
+    assert torch.equal(Sp, pack[0]) and torch.equal(zp, pack[1])
+
+    # the cache from here on: the packed state and its unpacked copy
+    o_p, st_p = parallel_kata_attn_cached(q[:, :n0], k[:, :n0], v[:, :n0], None, M, scale,
+                                          variant=variant, c=cc(0, n0))
+    assert st_p.S.shape == (B, H, Pp, 64) and st_p.z.shape == (B, H, Pp)
+    assert torch.equal(st_p.S, pack[0]) and torch.equal(st_p.z, pack[1])
+    st_f = KataState(*spd_state.unpack_state(st_p.S, st_p.z, G), n0, variant, M)
+    assert torch.equal(st_f.S, full[0]) and torch.equal(st_f.z, full[1])
+    for s, e in zip(splits[1:-1], splits[2:]):
+        o_p, st_p = parallel_kata_attn_cached(q[:, s:e], k[:, s:e], v[:, s:e], st_p, M, scale,
+                                              variant=variant, c=cc(s, e))
+        o_f, st_f = parallel_kata_attn_cached(q[:, s:e], k[:, s:e], v[:, s:e], st_f, M, scale,
+                                              variant=variant, c=cc(s, e))
+        assert st_f.S.shape[2] == Pf and st_p.S.shape[2] == Pp
+        Sp, zp = spd_state.pack_state(st_f.S, st_f.z, G)
+        assert torch.equal(Sp, st_p.S) and torch.equal(zp, st_p.z), (s, e)
+        err = mar(o_p, o_f)
+        print(f"  call {s}:{e} packed vs full o {err:.1e}", flush=True)
+        assert err < 1e-2
