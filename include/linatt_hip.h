@@ -272,7 +272,10 @@ int linatt_kata_gen_readout(const void* q, const float* c, const float* S, const
 
 /* The state after the call's tokens: S <- (init ? e^{c_T} S : 0) +
  * sum_s e^{c_T - c_s} psi(k_s) v_s^T, z likewise; k (B,T,H,dk), v (B,T,H,64),
- * c (B,T,H) or NULL; S, z updated in place. */
+ * c (B,T,H) or NULL; S, z updated in place; k, v and S 16-byte aligned.
+ * 16-bit inputs: the products psi(k_s) v_s^T run on the matrix cores with
+ * psi(k_s) (formed in float32) and v_s rounded to bfloat16, accumulated in
+ * float32; z adds the float32 features; float32 inputs stay float32. */
 int linatt_kata_gen_update(const void* k, const void* v, const float* c, float* S, float* z,
                            int init, int B, int T, int H, int dk, int dv, int num_groups,
                            int variant, float scale, int dtype, void* stream);

@@ -1156,7 +1156,8 @@ int linatt_kata_gen_update(const void* k, const void* v, const float* c, float* 
   int st = gen_state_args(fn, a, B, T, H, dk, dv, num_groups, variant, scale, 1.f, dtype);
   if (st) return st;
   if (!k || !v || !S || !z) return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
-  if (!aligned16(S)) return fail(LINATT_EINVAL, std::string(fn) + ": S must be 16-byte aligned");
+  if (!aligned16(S) || !aligned16(k) || !aligned16(v))
+    return fail(LINATT_EINVAL, std::string(fn) + ": k, v and S must be 16-byte aligned");
   a.k = k; a.v = v; a.c = c; a.S = S; a.z = z; a.init = init ? 1 : 0;
   return gen_state_launch(fn, a, KATA_GEN_UPDATE, dtype, stream);
 }

@@ -31,6 +31,8 @@
 //   kata_gen_update_kernel   S <- f_T S + sum_s f_Ts psi(k_s) v_s^T (and z)
 // The concat score without decay at (dk, M) = (64, 2), (64, 4) keeps its
 // MFMA state-form kernels (kata_state.hip); these cover the rest.
+#include <type_traits>
+
 #include "common.h"
 #include "kata_kernels.h"
 
@@ -333,13 +335,427 @@ __global__ __launch_bounds__(256) void kata_gen_update_kernel(KataGenStateArgs a
   }
 }
 
+// State update for 16-bit inputs, by MFMA: per (b, h, 128 RB state rows),
+// four waves of RB 32-row blocks, and NCB of the two 32-column halves of the
+// state (NCB = 1: blockIdx.z picks the half; a small state takes RB = 1,
+// NCB = 1, so that more workgroups share it).  Tokens stream through LDS 64 at
+// a time, the next 64's global loads in flight while the current ones are used:
+//   Kt[d][s] = sqrt(scale f_Ts) k_s[d]  (fp32, dimension-major),
+//   Vt[n][s] = v_s[n]                   (bf16, column-major).
+// Lane l of a wave forms, for each of its rows p (l % 32 of a block) and the
+// tokens 8 (l / 32) + 0..7 of each 16-token step, the features
+// scale f_Ts k_s[a] k_s[b] = Kt[a][s] Kt[b][s] (the sum score: summed over
+// the groups) in fp32, rounded to bf16 as the A operand of
+// v_mfma_f32_32x32x16_bf16; the 32-column halves of Vt are the B operands,
+// shared by the row blocks.  z sums the fp32 features per lane (the two lane
+// halves are added at the end; with NCB = 1 the first half's workgroup
+// stores it).  Staging moves token pairs:
+// one 8-byte LDS write per (dimension, pair) of K, one 4-byte write per
+// (column, pair) of V.
+//   S <- (init ? f_T S : 0) + sum_s f_Ts psi(k_s) v_s^T,  z likewise.
+constexpr int kUpTok = 64, kUpKp = kUpTok + 4, kUpVp = kUpTok + 8;
+
+template <typename T, bool SUM, int RB, int NCB>
+__global__ __launch_bounds__(256) void kata_gen_update_mfma_kernel(KataGenStateArgs a) {
+  static_assert(sizeof(T) == 2, "16-bit inputs");
+  __shared__ __attribute__((aligned(16))) float Kt[128][kUpKp];
+  __shared__ __attribute__((aligned(16))) __bf16 Vt[32 * NCB][kUpVp];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hh = lane >> 5, cl = lane & 31;
+  const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H;
+  const int n0c = NCB == 2 ? 0 : 32 * blockIdx.z;  // first state column of this workgroup
+  const int pw = blockIdx.y * 128 * RB + 32 * RB * w;  // this wave's first row
+  const bool wlive = pw < a.P;
+  int ia[RB], ib[RB];
+  bool live[RB];
+#pragma unroll
+  for (int k = 0; k < RB; ++k) {
+    const int p = pw + 32 * k + cl;
+    live[k] = p < a.P;
+    const RowPair rp = row_pair(a, live[k] ? p : 0);
+    ia[k] = rp.g * a.E + rp.a;
+    ib[k] = rp.g * a.E + rp.b;
+  }
+  const float cT = a.c ? a.c[((int64_t)b * a.T + a.T - 1) * a.H + h] : 0.f;
+  const int dk8 = a.dk >> 3;
+  const T* kg = reinterpret_cast<const T*>(a.k);
+  const T* vg = reinterpret_cast<const T*>(a.v);
+
+  // prefetch registers: K items (token pair, 8 dimensions), up to two per
+  // thread (32 pairs x dk / 8 / 256 threads at dk = 128); one V item (token
+  // pair, 8 columns; the first 128 threads when NCB = 1)
+  v8_t<T> kr[2][2], vr[2];
+  float kc[2][2];
+  auto load = [&](int s0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int i = tid + 256 * it, sp = i / dk8, d0 = 8 * (i % dk8);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int t = s0 + 2 * sp + u;
+        kr[it][u] = zero8<T>();
+        kc[it][u] = 0.f;
+        if (i < (kUpTok / 2) * dk8 && t < a.T) {
+          const int64_t row = ((int64_t)b * a.T + t) * a.H + h;
+          kr[it][u] = ld8<T>(kg + row * a.dk + d0);
+          kc[it][u] = a.c ? a.c[row] : 0.f;
+        }
+      }
+    }
+    const int sp = tid / (4 * NCB), n0 = 8 * (tid % (4 * NCB));
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int t = s0 + 2 * sp + u;
+      vr[u] = sp < kUpTok / 2 && t < a.T ? ld8<T>(vg + (((int64_t)b * a.T + t) * a.H + h) * kGenDV + n0c + n0)
+                                          : zero8<T>();
+    }
+  };
+  auto stage = [&](int s0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int i = tid + 256 * it;
+      if (i < (kUpTok / 2) * dk8) {
+        const int sp = i / dk8, d0 = 8 * (i % dk8);
+        float f[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          f[u] = s0 + 2 * sp + u < a.T ? sqrtf(a.scale * (a.c ? __expf(cT - kc[it][u]) : 1.f)) : 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          *reinterpret_cast<float2*>(&Kt[d0 + j][2 * sp]) =
+              make_float2((float)kr[it][0][j] * f[0], (float)kr[it][1][j] * f[1]);
+      }
+    }
+    const int sp = tid / (4 * NCB), n0 = 8 * (tid % (4 * NCB));
+    if (sp < kUpTok / 2) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<bf16x2*>(&Vt[n0 + j][2 * sp]) =
+            bf16x2{(__bf16)(float)vr[0][j], (__bf16)(float)vr[1][j]};
+      }
+    }
+  };
+  auto features = [&](int k, int sb) __attribute__((always_inline)) {
+    f32x8 fe{};
+#pragma unroll
+    for (int g = 0; g < (SUM ? 8 : 1); ++g) {
+      if (SUM && g >= a.M) break;
+      const float* ra = &Kt[ia[k] + g * a.E][sb];
+      const float* rb = &Kt[ib[k] + g * a.E][sb];
+      const f32x4 a0 = *reinterpret_cast<const f32x4*>(ra), a1 = *reinterpret_cast<const f32x4*>(ra + 4);
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(rb), b1 = *reinterpret_cast<const f32x4*>(rb + 4);
+      fe += f32x8{a0[0] * b0[0], a0[1] * b0[1], a0[2] * b0[2], a0[3] * b0[3],
+                  a1[0] * b1[0], a1[1] * b1[1], a1[2] * b1[2], a1[3] * b1[3]};
+    }
+    return live[k] ? fe : f32x8{};
+  };
+
+  f32x16 acc[RB][NCB] = {};
+  float zacc[RB] = {};
+  load(0);
+  for (int s0 = 0; s0 < a.T; s0 += kUpTok) {
+    __syncthreads();  // the previous tokens are consumed
+    stage(s0);
+    __syncthreads();
+    if (s0 + kUpTok < a.T) load(s0 + kUpTok);
+    if (wlive) {
+#pragma unroll
+      for (int kk = 0; kk < kUpTok / 16; ++kk) {
+        const int sb = 16 * kk + 8 * hh;
+        bf16x8 Bv[NCB];
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) Bv[cb] = *reinterpret_cast<const bf16x8*>(&Vt[32 * cb + cl][sb]);
+#pragma unroll
+        for (int k = 0; k < RB; ++k) {
+          const f32x8 fe = features(k, sb);
+          zacc[k] += ((fe[0] + fe[1]) + (fe[2] + fe[3])) + ((fe[4] + fe[5]) + (fe[6] + fe[7]));
+          const bf16x8 A = __builtin_convertvector(fe, bf16x8);
+#pragma unroll
+          for (int cb = 0; cb < NCB; ++cb) acc[k][cb] = mma(A, Bv[cb], acc[k][cb]);
+        }
+      }
+    }
+  }
+  if (!wlive) return;
+  const float fT = a.c ? __expf(cT) : 1.f;
+  float* S = a.S + (size_t)bh * a.P * kGenDV;
+  float* z = a.z + (size_t)bh * a.P;
+#pragma unroll
+  for (int k = 0; k < RB; ++k) {
+    zacc[k] += __shfl_xor(zacc[k], 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int p = pw + 32 * k + 8 * i + 4 * hh + r;
+        if (p < a.P) {
+          float* sp = S + (size_t)p * kGenDV + n0c;
+#pragma unroll
+          for (int cb = 0; cb < NCB; ++cb) {
+            float x = acc[k][cb][4 * i + r];
+            if (a.init) x += fT * sp[32 * cb + cl];
+            sp[32 * cb + cl] = x;
+          }
+        }
+      }
+    const int p = pw + 32 * k + cl;
+    if (hh == 0 && live[k] && n0c == 0) z[p] = (a.init ? fT * z[p] : 0.f) + zacc[k];
+  }
+}
+
+// Continued prefill's state part for 16-bit inputs, by MFMA: per (b, h, 128
+// queries), four waves of 32 queries.  The queries sit in LDS as fp32
+// q~ = sqrt(scale) q.  The state rows are taken in chunks of 16 with one
+// first index a and consecutive second indices b = 16 j .. 16 j + 15 of a
+// group g: the full layout's rows in order; for the packed layout every
+// (a, j) with 16 j + 15 >= a, the rows b < a of such a chunk being zero.  So
+// lane l of a wave forms, for its query t (l % 32) and the rows
+// 8 (l / 32) + 0..7 of a chunk, the features q~_t[gE + a] q~_t[gE + b] from
+// one scalar and two 16-byte LDS reads (summed over the groups for the sum
+// score), in fp32, rounded to bf16 as the A operand of
+// v_mfma_f32_32x32x16_bf16.  Per four chunks the workgroup stages
+//   Bt[n][r] = w_r S[row r][n] (bf16, column-major: the B operands) and
+//   Zs[r] = w_r z[row r],
+// w_r = 2 for an off-diagonal packed row (exact in bf16), 1 on the diagonal
+// and in the full layout, 0 for a padding row; the next four chunks' S and z
+// are in registers meanwhile.  den adds the fp32 features times Zs.  The
+// result is combined with the flash forward's (o, den) as the VALU kernel
+// does.  Each group has the same chunks, a multiple of four of them; their
+// (a, 16 j) sit in an LDS table built once per workgroup.  DKMAX (64 or 128)
+// sizes the query tile and the table (at most E^2 / 16 chunks, E <= dk); at
+// DKMAX = 128 the tile keeps the inputs' 16-bit values (exact), converted as
+// they are read, and the scale multiplies the sums instead, so that three
+// workgroups fit a CU's LDS.
+constexpr int kRoRows = 64, kRoBp = kRoRows + 8;
+
+// chunk cc of a group in the readout's chunk order: (a, 16 j)
+__device__ __forceinline__ int2 readout_chunk(const KataGenStateArgs& k, int cc) {
+  const int nb = k.E >> 4;
+  int a, j;
+  if (!k.tri) {
+    a = cc / nb;
+    j = cc - a * nb;
+  } else {
+    // a in block beta = a / 16 has nb - beta chunks (j = beta .. nb - 1)
+    int beta = 0, base = 0;
+    while (beta + 1 < nb && base + 16 * (nb - beta) <= cc) {
+      base += 16 * (nb - beta);
+      ++beta;
+    }
+    const int per = nb - beta, rem = cc - base;
+    a = 16 * beta + rem / per;
+    j = beta + rem % per;
+  }
+  return make_int2(a, 16 * j);
+}
+
+template <typename T, bool SUM, int DKMAX>
+__global__ __launch_bounds__(256) void kata_gen_readout_mfma_kernel(KataGenStateArgs a) {
+  static_assert(sizeof(T) == 2, "16-bit inputs");
+  constexpr bool kQ16 = DKMAX > 64;
+  using QT = typename std::conditional<kQ16, T, float>::type;
+  constexpr int kRoQp = DKMAX + (kQ16 ? 8 : 4), kRoMaxCpg = DKMAX * DKMAX / 16;
+  __shared__ __attribute__((aligned(16))) QT Qs[128 * kRoQp];
+  __shared__ __attribute__((aligned(16))) __bf16 Bt[kGenDV][kRoBp];
+  __shared__ __attribute__((aligned(16))) float Zs[kRoRows];
+  __shared__ int2 Ci[kRoRows / 16];
+  __shared__ int2 Ctab[kRoMaxCpg];
+  __shared__ float Dq[4][32];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hh = lane >> 5, cl = lane & 31;
+  const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H, t0 = blockIdx.y * 128;
+  const T* qg = reinterpret_cast<const T*>(a.q);
+  const float sq = sqrtf(a.scale);
+  {
+    const int dk8 = a.dk >> 3;
+    for (int i = tid; i < 128 * dk8; i += 256) {
+      const int t = i / dk8, d0 = 8 * (i % dk8);
+      v8_t<T> x = zero8<T>();
+      if (t0 + t < a.T) x = ld8<T>(qg + (((int64_t)b * a.T + t0 + t) * a.H + h) * a.dk + d0);
+      if constexpr (kQ16) {
+        *reinterpret_cast<v8_t<T>*>(&Qs[t * kRoQp + d0]) = x;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) Qs[t * kRoQp + d0 + j] = (float)x[j] * sq;
+      }
+    }
+  }
+  const float* S = a.S + (size_t)bh * a.P * kGenDV;
+  const float* z = a.z + (size_t)bh * a.P;
+  const int nb = a.E >> 4;
+  const int cpg = a.tri ? a.E * (a.E + 16) / 32 : a.E * nb;  // chunks per group
+  const int nch = (a.sum ? 1 : a.M) * cpg;
+  for (int c = tid; c < cpg; c += 256) Ctab[c] = readout_chunk(a, c);
+  __syncthreads();
+  // thread: row 16 it + tid / 16 (chunk it, b offset tid / 16) of the four
+  // chunks, columns 4 (tid % 16) .. + 3; z of row tid by the first 64 threads
+  float4 sr[4];
+  float wr[4];
+  float zr = 0.f;
+  int2 cr[4];
+  auto row_of = [&](int g, int2 t, int bo, float& wgt) __attribute__((always_inline)) {
+    // t = (a, 16 j) of group g: the storage row of (a, b = 16 j + bo), or -1
+    const int ra = t.x, rb = t.y + bo;
+    if (!a.tri) {
+      wgt = 1.f;
+      return (g * a.E + ra) * a.E + rb;
+    }
+    if (rb < ra) {
+      wgt = 0.f;
+      return -1;
+    }
+    wgt = rb == ra ? 1.f : 2.f;
+    return g * a.TE + ra * a.E - ra * (ra - 1) / 2 + (rb - ra);
+  };
+  // c0: a multiple of four, so the four chunks share the group
+  auto load = [&](int c0) __attribute__((always_inline)) {
+    const int g = c0 / cpg, cc0 = c0 - g * cpg;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int2 t = Ctab[cc0 + it];
+      cr[it] = make_int2(g * a.E + t.x, g * a.E + t.y);
+      float wg = 0.f;
+      const int p = row_of(g, t, tid >> 4, wg);
+      wr[it] = p >= 0 ? wg : 0.f;
+      sr[it] = p >= 0 ? *reinterpret_cast<const float4*>(S + (size_t)p * kGenDV + 4 * (tid & 15))
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (tid < kRoRows) {
+      float wg = 0.f;
+      const int p = row_of(g, Ctab[cc0 + (tid >> 4)], tid & 15, wg);
+      zr = p >= 0 ? wg * z[p] : 0.f;
+    }
+  };
+  auto stage = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int r = 16 * it + (tid >> 4), n0 = 4 * (tid & 15);
+      Bt[n0 + 0][r] = (__bf16)(wr[it] * sr[it].x);
+      Bt[n0 + 1][r] = (__bf16)(wr[it] * sr[it].y);
+      Bt[n0 + 2][r] = (__bf16)(wr[it] * sr[it].z);
+      Bt[n0 + 3][r] = (__bf16)(wr[it] * sr[it].w);
+    }
+    if (tid < kRoRows) Zs[tid] = zr;
+    if (tid == 0) {
+#pragma unroll
+      for (int it = 0; it < 4; ++it) Ci[it] = cr[it];
+    }
+  };
+
+  const QT* qrow = Qs + (32 * w + cl) * kRoQp;
+  f32x16 acc0{}, acc1{};
+  float dacc = 0.f;
+  load(0);
+  for (int c0 = 0; c0 < nch; c0 += kRoRows / 16) {
+    __syncthreads();  // the previous rows are consumed (and Qs is complete)
+    stage();
+    __syncthreads();
+    if (c0 + kRoRows / 16 < nch) load(c0 + kRoRows / 16);
+#pragma unroll
+    for (int kk = 0; kk < kRoRows / 16; ++kk) {
+      const int2 ci = Ci[kk];
+      const int rb = 16 * kk + 8 * hh;
+      f32x8 fe{};
+#pragma unroll
+      for (int g = 0; g < (SUM ? 8 : 1); ++g) {
+        if (SUM && g >= a.M) break;
+        const float qa = (float)qrow[ci.x + g * a.E];
+        const QT* qb = qrow + ci.y + g * a.E + 8 * hh;
+        f32x8 bq;
+        if constexpr (kQ16) {
+          const v8_t<T> x = *reinterpret_cast<const v8_t<T>*>(qb);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) bq[j] = (float)x[j];
+        } else {
+          const f32x4 b0 = *reinterpret_cast<const f32x4*>(qb), b1 = *reinterpret_cast<const f32x4*>(qb + 4);
+          bq = f32x8{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+        }
+        fe += qa * bq;
+      }
+      const f32x4 z0 = *reinterpret_cast<const f32x4*>(&Zs[rb]);
+      const f32x4 z1 = *reinterpret_cast<const f32x4*>(&Zs[rb + 4]);
+      dacc += ((fe[0] * z0[0] + fe[1] * z0[1]) + (fe[2] * z0[2] + fe[3] * z0[3])) +
+              ((fe[4] * z1[0] + fe[5] * z1[1]) + (fe[6] * z1[2] + fe[7] * z1[3]));
+      const bf16x8 A = __builtin_convertvector(fe, bf16x8);
+      acc0 = mma(A, *reinterpret_cast<const bf16x8*>(&Bt[cl][rb]), acc0);
+      acc1 = mma(A, *reinterpret_cast<const bf16x8*>(&Bt[32 + cl][rb]), acc1);
+    }
+  }
+  // den part of query 32 w + l % 32: the two lane halves; then every lane
+  // reads the queries of its C-layout rows
+  dacc += __shfl_xor(dacc, 32);
+  // the 16-bit tile holds q, not q~: the scale multiplies the sums
+  const float fs = kQ16 ? a.scale : 1.f;
+  if (hh == 0) Dq[w][cl] = dacc;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tq = 32 * w + 8 * i + 4 * hh + r, t = t0 + tq;
+      if (t >= a.T) continue;
+      const int64_t row = ((int64_t)b * a.T + t) * a.H + h;
+      const float fd = (a.c ? __expf(a.c[row]) : 1.f) * fs;
+      const float df = a.den[row];
+      const float dsc = fmaxf(df + fd * Dq[w][8 * i + 4 * hh + r], a.eps), inv = 1.f / dsc;
+      T* orow = (T*)a.o + row * kGenDV;
+      orow[cl] = (T)(((float)orow[cl] * df + fd * acc0[4 * i + r]) * inv);
+      orow[32 + cl] = (T)(((float)orow[32 + cl] * df + fd * acc1[4 * i + r]) * inv);
+    }
+  // den after every lane of the wave has read it (its queries are this
+  // wave's alone)
+  __syncthreads();
+  if (hh == 0) {
+    const int t = t0 + 32 * w + cl;
+    if (t < a.T) {
+      const int64_t row = ((int64_t)b * a.T + t) * a.H + h;
+      const float fd = (a.c ? __expf(a.c[row]) : 1.f) * fs;
+      a.den[row] = fmaxf(a.den[row] + fd * Dq[w][cl], a.eps);
+    }
+  }
+}
+
 template <typename T>
 hipError_t launch_kata_gen_state(const KataGenStateArgs& a, int which, hipStream_t stream) {
   const int BH = a.B * a.H;
   if (which == KATA_GEN_DECODE)
     kata_gen_decode_kernel<T><<<dim3(BH), dim3(256), 0, stream>>>(a);
-  else if (which == KATA_GEN_READOUT)
-    kata_gen_readout_kernel<T><<<dim3(BH, (a.T + 63) / 64), dim3(256), 0, stream>>>(a);
+  else if (which == KATA_GEN_READOUT) {
+    if constexpr (sizeof(T) == 2) {
+      const dim3 grid(BH, (a.T + 127) / 128);
+      if (a.dk <= 64) {
+        if (a.sum)
+          kata_gen_readout_mfma_kernel<T, true, 64><<<grid, dim3(256), 0, stream>>>(a);
+        else
+          kata_gen_readout_mfma_kernel<T, false, 64><<<grid, dim3(256), 0, stream>>>(a);
+      } else {
+        if (a.sum)
+          kata_gen_readout_mfma_kernel<T, true, 128><<<grid, dim3(256), 0, stream>>>(a);
+        else
+          kata_gen_readout_mfma_kernel<T, false, 128><<<grid, dim3(256), 0, stream>>>(a);
+      }
+    }
+    else
+      kata_gen_readout_kernel<T><<<dim3(BH, (a.T + 63) / 64), dim3(256), 0, stream>>>(a);
+  }
+  else if constexpr (sizeof(T) == 2) {
+    // 256 rows and both column halves per workgroup; a state of at most
+    // 256 rows that would leave CUs idle takes 128 rows and one half (more
+    // workgroups, each streaming every token: the staging, not the products,
+    // is this kernel's cost, so larger states keep the 256-row tiles)
+    if (a.P > 256 || (int64_t)BH * ((a.P + 255) / 256) >= 512) {
+      const dim3 grid(BH, (a.P + 255) / 256);
+      if (a.sum)
+        kata_gen_update_mfma_kernel<T, true, 2, 2><<<grid, dim3(256), 0, stream>>>(a);
+      else
+        kata_gen_update_mfma_kernel<T, false, 2, 2><<<grid, dim3(256), 0, stream>>>(a);
+    } else {
+      const dim3 grid(BH, (a.P + 127) / 128, 2);
+      if (a.sum)
+        kata_gen_update_mfma_kernel<T, true, 1, 1><<<grid, dim3(256), 0, stream>>>(a);
+      else
+        kata_gen_update_mfma_kernel<T, false, 1, 1><<<grid, dim3(256), 0, stream>>>(a);
+    }
+  }
   else
     kata_gen_update_kernel<T><<<dim3(BH, (a.P + 63) / 64), dim3(256), 0, stream>>>(a);
   return hipGetLastError();

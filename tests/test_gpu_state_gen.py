@@ -174,3 +174,81 @@ def test_packed_state_equals_full(case):
         err = mar(o_p, o_f)
         print(f"  call {s}:{e} packed vs full o {err:.1e}", flush=True)
         assert err < 1e-2
+
+
+DIRECT = [  # (dk, M, variant, packed, decay): group widths 128 (M = 1, dk = 128), 64, 32 and 16
+    (128, 1, "concat", False, False),
+    (128, 1, "concat", True, True),
+    (64, 2, "concat", True, False),
+    (64, 2, "sum", False, True),
+    (64, 4, "sum", True, False),
+    (128, 4, "concat", True, False),
+]
+
+
+@pytest.mark.parametrize("dk,M,variant,packed,decay", DIRECT)
+def test_update_readout_direct(dk, M, variant, packed, decay):
+    """``linatt_kata_gen_update`` from zero then ``linatt_kata_gen_readout``
+    through the C ABI against the state formulas in float64 with the full
+    feature map psi(x) = vec(scale x_g x_g^T) (summed over g for the sum
+    score), including group widths the cached attention cannot reach."""
+    from linatt_amd import _lib, spd_state
+    from linatt_amd.kata_cache import state_rows
+    B, H, T, dv = 2, 3, 150, 64
+    E = dk // M
+    G = 1 if variant == "sum" else M
+    print(f"\ndirect gen update/readout dk{dk} M{M} {variant} packed={packed} decay={decay}",
+          flush=True)
+    g0 = 900 + dk + M + 7 * packed
+    q, k = gen((B, T, H, dk), g0, 0.5).bfloat16(), gen((B, T, H, dk), g0 + 1, 0.5).bfloat16()
+    v = gen((B, T, H, dv), g0 + 2).bfloat16()
+    c = -(gen((B, T, H), g0 + 3).abs() * 0.05).cumsum(1) if decay else None
+    o_in = gen((B, T, H, dv), g0 + 4).bfloat16()
+    den_in = gen((B, T, H), g0 + 5).abs() + 0.5
+    scale = 1.0 / math.sqrt(E)
+
+    def psi(x):
+        xg = x.double().reshape(*x.shape[:-1], M, E)
+        outer = scale * xg[..., :, None] * xg[..., None, :]
+        if variant == "sum":
+            return outer.sum(-3).flatten(-2)
+        return outer.flatten(-3)
+
+    pk, pq = psi(k), psi(q)  # (B, T, H, Pf)
+    wk = torch.ones(B, T, H, dtype=torch.float64)
+    fq = torch.ones(B, T, H, dtype=torch.float64)
+    if decay:
+        cd = c.double()
+        wk = torch.exp(cd[:, -1:] - cd)
+        fq = torch.exp(cd)
+    S_ref = torch.einsum("bthp,bthn->bhpn", pk * wk[..., None], v.double())
+    z_ref = (pk * wk[..., None]).sum(1)
+    num = o_in.double() * den_in.double()[..., None] + fq[..., None] * torch.einsum(
+        "bthp,bhpn->bthn", pq, S_ref)
+    den = den_in.double() + fq * torch.einsum("bthp,bhp->bth", pq, z_ref)
+    o_ref = num / den.clamp_min(1e-6)[..., None]
+
+    L = _lib.load()
+    var = (1 if variant == "sum" else 0) | (_lib.LINATT_KATA_PACKED_STATE if packed else 0)
+    P = state_rows(dk, M, variant, packed)
+    assert L.linatt_kata_gen_state_rows(dk, M, var) == P
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    cdv = c.float().cuda() if decay else None
+    S = torch.empty(B, H, P, dv, device="cuda")
+    z = torch.empty(B, H, P, device="cuda")
+    code, sp = _lib.dtype_code(v.dtype), _lib.stream_of(vd)
+    _lib.check("linatt_kata_gen_update", L.linatt_kata_gen_update(
+        _lib.ptr(kd), _lib.ptr(vd), _lib.ptr(cdv), _lib.ptr(S), _lib.ptr(z), 0, B, T, H, dk, dv,
+        M, var, scale, code, sp))
+    o = o_in.cuda()
+    dn = den_in.float().cuda()
+    _lib.check("linatt_kata_gen_readout", L.linatt_kata_gen_readout(
+        _lib.ptr(qd), _lib.ptr(cdv), _lib.ptr(S), _lib.ptr(z), _lib.ptr(o), _lib.ptr(dn), B, T, H,
+        dk, dv, M, var, scale, 1e-6, code, sp))
+    torch.cuda.synchronize()
+    S_c, z_c = S.cpu(), z.cpu()
+    if packed:
+        S_c, z_c = spd_state.unpack_state(S_c, z_c, G)
+    errs = (mar(S_c, S_ref), mar(z_c, z_ref), mar(o, o_ref), mar(dn, den.clamp_min(1e-6)))
+    print("  S %.1e z %.1e o %.1e den %.1e" % errs, flush=True)
+    assert max(errs) < BAR
