@@ -666,6 +666,71 @@ def bench_gen_decode(decode_steps):
     return out
 
 
+def bench_gen_prefill(reps):
+    """Cached prefill of the flash scores outside the MFMA state form
+    (``kata_cache.parallel_kata_attn_cached``: the flash forward, then the
+    generic state kernels) at B8 H12 T2048 bf16: from an empty cache
+    (forward + state update) and continued from a state of 2048 tokens
+    (forward + readout + update).  The update's and readout's products are
+    2 B H T P dv FLOP each (P the packed state rows)."""
+    import torch
+    from linatt_amd.kata_cache import parallel_kata_attn_cached
+    from linatt_amd.parallel_kata_attn import _fwd as kata_fwd
+    dev = torch.device("cuda", 0)
+    B, H, T, dv = 8, 12, 2048, 64
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    out = {}
+    for name, dk, M, variant, decay in (("concat_m1_d64", 64, 1, "concat", False),
+                                        ("sum_m4_d64", 64, 4, "sum", False),
+                                        ("sum_m2_d64", 64, 2, "sum", False),
+                                        ("decay_m2_dk128", 128, 2, "concat", True)):
+        g = torch.Generator().manual_seed(31)
+        q, k = ((torch.randn(B, T, H, dk, generator=g) * 0.5).to(torch.bfloat16).to(dev)
+                for _ in range(2))
+        v = torch.randn(B, T, H, dv, generator=g).to(torch.bfloat16).to(dev)
+        c = -(torch.rand(B, T, H, generator=g) * 0.05).cumsum(1).to(dev) if decay else None
+        sc = 1.0 / math.sqrt(dk // M)
+        fwd_ms = timed(lambda: kata_fwd(q, k, v, M, sc, variant, c))
+        pre_ms = timed(lambda: parallel_kata_attn_cached(q, k, v, None, M, None, variant=variant,
+                                                         c=c))
+        _, st = parallel_kata_attn_cached(q, k, v, None, M, None, variant=variant, c=c)
+        S0, z0 = st.S.clone(), st.z.clone()
+
+        def restore():
+            st.S.copy_(S0)
+            st.z.copy_(z0)
+
+        def cont():
+            restore()
+            parallel_kata_attn_cached(q, k, v, st, M, None, variant=variant, c=c)
+
+        cont_ms = timed(cont) - timed(restore)
+        P = st.S.shape[2]
+        flop = 2 * B * H * T * P * dv
+        upd_ms = pre_ms - fwd_ms
+        out[name] = {"state_rows": P, "forward_ms": round(fwd_ms, 4),
+                     "prefill_from_empty_ms": round(pre_ms, 4),
+                     "continued_prefill_ms": round(cont_ms, 4),
+                     "update_ms": round(upd_ms, 4), "readout_ms": round(cont_ms - pre_ms, 4),
+                     "update_tflops": round(flop / (upd_ms * 1e-3) / 1e12, 1),
+                     "readout_tflops": round(flop / ((cont_ms - pre_ms) * 1e-3) / 1e12, 1)}
+        del st, S0, z0
+    out["config"] = {"B": B, "H": H, "T": T, "dv": dv, "dtype": "bf16", "reps": reps, "seed": 31}
+    return out
+
+
 def _cpu_threads():
     """Threads for the CPU baselines: every core the host reports, capped at
     the 16 CPUs the GPU box allots to one GPU."""
@@ -940,10 +1005,11 @@ def main():
                  "deltanet_h12_d64": bench_delta(False, ds, 2, st / 2, H=12, K=64),
                  "gated_deltanet_h12_d64": bench_delta(True, ds, 2, st / 2, H=12, K=64)}
 
-    state = gen_decode = None
+    state = gen_decode = gen_prefill = None
     if not args.no_state:
         state = bench_state(3, args.decode_steps, args.settle_seconds / 3)
         gen_decode = bench_gen_decode(max(16, args.decode_steps // 4))
+        gen_prefill = bench_gen_prefill(5)
 
     q1, config1 = bench_config1(max(10, args.steps))
     delta_kata = None if args.no_delta else bench_delta_kata(max(3, args.steps // 2),
@@ -1001,6 +1067,7 @@ def main():
         "delta_rule": delta,
         "kata_state_config5": state,
         "kata_state_decode_generic": gen_decode,
+        "kata_state_prefill_generic": gen_prefill,
         "kata_config1": config1,
         "delta_kata_fwd_bwd": delta_kata,
         "mixer_ops": mixer,

@@ -23,12 +23,17 @@
 // the full layout's row (a, b) bit for bit (the same products in the same
 // order); the readouts weigh an off-diagonal row's q-side feature by 2.
 //
-// Three kernels, fp32 throughout (the state is fp32 (B, H, P, 64)):
+// The kernels (the state is fp32 (B, H, P, 64)):
 //   kata_gen_decode_kernel   one token per (b, h): S, z updated in place, o
 //   kata_gen_readout_kernel  a prefill continued from a state: the flash
 //                            forward's (o, den) over the call's tokens plus
 //                            f_t psi(q_t)^T S and f_t psi(q_t) . z
 //   kata_gen_update_kernel   S <- f_T S + sum_s f_Ts psi(k_s) v_s^T (and z)
+// The readout and the update are fp32 VALU kernels for fp32 inputs; 16-bit
+// inputs take kata_gen_readout_mfma_kernel / kata_gen_update_mfma_kernel,
+// whose products psi . S and psi v^T run on the matrix cores with bf16
+// operands (psi formed in fp32, then rounded; S rounded for the readout) and
+// fp32 sums, z and den in fp32.  The decode step is fp32 throughout.
 // The concat score without decay at (dk, M) = (64, 2), (64, 4) keeps its
 // MFMA state-form kernels (kata_state.hip); these cover the rest.
 #include <type_traits>
