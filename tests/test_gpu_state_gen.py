@@ -176,34 +176,40 @@ def test_packed_state_equals_full(case):
         assert err < 1e-2
 
 
-DIRECT = [  # (dk, M, variant, packed, decay): group widths 128 (M = 1, dk = 128), 64, 32 and 16
-    (128, 1, "concat", False, False),
-    (128, 1, "concat", True, True),
-    (64, 2, "concat", True, False),
-    (64, 2, "sum", False, True),
-    (64, 4, "sum", True, False),
-    (128, 4, "concat", True, False),
+DIRECT = [  # (dk, M, variant, packed, decay, dtype): group widths 128 (M = 1), 64, 32 and 16
+    (128, 1, "concat", False, False, torch.bfloat16),
+    (128, 1, "concat", True, True, torch.bfloat16),
+    (64, 2, "concat", True, False, torch.bfloat16),
+    (64, 2, "sum", False, True, torch.bfloat16),
+    (64, 4, "sum", True, False, torch.bfloat16),
+    (128, 4, "concat", True, False, torch.bfloat16),
+    (64, 2, "concat", True, True, torch.float16),
+    (64, 2, "concat", True, True, torch.float32),
+    (64, 4, "sum", False, False, torch.float32),
 ]
+DIRECT_BAR = {torch.bfloat16: 2e-2, torch.float16: 1e-2, torch.float32: 1e-4}
 
 
-@pytest.mark.parametrize("dk,M,variant,packed,decay", DIRECT)
-def test_update_readout_direct(dk, M, variant, packed, decay):
+@pytest.mark.parametrize("dk,M,variant,packed,decay,dtype", DIRECT)
+def test_update_readout_direct(dk, M, variant, packed, decay, dtype):
     """``linatt_kata_gen_update`` from zero then ``linatt_kata_gen_readout``
     through the C ABI against the state formulas in float64 with the full
     feature map psi(x) = vec(scale x_g x_g^T) (summed over g for the sum
-    score), including group widths the cached attention cannot reach."""
+    score), including group widths the cached attention cannot reach.  16-bit
+    inputs run the matrix-core kernels (bf16 products), float32 inputs the
+    float32 ones (held to 1e-4)."""
     from linatt_amd import _lib, spd_state
     from linatt_amd.kata_cache import state_rows
     B, H, T, dv = 2, 3, 150, 64
     E = dk // M
     G = 1 if variant == "sum" else M
-    print(f"\ndirect gen update/readout dk{dk} M{M} {variant} packed={packed} decay={decay}",
-          flush=True)
+    print(f"\ndirect gen update/readout dk{dk} M{M} {variant} packed={packed} decay={decay} "
+          f"{dtype}", flush=True)
     g0 = 900 + dk + M + 7 * packed
-    q, k = gen((B, T, H, dk), g0, 0.5).bfloat16(), gen((B, T, H, dk), g0 + 1, 0.5).bfloat16()
-    v = gen((B, T, H, dv), g0 + 2).bfloat16()
+    q, k = gen((B, T, H, dk), g0, 0.5).to(dtype), gen((B, T, H, dk), g0 + 1, 0.5).to(dtype)
+    v = gen((B, T, H, dv), g0 + 2).to(dtype)
     c = -(gen((B, T, H), g0 + 3).abs() * 0.05).cumsum(1) if decay else None
-    o_in = gen((B, T, H, dv), g0 + 4).bfloat16()
+    o_in = gen((B, T, H, dv), g0 + 4).to(dtype)
     den_in = gen((B, T, H), g0 + 5).abs() + 0.5
     scale = 1.0 / math.sqrt(E)
 
@@ -251,4 +257,4 @@ def test_update_readout_direct(dk, M, variant, packed, decay):
         S_c, z_c = spd_state.unpack_state(S_c, z_c, G)
     errs = (mar(S_c, S_ref), mar(z_c, z_ref), mar(o, o_ref), mar(dn, den.clamp_min(1e-6)))
     print("  S %.1e z %.1e o %.1e den %.1e" % errs, flush=True)
-    assert max(errs) < BAR
+    assert max(errs) < DIRECT_BAR[dtype]
