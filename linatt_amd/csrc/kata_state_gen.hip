@@ -354,14 +354,22 @@ __global__ __launch_bounds__(256) void kata_gen_update_kernel(KataGenStateArgs a
 // v_mfma_f32_32x32x16_bf16; the 32-column halves of Vt are the B operands,
 // shared by the row blocks.  z sums the fp32 features per lane (the two lane
 // halves are added at the end; with NCB = 1 the first half's workgroup
-// stores it).  Staging moves token pairs:
-// one 8-byte LDS write per (dimension, pair) of K, one 4-byte write per
-// (column, pair) of V.
+// stores it).  Staging moves token pairs: one 8-byte LDS write per
+// (dimension, pair) of K, one 4-byte write per (column, pair) of V, the 32
+// pairs of a chunk on consecutive lanes so that each write instruction covers
+// consecutive banks (a mapping with the dimensions on consecutive lanes put
+// eight lanes on two bank offsets; SQ counters showed 5 to 8 conflict cycles
+// per LDS instruction).  Vt's 16-byte chunks are XOR-swizzled by bit 4 of the
+// column, so the B-operand reads of columns 16 apart (same banks at the
+// 144-byte pitch) fall on different banks.
 //   S <- (init ? f_T S : 0) + sum_s f_Ts psi(k_s) v_s^T,  z likewise.
 constexpr int kUpTok = 64, kUpKp = kUpTok + 4, kUpVp = kUpTok + 8;
 
-template <typename T, bool SUM, int RB, int NCB>
+template <typename T, int MS, int RB, int NCB>
 __global__ __launch_bounds__(256) void kata_gen_update_mfma_kernel(KataGenStateArgs a) {
+  // MS: the sum score's groups (0: the concat score, -1: the sum score over
+  // a.M groups, counted at run time)
+  constexpr bool SUM = MS != 0;
   static_assert(sizeof(T) == 2, "16-bit inputs");
   __shared__ __attribute__((aligned(16))) float Kt[128][kUpKp];
   __shared__ __attribute__((aligned(16))) __bf16 Vt[32 * NCB][kUpVp];
@@ -387,13 +395,21 @@ __global__ __launch_bounds__(256) void kata_gen_update_mfma_kernel(KataGenStateA
 
   // prefetch registers: K items (token pair, 8 dimensions), up to two per
   // thread (32 pairs x dk / 8 / 256 threads at dk = 128); one V item (token
-  // pair, 8 columns; the first 128 threads when NCB = 1)
-  v8_t<T> kr[2][2], vr[2];
-  float kc[2][2];
-  auto load = [&](int s0) __attribute__((always_inline)) {
+  // pair, 8 columns; the first 128 threads when NCB = 1), NPF chunks ahead
+  // (two measured no faster than one at 44 more registers)
+  struct Pf {
+    v8_t<T> kr[2][2], vr[2];
+    float kc[2][2];
+  };
+  constexpr int NPF = 1;
+  Pf pf[NPF];
+  auto load = [&](Pf& f, int s0) __attribute__((always_inline)) {
+    auto& kr = f.kr;
+    auto& vr = f.vr;
+    auto& kc = f.kc;
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
-      const int i = tid + 256 * it, sp = i / dk8, d0 = 8 * (i % dk8);
+      const int i = tid + 256 * it, sp = i & 31, d0 = 8 * (i >> 5);
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int t = s0 + 2 * sp + u;
@@ -406,36 +422,40 @@ __global__ __launch_bounds__(256) void kata_gen_update_mfma_kernel(KataGenStateA
         }
       }
     }
-    const int sp = tid / (4 * NCB), n0 = 8 * (tid % (4 * NCB));
+    const int sp = tid & 31, n0 = 8 * (tid >> 5);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int t = s0 + 2 * sp + u;
-      vr[u] = sp < kUpTok / 2 && t < a.T ? ld8<T>(vg + (((int64_t)b * a.T + t) * a.H + h) * kGenDV + n0c + n0)
+      vr[u] = n0 < 32 * NCB && t < a.T ? ld8<T>(vg + (((int64_t)b * a.T + t) * a.H + h) * kGenDV + n0c + n0)
                                           : zero8<T>();
     }
   };
-  auto stage = [&](int s0) __attribute__((always_inline)) {
+  auto stage = [&](const Pf& f, int s0) __attribute__((always_inline)) {
+    const auto& kr = f.kr;
+    const auto& vr = f.vr;
+    const auto& kc = f.kc;
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
       const int i = tid + 256 * it;
       if (i < (kUpTok / 2) * dk8) {
-        const int sp = i / dk8, d0 = 8 * (i % dk8);
-        float f[2];
+        const int sp = i & 31, d0 = 8 * (i >> 5);
+        float fs[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u)
-          f[u] = s0 + 2 * sp + u < a.T ? sqrtf(a.scale * (a.c ? __expf(cT - kc[it][u]) : 1.f)) : 0.f;
+          fs[u] = s0 + 2 * sp + u < a.T ? sqrtf(a.scale * (a.c ? __expf(cT - kc[it][u]) : 1.f)) : 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j)
           *reinterpret_cast<float2*>(&Kt[d0 + j][2 * sp]) =
-              make_float2((float)kr[it][0][j] * f[0], (float)kr[it][1][j] * f[1]);
+              make_float2((float)kr[it][0][j] * fs[0], (float)kr[it][1][j] * fs[1]);
       }
     }
-    const int sp = tid / (4 * NCB), n0 = 8 * (tid % (4 * NCB));
-    if (sp < kUpTok / 2) {
+    const int sp = tid & 31, n0 = 8 * (tid >> 5);
+    if (n0 < 32 * NCB) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-        *reinterpret_cast<bf16x2*>(&Vt[n0 + j][2 * sp]) =
+        const int n = n0 + j;
+        *reinterpret_cast<bf16x2*>(&Vt[n][(2 * sp) ^ (8 * ((n >> 4) & 1))]) =
             bf16x2{(__bf16)(float)vr[0][j], (__bf16)(float)vr[1][j]};
       }
     }
@@ -443,8 +463,7 @@ __global__ __launch_bounds__(256) void kata_gen_update_mfma_kernel(KataGenStateA
   auto features = [&](int k, int sb) __attribute__((always_inline)) {
     f32x8 fe{};
 #pragma unroll
-    for (int g = 0; g < (SUM ? 8 : 1); ++g) {
-      if (SUM && g >= a.M) break;
+    for (int g = 0; g < (MS > 0 ? MS : MS < 0 ? a.M : 1); ++g) {
       const float* ra = &Kt[ia[k] + g * a.E][sb];
       const float* rb = &Kt[ib[k] + g * a.E][sb];
       const f32x4 a0 = *reinterpret_cast<const f32x4*>(ra), a1 = *reinterpret_cast<const f32x4*>(ra + 4);
@@ -457,19 +476,15 @@ __global__ __launch_bounds__(256) void kata_gen_update_mfma_kernel(KataGenStateA
 
   f32x16 acc[RB][NCB] = {};
   float zacc[RB] = {};
-  load(0);
-  for (int s0 = 0; s0 < a.T; s0 += kUpTok) {
-    __syncthreads();  // the previous tokens are consumed
-    stage(s0);
-    __syncthreads();
-    if (s0 + kUpTok < a.T) load(s0 + kUpTok);
+  auto compute = [&]() __attribute__((always_inline)) {
     if (wlive) {
 #pragma unroll
       for (int kk = 0; kk < kUpTok / 16; ++kk) {
         const int sb = 16 * kk + 8 * hh;
         bf16x8 Bv[NCB];
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) Bv[cb] = *reinterpret_cast<const bf16x8*>(&Vt[32 * cb + cl][sb]);
+        for (int cb = 0; cb < NCB; ++cb)
+          Bv[cb] = *reinterpret_cast<const bf16x8*>(&Vt[32 * cb + cl][sb ^ (8 * ((cl >> 4) & 1))]);
 #pragma unroll
         for (int k = 0; k < RB; ++k) {
           const f32x8 fe = features(k, sb);
@@ -478,6 +493,21 @@ __global__ __launch_bounds__(256) void kata_gen_update_mfma_kernel(KataGenStateA
 #pragma unroll
           for (int cb = 0; cb < NCB; ++cb) acc[k][cb] = mma(A, Bv[cb], acc[k][cb]);
         }
+      }
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < NPF; ++u) load(pf[u], u * kUpTok);
+  for (int s0 = 0; s0 < a.T; s0 += NPF * kUpTok) {
+#pragma unroll
+    for (int u = 0; u < NPF; ++u) {
+      const int sc = s0 + u * kUpTok;
+      if (sc < a.T) {  // uniform over the workgroup
+        __syncthreads();  // the previous tokens are consumed
+        stage(pf[u], sc);
+        __syncthreads();
+        if (sc + NPF * kUpTok < a.T) load(pf[u], sc + NPF * kUpTok);
+        compute();
       }
     }
   }
@@ -554,8 +584,11 @@ __device__ __forceinline__ int2 readout_chunk(const KataGenStateArgs& k, int cc)
   return make_int2(a, 16 * j);
 }
 
-template <typename T, bool SUM, int DKMAX>
+template <typename T, int MS, int DKMAX>
 __global__ __launch_bounds__(256) void kata_gen_readout_mfma_kernel(KataGenStateArgs a) {
+  // MS: the sum score's groups (0: the concat score, -1: the sum score over
+  // a.M groups, counted at run time)
+  constexpr bool SUM = MS != 0;
   static_assert(sizeof(T) == 2, "16-bit inputs");
   constexpr bool kQ16 = DKMAX > 64;
   using QT = typename std::conditional<kQ16, T, float>::type;
@@ -591,12 +624,17 @@ __global__ __launch_bounds__(256) void kata_gen_readout_mfma_kernel(KataGenState
   const int nch = (a.sum ? 1 : a.M) * cpg;
   for (int c = tid; c < cpg; c += 256) Ctab[c] = readout_chunk(a, c);
   __syncthreads();
-  // thread: row 16 it + tid / 16 (chunk it, b offset tid / 16) of the four
-  // chunks, columns 4 (tid % 16) .. + 3; z of row tid by the first 64 threads
-  float4 sr[4];
-  float wr[4];
+  // thread (rp, cg) = (tid % 32, tid / 32): rows 2 rp, 2 rp + 1 of the four
+  // chunks' 64 (chunk r / 16, b offset r % 16), column groups cg and cg + 8
+  // (4 columns each), so that the staging writes one 4-byte row pair per
+  // column with the row pairs of 32 lanes on consecutive banks; Bt's
+  // 16-byte chunks are XOR-swizzled by bit 4 of the column, so the B-operand
+  // reads of columns 16 apart fall on different banks.  z of row tid by the
+  // first 64 threads.
+  const int rp = tid & 31, cg = tid >> 5;
+  float4 sr[2][2];
+  float wr[2];
   float zr = 0.f;
-  int2 cr[4];
   auto row_of = [&](int g, int2 t, int bo, float& wgt) __attribute__((always_inline)) {
     // t = (a, 16 j) of group g: the storage row of (a, b = 16 j + bo), or -1
     const int ra = t.x, rb = t.y + bo;
@@ -611,18 +649,21 @@ __global__ __launch_bounds__(256) void kata_gen_readout_mfma_kernel(KataGenState
     wgt = rb == ra ? 1.f : 2.f;
     return g * a.TE + ra * a.E - ra * (ra - 1) / 2 + (rb - ra);
   };
-  // c0: a multiple of four, so the four chunks share the group
+  // c0: a multiple of four, so the four chunks share the group g
+  int g = 0, cc0 = 0;
   auto load = [&](int c0) __attribute__((always_inline)) {
-    const int g = c0 / cpg, cc0 = c0 - g * cpg;
+    g = c0 / cpg;
+    cc0 = c0 - g * cpg;
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int2 t = Ctab[cc0 + it];
-      cr[it] = make_int2(g * a.E + t.x, g * a.E + t.y);
+    for (int u = 0; u < 2; ++u) {
+      const int r = 2 * rp + u;
       float wg = 0.f;
-      const int p = row_of(g, t, tid >> 4, wg);
-      wr[it] = p >= 0 ? wg : 0.f;
-      sr[it] = p >= 0 ? *reinterpret_cast<const float4*>(S + (size_t)p * kGenDV + 4 * (tid & 15))
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
+      const int p = row_of(g, Ctab[cc0 + (r >> 4)], r & 15, wg);
+      wr[u] = p >= 0 ? wg : 0.f;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+        sr[u][hf] = p >= 0 ? *reinterpret_cast<const float4*>(S + (size_t)p * kGenDV + 4 * (cg + 8 * hf))
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     if (tid < kRoRows) {
       float wg = 0.f;
@@ -631,18 +672,22 @@ __global__ __launch_bounds__(256) void kata_gen_readout_mfma_kernel(KataGenState
     }
   };
   auto stage = [&]() __attribute__((always_inline)) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int r = 16 * it + (tid >> 4), n0 = 4 * (tid & 15);
-      Bt[n0 + 0][r] = (__bf16)(wr[it] * sr[it].x);
-      Bt[n0 + 1][r] = (__bf16)(wr[it] * sr[it].y);
-      Bt[n0 + 2][r] = (__bf16)(wr[it] * sr[it].z);
-      Bt[n0 + 3][r] = (__bf16)(wr[it] * sr[it].w);
+    for (int hf = 0; hf < 2; ++hf) {
+      const float x0[4] = {sr[0][hf].x, sr[0][hf].y, sr[0][hf].z, sr[0][hf].w};
+      const float x1[4] = {sr[1][hf].x, sr[1][hf].y, sr[1][hf].z, sr[1][hf].w};
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) {
+        const int n = 4 * (cg + 8 * hf) + cc;
+        *reinterpret_cast<bf16x2*>(&Bt[n][(2 * rp) ^ (8 * ((n >> 4) & 1))]) =
+            bf16x2{(__bf16)(wr[0] * x0[cc]), (__bf16)(wr[1] * x1[cc])};
+      }
     }
     if (tid < kRoRows) Zs[tid] = zr;
-    if (tid == 0) {
-#pragma unroll
-      for (int it = 0; it < 4; ++it) Ci[it] = cr[it];
+    if (tid < 4) {
+      const int2 t = Ctab[cc0 + tid];
+      Ci[tid] = make_int2(g * a.E + t.x, g * a.E + t.y);
     }
   };
 
@@ -661,8 +706,7 @@ __global__ __launch_bounds__(256) void kata_gen_readout_mfma_kernel(KataGenState
       const int rb = 16 * kk + 8 * hh;
       f32x8 fe{};
 #pragma unroll
-      for (int g = 0; g < (SUM ? 8 : 1); ++g) {
-        if (SUM && g >= a.M) break;
+      for (int g = 0; g < (MS > 0 ? MS : MS < 0 ? a.M : 1); ++g) {
         const float qa = (float)qrow[ci.x + g * a.E];
         const QT* qb = qrow + ci.y + g * a.E + 8 * hh;
         f32x8 bq;
@@ -681,8 +725,9 @@ __global__ __launch_bounds__(256) void kata_gen_readout_mfma_kernel(KataGenState
       dacc += ((fe[0] * z0[0] + fe[1] * z0[1]) + (fe[2] * z0[2] + fe[3] * z0[3])) +
               ((fe[4] * z1[0] + fe[5] * z1[1]) + (fe[6] * z1[2] + fe[7] * z1[3]));
       const bf16x8 A = __builtin_convertvector(fe, bf16x8);
-      acc0 = mma(A, *reinterpret_cast<const bf16x8*>(&Bt[cl][rb]), acc0);
-      acc1 = mma(A, *reinterpret_cast<const bf16x8*>(&Bt[32 + cl][rb]), acc1);
+      const int rbs = rb ^ (8 * ((cl >> 4) & 1));
+      acc0 = mma(A, *reinterpret_cast<const bf16x8*>(&Bt[cl][rbs]), acc0);
+      acc1 = mma(A, *reinterpret_cast<const bf16x8*>(&Bt[32 + cl][rbs]), acc1);
     }
   }
   // den part of query 32 w + l % 32: the two lane halves; then every lane
@@ -719,50 +764,53 @@ __global__ __launch_bounds__(256) void kata_gen_readout_mfma_kernel(KataGenState
   }
 }
 
+// the sum score's group count as a template argument where it is 2, 4 or 8
+// (so the group loop unrolls), -1 for the other counts dk <= 128 allows
+// (3, 5, 6, 7: a loop bounded at run time); the sum score over one group is
+// the concat score
+template <typename F>
+hipError_t by_sum_groups(const KataGenStateArgs& a, F&& f) {
+  if (!a.sum || a.M == 1) return f(std::integral_constant<int, 0>{});
+  if (a.M == 2) return f(std::integral_constant<int, 2>{});
+  if (a.M == 4) return f(std::integral_constant<int, 4>{});
+  if (a.M == 8) return f(std::integral_constant<int, 8>{});
+  return f(std::integral_constant<int, -1>{});
+}
+
 template <typename T>
 hipError_t launch_kata_gen_state(const KataGenStateArgs& a, int which, hipStream_t stream) {
   const int BH = a.B * a.H;
-  if (which == KATA_GEN_DECODE)
+  if (which == KATA_GEN_DECODE) {
     kata_gen_decode_kernel<T><<<dim3(BH), dim3(256), 0, stream>>>(a);
-  else if (which == KATA_GEN_READOUT) {
+  } else if (which == KATA_GEN_READOUT) {
     if constexpr (sizeof(T) == 2) {
       const dim3 grid(BH, (a.T + 127) / 128);
-      if (a.dk <= 64) {
-        if (a.sum)
-          kata_gen_readout_mfma_kernel<T, true, 64><<<grid, dim3(256), 0, stream>>>(a);
+      by_sum_groups(a, [&](auto ms) {
+        if (a.dk <= 64)
+          kata_gen_readout_mfma_kernel<T, decltype(ms)::value, 64><<<grid, dim3(256), 0, stream>>>(a);
         else
-          kata_gen_readout_mfma_kernel<T, false, 64><<<grid, dim3(256), 0, stream>>>(a);
-      } else {
-        if (a.sum)
-          kata_gen_readout_mfma_kernel<T, true, 128><<<grid, dim3(256), 0, stream>>>(a);
-        else
-          kata_gen_readout_mfma_kernel<T, false, 128><<<grid, dim3(256), 0, stream>>>(a);
-      }
-    }
-    else
+          kata_gen_readout_mfma_kernel<T, decltype(ms)::value, 128><<<grid, dim3(256), 0, stream>>>(a);
+        return hipSuccess;
+      });
+    } else {
       kata_gen_readout_kernel<T><<<dim3(BH, (a.T + 63) / 64), dim3(256), 0, stream>>>(a);
-  }
-  else if constexpr (sizeof(T) == 2) {
+    }
+  } else if constexpr (sizeof(T) == 2) {
     // 256 rows and both column halves per workgroup; a state of at most
     // 256 rows that would leave CUs idle takes 128 rows and one half (more
     // workgroups, each streaming every token: the staging, not the products,
     // is this kernel's cost, so larger states keep the 256-row tiles)
-    if (a.P > 256 || (int64_t)BH * ((a.P + 255) / 256) >= 512) {
-      const dim3 grid(BH, (a.P + 255) / 256);
-      if (a.sum)
-        kata_gen_update_mfma_kernel<T, true, 2, 2><<<grid, dim3(256), 0, stream>>>(a);
+    by_sum_groups(a, [&](auto ms) {
+      constexpr int MS = decltype(ms)::value;
+      if (a.P > 256 || (int64_t)BH * ((a.P + 255) / 256) >= 512)
+        kata_gen_update_mfma_kernel<T, MS, 2, 2><<<dim3(BH, (a.P + 255) / 256), dim3(256), 0, stream>>>(a);
       else
-        kata_gen_update_mfma_kernel<T, false, 2, 2><<<grid, dim3(256), 0, stream>>>(a);
-    } else {
-      const dim3 grid(BH, (a.P + 127) / 128, 2);
-      if (a.sum)
-        kata_gen_update_mfma_kernel<T, true, 1, 1><<<grid, dim3(256), 0, stream>>>(a);
-      else
-        kata_gen_update_mfma_kernel<T, false, 1, 1><<<grid, dim3(256), 0, stream>>>(a);
-    }
-  }
-  else
+        kata_gen_update_mfma_kernel<T, MS, 1, 1><<<dim3(BH, (a.P + 127) / 128, 2), dim3(256), 0, stream>>>(a);
+      return hipSuccess;
+    });
+  } else {
     kata_gen_update_kernel<T><<<dim3(BH, (a.P + 63) / 64), dim3(256), 0, stream>>>(a);
+  }
   return hipGetLastError();
 }
 

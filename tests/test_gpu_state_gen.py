@@ -186,6 +186,8 @@ DIRECT = [  # (dk, M, variant, packed, decay, dtype): group widths 128 (M = 1), 
     (64, 2, "concat", True, True, torch.float16),
     (64, 2, "concat", True, True, torch.float32),
     (64, 4, "sum", False, False, torch.float32),
+    (48, 3, "sum", True, False, torch.bfloat16),  # three groups: a group count known at run time
+    (128, 8, "sum", False, False, torch.bfloat16),
 ]
 DIRECT_BAR = {torch.bfloat16: 2e-2, torch.float16: 1e-2, torch.float32: 1e-4}
 
