@@ -471,7 +471,9 @@ __global__ __launch_bounds__(256) void kata_gen_update_mfma_kernel(KataGenStateA
       fe += f32x8{a0[0] * b0[0], a0[1] * b0[1], a0[2] * b0[2], a0[3] * b0[3],
                   a1[0] * b1[0], a1[1] * b1[1], a1[2] * b1[2], a1[3] * b1[3]};
     }
-    return live[k] ? fe : f32x8{};
+    // a row past P (its (a, b) those of row 0) is neither stored nor added
+    // to z, so its features need no mask
+    return fe;
   };
 
   f32x16 acc[RB][NCB] = {};
