@@ -264,7 +264,9 @@ int linatt_kata_gen_decode(const void* q, const void* k, const void* v, const fl
  * float32 hold the flash forward (linatt_kata_fwd) over the call's tokens on
  * entry; on return o = (o den + e^{c_t} psi(q_t)^T S) / max(den', eps) with
  * den' = den + e^{c_t} psi(q_t) . z, and den = max(den', eps).  q (B,T,H,dk);
- * c (B,T,H) or NULL; S, z are read only. */
+ * c (B,T,H) or NULL; S, z are read only; q, S and o 16-byte aligned.
+ * 16-bit inputs: psi(q_t)^T S runs on the matrix cores with psi(q_t) and S
+ * rounded to bfloat16 and float32 sums; den stays float32. */
 int linatt_kata_gen_readout(const void* q, const float* c, const float* S, const float* z,
                             void* o, float* den, int B, int T, int H, int dk, int dv,
                             int num_groups, int variant, float scale, float eps, int dtype,

@@ -1142,7 +1142,8 @@ int linatt_kata_gen_readout(const void* q, const float* c, const float* S, const
   int st = gen_state_args(fn, a, B, T, H, dk, dv, num_groups, variant, scale, eps, dtype);
   if (st) return st;
   if (!q || !S || !z || !o || !den) return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
-  if (!aligned16(S) || !aligned16(o)) return fail(LINATT_EINVAL, std::string(fn) + ": S and o must be 16-byte aligned");
+  if (!aligned16(q) || !aligned16(S) || !aligned16(o))
+    return fail(LINATT_EINVAL, std::string(fn) + ": q, S and o must be 16-byte aligned");
   a.q = q; a.c = c; a.S = const_cast<float*>(S); a.z = const_cast<float*>(z); a.o = o; a.den = den;
   return gen_state_launch(fn, a, KATA_GEN_READOUT, dtype, stream);
 }

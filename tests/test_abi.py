@@ -112,6 +112,19 @@ def test_gen_state_rejects_unknown_variant_bits(lib):
         assert b"unknown KATA variant" in lib.linatt_last_error()
 
 
+def test_gen_state_alignment_checked_before_launch(lib):
+    odd = ctypes.c_void_p((1 << 20) + 2)  # 2-byte aligned only, never dereferenced
+    null = None
+    assert lib.linatt_kata_gen_readout(odd, null, FAKE, FAKE, FAKE, FAKE, 1, 8, 2, 64, 64, 2, 0,
+                                       0.25, 1e-6, 1, null) == -1
+    assert b"16-byte aligned" in lib.linatt_last_error()
+    assert lib.linatt_kata_gen_update(odd, FAKE, null, FAKE, FAKE, 0, 1, 8, 2, 64, 64, 2, 0, 0.25, 1,
+                                      null) == -1
+    assert b"16-byte aligned" in lib.linatt_last_error()
+    assert lib.linatt_kata_gen_update(FAKE, odd, null, FAKE, FAKE, 0, 1, 8, 2, 64, 64, 2, 0, 0.25, 1,
+                                      null) == -1
+
+
 FAKE = ctypes.c_void_p(1 << 20)  # aligned, never dereferenced on the host
 
 
