@@ -97,18 +97,29 @@ __device__ __forceinline__ float ldf(const void* p, int64_t i) {
 
 // One workgroup per (b, h); 16 threads per state row (4 value columns each),
 // 16 rows per pass; q, k (B, H, dk), v, o (B, H, 64); c (B, H) the step's
-// log-decay or null.
+// log-decay or null.  The packed layout's rows are mapped to their dimensions
+// once per workgroup into an LDS table (dims < 256: 8 bits each), not by
+// each of a row's 16 threads.
+constexpr int kMaxPackedRows = 128 * 129 / 2;  // dk <= 128, one group of 128
+
 template <typename T>
 __global__ __launch_bounds__(256) void kata_gen_decode_kernel(KataGenStateArgs a) {
   __shared__ float qs[128], ks[128], vs[kGenDV];
   __shared__ float4 red[16][16];
   __shared__ float dred[16];
+  __shared__ unsigned short pairs[kMaxPackedRows];
   const int tid = threadIdx.x, bh = blockIdx.x;
   if (tid < a.dk) {
     qs[tid] = ldf<T>(a.q, (int64_t)bh * a.dk + tid);
     ks[tid] = ldf<T>(a.k, (int64_t)bh * a.dk + tid);
   }
   if (tid < kGenDV) vs[tid] = ldf<T>(a.v, (int64_t)bh * kGenDV + tid);
+  if (a.tri) {
+    for (int p = tid; p < a.P; p += 256) {
+      const RowPair rp = row_pair(a, p);
+      pairs[p] = (unsigned short)(((rp.g * a.E + rp.a) << 8) | (rp.g * a.E + rp.b));
+    }
+  }
   __syncthreads();
   const float f = a.c ? __expf(a.c[bh]) : 1.f;
   const int c4 = tid & 15, r = tid >> 4;
@@ -137,7 +148,16 @@ __global__ __launch_bounds__(256) void kata_gen_decode_kernel(KataGenStateArgs a
     for (int u = 0; u < kDecU; ++u) {
       const int p = p0 + 16 * u;
       if (p >= a.P) break;
-      const RowPair rp = row_pair(a, p);
+      RowPair rp;
+      if (a.tri) {
+        const unsigned pr = pairs[p];
+        rp.g = 0;  // the group is folded into the dimensions
+        rp.a = (int)(pr >> 8);
+        rp.b = (int)(pr & 255u);
+        rp.w = rp.a == rp.b ? 1.f : 2.f;
+      } else {
+        rp = row_pair(a, p);
+      }
       const float pk = psi_feat(ks, rp, a.E, a.M, a.sum, a.scale);
       const float pq = rp.w * psi_feat(qs, rp, a.E, a.M, a.sum, a.scale);
       float4 x = xs[u];
