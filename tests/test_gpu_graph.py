@@ -2,7 +2,11 @@
 
 Captured: a KATA training step (concat score, forward + backward through
 ``parallel_kata_attn``), the gated delta rule forward + backward with an
-initial state, and a loop of four decode steps on the psi-state.  Each
+initial state, a loop of four decode steps on the psi-state, and the decode
+cache of the flash scores outside the MFMA state form (a prefill from an
+empty cache, four decode steps and a continued prefill, through
+``kata_cache.parallel_kata_attn_cached`` and the ``linatt_kata_gen_*``
+kernels).  Each
 graph is replayed three times, with unrelated eager work and a host
 synchronisation before every replay, and each replay must reproduce the
 eager result bit for bit: the kernels are deterministic, so any difference
@@ -135,3 +139,34 @@ def test_decode_loop_graph():
 
     _replay_and_check(g, list(outs) + [S, z], ref,
                       tuple(f"o{i}" for i in range(n)) + ("S", "z"), reset)
+
+
+@pytest.mark.parametrize("variant,M,decay", [("sum", 4, False), ("concat", 1, True)])
+def test_generic_cache_graph(variant, M, decay):
+    from linatt_amd.kata_cache import parallel_kata_attn_cached
+    B, H, dk = 2, 3, 64
+    splits = [0, 70, 71, 72, 73, 74, 104]
+    T = splits[-1]
+    print(f"\ngeneric cache in a graph: {variant} M{M} decay={decay} B{B} H{H} T{T}", flush=True)
+    q = gen((B, T, H, dk), 60, 0.5).to(BF).cuda()
+    k = gen((B, T, H, dk), 61, 0.5).to(BF).cuda()
+    v = gen((B, T, H, 64), 62).to(BF).cuda()
+    c = -(gen((B, T, H), 63).abs() * 0.05).cumsum(1).cuda() if decay else None
+
+    def cc(s, e):
+        if c is None:
+            return None
+        return (c[:, s:e] - (c[:, s - 1:s] if s > 0 else 0.0)).contiguous()
+
+    def run():
+        st, outs = None, []
+        for s, e in zip(splits[:-1], splits[1:]):
+            o, st = parallel_kata_attn_cached(q[:, s:e], k[:, s:e], v[:, s:e], st, M, None,
+                                              variant=variant, c=cc(s, e))
+            outs.append(o)
+        return outs + [st.S, st.z]
+
+    ref = [t.clone() for t in run()]
+    torch.cuda.synchronize()
+    g, out = _capture(run)
+    _replay_and_check(g, out, ref, tuple(f"o{i}" for i in range(len(splits) - 1)) + ("S", "z"))
