@@ -866,8 +866,10 @@ __global__ __launch_bounds__(256) void dkata_bwd_fix_kernel(DKataBwdArgs a) {
   static_assert(D == 64 && DV == 64 && E % 16 == 0, "64-wide heads");
   __shared__ __attribute__((aligned(16))) T Ks[TE];   // K rows of the chunk
   __shared__ __attribute__((aligned(16))) T UTs[TE];  // U^T [j][s] of the chunk
-  __shared__ __attribute__((aligned(16))) float Xc[4][16][64];
-  __shared__ float Db[2][64];                          // dbeta partials per j block
+  // sum over s of A^T[s][t] U^T[j][s], [t][j]; the odd pitch keeps both the
+  // C-layout writes (32 tokens per instruction) and the row reads below free
+  // of bank conflicts
+  __shared__ float Ecs[64][65];
 
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int cl = lane & 31, hh = lane >> 5;
@@ -888,28 +890,31 @@ __global__ __launch_bounds__(256) void dkata_bwd_fix_kernel(DKataBwdArgs a) {
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk)
     kc[kk] = tl < Tn ? ld8<T>(kb + (int64_t)tl * rs + 16 * kk + 8 * hh) : zero8<T>();
-  // this lane's rows of everything else, loaded while the tiles land
-  const bool in = tl < Tn;
-  const int64_t row = ((int64_t)b * Tn + (in ? tl : t0)) * a.H + h;
+
+  // the elementwise part's rows, loaded while the tiles land: thread
+  // (tk, q) = (tid / 4, tid % 4) owns token t0 + tk, value columns and key
+  // dims 16 q .. 16 q + 15, so four consecutive lanes cover a whole row
+  const int tk = tid >> 2, q = tid & 3, tg = t0 + tk;
+  const bool in = tg < Tn;
+  const int64_t row = ((int64_t)b * Tn + (in ? tg : t0)) * a.H + h;
   float4 g4[4], e4[4];
   v4_t<T> v4[4], x4[4], y4[4], z4[4];
-  const float bt = in ? a.beta[((int64_t)b * Tn + tl) * a.H + h] : 0.f;
+  const float bt = in ? a.beta[((int64_t)b * Tn + tg) * a.H + h] : 0.f;
   {
-    const float* dbv = (const float*)(a.bws + a.BL.dbV) + row * DV;
-    const float* ein = (const float*)(a.ws + a.L.Ein) + row * DV;
-    const T* vr = (const T*)a.v + row * DV;
-    const T* dkr = (const T*)(a.bws + a.BL.dkr) + row * D;
-    const T* dke = (const T*)(a.bws + a.BL.dke) + row * D;
-    const T* dqe = (const T*)(a.bws + a.BL.dqe) + (row - a.H) * D;
+    const float* dbv = (const float*)(a.bws + a.BL.dbV) + row * DV + 16 * q;
+    const float* ein = (const float*)(a.ws + a.L.Ein) + row * DV + 16 * q;
+    const T* vr = (const T*)a.v + row * DV + 16 * q;
+    const T* dkr = (const T*)(a.bws + a.BL.dkr) + row * D + 16 * q;
+    const T* dke = (const T*)(a.bws + a.BL.dke) + row * D + 16 * q;
+    const T* dqe = (const T*)(a.bws + a.BL.dqe) + (row - a.H) * D + 16 * q;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int j0 = 32 * ub + 8 * i + 4 * hh, d0 = 32 * ub + 16 * hh + 4 * i;
-      g4[i] = in ? *reinterpret_cast<const float4*>(dbv + j0) : make_float4(0.f, 0.f, 0.f, 0.f);
-      e4[i] = in ? *reinterpret_cast<const float4*>(ein + j0) : make_float4(0.f, 0.f, 0.f, 0.f);
-      v4[i] = in ? ld4<T>(vr + j0) : v4_t<T>{};
-      x4[i] = in ? ld4<T>(dkr + d0) : v4_t<T>{};
-      y4[i] = in ? ld4<T>(dke + d0) : v4_t<T>{};
-      z4[i] = in && tl > 0 ? ld4<T>(dqe + d0) : v4_t<T>{};
+      g4[i] = in ? *reinterpret_cast<const float4*>(dbv + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+      e4[i] = in ? *reinterpret_cast<const float4*>(ein + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+      v4[i] = in ? ld4<T>(vr + 4 * i) : v4_t<T>{};
+      x4[i] = in ? ld4<T>(dkr + 4 * i) : v4_t<T>{};
+      y4[i] = in ? ld4<T>(dke + 4 * i) : v4_t<T>{};
+      z4[i] = in && tg > 0 ? ld4<T>(dqe + 4 * i) : v4_t<T>{};
     }
   }
   vm_wait_barrier<0>();
@@ -939,42 +944,46 @@ __global__ __launch_bounds__(256) void dkata_bwd_fix_kernel(DKataBwdArgs a) {
     for (int jb = 0; jb < 2; ++jb)
       ec[jb] = mma(tile_ldp8<T>(UTs, 32 * jb + cl, 32 * ub, ks, hh), bop, ec[jb]);
   }
+  // the s-block 0 waves write their part, then the s-block 1 waves add theirs
 #pragma unroll
-  for (int e = 0; e < 16; ++e) Xc[w][e][lane] = ec[1 - ub][e];
-  block_barrier();
-  const int partner = tb | ((1 - ub) << 1);
-  // dbeta partial over this wave's 32 value columns j (block ub); dv
+  for (int pass = 0; pass < 2; ++pass) {
+    if (ub == pass) {
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float& d = Ecs[32 * tb + cl][32 * jb + 8 * (e >> 2) + 4 * hh + (e & 3)];
+          d = pass == 0 ? ec[jb][e] : d + ec[jb][e];
+        }
+    }
+    __syncthreads();
+  }
+  // dbeta over the row's value columns; dv; dk
   float part = 0.f;
-  T* dvr = (T*)a.dv + row * DV;
+  T* dvr = (T*)a.dv + row * DV + 16 * q;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int j0 = 32 * ub + 8 * i + 4 * hh;
     const float gv[4] = {g4[i].x, g4[i].y, g4[i].z, g4[i].w};
     const float ev[4] = {e4[i].x, e4[i].y, e4[i].z, e4[i].w};
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int e = 4 * i + r;
-      const float Et = ev[r] + a.scale2 * (ec[ub][e] + Xc[partner][e][lane]);
+      const float Et = ev[r] + a.scale2 * Ecs[tk][16 * q + 4 * i + r];
       part += ((float)v4[i][r] - Et) * gv[r];
     }
-    if (in) st4<T>(dvr + j0, to4<T>(bt * gv[0], bt * gv[1], bt * gv[2], bt * gv[3]));
+    if (in) st4<T>(dvr + 4 * i, to4<T>(bt * gv[0], bt * gv[1], bt * gv[2], bt * gv[3]));
   }
-  part += __shfl_xor(part, 32);
-  if (hh == 0) Db[ub][32 * tb + cl] = part;
-  // dk: the wave's 32 tokens (tb) x half of the key dims (ub), 16 per lane
+  part += __shfl_xor(part, 1);
+  part += __shfl_xor(part, 2);
   if (in) {
-    T* dko = (T*)a.dk + row * D;
+    T* dko = (T*)a.dk + row * D + 16 * q;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d0 = 32 * ub + 16 * hh + 4 * i;
-      st4<T>(dko + d0, to4<T>((float)x4[i][0] + (float)y4[i][0] + (float)z4[i][0],
-                              (float)x4[i][1] + (float)y4[i][1] + (float)z4[i][1],
-                              (float)x4[i][2] + (float)y4[i][2] + (float)z4[i][2],
-                              (float)x4[i][3] + (float)y4[i][3] + (float)z4[i][3]));
-    }
+    for (int i = 0; i < 4; ++i)
+      st4<T>(dko + 4 * i, to4<T>((float)x4[i][0] + (float)y4[i][0] + (float)z4[i][0],
+                                 (float)x4[i][1] + (float)y4[i][1] + (float)z4[i][1],
+                                 (float)x4[i][2] + (float)y4[i][2] + (float)z4[i][2],
+                                 (float)x4[i][3] + (float)y4[i][3] + (float)z4[i][3]));
+    if (q == 0) a.dbeta[((int64_t)b * Tn + tg) * a.H + h] = part;
   }
-  block_barrier();
-  if (ub == 0 && hh == 0 && in) a.dbeta[((int64_t)b * Tn + tl) * a.H + h] = Db[0][32 * tb + cl] + Db[1][32 * tb + cl];
 }
 
 template <typename T, int D, int DV, int M>
