@@ -21,8 +21,9 @@ halves a decode step's bytes and the cache's memory.
 The concat score without decay at the MFMA state-form shapes
 (``linatt_kata_state_supported``) takes a chunk of T > 1 tokens through the
 state-form prefill continued from the current state
-(``linatt_kata_prefill_state``) and a single token through
-``linatt_kata_decode_step``.  Every other flash score (M = 1, the sum
+(``linatt_kata_prefill_state``; a short prompt into an empty cache, where the
+flash forward is faster, goes the generic way below) and a single token
+through ``linatt_kata_decode_step``.  Every other flash score (M = 1, the sum
 score, the decayed score, the offset gate's padded width dk = 128) takes a
 chunk through the flash forward plus the stored state's readout and a state
 update, and a single token through ``linatt_kata_gen_decode``.
@@ -97,8 +98,9 @@ def parallel_kata_attn_cached(q, k, v, state=None, num_groups=4, scale=None, eps
 
     The concat score without decay at the shapes of
     ``linatt_kata_state_supported`` runs the MFMA state-form prefill
-    (``spd_state.kata_prefill``); every other flash score runs the flash
-    forward over the call's tokens plus the generic state kernels
+    (``spd_state.kata_prefill``), except for a call of at most 1024 tokens
+    (2048 with two groups) into an empty cache; every other call runs the
+    flash forward over the call's tokens plus the generic state kernels
     (``linatt_kata_gen_*``: dk <= 128, dv = 64)."""
     if q.dim() != 4 or k.shape != q.shape or v.shape[:3] != q.shape[:3]:
         raise ValueError(f"q, k must be (B, T, H, dk) and v (B, T, H, dv); got {tuple(q.shape)}, "
@@ -121,6 +123,13 @@ def parallel_kata_attn_cached(q, k, v, state=None, num_groups=4, scale=None, eps
     dt = v.dtype
     fast = (variant == "concat" and c is None
             and L.linatt_kata_state_supported(_lib.dtype_code(dt), dk, dv, M))
+    # a prompt of a few thousand tokens into an empty cache: the flash forward
+    # plus the state update beat the state-form prefill (whose output kernel
+    # repeats the flash work inside each 1024-token segment) at T <= 1024, and
+    # at T <= 2048 for two groups (measured at B = 1 .. 16, H = 12); both
+    # leave the same packed state
+    if fast and state is None and (T <= 1024 or (T <= 2048 and M == 2)):
+        fast = False
     if fast:
         if T == 1 and state is not None:
             o = spd_state.kata_decode_step(state.S, state.z, q[:, 0], k[:, 0], v[:, 0], M,
