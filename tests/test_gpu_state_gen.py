@@ -260,3 +260,28 @@ def test_update_readout_direct(dk, M, variant, packed, decay, dtype):
     errs = (mar(S_c, S_ref), mar(z_c, z_ref), mar(o, o_ref), mar(dn, den.clamp_min(1e-6)))
     print("  S %.1e z %.1e o %.1e den %.1e" % errs, flush=True)
     assert max(errs) < DIRECT_BAR[dtype]
+
+
+@pytest.mark.parametrize("variant,M,dtype", [("sum", 2, torch.bfloat16), ("concat", 1, torch.float16),
+                                             ("concat", 4, torch.float16)])
+def test_single_token_prompt_then_decode(variant, M, dtype):
+    """A one-token prompt into an empty cache (the state update over T = 1),
+    then decode steps and a short continued prefill, against the oracle's
+    parallel form; fp16 inputs run the bf16 matrix-core products."""
+    from linatt_amd.kata_cache import parallel_kata_attn_cached
+    B, H, dk = 2, 3, 64
+    splits = [0, 1, 2, 3, 40, 41]
+    T = splits[-1]
+    print(f"\nsingle-token prompt: {variant} M{M} {dtype}", flush=True)
+    q, k = gen((B, T, H, dk), 80 + M, 0.5).to(dtype), gen((B, T, H, dk), 81 + M, 0.5).to(dtype)
+    v = gen((B, T, H, 64), 82 + M).to(dtype)
+    o_ref, _ = K.kata_fwd(q.double(), k.double(), v.double(), M, None, variant, None)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    st, outs = None, []
+    for s, e in zip(splits[:-1], splits[1:]):
+        o, st = parallel_kata_attn_cached(qd[:, s:e], kd[:, s:e], vd[:, s:e], st, M, variant=variant)
+        assert o.dtype == dtype and o.shape == (B, e - s, H, 64)
+        outs.append(o)
+    err = mar(torch.cat(outs, 1), o_ref)
+    print(f"  max rel err {err:.1e}", flush=True)
+    assert err < (1e-2 if dtype == torch.float16 else BAR)
