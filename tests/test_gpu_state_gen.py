@@ -189,11 +189,15 @@ DIRECT = [  # (dk, M, variant, packed, decay, dtype): group widths 128 (M = 1), 
     (48, 3, "sum", True, False, torch.bfloat16),  # three groups: a group count known at run time
     (128, 8, "sum", False, False, torch.bfloat16),
 ]
+# long prompts: the bf16 products accumulate over thousands of tokens
+DIRECT_LONG = [(64, 1, "concat", True, True, torch.bfloat16, 2048),
+               (64, 4, "sum", True, False, torch.bfloat16, 1536)]
 DIRECT_BAR = {torch.bfloat16: 2e-2, torch.float16: 1e-2, torch.float32: 1e-4}
 
 
-@pytest.mark.parametrize("dk,M,variant,packed,decay,dtype", DIRECT)
-def test_update_readout_direct(dk, M, variant, packed, decay, dtype):
+@pytest.mark.parametrize("dk,M,variant,packed,decay,dtype,T",
+                         [c + (150,) for c in DIRECT] + DIRECT_LONG)
+def test_update_readout_direct(dk, M, variant, packed, decay, dtype, T):
     """``linatt_kata_gen_update`` from zero then ``linatt_kata_gen_readout``
     through the C ABI against the state formulas in float64 with the full
     feature map psi(x) = vec(scale x_g x_g^T) (summed over g for the sum
@@ -202,11 +206,11 @@ def test_update_readout_direct(dk, M, variant, packed, decay, dtype):
     float32 ones (held to 1e-4)."""
     from linatt_amd import _lib, spd_state
     from linatt_amd.kata_cache import state_rows
-    B, H, T, dv = 2, 3, 150, 64
+    B, H, dv = 2, 3, 64
     E = dk // M
     G = 1 if variant == "sum" else M
     print(f"\ndirect gen update/readout dk{dk} M{M} {variant} packed={packed} decay={decay} "
-          f"{dtype}", flush=True)
+          f"{dtype} T{T}", flush=True)
     g0 = 900 + dk + M + 7 * packed
     q, k = gen((B, T, H, dk), g0, 0.5).to(dtype), gen((B, T, H, dk), g0 + 1, 0.5).to(dtype)
     v = gen((B, T, H, dv), g0 + 2).to(dtype)
