@@ -99,9 +99,10 @@ def parallel_kata_attn_cached(q, k, v, state=None, num_groups=4, scale=None, eps
     The concat score without decay at the shapes of
     ``linatt_kata_state_supported`` runs the MFMA state-form prefill
     (``spd_state.kata_prefill``), except for a call of at most 1024 tokens
-    (2048 with two groups) into an empty cache; every other call runs the
-    flash forward over the call's tokens plus the generic state kernels
-    (``linatt_kata_gen_*``: dk <= 128, dv = 64)."""
+    (2048 with two groups) into an empty cache and a continued chunk of at
+    most 1024 tokens over at least 96 (batch, head) pairs; every other call
+    runs the flash forward over the call's tokens plus the generic state
+    kernels (``linatt_kata_gen_*``: dk <= 128, dv = 64)."""
     if q.dim() != 4 or k.shape != q.shape or v.shape[:3] != q.shape[:3]:
         raise ValueError(f"q, k must be (B, T, H, dk) and v (B, T, H, dv); got {tuple(q.shape)}, "
                          f"{tuple(k.shape)}, {tuple(v.shape)}")
@@ -126,9 +127,13 @@ def parallel_kata_attn_cached(q, k, v, state=None, num_groups=4, scale=None, eps
     # a prompt of a few thousand tokens into an empty cache: the flash forward
     # plus the state update beat the state-form prefill (whose output kernel
     # repeats the flash work inside each 1024-token segment) at T <= 1024, and
-    # at T <= 2048 for two groups (measured at B = 1 .. 16, H = 12); both
-    # leave the same packed state
+    # at T <= 2048 for two groups; so do the flash forward, the state readout
+    # and the update for a continued chunk of at most 1024 tokens over 96 or
+    # more (batch, head) pairs (measured at B = 1 .. 16, H = 12).  Both paths
+    # keep the same packed row order, so a state passes between them
     if fast and state is None and (T <= 1024 or (T <= 2048 and M == 2)):
+        fast = False
+    if fast and state is not None and 1 < T <= 1024 and B * H >= 96:
         fast = False
     if fast:
         if T == 1 and state is not None:

@@ -379,3 +379,28 @@ def test_layer_cache_decode_loop():
     for li, (q, k, v) in enumerate(xs):
         o_ref, _ = K.kata_fwd(q.cpu(), k.cpu(), v.cpu(), M)
         assert mar(torch.cat(outs[li], 1), o_ref) < TOL
+
+
+def test_cache_paths_share_the_state():
+    """A state from the state-form prefill (1100 tokens) continued by a chunk
+    that the cache sends down the flash path (64 tokens over B H = 96 pairs),
+    then decode steps on the state-form decode: every output equals the rows
+    of the flash forward over all tokens."""
+    from linatt_amd import parallel_kata_attn as P
+    from linatt_amd.kata_cache import parallel_kata_attn_cached
+    B, H, M = 32, 3, 4
+    n0, n1, steps = 1100, 64, 2
+    T = n0 + n1 + steps
+    print(f"\ncache paths share the state: B{B} H{H} T{T}", flush=True)
+    q, k, v = (gen((B, T, H, 64), 90 + i).cuda() for i in range(3))
+    o_par, _ = P.parallel_kata_attn_fwd(q, k, v, num_groups=M)
+    o0, st = parallel_kata_attn_cached(q[:, :n0], k[:, :n0], v[:, :n0], None, M)
+    o1, st = parallel_kata_attn_cached(q[:, n0:n0 + n1], k[:, n0:n0 + n1], v[:, n0:n0 + n1], st, M)
+    outs = [o0, o1]
+    for t in range(n0 + n1, T):
+        o, st = parallel_kata_attn_cached(q[:, t:t + 1], k[:, t:t + 1], v[:, t:t + 1], st, M)
+        outs.append(o)
+    assert st.offset == T
+    err = mar(torch.cat(outs, 1), o_par.float())
+    print(f"  max rel err against the flash forward {err:.1e}", flush=True)
+    assert err < TOL
