@@ -415,14 +415,13 @@ __global__ __launch_bounds__(256) void kata_gen_update_mfma_kernel(KataGenStateA
 
   // prefetch registers: K items (token pair, 8 dimensions), up to two per
   // thread (32 pairs x dk / 8 / 256 threads at dk = 128); one V item (token
-  // pair, 8 columns; the first 128 threads when NCB = 1), NPF chunks ahead
-  // (two measured no faster than one at 44 more registers)
+  // pair, 8 columns; the first 128 threads when NCB = 1), one chunk ahead
+  // (two chunks ahead measured no faster at 44 more registers)
   struct Pf {
     v8_t<T> kr[2][2], vr[2];
     float kc[2][2];
   };
-  constexpr int NPF = 1;
-  Pf pf[NPF];
+  Pf pf;
   auto load = [&](Pf& f, int s0) __attribute__((always_inline)) {
     auto& kr = f.kr;
     auto& vr = f.vr;
@@ -518,20 +517,13 @@ __global__ __launch_bounds__(256) void kata_gen_update_mfma_kernel(KataGenStateA
       }
     }
   };
-#pragma unroll
-  for (int u = 0; u < NPF; ++u) load(pf[u], u * kUpTok);
-  for (int s0 = 0; s0 < a.T; s0 += NPF * kUpTok) {
-#pragma unroll
-    for (int u = 0; u < NPF; ++u) {
-      const int sc = s0 + u * kUpTok;
-      if (sc < a.T) {  // uniform over the workgroup
-        __syncthreads();  // the previous tokens are consumed
-        stage(pf[u], sc);
-        __syncthreads();
-        if (sc + NPF * kUpTok < a.T) load(pf[u], sc + NPF * kUpTok);
-        compute();
-      }
-    }
+  load(pf, 0);
+  for (int s0 = 0; s0 < a.T; s0 += kUpTok) {
+    __syncthreads();  // the previous tokens are consumed
+    stage(pf, s0);
+    __syncthreads();
+    if (s0 + kUpTok < a.T) load(pf, s0 + kUpTok);
+    compute();
   }
   if (!wlive) return;
   const float fT = a.c ? __expf(cT) : 1.f;
