@@ -731,6 +731,89 @@ def bench_gen_prefill(reps):
     return out
 
 
+def bench_cache_serving(decode_steps):
+    """The decode cache end to end through its public call
+    (``kata_cache.parallel_kata_attn_cached``), as a serving loop drives it:
+    a B8 H12 T2048 bf16 prompt into an empty cache, then single-token decode
+    steps (fresh q, k, v ~ N(0,1)/8 per step, resident before timing) on the
+    state it left.  Per score: the prompt's ms and the decode step's ms
+    (tokens/s = B / step), called eagerly and replayed from a HIP graph of 16
+    steps."""
+    import torch
+    from linatt_amd.kata_cache import parallel_kata_attn_cached
+    dev = torch.device("cuda", 0)
+    B, H, T, dv = 8, 12, 2048, 64
+    stream = torch.cuda.current_stream(dev)
+    out = {}
+    for name, dk, M, variant, decay in (("concat_m4_d64", 64, 4, "concat", False),
+                                        ("concat_m1_d64", 64, 1, "concat", False),
+                                        ("sum_m4_d64", 64, 4, "sum", False),
+                                        ("decay_m2_dk128", 128, 2, "concat", True)):
+        g = torch.Generator().manual_seed(41)
+        q, k = ((torch.randn(B, T, H, dk, generator=g) / 8).to(torch.bfloat16).to(dev)
+                for _ in range(2))
+        v = (torch.randn(B, T, H, dv, generator=g) / 8).to(torch.bfloat16).to(dev)
+        c = -(torch.rand(B, T, H, generator=g) * 0.05).cumsum(1).to(dev) if decay else None
+        steps = [tuple((torch.randn(B, 1, H, w, generator=g) / 8).to(torch.bfloat16).to(dev)
+                       for w in (dk, dk, dv)) for _ in range(decode_steps)]
+        cs = torch.full((B, 1, H), -0.01, device=dev) if decay else None
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        parallel_kata_attn_cached(q, k, v, None, M, None, variant=variant, c=c)  # warm
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(3):
+            _, st = parallel_kata_attn_cached(q, k, v, None, M, None, variant=variant, c=c)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        pre_ms = e0.elapsed_time(e1) / 3
+        parallel_kata_attn_cached(*steps[0], st, M, None, variant=variant, c=cs)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for x in steps:
+            _, st = parallel_kata_attn_cached(*x, st, M, None, variant=variant, c=cs)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        dec_ms = e0.elapsed_time(e1) / decode_steps
+        # the same steps replayed from a HIP graph (the calls are capturable:
+        # no memsets, no host synchronisation), which removes the host side
+        # of each call
+        ng = 16
+
+        def loop():
+            s_ = st
+            for x in steps[:ng]:
+                _, s_ = parallel_kata_attn_cached(*x, s_, M, None, variant=variant, c=cs)
+            return s_
+
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            loop()
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            loop()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(4):
+            graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        gr_ms = e0.elapsed_time(e1) / (4 * ng)
+        out[name] = {"state_rows": st.S.shape[2], "prompt_ms": round(pre_ms, 4),
+                     "prompt_tokens_per_s": round(B * T / (pre_ms * 1e-3), 1),
+                     "decode_ms_per_step": round(dec_ms, 4),
+                     "decode_tokens_per_s": round(B / (dec_ms * 1e-3), 1),
+                     "decode_graph_ms_per_step": round(gr_ms, 4),
+                     "decode_graph_tokens_per_s": round(B / (gr_ms * 1e-3), 1)}
+        del st, graph
+    out["config"] = {"B": B, "H": H, "T": T, "dv": dv, "dtype": "bf16",
+                     "decode_steps": decode_steps, "seed": 41}
+    return out
+
+
 def _cpu_threads():
     """Threads for the CPU baselines: every core the host reports, capped at
     the 16 CPUs the GPU box allots to one GPU."""
@@ -1005,11 +1088,12 @@ def main():
                  "deltanet_h12_d64": bench_delta(False, ds, 2, st / 2, H=12, K=64),
                  "gated_deltanet_h12_d64": bench_delta(True, ds, 2, st / 2, H=12, K=64)}
 
-    state = gen_decode = gen_prefill = None
+    state = gen_decode = gen_prefill = serving = None
     if not args.no_state:
         state = bench_state(3, args.decode_steps, args.settle_seconds / 3)
         gen_decode = bench_gen_decode(max(16, args.decode_steps // 4))
         gen_prefill = bench_gen_prefill(5)
+        serving = bench_cache_serving(64)
 
     q1, config1 = bench_config1(max(10, args.steps))
     delta_kata = None if args.no_delta else bench_delta_kata(max(3, args.steps // 2),
@@ -1068,6 +1152,7 @@ def main():
         "kata_state_config5": state,
         "kata_state_decode_generic": gen_decode,
         "kata_state_prefill_generic": gen_prefill,
+        "kata_cache_serving": serving,
         "kata_config1": config1,
         "delta_kata_fwd_bwd": delta_kata,
         "mixer_ops": mixer,
