@@ -260,6 +260,22 @@ int linatt_kata_gen_decode(const void* q, const void* k, const void* v, const fl
                            float* z, void* o, int B, int H, int dk, int dv, int num_groups,
                            int variant, float scale, float eps, int dtype, void* stream);
 
+/* No reference counterpart; for serving at small batch.  The same decode
+ * step with each (b, h)'s state rows split over several workgroups (about
+ * 768 workgroups in all, at least 64 rows each; states of fewer than 512 rows
+ * are not split), whose partial sums a second
+ * launch adds in a fixed order: B*H (b, h) pairs then fill the chip instead
+ * of walking their rows on B*H workgroups.  workspace (16-byte aligned) holds
+ * linatt_kata_gen_decode_workspace_bytes bytes, 0 when no split pays (the
+ * workspace may then be NULL).  Same results as linatt_kata_gen_decode up to
+ * the order of the final fp32 sums. */
+size_t linatt_kata_gen_decode_workspace_bytes(int B, int H, int dk, int num_groups, int variant);
+int linatt_kata_gen_decode_split(const void* q, const void* k, const void* v, const float* c,
+                                 float* S, float* z, void* o, void* workspace,
+                                 size_t workspace_bytes, int B, int H, int dk, int dv,
+                                 int num_groups, int variant, float scale, float eps, int dtype,
+                                 void* stream);
+
 /* A prefill continued from a state: o (B,T,H,64) [dtype] and den (B,T,H)
  * float32 hold the flash forward (linatt_kata_fwd) over the call's tokens on
  * entry; on return o = (o den + e^{c_t} psi(q_t)^T S) / max(den', eps) with
@@ -353,6 +369,19 @@ int linatt_kata_prefill_state_packed(const void* q, const void* k, const void* v
 int linatt_kata_decode_step_packed(const void* q, const void* k, const void* v, float* S, float* z,
                                    void* o, int B, int H, int dk, int dv, int num_groups,
                                    float scale, float eps, int dtype, void* stream);
+
+/* No reference counterpart; for serving at small batch.  linatt_kata_decode_step
+ * (packed = 0) or _packed (packed = 1) with each (b, h)'s state rows split
+ * over several workgroups (about 768 in all, at least 64 rows each), their
+ * partial sums added in a fixed order by a second launch; workspace (16-byte
+ * aligned) holds linatt_kata_decode_workspace_bytes bytes (0: no split; the
+ * workspace may then be NULL).  Same results up to the order of the final
+ * fp32 sums. */
+size_t linatt_kata_decode_workspace_bytes(int B, int H, int dk, int num_groups, int packed);
+int linatt_kata_decode_step_split(const void* q, const void* k, const void* v, float* S, float* z,
+                                  void* o, void* workspace, size_t workspace_bytes, int B, int H,
+                                  int dk, int dv, int num_groups, int packed, float scale, float eps,
+                                  int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------
  * SPD delta rule (DeltaKata).  Replaces the forward of flash_delta

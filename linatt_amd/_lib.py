@@ -61,6 +61,10 @@ SIGNATURES = {
     "linatt_kata_state_supported": (_i, [_i, _i, _i, _i]),
     "linatt_kata_gen_state_rows": (_i, [_i, _i, _i]),
     "linatt_kata_gen_decode": (_i, [_vp] * 7 + [_i] * 6 + [_f, _f, _i, _vp]),
+    "linatt_kata_gen_decode_workspace_bytes": (_sz, [_i] * 5),
+    "linatt_kata_decode_workspace_bytes": (_sz, [_i] * 5),
+    "linatt_kata_decode_step_split": (_i, [_vp] * 7 + [_sz] + [_i] * 6 + [_f, _f, _i, _vp]),
+    "linatt_kata_gen_decode_split": (_i, [_vp] * 8 + [_sz] + [_i] * 6 + [_f, _f, _i, _vp]),
     "linatt_kata_gen_readout": (_i, [_vp] * 6 + [_i] * 7 + [_f, _f, _i, _vp]),
     "linatt_kata_gen_update": (_i, [_vp] * 5 + [_i] * 8 + [_f, _i, _vp]),
     "linatt_kata_prefill_workspace_bytes": (_sz, [_i] * 8),
@@ -139,6 +143,36 @@ def ptr(t: torch.Tensor | None):
 def stream_of(t: torch.Tensor):
     """Current HIP stream of the tensor's device, as a void pointer."""
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+_scratch_by_stream: dict = {}
+
+
+def stream_scratch(device: torch.device, nbytes: int):
+    """A uint8 device buffer of at least ``nbytes``, kept per (device, current
+    stream) and reused by the next call on that stream, which runs after this
+    one's kernels (stream order).  Under graph capture a fresh buffer from the
+    graph's pool is returned and not kept.  ``None`` for ``nbytes == 0``."""
+    if not nbytes:
+        return None
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(nbytes, device=device, dtype=torch.uint8)
+    stream = torch.cuda.current_stream(device)
+    key = (stream.device_index, stream.cuda_stream)
+    buf = _scratch_by_stream.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(nbytes, device=device, dtype=torch.uint8)
+        _scratch_by_stream[key] = buf
+    return buf
+
+
+def split_decode_pays(rows: int) -> bool:
+    """Whether a decode step should split each (b, h)'s rows over several
+    workgroups (when the library offers a split at all): under graph capture
+    the step is bound by its kernels, and a split fills the chip; called
+    eagerly the host's launches bound a short step, and the split's second
+    launch pays only for states of 1024 or more rows."""
+    return rows >= 1024 or torch.cuda.is_current_stream_capturing()
 
 
 def require_device(*ts: torch.Tensor) -> None:

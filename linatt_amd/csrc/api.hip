@@ -1034,7 +1034,8 @@ int linatt_kata_prefill(const void* q, const void* k, const void* v, void* o, fl
 static int kata_decode_step_impl(const char* fn, int tri, const void* q, const void* k,
                                  const void* v, float* S, float* z, void* o, int B, int H, int dk,
                                  int dv, int num_groups, float scale, float eps, int dtype,
-                                 void* stream) {
+                                 void* stream, bool split = false, void* workspace = nullptr,
+                                 size_t workspace_bytes = 0) {
   g_last_error.clear();
   int st = check_state(fn, B, 1, H, dk, dv, num_groups, scale, eps, 128, dtype);
   if (st) return st;
@@ -1047,6 +1048,19 @@ static int kata_decode_step_impl(const char* fn, int tri, const void* q, const v
   KataDecodeArgs a{};
   a.q = q; a.k = k; a.v = v; a.o = o; a.S = S; a.z = z; a.B = B; a.H = H;
   a.scale = scale; a.eps = eps; a.tri = tri;
+  a.nsplit = 1;
+  if (split) {
+    const int E = dk / num_groups;
+    const int rows = num_groups * (tri ? E * (E + 1) / 2 : E * E);
+    a.nsplit = kata_gen_decode_splits(B * H, rows);
+    if (a.nsplit > 1) {
+      const size_t need = (size_t)B * H * a.nsplit * kGenDecPart * sizeof(float);
+      if (!workspace || workspace_bytes < need)
+        return fail(LINATT_EINVAL, std::string(fn) + ": workspace smaller than linatt_kata_decode_workspace_bytes");
+      if (!aligned16(workspace)) return fail(LINATT_EINVAL, std::string(fn) + ": workspace must be 16-byte aligned");
+      a.part = reinterpret_cast<float*>(workspace);
+    }
+  }
   hipError_t e = hipErrorInvalidValue;
   hipStream_t sm = (hipStream_t)stream;
 #define LINATT_TRY_DEC(T_, DK_, DV_, M_) \
@@ -1056,6 +1070,23 @@ static int kata_decode_step_impl(const char* fn, int tri, const void* q, const v
   if (e != hipSuccess)
     return fail(LINATT_ELAUNCH, std::string(fn) + ": launch failed: " + hipGetErrorString(e));
   return LINATT_OK;
+}
+
+size_t linatt_kata_decode_workspace_bytes(int B, int H, int dk, int num_groups, int packed) {
+  if (B <= 0 || H <= 0 || dk <= 0 || num_groups <= 0 || dk % num_groups) return 0;
+  const int E = dk / num_groups;
+  const int rows = num_groups * (packed ? E * (E + 1) / 2 : E * E);
+  const int ns = kata_gen_decode_splits(B * H, rows);
+  return ns > 1 ? (size_t)B * H * ns * kGenDecPart * sizeof(float) : 0;
+}
+
+int linatt_kata_decode_step_split(const void* q, const void* k, const void* v, float* S, float* z,
+                                  void* o, void* workspace, size_t workspace_bytes, int B, int H,
+                                  int dk, int dv, int num_groups, int packed, float scale, float eps,
+                                  int dtype, void* stream) {
+  return kata_decode_step_impl("linatt_kata_decode_step_split", packed ? 1 : 0, q, k, v, S, z, o,
+                               B, H, dk, dv, num_groups, scale, eps, dtype, stream, true, workspace,
+                               workspace_bytes);
 }
 
 int linatt_kata_decode_step(const void* q, const void* k, const void* v, float* S, float* z,
@@ -1099,6 +1130,7 @@ static int gen_state_args(const char* fn, KataGenStateArgs& a, int B, int T, int
   a.tri = tri;
   a.TE = E * (E + 1) / 2;
   a.P = (a.sum ? 1 : M) * (tri ? a.TE : E * E);
+  a.nsplit = 1;
   a.scale = scale; a.eps = eps;
   return LINATT_OK;
 }
@@ -1128,6 +1160,37 @@ int linatt_kata_gen_decode(const void* q, const void* k, const void* v, const fl
   if (st) return st;
   if (!q || !k || !v || !S || !z || !o) return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
   if (!aligned16(S) || !aligned16(o)) return fail(LINATT_EINVAL, std::string(fn) + ": S and o must be 16-byte aligned");
+  a.q = q; a.k = k; a.v = v; a.c = c; a.S = S; a.z = z; a.o = o;
+  return gen_state_launch(fn, a, KATA_GEN_DECODE, dtype, stream);
+}
+
+size_t linatt_kata_gen_decode_workspace_bytes(int B, int H, int dk, int num_groups, int variant) {
+  const int rows = linatt_kata_gen_state_rows(dk, num_groups, variant);
+  if (B <= 0 || H <= 0 || rows <= 0) return 0;
+  const int ns = kata_gen_decode_splits(B * H, rows);
+  return ns > 1 ? (size_t)B * H * ns * kGenDecPart * sizeof(float) : 0;
+}
+
+int linatt_kata_gen_decode_split(const void* q, const void* k, const void* v, const float* c,
+                                 float* S, float* z, void* o, void* workspace,
+                                 size_t workspace_bytes, int B, int H, int dk, int dv,
+                                 int num_groups, int variant, float scale, float eps, int dtype,
+                                 void* stream) {
+  g_last_error.clear();
+  const char* fn = "linatt_kata_gen_decode_split";
+  KataGenStateArgs a{};
+  int st = gen_state_args(fn, a, B, 1, H, dk, dv, num_groups, variant, scale, eps, dtype);
+  if (st) return st;
+  if (!q || !k || !v || !S || !z || !o) return fail(LINATT_EINVAL, std::string(fn) + ": null tensor pointer");
+  if (!aligned16(S) || !aligned16(o)) return fail(LINATT_EINVAL, std::string(fn) + ": S and o must be 16-byte aligned");
+  a.nsplit = kata_gen_decode_splits(B * H, a.P);
+  if (a.nsplit > 1) {
+    const size_t need = (size_t)B * H * a.nsplit * kGenDecPart * sizeof(float);
+    if (!workspace || workspace_bytes < need)
+      return fail(LINATT_EINVAL, std::string(fn) + ": workspace smaller than linatt_kata_gen_decode_workspace_bytes");
+    if (!aligned16(workspace)) return fail(LINATT_EINVAL, std::string(fn) + ": workspace must be 16-byte aligned");
+    a.part = reinterpret_cast<float*>(workspace);
+  }
   a.q = q; a.k = k; a.v = v; a.c = c; a.S = S; a.z = z; a.o = o;
   return gen_state_launch(fn, a, KATA_GEN_DECODE, dtype, stream);
 }

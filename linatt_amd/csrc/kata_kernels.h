@@ -125,6 +125,19 @@ hipError_t launch_kata_prefill(const KataStateArgs& a, hipStream_t stream);
 // n floats from src to dst on the stream (a small copy kernel)
 hipError_t launch_f32_copy(const float* src, float* dst, int64_t n, hipStream_t stream);
 
+constexpr int kGenDecPart = 68;     // floats per decode partial: num[64], den, padding
+constexpr int kGenDecMaxSplit = 16;  // workgroups per (b, h) of a split decode step
+// workgroups per (b, h) for a decode step over P state rows: about 768 in all,
+// at least 64 rows each; a state of fewer than 512 rows is not split (its
+// step is short anyway, and the second launch would cost more than it saves)
+inline int kata_gen_decode_splits(int BH, int P) {
+  if (P < 512) return 1;
+  int ns = (768 + BH - 1) / BH;
+  if (ns > P / 64) ns = P / 64;
+  if (ns > kGenDecMaxSplit) ns = kGenDecMaxSplit;
+  return ns < 1 ? 1 : ns;
+}
+
 struct KataDecodeArgs {
   const void* q;   // (B, H, DK)
   const void* k;
@@ -135,6 +148,8 @@ struct KataDecodeArgs {
   int B, H;
   float scale, eps;
   int tri;         // packed state layout (kata_state_tri_row)
+  int nsplit;      // workgroups per (b, h) (1: o written directly)
+  float* part;     // nsplit > 1: (B*H, nsplit, kGenDecPart) partial num (64) and den
 };
 
 template <typename T, int DK, int DV, int M>
@@ -154,6 +169,8 @@ struct KataGenStateArgs {
   int B, T, H, dk, E, lgE, M, P, sum;
   int tri;           // 1: packed rows, one per unordered pair a <= b of each group
   int TE;            // packed rows per group, E (E + 1) / 2
+  int nsplit;        // decode: workgroups per (b, h) (1: o written directly)
+  float* part;       // decode, nsplit > 1: (B*H, nsplit, kGenDecPart) partial num (64) and den
   float scale, eps;
   int init;          // update: 1 = add to f_T S, 0 = start from zero
 };

@@ -638,14 +638,17 @@ __global__ __launch_bounds__(256) void kata_decode_kernel(KataDecodeArgs a) {
   __shared__ float dred[16];
   __shared__ unsigned short pairs[TRI ? PT : 1];  // packed row -> (dim a << 8) | dim b
   const int tid = threadIdx.x;
-  const int bh = blockIdx.x;
+  const int bh = blockIdx.x, sp = blockIdx.y;
+  // this workgroup's rows [p_lo, p_hi) of the a.nsplit runs (multiples of 16)
+  const int run = ((NR + a.nsplit - 1) / a.nsplit + 15) & ~15;
+  const int p_lo = sp * run, p_hi = min(NR, p_lo + run);
   if (tid < DK) {
     qs[tid] = (float)((const T*)a.q)[(size_t)bh * DK + tid];
     ks[tid] = (float)((const T*)a.k)[(size_t)bh * DK + tid];
   }
   if (tid < DV) vs[tid] = (float)((const T*)a.v)[(size_t)bh * DV + tid];
   if constexpr (TRI) {
-    for (int t = tid; t < PT; t += 256) {
+    for (int t = p_lo + tid; t < p_hi; t += 256) {
       const int g = t / (E * (E + 1) / 2);
       int za = 0, r = t % (E * (E + 1) / 2);
       while (r >= E - za) {
@@ -662,7 +665,7 @@ __global__ __launch_bounds__(256) void kata_decode_kernel(KataDecodeArgs a) {
   float dacc = 0.f;
   float* S = a.S + (size_t)bh * NR * DV;
   float* z = a.z + (size_t)bh * NR;
-  for (int p = r; p < NR; p += 16) {
+  for (int p = p_lo + r; p < p_hi; p += 16) {
     int ia, ib;
     float wq = a.scale;
     if constexpr (TRI) {
@@ -699,17 +702,38 @@ __global__ __launch_bounds__(256) void kata_decode_kernel(KataDecodeArgs a) {
     }
     float d = 0.f;
     for (int rr = 0; rr < 16; ++rr) d += dred[rr];
-    const float inv = 1.f / fmaxf(d, a.eps);
-    st4<T>((T*)a.o + (size_t)bh * DV + 4 * tid, to4<T>(s.x * inv, s.y * inv, s.z * inv, s.w * inv));
+    if (a.nsplit == 1) {
+      const float inv = 1.f / fmaxf(d, a.eps);
+      st4<T>((T*)a.o + (size_t)bh * DV + 4 * tid, to4<T>(s.x * inv, s.y * inv, s.z * inv, s.w * inv));
+    } else {
+      float* pt = a.part + ((size_t)bh * a.nsplit + sp) * kGenDecPart;
+      *reinterpret_cast<float4*>(pt + 4 * tid) = s;
+      if (tid == 0) pt[DV] = d;
+    }
   }
+}
+
+// A split decode step's output: per (b, h), the partials of its a.nsplit
+// workgroups added in split order, o = num / max(den, eps).
+template <typename T>
+__global__ __launch_bounds__(64) void kata_decode_finish_kernel(KataDecodeArgs a) {
+  const int bh = blockIdx.x, n = threadIdx.x;
+  const float* pt = a.part + (size_t)bh * a.nsplit * kGenDecPart;
+  float num = 0.f, den = 0.f;
+  for (int s = 0; s < a.nsplit; ++s) {
+    num += pt[s * kGenDecPart + n];
+    den += pt[s * kGenDecPart + 64];
+  }
+  reinterpret_cast<T*>(a.o)[(size_t)bh * 64 + n] = (T)(num / fmaxf(den, a.eps));
 }
 
 template <typename T, int DK, int DV, int M>
 hipError_t launch_kata_decode(const KataDecodeArgs& a, hipStream_t stream) {
   if (a.tri)
-    kata_decode_kernel<T, DK, DV, M, true><<<dim3(a.B * a.H), dim3(256), 0, stream>>>(a);
+    kata_decode_kernel<T, DK, DV, M, true><<<dim3(a.B * a.H, a.nsplit), dim3(256), 0, stream>>>(a);
   else
-    kata_decode_kernel<T, DK, DV, M, false><<<dim3(a.B * a.H), dim3(256), 0, stream>>>(a);
+    kata_decode_kernel<T, DK, DV, M, false><<<dim3(a.B * a.H, a.nsplit), dim3(256), 0, stream>>>(a);
+  if (a.nsplit > 1) kata_decode_finish_kernel<T><<<dim3(a.B * a.H), dim3(64), 0, stream>>>(a);
   return hipGetLastError();
 }
 

@@ -95,9 +95,13 @@ __device__ __forceinline__ float ldf(const void* p, int64_t i) {
 
 }  // namespace
 
-// One workgroup per (b, h); 16 threads per state row (4 value columns each),
-// 16 rows per pass; q, k (B, H, dk), v, o (B, H, 64); c (B, H) the step's
-// log-decay or null.  The packed layout's rows are mapped to their dimensions
+// One workgroup per (b, h) and split (blockIdx.y of a.nsplit, each a run of
+// rows); 16 threads per state row (4 value columns each), 16 rows per pass;
+// q, k (B, H, dk), v, o (B, H, 64); c (B, H) the step's log-decay or null.
+// With one split the workgroup writes o; with more, each writes its partial
+// numerator and denominator to a.part and kata_gen_decode_finish_kernel adds
+// them in split order (a small batch then fills the chip: its rows are few
+// workgroups' dependent loads otherwise).  The packed layout's rows are mapped to their dimensions
 // once per workgroup into an LDS table (dims < 256: 8 bits each), not by
 // each of a row's 16 threads.
 constexpr int kMaxPackedRows = 128 * 129 / 2;  // dk <= 128, one group of 128
@@ -108,14 +112,17 @@ __global__ __launch_bounds__(256) void kata_gen_decode_kernel(KataGenStateArgs a
   __shared__ float4 red[16][16];
   __shared__ float dred[16];
   __shared__ unsigned short pairs[kMaxPackedRows];
-  const int tid = threadIdx.x, bh = blockIdx.x;
+  const int tid = threadIdx.x, bh = blockIdx.x, sp = blockIdx.y;
+  // this workgroup's rows [p_lo, p_hi): runs of a multiple of 16 rows
+  const int run = ((a.P + a.nsplit - 1) / a.nsplit + 15) & ~15;
+  const int p_lo = sp * run, p_hi = min(a.P, p_lo + run);
   if (tid < a.dk) {
     qs[tid] = ldf<T>(a.q, (int64_t)bh * a.dk + tid);
     ks[tid] = ldf<T>(a.k, (int64_t)bh * a.dk + tid);
   }
   if (tid < kGenDV) vs[tid] = ldf<T>(a.v, (int64_t)bh * kGenDV + tid);
   if (a.tri) {
-    for (int p = tid; p < a.P; p += 256) {
+    for (int p = p_lo + tid; p < p_hi; p += 256) {
       const RowPair rp = row_pair(a, p);
       pairs[p] = (unsigned short)(((rp.g * a.E + rp.a) << 8) | (rp.g * a.E + rp.b));
     }
@@ -131,7 +138,7 @@ __global__ __launch_bounds__(256) void kata_gen_decode_kernel(KataGenStateArgs a
   // rows r, r + 16, ...: each thread loads kDecU rows before updating them,
   // so that kDecU loads per thread are in flight
   constexpr int kDecU = 4;
-  for (int p0 = r; p0 < a.P; p0 += 16 * kDecU) {
+  for (int p0 = p_lo + r; p0 < p_hi; p0 += 16 * kDecU) {
     float4 xs[kDecU];
     float zs[kDecU];
 #pragma unroll
@@ -139,7 +146,7 @@ __global__ __launch_bounds__(256) void kata_gen_decode_kernel(KataGenStateArgs a
       const int p = p0 + 16 * u;
       xs[u] = make_float4(0.f, 0.f, 0.f, 0.f);
       zs[u] = 0.f;
-      if (p < a.P) {
+      if (p < p_hi) {
         xs[u] = *reinterpret_cast<const float4*>(S + (size_t)p * kGenDV + 4 * c4);
         if (c4 == 0) zs[u] = z[p];
       }
@@ -147,7 +154,7 @@ __global__ __launch_bounds__(256) void kata_gen_decode_kernel(KataGenStateArgs a
 #pragma unroll
     for (int u = 0; u < kDecU; ++u) {
       const int p = p0 + 16 * u;
-      if (p >= a.P) break;
+      if (p >= p_hi) break;
       RowPair rp;
       if (a.tri) {
         const unsigned pr = pairs[p];
@@ -183,9 +190,29 @@ __global__ __launch_bounds__(256) void kata_gen_decode_kernel(KataGenStateArgs a
     }
     float d = 0.f;
     for (int rr = 0; rr < 16; ++rr) d += dred[rr];
-    const float inv = 1.f / fmaxf(d, a.eps);
-    st4<T>((T*)a.o + (size_t)bh * kGenDV + 4 * tid, to4<T>(s.x * inv, s.y * inv, s.z * inv, s.w * inv));
+    if (a.nsplit == 1) {
+      const float inv = 1.f / fmaxf(d, a.eps);
+      st4<T>((T*)a.o + (size_t)bh * kGenDV + 4 * tid, to4<T>(s.x * inv, s.y * inv, s.z * inv, s.w * inv));
+    } else {
+      float* pt = a.part + ((size_t)bh * a.nsplit + sp) * kGenDecPart;
+      *reinterpret_cast<float4*>(pt + 4 * tid) = s;
+      if (tid == 0) pt[kGenDV] = d;
+    }
   }
+}
+
+// The split decode step's output: per (b, h), the partials of its a.nsplit
+// workgroups added in split order, o = num / max(den, eps).
+template <typename T>
+__global__ __launch_bounds__(64) void kata_gen_decode_finish_kernel(KataGenStateArgs a) {
+  const int bh = blockIdx.x, n = threadIdx.x;
+  const float* pt = a.part + (size_t)bh * a.nsplit * kGenDecPart;
+  float num = 0.f, den = 0.f;
+  for (int s = 0; s < a.nsplit; ++s) {
+    num += pt[s * kGenDecPart + n];
+    den += pt[s * kGenDecPart + kGenDV];
+  }
+  reinterpret_cast<T*>(a.o)[(size_t)bh * kGenDV + n] = (T)(num / fmaxf(den, a.eps));
 }
 
 // Continued prefill: per (b, h, 64 queries).  Thread (qi, cj) = (tid / 16,
@@ -795,7 +822,8 @@ template <typename T>
 hipError_t launch_kata_gen_state(const KataGenStateArgs& a, int which, hipStream_t stream) {
   const int BH = a.B * a.H;
   if (which == KATA_GEN_DECODE) {
-    kata_gen_decode_kernel<T><<<dim3(BH), dim3(256), 0, stream>>>(a);
+    kata_gen_decode_kernel<T><<<dim3(BH, a.nsplit), dim3(256), 0, stream>>>(a);
+    if (a.nsplit > 1) kata_gen_decode_finish_kernel<T><<<dim3(BH), dim3(kGenDV), 0, stream>>>(a);
   } else if (which == KATA_GEN_READOUT) {
     if constexpr (sizeof(T) == 2) {
       const dim3 grid(BH, (a.T + 127) / 128);

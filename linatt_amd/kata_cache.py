@@ -48,6 +48,7 @@ Scope: dv = 64, dk <= 128 with a power-of-two group width of at least 16
 
 from __future__ import annotations
 
+import functools
 import math
 from typing import NamedTuple
 
@@ -150,6 +151,11 @@ def parallel_kata_attn_cached(q, k, v, state=None, num_groups=4, scale=None, eps
     return _generic(q, k, v, state, M, scale, eps, variant, c, offset)
 
 
+@functools.lru_cache(maxsize=64)
+def _decode_workspace_bytes(B, H, dk, M, var):
+    return _lib.load().linatt_kata_gen_decode_workspace_bytes(B, H, dk, M, var)
+
+
 def _generic(q, k, v, state, M, scale, eps, variant, c, offset):
     _lib.require_device(q, k, v)
     B, T, H, dk = q.shape
@@ -183,9 +189,17 @@ def _generic(q, k, v, state, M, scale, eps, variant, c, offset):
     code, sp = _lib.dtype_code(dt), _lib.stream_of(q)
     if T == 1 and state is not None:
         o = torch.empty(B, H, dv, device=q.device, dtype=dt)
-        _lib.check("linatt_kata_gen_decode", L.linatt_kata_gen_decode(
-            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(cf), _lib.ptr(S), _lib.ptr(z),
-            _lib.ptr(o), B, H, dk, dv, M, var, sc, float(eps), code, sp))
+        # a small batch splits each (b, h)'s rows over several workgroups
+        nws = _decode_workspace_bytes(B, H, dk, M, var)
+        if nws and _lib.split_decode_pays(P):
+            ws = _lib.stream_scratch(q.device, nws)
+            _lib.check("linatt_kata_gen_decode_split", L.linatt_kata_gen_decode_split(
+                _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(cf), _lib.ptr(S), _lib.ptr(z),
+                _lib.ptr(o), _lib.ptr(ws), nws, B, H, dk, dv, M, var, sc, float(eps), code, sp))
+        else:
+            _lib.check("linatt_kata_gen_decode", L.linatt_kata_gen_decode(
+                _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(cf), _lib.ptr(S), _lib.ptr(z),
+                _lib.ptr(o), B, H, dk, dv, M, var, sc, float(eps), code, sp))
         return o[:, None], KataState(S, z, offset + 1, variant, M)
     # the call's own tokens by the flash forward, then the stored state's part
     o, den = _kata_fwd(q, k, v, M, sc, variant, cf)

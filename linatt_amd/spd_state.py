@@ -34,6 +34,7 @@ shapes raise.
 
 from __future__ import annotations
 
+import functools
 import math
 
 import torch
@@ -221,8 +222,22 @@ def kata_decode_step(S, z, q, k, v, num_groups=4, scale=None, eps=1e-6):
     L = _check(q.dtype, dk, dv, M)
     q, k, v = q.contiguous(), k.to(q.dtype).contiguous(), v.to(q.dtype).contiguous()
     o = torch.empty(B, H, dv, device=q.device, dtype=q.dtype)
+    # a small batch splits each (b, h)'s rows over several workgroups
+    nws = _decode_workspace_bytes(B, H, dk, M, int(packed))
+    if nws and _lib.split_decode_pays(R):
+        ws = _lib.stream_scratch(q.device, nws)
+        _lib.check("linatt_kata_decode_step_split", L.linatt_kata_decode_step_split(
+            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(S), _lib.ptr(z), _lib.ptr(o),
+            _lib.ptr(ws), nws, B, H, dk, dv, M, int(packed), _scale(dk, M, scale), float(eps),
+            _lib.dtype_code(q.dtype), _lib.stream_of(q)))
+        return o
     name = "linatt_kata_decode_step_packed" if packed else "linatt_kata_decode_step"
     _lib.check(name, getattr(L, name)(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(S), _lib.ptr(z), _lib.ptr(o), B, H, dk,
         dv, M, _scale(dk, M, scale), float(eps), _lib.dtype_code(q.dtype), _lib.stream_of(q)))
     return o
+
+
+@functools.lru_cache(maxsize=64)
+def _decode_workspace_bytes(B, H, dk, M, packed):
+    return _lib.load().linatt_kata_decode_workspace_bytes(B, H, dk, M, packed)

@@ -404,3 +404,38 @@ def test_cache_paths_share_the_state():
     err = mar(torch.cat(outs, 1), o_par.float())
     print(f"  max rel err against the flash forward {err:.1e}", flush=True)
     assert err < TOL
+
+
+@pytest.mark.parametrize("M,packed", [(4, True), (4, False), (2, True)])
+def test_split_decode_step_equals_decode_step(M, packed):
+    """``linatt_kata_decode_step_split`` (rows over several workgroups per
+    (b, h), partials added by a second launch) against the one-workgroup
+    decode step: S and z bit for bit, o to the rounding of the final sums."""
+    from linatt_amd import _lib, spd_state as S_
+    B, H, dk = 2, 5, 64
+    L = _lib.load()
+    R = S_.state_rows(dk, M, packed)
+    nws = L.linatt_kata_decode_workspace_bytes(B, H, dk, M, int(packed))
+    assert nws > 0
+    print(f"\nsplit MFMA-path decode M{M} packed={packed} rows {R}", flush=True)
+    S0 = (gen((B, H, R, 64), 600 + M, 0.05).float()).cuda()
+    z0 = (gen((B, H, R), 601 + M).float().abs() + 0.5).cuda()
+    q, k, v = (gen((B, H, 64), 602 + i, 0.5).cuda() for i in range(3))
+    sc = 1.0 / (dk // M) ** 0.5
+    outs = []
+    for split in (False, True):
+        S, z = S0.clone(), z0.clone()
+        o = torch.empty(B, H, 64, device="cuda", dtype=BF)
+        head = (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(S), _lib.ptr(z), _lib.ptr(o))
+        if split:
+            ws = torch.empty(nws, device="cuda", dtype=torch.uint8)
+            _lib.check("split", L.linatt_kata_decode_step_split(
+                *head, _lib.ptr(ws), nws, B, H, dk, 64, M, int(packed), sc, 1e-6, 1, _lib.stream_of(q)))
+        else:
+            name = "linatt_kata_decode_step_packed" if packed else "linatt_kata_decode_step"
+            _lib.check(name, getattr(L, name)(*head, B, H, dk, 64, M, sc, 1e-6, 1, _lib.stream_of(q)))
+        outs.append((S, z, o))
+    torch.cuda.synchronize()
+    (S1, z1, o1), (S2, z2, o2) = outs
+    assert torch.equal(S1, S2) and torch.equal(z1, z2)
+    assert mar(o2, o1) < 1e-2

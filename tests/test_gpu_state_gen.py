@@ -289,3 +289,46 @@ def test_single_token_prompt_then_decode(variant, M, dtype):
     err = mar(torch.cat(outs, 1), o_ref)
     print(f"  max rel err {err:.1e}", flush=True)
     assert err < (1e-2 if dtype == torch.float16 else BAR)
+
+
+@pytest.mark.parametrize("dk,M,variant,packed,decay", [(64, 1, "concat", True, False),
+                                                       (64, 2, "sum", True, True),
+                                                       (128, 2, "concat", False, True),
+                                                       (64, 2, "sum", False, False)])
+def test_split_decode_equals_decode(dk, M, variant, packed, decay):
+    """``linatt_kata_gen_decode_split`` (each (b, h)'s rows over several
+    workgroups, partials added in a second launch) against
+    ``linatt_kata_gen_decode``: the updated S and z bit for bit (each row is
+    updated the same way), o to fp32 rounding of the final sums."""
+    from linatt_amd import _lib
+    from linatt_amd.kata_cache import state_rows
+    B, H = 2, 5
+    E = dk // M
+    print(f"\nsplit decode dk{dk} M{M} {variant} packed={packed} decay={decay}", flush=True)
+    L = _lib.load()
+    var = (1 if variant == "sum" else 0) | (_lib.LINATT_KATA_PACKED_STATE if packed else 0)
+    P = state_rows(dk, M, variant, packed)
+    nws = L.linatt_kata_gen_decode_workspace_bytes(B, H, dk, M, var)
+    assert nws > 0  # ten (b, h) pairs: the step splits
+    S0 = (gen((B, H, P, 64), 500 + dk + M) * 0.05).cuda()
+    z0 = (gen((B, H, P), 501 + dk + M).abs() + 0.5).cuda()
+    q, k, v = (gen((B, H, w), 502 + i, 0.5).bfloat16().cuda() for i, w in enumerate((dk, dk, 64)))
+    c = torch.full((B, H), -0.02, device="cuda") if decay else None
+    outs = []
+    for split in (False, True):
+        S, z = S0.clone(), z0.clone()
+        o = torch.empty(B, H, 64, device="cuda", dtype=torch.bfloat16)
+        args = (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(c), _lib.ptr(S), _lib.ptr(z), _lib.ptr(o))
+        tail = (B, H, dk, 64, M, var, 1.0 / math.sqrt(E), 1e-6, 1, _lib.stream_of(q))
+        if split:
+            ws = torch.empty(nws, device="cuda", dtype=torch.uint8)
+            _lib.check("split", L.linatt_kata_gen_decode_split(*args, _lib.ptr(ws), nws, *tail))
+        else:
+            _lib.check("decode", L.linatt_kata_gen_decode(*args, *tail))
+        outs.append((S, z, o))
+    torch.cuda.synchronize()
+    (S1, z1, o1), (S2, z2, o2) = outs
+    assert torch.equal(S1, S2) and torch.equal(z1, z2)
+    err = mar(o2, o1)
+    print(f"  o split vs one workgroup {err:.1e}", flush=True)
+    assert err < 1e-2
